@@ -1,0 +1,278 @@
+"""ctypes bindings for the CPU oracle (``oracle/liboracle.so``).
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py``, always as the checker or the timed CPU baseline, never by
+the product path. Build with ``make -C oracle``.
+
+Each wrapper names the reference function it restates; see ``oracle.h`` for file:line.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, Q4_0, Q8_0 = 0, 1, 2, 8
+QK = 32
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle not built: run `make -C {HERE}`")
+        L = ctypes.CDLL(LIB_PATH)
+        P, S, U32, U64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint64
+        sig = {
+            "fo_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+            "fo_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+            "fo_nbytes": (ctypes.c_int64, [U32, S]),
+            "fo_decode": (ctypes.c_int, [U32, P, S, S, P]),
+            "fo_encode": (ctypes.c_int, [U32, P, S, P]),
+            "fo_transpose": (None, [P, S, S, P]),
+            "fo_quantise_matrix": (ctypes.c_int, [U32, P, S, S, P]),
+            "fo_snap_block": (None, [P, P]),
+            "fo_snap_rows": (None, [P, S, S]),
+            "fo_snap_cols": (None, [P, S, S]),
+            "fo_matmul": (ctypes.c_int, [P, P, S, S, S, P]),
+            "fo_matmul_threaded": (ctypes.c_int, [P, P, S, S, S, ctypes.c_int, P]),
+            "fo_matmul_tuned": (ctypes.c_int, [P, P, S, S, S, ctypes.c_int, P]),
+            "fo_gemv": (None, [P, P, P, S, S, P]),
+            "fo_rand_vec": (None, [S, U64, P]),
+            "fo_max_rel_err": (ctypes.c_float, [P, P, S]),
+            "fo_gelu": (ctypes.c_float, [ctypes.c_float]),
+            "fo_layernorm": (None, [P, P, P, S, P]),
+            "fo_argmax": (S, [P, S]),
+            "fo_gpt2_generate": (ctypes.c_int, [P, P, S, S, P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def f16_to_f32(h: int) -> float:
+    """ferrum_gguf/src/codec/f16.rs:4-22"""
+    return lib().fo_f16_to_f32(h)
+
+
+def f32_to_f16(x: float) -> int:
+    """ferrum_gguf/src/codec/f16.rs:25-53"""
+    return lib().fo_f32_to_f16(x)
+
+
+def f16_to_f32_array(h: np.ndarray) -> np.ndarray:
+    """Element-wise :func:`f16_to_f32` (via the codec's F16 decode)."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    return decode(F16, h.view(np.uint8), h.size)
+
+
+def f32_to_f16_array(x: np.ndarray) -> np.ndarray:
+    x = _f32(x)
+    return encode(F16, x).view(np.uint16)
+
+
+def nbytes(ty: int, n: int) -> int:
+    """ferrum_gguf/src/codec/quant.rs:17-47 (-1 for an error)."""
+    return lib().fo_nbytes(ty, n)
+
+
+def decode(ty: int, data: np.ndarray, n: int) -> np.ndarray:
+    """ferrum_gguf/src/codec/quant.rs:50-88"""
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty(n, np.float32)
+    if lib().fo_decode(ty, _p(data), data.size, n, _p(out)) != 0:
+        raise ValueError("tensor byte length does not match its type and element count")
+    return out
+
+
+def encode(ty: int, data) -> np.ndarray:
+    """ferrum_gguf/src/codec/quant.rs:91-136"""
+    data = _f32(data)
+    nb = nbytes(ty, data.size)
+    if nb < 0:
+        raise ValueError(f"{data.size} elements is not a multiple of the block size 32")
+    out = np.empty(nb, np.uint8)
+    if lib().fo_encode(ty, _p(data), data.size, _p(out)) != 0:
+        raise ValueError("encode failed")
+    return out
+
+
+def transpose(a, rows: int, cols: int) -> np.ndarray:
+    """ferrum_ref/src/models/llama/params.rs:24-32"""
+    a = _f32(a)
+    out = np.empty(rows * cols, np.float32)
+    lib().fo_transpose(_p(a), rows, cols, _p(out))
+    return out
+
+
+def quantise_matrix(ty: int, w, k: int, n: int) -> np.ndarray:
+    """ferrum_wgpu/src/ops/quant.rs:238-252: [k, n] f32 -> GGUF rows [n][k/32]."""
+    w = _f32(w)
+    if k == 0 or k % QK or w.size != k * n:
+        raise ValueError(f"cannot quantise {w.size} elements as a {k} x {n} weight")
+    out = np.empty(n * (k // QK) * BLOCK_BYTES[ty], np.uint8)
+    if lib().fo_quantise_matrix(ty, _p(w), k, n, _p(out)) != 0:
+        raise ValueError("quantise failed")
+    return out
+
+
+def dequantise_bytes(ty: int, data, n: int) -> np.ndarray:
+    """ferrum_wgpu/src/ops/quant.rs:256-264"""
+    return decode(ty, data, n)
+
+
+def dequantised_in_out(ty: int, data, k: int, n: int) -> np.ndarray:
+    """The [k, n] f32 weight the reference's CPU path multiplies by: transpose(decode(bytes))
+    (ferrum_wgpu/src/models/llama/mod.rs:188-200; ops/quant/tests.rs:27-29,143)."""
+    return transpose(decode(ty, data, k * n), n, k)
+
+
+def snap_block(block) -> np.ndarray:
+    """ferrum_ref/src/training/qat.rs:20-24"""
+    block = _f32(block)
+    out = np.empty(32, np.float32)
+    lib().fo_snap_block(_p(block), _p(out))
+    return out
+
+
+def snap_rows(data, ne0: int) -> np.ndarray:
+    """ferrum_ref/src/training/qat.rs:27-35 (returns a snapped copy)."""
+    d = _f32(data).copy()
+    lib().fo_snap_rows(_p(d), d.size, ne0)
+    return d
+
+
+def snap_cols(data, rows_in: int, cols_out: int) -> np.ndarray:
+    """ferrum_ref/src/training/qat.rs:38-54 (returns a snapped copy)."""
+    d = _f32(data).copy()
+    lib().fo_snap_cols(_p(d), rows_in, cols_out)
+    return d
+
+
+def matmul(a, b, m: int, k: int, n: int) -> np.ndarray:
+    """ferrum_ref/src/kernels/matmul.rs:62-69"""
+    a, b = _f32(a), _f32(b)
+    assert a.size == m * k and b.size == k * n
+    out = np.empty(m * n, np.float32)
+    lib().fo_matmul(_p(a), _p(b), m, k, n, _p(out))
+    return out
+
+
+def matmul_threaded(a, b, m: int, k: int, n: int, threads: int) -> np.ndarray:
+    """ferrum_ref/src/kernels/matmul.rs:73-94"""
+    a, b = _f32(a), _f32(b)
+    out = np.empty(m * n, np.float32)
+    lib().fo_matmul_threaded(_p(a), _p(b), m, k, n, threads, _p(out))
+    return out
+
+
+def matmul_tuned(a, b, m: int, k: int, n: int, threads: int) -> np.ndarray:
+    """ferrum_ref/src/kernels/tuned.rs:99-134"""
+    a, b = _f32(a), _f32(b)
+    out = np.empty(m * n, np.float32)
+    lib().fo_matmul_tuned(_p(a), _p(b), m, k, n, threads, _p(out))
+    return out
+
+
+def gemv(x, w, bias, k: int, n: int) -> np.ndarray:
+    """ferrum_ref/src/models/gpt2/decode.rs:42-53 (w is [k, n])."""
+    x, w = _f32(x), _f32(w)
+    b = None if bias is None else _f32(bias)
+    y = np.empty(n, np.float32)
+    lib().fo_gemv(_p(x), _p(w), None if b is None else _p(b), k, n, _p(y))
+    return y
+
+
+def rand_vec(length: int, seed: int) -> np.ndarray:
+    """ferrum_ref/src/kernels/matmul.rs:97-107"""
+    out = np.empty(length, np.float32)
+    lib().fo_rand_vec(length, seed, _p(out))
+    return out
+
+
+def max_rel_err(got, want) -> float:
+    """ferrum_wgpu/src/tolerance.rs:14-26"""
+    got, want = _f32(got), _f32(want)
+    if got.size != want.size:
+        return float("inf")
+    return lib().fo_max_rel_err(_p(got), _p(want), got.size)
+
+
+def gelu(x: float) -> float:
+    """ferrum_ref/src/kernels/nn.rs:12-15"""
+    return lib().fo_gelu(x)
+
+
+def layernorm(x, g, b) -> np.ndarray:
+    """ferrum_ref/src/kernels/nn.rs:31-44 (one row)."""
+    x, g, b = _f32(x), _f32(g), _f32(b)
+    y = np.empty_like(x)
+    lib().fo_layernorm(_p(x), _p(g), _p(b), x.size, _p(y))
+    return y
+
+
+def argmax(v) -> int:
+    """ferrum_model/src/sampling.rs:32-40"""
+    v = _f32(v)
+    return lib().fo_argmax(_p(v), v.size)
+
+
+class _Gpt2(ctypes.Structure):
+    _fields_ = [
+        ("vocab", ctypes.c_size_t), ("ctx", ctypes.c_size_t), ("dim", ctypes.c_size_t),
+        ("heads", ctypes.c_size_t), ("layers", ctypes.c_size_t), ("hidden", ctypes.c_size_t),
+        ("tok", ctypes.c_void_p), ("pos", ctypes.c_void_p), ("blocks", ctypes.c_void_p),
+        ("lnf_g", ctypes.c_void_p), ("lnf_b", ctypes.c_void_p), ("head", ctypes.c_void_p),
+    ]
+
+
+# Per-block tensor order of the reference (ferrum_ref/src/models/gpt2/mod.rs:57-90).
+GPT2_BLOCK_NAMES = ("ln1_g", "ln1_b", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "bo",
+                    "ln2_g", "ln2_b", "w1", "b1", "w2", "b2")
+
+
+def gpt2_generate(model: dict, prompt, n_new: int) -> list[int]:
+    """Greedy cached decode (ferrum_ref/src/models/gpt2/decode.rs:57-117 per token).
+
+    ``model`` holds cfg ints (vocab, ctx, dim, heads, layers, hidden) and f32 arrays ``tok``,
+    ``pos``, ``blocks`` (list of dicts keyed by GPT2_BLOCK_NAMES), ``lnf_g``, ``lnf_b``, ``head``.
+    """
+    keep = []
+
+    def ptr(a):
+        a = _f32(a)
+        keep.append(a)
+        return a.ctypes.data
+
+    blocks = (ctypes.c_void_p * (model["layers"] * 16))()
+    for l, blk in enumerate(model["blocks"]):
+        for i, name in enumerate(GPT2_BLOCK_NAMES):
+            blocks[l * 16 + i] = ptr(blk[name])
+    g = _Gpt2(model["vocab"], model["ctx"], model["dim"], model["heads"], model["layers"],
+              model["hidden"], ptr(model["tok"]), ptr(model["pos"]),
+              ctypes.cast(blocks, ctypes.c_void_p), ptr(model["lnf_g"]), ptr(model["lnf_b"]),
+              ptr(model["head"]))
+    pr = np.ascontiguousarray(prompt, dtype=np.uint64)
+    out = np.zeros(max(n_new, 1), np.uint64)
+    rc = lib().fo_gpt2_generate(ctypes.byref(g), _p(pr), pr.size, n_new, _p(out))
+    if rc != 0:
+        raise ValueError("gpt2 generate failed (context full or token out of range)")
+    return [int(t) for t in out[:n_new]]

@@ -1,0 +1,333 @@
+"""Pins the CPU oracle before anything is checked against it.
+
+Each check is one the reference's own tests make (cited file:line), a golden fixture, an
+independent restatement (numpy's IEEE casts, oracle/np_oracle.py) or a closed form. A planted
+mistake (swapped nibbles, round-half-even, a dropped scale rounding, a transposed operand) fails
+at least one of them; ``test_planted_mistakes_are_caught`` shows that for the codec.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import np_oracle
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def data(n):
+    """ferrum_gguf/src/codec/quant.rs:189-193"""
+    i = np.arange(n)
+    return (((i * 37) % 101).astype(np.float32) - np.float32(50.0)) / np.float32(13.0)
+
+
+# ---- f16 (ferrum_gguf/src/codec/f16.rs:59-95) ----
+
+def test_f16_known_values(orc):
+    assert orc.f16_to_f32(0x3C00) == 1.0
+    assert orc.f16_to_f32(0xC000) == -2.0
+    assert orc.f16_to_f32(0x0000) == 0.0
+    assert orc.f16_to_f32(0x7BFF) == 65504.0
+    assert orc.f16_to_f32(0x0001) == 2.0 ** -24
+    assert np.isinf(orc.f16_to_f32(0x7C00))
+    assert np.isnan(orc.f16_to_f32(0x7E00))
+    assert orc.f32_to_f16(1.0) == 0x3C00
+    assert orc.f32_to_f16(-2.0) == 0xC000
+    assert orc.f32_to_f16(65504.0) == 0x7BFF
+    assert orc.f32_to_f16(1e9) == 0x7C00
+    assert orc.f32_to_f16(1e-30) == 0
+    assert np.isnan(orc.f16_to_f32(orc.f32_to_f16(float("nan"))))
+
+
+def test_every_half_round_trips_and_matches_ieee(orc):
+    h = np.arange(65536, dtype=np.uint16)
+    x = orc.f16_to_f32_array(h)
+    ieee = h.view(np.float16).astype(np.float32)
+    finite = ~np.isnan(ieee)
+    assert np.array_equal(x[finite].view(np.uint32), ieee[finite].view(np.uint32))
+    back = orc.f32_to_f16_array(x)
+    assert np.array_equal(back[finite], h[finite])
+
+
+def test_f16_rounding_is_nearest_even(orc):
+    f = np.float32
+    assert orc.f32_to_f16(f(1.0) + f(2.0) ** -11) == 0x3C00
+    assert orc.f32_to_f16(f(1.0) + f(3.0) * f(2.0) ** -11) == 0x3C02
+    assert orc.f32_to_f16(f(1.0) + f(2.0) ** -11 + f(2.0) ** -20) == 0x3C01
+
+
+def test_f32_to_f16_matches_numpy_on_random_bits(orc):
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**32, 200_000, dtype=np.uint64).astype(np.uint32)
+    # concentrate on the interesting exponents too: subnormal halves, overflow, ties
+    near = (rng.integers(0x33000000, 0x47800000, 200_000, dtype=np.uint64)).astype(np.uint32)
+    x = np.concatenate([bits, near]).view(np.float32)
+    x = x[~np.isnan(x)]
+    mine = orc.f32_to_f16_array(x)
+    ieee = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(mine, ieee)
+
+
+# ---- sizes and codec known answers (ferrum_gguf/src/codec/quant.rs:194-286) ----
+
+def test_sizes(orc):
+    assert orc.nbytes(orc.F32, 5) == 20
+    assert orc.nbytes(orc.F16, 5) == 10
+    assert orc.nbytes(orc.Q8_0, 64) == 68
+    assert orc.nbytes(orc.Q4_0, 64) == 36
+    assert orc.nbytes(orc.Q8_0, 33) == -1
+    assert orc.nbytes(orc.Q4_0, 31) == -1
+    assert orc.nbytes(15, 256) == -1  # Q8_K: unsupported
+
+
+def test_q8_0_known_block(orc):
+    blk = np.zeros(32, np.float32)
+    blk[0], blk[1] = 127.0, -63.5
+    b = orc.encode(orc.Q8_0, blk)
+    assert orc.f16_to_f32(int(b[0]) | int(b[1]) << 8) == 1.0
+    assert b[2].view(np.int8) == 127
+    assert b[3:4].view(np.int8)[0] == -64  # -63.5 rounds away from zero
+    assert orc.decode(orc.Q8_0, b, 32)[0] == 127.0
+
+
+def test_q8_0_error_within_half_a_step(orc):
+    d = data(96)
+    back = orc.decode(orc.Q8_0, orc.encode(orc.Q8_0, d), 96)
+    for blk, got in zip(d.reshape(-1, 32), back.reshape(-1, 32)):
+        step = np.abs(blk).max() / np.float32(127)
+        assert np.all(np.abs(blk - got) <= step * 0.51 + 1e-4)
+
+
+def test_q4_0_bounded_and_idempotent(orc):
+    d = data(64)
+    once = orc.decode(orc.Q4_0, orc.encode(orc.Q4_0, d), 64)
+    for blk, got in zip(d.reshape(-1, 32), once.reshape(-1, 32)):
+        amax = np.abs(blk).max()
+        assert np.all(np.abs(blk - got) <= amax / 8 * 1.01 + 1e-4)
+    twice = orc.decode(orc.Q4_0, orc.encode(orc.Q4_0, once), 64)
+    assert np.array_equal(once, twice)
+
+
+def test_q4_0_nibble_order_low_half_first(orc):
+    blk = np.zeros(32, np.float32)
+    blk[0], blk[16] = -8.0, 7.0
+    back = orc.decode(orc.Q4_0, orc.encode(orc.Q4_0, blk), 32)
+    assert back[0] == -8.0 and back[16] == 7.0 and back[1] == 0.0
+
+
+def test_zero_blocks_and_length_errors(orc):
+    for ty in (orc.Q8_0, orc.Q4_0):
+        assert np.all(orc.decode(ty, orc.encode(ty, np.zeros(32, np.float32)), 32) == 0)
+    # derived from the formula (no reference test pins these bytes): a zero Q4_0 block has
+    # d = 0 / -8 = -0.0, so its scale bytes are 00 80 and every quant byte is 8 | 8 << 4
+    z4 = orc.encode(orc.Q4_0, np.zeros(32, np.float32))
+    assert list(z4[:2]) == [0x00, 0x80] and np.all(z4[2:] == 0x88)
+    z8 = orc.encode(orc.Q8_0, np.zeros(32, np.float32))
+    assert np.all(z8 == 0)
+    with pytest.raises(ValueError):
+        orc.decode(orc.F32, np.zeros(7, np.uint8), 2)
+    with pytest.raises(ValueError):
+        orc.encode(orc.Q8_0, np.ones(5, np.float32))
+
+
+def test_decode_is_the_closed_form(orc):
+    rng = np.random.default_rng(3)
+    raw8 = rng.integers(0, 256, 34 * 200, dtype=np.uint8).reshape(200, 34)
+    raw8[:, 1] &= 0x7B  # finite scales
+    d = raw8[:, :2].copy().view(np.float16).astype(np.float64)
+    want = (d * raw8[:, 2:].view(np.int8).astype(np.float64)).astype(np.float32).reshape(-1)
+    got = orc.decode(orc.Q8_0, raw8.reshape(-1), 200 * 32)
+    assert np.array_equal(got, want)  # d*q has <= 19 significant bits: exact in f32
+
+
+# ---- the reference's golden GGUF (fixtures/bpe/model.gguf, written by another encoder) ----
+
+def test_gguf_fixture_blocks_reencode_byte_identically(orc):
+    info = json.load(open(os.path.join(GOLDEN, "model_gguf_q8_0.json")))
+    blob = np.fromfile(os.path.join(GOLDEN, "model_gguf_q8_0.bin"), np.uint8)
+    assert sum(t["bytes"] for t in info["tensors"]) == blob.size == 4352 * 34
+    vals = orc.decode(orc.Q8_0, blob, blob.size // 34 * 32)
+    assert np.array_equal(orc.encode(orc.Q8_0, vals), blob)
+    assert np.array_equal(np_oracle.encode_q8_0(vals), blob)
+    assert np.array_equal(np_oracle.decode_q8_0(blob).view(np.uint32), vals.view(np.uint32))
+
+
+def test_codec_fixture_is_reproduced(orc):
+    g = np.load(os.path.join(GOLDEN, "codec_nasty.npz"))
+    x = g["x"]
+    assert np.array_equal(orc.encode(orc.Q8_0, x), g["q8_0"])
+    assert np.array_equal(orc.encode(orc.Q4_0, x), g["q4_0"])
+    assert np.array_equal(orc.decode(orc.Q8_0, g["q8_0"], x.size).view(np.uint32),
+                          g["dq8_0"].view(np.uint32))
+    assert np.array_equal(orc.snap_cols(x, 64, 32).view(np.uint32),
+                          g["snap_cols_64x32"].view(np.uint32))
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_c_and_numpy_codecs_agree_on_wide_inputs(orc, seed):
+    rng = np.random.default_rng(seed)
+    n = 32 * 4096
+    x = (rng.standard_normal(n) * np.exp(rng.uniform(-30, 30, n))).astype(np.float32)
+    x[rng.integers(0, n, 500)] = 0.0
+    x[rng.integers(0, n, 50)] = np.inf
+    x[rng.integers(0, n, 50)] = np.nan
+    for ty, enc, dec in [(orc.Q8_0, np_oracle.encode_q8_0, np_oracle.decode_q8_0),
+                         (orc.Q4_0, np_oracle.encode_q4_0, np_oracle.decode_q4_0)]:
+        b = orc.encode(ty, x)
+        assert np.array_equal(b, enc(x))
+        assert np.array_equal(orc.decode(ty, b, n).view(np.uint32), dec(b).view(np.uint32),
+                              equal_nan=False) or np.array_equal(
+            orc.decode(ty, b, n), dec(b), equal_nan=True)
+
+
+def test_requantising_dequantised_weights_reproduces_the_values(orc):
+    """ferrum_wgpu/src/ops/quant/tests.rs:90-104"""
+    g = np.load(os.path.join(GOLDEN, "codec_nasty.npz"))
+    for ty in (orc.Q8_0, orc.Q4_0):
+        for k, n in [(32, 1), (64, 7), (96, 40), (256, 8)]:
+            w = np.resize(g["x"], k * n)
+            b = orc.quantise_matrix(ty, w, k, n)
+            rows = orc.decode(ty, b, k * n)
+            again = orc.quantise_matrix(ty, orc.transpose(rows, n, k), k, n)
+            assert np.array_equal(orc.decode(ty, again, k * n), rows)
+
+
+# ---- snap (ferrum_wgpu/src/ops/qat.rs:90-174, ferrum_ref/src/training/qat.rs:101-170) ----
+
+def test_snap_positive_zero_ties_and_f16_scale(orc):
+    blk = np.zeros(32, np.float32)
+    blk[0], blk[1], blk[2] = 127.0, -0.3, -0.0
+    s = orc.snap_rows(blk, 32)
+    assert s[1].view(np.uint32) == 0 and s[2].view(np.uint32) == 0
+    blk = np.zeros(32, np.float32)
+    blk[:5] = [127.0, 2.5, -2.5, 0.5, -0.49999997]
+    assert list(orc.snap_rows(blk, 32)[:5]) == [127.0, 3.0, -3.0, 1.0, 0.0]
+    blk = np.zeros(32, np.float32)
+    blk[0], blk[1] = np.float32(127.0) / np.float32(3.0), 1.0
+    d16 = np.float32(np.float32(127.0 / 3.0) / np.float32(127)).astype(np.float16).astype(np.float32)
+    s = orc.snap_rows(blk, 32)
+    assert s[1] == d16 * np.float32(round(float(np.float32(1.0) / (np.float32(blk[0]) / np.float32(127)))))
+
+
+def test_snap_is_idempotent_bounded_and_blocks_the_right_way(orc):
+    blk = orc.rand_vec(32, 1)
+    once = orc.snap_block(blk)
+    assert not np.array_equal(once, blk)
+    assert np.array_equal(orc.snap_block(once), once)
+    step = np.abs(blk).max() / np.float32(127)
+    assert np.all(np.abs(blk - once) <= step * 0.51 + 1e-6)
+    m = orc.rand_vec(64 * 3, 3)
+    snapped = orc.snap_cols(m, 64, 3)
+    for j in range(3):
+        for b in range(2):
+            col = m.reshape(64, 3)[b * 32:(b + 1) * 32, j]
+            assert np.array_equal(snapped.reshape(64, 3)[b * 32:(b + 1) * 32, j], orc.snap_block(col))
+    a = orc.rand_vec(40, 4)
+    assert np.array_equal(orc.snap_rows(a, 8), a)
+    assert np.array_equal(orc.snap_cols(a, 8, 5), a)
+
+
+# ---- products (ferrum_ref/src/kernels/matmul.rs:109-190, tuned.rs:136-172) ----
+
+def test_matmul_known_values_and_variants(orc):
+    a = np.array([1, 2, 3, 4, 5, 6], np.float32)
+    b = np.array([7, 8, 9, 10, 11, 12], np.float32)
+    assert list(orc.matmul(a, b, 2, 3, 2)) == [58, 64, 139, 154]
+    for m, k, n in [(1, 1, 1), (3, 5, 7), (5, 9, 17), (9, 300, 11), (13, 513, 261)]:
+        a, b = orc.rand_vec(m * k, 1), orc.rand_vec(k * n, 2)
+        want = orc.matmul(a, b, m, k, n)
+        for t in (1, 2, 3, 8):
+            assert np.array_equal(orc.matmul_threaded(a, b, m, k, n, t), want)
+            assert np.array_equal(orc.matmul_tuned(a, b, m, k, n, t), want)
+        ref = a.astype(np.float64).reshape(m, k) @ b.astype(np.float64).reshape(k, n)
+        assert np.max(np.abs(want - ref.reshape(-1))) < 1e-4 * max(1, np.abs(ref).max())
+
+
+def test_gemv_is_the_one_row_matmul(orc):
+    k, n = 96, 37
+    x, w, bias = orc.rand_vec(k, 5), orc.rand_vec(k * n, 6), orc.rand_vec(n, 7)
+    y = orc.gemv(x, w, None, k, n)
+    assert np.array_equal(y, orc.matmul(x, w, 1, k, n))
+    assert np.array_equal(orc.gemv(x, w, bias, k, n), (y + bias).astype(np.float32))
+
+
+def test_rand_vec_deterministic_in_range(orc):
+    assert np.array_equal(orc.rand_vec(8, 7), orc.rand_vec(8, 7))
+    assert not np.array_equal(orc.rand_vec(8, 7), orc.rand_vec(8, 8))
+    v = orc.rand_vec(1000, 9)
+    assert np.all((v >= -1) & (v < 1))
+    # first value by hand: xorshift64 from seed 7
+    s = 7
+    s ^= (s << 13) & (2**64 - 1)
+    s ^= s >> 7
+    s ^= (s << 17) & (2**64 - 1)
+    assert orc.rand_vec(1, 7)[0] == np.float32((s >> 40) / 2**24 * 2 - 1)
+
+
+def test_max_rel_err_basics(orc):
+    assert orc.max_rel_err([1, 2], [1, 2]) == 0
+    assert abs(orc.max_rel_err([1.5], [1.0]) - 0.5) < 1e-7
+    assert abs(orc.max_rel_err([101.0], [100.0]) - 0.01) < 1e-6
+    assert orc.max_rel_err([1.0], [1.0, 2.0]) == float("inf")
+    assert orc.max_rel_err([float("nan")], [1.0]) == float("inf")
+    assert orc.max_rel_err([], []) == 0
+
+
+def test_gelu_and_layernorm_match_float64(orc):
+    for x in np.linspace(-6, 6, 97, dtype=np.float32):
+        x64 = float(x)
+        want = 0.5 * x64 * (1 + np.tanh(0.7978846 * (x64 + 0.044715 * x64 ** 3)))
+        assert abs(orc.gelu(float(x)) - want) <= 1e-6 * max(1, abs(want))
+    x, g, b = orc.rand_vec(768, 1) * 3, 1 + 0.1 * orc.rand_vec(768, 2), 0.1 * orc.rand_vec(768, 3)
+    x64 = x.astype(np.float64)
+    want = (x64 - x64.mean()) / np.sqrt(x64.var() + 1e-5) * g + b
+    assert np.max(np.abs(orc.layernorm(x, g, b) - want)) < 1e-5
+    assert orc.argmax(np.array([1, 3, 3, 2], np.float32)) == 1  # first maximum wins
+
+
+def test_planted_mistakes_are_caught(orc):
+    """A wrong codec must fail the checks above: plant three mistakes in copies of the numpy
+    restatement and show each one disagrees with the pinned oracle on the golden data."""
+    g = np.load(os.path.join(GOLDEN, "codec_nasty.npz"))
+    x = g["x"]
+
+    def swapped_nibbles(v):
+        b = np_oracle.encode_q4_0(v).reshape(-1, 18).copy()
+        b[:, 2:] = (b[:, 2:] >> 4) | (b[:, 2:] << 4)
+        return b.reshape(-1)
+
+    def half_even(v):
+        b = np.asarray(v, np.float32).reshape(-1, 32)
+        d = (np.abs(b).max(1) / np.float32(127)).astype(np.float32)
+        idv = np.where(d != 0, 1 / np.where(d != 0, d, 1), 0).astype(np.float32)
+        q = np.clip(np.round(b * idv[:, None]), -128, 127).astype(np.int8)
+        out = np.empty((b.shape[0], 34), np.uint8)
+        out[:, :2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+        out[:, 2:] = q.view(np.uint8)
+        return out.reshape(-1)
+
+    def rounded_scale_inverse(v):  # id = 1/f16(d) instead of 1/d
+        b = np.asarray(v, np.float32).reshape(-1, 32)
+        d = (np.abs(b).max(1) / np.float32(127)).astype(np.float16).astype(np.float32)
+        idv = np.where(d != 0, 1 / np.where(d != 0, d, 1), 0).astype(np.float32)
+        q = np.clip(np_oracle._round_half_away(b * idv[:, None]), -128, 127).astype(np.int8)
+        out = np.empty((b.shape[0], 34), np.uint8)
+        out[:, :2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+        out[:, 2:] = q.view(np.uint8)
+        return out.reshape(-1)
+
+    assert not np.array_equal(swapped_nibbles(x), g["q4_0"])
+    blk = np.zeros(32, np.float32)
+    # the -63.5 known block cannot tell half-even from half-away (-64 is even); the snap's tie
+    # block (ferrum_wgpu/src/ops/qat.rs:138-150: 2.5 -> 3, 0.5 -> 1) does
+    blk[:4] = [127.0, 2.5, -2.5, 0.5]
+    assert not np.array_equal(half_even(blk), orc.encode(orc.Q8_0, blk))
+    assert np.array_equal(np_oracle.encode_q8_0(blk), orc.encode(orc.Q8_0, blk))
+    info = json.load(open(os.path.join(GOLDEN, "model_gguf_q8_0.json")))
+    blob = np.fromfile(os.path.join(GOLDEN, "model_gguf_q8_0.bin"), np.uint8)
+    vals = orc.decode(orc.Q8_0, blob, blob.size // 34 * 32)
+    rng = np.random.default_rng(0)
+    wide = (rng.standard_normal(32 * 4096) * 0.02).astype(np.float32)
+    assert not np.array_equal(rounded_scale_inverse(wide), orc.encode(orc.Q8_0, wide))
+    assert info["tensors"]
