@@ -1,0 +1,395 @@
+// GGUF Q8_0 / Q4_0 codec kernels for gfx950: f32 -> blocks (encode), blocks -> f32 (decode) and
+// the fused QAT snap (encode then decode), in "rows" form (blocks of 32 consecutive values, the
+// GGUF tensor order) and "cols" form (blocks running down the columns of an [in, out] matrix).
+// Bit-exact with ferrum_gguf/src/codec/quant.rs:50-136 and ferrum_ref/src/training/qat.rs:20-54.
+//
+// All of this is HBM-bound byte work. The rows kernels give each block to 8 lanes, each lane a
+// 16-byte f32x4 of the block, so a wavefront reads or writes 1 KiB of f32 per instruction,
+// perfectly coalesced; the odd-sized packed side (34 or 18 bytes per block) is staged through
+// LDS so it, too, moves as aligned 16-byte chunks. The cols kernels map consecutive lanes to
+// consecutive columns, which makes the column walks coalesced across the wavefront.
+#include "device_common.hpp"
+#include "internal.hpp"
+
+// The codec must round exactly like the reference: v * id and (v * id) + 8.5 are separate
+// roundings, never one fused multiply-add.
+#pragma clang fp contract(off)
+
+namespace fh {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;                            // 8-block groups per wavefront per task
+constexpr int kTaskBlocks = (kThreads / 64) * kUnroll * 8;  // 128 blocks per workgroup task
+
+template <int KIND>
+struct Fmt;
+template <>
+struct Fmt<FH_Q8_0> {
+    static constexpr int bytes = 34;
+};
+template <>
+struct Fmt<FH_Q4_0> {
+    static constexpr int bytes = 18;
+};
+
+// Reduce over the 8 lanes of a block (lanes 8b..8b+7 of the wavefront).
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, __shfl_xor(v, 1));
+    v = fmaxf(v, __shfl_xor(v, 2));
+    v = fmaxf(v, __shfl_xor(v, 4));
+    return v;
+}
+
+// The signed value of largest magnitude, the lowest index winning ties (the reference's strict
+// `>` fold from 0.0, quant.rs:123-126). `mine` is this lane's candidate for elements
+// 4j..4j+3; lanes are ordered by element index.
+__device__ __forceinline__ float argmax_abs8(float mine, int lane) {
+#pragma unroll
+    for (int s = 1; s < 8; s <<= 1) {
+        float other = __shfl_xor(mine, s);
+        bool lower = (lane & s) == 0;  // this lane's elements come first
+        float lo = lower ? mine : other, hi = lower ? other : mine;
+        mine = fabsf(hi) > fabsf(lo) ? hi : lo;
+    }
+    return mine;
+}
+
+// One quantisation step shared by encode and snap: from this lane's 4 values and the block's
+// statistics, the 4 quant codes (Q8_0: signed q; Q4_0: nibble 0..15) and the f16 scale bits.
+template <int KIND>
+__device__ __forceinline__ void quantise4(const f32x4 v, int lane, int32_t (&q)[4], uint32_t &h) {
+    if constexpr (KIND == FH_Q8_0) {
+        float amax = fmaxf(fmaxf(fmaxf(0.0f, fabsf(v.x)), fmaxf(fabsf(v.y), fabsf(v.z))), fabsf(v.w));
+        amax = max8(amax);
+        float d = amax / 127.0f;
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        h = float_to_half_bits(d);
+        q[0] = round_sat_i8(v.x * id);
+        q[1] = round_sat_i8(v.y * id);
+        q[2] = round_sat_i8(v.z * id);
+        q[3] = round_sat_i8(v.w * id);
+    } else {
+        float m = 0.0f;
+        if (fabsf(v.x) > fabsf(m)) m = v.x;
+        if (fabsf(v.y) > fabsf(m)) m = v.y;
+        if (fabsf(v.z) > fabsf(m)) m = v.z;
+        if (fabsf(v.w) > fabsf(m)) m = v.w;
+        m = argmax_abs8(m, lane);
+        float d = m / -8.0f;
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        h = float_to_half_bits(d);
+        q[0] = trunc_clamp_0_15(v.x * id + 8.5f);
+        q[1] = trunc_clamp_0_15(v.y * id + 8.5f);
+        q[2] = trunc_clamp_0_15(v.z * id + 8.5f);
+        q[3] = trunc_clamp_0_15(v.w * id + 8.5f);
+    }
+}
+
+// ---- encode, rows: f32[nblocks * 32] -> GGUF blocks ----
+template <int KIND>
+__global__ __launch_bounds__(kThreads) void encode_rows_kernel(const float *__restrict__ src,
+                                                               uint8_t *__restrict__ dst,
+                                                               size_t nblocks) {
+    constexpr int BB = Fmt<KIND>::bytes;
+    constexpr int OUT = kTaskBlocks * BB;  // staged output bytes per task (16-byte multiple)
+    __shared__ __attribute__((aligned(16))) uint8_t stage[OUT];
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const size_t ntasks = (nblocks + kTaskBlocks - 1) / kTaskBlocks;
+    for (size_t task = blockIdx.x; task < ntasks; task += gridDim.x) {
+        const size_t blk0 = task * kTaskBlocks;
+        f32x4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            size_t blk = blk0 + (size_t)(wave * kUnroll + u) * 8 + lane / 8;
+            v[u] = blk < nblocks ? __builtin_nontemporal_load((const f32x4 *)src + blk * 8 + lane % 8)
+                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        __syncthreads();  // the previous task's stage has been written out
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            const int lb = (wave * kUnroll + u) * 8 + lane / 8;  // block within the task
+            const int j = lane % 8;
+            int32_t q[4];
+            uint32_t h;
+            quantise4<KIND>(v[u], lane, q, h);
+            uint8_t *blk = stage + lb * BB;
+            if (j == 0) *(uint16_t *)blk = (uint16_t)h;
+            if constexpr (KIND == FH_Q8_0) {
+                uint32_t w = (q[0] & 0xff) | (q[1] & 0xff) << 8 | (q[2] & 0xff) << 16 | (uint32_t)(q[3] & 0xff) << 24;
+                *(uint16_t *)(blk + 2 + 4 * j) = (uint16_t)w;
+                *(uint16_t *)(blk + 4 + 4 * j) = (uint16_t)(w >> 16);
+            } else {
+                // lanes j < 4 hold elements 4j.. (low nibbles), lane j + 4 the elements 16 + 4j..
+                uint32_t lo = q[0] | q[1] << 8 | q[2] << 16 | (uint32_t)q[3] << 24;
+                uint32_t hi = (uint32_t)__shfl_xor((int)lo, 4);
+                if (j < 4) {
+                    uint32_t w = lo | hi << 4;
+                    *(uint16_t *)(blk + 2 + 4 * j) = (uint16_t)w;
+                    *(uint16_t *)(blk + 4 + 4 * j) = (uint16_t)(w >> 16);
+                }
+            }
+        }
+        __syncthreads();
+        const size_t nvalid = nblocks - blk0 < (size_t)kTaskBlocks ? nblocks - blk0 : kTaskBlocks;
+        const size_t valid = nvalid * BB;
+        uint8_t *out = dst + blk0 * BB;
+        for (int c = tid; c < OUT / 16; c += kThreads) {
+            size_t off = (size_t)c * 16;
+            if (off + 16 <= valid) {
+                *(u32x4 *)(out + off) = *(const u32x4 *)(stage + off);
+            } else if (off < valid) {
+                for (size_t b = off; b < valid; b += 2) *(uint16_t *)(out + b) = *(const uint16_t *)(stage + b);
+            }
+        }
+    }
+}
+
+// ---- decode, rows: GGUF blocks -> f32[nblocks * 32] ----
+template <int KIND>
+__global__ __launch_bounds__(kThreads) void decode_rows_kernel(const uint8_t *__restrict__ src,
+                                                               float *__restrict__ dst,
+                                                               size_t nblocks) {
+    constexpr int BB = Fmt<KIND>::bytes;
+    constexpr int IN = kTaskBlocks * BB;
+    __shared__ __attribute__((aligned(16))) uint8_t stage[IN];
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    const size_t ntasks = (nblocks + kTaskBlocks - 1) / kTaskBlocks;
+    for (size_t task = blockIdx.x; task < ntasks; task += gridDim.x) {
+        const size_t blk0 = task * kTaskBlocks;
+        const size_t nvalid = nblocks - blk0 < (size_t)kTaskBlocks ? nblocks - blk0 : kTaskBlocks;
+        const size_t valid = nvalid * BB;
+        const uint8_t *in = src + blk0 * BB;
+        __syncthreads();
+        for (int c = tid; c < IN / 16; c += kThreads) {
+            size_t off = (size_t)c * 16;
+            if (off < valid)  // a partial last chunk reads into the allocation's padding
+                *(u32x4 *)(stage + off) = __builtin_nontemporal_load((const u32x4 *)(in + off));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            const int lb = (wave * kUnroll + u) * 8 + lane / 8;
+            const int j = lane % 8;
+            const size_t blk = blk0 + lb;
+            if (blk >= nblocks) continue;
+            const uint8_t *b = stage + lb * BB;
+            float d = half_bits_to_float(*(const uint16_t *)b);
+            f32x4 o;
+            if constexpr (KIND == FH_Q8_0) {
+                uint32_t w = *(const uint16_t *)(b + 2 + 4 * j) | (uint32_t) * (const uint16_t *)(b + 4 + 4 * j) << 16;
+                o.x = d * (float)(int8_t)(w);
+                o.y = d * (float)(int8_t)(w >> 8);
+                o.z = d * (float)(int8_t)(w >> 16);
+                o.w = d * (float)(int8_t)(w >> 24);
+            } else {
+                const int jj = j & 3, sh = (j >> 2) * 4;  // lanes 4..7 take the high nibbles
+                uint32_t w = *(const uint16_t *)(b + 2 + 4 * jj) | (uint32_t) * (const uint16_t *)(b + 4 + 4 * jj) << 16;
+                w >>= sh;
+                o.x = d * ((float)(w & 15) - 8.0f);
+                o.y = d * ((float)((w >> 8) & 15) - 8.0f);
+                o.z = d * ((float)((w >> 16) & 15) - 8.0f);
+                o.w = d * ((float)((w >> 24) & 15) - 8.0f);
+            }
+            __builtin_nontemporal_store(o, (f32x4 *)dst + blk * 8 + j);
+        }
+    }
+}
+
+// ---- snap, rows: f32 -> f32, decode(encode(block)) for blocks of 32 consecutive values ----
+__global__ __launch_bounds__(kThreads) void snap_rows_kernel(const float *__restrict__ src,
+                                                             float *__restrict__ dst,
+                                                             size_t nblocks) {
+    const int lane = threadIdx.x % 64;
+    const size_t waves = (size_t)gridDim.x * (kThreads / 64);
+    const size_t wave = (size_t)blockIdx.x * (kThreads / 64) + threadIdx.x / 64;
+    const size_t groups = (nblocks + 7) / 8;
+    for (size_t g0 = wave * kUnroll; g0 < groups; g0 += waves * kUnroll) {
+        f32x4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            size_t blk = (g0 + u) * 8 + lane / 8;
+            v[u] = blk < nblocks ? __builtin_nontemporal_load((const f32x4 *)src + blk * 8 + lane % 8)
+                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            int32_t q[4];
+            uint32_t h;
+            quantise4<FH_Q8_0>(v[u], lane, q, h);
+            float d = half_bits_to_float(h);
+            f32x4 o = {d * (float)q[0], d * (float)q[1], d * (float)q[2], d * (float)q[3]};
+            size_t blk = (g0 + u) * 8 + lane / 8;
+            if (blk < nblocks) __builtin_nontemporal_store(o, (f32x4 *)dst + blk * 8 + lane % 8);
+        }
+    }
+}
+
+// ---- cols: one thread per (column c, block kb) of an [k, n] matrix ----
+// Quantise down the columns into GGUF rows: row c of the output holds the blocks of column c
+// (quantise_matrix, ferrum_wgpu/src/ops/quant.rs:238-252).
+template <int KIND>
+__global__ __launch_bounds__(kThreads) void encode_cols_kernel(const float *__restrict__ w,
+                                                               uint8_t *__restrict__ dst, size_t k,
+                                                               size_t n) {
+    constexpr int BB = Fmt<KIND>::bytes;
+    const size_t nb = k / 32;
+    const size_t total = nb * n;
+    for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (size_t)gridDim.x * kThreads) {
+        const size_t kb = t / n, c = t % n;
+        float v[32];
+#pragma unroll
+        for (int e = 0; e < 32; e++) v[e] = w[(kb * 32 + e) * n + c];
+        uint8_t *out = dst + (c * nb + kb) * BB;
+        uint32_t h;
+        if constexpr (KIND == FH_Q8_0) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(v[e]));
+            float d = amax / 127.0f;
+            float id = d != 0.0f ? 1.0f / d : 0.0f;
+            h = float_to_half_bits(d);
+            *(uint16_t *)out = (uint16_t)h;
+#pragma unroll
+            for (int e = 0; e < 32; e += 2) {
+                uint32_t a = round_sat_i8(v[e] * id) & 0xff, b = round_sat_i8(v[e + 1] * id) & 0xff;
+                *(uint16_t *)(out + 2 + e) = (uint16_t)(a | b << 8);
+            }
+        } else {
+            float m = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 32; e++)
+                if (fabsf(v[e]) > fabsf(m)) m = v[e];
+            float d = m / -8.0f;
+            float id = d != 0.0f ? 1.0f / d : 0.0f;
+            h = float_to_half_bits(d);
+            *(uint16_t *)out = (uint16_t)h;
+#pragma unroll
+            for (int j = 0; j < 16; j += 2) {
+                uint32_t b0 = trunc_clamp_0_15(v[j] * id + 8.5f) | trunc_clamp_0_15(v[j + 16] * id + 8.5f) << 4;
+                uint32_t b1 = trunc_clamp_0_15(v[j + 1] * id + 8.5f) | trunc_clamp_0_15(v[j + 17] * id + 8.5f) << 4;
+                *(uint16_t *)(out + 2 + j) = (uint16_t)(b0 | b1 << 8);
+            }
+        }
+    }
+}
+
+// Dequantise GGUF rows back to the [k, n] f32 weight (transpose(decode(bytes))).
+template <int KIND>
+__global__ __launch_bounds__(kThreads) void decode_cols_kernel(const uint8_t *__restrict__ src,
+                                                               float *__restrict__ w, size_t k,
+                                                               size_t n) {
+    constexpr int BB = Fmt<KIND>::bytes;
+    constexpr int WORDS = KIND == FH_Q8_0 ? 9 : 5;
+    const size_t nb = k / 32;
+    const size_t total = nb * n;
+    for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (size_t)gridDim.x * kThreads) {
+        const size_t kb = t / n, c = t % n;
+        const size_t off = (c * nb + kb) * BB;
+        uint32_t win[WORDS];
+        load_window<WORDS>(src, off, win);
+        const float d = half_bits_to_float(scale_bits(win[0], off));
+        const uint32_t sel = quant_sel(off);
+        float *col = w + kb * 32 * n + c;
+        if constexpr (KIND == FH_Q8_0) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                uint32_t q = quant_word(win, i, sel);
+#pragma unroll
+                for (int b = 0; b < 4; b++) col[(4 * i + b) * n] = d * (float)(int8_t)(q >> (8 * b));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint32_t q = quant_word(win, i, sel);
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    col[(4 * i + b) * n] = d * ((float)((q >> (8 * b)) & 15) - 8.0f);
+                    col[(16 + 4 * i + b) * n] = d * ((float)((q >> (8 * b + 4)) & 15) - 8.0f);
+                }
+            }
+        }
+    }
+}
+
+// Snap an [rows_in, cols_out] matrix down its columns (q8_snap_cols, ops/qat.rs:33-57).
+__global__ __launch_bounds__(kThreads) void snap_cols_kernel(const float *__restrict__ src,
+                                                             float *__restrict__ dst, size_t k,
+                                                             size_t n) {
+    const size_t nb = k / 32;
+    const size_t total = nb * n;
+    for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (size_t)gridDim.x * kThreads) {
+        const size_t kb = t / n, c = t % n;
+        const float *in = src + kb * 32 * n + c;
+        float v[32];
+#pragma unroll
+        for (int e = 0; e < 32; e++) v[e] = in[e * n];
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(v[e]));
+        float d = amax / 127.0f;
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        float dh = half_bits_to_float(float_to_half_bits(d));
+        float *out = dst + kb * 32 * n + c;
+#pragma unroll
+        for (int e = 0; e < 32; e++) out[e * n] = dh * (float)round_sat_i8(v[e] * id);
+    }
+}
+
+unsigned grid_for(size_t work_items, size_t per_group, unsigned cap) {
+    size_t g = (work_items + per_group - 1) / per_group;
+    if (g < 1) g = 1;
+    return g > cap ? cap : (unsigned)g;
+}
+
+}  // namespace
+
+hipError_t launch_encode_rows(hipStream_t s, fh_kind kind, const float *src, uint8_t *dst, size_t nblocks) {
+    unsigned g = grid_for(nblocks, kTaskBlocks, 65535);
+    if (kind == FH_Q8_0)
+        encode_rows_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(src, dst, nblocks);
+    else
+        encode_rows_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(src, dst, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_rows(hipStream_t s, fh_kind kind, const uint8_t *src, float *dst, size_t nblocks) {
+    unsigned g = grid_for(nblocks, kTaskBlocks, 65535);
+    if (kind == FH_Q8_0)
+        decode_rows_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(src, dst, nblocks);
+    else
+        decode_rows_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(src, dst, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_snap_rows(hipStream_t s, const float *src, float *dst, size_t nblocks) {
+    unsigned g = grid_for(nblocks, kTaskBlocks, 65535);
+    snap_rows_kernel<<<g, kThreads, 0, s>>>(src, dst, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_encode_cols(hipStream_t s, fh_kind kind, const float *w, uint8_t *dst, size_t k, size_t n) {
+    unsigned g = grid_for(k / 32 * n, kThreads, 65535);
+    if (kind == FH_Q8_0)
+        encode_cols_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(w, dst, k, n);
+    else
+        encode_cols_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(w, dst, k, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_cols(hipStream_t s, fh_kind kind, const uint8_t *src, float *w, size_t k, size_t n) {
+    unsigned g = grid_for(k / 32 * n, kThreads, 65535);
+    if (kind == FH_Q8_0)
+        decode_cols_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(src, w, k, n);
+    else
+        decode_cols_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(src, w, k, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_snap_cols(hipStream_t s, const float *src, float *dst, size_t rows_in, size_t cols_out) {
+    unsigned g = grid_for(rows_in / 32 * cols_out, kThreads, 65535);
+    snap_cols_kernel<<<g, kThreads, 0, s>>>(src, dst, rows_in, cols_out);
+    return hipGetLastError();
+}
+
+}  // namespace fh

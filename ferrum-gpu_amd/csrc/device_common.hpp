@@ -1,0 +1,104 @@
+// Device helpers shared by the kernels: exact f16 <-> f32 bit conversions, the saturating
+// casts of the reference's Rust code, and dword-window loads of the 2-byte-aligned GGUF blocks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fh {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// IEEE binary16 bits -> f32, exact (subnormals normalised by count-leading-zeros). Restates
+// ferrum_gguf/src/codec/f16.rs:4-22 with integer operations, so the result does not depend on
+// the shader's denormal mode.
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    uint32_t sign = (h >> 15) << 31;
+    uint32_t exp = (h >> 10) & 0x1f;
+    uint32_t man = h & 0x3ff;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            uint32_t shift = (uint32_t)__clz((int)man) - 21;
+            uint32_t m = (man << shift) & 0x3ff;
+            bits = sign | ((127u - 15u + 1u - shift) << 23) | (m << 13);
+        }
+    } else if (exp == 0x1f) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 112u) << 23) | (man << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+// f32 -> binary16 bits, round to nearest even, overflow to infinity, NaN quiet
+// (ferrum_gguf/src/codec/f16.rs:25-53), by integer operations.
+__device__ __forceinline__ uint32_t float_to_half_bits(float x) {
+    uint32_t b = __float_as_uint(x);
+    uint32_t sign = (b >> 16) & 0x8000u;
+    int32_t exp = (int32_t)((b >> 23) & 0xff);
+    uint32_t man = b & 0x007fffffu;
+    if (exp == 0xff) return sign | 0x7c00u | (man != 0 ? 0x200u : 0u);
+    int32_t e = exp - 127 + 15;
+    if (e >= 0x1f) return sign | 0x7c00u;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        uint32_t m = man | 0x00800000u;
+        uint32_t shift = (uint32_t)(14 - e);
+        uint32_t half = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t mid = 1u << (shift - 1u);
+        uint32_t up = (rem > mid || (rem == mid && (half & 1u))) ? 1u : 0u;
+        return sign | (half + up);
+    }
+    uint32_t half = ((uint32_t)e << 10) | (man >> 13);
+    uint32_t rem = man & 0x1fffu;
+    uint32_t up = (rem > 0x1000u || (rem == 0x1000u && (half & 1u))) ? 1u : 0u;
+    return sign | (half + up);
+}
+
+// Rust `f as i8` after f32::round: round half away from zero, saturate, NaN -> 0.
+__device__ __forceinline__ int32_t round_sat_i8(float f) {
+    if (f != f) return 0;
+    float r = roundf(f);  // llvm.round: exact half-away-from-zero
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    return (int32_t)r;
+}
+
+// Rust `(f as i32).clamp(0, 15)`: truncate toward zero, saturate, NaN -> 0, then clamp.
+__device__ __forceinline__ int32_t trunc_clamp_0_15(float f) {
+    if (f != f) return 0;
+    float t = truncf(f);
+    t = fminf(fmaxf(t, 0.0f), 15.0f);
+    return (int32_t)t;
+}
+
+// A GGUF block starts at an even byte offset. Load the dword-aligned window that holds it
+// (WORDS dwords starting at the block's offset rounded down to 4); the block's first byte is
+// then at byte `(off & 3)` (0 or 2) of word 0. Reads at most 2 bytes past the block, which
+// every allocation of this library pads for.
+template <int WORDS>
+__device__ __forceinline__ void load_window(const uint8_t *base, size_t off, uint32_t (&w)[WORDS]) {
+    const uint32_t *p = (const uint32_t *)(base + (off & ~(size_t)3));
+#pragma unroll
+    for (int i = 0; i < WORDS; i++) w[i] = __builtin_nontemporal_load(p + i);
+}
+
+// Realign: the i-th dword of the block's quants (which start 2 bytes after the block start).
+// sel = 0x05040302 when the block starts at byte 0 of the window, 0x07060504 when at byte 2.
+__device__ __forceinline__ uint32_t quant_word(const uint32_t *w, int i, uint32_t sel) {
+    return __builtin_amdgcn_perm(w[i + 1], w[i], sel);
+}
+
+__device__ __forceinline__ uint32_t quant_sel(size_t off) {
+    return (off & 2) ? 0x07060504u : 0x05040302u;
+}
+
+__device__ __forceinline__ uint32_t scale_bits(uint32_t w0, size_t off) {
+    return (off & 2) ? (w0 >> 16) : (w0 & 0xffffu);
+}
+
+}  // namespace fh

@@ -1,0 +1,97 @@
+// Internal declarations shared by the runtime and the kernel files of libferrum_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/ferrum_hip.h"
+
+struct fh_device {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    int cus = 0;
+    std::string name;
+    std::atomic<int64_t> fail_after{-1};
+    std::atomic<uint64_t> commands{0};
+    std::atomic<bool> lost{false};
+};
+
+struct fh_buffer {
+    fh_device *dev = nullptr;
+    void *ptr = nullptr;
+    size_t nbytes = 0;
+};
+
+struct fh_qweight {
+    fh_device *dev = nullptr;
+    fh_kind kind = FH_Q8_0;
+    size_t k = 0, n = 0;
+    uint8_t *ptr = nullptr;  // GGUF rows, n * (k/32) blocks, 256-byte aligned, padded
+    size_t nbytes = 0;       // exact GGUF byte count (without the padding)
+};
+
+namespace fh {
+
+constexpr size_t QK = 32;
+// Every device allocation is padded so kernels may read a dword window that runs up to a few
+// bytes past the last block (the 34- and 18-byte blocks are only 2-byte aligned).
+constexpr size_t kPad = 256;
+
+inline size_t block_bytes(fh_kind k) { return k == FH_Q8_0 ? 34 : 18; }
+inline bool kind_ok(int k) { return k == FH_Q8_0 || k == FH_Q4_0; }
+
+// Thread-local error text; returns the status for `return fail(...)`.
+fh_status fail(fh_status st, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Account for one command about to be issued on dev: reports a lost device or an armed
+// injected fault, and counts the command (device/runtime.rs:218-256 semantics).
+fh_status begin_command(fh_device *dev, const char *what);
+// Check the launch that was just issued; a launch error marks the device lost.
+fh_status end_command(fh_device *dev, const char *what);
+// Map a HIP error to a status and message; illegal-address style errors make dev lost.
+fh_status hip_fail(fh_device *dev, hipError_t e, const char *what);
+
+fh_status alloc_bytes(fh_device *dev, size_t nbytes, void **out);
+
+// ---- kernel launchers (each issues exactly one kernel on dev->stream) ----
+// codec.hip
+hipError_t launch_encode_rows(hipStream_t s, fh_kind kind, const float *src, uint8_t *dst,
+                              size_t nblocks);
+hipError_t launch_decode_rows(hipStream_t s, fh_kind kind, const uint8_t *src, float *dst,
+                              size_t nblocks);
+hipError_t launch_encode_cols(hipStream_t s, fh_kind kind, const float *w, uint8_t *dst,
+                              size_t k, size_t n);
+hipError_t launch_decode_cols(hipStream_t s, fh_kind kind, const uint8_t *src, float *w,
+                              size_t k, size_t n);
+hipError_t launch_snap_rows(hipStream_t s, const float *src, float *dst, size_t nblocks);
+hipError_t launch_snap_cols(hipStream_t s, const float *src, float *dst, size_t rows_in,
+                            size_t cols_out);
+
+// gemv.hip
+struct GemvDesc {          // one batch-1 product, as the grouped kernel reads it
+    const uint8_t *w;      // GGUF rows
+    const float *x;
+    float *y;
+    uint32_t nb;           // blocks per row (k / 32)
+    uint32_t n;            // rows (outputs)
+    uint32_t task0;        // first task index of this product in its launch
+    uint32_t pad;
+};
+int gemv_class(size_t nb);  // launch class of a row width in blocks (0 = not supported)
+hipError_t launch_gemv(hipStream_t s, fh_kind kind, const uint8_t *w, const float *x, float *y,
+                       size_t k, size_t n, int cus);
+hipError_t launch_gemv_group(hipStream_t s, fh_kind kind, int cls, const GemvDesc *descs,
+                             uint32_t count, uint32_t tasks, int cus);
+uint32_t gemv_tasks(int cls, size_t n);
+
+// gemm.hip
+hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *w, const float *x, float *y,
+                        size_t rows, size_t k, size_t n);
+hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *w, const float *x, float *y,
+                       size_t rows, size_t k, size_t n);
+
+}  // namespace fh

@@ -1,0 +1,641 @@
+// Runtime of libferrum_hip: devices, buffers, resident quantized weights, argument checks,
+// kernel choice and the C ABI declared in include/ferrum_hip.h. Kernels live in codec.hip,
+// gemv.hip and gemm.hip; this file only validates, accounts and launches.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace fh {
+
+static thread_local std::string g_err;
+
+fh_status fail(fh_status st, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return st;
+}
+
+static bool is_fatal(hipError_t e) {
+    switch (e) {
+    case hipErrorIllegalAddress:
+    case hipErrorLaunchFailure:
+    case hipErrorLaunchTimeOut:
+    case hipErrorAssert:
+    case hipErrorUnknown:
+        return true;
+    default:
+        return false;
+    }
+}
+
+fh_status hip_fail(fh_device *dev, hipError_t e, const char *what) {
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+        return fail(FH_ERR_OOM, "%s: GPU out of memory", what);
+    if (dev && is_fatal(e)) {
+        dev->lost.store(true);
+        return fail(FH_ERR_LOST, "%s: device lost: %s", what, hipGetErrorString(e));
+    }
+    return fail(FH_ERR_DEVICE, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+}
+
+fh_status begin_command(fh_device *dev, const char *what) {
+    if (dev->lost.load()) return fail(FH_ERR_LOST, "%s: the device was lost earlier", what);
+    int64_t n = dev->fail_after.load();
+    if (n == 0) return fail(FH_ERR_INJECTED, "%s: injected fault", what);
+    if (n > 0) dev->fail_after.store(n - 1);
+    dev->commands.fetch_add(1);
+    return FH_OK;
+}
+
+fh_status end_command(fh_device *dev, const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(dev, e, what);
+    return FH_OK;
+}
+
+fh_status alloc_bytes(fh_device *dev, size_t nbytes, void **out) {
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, nbytes + kPad);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return hip_fail(dev, e, "allocate");
+    }
+    e = hipMemsetAsync(p, 0, nbytes + kPad, dev->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return hip_fail(dev, e, "allocate");
+    }
+    *out = p;
+    return FH_OK;
+}
+
+}  // namespace fh
+
+using namespace fh;
+
+namespace {
+
+fh_status check_dev(fh_device *dev) {
+    if (!dev) return fail(FH_ERR_INVALID, "no device");
+    if (dev->lost.load()) return fail(FH_ERR_LOST, "the device was lost earlier");
+    hipError_t e = hipSetDevice(dev->ordinal);
+    if (e != hipSuccess) return hip_fail(dev, e, "select device");
+    return FH_OK;
+}
+
+fh_status sync(fh_device *dev, const char *what) {
+    hipError_t e = hipStreamSynchronize(dev->stream);
+    if (e != hipSuccess) return hip_fail(dev, e, what);
+    return FH_OK;
+}
+
+fh_status new_buffer(fh_device *dev, size_t nbytes, fh_buffer **out) {
+    void *p = nullptr;
+    fh_status st = alloc_bytes(dev, nbytes, &p);
+    if (st) return st;
+    fh_buffer *b = new (std::nothrow) fh_buffer;
+    if (!b) {
+        (void)hipFree(p);
+        return fail(FH_ERR_OOM, "host out of memory");
+    }
+    b->dev = dev;
+    b->ptr = p;
+    b->nbytes = nbytes;
+    *out = b;
+    return FH_OK;
+}
+
+fh_status upload_bytes(fh_device *dev, void *dst, const void *src, size_t nbytes, const char *w) {
+    if (nbytes == 0) return FH_OK;
+    fh_status st = begin_command(dev, w);
+    if (st) return st;
+    hipError_t e = hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, dev->stream);
+    if (e != hipSuccess) return hip_fail(dev, e, w);
+    return sync(dev, w);  // the host memory may be reused as soon as this returns
+}
+
+fh_status read_bytes(fh_device *dev, void *dst, const void *src, size_t nbytes, const char *w) {
+    fh_status st = begin_command(dev, w);
+    if (st) return st;
+    if (nbytes) {
+        hipError_t e = hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost, dev->stream);
+        if (e != hipSuccess) return hip_fail(dev, e, w);
+    }
+    return sync(dev, w);
+}
+
+fh_status need(const char *name, const fh_buffer *b, size_t want) {
+    if (!b) return fail(FH_ERR_INVALID, "%s: no buffer", name);
+    size_t have = b->nbytes / 4;
+    if (have != want)
+        return fail(FH_ERR_INVALID, "%s: buffer holds %zu elements, expected %zu", name, have, want);
+    return FH_OK;
+}
+
+fh_status new_qweight(fh_device *dev, fh_kind kind, size_t k, size_t n, fh_qweight **out) {
+    if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
+    if (k == 0 || k % QK)
+        return fail(FH_ERR_INVALID, "a %zu x %zu weight is not whole 32-element blocks", k, n);
+    if (n == 0 || n > (1u << 30) || k > (1u << 30) || (k / QK) * n > (1ull << 32))
+        return fail(FH_ERR_INVALID, "a %zu x %zu weight is out of range", k, n);
+    size_t nbytes = (k / QK) * n * block_bytes(kind);
+    void *p = nullptr;
+    fh_status st = alloc_bytes(dev, nbytes, &p);
+    if (st) return st;
+    fh_qweight *w = new (std::nothrow) fh_qweight;
+    if (!w) {
+        (void)hipFree(p);
+        return fail(FH_ERR_OOM, "host out of memory");
+    }
+    w->dev = dev;
+    w->kind = kind;
+    w->k = k;
+    w->n = n;
+    w->ptr = (uint8_t *)p;
+    w->nbytes = nbytes;
+    *out = w;
+    return FH_OK;
+}
+
+}  // namespace
+
+struct fh_gemv_plan {
+    fh_device *dev = nullptr;
+    struct Launch {
+        fh_kind kind;
+        int cls;
+        size_t first, count;
+        uint32_t tasks;
+    };
+    std::vector<Launch> launches;
+    GemvDesc *descs = nullptr;  // device array
+    uint64_t bytes = 0;
+};
+
+extern "C" {
+
+const char *fh_last_error(void) { return g_err.c_str(); }
+int fh_abi_version(void) { return FH_ABI_VERSION; }
+
+fh_status fh_device_open(int ordinal, fh_device **out) {
+    if (!out) return fail(FH_ERR_INVALID, "fh_device_open: null out");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0) {
+        (void)hipGetLastError();
+        return fail(FH_ERR_DEVICE, "no HIP device available");
+    }
+    if (ordinal < 0 || ordinal >= count)
+        return fail(FH_ERR_INVALID, "device %d does not exist (%d present)", ordinal, count);
+    if ((e = hipSetDevice(ordinal)) != hipSuccess) return hip_fail(nullptr, e, "select device");
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, ordinal)) != hipSuccess)
+        return hip_fail(nullptr, e, "device properties");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(FH_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950",
+                    ordinal, prop.gcnArchName);
+    fh_device *d = new (std::nothrow) fh_device;
+    if (!d) return fail(FH_ERR_OOM, "host out of memory");
+    d->ordinal = ordinal;
+    d->cus = prop.multiProcessorCount;
+    d->name = prop.name[0] ? prop.name : prop.gcnArchName;
+    if ((e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking)) != hipSuccess) {
+        delete d;
+        return hip_fail(nullptr, e, "create stream");
+    }
+    *out = d;
+    return FH_OK;
+}
+
+void fh_device_close(fh_device *dev) {
+    if (!dev) return;
+    (void)hipSetDevice(dev->ordinal);
+    (void)hipStreamSynchronize(dev->stream);
+    (void)hipStreamDestroy(dev->stream);
+    delete dev;
+}
+
+fh_status fh_device_sync(fh_device *dev) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    return sync(dev, "sync");
+}
+
+fh_status fh_device_info(fh_device *dev, char *name, size_t cap, int *compute_units) {
+    if (!dev) return fail(FH_ERR_INVALID, "no device");
+    if (name && cap) snprintf(name, cap, "%s", dev->name.c_str());
+    if (compute_units) *compute_units = dev->cus;
+    return FH_OK;
+}
+
+void *fh_device_stream(fh_device *dev) { return dev ? (void *)dev->stream : nullptr; }
+void fh_debug_fail_after(fh_device *dev, int64_t n) {
+    if (dev) dev->fail_after.store(n < 0 ? -1 : n);
+}
+uint64_t fh_debug_commands(fh_device *dev) { return dev ? dev->commands.load() : 0; }
+
+// ---- buffers ----
+
+fh_status fh_buffer_zeros(fh_device *dev, size_t len, fh_buffer **out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (len > (SIZE_MAX / 8)) return fail(FH_ERR_INVALID, "buffer of %zu elements is too large", len);
+    return new_buffer(dev, len * 4, out);
+}
+
+fh_status fh_buffer_upload(fh_device *dev, const float *host, size_t len, fh_buffer **out) {
+    fh_status st = fh_buffer_zeros(dev, len, out);
+    if (st) return st;
+    st = upload_bytes(dev, (*out)->ptr, host, len * 4, "upload");
+    if (st) {
+        fh_buffer_free(*out);
+        *out = nullptr;
+    }
+    return st;
+}
+
+fh_status fh_buffer_read(fh_device *dev, const fh_buffer *buf, float *host, size_t len) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if ((st = need("read", buf, len))) return st;
+    return read_bytes(dev, host, buf->ptr, len * 4, "read");
+}
+
+fh_status fh_buffer_write(fh_device *dev, fh_buffer *buf, const float *host, size_t len) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if ((st = need("write", buf, len))) return st;
+    return upload_bytes(dev, buf->ptr, host, len * 4, "write");
+}
+
+fh_status fh_bytes_zeros(fh_device *dev, size_t nbytes, fh_buffer **out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    return new_buffer(dev, nbytes, out);
+}
+
+fh_status fh_bytes_upload(fh_device *dev, const uint8_t *host, size_t nbytes, fh_buffer **out) {
+    fh_status st = fh_bytes_zeros(dev, nbytes, out);
+    if (st) return st;
+    st = upload_bytes(dev, (*out)->ptr, host, nbytes, "upload");
+    if (st) {
+        fh_buffer_free(*out);
+        *out = nullptr;
+    }
+    return st;
+}
+
+fh_status fh_bytes_read(fh_device *dev, const fh_buffer *buf, uint8_t *host, size_t nbytes) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!buf || buf->nbytes != nbytes)
+        return fail(FH_ERR_INVALID, "read: buffer holds %zu bytes, expected %zu",
+                    buf ? buf->nbytes : 0, nbytes);
+    return read_bytes(dev, host, buf->ptr, nbytes, "read");
+}
+
+size_t fh_buffer_len(const fh_buffer *buf) { return buf ? buf->nbytes / 4 : 0; }
+size_t fh_buffer_nbytes(const fh_buffer *buf) { return buf ? buf->nbytes : 0; }
+void *fh_buffer_device_ptr(const fh_buffer *buf) { return buf ? buf->ptr : nullptr; }
+
+void fh_buffer_free(fh_buffer *buf) {
+    if (!buf) return;
+    (void)hipSetDevice(buf->dev->ordinal);
+    (void)hipStreamSynchronize(buf->dev->stream);  // no kernel may still use it
+    (void)hipFree(buf->ptr);
+    delete buf;
+}
+
+fh_status fh_copy_f32(fh_device *dev, const fh_buffer *src, size_t src_off, fh_buffer *dst,
+                      size_t dst_off, size_t len) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!src || !dst) return fail(FH_ERR_INVALID, "copy_f32: no buffer");
+    if (src_off + len > src->nbytes / 4 || dst_off + len > dst->nbytes / 4)
+        return fail(FH_ERR_INVALID, "copy_f32: range out of bounds");
+    if ((st = begin_command(dev, "copy_f32"))) return st;
+    if (len) {
+        hipError_t e = hipMemcpyAsync((float *)dst->ptr + dst_off, (const float *)src->ptr + src_off,
+                                      len * 4, hipMemcpyDeviceToDevice, dev->stream);
+        if (e != hipSuccess) return hip_fail(dev, e, "copy_f32");
+    }
+    return FH_OK;
+}
+
+// ---- device codec ----
+
+size_t fh_nbytes(fh_kind kind, size_t n) {
+    if (!kind_ok(kind)) {
+        fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
+        return 0;
+    }
+    if (n % QK) {
+        fail(FH_ERR_INVALID, "%zu elements is not a multiple of the block size 32", n);
+        return 0;
+    }
+    return n / QK * block_bytes(kind);
+}
+
+fh_status fh_encode(fh_device *dev, fh_kind kind, const fh_buffer *src, size_t n, fh_buffer *dst) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
+    if (n % QK) return fail(FH_ERR_INVALID, "%zu elements is not a multiple of the block size 32", n);
+    if (!src || !dst || src->nbytes < n * 4 || dst->nbytes < n / QK * block_bytes(kind))
+        return fail(FH_ERR_INVALID, "encode: buffers too small for %zu elements", n);
+    if ((st = begin_command(dev, "encode"))) return st;
+    if (n) (void)launch_encode_rows(dev->stream, kind, (const float *)src->ptr, (uint8_t *)dst->ptr, n / QK);
+    return end_command(dev, "encode");
+}
+
+fh_status fh_decode(fh_device *dev, fh_kind kind, const fh_buffer *src, size_t n, fh_buffer *dst) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
+    if (n % QK) return fail(FH_ERR_INVALID, "%zu elements is not a multiple of the block size 32", n);
+    if (!src || !dst || src->nbytes < n / QK * block_bytes(kind) || dst->nbytes < n * 4)
+        return fail(FH_ERR_INVALID, "decode: buffers too small for %zu elements", n);
+    if ((st = begin_command(dev, "decode"))) return st;
+    if (n) (void)launch_decode_rows(dev->stream, kind, (const uint8_t *)src->ptr, (float *)dst->ptr, n / QK);
+    return end_command(dev, "decode");
+}
+
+// ---- resident weights ----
+
+fh_status fh_qweight_upload_gguf(fh_device *dev, fh_kind kind, const uint8_t *bytes, size_t len,
+                                 size_t k, size_t n, fh_qweight **out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
+    if (k == 0 || k % QK)
+        return fail(FH_ERR_INVALID, "a %zu x %zu weight is not whole 32-element blocks", k, n);
+    size_t want = k / QK * n * block_bytes(kind);
+    if (len != want)
+        return fail(FH_ERR_INVALID, "%zu bytes is not the %zu a %zu x %zu %s weight needs", len,
+                    want, k, n, kind == FH_Q8_0 ? "Q8_0" : "Q4_0");
+    if ((st = new_qweight(dev, kind, k, n, out))) return st;
+    st = upload_bytes(dev, (*out)->ptr, bytes, len, "upload_qweight");
+    if (st) {
+        fh_qweight_free(*out);
+        *out = nullptr;
+    }
+    return st;
+}
+
+fh_status fh_qweight_quantise(fh_device *dev, fh_kind kind, const fh_buffer *w, size_t k, size_t n,
+                              fh_qweight **out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
+    if (k == 0 || k % QK || !w || w->nbytes / 4 != k * n)
+        return fail(FH_ERR_INVALID,
+                    "cannot quantise %zu elements as a %zu x %zu weight in whole 32-blocks",
+                    w ? w->nbytes / 4 : 0, k, n);
+    if ((st = new_qweight(dev, kind, k, n, out))) return st;
+    if ((st = begin_command(dev, "quantise_matrix")) == FH_OK) {
+        (void)launch_encode_cols(dev->stream, kind, (const float *)w->ptr, (*out)->ptr, k, n);
+        st = end_command(dev, "quantise_matrix");
+    }
+    if (st) {
+        fh_qweight_free(*out);
+        *out = nullptr;
+    }
+    return st;
+}
+
+fh_status fh_qweight_upload_f32(fh_device *dev, fh_kind kind, const float *w, size_t k, size_t n,
+                                fh_qweight **out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
+    if (k == 0 || k % QK)
+        return fail(FH_ERR_INVALID,
+                    "cannot quantise %zu elements as a %zu x %zu weight in whole 32-blocks",
+                    k * n, k, n);
+    fh_buffer *tmp = nullptr;
+    if ((st = fh_buffer_upload(dev, w, k * n, &tmp))) return st;
+    st = fh_qweight_quantise(dev, kind, tmp, k, n, out);
+    fh_buffer_free(tmp);  // synchronizes: the encode has finished reading it
+    return st;
+}
+
+void fh_qweight_free(fh_qweight *w) {
+    if (!w) return;
+    (void)hipSetDevice(w->dev->ordinal);
+    (void)hipStreamSynchronize(w->dev->stream);
+    (void)hipFree(w->ptr);
+    delete w;
+}
+
+fh_kind fh_qweight_kind(const fh_qweight *w) { return w->kind; }
+size_t fh_qweight_k(const fh_qweight *w) { return w->k; }
+size_t fh_qweight_n(const fh_qweight *w) { return w->n; }
+uint64_t fh_qweight_device_bytes(const fh_qweight *w) { return w->nbytes; }
+
+fh_status fh_qweight_read_gguf(fh_device *dev, const fh_qweight *w, uint8_t *host, size_t len) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!w || len != w->nbytes)
+        return fail(FH_ERR_INVALID, "read_gguf: %zu bytes requested, the weight holds %zu", len,
+                    w ? w->nbytes : 0);
+    return read_bytes(dev, host, w->ptr, len, "read_gguf");
+}
+
+fh_status fh_qweight_dequantise(fh_device *dev, const fh_qweight *w, fh_buffer *out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!w) return fail(FH_ERR_INVALID, "dequantise: no weight");
+    if ((st = need("dequantise out", out, w->k * w->n))) return st;
+    if ((st = begin_command(dev, "dequantise"))) return st;
+    (void)launch_decode_cols(dev->stream, w->kind, w->ptr, (float *)out->ptr, w->k, w->n);
+    return end_command(dev, "dequantise");
+}
+
+// ---- linear layers ----
+
+fh_path fh_choose(size_t rows, fh_kind kind, size_t k, size_t n) {
+    (void)kind;
+    (void)n;
+    if (rows == 1 && gemv_class(k / QK)) return FH_PATH_GEMV;
+    return FH_PATH_TILED;
+}
+
+static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, float *y, size_t rows,
+                        fh_path path) {
+    if (path == FH_PATH_AUTO) path = fh_choose(rows, w->kind, w->k, w->n);
+    fh_status st;
+    switch (path) {
+    case FH_PATH_GEMV:
+        if (rows != 1) return fail(FH_ERR_INVALID, "the GEMV kernel takes one row, not %zu", rows);
+        if (!gemv_class(w->k / QK))
+            return fail(FH_ERR_INVALID, "the GEMV kernel takes k <= 8192, not %zu", w->k);
+        if ((st = begin_command(dev, "linear_q"))) return st;
+        (void)launch_gemv(dev->stream, w->kind, w->ptr, x, y, w->k, w->n, dev->cus);
+        return end_command(dev, "linear_q");
+    case FH_PATH_NAIVE:
+        if ((st = begin_command(dev, "linear_q"))) return st;
+        if (rows) (void)launch_naive(dev->stream, w->kind, w->ptr, x, y, rows, w->k, w->n);
+        return end_command(dev, "linear_q");
+    case FH_PATH_TILED:
+        if ((st = begin_command(dev, "linear_q"))) return st;
+        if (rows) (void)launch_gemm(dev->stream, w->kind, w->ptr, x, y, rows, w->k, w->n);
+        return end_command(dev, "linear_q");
+    default:
+        return fail(FH_ERR_INVALID, "unknown kernel path %d", (int)path);
+    }
+}
+
+fh_status fh_linear_q(fh_device *dev, const fh_buffer *x, const fh_qweight *w, fh_buffer *y,
+                      size_t rows, fh_path path) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!w) return fail(FH_ERR_INVALID, "linear_q: no weight");
+    if (rows > (1u << 24)) return fail(FH_ERR_INVALID, "linear_q: %zu rows is too many", rows);
+    if ((st = need("linear_q x", x, rows * w->k))) return st;
+    if ((st = need("linear_q y", y, rows * w->n))) return st;
+    return linear(dev, (const float *)x->ptr, w, (float *)y->ptr, rows, path);
+}
+
+fh_status fh_linear_q_ptr(fh_device *dev, const float *x, const fh_qweight *w, float *y,
+                          size_t rows, fh_path path) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!w) return fail(FH_ERR_INVALID, "linear_q: no weight");
+    if (rows > (1u << 24)) return fail(FH_ERR_INVALID, "linear_q: %zu rows is too many", rows);
+    if (!x) return fail(FH_ERR_INVALID, "linear_q x: null pointer");
+    if (!y) return fail(FH_ERR_INVALID, "linear_q y: null pointer");
+    return linear(dev, x, w, y, rows, path);
+}
+
+// ---- grouped batch-1 GEMV ----
+
+fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, size_t count,
+                              fh_gemv_plan **out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!out || (count && !problems)) return fail(FH_ERR_INVALID, "gemv plan: null argument");
+    fh_gemv_plan *plan = new (std::nothrow) fh_gemv_plan;
+    if (!plan) return fail(FH_ERR_OOM, "host out of memory");
+    plan->dev = dev;
+    // Group by (kind, class) keeping the caller's order inside a group.
+    std::vector<GemvDesc> host;
+    host.reserve(count);
+    for (int kind : {FH_Q8_0, FH_Q4_0}) {
+        for (int cls = 1; cls <= 5; cls++) {
+            fh_gemv_plan::Launch L{(fh_kind)kind, cls, host.size(), 0, 0};
+            for (size_t i = 0; i < count; i++) {
+                const fh_gemv_problem &p = problems[i];
+                if (!p.w || !p.x || !p.y) {
+                    delete plan;
+                    return fail(FH_ERR_INVALID, "gemv plan: problem %zu has a null pointer", i);
+                }
+                if (p.w->dev != dev) {
+                    delete plan;
+                    return fail(FH_ERR_INVALID, "gemv plan: problem %zu lives on another device", i);
+                }
+                int c = gemv_class(p.w->k / QK);
+                if (c == 0) {
+                    delete plan;
+                    return fail(FH_ERR_INVALID, "gemv plan: problem %zu has k = %zu > 8192", i, p.w->k);
+                }
+                if ((int)p.w->kind != kind || c != cls) continue;
+                GemvDesc d{p.w->ptr, p.x, p.y, (uint32_t)(p.w->k / QK), (uint32_t)p.w->n, L.tasks, 0};
+                uint64_t t = (uint64_t)L.tasks + gemv_tasks(cls, p.w->n);
+                if (t > (1ull << 31)) {
+                    delete plan;
+                    return fail(FH_ERR_INVALID, "gemv plan: too many rows in one launch");
+                }
+                L.tasks = (uint32_t)t;
+                host.push_back(d);
+                plan->bytes += p.w->nbytes + 4ull * (p.w->k + p.w->n);
+                L.count++;
+            }
+            if (L.count) plan->launches.push_back(L);
+        }
+    }
+    if (!host.empty()) {
+        void *p = nullptr;
+        if ((st = alloc_bytes(dev, host.size() * sizeof(GemvDesc), &p))) {
+            delete plan;
+            return st;
+        }
+        plan->descs = (GemvDesc *)p;
+        if ((st = upload_bytes(dev, p, host.data(), host.size() * sizeof(GemvDesc), "gemv plan"))) {
+            fh_gemv_plan_free(plan);
+            return st;
+        }
+    }
+    *out = plan;
+    return FH_OK;
+}
+
+fh_status fh_gemv_plan_run(fh_device *dev, const fh_gemv_plan *plan) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!plan || plan->dev != dev) return fail(FH_ERR_INVALID, "gemv plan: wrong device");
+    for (const auto &L : plan->launches) {
+        if ((st = begin_command(dev, "gemv plan"))) return st;
+        (void)launch_gemv_group(dev->stream, L.kind, L.cls, plan->descs + L.first, (uint32_t)L.count,
+                                L.tasks, dev->cus);
+        if ((st = end_command(dev, "gemv plan"))) return st;
+    }
+    return FH_OK;
+}
+
+size_t fh_gemv_plan_launches(const fh_gemv_plan *plan) { return plan ? plan->launches.size() : 0; }
+uint64_t fh_gemv_plan_bytes(const fh_gemv_plan *plan) { return plan ? plan->bytes : 0; }
+
+void fh_gemv_plan_free(fh_gemv_plan *plan) {
+    if (!plan) return;
+    if (plan->descs) {
+        (void)hipSetDevice(plan->dev->ordinal);
+        (void)hipStreamSynchronize(plan->dev->stream);
+        (void)hipFree(plan->descs);
+    }
+    delete plan;
+}
+
+// ---- QAT snap ----
+
+fh_status fh_q8_snap_rows(fh_device *dev, const fh_buffer *src, fh_buffer *dst, size_t ne0) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!src || !dst) return fail(FH_ERR_INVALID, "q8_snap: no buffer");
+    size_t len = src->nbytes / 4;
+    if (len != dst->nbytes / 4)
+        return fail(FH_ERR_INVALID, "q8_snap: source holds %zu elements but destination %zu", len,
+                    dst->nbytes / 4);
+    if (ne0 == 0 || ne0 % QK || len % QK) return fh_copy_f32(dev, src, 0, dst, 0, len);
+    if ((st = begin_command(dev, "q8_snap"))) return st;
+    if (len) (void)launch_snap_rows(dev->stream, (const float *)src->ptr, (float *)dst->ptr, len / QK);
+    return end_command(dev, "q8_snap");
+}
+
+fh_status fh_q8_snap_cols(fh_device *dev, const fh_buffer *src, fh_buffer *dst, size_t rows_in,
+                          size_t cols_out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!src || !dst) return fail(FH_ERR_INVALID, "q8_snap: no buffer");
+    size_t len = src->nbytes / 4;
+    if (len != dst->nbytes / 4)
+        return fail(FH_ERR_INVALID, "q8_snap: source holds %zu elements but destination %zu", len,
+                    dst->nbytes / 4);
+    if (len != rows_in * cols_out)
+        return fail(FH_ERR_INVALID, "q8_snap: %zu elements is not %zu x %zu", len, rows_in, cols_out);
+    if (rows_in == 0 || rows_in % QK) return fh_copy_f32(dev, src, 0, dst, 0, len);
+    if ((st = begin_command(dev, "q8_snap"))) return st;
+    if (len)
+        (void)launch_snap_cols(dev->stream, (const float *)src->ptr, (float *)dst->ptr, rows_in, cols_out);
+    return end_command(dev, "q8_snap");
+}
+
+}  // extern "C"

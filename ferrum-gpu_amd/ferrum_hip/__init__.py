@@ -1,0 +1,446 @@
+"""Python host mirror of ferrum_wgpu's quantized-weight API over libferrum_hip (the C ABI in
+include/ferrum_hip.h).
+
+Names, argument meanings and error texts follow the reference's `ops_quant` / `ops_qat` modules
+(ferrum_wgpu/src/ops/quant.rs, ferrum_wgpu/src/ops/qat.rs) and the slice of the device layer
+they use (`Gpu`, `GpuBuf`; ferrum_wgpu/src/device/). Every call goes through the native
+library; there is no fallback: if the library is missing the import fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+from typing import Callable, Optional, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libferrum_hip.so")
+HEADER = os.path.join(os.path.dirname(os.path.dirname(HERE)), "include", "ferrum_hip.h")
+
+QK = 32
+
+
+class GpuError(RuntimeError):
+    """ferrum_wgpu::device::GpuError: a message tests match by substring."""
+
+
+class QKind(enum.IntEnum):
+    """ferrum_wgpu/src/ops/quant.rs:27-121 (the two GGUF block formats of this path)."""
+    Q4_0 = 2
+    Q8_0 = 8
+
+    def label(self) -> str:
+        return "Q8_0" if self == QKind.Q8_0 else "Q4_0"
+
+    def elems(self) -> int:
+        return QK
+
+    def file_bytes(self) -> int:
+        return 34 if self == QKind.Q8_0 else 18
+
+
+class QPath(enum.IntEnum):
+    """ferrum_wgpu/src/ops/quant.rs:292-305. Tiled is the MFMA dequant-GEMM here."""
+    Auto = 0
+    Naive = 1
+    Gemv = 2
+    Tiled = 3
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is not built: run `make -C {os.path.dirname(HERE)}` "
+            "(or __graft_entry__.build()); there is no CPU fallback")
+    L = ctypes.CDLL(LIB_PATH)
+    P, S, I, U64, I64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_int64
+    PP = ctypes.POINTER(ctypes.c_void_p)
+    sigs = {
+        "fh_last_error": (ctypes.c_char_p, []),
+        "fh_abi_version": (I, []),
+        "fh_device_open": (I, [I, PP]),
+        "fh_device_close": (None, [P]),
+        "fh_device_sync": (I, [P]),
+        "fh_device_info": (I, [P, ctypes.c_char_p, S, ctypes.POINTER(I)]),
+        "fh_device_stream": (P, [P]),
+        "fh_debug_fail_after": (None, [P, I64]),
+        "fh_debug_commands": (U64, [P]),
+        "fh_buffer_zeros": (I, [P, S, PP]),
+        "fh_buffer_upload": (I, [P, P, S, PP]),
+        "fh_buffer_read": (I, [P, P, P, S]),
+        "fh_buffer_write": (I, [P, P, P, S]),
+        "fh_bytes_zeros": (I, [P, S, PP]),
+        "fh_bytes_upload": (I, [P, P, S, PP]),
+        "fh_bytes_read": (I, [P, P, P, S]),
+        "fh_buffer_len": (S, [P]),
+        "fh_buffer_nbytes": (S, [P]),
+        "fh_buffer_device_ptr": (P, [P]),
+        "fh_buffer_free": (None, [P]),
+        "fh_copy_f32": (I, [P, P, S, P, S, S]),
+        "fh_nbytes": (S, [I, S]),
+        "fh_encode": (I, [P, I, P, S, P]),
+        "fh_decode": (I, [P, I, P, S, P]),
+        "fh_qweight_upload_gguf": (I, [P, I, P, S, S, S, PP]),
+        "fh_qweight_upload_f32": (I, [P, I, P, S, S, PP]),
+        "fh_qweight_quantise": (I, [P, I, P, S, S, PP]),
+        "fh_qweight_free": (None, [P]),
+        "fh_qweight_kind": (I, [P]),
+        "fh_qweight_k": (S, [P]),
+        "fh_qweight_n": (S, [P]),
+        "fh_qweight_device_bytes": (U64, [P]),
+        "fh_qweight_read_gguf": (I, [P, P, P, S]),
+        "fh_qweight_dequantise": (I, [P, P, P]),
+        "fh_choose": (I, [S, I, S, S]),
+        "fh_linear_q": (I, [P, P, P, P, S, I]),
+        "fh_linear_q_ptr": (I, [P, P, P, P, S, I]),
+        "fh_gemv_plan_create": (I, [P, P, S, PP]),
+        "fh_gemv_plan_run": (I, [P, P]),
+        "fh_gemv_plan_launches": (S, [P]),
+        "fh_gemv_plan_bytes": (U64, [P]),
+        "fh_gemv_plan_free": (None, [P]),
+        "fh_q8_snap_rows": (I, [P, P, P, S]),
+        "fh_q8_snap_cols": (I, [P, P, P, S, S]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    if L.fh_abi_version() != 1:
+        raise RuntimeError("libferrum_hip ABI version mismatch")
+    _lib = L
+    return L
+
+
+def exported_symbols() -> list[str]:
+    """Names the header declares (every one must resolve in the library)."""
+    import re
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^FH_API [^(]*?\b(fh_\w+)\(", text, re.M)))
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise GpuError(lib().fh_last_error().decode("utf-8", "replace"))
+
+
+def _np(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class GpuBuf:
+    """ferrum_wgpu::tensor::GpuBuf (f32 elements), or a byte buffer for packed blocks."""
+
+    def __init__(self, gpu: "Gpu", handle: ctypes.c_void_p):
+        self.gpu, self._h = gpu, handle
+
+    @property
+    def handle(self):
+        return self._h
+
+    def len(self) -> int:
+        return lib().fh_buffer_len(self._h)
+
+    def __len__(self) -> int:
+        return self.len()
+
+    def nbytes(self) -> int:
+        return lib().fh_buffer_nbytes(self._h)
+
+    def device_ptr(self) -> int:
+        return lib().fh_buffer_device_ptr(self._h)
+
+    def free(self) -> None:
+        if self._h:
+            lib().fh_buffer_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Gpu:
+    """ferrum_wgpu::device::Gpu, reduced to what the quantized path uses."""
+
+    def __init__(self, ordinal: int = 0):
+        h = ctypes.c_void_p()
+        _check(lib().fh_device_open(ordinal, ctypes.byref(h)))
+        self._h = h
+
+    @staticmethod
+    def open_for_test() -> Optional["Gpu"]:
+        """device/mod.rs:192-201: a device, or None (with the reason printed) when there is none."""
+        try:
+            return Gpu(int(os.environ.get("FERRUM_HIP_DEVICE", "0")))
+        except (GpuError, RuntimeError) as e:
+            print(f"no GPU for this test: {e}")
+            return None
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self) -> None:
+        if self._h:
+            lib().fh_device_close(self._h)
+            self._h = None
+
+    def info(self) -> tuple[str, int]:
+        name = ctypes.create_string_buffer(256)
+        cus = ctypes.c_int()
+        _check(lib().fh_device_info(self._h, name, 256, ctypes.byref(cus)))
+        return name.value.decode(), cus.value
+
+    def stream(self) -> int:
+        return lib().fh_device_stream(self._h)
+
+    def sync(self) -> None:
+        _check(lib().fh_device_sync(self._h))
+
+    def zeros(self, n: int) -> GpuBuf:
+        h = ctypes.c_void_p()
+        _check(lib().fh_buffer_zeros(self._h, n, ctypes.byref(h)))
+        return GpuBuf(self, h)
+
+    def upload(self, data) -> GpuBuf:
+        a = _np(data).reshape(-1)
+        h = ctypes.c_void_p()
+        _check(lib().fh_buffer_upload(self._h, _ptr(a), a.size, ctypes.byref(h)))
+        return GpuBuf(self, h)
+
+    def write(self, buf: GpuBuf, data) -> None:
+        a = _np(data).reshape(-1)
+        _check(lib().fh_buffer_write(self._h, buf.handle, _ptr(a), a.size))
+
+    def read(self, buf: GpuBuf) -> np.ndarray:
+        out = np.empty(buf.len(), np.float32)
+        _check(lib().fh_buffer_read(self._h, buf.handle, _ptr(out), out.size))
+        return out
+
+    def bytes_zeros(self, nbytes: int) -> GpuBuf:
+        h = ctypes.c_void_p()
+        _check(lib().fh_bytes_zeros(self._h, nbytes, ctypes.byref(h)))
+        return GpuBuf(self, h)
+
+    def upload_bytes(self, data) -> GpuBuf:
+        a = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+        h = ctypes.c_void_p()
+        _check(lib().fh_bytes_upload(self._h, _ptr(a), a.size, ctypes.byref(h)))
+        return GpuBuf(self, h)
+
+    def read_bytes(self, buf: GpuBuf) -> np.ndarray:
+        out = np.empty(buf.nbytes(), np.uint8)
+        _check(lib().fh_bytes_read(self._h, buf.handle, _ptr(out), out.size))
+        return out
+
+    def copy_f32(self, src: GpuBuf, src_off: int, dst: GpuBuf, dst_off: int, n: int) -> None:
+        _check(lib().fh_copy_f32(self._h, src.handle, src_off, dst.handle, dst_off, n))
+
+    # ---- test hooks (device/runtime.rs:218-256) ----
+    def fail_after(self, n: Optional[int]) -> None:
+        lib().fh_debug_fail_after(self._h, -1 if n is None else n)
+
+    def commands(self) -> int:
+        return lib().fh_debug_commands(self._h)
+
+    def sweep_faults(self, f: Callable[[], None]) -> int:
+        """Fail command 0, then 1, ... until `f` succeeds; every failure must be the injected
+        fault. Returns how many commands `f` issues."""
+        for k in range(100_000):
+            self.fail_after(k)
+            try:
+                f()
+            except GpuError as e:
+                assert "injected fault" in str(e), f"command {k}: {e}"
+                continue
+            self.fail_after(None)
+            return k
+        raise AssertionError("the operation never succeeded")
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class QWeight:
+    """ferrum_wgpu/src/ops/quant.rs:155-182: a resident quantized weight (GGUF rows)."""
+
+    def __init__(self, gpu: Gpu, handle):
+        self.gpu, self._h = gpu, handle
+
+    @property
+    def handle(self):
+        return self._h
+
+    def kind(self) -> QKind:
+        return QKind(lib().fh_qweight_kind(self._h))
+
+    def k(self) -> int:
+        return lib().fh_qweight_k(self._h)
+
+    def n(self) -> int:
+        return lib().fh_qweight_n(self._h)
+
+    def device_bytes(self) -> int:
+        return lib().fh_qweight_device_bytes(self._h)
+
+    def read_gguf(self) -> np.ndarray:
+        out = np.empty(self.device_bytes(), np.uint8)
+        _check(lib().fh_qweight_read_gguf(self.gpu.handle, self._h, _ptr(out), out.size))
+        return out
+
+    def dequantised(self) -> np.ndarray:
+        """The [k, n] f32 weight the CPU path multiplies by, dequantised on the device."""
+        out = self.gpu.zeros(self.k() * self.n())
+        _check(lib().fh_qweight_dequantise(self.gpu.handle, self._h, out.handle))
+        return self.gpu.read(out)
+
+    def free(self) -> None:
+        if self._h:
+            lib().fh_qweight_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def eligible(k: int) -> bool:
+    """quant.rs:125-129"""
+    return k > 0 and k % QK == 0
+
+
+def nbytes(kind: QKind, n: int) -> int:
+    """ferrum_gguf/src/codec/quant.rs:17-47"""
+    r = lib().fh_nbytes(int(kind), n)
+    if r == 0 and n != 0:
+        raise GpuError(lib().fh_last_error().decode())
+    return r
+
+
+def upload_qweight(gpu: Gpu, kind: QKind, data, k: int, n: int) -> QWeight:
+    """quant.rs:267-277: GGUF rows (n rows of k/32 blocks), resident bit-exact."""
+    a = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
+    h = ctypes.c_void_p()
+    _check(lib().fh_qweight_upload_gguf(gpu.handle, int(kind), _ptr(a), a.size, k, n, ctypes.byref(h)))
+    return QWeight(gpu, h)
+
+
+def upload_quantised(gpu: Gpu, kind: QKind, w, k: int, n: int) -> QWeight:
+    """quant.rs:279-288: quantise an [in, out] f32 weight (on the device) and keep it resident."""
+    a = _np(w).reshape(-1)
+    if a.size != k * n:
+        raise GpuError(f"cannot quantise {a.size} elements as a {k} x {n} weight in whole 32-blocks")
+    h = ctypes.c_void_p()
+    _check(lib().fh_qweight_upload_f32(gpu.handle, int(kind), _ptr(a), k, n, ctypes.byref(h)))
+    return QWeight(gpu, h)
+
+
+def quantise_matrix(gpu: Gpu, kind: QKind, w: GpuBuf, k: int, n: int) -> QWeight:
+    """quant.rs:238-252 on the device, from a resident [k, n] f32 buffer."""
+    h = ctypes.c_void_p()
+    _check(lib().fh_qweight_quantise(gpu.handle, int(kind), w.handle, k, n, ctypes.byref(h)))
+    return QWeight(gpu, h)
+
+
+def encode(gpu: Gpu, kind: QKind, src: GpuBuf, n: int, dst: Optional[GpuBuf] = None) -> GpuBuf:
+    """ferrum_gguf quant::encode on the device: n values -> GGUF blocks."""
+    dst = dst or gpu.bytes_zeros(nbytes(kind, n))
+    _check(lib().fh_encode(gpu.handle, int(kind), src.handle, n, dst.handle))
+    return dst
+
+
+def decode(gpu: Gpu, kind: QKind, src: GpuBuf, n: int, dst: Optional[GpuBuf] = None) -> GpuBuf:
+    """ferrum_gguf quant::decode on the device: GGUF blocks -> n f32 values."""
+    dst = dst or gpu.zeros(n)
+    _check(lib().fh_decode(gpu.handle, int(kind), src.handle, n, dst.handle))
+    return dst
+
+
+def choose(rows: int, kind: QKind, k: int, n: int) -> QPath:
+    """quant.rs:306-323, re-derived for MI355X."""
+    return QPath(lib().fh_choose(rows, int(kind), k, n))
+
+
+def linear_q(gpu: Gpu, x: GpuBuf, w: QWeight, y: GpuBuf, rows: int) -> None:
+    """quant.rs:326-335: y[rows, n] = x[rows, k] * W (no bias)."""
+    linear_q_with(gpu, x, w, y, rows, QPath.Auto)
+
+
+def linear_q_with(gpu: Gpu, x: GpuBuf, w: QWeight, y: GpuBuf, rows: int, path: QPath) -> None:
+    """quant.rs:337-381"""
+    _check(lib().fh_linear_q(gpu.handle, x.handle, w.handle, y.handle, rows, int(path)))
+
+
+def linear_q_ptr(gpu: Gpu, x_ptr: int, w: QWeight, y_ptr: int, rows: int, path: QPath = QPath.Auto) -> None:
+    """linear_q on raw device pointers (e.g. torch tensors' data_ptr())."""
+    _check(lib().fh_linear_q_ptr(gpu.handle, x_ptr, w.handle, y_ptr, rows, int(path)))
+
+
+class _Problem(ctypes.Structure):
+    _fields_ = [("w", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p)]
+
+
+class GemvPlan:
+    """Many independent batch-1 products in one launch per (format, width class); no
+    counterpart in the reference (which issues one linear_q per matrix)."""
+
+    def __init__(self, gpu: Gpu, problems: Sequence[tuple[QWeight, int, int]]):
+        arr = (_Problem * max(len(problems), 1))()
+        for i, (w, xp, yp) in enumerate(problems):
+            arr[i] = _Problem(w.handle.value if hasattr(w.handle, "value") else w.handle, xp, yp)
+        self._keep = [p[0] for p in problems]
+        self.gpu = gpu
+        h = ctypes.c_void_p()
+        _check(lib().fh_gemv_plan_create(gpu.handle, ctypes.cast(arr, ctypes.c_void_p), len(problems),
+                                         ctypes.byref(h)))
+        self._h = h
+
+    def run(self) -> None:
+        _check(lib().fh_gemv_plan_run(self.gpu.handle, self._h))
+
+    def launches(self) -> int:
+        return lib().fh_gemv_plan_launches(self._h)
+
+    def bytes(self) -> int:
+        return lib().fh_gemv_plan_bytes(self._h)
+
+    def free(self) -> None:
+        if self._h:
+            lib().fh_gemv_plan_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def q8_snap_rows(gpu: Gpu, src: GpuBuf, dst: GpuBuf, ne0: int) -> None:
+    """ferrum_wgpu/src/ops/qat.rs:21-29"""
+    _check(lib().fh_q8_snap_rows(gpu.handle, src.handle, dst.handle, ne0))
+
+
+def q8_snap_cols(gpu: Gpu, src: GpuBuf, dst: GpuBuf, shape: tuple[int, int]) -> None:
+    """ferrum_wgpu/src/ops/qat.rs:33-57"""
+    rows_in, cols_out = shape
+    _check(lib().fh_q8_snap_cols(gpu.handle, src.handle, dst.handle, rows_in, cols_out))

@@ -1,0 +1,188 @@
+/* ferrum_hip: MI355X-native (gfx950) quantized-weight path for ferrum-gpu.
+ *
+ * C ABI over hand-written HIP kernels. It is a drop-in for ferrum_wgpu's `ops_quant` and
+ * `ops_qat` modules and the slice of the `Gpu`/`GpuBuf` device layer they use. Every entry point
+ * names the reference interface it replaces (paths relative to the ferrum-gpu repository).
+ * Plain pointers, sizes and opaque handles only; no C++ or HIP types cross the boundary.
+ *
+ * Formats: GGUF Q8_0 (34-byte blocks: f16 scale + 32 x i8) and Q4_0 (18-byte blocks: f16 scale
+ * + 16 bytes, byte j holds element j in its low nibble and element j+16 in its high nibble),
+ * blocks of 32 along the input dimension. A quantized weight W of k inputs and n outputs is
+ * resident as GGUF rows: n rows of k/32 blocks, byte-for-byte the tensor data of a GGUF file.
+ *
+ * Errors: every call returns an fh_status; on failure fh_last_error() (thread-local) holds a
+ * message carrying the same substrings the reference's GpuError texts carry, so tests can match
+ * them: "linear_q x", "linear_q y", "one row", "whole", "needs", "injected fault",
+ * "GPU out of memory", "destination", "is not". A device fault makes the device "lost"
+ * (sticky). Nothing aborts the process.
+ *
+ * Ordering: each device owns one HIP stream. Calls enqueue asynchronously and in order on it
+ * (ferrum_wgpu/src/device/runtime.rs:152-192); results are observed by the reading calls, which
+ * synchronize (device/tensor.rs:128-160).
+ */
+#ifndef FERRUM_HIP_H
+#define FERRUM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FH_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define FH_API __attribute__((visibility("default")))
+#else
+#define FH_API
+#endif
+
+typedef enum fh_status {
+    FH_OK = 0,
+    FH_ERR_INVALID = 1,     /* bad argument or shape */
+    FH_ERR_UNSUPPORTED = 2, /* a block format other than Q8_0 / Q4_0 */
+    FH_ERR_DEVICE = 3,      /* HIP runtime error */
+    FH_ERR_OOM = 4,         /* "GPU out of memory" */
+    FH_ERR_INJECTED = 5,    /* "injected fault" from fh_debug_fail_after */
+    FH_ERR_LOST = 6         /* the device faulted earlier; sticky */
+} fh_status;
+
+/* Block formats, by ggml tensor type id (ferrum_gguf/src/lib.rs:43,55). Replaces
+ * ferrum_wgpu::ops_quant::QKind::{Q8_0, Q4_0} (ferrum_wgpu/src/ops/quant.rs:27-37). */
+typedef enum fh_kind { FH_Q4_0 = 2, FH_Q8_0 = 8 } fh_kind;
+
+/* Which kernel runs a quantized linear layer. Replaces QPath (ferrum_wgpu/src/ops/quant.rs:292-305):
+ * NAIVE = one thread per output (the baseline kernel), GEMV = batch-1 wavefront GEMV (exactly one
+ * row), TILED = the LDS-staged MFMA dequant-GEMM (any rows), AUTO = fh_choose. */
+typedef enum fh_path {
+    FH_PATH_AUTO = 0,
+    FH_PATH_NAIVE = 1,
+    FH_PATH_GEMV = 2,
+    FH_PATH_TILED = 3
+} fh_path;
+
+typedef struct fh_device fh_device;   /* replaces ferrum_wgpu::device::Gpu */
+typedef struct fh_buffer fh_buffer;   /* replaces ferrum_wgpu::tensor::GpuBuf (plus byte buffers) */
+typedef struct fh_qweight fh_qweight; /* replaces ferrum_wgpu::ops_quant::QWeight */
+typedef struct fh_gemv_plan fh_gemv_plan;
+
+/* ---- errors and version ---- */
+FH_API const char *fh_last_error(void); /* thread-local message of this thread's last failure */
+FH_API int fh_abi_version(void);
+
+/* ---- device (ferrum_wgpu/src/device/mod.rs:127-165 Gpu::open; runtime.rs:67-93 check) ---- */
+FH_API fh_status fh_device_open(int ordinal, fh_device **out);
+FH_API void fh_device_close(fh_device *dev);
+/* Wait for every command enqueued so far (the reference waits inside Gpu::read). */
+FH_API fh_status fh_device_sync(fh_device *dev);
+/* Adapter name and compute-unit count (device/mod.rs:88-95 AdapterInfo). */
+FH_API fh_status fh_device_info(fh_device *dev, char *name, size_t cap, int *compute_units);
+/* The device's HIP stream (a hipStream_t) for callers that interleave their own work. */
+FH_API void *fh_device_stream(fh_device *dev);
+/* Test hook: the n-th command from now fails with "injected fault"; n < 0 disarms
+ * (device/runtime.rs:218-240 Gpu::fail_after). */
+FH_API void fh_debug_fail_after(fh_device *dev, int64_t n);
+/* Commands (kernel launches and copies) issued so far on this device (runtime.rs:127-135). */
+FH_API uint64_t fh_debug_commands(fh_device *dev);
+
+/* ---- buffers (ferrum_wgpu/src/device/tensor.rs:7-160) ---- */
+/* f32 buffer of len zeros (Gpu::zeros, tensor.rs:36-66). */
+FH_API fh_status fh_buffer_zeros(fh_device *dev, size_t len, fh_buffer **out);
+/* f32 buffer holding host[0..len) (Gpu::upload, tensor.rs:69-101). */
+FH_API fh_status fh_buffer_upload(fh_device *dev, const float *host, size_t len, fh_buffer **out);
+/* Copy the whole buffer to host (len must equal its length); synchronizes (Gpu::read). */
+FH_API fh_status fh_buffer_read(fh_device *dev, const fh_buffer *buf, float *host, size_t len);
+/* Overwrite the whole buffer from host (queue.write_buffer). */
+FH_API fh_status fh_buffer_write(fh_device *dev, fh_buffer *buf, const float *host, size_t len);
+/* Byte buffers hold packed blocks for the device codec. */
+FH_API fh_status fh_bytes_zeros(fh_device *dev, size_t nbytes, fh_buffer **out);
+FH_API fh_status fh_bytes_upload(fh_device *dev, const uint8_t *host, size_t nbytes, fh_buffer **out);
+FH_API fh_status fh_bytes_read(fh_device *dev, const fh_buffer *buf, uint8_t *host, size_t nbytes);
+FH_API size_t fh_buffer_len(const fh_buffer *buf);    /* f32 elements (nbytes / 4) */
+FH_API size_t fh_buffer_nbytes(const fh_buffer *buf);
+FH_API void *fh_buffer_device_ptr(const fh_buffer *buf);
+FH_API void fh_buffer_free(fh_buffer *buf);
+/* dst[dst_off..+len) = src[src_off..+len) in f32 elements (Gpu::copy_f32, runtime.rs:294-336). */
+FH_API fh_status fh_copy_f32(fh_device *dev, const fh_buffer *src, size_t src_off, fh_buffer *dst,
+                      size_t dst_off, size_t len);
+
+/* ---- block codec on the device (ferrum_gguf/src/codec/quant.rs) ---- */
+/* Bytes n elements occupy, 0 with an error for an unsupported kind or n not whole blocks
+ * (quant.rs:17-47). */
+FH_API size_t fh_nbytes(fh_kind kind, size_t n);
+/* Encode n f32 values (blocks of 32 consecutive values) into GGUF blocks (quant::encode,
+ * quant.rs:91-136), bit-exact. src holds >= n floats, dst >= fh_nbytes bytes. */
+FH_API fh_status fh_encode(fh_device *dev, fh_kind kind, const fh_buffer *src, size_t n, fh_buffer *dst);
+/* Decode n elements of GGUF blocks to f32 (quant::decode, quant.rs:50-88), bit-exact. */
+FH_API fh_status fh_decode(fh_device *dev, fh_kind kind, const fh_buffer *src, size_t n, fh_buffer *dst);
+
+/* ---- resident quantized weights (ferrum_wgpu/src/ops/quant.rs:155-288) ---- */
+/* upload_qweight (quant.rs:267-277): bytes are GGUF rows, n rows of k/32 blocks; kept bit-exact.
+ * Errors: "whole" when k is not a positive multiple of 32, "needs" when len is wrong. */
+FH_API fh_status fh_qweight_upload_gguf(fh_device *dev, fh_kind kind, const uint8_t *bytes, size_t len,
+                                 size_t k, size_t n, fh_qweight **out);
+/* upload_quantised (quant.rs:279-288): w is the [k, n] (in, out) row-major f32 weight on the
+ * host; it is uploaded and quantised on the device (transpose + encode, quantise_matrix). */
+FH_API fh_status fh_qweight_upload_f32(fh_device *dev, fh_kind kind, const float *w, size_t k, size_t n,
+                                fh_qweight **out);
+/* quantise_matrix on the device (quant.rs:238-252) from a resident [k, n] f32 buffer. */
+FH_API fh_status fh_qweight_quantise(fh_device *dev, fh_kind kind, const fh_buffer *w, size_t k,
+                              size_t n, fh_qweight **out);
+FH_API void fh_qweight_free(fh_qweight *w);
+/* QWeight::{kind, k, n, device_bytes} (quant.rs:163-182). */
+FH_API fh_kind fh_qweight_kind(const fh_qweight *w);
+FH_API size_t fh_qweight_k(const fh_qweight *w);
+FH_API size_t fh_qweight_n(const fh_qweight *w);
+FH_API uint64_t fh_qweight_device_bytes(const fh_qweight *w);
+/* The resident GGUF bytes, read back bit-exactly (len must equal n * k/32 * block bytes). */
+FH_API fh_status fh_qweight_read_gguf(fh_device *dev, const fh_qweight *w, uint8_t *host, size_t len);
+/* dequantise_bytes + transpose on the device: out = the [k, n] f32 weight the CPU multiplies by
+ * (quant.rs:256-264; models/llama/mod.rs:188-213). out holds k*n floats. */
+FH_API fh_status fh_qweight_dequantise(fh_device *dev, const fh_qweight *w, fh_buffer *out);
+
+/* ---- quantized linear layers (ferrum_wgpu/src/ops/quant.rs:306-381) ---- */
+/* choose (quant.rs:306-323): the kernel AUTO picks for rows x (k, n), from MI355X measurements. */
+FH_API fh_path fh_choose(size_t rows, fh_kind kind, size_t k, size_t n);
+/* linear_q / linear_q_with: y[rows, n] = x[rows, k] * W, W dequantized in the kernel, no bias.
+ * x must hold exactly rows*k floats ("linear_q x"), y exactly rows*n ("linear_q y"); y is
+ * overwritten. GEMV takes exactly one row ("one row"). One command; does not wait. */
+FH_API fh_status fh_linear_q(fh_device *dev, const fh_buffer *x, const fh_qweight *w, fh_buffer *y,
+                      size_t rows, fh_path path);
+/* The same product on raw device pointers (x: rows*k floats, y: rows*n floats), for callers that
+ * own their memory (a torch tensor, a KV-cache arena). Same checks on rows and shapes. */
+FH_API fh_status fh_linear_q_ptr(fh_device *dev, const float *x, const fh_qweight *w, float *y,
+                          size_t rows, fh_path path);
+
+/* No counterpart in the reference: one launch for many independent batch-1 products
+ * y_i = x_i * W_i (a decode step's projections, or several models' layers). The plan is built
+ * once (the descriptors are uploaded then) and run any number of times; x_i and y_i are device
+ * pointers of k_i and n_i floats. Products with the same block format and input width class
+ * share a launch. */
+typedef struct fh_gemv_problem {
+    const fh_qweight *w;
+    const float *x;
+    float *y;
+} fh_gemv_problem;
+FH_API fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, size_t count,
+                              fh_gemv_plan **out);
+FH_API fh_status fh_gemv_plan_run(fh_device *dev, const fh_gemv_plan *plan);
+/* Launches one run issues, and the algorithmic bytes it moves (weights + x + y). */
+FH_API size_t fh_gemv_plan_launches(const fh_gemv_plan *plan);
+FH_API uint64_t fh_gemv_plan_bytes(const fh_gemv_plan *plan);
+FH_API void fh_gemv_plan_free(fh_gemv_plan *plan);
+
+/* ---- quantisation-aware training snap (ferrum_wgpu/src/ops/qat.rs:21-57) ---- */
+/* q8_snap_rows: snap src into dst along rows (blocks of 32 consecutive values). ne0 not a
+ * positive multiple of 32, or a length that is not whole blocks, copies unchanged.
+ * "destination" when the lengths differ. Bit-exact with decode(encode(block)). */
+FH_API fh_status fh_q8_snap_rows(fh_device *dev, const fh_buffer *src, fh_buffer *dst, size_t ne0);
+/* q8_snap_cols: snap an [rows_in, cols_out] row-major weight down its columns. "is not" when
+ * the length is not rows_in*cols_out; rows_in not a multiple of 32 copies unchanged. */
+FH_API fh_status fh_q8_snap_cols(fh_device *dev, const fh_buffer *src, fh_buffer *dst, size_t rows_in,
+                          size_t cols_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

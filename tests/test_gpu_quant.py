@@ -1,0 +1,320 @@
+"""GPU parity tests for the quantized linear path, through the C ABI (via the Python mirror of
+ferrum_wgpu's ops_quant). Each test names the reference test it mirrors. The oracle is the C
+restatement under oracle/ (pinned by tests/test_oracle.py).
+
+Tolerances (written here, as in ferrum_wgpu/src/tolerance.rs):
+  * dequantised values and the device codec: bit-exact;
+  * every linear_q kernel (GEMV, naive, MFMA GEMM): max_rel_err < REDUCING = 1e-5 against the
+    CPU matmul on the dequantised weights;
+  * the MFMA GEMM at the scoring shapes additionally: |g - w| <= 1e-3 + 2e-3 |w| everywhere.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+REDUCING = 1e-5
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def fh():
+    import ferrum_hip
+
+    return ferrum_hip
+
+
+@pytest.fixture(scope="module")
+def g(fh):
+    gpu = fh.Gpu.open_for_test()
+    if gpu is None:
+        pytest.skip("no gfx950 device")
+    say("device:", gpu.info())
+    yield gpu
+    gpu.close()
+
+
+KINDS = None
+
+
+def kinds(fh):
+    return [fh.QKind.Q8_0, fh.QKind.Q4_0]
+
+
+def nasty(orc, n):
+    """ferrum_wgpu/src/ops/quant/tests.rs:11-23"""
+    v = orc.rand_vec(n, 9) * np.float32(3.0)
+    i = np.arange(n)
+    sel = (i // 32) % 7
+    v = np.where(sel == 0, v * np.float32(1e-6), v)
+    v = np.where(sel == 1, np.float32(0), v)
+    v = np.where(sel == 2, v * np.float32(1e4), v)
+    v = np.where(sel == 3, (i % 9).astype(np.float32) - np.float32(4), v)
+    return v.astype(np.float32)
+
+
+def cpu_linear(orc, kind, gguf, x, rows, k, n):
+    """What the reference's CPU path computes: matmul on transpose(decode(bytes))."""
+    w = orc.dequantised_in_out(int(kind), gguf, k, n)
+    if rows * k * n > 5e7:
+        return orc.matmul_tuned(x, w, rows, k, n, 8)
+    return orc.matmul(x, w, rows, k, n)
+
+
+# ---- quant.rs tests ----
+
+def test_pack_and_quantise_refuse_bad_shapes(fh, g):
+    """ops/quant/tests.rs:74-87"""
+    for kind in kinds(fh):
+        with pytest.raises(fh.GpuError, match="whole"):
+            fh.upload_qweight(g, kind, np.zeros(100, np.uint8), 33, 1)
+        with pytest.raises(fh.GpuError, match="needs"):
+            fh.upload_qweight(g, kind, np.zeros(3, np.uint8), 32, 1)
+        with pytest.raises(fh.GpuError):
+            fh.upload_quantised(g, kind, np.zeros(33, np.float32), 33, 1)
+        with pytest.raises(fh.GpuError):
+            fh.upload_quantised(g, kind, np.zeros(63, np.float32), 32, 2)
+
+
+def test_resident_bytes_are_the_gguf_bytes_and_the_size_is_the_file_size(fh, g, orc):
+    """ops/quant/tests.rs:182-198 (our resident layout is the GGUF bytes themselves: 34 / 18
+    bytes per 32 weights, against the reference's widened 36 / 20)."""
+    k, n = 64, 32
+    w = orc.rand_vec(k * n, 1)
+    for kind, ratio in [(fh.QKind.Q8_0, 128 / 34), (fh.QKind.Q4_0, 128 / 18)]:
+        b = orc.quantise_matrix(int(kind), w, k, n)
+        qw = fh.upload_qweight(g, kind, b, k, n)
+        assert np.array_equal(qw.read_gguf(), b)
+        assert abs(k * n * 4 / qw.device_bytes() - ratio) < 1e-9
+        assert (qw.k(), qw.n(), qw.kind()) == (k, n, kind)
+
+
+def test_device_quantise_matrix_is_bit_exact(fh, g, orc):
+    """upload_quantised encodes on the device; the bytes must equal quantise_matrix's."""
+    for kind in kinds(fh):
+        for k, n in [(32, 1), (64, 7), (96, 40), (256, 9), (768, 130)]:
+            say("quantise_matrix", kind.label(), k, n)
+            w = nasty(orc, k * n)
+            qw = fh.upload_quantised(g, kind, w, k, n)
+            assert np.array_equal(qw.read_gguf(), orc.quantise_matrix(int(kind), w, k, n)), (kind, k, n)
+
+
+def test_requantising_dequantised_weights_reproduces_the_values(fh, g, orc):
+    """ops/quant/tests.rs:90-104, on the device (dequantise + quantise kernels)."""
+    for kind in kinds(fh):
+        for k, n in [(32, 1), (64, 7), (96, 40), (256, 9)]:
+            qw = fh.upload_quantised(g, kind, nasty(orc, k * n), k, n)
+            deq = qw.dequantised()
+            again = fh.upload_quantised(g, kind, deq, k, n).dequantised()
+            assert np.array_equal(again.view(np.uint32), deq.view(np.uint32)), (kind, k, n)
+
+
+def test_dequantised_values_are_bit_identical_to_the_cpu_decode(fh, g, orc):
+    """ops/quant/tests.rs:107-131: x = identity reads the weight back through linear_q, on every
+    multi-row kernel; and the dequantise kernel gives the same bits."""
+    for kind in kinds(fh):
+        for k, n in [(32, 1), (32, 5), (64, 3), (96, 65), (128, 64)]:
+            b = orc.quantise_matrix(int(kind), nasty(orc, k * n), k, n)
+            want = orc.dequantised_in_out(int(kind), b, k, n)  # [k, n]
+            qw = fh.upload_qweight(g, kind, b, k, n)
+            assert np.array_equal(qw.dequantised().view(np.uint32), want.view(np.uint32))
+            eye = np.eye(k, dtype=np.float32)
+            for path in (fh.QPath.Naive, fh.QPath.Tiled, fh.QPath.Auto):
+                say("identity readback", kind.label(), k, n, path.name)
+                gx, gy = g.upload(eye), g.zeros(k * n)
+                fh.linear_q_with(g, gx, qw, gy, k, path)
+                got = g.read(gy)
+                assert np.array_equal(got, want), (kind, k, n, path)
+
+
+def test_linear_matches_the_cpu_matmul_on_the_dequantised_weights(fh, g, orc):
+    """ops/quant/tests.rs:134-157"""
+    for kind in kinds(fh):
+        for rows, k, n in [(1, 32, 1), (1, 256, 100), (7, 96, 13), (33, 64, 65), (2, 512, 3)]:
+            w = orc.rand_vec(k * n, 4)
+            b = orc.quantise_matrix(int(kind), w, k, n)
+            x = orc.rand_vec(rows * k, 5)
+            want = cpu_linear(orc, kind, b, x, rows, k, n)
+            qw = fh.upload_qweight(g, kind, b, k, n)
+            gx, gy = g.upload(x), g.zeros(rows * n)
+            say("linear_q", kind.label(), rows, k, n)
+            fh.linear_q(g, gx, qw, gy, rows)
+            e = orc.max_rel_err(g.read(gy), want)
+            say(f"  max rel err {e:.2e} (tol {REDUCING:.0e})")
+            assert e < REDUCING, (kind, rows, k, n, e)
+
+
+def test_every_kernel_matches_the_cpu_matmul_on_awkward_shapes(fh, g, orc):
+    """ops/quant/tests.rs:272-304"""
+    for kind in kinds(fh):
+        for rows, k, n in [(1, 32, 1), (1, 96, 17), (1, 512, 70), (17, 64, 1), (33, 96, 17),
+                           (16, 32, 16), (3, 256, 40), (1, 8192, 33), (1, 8224, 20), (5, 8224, 9)]:
+            w = orc.rand_vec(k * n, 6)
+            b = orc.quantise_matrix(int(kind), w, k, n)
+            x = orc.rand_vec(rows * k, 9)
+            want = cpu_linear(orc, kind, b, x, rows, k, n)
+            qw = fh.upload_qweight(g, kind, b, k, n)
+            paths = [fh.QPath.Naive, fh.QPath.Tiled, fh.QPath.Auto]
+            if rows == 1 and k <= 8192:
+                paths.append(fh.QPath.Gemv)
+            for path in paths:
+                say("kernel", kind.label(), path.name, rows, k, n)
+                gx, gy = g.upload(x), g.zeros(rows * n)
+                fh.linear_q_with(g, gx, qw, gy, rows, path)
+                e = orc.max_rel_err(g.read(gy), want)
+                assert e < REDUCING, (kind, path, rows, k, n, e)
+
+
+def test_quantised_output_stays_close_to_the_f32_product(fh, g, orc):
+    """ops/quant/tests.rs:160-179 (sanity bounds, not tolerances)."""
+    rows, k, n = 4, 256, 64
+    w, x = orc.rand_vec(k * n, 7), orc.rand_vec(rows * k, 8)
+    exact = orc.matmul(x, w, rows, k, n)
+
+    def err(kind):
+        qw = fh.upload_quantised(g, kind, w, k, n)
+        gx, gy = g.upload(x), g.zeros(rows * n)
+        fh.linear_q(g, gx, qw, gy, rows)
+        return orc.max_rel_err(g.read(gy), exact)
+
+    e8, e4 = err(fh.QKind.Q8_0), err(fh.QKind.Q4_0)
+    say(f"quantised vs f32 product: q8 {e8:.2e}, q4 {e4:.2e}")
+    assert e8 < 0.15 and e4 < 2.0 and e8 * 5 < e4
+
+
+def test_linear_refuses_mismatched_buffers_and_fails_cleanly(fh, g, orc):
+    """ops/quant/tests.rs:200-215 and :306-315"""
+    qw = fh.upload_quantised(g, fh.QKind.Q8_0, orc.rand_vec(64 * 4, 1), 64, 4)
+    x, y = g.zeros(2 * 64), g.zeros(2 * 4)
+    with pytest.raises(fh.GpuError, match="linear_q x"):
+        fh.linear_q(g, x, qw, y, 3)
+    with pytest.raises(fh.GpuError, match="linear_q y"):
+        fh.linear_q(g, x, qw, g.zeros(7), 2)
+    assert g.sweep_faults(lambda: fh.linear_q(g, x, qw, y, 2)) == 1
+    with pytest.raises(fh.GpuError, match="one row"):
+        fh.linear_q_with(g, x, qw, y, 2, fh.QPath.Gemv)
+    with pytest.raises(fh.GpuError):
+        fh.upload_quantised(g, fh.QKind.Q4_0, np.zeros(33, np.float32), 33, 1)
+
+
+def test_every_f16_scale_dequantises_exactly(fh, g, orc):
+    """All 65536 half-precision scales through the GEMV: row r is one Q8_0 block whose scale is
+    half r and whose first quant is 1, x = e0, so y[r] = f16_to_f32(r) (NaN rows: NaN)."""
+    n = 65536
+    blocks = np.zeros((n, 34), np.uint8)
+    blocks[:, 0] = np.arange(n) & 0xFF
+    blocks[:, 1] = np.arange(n) >> 8
+    blocks[:, 2] = 1
+    x = np.zeros(32, np.float32)
+    x[0] = 1.0
+    want = orc.f16_to_f32_array(np.arange(n, dtype=np.uint16))
+    qw = fh.upload_qweight(g, fh.QKind.Q8_0, blocks.reshape(-1), 32, n)
+    for path in (fh.QPath.Gemv, fh.QPath.Naive):
+        gx, gy = g.upload(x), g.zeros(n)
+        fh.linear_q_with(g, gx, qw, gy, 1, path)
+        got = g.read(gy)
+        fin = ~np.isnan(want)
+        assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32)), path
+        assert np.all(np.isnan(got[~fin])), path
+
+
+# ---- BASELINE.json configs ----
+
+def test_config1_q8_0_gemv_gpt2_qkv(fh, g, orc):
+    """Config 1: x ~ N(0,1) [768], W ~ N(0,0.02) [768 x 2304] packed Q8_0; GEMV within 1e-5;
+    the pack and dequant round trip bit-exact against the oracle."""
+    rng = np.random.default_rng(1)
+    k, n = 768, 2304
+    x = rng.standard_normal(k).astype(np.float32)
+    w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+    b = orc.quantise_matrix(orc.Q8_0, w, k, n)
+    qw = fh.upload_quantised(g, fh.QKind.Q8_0, w, k, n)
+    assert np.array_equal(qw.read_gguf(), b)
+    want_w = orc.dequantised_in_out(orc.Q8_0, b, k, n)
+    assert np.array_equal(qw.dequantised().view(np.uint32), want_w.view(np.uint32))
+    want = orc.gemv(x, want_w, None, k, n)
+    gx, gy = g.upload(x), g.zeros(n)
+    fh.linear_q_with(g, gx, qw, gy, 1, fh.QPath.Gemv)
+    e = orc.max_rel_err(g.read(gy), want)
+    say(f"config1 GEMV max rel err {e:.2e}")
+    assert e < REDUCING
+
+
+@pytest.mark.parametrize("k,n", [(896, 1152), (896, 4864), (4864, 896)])
+def test_config2_q4_0_gemv_sweep(fh, g, orc, k, n):
+    rng = np.random.default_rng(k + n)
+    x = rng.standard_normal(k).astype(np.float32)
+    w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+    b = orc.quantise_matrix(orc.Q4_0, w, k, n)
+    qw = fh.upload_qweight(g, fh.QKind.Q4_0, b, k, n)
+    want = orc.gemv(x, orc.dequantised_in_out(orc.Q4_0, b, k, n), None, k, n)
+    gx, gy = g.upload(x), g.zeros(n)
+    fh.linear_q_with(g, gx, qw, gy, 1, fh.QPath.Gemv)
+    e = orc.max_rel_err(g.read(gy), want)
+    say(f"config2 Q4_0 GEMV {k}x{n} max rel err {e:.2e}")
+    assert e < REDUCING
+
+
+@pytest.mark.parametrize("kind_name,m,k,n", [
+    ("Q4_0", 512, 896, 1152), ("Q4_0", 512, 896, 4864), ("Q4_0", 512, 4864, 896),
+    ("Q8_0", 64, 2048, 5632), ("Q4_0", 8, 5632, 2048), ("Q8_0", 512, 5632, 256)])
+def test_gemm_scoring_shapes_meet_both_tolerances(fh, g, orc, kind_name, m, k, n):
+    kind = fh.QKind[kind_name]
+    rng = np.random.default_rng(m + k + n)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+    b = orc.quantise_matrix(int(kind), w, k, n)
+    want = cpu_linear(orc, kind, b, x, m, k, n)
+    qw = fh.upload_qweight(g, kind, b, k, n)
+    gx, gy = g.upload(x), g.zeros(m * n)
+    say("gemm", kind_name, m, k, n)
+    fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.Tiled)
+    got = g.read(gy)
+    err = np.abs(got - want)
+    viol = np.mean(err > 1e-3 + 2e-3 * np.abs(want))
+    e = orc.max_rel_err(got, want)
+    say(f"  max abs {err.max():.2e}, max rel {e:.2e}, violations {viol:.2e}")
+    assert viol == 0 and e < REDUCING
+
+
+def test_grouped_gemv_plan_equals_single_launches(fh, g, orc):
+    """The grouped launch runs the same per-row code: results are bit-identical to linear_q."""
+    rng = np.random.default_rng(5)
+    probs, singles, keep = [], [], []
+    for i, (kind, k, n) in enumerate([(fh.QKind.Q4_0, 896, 1152), (fh.QKind.Q4_0, 896, 300),
+                                      (fh.QKind.Q8_0, 768, 2304), (fh.QKind.Q4_0, 4864, 896),
+                                      (fh.QKind.Q8_0, 4096, 77), (fh.QKind.Q4_0, 2048, 65)]):
+        w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+        x = rng.standard_normal(k).astype(np.float32)
+        qw = fh.upload_quantised(g, kind, w, k, n)
+        gx, gy, gs = g.upload(x), g.zeros(n), g.zeros(n)
+        fh.linear_q_with(g, gx, qw, gs, 1, fh.QPath.Gemv)
+        probs.append((qw, gx.device_ptr(), gy.device_ptr()))
+        singles.append((gy, gs))
+        keep += [qw, gx, gy, gs]
+    plan = fh.GemvPlan(g, probs)
+    assert plan.launches() >= 3
+    plan.run()
+    for gy, gs in singles:
+        assert np.array_equal(g.read(gy), g.read(gs))
+    plan.free()
+
+
+def test_large_gemv_is_linear_in_x(fh, g, orc):
+    """Size-independent property at a full decode-head size (Qwen2 vocab 151936 x 896, Q4_0):
+    y(x1) + y(x2) = y(x1 + x2) within f32 rounding, and y(2x) = 2 y(x) exactly."""
+    rng = np.random.default_rng(9)
+    k, n = 896, 151936
+    w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+    qw = fh.upload_quantised(g, fh.QKind.Q4_0, w, k, n)
+    x1, x2 = rng.standard_normal(k).astype(np.float32), rng.standard_normal(k).astype(np.float32)
+    outs = []
+    for x in (x1, x2, x1 + x2, 2 * x1):
+        gx, gy = g.upload(x), g.zeros(n)
+        fh.linear_q(g, gx, qw, gy, 1)
+        outs.append(g.read(gy))
+    assert np.max(np.abs(outs[0] + outs[1] - outs[2])) < 1e-4 * max(1, np.abs(outs[2]).max())
+    assert np.array_equal(outs[3], 2 * outs[0])
