@@ -17,6 +17,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -30,6 +31,8 @@ sys.path[:0] = [REPO, os.path.join(REPO, "ferrum-gpu_amd")]
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 QWEN_SHAPES = [(896, 1152), (896, 4864), (4864, 896)]
+# one grouped launch per input width (the two 896-wide products share a kernel instantiation)
+QWEN_GROUPS = [[(896, 1152), (896, 4864)], [(4864, 896)]]
 
 
 def log(*a):
@@ -41,63 +44,108 @@ def gemv_bytes(kind_bytes: int, k: int, n: int) -> int:
     return (k // 32) * n * kind_bytes + 4 * k + 4 * n
 
 
-class Timer:
-    """HIP events on the library's own stream (the stream the kernels run on)."""
+class HipEvents:
+    """HIP events recorded on the library's own stream (the one its kernels run on), through the
+    HIP runtime libferrum_hip already loaded (RTLD_NOLOAD: never a second runtime)."""
 
     def __init__(self, g):
-        import torch
+        self.hip = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD | ctypes.RTLD_GLOBAL)
+        self.stream = ctypes.c_void_p(g.stream())
+        for name in ("hipEventCreate", "hipEventRecord", "hipEventSynchronize", "hipEventElapsedTime",
+                     "hipEventDestroy"):
+            getattr(self.hip, name).restype = ctypes.c_int
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
 
-        self.torch = torch
-        self.stream = torch.cuda.ExternalStream(g.stream())
+    def create(self, n):
+        evs = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            if self.hip.hipEventCreate(ctypes.byref(e)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            evs.append(e)
+        return evs
 
-    def event(self):
-        e = self.torch.cuda.Event(enable_timing=True)
-        e.record(self.stream)
-        return e
+    def record(self, e):
+        if self.hip.hipEventRecord(e, self.stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def ms(self, e0, e1):
+        if self.hip.hipEventSynchronize(e1) != 0:
+            raise RuntimeError("hipEventSynchronize failed")
+        out = ctypes.c_float()
+        if self.hip.hipEventElapsedTime(ctypes.byref(out), e0, e1) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return out.value
+
+    def destroy(self, evs):
+        for e in evs:
+            self.hip.hipEventDestroy(e)
 
 
-def bench_gemv_pool(fh, g, timer, kind, shapes, pool_bytes, steps, warmup, seed=0):
+def bench_gemv_pool(fh, g, ev, kind, groups, pool_bytes, steps, warmup, seed=0):
+    """Batch-1 GEMV over a pool of distinct resident weights. `groups` is a list of shape lists;
+    each group becomes one grouped launch (one plan) per step, timed with its own pair of HIP
+    events, so each launch's average duration is known as well as the step's."""
     rng = np.random.default_rng(seed)
     kb = kind.file_bytes()
+    shapes = [s for grp in groups for s in grp]
     set_bytes = sum((k // 32) * n * kb for k, n in shapes)
     copies = max(1, int(pool_bytes // set_bytes))
-    packed = []  # packed once on the device, then uploaded as distinct copies
+    packed = {}  # packed once on the device, then uploaded as distinct copies
     for k, n in shapes:
         w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
-        packed.append(fh.upload_quantised(g, kind, w, k, n).read_gguf())
-    keep, probs = [], []
-    for c in range(copies):
-        for (k, n), b in zip(shapes, packed):
-            qw = fh.upload_qweight(g, kind, b, k, n)
-            gx = g.upload(rng.standard_normal(k).astype(np.float32))
-            gy = g.zeros(n)
-            keep += [qw, gx, gy]
-            probs.append((qw, gx.device_ptr(), gy.device_ptr()))
-    plan = fh.GemvPlan(g, probs)
-    step_bytes = plan.bytes()
+        packed[(k, n)] = fh.upload_quantised(g, kind, w, k, n).read_gguf()
+    keep, plans = [], []
+    for grp in groups:
+        probs = []
+        for c in range(copies):
+            for k, n in grp:
+                qw = fh.upload_qweight(g, kind, packed[(k, n)], k, n)
+                gx = g.upload(rng.standard_normal(k).astype(np.float32))
+                gy = g.zeros(n)
+                keep += [qw, gx, gy]
+                probs.append((qw, gx.device_ptr(), gy.device_ptr()))
+        plans.append(fh.GemvPlan(g, probs))
+    for p in plans:
+        assert p.launches() == 1, "each group must be one launch"
     for _ in range(warmup):
-        plan.run()
+        for p in plans:
+            p.run()
     g.sync()
+    npl = len(plans)
+    evs = ev.create(steps * (npl + 1))
     t0 = time.perf_counter()
-    e0 = timer.event()
-    for _ in range(steps):
-        plan.run()
-    e1 = timer.event()
+    for s in range(steps):
+        for i, p in enumerate(plans):
+            ev.record(evs[s * (npl + 1) + i])
+            p.run()
+        ev.record(evs[s * (npl + 1) + npl])
     g.sync()
     wall = time.perf_counter() - t0
-    ev_ms = e0.elapsed_time(e1)
-    res = {
-        "copies": copies, "products": len(probs), "launches_per_step": plan.launches(),
-        "bytes_per_step": step_bytes, "ms_per_step": ev_ms / steps,
-        "wall_ms_per_step": wall * 1e3 / steps,
-        "gbs": step_bytes * steps / (ev_ms * 1e-3) / 1e9,
-    }
-    plan.free()
+    launch_ms = [[ev.ms(evs[s * (npl + 1) + i], evs[s * (npl + 1) + i + 1]) for s in range(steps)]
+                 for i in range(npl)]
+    step_ms = ev.ms(evs[0], evs[-1]) / steps  # first event of step 0 to the last of the last step
+    ev.destroy(evs)
+    step_bytes = sum(p.bytes() for p in plans)
+    launches = []
+    for grp, p, ms in zip(groups, plans, launch_ms):
+        avg = float(np.mean(ms))
+        launches.append({"shapes": grp, "products": copies * len(grp), "bytes": p.bytes(),
+                         "avg_ms": avg, "gbs": p.bytes() / (avg * 1e-3) / 1e9})
+    for p in plans:
+        p.free()
     del keep
-    return res
+    return {"copies": copies, "products": copies * len(shapes), "launches_per_step": npl,
+            "bytes_per_step": step_bytes, "ms_per_step": step_ms,
+            "wall_ms_per_step": wall * 1e3 / steps,
+            "gbs": step_bytes / (step_ms * 1e-3) / 1e9, "launches": launches}
 
 
-def bench_gemm(fh, g, timer, kind, m, shapes, steps, seed=0):
+def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0):
     rng = np.random.default_rng(seed)
     items = []
     for k, n in shapes:
@@ -110,13 +158,15 @@ def bench_gemm(fh, g, timer, kind, m, shapes, steps, seed=0):
     for qw, gx, gy in items:
         fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.Tiled)
     g.sync()
-    e0 = timer.event()
+    e0, e1 = ev.create(2)
+    ev.record(e0)
     for _ in range(steps):
         for qw, gx, gy in items:
             fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.Tiled)
-    e1 = timer.event()
+    ev.record(e1)
     g.sync()
-    ms = e0.elapsed_time(e1) / steps
+    ms = ev.ms(e0, e1) / steps
+    ev.destroy([e0, e1])
     return {"m": m, "flops_per_step": flops, "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
@@ -164,24 +214,28 @@ def main():
     import ferrum_hip as fh
 
     g = fh.Gpu(0)
-    timer = Timer(g)
+    ev = HipEvents(g)
     name, cus = g.info()
     log(f"device {name}, {cus} CUs")
 
-    head = bench_gemv_pool(fh, g, timer, fh.QKind.Q4_0, QWEN_SHAPES, a.pool_gib * 2**30, a.steps, a.warmup)
+    head = bench_gemv_pool(fh, g, ev, fh.QKind.Q4_0, QWEN_GROUPS, a.pool_gib * 2**30, a.steps, a.warmup)
     log("Q4_0 GEMV pool:", head)
     extra = {}
     if not a.no_extra:
-        q8 = bench_gemv_pool(fh, g, timer, fh.QKind.Q8_0, [(768, 2304)], a.pool_gib * 2**30, a.steps, a.warmup, seed=1)
+        q8 = bench_gemv_pool(fh, g, ev, fh.QKind.Q8_0, [[(768, 2304)]], a.pool_gib * 2**30, a.steps, a.warmup,
+                             seed=1)
         log("Q8_0 GEMV pool:", q8)
-        extra["q8_0_gemv_768x2304"] = {"gbs": q8["gbs"], "frac": q8["gbs"] / HBM_PEAK_GBS, "ms_per_step": q8["ms_per_step"],
-                                       "bytes_per_step": q8["bytes_per_step"]}
+        extra["q8_0_gemv_768x2304"] = {"gbs": round(q8["gbs"], 2), "frac": round(q8["gbs"] / HBM_PEAK_GBS, 4),
+                                       "ms_per_step": q8["ms_per_step"], "bytes_per_step": q8["bytes_per_step"],
+                                       "products_per_step": q8["products"]}
         for m in (512, 2048):
-            r = bench_gemm(fh, g, timer, fh.QKind.Q4_0, m, QWEN_SHAPES, 10)
+            r = bench_gemm(fh, g, ev, fh.QKind.Q4_0, m, QWEN_SHAPES, 10)
             log(f"Q4_0 GEMM M={m}:", r)
-            extra[f"q4_0_gemm_m{m}"] = {"tflops": r["tflops"], "frac": r["tflops"] / MFMA_F16_PEAK_TFLOPS,
+            extra[f"q4_0_gemm_m{m}"] = {"tflops": round(r["tflops"], 2),
+                                        "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                                         "ms_per_step": r["ms_per_step"], "flops_per_step": r["flops_per_step"],
-                                        "operands": "split-f16 x (hi+lo) x exact integer q, f32 accumulate, f32 block scale"}
+                                        "operands": "split-f16 x (hi+lo) x exact integer q, f32 accumulate, "
+                                                    "f32 block scale"}
 
     cpu = None
     if not a.no_cpu:
@@ -189,6 +243,7 @@ def main():
         log("cpu baseline:", cpu)
 
     gbs = head["gbs"]
+    dom = max(head["launches"], key=lambda L: L["avg_ms"])  # the launch that takes the most time
     out = {
         "metric": "Q4_0 batch-1 GEMV HBM GB/s at Qwen2-0.5B layer shapes",
         "value": round(gbs, 2),
@@ -205,8 +260,12 @@ def main():
         "config": {"workload": "Q4_0 GEMV sweep, K x N in {896x1152, 896x4864, 4864x896}, "
                                f"{head['copies']} distinct copies each ({head['bytes_per_step'] / 2**30:.2f} GiB per step)",
                    "products_per_step": head["products"], "launches_per_step": head["launches_per_step"]},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": f"grouped Q4_0 GEMV over {dom['shapes']} x {head['copies']}",
+                     "bytes_per_launch": dom["bytes"], "avg_launch_ms": round(dom["avg_ms"], 5)},
+        "launches": [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in L.items()}
+                     for L in head["launches"]],
         "cpu_baseline": cpu and {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "extra": extra,
     }

@@ -10,6 +10,9 @@
 
 #include "../../include/ferrum_hip.h"
 
+// A device lives until fh_device_close AND the last buffer, weight and plan made on it are
+// freed: each of those holds a reference (the reference shares Gpu through Arc, engine/gpu.rs:18-22),
+// so freeing a buffer after its device was closed is safe.
 struct fh_device {
     int ordinal = 0;
     hipStream_t stream = nullptr;
@@ -18,6 +21,8 @@ struct fh_device {
     std::atomic<int64_t> fail_after{-1};
     std::atomic<uint64_t> commands{0};
     std::atomic<bool> lost{false};
+    std::atomic<bool> closed{false};
+    std::atomic<int64_t> refs{1};  // the opener's reference, dropped by fh_device_close
 };
 
 struct fh_buffer {
@@ -56,6 +61,10 @@ fh_status end_command(fh_device *dev, const char *what);
 fh_status hip_fail(fh_device *dev, hipError_t e, const char *what);
 
 fh_status alloc_bytes(fh_device *dev, size_t nbytes, void **out);
+
+// Reference counting of devices (see struct fh_device).
+void dev_retain(fh_device *dev);
+void dev_release(fh_device *dev);  // destroys the stream and the device on the last release
 
 // ---- kernel launchers (each issues exactly one kernel on dev->stream) ----
 // codec.hip

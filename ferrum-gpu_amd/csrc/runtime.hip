@@ -61,6 +61,23 @@ fh_status end_command(fh_device *dev, const char *what) {
     return FH_OK;
 }
 
+void dev_retain(fh_device *dev) { dev->refs.fetch_add(1); }
+
+void dev_release(fh_device *dev) {
+    if (dev->refs.fetch_sub(1) != 1) return;
+    (void)hipSetDevice(dev->ordinal);
+    (void)hipStreamSynchronize(dev->stream);
+    (void)hipStreamDestroy(dev->stream);
+    delete dev;
+}
+
+// Free device memory made by alloc_bytes once no queued command can still use it.
+static void free_bytes(fh_device *dev, void *p) {
+    (void)hipSetDevice(dev->ordinal);
+    (void)hipStreamSynchronize(dev->stream);
+    (void)hipFree(p);
+}
+
 fh_status alloc_bytes(fh_device *dev, size_t nbytes, void **out) {
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, nbytes + kPad);
@@ -85,6 +102,7 @@ namespace {
 
 fh_status check_dev(fh_device *dev) {
     if (!dev) return fail(FH_ERR_INVALID, "no device");
+    if (dev->closed.load()) return fail(FH_ERR_INVALID, "the device was closed");
     if (dev->lost.load()) return fail(FH_ERR_LOST, "the device was lost earlier");
     hipError_t e = hipSetDevice(dev->ordinal);
     if (e != hipSuccess) return hip_fail(dev, e, "select device");
@@ -106,6 +124,7 @@ fh_status new_buffer(fh_device *dev, size_t nbytes, fh_buffer **out) {
         (void)hipFree(p);
         return fail(FH_ERR_OOM, "host out of memory");
     }
+    dev_retain(dev);
     b->dev = dev;
     b->ptr = p;
     b->nbytes = nbytes;
@@ -155,6 +174,7 @@ fh_status new_qweight(fh_device *dev, fh_kind kind, size_t k, size_t n, fh_qweig
         (void)hipFree(p);
         return fail(FH_ERR_OOM, "host out of memory");
     }
+    dev_retain(dev);
     w->dev = dev;
     w->kind = kind;
     w->k = k;
@@ -217,11 +237,10 @@ fh_status fh_device_open(int ordinal, fh_device **out) {
 }
 
 void fh_device_close(fh_device *dev) {
-    if (!dev) return;
+    if (!dev || dev->closed.exchange(true)) return;
     (void)hipSetDevice(dev->ordinal);
     (void)hipStreamSynchronize(dev->stream);
-    (void)hipStreamDestroy(dev->stream);
-    delete dev;
+    dev_release(dev);
 }
 
 fh_status fh_device_sync(fh_device *dev) {
@@ -309,10 +328,10 @@ void *fh_buffer_device_ptr(const fh_buffer *buf) { return buf ? buf->ptr : nullp
 
 void fh_buffer_free(fh_buffer *buf) {
     if (!buf) return;
-    (void)hipSetDevice(buf->dev->ordinal);
-    (void)hipStreamSynchronize(buf->dev->stream);  // no kernel may still use it
-    (void)hipFree(buf->ptr);
+    fh_device *dev = buf->dev;
+    free_bytes(dev, buf->ptr);  // no queued kernel may still use it
     delete buf;
+    dev_release(dev);
 }
 
 fh_status fh_copy_f32(fh_device *dev, const fh_buffer *src, size_t src_off, fh_buffer *dst,
@@ -430,10 +449,10 @@ fh_status fh_qweight_upload_f32(fh_device *dev, fh_kind kind, const float *w, si
 
 void fh_qweight_free(fh_qweight *w) {
     if (!w) return;
-    (void)hipSetDevice(w->dev->ordinal);
-    (void)hipStreamSynchronize(w->dev->stream);
-    (void)hipFree(w->ptr);
+    fh_device *dev = w->dev;
+    free_bytes(dev, w->ptr);
     delete w;
+    dev_release(dev);
 }
 
 fh_kind fh_qweight_kind(const fh_qweight *w) { return w->kind; }
@@ -525,6 +544,7 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
     if (!out || (count && !problems)) return fail(FH_ERR_INVALID, "gemv plan: null argument");
     fh_gemv_plan *plan = new (std::nothrow) fh_gemv_plan;
     if (!plan) return fail(FH_ERR_OOM, "host out of memory");
+    dev_retain(dev);
     plan->dev = dev;
     // Group by (kind, class) keeping the caller's order inside a group.
     std::vector<GemvDesc> host;
@@ -535,23 +555,23 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
             for (size_t i = 0; i < count; i++) {
                 const fh_gemv_problem &p = problems[i];
                 if (!p.w || !p.x || !p.y) {
-                    delete plan;
+                    fh_gemv_plan_free(plan);
                     return fail(FH_ERR_INVALID, "gemv plan: problem %zu has a null pointer", i);
                 }
                 if (p.w->dev != dev) {
-                    delete plan;
+                    fh_gemv_plan_free(plan);
                     return fail(FH_ERR_INVALID, "gemv plan: problem %zu lives on another device", i);
                 }
                 int c = gemv_class(p.w->k / QK);
                 if (c == 0) {
-                    delete plan;
+                    fh_gemv_plan_free(plan);
                     return fail(FH_ERR_INVALID, "gemv plan: problem %zu has k = %zu > 8192", i, p.w->k);
                 }
                 if ((int)p.w->kind != kind || c != cls) continue;
                 GemvDesc d{p.w->ptr, p.x, p.y, (uint32_t)(p.w->k / QK), (uint32_t)p.w->n, L.tasks, 0};
                 uint64_t t = (uint64_t)L.tasks + gemv_tasks(cls, p.w->n);
                 if (t > (1ull << 31)) {
-                    delete plan;
+                    fh_gemv_plan_free(plan);
                     return fail(FH_ERR_INVALID, "gemv plan: too many rows in one launch");
                 }
                 L.tasks = (uint32_t)t;
@@ -565,7 +585,7 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
     if (!host.empty()) {
         void *p = nullptr;
         if ((st = alloc_bytes(dev, host.size() * sizeof(GemvDesc), &p))) {
-            delete plan;
+            fh_gemv_plan_free(plan);
             return st;
         }
         plan->descs = (GemvDesc *)p;
@@ -596,12 +616,10 @@ uint64_t fh_gemv_plan_bytes(const fh_gemv_plan *plan) { return plan ? plan->byte
 
 void fh_gemv_plan_free(fh_gemv_plan *plan) {
     if (!plan) return;
-    if (plan->descs) {
-        (void)hipSetDevice(plan->dev->ordinal);
-        (void)hipStreamSynchronize(plan->dev->stream);
-        (void)hipFree(plan->descs);
-    }
+    fh_device *dev = plan->dev;
+    if (plan->descs) free_bytes(dev, plan->descs);
     delete plan;
+    dev_release(dev);
 }
 
 // ---- QAT snap ----
