@@ -170,6 +170,26 @@ def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0):
     return {"m": m, "flops_per_step": flops, "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12}
 
 
+def bench_copy(g, ev, nbytes=512 * 2**20, reps=10):
+    """A plain device copy (Gpu::copy_f32, one 16-byte-vector kernel) of a known size: the
+    measured HBM ceiling for a read+write stream, and the known-size dispatch that calibrates the
+    FETCH_SIZE / WRITE_SIZE counters (it is the first kernel this script launches)."""
+    n = nbytes // 4
+    src, dst = g.zeros(n), g.zeros(n)
+    g.copy_f32(src, 0, dst, 0, n)  # calibration dispatch (also a warm-up)
+    g.sync()
+    e0, e1 = ev.create(2)
+    ev.record(e0)
+    for _ in range(reps):
+        g.copy_f32(src, 0, dst, 0, n)
+    ev.record(e1)
+    ms = ev.ms(e0, e1) / reps
+    ev.destroy([e0, e1])
+    src.free()
+    dst.free()
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "avg_ms": ms, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
+
+
 def cpu_baseline(shapes, kind_bytes, budget_s=12.0):
     """The reference's CPU decode path restated in C (oracle/gemv: f32 weights [k, n], ascending
     k, one thread), on the same shapes; the rate is the same algorithmic bytes (the packed
@@ -217,6 +237,8 @@ def main():
     ev = HipEvents(g)
     name, cus = g.info()
     log(f"device {name}, {cus} CUs")
+    copy = bench_copy(g, ev)
+    log("copy:", copy)
 
     head = bench_gemv_pool(fh, g, ev, fh.QKind.Q4_0, QWEN_GROUPS, a.pool_gib * 2**30, a.steps, a.warmup)
     log("Q4_0 GEMV pool:", head)
@@ -268,6 +290,7 @@ def main():
                      for L in head["launches"]],
         "cpu_baseline": cpu and {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "extra": extra,
+        "hbm_copy_gbs": round(copy["gbs"], 1),
     }
     print(json.dumps(out))
     g.close()

@@ -336,6 +336,19 @@ __global__ __launch_bounds__(kThreads) void snap_cols_kernel(const float *__rest
     }
 }
 
+// ---- plain f32 copy (Gpu::copy_f32): 16-byte loads and stores when both ends allow them ----
+__global__ __launch_bounds__(kThreads) void copy_f32x4_kernel(const f32x4 *__restrict__ src,
+                                                              f32x4 *__restrict__ dst, size_t n4) {
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n4; i += (size_t)gridDim.x * kThreads)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+__global__ __launch_bounds__(kThreads) void copy_f32_kernel(const float *__restrict__ src,
+                                                            float *__restrict__ dst, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (size_t)gridDim.x * kThreads)
+        dst[i] = src[i];
+}
+
 unsigned grid_for(size_t work_items, size_t per_group, unsigned cap) {
     size_t g = (work_items + per_group - 1) / per_group;
     if (g < 1) g = 1;
@@ -383,6 +396,16 @@ hipError_t launch_decode_cols(hipStream_t s, fh_kind kind, const uint8_t *src, f
         decode_cols_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(src, w, k, n);
     else
         decode_cols_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(src, w, k, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_f32(hipStream_t s, const float *src, float *dst, size_t n) {
+    if (((uintptr_t)src | (uintptr_t)dst) % 16 == 0 && n % 4 == 0) {
+        copy_f32x4_kernel<<<grid_for(n / 4, kThreads * 4, 16384), kThreads, 0, s>>>(
+            (const f32x4 *)src, (f32x4 *)dst, n / 4);
+    } else {
+        copy_f32_kernel<<<grid_for(n, kThreads * 4, 16384), kThreads, 0, s>>>(src, dst, n);
+    }
     return hipGetLastError();
 }
 

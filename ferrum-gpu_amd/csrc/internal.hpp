@@ -79,6 +79,7 @@ hipError_t launch_decode_cols(hipStream_t s, fh_kind kind, const uint8_t *src, f
 hipError_t launch_snap_rows(hipStream_t s, const float *src, float *dst, size_t nblocks);
 hipError_t launch_snap_cols(hipStream_t s, const float *src, float *dst, size_t rows_in,
                             size_t cols_out);
+hipError_t launch_copy_f32(hipStream_t s, const float *src, float *dst, size_t n);
 
 // gemv.hip
 struct GemvDesc {          // one batch-1 product, as the grouped kernel reads it

@@ -342,12 +342,9 @@ fh_status fh_copy_f32(fh_device *dev, const fh_buffer *src, size_t src_off, fh_b
     if (src_off + len > src->nbytes / 4 || dst_off + len > dst->nbytes / 4)
         return fail(FH_ERR_INVALID, "copy_f32: range out of bounds");
     if ((st = begin_command(dev, "copy_f32"))) return st;
-    if (len) {
-        hipError_t e = hipMemcpyAsync((float *)dst->ptr + dst_off, (const float *)src->ptr + src_off,
-                                      len * 4, hipMemcpyDeviceToDevice, dev->stream);
-        if (e != hipSuccess) return hip_fail(dev, e, "copy_f32");
-    }
-    return FH_OK;
+    if (len)
+        (void)launch_copy_f32(dev->stream, (const float *)src->ptr + src_off, (float *)dst->ptr + dst_off, len);
+    return end_command(dev, "copy_f32");
 }
 
 // ---- device codec ----
