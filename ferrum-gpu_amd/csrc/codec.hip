@@ -226,13 +226,13 @@ __global__ __launch_bounds__(kThreads) void snap_rows_kernel(const float *__rest
 }
 
 // ---- cols: one thread per (column c, block kb) of an [k, n] matrix ----
-// Quantise down the columns into GGUF rows: row c of the output holds the blocks of column c
-// (quantise_matrix, ferrum_wgpu/src/ops/quant.rs:238-252).
+// Quantise down the columns into the planes of GGUF row c (quantise_matrix,
+// ferrum_wgpu/src/ops/quant.rs:238-252): block (c, kb) is block c * nb + kb of the planes.
 template <int KIND>
 __global__ __launch_bounds__(kThreads) void encode_cols_kernel(const float *__restrict__ w,
-                                                               uint8_t *__restrict__ dst, size_t k,
+                                                               uint8_t *__restrict__ qs,
+                                                               uint16_t *__restrict__ ds, size_t k,
                                                                size_t n) {
-    constexpr int BB = Fmt<KIND>::bytes;
     const size_t nb = k / 32;
     const size_t total = nb * n;
     for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (size_t)gridDim.x * kThreads) {
@@ -240,21 +240,24 @@ __global__ __launch_bounds__(kThreads) void encode_cols_kernel(const float *__re
         float v[32];
 #pragma unroll
         for (int e = 0; e < 32; e++) v[e] = w[(kb * 32 + e) * n + c];
-        uint8_t *out = dst + (c * nb + kb) * BB;
-        uint32_t h;
+        const size_t blk = c * nb + kb;
         if constexpr (KIND == FH_Q8_0) {
             float amax = 0.0f;
 #pragma unroll
             for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(v[e]));
             float d = amax / 127.0f;
             float id = d != 0.0f ? 1.0f / d : 0.0f;
-            h = float_to_half_bits(d);
-            *(uint16_t *)out = (uint16_t)h;
+            ds[blk] = (uint16_t)float_to_half_bits(d);
+            u32x4 o[2];
 #pragma unroll
-            for (int e = 0; e < 32; e += 2) {
-                uint32_t a = round_sat_i8(v[e] * id) & 0xff, b = round_sat_i8(v[e + 1] * id) & 0xff;
-                *(uint16_t *)(out + 2 + e) = (uint16_t)(a | b << 8);
+            for (int e = 0; e < 32; e += 4) {
+                uint32_t word = (round_sat_i8(v[e] * id) & 0xff) | (round_sat_i8(v[e + 1] * id) & 0xff) << 8 |
+                                (round_sat_i8(v[e + 2] * id) & 0xff) << 16 |
+                                (uint32_t)(round_sat_i8(v[e + 3] * id) & 0xff) << 24;
+                o[e / 16][(e / 4) % 4] = word;
             }
+            *(u32x4 *)(qs + blk * 32) = o[0];
+            *(u32x4 *)(qs + blk * 32 + 16) = o[1];
         } else {
             float m = 0.0f;
 #pragma unroll
@@ -262,51 +265,103 @@ __global__ __launch_bounds__(kThreads) void encode_cols_kernel(const float *__re
                 if (fabsf(v[e]) > fabsf(m)) m = v[e];
             float d = m / -8.0f;
             float id = d != 0.0f ? 1.0f / d : 0.0f;
-            h = float_to_half_bits(d);
-            *(uint16_t *)out = (uint16_t)h;
+            ds[blk] = (uint16_t)float_to_half_bits(d);
+            u32x4 o;
 #pragma unroll
-            for (int j = 0; j < 16; j += 2) {
-                uint32_t b0 = trunc_clamp_0_15(v[j] * id + 8.5f) | trunc_clamp_0_15(v[j + 16] * id + 8.5f) << 4;
-                uint32_t b1 = trunc_clamp_0_15(v[j + 1] * id + 8.5f) | trunc_clamp_0_15(v[j + 17] * id + 8.5f) << 4;
-                *(uint16_t *)(out + 2 + j) = (uint16_t)(b0 | b1 << 8);
+            for (int j = 0; j < 16; j += 4) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    uint32_t byte = trunc_clamp_0_15(v[j + b] * id + 8.5f) |
+                                    trunc_clamp_0_15(v[j + b + 16] * id + 8.5f) << 4;
+                    word |= byte << (8 * b);
+                }
+                o[j / 4] = word;
+            }
+            *(u32x4 *)(qs + blk * 16) = o;
+        }
+    }
+}
+
+// Dequantise the planes back to the [k, n] f32 weight (transpose(decode(bytes))).
+template <int KIND>
+__global__ __launch_bounds__(kThreads) void decode_cols_kernel(const uint8_t *__restrict__ qs,
+                                                               const uint16_t *__restrict__ ds,
+                                                               float *__restrict__ w, size_t k,
+                                                               size_t n) {
+    const size_t nb = k / 32;
+    const size_t total = nb * n;
+    for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (size_t)gridDim.x * kThreads) {
+        const size_t kb = t / n, c = t % n;
+        const size_t blk = c * nb + kb;
+        const float d = half_bits_to_float(ds[blk]);
+        float *col = w + kb * 32 * n + c;
+        if constexpr (KIND == FH_Q8_0) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const u32x4 q = *(const u32x4 *)(qs + blk * 32 + 16 * h);
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int b = 0; b < 4; b++)
+                        col[(16 * h + 4 * i + b) * n] = d * (float)(int8_t)(q[i] >> (8 * b));
+            }
+        } else {
+            const u32x4 q = *(const u32x4 *)(qs + blk * 16);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    col[(4 * i + b) * n] = d * ((float)((q[i] >> (8 * b)) & 15) - 8.0f);
+                    col[(16 + 4 * i + b) * n] = d * ((float)((q[i] >> (8 * b + 4)) & 15) - 8.0f);
+                }
             }
         }
     }
 }
 
-// Dequantise GGUF rows back to the [k, n] f32 weight (transpose(decode(bytes))).
+// ---- GGUF blocks <-> planes, one thread per block ----
 template <int KIND>
-__global__ __launch_bounds__(kThreads) void decode_cols_kernel(const uint8_t *__restrict__ src,
-                                                               float *__restrict__ w, size_t k,
-                                                               size_t n) {
+__global__ __launch_bounds__(kThreads) void gguf_to_planes_kernel(const uint8_t *__restrict__ src,
+                                                                  uint8_t *__restrict__ qs,
+                                                                  uint16_t *__restrict__ ds,
+                                                                  size_t nblocks) {
     constexpr int BB = Fmt<KIND>::bytes;
     constexpr int WORDS = KIND == FH_Q8_0 ? 9 : 5;
-    const size_t nb = k / 32;
-    const size_t total = nb * n;
-    for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (size_t)gridDim.x * kThreads) {
-        const size_t kb = t / n, c = t % n;
-        const size_t off = (c * nb + kb) * BB;
+    for (size_t blk = (size_t)blockIdx.x * kThreads + threadIdx.x; blk < nblocks;
+         blk += (size_t)gridDim.x * kThreads) {
+        const size_t off = blk * BB;
         uint32_t win[WORDS];
         load_window<WORDS>(src, off, win);
-        const float d = half_bits_to_float(scale_bits(win[0], off));
         const uint32_t sel = quant_sel(off);
-        float *col = w + kb * 32 * n + c;
-        if constexpr (KIND == FH_Q8_0) {
+        ds[blk] = (uint16_t)scale_bits(win[0], off);
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                uint32_t q = quant_word(win, i, sel);
+        for (int h = 0; h < (KIND == FH_Q8_0 ? 2 : 1); h++) {
+            u32x4 q;
 #pragma unroll
-                for (int b = 0; b < 4; b++) col[(4 * i + b) * n] = d * (float)(int8_t)(q >> (8 * b));
-            }
-        } else {
+            for (int i = 0; i < 4; i++) q[i] = quant_word(win, 4 * h + i, sel);
+            __builtin_nontemporal_store(q, (u32x4 *)(qs + blk * (BB - 2) + 16 * h));
+        }
+    }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(kThreads) void planes_to_gguf_kernel(const uint8_t *__restrict__ qs,
+                                                                  const uint16_t *__restrict__ ds,
+                                                                  uint8_t *__restrict__ dst,
+                                                                  size_t nblocks) {
+    constexpr int BB = Fmt<KIND>::bytes;
+    for (size_t blk = (size_t)blockIdx.x * kThreads + threadIdx.x; blk < nblocks;
+         blk += (size_t)gridDim.x * kThreads) {
+        uint16_t *out = (uint16_t *)(dst + blk * BB);  // GGUF blocks are 2-byte aligned
+        out[0] = ds[blk];
+#pragma unroll
+        for (int h = 0; h < (KIND == FH_Q8_0 ? 2 : 1); h++) {
+            const u32x4 q = *(const u32x4 *)(qs + blk * (BB - 2) + 16 * h);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                uint32_t q = quant_word(win, i, sel);
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    col[(4 * i + b) * n] = d * ((float)((q >> (8 * b)) & 15) - 8.0f);
-                    col[(16 + 4 * i + b) * n] = d * ((float)((q >> (8 * b + 4)) & 15) - 8.0f);
-                }
+                out[1 + 8 * h + 2 * i] = (uint16_t)q[i];
+                out[2 + 8 * h + 2 * i] = (uint16_t)(q[i] >> 16);
             }
         }
     }
@@ -381,21 +436,43 @@ hipError_t launch_snap_rows(hipStream_t s, const float *src, float *dst, size_t 
     return hipGetLastError();
 }
 
-hipError_t launch_encode_cols(hipStream_t s, fh_kind kind, const float *w, uint8_t *dst, size_t k, size_t n) {
+hipError_t launch_encode_cols(hipStream_t s, fh_kind kind, const float *w, uint8_t *qs, uint16_t *ds, size_t k,
+                              size_t n) {
     unsigned g = grid_for(k / 32 * n, kThreads, 65535);
     if (kind == FH_Q8_0)
-        encode_cols_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(w, dst, k, n);
+        encode_cols_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(w, qs, ds, k, n);
     else
-        encode_cols_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(w, dst, k, n);
+        encode_cols_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(w, qs, ds, k, n);
     return hipGetLastError();
 }
 
-hipError_t launch_decode_cols(hipStream_t s, fh_kind kind, const uint8_t *src, float *w, size_t k, size_t n) {
+hipError_t launch_decode_cols(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, float *w,
+                              size_t k, size_t n) {
     unsigned g = grid_for(k / 32 * n, kThreads, 65535);
     if (kind == FH_Q8_0)
-        decode_cols_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(src, w, k, n);
+        decode_cols_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(qs, ds, w, k, n);
     else
-        decode_cols_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(src, w, k, n);
+        decode_cols_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(qs, ds, w, k, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_gguf_to_planes(hipStream_t s, fh_kind kind, const uint8_t *src, uint8_t *qs, uint16_t *ds,
+                                 size_t nblocks) {
+    unsigned g = grid_for(nblocks, kThreads, 65535);
+    if (kind == FH_Q8_0)
+        gguf_to_planes_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(src, qs, ds, nblocks);
+    else
+        gguf_to_planes_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(src, qs, ds, nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_planes_to_gguf(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, uint8_t *dst,
+                                 size_t nblocks) {
+    unsigned g = grid_for(nblocks, kThreads, 65535);
+    if (kind == FH_Q8_0)
+        planes_to_gguf_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(qs, ds, dst, nblocks);
+    else
+        planes_to_gguf_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(qs, ds, dst, nblocks);
     return hipGetLastError();
 }
 

@@ -1,5 +1,5 @@
-// Multi-row products on GGUF-resident Q8_0 / Q4_0 weights for gfx950:
-// y[M, N] = x[M, K] * W^T with W as GGUF rows (N rows of K/32 blocks).
+// Multi-row products on resident Q8_0 / Q4_0 weights for gfx950: y[M, N] = x[M, K] * W^T, W held
+// as the quant and scale planes of its N GGUF rows of K/32 blocks (see gemv.hip).
 //
 // naive_kernel: one thread per output, ascending k, the dequantised value formed first and then
 // multiplied (ferrum_wgpu/src/shaders/quant/qlinear.wgsl:18-59). Kept as the baseline path.
@@ -33,33 +33,30 @@ __device__ __forceinline__ float half_to_float(uint32_t h) {
 
 // ---- naive baseline ----
 template <int KIND>
-__global__ __launch_bounds__(256) void naive_kernel(const uint8_t *__restrict__ w, const float *__restrict__ x,
-                                                    float *__restrict__ y, uint32_t rows, uint32_t k,
-                                                    uint32_t n) {
-    constexpr int BB = KIND == FH_Q8_0 ? 34 : 18;
-    constexpr int WORDS = KIND == FH_Q8_0 ? 9 : 5;
+__global__ __launch_bounds__(256) void naive_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ ds,
+                                                    const float *__restrict__ x, float *__restrict__ y,
+                                                    uint32_t rows, uint32_t k, uint32_t n) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (size_t)rows * n) return;
     const uint32_t r = idx / n, c = idx % n, nb = k / 32;
     const float *xr = x + (size_t)r * k;
     float acc = 0.0f;
     for (uint32_t b = 0; b < nb; b++) {
-        const size_t off = ((size_t)c * nb + b) * BB;
-        uint32_t win[WORDS];
-        load_window<WORDS>(w, off, win);
-        const float d = half_bits_to_float(scale_bits(win[0], off));
-        const uint32_t sel = quant_sel(off);
+        const size_t blk = (size_t)c * nb + b;
+        const float d = half_bits_to_float(ds[blk]);
         if constexpr (KIND == FH_Q8_0) {
-            for (int i = 0; i < 8; i++) {
-                uint32_t q = quant_word(win, i, sel);
-                for (int e = 0; e < 4; e++) acc += xr[b * 32 + 4 * i + e] * (d * (float)(int8_t)(q >> (8 * e)));
+            for (int h = 0; h < 2; h++) {
+                const u32x4 q = *(const u32x4 *)(qs + blk * 32 + 16 * h);
+                for (int i = 0; i < 4; i++)
+                    for (int e = 0; e < 4; e++)
+                        acc += xr[b * 32 + 16 * h + 4 * i + e] * (d * (float)(int8_t)(q[i] >> (8 * e)));
             }
         } else {
+            const u32x4 q = *(const u32x4 *)(qs + blk * 16);
             for (int i = 0; i < 4; i++) {
-                uint32_t q = quant_word(win, i, sel);
                 for (int e = 0; e < 4; e++) {
-                    acc += xr[b * 32 + 4 * i + e] * (d * ((float)((q >> (8 * e)) & 15) - 8.0f));
-                    acc += xr[b * 32 + 16 + 4 * i + e] * (d * ((float)((q >> (8 * e + 4)) & 15) - 8.0f));
+                    acc += xr[b * 32 + 4 * i + e] * (d * ((float)((q[i] >> (8 * e)) & 15) - 8.0f));
+                    acc += xr[b * 32 + 16 + 4 * i + e] * (d * ((float)((q[i] >> (8 * e + 4)) & 15) - 8.0f));
                 }
             }
         }
@@ -81,28 +78,27 @@ struct GemmCfg {
     static_assert(BM * 8 % 256 == 0 && BN * 2 % 256 == 0, "staging must divide over 256 threads");
 };
 
-// One (column, byte-half bh) item of a weight block: the 16 quants it owns as f16, in the order
-// the MFMA B operand wants them (elements 8bh..8bh+7, then 16+8bh..16+8bh+7), and the scale.
+// One (column, byte-half bh) item of a weight block: the 16 quants it owns (elements
+// 8bh..8bh+7 and 16+8bh..16+8bh+7, in the order the MFMA B operand wants them) and the scale.
 template <int KIND>
 struct BItem {
-    uint32_t w[KIND == FH_Q8_0 ? 6 : 3];
-    uint32_t sw;
-    uint32_t odd;
+    uint32_t w[4];
+    uint32_t h;
 };
 
 template <int KIND>
-__device__ __forceinline__ void load_b(const uint8_t *__restrict__ wq, size_t off, int bh, BItem<KIND> &it) {
-    // off: byte offset of the block (2-byte aligned)
-    it.odd = (uint32_t)off & 2u;
-    it.sw = *(const uint32_t *)(wq + (off & ~(size_t)3));
-    // the 8 wanted quant bytes start at block byte 2 + 8bh: load the 3 dwords that cover them
-    const size_t first = off + 2 + 8 * bh;
-    const uint32_t *p0 = (const uint32_t *)(wq + (first & ~(size_t)3));
-    it.w[0] = p0[0]; it.w[1] = p0[1]; it.w[2] = p0[2];
+__device__ __forceinline__ void load_b(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ ds,
+                                       size_t blk, int bh, BItem<KIND> &it) {
+    it.h = ds[blk];
     if constexpr (KIND == FH_Q8_0) {
-        // Q8_0 also needs quants 16 + 8bh.. at block byte 18 + 8bh (same dword phase)
-        const uint32_t *p1 = (const uint32_t *)(wq + ((first + 16) & ~(size_t)3));
-        it.w[3] = p1[0]; it.w[4] = p1[1]; it.w[5] = p1[2];
+        // bytes 8bh..8bh+7 and 16+8bh..16+8bh+7 of the block's 32 quants
+        const uint2 a = *(const uint2 *)(qs + blk * 32 + 8 * bh);
+        const uint2 b = *(const uint2 *)(qs + blk * 32 + 16 + 8 * bh);
+        it.w[0] = a.x; it.w[1] = a.y; it.w[2] = b.x; it.w[3] = b.y;
+    } else {
+        // bytes 8bh..8bh+7: low nibbles are elements 8bh.., high nibbles 16+8bh..
+        const uint2 a = *(const uint2 *)(qs + blk * 16 + 8 * bh);
+        it.w[0] = a.x; it.w[1] = a.y; it.w[2] = 0; it.w[3] = 0;
     }
 }
 
@@ -111,31 +107,22 @@ __device__ __forceinline__ _Float16 i2h(int v) { return (_Float16)(float)v; }
 
 template <int KIND>
 __device__ __forceinline__ void unpack_b(const BItem<KIND> &it, f16x8 &lo8, f16x8 &hi8, float &d) {
-    d = half_to_float(it.odd ? (it.sw >> 16) : (it.sw & 0xffffu));
-    // byte position of the first wanted quant inside the loaded dwords: (2 + 8bh + off) & 3,
-    // which is 2 when the block starts at a dword boundary and 0 when it starts 2 bytes in
-    const uint32_t sel = it.odd ? 0x03020100u : 0x05040302u;
+    d = half_to_float(it.h);
     if constexpr (KIND == FH_Q8_0) {
-        uint32_t a0 = __builtin_amdgcn_perm(it.w[1], it.w[0], sel);
-        uint32_t a1 = __builtin_amdgcn_perm(it.w[2], it.w[1], sel);
-        uint32_t b0 = __builtin_amdgcn_perm(it.w[4], it.w[3], sel);
-        uint32_t b1 = __builtin_amdgcn_perm(it.w[5], it.w[4], sel);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            lo8[e] = i2h((int8_t)(a0 >> (8 * e)));
-            lo8[4 + e] = i2h((int8_t)(a1 >> (8 * e)));
-            hi8[e] = i2h((int8_t)(b0 >> (8 * e)));
-            hi8[4 + e] = i2h((int8_t)(b1 >> (8 * e)));
+            lo8[e] = i2h((int8_t)(it.w[0] >> (8 * e)));
+            lo8[4 + e] = i2h((int8_t)(it.w[1] >> (8 * e)));
+            hi8[e] = i2h((int8_t)(it.w[2] >> (8 * e)));
+            hi8[4 + e] = i2h((int8_t)(it.w[3] >> (8 * e)));
         }
     } else {
-        uint32_t a0 = __builtin_amdgcn_perm(it.w[1], it.w[0], sel);
-        uint32_t a1 = __builtin_amdgcn_perm(it.w[2], it.w[1], sel);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            lo8[e] = i2h((int)((a0 >> (8 * e)) & 15) - 8);
-            lo8[4 + e] = i2h((int)((a1 >> (8 * e)) & 15) - 8);
-            hi8[e] = i2h((int)((a0 >> (8 * e + 4)) & 15) - 8);
-            hi8[4 + e] = i2h((int)((a1 >> (8 * e + 4)) & 15) - 8);
+            lo8[e] = i2h((int)((it.w[0] >> (8 * e)) & 15) - 8);
+            lo8[4 + e] = i2h((int)((it.w[1] >> (8 * e)) & 15) - 8);
+            hi8[e] = i2h((int)((it.w[0] >> (8 * e + 4)) & 15) - 8);
+            hi8[4 + e] = i2h((int)((it.w[1] >> (8 * e + 4)) & 15) - 8);
         }
     }
 }
@@ -148,12 +135,12 @@ __device__ __forceinline__ void split_f16(float v, _Float16 &hi, _Float16 &lo) {
 }
 
 template <int KIND, int BM, int BN, int WAVES_M>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(const uint8_t *__restrict__ wq,
+__global__ __launch_bounds__(256, 2) void gemm_kernel(const uint8_t *__restrict__ qs,
+                                                      const uint16_t *__restrict__ ds,
                                                       const float *__restrict__ x,
                                                       float *__restrict__ y, uint32_t M, uint32_t K,
                                                       uint32_t N) {
     using C = GemmCfg<KIND, BM, BN, WAVES_M>;
-    constexpr int BB = KIND == FH_Q8_0 ? 34 : 18;
     __shared__ __attribute__((aligned(16))) _Float16 sAh[BM * kRowHalfs];
     __shared__ __attribute__((aligned(16))) _Float16 sAl[BM * kRowHalfs];
     __shared__ __attribute__((aligned(16))) _Float16 sB[BN * kRowHalfs];
@@ -163,7 +150,6 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const uint8_t *__restrict_
     const int wm = wave % WAVES_M, wn = wave / WAVES_M;
     const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const uint32_t nb = K / 32;
-    const size_t row_bytes = (size_t)nb * BB;
 
     f32x4 ra[C::A_CHUNKS];
     BItem<KIND> rb[C::B_ITEMS];
@@ -180,12 +166,11 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const uint8_t *__restrict_
             const int it = tid + 256 * i, col = it / 2, bh = it % 2;
             const uint32_t n = n0 + col;
             if (n < N) {
-                load_b<KIND>(wq, (size_t)n * row_bytes + (size_t)kb * BB, bh, rb[i]);
+                load_b<KIND>(qs, ds, (size_t)n * nb + kb, bh, rb[i]);
             } else {
-                rb[i].sw = 0;
-                rb[i].odd = 0;
+                rb[i].h = 0;
 #pragma unroll
-                for (int t = 0; t < (KIND == FH_Q8_0 ? 6 : 3); t++) rb[i].w[t] = 0;
+                for (int t = 0; t < 4; t++) rb[i].w[t] = 0;
             }
         }
     };
@@ -282,37 +267,39 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const uint8_t *__restrict_
 }
 
 template <int KIND, int BM, int BN, int WAVES_M>
-hipError_t run_gemm(hipStream_t s, const uint8_t *w, const float *x, float *y, uint32_t M, uint32_t K, uint32_t N) {
+hipError_t run_gemm(hipStream_t s, const uint8_t *qs, const uint16_t *ds, const float *x, float *y, uint32_t M,
+                    uint32_t K, uint32_t N) {
     dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-    gemm_kernel<KIND, BM, BN, WAVES_M><<<grid, 256, 0, s>>>(w, x, y, M, K, N);
+    gemm_kernel<KIND, BM, BN, WAVES_M><<<grid, 256, 0, s>>>(qs, ds, x, y, M, K, N);
     return hipGetLastError();
 }
 
 template <int KIND>
-hipError_t gemm_dispatch(hipStream_t s, const uint8_t *w, const float *x, float *y, uint32_t M, uint32_t K,
-                         uint32_t N) {
-    if (M <= 32) return run_gemm<KIND, 32, 256, 1>(s, w, x, y, M, K, N);
-    if (M <= 64) return run_gemm<KIND, 64, 128, 2>(s, w, x, y, M, K, N);
-    return run_gemm<KIND, 128, 128, 2>(s, w, x, y, M, K, N);
+hipError_t gemm_dispatch(hipStream_t s, const uint8_t *qs, const uint16_t *ds, const float *x, float *y,
+                         uint32_t M, uint32_t K, uint32_t N) {
+    if (M <= 32) return run_gemm<KIND, 32, 256, 1>(s, qs, ds, x, y, M, K, N);
+    if (M <= 64) return run_gemm<KIND, 64, 128, 2>(s, qs, ds, x, y, M, K, N);
+    return run_gemm<KIND, 128, 128, 2>(s, qs, ds, x, y, M, K, N);
 }
 
 }  // namespace
 
-hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *w, const float *x, float *y, size_t rows,
-                        size_t k, size_t n) {
+hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
+                        float *y, size_t rows, size_t k, size_t n) {
     const size_t total = rows * n;
     const unsigned grid = (unsigned)((total + 255) / 256);
     if (kind == FH_Q8_0)
-        naive_kernel<FH_Q8_0><<<grid, 256, 0, s>>>(w, x, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+        naive_kernel<FH_Q8_0><<<grid, 256, 0, s>>>(qs, ds, x, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
     else
-        naive_kernel<FH_Q4_0><<<grid, 256, 0, s>>>(w, x, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+        naive_kernel<FH_Q4_0><<<grid, 256, 0, s>>>(qs, ds, x, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
     return hipGetLastError();
 }
 
-hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *w, const float *x, float *y, size_t rows,
-                       size_t k, size_t n) {
-    if (kind == FH_Q8_0) return gemm_dispatch<FH_Q8_0>(s, w, x, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
-    return gemm_dispatch<FH_Q4_0>(s, w, x, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
+                       float *y, size_t rows, size_t k, size_t n) {
+    if (kind == FH_Q8_0)
+        return gemm_dispatch<FH_Q8_0>(s, qs, ds, x, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+    return gemm_dispatch<FH_Q4_0>(s, qs, ds, x, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
 }
 
 }  // namespace fh

@@ -31,12 +31,18 @@ struct fh_buffer {
     size_t nbytes = 0;
 };
 
+// A resident quantized weight of k inputs and n outputs (n GGUF rows of nb = k/32 blocks),
+// repacked at upload into two planes that hold exactly the GGUF bytes: the quants of row r at
+// qs + r * nb * QB (QB = 16 Q4_0 / 32 Q8_0, the block without its scale, 16-byte aligned) and
+// the f16 scales of row r at ds + r * nb.
 struct fh_qweight {
     fh_device *dev = nullptr;
     fh_kind kind = FH_Q8_0;
     size_t k = 0, n = 0;
-    uint8_t *ptr = nullptr;  // GGUF rows, n * (k/32) blocks, 256-byte aligned, padded
-    size_t nbytes = 0;       // exact GGUF byte count (without the padding)
+    uint8_t *ptr = nullptr;   // the allocation: quant plane, then scale plane
+    uint8_t *qs = nullptr;    // quant plane (256-byte aligned)
+    uint16_t *ds = nullptr;   // scale plane
+    size_t nbytes = 0;        // exact GGUF byte count (= the two planes' payload)
 };
 
 namespace fh {
@@ -47,6 +53,11 @@ constexpr size_t QK = 32;
 constexpr size_t kPad = 256;
 
 inline size_t block_bytes(fh_kind k) { return k == FH_Q8_0 ? 34 : 18; }
+inline size_t quant_bytes(fh_kind k) { return k == FH_Q8_0 ? 32 : 16; }
+// Offset of the scale plane inside a weight allocation of nblocks blocks.
+inline size_t scale_plane_offset(fh_kind k, size_t nblocks) {
+    return (nblocks * quant_bytes(k) + 255) / 256 * 256;
+}
 inline bool kind_ok(int k) { return k == FH_Q8_0 || k == FH_Q4_0; }
 
 // Thread-local error text; returns the status for `return fail(...)`.
@@ -72,18 +83,26 @@ hipError_t launch_encode_rows(hipStream_t s, fh_kind kind, const float *src, uin
                               size_t nblocks);
 hipError_t launch_decode_rows(hipStream_t s, fh_kind kind, const uint8_t *src, float *dst,
                               size_t nblocks);
-hipError_t launch_encode_cols(hipStream_t s, fh_kind kind, const float *w, uint8_t *dst,
+// quantise_matrix into planes / dequantise planes back to the [k, n] f32 weight
+hipError_t launch_encode_cols(hipStream_t s, fh_kind kind, const float *w, uint8_t *qs, uint16_t *ds,
                               size_t k, size_t n);
-hipError_t launch_decode_cols(hipStream_t s, fh_kind kind, const uint8_t *src, float *w,
+hipError_t launch_decode_cols(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, float *w,
                               size_t k, size_t n);
 hipError_t launch_snap_rows(hipStream_t s, const float *src, float *dst, size_t nblocks);
 hipError_t launch_snap_cols(hipStream_t s, const float *src, float *dst, size_t rows_in,
                             size_t cols_out);
 hipError_t launch_copy_f32(hipStream_t s, const float *src, float *dst, size_t n);
 
+// GGUF bytes <-> planes (upload_qweight and read_gguf)
+hipError_t launch_gguf_to_planes(hipStream_t s, fh_kind kind, const uint8_t *src, uint8_t *qs,
+                                 uint16_t *ds, size_t nblocks);
+hipError_t launch_planes_to_gguf(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds,
+                                 uint8_t *dst, size_t nblocks);
+
 // gemv.hip
-struct GemvDesc {          // one batch-1 product, as the grouped kernel reads it
-    const uint8_t *w;      // GGUF rows
+struct GemvDesc {          // one batch-1 product, as the kernel reads it
+    const uint8_t *qs;     // quant plane
+    const uint16_t *ds;    // scale plane
     const float *x;
     float *y;
     uint32_t nb;           // blocks per row (k / 32)
@@ -91,17 +110,19 @@ struct GemvDesc {          // one batch-1 product, as the grouped kernel reads i
     uint32_t task0;        // first task index of this product in its launch
     uint32_t pad;
 };
-int gemv_class(size_t nb);  // launch class of a row width in blocks (0 = not supported)
-hipError_t launch_gemv(hipStream_t s, fh_kind kind, const uint8_t *w, const float *x, float *y,
-                       size_t k, size_t n, int cus);
-hipError_t launch_gemv_group(hipStream_t s, fh_kind kind, int cls, const GemvDesc *descs,
-                             uint32_t count, uint32_t tasks, int cus);
-uint32_t gemv_tasks(int cls, size_t n);
+// Launch shape for n rows of nb blocks, or -1 when a row is too wide for the kernel's registers
+// (k > 8192) or the weight too large for its 32-bit offsets.
+int gemv_shape(fh_kind kind, size_t nb, size_t n);
+uint32_t gemv_tasks(int shape, size_t n);
+hipError_t launch_gemv(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
+                       float *y, size_t k, size_t n, int cus);
+hipError_t launch_gemv_group(hipStream_t s, fh_kind kind, int shape, const GemvDesc *descs, uint32_t count,
+                             uint32_t tasks, int cus);
 
 // gemm.hip
-hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *w, const float *x, float *y,
-                        size_t rows, size_t k, size_t n);
-hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *w, const float *x, float *y,
-                       size_t rows, size_t k, size_t n);
+hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
+                        float *y, size_t rows, size_t k, size_t n);
+hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
+                       float *y, size_t rows, size_t k, size_t n);
 
 }  // namespace fh

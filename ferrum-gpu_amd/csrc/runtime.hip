@@ -165,9 +165,10 @@ fh_status new_qweight(fh_device *dev, fh_kind kind, size_t k, size_t n, fh_qweig
         return fail(FH_ERR_INVALID, "a %zu x %zu weight is not whole 32-element blocks", k, n);
     if (n == 0 || n > (1u << 30) || k > (1u << 30) || (k / QK) * n > (1ull << 32))
         return fail(FH_ERR_INVALID, "a %zu x %zu weight is out of range", k, n);
-    size_t nbytes = (k / QK) * n * block_bytes(kind);
+    const size_t nblocks = (k / QK) * n;
+    size_t nbytes = nblocks * block_bytes(kind);
     void *p = nullptr;
-    fh_status st = alloc_bytes(dev, nbytes, &p);
+    fh_status st = alloc_bytes(dev, scale_plane_offset(kind, nblocks) + nblocks * 2, &p);
     if (st) return st;
     fh_qweight *w = new (std::nothrow) fh_qweight;
     if (!w) {
@@ -180,6 +181,8 @@ fh_status new_qweight(fh_device *dev, fh_kind kind, size_t k, size_t n, fh_qweig
     w->k = k;
     w->n = n;
     w->ptr = (uint8_t *)p;
+    w->qs = (uint8_t *)p;
+    w->ds = (uint16_t *)((uint8_t *)p + scale_plane_offset(kind, nblocks));
     w->nbytes = nbytes;
     *out = w;
     return FH_OK;
@@ -191,7 +194,7 @@ struct fh_gemv_plan {
     fh_device *dev = nullptr;
     struct Launch {
         fh_kind kind;
-        int cls;
+        int shape;
         size_t first, count;
         uint32_t tasks;
     };
@@ -399,7 +402,17 @@ fh_status fh_qweight_upload_gguf(fh_device *dev, fh_kind kind, const uint8_t *by
         return fail(FH_ERR_INVALID, "%zu bytes is not the %zu a %zu x %zu %s weight needs", len,
                     want, k, n, kind == FH_Q8_0 ? "Q8_0" : "Q4_0");
     if ((st = new_qweight(dev, kind, k, n, out))) return st;
-    st = upload_bytes(dev, (*out)->ptr, bytes, len, "upload_qweight");
+    // the GGUF bytes go to a staging buffer and are repacked into the weight's planes
+    void *stage = nullptr;
+    if ((st = alloc_bytes(dev, len, &stage)) == FH_OK) {
+        st = upload_bytes(dev, stage, bytes, len, "upload_qweight");
+        if (st == FH_OK && (st = begin_command(dev, "upload_qweight")) == FH_OK) {
+            (void)launch_gguf_to_planes(dev->stream, kind, (const uint8_t *)stage, (*out)->qs, (*out)->ds,
+                                        len / block_bytes(kind));
+            st = end_command(dev, "upload_qweight");
+        }
+        free_bytes(dev, stage);  // waits for the repack
+    }
     if (st) {
         fh_qweight_free(*out);
         *out = nullptr;
@@ -418,7 +431,7 @@ fh_status fh_qweight_quantise(fh_device *dev, fh_kind kind, const fh_buffer *w, 
                     w ? w->nbytes / 4 : 0, k, n);
     if ((st = new_qweight(dev, kind, k, n, out))) return st;
     if ((st = begin_command(dev, "quantise_matrix")) == FH_OK) {
-        (void)launch_encode_cols(dev->stream, kind, (const float *)w->ptr, (*out)->ptr, k, n);
+        (void)launch_encode_cols(dev->stream, kind, (const float *)w->ptr, (*out)->qs, (*out)->ds, k, n);
         st = end_command(dev, "quantise_matrix");
     }
     if (st) {
@@ -463,7 +476,14 @@ fh_status fh_qweight_read_gguf(fh_device *dev, const fh_qweight *w, uint8_t *hos
     if (!w || len != w->nbytes)
         return fail(FH_ERR_INVALID, "read_gguf: %zu bytes requested, the weight holds %zu", len,
                     w ? w->nbytes : 0);
-    return read_bytes(dev, host, w->ptr, len, "read_gguf");
+    void *stage = nullptr;
+    if ((st = alloc_bytes(dev, len, &stage))) return st;
+    if ((st = begin_command(dev, "read_gguf")) == FH_OK) {
+        (void)launch_planes_to_gguf(dev->stream, w->kind, w->qs, w->ds, (uint8_t *)stage, len / block_bytes(w->kind));
+        if ((st = end_command(dev, "read_gguf")) == FH_OK) st = read_bytes(dev, host, stage, len, "read_gguf");
+    }
+    free_bytes(dev, stage);
+    return st;
 }
 
 fh_status fh_qweight_dequantise(fh_device *dev, const fh_qweight *w, fh_buffer *out) {
@@ -472,16 +492,15 @@ fh_status fh_qweight_dequantise(fh_device *dev, const fh_qweight *w, fh_buffer *
     if (!w) return fail(FH_ERR_INVALID, "dequantise: no weight");
     if ((st = need("dequantise out", out, w->k * w->n))) return st;
     if ((st = begin_command(dev, "dequantise"))) return st;
-    (void)launch_decode_cols(dev->stream, w->kind, w->ptr, (float *)out->ptr, w->k, w->n);
+    (void)launch_decode_cols(dev->stream, w->kind, w->qs, w->ds, (float *)out->ptr, w->k, w->n);
     return end_command(dev, "dequantise");
 }
 
 // ---- linear layers ----
 
 fh_path fh_choose(size_t rows, fh_kind kind, size_t k, size_t n) {
-    (void)kind;
     (void)n;
-    if (rows == 1 && gemv_class(k / QK)) return FH_PATH_GEMV;
+    if (rows == 1 && kind_ok(kind) && gemv_shape(kind, k / QK, n) >= 0) return FH_PATH_GEMV;
     return FH_PATH_TILED;
 }
 
@@ -492,18 +511,18 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
     switch (path) {
     case FH_PATH_GEMV:
         if (rows != 1) return fail(FH_ERR_INVALID, "the GEMV kernel takes one row, not %zu", rows);
-        if (!gemv_class(w->k / QK))
+        if (gemv_shape(w->kind, w->k / QK, w->n) < 0)
             return fail(FH_ERR_INVALID, "the GEMV kernel takes k <= 8192, not %zu", w->k);
         if ((st = begin_command(dev, "linear_q"))) return st;
-        (void)launch_gemv(dev->stream, w->kind, w->ptr, x, y, w->k, w->n, dev->cus);
+        (void)launch_gemv(dev->stream, w->kind, w->qs, w->ds, x, y, w->k, w->n, dev->cus);
         return end_command(dev, "linear_q");
     case FH_PATH_NAIVE:
         if ((st = begin_command(dev, "linear_q"))) return st;
-        if (rows) (void)launch_naive(dev->stream, w->kind, w->ptr, x, y, rows, w->k, w->n);
+        if (rows) (void)launch_naive(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n);
         return end_command(dev, "linear_q");
     case FH_PATH_TILED:
         if ((st = begin_command(dev, "linear_q"))) return st;
-        if (rows) (void)launch_gemm(dev->stream, w->kind, w->ptr, x, y, rows, w->k, w->n);
+        if (rows) (void)launch_gemm(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n);
         return end_command(dev, "linear_q");
     default:
         return fail(FH_ERR_INVALID, "unknown kernel path %d", (int)path);
@@ -543,30 +562,35 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
     if (!plan) return fail(FH_ERR_OOM, "host out of memory");
     dev_retain(dev);
     plan->dev = dev;
-    // Group by (kind, class) keeping the caller's order inside a group.
+    // Check every problem, then group by (format, launch shape), keeping the caller's order
+    // inside a group: each group is one launch.
+    std::vector<int> shape(count);
+    for (size_t i = 0; i < count; i++) {
+        const fh_gemv_problem &p = problems[i];
+        if (!p.w || !p.x || !p.y) {
+            fh_gemv_plan_free(plan);
+            return fail(FH_ERR_INVALID, "gemv plan: problem %zu has a null pointer", i);
+        }
+        if (p.w->dev != dev) {
+            fh_gemv_plan_free(plan);
+            return fail(FH_ERR_INVALID, "gemv plan: problem %zu lives on another device", i);
+        }
+        shape[i] = gemv_shape(p.w->kind, p.w->k / QK, p.w->n);
+        if (shape[i] < 0) {
+            fh_gemv_plan_free(plan);
+            return fail(FH_ERR_INVALID, "gemv plan: problem %zu has k = %zu > 8192", i, p.w->k);
+        }
+    }
     std::vector<GemvDesc> host;
     host.reserve(count);
     for (int kind : {FH_Q8_0, FH_Q4_0}) {
-        for (int cls = 1; cls <= 5; cls++) {
-            fh_gemv_plan::Launch L{(fh_kind)kind, cls, host.size(), 0, 0};
+        for (int sh = 0; sh < 64; sh++) {
+            fh_gemv_plan::Launch L{(fh_kind)kind, sh, host.size(), 0, 0};
             for (size_t i = 0; i < count; i++) {
                 const fh_gemv_problem &p = problems[i];
-                if (!p.w || !p.x || !p.y) {
-                    fh_gemv_plan_free(plan);
-                    return fail(FH_ERR_INVALID, "gemv plan: problem %zu has a null pointer", i);
-                }
-                if (p.w->dev != dev) {
-                    fh_gemv_plan_free(plan);
-                    return fail(FH_ERR_INVALID, "gemv plan: problem %zu lives on another device", i);
-                }
-                int c = gemv_class(p.w->k / QK);
-                if (c == 0) {
-                    fh_gemv_plan_free(plan);
-                    return fail(FH_ERR_INVALID, "gemv plan: problem %zu has k = %zu > 8192", i, p.w->k);
-                }
-                if ((int)p.w->kind != kind || c != cls) continue;
-                GemvDesc d{p.w->ptr, p.x, p.y, (uint32_t)(p.w->k / QK), (uint32_t)p.w->n, L.tasks, 0};
-                uint64_t t = (uint64_t)L.tasks + gemv_tasks(cls, p.w->n);
+                if ((int)p.w->kind != kind || shape[i] != sh) continue;
+                GemvDesc d{p.w->qs, p.w->ds, p.x, p.y, (uint32_t)(p.w->k / QK), (uint32_t)p.w->n, L.tasks, 0};
+                uint64_t t = (uint64_t)L.tasks + gemv_tasks(sh, p.w->n);
                 if (t > (1ull << 31)) {
                     fh_gemv_plan_free(plan);
                     return fail(FH_ERR_INVALID, "gemv plan: too many rows in one launch");
@@ -601,7 +625,7 @@ fh_status fh_gemv_plan_run(fh_device *dev, const fh_gemv_plan *plan) {
     if (!plan || plan->dev != dev) return fail(FH_ERR_INVALID, "gemv plan: wrong device");
     for (const auto &L : plan->launches) {
         if ((st = begin_command(dev, "gemv plan"))) return st;
-        (void)launch_gemv_group(dev->stream, L.kind, L.cls, plan->descs + L.first, (uint32_t)L.count,
+        (void)launch_gemv_group(dev->stream, L.kind, L.shape, plan->descs + L.first, (uint32_t)L.count,
                                 L.tasks, dev->cus);
         if ((st = end_command(dev, "gemv plan"))) return st;
     }
