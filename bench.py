@@ -31,6 +31,8 @@ sys.path[:0] = [REPO, os.path.join(REPO, "ferrum-gpu_amd")]
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 QWEN_SHAPES = [(896, 1152), (896, 4864), (4864, 896)]
+# TinyLlama-1.1B layer products (K x N): fused QKV (2048 + 2 * 256), o, fused gate+up, down
+LLAMA1B_SHAPES = [(2048, 2560), (2048, 2048), (2048, 11264), (5632, 2048)]
 # one grouped launch per input width (the two 896-wide products share a kernel instantiation)
 QWEN_GROUPS = [[(896, 1152), (896, 4864)], [(4864, 896)]]
 
@@ -250,14 +252,17 @@ def main():
         extra["q8_0_gemv_768x2304"] = {"gbs": round(q8["gbs"], 2), "frac": round(q8["gbs"] / HBM_PEAK_GBS, 4),
                                        "ms_per_step": q8["ms_per_step"], "bytes_per_step": q8["bytes_per_step"],
                                        "products_per_step": q8["products"]}
-        for m in (512, 2048):
-            r = bench_gemm(fh, g, ev, fh.QKind.Q4_0, m, QWEN_SHAPES, 10)
-            log(f"Q4_0 GEMM M={m}:", r)
-            extra[f"q4_0_gemm_m{m}"] = {"tflops": round(r["tflops"], 2),
-                                        "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
-                                        "ms_per_step": r["ms_per_step"], "flops_per_step": r["flops_per_step"],
-                                        "operands": "split-f16 x (hi+lo) x exact integer q, f32 accumulate, "
-                                                    "f32 block scale"}
+        for name, kind, shapes, ms in (("q4_0_gemm_qwen", fh.QKind.Q4_0, QWEN_SHAPES, (512, 2048)),
+                                       ("q4_0_gemm_llama1b", fh.QKind.Q4_0, LLAMA1B_SHAPES, (512, 4096)),
+                                       ("q8_0_gemm_llama1b", fh.QKind.Q8_0, LLAMA1B_SHAPES, (512, 4096))):
+            for m in ms:
+                r = bench_gemm(fh, g, ev, kind, m, shapes, 10)
+                log(f"{name} M={m}:", r)
+                extra[f"{name}_m{m}"] = {"tflops": round(r["tflops"], 2),
+                                         "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+                                         "ms_per_step": r["ms_per_step"], "flops_per_step": r["flops_per_step"]}
+        extra["gemm_operands"] = ("split-f16 x (hi + lo) times exact integer quants on f16 MFMA, f32 accumulate, "
+                                  "f32 block scale per 32-element block")
 
     cpu = None
     if not a.no_cpu:

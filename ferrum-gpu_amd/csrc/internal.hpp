@@ -6,6 +6,7 @@
 #include <atomic>
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "../../include/ferrum_hip.h"
@@ -23,6 +24,11 @@ struct fh_device {
     std::atomic<bool> lost{false};
     std::atomic<bool> closed{false};
     std::atomic<int64_t> refs{1};  // the opener's reference, dropped by fh_device_close
+    // Scratch device memory some launches need (the GEMM's split x), grown on demand and kept
+    // until the device goes away. Commands on the one stream use it in order.
+    std::mutex ws_mu;
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
 };
 
 struct fh_buffer {
@@ -73,6 +79,9 @@ fh_status hip_fail(fh_device *dev, hipError_t e, const char *what);
 
 fh_status alloc_bytes(fh_device *dev, size_t nbytes, void **out);
 
+// The device's workspace, at least `bytes` long (grown after the stream drains).
+fh_status workspace(fh_device *dev, size_t bytes, void **out);
+
 // Reference counting of devices (see struct fh_device).
 void dev_retain(fh_device *dev);
 void dev_release(fh_device *dev);  // destroys the stream and the device on the last release
@@ -122,7 +131,10 @@ hipError_t launch_gemv_group(hipStream_t s, fh_kind kind, int shape, const GemvD
 // gemm.hip
 hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
                         float *y, size_t rows, size_t k, size_t n);
+// The MFMA GEMM (two launches: split x into workspace, then the product); workspace holds
+// gemm_workspace_bytes(rows, k) bytes.
+size_t gemm_workspace_bytes(size_t rows, size_t k);
 hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
-                       float *y, size_t rows, size_t k, size_t n);
+                       float *y, size_t rows, size_t k, size_t n, void *workspace);
 
 }  // namespace fh

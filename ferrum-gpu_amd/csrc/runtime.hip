@@ -67,6 +67,7 @@ void dev_release(fh_device *dev) {
     if (dev->refs.fetch_sub(1) != 1) return;
     (void)hipSetDevice(dev->ordinal);
     (void)hipStreamSynchronize(dev->stream);
+    if (dev->ws) (void)hipFree(dev->ws);
     (void)hipStreamDestroy(dev->stream);
     delete dev;
 }
@@ -76,6 +77,28 @@ static void free_bytes(fh_device *dev, void *p) {
     (void)hipSetDevice(dev->ordinal);
     (void)hipStreamSynchronize(dev->stream);
     (void)hipFree(p);
+}
+
+fh_status workspace(fh_device *dev, size_t bytes, void **out) {
+    std::lock_guard<std::mutex> lock(dev->ws_mu);
+    if (bytes > dev->ws_bytes) {
+        if (dev->ws) {
+            free_bytes(dev, dev->ws);  // waits for the commands still using it
+            dev->ws = nullptr;
+            dev->ws_bytes = 0;
+        }
+        void *p = nullptr;
+        const size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+        hipError_t e = hipMalloc(&p, want);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return hip_fail(dev, e, "workspace");
+        }
+        dev->ws = p;
+        dev->ws_bytes = want;
+    }
+    *out = dev->ws;
+    return FH_OK;
 }
 
 fh_status alloc_bytes(fh_device *dev, size_t nbytes, void **out) {
@@ -520,10 +543,13 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
         if ((st = begin_command(dev, "linear_q"))) return st;
         if (rows) (void)launch_naive(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n);
         return end_command(dev, "linear_q");
-    case FH_PATH_TILED:
+    case FH_PATH_TILED: {
+        void *ws = nullptr;
+        if (rows && (st = workspace(dev, gemm_workspace_bytes(rows, w->k), &ws))) return st;
         if ((st = begin_command(dev, "linear_q"))) return st;
-        if (rows) (void)launch_gemm(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n);
+        if (rows) (void)launch_gemm(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, ws);
         return end_command(dev, "linear_q");
+    }
     default:
         return fail(FH_ERR_INVALID, "unknown kernel path %d", (int)path);
     }
