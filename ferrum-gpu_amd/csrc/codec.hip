@@ -227,7 +227,7 @@ __global__ __launch_bounds__(kThreads) void snap_rows_kernel(const float *__rest
 
 // ---- cols: one thread per (column c, block kb) of an [k, n] matrix ----
 // Quantise down the columns into the planes of GGUF row c (quantise_matrix,
-// ferrum_wgpu/src/ops/quant.rs:238-252): block (c, kb) is block c * nb + kb of the planes.
+// ferrum_wgpu/src/ops/quant.rs:238-252): block (c, kb) goes to slot tile_slot(c, kb, nb) of the planes.
 template <int KIND>
 __global__ __launch_bounds__(kThreads) void encode_cols_kernel(const float *__restrict__ w,
                                                                uint8_t *__restrict__ qs,
@@ -240,14 +240,14 @@ __global__ __launch_bounds__(kThreads) void encode_cols_kernel(const float *__re
         float v[32];
 #pragma unroll
         for (int e = 0; e < 32; e++) v[e] = w[(kb * 32 + e) * n + c];
-        const size_t blk = c * nb + kb;
+        const size_t blk = tile_slot(c, kb, nb), sc = scale_slot(c, kb, nb);
         if constexpr (KIND == FH_Q8_0) {
             float amax = 0.0f;
 #pragma unroll
             for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(v[e]));
             float d = amax / 127.0f;
             float id = d != 0.0f ? 1.0f / d : 0.0f;
-            ds[blk] = (uint16_t)float_to_half_bits(d);
+            ds[sc] = (uint16_t)float_to_half_bits(d);
             u32x4 o[2];
 #pragma unroll
             for (int e = 0; e < 32; e += 4) {
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(kThreads) void encode_cols_kernel(const float *__re
                 if (fabsf(v[e]) > fabsf(m)) m = v[e];
             float d = m / -8.0f;
             float id = d != 0.0f ? 1.0f / d : 0.0f;
-            ds[blk] = (uint16_t)float_to_half_bits(d);
+            ds[sc] = (uint16_t)float_to_half_bits(d);
             u32x4 o;
 #pragma unroll
             for (int j = 0; j < 16; j += 4) {
@@ -293,8 +293,8 @@ __global__ __launch_bounds__(kThreads) void decode_cols_kernel(const uint8_t *__
     const size_t total = nb * n;
     for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (size_t)gridDim.x * kThreads) {
         const size_t kb = t / n, c = t % n;
-        const size_t blk = c * nb + kb;
-        const float d = half_bits_to_float(ds[blk]);
+        const size_t blk = tile_slot(c, kb, nb);
+        const float d = half_bits_to_float(ds[scale_slot(c, kb, nb)]);
         float *col = w + kb * 32 * n + c;
         if constexpr (KIND == FH_Q8_0) {
 #pragma unroll
@@ -324,23 +324,25 @@ __global__ __launch_bounds__(kThreads) void decode_cols_kernel(const uint8_t *__
 template <int KIND>
 __global__ __launch_bounds__(kThreads) void gguf_to_planes_kernel(const uint8_t *__restrict__ src,
                                                                   uint8_t *__restrict__ qs,
-                                                                  uint16_t *__restrict__ ds,
-                                                                  size_t nblocks) {
+                                                                  uint16_t *__restrict__ ds, size_t n,
+                                                                  size_t nb) {
     constexpr int BB = Fmt<KIND>::bytes;
     constexpr int WORDS = KIND == FH_Q8_0 ? 9 : 5;
+    const size_t nblocks = n * nb;
     for (size_t blk = (size_t)blockIdx.x * kThreads + threadIdx.x; blk < nblocks;
          blk += (size_t)gridDim.x * kThreads) {
-        const size_t off = blk * BB;
+        const size_t off = blk * BB;  // block blk of the GGUF rows: row blk / nb, block blk % nb
+        const size_t slot = tile_slot(blk / nb, blk % nb, nb);
         uint32_t win[WORDS];
         load_window<WORDS>(src, off, win);
         const uint32_t sel = quant_sel(off);
-        ds[blk] = (uint16_t)scale_bits(win[0], off);
+        ds[scale_slot(blk / nb, blk % nb, nb)] = (uint16_t)scale_bits(win[0], off);
 #pragma unroll
         for (int h = 0; h < (KIND == FH_Q8_0 ? 2 : 1); h++) {
             u32x4 q;
 #pragma unroll
             for (int i = 0; i < 4; i++) q[i] = quant_word(win, 4 * h + i, sel);
-            __builtin_nontemporal_store(q, (u32x4 *)(qs + blk * (BB - 2) + 16 * h));
+            __builtin_nontemporal_store(q, (u32x4 *)(qs + slot * (BB - 2) + 16 * h));
         }
     }
 }
@@ -348,16 +350,18 @@ __global__ __launch_bounds__(kThreads) void gguf_to_planes_kernel(const uint8_t 
 template <int KIND>
 __global__ __launch_bounds__(kThreads) void planes_to_gguf_kernel(const uint8_t *__restrict__ qs,
                                                                   const uint16_t *__restrict__ ds,
-                                                                  uint8_t *__restrict__ dst,
-                                                                  size_t nblocks) {
+                                                                  uint8_t *__restrict__ dst, size_t n,
+                                                                  size_t nb) {
     constexpr int BB = Fmt<KIND>::bytes;
+    const size_t nblocks = n * nb;
     for (size_t blk = (size_t)blockIdx.x * kThreads + threadIdx.x; blk < nblocks;
          blk += (size_t)gridDim.x * kThreads) {
+        const size_t slot = tile_slot(blk / nb, blk % nb, nb);
         uint16_t *out = (uint16_t *)(dst + blk * BB);  // GGUF blocks are 2-byte aligned
-        out[0] = ds[blk];
+        out[0] = ds[scale_slot(blk / nb, blk % nb, nb)];
 #pragma unroll
         for (int h = 0; h < (KIND == FH_Q8_0 ? 2 : 1); h++) {
-            const u32x4 q = *(const u32x4 *)(qs + blk * (BB - 2) + 16 * h);
+            const u32x4 q = *(const u32x4 *)(qs + slot * (BB - 2) + 16 * h);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 out[1 + 8 * h + 2 * i] = (uint16_t)q[i];
@@ -457,22 +461,22 @@ hipError_t launch_decode_cols(hipStream_t s, fh_kind kind, const uint8_t *qs, co
 }
 
 hipError_t launch_gguf_to_planes(hipStream_t s, fh_kind kind, const uint8_t *src, uint8_t *qs, uint16_t *ds,
-                                 size_t nblocks) {
-    unsigned g = grid_for(nblocks, kThreads, 65535);
+                                 size_t n, size_t nb) {
+    unsigned g = grid_for(n * nb, kThreads, 65535);
     if (kind == FH_Q8_0)
-        gguf_to_planes_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(src, qs, ds, nblocks);
+        gguf_to_planes_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(src, qs, ds, n, nb);
     else
-        gguf_to_planes_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(src, qs, ds, nblocks);
+        gguf_to_planes_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(src, qs, ds, n, nb);
     return hipGetLastError();
 }
 
 hipError_t launch_planes_to_gguf(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, uint8_t *dst,
-                                 size_t nblocks) {
-    unsigned g = grid_for(nblocks, kThreads, 65535);
+                                 size_t n, size_t nb) {
+    unsigned g = grid_for(n * nb, kThreads, 65535);
     if (kind == FH_Q8_0)
-        planes_to_gguf_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(qs, ds, dst, nblocks);
+        planes_to_gguf_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(qs, ds, dst, n, nb);
     else
-        planes_to_gguf_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(qs, ds, dst, nblocks);
+        planes_to_gguf_kernel<FH_Q4_0><<<g, kThreads, 0, s>>>(qs, ds, dst, n, nb);
     return hipGetLastError();
 }
 

@@ -7,6 +7,19 @@
 
 namespace fh {
 
+// Resident weights are stored as tiles: the rows of a weight are taken in groups of 32. In the
+// quant plane the blocks of a group are stored block by block, the group's 32 rows side by side:
+// the quants of block b of row n are slot tile_slot(n, b, nb) (QB bytes each), nb being the
+// row's block count. In the scale plane a group's blocks are taken eight at a time, each row's
+// eight f16 scales side by side (16 bytes), so the scale of block b of row n is element
+// scale_slot(n, b, nb); the last run of eight is padded with zero scales.
+__host__ __device__ __forceinline__ size_t tile_slot(size_t n, size_t b, size_t nb) {
+    return ((n >> 5) * nb + b) * 32 + (n & 31);
+}
+__host__ __device__ __forceinline__ size_t scale_slot(size_t n, size_t b, size_t nb) {
+    return (((n >> 5) * ((nb + 7) >> 3) + (b >> 3)) * 32 + (n & 31)) * 8 + (b & 7);
+}
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 

@@ -1,5 +1,5 @@
 // Multi-row products on resident Q8_0 / Q4_0 weights for gfx950: y[M, N] = x[M, K] * W^T, W held
-// as the quant and scale planes of its N GGUF rows of K/32 blocks (see gemv.hip).
+// as the tiled quant and scale planes of its N GGUF rows of K/32 blocks (tile_slot, scale_slot).
 //
 // naive_kernel: one thread per output, ascending k, the dequantised value formed first and then
 // multiplied (ferrum_wgpu/src/shaders/quant/qlinear.wgsl:18-59). Kept as the baseline path.
@@ -52,8 +52,8 @@ __global__ __launch_bounds__(256) void naive_kernel(const uint8_t *__restrict__ 
     const float *xr = x + (size_t)r * k;
     float acc = 0.0f;
     for (uint32_t b = 0; b < nb; b++) {
-        const size_t blk = (size_t)c * nb + b;
-        const float d = half_bits_to_float(ds[blk]);
+        const size_t blk = tile_slot(c, b, nb);
+        const float d = half_bits_to_float(ds[scale_slot(c, b, nb)]);
         if constexpr (KIND == FH_Q8_0) {
             for (int h = 0; h < 2; h++) {
                 const u32x4 q = *(const u32x4 *)(qs + blk * 32 + 16 * h);
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
                 const int col = cc / CPR, bb = (cc % CPR) / (C::QB / 16), part = cc % (C::QB / 16);
                 const uint32_t n = n0 + col, kb = st * kBKB + bb;
                 rb[i] = n < N && kb < nb ? __builtin_nontemporal_load(
-                                               (const u32x4 *)(qs + ((size_t)n * nb + kb) * C::QB + part * 16))
+                                               (const u32x4 *)(qs + tile_slot(n, kb, nb) * C::QB + part * 16))
                                          : u32x4{0u, 0u, 0u, 0u};
             }
         }
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
             if (cc < kBKB * BN) {
                 const int col = cc / kBKB, bb = cc % kBKB;
                 const uint32_t n = n0 + col, kb = st * kBKB + bb;
-                rh[i] = n < N && kb < nb ? ds[(size_t)n * nb + kb] : 0u;
+                rh[i] = n < N && kb < nb ? ds[scale_slot(n, kb, nb)] : 0u;
             }
         }
     };

@@ -38,9 +38,10 @@ struct fh_buffer {
 };
 
 // A resident quantized weight of k inputs and n outputs (n GGUF rows of nb = k/32 blocks),
-// repacked at upload into two planes that hold exactly the GGUF bytes: the quants of row r at
-// qs + r * nb * QB (QB = 16 Q4_0 / 32 Q8_0, the block without its scale, 16-byte aligned) and
-// the f16 scales of row r at ds + r * nb.
+// repacked at upload into two planes holding the GGUF bytes as tiles (see tile_slot and
+// scale_slot in device_common.hpp): the quants (QB = 16 Q4_0 / 32 Q8_0 bytes per block, the
+// block without its scale) and the f16 scales. Rows are padded to a multiple of 32 with zero
+// blocks.
 struct fh_qweight {
     fh_device *dev = nullptr;
     fh_kind kind = FH_Q8_0;
@@ -48,7 +49,7 @@ struct fh_qweight {
     uint8_t *ptr = nullptr;   // the allocation: quant plane, then scale plane
     uint8_t *qs = nullptr;    // quant plane (256-byte aligned)
     uint16_t *ds = nullptr;   // scale plane
-    size_t nbytes = 0;        // exact GGUF byte count (= the two planes' payload)
+    size_t nbytes = 0;        // exact GGUF byte count of the weight
 };
 
 namespace fh {
@@ -60,9 +61,13 @@ constexpr size_t kPad = 256;
 
 inline size_t block_bytes(fh_kind k) { return k == FH_Q8_0 ? 34 : 18; }
 inline size_t quant_bytes(fh_kind k) { return k == FH_Q8_0 ? 32 : 16; }
-// Offset of the scale plane inside a weight allocation of nblocks blocks.
-inline size_t scale_plane_offset(fh_kind k, size_t nblocks) {
-    return (nblocks * quant_bytes(k) + 255) / 256 * 256;
+// Quant slots of a weight of n rows and nb blocks per row (rows padded to a multiple of 32).
+inline size_t tile_slots(size_t n, size_t nb) { return (n + 31) / 32 * 32 * nb; }
+// Scale-plane elements of the same weight (blocks padded to a multiple of 8).
+inline size_t scale_slots(size_t n, size_t nb) { return (n + 31) / 32 * 32 * ((nb + 7) / 8 * 8); }
+// Offset of the scale plane inside a weight allocation of `slots` quant slots.
+inline size_t scale_plane_offset(fh_kind k, size_t slots) {
+    return (slots * quant_bytes(k) + 255) / 256 * 256;
 }
 inline bool kind_ok(int k) { return k == FH_Q8_0 || k == FH_Q4_0; }
 
@@ -102,31 +107,36 @@ hipError_t launch_snap_cols(hipStream_t s, const float *src, float *dst, size_t 
                             size_t cols_out);
 hipError_t launch_copy_f32(hipStream_t s, const float *src, float *dst, size_t n);
 
-// GGUF bytes <-> planes (upload_qweight and read_gguf)
+// GGUF rows (n rows of nb blocks) <-> tiled planes (upload_qweight and read_gguf)
 hipError_t launch_gguf_to_planes(hipStream_t s, fh_kind kind, const uint8_t *src, uint8_t *qs,
-                                 uint16_t *ds, size_t nblocks);
+                                 uint16_t *ds, size_t n, size_t nb);
 hipError_t launch_planes_to_gguf(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds,
-                                 uint8_t *dst, size_t nblocks);
+                                 uint8_t *dst, size_t n, size_t nb);
 
 // gemv.hip
-struct GemvDesc {          // one batch-1 product, as the kernel reads it
+struct GemvDesc {          // one batch-1 product, as the kernels read it
     const uint8_t *qs;     // quant plane
     const uint16_t *ds;    // scale plane
     const float *x;
     float *y;
+    uint8_t *prep;         // gemv_prep_bytes(k) bytes of prepared x
     uint32_t nb;           // blocks per row (k / 32)
     uint32_t n;            // rows (outputs)
-    uint32_t task0;        // first task index of this product in its launch
+    uint32_t task0;        // first task (group of 32 rows) of this product in its launch
     uint32_t pad;
 };
-// Launch shape for n rows of nb blocks, or -1 when a row is too wide for the kernel's registers
-// (k > 8192) or the weight too large for its 32-bit offsets.
-int gemv_shape(fh_kind kind, size_t nb, size_t n);
-uint32_t gemv_tasks(int shape, size_t n);
+// Whether the kernel's 32-bit offsets cover rows of k inputs (k a multiple of 32, up to 2^25).
+bool gemv_supported(fh_kind kind, size_t k, size_t n);
+size_t gemv_prep_bytes(size_t k);
+uint32_t gemv_tasks(size_t n);
+// Two launches: prepare x into `prep` (gemv_prep_bytes(k) bytes), then the product.
 hipError_t launch_gemv(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
-                       float *y, size_t k, size_t n, int cus);
-hipError_t launch_gemv_group(hipStream_t s, fh_kind kind, int shape, const GemvDesc *descs, uint32_t count,
-                             uint32_t tasks, int cus);
+                       float *y, size_t k, size_t n, void *prep, int cus);
+// Many products of one format: `descs` (device memory) in task order with task0 prefix sums,
+// `map` (device memory) the product of each of the `tasks` tasks, max_nb the widest product's
+// block count.
+hipError_t launch_gemv_group(hipStream_t s, fh_kind kind, const GemvDesc *descs, const uint32_t *map,
+                             uint32_t count, uint32_t tasks, uint32_t max_nb, int cus);
 
 // gemm.hip
 hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,

@@ -188,10 +188,10 @@ fh_status new_qweight(fh_device *dev, fh_kind kind, size_t k, size_t n, fh_qweig
         return fail(FH_ERR_INVALID, "a %zu x %zu weight is not whole 32-element blocks", k, n);
     if (n == 0 || n > (1u << 30) || k > (1u << 30) || (k / QK) * n > (1ull << 32))
         return fail(FH_ERR_INVALID, "a %zu x %zu weight is out of range", k, n);
-    const size_t nblocks = (k / QK) * n;
-    size_t nbytes = nblocks * block_bytes(kind);
+    const size_t slots = tile_slots(n, k / QK);
+    size_t nbytes = (k / QK) * n * block_bytes(kind);
     void *p = nullptr;
-    fh_status st = alloc_bytes(dev, scale_plane_offset(kind, nblocks) + nblocks * 2, &p);
+    fh_status st = alloc_bytes(dev, scale_plane_offset(kind, slots) + scale_slots(n, k / QK) * 2, &p);
     if (st) return st;
     fh_qweight *w = new (std::nothrow) fh_qweight;
     if (!w) {
@@ -205,7 +205,7 @@ fh_status new_qweight(fh_device *dev, fh_kind kind, size_t k, size_t n, fh_qweig
     w->n = n;
     w->ptr = (uint8_t *)p;
     w->qs = (uint8_t *)p;
-    w->ds = (uint16_t *)((uint8_t *)p + scale_plane_offset(kind, nblocks));
+    w->ds = (uint16_t *)((uint8_t *)p + scale_plane_offset(kind, slots));
     w->nbytes = nbytes;
     *out = w;
     return FH_OK;
@@ -217,12 +217,14 @@ struct fh_gemv_plan {
     fh_device *dev = nullptr;
     struct Launch {
         fh_kind kind;
-        int shape;
-        size_t first, count;
-        uint32_t tasks;
+        size_t first, count;  // descriptors
+        size_t map0;          // first entry of the launch's task -> product map
+        uint32_t tasks, max_nb;
     };
     std::vector<Launch> launches;
     GemvDesc *descs = nullptr;  // device array
+    uint32_t *map = nullptr;    // device array: per launch, the product of each task
+    uint8_t *prep = nullptr;    // prepared x of every product
     uint64_t bytes = 0;
 };
 
@@ -430,8 +432,8 @@ fh_status fh_qweight_upload_gguf(fh_device *dev, fh_kind kind, const uint8_t *by
     if ((st = alloc_bytes(dev, len, &stage)) == FH_OK) {
         st = upload_bytes(dev, stage, bytes, len, "upload_qweight");
         if (st == FH_OK && (st = begin_command(dev, "upload_qweight")) == FH_OK) {
-            (void)launch_gguf_to_planes(dev->stream, kind, (const uint8_t *)stage, (*out)->qs, (*out)->ds,
-                                        len / block_bytes(kind));
+            (void)launch_gguf_to_planes(dev->stream, kind, (const uint8_t *)stage, (*out)->qs, (*out)->ds, n,
+                                        k / QK);
             st = end_command(dev, "upload_qweight");
         }
         free_bytes(dev, stage);  // waits for the repack
@@ -502,7 +504,7 @@ fh_status fh_qweight_read_gguf(fh_device *dev, const fh_qweight *w, uint8_t *hos
     void *stage = nullptr;
     if ((st = alloc_bytes(dev, len, &stage))) return st;
     if ((st = begin_command(dev, "read_gguf")) == FH_OK) {
-        (void)launch_planes_to_gguf(dev->stream, w->kind, w->qs, w->ds, (uint8_t *)stage, len / block_bytes(w->kind));
+        (void)launch_planes_to_gguf(dev->stream, w->kind, w->qs, w->ds, (uint8_t *)stage, w->n, w->k / QK);
         if ((st = end_command(dev, "read_gguf")) == FH_OK) st = read_bytes(dev, host, stage, len, "read_gguf");
     }
     free_bytes(dev, stage);
@@ -522,8 +524,7 @@ fh_status fh_qweight_dequantise(fh_device *dev, const fh_qweight *w, fh_buffer *
 // ---- linear layers ----
 
 fh_path fh_choose(size_t rows, fh_kind kind, size_t k, size_t n) {
-    (void)n;
-    if (rows == 1 && kind_ok(kind) && gemv_shape(kind, k / QK, n) >= 0) return FH_PATH_GEMV;
+    if (rows == 1 && kind_ok(kind) && gemv_supported(kind, k, n)) return FH_PATH_GEMV;
     return FH_PATH_TILED;
 }
 
@@ -532,13 +533,17 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
     if (path == FH_PATH_AUTO) path = fh_choose(rows, w->kind, w->k, w->n);
     fh_status st;
     switch (path) {
-    case FH_PATH_GEMV:
+    case FH_PATH_GEMV: {
         if (rows != 1) return fail(FH_ERR_INVALID, "the GEMV kernel takes one row, not %zu", rows);
-        if (gemv_shape(w->kind, w->k / QK, w->n) < 0)
-            return fail(FH_ERR_INVALID, "the GEMV kernel takes k <= 8192, not %zu", w->k);
+        if (!gemv_supported(w->kind, w->k, w->n))
+            return fail(FH_ERR_INVALID, "the GEMV kernel's 32-bit offsets do not cover a %zu x %zu weight",
+                        w->n, w->k);
+        void *prep = nullptr;
+        if ((st = workspace(dev, gemv_prep_bytes(w->k), &prep))) return st;
         if ((st = begin_command(dev, "linear_q"))) return st;
-        (void)launch_gemv(dev->stream, w->kind, w->qs, w->ds, x, y, w->k, w->n, dev->cus);
+        (void)launch_gemv(dev->stream, w->kind, w->qs, w->ds, x, y, w->k, w->n, prep, dev->cus);
         return end_command(dev, "linear_q");
+    }
     case FH_PATH_NAIVE:
         if ((st = begin_command(dev, "linear_q"))) return st;
         if (rows) (void)launch_naive(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n);
@@ -588,9 +593,8 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
     if (!plan) return fail(FH_ERR_OOM, "host out of memory");
     dev_retain(dev);
     plan->dev = dev;
-    // Check every problem, then group by (format, launch shape), keeping the caller's order
-    // inside a group: each group is one launch.
-    std::vector<int> shape(count);
+    // Check every problem, then group by format, keeping the caller's order inside a group:
+    // each group is one launch (x preparation, then the products).
     for (size_t i = 0; i < count; i++) {
         const fh_gemv_problem &p = problems[i];
         if (!p.w || !p.x || !p.y) {
@@ -601,42 +605,63 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
             fh_gemv_plan_free(plan);
             return fail(FH_ERR_INVALID, "gemv plan: problem %zu lives on another device", i);
         }
-        shape[i] = gemv_shape(p.w->kind, p.w->k / QK, p.w->n);
-        if (shape[i] < 0) {
+        if (!gemv_supported(p.w->kind, p.w->k, p.w->n)) {
             fh_gemv_plan_free(plan);
-            return fail(FH_ERR_INVALID, "gemv plan: problem %zu has k = %zu > 8192", i, p.w->k);
+            return fail(FH_ERR_INVALID, "gemv plan: problem %zu (%zu x %zu) is too large for one product", i,
+                        p.w->n, p.w->k);
         }
     }
     std::vector<GemvDesc> host;
+    std::vector<uint32_t> map;      // per launch, the product (launch-local index) of each task
+    std::vector<size_t> prep_off;  // byte offset of each product's prepared x in plan->prep
     host.reserve(count);
+    size_t prep_bytes = 0;
     for (int kind : {FH_Q8_0, FH_Q4_0}) {
-        for (int sh = 0; sh < 64; sh++) {
-            fh_gemv_plan::Launch L{(fh_kind)kind, sh, host.size(), 0, 0};
-            for (size_t i = 0; i < count; i++) {
-                const fh_gemv_problem &p = problems[i];
-                if ((int)p.w->kind != kind || shape[i] != sh) continue;
-                GemvDesc d{p.w->qs, p.w->ds, p.x, p.y, (uint32_t)(p.w->k / QK), (uint32_t)p.w->n, L.tasks, 0};
-                uint64_t t = (uint64_t)L.tasks + gemv_tasks(sh, p.w->n);
-                if (t > (1ull << 31)) {
-                    fh_gemv_plan_free(plan);
-                    return fail(FH_ERR_INVALID, "gemv plan: too many rows in one launch");
-                }
-                L.tasks = (uint32_t)t;
-                host.push_back(d);
-                plan->bytes += p.w->nbytes + 4ull * (p.w->k + p.w->n);
-                L.count++;
+        fh_gemv_plan::Launch L{(fh_kind)kind, host.size(), 0, map.size(), 0, 0};
+        for (size_t i = 0; i < count; i++) {
+            const fh_gemv_problem &p = problems[i];
+            if ((int)p.w->kind != kind) continue;
+            const uint32_t nb = (uint32_t)(p.w->k / QK);
+            GemvDesc d{p.w->qs, p.w->ds, p.x, p.y, nullptr, nb, (uint32_t)p.w->n, L.tasks, 0};
+            const uint64_t t = (uint64_t)L.tasks + gemv_tasks(p.w->n);
+            if (t >= (1ull << 31)) {
+                fh_gemv_plan_free(plan);
+                return fail(FH_ERR_INVALID, "gemv plan: too many rows in one launch");
             }
-            if (L.count) plan->launches.push_back(L);
+            map.insert(map.end(), gemv_tasks(p.w->n), (uint32_t)L.count);
+            L.tasks = (uint32_t)t;
+            L.max_nb = nb > L.max_nb ? nb : L.max_nb;
+            host.push_back(d);
+            prep_off.push_back(prep_bytes);
+            prep_bytes += gemv_prep_bytes(p.w->k);
+            plan->bytes += p.w->nbytes + 4ull * (p.w->k + p.w->n);
+            L.count++;
         }
+        if (L.count) plan->launches.push_back(L);
     }
     if (!host.empty()) {
         void *p = nullptr;
+        if ((st = alloc_bytes(dev, prep_bytes, &p))) {
+            fh_gemv_plan_free(plan);
+            return st;
+        }
+        plan->prep = (uint8_t *)p;
+        for (size_t i = 0; i < host.size(); i++) host[i].prep = plan->prep + prep_off[i];
         if ((st = alloc_bytes(dev, host.size() * sizeof(GemvDesc), &p))) {
             fh_gemv_plan_free(plan);
             return st;
         }
         plan->descs = (GemvDesc *)p;
         if ((st = upload_bytes(dev, p, host.data(), host.size() * sizeof(GemvDesc), "gemv plan"))) {
+            fh_gemv_plan_free(plan);
+            return st;
+        }
+        if ((st = alloc_bytes(dev, map.size() * sizeof(uint32_t), &p))) {
+            fh_gemv_plan_free(plan);
+            return st;
+        }
+        plan->map = (uint32_t *)p;
+        if ((st = upload_bytes(dev, p, map.data(), map.size() * sizeof(uint32_t), "gemv plan"))) {
             fh_gemv_plan_free(plan);
             return st;
         }
@@ -651,8 +676,8 @@ fh_status fh_gemv_plan_run(fh_device *dev, const fh_gemv_plan *plan) {
     if (!plan || plan->dev != dev) return fail(FH_ERR_INVALID, "gemv plan: wrong device");
     for (const auto &L : plan->launches) {
         if ((st = begin_command(dev, "gemv plan"))) return st;
-        (void)launch_gemv_group(dev->stream, L.kind, L.shape, plan->descs + L.first, (uint32_t)L.count,
-                                L.tasks, dev->cus);
+        (void)launch_gemv_group(dev->stream, L.kind, plan->descs + L.first, plan->map + L.map0, (uint32_t)L.count,
+                                L.tasks, L.max_nb, dev->cus);
         if ((st = end_command(dev, "gemv plan"))) return st;
     }
     return FH_OK;
@@ -665,6 +690,8 @@ void fh_gemv_plan_free(fh_gemv_plan *plan) {
     if (!plan) return;
     fh_device *dev = plan->dev;
     if (plan->descs) free_bytes(dev, plan->descs);
+    if (plan->prep) free_bytes(dev, plan->prep);
+    if (plan->map) free_bytes(dev, plan->map);
     delete plan;
     dev_release(dev);
 }

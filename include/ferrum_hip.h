@@ -157,8 +157,8 @@ FH_API fh_status fh_linear_q_ptr(fh_device *dev, const float *x, const fh_qweigh
 /* No counterpart in the reference: one launch for many independent batch-1 products
  * y_i = x_i * W_i (a decode step's projections, or several models' layers). The plan is built
  * once (the descriptors are uploaded then) and run any number of times; x_i and y_i are device
- * pointers of k_i and n_i floats. Products with the same block format and input width class
- * share a launch. */
+ * pointers of k_i and n_i floats. Products with the same block format share a launch (two
+ * kernels: x preparation, then the products). */
 typedef struct fh_gemv_problem {
     const fh_qweight *w;
     const float *x;
@@ -167,7 +167,7 @@ typedef struct fh_gemv_problem {
 FH_API fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, size_t count,
                               fh_gemv_plan **out);
 FH_API fh_status fh_gemv_plan_run(fh_device *dev, const fh_gemv_plan *plan);
-/* Launches one run issues, and the algorithmic bytes it moves (weights + x + y). */
+/* Grouped launches one run issues (one per block format), and the algorithmic bytes it moves (weights + x + y). */
 FH_API size_t fh_gemv_plan_launches(const fh_gemv_plan *plan);
 FH_API uint64_t fh_gemv_plan_bytes(const fh_gemv_plan *plan);
 FH_API void fh_gemv_plan_free(fh_gemv_plan *plan);
