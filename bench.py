@@ -50,13 +50,15 @@ class HipEvents:
     """HIP events recorded on the library's own stream (the one its kernels run on), through the
     HIP runtime libferrum_hip already loaded (RTLD_NOLOAD: never a second runtime)."""
 
+    DISABLE_SYSTEM_FENCE = 0x20000000  # hipEventDisableSystemFence
+
     def __init__(self, g):
         self.hip = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD | ctypes.RTLD_GLOBAL)
         self.stream = ctypes.c_void_p(g.stream())
-        for name in ("hipEventCreate", "hipEventRecord", "hipEventSynchronize", "hipEventElapsedTime",
+        for name in ("hipEventCreateWithFlags", "hipEventRecord", "hipEventSynchronize", "hipEventElapsedTime",
                      "hipEventDestroy"):
             getattr(self.hip, name).restype = ctypes.c_int
-        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
         self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
         self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
@@ -66,8 +68,10 @@ class HipEvents:
         evs = []
         for _ in range(n):
             e = ctypes.c_void_p()
-            if self.hip.hipEventCreate(ctypes.byref(e)) != 0:
-                raise RuntimeError("hipEventCreate failed")
+            # timing events without a system-scope fence: a device-scope release is enough to
+            # order them after the kernels on the stream, and the system fence costs microseconds
+            if self.hip.hipEventCreateWithFlags(ctypes.byref(e), self.DISABLE_SYSTEM_FENCE) != 0:
+                raise RuntimeError("hipEventCreateWithFlags failed")
             evs.append(e)
         return evs
 
@@ -90,8 +94,9 @@ class HipEvents:
 
 def bench_gemv_pool(fh, g, ev, kind, groups, pool_bytes, steps, warmup, seed=0):
     """Batch-1 GEMV over a pool of distinct resident weights. `groups` is a list of shape lists;
-    each group becomes one grouped launch (one plan) per step, timed with its own pair of HIP
-    events, so each launch's average duration is known as well as the step's."""
+    each group becomes one grouped launch (one plan) per step. The K timed steps run back to back
+    between two HIP events (the step time); a second pass of K steps records an event pair around
+    every launch, so each launch's average duration is known too."""
     rng = np.random.default_rng(seed)
     kb = kind.file_bytes()
     shapes = [s for grp in groups for s in grp]
@@ -118,19 +123,29 @@ def bench_gemv_pool(fh, g, ev, kind, groups, pool_bytes, steps, warmup, seed=0):
         for p in plans:
             p.run()
     g.sync()
-    npl = len(plans)
-    evs = ev.create(steps * (npl + 1))
+    # the timed steps
+    e0, e1 = ev.create(2)
     t0 = time.perf_counter()
+    ev.record(e0)
     for s in range(steps):
-        for i, p in enumerate(plans):
-            ev.record(evs[s * (npl + 1) + i])
+        for p in plans:
             p.run()
-        ev.record(evs[s * (npl + 1) + npl])
+    ev.record(e1)
     g.sync()
     wall = time.perf_counter() - t0
-    launch_ms = [[ev.ms(evs[s * (npl + 1) + i], evs[s * (npl + 1) + i + 1]) for s in range(steps)]
+    step_ms = ev.ms(e0, e1) / steps
+    ev.destroy([e0, e1])
+    # per-launch durations
+    npl = len(plans)
+    evs = ev.create(steps * npl * 2)
+    for s in range(steps):
+        for i, p in enumerate(plans):
+            ev.record(evs[2 * (s * npl + i)])
+            p.run()
+            ev.record(evs[2 * (s * npl + i) + 1])
+    g.sync()
+    launch_ms = [[ev.ms(evs[2 * (s * npl + i)], evs[2 * (s * npl + i) + 1]) for s in range(steps)]
                  for i in range(npl)]
-    step_ms = ev.ms(evs[0], evs[-1]) / steps  # first event of step 0 to the last of the last step
     ev.destroy(evs)
     step_bytes = sum(p.bytes() for p in plans)
     launches = []

@@ -63,27 +63,54 @@ constexpr int kBatch = 8;                   // blocks per pipeline batch
 // 16 slots; B lane (row, h) loads quant bytes 8h..8h+7 (Q4_0: low nibbles are slots 0..7, high
 // nibbles slots 8..15) or 16h..16h+15 (Q8_0: slot i is byte i).
 template <int KIND>
-__device__ __forceinline__ int elem_of_slot(int h, int i) {
+__host__ __device__ constexpr int elem_of_slot(int h, int i) {
     if constexpr (KIND == FH_Q8_0)
         return 16 * h + i;
     else
         return i < 8 ? 8 * h + i : 16 + 8 * h + (i - 8);
 }
 
-// ---- x preparation: one thread per block, one workgroup row per product ----
+// The prepared-x writer gives lane j (elements 4j .. 4j + 3 of a block) one dword of each
+// 32-byte limb row: the slots of those four elements, in order.
+template <int KIND>
+__host__ __device__ constexpr int prep_dword(int j) {
+    return KIND == FH_Q8_0 ? j : (j == 2 || j == 3) ? j + 2 : (j == 4 || j == 5) ? j - 2 : j;
+}
+template <int KIND>
+constexpr bool prep_dwords_match_slots() {
+    for (int j = 0; j < 8; j++)
+        for (int k = 0; k < 4; k++) {
+            const int byte = 4 * prep_dword<KIND>(j) + k;
+            if (elem_of_slot<KIND>(byte / 16, byte % 16) != 4 * j + k) return false;
+        }
+    return true;
+}
+static_assert(prep_dwords_match_slots<FH_Q8_0>() && prep_dwords_match_slots<FH_Q4_0>(),
+              "prepared-x dwords must hold the MFMA k slots");
+
+// ---- x preparation: eight lanes per block (four elements each), a row of workgroups per product ----
 template <int KIND>
 __global__ __launch_bounds__(256) void gemv_prep_kernel(const GemvDesc *__restrict__ descs, GemvDesc one) {
     const GemvDesc d = descs ? descs[blockIdx.x] : one;
-    for (uint32_t b = blockIdx.y * 256 + threadIdx.x; b < d.nb; b += gridDim.y * 256) {
-        float v[32];  // (4-byte loads: x may be any float-aligned device pointer)
+    const int j = threadIdx.x % 8;  // elements 4j .. 4j + 3 of the block
+    const bool aligned = ((uintptr_t)d.x & 15) == 0;
+    // (the loop bound is the same for the eight lanes of a block, so the shuffles below see
+    // all eight)
+    for (uint32_t b = (blockIdx.y * 256 + threadIdx.x) / 8; b < d.nb; b += gridDim.y * 32) {
+        const float *xb = d.x + (size_t)b * 32 + 4 * j;
+        f32x4 v;
+        if (aligned) {
+            v = *(const f32x4 *)xb;
+        } else {
+            v = f32x4{xb[0], xb[1], xb[2], xb[3]};
+        }
+        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        int finite = (int)(fabsf(v.x) <= 3.4028235e38f) & (int)(fabsf(v.y) <= 3.4028235e38f) &
+                     (int)(fabsf(v.z) <= 3.4028235e38f) & (int)(fabsf(v.w) <= 3.4028235e38f);  // 0: inf, NaN
 #pragma unroll
-        for (int e = 0; e < 32; e++) v[e] = d.x[(size_t)b * 32 + e];
-        float amax = 0.0f;
-        bool finite = true;
-#pragma unroll
-        for (int e = 0; e < 32; e++) {
-            amax = fmaxf(amax, fabsf(v[e]));
-            finite = finite && (fabsf(v[e]) <= 3.4028235e38f);  // false for inf and NaN
+        for (int m = 1; m < 8; m *= 2) {
+            amax = fmaxf(amax, __shfl_xor(amax, m, 8));
+            finite &= __shfl_xor(finite, m, 8);
         }
         // grid 2^-sh with 2^21 <= amax * 2^sh < 2^22 (subnormal amax: exponent field 1); the
         // scaling is split in two exact power-of-two products so that no factor overflows
@@ -94,40 +121,34 @@ __global__ __launch_bounds__(256) void gemv_prep_kernel(const GemvDesc *__restri
         const float xs = !finite ? __builtin_nanf("")
                          : sh <= 126 ? __uint_as_float((uint32_t)(127 - sh) << 23)  // 2^-sh, normal
                                      : __uint_as_float(1u << (149 - sh));            // 2^-sh, subnormal
-        uint32_t rows[3][8];  // limb rows, 32 slot bytes each
+        uint32_t la = 0, lb = 0, lc = 0;
         int32_t sum = 0;
 #pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                uint32_t la = 0, lb = 0, lc = 0;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    // |xi| <= 2^22; non-finite blocks take 0 here and NaN through xs
-                    const float sx = finite ? (v[elem_of_slot<KIND>(h, 4 * w + k)] * m1) * m2 : 0.0f;
-                    const int32_t xi = (int32_t)rintf(sx);
-                    const int32_t c = (xi << 24) >> 24;
-                    const int32_t r = (xi - c) >> 8;
-                    const int32_t bb = (r << 24) >> 24;
-                    const int32_t a = (r - bb) >> 8;
-                    la |= (uint32_t)(a & 0xff) << (8 * k);
-                    lb |= (uint32_t)(bb & 0xff) << (8 * k);
-                    lc |= (uint32_t)(c & 0xff) << (8 * k);
-                    sum += xi;
-                }
-                rows[0][4 * h + w] = la;
-                rows[1][4 * h + w] = lb;
-                rows[2][4 * h + w] = lc;
-            }
-        u32x4 *out = (u32x4 *)(d.prep + (size_t)b * kPrepBytes);
-#pragma unroll
-        for (int l = 0; l < 3; l++) {
-            out[2 * l] = u32x4{rows[l][0], rows[l][1], rows[l][2], rows[l][3]};
-            out[2 * l + 1] = u32x4{rows[l][4], rows[l][5], rows[l][6], rows[l][7]};
+        for (int k = 0; k < 4; k++) {
+            // |xi| <= 2^22; non-finite blocks take 0 here and NaN through xs
+            const float sx = finite ? (v[k] * m1) * m2 : 0.0f;
+            const int32_t xi = (int32_t)rintf(sx);
+            const int32_t c = (xi << 24) >> 24;
+            const int32_t r = (xi - c) >> 8;
+            const int32_t bb = (r << 24) >> 24;
+            const int32_t a = (r - bb) >> 8;
+            la |= (uint32_t)(a & 0xff) << (8 * k);
+            lb |= (uint32_t)(bb & 0xff) << (8 * k);
+            lc |= (uint32_t)(c & 0xff) << (8 * k);
+            sum += xi;
         }
-        const int32_t bias = KIND == FH_Q4_0 ? -8 * sum : 0;
-        out[6] = u32x4{__float_as_uint(xs), (uint32_t)bias, 0u, 0u};
-        out[7] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int m = 1; m < 8; m *= 2) sum += __shfl_xor(sum, m, 8);
+        const int dw = prep_dword<KIND>(j);
+        uint32_t *rec = (uint32_t *)(d.prep + (size_t)b * kPrepBytes);
+        rec[dw] = la;
+        rec[8 + dw] = lb;
+        rec[16 + dw] = lc;
+        if (j == 0) {
+            const int32_t bias = KIND == FH_Q4_0 ? -8 * sum : 0;
+            ((u32x4 *)rec)[6] = u32x4{__float_as_uint(xs), (uint32_t)bias, 0u, 0u};
+            ((u32x4 *)rec)[7] = u32x4{0u, 0u, 0u, 0u};
+        }
     }
 }
 
@@ -223,10 +244,10 @@ __device__ __forceinline__ i32x4 nibbles(uint32_t q0, uint32_t q1) {
 
 // The batch's contribution to the lane's accumulator: lanes 0..31 take the even blocks of the
 // batch, lanes 32..63 the odd ones (row lane % 32 in both halves).
-template <int KIND>
+template <int KIND, int PAIRS = kBatch / 2>
 __device__ __forceinline__ void compute_batch(const Batch<KIND> &bt, bool upper, float &acc) {
 #pragma unroll
-    for (int p = 0; p < kBatch / 2; p++) {  // blocks 2p and 2p + 1 of the batch
+    for (int p = 0; p < PAIRS; p++) {  // blocks 2p and 2p + 1 of the batch
         i32x4 be, bo;
         if constexpr (KIND == FH_Q8_0) {
             be = __builtin_bit_cast(i32x4, bt.q[2 * p]);
@@ -329,7 +350,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ 
     for (;;) {
         load_batch<KIND>(b1, ltk, lp.b, o);
         __builtin_amdgcn_sched_barrier(0);
-        compute_batch<KIND>(b0, upper, acc);
+        if (cp.b + kBatch / 2 >= cp.nb)
+            compute_batch<KIND, kBatch / 4>(b0, upper, acc);  // a task's last half batch
+        else
+            compute_batch<KIND>(b0, upper, acc);
         __builtin_amdgcn_sched_barrier(0);
         finish(cp);
         if (lp.t >= t1) break;
@@ -337,7 +361,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ 
         advance();
         load_batch<KIND>(b0, ltk, lp.b, o);
         __builtin_amdgcn_sched_barrier(0);
-        compute_batch<KIND>(b1, upper, acc);
+        if (cp.b + kBatch / 2 >= cp.nb)
+            compute_batch<KIND, kBatch / 4>(b1, upper, acc);
+        else
+            compute_batch<KIND>(b1, upper, acc);
         __builtin_amdgcn_sched_barrier(0);
         finish(cp);
         if (lp.t >= t1) break;
@@ -360,8 +387,8 @@ uint32_t waves_per_cu() {
 template <int KIND>
 hipError_t launch_kind(hipStream_t s, const GemvDesc *descs, const uint32_t *map, const GemvDesc &one,
                        uint32_t count, uint32_t tasks, uint32_t max_nb, int cus) {
-    // x preparation: a row of workgroups per product
-    const uint32_t py = (max_nb + 255) / 256;
+    // x preparation: a row of workgroups per product (32 blocks per workgroup)
+    const uint32_t py = (max_nb + 31) / 32;
     gemv_prep_kernel<KIND><<<dim3(count, py < 4096 ? py : 4096), 256, 0, s>>>(descs, one);
     // as many wavefronts as fit on the chip at once (or the requested per-CU count), each an
     // equal share of the tasks
