@@ -92,6 +92,20 @@ class HipEvents:
             self.hip.hipEventDestroy(e)
 
 
+def measured_traffic(bytes_per_launch):
+    """HBM bytes per launch of this workload from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes (calibrated against the copy kernel), when they were taken on the same launch (same
+    algorithmic bytes); None otherwise."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_q4_0_qwen_pool.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return None
+    L = d.get("launches", {}).get(str(bytes_per_launch))
+    return L and {"traffic_bytes": L["traffic_bytes"], "source": d.get("source", path)}
+
+
 def bench_gemv_pool(fh, g, ev, kind, groups, pool_bytes, steps, warmup, seed=0):
     """Batch-1 GEMV over a pool of distinct resident weights. `groups` is a list of shape lists;
     each group becomes one grouped launch (one plan) per step. The K timed steps run back to back
@@ -286,6 +300,7 @@ def main():
 
     gbs = head["gbs"]
     dom = max(head["launches"], key=lambda L: L["avg_ms"])  # the launch that takes the most time
+    traffic = measured_traffic(dom["bytes"])
     out = {
         "metric": "Q4_0 batch-1 GEMV HBM GB/s at Qwen2-0.5B layer shapes",
         "value": round(gbs, 2),
@@ -303,9 +318,11 @@ def main():
                                f"{head['copies']} distinct copies each ({head['bytes_per_step'] / 2**30:.2f} GiB per step)",
                    "products_per_step": head["products"], "launches_per_step": head["launches_per_step"]},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": f"grouped Q4_0 GEMV over {dom['shapes']} x {head['copies']}",
-                     "bytes_per_launch": dom["bytes"], "avg_launch_ms": round(dom["avg_ms"], 5)},
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic and traffic["traffic_bytes"],
+                     "kernel": f"grouped Q4_0 GEMV (x preparation + product kernels) over {dom['shapes']} x "
+                               f"{head['copies']}",
+                     "bytes_per_launch": dom["bytes"], "avg_launch_ms": round(dom["avg_ms"], 5),
+                     "traffic_source": traffic and traffic["source"]},
         "launches": [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in L.items()}
                      for L in head["launches"]],
         "cpu_baseline": cpu and {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
