@@ -29,11 +29,12 @@
 //
 // Work: a task is one group of 32 rows of one product; each wavefront takes a contiguous range
 // of tasks (one launch can hold many products: descriptors in device memory, and a map from
-// task to product for each wavefront's first task), and within a task walks the blocks eight at
-// a time with the next eight blocks' loads
-// in flight while the current eight are computed. A task's buffer descriptors end at its last
-// block, and block offsets are added in the offset register the range check covers, so loads
-// past it read 0.
+// task to product for each wavefront's first task) and streams them as one sequence of 8-block
+// batches, the next batch's loads in flight while the current one is computed. A task's buffer
+// descriptors end at its last block, and block offsets are added in the offset register the
+// range check covers, so loads past it read 0. The prepared x comes from the preparation
+// kernel's global buffer or, when a wavefront's share of tasks is long enough, from its own
+// LDS region, filled when it starts each product (no separate launch).
 #include <cstdlib>
 
 #include "device_common.hpp"
@@ -88,68 +89,78 @@ constexpr bool prep_dwords_match_slots() {
 static_assert(prep_dwords_match_slots<FH_Q8_0>() && prep_dwords_match_slots<FH_Q4_0>(),
               "prepared-x dwords must hold the MFMA k slots");
 
-// ---- x preparation: eight lanes per block (four elements each), a row of workgroups per product ----
+// ---- x preparation: eight lanes per block, lane j taking elements 4j .. 4j + 3 ----
+// Writes block b's 128-byte record at rec (a global or an LDS pointer). The eight lanes of a
+// block must run this together (they reduce over one another with shuffles).
+template <int KIND, class U32Ptr>
+__device__ __forceinline__ void prep_block(const float *__restrict__ x, bool aligned, uint32_t b, int j, U32Ptr rec) {
+    // (global-address-space loads: flat ones would also count against the LDS counter)
+    typedef __attribute__((address_space(1))) const float gfloat;
+    typedef __attribute__((address_space(1))) const f32x4 gf32x4;
+    gfloat *xb = (gfloat *)(x + (size_t)b * 32 + 4 * j);
+    f32x4 v;
+    if (aligned) {
+        v = *(gf32x4 *)xb;
+    } else {
+        v = f32x4{xb[0], xb[1], xb[2], xb[3]};
+    }
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    int finite = (int)(fabsf(v.x) <= 3.4028235e38f) & (int)(fabsf(v.y) <= 3.4028235e38f) &
+                 (int)(fabsf(v.z) <= 3.4028235e38f) & (int)(fabsf(v.w) <= 3.4028235e38f);  // 0: inf, NaN
+#pragma unroll
+    for (int m = 1; m < 8; m *= 2) {
+        amax = fmaxf(amax, __shfl_xor(amax, m, 8));
+        finite &= __shfl_xor(finite, m, 8);
+    }
+    // grid 2^-sh with 2^21 <= amax * 2^sh < 2^22 (subnormal amax: exponent field 1); the
+    // scaling is split in two exact power-of-two products so that no factor overflows
+    const int sh = 148 - (int)max(__float_as_uint(amax) >> 23, 1u);  // -106 .. 147
+    const int sh1 = min(sh, 100);
+    const float m1 = __uint_as_float((uint32_t)(127 + sh1) << 23);
+    const float m2 = __uint_as_float((uint32_t)(127 + sh - sh1) << 23);
+    const float xs = !finite ? __builtin_nanf("")
+                     : sh <= 126 ? __uint_as_float((uint32_t)(127 - sh) << 23)  // 2^-sh, normal
+                                 : __uint_as_float(1u << (149 - sh));            // 2^-sh, subnormal
+    uint32_t la = 0, lb = 0, lc = 0;
+    int32_t sum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        // |xi| <= 2^22; non-finite blocks take 0 here and NaN through xs
+        const float sx = finite ? (v[k] * m1) * m2 : 0.0f;
+        const int32_t xi = (int32_t)rintf(sx);
+        const int32_t c = (xi << 24) >> 24;
+        const int32_t r = (xi - c) >> 8;
+        const int32_t bb = (r << 24) >> 24;
+        const int32_t a = (r - bb) >> 8;
+        la |= (uint32_t)(a & 0xff) << (8 * k);
+        lb |= (uint32_t)(bb & 0xff) << (8 * k);
+        lc |= (uint32_t)(c & 0xff) << (8 * k);
+        sum += xi;
+    }
+#pragma unroll
+    for (int m = 1; m < 8; m *= 2) sum += __shfl_xor(sum, m, 8);
+    const int dw = prep_dword<KIND>(j);
+    rec[dw] = la;
+    rec[8 + dw] = lb;
+    rec[16 + dw] = lc;
+    if (j == 0) {
+        const int32_t bias = KIND == FH_Q4_0 ? -8 * sum : 0;
+        rec[24] = __float_as_uint(xs);
+        rec[25] = (uint32_t)bias;
+    } else if (j < 7) {
+        rec[24 + j + 1] = 0u;  // bytes 104 .. 127 are zero
+    }
+}
+
+// One workgroup row per product (blockIdx.x), 32 blocks per workgroup.
 template <int KIND>
 __global__ __launch_bounds__(256) void gemv_prep_kernel(const GemvDesc *__restrict__ descs, GemvDesc one) {
     const GemvDesc d = descs ? descs[blockIdx.x] : one;
-    const int j = threadIdx.x % 8;  // elements 4j .. 4j + 3 of the block
     const bool aligned = ((uintptr_t)d.x & 15) == 0;
-    // (the loop bound is the same for the eight lanes of a block, so the shuffles below see
-    // all eight)
-    for (uint32_t b = (blockIdx.y * 256 + threadIdx.x) / 8; b < d.nb; b += gridDim.y * 32) {
-        const float *xb = d.x + (size_t)b * 32 + 4 * j;
-        f32x4 v;
-        if (aligned) {
-            v = *(const f32x4 *)xb;
-        } else {
-            v = f32x4{xb[0], xb[1], xb[2], xb[3]};
-        }
-        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        int finite = (int)(fabsf(v.x) <= 3.4028235e38f) & (int)(fabsf(v.y) <= 3.4028235e38f) &
-                     (int)(fabsf(v.z) <= 3.4028235e38f) & (int)(fabsf(v.w) <= 3.4028235e38f);  // 0: inf, NaN
-#pragma unroll
-        for (int m = 1; m < 8; m *= 2) {
-            amax = fmaxf(amax, __shfl_xor(amax, m, 8));
-            finite &= __shfl_xor(finite, m, 8);
-        }
-        // grid 2^-sh with 2^21 <= amax * 2^sh < 2^22 (subnormal amax: exponent field 1); the
-        // scaling is split in two exact power-of-two products so that no factor overflows
-        const int sh = 148 - (int)max(__float_as_uint(amax) >> 23, 1u);  // -106 .. 147
-        const int sh1 = min(sh, 100);
-        const float m1 = __uint_as_float((uint32_t)(127 + sh1) << 23);
-        const float m2 = __uint_as_float((uint32_t)(127 + sh - sh1) << 23);
-        const float xs = !finite ? __builtin_nanf("")
-                         : sh <= 126 ? __uint_as_float((uint32_t)(127 - sh) << 23)  // 2^-sh, normal
-                                     : __uint_as_float(1u << (149 - sh));            // 2^-sh, subnormal
-        uint32_t la = 0, lb = 0, lc = 0;
-        int32_t sum = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            // |xi| <= 2^22; non-finite blocks take 0 here and NaN through xs
-            const float sx = finite ? (v[k] * m1) * m2 : 0.0f;
-            const int32_t xi = (int32_t)rintf(sx);
-            const int32_t c = (xi << 24) >> 24;
-            const int32_t r = (xi - c) >> 8;
-            const int32_t bb = (r << 24) >> 24;
-            const int32_t a = (r - bb) >> 8;
-            la |= (uint32_t)(a & 0xff) << (8 * k);
-            lb |= (uint32_t)(bb & 0xff) << (8 * k);
-            lc |= (uint32_t)(c & 0xff) << (8 * k);
-            sum += xi;
-        }
-#pragma unroll
-        for (int m = 1; m < 8; m *= 2) sum += __shfl_xor(sum, m, 8);
-        const int dw = prep_dword<KIND>(j);
-        uint32_t *rec = (uint32_t *)(d.prep + (size_t)b * kPrepBytes);
-        rec[dw] = la;
-        rec[8 + dw] = lb;
-        rec[16 + dw] = lc;
-        if (j == 0) {
-            const int32_t bias = KIND == FH_Q4_0 ? -8 * sum : 0;
-            ((u32x4 *)rec)[6] = u32x4{__float_as_uint(xs), (uint32_t)bias, 0u, 0u};
-            ((u32x4 *)rec)[7] = u32x4{0u, 0u, 0u, 0u};
-        }
-    }
+    // (the loop bound is the same for the eight lanes of a block)
+    for (uint32_t b = (blockIdx.y * 256 + threadIdx.x) / 8; b < d.nb; b += gridDim.y * 32)
+        prep_block<KIND>(d.x, aligned, b, threadIdx.x % 8,
+                         (__attribute__((address_space(1))) uint32_t *)(d.prep + (size_t)b * kPrepBytes));
 }
 
 // ---- the GEMV ----
@@ -219,9 +230,13 @@ struct LaneOffsets {
     uint32_t q, s, a;
 };
 
-template <int KIND>
+// Prepared x in LDS: one region per wavefront (kernel argument lds_blocks records, a multiple
+// of eight), holding the records of the product the wavefront works on.
+extern __shared__ __attribute__((aligned(16))) uint8_t gemv_lds[];
+
+template <int KIND, bool LDSX>
 __device__ __forceinline__ void load_batch(Batch<KIND> &bt, const Task<KIND> &tk, uint32_t b,
-                                           const LaneOffsets &o) {
+                                           const LaneOffsets &o, uint32_t lds_base) {
     if constexpr (KIND == FH_Q8_0) {
 #pragma unroll
         for (int i = 0; i < kBatch; i++)
@@ -234,7 +249,10 @@ __device__ __forceinline__ void load_batch(Batch<KIND> &bt, const Task<KIND> &tk
                 u32x4, __builtin_amdgcn_raw_buffer_load_b128(tk.rq, (int)(o.q + (b + 2 * i) * 512), 0, kNonTemporal));
     }
     bt.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(tk.rd, (int)(o.s + b * 64), 0, 0));
-    bt.a = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(tk.ra, (int)(o.a + b * kPrepBytes), 0, 0));
+    if constexpr (LDSX)
+        bt.a = *(const i32x4 *)&gemv_lds[lds_base + b * kPrepBytes + o.a];
+    else
+        bt.a = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(tk.ra, (int)(o.a + b * kPrepBytes), 0, 0));
 }
 
 __device__ __forceinline__ i32x4 nibbles(uint32_t q0, uint32_t q1) {
@@ -287,10 +305,10 @@ __device__ __forceinline__ void compute_batch(const Batch<KIND> &bt, bool upper,
     }
 }
 
-template <int KIND>
+template <int KIND, bool LDSX>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ descs,
                                                    const uint32_t *__restrict__ map, GemvDesc one, uint32_t count,
-                                                   uint32_t tasks, uint32_t tasks_per_wave) {
+                                                   uint32_t tasks, uint32_t tasks_per_wave, uint32_t lds_blocks) {
     const int lane = threadIdx.x % 64;
     // wave-uniform (readfirstlane): descriptor reads are scalar loads
     const uint32_t wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
@@ -308,6 +326,27 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ 
     // task boundary. lp is the batch being loaded, cp the batch being computed.
     Cursor cur{descs, count, tasks, 0, 0, {}};
     cur.seek(t0, map, one);
+    // With LDSX the wavefront prepares its product's x into its LDS region (all of it, padded
+    // with zero records to a multiple of eight blocks), whenever it starts a product; the
+    // batch in flight already holds its own x in registers, so the region can be rewritten.
+    const uint32_t lds_base = (threadIdx.x / 64) * lds_blocks * kPrepBytes;
+    auto prepare = [&](const GemvDesc &d) {
+        if constexpr (LDSX) {
+            const bool aligned = ((uintptr_t)d.x & 15) == 0;
+            const uint32_t nb8 = (d.nb + 7) / 8 * 8;
+            for (uint32_t b = lane / 8; b < nb8; b += 8) {
+                __attribute__((address_space(3))) uint32_t *rec =
+                    (__attribute__((address_space(3))) uint32_t *)&gemv_lds[lds_base + b * kPrepBytes];
+                if (b < d.nb) {
+                    prep_block<KIND>(d.x, aligned, b, lane % 8, rec);
+                } else {
+                    // padding records: four zero dwords per lane
+                    *(__attribute__((address_space(3))) u32x4 *)(rec + 4 * (lane % 8)) = u32x4{0u, 0u, 0u, 0u};
+                }
+            }
+        }
+    };
+    prepare(cur.d);
     Task<KIND> ltk;
     Pos lp{t0, 0, t0 - cur.d.task0, cur.d.n, cur.d.nb, cur.d.y};
     ltk.set(cur.d, lp.g);
@@ -317,7 +356,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ 
             lp.t++;
             lp.b = 0;
             if (lp.t < t1) {
+                const uint32_t p0 = cur.p;
                 cur.advance(lp.t);
+                if (cur.p != p0) prepare(cur.d);
                 lp.g = lp.t - cur.d.task0;
                 lp.n = cur.d.n;
                 lp.nb = cur.d.nb;
@@ -343,12 +384,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ 
         }
     };
     Batch<KIND> b0, b1;
-    load_batch<KIND>(b0, ltk, lp.b, o);
+    load_batch<KIND, LDSX>(b0, ltk, lp.b, o, lds_base);
     Pos cp = lp;
     advance();
     // (scheduling barriers keep each batch's loads together, so a batch waits only for its own)
     for (;;) {
-        load_batch<KIND>(b1, ltk, lp.b, o);
+        load_batch<KIND, LDSX>(b1, ltk, lp.b, o, lds_base);
         __builtin_amdgcn_sched_barrier(0);
         if (cp.b + kBatch / 2 >= cp.nb)
             compute_batch<KIND, kBatch / 4>(b0, upper, acc);  // a task's last half batch
@@ -359,7 +400,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ 
         if (lp.t >= t1) break;
         cp = lp;
         advance();
-        load_batch<KIND>(b0, ltk, lp.b, o);
+        load_batch<KIND, LDSX>(b0, ltk, lp.b, o, lds_base);
         __builtin_amdgcn_sched_barrier(0);
         if (cp.b + kBatch / 2 >= cp.nb)
             compute_batch<KIND, kBatch / 4>(b1, upper, acc);
@@ -384,24 +425,54 @@ uint32_t waves_per_cu() {
     return w;
 }
 
+constexpr uint32_t kMaxLdsBlocks = 160;  // per wavefront: 20 KiB of prepared x, 80 KiB per workgroup
+constexpr uint32_t kMinLdsTasks = 8;     // tasks per wavefront below which x is prepared once, globally
+
+// Resident workgroups per CU for a kernel and its dynamic LDS (cached per LDS size).
+template <int KIND, bool LDSX>
+int resident_groups(uint32_t lds_bytes) {
+    static int cache[kMaxLdsBlocks / 8 + 1] = {};
+    const uint32_t key = lds_bytes / (4 * 8 * kPrepBytes);
+    if (key <= kMaxLdsBlocks / 8 && cache[key] > 0) return cache[key];
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, gemv_kernel<KIND, LDSX>, 256, lds_bytes) != hipSuccess ||
+        b < 1)
+        b = 1;
+    if (key <= kMaxLdsBlocks / 8) cache[key] = b;
+    return b;
+}
+
 template <int KIND>
 hipError_t launch_kind(hipStream_t s, const GemvDesc *descs, const uint32_t *map, const GemvDesc &one,
                        uint32_t count, uint32_t tasks, uint32_t max_nb, int cus) {
-    // x preparation: a row of workgroups per product (32 blocks per workgroup)
-    const uint32_t py = (max_nb + 31) / 32;
-    gemv_prep_kernel<KIND><<<dim3(count, py < 4096 ? py : 4096), 256, 0, s>>>(descs, one);
+    // Prepared x in LDS when every product's fits in a wavefront's region and a wavefront's
+    // share of tasks is long enough to pay for preparing it (each wavefront prepares every
+    // product it touches); otherwise a separate preparation kernel (a row of workgroups per
+    // product, 32 blocks per workgroup) writes it to global memory once.
+    const uint32_t nb8 = (max_nb + 7) / 8 * 8;
+    const uint32_t waves_est = (uint32_t)(cus > 0 ? cus : 256) * min(4u * resident_groups<KIND, false>(0), waves_per_cu());
+    const bool ldsx = nb8 <= kMaxLdsBlocks && (tasks + waves_est - 1) / waves_est >= kMinLdsTasks;
+    const uint32_t lds_bytes = ldsx ? 4 * nb8 * kPrepBytes : 0;
+    if (!ldsx) {
+        const uint32_t py = (max_nb + 31) / 32;
+        gemv_prep_kernel<KIND><<<dim3(count, py < 4096 ? py : 4096), 256, 0, s>>>(descs, one);
+    } else {
+        static const hipError_t attr = hipFuncSetAttribute((const void *)gemv_kernel<KIND, true>,
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                           (int)(4 * kMaxLdsBlocks * kPrepBytes));
+        (void)attr;
+    }
     // as many wavefronts as fit on the chip at once (or the requested per-CU count), each an
     // equal share of the tasks
-    static const int resident = [] {
-        int b = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, gemv_kernel<KIND>, 256, 0) != hipSuccess || b < 1) b = 1;
-        return b * 4;
-    }();
+    const int resident = 4 * (ldsx ? resident_groups<KIND, true>(lds_bytes) : resident_groups<KIND, false>(0));
     const uint32_t per_cu = min((uint32_t)resident, waves_per_cu());
     const uint32_t max_waves = (uint32_t)(cus > 0 ? cus : 256) * per_cu;
     const uint32_t per = (tasks + max_waves - 1) / max_waves;
     const uint32_t waves = (tasks + per - 1) / per;
-    gemv_kernel<KIND><<<(waves + 3) / 4, 256, 0, s>>>(descs, map, one, count, tasks, per);
+    if (ldsx)
+        gemv_kernel<KIND, true><<<(waves + 3) / 4, 256, lds_bytes, s>>>(descs, map, one, count, tasks, per, nb8);
+    else
+        gemv_kernel<KIND, false><<<(waves + 3) / 4, 256, 0, s>>>(descs, map, one, count, tasks, per, 0);
     return hipGetLastError();
 }
 
