@@ -408,6 +408,13 @@ __global__ __launch_bounds__(kThreads) void copy_f32_kernel(const float *__restr
         dst[i] = src[i];
 }
 
+// ---- F16 tensor -> f32 (Gguf::tensor_f32 for GGML_F16), exact ----
+__global__ __launch_bounds__(kThreads) void decode_f16_kernel(const uint16_t *__restrict__ src,
+                                                              float *__restrict__ dst, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (size_t)gridDim.x * kThreads)
+        dst[i] = half_bits_to_float(src[i]);
+}
+
 unsigned grid_for(size_t work_items, size_t per_group, unsigned cap) {
     size_t g = (work_items + per_group - 1) / per_group;
     if (g < 1) g = 1;
@@ -487,6 +494,11 @@ hipError_t launch_copy_f32(hipStream_t s, const float *src, float *dst, size_t n
     } else {
         copy_f32_kernel<<<grid_for(n, kThreads * 4, 16384), kThreads, 0, s>>>(src, dst, n);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_f16(hipStream_t s, const uint16_t *src, float *dst, size_t n) {
+    decode_f16_kernel<<<grid_for(n, kThreads * 4, 16384), kThreads, 0, s>>>(src, dst, n);
     return hipGetLastError();
 }
 

@@ -106,6 +106,7 @@ hipError_t launch_snap_rows(hipStream_t s, const float *src, float *dst, size_t 
 hipError_t launch_snap_cols(hipStream_t s, const float *src, float *dst, size_t rows_in,
                             size_t cols_out);
 hipError_t launch_copy_f32(hipStream_t s, const float *src, float *dst, size_t n);
+hipError_t launch_decode_f16(hipStream_t s, const uint16_t *src, float *dst, size_t n);
 
 // GGUF rows (n rows of nb blocks) <-> tiled planes (upload_qweight and read_gguf)
 hipError_t launch_gguf_to_planes(hipStream_t s, fh_kind kind, const uint8_t *src, uint8_t *qs,

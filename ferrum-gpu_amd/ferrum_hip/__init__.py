@@ -62,6 +62,7 @@ def lib() -> ctypes.CDLL:
             "(or __graft_entry__.build()); there is no CPU fallback")
     L = ctypes.CDLL(LIB_PATH)
     P, S, I, U64, I64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_int64
+    U32 = ctypes.c_uint32
     PP = ctypes.POINTER(ctypes.c_void_p)
     sigs = {
         "fh_last_error": (ctypes.c_char_p, []),
@@ -108,6 +109,28 @@ def lib() -> ctypes.CDLL:
         "fh_gemv_plan_free": (None, [P]),
         "fh_q8_snap_rows": (I, [P, P, P, S]),
         "fh_q8_snap_cols": (I, [P, P, P, S, S]),
+        "fh_ggml_nbytes": (I, [U32, U64, ctypes.POINTER(U64)]),
+        "fh_gguf_parse": (I, [P, S, PP]),
+        "fh_gguf_parse_prefix": (I, [P, S, U64, PP]),
+        "fh_gguf_open": (I, [ctypes.c_char_p, PP]),
+        "fh_gguf_close": (None, [P]),
+        "fh_gguf_describe": (S, [P, ctypes.c_char_p, S]),
+        "fh_gguf_kv_count": (S, [P]),
+        "fh_gguf_kv_key": (I, [P, S, PP, ctypes.POINTER(S)]),
+        "fh_gguf_kv_value": (I, [P, S, ctypes.POINTER(U32), PP, ctypes.POINTER(S)]),
+        "fh_gguf_kv_array": (I, [P, S, ctypes.POINTER(U32), ctypes.POINTER(U64)]),
+        "fh_gguf_kv_array_string": (I, [P, S, U64, PP, ctypes.POINTER(S)]),
+        "fh_gguf_find_key": (I, [P, ctypes.c_char_p, ctypes.POINTER(S)]),
+        "fh_gguf_get_uint": (I, [P, ctypes.c_char_p, ctypes.POINTER(U64)]),
+        "fh_gguf_get_float": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float)]),
+        "fh_gguf_get_string": (I, [P, ctypes.c_char_p, PP, ctypes.POINTER(S)]),
+        "fh_gguf_tensor_count": (S, [P]),
+        "fh_gguf_tensor_info": (I, [P, S, P]),
+        "fh_gguf_find_tensor": (I, [P, ctypes.c_char_p, ctypes.POINTER(S)]),
+        "fh_gguf_tensor_bytes": (I, [P, ctypes.c_char_p, PP, ctypes.POINTER(S)]),
+        "fh_gguf_data_offset": (U64, [P]),
+        "fh_gguf_upload_qweight": (I, [P, P, ctypes.c_char_p, PP]),
+        "fh_gguf_upload_f32": (I, [P, P, ctypes.c_char_p, PP]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)

@@ -182,6 +182,96 @@ FH_API fh_status fh_q8_snap_rows(fh_device *dev, const fh_buffer *src, fh_buffer
 FH_API fh_status fh_q8_snap_cols(fh_device *dev, const fh_buffer *src, fh_buffer *dst, size_t rows_in,
                           size_t cols_out);
 
+/* ---- GGUF v3 container (ferrum_gguf/src/io/reader.rs:167-322) ----
+ * Replaces ferrum_gguf::Gguf. The parser is hostile-input safe: every read is bounds-checked,
+ * sizes use checked arithmetic, and nothing is allocated from a header count before the count is
+ * proven to fit in the file. Failures return FH_ERR_INVALID (FH_ERR_UNSUPPORTED for an unknown
+ * ggml tensor type) with fh_last_error() text "gguf: ..." carrying the reference's substrings:
+ * "magic", "version", "unexpected end of file", "exceed", "array length", "nested arrays",
+ * "unknown metadata value type", "dims", "alignment", "past the end", "duplicate",
+ * "missing key", "non-negative integer", "is not an f32", "is not a string", "missing tensor",
+ * "header-only", "not a multiple of the block size", "unsupported ggml tensor type".
+ * A parsed file keeps its bytes (an owned copy, or a read-only mapping of the file); every
+ * pointer handed out below stays valid until fh_gguf_close. */
+typedef struct fh_gguf fh_gguf;
+
+/* ggml tensor type ids (ferrum_gguf/src/lib.rs:24-55). */
+enum {
+    FH_GGML_F32 = 0, FH_GGML_F16 = 1, FH_GGML_Q4_0 = 2, FH_GGML_Q4_1 = 3, FH_GGML_Q5_0 = 6,
+    FH_GGML_Q5_1 = 7, FH_GGML_Q8_0 = 8, FH_GGML_Q8_1 = 9, FH_GGML_Q2_K = 10, FH_GGML_Q3_K = 11,
+    FH_GGML_Q4_K = 12, FH_GGML_Q5_K = 13, FH_GGML_Q6_K = 14, FH_GGML_I16 = 25, FH_GGML_I32 = 26,
+    FH_GGML_MXFP4 = 39
+};
+/* Metadata value tags (GGUF v3; reader.rs:125-155): U8 0, I8 1, U16 2, I16 3, U32 4, I32 5,
+ * F32 6, BOOL 7, STRING 8, ARRAY 9, U64 10, I64 11, F64 12. */
+
+/* quant::nbytes (ferrum_gguf/src/codec/quant.rs:17-47): bytes n elements of a ggml type occupy. */
+FH_API fh_status fh_ggml_nbytes(uint32_t ggml_type, uint64_t n, uint64_t *out);
+
+/* Gguf::parse (reader.rs:165-170): parse a whole file held in memory (the bytes are copied). */
+FH_API fh_status fh_gguf_parse(const uint8_t *bytes, size_t len, fh_gguf **out);
+/* Gguf::parse_prefix (reader.rs:172-247): parse from the first `len` bytes of a file `total`
+ * bytes long; tensor extents are checked against `total`, and reading data beyond `len` fails
+ * ("header-only"). */
+FH_API fh_status fh_gguf_parse_prefix(const uint8_t *bytes, size_t len, uint64_t total, fh_gguf **out);
+/* Open a file by path through a read-only memory mapping: nothing is read until used, and
+ * tensor bytes go from the mapping to the device without an intermediate host copy. */
+FH_API fh_status fh_gguf_open(const char *path, fh_gguf **out);
+FH_API void fh_gguf_close(fh_gguf *g);
+/* Debug summary (reader.rs:91-101): "Gguf { K keys, T tensors, B bytes }" into buf. */
+FH_API size_t fh_gguf_describe(const fh_gguf *g, char *buf, size_t cap);
+
+/* Metadata, in file order (Gguf::kv, reader.rs:83-84). Strings are not NUL-terminated. */
+FH_API size_t fh_gguf_kv_count(const fh_gguf *g);
+FH_API fh_status fh_gguf_kv_key(const fh_gguf *g, size_t i, const char **key, size_t *len);
+/* Entry i: its tag, and for scalars and strings the little-endian payload (a string's bytes).
+ * For arrays: data and nbytes span the packed elements, and fh_gguf_kv_array gives the element
+ * tag and count. */
+FH_API fh_status fh_gguf_kv_value(const fh_gguf *g, size_t i, uint32_t *type, const uint8_t **data,
+                                  size_t *nbytes);
+FH_API fh_status fh_gguf_kv_array(const fh_gguf *g, size_t i, uint32_t *elem_type, uint64_t *count);
+/* Element j of a string array. */
+FH_API fh_status fh_gguf_kv_array_string(const fh_gguf *g, size_t i, uint64_t j, const char **s,
+                                         size_t *len);
+/* Gguf::get (reader.rs:249-252): index of the first entry with this key, or "missing key". */
+FH_API fh_status fh_gguf_find_key(const fh_gguf *g, const char *key, size_t *index);
+/* Typed getters (reader.rs:254-286). */
+FH_API fh_status fh_gguf_get_uint(const fh_gguf *g, const char *key, uint64_t *out);
+FH_API fh_status fh_gguf_get_float(const fh_gguf *g, const char *key, float *out);
+FH_API fh_status fh_gguf_get_string(const fh_gguf *g, const char *key, const char **s, size_t *len);
+
+/* Tensor directory, in file order (TensorInfo, reader.rs:58-80). */
+typedef struct fh_gguf_tensor {
+    const char *name; /* not NUL-terminated */
+    size_t name_len;
+    uint32_t n_dims;  /* 1 to 4 */
+    uint64_t dims[4]; /* ggml order: dims[0] is contiguous */
+    uint32_t ggml_type;
+    uint64_t offset;   /* from the start of the data section */
+    uint64_t elements;
+    uint64_t nbytes;
+} fh_gguf_tensor;
+FH_API size_t fh_gguf_tensor_count(const fh_gguf *g);
+FH_API fh_status fh_gguf_tensor_info(const fh_gguf *g, size_t i, fh_gguf_tensor *out);
+/* Gguf::tensor (reader.rs:289-291): "missing tensor" when absent. */
+FH_API fh_status fh_gguf_find_tensor(const fh_gguf *g, const char *name, size_t *index);
+/* Gguf::tensor_bytes (reader.rs:294-305): the stored bytes, undecoded. */
+FH_API fh_status fh_gguf_tensor_bytes(const fh_gguf *g, const char *name, const uint8_t **data,
+                                      size_t *len);
+/* Gguf::data_offset (reader.rs:308-310). */
+FH_API uint64_t fh_gguf_data_offset(const fh_gguf *g);
+
+/* No dequantise/requantise round trip: a Q8_0 or Q4_0 tensor of ggml dims [k, n...] becomes a
+ * resident weight of k inputs and n = dims[1]*...*dims[nd-1] outputs straight from its stored
+ * bytes (the rows are the weight's GGUF rows). Replaces the load-time re-encode the reference's
+ * GGUF loaders perform (ferrum_model/src/gguf/quant.rs:57-69 into ops_quant::upload_quantised). */
+FH_API fh_status fh_gguf_upload_qweight(fh_device *dev, const fh_gguf *g, const char *name,
+                                        fh_qweight **out);
+/* Gguf::tensor_f32 (reader.rs:313-318) onto the device: the tensor decoded to f32 in GGUF order
+ * (dims[0] contiguous) in a new buffer. F32 is copied; F16, Q8_0 and Q4_0 are decoded by the
+ * device codec. Other types: FH_ERR_UNSUPPORTED. */
+FH_API fh_status fh_gguf_upload_f32(fh_device *dev, const fh_gguf *g, const char *name, fh_buffer **out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,10 +1,12 @@
 """Regenerate the golden fixtures under tests/golden/ (run in the build container, where the
 reference checkout is mounted; the GPU box never runs this).
 
-1. ``model_gguf_q8_0.bin`` / ``.json``: the raw bytes of every Q8_0 tensor in the reference's
-   fixture ``fixtures/bpe/model.gguf`` (a GPT-2 written by a different encoder, ferrum-cpu; see
-   the reference's fixtures/README.md ledger). The file is parsed here as data by a small GGUF
-   v3 reader of our own; nothing from the reference is executed.
+1. ``model.gguf``: the reference's fixture ``fixtures/bpe/model.gguf`` copied byte for byte (a
+   2-layer GPT-2 with Q8_0 matrices and F32 vectors, written by a different encoder, ferrum-cpu;
+   sha256 623af38b...6ec as in the reference's fixtures/README.md ledger). It is data: the tests
+   parse it with the native reader and with oracle/gguf.py.
+   ``model_gguf_q8_0.bin`` / ``.json``: the raw bytes of its Q8_0 tensors and their directory,
+   cut out by oracle/gguf.py's reader; nothing from the reference is executed.
 2. ``codec_nasty.npz``: the reference's "nasty" inputs (ferrum_wgpu/src/ops/quant/tests.rs:11-23,
    ferrum_wgpu/src/ops/qat.rs:68-80) encoded to Q8_0 and Q4_0, decoded, and snapped (rows and
    columns) by the C oracle. Every byte and every float is cross-checked against the
@@ -17,7 +19,6 @@ from __future__ import annotations
 import hashlib
 import json
 import os
-import struct
 import sys
 
 import numpy as np
@@ -27,62 +28,16 @@ REPO = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, REPO)
 
 import oracle  # noqa: E402
-from oracle import np_oracle  # noqa: E402
+from oracle import gguf, np_oracle  # noqa: E402
 
 GGUF_PATH = "/root/reference/fixtures/bpe/model.gguf"
 
 
-class _Reader:
-    def __init__(self, data: bytes):
-        self.d, self.o = data, 0
-
-    def take(self, fmt: str):
-        v = struct.unpack_from("<" + fmt, self.d, self.o)
-        self.o += struct.calcsize("<" + fmt)
-        return v[0] if len(v) == 1 else v
-
-    def string(self) -> str:
-        n = self.take("Q")
-        s = self.d[self.o:self.o + n].decode("utf-8", "replace")
-        self.o += n
-        return s
-
-    _SCALAR = {0: "B", 1: "b", 2: "H", 3: "h", 4: "I", 5: "i", 6: "f", 7: "?", 10: "Q", 11: "q",
-               12: "d"}
-
-    def value(self, ty: int):
-        if ty in self._SCALAR:
-            return self.take(self._SCALAR[ty])
-        if ty == 8:
-            return self.string()
-        if ty == 9:
-            ety, cnt = self.take("I"), self.take("Q")
-            return [self.value(ety) for _ in range(cnt)]
-        raise ValueError(f"unknown GGUF value type {ty}")
-
-
 def parse_gguf(path: str):
-    """Minimal GGUF v3 reader: returns (metadata dict, tensor list, data-section offset)."""
+    """(file bytes, metadata dict, tensor list, data-section offset) by oracle/gguf.py's reader."""
     data = open(path, "rb").read()
-    r = _Reader(data)
-    magic, version = r.take("I"), r.take("I")
-    if magic != 0x46554747 or version != 3:
-        raise ValueError("not a GGUF v3 file")
-    n_tensors, n_kv = r.take("Q"), r.take("Q")
-    meta = {}
-    for _ in range(n_kv):
-        key = r.string()
-        meta[key] = r.value(r.take("I"))
-    tensors = []
-    for _ in range(n_tensors):
-        name = r.string()
-        nd = r.take("I")
-        dims = [r.take("Q") for _ in range(nd)]
-        ty, off = r.take("I"), r.take("Q")
-        tensors.append({"name": name, "dims": dims, "type": ty, "offset": off})
-    align = int(meta.get("general.alignment", 32))
-    base = (r.o + align - 1) // align * align
-    return data, meta, tensors, base
+    kv, tensors, base = gguf.parse(data)
+    return data, {k: v for k, v in kv}, tensors, base
 
 
 def nasty(n: int) -> np.ndarray:
@@ -97,8 +52,15 @@ def nasty(n: int) -> np.ndarray:
     return v.astype(np.float32)
 
 
+MODEL_SHA256 = "623af38b770ace7617725682bf84c0bb212d62ab78be1784e6b9775928af36ec"
+
+
 def make_model_fixture(path: str) -> None:
     data, meta, tensors, base = parse_gguf(path)
+    if hashlib.sha256(data).hexdigest() != MODEL_SHA256:
+        raise SystemExit(f"{path} is not the ledger's model.gguf")
+    with open(os.path.join(HERE, "model.gguf"), "wb") as f:
+        f.write(data)
     blobs, table, off = [], [], 0
     for t in tensors:
         if t["type"] != oracle.Q8_0:
