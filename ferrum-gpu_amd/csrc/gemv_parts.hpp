@@ -1,0 +1,189 @@
+// Device pieces shared by the batch-1 GEMV kernels (gemv.hip, decode.hip): the prepared-x
+// record of a block (three signed-byte limb rows in the MFMA's k order, the block's x scale and
+// the Q4_0 bias) and the exact integer block products on the matrix cores. Included by .hip files
+// only; everything is internal to the including file.
+#pragma once
+
+#include "device_common.hpp"
+#include "internal.hpp"
+
+namespace fh {
+namespace {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float half_to_float(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// A raw buffer resource over [base, base + bytes): loads at offsets at or past `bytes` return 0
+// (gfx9 descriptor word 3 = 0x00020000, 32-bit data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+constexpr int kNonTemporal = 2;             // cache-policy bit of a streaming load
+constexpr int kPrepBytes = 128;             // prepared-x record per block
+constexpr int kBatch = 8;                   // blocks per pipeline batch
+
+// k slot of the MFMA operands -> element of the block. Lane half h (lanes 32h..32h+31) holds
+// 16 slots; B lane (row, h) loads quant bytes 8h..8h+7 (Q4_0: low nibbles are slots 0..7, high
+// nibbles slots 8..15) or 16h..16h+15 (Q8_0: slot i is byte i).
+template <int KIND>
+__host__ __device__ constexpr int elem_of_slot(int h, int i) {
+    if constexpr (KIND == FH_Q8_0)
+        return 16 * h + i;
+    else
+        return i < 8 ? 8 * h + i : 16 + 8 * h + (i - 8);
+}
+
+// The prepared-x writer gives lane j (elements 4j .. 4j + 3 of a block) one dword of each
+// 32-byte limb row: the slots of those four elements, in order.
+template <int KIND>
+__host__ __device__ constexpr int prep_dword(int j) {
+    return KIND == FH_Q8_0 ? j : (j == 2 || j == 3) ? j + 2 : (j == 4 || j == 5) ? j - 2 : j;
+}
+template <int KIND>
+constexpr bool prep_dwords_match_slots() {
+    for (int j = 0; j < 8; j++)
+        for (int k = 0; k < 4; k++) {
+            const int byte = 4 * prep_dword<KIND>(j) + k;
+            if (elem_of_slot<KIND>(byte / 16, byte % 16) != 4 * j + k) return false;
+        }
+    return true;
+}
+static_assert(prep_dwords_match_slots<FH_Q8_0>() && prep_dwords_match_slots<FH_Q4_0>(),
+              "prepared-x dwords must hold the MFMA k slots");
+
+// ---- x preparation: eight lanes per block, lane j taking elements 4j .. 4j + 3 ----
+// Writes the 128-byte record of the block whose elements 4j .. 4j + 3 are v at rec (a global or
+// an LDS pointer). The eight lanes of a block must run this together (they reduce over one
+// another with shuffles).
+template <int KIND, class U32Ptr>
+__device__ __forceinline__ void prep_values(f32x4 v, int j, U32Ptr rec) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    int finite = (int)(fabsf(v.x) <= 3.4028235e38f) & (int)(fabsf(v.y) <= 3.4028235e38f) &
+                 (int)(fabsf(v.z) <= 3.4028235e38f) & (int)(fabsf(v.w) <= 3.4028235e38f);  // 0: inf, NaN
+#pragma unroll
+    for (int m = 1; m < 8; m *= 2) {
+        amax = fmaxf(amax, __shfl_xor(amax, m, 8));
+        finite &= __shfl_xor(finite, m, 8);
+    }
+    // grid 2^-sh with 2^21 <= amax * 2^sh < 2^22 (subnormal amax: exponent field 1); the
+    // scaling is split in two exact power-of-two products so that no factor overflows
+    const int sh = 148 - (int)max(__float_as_uint(amax) >> 23, 1u);  // -106 .. 147
+    const int sh1 = min(sh, 100);
+    const float m1 = __uint_as_float((uint32_t)(127 + sh1) << 23);
+    const float m2 = __uint_as_float((uint32_t)(127 + sh - sh1) << 23);
+    const float xs = !finite ? __builtin_nanf("")
+                     : sh <= 126 ? __uint_as_float((uint32_t)(127 - sh) << 23)  // 2^-sh, normal
+                                 : __uint_as_float(1u << (149 - sh));            // 2^-sh, subnormal
+    uint32_t la = 0, lb = 0, lc = 0;
+    int32_t sum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        // |xi| <= 2^22; non-finite blocks take 0 here and NaN through xs
+        const float sx = finite ? (v[k] * m1) * m2 : 0.0f;
+        const int32_t xi = (int32_t)rintf(sx);
+        const int32_t c = (xi << 24) >> 24;
+        const int32_t r = (xi - c) >> 8;
+        const int32_t bb = (r << 24) >> 24;
+        const int32_t a = (r - bb) >> 8;
+        la |= (uint32_t)(a & 0xff) << (8 * k);
+        lb |= (uint32_t)(bb & 0xff) << (8 * k);
+        lc |= (uint32_t)(c & 0xff) << (8 * k);
+        sum += xi;
+    }
+#pragma unroll
+    for (int m = 1; m < 8; m *= 2) sum += __shfl_xor(sum, m, 8);
+    const int dw = prep_dword<KIND>(j);
+    rec[dw] = la;
+    rec[8 + dw] = lb;
+    rec[16 + dw] = lc;
+    if (j == 0) {
+        const int32_t bias = KIND == FH_Q4_0 ? -8 * sum : 0;
+        rec[24] = __float_as_uint(xs);
+        rec[25] = (uint32_t)bias;
+    } else if (j < 7) {
+        rec[24 + j + 1] = 0u;  // bytes 104 .. 127 are zero
+    }
+}
+
+// The same for block b of x in global memory.
+template <int KIND, class U32Ptr>
+__device__ __forceinline__ void prep_block(const float *__restrict__ x, bool aligned, uint32_t b, int j, U32Ptr rec) {
+    // (global-address-space loads: flat ones would also count against the LDS counter)
+    typedef __attribute__((address_space(1))) const float gfloat;
+    typedef __attribute__((address_space(1))) const f32x4 gf32x4;
+    gfloat *xb = (gfloat *)(x + (size_t)b * 32 + 4 * j);
+    f32x4 v;
+    if (aligned) {
+        v = *(gf32x4 *)xb;
+    } else {
+        v = f32x4{xb[0], xb[1], xb[2], xb[3]};
+    }
+    prep_values<KIND>(v, j, rec);
+}
+
+template <int KIND>
+struct Batch {  // what one lane loads for a batch of kBatch blocks of its task
+    static constexpr int QL = KIND == FH_Q8_0 ? kBatch : kBatch / 2;  // 16-byte quant loads
+    u32x4 q[QL];  // Q4_0: blocks 2i (lanes 0..31) and 2i + 1 (lanes 32..63) of row lane % 32
+                  // Q8_0: bytes 16h .. 16h + 15 of block i of the row (h = lane / 32)
+    u32x4 s;      // the row's eight scales
+    i32x4 a;      // the prepared x of the eight blocks, as the MFMA's A operand
+};
+
+__device__ __forceinline__ i32x4 nibbles(uint32_t q0, uint32_t q1) {
+    return i32x4{(int32_t)(q0 & 0x0f0f0f0fu), (int32_t)(q1 & 0x0f0f0f0fu), (int32_t)((q0 >> 4) & 0x0f0f0f0fu),
+                 (int32_t)((q1 >> 4) & 0x0f0f0f0fu)};
+}
+
+// The batch's contribution to the lane's accumulator: lanes 0..31 take the even blocks of the
+// batch, lanes 32..63 the odd ones (row lane % 32 in both halves).
+template <int KIND, int PAIRS = kBatch / 2>
+__device__ __forceinline__ void compute_batch(const Batch<KIND> &bt, bool upper, float &acc) {
+#pragma unroll
+    for (int p = 0; p < PAIRS; p++) {  // blocks 2p and 2p + 1 of the batch
+        i32x4 be, bo;
+        if constexpr (KIND == FH_Q8_0) {
+            be = __builtin_bit_cast(i32x4, bt.q[2 * p]);
+            bo = __builtin_bit_cast(i32x4, bt.q[2 * p + 1]);
+        } else {
+            // lane r holds all 16 bytes of block 2p, lane 32 + r those of block 2p + 1; after
+            // swapping the upper lanes' first 8 bytes with the lower lanes' last 8, each lane
+            // holds half h of both blocks, as the MFMA's B operand takes them
+            const auto s0 = __builtin_amdgcn_permlane32_swap(bt.q[p][0], bt.q[p][2], false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap(bt.q[p][1], bt.q[p][3], false, false);
+            be = nibbles(s0[0], s1[0]);
+            bo = nibbles(s0[1], s1[1]);
+        }
+        // A rows 4j .. 4j + 2 hold block j's limb rows (row 4j + 3 its x scale and bias), so
+        // C rows 4j .. 4j + 2 are block j's limb sums: for j = 2p in registers 4p .. 4p + 2 of
+        // lanes 0..31, for j = 2p + 1 in the same registers of lanes 32..63. The other rows
+        // mix blocks and are not used.
+        const i32x16 ce = __builtin_amdgcn_mfma_i32_32x32x32_i8(bt.a, be, i32x16{}, 0, 0, 0);
+        const i32x16 co = __builtin_amdgcn_mfma_i32_32x32x32_i8(bt.a, bo, i32x16{}, 0, 0, 0);
+        const int32_t c0 = upper ? co[4 * p] : ce[4 * p];
+        const int32_t c1 = upper ? co[4 * p + 1] : ce[4 * p + 1];
+        const int32_t c2 = upper ? co[4 * p + 2] : ce[4 * p + 2];
+        // the block's x scale and bias: A row 4j + 3 is lane 4j + 3
+        const float xe = __int_as_float(__builtin_amdgcn_readlane(bt.a[0], 8 * p + 3));
+        const float xo = __int_as_float(__builtin_amdgcn_readlane(bt.a[0], 8 * p + 7));
+        float f;
+        if constexpr (KIND == FH_Q8_0) {
+            f = fmaf((float)c0, 65536.0f, (float)((c1 << 8) + c2));  // |sum| < 2^34: two roundings
+        } else {
+            // exact: |sum nibble * xi| < 2^31 and |sum (nibble - 8) * xi| <= 2^30
+            const int32_t ie = __builtin_amdgcn_readlane(bt.a[1], 8 * p + 3);
+            const int32_t io = __builtin_amdgcn_readlane(bt.a[1], 8 * p + 7);
+            f = (float)((c0 << 16) + (c1 << 8) + c2 + (upper ? io : ie));
+        }
+        const float d = half_to_float(bt.s[p] >> (upper ? 16 : 0));
+        acc = fmaf(d * f, upper ? xo : xe, acc);
+    }
+}
+
+}  // namespace
+}  // namespace fh

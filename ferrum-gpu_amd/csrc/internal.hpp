@@ -84,6 +84,9 @@ fh_status hip_fail(fh_device *dev, hipError_t e, const char *what);
 
 fh_status alloc_bytes(fh_device *dev, size_t nbytes, void **out);
 
+// A usable device: open, not closed, not lost; makes it the current HIP device.
+fh_status check_dev(fh_device *dev);
+
 // The device's workspace, at least `bytes` long (grown after the stream drains).
 fh_status workspace(fh_device *dev, size_t bytes, void **out);
 

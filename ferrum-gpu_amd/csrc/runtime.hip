@@ -121,9 +121,7 @@ fh_status alloc_bytes(fh_device *dev, size_t nbytes, void **out) {
 
 using namespace fh;
 
-namespace {
-
-fh_status check_dev(fh_device *dev) {
+fh_status fh::check_dev(fh_device *dev) {
     if (!dev) return fail(FH_ERR_INVALID, "no device");
     if (dev->closed.load()) return fail(FH_ERR_INVALID, "the device was closed");
     if (dev->lost.load()) return fail(FH_ERR_LOST, "the device was lost earlier");
@@ -131,6 +129,8 @@ fh_status check_dev(fh_device *dev) {
     if (e != hipSuccess) return hip_fail(dev, e, "select device");
     return FH_OK;
 }
+
+namespace {
 
 fh_status sync(fh_device *dev, const char *what) {
     hipError_t e = hipStreamSynchronize(dev->stream);

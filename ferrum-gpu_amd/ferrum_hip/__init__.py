@@ -131,6 +131,15 @@ def lib() -> ctypes.CDLL:
         "fh_gguf_data_offset": (U64, [P]),
         "fh_gguf_upload_qweight": (I, [P, P, ctypes.c_char_p, PP]),
         "fh_gguf_upload_f32": (I, [P, P, ctypes.c_char_p, PP]),
+        "fh_gpt2_from_gguf": (I, [P, P, PP]),
+        "fh_gpt2_free": (None, [P]),
+        "fh_gpt2_config": (I, [P] + [ctypes.POINTER(S)] * 6),
+        "fh_gpt2_kind": (I, [P]),
+        "fh_gpt2_pos": (S, [P]),
+        "fh_gpt2_reset": (None, [P]),
+        "fh_gpt2_step_bytes": (U64, [P]),
+        "fh_gpt2_feed": (I, [P, P, S, P]),
+        "fh_gpt2_generate": (I, [P, P, P, S, S, P]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)

@@ -239,3 +239,53 @@ class Gguf:
         h = ctypes.c_void_p()
         _check(lib().fh_gguf_upload_qweight(gpu.handle, self._h, name.encode(), ctypes.byref(h)))
         return QWeight(gpu, h)
+
+
+class GgufBuilder:
+    """ferrum_gguf's GgufBuilder (ferrum_gguf/src/io/writer.rs:7-115): metadata and tensors in,
+    one GGUF v3 file out (header, metadata, tensor directory, padding to the alignment after the
+    header and after every tensor). Values are `Value(tag, v)`; arrays hold Values."""
+
+    def __init__(self):
+        self._kv: list = []
+        self._tensors: list = []
+
+    def meta(self, key: str, val: Value) -> None:
+        self._kv.append((key, val))
+
+    def tensor_f32(self, name: str, dims, data) -> None:
+        self.tensor_raw(name, dims, GGML_F32, np.ascontiguousarray(data, dtype="<f4").tobytes())
+
+    def tensor_raw(self, name: str, dims, ggml_type: int, data) -> None:
+        self._tensors.append((name, [int(d) for d in dims], int(ggml_type), bytes(data)))
+
+    @staticmethod
+    def _str(s: str) -> bytes:
+        b = s.encode("utf-8")
+        return struct.pack("<Q", len(b)) + b
+
+    @classmethod
+    def _value(cls, val: Value) -> bytes:
+        if val.tag == STR:
+            return cls._str(val.v)
+        if val.tag == ARR:
+            head = struct.pack("<IQ", val.v[0].tag if val.v else U32, len(val.v))
+            return head + b"".join(cls._value(e) for e in val.v)
+        return struct.pack("<" + _FMT[val.tag], val.v)
+
+    def into_bytes(self) -> bytes:
+        parts = [struct.pack("<IIQQ", MAGIC, 3, len(self._tensors), len(self._kv))]
+        alignment = DEFAULT_ALIGNMENT
+        for key, val in self._kv:
+            parts += [self._str(key), struct.pack("<I", val.tag), self._value(val)]
+            if key == "general.alignment" and val.tag == U32:
+                alignment = max(int(val.v), 1)
+        data, offset = [], 0
+        for name, dims, ty, raw in self._tensors:
+            parts += [self._str(name), struct.pack("<I", len(dims)), struct.pack(f"<{len(dims)}Q", *dims),
+                      struct.pack("<IQ", ty, offset)]
+            pad = -len(raw) % alignment
+            data += [raw, bytes(pad)]
+            offset += len(raw) + pad
+        head = b"".join(parts)
+        return head + bytes(-len(head) % alignment) + b"".join(data)

@@ -272,6 +272,37 @@ FH_API fh_status fh_gguf_upload_qweight(fh_device *dev, const fh_gguf *g, const 
  * device codec. Other types: FH_ERR_UNSUPPORTED. */
 FH_API fh_status fh_gguf_upload_f32(fh_device *dev, const fh_gguf *g, const char *name, fh_buffer **out);
 
+/* ---- GPT-2 KV-cached decode on resident Q8_0 / Q4_0 weights ----
+ * Replaces ferrum_wgpu::models::gpt2::GpuGpt2 (ferrum_wgpu/src/models/gpt2.rs:52-265: new, feed,
+ * reset, pos), whose weights are f32; here every matrix stays packed. The model comes from a
+ * `gpt2` GGUF laid out as ferrum_model writes it (ferrum_model/src/gguf/gpt2.rs:179-233): Q8_0 or
+ * Q4_0 matrices (one format per model), F32 vectors, `output.weight` absent for a head tied to
+ * `token_embd.weight`. Its CPU counterpart is ferrum_ref's Gpt2::feed on the fake-quantised
+ * weights (ferrum_ref/src/models/gpt2/decode.rs:57-117). One step is one HIP graph launch
+ * (FERRUM_HIP_NO_GRAPH=1: plain launches); the position lives on the device. */
+typedef struct fh_gpt2 fh_gpt2;
+FH_API fh_status fh_gpt2_from_gguf(fh_device *dev, const fh_gguf *g, fh_gpt2 **out);
+FH_API void fh_gpt2_free(fh_gpt2 *m);
+/* Config (ferrum_ref/src/models/gpt2/mod.rs:16-31); any pointer may be NULL. */
+FH_API fh_status fh_gpt2_config(const fh_gpt2 *m, size_t *vocab, size_t *ctx, size_t *dim, size_t *heads,
+                                size_t *layers, size_t *hidden);
+FH_API fh_kind fh_gpt2_kind(const fh_gpt2 *m);
+/* GpuGpt2::pos / reset (gpt2.rs:205-213). */
+FH_API size_t fh_gpt2_pos(const fh_gpt2 *m);
+FH_API void fh_gpt2_reset(fh_gpt2 *m);
+/* Packed weight bytes one step reads (every matrix and the head). */
+FH_API uint64_t fh_gpt2_step_bytes(const fh_gpt2 *m);
+/* GpuGpt2::feed (gpt2.rs:216-265): consume `token` at the next position; when logits is not NULL
+ * it receives the vocab next-token logits (and the call waits for them). Errors: "context of N
+ * tokens is full", "token T is out of range for vocab V". */
+FH_API fh_status fh_gpt2_feed(fh_device *dev, fh_gpt2 *m, size_t token, float *logits);
+/* Greedy generation from the current position: feed the prompt, then pick n_new tokens by argmax
+ * (ferrum_model/src/sampling.rs:32-40), each fed back except the last (the reference's generate
+ * loop, ferrum_gpu_core/src/engine/mod.rs:204-242). Picks stay on the device; out receives them
+ * at the end, after the only wait. */
+FH_API fh_status fh_gpt2_generate(fh_device *dev, fh_gpt2 *m, const int32_t *prompt, size_t n_prompt,
+                                  size_t n_new, int32_t *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,9 @@ def lib() -> ctypes.CDLL:
             "fo_layernorm": (None, [P, P, P, S, P]),
             "fo_argmax": (S, [P, S]),
             "fo_gpt2_generate": (ctypes.c_int, [P, P, S, S, P]),
+            "fo_gpt2_cache_new": (P, [P]),
+            "fo_gpt2_cache_free": (None, [P, P]),
+            "fo_gpt2_feed": (ctypes.c_int, [P, P, S, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -249,20 +252,14 @@ GPT2_BLOCK_NAMES = ("ln1_g", "ln1_b", "wq", "bq", "wk", "bk", "wv", "bv", "wo", 
                     "ln2_g", "ln2_b", "w1", "b1", "w2", "b2")
 
 
-def gpt2_generate(model: dict, prompt, n_new: int) -> list[int]:
-    """Greedy cached decode (ferrum_ref/src/models/gpt2/decode.rs:57-117 per token).
-
-    ``model`` holds cfg ints (vocab, ctx, dim, heads, layers, hidden) and f32 arrays ``tok``,
-    ``pos``, ``blocks`` (list of dicts keyed by GPT2_BLOCK_NAMES), ``lnf_g``, ``lnf_b``, ``head``.
-    """
-    keep = []
-
+def _gpt2_struct(model: dict, keep: list):
     def ptr(a):
         a = _f32(a)
         keep.append(a)
         return a.ctypes.data
 
     blocks = (ctypes.c_void_p * (model["layers"] * 16))()
+    keep.append(blocks)
     for l, blk in enumerate(model["blocks"]):
         for i, name in enumerate(GPT2_BLOCK_NAMES):
             blocks[l * 16 + i] = ptr(blk[name])
@@ -270,6 +267,41 @@ def gpt2_generate(model: dict, prompt, n_new: int) -> list[int]:
               model["hidden"], ptr(model["tok"]), ptr(model["pos"]),
               ctypes.cast(blocks, ctypes.c_void_p), ptr(model["lnf_g"]), ptr(model["lnf_b"]),
               ptr(model["head"]))
+    keep.append(g)
+    return g
+
+
+class Gpt2Cpu:
+    """Gpt2::feed with its Cache (ferrum_ref/src/models/gpt2/decode.rs:7-117): one token at a
+    time, the next-token logits back."""
+
+    def __init__(self, model: dict):
+        self._keep = []
+        self._g = _gpt2_struct(model, self._keep)
+        self.vocab = model["vocab"]
+        self._c = lib().fo_gpt2_cache_new(ctypes.byref(self._g))
+
+    def feed(self, token: int) -> np.ndarray:
+        out = np.empty(self.vocab, np.float32)
+        if lib().fo_gpt2_feed(ctypes.byref(self._g), self._c, int(token), _p(out)) != 0:
+            raise ValueError("context full or token out of range")
+        return out
+
+    def __del__(self):
+        try:
+            lib().fo_gpt2_cache_free(ctypes.byref(self._g), self._c)
+        except Exception:
+            pass
+
+
+def gpt2_generate(model: dict, prompt, n_new: int) -> list[int]:
+    """Greedy cached decode (ferrum_ref/src/models/gpt2/decode.rs:57-117 per token).
+
+    ``model`` holds cfg ints (vocab, ctx, dim, heads, layers, hidden) and f32 arrays ``tok``,
+    ``pos``, ``blocks`` (list of dicts keyed by GPT2_BLOCK_NAMES), ``lnf_g``, ``lnf_b``, ``head``.
+    """
+    keep = []
+    g = _gpt2_struct(model, keep)
     pr = np.ascontiguousarray(prompt, dtype=np.uint64)
     out = np.zeros(max(n_new, 1), np.uint64)
     rc = lib().fo_gpt2_generate(ctypes.byref(g), _p(pr), pr.size, n_new, _p(out))
