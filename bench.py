@@ -9,8 +9,9 @@ HBM), each with its own x and y, launched as one grouped launch per width class.
 resident in HBM before the timed region. Weights are seeded N(0, 0.02), x ~ N(0, 1) (synthetic).
 
 Also reported (extra keys): the Q8_0 GPT-2 QKV GEMV (config 0), the MFMA dequant-GEMM at the
-Qwen2 scoring shapes (M = 512, 2048) in TFLOP/s, and the CPU baseline (the reference's CPU
-path restated in C: f32 GEMV on the dequantised weights, one thread).
+Qwen2 scoring shapes (M = 512, 2048) in TFLOP/s, the GPT-2-small Q8_0 greedy decode in tokens/s
+(config 2) with its one-thread CPU counterpart, and the CPU baseline (the reference's CPU path
+restated in C: f32 GEMV on the dequantised weights, one thread).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -221,6 +222,51 @@ def bench_copy(g, ev, nbytes=512 * 2**20, reps=10):
     return {"bytes_read": nbytes, "bytes_written": nbytes, "avg_ms": ms, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
 
 
+GPT2_SMALL = {"vocab": 50257, "ctx": 1024, "dim": 768, "heads": 12, "layers": 12, "hidden": 3072}
+
+
+def bench_decode(fh, g, n_prompt=32, n_new=256, reps=3, cpu=True):
+    """GPT-2-small (GPT-2 initialisation, tied head) with Q8_0 weights, KV-cached
+    greedy decode of n_new tokens from an n_prompt-token seeded uniform-random prompt. One rep is one
+    fh_gpt2_generate call from position 0 (the prompt is fed token by token, so a rep is
+    n_prompt + n_new - 1 decode steps); the median rep is reported."""
+    from ferrum_hip.gguf import Gguf
+    from ferrum_hip.gpt2 import GpuGpt2, gpt2_init, to_gguf
+
+    cfg = GPT2_SMALL
+    m = gpt2_init(cfg, 1)
+    data = to_gguf(g, m, fh.QKind.Q8_0)
+    model = GpuGpt2.from_gguf(g, Gguf.parse(data))
+    prompt = [int(t) for t in np.random.default_rng(2024).integers(0, cfg["vocab"], n_prompt)]
+    model.generate(prompt, 8)  # graph capture and warm-up
+    times, toks = [], None
+    for _ in range(reps):
+        model.reset()
+        t0 = time.perf_counter()
+        toks = model.generate(prompt, n_new)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    steps = n_prompt + n_new - 1
+    out = {"tok_s": n_new / t, "steps_per_s": steps / t, "ms_per_step": t / steps * 1e3,
+           "weight_gbs": model.step_bytes() * steps / t / 1e9, "step_bytes": model.step_bytes(),
+           "first_tokens": toks[:8], "reps": reps}
+    if cpu:  # ferrum_ref's Gpt2::feed (restated in C) on the fake-quantised f32 weights, one thread
+        import oracle as orc
+        from oracle import gpt2_model as gm
+
+        cpu_m = orc.Gpt2Cpu(gm.from_gguf(data))
+        for tkn in prompt[:2]:
+            cpu_m.feed(tkn)
+        t0, n = time.perf_counter(), 0
+        while time.perf_counter() - t0 < 5.0 or n < 5:
+            cpu_m.feed(prompt[2 + n % 30])
+            n += 1
+        out["cpu_tok_s"] = n / (time.perf_counter() - t0)
+        out["cpu_sample"] = f"{n} Gpt2::feed steps at positions 2..{n + 1}, f32 weights, 1 thread"
+    model.free()
+    return out
+
+
 def cpu_baseline(shapes, kind_bytes, budget_s=12.0):
     """The reference's CPU decode path restated in C (oracle/gemv: f32 weights [k, n], ascending
     k, one thread), on the same shapes; the rate is the same algorithmic bytes (the packed
@@ -256,6 +302,8 @@ def main():
     ap.add_argument("--pool-gib", type=float, default=1.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the GPT-2-small decode (config 2), one JSON line (for profiling)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the path shards by "
@@ -265,6 +313,12 @@ def main():
     import ferrum_hip as fh
 
     g = fh.Gpu(0)
+    if a.decode_only:
+        dec = bench_decode(fh, g, cpu=not a.no_cpu)
+        print(json.dumps({"metric": "GPT-2-small Q8_0 greedy decode tokens/s", "value": round(dec["tok_s"], 2),
+                          "unit": "tok/s", "n_gpus": 1, "higher_is_better": True, "detail": dec}))
+        g.close()
+        return
     ev = HipEvents(g)
     name, cus = g.info()
     log(f"device {name}, {cus} CUs")
@@ -290,6 +344,9 @@ def main():
                 extra[f"{name}_m{m}"] = {"tflops": round(r["tflops"], 2),
                                          "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                                          "ms_per_step": r["ms_per_step"], "flops_per_step": r["flops_per_step"]}
+        dec = bench_decode(fh, g, cpu=not a.no_cpu)
+        log("GPT-2-small Q8_0 decode:", dec)
+        extra["gpt2_small_q8_0_decode"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec.items()}
         extra["gemm_operands"] = ("split-f16 x (hi + lo) times exact integer quants on f16 MFMA, f32 accumulate, "
                                   "f32 block scale per 32-element block")
 

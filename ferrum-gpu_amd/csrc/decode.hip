@@ -24,6 +24,7 @@
 // LayerNorm prologue on the way, and the epilogue adds the bias and applies GELU, the residual or
 // the QKV scatter into the caches. The block products are the exact integer MFMA products of the
 // batch-1 GEMV (gemv_parts.hpp).
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -35,22 +36,31 @@
 namespace fh {
 namespace {
 
-enum { PRO_NONE = 0, PRO_LN = 1 };
-enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_GELU = 2, EPI_QKV = 3 };
+enum { PRO_NONE = 0, PRO_LN = 1, PRO_GLOBAL = 2 };
+enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_GELU = 2, EPI_QKV = 3, EPI_ARGMAX = 4 };
 
-constexpr int kMaxWaves = 8;          // wavefronts per decode-GEMV workgroup (two per SIMD)
-constexpr uint32_t kMaxBlocks = 512;  // blocks per row (k <= 16384): 64 KiB of prepared x in LDS
+constexpr int kMaxWaves = 8;           // wavefronts per decode-GEMV workgroup (two per SIMD)
+constexpr uint32_t kMaxBlocks = 512;   // blocks per row (k <= 16384): 64 KiB of prepared x in LDS
+constexpr uint32_t kLnSlots = 2;       // LayerNorm prologue: (block, lane) slots a thread keeps in registers
+constexpr uint32_t kNone = 0xffffffffu;
+constexpr int kAttnThreads = 512;
 
 struct DecodeGemv {
     const uint8_t *qs;
     const uint16_t *ds;
     const float *x;            // k inputs
     const float *ln_g, *ln_b;  // PRO_LN
+    const uint8_t *prep;       // PRO_GLOBAL: the prepared records of x
     const float *bias;         // n, or null
     float *y;                  // n outputs; EPI_RESIDUAL adds into it; EPI_QKV: the q part
     float *kc, *vc;            // EPI_QKV: caches [ctx, split]
-    const int32_t *state;      // state[0]: the position
+    int32_t *state;            // [0] position, [1] first position whose input a pick fills, [2] last pick
+    int32_t *inputs;           // EPI_ARGMAX: the token of each position
+    float *partial;            // split K: row sums [splits][groups * 32]; EPI_ARGMAX: best value per group
+    uint32_t *pick;            // EPI_ARGMAX: best row per group
+    uint32_t *ticket;          // split K: one counter per row group; EPI_ARGMAX: one counter
     uint32_t nb, n, split;     // split: EPI_QKV width of each of q, k, v
+    uint32_t chunk;            // blocks per K split (a multiple of 8)
     float eps;
 };
 
@@ -58,6 +68,10 @@ struct DecodeGemv {
 __device__ __forceinline__ float gelu(float x) {
     return 0.5f * x * (1.0f + tanhf(0.7978846f * (x + 0.044715f * x * x * x)));
 }
+
+typedef __attribute__((address_space(1))) const f32x4 gf32x4;
+
+__device__ __forceinline__ f32x4 gload4(const float *p) { return *(gf32x4 *)p; }
 
 // Sum over the workgroup (every thread gets the total); red holds one float per wavefront.
 __device__ __forceinline__ float block_sum(float v, float *red) {
@@ -70,6 +84,85 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     float t = 0.0f;
     for (uint32_t i = 0; i < nw; i++) t += red[i];
     return t;
+}
+
+// Loads from memory other workgroups wrote in this launch (past the per-CU caches).
+__device__ __forceinline__ float coherent_load(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t coherent_load(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The first maximum wins; NaN never does (ferrum_model/src/sampling.rs:32-40). kNone: no candidate.
+__device__ __forceinline__ bool better(float v2, uint32_t i2, float v1, uint32_t i1) {
+    return i2 != kNone && (i1 == kNone || v2 > v1 || (v2 == v1 && i2 < i1));
+}
+
+// LayerNorm (ferrum_ref/src/kernels/nn.rs:31-44) of the k = 32 nb values of x, written as the
+// prepared records of `span` blocks (zero records past nb) at out (LDS, or global when GLOBAL).
+// x is read once: each thread keeps its kLnSlots (block, lane) slots in registers, so
+// span * 8 <= kLnSlots * blockDim.x.
+template <int KIND, bool GLOBAL>
+__device__ __forceinline__ void ln_prep(const float *x, const float *lg, const float *lb, float eps, uint32_t nb,
+                                        uint32_t span, uint8_t *out, float *red) {
+    const uint32_t k = nb * 32;
+    f32x4 v[kLnSlots], gg[kLnSlots], bb[kLnSlots];
+    float s = 0.0f;
+#pragma unroll
+    for (uint32_t u = 0; u < kLnSlots; u++) {
+        const uint32_t sl = threadIdx.x + u * blockDim.x;  // slot: block sl / 8, elements 4 sl .. 4 sl + 3
+        if (sl / 8 < nb) {
+            v[u] = gload4(x + sl * 4);
+            gg[u] = gload4(lg + sl * 4);
+            bb[u] = gload4(lb + sl * 4);
+            s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+        }
+    }
+    const float mean = block_sum(s, red) / (float)k;
+    float q = 0.0f;
+#pragma unroll
+    for (uint32_t u = 0; u < kLnSlots; u++) {
+        if ((threadIdx.x + u * blockDim.x) / 8 < nb) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float t = v[u][c] - mean;
+                q += t * t;
+            }
+        }
+    }
+    const float rstd = 1.0f / sqrtf(block_sum(q, red) / (float)k + eps);
+#pragma unroll
+    for (uint32_t u = 0; u < kLnSlots; u++) {
+        const uint32_t sl = threadIdx.x + u * blockDim.x, blk = sl / 8;
+        const int j = (int)(sl % 8);
+        if (blk >= span) continue;  // the eight lanes of a block agree
+        uint8_t *rec = out + blk * kPrepBytes;
+        if (blk < nb) {
+            f32x4 h;
+#pragma unroll
+            for (int c = 0; c < 4; c++) h[c] = (v[u][c] - mean) * rstd * gg[u][c] + bb[u][c];
+            if constexpr (GLOBAL)
+                prep_values<KIND>(h, j, (__attribute__((address_space(1))) uint32_t *)rec);
+            else
+                prep_values<KIND>(h, j, (__attribute__((address_space(3))) uint32_t *)rec);
+        } else {
+            if constexpr (GLOBAL)
+                *(__attribute__((address_space(1))) u32x4 *)(rec + 16 * j) = u32x4{0u, 0u, 0u, 0u};
+            else
+                *(__attribute__((address_space(3))) u32x4 *)(rec + 16 * j) = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+}
+
+// One workgroup: LayerNorm of x into global prepared records (for a product whose many row groups
+// would each repeat it).
+template <int KIND>
+__global__ __launch_bounds__(64 * kMaxWaves) void ln_prep_kernel(const float *__restrict__ x, const float *__restrict__ lg,
+                                                                 const float *__restrict__ lb, float eps, uint32_t nb,
+                                                                 uint8_t *__restrict__ out) {
+    __shared__ float red[kMaxWaves];
+    ln_prep<KIND, true>(x, lg, lb, eps, nb, (nb + 7) / 8 * 8, out, red);
 }
 
 template <int KIND>
@@ -89,8 +182,11 @@ __device__ __forceinline__ void load_weights(Batch<KIND> &bt, __amdgpu_buffer_rs
     bt.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rd, (int)(os + b * 64), 0, 0));
 }
 
-// One workgroup per 32 output rows (blockIdx.x), W = blockDim.x / 64 wavefronts; wavefront w
-// takes the batches 8w, 8w + 8W, ... of the row's blocks.
+// Workgroup (g, s): the 32 output rows g (blockIdx.x) over the blocks [s chunk, (s + 1) chunk)
+// of their rows (blockIdx.y, a K split); W = blockDim.x / 64 wavefronts, wavefront w taking the
+// batches 8w, 8w + 8W, ... of the split. With more than one split the splits' row sums go to
+// a.partial and the last split to arrive (a counter per row group) adds them in split order and
+// runs the epilogue, so the result does not depend on timing.
 template <int KIND, int PRO, int EPI>
 __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t dlds[];
@@ -100,64 +196,55 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
     const bool upper = lane >= 32;
     const uint32_t nb = a.nb, nb8 = (nb + 7) / 8, span = nb8 * 8;
     constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
-    const uint32_t g = blockIdx.x;
+    const uint32_t g = blockIdx.x, S = gridDim.y, sp = blockIdx.y;
+    const uint32_t b0 = sp * a.chunk, b1 = min(span, b0 + a.chunk);
     const auto rq = make_rsrc(a.qs + (size_t)g * nb * 32 * QB, nb * 32 * QB);
     const auto rd = make_rsrc(a.ds + (size_t)g * nb8 * 256, nb8 * 512);
+    const auto ra = make_rsrc(a.prep, PRO == PRO_GLOBAL ? span * kPrepBytes : 0);
     const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16);
     const uint32_t os = (uint32_t)(r * 16), oa = (uint32_t)(r * 32 + 16 * upper);
-    uint8_t *prep = dlds;                                   // span records
-    float *part = (float *)(dlds + span * kPrepBytes);      // [W][32] row sums
-    float *red = part + W * 32;                             // [W] reduction scratch
+    uint8_t *prep = dlds;  // records of blocks b0 .. b1 (PRO_LN: of every block)
+    float *part = (float *)(dlds + (PRO == PRO_GLOBAL ? 0 : (PRO == PRO_LN ? span : a.chunk) * kPrepBytes));
+    float *red = part + W * 32;
 
-    // the weights of the wavefront's first batch are requested before x is prepared
-    Batch<KIND> cur;
-    uint32_t b = wave * kBatch;  // W <= nb8: every wavefront has a batch
-    load_weights<KIND>(cur, rq, rd, oq, os, b);
-
-    const uint32_t k = nb * 32;
-    float mean = 0.0f, rstd = 1.0f;
-    if constexpr (PRO == PRO_LN) {  // ferrum_ref/src/kernels/nn.rs:31-44
-        float s = 0.0f;
-        for (uint32_t i = threadIdx.x; i < k; i += blockDim.x) s += a.x[i];
-        mean = block_sum(s, red) / (float)k;
-        float v = 0.0f;
-        for (uint32_t i = threadIdx.x; i < k; i += blockDim.x) {
-            const float t = a.x[i] - mean;
-            v += t * t;
-        }
-        rstd = 1.0f / sqrtf(block_sum(v, red) / (float)k + a.eps);
+    // the wavefront's first batch is requested before x is prepared
+    Batch<KIND> cur, nx;
+    uint32_t bb = b0 + wave * kBatch;
+    if (bb < b1) {
+        load_weights<KIND>(cur, rq, rd, oq, os, bb);
+        if constexpr (PRO == PRO_GLOBAL)
+            cur.a = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(bb * kPrepBytes + oa), 0, 0));
     }
-    // every block's prepared x, eight lanes per block (the eight lanes share the loop bound)
-    for (uint32_t blk = threadIdx.x / 8; blk < span; blk += blockDim.x / 8) {
-        const int j = threadIdx.x % 8;
-        __attribute__((address_space(3))) uint32_t *rec =
-            (__attribute__((address_space(3))) uint32_t *)(prep + blk * kPrepBytes);
-        if (blk < nb) {
-            const uint32_t e = blk * 32 + 4 * j;
-            f32x4 v = *(const __attribute__((address_space(1))) f32x4 *)(a.x + e);
-            if constexpr (PRO == PRO_LN) {
-                const f32x4 gg = *(const __attribute__((address_space(1))) f32x4 *)(a.ln_g + e);
-                const f32x4 bb = *(const __attribute__((address_space(1))) f32x4 *)(a.ln_b + e);
-#pragma unroll
-                for (int c = 0; c < 4; c++) v[c] = (v[c] - mean) * rstd * gg[c] + bb[c];
-            }
-            prep_values<KIND>(v, j, rec);
-        } else {
-            *(__attribute__((address_space(3))) u32x4 *)(rec + 4 * j) = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (PRO == PRO_LN) {
+        ln_prep<KIND, false>(a.x, a.ln_g, a.ln_b, a.eps, nb, span, prep, red);
+        __syncthreads();
+    } else if constexpr (PRO == PRO_NONE) {
+        // the split's blocks of x, eight lanes per block (the eight lanes share the loop bound)
+        for (uint32_t blk = b0 + threadIdx.x / 8; blk < b1; blk += blockDim.x / 8) {
+            const int j = threadIdx.x % 8;
+            __attribute__((address_space(3))) uint32_t *rec =
+                (__attribute__((address_space(3))) uint32_t *)(prep + (blk - b0) * kPrepBytes);
+            if (blk < nb)
+                prep_values<KIND>(gload4(a.x + blk * 32 + 4 * j), j, rec);
+            else
+                *(__attribute__((address_space(3))) u32x4 *)(rec + 4 * j) = u32x4{0u, 0u, 0u, 0u};
         }
+        __syncthreads();
     }
-    __syncthreads();
-
+    const uint32_t pbase = PRO == PRO_LN ? 0 : b0;
     float acc = 0.0f;
-    for (;;) {
-        const uint32_t nxt = b + W * kBatch;
-        Batch<KIND> nx;
-        if (nxt < span) load_weights<KIND>(nx, rq, rd, oq, os, nxt);
-        cur.a = *(const __attribute__((address_space(3))) i32x4 *)(prep + b * kPrepBytes + oa);
+    while (bb < b1) {
+        const uint32_t nxt = bb + W * kBatch;
+        if (nxt < b1) {
+            load_weights<KIND>(nx, rq, rd, oq, os, nxt);
+            if constexpr (PRO == PRO_GLOBAL)
+                nx.a = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(nxt * kPrepBytes + oa), 0, 0));
+        }
+        if constexpr (PRO != PRO_GLOBAL)
+            cur.a = *(const __attribute__((address_space(3))) i32x4 *)(prep + (bb - pbase) * kPrepBytes + oa);
         compute_batch<KIND>(cur, upper, acc);
-        if (nxt >= span) break;
         cur = nx;
-        b = nxt;
+        bb = nxt;
     }
     // row r's odd blocks (lane 32 + r) join its even ones (lane r); the wavefronts' partial sums
     // meet in LDS and are added in wavefront order
@@ -169,6 +256,37 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
     float t = 0.0f;
     for (uint32_t w = 0; w < W; w++) t += part[w * 32 + r];
     const uint32_t row = g * 32 + r;
+    if (S > 1) {
+        a.partial[(size_t)sp * gridDim.x * 32 + row] = t;
+        __threadfence();
+        uint32_t last = 0;
+        if (r == 0) last = atomicAdd(&a.ticket[g], 1u) == S - 1 ? 1u : 0u;
+        if (__shfl(last, 0, 32) == 0) return;
+        __threadfence();
+        t = 0.0f;
+        for (uint32_t q = 0; q < S; q++) t += coherent_load(&a.partial[(size_t)q * gridDim.x * 32 + row]);
+        if (r == 0) a.ticket[g] = 0;  // every split has arrived: ready for the next launch
+    }
+    if constexpr (EPI == EPI_ARGMAX) {
+        // the logits row, and the row group's offer for the pick (pick_kernel reduces the offers)
+        if (row < a.n) a.y[row] = t;
+        float bv = t;
+        uint32_t bi = (row < a.n && t == t) ? row : kNone;
+#pragma unroll
+        for (int o = 16; o >= 1; o /= 2) {
+            const float ov = __shfl_xor(bv, o, 32);
+            const uint32_t oi = __shfl_xor(bi, o, 32);
+            if (better(ov, oi, bv, bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (r == 0) {
+            a.partial[g] = bv;
+            a.pick[g] = bi;
+        }
+        return;
+    }
     if (row >= a.n) return;
     if (a.bias) t = t + a.bias[row];  // decode.rs:42-53: the bias joins after the products
     if constexpr (EPI == EPI_STORE) {
@@ -213,99 +331,122 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *__restrict__ 
     }
 }
 
-// One workgroup (256 threads) per head: decode.rs:81-105 over the cached positions 0..p.
-__global__ __launch_bounds__(256) void attention_kernel(const float *__restrict__ q, const float *__restrict__ kc,
-                                                        const float *__restrict__ vc, const int32_t *__restrict__ state,
-                                                        float *__restrict__ out, uint32_t d, uint32_t hd, uint32_t ctx,
-                                                        float scale) {
-    extern __shared__ float alds[];
-    float *s = alds;          // [ctx] scores, then probabilities
-    float *red = alds + ctx;  // [256]
-    const uint32_t h = blockIdx.x, T = (uint32_t)state[0] + 1, tid = threadIdx.x;
-    const float *qh = q + h * hd;
-    for (uint32_t j = tid; j < T; j += 256) {
-        const float *kj = kc + (size_t)j * d + h * hd;
-        float dot = 0.0f;
-        for (uint32_t i = 0; i < hd; i++) dot += qh[i] * kj[i];
-        s[j] = dot * scale;
-    }
-    __syncthreads();
-    float m = -INFINITY;
-    for (uint32_t j = tid; j < T; j += 256) m = fmaxf(m, s[j]);
+// The greedy pick over the head's row-group offers (the first maximum; NaN never wins), then
+// the step's bookkeeping: the pick becomes the next input when the position is past the prompt,
+// and the position advances.
+__global__ __launch_bounds__(1024) void pick_kernel(const float *__restrict__ offer_v, const uint32_t *__restrict__ offer_i,
+                                                    uint32_t groups, int32_t *__restrict__ state,
+                                                    int32_t *__restrict__ inputs) {
+    __shared__ float sv[16];
+    __shared__ uint32_t si[16];
+    float bv = 0.0f;
+    uint32_t bi = kNone;
+    for (uint32_t q = threadIdx.x; q < groups; q += blockDim.x)
+        if (better(offer_v[q], offer_i[q], bv, bi)) {
+            bv = offer_v[q];
+            bi = offer_i[q];
+        }
 #pragma unroll
-    for (int o = 32; o >= 1; o /= 2) m = fmaxf(m, __shfl_xor(m, o, 64));
-    if (tid % 64 == 0) red[tid / 64] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float z = 0.0f;
-    for (uint32_t j = tid; j < T; j += 256) {
-        const float e = expf(s[j] - m);
-        s[j] = e;
-        z += e;
-    }
-    __syncthreads();  // red is rewritten below
-#pragma unroll
-    for (int o = 32; o >= 1; o /= 2) z += __shfl_xor(z, o, 64);
-    if (tid % 64 == 0) red[4 + tid / 64] = z;
-    __syncthreads();
-    const float sum = red[4] + red[5] + red[6] + red[7];
-    for (uint32_t j = tid; j < T; j += 256) s[j] = s[j] / sum;
-    __syncthreads();
-    // output element i of the head from positions j = part, part + P, ...; the P partial sums
-    // are added in order
-    const uint32_t P = 256 / hd, i = tid % hd, part = tid / hd;
-    float acc = 0.0f;
-    if (part < P)
-        for (uint32_t j = part; j < T; j += P) acc += s[j] * vc[(size_t)j * d + h * hd + i];
-    __syncthreads();
-    red[tid] = acc;
-    __syncthreads();
-    if (tid < hd) {
-        float t = 0.0f;
-        for (uint32_t pp = 0; pp < P; pp++) t += red[pp * hd + tid];
-        out[h * hd + tid] = t;
-    }
-}
-
-// Greedy pick (ferrum_model/src/sampling.rs:32-40: the first maximum; NaN never wins), then the
-// step's bookkeeping: the pick becomes the next input when the position is past the prompt, and
-// the position advances.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ logits, uint32_t vocab,
-                                                      int32_t *__restrict__ state, int32_t *__restrict__ inputs) {
-    __shared__ float bv[1024];
-    __shared__ uint32_t bi[1024];
-    const uint32_t tid = threadIdx.x;
-    float best = 0.0f;
-    uint32_t idx = 0xffffffffu;  // none yet
-    for (uint32_t i = tid; i < vocab; i += 1024) {
-        const float v = logits[i];
-        if (v == v && (idx == 0xffffffffu || v > best)) {
-            best = v;
-            idx = i;
+    for (int o = 32; o >= 1; o /= 2) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const uint32_t oi = __shfl_xor(bi, o, 64);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
         }
     }
-    bv[tid] = best;
-    bi[tid] = idx;
+    if (threadIdx.x % 64 == 0) {
+        sv[threadIdx.x / 64] = bv;
+        si[threadIdx.x / 64] = bi;
+    }
     __syncthreads();
-    for (uint32_t o = 512; o >= 1; o /= 2) {
-        if (tid < o) {
-            const float v2 = bv[tid + o];
-            const uint32_t i2 = bi[tid + o];
-            const uint32_t i1 = bi[tid];
-            if (i2 != 0xffffffffu &&
-                (i1 == 0xffffffffu || v2 > bv[tid] || (v2 == bv[tid] && i2 < i1))) {
-                bv[tid] = v2;
-                bi[tid] = i2;
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < blockDim.x / 64; w++)
+            if (better(sv[w], si[w], bv, bi)) {
+                bv = sv[w];
+                bi = si[w];
             }
-        }
-        __syncthreads();
-    }
-    if (tid == 0) {
-        const int32_t pick = bi[0] == 0xffffffffu ? 0 : (int32_t)bi[0];
+        const int32_t pick = bi == kNone ? 0 : (int32_t)bi;
         const int32_t p = state[0];
         state[2] = pick;
         if (p + 1 >= state[1]) inputs[p + 1] = pick;
         state[0] = p + 1;
+    }
+}
+
+// One workgroup per head (decode.rs:81-105 over the cached positions 0..p). L = hd / 4 lanes
+// share a cache row (a 16-byte load each), so a pass over the workgroup reads kAttnThreads / L
+// rows at once; the lanes of a row add their parts with shuffles.
+template <int L>
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float *__restrict__ q, const float *__restrict__ kc,
+                                                                 const float *__restrict__ vc, const int32_t *__restrict__ state,
+                                                                 float *__restrict__ out, uint32_t d, uint32_t ctx,
+                                                                 float scale) {
+    constexpr uint32_t hd = 4 * L, NR = kAttnThreads / L;
+    extern __shared__ float alds[];
+    float *s = alds;              // [ctx] scores, then probabilities
+    float *accs = alds + ctx;     // [NR][hd] output partial sums
+    float *red = accs + NR * hd;  // [2 * waves]
+    const uint32_t h = blockIdx.x, T = (uint32_t)state[0] + 1, tid = threadIdx.x;
+    const uint32_t li = tid % L, rg = tid / L;
+    const f32x4 qv = gload4(q + h * hd + 4 * li);
+    const float *kb = kc + h * hd + 4 * li;
+    const float *vb = vc + h * hd + 4 * li;
+    for (uint32_t j = rg; j < T; j += 2 * NR) {  // the L lanes of a row share the loop bound
+        const bool two = j + NR < T;
+        const f32x4 k0 = gload4(kb + (size_t)j * d);
+        const f32x4 k1 = two ? gload4(kb + (size_t)(j + NR) * d) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float d0 = (qv.x * k0.x + qv.y * k0.y) + (qv.z * k0.z + qv.w * k0.w);
+        float d1 = (qv.x * k1.x + qv.y * k1.y) + (qv.z * k1.z + qv.w * k1.w);
+#pragma unroll
+        for (int o = L / 2; o >= 1; o /= 2) {
+            d0 += __shfl_xor(d0, o, L);
+            d1 += __shfl_xor(d1, o, L);
+        }
+        if (li == 0) {
+            s[j] = d0 * scale;
+            if (two) s[j + NR] = d1 * scale;
+        }
+    }
+    __syncthreads();
+    constexpr uint32_t NW = kAttnThreads / 64;
+    float m = -INFINITY;
+    for (uint32_t j = tid; j < T; j += kAttnThreads) m = fmaxf(m, s[j]);
+#pragma unroll
+    for (int o = 32; o >= 1; o /= 2) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (tid % 64 == 0) red[tid / 64] = m;
+    __syncthreads();
+    m = red[0];
+    for (uint32_t w = 1; w < NW; w++) m = fmaxf(m, red[w]);
+    float z = 0.0f;
+    for (uint32_t j = tid; j < T; j += kAttnThreads) {
+        const float e = expf(s[j] - m);
+        s[j] = e;
+        z += e;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o /= 2) z += __shfl_xor(z, o, 64);
+    if (tid % 64 == 0) red[NW + tid / 64] = z;
+    __syncthreads();
+    float sum = 0.0f;
+    for (uint32_t w = 0; w < NW; w++) sum += red[NW + w];
+    for (uint32_t j = tid; j < T; j += kAttnThreads) s[j] = s[j] / sum;
+    __syncthreads();
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t j = rg; j < T; j += 2 * NR) {
+        const bool two = j + NR < T;
+        const f32x4 v0 = gload4(vb + (size_t)j * d);
+        const f32x4 v1 = two ? gload4(vb + (size_t)(j + NR) * d) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const float p0 = s[j], p1 = two ? s[j + NR] : 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[c] += p0 * v0[c] + p1 * v1[c];
+    }
+    *(f32x4 *)&accs[rg * hd + 4 * li] = acc;
+    __syncthreads();
+    if (tid < hd) {
+        float t = 0.0f;
+        for (uint32_t g = 0; g < NR; g++) t += accs[g * hd + tid];
+        out[h * hd + tid] = t;
     }
 }
 
@@ -341,10 +482,16 @@ struct fh_gpt2 {
     void *arena = nullptr;
     float *x = nullptr, *q = nullptr, *att = nullptr, *f = nullptr, *logits = nullptr;
     int32_t *state = nullptr, *inputs = nullptr;
+    uint8_t *prep = nullptr;      // prepared records of the final LayerNorm's output (the head's x)
+    float *partial = nullptr;     // split-K row sums, and the head's per-group best values
+    uint32_t *pick = nullptr;     // the head's per-group best rows
+    uint32_t *tickets = nullptr;  // split-K counters per row group; the last one is the head's
+    size_t n_tickets = 0;
     size_t pos = 0;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;
+    bool split_k = false;  // FERRUM_HIP_DECODE_SPLIT_K=1: K splits for the narrow products
     uint64_t step_bytes = 0;
 };
 
@@ -355,42 +502,66 @@ fh_status gpt2_fail_free(fh_gpt2 *m, fh_status st) {
     return st;
 }
 
-// Launch shape of a decode GEMV: workgroups of 32 rows, wavefronts sharing the row's batches.
+// K splits for a product of `groups` row groups and nb8 batches per row: enough workgroups to
+// spread a narrow product (few row groups) over the chip, each split a whole number of batches.
+void plan_splits(uint32_t groups, uint32_t nb8, uint32_t *splits, uint32_t *chunk8) {
+    uint32_t s = (192 + groups - 1) / groups;
+    if (s > nb8) s = nb8;
+    if (s < 1) s = 1;
+    const uint32_t c = (nb8 + s - 1) / s;
+    *chunk8 = c;
+    *splits = (nb8 + c - 1) / c;
+}
+
+// Launch shape of a decode GEMV: workgroups of 32 rows (x K splits), wavefronts sharing the
+// split's batches.
 template <int KIND, int PRO, int EPI>
-hipError_t launch_dgemv(hipStream_t s, const DecodeGemv &a) {
-    const uint32_t nb8 = (a.nb + 7) / 8;
-    const uint32_t W = nb8 < (uint32_t)kMaxWaves ? nb8 : (uint32_t)kMaxWaves;
-    const size_t lds = (size_t)nb8 * 8 * kPrepBytes + (size_t)W * 32 * 4 + (size_t)W * 4;
-    decode_gemv_kernel<KIND, PRO, EPI><<<(a.n + 31) / 32, 64 * W, lds, s>>>(a);
+hipError_t launch_dgemv(hipStream_t s, DecodeGemv a, bool allow_split) {
+    const uint32_t nb8 = (a.nb + 7) / 8, groups = (a.n + 31) / 32;
+    uint32_t splits = 1, chunk8 = nb8;
+    if (allow_split && PRO == PRO_NONE && EPI != EPI_ARGMAX) plan_splits(groups, nb8, &splits, &chunk8);
+    a.chunk = chunk8 * 8;
+    const uint32_t W = chunk8 < (uint32_t)kMaxWaves ? chunk8 : (uint32_t)kMaxWaves;
+    const size_t recs = PRO == PRO_GLOBAL ? 0 : (PRO == PRO_LN ? nb8 * 8 : a.chunk);
+    const size_t lds = recs * kPrepBytes + (size_t)W * 32 * 4 + (size_t)kMaxWaves * 4;
+    decode_gemv_kernel<KIND, PRO, EPI><<<dim3(groups, splits), 64 * W, lds, s>>>(a);
     return hipGetLastError();
 }
+
+#define FH_DGEMV_KERNELS(K)                                                                             \
+    (const void *)decode_gemv_kernel<K, PRO_LN, EPI_QKV>, (const void *)decode_gemv_kernel<K, PRO_NONE, EPI_RESIDUAL>, \
+        (const void *)decode_gemv_kernel<K, PRO_LN, EPI_GELU>, (const void *)decode_gemv_kernel<K, PRO_GLOBAL, EPI_ARGMAX>
 
 // Dynamic LDS beyond the default 64 KiB: prepared x of up to kMaxBlocks blocks plus the row
 // sums, and the attention scores of up to 16384 positions. Set once, before any capture.
 hipError_t set_lds_limits() {
     static const hipError_t e = [] {
         const int gemv_lds = (int)(kMaxBlocks * kPrepBytes + kMaxWaves * 33 * 4);
-        const void *fns[] = {
-            (const void *)decode_gemv_kernel<FH_Q8_0, PRO_LN, EPI_QKV>, (const void *)decode_gemv_kernel<FH_Q8_0, PRO_NONE, EPI_RESIDUAL>,
-            (const void *)decode_gemv_kernel<FH_Q8_0, PRO_LN, EPI_GELU>, (const void *)decode_gemv_kernel<FH_Q8_0, PRO_LN, EPI_STORE>,
-            (const void *)decode_gemv_kernel<FH_Q4_0, PRO_LN, EPI_QKV>, (const void *)decode_gemv_kernel<FH_Q4_0, PRO_NONE, EPI_RESIDUAL>,
-            (const void *)decode_gemv_kernel<FH_Q4_0, PRO_LN, EPI_GELU>, (const void *)decode_gemv_kernel<FH_Q4_0, PRO_LN, EPI_STORE>};
+        const void *fns[] = {FH_DGEMV_KERNELS(FH_Q8_0), FH_DGEMV_KERNELS(FH_Q4_0)};
         for (const void *f : fns) {
             hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, gemv_lds);
             if (r) return r;
         }
-        return hipFuncSetAttribute((const void *)attention_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   (16384 + 256) * 4);
+        const void *att[] = {(const void *)attention_kernel<2>, (const void *)attention_kernel<4>,
+                             (const void *)attention_kernel<8>, (const void *)attention_kernel<16>,
+                             (const void *)attention_kernel<32>, (const void *)attention_kernel<64>};
+        for (const void *f : att) {
+            hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+            if (r) return r;
+        }
+        return hipSuccess;
     }();
     return e;
 }
+#undef FH_DGEMV_KERNELS
 
 template <int PRO, int EPI>
-hipError_t dgemv(hipStream_t s, fh_kind kind, const DecodeGemv &a) {
-    return kind == FH_Q8_0 ? launch_dgemv<FH_Q8_0, PRO, EPI>(s, a) : launch_dgemv<FH_Q4_0, PRO, EPI>(s, a);
+hipError_t dgemv(hipStream_t s, fh_kind kind, const DecodeGemv &a, bool allow_split = false) {
+    return kind == FH_Q8_0 ? launch_dgemv<FH_Q8_0, PRO, EPI>(s, a, allow_split)
+                           : launch_dgemv<FH_Q4_0, PRO, EPI>(s, a, allow_split);
 }
 
-DecodeGemv dg(const fh_qweight *w, const float *x, float *y) {
+DecodeGemv dg(const fh_gpt2 *m, const fh_qweight *w, const float *x, float *y) {
     DecodeGemv a{};
     a.qs = w->qs;
     a.ds = w->ds;
@@ -398,10 +569,30 @@ DecodeGemv dg(const fh_qweight *w, const float *x, float *y) {
     a.y = y;
     a.nb = (uint32_t)(w->k / 32);
     a.n = (uint32_t)w->n;
+    a.partial = m->partial;
+    a.ticket = m->tickets;
+    a.state = m->state;
     return a;
 }
 
 const float *fp(const fh_buffer *b) { return (const float *)b->ptr; }
+
+hipError_t attention(hipStream_t s, const fh_gpt2 *m, const fh_gpt2::Layer &L) {
+    const uint32_t d = (uint32_t)m->dim, hd = (uint32_t)(m->dim / m->heads);
+    const float scale = 1.0f / sqrtf((float)hd);
+    const uint32_t nr = kAttnThreads / (hd / 4);
+    const size_t lds = (m->ctx + (size_t)nr * hd + 2 * kAttnThreads / 64) * sizeof(float);
+    const dim3 grid((uint32_t)m->heads);
+    switch (hd) {
+    case 8: attention_kernel<2><<<grid, kAttnThreads, lds, s>>>(m->q, L.kc, L.vc, m->state, m->att, d, (uint32_t)m->ctx, scale); break;
+    case 16: attention_kernel<4><<<grid, kAttnThreads, lds, s>>>(m->q, L.kc, L.vc, m->state, m->att, d, (uint32_t)m->ctx, scale); break;
+    case 32: attention_kernel<8><<<grid, kAttnThreads, lds, s>>>(m->q, L.kc, L.vc, m->state, m->att, d, (uint32_t)m->ctx, scale); break;
+    case 64: attention_kernel<16><<<grid, kAttnThreads, lds, s>>>(m->q, L.kc, L.vc, m->state, m->att, d, (uint32_t)m->ctx, scale); break;
+    case 128: attention_kernel<32><<<grid, kAttnThreads, lds, s>>>(m->q, L.kc, L.vc, m->state, m->att, d, (uint32_t)m->ctx, scale); break;
+    default: attention_kernel<64><<<grid, kAttnThreads, lds, s>>>(m->q, L.kc, L.vc, m->state, m->att, d, (uint32_t)m->ctx, scale); break;
+    }
+    return hipGetLastError();
+}
 
 // Enqueue one decode step (the graph's body).
 hipError_t enqueue_step(fh_gpt2 *m, hipStream_t s) {
@@ -411,43 +602,43 @@ hipError_t enqueue_step(fh_gpt2 *m, hipStream_t s) {
     else
         embed_kernel<FH_Q4_0><<<1, 256, 0, s>>>(m->tok->qs, m->tok->ds, fp(m->pos_tab), m->state, m->inputs, m->x, d);
     hipError_t e = hipGetLastError();
-    const uint32_t hd = (uint32_t)(m->dim / m->heads);
-    const float scale = 1.0f / sqrtf((float)hd);
     for (auto &L : m->blocks) {
         if (e) return e;
-        DecodeGemv a = dg(L.wqkv, m->x, m->q);
+        DecodeGemv a = dg(m, L.wqkv, m->x, m->q);
         a.ln_g = fp(L.ln1_g);
         a.ln_b = fp(L.ln1_b);
         a.eps = m->eps;
         a.bias = fp(L.bqkv);
         a.kc = L.kc;
         a.vc = L.vc;
-        a.state = m->state;
         a.split = d;
         if ((e = dgemv<PRO_LN, EPI_QKV>(s, m->kind, a))) return e;
-        attention_kernel<<<(uint32_t)m->heads, 256, (m->ctx + 256) * sizeof(float), s>>>(
-            m->q, L.kc, L.vc, m->state, m->att, d, hd, (uint32_t)m->ctx, scale);
-        if ((e = hipGetLastError())) return e;
-        a = dg(L.wo, m->att, m->x);
+        if ((e = attention(s, m, L))) return e;
+        a = dg(m, L.wo, m->att, m->x);
         a.bias = fp(L.bo);
-        if ((e = dgemv<PRO_NONE, EPI_RESIDUAL>(s, m->kind, a))) return e;
-        a = dg(L.w1, m->x, m->f);
+        if ((e = dgemv<PRO_NONE, EPI_RESIDUAL>(s, m->kind, a, m->split_k))) return e;
+        a = dg(m, L.w1, m->x, m->f);
         a.ln_g = fp(L.ln2_g);
         a.ln_b = fp(L.ln2_b);
         a.eps = m->eps;
         a.bias = fp(L.b1);
         if ((e = dgemv<PRO_LN, EPI_GELU>(s, m->kind, a))) return e;
-        a = dg(L.w2, m->f, m->x);
+        a = dg(m, L.w2, m->f, m->x);
         a.bias = fp(L.b2);
-        if ((e = dgemv<PRO_NONE, EPI_RESIDUAL>(s, m->kind, a))) return e;
+        if ((e = dgemv<PRO_NONE, EPI_RESIDUAL>(s, m->kind, a, m->split_k))) return e;
     }
     if (e) return e;
-    DecodeGemv a = dg(m->head, m->x, m->logits);
-    a.ln_g = fp(m->lnf_g);
-    a.ln_b = fp(m->lnf_b);
-    a.eps = m->eps;
-    if ((e = dgemv<PRO_LN, EPI_STORE>(s, m->kind, a))) return e;
-    argmax_kernel<<<1, 1024, 0, s>>>(m->logits, (uint32_t)m->vocab, m->state, m->inputs);
+    const uint32_t nbd = d / 32;
+    if (m->kind == FH_Q8_0)
+        ln_prep_kernel<FH_Q8_0><<<1, 64 * kMaxWaves, 0, s>>>(m->x, fp(m->lnf_g), fp(m->lnf_b), m->eps, nbd, m->prep);
+    else
+        ln_prep_kernel<FH_Q4_0><<<1, 64 * kMaxWaves, 0, s>>>(m->x, fp(m->lnf_g), fp(m->lnf_b), m->eps, nbd, m->prep);
+    if ((e = hipGetLastError())) return e;
+    DecodeGemv a = dg(m, m->head, m->x, m->logits);
+    a.prep = m->prep;
+    a.pick = m->pick;
+    if ((e = dgemv<PRO_GLOBAL, EPI_ARGMAX>(s, m->kind, a))) return e;
+    pick_kernel<<<1, 1024, 0, s>>>(m->partial, m->pick, (uint32_t)((m->vocab + 31) / 32), m->state, m->inputs);
     return hipGetLastError();
 }
 
@@ -558,11 +749,13 @@ fh_status fh_gpt2_from_gguf(fh_device *dev, const fh_gguf *g, fh_gpt2 **out) {
     if (d % m->heads)
         return gpt2_fail_free(m, fail(FH_ERR_INVALID, "gpt2: dim %zu is not divisible by heads %zu", d, m->heads));
     const size_t hd = d / m->heads;
-    if (d % 32 || h % 32 || d / 32 > kMaxBlocks || h / 32 > kMaxBlocks || hd > 256 || m->ctx > 16384 ||
+    if (d % 32 || h % 32 || d > 4096 || h / 32 > kMaxBlocks || (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128 && hd != 256) ||
+        m->ctx > 16384 ||
         m->vocab > (1u << 30))
         return gpt2_fail_free(m, fail(FH_ERR_UNSUPPORTED,
                                       "gpt2: dim %zu / hidden %zu / head %zu / ctx %zu outside what the decode kernels "
-                                      "take (multiples of 32 up to 16384, heads up to 256 wide, ctx up to 16384)",
+                                      "take (dim a multiple of 32 up to 4096, hidden up to 16384, heads 8, 16, 32, "
+                                      "64, 128 or 256 wide, ctx up to 16384)",
                                       d, h, hd, m->ctx));
     fh_kind kind = (fh_kind)0;
     if ((st = mat(dev, g, "token_embd.weight", d, m->vocab, &kind, &m->tok))) return gpt2_fail_free(m, st);
@@ -597,8 +790,20 @@ fh_status fh_gpt2_from_gguf(fh_device *dev, const fh_gguf *g, fh_gpt2 **out) {
     // caches and scratch in one allocation (every piece 256-byte aligned)
     auto up = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
     const size_t cache = up(m->ctx * d * 4);
+    // split-K scratch: the split products (attention output, FFN down) have d outputs and d or h
+    // inputs; the head needs one value per row group
+    const size_t groups_v = (m->vocab + 31) / 32, groups_d = d / 32;
+    size_t part_floats = groups_v;
+    for (size_t k : {d, h}) {
+        uint32_t sp, c8;
+        plan_splits((uint32_t)groups_d, (uint32_t)((k / 32 + 7) / 8), &sp, &c8);
+        part_floats = std::max(part_floats, (size_t)sp * groups_d * 32);
+    }
+    const size_t max_groups = groups_d;
+    m->n_tickets = max_groups + 1;
     const size_t total = 2 * m->layers * cache + 3 * up(d * 4) + up(h * 4) + up(m->vocab * 4) + up(16) +
-                         up((m->ctx + 1) * 4);
+                         up((m->ctx + 1) * 4) + up(d / 32 * 8 * 128 + 1024) + up(part_floats * 4) +
+                         up(groups_v * 4) + up(m->n_tickets * 4);
     if ((st = alloc_bytes(dev, total, &m->arena))) return gpt2_fail_free(m, st);
     uint8_t *p = (uint8_t *)m->arena;
     for (auto &L : m->blocks) {
@@ -620,9 +825,19 @@ fh_status fh_gpt2_from_gguf(fh_device *dev, const fh_gguf *g, fh_gpt2 **out) {
     m->state = (int32_t *)p;
     p += up(16);
     m->inputs = (int32_t *)p;
+    p += up((m->ctx + 1) * 4);
+    m->prep = p;
+    p += up(d / 32 * 8 * 128 + 1024);
+    m->partial = (float *)p;
+    p += up(part_floats * 4);
+    m->pick = (uint32_t *)p;
+    p += up(groups_v * 4);
+    m->tickets = (uint32_t *)p;  // zero from the allocation; every launch leaves them zero
     if (hipError_t e = set_lds_limits()) return gpt2_fail_free(m, hip_fail(dev, e, "gpt2 kernels"));
     const char *ng = getenv("FERRUM_HIP_NO_GRAPH");
     m->use_graph = !(ng && ng[0] == '1');
+    const char *sk = getenv("FERRUM_HIP_DECODE_SPLIT_K");
+    m->split_k = sk && sk[0] == '1';
     // the caches need no clearing: position p reads only entries 0..p, all written by then
     if ((st = begin_command(dev, "gpt2 state"))) return gpt2_fail_free(m, st);
     set_state_kernel<<<1, 1, 0, dev->stream>>>(m->state, 0, 0);
