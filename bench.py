@@ -177,7 +177,8 @@ def bench_gemv_pool(fh, g, ev, kind, groups, pool_bytes, steps, warmup, seed=0):
             "gbs": step_bytes / (step_ms * 1e-3) / 1e9, "launches": launches}
 
 
-def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0):
+def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0, path=None):
+    path = fh.QPath.Tiled if path is None else path
     rng = np.random.default_rng(seed)
     items = []
     for k, n in shapes:
@@ -188,13 +189,13 @@ def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0):
         items.append((qw, gx, gy))
     flops = sum(2 * m * k * n for k, n in shapes)
     for qw, gx, gy in items:
-        fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.Tiled)
+        fh.linear_q_with(g, gx, qw, gy, m, path)
     g.sync()
     e0, e1 = ev.create(2)
     ev.record(e0)
     for _ in range(steps):
         for qw, gx, gy in items:
-            fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.Tiled)
+            fh.linear_q_with(g, gx, qw, gy, m, path)
     ev.record(e1)
     g.sync()
     ms = ev.ms(e0, e1) / steps
@@ -339,16 +340,20 @@ def main():
                                        ("q4_0_gemm_llama1b", fh.QKind.Q4_0, LLAMA1B_SHAPES, (512, 4096)),
                                        ("q8_0_gemm_llama1b", fh.QKind.Q8_0, LLAMA1B_SHAPES, (512, 4096))):
             for m in ms:
-                r = bench_gemm(fh, g, ev, kind, m, shapes, 10)
-                log(f"{name} M={m}:", r)
-                extra[f"{name}_m{m}"] = {"tflops": round(r["tflops"], 2),
-                                         "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
-                                         "ms_per_step": r["ms_per_step"], "flops_per_step": r["flops_per_step"]}
+                for tag, path in (("", fh.QPath.TiledFast), ("_precise", fh.QPath.Tiled)):
+                    r = bench_gemm(fh, g, ev, kind, m, shapes, 10, path=path)
+                    log(f"{name}{tag} M={m}:", r)
+                    extra[f"{name}{tag}_m{m}"] = {"tflops": round(r["tflops"], 2),
+                                                  "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+                                                  "ms_per_step": r["ms_per_step"],
+                                                  "flops_per_step": r["flops_per_step"]}
         dec = bench_decode(fh, g, cpu=not a.no_cpu)
         log("GPT-2-small Q8_0 decode:", dec)
         extra["gpt2_small_q8_0_decode"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec.items()}
-        extra["gemm_operands"] = ("split-f16 x (hi + lo) times exact integer quants on f16 MFMA, f32 accumulate, "
-                                  "f32 block scale per 32-element block")
+        extra["gemm_operands"] = ("scoring GEMM (QPath.TiledFast): x as f16 times exact f16 integer quants on f16 "
+                                  "MFMA with the f32 block scale per block, plus an e4m3 correction (x's f16 "
+                                  "residual times e4m3 d*q) on the scaled fp8 MFMA; _precise: x as two f16 parts "
+                                  "(QPath.Tiled); f32 accumulate")
 
     cpu = None
     if not a.no_cpu:

@@ -4,29 +4,34 @@
 // naive_kernel: one thread per output, ascending k, the dequantised value formed first and then
 // multiplied (ferrum_wgpu/src/shaders/quant/qlinear.wgsl:18-59). Kept as the baseline path.
 //
-// The MFMA dequant-GEMM (the scoring / prefill path) runs in two launches:
-//   1. split_x_kernel writes x as two f16 parts, x = hi + lo (about 22 significant bits), per
-//      32-element block in the k order the MFMA operands use (below). Each x element is split
-//      once, not once per weight tile.
-//   2. gemm_kernel: a CTA computes a BM x BN tile of y with 4 wavefronts. A 32-element block of
-//      x (hi and lo) and of the weights form a pipeline stage in LDS (double-buffered, one
-//      barrier per stage; the next stage's global loads are in flight during the MFMAs); the
-//      weight quants become exact f16 integers (Q8_0 -128..127, Q4_0 -8..7) with a byte permute
-//      into an f16 exponent pattern and one packed f16 subtract; per 32 x 32 output tile,
-//      P = hi * q + lo * q over the block with four v_mfma_f32_32x32x16_f16 (f32 accumulate),
-//      then acc += d[col] * P with the block's f32 scale.
-// The scale is applied in f32 after the exact integer dot, so the product meets the reference's
-// 1e-5 relative bound for linear_q (ferrum_wgpu/src/tolerance.rs:7) as well as the
-// 1e-3 + 2e-3 |y| GEMM bound; plain f16 or bf16 activations do not.
+// Both MFMA dequant-GEMMs take the weights' quants as exact f16 integers (Q8_0 -128..127, Q4_0
+// -8..7, a byte permute into an f16 exponent pattern and one packed f16 subtract) and scale each
+// block's exact dot product by the block's f32 scale after the matrix cores (acc += d * P), so
+// the weights carry no rounding; they differ in how finely x is carried:
 //
-// k order inside a block. The unpack produces f16 pairs from a quant dword w: for Q8_0 the bytes
-// (0, 2) and (1, 3), i.e. elements 4i + {0, 2, 1, 3}; for Q4_0 the low nibbles of bytes (0, 2),
-// (1, 3), then the high nibbles, i.e. elements 4i + {0, 2, 1, 3} and 16 + 4i + {0, 2, 1, 3}. The
-// MFMA sums over k, so x is laid out in that same order and no shuffle is needed.
+// gemm_precise_kernel (FH_PATH_TILED, within the reference's 1e-5 product tolerance,
+// ferrum_wgpu/src/tolerance.rs:7): x = hi + lo, two f16 parts (about 22 bits), split once per
+// element by split_x_precise_kernel; per 32 x 32 tile and block four v_mfma_f32_32x32x16_f16.
 //
-// Tile order: CTAs are numbered so each XCD (CTAs go round-robin over the 8 XCDs) takes a
-// contiguous range of tiles, walked along N for a fixed M stripe: the XCD's L2 keeps the x rows
-// while the weights stream.
+// gemm_kernel (FH_PATH_TILED_FAST, the scoring GEMM, within |g - w| <= 1e-3 + 2e-3 |w|): x = hi
+// + lo with hi in f16 and lo kept as e4m3 (about 15 bits in all). Per tile and block two f16
+// MFMAs on hi; per two blocks one v_mfma_scale_f32_32x32x64_f8f6f4 on lo times the weights'
+// e4m3 correction operand (d * q per element, made once per weight by make_b8_kernel), whose
+// two power-of-two row / column scales the instruction applies itself, so the correction
+// accumulates over all of K with no per-block work. That is 1.5 f16-equivalent passes instead
+// of 2. split_x_kernel prepares hi, lo and the row scales.
+//
+// k order inside a block (f16 operands). The unpack produces f16 pairs from a quant dword w: for
+// Q8_0 the bytes (0, 2) and (1, 3), i.e. elements 4i + {0, 2, 1, 3}; for Q4_0 the low nibbles of
+// bytes (0, 2), (1, 3), then the high nibbles, i.e. elements 4i + {0, 2, 1, 3} and 16 + 4i +
+// {0, 2, 1, 3}. The MFMA sums over k, so x is laid out in that same order and no shuffle is
+// needed. The fp8 operands use the natural k order on both sides (the instruction pairs lane
+// (row, half h) byte j of A with lane (column, half h) byte j of B).
+//
+// Tile order (fast kernel): CTAs are dealt round-robin to the 8 XCDs, and each XCD works through
+// whole 8 x 8 super-tiles, so the CTAs that run together share stripes of x and of the weights.
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "internal.hpp"
 
@@ -39,6 +44,11 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float half_to_float(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// A raw buffer resource over [base, base + bytes): loads at offsets at or past `bytes` return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
 }
 
 // ---- naive baseline ----
@@ -86,6 +96,115 @@ __device__ __forceinline__ int elem_of_pos(int p) {
     }
 }
 
+// ---- x -> hi (f16, per block in operand order) and the fp8 correction ----
+// One workgroup per row m. hi = f16(x) (|x| beyond the f16 range saturates); lo = x - hi, kept as
+// e4m3 of lo * 2^s (natural k order, rows of K rounded up to 64 with a zero tail), where 2^s puts the row's largest lo (below 2^-11 of the
+// row's largest |x|) just under 2^8; xsc[m] holds the E8M0 byte of 2^-s (four copies) for the
+// scaled MFMA. Eight lanes per block, lane j taking elements 4j .. 4j + 3.
+__device__ __forceinline__ _Float16 f16_sat(float e) { return (_Float16)fminf(fmaxf(e, -65504.0f), 65504.0f); }
+
+__device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
+    // e4m3 has no infinity: values beyond +-448 would become NaN, so they are clamped first
+    const auto cl = [](float v) { return fminf(fmaxf(v, -448.0f), 448.0f); };
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(cl(a), cl(b), 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(cl(c), cl(d), w, true);
+    return (uint32_t)w;
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void split_x_kernel(const float *__restrict__ x, _Float16 *__restrict__ xh,
+                                                      uint8_t *__restrict__ xl, int32_t *__restrict__ xsc, uint32_t K) {
+    __shared__ float red[4];
+    const uint32_t m = blockIdx.x, tid = threadIdx.x, nb = K / 32, K64 = (K + 63) / 64 * 64;
+    if (K64 != K && tid < 8) *(uint32_t *)(xl + (size_t)m * K64 + K + 4 * tid) = 0u;  // the row's zero tail
+    const float *xr = x + (size_t)m * K;
+    float mx = 0.0f;
+    for (uint32_t i = tid * 4; i < K; i += 1024) {
+        const f32x4 v = *(const f32x4 *)(xr + i);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o /= 2) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (tid % 64 == 0) red[tid / 64] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // 2^E <= mx < 2^(E+1); |lo| < 2^(E-10); s = 18 - E puts |lo| 2^s below 2^8
+    int sc = 0;
+    if (mx > 0.0f && mx <= 3.4028235e38f) sc = 18 - ((int)(__float_as_uint(mx) >> 23) - 127);
+    sc = sc < -126 ? -126 : (sc > 126 ? 126 : sc);
+    const float f = __uint_as_float((uint32_t)(127 + sc) << 23);
+    if (tid == 0) xsc[m] = (127 - sc) * 0x01010101;
+    const int j = tid % 8;
+    for (uint32_t t = tid / 8; t < nb; t += 32) {
+        const f32x4 v = *(const f32x4 *)(xr + t * 32 + 4 * j);
+        _Float16 h[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) h[q] = f16_sat(v[q]);
+        *(uint32_t *)(xl + (size_t)m * K64 + t * 32 + 4 * j) =
+            fp8x4((v.x - (float)h[0]) * f, (v.y - (float)h[1]) * f, (v.z - (float)h[2]) * f, (v.w - (float)h[3]) * f);
+        _Float16 *out = xh + ((size_t)m * nb + t) * 32;
+        typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+        if constexpr (KIND == FH_Q8_0) {
+            // positions 4j..4j+3 hold elements 4j + {0, 2, 1, 3}
+            *(f16x4 *)(out + 4 * j) = f16x4{h[0], h[2], h[1], h[3]};
+        } else {
+            // positions 8i..8i+7 hold elements 4i + {0, 2, 1, 3} and 16 + 4i + {0, 2, 1, 3}: lane i < 4
+            // takes lane i + 4's four values and writes the eight
+            _Float16 o[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                o[q] = __builtin_bit_cast(_Float16, (uint16_t)__shfl_xor((int)__builtin_bit_cast(uint16_t, h[q]), 4, 8));
+            if (j < 4) *(f16x8 *)(out + 8 * j) = f16x8{h[0], h[2], h[1], h[3], o[0], o[2], o[1], o[3]};
+        }
+    }
+}
+
+// ---- the weights' fp8 correction operand: e4m3 of d * q * 2^t per element, natural k order, ----
+// ---- rows of K rounded up to 64 (zero tail) ----
+// One wavefront per weight row n (an output column of y): 2^t puts the row's largest |d q| just
+// under 2^8; bsc[n] holds the E8M0 byte of 2^-t (four copies). Built once per weight.
+template <int KIND>
+__global__ __launch_bounds__(256) void make_b8_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ ds,
+                                                      uint8_t *__restrict__ b8, int32_t *__restrict__ bsc, uint32_t K,
+                                                      uint32_t N) {
+    const uint32_t n = blockIdx.x * 4 + threadIdx.x / 64, lane = threadIdx.x % 64, nb = K / 32;
+    const uint32_t K64 = (K + 63) / 64 * 64;
+    if (n >= N) return;  // whole wavefront
+    if (K64 != K && lane < 2) *(u32x4 *)(b8 + (size_t)n * K64 + K + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+    float dm = 0.0f;
+    for (uint32_t b = lane; b < nb; b += 64) dm = fmaxf(dm, fabsf(half_bits_to_float(ds[scale_slot(n, b, nb)])));
+#pragma unroll
+    for (int o = 32; o >= 1; o /= 2) dm = fmaxf(dm, __shfl_xor(dm, o, 64));
+    const float amax = dm * (KIND == FH_Q8_0 ? 127.0f : 8.0f);
+    int t = 0;
+    if (amax > 0.0f && amax <= 3.4028235e38f) t = 7 - ((int)(__float_as_uint(amax) >> 23) - 127);
+    t = t < -126 ? -126 : (t > 126 ? 126 : t);
+    const float f = __uint_as_float((uint32_t)(127 + t) << 23);
+    if (lane == 0) bsc[n] = (127 - t) * 0x01010101;
+    for (uint32_t c = lane; c < 2 * nb; c += 64) {  // half blocks of 16 elements
+        const uint32_t b = c / 2, half = c % 2;
+        const size_t slot = tile_slot(n, b, nb);
+        const float d = half_bits_to_float(ds[scale_slot(n, b, nb)]) * f;  // exact: a power of two
+        u32x4 q;
+        if constexpr (KIND == FH_Q8_0)
+            q = *(const u32x4 *)(qs + slot * 32 + 16 * half);
+        else
+            q = *(const u32x4 *)(qs + slot * 16);
+        u32x4 o;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            float e[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t byte = (q[w] >> (8 * i)) & 0xffu;
+                e[i] = KIND == FH_Q8_0 ? (float)(int8_t)byte : (float)((int32_t)((byte >> (4 * half)) & 15u) - 8);
+            }
+            o[w] = fp8x4(d * e[0], d * e[1], d * e[2], d * e[3]);
+        }
+        *(u32x4 *)(b8 + (size_t)n * K64 + b * 32 + 16 * half) = o;
+    }
+}
+
 // ---- x -> (hi, lo) f16, per block in operand order: xs[m][b] = 32 hi halves then 32 lo ----
 // Eight lanes per (row, block), lane j loading elements 4j..4j+3 (a wavefront reads 1 KiB of
 // contiguous x per instruction). |x| beyond the f16 range saturates hi (|x| < 65504 is exact).
@@ -95,7 +214,7 @@ __device__ __forceinline__ void split1(float e, _Float16 &h, _Float16 &l) {
 }
 
 template <int KIND>
-__global__ __launch_bounds__(256) void split_x_kernel(const float *__restrict__ x, _Float16 *__restrict__ xs,
+__global__ __launch_bounds__(256) void split_x_precise_kernel(const float *__restrict__ x, _Float16 *__restrict__ xs,
                                                       size_t items) {
     const int j = threadIdx.x % 8;
     for (size_t t = ((size_t)blockIdx.x * 256 + threadIdx.x) / 8; t < items; t += (size_t)gridDim.x * 32) {
@@ -167,13 +286,333 @@ __device__ __forceinline__ void unpack_q8(const u32x4 q, u32x4 (&out)[2]) {
     }
 }
 
+struct GemmArgs {
+    const _Float16 *xh;
+    const uint8_t *xl;
+    const int32_t *xsc;
+    const uint8_t *qs;
+    const uint16_t *ds;
+    const uint8_t *b8;
+    const int32_t *bsc;
+    float *y;
+    float *partial;  // K-split partial products (up to 8 x M x N floats), or null: no split
+    uint32_t M, K, N;
+};
+
 // ---- the MFMA GEMM ----
-constexpr int kARow = 72;  // LDS halves per x row and block: 32 hi + 32 lo + 8 pad (144 B)
-constexpr int kBRow = 40;  // LDS halves per weight row and block: 32 + 8 pad (80 B)
-constexpr int kBKB = 1;    // blocks (of 32 k) per pipeline stage
+// Per pipeline stage (two blocks, 64 k) a CTA holds in LDS: x hi (f16, operand order), x lo (e4m3),
+// the weights' quants unpacked to exact f16 integers, their e4m3 correction operand and the two
+// blocks' scales. Per 32 x 32 output tile and block: P = hi * q (two v_mfma_f32_32x32x16_f16),
+// acc += d * P; per stage: acc += (lo 2^s) * (d q 2^t) * 2^-s 2^-t (one scaled
+// v_mfma_scale_f32_32x32x64_f8f6f4, which applies both powers of two and accumulates in f32).
+constexpr int kAStr = 72;   // LDS halves per x row and stage: 64 hi + 8 pad
+constexpr int kLStr = 80;   // LDS bytes per x row and stage: 64 e4m3 + 16 pad
+constexpr int kBStr = 72;   // LDS halves per weight row and stage: 64 + 8 pad
+constexpr int kB8Str = 80;  // LDS bytes per weight row and stage
+
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 
 template <int KIND, int BM, int BN, int WAVES_M>
 struct GemmCfg {
+    static constexpr int WAVES_N = 4 / WAVES_M;
+    static constexpr int TM = BM / WAVES_M / 32, TN = BN / WAVES_N / 32;  // 32x32 tiles per wave
+    static constexpr int QB = KIND == FH_Q8_0 ? 32 : 16;                   // quant bytes per block
+    static constexpr int XH = BM * 8 / 256;                                // 16-byte x-hi chunks per thread
+    static constexpr int XL = (BM * 4 + 255) / 256;                        // 16-byte x-lo chunks per thread
+    static constexpr int QC = BN * 2 * QB / 16;                            // 16-byte quant chunks per stage
+    static constexpr int QL = (QC + 255) / 256;
+    static constexpr int BL = (BN * 4 + 255) / 256;                        // 16-byte b8 chunks per thread
+    static constexpr int DL = (BN * 2 + 255) / 256;                        // scales per thread
+    static_assert(TM >= 1 && TN >= 1, "wave tile must be whole 32x32 tiles");
+    static_assert(BM * 8 % 256 == 0, "x staging must divide over 256 threads");
+};
+
+template <int KIND, int BM, int BN, int WAVES_M>
+__global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict__ xh, const uint8_t *__restrict__ xl,
+                                                      const int32_t *__restrict__ xsc, const uint8_t *__restrict__ qs,
+                                                      const uint16_t *__restrict__ ds, const uint8_t *__restrict__ b8,
+                                                      const int32_t *__restrict__ bsc, float *__restrict__ y,
+                                                      uint32_t M, uint32_t K, uint32_t N, uint32_t mt, uint32_t nt,
+                                                      uint32_t split_stages) {
+    using C = GemmCfg<KIND, BM, BN, WAVES_M>;
+    __shared__ __attribute__((aligned(16))) _Float16 sA[BM * kAStr];
+    __shared__ __attribute__((aligned(16))) uint8_t sL[BM * kLStr];
+    __shared__ __attribute__((aligned(16))) _Float16 sB[BN * kBStr];
+    __shared__ __attribute__((aligned(16))) uint8_t sB8[BN * kB8Str];
+    __shared__ float sD[2 * BN];
+
+    // Tile of this CTA. CTAs are dealt round-robin to the 8 XCDs; each XCD works through whole
+    // super-tiles of 8 x 8 tiles, so the CTAs that run together on one XCD share 8 stripes of x
+    // and 8 of weights in its L2 (a square working set: both operands are reused 8 times).
+    const uint32_t c = blockIdx.x, xcd = c % 8, u = c / 8;
+    const uint32_t snt = (nt + 7) / 8;                   // super-tiles along N
+    const uint32_t sidx = (u / 64) * 8 + xcd, v = u % 64;
+    const uint32_t mi = (sidx / snt) * 8 + v / 8, ni = (sidx % snt) * 8 + v % 8;
+    if (mi >= mt || ni >= nt) return;  // whole CTA: no barrier is left waiting
+    const uint32_t m0 = mi * BM, n0 = ni * BN;
+
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+    const uint32_t nb = K / 32, all_stages = (nb + 1) / 2;
+    // K split blockIdx.y: stages [st0, st1) (one split: all of them); each split writes its own
+    // partial product, y + split * M * N, added up by gemm_reduce_kernel in split order
+    const uint32_t st0 = blockIdx.y * split_stages, st1 = min(all_stages, st0 + split_stages);
+    const uint32_t stages = st1 > st0 ? st1 - st0 : 0;
+    y += (size_t)blockIdx.y * M * N;
+    const int fr = lane % 32;        // fragment row (x) / column (weights)
+    const int fk = 8 * (lane / 32);  // first of this lane's 8 positions in a K = 16 step
+    const int f8 = 32 * (lane / 32); // first of this lane's 32 bytes in the K = 64 correction step
+
+    // the correction's power-of-two scales per fragment row / column
+    int32_t asc[C::TM], bscv[C::TN];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++) {
+        const uint32_t m = m0 + (wm * C::TM + i) * 32 + fr;
+        asc[i] = m < M ? xsc[m] : 0x7f7f7f7f;
+    }
+#pragma unroll
+    for (int j = 0; j < C::TN; j++) {
+        const uint32_t n = n0 + (wn * C::TN + j) * 32 + fr;
+        bscv[j] = n < N ? bsc[n] : 0x7f7f7f7f;
+    }
+
+    // Per-thread operand offsets at stage 0 (bytes), advanced by a fixed stride per stage. Buffer
+    // loads return zeros past each array's end (rows past M and columns past the weight's padded
+    // row count); the second block of an odd last stage reads whatever follows, which the f16 pass
+    // skips, and the fp8 operands' zero row tails cover it for the correction.
+    const uint32_t K64 = (K + 63) / 64 * 64;
+    const auto r_xh = make_rsrc(xh, M * nb * 64);
+    const auto r_xl = make_rsrc(xl, M * K64);
+    const auto r_q = make_rsrc(qs, (N + 31) / 32 * 32 * nb * C::QB);
+    const auto r_b8 = make_rsrc(b8, N * K64);
+    const auto r_d = make_rsrc(ds, (N + 31) / 32 * 32 * ((nb + 7) / 8 * 8) * 2);
+    constexpr uint32_t kOut = 0x80000000u;  // an offset past every array: loads return zeros
+    uint32_t o_xh[C::XH], o_xl[C::XL], o_q[C::QL], o_b8[C::BL], o_d;
+    uint32_t s_xh[C::XH], s_xl[C::XL], s_q[C::QL], s_b8[C::BL];  // LDS byte offsets
+#pragma unroll
+    for (int i = 0; i < C::XH; i++) {
+        const int cc = tid + 256 * i, r = cc / 8, bb = (cc % 8) / 4, part = cc % 4;
+        const uint32_t m = m0 + r;
+        o_xh[i] = m < M ? ((m * nb + bb) * 32 + part * 8) * 2 : kOut;
+        s_xh[i] = (r * kAStr + bb * 32 + part * 8) * 2;
+    }
+#pragma unroll
+    for (int i = 0; i < C::XL; i++) {
+        const int cc = tid + 256 * i, r = cc / 4, part = cc % 4;
+        const uint32_t m = m0 + r;
+        o_xl[i] = cc < BM * 4 && m < M ? m * K64 + part * 16 : kOut;
+        s_xl[i] = cc < BM * 4 ? r * kLStr + part * 16 : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < C::QL; i++) {
+        const int cc = tid + 256 * i;
+        constexpr int CPB = C::QB / 16;  // 16-byte chunks per block
+        const int col = cc / (2 * CPB), bb = (cc % (2 * CPB)) / CPB, part = cc % CPB;
+        const uint32_t n = n0 + col;
+        o_q[i] = cc < C::QC ? (((n >> 5) * nb + bb) * 32 + (n & 31)) * C::QB + part * 16 : kOut;
+        s_q[i] = cc < C::QC ? (col * kBStr + bb * 32 + (KIND == FH_Q8_0 ? 16 * part : 0)) * 2 : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < C::BL; i++) {
+        const int cc = tid + 256 * i, col = cc / 4, part = cc % 4;
+        const uint32_t n = n0 + col;
+        o_b8[i] = cc < BN * 4 && n < N ? n * K64 + part * 16 : kOut;
+        s_b8[i] = cc < BN * 4 ? col * kB8Str + part * 16 : 0u;
+    }
+    {
+        const uint32_t n = n0 + tid;  // thread t < BN loads column t's two scales of the stage
+        o_d = tid < BN ? (((n >> 5) * ((nb + 7) / 8) * 32 + (n & 31)) * 8) * 2 : kOut;
+    }
+    // two register sets of staged operands: stage st + 2 is requested while stage st is computed
+    u32x4 rxh[2][C::XH], rxl[2][C::XL], rq[2][C::QL], rb8[2][C::BL];
+    uint32_t rd[2] = {0u, 0u};
+    auto load_stage = [&](uint32_t st, int rs) {
+#pragma unroll
+        for (int i = 0; i < C::XH; i++)
+            rxh[rs][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_xh, (int)(o_xh[i] + st * 128), 0, 0));
+#pragma unroll
+        for (int i = 0; i < C::XL; i++)
+            rxl[rs][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_xl, (int)(o_xl[i] + st * 64), 0, 0));
+#pragma unroll
+        for (int i = 0; i < C::QL; i++)
+            rq[rs][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_q, (int)(o_q[i] + st * 64 * C::QB), 0, 0));
+#pragma unroll
+        for (int i = 0; i < C::BL; i++)
+            rb8[rs][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_b8, (int)(o_b8[i] + st * 64), 0, 0));
+        // blocks 2 st and 2 st + 1 are neighbours in one run of eight scales
+        rd[rs] = __builtin_amdgcn_raw_buffer_load_b32(r_d, (int)(o_d + (st >> 2) * 512 + (st & 3) * 4), 0, 0);
+    };
+    auto store_stage = [&](int rs) {
+        uint8_t *sAb = (uint8_t *)sA, *sBb = (uint8_t *)sB;
+#pragma unroll
+        for (int i = 0; i < C::XH; i++) *(u32x4 *)(sAb + s_xh[i]) = rxh[rs][i];
+#pragma unroll
+        for (int i = 0; i < C::XL; i++)
+            if (tid + 256 * i < BM * 4) *(u32x4 *)(sL + s_xl[i]) = rxl[rs][i];
+#pragma unroll
+        for (int i = 0; i < C::QL; i++) {
+            if (tid + 256 * i < C::QC) {
+                if constexpr (KIND == FH_Q8_0) {
+                    u32x4 o[2];
+                    unpack_q8(rq[rs][i], o);
+                    *(u32x4 *)(sBb + s_q[i]) = o[0];
+                    *(u32x4 *)(sBb + s_q[i] + 16) = o[1];
+                } else {
+                    u32x4 o[4];
+                    unpack_q4(rq[rs][i], o);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) *(u32x4 *)(sBb + s_q[i] + 16 * e) = o[e];
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::BL; i++)
+            if (tid + 256 * i < BN * 4) *(u32x4 *)(sB8 + s_b8[i]) = rb8[rs][i];
+        if (tid < BN) {
+            sD[tid] = half_to_float(rd[rs] & 0xffffu);
+            sD[BN + tid] = half_to_float(rd[rs] >> 16);
+        }
+    };
+
+    f32x16 acc[C::TM][C::TN];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int j = 0; j < C::TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    // one stage: store the staged registers of set RS, request stage st + 2 into that set, compute
+    auto stage = [&](uint32_t st, auto rs_c) {
+        constexpr int rs = decltype(rs_c)::value;
+        __syncthreads();  // every wave is done reading the previous stage
+        store_stage(rs);
+        __syncthreads();
+        if (st + 2 < st1) load_stage(st + 2, rs);  // in flight during the next two stages' MFMAs
+        const int nbb = nb - 2 * st < 2u ? 1 : 2;  // wave-uniform
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) {
+            if (bb >= nbb) break;
+            f16x8 bf[C::TN][2];
+            float dcol[C::TN];
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) {
+                const int col = (wn * C::TN + j) * 32 + fr;
+#pragma unroll
+                for (int s2 = 0; s2 < 2; s2++) bf[j][s2] = *(const f16x8 *)(&sB[col * kBStr + bb * 32 + 16 * s2 + fk]);
+                dcol[j] = sD[bb * BN + col];
+            }
+            f16x8 ah[C::TM][2];
+#pragma unroll
+            for (int i = 0; i < C::TM; i++) {
+                const int r = (wm * C::TM + i) * 32 + fr;
+#pragma unroll
+                for (int s2 = 0; s2 < 2; s2++) ah[i][s2] = *(const f16x8 *)(&sA[r * kAStr + bb * 32 + 16 * s2 + fk]);
+            }
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                for (int j = 0; j < C::TN; j++) {
+                    f32x16 p = {};
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], bf[j][0], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], bf[j][1], p, 0, 0, 0);
+#pragma unroll
+                    for (int q = 0; q < 16; q++) acc[i][j][q] = fmaf(dcol[j], p[q], acc[i][j][q]);
+                }
+        }
+        // the correction over the stage's 64 k (blocks past nb hold zeros)
+        i32x8 b8f[C::TN], a8[C::TM];
+#pragma unroll
+        for (int j = 0; j < C::TN; j++) {
+            const int col = (wn * C::TN + j) * 32 + fr;
+            b8f[j] = *(const i32x8 *)(&sB8[col * kB8Str + f8]);
+        }
+#pragma unroll
+        for (int i = 0; i < C::TM; i++) {
+            const int r = (wm * C::TM + i) * 32 + fr;
+            a8[i] = *(const i32x8 *)(&sL[r * kLStr + f8]);
+        }
+#pragma unroll
+        for (int i = 0; i < C::TM; i++)
+#pragma unroll
+            for (int j = 0; j < C::TN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8[i], b8f[j], acc[i][j], 0, 0, 0, asc[i], 0,
+                                                                            bscv[j]);
+    };
+    if (stages > 0) load_stage(st0, 0);
+    if (stages > 1) load_stage(st0 + 1, 1);
+    for (uint32_t st = st0; st < st1; st += 2) {  // unrolled by two: register sets are named statically
+        stage(st, std::integral_constant<int, 0>{});
+        if (st + 1 < st1) stage(st + 1, std::integral_constant<int, 1>{});
+    }
+
+    // D layout of a 32x32 tile: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int j = 0; j < C::TN; j++) {
+            const uint32_t col = n0 + (wn * C::TN + j) * 32 + fr;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = m0 + (wm * C::TM + i) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+                if (row < M && col < N) y[(size_t)row * N + col] = acc[i][j][r];
+            }
+        }
+}
+
+// K splits for a grid of `tiles` CTAs over `stages` stages: enough CTAs to cover the chip twice,
+// each split at least two stages long (at most 8 splits).
+uint32_t gemm_splits(uint64_t tiles, uint32_t stages) {
+    if (tiles >= 512) return 1;
+    uint32_t sp = (uint32_t)((512 + tiles - 1) / tiles);
+    sp = min(sp, 8u);
+    sp = min(sp, max(stages / 2, 1u));
+    return max(sp, 1u);
+}
+
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restrict__ part, float *__restrict__ y,
+                                                          size_t n, uint32_t splits) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        float t = part[i];
+        for (uint32_t s = 1; s < splits; s++) t += part[s * n + i];
+        y[i] = t;
+    }
+}
+
+template <int KIND, int BM, int BN, int WAVES_M>
+hipError_t run_gemm(hipStream_t s, const GemmArgs &g) {
+    const uint32_t mt = (g.M + BM - 1) / BM, nt = (g.N + BN - 1) / BN;
+    const uint64_t supers = (uint64_t)((mt + 7) / 8) * ((nt + 7) / 8);
+    if (supers * 64 > 0x7fffffffull) return hipErrorInvalidValue;
+    const uint32_t grid = (uint32_t)((supers + 7) / 8 * 8 * 64);  // whole super-tiles on every XCD
+    const uint32_t stages = (g.K / 32 + 1) / 2;
+    const uint32_t sp = g.partial ? gemm_splits((uint64_t)mt * nt, stages) : 1;
+    const uint32_t per = (stages + sp - 1) / sp;
+    float *out = sp > 1 ? g.partial : g.y;
+    gemm_kernel<KIND, BM, BN, WAVES_M><<<dim3(grid, sp), 256, 0, s>>>(g.xh, g.xl, g.xsc, g.qs, g.ds, g.b8, g.bsc, out,
+                                                                       g.M, g.K, g.N, mt, nt, per);
+    if (sp > 1) {
+        const size_t n = (size_t)g.M * g.N;
+        const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
+        gemm_reduce_kernel<<<rg, 256, 0, s>>>(g.partial, g.y, n, sp);  // (a split past the last stage wrote zeros)
+    }
+    return hipGetLastError();
+}
+
+template <int KIND>
+hipError_t gemm_dispatch(hipStream_t s, const GemmArgs &g) {
+    if (g.M <= 32) return run_gemm<KIND, 32, 256, 1>(s, g);
+    if (g.M <= 64) return run_gemm<KIND, 64, 128, 2>(s, g);
+    return run_gemm<KIND, 128, 128, 2>(s, g);
+}
+
+// ---- the precise MFMA GEMM (FH_PATH_TILED): x as two f16 parts, about 22 bits ----
+constexpr int kARow2 = 72;  // LDS halves per x row and block: 32 hi + 32 lo + 8 pad (144 B)
+constexpr int kBRow2 = 40;  // LDS halves per weight row and block: 32 + 8 pad (80 B)
+constexpr int kBKB = 1;    // blocks (of 32 k) per pipeline stage
+
+template <int KIND, int BM, int BN, int WAVES_M>
+struct GemmCfg2 {
     static constexpr int WAVES_N = 4 / WAVES_M;
     static constexpr int TM = BM / WAVES_M / 32, TN = BN / WAVES_N / 32;  // 32x32 tiles per wave
     static constexpr int QB = KIND == FH_Q8_0 ? 32 : 16;                   // quant bytes per block
@@ -187,13 +626,13 @@ struct GemmCfg {
 };
 
 template <int KIND, int BM, int BN, int WAVES_M>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict__ xs, const uint8_t *__restrict__ qs,
+__global__ __launch_bounds__(256, 2) void gemm_precise_kernel(const _Float16 *__restrict__ xs, const uint8_t *__restrict__ qs,
                                                       const uint16_t *__restrict__ ds, float *__restrict__ y,
                                                       uint32_t M, uint32_t K, uint32_t N, uint32_t mt, uint32_t nt) {
-    using C = GemmCfg<KIND, BM, BN, WAVES_M>;
-    // stage layout: x row r, block bb at r * kBKB * kARow + bb * kARow; weight row likewise
-    __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * kBKB * kARow];
-    __shared__ __attribute__((aligned(16))) _Float16 sB[2][BN * kBKB * kBRow];
+    using C = GemmCfg2<KIND, BM, BN, WAVES_M>;
+    // stage layout: x row r, block bb at r * kBKB * kARow2 + bb * kARow2; weight row likewise
+    __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * kBKB * kARow2];
+    __shared__ __attribute__((aligned(16))) _Float16 sB[2][BN * kBKB * kBRow2];
     __shared__ float sD[2][kBKB * BN];
 
     // tile of this CTA: the XCD's contiguous share of the tiles, N fastest
@@ -248,7 +687,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
 #pragma unroll
         for (int i = 0; i < C::A_LD; i++) {
             const int cc = tid + 256 * i, r = cc / (8 * kBKB), bb = (cc / 8) % kBKB, ch = cc % 8;
-            *(u32x4 *)(&sA[buf][(r * kBKB + bb) * kARow + ch * 8]) = ra[i];
+            *(u32x4 *)(&sA[buf][(r * kBKB + bb) * kARow2 + ch * 8]) = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < C::B_PER; i++) {
@@ -256,7 +695,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
             if (cc < C::B_LD) {
                 constexpr int CPR = kBKB * C::QB / 16;
                 const int col = cc / CPR, bb = (cc % CPR) / (C::QB / 16), part = cc % (C::QB / 16);
-                _Float16 *row = &sB[buf][(col * kBKB + bb) * kBRow];
+                _Float16 *row = &sB[buf][(col * kBKB + bb) * kBRow2];
                 if constexpr (KIND == FH_Q8_0) {
                     u32x4 o[2];
                     unpack_q8(rb[i], o);
@@ -306,7 +745,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
 #pragma unroll
             for (int j = 0; j < C::TN; j++) {
                 const int col = (wn * C::TN + j) * 32 + fr;
-                const _Float16 *row = &sB[buf][(col * kBKB + bb) * kBRow];
+                const _Float16 *row = &sB[buf][(col * kBKB + bb) * kBRow2];
 #pragma unroll
                 for (int s = 0; s < 2; s++) bf[j][s] = *(const f16x8 *)(row + 16 * s + fk);
                 dcol[j] = sD[buf][bb * BN + col];
@@ -315,7 +754,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
 #pragma unroll
             for (int i = 0; i < C::TM; i++) {
                 const int r = (wm * C::TM + i) * 32 + fr;
-                const _Float16 *row = &sA[buf][(r * kBKB + bb) * kARow];
+                const _Float16 *row = &sA[buf][(r * kBKB + bb) * kARow2];
 #pragma unroll
                 for (int s = 0; s < 2; s++) {
                     ah[i][s] = *(const f16x8 *)(row + 16 * s + fk);
@@ -355,27 +794,74 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
 }
 
 template <int KIND, int BM, int BN, int WAVES_M>
-hipError_t run_gemm(hipStream_t s, const _Float16 *xs, const uint8_t *qs, const uint16_t *ds, float *y, uint32_t M,
+hipError_t run_gemm_precise(hipStream_t s, const _Float16 *xs, const uint8_t *qs, const uint16_t *ds, float *y, uint32_t M,
                     uint32_t K, uint32_t N) {
     const uint32_t mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
     const uint64_t tiles = (uint64_t)mt * nt;
     if (tiles > 0x7fffffffull) return hipErrorInvalidValue;
     const uint32_t grid = (uint32_t)((tiles + 7) / 8 * 8);  // a multiple of the XCD count
-    gemm_kernel<KIND, BM, BN, WAVES_M><<<grid, 256, 0, s>>>(xs, qs, ds, y, M, K, N, mt, nt);
+    gemm_precise_kernel<KIND, BM, BN, WAVES_M><<<grid, 256, 0, s>>>(xs, qs, ds, y, M, K, N, mt, nt);
     return hipGetLastError();
 }
 
 template <int KIND>
-hipError_t gemm_dispatch(hipStream_t s, const _Float16 *xs, const uint8_t *qs, const uint16_t *ds, float *y,
+hipError_t gemm_precise_dispatch(hipStream_t s, const _Float16 *xs, const uint8_t *qs, const uint16_t *ds, float *y,
                          uint32_t M, uint32_t K, uint32_t N) {
-    if (M <= 32) return run_gemm<KIND, 32, 256, 1>(s, xs, qs, ds, y, M, K, N);
-    if (M <= 64) return run_gemm<KIND, 64, 128, 2>(s, xs, qs, ds, y, M, K, N);
-    return run_gemm<KIND, 128, 128, 2>(s, xs, qs, ds, y, M, K, N);
+    if (M <= 32) return run_gemm_precise<KIND, 32, 256, 1>(s, xs, qs, ds, y, M, K, N);
+    if (M <= 64) return run_gemm_precise<KIND, 64, 128, 2>(s, xs, qs, ds, y, M, K, N);
+    return run_gemm_precise<KIND, 128, 128, 2>(s, xs, qs, ds, y, M, K, N);
 }
 
 }  // namespace
 
-size_t gemm_workspace_bytes(size_t rows, size_t k) { return rows * k * 4; }
+// x hi (2 bytes per element), x lo (1 byte), one scale word per row, each piece 256-aligned
+size_t gemm_workspace_bytes(size_t rows, size_t k, size_t n) {
+    const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    return up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)) + up(rows * 4) + gemm_partial_bytes(rows, k, n);
+}
+
+// Room for the K-split partial products when the product's tile grid is too small to fill the
+// chip (the tile shapes and split rule of gemm_dispatch / run_gemm); none otherwise.
+size_t gemm_partial_bytes(size_t rows, size_t k, size_t n) {
+    const size_t bm = rows <= 32 ? 32 : rows <= 64 ? 64 : 128, bn = rows <= 32 ? 256 : 128;
+    const uint64_t tiles = (uint64_t)((rows + bm - 1) / bm) * ((n + bn - 1) / bn);
+    const uint32_t sp = gemm_splits(tiles, (uint32_t)((k / 32 + 1) / 2));
+    return sp > 1 ? (size_t)sp * rows * n * 4 : 0;
+}
+
+size_t gemm_b8_bytes(size_t k, size_t n) { return (n * ((k + 63) / 64 * 64) + 255) / 256 * 256 + n * 4; }
+
+bool gemm_supported(size_t rows, size_t k, size_t n) {
+    // every operand's byte offsets fit the kernel's 32-bit buffer offsets
+    const size_t k64 = (k + 63) / 64 * 64, lim = (size_t)1 << 31;
+    return rows * k * 2 < lim && rows * k64 < lim && n * k64 < lim && (n + 31) / 32 * 32 * (k / 32) * 32 < lim;
+}
+
+hipError_t launch_make_b8(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, uint8_t *b8, size_t k,
+                          size_t n) {
+    int32_t *bsc = (int32_t *)(b8 + (n * ((k + 63) / 64 * 64) + 255) / 256 * 256);
+    const unsigned grid = (unsigned)((n + 3) / 4);
+    if (kind == FH_Q8_0)
+        make_b8_kernel<FH_Q8_0><<<grid, 256, 0, s>>>(qs, ds, b8, bsc, (uint32_t)k, (uint32_t)n);
+    else
+        make_b8_kernel<FH_Q4_0><<<grid, 256, 0, s>>>(qs, ds, b8, bsc, (uint32_t)k, (uint32_t)n);
+    return hipGetLastError();
+}
+
+size_t gemm_precise_workspace_bytes(size_t rows, size_t k) { return rows * k * 4; }
+
+hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
+                               float *y, size_t rows, size_t k, size_t n, void *workspace) {
+    _Float16 *xs = (_Float16 *)workspace;
+    const size_t items = rows * (k / 32);
+    const unsigned g = (unsigned)(items / 32 + 1 < 65535 ? items / 32 + 1 : 65535);
+    if (kind == FH_Q8_0) {
+        split_x_precise_kernel<FH_Q8_0><<<g, 256, 0, s>>>(x, xs, items);
+        return gemm_precise_dispatch<FH_Q8_0>(s, xs, qs, ds, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+    }
+    split_x_precise_kernel<FH_Q4_0><<<g, 256, 0, s>>>(x, xs, items);
+    return gemm_precise_dispatch<FH_Q4_0>(s, xs, qs, ds, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+}
 
 hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
                         float *y, size_t rows, size_t k, size_t n) {
@@ -388,17 +874,30 @@ hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const ui
     return hipGetLastError();
 }
 
-hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
-                       float *y, size_t rows, size_t k, size_t n, void *workspace) {
-    _Float16 *xs = (_Float16 *)workspace;
-    const size_t items = rows * (k / 32);
-    const unsigned g = (unsigned)(items / 32 + 1 < 65535 ? items / 32 + 1 : 65535);
+hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
+                       const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace) {
+    const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    uint8_t *ws = (uint8_t *)workspace;
+    GemmArgs g;
+    g.xh = (const _Float16 *)ws;
+    g.xl = ws + up(rows * k * 2);
+    g.xsc = (const int32_t *)(ws + up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)));
+    g.qs = qs;
+    g.ds = ds;
+    g.b8 = b8;
+    g.bsc = (const int32_t *)(b8 + up(n * ((k + 63) / 64 * 64)));
+    g.y = y;
+    const size_t pb = gemm_partial_bytes(rows, k, n);
+    g.partial = pb ? (float *)(ws + up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)) + up(rows * 4)) : nullptr;
+    g.M = (uint32_t)rows;
+    g.K = (uint32_t)k;
+    g.N = (uint32_t)n;
     if (kind == FH_Q8_0) {
-        split_x_kernel<FH_Q8_0><<<g, 256, 0, s>>>(x, xs, items);
-        return gemm_dispatch<FH_Q8_0>(s, xs, qs, ds, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+        split_x_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
+        return gemm_dispatch<FH_Q8_0>(s, g);
     }
-    split_x_kernel<FH_Q4_0><<<g, 256, 0, s>>>(x, xs, items);
-    return gemm_dispatch<FH_Q4_0>(s, xs, qs, ds, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+    split_x_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
+    return gemm_dispatch<FH_Q4_0>(s, g);
 }
 
 }  // namespace fh

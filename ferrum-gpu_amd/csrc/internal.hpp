@@ -50,6 +50,9 @@ struct fh_qweight {
     uint8_t *qs = nullptr;    // quant plane (256-byte aligned)
     uint16_t *ds = nullptr;   // scale plane
     size_t nbytes = 0;        // exact GGUF byte count of the weight
+    // The MFMA GEMM's fp8 correction operand (e4m3 of d * q per element, per-row power-of-two
+    // scales; gemm_b8_bytes), built on the weight's first multi-row product and freed with it.
+    mutable uint8_t *b8 = nullptr;
 };
 
 namespace fh {
@@ -94,7 +97,7 @@ fh_status workspace(fh_device *dev, size_t bytes, void **out);
 void dev_retain(fh_device *dev);
 void dev_release(fh_device *dev);  // destroys the stream and the device on the last release
 
-// ---- kernel launchers (each issues exactly one kernel on dev->stream) ----
+// ---- kernel launchers (on dev->stream; a command may issue several) ----
 // codec.hip
 hipError_t launch_encode_rows(hipStream_t s, fh_kind kind, const float *src, uint8_t *dst,
                               size_t nblocks);
@@ -145,10 +148,20 @@ hipError_t launch_gemv_group(hipStream_t s, fh_kind kind, const GemvDesc *descs,
 // gemm.hip
 hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
                         float *y, size_t rows, size_t k, size_t n);
-// The MFMA GEMM (two launches: split x into workspace, then the product); workspace holds
-// gemm_workspace_bytes(rows, k) bytes.
-size_t gemm_workspace_bytes(size_t rows, size_t k);
-hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
-                       float *y, size_t rows, size_t k, size_t n, void *workspace);
+// The fast MFMA GEMM (two launches: split x into workspace, then the product); workspace holds
+// gemm_workspace_bytes(rows, k) bytes, b8 the weight's correction operand (launch_make_b8).
+size_t gemm_workspace_bytes(size_t rows, size_t k, size_t n);
+size_t gemm_partial_bytes(size_t rows, size_t k, size_t n);
+size_t gemm_b8_bytes(size_t k, size_t n);
+// Whether the GEMM's 32-bit buffer offsets cover rows x (k, n) (every operand under 2^31 bytes).
+bool gemm_supported(size_t rows, size_t k, size_t n);
+hipError_t launch_make_b8(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, uint8_t *b8, size_t k,
+                          size_t n);
+hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
+                       const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace);
+// The precise MFMA GEMM (x as two f16 parts; split into workspace, then the product).
+size_t gemm_precise_workspace_bytes(size_t rows, size_t k);
+hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
+                               float *y, size_t rows, size_t k, size_t n, void *workspace);
 
 }  // namespace fh

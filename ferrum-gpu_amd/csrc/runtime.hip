@@ -486,6 +486,7 @@ void fh_qweight_free(fh_qweight *w) {
     if (!w) return;
     fh_device *dev = w->dev;
     free_bytes(dev, w->ptr);
+    if (w->b8) free_bytes(dev, w->b8);
     delete w;
     dev_release(dev);
 }
@@ -524,6 +525,7 @@ fh_status fh_qweight_dequantise(fh_device *dev, const fh_qweight *w, fh_buffer *
 // ---- linear layers ----
 
 fh_path fh_choose(size_t rows, fh_kind kind, size_t k, size_t n) {
+    (void)n;
     if (rows == 1 && kind_ok(kind) && gemv_supported(kind, k, n)) return FH_PATH_GEMV;
     return FH_PATH_TILED;
 }
@@ -550,9 +552,28 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
         return end_command(dev, "linear_q");
     case FH_PATH_TILED: {
         void *ws = nullptr;
-        if (rows && (st = workspace(dev, gemm_workspace_bytes(rows, w->k), &ws))) return st;
+        if (rows && (st = workspace(dev, gemm_precise_workspace_bytes(rows, w->k), &ws))) return st;
         if ((st = begin_command(dev, "linear_q"))) return st;
-        if (rows) (void)launch_gemm(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, ws);
+        if (rows) (void)launch_gemm_precise(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, ws);
+        return end_command(dev, "linear_q");
+    }
+    case FH_PATH_TILED_FAST: {
+        if (!gemm_supported(rows, w->k, w->n))
+            return fail(FH_ERR_INVALID, "the MFMA GEMM's 32-bit offsets do not cover %zu rows of a %zu x %zu weight",
+                        rows, w->n, w->k);
+        void *ws = nullptr;
+        if (rows && (st = workspace(dev, gemm_workspace_bytes(rows, w->k, w->n), &ws))) return st;
+        void *fresh = nullptr;  // the correction operand, built within the weight's first multi-row command
+        if (rows && !w->b8 && (st = alloc_bytes(dev, gemm_b8_bytes(w->k, w->n), &fresh))) return st;
+        if ((st = begin_command(dev, "linear_q"))) {
+            if (fresh) free_bytes(dev, fresh);
+            return st;
+        }
+        if (fresh) {
+            (void)launch_make_b8(dev->stream, w->kind, w->qs, w->ds, (uint8_t *)fresh, w->k, w->n);
+            w->b8 = (uint8_t *)fresh;
+        }
+        if (rows) (void)launch_gemm(dev->stream, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, ws);
         return end_command(dev, "linear_q");
     }
     default:

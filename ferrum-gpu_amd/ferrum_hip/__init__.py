@@ -42,11 +42,14 @@ class QKind(enum.IntEnum):
 
 
 class QPath(enum.IntEnum):
-    """ferrum_wgpu/src/ops/quant.rs:292-305. Tiled is the MFMA dequant-GEMM here."""
+    """ferrum_wgpu/src/ops/quant.rs:292-305. Tiled is the MFMA dequant-GEMM here (within the
+    reference's 1e-5); TiledFast (no counterpart in the reference) is the scoring GEMM with an fp8
+    correction, within the MFMA-GEMM tolerance |g - w| <= 1e-3 + 2e-3 |w|."""
     Auto = 0
     Naive = 1
     Gemv = 2
     Tiled = 3
+    TiledFast = 4
 
 
 _lib = None

@@ -54,12 +54,16 @@ typedef enum fh_kind { FH_Q4_0 = 2, FH_Q8_0 = 8 } fh_kind;
 
 /* Which kernel runs a quantized linear layer. Replaces QPath (ferrum_wgpu/src/ops/quant.rs:292-305):
  * NAIVE = one thread per output (the baseline kernel), GEMV = batch-1 wavefront GEMV (exactly one
- * row), TILED = the LDS-staged MFMA dequant-GEMM (any rows), AUTO = fh_choose. */
+ * row), TILED = the LDS-staged MFMA dequant-GEMM (any rows; x carried to about 22 bits, within the
+ * reference's 1e-5 product tolerance), AUTO = fh_choose. No counterpart in the reference:
+ * TILED_FAST = the scoring GEMM (x as f16 plus an fp8 correction on the fp8 matrix cores; within
+ * the MFMA-GEMM tolerance |g - w| <= 1e-3 + 2e-3 |w|, about 5e-5 absolute at the scoring shapes). */
 typedef enum fh_path {
     FH_PATH_AUTO = 0,
     FH_PATH_NAIVE = 1,
     FH_PATH_GEMV = 2,
-    FH_PATH_TILED = 3
+    FH_PATH_TILED = 3,
+    FH_PATH_TILED_FAST = 4
 } fh_path;
 
 typedef struct fh_device fh_device;   /* replaces ferrum_wgpu::device::Gpu */

@@ -329,6 +329,81 @@ def test_gemm_scoring_shapes_meet_both_tolerances(fh, g, orc, kind_name, m, k, n
     assert e_gpu <= 2 * max(e_cpu, 1e-6), (e_gpu, e_cpu)
 
 
+# The scoring GEMM (QPath.TiledFast, no counterpart in the reference): x is carried as f16 plus an
+# e4m3 correction (about 15 bits), so it is held to the MFMA-GEMM bound of the task statement,
+# |g - w| <= 1e-3 + 2e-3 |w| on every output against the reference's f32 CPU product, and to a
+# stated precision: max_rel_err against the CPU product below FAST_BOUND (measured 2.5e-5 to
+# 5.5e-5 at these shapes; a dropped correction term gives about 2e-4).
+FAST_BOUND = 1e-4
+
+
+@pytest.mark.parametrize("kind_name,m,k,n", [
+    ("Q4_0", 512, 896, 1152), ("Q4_0", 512, 896, 4864), ("Q4_0", 512, 4864, 896),
+    ("Q8_0", 64, 2048, 5632), ("Q4_0", 8, 5632, 2048), ("Q8_0", 512, 5632, 256),
+    ("Q8_0", 2048, 896, 4864)])
+def test_fast_gemm_meets_the_gemm_bound_at_the_scoring_shapes(fh, g, orc, kind_name, m, k, n):
+    kind = fh.QKind[kind_name]
+    rng = np.random.default_rng(m + k + n)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+    b = orc.quantise_matrix(int(kind), w, k, n)
+    want = cpu_linear(orc, kind, b, x, m, k, n)
+    qw = fh.upload_qweight(g, kind, b, k, n)
+    gx, gy = g.upload(x), g.zeros(m * n)
+    say("fast gemm", kind_name, m, k, n)
+    fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.TiledFast)
+    got = g.read(gy)
+    err = np.abs(got - want)
+    viol = np.mean(err > 1e-3 + 2e-3 * np.abs(want))
+    e = orc.max_rel_err(got, want)
+    say(f"  vs cpu: max abs {err.max():.2e}, max rel {e:.2e}, violations {viol:.2e}")
+    assert viol == 0
+    assert e < FAST_BOUND, e
+    # a second product reuses the weight's correction operand and gives the same bits
+    gy2 = g.zeros(m * n)
+    fh.linear_q_with(g, gx, qw, gy2, m, fh.QPath.TiledFast)
+    assert np.array_equal(g.read(gy2), got)
+
+
+def test_fast_gemm_on_awkward_shapes_and_values(fh, g, orc):
+    """Odd block counts (the last stage holds one block), rows and columns that are not whole
+    tiles, the reference's uniform test data and rows of very different magnitudes (each row's
+    correction has its own power-of-two scale)."""
+    rng = np.random.default_rng(11)
+    for kind in kinds(fh):
+        for rows, k, n in [(2, 32, 1), (33, 96, 17), (17, 64, 40), (130, 160, 129), (257, 224, 300),
+                           (64, 2080, 70), (5, 4096, 33)]:
+            w = orc.rand_vec(k * n, 6)
+            b = orc.quantise_matrix(int(kind), w, k, n)
+            x = orc.rand_vec(rows * k, 9).reshape(rows, k)
+            x *= (10.0 ** rng.integers(-3, 4, rows)).astype(np.float32)[:, None]  # per-row magnitudes
+            x = x.reshape(-1).astype(np.float32)
+            want = cpu_linear(orc, kind, b, x, rows, k, n)
+            qw = fh.upload_qweight(g, kind, b, k, n)
+            gx, gy = g.upload(x), g.zeros(rows * n)
+            say("fast kernel", kind.label(), rows, k, n)
+            fh.linear_q_with(g, gx, qw, gy, rows, fh.QPath.TiledFast)
+            got = g.read(gy).reshape(rows, n)
+            ref = want.reshape(rows, n)
+            # per row, relative to the row's own scale (rows differ by up to 1e6)
+            for r in range(rows):
+                scale = max(np.abs(ref[r]).max(), 1e-30)
+                e = np.abs(got[r] - ref[r]).max() / scale
+                assert e < FAST_BOUND, (kind, rows, k, n, r, e)
+
+
+def test_fast_gemm_is_one_command_and_fails_cleanly(fh, g, orc):
+    """The first multi-row product of a weight also builds its correction operand: still one
+    command, and an injected fault at it leaves the weight usable."""
+    k, n, rows = 64, 40, 3
+    b = orc.quantise_matrix(orc.Q8_0, orc.rand_vec(k * n, 2), k, n)
+    qw = fh.upload_qweight(g, fh.QKind.Q8_0, b, k, n)
+    x, y = g.upload(orc.rand_vec(rows * k, 3)), g.zeros(rows * n)
+    assert g.sweep_faults(lambda: fh.linear_q_with(g, x, qw, y, rows, fh.QPath.TiledFast)) == 1
+    want = cpu_linear(orc, fh.QKind.Q8_0, b, orc.rand_vec(rows * k, 3), rows, k, n)
+    assert orc.max_rel_err(g.read(y), want) < FAST_BOUND
+
+
 def test_grouped_gemv_plan_equals_single_launches(fh, g, orc):
     """The grouped launch runs the same per-row code: results are bit-identical to linear_q."""
     rng = np.random.default_rng(5)
