@@ -305,6 +305,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the GPT-2-small decode (config 2), one JSON line (for profiling)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the scoring GEMM at the TinyLlama-1.1B shapes, M = 4096, one JSON line (for profiling)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the path shards by "
@@ -321,6 +323,13 @@ def main():
         g.close()
         return
     ev = HipEvents(g)
+    if a.gemm_only:
+        r = bench_gemm(fh, g, ev, fh.QKind.Q4_0, 4096, LLAMA1B_SHAPES, a.steps, path=fh.QPath.TiledFast)
+        print(json.dumps({"metric": "Q4_0 scoring GEMM TFLOP/s, TinyLlama-1.1B layer shapes, M = 4096",
+                          "value": round(r["tflops"], 2), "unit": "TFLOP/s", "n_gpus": 1, "higher_is_better": True,
+                          "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4), "detail": r}))
+        g.close()
+        return
     name, cus = g.info()
     log(f"device {name}, {cus} CUs")
     copy = bench_copy(g, ev)
