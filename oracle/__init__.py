@@ -54,6 +54,14 @@ def lib() -> ctypes.CDLL:
             "fo_gpt2_cache_new": (P, [P]),
             "fo_gpt2_cache_free": (None, [P, P]),
             "fo_gpt2_feed": (ctypes.c_int, [P, P, S, P]),
+            "fo_rope_tables": (None, [S, S, S, ctypes.c_float, P, ctypes.c_float, P, P]),
+            "fo_rmsnorm": (None, [P, P, S, S, ctypes.c_float, P]),
+            "fo_apply_rope": (None, [P, S, S, S, S, P, P, ctypes.c_int]),
+            "fo_attend_row": (None, [P, P, P, S, S, S, S, P, P]),
+            "fo_silu": (ctypes.c_float, [ctypes.c_float]),
+            "fo_swiglu": (None, [P, P, S, P]),
+            "fo_score": (None, [P, P, S, S, P, P]),
+            "fo_llama_forward": (ctypes.c_int, [P, P, S, ctypes.c_int, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -308,3 +316,128 @@ def gpt2_generate(model: dict, prompt, n_new: int) -> list[int]:
     if rc != 0:
         raise ValueError("gpt2 generate failed (context full or token out of range)")
     return [int(t) for t in out[:n_new]]
+
+
+# ---- Llama / Qwen2 (oracle/llama.c) ----
+
+# Per-block tensor order of the reference (ferrum_ref/src/models/llama/mod.rs:99-128).
+LLAMA_BLOCK_NAMES = ("attn_norm", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "ffn_norm", "gate", "up", "down")
+
+
+def rope_tables(start: int, n: int, rope_dim: int, base: float, freq_factors=None, linear_factor=1.0):
+    """ferrum_ref/src/models/llama/ops.rs:78-101: (cos, sin), each [n, rope_dim/2]."""
+    half = rope_dim // 2
+    c, s = np.empty(n * half, np.float32), np.empty(n * half, np.float32)
+    ff = None if freq_factors is None or len(freq_factors) == 0 else _f32(freq_factors)
+    lib().fo_rope_tables(start, n, rope_dim, base, None if ff is None else _p(ff), linear_factor, _p(c), _p(s))
+    return c, s
+
+
+def rmsnorm(x, g, rows: int, cols: int, eps: float) -> np.ndarray:
+    """ferrum_ref/src/models/llama/ops.rs:55-66"""
+    x, g = _f32(x), _f32(g)
+    y = np.empty(rows * cols, np.float32)
+    lib().fo_rmsnorm(_p(x), _p(g), rows, cols, eps, _p(y))
+    return y
+
+
+def apply_rope(x, rows: int, heads: int, hd: int, rope_dim: int, cos, sin, neox: bool) -> np.ndarray:
+    """ferrum_ref/src/models/llama/ops.rs:105-127 (returns a rotated copy)."""
+    y = _f32(x).copy()
+    c, s = _f32(cos), _f32(sin)
+    lib().fo_apply_rope(_p(y), rows, heads, hd, rope_dim, _p(c), _p(s), int(bool(neox)))
+    return y
+
+
+def attend_row(q, k, v, length: int, heads: int, kv_heads: int, hd: int) -> np.ndarray:
+    """ferrum_ref/src/models/llama/ops.rs:131-162"""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    out = np.empty(heads * hd, np.float32)
+    scratch = np.empty(max(length, 1), np.float32)
+    lib().fo_attend_row(_p(q), _p(k), _p(v), length, heads, kv_heads, hd, _p(scratch), _p(out))
+    return out
+
+
+def silu(x: float) -> float:
+    """ferrum_ref/src/models/llama/ops.rs:69-71"""
+    return lib().fo_silu(x)
+
+
+def swiglu(gate, up) -> np.ndarray:
+    """ferrum_ref/src/models/llama/ops.rs:74-76"""
+    g, u = _f32(gate), _f32(up)
+    out = np.empty(g.size, np.float32)
+    lib().fo_swiglu(_p(g), _p(u), g.size, _p(out))
+    return out
+
+
+def score(logits, targets, vocab: int):
+    """ferrum_ref/src/kernels/nn.rs:117-129: per row (log-probability of the target, whether the
+    target is the first maximum), as two arrays."""
+    lg = _f32(logits)
+    tg = np.ascontiguousarray(targets, dtype=np.uint64)
+    rows = tg.size
+    assert lg.size == rows * vocab
+    lp = np.empty(rows, np.float32)
+    hit = np.empty(rows, np.uint8)
+    lib().fo_score(_p(lg), _p(tg), rows, vocab, _p(lp), _p(hit))
+    return lp, hit.astype(bool)
+
+
+class _Llama(ctypes.Structure):
+    _fields_ = [
+        ("vocab", ctypes.c_size_t), ("ctx", ctypes.c_size_t), ("dim", ctypes.c_size_t),
+        ("heads", ctypes.c_size_t), ("kv_heads", ctypes.c_size_t), ("head_dim", ctypes.c_size_t),
+        ("layers", ctypes.c_size_t), ("hidden", ctypes.c_size_t), ("rope_dim", ctypes.c_size_t),
+        ("rope_base", ctypes.c_float), ("eps", ctypes.c_float), ("neox", ctypes.c_int),
+        ("freq_factors", ctypes.c_void_p), ("linear_factor", ctypes.c_float),
+        ("tok", ctypes.c_void_p), ("blocks", ctypes.c_void_p), ("out_norm", ctypes.c_void_p),
+        ("head", ctypes.c_void_p),
+    ]
+
+
+def _llama_struct(m: dict, keep: list):
+    def ptr(a):
+        if a is None or len(a) == 0:
+            return None
+        a = _f32(a)
+        keep.append(a)
+        return a.ctypes.data
+
+    n = len(LLAMA_BLOCK_NAMES)
+    blocks = (ctypes.c_void_p * (m["layers"] * n))()
+    keep.append(blocks)
+    for l, blk in enumerate(m["blocks"]):
+        for i, name in enumerate(LLAMA_BLOCK_NAMES):
+            blocks[l * n + i] = ptr(blk[name])
+    g = _Llama(m["vocab"], m["ctx"], m["dim"], m["heads"], m["kv_heads"], m["head_dim"], m["layers"],
+               m["hidden"], m["rope_dim"], m["rope_base"], m["eps"], int(bool(m["neox"])),
+               ptr(m.get("freq_factors")), m.get("linear_factor", 1.0), ptr(m["tok"]),
+               ctypes.cast(blocks, ctypes.c_void_p), ptr(m["out_norm"]), ptr(m["head"]))
+    keep.append(g)
+    return g
+
+
+def llama_forward(m: dict, ids, threads: int = 1) -> np.ndarray:
+    """Llama::forward_logits (ferrum_ref/src/models/llama/mod.rs:166-175,202-259): every
+    position's logits, [len(ids), vocab]; bit-identical for any thread count."""
+    keep = []
+    g = _llama_struct(m, keep)
+    ids = np.ascontiguousarray(ids, dtype=np.uint64)
+    out = np.empty(max(ids.size, 1) * m["vocab"], np.float32)
+    rc = lib().fo_llama_forward(ctypes.byref(g), _p(ids), ids.size, threads, _p(out))
+    if rc == -1:
+        raise ValueError(f"sequence length {ids.size} must be in 1..={m['ctx']} with tokens below {m['vocab']}")
+    if rc != 0:
+        raise MemoryError("llama forward: out of memory")
+    return out[: ids.size * m["vocab"]].reshape(ids.size, m["vocab"])
+
+
+def llama_score(m: dict, ids, threads: int = 1):
+    """GpuLlama::score's oracle (ferrum_wgpu/src/models/llama/forward.rs:76-88 over
+    forward_logits and nn::score): for each i < len - 1, the log-probability of ids[i + 1] after
+    ids[..=i] and whether it is the first argmax."""
+    if len(ids) < 2:
+        raise ValueError("scoring needs at least 2 tokens")
+    logits = llama_forward(m, ids[:-1], threads)
+    return score(logits, ids[1:], m["vocab"])
