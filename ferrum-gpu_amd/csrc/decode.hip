@@ -665,51 +665,6 @@ fh_status run_step(fh_gpt2 *m) {
     return end_command(dev, "gpt2 step");
 }
 
-std::string tname(const char *base, size_t layer, const char *suffix) {
-    return std::string(base) + std::to_string(layer) + "." + suffix;
-}
-
-// A GGUF vector of `len` floats on the device.
-fh_status vec(fh_device *dev, const fh_gguf *g, const std::string &name, size_t len, fh_buffer **out) {
-    size_t idx;
-    fh_status st = fh_gguf_find_tensor(g, name.c_str(), &idx);
-    if (st) return st;
-    fh_gguf_tensor t;
-    if ((st = fh_gguf_tensor_info(g, idx, &t))) return st;
-    if (t.elements != len || t.ggml_type != FH_GGML_F32)
-        return fail(FH_ERR_INVALID, "gpt2: tensor '%s' must be %zu F32 values (has %llu of ggml type %u)", name.c_str(),
-                    len, (unsigned long long)t.elements, t.ggml_type);
-    return fh_gguf_upload_f32(dev, g, name.c_str(), out);
-}
-
-// A GGUF matrix of k inputs and n outputs (GGML dims [k, n]) as a resident weight.
-fh_status mat(fh_device *dev, const fh_gguf *g, const std::string &name, size_t k, size_t n, fh_kind *kind,
-              fh_qweight **out) {
-    size_t idx;
-    fh_status st = fh_gguf_find_tensor(g, name.c_str(), &idx);
-    if (st) return st;
-    fh_gguf_tensor t;
-    if ((st = fh_gguf_tensor_info(g, idx, &t))) return st;
-    if (t.n_dims != 2 || t.dims[0] != k || t.dims[1] != n)
-        return fail(FH_ERR_INVALID, "gpt2: tensor '%s' must have dims [%zu, %zu]", name.c_str(), k, n);
-    if (t.ggml_type != FH_GGML_Q8_0 && t.ggml_type != FH_GGML_Q4_0)
-        return fail(FH_ERR_UNSUPPORTED, "gpt2: tensor '%s' has ggml type %u; the decoder multiplies Q8_0 or Q4_0 matrices",
-                    name.c_str(), t.ggml_type);
-    if (*kind == (fh_kind)0) *kind = (fh_kind)t.ggml_type;
-    if ((fh_kind)t.ggml_type != *kind)
-        return fail(FH_ERR_UNSUPPORTED, "gpt2: tensor '%s' mixes block formats (the model's matrices must share one)",
-                    name.c_str());
-    return fh_gguf_upload_qweight(dev, g, name.c_str(), out);
-}
-
-fh_status cfg_uint(const fh_gguf *g, const char *key, size_t *out) {
-    uint64_t v;
-    fh_status st = fh_gguf_get_uint(g, key, &v);
-    if (st) return st;
-    *out = (size_t)v;
-    return FH_OK;
-}
-
 }  // namespace
 
 extern "C" {
@@ -758,31 +713,31 @@ fh_status fh_gpt2_from_gguf(fh_device *dev, const fh_gguf *g, fh_gpt2 **out) {
                                       "64, 128 or 256 wide, ctx up to 16384)",
                                       d, h, hd, m->ctx));
     fh_kind kind = (fh_kind)0;
-    if ((st = mat(dev, g, "token_embd.weight", d, m->vocab, &kind, &m->tok))) return gpt2_fail_free(m, st);
+    if ((st = load_mat(dev, g, "gpt2", "token_embd.weight", d, m->vocab, &kind, &m->tok))) return gpt2_fail_free(m, st);
     if (fh_gguf_find_tensor(g, "output.weight", &tidx) == FH_OK) {
-        if ((st = mat(dev, g, "output.weight", d, m->vocab, &kind, &m->head))) return gpt2_fail_free(m, st);
+        if ((st = load_mat(dev, g, "gpt2", "output.weight", d, m->vocab, &kind, &m->head))) return gpt2_fail_free(m, st);
     } else {
         m->head = m->tok;  // tied (ferrum_model/src/gguf/gpt2.rs:228-231 omits a tied head)
     }
     m->kind = kind;
-    if ((st = vec(dev, g, "position_embd.weight", m->ctx * d, &m->pos_tab)) ||
-        (st = vec(dev, g, "output_norm.weight", d, &m->lnf_g)) || (st = vec(dev, g, "output_norm.bias", d, &m->lnf_b)))
+    if ((st = load_vec(dev, g, "gpt2", "position_embd.weight", m->ctx * d, &m->pos_tab)) ||
+        (st = load_vec(dev, g, "gpt2", "output_norm.weight", d, &m->lnf_g)) || (st = load_vec(dev, g, "gpt2", "output_norm.bias", d, &m->lnf_b)))
         return gpt2_fail_free(m, st);
     m->blocks.resize(m->layers);
     for (size_t l = 0; l < m->layers; l++) {
         auto &L = m->blocks[l];
-        if ((st = vec(dev, g, tname("blk.", l, "attn_norm.weight"), d, &L.ln1_g)) ||
-            (st = vec(dev, g, tname("blk.", l, "attn_norm.bias"), d, &L.ln1_b)) ||
-            (st = mat(dev, g, tname("blk.", l, "attn_qkv.weight"), d, 3 * d, &kind, &L.wqkv)) ||
-            (st = vec(dev, g, tname("blk.", l, "attn_qkv.bias"), 3 * d, &L.bqkv)) ||
-            (st = mat(dev, g, tname("blk.", l, "attn_output.weight"), d, d, &kind, &L.wo)) ||
-            (st = vec(dev, g, tname("blk.", l, "attn_output.bias"), d, &L.bo)) ||
-            (st = vec(dev, g, tname("blk.", l, "ffn_norm.weight"), d, &L.ln2_g)) ||
-            (st = vec(dev, g, tname("blk.", l, "ffn_norm.bias"), d, &L.ln2_b)) ||
-            (st = mat(dev, g, tname("blk.", l, "ffn_up.weight"), d, h, &kind, &L.w1)) ||
-            (st = vec(dev, g, tname("blk.", l, "ffn_up.bias"), h, &L.b1)) ||
-            (st = mat(dev, g, tname("blk.", l, "ffn_down.weight"), h, d, &kind, &L.w2)) ||
-            (st = vec(dev, g, tname("blk.", l, "ffn_down.bias"), d, &L.b2)))
+        if ((st = load_vec(dev, g, "gpt2", tensor_name("blk.", l, "attn_norm.weight"), d, &L.ln1_g)) ||
+            (st = load_vec(dev, g, "gpt2", tensor_name("blk.", l, "attn_norm.bias"), d, &L.ln1_b)) ||
+            (st = load_mat(dev, g, "gpt2", tensor_name("blk.", l, "attn_qkv.weight"), d, 3 * d, &kind, &L.wqkv)) ||
+            (st = load_vec(dev, g, "gpt2", tensor_name("blk.", l, "attn_qkv.bias"), 3 * d, &L.bqkv)) ||
+            (st = load_mat(dev, g, "gpt2", tensor_name("blk.", l, "attn_output.weight"), d, d, &kind, &L.wo)) ||
+            (st = load_vec(dev, g, "gpt2", tensor_name("blk.", l, "attn_output.bias"), d, &L.bo)) ||
+            (st = load_vec(dev, g, "gpt2", tensor_name("blk.", l, "ffn_norm.weight"), d, &L.ln2_g)) ||
+            (st = load_vec(dev, g, "gpt2", tensor_name("blk.", l, "ffn_norm.bias"), d, &L.ln2_b)) ||
+            (st = load_mat(dev, g, "gpt2", tensor_name("blk.", l, "ffn_up.weight"), d, h, &kind, &L.w1)) ||
+            (st = load_vec(dev, g, "gpt2", tensor_name("blk.", l, "ffn_up.bias"), h, &L.b1)) ||
+            (st = load_mat(dev, g, "gpt2", tensor_name("blk.", l, "ffn_down.weight"), h, d, &kind, &L.w2)) ||
+            (st = load_vec(dev, g, "gpt2", tensor_name("blk.", l, "ffn_down.bias"), d, &L.b2)))
             return gpt2_fail_free(m, st);
         m->step_bytes += L.wqkv->nbytes + L.wo->nbytes + L.w1->nbytes + L.w2->nbytes;
     }

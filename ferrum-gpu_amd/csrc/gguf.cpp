@@ -577,3 +577,99 @@ fh_status fh_gguf_upload_f32(fh_device *dev, const fh_gguf *g, const char *name,
 }
 
 }  // extern "C"
+
+// ---- model-loading helpers shared by the GPT-2 and Llama loaders ----
+namespace fh {
+
+std::string tensor_name(const char *base, size_t layer, const char *suffix) {
+    return std::string(base) + std::to_string(layer) + "." + suffix;
+}
+
+fh_status cfg_uint(const fh_gguf *g, const char *key, size_t *out) {
+    uint64_t v;
+    fh_status st = fh_gguf_get_uint(g, key, &v);
+    if (st) return st;
+    *out = (size_t)v;
+    return FH_OK;
+}
+
+fh_status host_vec(const fh_gguf *g, const char *who, const std::string &name, size_t len, std::vector<float> *out) {
+    const Tensor *t;
+    fh_status st = lookup(g, name.c_str(), &t);
+    if (st) return st;
+    if (t->elements != len || t->type != FH_GGML_F32)
+        return fail(FH_ERR_INVALID, "%s: tensor '%s' must be %zu F32 values (has %llu of ggml type %u)", who,
+                    name.c_str(), len, (unsigned long long)t->elements, t->type);
+    const uint8_t *data;
+    size_t n;
+    if ((st = span_of(g, name.c_str(), t, &data, &n))) return st;
+    try {
+        out->resize(len);
+    } catch (const std::bad_alloc &) {
+        return fail(FH_ERR_OOM, "host out of memory");
+    }
+    if (len) memcpy(out->data(), data, len * 4);  // the file's alignment may leave it unaligned
+    return FH_OK;
+}
+
+fh_status load_vec(fh_device *dev, const fh_gguf *g, const char *who, const std::string &name, size_t len,
+                   fh_buffer **out) {
+    std::vector<float> v;
+    fh_status st = host_vec(g, who, name, len, &v);
+    if (st) return st;
+    return fh_buffer_upload(dev, v.data(), len, out);
+}
+
+// The stored rows of a Q8_0/Q4_0 matrix of k inputs and n outputs (GGML dims [k, n]), checked
+// against the model's one block format.
+static fh_status mat_rows(const fh_gguf *g, const char *who, const std::string &name, size_t k, size_t n,
+                          fh_kind *kind, const uint8_t **data, size_t *len) {
+    const Tensor *t;
+    fh_status st = lookup(g, name.c_str(), &t);
+    if (st) return st;
+    if (t->nd != 2 || t->dims[0] != k || t->dims[1] != n)
+        return fail(FH_ERR_INVALID, "%s: tensor '%s' must have dims [%zu, %zu]", who, name.c_str(), k, n);
+    if (t->type != FH_GGML_Q8_0 && t->type != FH_GGML_Q4_0)
+        return fail(FH_ERR_UNSUPPORTED, "%s: tensor '%s' has ggml type %u; the model's matrices must be Q8_0 or Q4_0",
+                    who, name.c_str(), t->type);
+    if (*kind == (fh_kind)0) *kind = (fh_kind)t->type;
+    if ((fh_kind)t->type != *kind)
+        return fail(FH_ERR_UNSUPPORTED, "%s: tensor '%s' mixes block formats (the model's matrices must share one)",
+                    who, name.c_str());
+    return span_of(g, name.c_str(), t, data, len);
+}
+
+fh_status load_mat(fh_device *dev, const fh_gguf *g, const char *who, const std::string &name, size_t k, size_t n,
+                   fh_kind *kind, fh_qweight **out) {
+    const uint8_t *data;
+    size_t len;
+    fh_status st = mat_rows(g, who, name, k, n, kind, &data, &len);
+    if (st) return st;
+    return fh_qweight_upload_gguf(dev, *kind, data, len, k, n, out);
+}
+
+fh_status load_mat_rows(fh_device *dev, const fh_gguf *g, const char *who, const std::string *names,
+                        const size_t *ns, size_t count, size_t k, fh_kind *kind, fh_qweight **out) {
+    std::vector<std::pair<const uint8_t *, size_t>> parts(count);
+    size_t total = 0, rows = 0;
+    for (size_t i = 0; i < count; i++) {
+        fh_status st = mat_rows(g, who, names[i], k, ns[i], kind, &parts[i].first, &parts[i].second);
+        if (st) return st;
+        total += parts[i].second;
+        rows += ns[i];
+    }
+    std::vector<uint8_t> joined;
+    try {
+        joined.resize(total);
+    } catch (const std::bad_alloc &) {
+        return fail(FH_ERR_OOM, "host out of memory");
+    }
+    size_t at = 0;
+    for (auto &p : parts) {
+        memcpy(joined.data() + at, p.first, p.second);
+        at += p.second;
+    }
+    return fh_qweight_upload_gguf(dev, *kind, joined.data(), total, k, rows, out);
+}
+
+}  // namespace fh

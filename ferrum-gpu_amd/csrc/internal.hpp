@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/ferrum_hip.h"
 
@@ -96,6 +97,22 @@ fh_status workspace(fh_device *dev, size_t bytes, void **out);
 // Reference counting of devices (see struct fh_device).
 void dev_retain(fh_device *dev);
 void dev_release(fh_device *dev);  // destroys the stream and the device on the last release
+
+// ---- model loading from GGUF (gguf.cpp); `who` prefixes the error messages ----
+std::string tensor_name(const char *base, size_t layer, const char *suffix);
+fh_status cfg_uint(const fh_gguf *g, const char *key, size_t *out);
+// An F32 vector of exactly `len` values, copied out of the file's bytes.
+fh_status host_vec(const fh_gguf *g, const char *who, const std::string &name, size_t len, std::vector<float> *out);
+fh_status load_vec(fh_device *dev, const fh_gguf *g, const char *who, const std::string &name, size_t len,
+                   fh_buffer **out);
+// A Q8_0/Q4_0 matrix of GGML dims [k, n] as a resident weight; *kind is the model's one block
+// format (0: taken from this tensor).
+fh_status load_mat(fh_device *dev, const fh_gguf *g, const char *who, const std::string &name, size_t k, size_t n,
+                   fh_kind *kind, fh_qweight **out);
+// Several matrices of k inputs stacked into one weight: the rows of names[0] (ns[0] of them),
+// then those of names[1], ... (a fused projection).
+fh_status load_mat_rows(fh_device *dev, const fh_gguf *g, const char *who, const std::string *names,
+                        const size_t *ns, size_t count, size_t k, fh_kind *kind, fh_qweight **out);
 
 // ---- kernel launchers (on dev->stream; a command may issue several) ----
 // codec.hip

@@ -1,0 +1,808 @@
+// Llama / Qwen2 full-sequence forward and scoring on resident Q8_0 / Q4_0 weights.
+//
+// Replaces the batched passes of ferrum_wgpu's GpuLlama (ferrum_wgpu/src/models/llama/
+// forward.rs:13-88: forward_all and score over the ops of ops/llama.rs), whose CPU oracle is
+// ferrum_ref's Llama::forward_logits (ferrum_ref/src/models/llama/mod.rs:166-259) and
+// nn::score (ferrum_ref/src/kernels/nn.rs:117-129). The model comes from a `llama` or `qwen2`
+// GGUF as ferrum_model writes and reads it (ferrum_model/src/gguf/llama/mod.rs:107-323).
+//
+// One forward over t rows, all on the device stream, every activation row-major f32:
+//   embed (rows of the packed token_embd)                       -> x [t, d]
+//   per block: RMSNorm (fused with the previous residual add)   -> h
+//              h . [Wq; Wk; Wv] (one stacked weight)             -> qkv [t, qd + 2 kvd]
+//              bias + RoPE in place (host-built tables)
+//              causal GQA attention (f32 MFMA, online softmax)   -> att [t, qd]
+//              att . Wo                                         -> o
+//              x += o, RMSNorm                                   -> h
+//              h . [Wgate; Wup] (one stacked weight)             -> gu [t, 2 hidden]
+//              SwiGLU                                           -> act [t, hidden]
+//              act . Wdown                                      -> o
+//   x += o, final RMSNorm, h . head (chunks of rows)            -> logits, or straight into score
+// The products are the library's MFMA GEMMs on the packed weights: the precise one (x as two
+// f16 parts, FH_PATH_TILED) or the fast scoring one (FH_PATH_TILED_FAST), chosen at load.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "device_common.hpp"
+#include "internal.hpp"
+
+using namespace fh;
+
+struct fh_llama {
+    fh_device *dev = nullptr;
+    size_t vocab = 0, ctx = 0, dim = 0, heads = 0, kv_heads = 0, head_dim = 0, layers = 0, hidden = 0, rope_dim = 0;
+    float rope_base = 10000.0f, eps = 1e-5f, linear_factor = 1.0f;
+    bool neox = false, tied = false;
+    fh_kind kind = (fh_kind)0;
+    fh_path path = FH_PATH_TILED;
+    struct Layer {
+        fh_buffer *attn_norm = nullptr, *ffn_norm = nullptr, *bqkv = nullptr;
+        fh_qweight *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *down = nullptr;
+    };
+    std::vector<Layer> blocks;
+    fh_qweight *tok = nullptr, *head = nullptr;  // head == tok when tied
+    fh_buffer *out_norm = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
+    uint64_t weight_bytes = 0;
+    // Activations for up to `rows` rows, grown on demand and kept.
+    void *arena = nullptr;
+    size_t rows = 0, chunk = 0;  // chunk: rows of logits the arena holds
+    float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *o = nullptr, *gu = nullptr, *act = nullptr,
+          *logits = nullptr, *scores = nullptr;
+    int32_t *ids = nullptr;
+    void *ws = nullptr;
+
+    size_t q_dim() const { return heads * head_dim; }
+    size_t kv_dim() const { return kv_heads * head_dim; }
+    size_t qkv_width() const { return q_dim() + 2 * kv_dim(); }
+};
+
+namespace {
+
+constexpr uint32_t kMaxQkvWidth = 12288;  // floats of one qkv row the RoPE kernel stages in LDS (48 KiB)
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// ---- kernels ----
+
+// Row r of x = the token embedding of ids[r], dequantised from the packed rows. An id outside
+// the vocabulary reads row 0 and poisons the row with NaN (the host entry points refuse such ids
+// before launching; the device-resident one documents it).
+template <fh_kind KIND>
+__global__ __launch_bounds__(256) void embed_rows_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ ds,
+                                                         const int32_t *__restrict__ ids, float *__restrict__ x, uint32_t d,
+                                                         uint32_t vocab) {
+    const uint32_t r = blockIdx.x;
+    const int32_t id = ids[r];
+    const bool ok = id >= 0 && (uint32_t)id < vocab;
+    const uint32_t t = ok ? (uint32_t)id : 0u;
+    const uint32_t nb = d / 32;
+    for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) {
+        const uint32_t b = i / 32, j = i % 32;
+        const size_t slot = tile_slot(t, b, nb);
+        float q;
+        if constexpr (KIND == FH_Q8_0) {
+            q = (float)(int8_t)qs[slot * 32 + j];
+        } else {
+            const uint32_t byte = qs[slot * 16 + (j % 16)];
+            q = (float)((int32_t)(j < 16 ? byte & 15u : byte >> 4) - 8);
+        }
+        x[(size_t)r * d + i] = ok ? half_bits_to_float(ds[scale_slot(t, b, nb)]) * q : NAN;
+    }
+}
+
+// Sum over a block of 256 threads (four wavefronts); every thread gets the total.
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+    const uint32_t w = threadIdx.x >> 6;
+    __syncthreads();  // red may still be read by a previous call
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// RMSNorm per row (ferrum_ref/src/models/llama/ops.rs:55-66): h = v / sqrt(mean(v^2) + eps) * g,
+// v = x, or with ADD v = x + o stored back into x first (the residual add, nn::add).
+template <bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(float *__restrict__ x, const float *__restrict__ o,
+                                                      const float *__restrict__ g, float *__restrict__ h, uint32_t d,
+                                                      float eps) {
+    __shared__ float red[4];
+    const size_t base = (size_t)blockIdx.x * d;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < d; i += 256) {
+        float v = x[base + i];
+        if constexpr (ADD) {
+            v = v + o[base + i];
+            x[base + i] = v;
+        }
+        ss += v * v;
+    }
+    const float ms = block_sum_256(ss, red) / (float)d;
+    const float inv = 1.0f / sqrtf(ms + eps);
+    for (uint32_t i = threadIdx.x; i < d; i += 256) h[base + i] = __fmul_rn(__fmul_rn(x[base + i], inv), g[i]);
+}
+
+// q/k/v bias and RoPE in place on one row of qkv (ferrum_ref/src/models/llama/ops.rs:105-127):
+// the row's q and k heads rotate their first rope_dim channels by table row `row` (the position),
+// NORM pairing (2i, 2i + 1) or NEOX (i, i + rope_dim / 2). The row is staged in LDS so every
+// output reads the biased inputs.
+__global__ __launch_bounds__(256) void qkv_rope_kernel(float *__restrict__ qkv, const float *__restrict__ bias,
+                                                       const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+                                                       uint32_t width, uint32_t rot_heads, uint32_t hd, uint32_t rope_dim,
+                                                       int neox) {
+    extern __shared__ float row[];
+    const size_t base = (size_t)blockIdx.x * width;
+    for (uint32_t c = threadIdx.x; c < width; c += 256) row[c] = bias ? qkv[base + c] + bias[c] : qkv[base + c];
+    __syncthreads();
+    const uint32_t half = rope_dim / 2, rotated = rot_heads * hd;
+    const float *cr = cos_t + (size_t)blockIdx.x * half, *sr = sin_t + (size_t)blockIdx.x * half;
+    for (uint32_t c = threadIdx.x; c < width; c += 256) {
+        float v = row[c];
+        if (c < rotated) {
+            const uint32_t j = c % hd, off = c - j;
+            if (j < rope_dim) {
+                const bool first = neox ? j < half : (j & 1u) == 0;
+                const uint32_t i = neox ? (first ? j : j - half) : j / 2;
+                const uint32_t ia = neox ? off + i : off + 2 * i, ib = neox ? ia + half : ia + 1;
+                const float a = row[ia], b = row[ib], cs = cr[i], sn = sr[i];
+                v = first ? __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn)) : __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs));
+            }
+        }
+        qkv[base + c] = v;
+    }
+}
+
+// Causal grouped-query attention (ferrum_ref/src/models/llama/ops.rs:131-162 for every row) from
+// qkv [t, width] (the q heads, then the k heads, then the v heads, each HD wide) into att
+// [t, heads * HD]. One wavefront takes 32 query rows of one head and walks the key rows in tiles
+// of 32 with an online softmax; both products run on v_mfma_f32_32x32x2_f32 in f32:
+//   S^T (32 keys x 32 queries) = K . Q^T: lane l (key or query l % 32, slot l / 32) feeds dims
+//     8m + 4 slot + c at step 4m + c, so K and Q load as float4;
+//   O^T (32 dims x 32 queries) += V^T . P^T: at step s the B operand is the S^T accumulator's
+//     register s (key 8 (s / 4) + 4 slot + s % 4 of query l % 32) and the A operand that key's
+//     value at dim l % 32, a coalesced row segment.
+// Each lane owns one query (l % 32) throughout: lanes l and l ^ 32 share its running maximum and
+// split its running sum, added at the end.
+template <int HD>
+__global__ __launch_bounds__(64) void attention_kernel(const float *__restrict__ qkv, float *__restrict__ att, uint32_t t,
+                                                       uint32_t width, uint32_t heads, uint32_t group, float scale) {
+    constexpr int M4 = HD / 8;                  // float4 pairs per row
+    constexpr int DB = HD >= 32 ? HD / 32 : 1;  // 32-dim blocks of the output
+    const uint32_t lane = threadIdx.x, col = lane & 31u, slot = lane >> 5;
+    const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * 32;  // the longest tiles start first
+    const uint32_t h = blockIdx.y, g = h / group, kv_heads = heads / group;
+    const uint32_t qd = heads * HD;
+    const uint32_t kofs = qd + g * HD, vofs = qd + kv_heads * HD + g * HD;
+    const uint32_t query = q0 + col;
+    f32x4 qf[M4];
+    {
+        const bool ok = query < t;
+        const float *qrow = qkv + (size_t)(ok ? query : 0u) * width + h * HD + 4 * slot;
+#pragma unroll
+        for (int m = 0; m < M4; m++) qf[m] = ok ? *(const f32x4 *)(qrow + 8 * m) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    f32x16 o[DB];
+#pragma unroll
+    for (int b = 0; b < DB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[b][i] = 0.0f;
+    float mrun = -INFINITY, lrun = 0.0f;
+    const uint32_t last = min(q0 + 31u, t - 1u);
+    for (uint32_t k0 = 0; k0 <= last; k0 += 32) {
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; i++) s[i] = 0.0f;
+        {
+            const uint32_t key = k0 + col;
+            const bool ok = key < t;
+            const float *krow = qkv + (size_t)(ok ? key : 0u) * width + kofs + 4 * slot;
+#pragma unroll
+            for (int m = 0; m < M4; m++) {
+                const f32x4 kf = ok ? *(const f32x4 *)(krow + 8 * m) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[c], qf[m][c], s, 0, 0, 0);
+            }
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t key = k0 + 8 * (i / 4) + 4 * slot + (i % 4);
+            const float v = key <= query ? s[i] * scale : -INFINITY;
+            s[i] = v;
+            mt = fmaxf(mt, v);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mnew = fmaxf(mrun, mt);  // finite: key k0 <= query in every tile
+        const float alpha = __expf(mrun - mnew);
+        float ls = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            s[i] = __expf(s[i] - mnew);
+            ls += s[i];
+        }
+        lrun = lrun * alpha + ls;
+        mrun = mnew;
+#pragma unroll
+        for (int b = 0; b < DB; b++) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[b][i] *= alpha;
+            const uint32_t dim = 32 * b + col;
+            const bool dok = dim < (uint32_t)HD;
+#pragma unroll
+            for (int st = 0; st < 16; st++) {
+                const uint32_t key = k0 + 8 * (st / 4) + 4 * slot + (st % 4);
+                const float v = dok && key < t ? qkv[(size_t)key * width + vofs + dim] : 0.0f;
+                o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(v, s[st], o[b], 0, 0, 0);
+            }
+        }
+    }
+    const float inv = 1.0f / (lrun + __shfl_xor(lrun, 32));
+    if (query >= t) return;
+    float *out = att + (size_t)query * qd + h * HD;
+#pragma unroll
+    for (int b = 0; b < DB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t dim = 32 * b + 8 * (i / 4) + 4 * slot + (i % 4);
+            if (dim < (uint32_t)HD) out[dim] = o[b][i] * inv;
+        }
+}
+
+// SwiGLU (ferrum_ref/src/models/llama/ops.rs:69-76): act[r][j] = silu(gu[r][j]) * gu[r][hid + j].
+__global__ __launch_bounds__(256) void swiglu_kernel(const float *__restrict__ gu, float *__restrict__ act, uint32_t rows,
+                                                     uint32_t hid) {
+    const uint32_t q = hid / 4;
+    const size_t n = (size_t)rows * q;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const size_t r = i / q, j = i % q;
+        const f32x4 g = *(const f32x4 *)(gu + r * 2 * hid + 4 * j);
+        const f32x4 u = *(const f32x4 *)(gu + r * 2 * hid + hid + 4 * j);
+        f32x4 y;
+#pragma unroll
+        for (int c = 0; c < 4; c++) y[c] = __fmul_rn(g[c] / (1.0f + expf(-g[c])), u[c]);
+        *(f32x4 *)(act + r * hid + 4 * j) = y;
+    }
+}
+
+// Per row (nn::score, ferrum_ref/src/kernels/nn.rs:117-129): out[2r] = logits[r][t] - max -
+// ln(sum exp(logits[r] - max)), out[2r + 1] = 1 when t is the first maximum, else 0; t =
+// targets[r]. One pass with a running maximum; a target outside the vocabulary gives NaN.
+__global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ logits, const int32_t *__restrict__ targets,
+                                                    float *__restrict__ out, uint32_t vocab) {
+    __shared__ float sm[4], ss[4];
+    __shared__ uint32_t sf[4];
+    const float *x = logits + (size_t)blockIdx.x * vocab;
+    float m = -INFINITY, s = 0.0f;
+    uint32_t first = 0xffffffffu;
+    for (uint32_t j = threadIdx.x; j < vocab; j += 256) {
+        const float v = x[j];
+        if (v == -INFINITY) continue;  // adds nothing (and would make exp(-inf + inf))
+        if (v > m) {
+            s = s * expf(m - v) + 1.0f;
+            m = v;
+            first = j;
+        } else {
+            s += expf(v - m);
+        }
+    }
+    for (int o = 32; o; o >>= 1) {
+        const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+        const uint32_t f2 = __shfl_xor(first, o);
+        const float mx = fmaxf(m, m2);
+        s = (m == -INFINITY ? 0.0f : s * expf(m - mx)) + (m2 == -INFINITY ? 0.0f : s2 * expf(m2 - mx));
+        first = m2 > m || (m2 == m && f2 < first) ? f2 : first;
+        m = mx;
+    }
+    const uint32_t w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sm[w] = m;
+        ss[w] = s;
+        sf[w] = first;
+    }
+    __syncthreads();
+    if (threadIdx.x) return;
+    float M = sm[0], S = ss[0];
+    uint32_t F = sf[0];
+    for (int i = 1; i < 4; i++) {
+        const float mx = fmaxf(M, sm[i]);
+        S = (M == -INFINITY ? 0.0f : S * expf(M - mx)) + (sm[i] == -INFINITY ? 0.0f : ss[i] * expf(sm[i] - mx));
+        F = sm[i] > M || (sm[i] == M && sf[i] < F) ? sf[i] : F;
+        M = mx;
+    }
+    const int32_t t = targets[blockIdx.x];
+    const bool ok = t >= 0 && (uint32_t)t < vocab;
+    out[2 * (size_t)blockIdx.x] = ok ? x[t] - M - logf(S) : NAN;
+    out[2 * (size_t)blockIdx.x + 1] = ok && F == (uint32_t)t ? 1.0f : 0.0f;
+}
+
+// ---- host side ----
+
+fh_status llama_fail_free(fh_llama *m, fh_status st) {
+    fh_llama_free(m);
+    return st;
+}
+
+const float *fp(const fh_buffer *b) { return b ? (const float *)b->ptr : nullptr; }
+
+// RoPE scaling as the reference reads it (ferrum_model/src/gguf/llama/mod.rs:56-100): linear
+// (`rope.scaling.factor`, else `rope.scale_linear`), "none" only with factor 1, yarn and the rest
+// refused, attn_factor must be 1, per-frequency divisors from `rope_freqs.weight`.
+fh_status rope_scaling(const fh_gguf *g, const std::string &arch, size_t rope_dim, float *linear,
+                       std::vector<float> *freq) {
+    auto key = [&](const char *k) { return arch + ".rope." + k; };
+    auto opt_float = [&](const std::string &k, float *v, bool *has) -> fh_status {
+        size_t idx;
+        *has = fh_gguf_find_key(g, k.c_str(), &idx) == FH_OK;
+        return *has ? fh_gguf_get_float(g, k.c_str(), v) : FH_OK;
+    };
+    float factor = 0.0f;
+    bool has = false;
+    fh_status st = opt_float(key("scaling.factor"), &factor, &has);
+    if (st) return st;
+    if (!has && (st = opt_float(key("scale_linear"), &factor, &has))) return st;
+    if (!has || factor == 0.0f) factor = 1.0f;
+    std::string ty = "linear";
+    size_t idx;
+    if (fh_gguf_find_key(g, key("scaling.type").c_str(), &idx) == FH_OK) {
+        const char *s;
+        size_t n;
+        if ((st = fh_gguf_get_string(g, key("scaling.type").c_str(), &s, &n))) return st;
+        ty.assign(s, n);
+    }
+    if (ty == "none") {
+        if (factor != 1.0f)
+            return fail(FH_ERR_INVALID, "rope scaling type is \"none\" but the factor is %g", (double)factor);
+    } else if (ty != "linear") {
+        return fail(FH_ERR_INVALID, "rope scaling type '%s' is not supported (none, linear and rope_freqs.weight are)",
+                    ty.c_str());
+    }
+    *linear = ty == "linear" ? factor : 1.0f;
+    float attn = 1.0f;
+    if ((st = opt_float(key("scaling.attn_factor"), &attn, &has))) return st;
+    if (has && attn != 1.0f) return fail(FH_ERR_INVALID, "rope scaling attn_factor %g is not supported", (double)attn);
+    freq->clear();
+    if (fh_gguf_find_tensor(g, "rope_freqs.weight", &idx) == FH_OK) {
+        fh_gguf_tensor t;
+        if ((st = fh_gguf_tensor_info(g, idx, &t))) return st;
+        if (t.n_dims != 1 || t.dims[0] != rope_dim / 2)
+            return fail(FH_ERR_INVALID, "tensor 'rope_freqs.weight' has the wrong dims, expected [%zu] from the metadata",
+                        rope_dim / 2);
+        if ((st = host_vec(g, "llama", "rope_freqs.weight", rope_dim / 2, freq))) return st;
+    }
+    // RopeScaling::check (ferrum_ref/src/models/llama/ops.rs:38-52)
+    auto ok = [](float v) { return std::isfinite(v) && v > 0.0f; };
+    bool good = ok(*linear);
+    for (float v : *freq) good = good && ok(v);
+    if (!good) return fail(FH_ERR_INVALID, "RoPE scaling factors must be finite and > 0");
+    return FH_OK;
+}
+
+// rope_tables (ferrum_ref/src/models/llama/ops.rs:78-101) for positions 0 .. ctx - 1, built on
+// the host with the same f64 power and f32 sin/cos, so device and CPU share the exact angles.
+void rope_tables(size_t ctx, size_t rope_dim, float base, const std::vector<float> &ff, float linear,
+                 std::vector<float> *c, std::vector<float> *s) {
+    const size_t half = rope_dim / 2;
+    c->resize(ctx * half);
+    s->resize(ctx * half);
+    for (size_t p = 0; p < ctx; p++)
+        for (size_t i = 0; i < half; i++) {
+            const float freq = (float)std::pow((double)base, -2.0 * (double)i / (double)rope_dim);
+            const float f = ff.empty() ? 1.0f : ff[i];
+            const float theta = (float)p * freq / f * (1.0f / linear);
+            (*s)[p * half + i] = ::sinf(theta);
+            (*c)[p * half + i] = ::cosf(theta);
+        }
+}
+
+size_t up256(size_t b) { return (b + 255) / 256 * 256; }
+
+// Rows of logits per head product: as many as keep the logits under 2^31 bytes.
+size_t logit_chunk(const fh_llama *m, size_t t) {
+    const size_t lim = (((size_t)1 << 31) - 1) / (m->vocab * 4);
+    return std::max<size_t>(1, std::min(t, lim));
+}
+
+size_t linear_ws(const fh_llama *m, size_t rows, size_t k, size_t n) {
+    return m->path == FH_PATH_TILED_FAST ? gemm_workspace_bytes(rows, k, n) : gemm_precise_workspace_bytes(rows, k);
+}
+
+// The activations for t rows (kept when already large enough).
+fh_status ensure_rows(fh_llama *m, size_t t) {
+    if (t <= m->rows) return FH_OK;
+    const size_t d = m->dim, qd = m->q_dim(), w = m->qkv_width(), hid = m->hidden, chunk = logit_chunk(m, t);
+    size_t ws = 0;
+    for (auto kn : {std::pair<size_t, size_t>{d, w}, {qd, d}, {d, 2 * hid}, {hid, d}})
+        ws = std::max(ws, linear_ws(m, t, kn.first, kn.second));
+    ws = std::max(ws, linear_ws(m, chunk, d, m->vocab));
+    const size_t total = 3 * up256(t * d * 4) + up256(t * w * 4) + up256(t * qd * 4) + up256(t * 2 * hid * 4) +
+                         up256(t * hid * 4) + up256(chunk * m->vocab * 4) + up256(2 * t * 4) + up256((t + 1) * 4) +
+                         up256(ws);
+    void *p = nullptr;
+    fh_status st = alloc_bytes(m->dev, total, &p);
+    if (st) return st;
+    if (m->arena) {
+        (void)hipStreamSynchronize(m->dev->stream);
+        (void)hipFree(m->arena);
+    }
+    m->arena = p;
+    m->rows = t;
+    m->chunk = chunk;
+    uint8_t *q = (uint8_t *)p;
+    auto take = [&](size_t bytes) {
+        void *r = q;
+        q += up256(bytes);
+        return r;
+    };
+    m->x = (float *)take(t * d * 4);
+    m->h = (float *)take(t * d * 4);
+    m->o = (float *)take(t * d * 4);
+    m->qkv = (float *)take(t * w * 4);
+    m->att = (float *)take(t * qd * 4);
+    m->gu = (float *)take(t * 2 * hid * 4);
+    m->act = (float *)take(t * hid * 4);
+    m->logits = (float *)take(chunk * m->vocab * 4);
+    m->scores = (float *)take(2 * t * 4);
+    m->ids = (int32_t *)take((t + 1) * 4);
+    m->ws = take(ws);
+    return FH_OK;
+}
+
+fh_status check_shapes(const fh_llama *m, size_t t) {
+    if (m->path != FH_PATH_TILED_FAST) return FH_OK;
+    const size_t d = m->dim;
+    const std::pair<size_t, size_t> kn[] = {{d, m->qkv_width()}, {m->q_dim(), d}, {d, 2 * m->hidden}, {m->hidden, d}};
+    for (auto p : kn)
+        if (!gemm_supported(t, p.first, p.second))
+            return fail(FH_ERR_UNSUPPORTED, "llama: %zu rows exceed the MFMA GEMM's 32-bit offsets for a %zu x %zu weight",
+                        t, p.second, p.first);
+    if (!gemm_supported(logit_chunk(m, t), d, m->vocab))
+        return fail(FH_ERR_UNSUPPORTED, "llama: the head exceeds the MFMA GEMM's 32-bit offsets");
+    return FH_OK;
+}
+
+hipError_t linear(const fh_llama *m, hipStream_t s, const fh_qweight *w, const float *x, float *y, size_t rows) {
+    if (m->path == FH_PATH_TILED_FAST)
+        return launch_gemm(s, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, m->ws);
+    return launch_gemm_precise(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws);
+}
+
+hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t) {
+    const dim3 grid((unsigned)((t + 31) / 32), (unsigned)m->heads);
+    const uint32_t w = (uint32_t)m->qkv_width(), group = (uint32_t)(m->heads / m->kv_heads);
+    const float scale = 1.0f / sqrtf((float)m->head_dim);
+    switch (m->head_dim) {
+    case 8: attention_kernel<8><<<grid, 64, 0, s>>>(m->qkv, m->att, (uint32_t)t, w, (uint32_t)m->heads, group, scale); break;
+    case 16: attention_kernel<16><<<grid, 64, 0, s>>>(m->qkv, m->att, (uint32_t)t, w, (uint32_t)m->heads, group, scale); break;
+    case 32: attention_kernel<32><<<grid, 64, 0, s>>>(m->qkv, m->att, (uint32_t)t, w, (uint32_t)m->heads, group, scale); break;
+    case 64: attention_kernel<64><<<grid, 64, 0, s>>>(m->qkv, m->att, (uint32_t)t, w, (uint32_t)m->heads, group, scale); break;
+    default: attention_kernel<128><<<grid, 64, 0, s>>>(m->qkv, m->att, (uint32_t)t, w, (uint32_t)m->heads, group, scale); break;
+    }
+    return hipGetLastError();
+}
+
+// The forward over the t ids already in m->ids, up to the final norm's output in m->h.
+hipError_t enqueue_body(fh_llama *m, hipStream_t s, size_t t) {
+    const uint32_t d = (uint32_t)m->dim, T = (uint32_t)t;
+    if (m->kind == FH_Q8_0)
+        embed_rows_kernel<FH_Q8_0><<<T, 256, 0, s>>>(m->tok->qs, m->tok->ds, m->ids, m->x, d, (uint32_t)m->vocab);
+    else
+        embed_rows_kernel<FH_Q4_0><<<T, 256, 0, s>>>(m->tok->qs, m->tok->ds, m->ids, m->x, d, (uint32_t)m->vocab);
+    hipError_t e = hipGetLastError();
+    const uint32_t width = (uint32_t)m->qkv_width();
+    for (size_t l = 0; l < m->layers && !e; l++) {
+        const auto &L = m->blocks[l];
+        if (l == 0)
+            rmsnorm_kernel<false><<<T, 256, 0, s>>>(m->x, nullptr, fp(L.attn_norm), m->h, d, m->eps);
+        else
+            rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, m->o, fp(L.attn_norm), m->h, d, m->eps);
+        if ((e = linear(m, s, L.wqkv, m->h, m->qkv, t))) break;
+        qkv_rope_kernel<<<T, 256, width * 4, s>>>(m->qkv, fp(L.bqkv), fp(m->rope_cos), fp(m->rope_sin), width,
+                                                  (uint32_t)(m->heads + m->kv_heads), (uint32_t)m->head_dim,
+                                                  (uint32_t)m->rope_dim, m->neox ? 1 : 0);
+        if ((e = launch_attention(m, s, t))) break;
+        if ((e = linear(m, s, L.wo, m->att, m->o, t))) break;
+        rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, m->o, fp(L.ffn_norm), m->h, d, m->eps);
+        if ((e = linear(m, s, L.wgu, m->h, m->gu, t))) break;
+        const size_t quads = t * m->hidden / 4;
+        swiglu_kernel<<<(unsigned)std::min<size_t>((quads + 255) / 256, 65536), 256, 0, s>>>(m->gu, m->act, T,
+                                                                                           (uint32_t)m->hidden);
+        if ((e = linear(m, s, L.down, m->act, m->o, t))) break;
+        e = hipGetLastError();
+    }
+    if (e) return e;
+    rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, m->o, fp(m->out_norm), m->h, d, m->eps);
+    return hipGetLastError();
+}
+
+fh_status check_ids(const fh_llama *m, const int32_t *ids, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] < 0 || (size_t)ids[i] >= m->vocab)
+            return fail(FH_ERR_INVALID, "token %lld is out of range for vocab %zu", (long long)ids[i], m->vocab);
+    return FH_OK;
+}
+
+fh_status check_len(const fh_llama *m, size_t t) {
+    if (t == 0 || t > m->ctx) return fail(FH_ERR_INVALID, "sequence length %zu must be in 1..=%zu", t, m->ctx);
+    return check_shapes(m, t);
+}
+
+// The score pass over t rows whose ids (t + 1 of them, the targets being ids[1..]) are in m->ids;
+// out receives 2 t floats on the device.
+hipError_t enqueue_score(fh_llama *m, hipStream_t s, size_t t, float *out) {
+    hipError_t e = enqueue_body(m, s, t);
+    for (size_t r0 = 0; r0 < t && !e; r0 += m->chunk) {
+        const size_t rows = std::min(m->chunk, t - r0);
+        if ((e = linear(m, s, m->head, m->h + r0 * m->dim, m->logits, rows))) break;
+        score_kernel<<<(unsigned)rows, 256, 0, s>>>(m->logits, m->ids + 1 + r0, out + 2 * r0, (uint32_t)m->vocab);
+        e = hipGetLastError();
+    }
+    return e;
+}
+
+}  // namespace
+
+extern "C" {
+
+fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_llama **out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!g || !out) return fail(FH_ERR_INVALID, "llama: no file or output");
+    *out = nullptr;
+    if (path == FH_PATH_AUTO) path = FH_PATH_TILED;
+    if (path != FH_PATH_TILED && path != FH_PATH_TILED_FAST)
+        return fail(FH_ERR_INVALID, "llama: the forward runs on FH_PATH_TILED or FH_PATH_TILED_FAST, not path %d",
+                    (int)path);
+    const char *a;
+    size_t alen;
+    if ((st = fh_gguf_get_string(g, "general.architecture", &a, &alen))) return st;
+    const std::string arch(a, alen);
+    if (arch != "llama" && arch != "qwen2")
+        return fail(FH_ERR_INVALID, "architecture is '%s', only 'llama' and 'qwen2' are supported", arch.c_str());
+    fh_llama *m = new (std::nothrow) fh_llama;
+    if (!m) return fail(FH_ERR_OOM, "host out of memory");
+    dev_retain(dev);
+    m->dev = dev;
+    m->path = path;
+    m->neox = arch == "qwen2";  // ferrum_model/src/gguf/llama/mod.rs:108-117
+    auto key = [&](const char *k) { return arch + "." + k; };
+    auto has = [&](const std::string &k) {
+        size_t i;
+        return fh_gguf_find_key(g, k.c_str(), &i) == FH_OK;
+    };
+    auto opt_uint = [&](const char *k, size_t dflt, size_t *v) -> fh_status {
+        if (!has(key(k))) {
+            *v = dflt;
+            return FH_OK;
+        }
+        return cfg_uint(g, key(k).c_str(), v);
+    };
+    auto opt_float = [&](const char *k, float dflt, float *v) -> fh_status {
+        if (!has(key(k))) {
+            *v = dflt;
+            return FH_OK;
+        }
+        return fh_gguf_get_float(g, key(k).c_str(), v);
+    };
+    if ((st = cfg_uint(g, key("embedding_length").c_str(), &m->dim)) ||
+        (st = cfg_uint(g, key("attention.head_count").c_str(), &m->heads)) ||
+        (st = opt_uint("attention.head_count_kv", m->heads, &m->kv_heads)) ||
+        (st = cfg_uint(g, key("block_count").c_str(), &m->layers)))
+        return llama_fail_free(m, st);
+    if (m->layers > fh_gguf_tensor_count(g))
+        return llama_fail_free(m, fail(FH_ERR_INVALID, "block_count %zu exceeds the file's %zu tensors", m->layers,
+                                       fh_gguf_tensor_count(g)));
+    if ((st = opt_uint("attention.key_length", m->heads ? m->dim / m->heads : 0, &m->head_dim)) ||
+        (st = opt_float("attention.layer_norm_rms_epsilon", 1e-5f, &m->eps)))
+        return llama_fail_free(m, st);
+    size_t tidx;
+    fh_gguf_tensor tt;
+    if ((st = fh_gguf_find_tensor(g, "token_embd.weight", &tidx)) || (st = fh_gguf_tensor_info(g, tidx, &tt)))
+        return llama_fail_free(m, st);
+    if (tt.n_dims != 2 || tt.dims[0] != m->dim)
+        return llama_fail_free(m, fail(FH_ERR_INVALID, "token_embd.weight must be [embedding_length, vocab]"));
+    m->vocab = (size_t)tt.dims[1];
+    if ((st = opt_uint("context_length", 2048, &m->ctx)) || (st = cfg_uint(g, key("feed_forward_length").c_str(), &m->hidden)) ||
+        (st = opt_uint("rope.dimension_count", m->head_dim, &m->rope_dim)) ||
+        (st = opt_float("rope.freq_base", 10000.0f, &m->rope_base)))
+        return llama_fail_free(m, st);
+    // Config::validate (ferrum_ref/src/models/llama/mod.rs:63-95)
+    if (!m->vocab || !m->ctx || !m->dim || !m->heads || !m->kv_heads || !m->head_dim || !m->layers || !m->hidden ||
+        !m->rope_dim)
+        return llama_fail_free(m, fail(FH_ERR_INVALID, "every dimension must be positive"));
+    if (m->heads % m->kv_heads)
+        return llama_fail_free(m, fail(FH_ERR_INVALID, "heads %zu is not a multiple of kv_heads %zu", m->heads, m->kv_heads));
+    if (m->rope_dim > m->head_dim || m->rope_dim % 2)
+        return llama_fail_free(m, fail(FH_ERR_INVALID, "rope_dim %zu must be even and at most head_dim %zu", m->rope_dim,
+                                       m->head_dim));
+    if (!std::isfinite(m->eps) || m->eps <= 0.0f || !std::isfinite(m->rope_base) || m->rope_base <= 0.0f)
+        return llama_fail_free(m, fail(FH_ERR_INVALID, "eps and rope_base must be finite and positive"));
+    const size_t d = m->dim, hid = m->hidden, qd = m->q_dim(), kvd = m->kv_dim(), hd = m->head_dim;
+    // what the kernels take
+    if (d % 32 || hid % 32 || qd % 32 || (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128) ||
+        m->qkv_width() > kMaxQkvWidth || m->ctx > (1u << 20) || m->vocab > (1u << 30))
+        return llama_fail_free(m, fail(FH_ERR_UNSUPPORTED,
+                                       "llama: dim %zu / hidden %zu / q width %zu / head %zu outside what the kernels take "
+                                       "(packed matrices need widths in whole 32-blocks; heads 8, 16, 32, 64 or 128 wide; "
+                                       "q + k + v at most %u wide)",
+                                       d, hid, qd, hd, kMaxQkvWidth));
+    std::vector<float> ff, cos_t, sin_t;
+    if ((st = rope_scaling(g, arch, m->rope_dim, &m->linear_factor, &ff))) return llama_fail_free(m, st);
+    fh_kind kind = (fh_kind)0;
+    if ((st = load_mat(dev, g, "llama", "token_embd.weight", d, m->vocab, &kind, &m->tok))) return llama_fail_free(m, st);
+    m->tied = fh_gguf_find_tensor(g, "output.weight", &tidx) != FH_OK;
+    if (m->tied) {
+        m->head = m->tok;  // the file omits a head tied to the embedding (llama/mod.rs:191-197)
+    } else if ((st = load_mat(dev, g, "llama", "output.weight", d, m->vocab, &kind, &m->head))) {
+        return llama_fail_free(m, st);
+    }
+    if (fh_gguf_find_tensor(g, "output.bias", &tidx) == FH_OK)
+        return llama_fail_free(m, fail(FH_ERR_INVALID, "tensor 'output.bias' is not supported"));
+    if ((st = load_vec(dev, g, "llama", "output_norm.weight", d, &m->out_norm))) return llama_fail_free(m, st);
+    m->blocks.resize(m->layers);
+    for (size_t l = 0; l < m->layers; l++) {
+        auto &L = m->blocks[l];
+        auto n = [&](const char *s) { return tensor_name("blk.", l, s); };
+        for (const char *stem : {"attn_output.bias", "ffn_gate.bias", "ffn_up.bias", "ffn_down.bias"})
+            if (fh_gguf_find_tensor(g, n(stem).c_str(), &tidx) == FH_OK)
+                return llama_fail_free(m, fail(FH_ERR_INVALID,
+                                               "tensor '%s' is not supported: biases are loaded only for attn_q/k/v",
+                                               n(stem).c_str()));
+        const std::string qkv[3] = {n("attn_q.weight"), n("attn_k.weight"), n("attn_v.weight")};
+        const size_t qkv_n[3] = {qd, kvd, kvd};
+        const std::string gu[2] = {n("ffn_gate.weight"), n("ffn_up.weight")};
+        const size_t gu_n[2] = {hid, hid};
+        if ((st = load_vec(dev, g, "llama", n("attn_norm.weight"), d, &L.attn_norm)) ||
+            (st = load_mat_rows(dev, g, "llama", qkv, qkv_n, 3, d, &kind, &L.wqkv)) ||
+            (st = load_mat(dev, g, "llama", n("attn_output.weight"), qd, d, &kind, &L.wo)) ||
+            (st = load_vec(dev, g, "llama", n("ffn_norm.weight"), d, &L.ffn_norm)) ||
+            (st = load_mat_rows(dev, g, "llama", gu, gu_n, 2, d, &kind, &L.wgu)) ||
+            (st = load_mat(dev, g, "llama", n("ffn_down.weight"), hid, d, &kind, &L.down)))
+            return llama_fail_free(m, st);
+        // q/k/v biases, absent ones zero (one vector over the stacked rows)
+        std::vector<float> bias(m->qkv_width(), 0.0f), part;
+        bool any = false;
+        const char *bnames[3] = {"attn_q.bias", "attn_k.bias", "attn_v.bias"};
+        size_t at = 0;
+        for (int i = 0; i < 3; i++) {
+            if (fh_gguf_find_tensor(g, n(bnames[i]).c_str(), &tidx) == FH_OK) {
+                if ((st = host_vec(g, "llama", n(bnames[i]), qkv_n[i], &part))) return llama_fail_free(m, st);
+                std::copy(part.begin(), part.end(), bias.begin() + at);
+                any = true;
+            }
+            at += qkv_n[i];
+        }
+        if (any && (st = fh_buffer_upload(dev, bias.data(), bias.size(), &L.bqkv))) return llama_fail_free(m, st);
+        m->weight_bytes += L.wqkv->nbytes + L.wo->nbytes + L.wgu->nbytes + L.down->nbytes;
+    }
+    m->weight_bytes += m->head->nbytes;
+    m->kind = kind;
+    rope_tables(m->ctx, m->rope_dim, m->rope_base, ff, m->linear_factor, &cos_t, &sin_t);
+    if ((st = fh_buffer_upload(dev, cos_t.data(), cos_t.size(), &m->rope_cos)) ||
+        (st = fh_buffer_upload(dev, sin_t.data(), sin_t.size(), &m->rope_sin)))
+        return llama_fail_free(m, st);
+    if (path == FH_PATH_TILED_FAST) {  // the fast GEMM's fp8 correction operand of every weight
+        std::vector<fh_qweight *> ws = {m->head};
+        for (auto &L : m->blocks) ws.insert(ws.end(), {L.wqkv, L.wo, L.wgu, L.down});
+        for (fh_qweight *w : ws) {
+            void *b8 = nullptr;
+            if ((st = alloc_bytes(dev, gemm_b8_bytes(w->k, w->n), &b8))) return llama_fail_free(m, st);
+            w->b8 = (uint8_t *)b8;
+            if ((st = begin_command(dev, "llama load"))) return llama_fail_free(m, st);
+            (void)launch_make_b8(dev->stream, w->kind, w->qs, w->ds, w->b8, w->k, w->n);
+            if ((st = end_command(dev, "llama load"))) return llama_fail_free(m, st);
+        }
+    }
+    if ((st = fh_device_sync(dev))) return llama_fail_free(m, st);
+    *out = m;
+    return FH_OK;
+}
+
+void fh_llama_free(fh_llama *m) {
+    if (!m) return;
+    if (m->dev) (void)hipStreamSynchronize(m->dev->stream);
+    if (m->head && m->head != m->tok) fh_qweight_free(m->head);
+    fh_qweight_free(m->tok);
+    for (auto &L : m->blocks) {
+        for (fh_qweight *w : {L.wqkv, L.wo, L.wgu, L.down}) fh_qweight_free(w);
+        for (fh_buffer *b : {L.attn_norm, L.ffn_norm, L.bqkv}) fh_buffer_free(b);
+    }
+    for (fh_buffer *b : {m->out_norm, m->rope_cos, m->rope_sin}) fh_buffer_free(b);
+    if (m->arena) (void)hipFree(m->arena);
+    if (m->dev) dev_release(m->dev);
+    delete m;
+}
+
+fh_status fh_llama_config(const fh_llama *m, fh_llama_cfg *out) {
+    if (!m || !out) return fail(FH_ERR_INVALID, "llama: no model or output");
+    out->vocab = m->vocab;
+    out->ctx = m->ctx;
+    out->dim = m->dim;
+    out->heads = m->heads;
+    out->kv_heads = m->kv_heads;
+    out->head_dim = m->head_dim;
+    out->layers = m->layers;
+    out->hidden = m->hidden;
+    out->rope_dim = m->rope_dim;
+    out->rope_base = m->rope_base;
+    out->eps = m->eps;
+    out->linear_factor = m->linear_factor;
+    out->neox = m->neox ? 1 : 0;
+    out->tied = m->tied ? 1 : 0;
+    out->kind = m->kind;
+    out->path = m->path;
+    return FH_OK;
+}
+
+uint64_t fh_llama_weight_bytes(const fh_llama *m) { return m ? m->weight_bytes : 0; }
+
+fh_status fh_llama_forward_all(fh_device *dev, fh_llama *m, const int32_t *ids, size_t n, float *logits) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!m || m->dev != dev) return fail(FH_ERR_INVALID, "llama: no model on this device");
+    if ((st = check_len(m, n))) return st;
+    if (!ids || !logits) return fail(FH_ERR_INVALID, "llama: no ids or output");
+    if ((st = check_ids(m, ids, n)) || (st = ensure_rows(m, n))) return st;
+    if ((st = begin_command(dev, "llama forward"))) return st;
+    hipStream_t s = dev->stream;
+    hipError_t e = hipMemcpyAsync(m->ids, ids, n * 4, hipMemcpyHostToDevice, s);
+    if (!e) e = enqueue_body(m, s, n);
+    for (size_t r0 = 0; r0 < n && !e; r0 += m->chunk) {
+        const size_t rows = std::min(m->chunk, n - r0);
+        if ((e = linear(m, s, m->head, m->h + r0 * m->dim, m->logits, rows))) break;
+        e = hipMemcpyAsync(logits + r0 * m->vocab, m->logits, rows * m->vocab * 4, hipMemcpyDeviceToHost, s);
+    }
+    if (!e) e = hipStreamSynchronize(s);
+    if (e) return hip_fail(dev, e, "llama forward");
+    return end_command(dev, "llama forward");
+}
+
+fh_status fh_llama_score(fh_device *dev, fh_llama *m, const int32_t *ids, size_t n, float *logprob,
+                         uint8_t *is_first_max) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!m || m->dev != dev) return fail(FH_ERR_INVALID, "llama: no model on this device");
+    if (n < 2) return fail(FH_ERR_INVALID, "scoring needs at least 2 tokens");
+    if (!ids || !logprob || !is_first_max) return fail(FH_ERR_INVALID, "llama: no ids or output");
+    const size_t t = n - 1;
+    if ((st = check_len(m, t)) || (st = check_ids(m, ids, n)) || (st = ensure_rows(m, t))) return st;
+    if ((st = begin_command(dev, "llama score"))) return st;
+    hipStream_t s = dev->stream;
+    std::vector<float> pairs(2 * t);
+    hipError_t e = hipMemcpyAsync(m->ids, ids, n * 4, hipMemcpyHostToDevice, s);
+    if (!e) e = enqueue_score(m, s, t, m->scores);
+    if (!e) e = hipMemcpyAsync(pairs.data(), m->scores, 2 * t * 4, hipMemcpyDeviceToHost, s);
+    if (!e) e = hipStreamSynchronize(s);
+    if (e) return hip_fail(dev, e, "llama score");
+    for (size_t r = 0; r < t; r++) {
+        logprob[r] = pairs[2 * r];
+        is_first_max[r] = pairs[2 * r + 1] == 1.0f;
+    }
+    return end_command(dev, "llama score");
+}
+
+fh_status fh_llama_score_device(fh_device *dev, fh_llama *m, const fh_buffer *ids, size_t n, fh_buffer *out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!m || m->dev != dev) return fail(FH_ERR_INVALID, "llama: no model on this device");
+    if (n < 2) return fail(FH_ERR_INVALID, "scoring needs at least 2 tokens");
+    if (!ids || !out || ids->dev != dev || out->dev != dev) return fail(FH_ERR_INVALID, "llama: ids or output not on this device");
+    if (ids->nbytes < n * 4) return fail(FH_ERR_INVALID, "llama: the ids buffer holds %zu bytes, needs %zu", ids->nbytes, n * 4);
+    const size_t t = n - 1;
+    if (out->nbytes < 2 * t * 4)
+        return fail(FH_ERR_INVALID, "llama: the output holds %zu bytes, needs %zu", out->nbytes, 2 * t * 4);
+    if ((st = check_len(m, t)) || (st = ensure_rows(m, t))) return st;
+    if ((st = begin_command(dev, "llama score"))) return st;
+    hipStream_t s = dev->stream;
+    hipError_t e = hipMemcpyAsync(m->ids, ids->ptr, n * 4, hipMemcpyDeviceToDevice, s);
+    if (!e) e = enqueue_score(m, s, t, (float *)out->ptr);
+    if (e) return hip_fail(dev, e, "llama score");
+    return end_command(dev, "llama score");
+}
+
+}  // extern "C"

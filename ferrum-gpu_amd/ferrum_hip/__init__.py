@@ -143,6 +143,13 @@ def lib() -> ctypes.CDLL:
         "fh_gpt2_step_bytes": (U64, [P]),
         "fh_gpt2_feed": (I, [P, P, S, P]),
         "fh_gpt2_generate": (I, [P, P, P, S, S, P]),
+        "fh_llama_from_gguf": (I, [P, P, I, PP]),
+        "fh_llama_free": (None, [P]),
+        "fh_llama_config": (I, [P, P]),
+        "fh_llama_weight_bytes": (U64, [P]),
+        "fh_llama_forward_all": (I, [P, P, P, S, P]),
+        "fh_llama_score": (I, [P, P, P, S, P, P]),
+        "fh_llama_score_device": (I, [P, P, P, S, P]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)

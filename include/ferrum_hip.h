@@ -307,6 +307,46 @@ FH_API fh_status fh_gpt2_feed(fh_device *dev, fh_gpt2 *m, size_t token, float *l
 FH_API fh_status fh_gpt2_generate(fh_device *dev, fh_gpt2 *m, const int32_t *prompt, size_t n_prompt,
                                   size_t n_new, int32_t *out);
 
+/* ---- Llama / Qwen2 full-sequence forward and scoring on resident Q8_0 / Q4_0 weights ----
+ * Replaces the batched passes of ferrum_wgpu::models::llama::GpuLlama (ferrum_wgpu/src/models/
+ * llama/forward.rs:13-88: forward_all, score), whose weights may be f32; here every matrix stays
+ * packed. The model comes from a `llama` (NORM RoPE) or `qwen2` (NEOX RoPE) GGUF as
+ * ferrum_model reads and writes it (ferrum_model/src/gguf/llama/mod.rs:56-323): Q8_0 or Q4_0
+ * matrices (one format per model, widths in whole 32-blocks), F32 vectors, optional q/k/v biases,
+ * `output.weight` absent for a head tied to `token_embd.weight`, linear / rope_freqs RoPE scaling.
+ * Its CPU counterpart is ferrum_ref's Llama::forward_logits on the decoded weights
+ * (ferrum_ref/src/models/llama/mod.rs:166-259) and nn::score (ferrum_ref/src/kernels/nn.rs:117-129).
+ * `path` picks the products: FH_PATH_TILED (or AUTO) the precise MFMA GEMM, FH_PATH_TILED_FAST
+ * the scoring GEMM (x as f16 + an fp8 correction; its error bound is the one the GEMM states). */
+typedef struct fh_llama fh_llama;
+typedef struct fh_llama_cfg {
+    size_t vocab, ctx, dim, heads, kv_heads, head_dim, layers, hidden, rope_dim;
+    float rope_base, eps, linear_factor;
+    int neox, tied;
+    fh_kind kind;
+    fh_path path;
+} fh_llama_cfg;
+FH_API fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_llama **out);
+FH_API void fh_llama_free(fh_llama *m);
+/* Config (ferrum_ref/src/models/llama/mod.rs:24-51) and how the model is stored. */
+FH_API fh_status fh_llama_config(const fh_llama *m, fh_llama_cfg *out);
+/* Packed weight bytes one forward reads (every block matrix and the head). */
+FH_API uint64_t fh_llama_weight_bytes(const fh_llama *m);
+/* GpuLlama::forward_all (forward.rs:13-73): every position's logits of ids[0..n), [n, vocab]
+ * row-major into host memory. Errors: "sequence length N must be in 1..=ctx", "token T is out of
+ * range for vocab V". */
+FH_API fh_status fh_llama_forward_all(fh_device *dev, fh_llama *m, const int32_t *ids, size_t n, float *logits);
+/* GpuLlama::score (forward.rs:76-88): for each i < n - 1 the log-probability of ids[i + 1] after
+ * ids[..=i] and whether it is the first argmax; only 2 (n - 1) floats leave the device. Errors:
+ * "scoring needs at least 2 tokens" and those of forward_all. */
+FH_API fh_status fh_llama_score(fh_device *dev, fh_llama *m, const int32_t *ids, size_t n, float *logprob,
+                                uint8_t *is_first_max);
+/* The same pass on device-resident ids (n int32 values) into out (2 (n - 1) floats: log-probability,
+ * then 1.0 for a first argmax else 0.0, per row, as ops::score writes them, ferrum_wgpu/src/ops/
+ * mod.rs:157-175). Asynchronous on the device's stream. The ids are not read on the host: one
+ * outside the vocabulary is never read past, but it turns its row and the rows after it to NaN. */
+FH_API fh_status fh_llama_score_device(fh_device *dev, fh_llama *m, const fh_buffer *ids, size_t n, fh_buffer *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,213 @@
+"""Llama / Qwen2 full-sequence forward and scoring on the device against the CPU oracle
+(ferrum_ref's Llama::forward_logits and nn::score on the weights the GGUF stores). Mirrors
+ferrum_wgpu/src/models/llama/tests.rs (forward_all per variant, quantised GGUF models, score,
+RoPE scaling, bad input) on packed Q8_0 / Q4_0 weights, plus the Qwen2-0.5B shape of the scoring
+benchmark.
+
+Tolerances. The precise path (FH_PATH_TILED) keeps the reference's FORWARD bound on logits,
+max |g - w| / max(|w|, 1) < 1e-5 (ferrum_wgpu/src/tolerance.rs:11), and its score bound,
+|g - w| < 1e-4 max(|w|, 1) per log-probability with identical first-argmax flags
+(ferrum_wgpu/src/models/llama/tests.rs:177-194). The fast scoring path (FH_PATH_TILED_FAST) runs
+every product with x rounded to f16 plus an e4m3 correction (relative error ~3e-5 per product);
+its log-probabilities are held to FAST_LOGPROB = 5e-4 relative (observed 1.2e-4 at the
+Qwen2-0.5B shape, 3e-5 on the small variants; the MFMA-GEMM tolerance is 2e-3)."""
+import os
+import time
+
+import numpy as np
+import pytest
+
+from oracle import llama_model as lm
+
+pytestmark = pytest.mark.gpu
+FORWARD = 1e-5
+SCORE = 1e-4
+FAST_LOGPROB = 5e-4
+V = 17
+IDS = [3, 16, 0, 9, 9, 4, 11, 2, 7, 5]
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def cfg(**kw):
+    """ferrum_wgpu/src/models/llama/tests.rs:10-25"""
+    c = lm.config(vocab=V, ctx=10, dim=32, heads=4, kv_heads=2, head_dim=8, layers=2, hidden=64, rope_dim=8,
+                  rope_base=10000.0, neox=False, eps=1e-5)
+    c.update(kw)
+    return c
+
+
+def variants():
+    """tests.rs:29-45 without dim24, whose 24-wide matrices have no Q8_0/Q4_0 form (the device
+    multiplies packed matrices only; test_unpackable_widths_are_refused)."""
+    return [("llama", cfg(), False, False), ("qwen", cfg(neox=True), True, True),
+            ("mqa+partial", cfg(kv_heads=1, rope_dim=4), False, False)]
+
+
+@pytest.fixture(scope="module")
+def fh():
+    import ferrum_hip
+
+    return ferrum_hip
+
+
+@pytest.fixture(scope="module")
+def g(fh):
+    gpu = fh.Gpu.open_for_test()
+    if gpu is None:
+        pytest.skip("no gfx950 device")
+    yield gpu
+    gpu.close()
+
+
+def load(fh, g, data: bytes, path=None):
+    from ferrum_hip.gguf import Gguf
+    from ferrum_hip.llama import GpuLlama
+
+    return GpuLlama.from_gguf(g, Gguf.parse(data), fh.QPath.Tiled if path is None else path)
+
+
+def rel(got, want) -> float:
+    """ferrum_wgpu/src/tolerance.rs:14-26"""
+    return float((np.abs(got - want) / np.maximum(np.abs(want), 1.0)).max())
+
+
+def lp_err(got, want) -> float:
+    return float((np.abs(got - want) / np.maximum(np.abs(want), 1.0)).max())
+
+
+@pytest.mark.parametrize("kind", [lm.Q8_0, lm.Q4_0])
+@pytest.mark.parametrize("name,c,biases,tied", variants(), ids=[v[0] for v in variants()])
+def test_forward_all_matches_the_oracle_for_every_variant(fh, g, orc, kind, name, c, biases, tied):
+    """tests.rs:92-131: a model loaded from a quantised GGUF, every prefix length, FORWARD."""
+    data = lm.to_gguf(lm.llama_random(c, 5, biases, tied), kind)
+    ref = lm.from_gguf(data)
+    dev = load(fh, g, data)
+    cf = dev.config()
+    assert (cf.vocab, cf.dim, cf.heads, cf.kv_heads, cf.head_dim, cf.rope_dim, cf.neox, cf.tied) == \
+        (V, c["dim"], c["heads"], c["kv_heads"], c["head_dim"], c["rope_dim"], c["neox"], tied)
+    for t in (1, 2, 7, 10):
+        e = rel(dev.forward_all(IDS[:t]), orc.llama_forward(ref, IDS[:t]))
+        say(f"{name} kind {kind} t={t}: {e:.2e}")
+        assert e < FORWARD, (name, t, e)
+
+
+def test_bad_input_is_refused_with_the_reference_messages(fh, g, orc):
+    dev = load(fh, g, lm.to_gguf(lm.llama_random(cfg(), 1, False, False), lm.Q8_0))
+    for bad, msg in (([], "sequence length 0 must be in 1..=10"), ([0] * 11, "sequence length 11"),
+                     ([V], "token 17 is out of range for vocab 17")):
+        with pytest.raises(fh.GpuError) as err:
+            dev.forward_all(bad)
+        assert msg in str(err.value)
+    with pytest.raises(fh.GpuError) as err:
+        dev.score([1])
+    assert "scoring needs at least 2 tokens" in str(err.value)
+    with pytest.raises(fh.GpuError) as err:
+        dev.score([1, 2, V])
+    assert "out of range" in str(err.value)
+    assert dev.forward_all([1, 2]).shape == (2, V)  # still usable
+
+
+def test_score_matches_the_oracle(fh, g, orc):
+    """tests.rs:177-194: Llama::random(cfg, 8, biases, tied), ids [4, 8, 15, 16, 0, 1]."""
+    data = lm.to_gguf(lm.llama_random(cfg(), 8, True, True), lm.Q8_0)
+    ref = lm.from_gguf(data)
+    ids = [4, 8, 15, 16, 0, 1]
+    want_lp, want_hit = orc.llama_score(ref, ids)
+    dev = load(fh, g, data)
+    got = dev.score(ids)
+    assert len(got) == 5
+    for i, ((glp, ghit), wlp, whit) in enumerate(zip(got, want_lp, want_hit)):
+        assert abs(glp - wlp) < SCORE * max(abs(wlp), 1.0), (i, glp, wlp)
+        assert ghit == bool(whit), i
+    # a longer run over the whole context, flags included
+    lp, hit = dev.score_arrays(IDS)
+    wlp, whit = orc.llama_score(ref, IDS)
+    assert lp_err(lp, wlp) < SCORE and np.array_equal(hit, whit)
+
+
+def test_score_device_matches_score(fh, g, orc):
+    data = lm.to_gguf(lm.llama_random(cfg(neox=True), 9, True, False), lm.Q4_0)
+    dev = load(fh, g, data)
+    lp, hit = dev.score_arrays(IDS)
+    ids = g.upload_bytes(np.asarray(IDS, np.int32).view(np.uint8))
+    out = g.zeros(2 * (len(IDS) - 1))
+    dev.score_device(ids, len(IDS), out)
+    pairs = g.read(out).reshape(-1, 2)
+    assert np.array_equal(pairs[:, 0], lp)
+    assert np.array_equal(pairs[:, 1] == 1.0, hit)
+
+
+def test_rope_scaling_is_honoured_on_the_device(fh, g, orc):
+    """tests.rs:152-175: rope_freqs.weight and linear scaling from the GGUF."""
+    m = lm.llama_random(cfg(), 7, False, False)
+    m["freq_factors"] = np.array([1.0, 2.0, 4.0, 8.0], np.float32)
+    m["linear_factor"] = 2.0
+    data = lm.to_gguf(m, lm.Q8_0)
+    ref = lm.from_gguf(data)
+    assert ref["linear_factor"] == 2.0 and np.array_equal(ref["freq_factors"], m["freq_factors"])
+    plain = dict(ref, freq_factors=None, linear_factor=1.0)
+    want = orc.llama_forward(ref, IDS[:6])
+    assert np.abs(want - orc.llama_forward(plain, IDS[:6])).max() > 1e-3  # scaling must matter
+    assert rel(load(fh, g, data).forward_all(IDS[:6]), want) < FORWARD
+
+
+def test_unpackable_widths_are_refused(fh, g, orc):
+    c = cfg(dim=24, heads=3, kv_heads=3, head_dim=8, rope_dim=8)
+    with pytest.raises(fh.GpuError) as err:
+        load(fh, g, lm.to_gguf(lm.llama_random(c, 1, True, False), lm.Q8_0))
+    assert "Q8_0 or Q4_0" in str(err.value) or "32-blocks" in str(err.value)
+
+
+@pytest.mark.parametrize("name,c,biases,tied", variants(), ids=[v[0] for v in variants()])
+def test_fast_path_stays_within_its_bound(fh, g, orc, name, c, biases, tied):
+    data = lm.to_gguf(lm.llama_random(c, 11, biases, tied), lm.Q4_0)
+    ref = lm.from_gguf(data)
+    dev = load(fh, g, data, fh.QPath.TiledFast)
+    assert dev.config().path == fh.QPath.TiledFast
+    lp, hit = dev.score_arrays(IDS)
+    wlp, whit = orc.llama_score(ref, IDS)
+    e = lp_err(lp, wlp)
+    say(f"fast {name}: log-prob rel err {e:.2e}, logits {rel(dev.forward_all(IDS), orc.llama_forward(ref, IDS)):.2e}")
+    assert e < FAST_LOGPROB
+
+
+@pytest.fixture(scope="module")
+def qwen(fh, g):
+    """The scoring benchmark's model: Qwen2-0.5B shapes (24 layers, d 896, FFN 4864, 14 q / 2 kv
+    heads of 64, NEOX RoPE base 1e6, q/k/v biases, vocab 151936, tied head), Q4_0, with
+    Llama::random-distributed synthetic weights; and its decoded f32 form for the oracle."""
+    from ferrum_hip.llama import QWEN2_0_5B, random_gguf
+
+    t0 = time.time()
+    data = random_gguf(g, dict(QWEN2_0_5B, ctx=4096), fh.QKind.Q4_0, seed=1)
+    ref = lm.from_gguf(data)
+    say(f"qwen2-0.5b model built in {time.time() - t0:.1f} s ({len(data) / 1e6:.1f} MB GGUF)")
+    return data, ref
+
+
+@pytest.mark.parametrize("path", ["Tiled", "TiledFast"])
+def test_qwen2_0_5b_scoring_matches_the_oracle(fh, g, orc, qwen, path):
+    data, ref = qwen
+    dev = load(fh, g, data, fh.QPath[path])
+    assert dev.weight_bytes() == 277_853_184  # the packed Q4_0 bytes of every matrix and the head
+    ids = [int(t) for t in np.random.default_rng(2024).integers(0, 151936, 129)]
+    t0 = time.time()
+    wlp, whit = orc.llama_score(ref, ids, threads=min(16, os.cpu_count() or 1))
+    say(f"oracle score of 128 rows in {time.time() - t0:.1f} s")
+    lp, hit = dev.score_arrays(ids)
+    e = lp_err(lp, wlp)
+    say(f"{path}: log-prob rel err {e:.2e} (abs {np.abs(lp - wlp).max():.2e}); lp range {wlp.min():.1f}..{wlp.max():.1f}")
+    assert e < (SCORE if path == "Tiled" else FAST_LOGPROB)
+    if path == "Tiled":
+        assert np.array_equal(hit, whit)
+    # causality at the benchmark lengths: the 512- and 2048-row passes agree on the first rows
+    more = ids + [int(t) for t in np.random.default_rng(7).integers(0, 151936, 2048 - 128)]
+    lp512, _ = dev.score_arrays(more[:513])
+    lp2048, hit2048 = dev.score_arrays(more)
+    assert lp512.shape == (512,) and lp2048.shape == (2048,)
+    assert np.all(np.isfinite(lp2048)) and np.all(lp2048 <= 0)
+    bound = SCORE if path == "Tiled" else FAST_LOGPROB
+    assert lp_err(lp512[:128], wlp) < bound and lp_err(lp2048[:512], lp512) < bound
