@@ -268,6 +268,81 @@ def bench_decode(fh, g, n_prompt=32, n_new=256, reps=3, cpu=True):
     return out
 
 
+QWEN_LINEAR_WEIGHTS = 493_961_216  # packed weights one Qwen2-0.5B forward multiplies by (head included)
+
+
+def bench_scoring(fh, g, ev, ms=(512, 2048), paths=None, reps=5, cpu=True, cpu_rows=64):
+    """full-sequence scoring with the random-init Qwen2-0.5B-shape model (24
+    layers, d 896, FFN 4864 SwiGLU, RMSNorm, NEOX RoPE base 1e6, q/k/v biases, vocab 151936, tied
+    head), Q4_0 weights, M seeded uniform-random token IDs (M + 1 IDs, M scored rows). One rep is
+    one fh_llama_score_device call with the IDs already on the device; the median of `reps` reps
+    (HIP events on the device stream). TFLOP/s counts the linear layers only (2 M x 493.96M, the
+    reference's formula); the causal attention adds 2 x 2 x 14 x 64 x M (M + 1) / 2 x 24 flops.
+    The CPU leg runs the oracle's forward + score (all host threads, f32 decoded weights) on
+    `cpu_rows` rows and reports its rate and the device's largest log-probability error on them."""
+    from ferrum_hip.gguf import Gguf
+    from ferrum_hip.llama import QWEN2_0_5B, GpuLlama, random_gguf
+
+    paths = paths or (fh.QPath.TiledFast, fh.QPath.Tiled)
+    data = random_gguf(g, QWEN2_0_5B, fh.QKind.Q4_0, seed=1)
+    gg = Gguf.parse(data)
+    rng = np.random.default_rng(2024)
+    ids_all = rng.integers(0, QWEN2_0_5B["vocab"], max(ms) + 1).astype(np.int32)
+    out = {"weights": QWEN_LINEAR_WEIGHTS, "gguf_bytes": len(data)}
+    for path in paths:
+        model = GpuLlama.from_gguf(g, gg, path)
+        tag = "fast" if path == fh.QPath.TiledFast else "precise"
+        for m in ms:
+            ids = g.upload_bytes(ids_all[: m + 1].view(np.uint8))
+            res = g.zeros(2 * m)
+            for _ in range(2):
+                model.score_device(ids, m + 1, res)
+            g.sync()
+            times = []
+            for _ in range(reps):
+                e0, e1 = ev.create(2)
+                ev.record(e0)
+                model.score_device(ids, m + 1, res)
+                ev.record(e1)
+                g.sync()
+                times.append(ev.ms(e0, e1))
+                ev.destroy([e0, e1])
+            t = float(np.median(times))
+            lp = g.read(res)[0::2]
+            flops = 2 * m * QWEN_LINEAR_WEIGHTS
+            attn = 2 * 2 * 14 * 64 * m * (m + 1) // 2 * 24
+            out[f"{tag}_m{m}"] = {"ms": round(t, 4), "tok_s": round(m / (t * 1e-3), 1),
+                                  "linear_tflops": round(flops / (t * 1e-3) / 1e12, 2),
+                                  "frac": round(flops / (t * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                                  "attention_gflop": round(attn / 1e9, 1), "finite": bool(np.isfinite(lp).all()),
+                                  "mean_logprob": round(float(lp.mean()), 3)}
+            ids.free()
+            res.free()
+        if cpu:
+            import oracle as orc
+            from oracle import llama_model as lm
+
+            ref = out.get("_ref") or lm.from_gguf(data)
+            out["_ref"] = ref
+            sample = [int(t) for t in ids_all[: cpu_rows + 1]]
+            threads = min(16, os.cpu_count() or 1)
+            t0 = time.perf_counter()
+            wlp, whit = orc.llama_score(ref, sample, threads=threads)
+            dt = time.perf_counter() - t0
+            glp, ghit = model.score_arrays(sample)
+            err = float((np.abs(glp - wlp) / np.maximum(np.abs(wlp), 1.0)).max())
+            out[f"{tag}_logprob_rel_err_vs_cpu"] = err
+            out[f"{tag}_logprob_abs_err_vs_cpu"] = float(np.abs(glp - wlp).max())
+            out[f"{tag}_first_argmax_flags_equal"] = bool(np.array_equal(ghit, whit))
+            out["cpu_tok_s"] = round(cpu_rows / dt, 2)
+            out["cpu_sample"] = (f"oracle Llama::forward_logits + nn::score on {cpu_rows} rows, f32 decoded weights, "
+                                 f"{threads} threads, {dt:.2f} s")
+            out["cpu_threads"] = threads
+        model.free()
+    out.pop("_ref", None)
+    return out
+
+
 def cpu_baseline(shapes, kind_bytes, budget_s=12.0):
     """The reference's CPU decode path restated in C (oracle/gemv: f32 weights [k, n], ascending
     k, one thread), on the same shapes; the rate is the same algorithmic bytes (the packed
@@ -305,6 +380,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the GPT-2-small decode (config 2), one JSON line (for profiling)")
+    ap.add_argument("--score-only", action="store_true",
+                    help="only the Qwen2-0.5B Q4_0 scoring forward (config 4), one JSON line (for profiling)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the scoring GEMM at the TinyLlama-1.1B shapes, M = 4096, one JSON line (for profiling)")
     a = ap.parse_args()
@@ -323,6 +400,13 @@ def main():
         g.close()
         return
     ev = HipEvents(g)
+    if a.score_only:
+        r = bench_scoring(fh, g, ev, paths=(fh.QPath.TiledFast,), cpu=not a.no_cpu)
+        best = r["fast_m2048"]
+        print(json.dumps({"metric": "Qwen2-0.5B Q4_0 scoring tokens/s, M = 2048", "value": best["tok_s"],
+                          "unit": "tok/s", "n_gpus": 1, "higher_is_better": True, "detail": r}))
+        g.close()
+        return
     if a.gemm_only:
         r = bench_gemm(fh, g, ev, fh.QKind.Q4_0, 4096, LLAMA1B_SHAPES, a.steps, path=fh.QPath.TiledFast)
         print(json.dumps({"metric": "Q4_0 scoring GEMM TFLOP/s, TinyLlama-1.1B layer shapes, M = 4096",
@@ -356,6 +440,9 @@ def main():
                                                   "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                                                   "ms_per_step": r["ms_per_step"],
                                                   "flops_per_step": r["flops_per_step"]}
+        sc = bench_scoring(fh, g, ev, cpu=not a.no_cpu)
+        log("Qwen2-0.5B Q4_0 scoring:", sc)
+        extra["qwen2_0_5b_q4_0_scoring"] = sc
         dec = bench_decode(fh, g, cpu=not a.no_cpu)
         log("GPT-2-small Q8_0 decode:", dec)
         extra["gpt2_small_q8_0_decode"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec.items()}

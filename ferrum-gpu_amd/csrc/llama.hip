@@ -160,32 +160,64 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(float *__restrict__ qkv, 
 
 // Causal grouped-query attention (ferrum_ref/src/models/llama/ops.rs:131-162 for every row) from
 // qkv [t, width] (the q heads, then the k heads, then the v heads, each HD wide) into att
-// [t, heads * HD]. One wavefront takes 32 query rows of one head and walks the key rows in tiles
-// of 32 with an online softmax; both products run on v_mfma_f32_32x32x2_f32 in f32:
+// [t, heads * HD]. A workgroup takes 32 query rows of one head; its W wavefronts split the key
+// tiles (32 keys each) round robin, each keeping an online softmax, and are merged through LDS
+// at the end. Both products run on v_mfma_f32_32x32x2_f32 in f32:
 //   S^T (32 keys x 32 queries) = K . Q^T: lane l (key or query l % 32, slot l / 32) feeds dims
 //     8m + 4 slot + c at step 4m + c, so K and Q load as float4;
 //   O^T (32 dims x 32 queries) += V^T . P^T: at step s the B operand is the S^T accumulator's
 //     register s (key 8 (s / 4) + 4 slot + s % 4 of query l % 32) and the A operand that key's
 //     value at dim l % 32, a coalesced row segment.
 // Each lane owns one query (l % 32) throughout: lanes l and l ^ 32 share its running maximum and
-// split its running sum, added at the end.
+// split its running sum. A wavefront loads the next tile's K and V while it computes the current
+// one.
 template <int HD>
-__global__ __launch_bounds__(64) void attention_kernel(const float *__restrict__ qkv, float *__restrict__ att, uint32_t t,
-                                                       uint32_t width, uint32_t heads, uint32_t group, float scale) {
-    constexpr int M4 = HD / 8;                  // float4 pairs per row
-    constexpr int DB = HD >= 32 ? HD / 32 : 1;  // 32-dim blocks of the output
-    const uint32_t lane = threadIdx.x, col = lane & 31u, slot = lane >> 5;
+struct AttnTile {
+    static constexpr int M4 = HD / 8;                  // float4 pairs per row
+    static constexpr int DB = HD >= 32 ? HD / 32 : 1;  // 32-dim blocks of the output
+    f32x4 k[M4];
+    float v[DB][16];
+};
+
+template <int HD>
+__device__ __forceinline__ void attn_load(AttnTile<HD> &T, const float *__restrict__ qkv, uint32_t k0, uint32_t t,
+                                          uint32_t width, uint32_t kofs, uint32_t vofs, uint32_t col, uint32_t slot) {
+    const uint32_t key = k0 + col;
+    const bool ok = key < t;
+    const float *krow = qkv + (size_t)(ok ? key : 0u) * width + kofs + 4 * slot;
+#pragma unroll
+    for (int m = 0; m < AttnTile<HD>::M4; m++) T.k[m] = ok ? *(const f32x4 *)(krow + 8 * m) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < AttnTile<HD>::DB; b++) {
+        const uint32_t dim = 32 * b + col;
+        const bool dok = dim < (uint32_t)HD;
+#pragma unroll
+        for (int st = 0; st < 16; st++) {
+            const uint32_t kk = k0 + 8 * (st / 4) + 4 * slot + (st % 4);
+            T.v[b][st] = dok && kk < t ? qkv[(size_t)kk * width + vofs + dim] : 0.0f;
+        }
+    }
+}
+
+template <int HD, int W>
+__global__ __launch_bounds__(64 * W) void attention_kernel(const float *__restrict__ qkv, float *__restrict__ att,
+                                                           uint32_t t, uint32_t width, uint32_t heads, uint32_t group,
+                                                           float scale) {
+    using T = AttnTile<HD>;
+    constexpr int DB = T::DB;
+    __shared__ float red[W][2 + 16 * DB][64];
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6, col = lane & 31u, slot = lane >> 5;
     const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * 32;  // the longest tiles start first
     const uint32_t h = blockIdx.y, g = h / group, kv_heads = heads / group;
     const uint32_t qd = heads * HD;
     const uint32_t kofs = qd + g * HD, vofs = qd + kv_heads * HD + g * HD;
     const uint32_t query = q0 + col;
-    f32x4 qf[M4];
+    f32x4 qf[T::M4];
     {
         const bool ok = query < t;
         const float *qrow = qkv + (size_t)(ok ? query : 0u) * width + h * HD + 4 * slot;
 #pragma unroll
-        for (int m = 0; m < M4; m++) qf[m] = ok ? *(const f32x4 *)(qrow + 8 * m) : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < T::M4; m++) qf[m] = ok ? *(const f32x4 *)(qrow + 8 * m) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
     f32x16 o[DB];
 #pragma unroll
@@ -193,22 +225,19 @@ __global__ __launch_bounds__(64) void attention_kernel(const float *__restrict__
 #pragma unroll
         for (int i = 0; i < 16; i++) o[b][i] = 0.0f;
     float mrun = -INFINITY, lrun = 0.0f;
-    const uint32_t last = min(q0 + 31u, t - 1u);
-    for (uint32_t k0 = 0; k0 <= last; k0 += 32) {
+    const uint32_t tiles = (min(q0 + 31u, t - 1u)) / 32 + 1;  // key tiles any valid query of the block sees
+    T cur, nxt;
+    if (w < tiles) attn_load<HD>(cur, qkv, 32 * w, t, width, kofs, vofs, col, slot);
+    for (uint32_t kt = w; kt < tiles; kt += W) {
+        const uint32_t k0 = 32 * kt;
+        if (kt + W < tiles) attn_load<HD>(nxt, qkv, k0 + 32 * W, t, width, kofs, vofs, col, slot);
         f32x16 s;
 #pragma unroll
         for (int i = 0; i < 16; i++) s[i] = 0.0f;
-        {
-            const uint32_t key = k0 + col;
-            const bool ok = key < t;
-            const float *krow = qkv + (size_t)(ok ? key : 0u) * width + kofs + 4 * slot;
 #pragma unroll
-            for (int m = 0; m < M4; m++) {
-                const f32x4 kf = ok ? *(const f32x4 *)(krow + 8 * m) : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < T::M4; m++)
 #pragma unroll
-                for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[c], qf[m][c], s, 0, 0, 0);
-            }
-        }
+            for (int c = 0; c < 4; c++) s = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.k[m][c], qf[m][c], s, 0, 0, 0);
         float mt = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
@@ -232,17 +261,31 @@ __global__ __launch_bounds__(64) void attention_kernel(const float *__restrict__
         for (int b = 0; b < DB; b++) {
 #pragma unroll
             for (int i = 0; i < 16; i++) o[b][i] *= alpha;
-            const uint32_t dim = 32 * b + col;
-            const bool dok = dim < (uint32_t)HD;
 #pragma unroll
-            for (int st = 0; st < 16; st++) {
-                const uint32_t key = k0 + 8 * (st / 4) + 4 * slot + (st % 4);
-                const float v = dok && key < t ? qkv[(size_t)key * width + vofs + dim] : 0.0f;
-                o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(v, s[st], o[b], 0, 0, 0);
-            }
+            for (int st = 0; st < 16; st++) o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.v[b][st], s[st], o[b], 0, 0, 0);
         }
+        cur = nxt;
     }
-    const float inv = 1.0f / (lrun + __shfl_xor(lrun, 32));
+    // merge the wavefronts' partial softmaxes: M = max m_w, O = sum O_w e^(m_w - M), l likewise
+    red[w][0][lane] = mrun;
+    red[w][1][lane] = lrun;
+#pragma unroll
+    for (int b = 0; b < DB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) red[w][2 + 16 * b + i][lane] = o[b][i];
+    __syncthreads();
+    if (w) return;
+    float M = red[0][0][lane];
+#pragma unroll
+    for (int j = 1; j < W; j++) M = fmaxf(M, red[j][0][lane]);
+    float f[W], l = 0.0f;
+#pragma unroll
+    for (int j = 0; j < W; j++) {
+        f[j] = __expf(red[j][0][lane] - M);  // a wavefront without tiles: e^(-inf) = 0
+        l += red[j][1][lane] * f[j];
+    }
+    l += __shfl_xor(l, 32);
+    const float inv = 1.0f / l;
     if (query >= t) return;
     float *out = att + (size_t)query * qd + h * HD;
 #pragma unroll
@@ -250,7 +293,10 @@ __global__ __launch_bounds__(64) void attention_kernel(const float *__restrict__
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const uint32_t dim = 32 * b + 8 * (i / 4) + 4 * slot + (i % 4);
-            if (dim < (uint32_t)HD) out[dim] = o[b][i] * inv;
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < W; j++) acc += red[j][2 + 16 * b + i][lane] * f[j];
+            if (dim < (uint32_t)HD) out[dim] = acc * inv;
         }
 }
 
@@ -272,7 +318,18 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float *__restrict__ g
 
 // Per row (nn::score, ferrum_ref/src/kernels/nn.rs:117-129): out[2r] = logits[r][t] - max -
 // ln(sum exp(logits[r] - max)), out[2r + 1] = 1 when t is the first maximum, else 0; t =
-// targets[r]. One pass with a running maximum; a target outside the vocabulary gives NaN.
+// targets[r]. One pass with a running maximum per thread (rescaled when a larger value
+// arrives), four logits per load when rows are 16-byte aligned; a target outside the vocabulary
+// gives NaN.
+__device__ __forceinline__ void score_take(float v, uint32_t j, float &m, float &s, uint32_t &first) {
+    if (v > m) {
+        s = m == -INFINITY ? 0.0f : s * __expf(m - v);
+        m = v;
+        first = j;
+    }
+    s += __expf(v - m);
+}
+
 __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ logits, const int32_t *__restrict__ targets,
                                                     float *__restrict__ out, uint32_t vocab) {
     __shared__ float sm[4], ss[4];
@@ -280,22 +337,26 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ lo
     const float *x = logits + (size_t)blockIdx.x * vocab;
     float m = -INFINITY, s = 0.0f;
     uint32_t first = 0xffffffffu;
-    for (uint32_t j = threadIdx.x; j < vocab; j += 256) {
-        const float v = x[j];
-        if (v == -INFINITY) continue;  // adds nothing (and would make exp(-inf + inf))
-        if (v > m) {
-            s = s * expf(m - v) + 1.0f;
-            m = v;
-            first = j;
-        } else {
-            s += expf(v - m);
+    if ((vocab & 3u) == 0) {
+        const f32x4 *x4 = (const f32x4 *)x;
+        for (uint32_t j = threadIdx.x; j < vocab / 4; j += 256) {
+            const f32x4 v = x4[j];
+            const float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+            if (mx > m) {
+                s = m == -INFINITY ? 0.0f : s * __expf(m - mx);
+                m = mx;
+                first = 4 * j + (v[0] == mx ? 0u : v[1] == mx ? 1u : v[2] == mx ? 2u : 3u);
+            }
+            s += (__expf(v[0] - m) + __expf(v[1] - m)) + (__expf(v[2] - m) + __expf(v[3] - m));
         }
+    } else {
+        for (uint32_t j = threadIdx.x; j < vocab; j += 256) score_take(x[j], j, m, s, first);
     }
     for (int o = 32; o; o >>= 1) {
         const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
         const uint32_t f2 = __shfl_xor(first, o);
         const float mx = fmaxf(m, m2);
-        s = (m == -INFINITY ? 0.0f : s * expf(m - mx)) + (m2 == -INFINITY ? 0.0f : s2 * expf(m2 - mx));
+        s = (m == -INFINITY ? 0.0f : s * __expf(m - mx)) + (m2 == -INFINITY ? 0.0f : s2 * __expf(m2 - mx));
         first = m2 > m || (m2 == m && f2 < first) ? f2 : first;
         m = mx;
     }
@@ -311,7 +372,7 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ lo
     uint32_t F = sf[0];
     for (int i = 1; i < 4; i++) {
         const float mx = fmaxf(M, sm[i]);
-        S = (M == -INFINITY ? 0.0f : S * expf(M - mx)) + (sm[i] == -INFINITY ? 0.0f : ss[i] * expf(sm[i] - mx));
+        S = (M == -INFINITY ? 0.0f : S * __expf(M - mx)) + (sm[i] == -INFINITY ? 0.0f : ss[i] * __expf(sm[i] - mx));
         F = sm[i] > M || (sm[i] == M && sf[i] < F) ? sf[i] : F;
         M = mx;
     }
@@ -476,12 +537,13 @@ hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t) {
     const dim3 grid((unsigned)((t + 31) / 32), (unsigned)m->heads);
     const uint32_t w = (uint32_t)m->qkv_width(), group = (uint32_t)(m->heads / m->kv_heads);
     const float scale = 1.0f / sqrtf((float)m->head_dim);
+    const uint32_t T = (uint32_t)t, H = (uint32_t)m->heads;
     switch (m->head_dim) {
-    case 8: attention_kernel<8><<<grid, 64, 0, s>>>(m->qkv, m->att, (uint32_t)t, w, (uint32_t)m->heads, group, scale); break;
-    case 16: attention_kernel<16><<<grid, 64, 0, s>>>(m->qkv, m->att, (uint32_t)t, w, (uint32_t)m->heads, group, scale); break;
-    case 32: attention_kernel<32><<<grid, 64, 0, s>>>(m->qkv, m->att, (uint32_t)t, w, (uint32_t)m->heads, group, scale); break;
-    case 64: attention_kernel<64><<<grid, 64, 0, s>>>(m->qkv, m->att, (uint32_t)t, w, (uint32_t)m->heads, group, scale); break;
-    default: attention_kernel<128><<<grid, 64, 0, s>>>(m->qkv, m->att, (uint32_t)t, w, (uint32_t)m->heads, group, scale); break;
+    case 8: attention_kernel<8, 4><<<grid, 256, 0, s>>>(m->qkv, m->att, T, w, H, group, scale); break;
+    case 16: attention_kernel<16, 4><<<grid, 256, 0, s>>>(m->qkv, m->att, T, w, H, group, scale); break;
+    case 32: attention_kernel<32, 4><<<grid, 256, 0, s>>>(m->qkv, m->att, T, w, H, group, scale); break;
+    case 64: attention_kernel<64, 4><<<grid, 256, 0, s>>>(m->qkv, m->att, T, w, H, group, scale); break;
+    default: attention_kernel<128, 2><<<grid, 128, 0, s>>>(m->qkv, m->att, T, w, H, group, scale); break;
     }
     return hipGetLastError();
 }
