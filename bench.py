@@ -380,6 +380,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the GPT-2-small decode (config 2), one JSON line (for profiling)")
+    ap.add_argument("--gemm-path", default="TiledFast", choices=["Tiled", "TiledFast", "TiledF16"],
+                    help="the GEMM --gemm-only measures")
     ap.add_argument("--score-only", action="store_true",
                     help="only the Qwen2-0.5B Q4_0 scoring forward (config 4), one JSON line (for profiling)")
     ap.add_argument("--gemm-only", action="store_true",
@@ -408,7 +410,7 @@ def main():
         g.close()
         return
     if a.gemm_only:
-        r = bench_gemm(fh, g, ev, fh.QKind.Q4_0, 4096, LLAMA1B_SHAPES, a.steps, path=fh.QPath.TiledFast)
+        r = bench_gemm(fh, g, ev, fh.QKind.Q4_0, 4096, LLAMA1B_SHAPES, a.steps, path=fh.QPath[a.gemm_path])
         print(json.dumps({"metric": "Q4_0 scoring GEMM TFLOP/s, TinyLlama-1.1B layer shapes, M = 4096",
                           "value": round(r["tflops"], 2), "unit": "TFLOP/s", "n_gpus": 1, "higher_is_better": True,
                           "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4), "detail": r}))
@@ -433,7 +435,7 @@ def main():
                                        ("q4_0_gemm_llama1b", fh.QKind.Q4_0, LLAMA1B_SHAPES, (512, 4096)),
                                        ("q8_0_gemm_llama1b", fh.QKind.Q8_0, LLAMA1B_SHAPES, (512, 4096))):
             for m in ms:
-                for tag, path in (("", fh.QPath.TiledFast), ("_precise", fh.QPath.Tiled)):
+                for tag, path in (("", fh.QPath.TiledFast), ("_f16", fh.QPath.TiledF16), ("_precise", fh.QPath.Tiled)):
                     r = bench_gemm(fh, g, ev, kind, m, shapes, 10, path=path)
                     log(f"{name}{tag} M={m}:", r)
                     extra[f"{name}{tag}_m{m}"] = {"tflops": round(r["tflops"], 2),

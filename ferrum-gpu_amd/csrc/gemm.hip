@@ -812,6 +812,264 @@ hipError_t gemm_precise_dispatch(hipStream_t s, const _Float16 *xs, const uint8_
     return run_gemm_precise<KIND, 128, 128, 2>(s, xs, qs, ds, y, M, K, N);
 }
 
+// ---- the dequant-f16 GEMM (FH_PATH_TILED_F16): weights dequantised into LDS, plain f16 MFMA ----
+// x -> f16 of x 2^-s per row (2^s puts the row's largest |x| in [2^14, 2^15), so no element
+// overflows and every one keeps f16's 11 bits), in operand order, and xs[m] = 2^s.
+template <int KIND>
+__global__ __launch_bounds__(256) void split_x_f16_kernel(const float *__restrict__ x, _Float16 *__restrict__ xh,
+                                                          float *__restrict__ xs, uint32_t K) {
+    __shared__ float red[4];
+    const uint32_t m = blockIdx.x, tid = threadIdx.x, nb = K / 32;
+    const float *xr = x + (size_t)m * K;
+    float mx = 0.0f;
+    for (uint32_t i = tid * 4; i < K; i += 1024) {
+        const f32x4 v = *(const f32x4 *)(xr + i);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o /= 2) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (tid % 64 == 0) red[tid / 64] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    // 2^E <= mx < 2^(E+1); s = E - 14
+    int sc = 0;
+    if (mx > 0.0f && mx <= 3.4028235e38f) sc = ((int)(__float_as_uint(mx) >> 23) - 127) - 14;
+    sc = sc < -126 ? -126 : (sc > 126 ? 126 : sc);  // both 2^s and 2^-s stay normal floats
+    const float f = __uint_as_float((uint32_t)(127 - sc) << 23);
+    if (tid == 0) xs[m] = __uint_as_float((uint32_t)(127 + sc) << 23);
+    const int j = tid % 8;
+    for (uint32_t t = tid / 8; t < nb; t += 32) {
+        const f32x4 v = *(const f32x4 *)(xr + t * 32 + 4 * j);
+        _Float16 h[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) h[q] = (_Float16)(v[q] * f);
+        _Float16 *out = xh + ((size_t)m * nb + t) * 32;
+        typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+        if constexpr (KIND == FH_Q8_0) {
+            *(f16x4 *)(out + 4 * j) = f16x4{h[0], h[2], h[1], h[3]};
+        } else {
+            _Float16 o[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                o[q] = __builtin_bit_cast(_Float16, (uint16_t)__shfl_xor((int)__builtin_bit_cast(uint16_t, h[q]), 4, 8));
+            if (j < 4) *(f16x8 *)(out + 8 * j) = f16x8{h[0], h[2], h[1], h[3], o[0], o[2], o[1], o[3]};
+        }
+    }
+}
+
+// f16 pairs times one f16 scale (round to nearest: d q is exact before the rounding)
+__device__ __forceinline__ uint32_t f16x2_mul(uint32_t w, _Float16 d) {
+    const f16x2 v = __builtin_bit_cast(f16x2, w) * f16x2{d, d};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+template <int KIND, int BM, int BN, int WAVES_M>
+struct GemmCfgF16 {
+    static constexpr int WAVES_N = 4 / WAVES_M;
+    static constexpr int TM = BM / WAVES_M / 32, TN = BN / WAVES_N / 32;  // 32x32 tiles per wave
+    static constexpr int QB = KIND == FH_Q8_0 ? 32 : 16;                   // quant bytes per block
+    static constexpr int XH = BM * 8 / 256;                                // 16-byte x chunks per thread
+    static constexpr int QC = BN * 2 * QB / 16;                            // 16-byte quant chunks per stage
+    static constexpr int QL = (QC + 255) / 256;
+    static_assert(TM >= 1 && TN >= 1, "wave tile must be whole 32x32 tiles");
+    static_assert(BM * 8 % 256 == 0, "x staging must divide over 256 threads");
+};
+
+// Per pipeline stage (two blocks, 64 k) a CTA holds x (f16, operand order) and the weights as
+// f16 d q (dequantised while they are stored to LDS); per 32 x 32 output tile and stage four
+// v_mfma_f32_32x32x16_f16 accumulate straight into the f32 result, which the epilogue scales by
+// the row's 2^s. Tile order, register staging two stages ahead and the K split are those of
+// gemm_kernel.
+template <int KIND, int BM, int BN, int WAVES_M>
+__global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const _Float16 *__restrict__ xh, const float *__restrict__ xs,
+                                                          const uint8_t *__restrict__ qs, const uint16_t *__restrict__ ds,
+                                                          float *__restrict__ y, uint32_t M, uint32_t K, uint32_t N,
+                                                          uint32_t mt, uint32_t nt, uint32_t split_stages) {
+    using C = GemmCfgF16<KIND, BM, BN, WAVES_M>;
+    __shared__ __attribute__((aligned(16))) _Float16 sA[BM * kAStr];
+    __shared__ __attribute__((aligned(16))) _Float16 sB[BN * kBStr];
+
+    const uint32_t c = blockIdx.x, xcd = c % 8, u = c / 8;
+    const uint32_t snt = (nt + 7) / 8;
+    const uint32_t sidx = (u / 64) * 8 + xcd, v = u % 64;
+    const uint32_t mi = (sidx / snt) * 8 + v / 8, ni = (sidx % snt) * 8 + v % 8;
+    if (mi >= mt || ni >= nt) return;  // whole CTA: no barrier is left waiting
+    const uint32_t m0 = mi * BM, n0 = ni * BN;
+
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+    const uint32_t nb = K / 32, all_stages = (nb + 1) / 2;
+    const uint32_t st0 = blockIdx.y * split_stages, st1 = min(all_stages, st0 + split_stages);
+    y += (size_t)blockIdx.y * M * N;
+    const int fr = lane % 32, fk = 8 * (lane / 32);
+
+    const auto r_xh = make_rsrc(xh, M * nb * 64);
+    const auto r_q = make_rsrc(qs, (N + 31) / 32 * 32 * nb * C::QB);
+    const auto r_d = make_rsrc(ds, (N + 31) / 32 * 32 * ((nb + 7) / 8 * 8) * 2);
+    constexpr uint32_t kOut = 0x80000000u;
+    uint32_t o_xh[C::XH], s_xh[C::XH], o_q[C::QL], s_q[C::QL], o_d[C::QL];
+    int bsel[C::QL];
+#pragma unroll
+    for (int i = 0; i < C::XH; i++) {
+        const int cc = tid + 256 * i, r = cc / 8, bb = (cc % 8) / 4, part = cc % 4;
+        const uint32_t m = m0 + r;
+        o_xh[i] = m < M ? ((m * nb + bb) * 32 + part * 8) * 2 : kOut;
+        s_xh[i] = (r * kAStr + bb * 32 + part * 8) * 2;
+    }
+#pragma unroll
+    for (int i = 0; i < C::QL; i++) {
+        const int cc = tid + 256 * i;
+        constexpr int CPB = C::QB / 16;  // 16-byte chunks per block
+        const int col = cc / (2 * CPB), bb = (cc % (2 * CPB)) / CPB, part = cc % CPB;
+        const uint32_t n = n0 + col;
+        o_q[i] = cc < C::QC ? (((n >> 5) * nb + bb) * 32 + (n & 31)) * C::QB + part * 16 : kOut;
+        s_q[i] = cc < C::QC ? (col * kBStr + bb * 32 + (KIND == FH_Q8_0 ? 16 * part : 0)) * 2 : 0u;
+        // the chunk's column's scales of the stage's two blocks (one dword of its run of eight)
+        o_d[i] = cc < C::QC ? (((n >> 5) * ((nb + 7) / 8) * 32 + (n & 31)) * 8) * 2 : kOut;
+        bsel[i] = bb;
+    }
+    u32x4 rxh[2][C::XH], rq[2][C::QL];
+    uint32_t rd[2][C::QL];
+    auto load_stage = [&](uint32_t st, int rs) {
+#pragma unroll
+        for (int i = 0; i < C::XH; i++)
+            rxh[rs][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_xh, (int)(o_xh[i] + st * 128), 0, 0));
+#pragma unroll
+        for (int i = 0; i < C::QL; i++) {
+            rq[rs][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_q, (int)(o_q[i] + st * 64 * C::QB), 0, 0));
+            rd[rs][i] = __builtin_amdgcn_raw_buffer_load_b32(r_d, (int)(o_d[i] + (st >> 2) * 512 + (st & 3) * 4), 0, 0);
+        }
+    };
+    auto store_stage = [&](int rs) {
+        uint8_t *sAb = (uint8_t *)sA, *sBb = (uint8_t *)sB;
+#pragma unroll
+        for (int i = 0; i < C::XH; i++) *(u32x4 *)(sAb + s_xh[i]) = rxh[rs][i];
+#pragma unroll
+        for (int i = 0; i < C::QL; i++) {
+            if (tid + 256 * i < C::QC) {
+                const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(bsel[i] ? rd[rs][i] >> 16 : rd[rs][i] & 0xffffu));
+                if constexpr (KIND == FH_Q8_0) {
+                    u32x4 o[2];
+                    unpack_q8(rq[rs][i], o);
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+#pragma unroll
+                        for (int w = 0; w < 4; w++) o[e][w] = f16x2_mul(o[e][w], d);
+                        *(u32x4 *)(sBb + s_q[i] + 16 * e) = o[e];
+                    }
+                } else {
+                    u32x4 o[4];
+                    unpack_q4(rq[rs][i], o);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+#pragma unroll
+                        for (int w = 0; w < 4; w++) o[e][w] = f16x2_mul(o[e][w], d);
+                        *(u32x4 *)(sBb + s_q[i] + 16 * e) = o[e];
+                    }
+                }
+            }
+        }
+    };
+
+    f32x16 acc[C::TM][C::TN];
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int j = 0; j < C::TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    auto stage = [&](uint32_t st, auto rs_c) {
+        constexpr int rs = decltype(rs_c)::value;
+        __syncthreads();  // every wave is done reading the previous stage
+        store_stage(rs);
+        __syncthreads();
+        if (st + 2 < st1) load_stage(st + 2, rs);  // in flight during the next two stages' MFMAs
+        const int steps = nb - 2 * st < 2u ? 2 : 4;  // k16 steps: an odd last stage has one block
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            if (ks >= steps) break;
+            f16x8 bf[C::TN], ah[C::TM];
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) {
+                const int col = (wn * C::TN + j) * 32 + fr;
+                bf[j] = *(const f16x8 *)(&sB[col * kBStr + 16 * ks + fk]);
+            }
+#pragma unroll
+            for (int i = 0; i < C::TM; i++) {
+                const int r = (wm * C::TM + i) * 32 + fr;
+                ah[i] = *(const f16x8 *)(&sA[r * kAStr + 16 * ks + fk]);
+            }
+#pragma unroll
+            for (int i = 0; i < C::TM; i++)
+#pragma unroll
+                for (int j = 0; j < C::TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+    if (st0 < st1) load_stage(st0, 0);
+    if (st0 + 1 < st1) load_stage(st0 + 1, 1);
+    for (uint32_t st = st0; st < st1; st += 2) {
+        stage(st, std::integral_constant<int, 0>{});
+        if (st + 1 < st1) stage(st + 1, std::integral_constant<int, 1>{});
+    }
+
+#pragma unroll
+    for (int i = 0; i < C::TM; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const uint32_t row = m0 + (wm * C::TM + i) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+            if (row >= M) continue;
+            const float sx = xs[row];
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) {
+                const uint32_t col = n0 + (wn * C::TN + j) * 32 + fr;
+                if (col < N) y[(size_t)row * N + col] = acc[i][j][r] * sx;
+            }
+        }
+}
+
+struct GemmF16Args {
+    const _Float16 *xh;
+    const float *xs;
+    const uint8_t *qs;
+    const uint16_t *ds;
+    float *y, *partial;
+    uint32_t M, K, N;
+};
+
+template <int KIND, int BM, int BN, int WAVES_M>
+hipError_t run_gemm_f16(hipStream_t s, const GemmF16Args &g) {
+    const uint32_t mt = (g.M + BM - 1) / BM, nt = (g.N + BN - 1) / BN;
+    const uint64_t supers = (uint64_t)((mt + 7) / 8) * ((nt + 7) / 8);
+    if (supers * 64 > 0x7fffffffull) return hipErrorInvalidValue;
+    const uint32_t grid = (uint32_t)((supers + 7) / 8 * 8 * 64);
+    const uint32_t stages = (g.K / 32 + 1) / 2;
+    const uint32_t sp = g.partial ? gemm_splits((uint64_t)mt * nt, stages) : 1;
+    const uint32_t per = (stages + sp - 1) / sp;
+    float *out = sp > 1 ? g.partial : g.y;
+    gemm_f16_kernel<KIND, BM, BN, WAVES_M><<<dim3(grid, sp), 256, 0, s>>>(g.xh, g.xs, g.qs, g.ds, out, g.M, g.K, g.N,
+                                                                           mt, nt, per);
+    if (sp > 1) {
+        const size_t n = (size_t)g.M * g.N;
+        const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
+        gemm_reduce_kernel<<<rg, 256, 0, s>>>(g.partial, g.y, n, sp);
+    }
+    return hipGetLastError();
+}
+
+// tile shape by rows: (BM, BN, WAVES_M)
+void f16_tile(size_t rows, size_t *bm, size_t *bn) {
+    *bm = rows <= 32 ? 32 : rows <= 64 ? 64 : 128;
+    *bn = rows <= 32 ? 256 : rows <= 64 ? 128 : 256;
+}
+
+template <int KIND>
+hipError_t gemm_f16_dispatch(hipStream_t s, const GemmF16Args &g) {
+    if (g.M <= 32) return run_gemm_f16<KIND, 32, 256, 1>(s, g);
+    if (g.M <= 64) return run_gemm_f16<KIND, 64, 128, 2>(s, g);
+    return run_gemm_f16<KIND, 128, 256, 2>(s, g);
+}
+
 }  // namespace
 
 // x hi (2 bytes per element), x lo (1 byte), one scale word per row, each piece 256-aligned
@@ -898,6 +1156,45 @@ hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uin
     }
     split_x_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
     return gemm_dispatch<FH_Q4_0>(s, g);
+}
+
+// x as f16 (2 bytes per element), the row scales, then the K-split partials, each 256-aligned
+size_t gemm_f16_workspace_bytes(size_t rows, size_t k, size_t n) {
+    const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    size_t bm, bn;
+    f16_tile(rows, &bm, &bn);
+    const uint64_t tiles = (uint64_t)((rows + bm - 1) / bm) * ((n + bn - 1) / bn);
+    const uint32_t sp = gemm_splits(tiles, (uint32_t)((k / 32 + 1) / 2));
+    return up(rows * k * 2) + up(rows * 4) + (sp > 1 ? (size_t)sp * rows * n * 4 : 0);
+}
+
+bool gemm_f16_supported(size_t rows, size_t k, size_t n) {
+    const size_t lim = (size_t)1 << 31;
+    return rows * k * 2 < lim && (n + 31) / 32 * 32 * (k / 32) * 32 < lim;
+}
+
+hipError_t launch_gemm_f16(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x, float *y,
+                           size_t rows, size_t k, size_t n, void *workspace) {
+    const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    uint8_t *ws = (uint8_t *)workspace;
+    GemmF16Args g;
+    g.xh = (const _Float16 *)ws;
+    g.xs = (const float *)(ws + up(rows * k * 2));
+    g.qs = qs;
+    g.ds = ds;
+    g.y = y;
+    g.partial = gemm_f16_workspace_bytes(rows, k, n) > up(rows * k * 2) + up(rows * 4)
+                    ? (float *)(ws + up(rows * k * 2) + up(rows * 4))
+                    : nullptr;
+    g.M = (uint32_t)rows;
+    g.K = (uint32_t)k;
+    g.N = (uint32_t)n;
+    if (kind == FH_Q8_0) {
+        split_x_f16_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (float *)g.xs, g.K);
+        return gemm_f16_dispatch<FH_Q8_0>(s, g);
+    }
+    split_x_f16_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (float *)g.xs, g.K);
+    return gemm_f16_dispatch<FH_Q4_0>(s, g);
 }
 
 }  // namespace fh

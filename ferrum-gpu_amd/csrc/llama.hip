@@ -18,8 +18,9 @@
 //              SwiGLU                                           -> act [t, hidden]
 //              act . Wdown                                      -> o
 //   x += o, final RMSNorm, h . head (chunks of rows)            -> logits, or straight into score
-// The products are the library's MFMA GEMMs on the packed weights: the precise one (x as two
-// f16 parts, FH_PATH_TILED) or the fast scoring one (FH_PATH_TILED_FAST), chosen at load.
+// The products are the library's MFMA GEMMs on the packed weights, chosen at load: the precise
+// one (x as two f16 parts, FH_PATH_TILED), the fast scoring one (FH_PATH_TILED_FAST) or the
+// dequant-f16 one (FH_PATH_TILED_F16).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -470,7 +471,11 @@ size_t logit_chunk(const fh_llama *m, size_t t) {
 }
 
 size_t linear_ws(const fh_llama *m, size_t rows, size_t k, size_t n) {
-    return m->path == FH_PATH_TILED_FAST ? gemm_workspace_bytes(rows, k, n) : gemm_precise_workspace_bytes(rows, k);
+    switch (m->path) {
+    case FH_PATH_TILED_FAST: return gemm_workspace_bytes(rows, k, n);
+    case FH_PATH_TILED_F16: return gemm_f16_workspace_bytes(rows, k, n);
+    default: return gemm_precise_workspace_bytes(rows, k);
+    }
 }
 
 // The activations for t rows (kept when already large enough).
@@ -514,23 +519,32 @@ fh_status ensure_rows(fh_llama *m, size_t t) {
     return FH_OK;
 }
 
+bool linear_supported(const fh_llama *m, size_t rows, size_t k, size_t n) {
+    switch (m->path) {
+    case FH_PATH_TILED_FAST: return gemm_supported(rows, k, n);
+    case FH_PATH_TILED_F16: return gemm_f16_supported(rows, k, n);
+    default: return true;
+    }
+}
+
 fh_status check_shapes(const fh_llama *m, size_t t) {
-    if (m->path != FH_PATH_TILED_FAST) return FH_OK;
     const size_t d = m->dim;
     const std::pair<size_t, size_t> kn[] = {{d, m->qkv_width()}, {m->q_dim(), d}, {d, 2 * m->hidden}, {m->hidden, d}};
     for (auto p : kn)
-        if (!gemm_supported(t, p.first, p.second))
+        if (!linear_supported(m, t, p.first, p.second))
             return fail(FH_ERR_UNSUPPORTED, "llama: %zu rows exceed the MFMA GEMM's 32-bit offsets for a %zu x %zu weight",
                         t, p.second, p.first);
-    if (!gemm_supported(logit_chunk(m, t), d, m->vocab))
+    if (!linear_supported(m, logit_chunk(m, t), d, m->vocab))
         return fail(FH_ERR_UNSUPPORTED, "llama: the head exceeds the MFMA GEMM's 32-bit offsets");
     return FH_OK;
 }
 
 hipError_t linear(const fh_llama *m, hipStream_t s, const fh_qweight *w, const float *x, float *y, size_t rows) {
-    if (m->path == FH_PATH_TILED_FAST)
-        return launch_gemm(s, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, m->ws);
-    return launch_gemm_precise(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws);
+    switch (m->path) {
+    case FH_PATH_TILED_FAST: return launch_gemm(s, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, m->ws);
+    case FH_PATH_TILED_F16: return launch_gemm_f16(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws);
+    default: return launch_gemm_precise(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws);
+    }
 }
 
 hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t) {
@@ -617,8 +631,8 @@ fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_
     if (!g || !out) return fail(FH_ERR_INVALID, "llama: no file or output");
     *out = nullptr;
     if (path == FH_PATH_AUTO) path = FH_PATH_TILED;
-    if (path != FH_PATH_TILED && path != FH_PATH_TILED_FAST)
-        return fail(FH_ERR_INVALID, "llama: the forward runs on FH_PATH_TILED or FH_PATH_TILED_FAST, not path %d",
+    if (path != FH_PATH_TILED && path != FH_PATH_TILED_FAST && path != FH_PATH_TILED_F16)
+        return fail(FH_ERR_INVALID, "llama: the forward runs on FH_PATH_TILED, TILED_FAST or TILED_F16, not path %d",
                     (int)path);
     const char *a;
     size_t alen;

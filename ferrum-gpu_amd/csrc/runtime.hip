@@ -576,6 +576,16 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
         if (rows) (void)launch_gemm(dev->stream, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, ws);
         return end_command(dev, "linear_q");
     }
+    case FH_PATH_TILED_F16: {
+        if (!gemm_f16_supported(rows, w->k, w->n))
+            return fail(FH_ERR_INVALID, "the MFMA GEMM's 32-bit offsets do not cover %zu rows of a %zu x %zu weight",
+                        rows, w->n, w->k);
+        void *ws = nullptr;
+        if (rows && (st = workspace(dev, gemm_f16_workspace_bytes(rows, w->k, w->n), &ws))) return st;
+        if ((st = begin_command(dev, "linear_q"))) return st;
+        if (rows) (void)launch_gemm_f16(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, ws);
+        return end_command(dev, "linear_q");
+    }
     default:
         return fail(FH_ERR_INVALID, "unknown kernel path %d", (int)path);
     }

@@ -44,12 +44,15 @@ class QKind(enum.IntEnum):
 class QPath(enum.IntEnum):
     """ferrum_wgpu/src/ops/quant.rs:292-305. Tiled is the MFMA dequant-GEMM here (within the
     reference's 1e-5); TiledFast (no counterpart in the reference) is the scoring GEMM with an fp8
-    correction, within the MFMA-GEMM tolerance |g - w| <= 1e-3 + 2e-3 |w|."""
+    correction, within the MFMA-GEMM tolerance |g - w| <= 1e-3 + 2e-3 |w|; TiledF16 (no
+    counterpart either) dequantises the weights to f16 and runs plain f16 MFMA, within the same
+    tolerance."""
     Auto = 0
     Naive = 1
     Gemv = 2
     Tiled = 3
     TiledFast = 4
+    TiledF16 = 5
 
 
 _lib = None

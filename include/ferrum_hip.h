@@ -57,13 +57,17 @@ typedef enum fh_kind { FH_Q4_0 = 2, FH_Q8_0 = 8 } fh_kind;
  * row), TILED = the LDS-staged MFMA dequant-GEMM (any rows; x carried to about 22 bits, within the
  * reference's 1e-5 product tolerance), AUTO = fh_choose. No counterpart in the reference:
  * TILED_FAST = the scoring GEMM (x as f16 plus an fp8 correction on the fp8 matrix cores; within
- * the MFMA-GEMM tolerance |g - w| <= 1e-3 + 2e-3 |w|, about 5e-5 absolute at the scoring shapes). */
+ * the MFMA-GEMM tolerance |g - w| <= 1e-3 + 2e-3 |w|, about 5e-5 absolute at the scoring shapes);
+ * TILED_F16 = the dequant-f16 GEMM (weights dequantised to f16 d*q in LDS, x as f16 with a
+ * power-of-two row scale, plain f16 MFMA with f32 accumulation; each product rounds both operands
+ * to f16, so |g - w| <= 2^-10 sum_k |x_k w_k| roughly, within the MFMA-GEMM tolerance). */
 typedef enum fh_path {
     FH_PATH_AUTO = 0,
     FH_PATH_NAIVE = 1,
     FH_PATH_GEMV = 2,
     FH_PATH_TILED = 3,
-    FH_PATH_TILED_FAST = 4
+    FH_PATH_TILED_FAST = 4,
+    FH_PATH_TILED_F16 = 5
 } fh_path;
 
 typedef struct fh_device fh_device;   /* replaces ferrum_wgpu::device::Gpu */
@@ -317,7 +321,8 @@ FH_API fh_status fh_gpt2_generate(fh_device *dev, fh_gpt2 *m, const int32_t *pro
  * Its CPU counterpart is ferrum_ref's Llama::forward_logits on the decoded weights
  * (ferrum_ref/src/models/llama/mod.rs:166-259) and nn::score (ferrum_ref/src/kernels/nn.rs:117-129).
  * `path` picks the products: FH_PATH_TILED (or AUTO) the precise MFMA GEMM, FH_PATH_TILED_FAST
- * the scoring GEMM (x as f16 + an fp8 correction; its error bound is the one the GEMM states). */
+ * the scoring GEMM (x as f16 + an fp8 correction) or FH_PATH_TILED_F16 the dequant-f16 GEMM; their
+ * error bounds are those fh_path states. */
 typedef struct fh_llama fh_llama;
 typedef struct fh_llama_cfg {
     size_t vocab, ctx, dim, heads, kv_heads, head_dim, layers, hidden, rope_dim;

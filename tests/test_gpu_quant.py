@@ -404,6 +404,68 @@ def test_fast_gemm_is_one_command_and_fails_cleanly(fh, g, orc):
     assert orc.max_rel_err(g.read(y), want) < FAST_BOUND
 
 
+# The dequant-f16 GEMM (QPath.TiledF16, no counterpart in the reference): x rounded to f16 (with a
+# power-of-two row scale, so no element leaves f16's normal range) times f16(d q), f32
+# accumulation. Each product carries two f16 roundings, so against the exact product of the
+# stored weights every output obeys |g - e| <= (2^-10 + K 2^-24) sum_k |x_k w_k| (F16_BOUND
+# below, checked per output), and against the reference's f32 CPU product the MFMA-GEMM
+# tolerance holds in the max norm: max |g - w| <= 1e-3 + 2e-3 max |w|. (Per output, near-zero
+# results at K ~ 5000 can miss 1e-3 + 2e-3 |w|: the f16 roundings alone have a standard
+# deviation of ~4e-4 there; QPath.TiledFast meets that form.)
+def f16_bound(x, wd, m, k, n):
+    return (2.0 ** -10 + k * 2.0 ** -24) * (np.abs(x.astype(np.float64).reshape(m, k)) @
+                                            np.abs(wd.astype(np.float64).reshape(k, n))).reshape(-1)
+
+
+@pytest.mark.parametrize("kind_name,m,k,n", [
+    ("Q4_0", 512, 896, 1152), ("Q4_0", 512, 896, 4864), ("Q4_0", 512, 4864, 896),
+    ("Q8_0", 64, 2048, 5632), ("Q4_0", 8, 5632, 2048), ("Q8_0", 512, 5632, 256),
+    ("Q8_0", 2048, 896, 4864), ("Q4_0", 300, 2080, 200)])
+def test_f16_gemm_meets_its_bounds_at_the_scoring_shapes(fh, g, orc, kind_name, m, k, n):
+    kind = fh.QKind[kind_name]
+    rng = np.random.default_rng(m + k + n)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+    b = orc.quantise_matrix(int(kind), w, k, n)
+    want = cpu_linear(orc, kind, b, x, m, k, n)
+    wd = orc.dequantised_in_out(int(kind), b, k, n)
+    exact = (x.astype(np.float64).reshape(m, k) @ wd.astype(np.float64).reshape(k, n)).reshape(-1)
+    qw = fh.upload_qweight(g, kind, b, k, n)
+    gx, gy = g.upload(x), g.zeros(m * n)
+    say("f16 gemm", kind_name, m, k, n)
+    fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.TiledF16)
+    got = g.read(gy)
+    err = np.abs(got - want)
+    viol = np.mean(err > 1e-3 + 2e-3 * np.abs(want))
+    ratio = (np.abs(got - exact) / f16_bound(x, wd, m, k, n)).max()
+    say(f"  vs cpu: max abs {err.max():.2e} (max |w| {np.abs(want).max():.2f}), per-output violations {viol:.2e}; "
+        f"vs exact: worst error / bound {ratio:.3f}")
+    assert err.max() <= 1e-3 + 2e-3 * np.abs(want).max()
+    assert ratio <= 1.0
+
+
+def test_f16_gemm_on_awkward_shapes_and_values(fh, g, orc):
+    """Odd block counts, partial tiles, the reference's uniform data, rows whose magnitudes differ
+    by up to 1e6 (each row has its own power-of-two scale): every output within its bound."""
+    rng = np.random.default_rng(12)
+    for kind in kinds(fh):
+        for rows, k, n in [(2, 32, 1), (33, 96, 17), (17, 64, 40), (130, 160, 129), (257, 224, 300),
+                           (64, 2080, 70), (5, 4096, 33)]:
+            w = orc.rand_vec(k * n, 6)
+            b = orc.quantise_matrix(int(kind), w, k, n)
+            x = orc.rand_vec(rows * k, 9).reshape(rows, k)
+            x *= (10.0 ** rng.integers(-3, 4, rows)).astype(np.float32)[:, None]
+            x = x.reshape(-1).astype(np.float32)
+            wd = orc.dequantised_in_out(int(kind), b, k, n)
+            exact = (x.astype(np.float64).reshape(rows, k) @ wd.astype(np.float64).reshape(k, n)).reshape(-1)
+            qw = fh.upload_qweight(g, kind, b, k, n)
+            gx, gy = g.upload(x), g.zeros(rows * n)
+            say("f16 kernel", kind.label(), rows, k, n)
+            fh.linear_q_with(g, gx, qw, gy, rows, fh.QPath.TiledF16)
+            ratio = (np.abs(g.read(gy) - exact) / np.maximum(f16_bound(x, wd, rows, k, n), 1e-30)).max()
+            assert ratio <= 1.0, (kind, rows, k, n, ratio)
+
+
 def test_grouped_gemv_plan_equals_single_launches(fh, g, orc):
     """The grouped launch runs the same per-row code: results are bit-identical to linear_q."""
     rng = np.random.default_rng(5)
