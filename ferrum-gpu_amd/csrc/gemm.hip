@@ -863,31 +863,56 @@ __device__ __forceinline__ uint32_t f16x2_mul(uint32_t w, _Float16 d) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-template <int KIND, int BM, int BN, int WAVES_M>
+template <int KIND, int BM, int BN>
 struct GemmCfgF16 {
-    static constexpr int WAVES_N = 4 / WAVES_M;
-    static constexpr int TM = BM / WAVES_M / 32, TN = BN / WAVES_N / 32;  // 32x32 tiles per wave
-    static constexpr int QB = KIND == FH_Q8_0 ? 32 : 16;                   // quant bytes per block
-    static constexpr int XH = BM * 8 / 256;                                // 16-byte x chunks per thread
-    static constexpr int QC = BN * 2 * QB / 16;                            // 16-byte quant chunks per stage
+    static constexpr int TM = BM / 32, TN = BN / 4 / 32;  // 32x32 tiles per wave (4 waves side by side along N)
+    static constexpr int QB = KIND == FH_Q8_0 ? 32 : 16;  // quant bytes per block
+    static constexpr int QD = QB / 4;                     // quant dwords per block
+    static constexpr int BSTR = KIND == FH_Q8_0 ? 18 : 9; // LDS dwords per weight column and stage
+    static constexpr int XH = BM * 8 / 256;               // 16-byte x chunks per thread
+    static constexpr int QC = BN * 2 * QB / 16;           // 16-byte quant chunks per stage
     static constexpr int QL = (QC + 255) / 256;
-    static_assert(TM >= 1 && TN >= 1, "wave tile must be whole 32x32 tiles");
-    static_assert(BM * 8 % 256 == 0, "x staging must divide over 256 threads");
+    static_assert(BN % 128 == 0 && BM % 32 == 0 && BM * 8 % 256 == 0, "tile shape");
 };
 
-// Per pipeline stage (two blocks, 64 k) a CTA holds x (f16, operand order) and the weights as
-// f16 d q (dequantised while they are stored to LDS); per 32 x 32 output tile and stage four
-// v_mfma_f32_32x32x16_f16 accumulate straight into the f32 result, which the epilogue scales by
-// the row's 2^s. Tile order, register staging two stages ahead and the K split are those of
-// gemm_kernel.
-template <int KIND, int BM, int BN, int WAVES_M>
+// 8 operand positions of a Q4_0 block from one quant dword (positions 8i..8i+7 come from dword
+// i: the low nibbles of bytes (0, 2), (1, 3), then the high ones), times the block's scale
+__device__ __forceinline__ f16x8 dequant_q4_frag(uint32_t w, _Float16 d) {
+    u32x4 v;
+    v[0] = f16x2_mul(f16x2_add((w & 0x000f000fu) | 0x64006400u, (_Float16)-1032.0f), d);
+    v[1] = f16x2_mul(f16x2_add(((w >> 8) & 0x000f000fu) | 0x64006400u, (_Float16)-1032.0f), d);
+    v[2] = f16x2_mul(f16x2_add(((w >> 4) & 0x000f000fu) | 0x64006400u, (_Float16)-1032.0f), d);
+    v[3] = f16x2_mul(f16x2_add(((w >> 12) & 0x000f000fu) | 0x64006400u, (_Float16)-1032.0f), d);
+    return __builtin_bit_cast(f16x8, v);
+}
+
+// 8 operand positions of a Q8_0 block from two quant dwords (positions 4j..4j+3 from dword j)
+__device__ __forceinline__ f16x8 dequant_q8_frag(uint32_t w0, uint32_t w1, _Float16 d) {
+    u32x4 v;
+    const uint32_t t0 = w0 ^ 0x80808080u, t1 = w1 ^ 0x80808080u;
+    v[0] = f16x2_mul(f16x2_add(__builtin_amdgcn_perm(0x64646464u, t0, 0x04020400u), (_Float16)-1152.0f), d);
+    v[1] = f16x2_mul(f16x2_add(__builtin_amdgcn_perm(0x64646464u, t0, 0x04030401u), (_Float16)-1152.0f), d);
+    v[2] = f16x2_mul(f16x2_add(__builtin_amdgcn_perm(0x64646464u, t1, 0x04020400u), (_Float16)-1152.0f), d);
+    v[3] = f16x2_mul(f16x2_add(__builtin_amdgcn_perm(0x64646464u, t1, 0x04030401u), (_Float16)-1152.0f), d);
+    return __builtin_bit_cast(f16x8, v);
+}
+
+// Per pipeline stage (two blocks, 64 k) a CTA holds x (f16, operand order) and the weights'
+// packed quants with their scales in LDS, double-buffered: one barrier per stage, the next
+// stage stored to the other buffer and the one after requested from memory while this one
+// computes. Each wavefront owns a BM x BN/4 slab, so every weight fragment is dequantised by
+// exactly one wavefront, in registers (the unpack, one packed f16 subtract and one packed f16
+// multiply per pair: d q exact, then rounded once), right before its
+// v_mfma_f32_32x32x16_f16; results accumulate straight into f32 and the epilogue scales each row
+// by its 2^s. Tile order and the K split are those of gemm_kernel.
+template <int KIND, int BM, int BN>
 __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const _Float16 *__restrict__ xh, const float *__restrict__ xs,
                                                           const uint8_t *__restrict__ qs, const uint16_t *__restrict__ ds,
                                                           float *__restrict__ y, uint32_t M, uint32_t K, uint32_t N,
                                                           uint32_t mt, uint32_t nt, uint32_t split_stages) {
-    using C = GemmCfgF16<KIND, BM, BN, WAVES_M>;
-    __shared__ __attribute__((aligned(16))) _Float16 sA[BM * kAStr];
-    __shared__ __attribute__((aligned(16))) _Float16 sB[BN * kBStr];
+    using C = GemmCfgF16<KIND, BM, BN>;
+    __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * kAStr];
+    __shared__ __attribute__((aligned(16))) uint32_t sB[2][BN * C::BSTR];
 
     const uint32_t c = blockIdx.x, xcd = c % 8, u = c / 8;
     const uint32_t snt = (nt + 7) / 8;
@@ -897,18 +922,16 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const _Float16 *__rest
     const uint32_t m0 = mi * BM, n0 = ni * BN;
 
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-    const int wm = wave % WAVES_M, wn = wave / WAVES_M;
     const uint32_t nb = K / 32, all_stages = (nb + 1) / 2;
     const uint32_t st0 = blockIdx.y * split_stages, st1 = min(all_stages, st0 + split_stages);
     y += (size_t)blockIdx.y * M * N;
-    const int fr = lane % 32, fk = 8 * (lane / 32);
+    const int fr = lane % 32, hf = lane / 32, fk = 8 * hf;
 
     const auto r_xh = make_rsrc(xh, M * nb * 64);
     const auto r_q = make_rsrc(qs, (N + 31) / 32 * 32 * nb * C::QB);
     const auto r_d = make_rsrc(ds, (N + 31) / 32 * 32 * ((nb + 7) / 8 * 8) * 2);
     constexpr uint32_t kOut = 0x80000000u;
-    uint32_t o_xh[C::XH], s_xh[C::XH], o_q[C::QL], s_q[C::QL], o_d[C::QL];
-    int bsel[C::QL];
+    uint32_t o_xh[C::XH], s_xh[C::XH], o_q[C::QL], s_q[C::QL], o_d, s_d;
 #pragma unroll
     for (int i = 0; i < C::XH; i++) {
         const int cc = tid + 256 * i, r = cc / 8, bb = (cc % 8) / 4, part = cc % 4;
@@ -923,52 +946,35 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const _Float16 *__rest
         const int col = cc / (2 * CPB), bb = (cc % (2 * CPB)) / CPB, part = cc % CPB;
         const uint32_t n = n0 + col;
         o_q[i] = cc < C::QC ? (((n >> 5) * nb + bb) * 32 + (n & 31)) * C::QB + part * 16 : kOut;
-        s_q[i] = cc < C::QC ? (col * kBStr + bb * 32 + (KIND == FH_Q8_0 ? 16 * part : 0)) * 2 : 0u;
-        // the chunk's column's scales of the stage's two blocks (one dword of its run of eight)
-        o_d[i] = cc < C::QC ? (((n >> 5) * ((nb + 7) / 8) * 32 + (n & 31)) * 8) * 2 : kOut;
-        bsel[i] = bb;
+        s_q[i] = cc < C::QC ? col * C::BSTR + bb * C::QD + part * 4 : 0u;
     }
-    u32x4 rxh[2][C::XH], rq[2][C::QL];
-    uint32_t rd[2][C::QL];
-    auto load_stage = [&](uint32_t st, int rs) {
+    {
+        const uint32_t n = n0 + tid;  // thread t < BN loads column t's scales of the stage's two blocks
+        o_d = tid < BN ? (((n >> 5) * ((nb + 7) / 8) * 32 + (n & 31)) * 8) * 2 : kOut;
+        s_d = tid * C::BSTR + 2 * C::QD;
+    }
+    u32x4 rxh[C::XH], rq[C::QL];
+    uint32_t rd = 0;
+    auto load_stage = [&](uint32_t st) {
 #pragma unroll
         for (int i = 0; i < C::XH; i++)
-            rxh[rs][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_xh, (int)(o_xh[i] + st * 128), 0, 0));
+            rxh[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_xh, (int)(o_xh[i] + st * 128), 0, 0));
 #pragma unroll
-        for (int i = 0; i < C::QL; i++) {
-            rq[rs][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_q, (int)(o_q[i] + st * 64 * C::QB), 0, 0));
-            rd[rs][i] = __builtin_amdgcn_raw_buffer_load_b32(r_d, (int)(o_d[i] + (st >> 2) * 512 + (st & 3) * 4), 0, 0);
-        }
+        for (int i = 0; i < C::QL; i++)
+            rq[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_q, (int)(o_q[i] + st * 64 * C::QB), 0, 0));
+        rd = __builtin_amdgcn_raw_buffer_load_b32(r_d, (int)(o_d + (st >> 2) * 512 + (st & 3) * 4), 0, 0);
     };
-    auto store_stage = [&](int rs) {
-        uint8_t *sAb = (uint8_t *)sA, *sBb = (uint8_t *)sB;
+    auto store_stage = [&](int buf) {
+        uint8_t *sAb = (uint8_t *)sA[buf];
+        uint32_t *sBb = sB[buf];
 #pragma unroll
-        for (int i = 0; i < C::XH; i++) *(u32x4 *)(sAb + s_xh[i]) = rxh[rs][i];
+        for (int i = 0; i < C::XH; i++) *(u32x4 *)(sAb + s_xh[i]) = rxh[i];
 #pragma unroll
-        for (int i = 0; i < C::QL; i++) {
-            if (tid + 256 * i < C::QC) {
-                const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(bsel[i] ? rd[rs][i] >> 16 : rd[rs][i] & 0xffffu));
-                if constexpr (KIND == FH_Q8_0) {
-                    u32x4 o[2];
-                    unpack_q8(rq[rs][i], o);
+        for (int i = 0; i < C::QL; i++)
+            if (tid + 256 * i < C::QC)
 #pragma unroll
-                    for (int e = 0; e < 2; e++) {
-#pragma unroll
-                        for (int w = 0; w < 4; w++) o[e][w] = f16x2_mul(o[e][w], d);
-                        *(u32x4 *)(sBb + s_q[i] + 16 * e) = o[e];
-                    }
-                } else {
-                    u32x4 o[4];
-                    unpack_q4(rq[rs][i], o);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-#pragma unroll
-                        for (int w = 0; w < 4; w++) o[e][w] = f16x2_mul(o[e][w], d);
-                        *(u32x4 *)(sBb + s_q[i] + 16 * e) = o[e];
-                    }
-                }
-            }
-        }
+                for (int w = 0; w < 4; w++) sBb[s_q[i] + w] = rq[i][w];
+        if (tid < BN) sBb[s_d] = rd;
     };
 
     f32x16 acc[C::TM][C::TN];
@@ -979,50 +985,57 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const _Float16 *__rest
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    auto stage = [&](uint32_t st, auto rs_c) {
-        constexpr int rs = decltype(rs_c)::value;
-        __syncthreads();  // every wave is done reading the previous stage
-        store_stage(rs);
-        __syncthreads();
-        if (st + 2 < st1) load_stage(st + 2, rs);  // in flight during the next two stages' MFMAs
+    if (st0 < st1) {
+        load_stage(st0);
+        store_stage(0);
+        if (st0 + 1 < st1) load_stage(st0 + 1);
+    }
+    for (uint32_t st = st0; st < st1; st++) {
+        const int buf = (st - st0) & 1;
+        __syncthreads();  // stage st is in buf; every wave is done with the other buffer
+        if (st + 1 < st1) {
+            store_stage(buf ^ 1);
+            if (st + 2 < st1) load_stage(st + 2);  // in flight during this stage's MFMAs
+        }
+        const _Float16 *a = sA[buf];
+        const uint32_t *bq = sB[buf];
         const int steps = nb - 2 * st < 2u ? 2 : 4;  // k16 steps: an odd last stage has one block
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             if (ks >= steps) break;
+            const int bb = ks / 2, s2 = ks % 2;
             f16x8 bf[C::TN], ah[C::TM];
 #pragma unroll
             for (int j = 0; j < C::TN; j++) {
-                const int col = (wn * C::TN + j) * 32 + fr;
-                bf[j] = *(const f16x8 *)(&sB[col * kBStr + 16 * ks + fk]);
+                const uint32_t *cp = bq + ((wave * C::TN + j) * 32 + fr) * C::BSTR;
+                const uint32_t dd = cp[2 * C::QD];
+                const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(bb ? dd >> 16 : dd & 0xffffu));
+                if constexpr (KIND == FH_Q8_0) {
+                    const uint32_t *w = cp + bb * C::QD + 2 * (2 * s2 + hf);
+                    bf[j] = dequant_q8_frag(w[0], w[1], d);
+                } else {
+                    bf[j] = dequant_q4_frag(cp[bb * C::QD + 2 * s2 + hf], d);
+                }
             }
 #pragma unroll
-            for (int i = 0; i < C::TM; i++) {
-                const int r = (wm * C::TM + i) * 32 + fr;
-                ah[i] = *(const f16x8 *)(&sA[r * kAStr + 16 * ks + fk]);
-            }
+            for (int i = 0; i < C::TM; i++) ah[i] = *(const f16x8 *)(&a[(i * 32 + fr) * kAStr + 16 * ks + fk]);
 #pragma unroll
             for (int i = 0; i < C::TM; i++)
 #pragma unroll
                 for (int j = 0; j < C::TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bf[j], acc[i][j], 0, 0, 0);
         }
-    };
-    if (st0 < st1) load_stage(st0, 0);
-    if (st0 + 1 < st1) load_stage(st0 + 1, 1);
-    for (uint32_t st = st0; st < st1; st += 2) {
-        stage(st, std::integral_constant<int, 0>{});
-        if (st + 1 < st1) stage(st + 1, std::integral_constant<int, 1>{});
     }
 
 #pragma unroll
     for (int i = 0; i < C::TM; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const uint32_t row = m0 + (wm * C::TM + i) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+            const uint32_t row = m0 + i * 32 + 8 * (r / 4) + 4 * hf + r % 4;
             if (row >= M) continue;
             const float sx = xs[row];
 #pragma unroll
             for (int j = 0; j < C::TN; j++) {
-                const uint32_t col = n0 + (wn * C::TN + j) * 32 + fr;
+                const uint32_t col = n0 + (wave * C::TN + j) * 32 + fr;
                 if (col < N) y[(size_t)row * N + col] = acc[i][j][r] * sx;
             }
         }
@@ -1037,7 +1050,7 @@ struct GemmF16Args {
     uint32_t M, K, N;
 };
 
-template <int KIND, int BM, int BN, int WAVES_M>
+template <int KIND, int BM, int BN>
 hipError_t run_gemm_f16(hipStream_t s, const GemmF16Args &g) {
     const uint32_t mt = (g.M + BM - 1) / BM, nt = (g.N + BN - 1) / BN;
     const uint64_t supers = (uint64_t)((mt + 7) / 8) * ((nt + 7) / 8);
@@ -1047,8 +1060,8 @@ hipError_t run_gemm_f16(hipStream_t s, const GemmF16Args &g) {
     const uint32_t sp = g.partial ? gemm_splits((uint64_t)mt * nt, stages) : 1;
     const uint32_t per = (stages + sp - 1) / sp;
     float *out = sp > 1 ? g.partial : g.y;
-    gemm_f16_kernel<KIND, BM, BN, WAVES_M><<<dim3(grid, sp), 256, 0, s>>>(g.xh, g.xs, g.qs, g.ds, out, g.M, g.K, g.N,
-                                                                           mt, nt, per);
+    gemm_f16_kernel<KIND, BM, BN><<<dim3(grid, sp), 256, 0, s>>>(g.xh, g.xs, g.qs, g.ds, out, g.M, g.K, g.N, mt, nt,
+                                                                  per);
     if (sp > 1) {
         const size_t n = (size_t)g.M * g.N;
         const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
@@ -1057,17 +1070,17 @@ hipError_t run_gemm_f16(hipStream_t s, const GemmF16Args &g) {
     return hipGetLastError();
 }
 
-// tile shape by rows: (BM, BN, WAVES_M)
+// tile shape by rows
 void f16_tile(size_t rows, size_t *bm, size_t *bn) {
     *bm = rows <= 32 ? 32 : rows <= 64 ? 64 : 128;
-    *bn = rows <= 32 ? 256 : rows <= 64 ? 128 : 256;
+    *bn = 256;
 }
 
 template <int KIND>
 hipError_t gemm_f16_dispatch(hipStream_t s, const GemmF16Args &g) {
-    if (g.M <= 32) return run_gemm_f16<KIND, 32, 256, 1>(s, g);
-    if (g.M <= 64) return run_gemm_f16<KIND, 64, 128, 2>(s, g);
-    return run_gemm_f16<KIND, 128, 256, 2>(s, g);
+    if (g.M <= 32) return run_gemm_f16<KIND, 32, 256>(s, g);
+    if (g.M <= 64) return run_gemm_f16<KIND, 64, 256>(s, g);
+    return run_gemm_f16<KIND, 128, 256>(s, g);
 }
 
 }  // namespace
