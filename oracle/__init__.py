@@ -17,8 +17,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, F16, Q4_0, Q8_0 = 0, 1, 2, 8
-QK = 32
-BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
+Q4_1, Q5_0, Q5_1, Q8_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, MXFP4 = 3, 6, 7, 9, 10, 11, 12, 13, 14, 39
+FP8_E4M3, FP8_E5M2 = 1024, 1025  # no ggml type (ferrum_wgpu/src/ops/quant.rs:38-41); the oracle's own ids
+QK, QK_K = 32, 256
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18, F16: 64, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_1: 36, Q2_K: 84, Q3_K: 110, Q4_K: 144,
+               Q5_K: 176, Q6_K: 210, MXFP4: 17, FP8_E4M3: 34, FP8_E5M2: 34}
+BLOCK_ELEMS = {t: (QK_K if t in (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K) else QK) for t in BLOCK_BYTES}
 
 _lib = None
 
@@ -54,6 +58,12 @@ def lib() -> ctypes.CDLL:
             "fo_gpt2_cache_new": (P, [P]),
             "fo_gpt2_cache_free": (None, [P, P]),
             "fo_gpt2_feed": (ctypes.c_int, [P, P, S, P]),
+            "fo_layout": (ctypes.c_int, [U32, P, P]),
+            "fo_dequant": (ctypes.c_int, [U32, P, S, P]),
+            "fo_fp8_decode": (ctypes.c_float, [ctypes.c_int, ctypes.c_uint8]),
+            "fo_fp8_encode": (ctypes.c_uint8, [ctypes.c_int, ctypes.c_float]),
+            "fo_mxfp4_half_scale": (ctypes.c_float, [ctypes.c_uint8]),
+            "fo_q2k_nearest_int": (ctypes.c_int32, [ctypes.c_float]),
             "fo_rope_tables": (None, [S, S, S, ctypes.c_float, P, ctypes.c_float, P, P]),
             "fo_rmsnorm": (None, [P, P, S, S, ctypes.c_float, P]),
             "fo_apply_rope": (None, [P, S, S, S, S, P, P, ctypes.c_int]),
@@ -115,13 +125,16 @@ def decode(ty: int, data: np.ndarray, n: int) -> np.ndarray:
 
 
 def encode(ty: int, data) -> np.ndarray:
-    """ferrum_gguf/src/codec/quant.rs:91-136"""
+    """ferrum_gguf/src/codec/quant.rs:91-136 (q2k.rs, mxfp4.rs, fp8.rs for those formats)."""
     data = _f32(data)
     nb = nbytes(ty, data.size)
     if nb < 0:
-        raise ValueError(f"{data.size} elements is not a multiple of the block size 32")
+        raise ValueError(f"{data.size} elements is not a multiple of the block size {BLOCK_ELEMS.get(ty, QK)}")
     out = np.empty(nb, np.uint8)
-    if lib().fo_encode(ty, _p(data), data.size, _p(out)) != 0:
+    rc = lib().fo_encode(ty, _p(data), data.size, _p(out))
+    if rc == -2:
+        raise ValueError(f"tensor type {ty} is read-only: it can be loaded but not written")
+    if rc != 0:
         raise ValueError("encode failed")
     return out
 
@@ -135,11 +148,12 @@ def transpose(a, rows: int, cols: int) -> np.ndarray:
 
 
 def quantise_matrix(ty: int, w, k: int, n: int) -> np.ndarray:
-    """ferrum_wgpu/src/ops/quant.rs:238-252: [k, n] f32 -> GGUF rows [n][k/32]."""
+    """ferrum_wgpu/src/ops/quant.rs:238-252: [k, n] f32 -> GGUF rows [n][k/elems]."""
     w = _f32(w)
-    if k == 0 or k % QK or w.size != k * n:
-        raise ValueError(f"cannot quantise {w.size} elements as a {k} x {n} weight")
-    out = np.empty(n * (k // QK) * BLOCK_BYTES[ty], np.uint8)
+    e = BLOCK_ELEMS.get(ty, QK)
+    if k == 0 or k % e or w.size != k * n:
+        raise ValueError(f"cannot quantise {w.size} elements as a {k} x {n} weight in whole {e}-blocks")
+    out = np.empty(n * (k // e) * BLOCK_BYTES[ty], np.uint8)
     if lib().fo_quantise_matrix(ty, _p(w), k, n, _p(out)) != 0:
         raise ValueError("quantise failed")
     return out
@@ -441,3 +455,25 @@ def llama_score(m: dict, ids, threads: int = 1):
         raise ValueError("scoring needs at least 2 tokens")
     logits = llama_forward(m, ids[:-1], threads)
     return score(logits, ids[1:], m["vocab"])
+
+
+# ---- formats beyond Q8_0 / Q4_0 (oracle/formats.c) ----
+
+def fp8_decode(e5m2: bool, code: int) -> float:
+    """ferrum_gguf/src/codec/fp8.rs:34-63"""
+    return lib().fo_fp8_decode(int(e5m2), code)
+
+
+def fp8_encode(e5m2: bool, x: float) -> int:
+    """ferrum_gguf/src/codec/fp8.rs:65-96"""
+    return lib().fo_fp8_encode(int(e5m2), x)
+
+
+def mxfp4_half_scale(e: int) -> float:
+    """ferrum_gguf/src/codec/mxfp4.rs:26-33"""
+    return lib().fo_mxfp4_half_scale(e)
+
+
+def q2k_nearest_int(x: float) -> int:
+    """ferrum_gguf/src/codec/q2k.rs:16-19"""
+    return lib().fo_q2k_nearest_int(x)

@@ -3,6 +3,7 @@
  * reference's frozen tolerance (products). Compiled with -ffp-contract=off: Rust never fuses
  * a*b+c, so neither may this file. */
 #include "oracle.h"
+#include "formats.h"
 
 #include <math.h>
 #include <pthread.h>
@@ -61,8 +62,10 @@ uint16_t fo_f32_to_f16(float x) {
     return (uint16_t)(sign | (half + round)); /* a carry into the exponent rounds up a binade */
 }
 
-/* ferrum_gguf/src/codec/quant.rs:17-47 (the four types this path handles). */
+/* ferrum_gguf/src/codec/quant.rs:17-47, with the block types of blocks.rs:34-48 and FP8. */
 int64_t fo_nbytes(uint32_t ty, size_t n) {
+    size_t bb, be;
+    if (fo_layout(ty, &bb, &be)) return n % be ? -1 : (int64_t)(n / be * bb);
     switch (ty) {
     case FO_F32: return (int64_t)n * 4;
     case FO_F16: return (int64_t)n * 2;
@@ -82,6 +85,8 @@ static float half_at(const uint8_t *b) { return fo_f16_to_f32((uint16_t)(b[0] | 
 int fo_decode(uint32_t ty, const uint8_t *bytes, size_t len, size_t n, float *out) {
     int64_t need = fo_nbytes(ty, n);
     if (need < 0 || (size_t)need != len) return -1;
+    size_t bb, be;
+    if (fo_layout(ty, &bb, &be)) return fo_dequant(ty, bytes, n / be, out);
     switch (ty) {
     case FO_F32:
         memcpy(out, bytes, n * 4);
@@ -158,9 +163,18 @@ static void encode_q4_0_block(const float *v, uint8_t *out) {
     }
 }
 
-/* ferrum_gguf/src/codec/quant.rs:91-136 */
+/* ferrum_gguf/src/codec/quant.rs:91-136 (Q2_K and MXFP4 by q2k.rs / mxfp4.rs, FP8 by fp8.rs; the
+ * other block types are read-only: -2). */
 int fo_encode(uint32_t ty, const float *data, size_t n, uint8_t *out) {
     if (fo_nbytes(ty, n) < 0) return -1;
+    switch (ty) {
+    case FO_Q2_K: fo_q2k_encode_blocks(data, n / 256, out); return 0;
+    case FO_MXFP4: fo_mxfp4_encode_blocks(data, n / 32, out); return 0;
+    case FO_FP8_E4M3: fo_fp8_encode_blocks(0, data, n / 32, out); return 0;
+    case FO_FP8_E5M2: fo_fp8_encode_blocks(1, data, n / 32, out); return 0;
+    default:
+        if (fo_layout(ty, NULL, NULL)) return -2;
+    }
     switch (ty) {
     case FO_F32:
         memcpy(out, data, n * 4);
@@ -190,7 +204,12 @@ void fo_transpose(const float *data, size_t rows, size_t cols, float *out) {
 
 /* ferrum_wgpu/src/ops/quant.rs:238-252 */
 int fo_quantise_matrix(uint32_t ty, const float *w, size_t k, size_t n, uint8_t *out) {
-    if (k == 0 || k % FO_QK || (ty != FO_Q8_0 && ty != FO_Q4_0)) return -1;
+    size_t be = FO_QK;
+    if (ty != FO_Q8_0 && ty != FO_Q4_0 && ty != FO_F16 && ty != FO_Q2_K && ty != FO_MXFP4 && ty != FO_FP8_E4M3 &&
+        ty != FO_FP8_E5M2)
+        return -1;
+    fo_layout(ty, NULL, &be);
+    if (k == 0 || k % be) return -1;
     float *rows = (float *)malloc(k * n * sizeof(float) + 1);
     if (!rows) return -1;
     fo_transpose(w, k, n, rows);
