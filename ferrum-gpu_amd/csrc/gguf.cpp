@@ -523,8 +523,10 @@ fh_status fh_gguf_upload_qweight(fh_device *dev, const fh_gguf *g, const char *n
     fh_status st = lookup(g, name, &t);
     if (st) return st;
     if (!out) return fail(FH_ERR_INVALID, "gguf: no output");
-    if (t->type != FH_GGML_Q8_0 && t->type != FH_GGML_Q4_0)
-        return fail(FH_ERR_UNSUPPORTED, "gguf: tensor '%s' has ggml type %u, not Q8_0 or Q4_0", name, t->type);
+    if (t->type != FH_GGML_Q8_0 && t->type != FH_GGML_Q4_0 && !ext_kind((int)t->type))
+        return fail(FH_ERR_UNSUPPORTED,
+                    "gguf: tensor '%s' has ggml type %u, not a weight format (Q8_0, Q4_0, F16, MXFP4, Q2_K)", name,
+                    t->type);
     uint64_t n = 1;
     for (uint32_t d = 1; d < t->nd; d++) n *= t->dims[d];  // no overflow: the parse bounded the product
     const uint8_t *data;
@@ -548,6 +550,16 @@ fh_status fh_gguf_upload_f32(fh_device *dev, const fh_gguf *g, const char *name,
     case FH_GGML_F16:
     case FH_GGML_Q8_0:
     case FH_GGML_Q4_0: break;
+    case FH_GGML_Q4_1:
+    case FH_GGML_Q5_0:
+    case FH_GGML_Q5_1:
+    case FH_GGML_Q8_1:
+    case FH_GGML_Q2_K:
+    case FH_GGML_Q3_K:
+    case FH_GGML_Q4_K:
+    case FH_GGML_Q5_K:
+    case FH_GGML_Q6_K:
+    case FH_GGML_MXFP4: break;  // fh_decode's block decoders (formats.hip)
     case FH_GGML_I16:
     case FH_GGML_I32:
         return fail(FH_ERR_INVALID, "gguf: integer tensors have no f32 form; read them with tensor_bytes");

@@ -137,6 +137,17 @@ hipError_t launch_gguf_to_planes(hipStream_t s, fh_kind kind, const uint8_t *src
 hipError_t launch_planes_to_gguf(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds,
                                  uint8_t *dst, size_t n, size_t nb);
 
+// formats.hip: F16, MXFP4, FP8 E4M3 / E5M2, Q2_K weights (GGUF rows, decoded on the fly) and the
+// read-only block types (decode)
+bool ext_kind(int kind);                                               // a weight format of formats.hip
+bool ext_layout(uint32_t ty, size_t *block_bytes, size_t *block_elems);  // any type formats.hip decodes
+const char *ext_label(int kind);
+hipError_t launch_decode_ext(hipStream_t s, uint32_t ty, const uint8_t *src, float *dst, size_t n);
+hipError_t launch_encode_ext(hipStream_t s, int kind, const float *src, uint8_t *dst, size_t n);
+hipError_t launch_transpose(hipStream_t s, const float *src, float *dst, size_t rows, size_t cols);
+hipError_t launch_linear_ext(hipStream_t s, int kind, fh_path path, const uint8_t *w, const float *x, float *y,
+                             size_t rows, size_t k, size_t n);
+
 // gemv.hip
 struct GemvDesc {          // one batch-1 product, as the kernels read it
     const uint8_t *qs;     // quant plane

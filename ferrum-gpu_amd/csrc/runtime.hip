@@ -182,7 +182,38 @@ fh_status need(const char *name, const fh_buffer *b, size_t want) {
     return FH_OK;
 }
 
+// A weight of a formats.hip kind: its GGUF rows as they are.
+fh_status new_ext_qweight(fh_device *dev, fh_kind kind, size_t k, size_t n, fh_qweight **out) {
+    size_t bb, be;
+    ext_layout(kind, &bb, &be);
+    if (k == 0 || k % be)
+        return fail(FH_ERR_INVALID, "a %zu x %zu weight is not whole %zu-element blocks", k, n, be);
+    if (n == 0 || n > (1u << 30) || k > (1u << 30) || (k / be) * n > (1ull << 32))
+        return fail(FH_ERR_INVALID, "a %zu x %zu weight is out of range", k, n);
+    const size_t nbytes = (k / be) * n * bb;
+    void *p = nullptr;
+    fh_status st = alloc_bytes(dev, nbytes, &p);
+    if (st) return st;
+    fh_qweight *w = new (std::nothrow) fh_qweight;
+    if (!w) {
+        (void)hipFree(p);
+        return fail(FH_ERR_OOM, "host out of memory");
+    }
+    dev_retain(dev);
+    w->dev = dev;
+    w->kind = kind;
+    w->k = k;
+    w->n = n;
+    w->ptr = (uint8_t *)p;
+    w->qs = (uint8_t *)p;
+    w->ds = nullptr;
+    w->nbytes = nbytes;
+    *out = w;
+    return FH_OK;
+}
+
 fh_status new_qweight(fh_device *dev, fh_kind kind, size_t k, size_t n, fh_qweight **out) {
+    if (ext_kind(kind)) return new_ext_qweight(dev, kind, k, n, out);
     if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
     if (k == 0 || k % QK)
         return fail(FH_ERR_INVALID, "a %zu x %zu weight is not whole 32-element blocks", k, n);
@@ -378,6 +409,14 @@ fh_status fh_copy_f32(fh_device *dev, const fh_buffer *src, size_t src_off, fh_b
 // ---- device codec ----
 
 size_t fh_nbytes(fh_kind kind, size_t n) {
+    size_t bb, be;
+    if (!kind_ok(kind) && ext_layout(kind, &bb, &be)) {
+        if (n % be) {
+            fail(FH_ERR_INVALID, "%zu elements is not a multiple of the block size %zu", n, be);
+            return 0;
+        }
+        return n / be * bb;
+    }
     if (!kind_ok(kind)) {
         fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
         return 0;
@@ -392,6 +431,17 @@ size_t fh_nbytes(fh_kind kind, size_t n) {
 fh_status fh_encode(fh_device *dev, fh_kind kind, const fh_buffer *src, size_t n, fh_buffer *dst) {
     fh_status st = check_dev(dev);
     if (st) return st;
+    size_t bb, be;
+    if (!kind_ok(kind) && ext_layout(kind, &bb, &be)) {
+        if (!ext_kind(kind))
+            return fail(FH_ERR_UNSUPPORTED, "tensor type %d is read-only: it can be loaded but not written", (int)kind);
+        if (n % be) return fail(FH_ERR_INVALID, "%zu elements is not a multiple of the block size %zu", n, be);
+        if (!src || !dst || src->nbytes < n * 4 || dst->nbytes < n / be * bb)
+            return fail(FH_ERR_INVALID, "encode: buffers too small for %zu elements", n);
+        if ((st = begin_command(dev, "encode"))) return st;
+        (void)launch_encode_ext(dev->stream, kind, (const float *)src->ptr, (uint8_t *)dst->ptr, n);
+        return end_command(dev, "encode");
+    }
     if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
     if (n % QK) return fail(FH_ERR_INVALID, "%zu elements is not a multiple of the block size 32", n);
     if (!src || !dst || src->nbytes < n * 4 || dst->nbytes < n / QK * block_bytes(kind))
@@ -404,6 +454,15 @@ fh_status fh_encode(fh_device *dev, fh_kind kind, const fh_buffer *src, size_t n
 fh_status fh_decode(fh_device *dev, fh_kind kind, const fh_buffer *src, size_t n, fh_buffer *dst) {
     fh_status st = check_dev(dev);
     if (st) return st;
+    size_t bb, be;
+    if (!kind_ok(kind) && ext_layout(kind, &bb, &be)) {
+        if (n % be) return fail(FH_ERR_INVALID, "%zu elements is not a multiple of the block size %zu", n, be);
+        if (!src || !dst || src->nbytes < n / be * bb || dst->nbytes < n * 4)
+            return fail(FH_ERR_INVALID, "decode: buffers too small for %zu elements", n);
+        if ((st = begin_command(dev, "decode"))) return st;
+        (void)launch_decode_ext(dev->stream, kind, (const uint8_t *)src->ptr, (float *)dst->ptr, n);
+        return end_command(dev, "decode");
+    }
     if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
     if (n % QK) return fail(FH_ERR_INVALID, "%zu elements is not a multiple of the block size 32", n);
     if (!src || !dst || src->nbytes < n / QK * block_bytes(kind) || dst->nbytes < n * 4)
@@ -419,6 +478,22 @@ fh_status fh_qweight_upload_gguf(fh_device *dev, fh_kind kind, const uint8_t *by
                                  size_t k, size_t n, fh_qweight **out) {
     fh_status st = check_dev(dev);
     if (st) return st;
+    if (ext_kind(kind)) {  // kept as the GGUF rows
+        size_t bb, be;
+        ext_layout(kind, &bb, &be);
+        if (k == 0 || k % be)
+            return fail(FH_ERR_INVALID, "a %zu x %zu weight is not whole %zu-element blocks", k, n, be);
+        const size_t want = k / be * n * bb;
+        if (len != want)
+            return fail(FH_ERR_INVALID, "%zu bytes is not the %zu a %zu x %zu %s weight needs", len, want, k, n,
+                        ext_label(kind));
+        if ((st = new_qweight(dev, kind, k, n, out))) return st;
+        if ((st = upload_bytes(dev, (*out)->qs, bytes, len, "upload_qweight"))) {
+            fh_qweight_free(*out);
+            *out = nullptr;
+        }
+        return st;
+    }
     if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
     if (k == 0 || k % QK)
         return fail(FH_ERR_INVALID, "a %zu x %zu weight is not whole 32-element blocks", k, n);
@@ -449,6 +524,28 @@ fh_status fh_qweight_quantise(fh_device *dev, fh_kind kind, const fh_buffer *w, 
                               fh_qweight **out) {
     fh_status st = check_dev(dev);
     if (st) return st;
+    if (ext_kind(kind)) {  // transpose to GGUF rows, then encode them
+        size_t bb, be;
+        ext_layout(kind, &bb, &be);
+        if (k == 0 || k % be || !w || w->nbytes / 4 != k * n)
+            return fail(FH_ERR_INVALID, "cannot quantise %zu elements as a %zu x %zu weight in whole %zu-blocks",
+                        w ? w->nbytes / 4 : 0, k, n, be);
+        if ((st = new_qweight(dev, kind, k, n, out))) return st;
+        void *rows = nullptr;
+        if ((st = alloc_bytes(dev, k * n * 4, &rows)) == FH_OK) {
+            if ((st = begin_command(dev, "quantise_matrix")) == FH_OK) {
+                (void)launch_transpose(dev->stream, (const float *)w->ptr, (float *)rows, k, n);
+                (void)launch_encode_ext(dev->stream, kind, (const float *)rows, (*out)->qs, k * n);
+                st = end_command(dev, "quantise_matrix");
+            }
+            free_bytes(dev, rows);  // waits for the encode
+        }
+        if (st) {
+            fh_qweight_free(*out);
+            *out = nullptr;
+        }
+        return st;
+    }
     if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
     if (k == 0 || k % QK || !w || w->nbytes / 4 != k * n)
         return fail(FH_ERR_INVALID,
@@ -470,11 +567,14 @@ fh_status fh_qweight_upload_f32(fh_device *dev, fh_kind kind, const float *w, si
                                 fh_qweight **out) {
     fh_status st = check_dev(dev);
     if (st) return st;
-    if (!kind_ok(kind)) return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
-    if (k == 0 || k % QK)
+    if (!kind_ok(kind) && !ext_kind(kind))
+        return fail(FH_ERR_UNSUPPORTED, "unsupported block format %d", (int)kind);
+    size_t be = QK;
+    if (ext_kind(kind)) ext_layout(kind, nullptr, &be);
+    if (k == 0 || k % be)
         return fail(FH_ERR_INVALID,
-                    "cannot quantise %zu elements as a %zu x %zu weight in whole 32-blocks",
-                    k * n, k, n);
+                    "cannot quantise %zu elements as a %zu x %zu weight in whole %zu-blocks",
+                    k * n, k, n, be);
     fh_buffer *tmp = nullptr;
     if ((st = fh_buffer_upload(dev, w, k * n, &tmp))) return st;
     st = fh_qweight_quantise(dev, kind, tmp, k, n, out);
@@ -502,6 +602,7 @@ fh_status fh_qweight_read_gguf(fh_device *dev, const fh_qweight *w, uint8_t *hos
     if (!w || len != w->nbytes)
         return fail(FH_ERR_INVALID, "read_gguf: %zu bytes requested, the weight holds %zu", len,
                     w ? w->nbytes : 0);
+    if (ext_kind(w->kind)) return read_bytes(dev, host, w->qs, len, "read_gguf");
     void *stage = nullptr;
     if ((st = alloc_bytes(dev, len, &stage))) return st;
     if ((st = begin_command(dev, "read_gguf")) == FH_OK) {
@@ -517,6 +618,17 @@ fh_status fh_qweight_dequantise(fh_device *dev, const fh_qweight *w, fh_buffer *
     if (st) return st;
     if (!w) return fail(FH_ERR_INVALID, "dequantise: no weight");
     if ((st = need("dequantise out", out, w->k * w->n))) return st;
+    if (ext_kind(w->kind)) {  // decode the rows, then transpose to [k, n]
+        void *rows = nullptr;
+        if ((st = alloc_bytes(dev, w->k * w->n * 4, &rows))) return st;
+        if ((st = begin_command(dev, "dequantise")) == FH_OK) {
+            (void)launch_decode_ext(dev->stream, w->kind, w->qs, (float *)rows, w->k * w->n);
+            (void)launch_transpose(dev->stream, (const float *)rows, (float *)out->ptr, w->n, w->k);
+            st = end_command(dev, "dequantise");
+        }
+        free_bytes(dev, rows);
+        return st;
+    }
     if ((st = begin_command(dev, "dequantise"))) return st;
     (void)launch_decode_cols(dev->stream, w->kind, w->qs, w->ds, (float *)out->ptr, w->k, w->n);
     return end_command(dev, "dequantise");
@@ -526,6 +638,7 @@ fh_status fh_qweight_dequantise(fh_device *dev, const fh_qweight *w, fh_buffer *
 
 fh_path fh_choose(size_t rows, fh_kind kind, size_t k, size_t n) {
     (void)n;
+    if (ext_kind(kind)) return rows == 1 ? FH_PATH_GEMV : FH_PATH_TILED;
     if (rows == 1 && kind_ok(kind) && gemv_supported(kind, k, n)) return FH_PATH_GEMV;
     return FH_PATH_TILED;
 }
@@ -534,6 +647,15 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
                         fh_path path) {
     if (path == FH_PATH_AUTO) path = fh_choose(rows, w->kind, w->k, w->n);
     fh_status st;
+    if (ext_kind(w->kind)) {  // decoded on the fly, f32 products (formats.hip)
+        if (path != FH_PATH_NAIVE && path != FH_PATH_GEMV && path != FH_PATH_TILED)
+            return fail(FH_ERR_UNSUPPORTED, "kernel path %d does not take %s weights", (int)path, ext_label(w->kind));
+        if (path == FH_PATH_GEMV && rows != 1)
+            return fail(FH_ERR_INVALID, "the GEMV kernel takes one row, not %zu", rows);
+        if ((st = begin_command(dev, "linear_q"))) return st;
+        (void)launch_linear_ext(dev->stream, w->kind, path, w->qs, x, y, rows, w->k, w->n);
+        return end_command(dev, "linear_q");
+    }
     switch (path) {
     case FH_PATH_GEMV: {
         if (rows != 1) return fail(FH_ERR_INVALID, "the GEMV kernel takes one row, not %zu", rows);
@@ -635,6 +757,11 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
         if (p.w->dev != dev) {
             fh_gemv_plan_free(plan);
             return fail(FH_ERR_INVALID, "gemv plan: problem %zu lives on another device", i);
+        }
+        if (!kind_ok(p.w->kind)) {
+            fh_gemv_plan_free(plan);
+            return fail(FH_ERR_UNSUPPORTED, "gemv plan: problem %zu is a %s weight; plans take Q8_0 and Q4_0", i,
+                        ext_label(p.w->kind));
         }
         if (!gemv_supported(p.w->kind, p.w->k, p.w->n)) {
             fh_gemv_plan_free(plan);

@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(HERE, "libferrum_hip.so")
 HEADER = os.path.join(os.path.dirname(os.path.dirname(HERE)), "include", "ferrum_hip.h")
 
 QK = 32
+QK_K = 256
 
 
 class GpuError(RuntimeError):
@@ -27,18 +28,33 @@ class GpuError(RuntimeError):
 
 
 class QKind(enum.IntEnum):
-    """ferrum_wgpu/src/ops/quant.rs:27-121 (the two GGUF block formats of this path)."""
+    """ferrum_wgpu/src/ops/quant.rs:27-121, by ggml type id (FP8 has none: 1024 and 1025 are this
+    library's ids). Q8_0 and Q4_0 run on the tiled planes and the MFMA kernels; F16, Fp4 (MXFP4),
+    the FP8 formats and Q2K stay as GGUF rows and are decoded on the fly."""
+    F16 = 1
     Q4_0 = 2
     Q8_0 = 8
+    Q2K = 10
+    Fp4 = 39
+    Fp8E4M3 = 1024
+    Fp8E5M2 = 1025
 
     def label(self) -> str:
-        return "Q8_0" if self == QKind.Q8_0 else "Q4_0"
+        return {QKind.Q8_0: "Q8_0", QKind.Q4_0: "Q4_0", QKind.F16: "F16", QKind.Fp4: "MXFP4",
+                QKind.Fp8E4M3: "FP8 E4M3", QKind.Fp8E5M2: "FP8 E5M2", QKind.Q2K: "Q2_K"}[self]
 
     def elems(self) -> int:
-        return QK
+        """Elements per block along the input axis."""
+        return QK_K if self == QKind.Q2K else QK
 
     def file_bytes(self) -> int:
-        return 34 if self == QKind.Q8_0 else 18
+        """Bytes of one block in a GGUF file (the FP8 formats use Q8_0's layout)."""
+        return {QKind.Q8_0: 34, QKind.Q4_0: 18, QKind.F16: 64, QKind.Fp4: 17, QKind.Fp8E4M3: 34,
+                QKind.Fp8E5M2: 34, QKind.Q2K: 84}[self]
+
+    def ggml(self):
+        """The GGUF tensor type, None for the FP8 formats (llama.cpp has none)."""
+        return None if self in (QKind.Fp8E4M3, QKind.Fp8E5M2) else int(self)
 
 
 class QPath(enum.IntEnum):
@@ -373,6 +389,18 @@ def eligible(k: int) -> bool:
     return k > 0 and k % QK == 0
 
 
+def eligible_for(kind: QKind, k: int) -> bool:
+    """quant.rs:131-134"""
+    return k > 0 and k % QKind(kind).elems() == 0
+
+
+def effective(kind: QKind, k: int) -> QKind:
+    """quant.rs:136-145: Q2_K needs 256-wide blocks; a width of whole 32s uses Q4_0 instead."""
+    if kind == QKind.Q2K and not eligible_for(kind, k) and eligible(k):
+        return QKind.Q4_0
+    return QKind(kind)
+
+
 def nbytes(kind: QKind, n: int) -> int:
     """ferrum_gguf/src/codec/quant.rs:17-47"""
     r = lib().fh_nbytes(int(kind), n)
@@ -382,7 +410,7 @@ def nbytes(kind: QKind, n: int) -> int:
 
 
 def upload_qweight(gpu: Gpu, kind: QKind, data, k: int, n: int) -> QWeight:
-    """quant.rs:267-277: GGUF rows (n rows of k/32 blocks), resident bit-exact."""
+    """quant.rs:267-277: GGUF rows (n rows of k/elems blocks), resident bit-exact."""
     a = np.ascontiguousarray(data, dtype=np.uint8).reshape(-1)
     h = ctypes.c_void_p()
     _check(lib().fh_qweight_upload_gguf(gpu.handle, int(kind), _ptr(a), a.size, k, n, ctypes.byref(h)))
@@ -393,7 +421,8 @@ def upload_quantised(gpu: Gpu, kind: QKind, w, k: int, n: int) -> QWeight:
     """quant.rs:279-288: quantise an [in, out] f32 weight (on the device) and keep it resident."""
     a = _np(w).reshape(-1)
     if a.size != k * n:
-        raise GpuError(f"cannot quantise {a.size} elements as a {k} x {n} weight in whole 32-blocks")
+        raise GpuError(f"cannot quantise {a.size} elements as a {k} x {n} weight in whole "
+                       f"{QKind(kind).elems()}-blocks")
     h = ctypes.c_void_p()
     _check(lib().fh_qweight_upload_f32(gpu.handle, int(kind), _ptr(a), k, n, ctypes.byref(h)))
     return QWeight(gpu, h)

@@ -48,9 +48,29 @@ typedef enum fh_status {
     FH_ERR_LOST = 6         /* the device faulted earlier; sticky */
 } fh_status;
 
-/* Block formats, by ggml tensor type id (ferrum_gguf/src/lib.rs:43,55). Replaces
- * ferrum_wgpu::ops_quant::QKind::{Q8_0, Q4_0} (ferrum_wgpu/src/ops/quant.rs:27-37). */
-typedef enum fh_kind { FH_Q4_0 = 2, FH_Q8_0 = 8 } fh_kind;
+/* Block formats, by ggml tensor type id (ferrum_gguf/src/lib.rs:25-55). Replaces
+ * ferrum_wgpu::ops_quant::QKind (ferrum_wgpu/src/ops/quant.rs:27-121): Q8_0, Q4_0 (the tiled
+ * planes and the MFMA kernels), F16, MXFP4 (Fp4), FP8 E4M3 / E5M2 (no ggml type: the ids 1024 and
+ * 1025 are this library's) and Q2_K (resident as GGUF rows, decoded on the fly, f32 products).
+ * The read-only GGUF block types (ferrum_gguf/src/codec/blocks.rs:34-48) are accepted by
+ * fh_nbytes and fh_decode only. */
+typedef enum fh_kind {
+    FH_F16 = 1,
+    FH_Q4_0 = 2,
+    FH_Q4_1 = 3,
+    FH_Q5_0 = 6,
+    FH_Q5_1 = 7,
+    FH_Q8_0 = 8,
+    FH_Q8_1 = 9,
+    FH_Q2_K = 10,
+    FH_Q3_K = 11,
+    FH_Q4_K = 12,
+    FH_Q5_K = 13,
+    FH_Q6_K = 14,
+    FH_MXFP4 = 39,
+    FH_FP8_E4M3 = 1024,
+    FH_FP8_E5M2 = 1025
+} fh_kind;
 
 /* Which kernel runs a quantized linear layer. Replaces QPath (ferrum_wgpu/src/ops/quant.rs:292-305):
  * NAIVE = one thread per output (the baseline kernel), GEMV = batch-1 wavefront GEMV (exactly one

@@ -1,0 +1,275 @@
+"""The weight formats beyond Q8_0 / Q4_0 on the device (F16, MXFP4, FP8 E4M3 / E5M2, Q2_K) and the
+read-only GGUF block types, against the CPU oracle. Mirrors ferrum_wgpu/src/ops/quant/
+ext_tests.rs (sizes and eligibility, bad shapes, requantisation, decode parity, every kernel
+against the CPU matmul, the kernel choice, the GEMV's one-row rule, closeness to the f32
+product), with this library's resident layout (the GGUF rows themselves, so the device bytes are
+the file bytes) in place of the reference's repacked records.
+
+Bars: encode, decode and dequantise bit-exact; the one-thread-per-output kernel bit-exact with
+the CPU matmul on the decoded weights (same operation order); the GEMV and tiled kernels within
+the reference's REDUCING 1e-5 (ferrum_wgpu/src/tolerance.rs:7)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+REDUCING = 1e-5
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def fh():
+    import ferrum_hip
+
+    return ferrum_hip
+
+
+@pytest.fixture(scope="module")
+def g(fh):
+    gpu = fh.Gpu.open_for_test()
+    if gpu is None:
+        pytest.skip("no gfx950 device")
+    yield gpu
+    gpu.close()
+
+
+def ext(fh):
+    return [fh.QKind.Fp4, fh.QKind.Fp8E4M3, fh.QKind.Fp8E5M2, fh.QKind.Q2K, fh.QKind.F16]
+
+
+def shapes(fh, kind):
+    """ext_tests.rs:12-18"""
+    if kind == fh.QKind.Q2K:
+        return [(256, 1), (256, 5), (512, 17)]
+    return [(32, 1), (32, 5), (64, 3), (96, 65)]
+
+
+def weights(orc, n):
+    """ext_tests.rs:20-31: rand_vec * 2 with blocks of 1e-5, 0 and 300 scale."""
+    v = orc.rand_vec(n, 21) * np.float32(2.0)
+    for i in range(n):
+        m = i // 32 % 5
+        if m == 0:
+            v[i] *= np.float32(1e-5)
+        elif m == 1:
+            v[i] = 0.0
+        elif m == 2:
+            v[i] *= np.float32(300.0)
+    return v
+
+
+def oid(orc, kind):
+    return int(kind)  # the oracle uses the same ids
+
+
+def test_sizes_eligibility_and_the_layout(fh, g, orc):
+    for kind in ext(fh):
+        e = kind.elems()
+        assert fh.nbytes(kind, 3 * e) == 3 * kind.file_bytes() == orc.nbytes(oid(orc, kind), 3 * e)
+        with pytest.raises(fh.GpuError):
+            fh.nbytes(kind, e + 1 if e == 256 else 33)
+    assert (fh.QKind.Fp4.elems(), fh.QKind.Q2K.elems()) == (32, 256)
+    assert fh.eligible_for(fh.QKind.Fp4, 96) and not fh.eligible_for(fh.QKind.Q2K, 96)
+    assert fh.eligible_for(fh.QKind.Q2K, 768) and not fh.eligible_for(fh.QKind.Q2K, 0)
+    assert fh.effective(fh.QKind.Q2K, 96) == fh.QKind.Q4_0 and fh.effective(fh.QKind.Q2K, 512) == fh.QKind.Q2K
+    assert fh.QKind.Fp8E4M3.ggml() is None and fh.QKind.Fp4.ggml() == 39
+    for kind in ext(fh):  # resident bytes are the GGUF bytes
+        k = kind.elems() * 2
+        qw = fh.upload_quantised(g, kind, orc.rand_vec(k * 8, 1), k, 8)
+        assert qw.device_bytes() == 8 * 2 * kind.file_bytes()
+        assert (qw.k(), qw.n(), qw.kind()) == (k, 8, kind)
+
+
+def test_pack_and_quantise_refuse_bad_shapes(fh, g, orc):
+    """ext_tests.rs:94-112"""
+    for kind in ext(fh):
+        k = kind.elems()
+        with pytest.raises(fh.GpuError, match="whole"):
+            fh.upload_qweight(g, kind, np.zeros(100, np.uint8), k + 1, 1)
+        with pytest.raises(fh.GpuError, match="needs"):
+            fh.upload_qweight(g, kind, np.zeros(3, np.uint8), k, 1)
+        with pytest.raises(fh.GpuError):
+            fh.upload_quantised(g, kind, np.zeros(k + 1), k + 1, 1)
+        with pytest.raises(fh.GpuError):
+            fh.upload_quantised(g, kind, np.zeros(2 * k - 1), k, 2)
+    with pytest.raises(fh.GpuError):
+        fh.upload_quantised(g, fh.QKind.Q2K, np.zeros(96), 96, 1)
+    fh.upload_quantised(g, fh.QKind.Fp4, np.zeros(96), 96, 1)
+
+
+def test_device_encode_is_bit_exact(fh, g, orc):
+    """The device encoders against the oracle's restatement of the reference's, on the reference's
+    awkward weights (blocks scaled by 1e-5, zero and 300) and wide random data."""
+    rng = np.random.default_rng(5)
+    for kind in ext(fh):
+        for data in (weights(orc, 4096), rng.standard_normal(8192).astype(np.float32) * np.float32(3.0),
+                     orc.rand_vec(2048, 9)):
+            n = data.size
+            want = orc.encode(oid(orc, kind), data)
+            got = g.read_bytes(fh.encode(g, kind, g.upload(data), n))[: want.size]
+            assert np.array_equal(got, want), (kind, n, np.flatnonzero(got != want)[:8])
+
+
+def test_device_decode_is_bit_exact_for_every_block_type(fh, g, orc):
+    """Random block bytes with finite f16 scales, for the weight formats and the read-only types
+    (Q4_1, Q5_0, Q5_1, Q8_1, Q3_K, Q4_K, Q5_K, Q6_K)."""
+    rng = np.random.default_rng(6)
+    scale_at = {orc.Q4_1: (0, 2), orc.Q5_0: (0,), orc.Q5_1: (0, 2), orc.Q8_1: (0, 2), orc.Q2_K: (80, 82),
+                orc.Q3_K: (108,), orc.Q4_K: (0, 2), orc.Q5_K: (0, 2), orc.Q6_K: (208,), orc.FP8_E4M3: (0,),
+                orc.FP8_E5M2: (0,), orc.MXFP4: (), orc.F16: ()}
+    for ty, offs in scale_at.items():
+        nb, ne = orc.BLOCK_BYTES[ty], orc.BLOCK_ELEMS[ty]
+        blocks = 67
+        raw = rng.integers(0, 256, blocks * nb, dtype=np.uint8).reshape(blocks, nb)
+        for o in offs:  # finite scales of modest size
+            raw[:, o:o + 2] = np.frombuffer(rng.uniform(-2, 2, blocks).astype(np.float16).tobytes(),
+                                            np.uint8).reshape(blocks, 2)
+        if ty == orc.F16:
+            raw = np.frombuffer(rng.standard_normal(blocks * 32).astype(np.float16).tobytes(), np.uint8)
+        if ty == orc.MXFP4:
+            raw[:, 0] = rng.integers(100, 150, blocks)
+        raw = raw.reshape(-1)
+        n = blocks * ne
+        want = orc.decode(ty, raw, n)
+        got = g.read(fh.decode(g, fh.QKind(ty) if ty in set(map(int, fh.QKind)) else ty, g.upload_bytes(raw), n))
+        nan = np.isnan(want)  # the FP8 NaN codes: NaN on both sides (payload bits may differ)
+        assert np.array_equal(np.isnan(got), nan), ty
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), \
+            (ty, np.flatnonzero(got[~nan] != want[~nan])[:5])
+
+
+def test_requantising_dequantised_weights_stays_close(fh, g, orc):
+    """ext_tests.rs:115-139 (the device quantiser; MXFP4 requantises exactly)."""
+    for kind in ext(fh):
+        for k, n in shapes(fh, kind):
+            qw = fh.upload_quantised(g, kind, weights(orc, k * n), k, n)
+            rows = orc.decode(oid(orc, kind), qw.read_gguf(), k * n)
+            again = fh.upload_quantised(g, kind, orc.transpose(rows, n, k), k, n)
+            back = orc.decode(oid(orc, kind), again.read_gguf(), k * n)
+            if kind in (fh.QKind.Fp4, fh.QKind.F16):
+                assert np.array_equal(back, rows), (kind, k, n)
+            else:
+                assert np.abs(rows - back).max() <= 0.35 * np.abs(rows).max() + 1e-30, (kind, k, n)
+
+
+def test_dequantised_values_match_the_cpu_decode(fh, g, orc):
+    """ext_tests.rs:142-170: the identity product returns the decoded weights, and dequantise
+    gives them too, bit for bit."""
+    for kind in ext(fh):
+        for k, n in shapes(fh, kind):
+            b = orc.quantise_matrix(oid(orc, kind), weights(orc, k * n), k, n)
+            rows = orc.decode(oid(orc, kind), b, k * n).reshape(n, k)
+            w = fh.upload_qweight(g, kind, b, k, n)
+            eye = np.eye(k, dtype=np.float32).reshape(-1)
+            gy = g.zeros(k * n)
+            fh.linear_q(g, g.upload(eye), w, gy, k)
+            assert np.array_equal(g.read(gy).reshape(k, n), rows.T), (kind, k, n)
+            assert np.array_equal(w.dequantised(), rows.T.reshape(-1)), (kind, k, n)
+            assert np.array_equal(w.read_gguf(), b)
+
+
+def test_every_kernel_matches_the_cpu_matmul(fh, g, orc):
+    """ext_tests.rs:173-238: every path, rows 1, 3, 17, 33; the one-thread-per-output kernel
+    bit-exact, the others within REDUCING."""
+    for kind in ext(fh):
+        for k, n in shapes(fh, kind):
+            b = orc.quantise_matrix(oid(orc, kind), orc.rand_vec(k * n, 17), k, n)
+            wd = orc.transpose(orc.decode(oid(orc, kind), b, k * n), n, k)
+            qw = fh.upload_qweight(g, kind, b, k, n)
+            for rows in (1, 3, 17, 33):
+                x = orc.rand_vec(rows * k, 5)
+                want = orc.matmul(x, wd, rows, k, n)
+                gx = g.upload(x)
+                paths = [fh.QPath.Naive, fh.QPath.Gemv, fh.QPath.Tiled, fh.QPath.Auto] if rows == 1 else \
+                    [fh.QPath.Naive, fh.QPath.Tiled, fh.QPath.Auto]
+                for path in paths:
+                    gy = g.zeros(rows * n)
+                    fh.linear_q_with(g, gx, qw, gy, rows, path)
+                    got = g.read(gy)
+                    if path == fh.QPath.Naive:
+                        assert np.array_equal(got, want), (kind, k, n, rows)
+                    else:
+                        e = orc.max_rel_err(got, want)
+                        assert e <= REDUCING, (kind, path, rows, k, n, e)
+
+
+def test_kernel_choice_and_the_one_row_gemv(fh, g, orc):
+    for kind in ext(fh):
+        assert fh.choose(32, kind, 512, 1408) == fh.QPath.Tiled and fh.choose(1, kind, 512, 512) == fh.QPath.Gemv
+    qw = fh.upload_quantised(g, fh.QKind.Fp4, orc.rand_vec(32 * 4, 2), 32, 4)
+    with pytest.raises(fh.GpuError, match="one row"):
+        fh.linear_q_with(g, g.upload(orc.rand_vec(64, 3)), qw, g.zeros(8), 2, fh.QPath.Gemv)
+    with pytest.raises(fh.GpuError):
+        fh.linear_q_with(g, g.upload(orc.rand_vec(64, 3)), qw, g.zeros(8), 2, fh.QPath.TiledFast)
+
+
+def test_the_quantised_product_stays_near_the_f32_product(fh, g, orc):
+    """ext_tests.rs:267-292: loose bounds that only a wrongly decoded format fails."""
+    for kind, k, bound in ((fh.QKind.Fp4, 128, 0.35), (fh.QKind.Fp8E4M3, 128, 0.04), (fh.QKind.Fp8E5M2, 128, 0.08),
+                           (fh.QKind.Q2K, 256, 0.9), (fh.QKind.F16, 128, 1e-3)):
+        n, rows = 24, 5
+        w, x = orc.rand_vec(k * n, 4), orc.rand_vec(rows * k, 6)
+        want = orc.matmul(x, w, rows, k, n)
+        qw = fh.upload_quantised(g, kind, w, k, n)
+        gy = g.zeros(rows * n)
+        fh.linear_q(g, g.upload(x), qw, gy, rows)
+        assert np.abs(g.read(gy) - want).max() <= bound * np.abs(want).max(), kind
+
+
+def test_larger_products_stay_within_reducing(fh, g, orc):
+    """Wider shapes than the reference's tests (k up to 2048, several tiles each way)."""
+    rng = np.random.default_rng(8)
+    for kind in ext(fh):
+        k, n, rows = 2048, 300, 70
+        w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+        b = orc.quantise_matrix(oid(orc, kind), w, k, n)
+        wd = orc.transpose(orc.decode(oid(orc, kind), b, k * n), n, k)
+        qw = fh.upload_qweight(g, kind, b, k, n)
+        for r in (1, rows):
+            x = rng.standard_normal(r * k).astype(np.float32)
+            want = orc.matmul(x, wd, r, k, n)
+            gy = g.zeros(r * n)
+            fh.linear_q(g, g.upload(x), qw, gy, r)
+            e = orc.max_rel_err(g.read(gy), want)
+            say(f"{kind.label()} {r}x{k}x{n}: {e:.2e}")
+            assert e <= REDUCING
+
+
+def test_gguf_uploads_of_the_new_formats(fh, g, orc):
+    """A GGUF holding MXFP4, Q2_K and F16 matrices and read-only block tensors: the matrices
+    upload as resident weights (bytes kept), every tensor decodes on the device as the oracle
+    decodes it."""
+    from oracle import gguf as og
+    from ferrum_hip.gguf import Gguf
+
+    rng = np.random.default_rng(9)
+    b = og.GgufBuilder()
+    b.meta("general.architecture", og.V(og.STR, "test"))
+    tensors = {}
+    for name, ty, k, n in (("w.mxfp4", orc.MXFP4, 64, 5), ("w.q2k", orc.Q2_K, 256, 3), ("w.f16", orc.F16, 32, 4)):
+        raw = orc.encode(ty, rng.standard_normal(k * n).astype(np.float32))
+        b.tensor_raw(name, [k, n], ty, raw.tobytes())
+        tensors[name] = (ty, k, n, raw)
+    for ty in (orc.Q4_1, orc.Q5_0, orc.Q5_1, orc.Q8_1, orc.Q3_K, orc.Q4_K, orc.Q5_K, orc.Q6_K):
+        nb, ne = orc.BLOCK_BYTES[ty], orc.BLOCK_ELEMS[ty]
+        raw = rng.integers(0, 256, 2 * nb, dtype=np.uint8).reshape(2, nb)
+        raw[:, 0:2] = np.frombuffer(np.float16([0.5, -0.25]).tobytes(), np.uint8).reshape(2, 2)
+        if ty in (orc.Q3_K,):
+            raw[:, 108:110] = np.frombuffer(np.float16([0.5, -0.25]).tobytes(), np.uint8).reshape(2, 2)
+        if ty in (orc.Q6_K,):
+            raw[:, 208:210] = np.frombuffer(np.float16([0.5, -0.25]).tobytes(), np.uint8).reshape(2, 2)
+        if ty in (orc.Q4_1, orc.Q5_1, orc.Q8_1, orc.Q4_K, orc.Q5_K):
+            raw[:, 2:4] = np.frombuffer(np.float16([0.125, 1.0]).tobytes(), np.uint8).reshape(2, 2)
+        raw = raw.reshape(-1)
+        b.tensor_raw(f"t.{ty}", [2 * ne], ty, raw.tobytes())
+        tensors[f"t.{ty}"] = (ty, 2 * ne, 1, raw)
+    gg = Gguf.parse(b.into_bytes())
+    for name, (ty, k, n, raw) in tensors.items():
+        got = g.read(gg.tensor_f32(g, name))
+        assert np.array_equal(got, orc.decode(ty, raw, k * n)), name
+        if name.startswith("w."):
+            qw = gg.upload_qweight(g, name)
+            assert (qw.k(), qw.n(), int(qw.kind())) == (k, n, ty)
+            assert np.array_equal(qw.read_gguf(), raw)
