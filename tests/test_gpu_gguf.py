@@ -124,12 +124,13 @@ def test_upload_errors(G, g):
     b.tensor_raw("q8", [32, 2], G.GGML_Q8_0, bytes(68))
     data = b.into_bytes()
     gf = G.Gguf.parse(data)
-    for name, call, text in [("f", "upload_qweight", "not Q8_0 or Q4_0"), ("q41", "tensor_f32", "no device decode"),
+    for name, call, text in [("f", "upload_qweight", "not a weight format"), ("q41", "upload_qweight", "not a weight format"),
                              ("i", "tensor_f32", "integer tensors"), ("nope", "upload_qweight", "missing tensor"),
                              ("nope", "tensor_f32", "missing tensor")]:
         with pytest.raises(G.GgufError) as e:
             getattr(gf, call)(g, name)
         assert text in str(e.value), (name, call, str(e.value))
+    assert not g.read(gf.tensor_f32(g, "q41")).any()  # a read-only block type decodes (all-zero block)
     head = G.Gguf.parse_prefix(data[:gf.data_offset()], len(data))
     with pytest.raises(G.GgufError) as e:
         head.upload_qweight(g, "q8")
