@@ -51,6 +51,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
 }
 
+// A CTA's tile: CTAs are dealt round-robin to the eight XCDs (blockIdx.x % 8), and XCD x takes
+// the x-th equal contiguous run of the tiles in a grouped order (groups of four row tiles, column
+// by column inside a group), so every XCD gets the same share and the CTAs running together on
+// one XCD share x rows and weight columns in its L2. The grid is 8 * ceil(tiles / 8) CTAs.
+__device__ __forceinline__ bool xcd_tile(uint32_t mt, uint32_t nt, uint32_t *mi, uint32_t *ni) {
+    constexpr uint32_t GM = 4;
+    const uint32_t tiles = mt * nt, per_xcd = (tiles + 7) / 8;
+    const uint32_t local = blockIdx.x / 8, t = (blockIdx.x % 8) * per_xcd + local;
+    if (local >= per_xcd || t >= tiles) return false;
+    const uint32_t grp = t / (GM * nt), in = t % (GM * nt), gm = min(GM, mt - grp * GM);
+    *mi = grp * GM + in % gm;
+    *ni = in / gm;
+    return true;
+}
+
 // ---- naive baseline ----
 template <int KIND>
 __global__ __launch_bounds__(256) void naive_kernel(const uint8_t *__restrict__ qs, const uint16_t *__restrict__ ds,
@@ -341,14 +356,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
     __shared__ __attribute__((aligned(16))) uint8_t sB8[BN * kB8Str];
     __shared__ float sD[2 * BN];
 
-    // Tile of this CTA. CTAs are dealt round-robin to the 8 XCDs; each XCD works through whole
-    // super-tiles of 8 x 8 tiles, so the CTAs that run together on one XCD share 8 stripes of x
-    // and 8 of weights in its L2 (a square working set: both operands are reused 8 times).
-    const uint32_t c = blockIdx.x, xcd = c % 8, u = c / 8;
-    const uint32_t snt = (nt + 7) / 8;                   // super-tiles along N
-    const uint32_t sidx = (u / 64) * 8 + xcd, v = u % 64;
-    const uint32_t mi = (sidx / snt) * 8 + v / 8, ni = (sidx % snt) * 8 + v % 8;
-    if (mi >= mt || ni >= nt) return;  // whole CTA: no barrier is left waiting
+    uint32_t mi, ni;
+    if (!xcd_tile(mt, nt, &mi, &ni)) return;  // whole CTA: no barrier is left waiting
     const uint32_t m0 = mi * BM, n0 = ni * BN;
 
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
@@ -582,9 +591,9 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restric
 template <int KIND, int BM, int BN, int WAVES_M>
 hipError_t run_gemm(hipStream_t s, const GemmArgs &g) {
     const uint32_t mt = (g.M + BM - 1) / BM, nt = (g.N + BN - 1) / BN;
-    const uint64_t supers = (uint64_t)((mt + 7) / 8) * ((nt + 7) / 8);
-    if (supers * 64 > 0x7fffffffull) return hipErrorInvalidValue;
-    const uint32_t grid = (uint32_t)((supers + 7) / 8 * 8 * 64);  // whole super-tiles on every XCD
+    const uint64_t tiles = (uint64_t)mt * nt;
+    if (tiles > 0x7ffffff0ull) return hipErrorInvalidValue;
+    const uint32_t grid = (uint32_t)((tiles + 7) / 8 * 8);  // an equal share for every XCD
     const uint32_t stages = (g.K / 32 + 1) / 2;
     const uint32_t sp = g.partial ? gemm_splits((uint64_t)mt * nt, stages) : 1;
     const uint32_t per = (stages + sp - 1) / sp;
@@ -914,11 +923,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const _Float16 *__rest
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * kAStr];
     __shared__ __attribute__((aligned(16))) uint32_t sB[2][BN * C::BSTR];
 
-    const uint32_t c = blockIdx.x, xcd = c % 8, u = c / 8;
-    const uint32_t snt = (nt + 7) / 8;
-    const uint32_t sidx = (u / 64) * 8 + xcd, v = u % 64;
-    const uint32_t mi = (sidx / snt) * 8 + v / 8, ni = (sidx % snt) * 8 + v % 8;
-    if (mi >= mt || ni >= nt) return;  // whole CTA: no barrier is left waiting
+    uint32_t mi, ni;
+    if (!xcd_tile(mt, nt, &mi, &ni)) return;  // whole CTA: no barrier is left waiting
     const uint32_t m0 = mi * BM, n0 = ni * BN;
 
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
@@ -1041,6 +1047,183 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const _Float16 *__rest
         }
 }
 
+// The large-tile variant: a CTA of eight wavefronts computes a 256 x 256 tile, each wavefront a
+// 128 x 64 part (eight 32 x 32 accumulators), one CTA per CU, so every SIMD holds two wavefronts
+// and one can issue MFMAs while the other waits. The weights are dequantised once per stage,
+// when the staged quants are written to LDS (f16(d q), the values gemm_f16_kernel computes), so a
+// stage's compute is LDS reads and MFMAs only: per k16 step four x and two weight fragments
+// (16-byte reads) feed eight v_mfma_f32_32x32x16_f16. Tiles as xcd_tile deals them.
+constexpr int kBigStr = 72;  // LDS halves per row (x) or column (weights) and stage: 64 + 8 pad
+
+template <int KIND>
+struct BigLoad {  // one thread's share of a stage in flight
+    static constexpr int QB = KIND == FH_Q8_0 ? 32 : 16;  // quant bytes per block
+    static constexpr int QL = QB / 16;                    // 16-byte quant loads: one block of its column
+    u32x4 a[4], q[QL];
+    uint32_t d, dmask;
+};
+
+template <int KIND>
+__global__ __launch_bounds__(512, 1) void gemm_f16_big_kernel(const _Float16 *__restrict__ xh,
+                                                              const float *__restrict__ xs,
+                                                              const uint8_t *__restrict__ qs,
+                                                              const uint16_t *__restrict__ ds, float *__restrict__ y,
+                                                              uint32_t M, uint32_t K, uint32_t N, uint32_t mt,
+                                                              uint32_t nt, uint32_t split_stages) {
+    using L = BigLoad<KIND>;
+    __shared__ __attribute__((aligned(16))) _Float16 sA0[256 * kBigStr], sA1[256 * kBigStr];
+    __shared__ __attribute__((aligned(16))) _Float16 sB0[256 * kBigStr], sB1[256 * kBigStr];
+
+    uint32_t mi, ni;
+    if (!xcd_tile(mt, nt, &mi, &ni)) return;  // whole CTA: no barrier is left waiting
+    const uint32_t m0 = mi * 256, n0 = ni * 256;
+
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, wm = wave % 2, wn = wave / 2;
+    const uint32_t nb = K / 32, all_stages = (nb + 1) / 2;
+    const uint32_t st0 = blockIdx.y * split_stages, st1 = min(all_stages, st0 + split_stages);
+    y += (size_t)blockIdx.y * M * N;
+    const int fr = lane % 32, hf = lane / 32;
+
+    const auto r_xh = make_rsrc(xh, M * nb * 64);
+    const auto r_q = make_rsrc(qs, (N + 31) / 32 * 32 * nb * L::QB);
+    const auto r_d = make_rsrc(ds, (N + 31) / 32 * 32 * ((nb + 7) / 8 * 8) * 2);
+    constexpr uint32_t kOut = 0x80000000u;
+    // x: chunk c = tid + 512 i is row c / 8, 16 bytes (c % 8) of the row's 128-byte stage
+    uint32_t o_a[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t m = m0 + (tid + 512 * i) / 8;
+        o_a[i] = m < M ? (m * nb * 32 + (tid % 8) * 8) * 2 : kOut;
+    }
+    // weights: thread t owns block bq = t / 256 of the stage in column n0 + t % 256 (its quants
+    // and the column's scale dword, of which it uses half bq)
+    const int cq = tid % 256, bq = tid / 256;
+    const uint32_t n = n0 + cq;
+    const uint32_t o_q = ((n >> 5) * nb * 32 + (n & 31)) * L::QB;
+    const uint32_t o_d = ((n >> 5) * ((nb + 7) / 8) * 32 + (n & 31)) * 16;
+
+    L ld0, ld1;  // two stages in flight: each load has two stages of MFMAs to arrive
+    auto load_stage = [&](L &ld, uint32_t st) {
+        // past the CTA's stages everything reads 0 (the loop runs an even number of stages);
+        // an odd last stage of the product has one block, and its second block reads 0
+        const bool live = st < st1, two = live && 2 * st + 1 < nb;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t off = (live && (tid % 8) < 4) || two ? o_a[i] + st * 128 : kOut;
+            ld.a[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_xh, (int)off, 0, 0));
+        }
+        const bool mine = bq == 0 ? live : two;
+#pragma unroll
+        for (int i = 0; i < L::QL; i++) {
+            const uint32_t off = mine ? o_q + ((2 * st + bq) * 32 * L::QB + i * 16) : kOut;
+            ld.q[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_q, (int)off, 0, 0));
+        }
+        ld.d = __builtin_amdgcn_raw_buffer_load_b32(r_d, mine ? (int)(o_d + (st >> 2) * 512 + (st & 3) * 4) : (int)kOut,
+                                                    0, 0);
+        ld.dmask = mine ? 0xffffffffu : 0u;  // a missing block's scale is 0, so its values are 0
+        // (applied when the stage is stored: using the loaded value here would wait for the load)
+    };
+    auto store_stage = [&](const L &ld, _Float16 *sa, _Float16 *sb) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) *(u32x4 *)(sa + ((tid + 512 * i) / 8) * kBigStr + (tid % 8) * 8) = ld.a[i];
+        _Float16 *col = sb + cq * kBigStr + bq * 32;
+        const uint32_t dd = ld.d & ld.dmask;
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(bq ? dd >> 16 : dd & 0xffffu));
+#pragma unroll
+        for (int f = 0; f < 4; f++) {
+            f16x8 v;
+            if constexpr (KIND == FH_Q8_0) {
+                const u32x4 &w = ld.q[f / 2];
+                v = dequant_q8_frag(w[2 * (f % 2)], w[2 * (f % 2) + 1], d);
+            } else {
+                v = dequant_q4_frag(ld.q[0][f], d);
+            }
+            *(f16x8 *)(col + 8 * f) = v;
+        }
+    };
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    // The fragments of k16 step ks + 1 are read while step ks's eight MFMAs run (a read after
+    // each of the first six, an order the scheduling-group barriers pin down).
+    auto compute = [&](const _Float16 *sa, const _Float16 *sb) {
+        const _Float16 *a = sa + (wm * 128 + fr) * kBigStr + 8 * hf;
+        const _Float16 *b = sb + (wn * 64 + fr) * kBigStr + 8 * hf;
+        f16x8 ah[2][4], bf[2][2];
+        auto read = [&](int ks) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) ah[ks % 2][i] = *(const f16x8 *)(a + i * 32 * kBigStr + 16 * ks);
+#pragma unroll
+            for (int j = 0; j < 2; j++) bf[ks % 2][j] = *(const f16x8 *)(b + j * 32 * kBigStr + 16 * ks);
+        };
+        read(0);
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            if (ks < 3) read(ks + 1);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[ks % 2][i], bf[ks % 2][j], acc[i][j], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // step 0's reads
+#pragma unroll
+        for (int ks = 0; ks < 3; ks++) {
+#pragma unroll
+            for (int r = 0; r < 6; r++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of step ks
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a read of step ks + 1
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // step 3's MFMAs
+    };
+
+    load_stage(ld0, st0);
+    load_stage(ld1, st0 + 1);
+    store_stage(ld0, sA0, sB0);
+    load_stage(ld0, st0 + 2);
+    // Two stages per trip (the buffers and staging registers are then known apart); an odd count
+    // ends with a stage of zeros. Scheduling barriers keep each phase in place: nothing that
+    // reads a staged load may be moved up into the MFMAs issued while that load is in flight.
+    const uint32_t stages = st1 > st0 ? st1 - st0 : 0;
+    uint32_t st = st0;
+    for (uint32_t it = 0; it < (stages + 1) / 2; it++, st += 2) {
+        __syncthreads();  // stage st is in buffer 0; every wave is done with buffer 1
+        __builtin_amdgcn_sched_barrier(0);
+        store_stage(ld1, sA1, sB1);
+        load_stage(ld1, st + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(sA0, sB0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        store_stage(ld0, sA0, sB0);
+        load_stage(ld0, st + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(sA1, sB1);
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * hf + r % 4;
+            if (row >= M) continue;
+            const float sx = xs[row];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint32_t col = n0 + wn * 64 + j * 32 + fr;
+                if (col < N) y[(size_t)row * N + col] = acc[i][j][r] * sx;
+            }
+        }
+}
+
 struct GemmF16Args {
     const _Float16 *xh;
     const float *xs;
@@ -1053,9 +1236,9 @@ struct GemmF16Args {
 template <int KIND, int BM, int BN>
 hipError_t run_gemm_f16(hipStream_t s, const GemmF16Args &g) {
     const uint32_t mt = (g.M + BM - 1) / BM, nt = (g.N + BN - 1) / BN;
-    const uint64_t supers = (uint64_t)((mt + 7) / 8) * ((nt + 7) / 8);
-    if (supers * 64 > 0x7fffffffull) return hipErrorInvalidValue;
-    const uint32_t grid = (uint32_t)((supers + 7) / 8 * 8 * 64);
+    const uint64_t tiles = (uint64_t)mt * nt;
+    if (tiles > 0x7ffffff0ull) return hipErrorInvalidValue;
+    const uint32_t grid = (uint32_t)((tiles + 7) / 8 * 8);  // an equal share for every XCD
     const uint32_t stages = (g.K / 32 + 1) / 2;
     const uint32_t sp = g.partial ? gemm_splits((uint64_t)mt * nt, stages) : 1;
     const uint32_t per = (stages + sp - 1) / sp;
@@ -1076,8 +1259,49 @@ void f16_tile(size_t rows, size_t *bm, size_t *bn) {
     *bn = 256;
 }
 
+// The 256 x 256 kernel's plan: taken when the product has at least 128 such tiles; the K split
+// (at most 4, at least 8 stages per split) that best fills whole rounds of one CTA per CU.
+bool f16_big_plan(size_t rows, size_t k, size_t n, uint32_t *splits) {
+    const uint64_t tiles = (uint64_t)((rows + 255) / 256) * ((n + 255) / 256);
+    if (tiles < 128) return false;
+    const uint32_t stages = (uint32_t)((k / 32 + 1) / 2), cus = 256;
+    uint32_t best = 1;
+    double best_eff = 0.0;
+    for (uint32_t sp = 1; sp <= 4 && (sp == 1 || stages / sp >= 8); sp++) {
+        const uint64_t ctas = tiles * sp, rounds = (ctas + cus - 1) / cus;
+        const double eff = (double)ctas / (double)(rounds * cus) - 0.04 * (sp - 1);  // the reduce pass
+        if (eff > best_eff + 1e-9) {
+            best_eff = eff;
+            best = sp;
+        }
+    }
+    *splits = best;
+    return true;
+}
+
+template <int KIND>
+hipError_t run_gemm_f16_big(hipStream_t s, const GemmF16Args &g, uint32_t sp) {
+    const uint32_t mt = (g.M + 255) / 256, nt = (g.N + 255) / 256;
+    const uint64_t tiles = (uint64_t)mt * nt;
+    if (tiles > 0x7ffffff0ull) return hipErrorInvalidValue;
+    const uint32_t per_xcd = (uint32_t)((tiles + 7) / 8);
+    const uint32_t stages = (g.K / 32 + 1) / 2;
+    const uint32_t per = ((stages + sp - 1) / sp + 1) & ~1u;  // even: the kernel runs stages in pairs
+    float *out = sp > 1 ? g.partial : g.y;
+    gemm_f16_big_kernel<KIND><<<dim3(8 * per_xcd, sp), 512, 0, s>>>(g.xh, g.xs, g.qs, g.ds, out, g.M, g.K, g.N, mt,
+                                                                     nt, per);
+    if (sp > 1) {
+        const size_t n = (size_t)g.M * g.N;
+        const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
+        gemm_reduce_kernel<<<rg, 256, 0, s>>>(g.partial, g.y, n, sp);
+    }
+    return hipGetLastError();
+}
+
 template <int KIND>
 hipError_t gemm_f16_dispatch(hipStream_t s, const GemmF16Args &g) {
+    uint32_t sp = 1;
+    if (f16_big_plan(g.M, g.K, g.N, &sp)) return run_gemm_f16_big<KIND>(s, g, sp);
     if (g.M <= 32) return run_gemm_f16<KIND, 32, 256>(s, g);
     if (g.M <= 64) return run_gemm_f16<KIND, 64, 256>(s, g);
     return run_gemm_f16<KIND, 128, 256>(s, g);
@@ -1174,10 +1398,13 @@ hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uin
 // x as f16 (2 bytes per element), the row scales, then the K-split partials, each 256-aligned
 size_t gemm_f16_workspace_bytes(size_t rows, size_t k, size_t n) {
     const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
-    size_t bm, bn;
-    f16_tile(rows, &bm, &bn);
-    const uint64_t tiles = (uint64_t)((rows + bm - 1) / bm) * ((n + bn - 1) / bn);
-    const uint32_t sp = gemm_splits(tiles, (uint32_t)((k / 32 + 1) / 2));
+    uint32_t sp = 1;
+    if (!f16_big_plan(rows, k, n, &sp)) {
+        size_t bm, bn;
+        f16_tile(rows, &bm, &bn);
+        const uint64_t tiles = (uint64_t)((rows + bm - 1) / bm) * ((n + bn - 1) / bn);
+        sp = gemm_splits(tiles, (uint32_t)((k / 32 + 1) / 2));
+    }
     return up(rows * k * 2) + up(rows * 4) + (sp > 1 ? (size_t)sp * rows * n * 4 : 0);
 }
 
