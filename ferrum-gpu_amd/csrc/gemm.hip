@@ -637,7 +637,8 @@ struct GemmCfg2 {
 template <int KIND, int BM, int BN, int WAVES_M>
 __global__ __launch_bounds__(256, 2) void gemm_precise_kernel(const _Float16 *__restrict__ xs, const uint8_t *__restrict__ qs,
                                                       const uint16_t *__restrict__ ds, float *__restrict__ y,
-                                                      uint32_t M, uint32_t K, uint32_t N, uint32_t mt, uint32_t nt) {
+                                                      uint32_t M, uint32_t K, uint32_t N, uint32_t mt, uint32_t nt,
+                                                      uint32_t split_stages) {
     using C = GemmCfg2<KIND, BM, BN, WAVES_M>;
     // stage layout: x row r, block bb at r * kBKB * kARow2 + bb * kARow2; weight row likewise
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * kBKB * kARow2];
@@ -655,7 +656,11 @@ __global__ __launch_bounds__(256, 2) void gemm_precise_kernel(const _Float16 *__
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
     const int wm = wave % WAVES_M, wn = wave / WAVES_M;
     const uint32_t nb = K / 32;
-    const uint32_t stages = (nb + kBKB - 1) / kBKB;
+    // split blockIdx.y of the K range: stages st0 .. st1 - 1, its partial product at y + split * M * N
+    // (added up by gemm_reduce_kernel in split order)
+    const uint32_t all_stages = (nb + kBKB - 1) / kBKB;
+    const uint32_t st0 = blockIdx.y * split_stages, st1 = min(all_stages, st0 + split_stages);
+    y += (size_t)blockIdx.y * M * N;
 
     u32x4 ra[C::A_LD];
     u32x4 rb[C::B_PER];
@@ -736,14 +741,14 @@ __global__ __launch_bounds__(256, 2) void gemm_precise_kernel(const _Float16 *__
     const int fr = lane % 32;        // fragment row (x) / column (weights)
     const int fk = 8 * (lane / 32);  // first of this lane's 8 positions in a K = 16 step
 
-    if (stages > 0) {
-        load_stage(0);
+    if (st0 < st1) {
+        load_stage(st0);
         store_stage(0);
     }
     __syncthreads();
-    for (uint32_t st = 0; st < stages; st++) {
-        const int buf = st & 1;
-        const bool more = st + 1 < stages;
+    for (uint32_t st = st0; st < st1; st++) {
+        const int buf = (st - st0) & 1;
+        const bool more = st + 1 < st1;
         if (more) load_stage(st + 1);  // in flight during the MFMAs below
         const int nbb = nb - st * kBKB < (uint32_t)kBKB ? (int)(nb - st * kBKB) : kBKB;  // wave-uniform
 #pragma unroll
@@ -802,23 +807,45 @@ __global__ __launch_bounds__(256, 2) void gemm_precise_kernel(const _Float16 *__
         }
 }
 
+// The precise kernel's tile shape by rows and its K split (the rule of gemm_splits).
+void precise_tile(size_t rows, size_t *bm, size_t *bn) {
+    *bm = rows <= 32 ? 32 : rows <= 64 ? 64 : 128;
+    *bn = rows <= 32 ? 256 : 128;
+}
+
+uint32_t precise_splits(size_t rows, size_t k, size_t n) {
+    size_t bm, bn;
+    precise_tile(rows, &bm, &bn);
+    const uint64_t tiles = (uint64_t)((rows + bm - 1) / bm) * ((n + bn - 1) / bn);
+    return gemm_splits(tiles, (uint32_t)((k / 32 + kBKB - 1) / kBKB));
+}
+
 template <int KIND, int BM, int BN, int WAVES_M>
-hipError_t run_gemm_precise(hipStream_t s, const _Float16 *xs, const uint8_t *qs, const uint16_t *ds, float *y, uint32_t M,
-                    uint32_t K, uint32_t N) {
+hipError_t run_gemm_precise(hipStream_t s, const _Float16 *xs, const uint8_t *qs, const uint16_t *ds, float *y,
+                            float *partial, uint32_t M, uint32_t K, uint32_t N) {
     const uint32_t mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
     const uint64_t tiles = (uint64_t)mt * nt;
     if (tiles > 0x7fffffffull) return hipErrorInvalidValue;
     const uint32_t grid = (uint32_t)((tiles + 7) / 8 * 8);  // a multiple of the XCD count
-    gemm_precise_kernel<KIND, BM, BN, WAVES_M><<<grid, 256, 0, s>>>(xs, qs, ds, y, M, K, N, mt, nt);
+    const uint32_t stages = (K / 32 + kBKB - 1) / kBKB;
+    const uint32_t sp = partial ? precise_splits(M, K, N) : 1;
+    const uint32_t per = (stages + sp - 1) / sp;
+    float *out = sp > 1 ? partial : y;
+    gemm_precise_kernel<KIND, BM, BN, WAVES_M><<<dim3(grid, sp), 256, 0, s>>>(xs, qs, ds, out, M, K, N, mt, nt, per);
+    if (sp > 1) {
+        const size_t n = (size_t)M * N;
+        const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
+        gemm_reduce_kernel<<<rg, 256, 0, s>>>(partial, y, n, sp);  // (a split past the last stage wrote zeros)
+    }
     return hipGetLastError();
 }
 
 template <int KIND>
 hipError_t gemm_precise_dispatch(hipStream_t s, const _Float16 *xs, const uint8_t *qs, const uint16_t *ds, float *y,
-                         uint32_t M, uint32_t K, uint32_t N) {
-    if (M <= 32) return run_gemm_precise<KIND, 32, 256, 1>(s, xs, qs, ds, y, M, K, N);
-    if (M <= 64) return run_gemm_precise<KIND, 64, 128, 2>(s, xs, qs, ds, y, M, K, N);
-    return run_gemm_precise<KIND, 128, 128, 2>(s, xs, qs, ds, y, M, K, N);
+                                 float *partial, uint32_t M, uint32_t K, uint32_t N) {
+    if (M <= 32) return run_gemm_precise<KIND, 32, 256, 1>(s, xs, qs, ds, y, partial, M, K, N);
+    if (M <= 64) return run_gemm_precise<KIND, 64, 128, 2>(s, xs, qs, ds, y, partial, M, K, N);
+    return run_gemm_precise<KIND, 128, 128, 2>(s, xs, qs, ds, y, partial, M, K, N);
 }
 
 // ---- the dequant-f16 GEMM (FH_PATH_TILED_F16): weights dequantised into LDS, plain f16 MFMA ----
@@ -1343,19 +1370,26 @@ hipError_t launch_make_b8(hipStream_t s, fh_kind kind, const uint8_t *qs, const 
     return hipGetLastError();
 }
 
-size_t gemm_precise_workspace_bytes(size_t rows, size_t k) { return rows * k * 4; }
+// x split into f16 pairs (4 bytes per element), then the K-split partial products (256-aligned)
+size_t gemm_precise_workspace_bytes(size_t rows, size_t k, size_t n) {
+    const uint32_t sp = precise_splits(rows, k, n);
+    return (rows * k * 4 + 255) / 256 * 256 + (sp > 1 ? (size_t)sp * rows * n * 4 : 0);
+}
 
 hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
                                float *y, size_t rows, size_t k, size_t n, void *workspace) {
     _Float16 *xs = (_Float16 *)workspace;
+    float *partial = precise_splits(rows, k, n) > 1
+                         ? (float *)((uint8_t *)workspace + (rows * k * 4 + 255) / 256 * 256)
+                         : nullptr;
     const size_t items = rows * (k / 32);
     const unsigned g = (unsigned)(items / 32 + 1 < 65535 ? items / 32 + 1 : 65535);
     if (kind == FH_Q8_0) {
         split_x_precise_kernel<FH_Q8_0><<<g, 256, 0, s>>>(x, xs, items);
-        return gemm_precise_dispatch<FH_Q8_0>(s, xs, qs, ds, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+        return gemm_precise_dispatch<FH_Q8_0>(s, xs, qs, ds, y, partial, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
     }
     split_x_precise_kernel<FH_Q4_0><<<g, 256, 0, s>>>(x, xs, items);
-    return gemm_precise_dispatch<FH_Q4_0>(s, xs, qs, ds, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+    return gemm_precise_dispatch<FH_Q4_0>(s, xs, qs, ds, y, partial, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
 }
 
 hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,

@@ -194,7 +194,7 @@ bool gemm_f16_supported(size_t rows, size_t k, size_t n);
 hipError_t launch_gemm_f16(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x, float *y,
                            size_t rows, size_t k, size_t n, void *workspace);
 // The precise MFMA GEMM (x as two f16 parts; split into workspace, then the product).
-size_t gemm_precise_workspace_bytes(size_t rows, size_t k);
+size_t gemm_precise_workspace_bytes(size_t rows, size_t k, size_t n);
 hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
                                float *y, size_t rows, size_t k, size_t n, void *workspace);
 

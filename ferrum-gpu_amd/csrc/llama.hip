@@ -474,7 +474,7 @@ size_t linear_ws(const fh_llama *m, size_t rows, size_t k, size_t n) {
     switch (m->path) {
     case FH_PATH_TILED_FAST: return gemm_workspace_bytes(rows, k, n);
     case FH_PATH_TILED_F16: return gemm_f16_workspace_bytes(rows, k, n);
-    default: return gemm_precise_workspace_bytes(rows, k);
+    default: return gemm_precise_workspace_bytes(rows, k, n);
     }
 }
 

@@ -674,7 +674,7 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
         return end_command(dev, "linear_q");
     case FH_PATH_TILED: {
         void *ws = nullptr;
-        if (rows && (st = workspace(dev, gemm_precise_workspace_bytes(rows, w->k), &ws))) return st;
+        if (rows && (st = workspace(dev, gemm_precise_workspace_bytes(rows, w->k, w->n), &ws))) return st;
         if ((st = begin_command(dev, "linear_q"))) return st;
         if (rows) (void)launch_gemm_precise(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, ws);
         return end_command(dev, "linear_q");
