@@ -1178,28 +1178,27 @@ __global__ __launch_bounds__(512, 1) void gemm_f16_big_kernel(const _Float16 *__
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
     // The fragments of k16 step ks + 1 are read while step ks's eight MFMAs run (a read after
-    // each of the first six, an order the scheduling-group barriers pin down).
-    auto compute = [&](const _Float16 *sa, const _Float16 *sb) {
+    // each of the first six, an order the scheduling-group barriers pin down); step 0's are read
+    // before the stage's stores, so they arrive while the next stage is stored.
+    f16x8 ah[2][4], bf[2][2];
+    auto read = [&](const _Float16 *sa, const _Float16 *sb, int ks) {
         const _Float16 *a = sa + (wm * 128 + fr) * kBigStr + 8 * hf;
         const _Float16 *b = sb + (wn * 64 + fr) * kBigStr + 8 * hf;
-        f16x8 ah[2][4], bf[2][2];
-        auto read = [&](int ks) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) ah[ks % 2][i] = *(const f16x8 *)(a + i * 32 * kBigStr + 16 * ks);
+        for (int i = 0; i < 4; i++) ah[ks % 2][i] = *(const f16x8 *)(a + i * 32 * kBigStr + 16 * ks);
 #pragma unroll
-            for (int j = 0; j < 2; j++) bf[ks % 2][j] = *(const f16x8 *)(b + j * 32 * kBigStr + 16 * ks);
-        };
-        read(0);
+        for (int j = 0; j < 2; j++) bf[ks % 2][j] = *(const f16x8 *)(b + j * 32 * kBigStr + 16 * ks);
+    };
+    auto compute = [&](const _Float16 *sa, const _Float16 *sb) {
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            if (ks < 3) read(ks + 1);
+            if (ks < 3) read(sa, sb, ks + 1);
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
                 for (int j = 0; j < 2; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[ks % 2][i], bf[ks % 2][j], acc[i][j], 0, 0, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // step 0's reads
 #pragma unroll
         for (int ks = 0; ks < 3; ks++) {
 #pragma unroll
@@ -1224,11 +1223,15 @@ __global__ __launch_bounds__(512, 1) void gemm_f16_big_kernel(const _Float16 *__
     for (uint32_t it = 0; it < (stages + 1) / 2; it++, st += 2) {
         __syncthreads();  // stage st is in buffer 0; every wave is done with buffer 1
         __builtin_amdgcn_sched_barrier(0);
+        read(sA0, sB0, 0);
+        __builtin_amdgcn_sched_barrier(0);
         store_stage(ld1, sA1, sB1);
         load_stage(ld1, st + 3);
         __builtin_amdgcn_sched_barrier(0);
         compute(sA0, sB0);
         __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        read(sA1, sB1, 0);
         __builtin_amdgcn_sched_barrier(0);
         store_stage(ld0, sA0, sB0);
         load_stage(ld0, st + 4);
