@@ -58,6 +58,9 @@ struct fh_llama {
           *logits = nullptr, *scores = nullptr;
     int32_t *ids = nullptr;
     void *ws = nullptr;
+    // split attention operands (head dims 32, 64, 128): f16 parts and exponents, rows padded to 32
+    _Float16 *sqh = nullptr, *sql = nullptr, *skh = nullptr, *skl = nullptr, *svh = nullptr, *svl = nullptr;
+    int8_t *seq = nullptr, *sek = nullptr, *sev = nullptr;
 
     size_t q_dim() const { return heads * head_dim; }
     size_t kv_dim() const { return kv_heads * head_dim; }
@@ -301,6 +304,259 @@ __global__ __launch_bounds__(64 * W) void attention_kernel(const float *__restri
         }
 }
 
+// ---- attention on the f16 matrix cores, f32-accurate (head dims 32, 64, 128) ----
+// Every head row of q, k and v (after RoPE) is put on a power-of-two scale, x' = x 2^-e with
+// max |x'| in [2^14, 2^15), and split into two f16 parts x' = hi + lo (hi = f16(x'), lo =
+// f16(x' - hi): 22 significant bits, no f16 overflow or underflow to speak of). A product of
+// two such values is hi hi + hi lo + lo hi up to 2^-22 of its size (the lo lo term dropped), so
+// each f32-accurate 32 x 32 x 16 product costs three v_mfma_f32_32x32x16_f16 instead of eight
+// v_mfma_f32_32x32x2_f32 of twice the length. Layouts (tp = t rounded up to 32, rows t .. tp - 1
+// zero with exponent -127): q' [tp, heads HD] and k' [tp, kv_heads HD] row-major, v' transposed
+// per kv head [kv_heads HD, tp] (keys contiguous), exponents [slot, tp] as bytes.
+constexpr int kSplitPad = -127;
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict__ qkv, _Float16 *__restrict__ qh,
+                                                         _Float16 *__restrict__ ql, _Float16 *__restrict__ kh,
+                                                         _Float16 *__restrict__ kl, _Float16 *__restrict__ vh,
+                                                         _Float16 *__restrict__ vl, int8_t *__restrict__ eq,
+                                                         int8_t *__restrict__ ek, int8_t *__restrict__ ev, uint32_t t,
+                                                         uint32_t tp, uint32_t width, uint32_t heads,
+                                                         uint32_t kv_heads) {
+    const uint32_t row = blockIdx.x, lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const uint32_t qd = heads * HD, kvd = kv_heads * HD;
+    for (uint32_t slot = wave; slot < heads + 2 * kv_heads; slot += 4) {
+        float v[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t d = lane + 64 * i;
+            v[i] = row < t && d < (uint32_t)HD ? qkv[(size_t)row * width + slot * HD + d] : 0.0f;
+        }
+        float mx = fmaxf(fabsf(v[0]), fabsf(v[1]));
+#pragma unroll
+        for (int o = 32; o >= 1; o /= 2) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        // 2^E <= mx < 2^(E+1), e = E - 14; zero rows, padding rows and non-finite rows keep e = 0
+        // (non-finite values then stay non-finite) and padding rows report -127
+        int e = 0;
+        if (mx > 0.0f && mx <= 3.4028235e38f) e = ((int)(__float_as_uint(mx) >> 23) - 127) - 14;
+        e = e < -100 ? -100 : (e > 100 ? 100 : e);
+        const float f = ldexpf(1.0f, -e);
+        const int8_t code = row < t ? (int8_t)e : (int8_t)kSplitPad;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t d = lane + 64 * i;
+            if (d >= (uint32_t)HD) continue;
+            const float x = v[i] * f;
+            const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
+            if (slot < heads) {
+                const size_t o = (size_t)row * qd + slot * HD + d;
+                qh[o] = hi;
+                ql[o] = lo;
+            } else if (slot < heads + kv_heads) {
+                const size_t o = (size_t)row * kvd + (slot - heads) * HD + d;
+                kh[o] = hi;
+                kl[o] = lo;
+            } else {
+                const size_t o = ((size_t)(slot - heads - kv_heads) * HD + d) * tp + row;
+                vh[o] = hi;
+                vl[o] = lo;
+            }
+        }
+        if (lane == 0) {
+            if (slot < heads)
+                eq[(size_t)slot * tp + row] = code;
+            else if (slot < heads + kv_heads)
+                ek[(size_t)(slot - heads) * tp + row] = code;
+            else
+                ev[(size_t)(slot - heads - kv_heads) * tp + row] = code;
+        }
+    }
+}
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// One key tile (32 keys) of one wavefront's lanes: k' fragments of A row l % 32 (key k0 + pi(l %
+// 32)) and the exponents of the lane's sixteen accumulator keys 16 u + 8 (l / 32) + 0..7 (loaded
+// a tile ahead); v' fragments (dims 32 b + l % 32, keys 16 u + 8 (l / 32) + 0..7), loaded when the
+// tile starts.
+template <int HD>
+struct SplitTile {
+    static constexpr int KS = HD / 16, DB = HD / 32;
+    f16x8 kh[KS], kl[KS];
+    uint64_t ek[2], ev[2];
+};
+template <int HD>
+struct SplitV {
+    f16x8 vh[HD / 32][2], vl[HD / 32][2];
+};
+
+template <int HD>
+__device__ __forceinline__ void split_load_v(SplitV<HD> &T, const _Float16 *__restrict__ vh,
+                                             const _Float16 *__restrict__ vl, uint32_t k0, uint32_t tp, uint32_t g,
+                                             uint32_t col, uint32_t hf) {
+#pragma unroll
+    for (int b = 0; b < HD / 32; b++)
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const size_t vo = (size_t)(g * HD + 32 * b + col) * tp + k0 + 16 * u + 8 * hf;
+            T.vh[b][u] = *(const f16x8 *)(vh + vo);
+            T.vl[b][u] = *(const f16x8 *)(vl + vo);
+        }
+}
+
+template <int HD>
+__device__ __forceinline__ void split_load(SplitTile<HD> &T, const _Float16 *__restrict__ kh,
+                                           const _Float16 *__restrict__ kl, const int8_t *__restrict__ ek,
+                                           const int8_t *__restrict__ ev, uint32_t k0, uint32_t tp, uint32_t kvd,
+                                           uint32_t g, uint32_t col, uint32_t hf) {
+    // A row rho of S^T holds key pi(rho) = 16 u + 8 ((w % 8) / 4) + 4 (w / 8) + w % 4 (rho = 16 u + w),
+    // so that register r of lane half h holds key 16 (r / 8) + 8 h + r % 8
+    const uint32_t w = col % 16, key = k0 + 16 * (col / 16) + 8 * ((w % 8) / 4) + 4 * (w / 8) + w % 4;
+    const size_t ko = (size_t)key * kvd + g * HD + 8 * hf;
+#pragma unroll
+    for (int s = 0; s < SplitTile<HD>::KS; s++) {
+        T.kh[s] = *(const f16x8 *)(kh + ko + 16 * s);
+        T.kl[s] = *(const f16x8 *)(kl + ko + 16 * s);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        T.ek[u] = *(const uint64_t *)(ek + (size_t)g * tp + k0 + 16 * u + 8 * hf);
+        T.ev[u] = *(const uint64_t *)(ev + (size_t)g * tp + k0 + 16 * u + 8 * hf);
+    }
+}
+
+__device__ __forceinline__ int exp_byte(uint64_t w, int i) { return (int)(int8_t)(uint8_t)(w >> (8 * i)); }
+
+// Causal grouped-query attention on the split operands; the work split, the online softmax and
+// the merge are attention_kernel's. Per key tile: S'^T = k' q'^T (three f16 MFMAs per 16 dims),
+// S = S' 2^(e_q + e_k) scale, masked, online softmax -> p; p' = p 2^(14 + e_v - sigma) (sigma the
+// tile's largest v exponent, so p' <= 2^14) split into two f16 parts; the tile's O'^T = v'^T p'^T
+// (three f16 MFMAs per 16 keys per 32 dims) enters the f32 accumulator scaled by 2^(sigma - 14).
+template <int HD, int W>
+__global__ __launch_bounds__(64 * W) void attention_split_kernel(
+    const _Float16 *__restrict__ qh, const _Float16 *__restrict__ ql, const _Float16 *__restrict__ kh,
+    const _Float16 *__restrict__ kl, const _Float16 *__restrict__ vh, const _Float16 *__restrict__ vl,
+    const int8_t *__restrict__ eq, const int8_t *__restrict__ ek, const int8_t *__restrict__ ev,
+    float *__restrict__ att, uint32_t t, uint32_t tp, uint32_t heads, uint32_t group, float scale) {
+    using T = SplitTile<HD>;
+    constexpr int DB = T::DB, KS = T::KS;
+    __shared__ float red[W][2 + 16 * DB][64];
+    const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6, col = lane & 31u, hf = lane >> 5;
+    const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * 32;  // the longest tiles start first
+    const uint32_t h = blockIdx.y, g = h / group, kv_heads = heads / group;
+    const uint32_t qd = heads * HD, kvd = kv_heads * HD;
+    const uint32_t query = q0 + col;
+    f16x8 qfh[KS], qfl[KS];
+    {
+        const size_t qo = (size_t)query * qd + h * HD + 8 * hf;  // query < tp: rows past t are zero
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            qfh[s] = *(const f16x8 *)(qh + qo + 16 * s);
+            qfl[s] = *(const f16x8 *)(ql + qo + 16 * s);
+        }
+    }
+    const int e_q = (int)eq[(size_t)h * tp + query];
+    f32x16 o[DB];
+#pragma unroll
+    for (int b = 0; b < DB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[b][i] = 0.0f;
+    float mrun = -INFINITY, lrun = 0.0f;
+    const uint32_t tiles = (min(q0 + 31u, t - 1u)) / 32 + 1;  // key tiles any valid query of the block sees
+    T cur, nxt;
+    if (w < tiles) split_load<HD>(cur, kh, kl, ek, ev, 32 * w, tp, kvd, g, col, hf);
+    for (uint32_t kt = w; kt < tiles; kt += W) {
+        const uint32_t k0 = 32 * kt;
+        SplitV<HD> vt;  // the tile's values, needed after the softmax
+        split_load_v<HD>(vt, vh, vl, k0, tp, g, col, hf);
+        if (kt + W < tiles) split_load<HD>(nxt, kh, kl, ek, ev, k0 + 32 * W, tp, kvd, g, col, hf);
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; i++) s[i] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < KS; st++) {
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.kh[st], qfh[st], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.kh[st], qfl[st], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.kl[st], qfh[st], s, 0, 0, 0);
+        }
+        float mt = -INFINITY;
+        int sig = kSplitPad;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t key = k0 + 16 * (i / 8) + 8 * hf + i % 8;
+            const float v = key <= query ? ldexpf(s[i], e_q + exp_byte(cur.ek[i / 8], i % 8)) * scale : -INFINITY;
+            s[i] = v;
+            mt = fmaxf(mt, v);
+            sig = max(sig, exp_byte(cur.ev[i / 8], i % 8));
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        sig = max(sig, __shfl_xor(sig, 32));
+        const float mnew = fmaxf(mrun, mt);  // finite: key k0 <= query in every tile
+        const float alpha = __expf(mrun - mnew);
+        float ls = 0.0f;
+        f16x8 ph[2], pl[2];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float p = __expf(s[i] - mnew);
+            ls += p;
+            const float x = ldexpf(p, 14 + exp_byte(cur.ev[i / 8], i % 8) - sig);
+            const _Float16 hi = (_Float16)x;
+            ph[i / 8][i % 8] = hi;
+            pl[i / 8][i % 8] = (_Float16)(x - (float)hi);
+        }
+        lrun = lrun * alpha + ls;
+        mrun = mnew;
+        const float back = ldexpf(1.0f, sig - 14);
+#pragma unroll
+        for (int b = 0; b < DB; b++) {
+            f32x16 tb;
+#pragma unroll
+            for (int i = 0; i < 16; i++) tb[i] = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                tb = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt.vh[b][u], ph[u], tb, 0, 0, 0);
+                tb = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt.vh[b][u], pl[u], tb, 0, 0, 0);
+                tb = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt.vl[b][u], ph[u], tb, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[b][i] = fmaf(tb[i], back, o[b][i] * alpha);
+        }
+        cur = nxt;
+    }
+    // merge the wavefronts' partial softmaxes: M = max m_w, O = sum O_w e^(m_w - M), l likewise
+    red[w][0][lane] = mrun;
+    red[w][1][lane] = lrun;
+#pragma unroll
+    for (int b = 0; b < DB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) red[w][2 + 16 * b + i][lane] = o[b][i];
+    __syncthreads();
+    if (w) return;
+    float M = red[0][0][lane];
+#pragma unroll
+    for (int j = 1; j < W; j++) M = fmaxf(M, red[j][0][lane]);
+    float f[W], l = 0.0f;
+#pragma unroll
+    for (int j = 0; j < W; j++) {
+        f[j] = __expf(red[j][0][lane] - M);  // a wavefront without tiles: e^(-inf) = 0
+        l += red[j][1][lane] * f[j];
+    }
+    l += __shfl_xor(l, 32);
+    const float inv = 1.0f / l;
+    if (query >= t) return;
+    float *out = att + (size_t)query * qd + h * HD;
+#pragma unroll
+    for (int b = 0; b < DB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t dim = 32 * b + 8 * (i / 4) + 4 * hf + (i % 4);
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < W; j++) acc += red[j][2 + 16 * b + i][lane] * f[j];
+            out[dim] = acc * inv;
+        }
+}
+
 // SwiGLU (ferrum_ref/src/models/llama/ops.rs:69-76): act[r][j] = silu(gu[r][j]) * gu[r][hid + j].
 __global__ __launch_bounds__(256) void swiglu_kernel(const float *__restrict__ gu, float *__restrict__ act, uint32_t rows,
                                                      uint32_t hid) {
@@ -479,6 +735,9 @@ size_t linear_ws(const fh_llama *m, size_t rows, size_t k, size_t n) {
 }
 
 // The activations for t rows (kept when already large enough).
+// Head dims whose attention runs on the split f16 operands (the f32-MFMA kernel takes the rest).
+bool split_attention(const fh_llama *m) { return m->head_dim == 32 || m->head_dim == 64 || m->head_dim == 128; }
+
 fh_status ensure_rows(fh_llama *m, size_t t) {
     if (t <= m->rows) return FH_OK;
     const size_t d = m->dim, qd = m->q_dim(), w = m->qkv_width(), hid = m->hidden, chunk = logit_chunk(m, t);
@@ -486,9 +745,13 @@ fh_status ensure_rows(fh_llama *m, size_t t) {
     for (auto kn : {std::pair<size_t, size_t>{d, w}, {qd, d}, {d, 2 * hid}, {hid, d}})
         ws = std::max(ws, linear_ws(m, t, kn.first, kn.second));
     ws = std::max(ws, linear_ws(m, chunk, d, m->vocab));
+    const size_t tp = (t + 31) / 32 * 32, kvd = m->kv_dim();
+    const size_t split = split_attention(m) ? 2 * up256(tp * qd * 2) + 4 * up256(tp * kvd * 2) + up256(tp * m->heads) +
+                                                  2 * up256(tp * m->kv_heads)
+                                            : 0;
     const size_t total = 3 * up256(t * d * 4) + up256(t * w * 4) + up256(t * qd * 4) + up256(t * 2 * hid * 4) +
                          up256(t * hid * 4) + up256(chunk * m->vocab * 4) + up256(2 * t * 4) + up256((t + 1) * 4) +
-                         up256(ws);
+                         up256(ws) + split;
     void *p = nullptr;
     fh_status st = alloc_bytes(m->dev, total, &p);
     if (st) return st;
@@ -516,6 +779,17 @@ fh_status ensure_rows(fh_llama *m, size_t t) {
     m->scores = (float *)take(2 * t * 4);
     m->ids = (int32_t *)take((t + 1) * 4);
     m->ws = take(ws);
+    if (split) {
+        m->sqh = (_Float16 *)take(tp * qd * 2);
+        m->sql = (_Float16 *)take(tp * qd * 2);
+        m->skh = (_Float16 *)take(tp * kvd * 2);
+        m->skl = (_Float16 *)take(tp * kvd * 2);
+        m->svh = (_Float16 *)take(tp * kvd * 2);
+        m->svl = (_Float16 *)take(tp * kvd * 2);
+        m->seq = (int8_t *)take(tp * m->heads);
+        m->sek = (int8_t *)take(tp * m->kv_heads);
+        m->sev = (int8_t *)take(tp * m->kv_heads);
+    }
     return FH_OK;
 }
 
@@ -552,6 +826,21 @@ hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t) {
     const uint32_t w = (uint32_t)m->qkv_width(), group = (uint32_t)(m->heads / m->kv_heads);
     const float scale = 1.0f / sqrtf((float)m->head_dim);
     const uint32_t T = (uint32_t)t, H = (uint32_t)m->heads;
+    if (split_attention(m)) {
+        const uint32_t tp = (T + 31) / 32 * 32, KV = (uint32_t)m->kv_heads;
+#define FH_SPLIT_ATTN(HD, W)                                                                                        \
+    attn_split_kernel<HD><<<tp, 256, 0, s>>>(m->qkv, m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl, m->seq, m->sek, \
+                                             m->sev, T, tp, w, H, KV);                                             \
+    attention_split_kernel<HD, W><<<grid, 64 * W, 0, s>>>(m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl, m->seq,  \
+                                                          m->sek, m->sev, m->att, T, tp, H, group, scale)
+        switch (m->head_dim) {
+        case 32: FH_SPLIT_ATTN(32, 4); break;
+        case 64: FH_SPLIT_ATTN(64, 4); break;
+        default: FH_SPLIT_ATTN(128, 2); break;
+        }
+#undef FH_SPLIT_ATTN
+        return hipGetLastError();
+    }
     switch (m->head_dim) {
     case 8: attention_kernel<8, 4><<<grid, 256, 0, s>>>(m->qkv, m->att, T, w, H, group, scale); break;
     case 16: attention_kernel<16, 4><<<grid, 256, 0, s>>>(m->qkv, m->att, T, w, H, group, scale); break;
