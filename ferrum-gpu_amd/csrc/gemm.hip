@@ -1087,7 +1087,7 @@ struct BigLoad {  // one thread's share of a stage in flight
     static constexpr int QB = KIND == FH_Q8_0 ? 32 : 16;  // quant bytes per block
     static constexpr int QL = QB / 16;                    // 16-byte quant loads: one block of its column
     u32x4 a[4], q[QL];
-    uint32_t d, dmask;
+    uint32_t d, dmask, sx;
 };
 
 template <int KIND>
@@ -1097,43 +1097,62 @@ __global__ __launch_bounds__(512, 1) void gemm_f16_big_kernel(const _Float16 *__
                                                               const uint16_t *__restrict__ ds, float *__restrict__ y,
                                                               uint32_t M, uint32_t K, uint32_t N, uint32_t mt,
                                                               uint32_t nt, uint32_t split_stages) {
+    // split_stages is even (the stage loop runs pairs)
     using L = BigLoad<KIND>;
     __shared__ __attribute__((aligned(16))) _Float16 sA0[256 * kBigStr], sA1[256 * kBigStr];
     __shared__ __attribute__((aligned(16))) _Float16 sB0[256 * kBigStr], sB1[256 * kBigStr];
+    __shared__ float sxs[2][256];  // the row scales of the tiles in flight (by tile parity)
 
-    uint32_t mi, ni;
-    if (!xcd_tile(mt, nt, &mi, &ni)) return;  // whole CTA: no barrier is left waiting
-    const uint32_t m0 = mi * 256, n0 = ni * 256;
+    // This CTA's tiles: XCD x (blockIdx.x % 8) owns the x-th equal run of xcd_tile's grouped tile
+    // order and its CTAs take the run's tiles round robin. A CTA works through its tiles' stages
+    // as one stream: the first stages of its next tile are loaded and stored while it computes
+    // the last ones of the current tile, and a tile's output stores drain during the next one.
+    constexpr uint32_t GM = 4;
+    const uint32_t tiles = mt * nt, per_xcd = (tiles + 7) / 8, ctas = gridDim.x / 8;
+    const uint32_t run0 = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8, run1 = min(tiles, (blockIdx.x % 8 + 1) * per_xcd);
+    if (run0 >= run1) return;  // whole CTA: no barrier is left waiting
+    const uint32_t my_tiles = (run1 - run0 + ctas - 1) / ctas;
+    auto origin = [&](uint32_t k, uint32_t &m0, uint32_t &n0) {  // row and column of my k-th tile
+        const uint32_t t = run0 + k * ctas;
+        const uint32_t grp = t / (GM * nt), in = t % (GM * nt), gm = min(GM, mt - grp * GM);
+        m0 = (grp * GM + in % gm) * 256;
+        n0 = (in / gm) * 256;
+    };
 
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, wm = wave % 2, wn = wave / 2;
     const uint32_t nb = K / 32, all_stages = (nb + 1) / 2;
     const uint32_t st0 = blockIdx.y * split_stages, st1 = min(all_stages, st0 + split_stages);
+    const uint32_t stream = my_tiles * split_stages;  // positions p: tile p / split_stages, stage st0 + p % split_stages
     y += (size_t)blockIdx.y * M * N;
     const int fr = lane % 32, hf = lane / 32;
 
     const auto r_xh = make_rsrc(xh, M * nb * 64);
     const auto r_q = make_rsrc(qs, (N + 31) / 32 * 32 * nb * L::QB);
     const auto r_d = make_rsrc(ds, (N + 31) / 32 * 32 * ((nb + 7) / 8 * 8) * 2);
+    const auto r_s = make_rsrc(xs, M * 4);
     constexpr uint32_t kOut = 0x80000000u;
-    // x: chunk c = tid + 512 i is row c / 8, 16 bytes (c % 8) of the row's 128-byte stage
-    uint32_t o_a[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t m = m0 + (tid + 512 * i) / 8;
-        o_a[i] = m < M ? (m * nb * 32 + (tid % 8) * 8) * 2 : kOut;
-    }
+    // x: chunk c = tid + 512 i is row c / 8, 16 bytes (c % 8) of the row's 128-byte stage;
     // weights: thread t owns block bq = t / 256 of the stage in column n0 + t % 256 (its quants
     // and the column's scale dword, of which it uses half bq)
     const int cq = tid % 256, bq = tid / 256;
-    const uint32_t n = n0 + cq;
-    const uint32_t o_q = ((n >> 5) * nb * 32 + (n & 31)) * L::QB;
-    const uint32_t o_d = ((n >> 5) * ((nb + 7) / 8) * 32 + (n & 31)) * 16;
 
     L ld0, ld1;  // two stages in flight: each load has two stages of MFMAs to arrive
-    auto load_stage = [&](L &ld, uint32_t st) {
-        // past the CTA's stages everything reads 0 (the loop runs an even number of stages);
-        // an odd last stage of the product has one block, and its second block reads 0
-        const bool live = st < st1, two = live && 2 * st + 1 < nb;
+    auto load_stage = [&](L &ld, uint32_t p) {
+        // past the tile's stages (the loop runs an even number) and past the stream everything
+        // reads 0; an odd last stage of the product has one block, and its second block reads 0
+        const uint32_t st = st0 + p % split_stages;
+        const bool live = p < stream && st < st1, two = live && 2 * st + 1 < nb;
+        uint32_t m0, n0;
+        origin(p / split_stages, m0, n0);
+        uint32_t o_a[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t m = m0 + (tid + 512 * i) / 8;
+            o_a[i] = m < M ? (m * nb * 32 + (tid % 8) * 8) * 2 : kOut;
+        }
+        const uint32_t n = n0 + cq;
+        const uint32_t o_q = ((n >> 5) * nb * 32 + (n & 31)) * L::QB;
+        const uint32_t o_d = ((n >> 5) * ((nb + 7) / 8) * 32 + (n & 31)) * 16;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t off = (live && (tid % 8) < 4) || two ? o_a[i] + st * 128 : kOut;
@@ -1148,9 +1167,14 @@ __global__ __launch_bounds__(512, 1) void gemm_f16_big_kernel(const _Float16 *__
         ld.d = __builtin_amdgcn_raw_buffer_load_b32(r_d, mine ? (int)(o_d + (st >> 2) * 512 + (st & 3) * 4) : (int)kOut,
                                                     0, 0);
         ld.dmask = mine ? 0xffffffffu : 0u;  // a missing block's scale is 0, so its values are 0
+        // a tile's first stage also carries its row scales (thread t < 256: row m0 + t), for the
+        // epilogue through LDS: a global load there would wait behind the next tile's loads
+        ld.sx = __builtin_amdgcn_raw_buffer_load_b32(
+            r_s, p % split_stages == 0 && p < stream && tid < 256 ? (int)((m0 + tid) * 4) : (int)kOut, 0, 0);
         // (applied when the stage is stored: using the loaded value here would wait for the load)
     };
-    auto store_stage = [&](const L &ld, _Float16 *sa, _Float16 *sb) {
+    auto store_stage = [&](const L &ld, _Float16 *sa, _Float16 *sb, int first) {
+        if (first >= 0 && tid < 256) sxs[first][tid] = __uint_as_float(ld.sx);
 #pragma unroll
         for (int i = 0; i < 4; i++) *(u32x4 *)(sa + ((tid + 512 * i) / 8) * kBigStr + (tid % 8) * 8) = ld.a[i];
         _Float16 *col = sb + cq * kBigStr + bq * 32;
@@ -1211,47 +1235,56 @@ __global__ __launch_bounds__(512, 1) void gemm_f16_big_kernel(const _Float16 *__
         __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // step 3's MFMAs
     };
 
-    load_stage(ld0, st0);
-    load_stage(ld1, st0 + 1);
-    store_stage(ld0, sA0, sB0);
-    load_stage(ld0, st0 + 2);
-    // Two stages per trip (the buffers and staging registers are then known apart); an odd count
-    // ends with a stage of zeros. Scheduling barriers keep each phase in place: nothing that
-    // reads a staged load may be moved up into the MFMAs issued while that load is in flight.
-    const uint32_t stages = st1 > st0 ? st1 - st0 : 0;
-    uint32_t st = st0;
-    for (uint32_t it = 0; it < (stages + 1) / 2; it++, st += 2) {
-        __syncthreads();  // stage st is in buffer 0; every wave is done with buffer 1
+    auto epilogue = [&](uint32_t k) {
+        uint32_t m0, n0;
+        origin(k, m0, n0);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * hf + r % 4;
+                if (row >= M) continue;
+                const float sx = sxs[k % 2][row - m0];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const uint32_t col = n0 + wn * 64 + j * 32 + fr;
+                    if (col < N) y[(size_t)row * N + col] = acc[i][j][r] * sx;
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    };
+
+    load_stage(ld0, 0);
+    load_stage(ld1, 1);
+    store_stage(ld0, sA0, sB0, 0);
+    load_stage(ld0, 2);
+    // Two stages per trip (the buffers and staging registers are then known apart). Scheduling
+    // barriers keep each phase in place: nothing that reads a staged load may be moved up into
+    // the MFMAs issued while that load is in flight.
+    for (uint32_t p = 0; p < stream; p += 2) {
+        __syncthreads();  // stage p is in buffer 0; every wave is done with buffer 1
         __builtin_amdgcn_sched_barrier(0);
         read(sA0, sB0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        store_stage(ld1, sA1, sB1);
-        load_stage(ld1, st + 3);
+        store_stage(ld1, sA1, sB1, -1);  // (odd stages never start a tile)
+        load_stage(ld1, p + 3);
         __builtin_amdgcn_sched_barrier(0);
         compute(sA0, sB0);
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         read(sA1, sB1, 0);
         __builtin_amdgcn_sched_barrier(0);
-        store_stage(ld0, sA0, sB0);
-        load_stage(ld0, st + 4);
+        store_stage(ld0, sA0, sB0, (p + 2) % split_stages == 0 ? (int)(((p + 2) / split_stages) % 2) : -1);
+        load_stage(ld0, p + 4);
         __builtin_amdgcn_sched_barrier(0);
         compute(sA1, sB1);
+        if ((p + 2) % split_stages == 0) epilogue(p / split_stages);  // the tile's last stage pair
     }
-
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r / 4) + 4 * hf + r % 4;
-            if (row >= M) continue;
-            const float sx = xs[row];
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const uint32_t col = n0 + wn * 64 + j * 32 + fr;
-                if (col < N) y[(size_t)row * N + col] = acc[i][j][r] * sx;
-            }
-        }
 }
 
 struct GemmF16Args {
@@ -1315,10 +1348,15 @@ hipError_t run_gemm_f16_big(hipStream_t s, const GemmF16Args &g, uint32_t sp) {
     const uint64_t tiles = (uint64_t)mt * nt;
     if (tiles > 0x7ffffff0ull) return hipErrorInvalidValue;
     const uint32_t per_xcd = (uint32_t)((tiles + 7) / 8);
+    // one CTA per CU, each XCD's CTAs working through its run of tiles
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8)
+        cus = 256;
+    const uint32_t ctas = min(per_xcd, (uint32_t)cus / 8);
     const uint32_t stages = (g.K / 32 + 1) / 2;
     const uint32_t per = ((stages + sp - 1) / sp + 1) & ~1u;  // even: the kernel runs stages in pairs
     float *out = sp > 1 ? g.partial : g.y;
-    gemm_f16_big_kernel<KIND><<<dim3(8 * per_xcd, sp), 512, 0, s>>>(g.xh, g.xs, g.qs, g.ds, out, g.M, g.K, g.N, mt,
+    gemm_f16_big_kernel<KIND><<<dim3(8 * ctas, sp), 512, 0, s>>>(g.xh, g.xs, g.qs, g.ds, out, g.M, g.K, g.N, mt,
                                                                      nt, per);
     if (sp > 1) {
         const size_t n = (size_t)g.M * g.N;
