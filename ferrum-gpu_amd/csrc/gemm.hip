@@ -132,12 +132,22 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float *__restrict__ 
     __shared__ float red[4];
     const uint32_t m = blockIdx.x, tid = threadIdx.x, nb = K / 32, K64 = (K + 63) / 64 * 64;
     if (K64 != K && tid < 8) *(uint32_t *)(xl + (size_t)m * K64 + K + 4 * tid) = 0u;  // the row's zero tail
-    const float *xr = x + (size_t)m * K;
+    // The row is read once: thread t keeps float4 t + 256 i for i < kKeep in registers (rows up
+    // to 8192 wide; wider rows read the rest twice). Float4 q is elements 4 (q % 8) .. + 3 of
+    // block q / 8, so eight consecutive lanes hold one block.
+    constexpr int kKeep = 8;
+    const uint32_t nq = K / 4;
+    const f32x4 *xr = (const f32x4 *)(x + (size_t)m * K);
+    f32x4 v[kKeep];
     float mx = 0.0f;
-    for (uint32_t i = tid * 4; i < K; i += 1024) {
-        const f32x4 v = *(const f32x4 *)(xr + i);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    auto amax = [](f32x4 a) { return fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))); };
+#pragma unroll
+    for (int i = 0; i < kKeep; i++) {
+        const uint32_t q = tid + 256 * i;
+        v[i] = q < nq ? xr[q] : f32x4{0.f, 0.f, 0.f, 0.f};
+        mx = fmaxf(mx, amax(v[i]));
     }
+    for (uint32_t q = tid + 256 * kKeep; q < nq; q += 256) mx = fmaxf(mx, amax(xr[q]));
 #pragma unroll
     for (int o = 32; o >= 1; o /= 2) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     if (tid % 64 == 0) red[tid / 64] = mx;
@@ -150,8 +160,9 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float *__restrict__ 
     const float f = __uint_as_float((uint32_t)(127 + sc) << 23);
     if (tid == 0) xsc[m] = (127 - sc) * 0x01010101;
     const int j = tid % 8;
-    for (uint32_t t = tid / 8; t < nb; t += 32) {
-        const f32x4 v = *(const f32x4 *)(xr + t * 32 + 4 * j);
+    // (q < nq is the same for the eight lanes of a block: nq is a multiple of 8)
+    auto put = [&](uint32_t qi, f32x4 v) {
+        const uint32_t t = qi / 8;
         _Float16 h[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) h[q] = f16_sat(v[q]);
@@ -171,7 +182,13 @@ __global__ __launch_bounds__(256) void split_x_kernel(const float *__restrict__ 
                 o[q] = __builtin_bit_cast(_Float16, (uint16_t)__shfl_xor((int)__builtin_bit_cast(uint16_t, h[q]), 4, 8));
             if (j < 4) *(f16x8 *)(out + 8 * j) = f16x8{h[0], h[2], h[1], h[3], o[0], o[2], o[1], o[3]};
         }
+    };
+#pragma unroll
+    for (int i = 0; i < kKeep; i++) {
+        const uint32_t q = tid + 256 * i;
+        if (q < nq) put(q, v[i]);
     }
+    for (uint32_t q = tid + 256 * kKeep; q < nq; q += 256) put(q, xr[q]);
 }
 
 // ---- the weights' fp8 correction operand: e4m3 of d * q * 2^t per element, natural k order, ----
@@ -854,14 +871,23 @@ hipError_t gemm_precise_dispatch(hipStream_t s, const _Float16 *xs, const uint8_
 template <int KIND>
 __global__ __launch_bounds__(256) void split_x_f16_kernel(const float *__restrict__ x, _Float16 *__restrict__ xh,
                                                           float *__restrict__ xs, uint32_t K) {
+    // The row is read once: thread t keeps float4 t + 256 i for i < kKeep in registers (rows up to
+    // 8192 wide; wider rows read the rest twice). Float4 q is elements 4 (q % 8) .. + 3 of block
+    // q / 8, so eight consecutive lanes hold one block.
+    constexpr int kKeep = 8;
     __shared__ float red[4];
-    const uint32_t m = blockIdx.x, tid = threadIdx.x, nb = K / 32;
-    const float *xr = x + (size_t)m * K;
+    const uint32_t m = blockIdx.x, tid = threadIdx.x, nb = K / 32, nq = K / 4;
+    const f32x4 *xr = (const f32x4 *)(x + (size_t)m * K);
+    f32x4 v[kKeep];
     float mx = 0.0f;
-    for (uint32_t i = tid * 4; i < K; i += 1024) {
-        const f32x4 v = *(const f32x4 *)(xr + i);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    auto amax = [](f32x4 a) { return fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))); };
+#pragma unroll
+    for (int i = 0; i < kKeep; i++) {
+        const uint32_t q = tid + 256 * i;
+        v[i] = q < nq ? xr[q] : f32x4{0.f, 0.f, 0.f, 0.f};
+        mx = fmaxf(mx, amax(v[i]));
     }
+    for (uint32_t q = tid + 256 * kKeep; q < nq; q += 256) mx = fmaxf(mx, amax(xr[q]));
 #pragma unroll
     for (int o = 32; o >= 1; o /= 2) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
     if (tid % 64 == 0) red[tid / 64] = mx;
@@ -874,11 +900,12 @@ __global__ __launch_bounds__(256) void split_x_f16_kernel(const float *__restric
     const float f = __uint_as_float((uint32_t)(127 - sc) << 23);
     if (tid == 0) xs[m] = __uint_as_float((uint32_t)(127 + sc) << 23);
     const int j = tid % 8;
-    for (uint32_t t = tid / 8; t < nb; t += 32) {
-        const f32x4 v = *(const f32x4 *)(xr + t * 32 + 4 * j);
+    // (q < nq is the same for the eight lanes of a block: nq is a multiple of 8)
+    auto put = [&](uint32_t q, f32x4 w) {
+        const uint32_t t = q / 8;
         _Float16 h[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) h[q] = (_Float16)(v[q] * f);
+        for (int c = 0; c < 4; c++) h[c] = (_Float16)(w[c] * f);
         _Float16 *out = xh + ((size_t)m * nb + t) * 32;
         typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
         if constexpr (KIND == FH_Q8_0) {
@@ -886,11 +913,17 @@ __global__ __launch_bounds__(256) void split_x_f16_kernel(const float *__restric
         } else {
             _Float16 o[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-                o[q] = __builtin_bit_cast(_Float16, (uint16_t)__shfl_xor((int)__builtin_bit_cast(uint16_t, h[q]), 4, 8));
+            for (int c = 0; c < 4; c++)
+                o[c] = __builtin_bit_cast(_Float16, (uint16_t)__shfl_xor((int)__builtin_bit_cast(uint16_t, h[c]), 4, 8));
             if (j < 4) *(f16x8 *)(out + 8 * j) = f16x8{h[0], h[2], h[1], h[3], o[0], o[2], o[1], o[3]};
         }
+    };
+#pragma unroll
+    for (int i = 0; i < kKeep; i++) {
+        const uint32_t q = tid + 256 * i;
+        if (q < nq) put(q, v[i]);
     }
+    for (uint32_t q = tid + 256 * kKeep; q < nq; q += 256) put(q, xr[q]);
 }
 
 // f16 pairs times one f16 scale (round to nearest: d q is exact before the rounding)
