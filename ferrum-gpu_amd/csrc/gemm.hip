@@ -329,6 +329,7 @@ struct GemmArgs {
     float *y;
     float *partial;  // K-split partial products (up to 8 x M x N floats), or null: no split
     uint32_t M, K, N;
+    SplitOut *defer = nullptr;  // set: the partial sums are left for the consumer
 };
 
 // ---- the MFMA GEMM ----
@@ -617,7 +618,8 @@ hipError_t run_gemm(hipStream_t s, const GemmArgs &g) {
     float *out = sp > 1 ? g.partial : g.y;
     gemm_kernel<KIND, BM, BN, WAVES_M><<<dim3(grid, sp), 256, 0, s>>>(g.xh, g.xl, g.xsc, g.qs, g.ds, g.b8, g.bsc, out,
                                                                        g.M, g.K, g.N, mt, nt, per);
-    if (sp > 1) {
+    if (g.defer) *g.defer = sp > 1 ? SplitOut{g.partial, sp} : SplitOut{g.y, 1u};
+    if (sp > 1 && !g.defer) {
         const size_t n = (size_t)g.M * g.N;
         const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
         gemm_reduce_kernel<<<rg, 256, 0, s>>>(g.partial, g.y, n, sp);  // (a split past the last stage wrote zeros)
@@ -839,7 +841,7 @@ uint32_t precise_splits(size_t rows, size_t k, size_t n) {
 
 template <int KIND, int BM, int BN, int WAVES_M>
 hipError_t run_gemm_precise(hipStream_t s, const _Float16 *xs, const uint8_t *qs, const uint16_t *ds, float *y,
-                            float *partial, uint32_t M, uint32_t K, uint32_t N) {
+                            float *partial, uint32_t M, uint32_t K, uint32_t N, SplitOut *defer) {
     const uint32_t mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
     const uint64_t tiles = (uint64_t)mt * nt;
     if (tiles > 0x7fffffffull) return hipErrorInvalidValue;
@@ -849,7 +851,8 @@ hipError_t run_gemm_precise(hipStream_t s, const _Float16 *xs, const uint8_t *qs
     const uint32_t per = (stages + sp - 1) / sp;
     float *out = sp > 1 ? partial : y;
     gemm_precise_kernel<KIND, BM, BN, WAVES_M><<<dim3(grid, sp), 256, 0, s>>>(xs, qs, ds, out, M, K, N, mt, nt, per);
-    if (sp > 1) {
+    if (defer) *defer = sp > 1 ? SplitOut{partial, sp} : SplitOut{y, 1u};
+    if (sp > 1 && !defer) {
         const size_t n = (size_t)M * N;
         const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
         gemm_reduce_kernel<<<rg, 256, 0, s>>>(partial, y, n, sp);  // (a split past the last stage wrote zeros)
@@ -859,10 +862,10 @@ hipError_t run_gemm_precise(hipStream_t s, const _Float16 *xs, const uint8_t *qs
 
 template <int KIND>
 hipError_t gemm_precise_dispatch(hipStream_t s, const _Float16 *xs, const uint8_t *qs, const uint16_t *ds, float *y,
-                                 float *partial, uint32_t M, uint32_t K, uint32_t N) {
-    if (M <= 32) return run_gemm_precise<KIND, 32, 256, 1>(s, xs, qs, ds, y, partial, M, K, N);
-    if (M <= 64) return run_gemm_precise<KIND, 64, 128, 2>(s, xs, qs, ds, y, partial, M, K, N);
-    return run_gemm_precise<KIND, 128, 128, 2>(s, xs, qs, ds, y, partial, M, K, N);
+                                 float *partial, uint32_t M, uint32_t K, uint32_t N, SplitOut *defer) {
+    if (M <= 32) return run_gemm_precise<KIND, 32, 256, 1>(s, xs, qs, ds, y, partial, M, K, N, defer);
+    if (M <= 64) return run_gemm_precise<KIND, 64, 128, 2>(s, xs, qs, ds, y, partial, M, K, N, defer);
+    return run_gemm_precise<KIND, 128, 128, 2>(s, xs, qs, ds, y, partial, M, K, N, defer);
 }
 
 // ---- the dequant-f16 GEMM (FH_PATH_TILED_F16): weights dequantised into LDS, plain f16 MFMA ----
@@ -1327,6 +1330,7 @@ struct GemmF16Args {
     const uint16_t *ds;
     float *y, *partial;
     uint32_t M, K, N;
+    SplitOut *defer = nullptr;  // set: the partial sums are left for the consumer
 };
 
 template <int KIND, int BM, int BN>
@@ -1341,7 +1345,8 @@ hipError_t run_gemm_f16(hipStream_t s, const GemmF16Args &g) {
     float *out = sp > 1 ? g.partial : g.y;
     gemm_f16_kernel<KIND, BM, BN><<<dim3(grid, sp), 256, 0, s>>>(g.xh, g.xs, g.qs, g.ds, out, g.M, g.K, g.N, mt, nt,
                                                                   per);
-    if (sp > 1) {
+    if (g.defer) *g.defer = sp > 1 ? SplitOut{g.partial, sp} : SplitOut{g.y, 1u};
+    if (sp > 1 && !g.defer) {
         const size_t n = (size_t)g.M * g.N;
         const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
         gemm_reduce_kernel<<<rg, 256, 0, s>>>(g.partial, g.y, n, sp);
@@ -1391,7 +1396,8 @@ hipError_t run_gemm_f16_big(hipStream_t s, const GemmF16Args &g, uint32_t sp) {
     float *out = sp > 1 ? g.partial : g.y;
     gemm_f16_big_kernel<KIND><<<dim3(8 * ctas, sp), 512, 0, s>>>(g.xh, g.xs, g.qs, g.ds, out, g.M, g.K, g.N, mt,
                                                                      nt, per);
-    if (sp > 1) {
+    if (g.defer) *g.defer = sp > 1 ? SplitOut{g.partial, sp} : SplitOut{g.y, 1u};
+    if (sp > 1 && !g.defer) {
         const size_t n = (size_t)g.M * g.N;
         const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
         gemm_reduce_kernel<<<rg, 256, 0, s>>>(g.partial, g.y, n, sp);
@@ -1451,7 +1457,7 @@ size_t gemm_precise_workspace_bytes(size_t rows, size_t k, size_t n) {
 }
 
 hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
-                               float *y, size_t rows, size_t k, size_t n, void *workspace) {
+                               float *y, size_t rows, size_t k, size_t n, void *workspace, SplitOut *defer) {
     _Float16 *xs = (_Float16 *)workspace;
     float *partial = precise_splits(rows, k, n) > 1
                          ? (float *)((uint8_t *)workspace + (rows * k * 4 + 255) / 256 * 256)
@@ -1460,10 +1466,12 @@ hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, c
     const unsigned g = (unsigned)(items / 32 + 1 < 65535 ? items / 32 + 1 : 65535);
     if (kind == FH_Q8_0) {
         split_x_precise_kernel<FH_Q8_0><<<g, 256, 0, s>>>(x, xs, items);
-        return gemm_precise_dispatch<FH_Q8_0>(s, xs, qs, ds, y, partial, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+        return gemm_precise_dispatch<FH_Q8_0>(s, xs, qs, ds, y, partial, (uint32_t)rows, (uint32_t)k, (uint32_t)n,
+                                              defer);
     }
     split_x_precise_kernel<FH_Q4_0><<<g, 256, 0, s>>>(x, xs, items);
-    return gemm_precise_dispatch<FH_Q4_0>(s, xs, qs, ds, y, partial, (uint32_t)rows, (uint32_t)k, (uint32_t)n);
+    return gemm_precise_dispatch<FH_Q4_0>(s, xs, qs, ds, y, partial, (uint32_t)rows, (uint32_t)k, (uint32_t)n,
+                                          defer);
 }
 
 hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
@@ -1478,7 +1486,7 @@ hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const ui
 }
 
 hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
-                       const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace) {
+                       const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace, SplitOut *defer) {
     const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     uint8_t *ws = (uint8_t *)workspace;
     GemmArgs g;
@@ -1495,6 +1503,7 @@ hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uin
     g.M = (uint32_t)rows;
     g.K = (uint32_t)k;
     g.N = (uint32_t)n;
+    g.defer = defer;
     if (kind == FH_Q8_0) {
         split_x_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
         return gemm_dispatch<FH_Q8_0>(s, g);
@@ -1522,7 +1531,7 @@ bool gemm_f16_supported(size_t rows, size_t k, size_t n) {
 }
 
 hipError_t launch_gemm_f16(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x, float *y,
-                           size_t rows, size_t k, size_t n, void *workspace) {
+                           size_t rows, size_t k, size_t n, void *workspace, SplitOut *defer) {
     const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     uint8_t *ws = (uint8_t *)workspace;
     GemmF16Args g;
@@ -1537,6 +1546,7 @@ hipError_t launch_gemm_f16(hipStream_t s, fh_kind kind, const uint8_t *qs, const
     g.M = (uint32_t)rows;
     g.K = (uint32_t)k;
     g.N = (uint32_t)n;
+    g.defer = defer;
     if (kind == FH_Q8_0) {
         split_x_f16_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (float *)g.xs, g.K);
         return gemm_f16_dispatch<FH_Q8_0>(s, g);

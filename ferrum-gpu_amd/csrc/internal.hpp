@@ -173,6 +173,14 @@ hipError_t launch_gemv(hipStream_t s, fh_kind kind, const uint8_t *qs, const uin
 hipError_t launch_gemv_group(hipStream_t s, fh_kind kind, const GemvDesc *descs, const uint32_t *map,
                              uint32_t count, uint32_t tasks, uint32_t max_nb, int cus);
 
+// A K-split product left unreduced for its consumer: y(r, c) = the sum over s < splits of
+// part[s * rows * n + r * n + c], added in split order (the reduction kernel's order, so a
+// consumer that sums them reproduces the reduced product bit for bit). splits == 1: part is y.
+struct SplitOut {
+    float *part;
+    uint32_t splits;
+};
+
 // gemm.hip
 hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
                         float *y, size_t rows, size_t k, size_t n);
@@ -186,16 +194,18 @@ bool gemm_supported(size_t rows, size_t k, size_t n);
 hipError_t launch_make_b8(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, uint8_t *b8, size_t k,
                           size_t n);
 hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
-                       const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace);
+                       const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace,
+                       SplitOut *defer = nullptr);
 // The dequant-f16 MFMA GEMM (x as f16 with a power-of-two row scale, weights dequantised to f16
 // in LDS; split into workspace, then the product).
 size_t gemm_f16_workspace_bytes(size_t rows, size_t k, size_t n);
 bool gemm_f16_supported(size_t rows, size_t k, size_t n);
 hipError_t launch_gemm_f16(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x, float *y,
-                           size_t rows, size_t k, size_t n, void *workspace);
+                           size_t rows, size_t k, size_t n, void *workspace, SplitOut *defer = nullptr);
 // The precise MFMA GEMM (x as two f16 parts; split into workspace, then the product).
 size_t gemm_precise_workspace_bytes(size_t rows, size_t k, size_t n);
 hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
-                               float *y, size_t rows, size_t k, size_t n, void *workspace);
+                               float *y, size_t rows, size_t k, size_t n, void *workspace,
+                               SplitOut *defer = nullptr);
 
 }  // namespace fh

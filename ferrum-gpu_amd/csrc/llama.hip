@@ -110,19 +110,28 @@ __device__ __forceinline__ float block_sum_256(float v, float *red) {
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+
+// Element i of a product that a GEMM left as K-split partial sums (SplitOut: `splits` slices
+// `stride` floats apart, summed in split order as the reduction kernel would; one slice: p[i]).
+__device__ __forceinline__ float split_sum(const float *__restrict__ p, size_t i, uint32_t splits, size_t stride) {
+    float t = p[i];
+    for (uint32_t sl = 1; sl < splits; sl++) t += p[sl * stride + i];
+    return t;
+}
+
 // RMSNorm per row (ferrum_ref/src/models/llama/ops.rs:55-66): h = v / sqrt(mean(v^2) + eps) * g,
 // v = x, or with ADD v = x + o stored back into x first (the residual add, nn::add).
 template <bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(float *__restrict__ x, const float *__restrict__ o,
                                                       const float *__restrict__ g, float *__restrict__ h, uint32_t d,
-                                                      float eps) {
+                                                      float eps, uint32_t o_splits, size_t o_stride) {
     __shared__ float red[4];
     const size_t base = (size_t)blockIdx.x * d;
     float ss = 0.0f;
     for (uint32_t i = threadIdx.x; i < d; i += 256) {
         float v = x[base + i];
         if constexpr (ADD) {
-            v = v + o[base + i];
+            v = v + split_sum(o, base + i, o_splits, o_stride);
             x[base + i] = v;
         }
         ss += v * v;
@@ -136,13 +145,17 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *__restrict__ x, con
 // the row's q and k heads rotate their first rope_dim channels by table row `row` (the position),
 // NORM pairing (2i, 2i + 1) or NEOX (i, i + rope_dim / 2). The row is staged in LDS so every
 // output reads the biased inputs.
-__global__ __launch_bounds__(256) void qkv_rope_kernel(float *__restrict__ qkv, const float *__restrict__ bias,
-                                                       const float *__restrict__ cos_t, const float *__restrict__ sin_t,
-                                                       uint32_t width, uint32_t rot_heads, uint32_t hd, uint32_t rope_dim,
-                                                       int neox) {
+__global__ __launch_bounds__(256) void qkv_rope_kernel(const float *__restrict__ src, uint32_t src_splits,
+                                                       size_t src_stride, float *__restrict__ qkv,
+                                                       const float *__restrict__ bias, const float *__restrict__ cos_t,
+                                                       const float *__restrict__ sin_t, uint32_t width,
+                                                       uint32_t rot_heads, uint32_t hd, uint32_t rope_dim, int neox) {
     extern __shared__ float row[];
     const size_t base = (size_t)blockIdx.x * width;
-    for (uint32_t c = threadIdx.x; c < width; c += 256) row[c] = bias ? qkv[base + c] + bias[c] : qkv[base + c];
+    for (uint32_t c = threadIdx.x; c < width; c += 256) {
+        const float v = split_sum(src, base + c, src_splits, src_stride);
+        row[c] = bias ? v + bias[c] : v;
+    }
     __syncthreads();
     const uint32_t half = rope_dim / 2, rotated = rot_heads * hd;
     const float *cr = cos_t + (size_t)blockIdx.x * half, *sr = sin_t + (size_t)blockIdx.x * half;
@@ -558,14 +571,19 @@ __global__ __launch_bounds__(64 * W) void attention_split_kernel(
 }
 
 // SwiGLU (ferrum_ref/src/models/llama/ops.rs:69-76): act[r][j] = silu(gu[r][j]) * gu[r][hid + j].
-__global__ __launch_bounds__(256) void swiglu_kernel(const float *__restrict__ gu, float *__restrict__ act, uint32_t rows,
-                                                     uint32_t hid) {
+__global__ __launch_bounds__(256) void swiglu_kernel(const float *__restrict__ gu, uint32_t gu_splits, size_t gu_stride,
+                                                     float *__restrict__ act, uint32_t rows, uint32_t hid) {
     const uint32_t q = hid / 4;
     const size_t n = (size_t)rows * q;
+    auto load4 = [&](size_t o) {  // four consecutive elements of the (possibly K-split) product
+        f32x4 v = *(const f32x4 *)(gu + o);
+        for (uint32_t sl = 1; sl < gu_splits; sl++) v += *(const f32x4 *)(gu + sl * gu_stride + o);
+        return v;
+    };
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
         const size_t r = i / q, j = i % q;
-        const f32x4 g = *(const f32x4 *)(gu + r * 2 * hid + 4 * j);
-        const f32x4 u = *(const f32x4 *)(gu + r * 2 * hid + hid + 4 * j);
+        const f32x4 g = load4(r * 2 * hid + 4 * j);
+        const f32x4 u = load4(r * 2 * hid + hid + 4 * j);
         f32x4 y;
 #pragma unroll
         for (int c = 0; c < 4; c++) y[c] = __fmul_rn(g[c] / (1.0f + expf(-g[c])), u[c]);
@@ -813,11 +831,14 @@ fh_status check_shapes(const fh_llama *m, size_t t) {
     return FH_OK;
 }
 
-hipError_t linear(const fh_llama *m, hipStream_t s, const fh_qweight *w, const float *x, float *y, size_t rows) {
+// With defer, a K-split product is left as partial sums in the workspace for the next kernel to
+// add up (every consumer runs before the next product overwrites the workspace).
+hipError_t linear(const fh_llama *m, hipStream_t s, const fh_qweight *w, const float *x, float *y, size_t rows,
+                  SplitOut *defer = nullptr) {
     switch (m->path) {
-    case FH_PATH_TILED_FAST: return launch_gemm(s, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, m->ws);
-    case FH_PATH_TILED_F16: return launch_gemm_f16(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws);
-    default: return launch_gemm_precise(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws);
+    case FH_PATH_TILED_FAST: return launch_gemm(s, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, m->ws, defer);
+    case FH_PATH_TILED_F16: return launch_gemm_f16(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws, defer);
+    default: return launch_gemm_precise(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws, defer);
     }
 }
 
@@ -860,28 +881,31 @@ hipError_t enqueue_body(fh_llama *m, hipStream_t s, size_t t) {
         embed_rows_kernel<FH_Q4_0><<<T, 256, 0, s>>>(m->tok->qs, m->tok->ds, m->ids, m->x, d, (uint32_t)m->vocab);
     hipError_t e = hipGetLastError();
     const uint32_t width = (uint32_t)m->qkv_width();
+    const size_t td = t * m->dim;
+    SplitOut down{m->o, 1};  // the previous block's FFN output, added to x by the next RMSNorm
     for (size_t l = 0; l < m->layers && !e; l++) {
         const auto &L = m->blocks[l];
         if (l == 0)
-            rmsnorm_kernel<false><<<T, 256, 0, s>>>(m->x, nullptr, fp(L.attn_norm), m->h, d, m->eps);
+            rmsnorm_kernel<false><<<T, 256, 0, s>>>(m->x, nullptr, fp(L.attn_norm), m->h, d, m->eps, 1, 0);
         else
-            rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, m->o, fp(L.attn_norm), m->h, d, m->eps);
-        if ((e = linear(m, s, L.wqkv, m->h, m->qkv, t))) break;
-        qkv_rope_kernel<<<T, 256, width * 4, s>>>(m->qkv, fp(L.bqkv), fp(m->rope_cos), fp(m->rope_sin), width,
-                                                  (uint32_t)(m->heads + m->kv_heads), (uint32_t)m->head_dim,
-                                                  (uint32_t)m->rope_dim, m->neox ? 1 : 0);
+            rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, down.part, fp(L.attn_norm), m->h, d, m->eps, down.splits, td);
+        SplitOut qkv{m->qkv, 1}, att{m->o, 1}, gu{m->gu, 1};
+        if ((e = linear(m, s, L.wqkv, m->h, m->qkv, t, &qkv))) break;
+        qkv_rope_kernel<<<T, 256, width * 4, s>>>(qkv.part, qkv.splits, t * width, m->qkv, fp(L.bqkv), fp(m->rope_cos),
+                                                  fp(m->rope_sin), width, (uint32_t)(m->heads + m->kv_heads),
+                                                  (uint32_t)m->head_dim, (uint32_t)m->rope_dim, m->neox ? 1 : 0);
         if ((e = launch_attention(m, s, t))) break;
-        if ((e = linear(m, s, L.wo, m->att, m->o, t))) break;
-        rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, m->o, fp(L.ffn_norm), m->h, d, m->eps);
-        if ((e = linear(m, s, L.wgu, m->h, m->gu, t))) break;
+        if ((e = linear(m, s, L.wo, m->att, m->o, t, &att))) break;
+        rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, att.part, fp(L.ffn_norm), m->h, d, m->eps, att.splits, td);
+        if ((e = linear(m, s, L.wgu, m->h, m->gu, t, &gu))) break;
         const size_t quads = t * m->hidden / 4;
-        swiglu_kernel<<<(unsigned)std::min<size_t>((quads + 255) / 256, 65536), 256, 0, s>>>(m->gu, m->act, T,
-                                                                                           (uint32_t)m->hidden);
-        if ((e = linear(m, s, L.down, m->act, m->o, t))) break;
+        swiglu_kernel<<<(unsigned)std::min<size_t>((quads + 255) / 256, 65536), 256, 0, s>>>(
+            gu.part, gu.splits, t * 2 * m->hidden, m->act, T, (uint32_t)m->hidden);
+        if ((e = linear(m, s, L.down, m->act, m->o, t, &down))) break;
         e = hipGetLastError();
     }
     if (e) return e;
-    rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, m->o, fp(m->out_norm), m->h, d, m->eps);
+    rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, down.part, fp(m->out_norm), m->h, d, m->eps, down.splits, td);
     return hipGetLastError();
 }
 
