@@ -420,7 +420,10 @@ def f16_bound(x, wd, m, k, n):
 @pytest.mark.parametrize("kind_name,m,k,n", [
     ("Q4_0", 512, 896, 1152), ("Q4_0", 512, 896, 4864), ("Q4_0", 512, 4864, 896),
     ("Q8_0", 64, 2048, 5632), ("Q4_0", 8, 5632, 2048), ("Q8_0", 512, 5632, 256),
-    ("Q8_0", 2048, 896, 4864), ("Q4_0", 300, 2080, 200), ("Q4_0", 2048, 2080, 4096), ("Q8_0", 1030, 992, 8010)])
+    ("Q8_0", 2048, 896, 4864), ("Q4_0", 300, 2080, 200), ("Q4_0", 2048, 2080, 4096), ("Q8_0", 1030, 992, 8010),
+    # 256 x 256 tiles: CTAs that stream two tiles each, with a K split and an odd block count
+    # (2304 x 8192: 288 tiles, 4 splits) and without a split (4096 x 8192: 512 tiles)
+    ("Q4_0", 2304, 2080, 8192), ("Q8_0", 4096, 512, 8192)])
 def test_f16_gemm_meets_its_bounds_at_the_scoring_shapes(fh, g, orc, kind_name, m, k, n):
     kind = fh.QKind[kind_name]
     rng = np.random.default_rng(m + k + n)
