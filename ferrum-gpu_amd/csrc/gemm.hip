@@ -1140,10 +1140,11 @@ __global__ __launch_bounds__(512, 1) void gemm_f16_big_kernel(const _Float16 *__
     __shared__ float sxs[2][256];  // the row scales of the tiles in flight (by tile parity)
 
     // This CTA's tiles: XCD x (blockIdx.x % 8) owns the x-th equal run of a grouped tile order
-    // (xcd_tile's, with groups of eight row tiles) and its CTAs take the run's tiles round robin. A CTA works through its tiles' stages
-    // as one stream: the first stages of its next tile are loaded and stored while it computes
-    // the last ones of the current tile, and a tile's output stores drain during the next one.
-    constexpr uint32_t GM = 8;  // (measured: 4% faster than groups of 4 on the widest TinyLlama product)
+    // (xcd_tile's, with groups of eight row tiles) and its CTAs take the run's tiles round robin.
+    // A CTA works through its tiles' stages as one stream: the first stages of its next tile are
+    // loaded and stored while it computes the last ones of the current tile, and a tile's output
+    // stores drain during the next one.
+    constexpr uint32_t GM = 8;  // (measured: 4% faster than groups of four on the widest product)
     const uint32_t tiles = mt * nt, per_xcd = (tiles + 7) / 8, ctas = gridDim.x / 8;
     const uint32_t run0 = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8, run1 = min(tiles, (blockIdx.x % 8 + 1) * per_xcd);
     if (run0 >= run1) return;  // whole CTA: no barrier is left waiting
