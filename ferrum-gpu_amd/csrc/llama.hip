@@ -224,8 +224,10 @@ __global__ __launch_bounds__(64 * W) void attention_kernel(const float *__restri
     constexpr int DB = T::DB;
     __shared__ float red[W][2 + 16 * DB][64];
     const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6, col = lane & 31u, slot = lane >> 5;
-    const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * 32;  // the longest tiles start first
-    const uint32_t h = blockIdx.y, g = h / group, kv_heads = heads / group;
+    // grid (heads, query blocks): workgroups are dispatched x fastest, so every head's longest
+    // query blocks start first and the short ones fill in at the end
+    const uint32_t q0 = (gridDim.y - 1 - blockIdx.y) * 32;
+    const uint32_t h = blockIdx.x, g = h / group, kv_heads = heads / group;
     const uint32_t qd = heads * HD;
     const uint32_t kofs = qd + g * HD, vofs = qd + kv_heads * HD + g * HD;
     const uint32_t query = q0 + col;
@@ -455,8 +457,10 @@ __global__ __launch_bounds__(64 * W) void attention_split_kernel(
     constexpr int DB = T::DB, KS = T::KS;
     __shared__ float red[W][2 + 16 * DB][64];
     const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6, col = lane & 31u, hf = lane >> 5;
-    const uint32_t q0 = (gridDim.x - 1 - blockIdx.x) * 32;  // the longest tiles start first
-    const uint32_t h = blockIdx.y, g = h / group, kv_heads = heads / group;
+    // grid (heads, query blocks): workgroups are dispatched x fastest, so every head's longest
+    // query blocks start first and the short ones fill in at the end
+    const uint32_t q0 = (gridDim.y - 1 - blockIdx.y) * 32;
+    const uint32_t h = blockIdx.x, g = h / group, kv_heads = heads / group;
     const uint32_t qd = heads * HD, kvd = kv_heads * HD;
     const uint32_t query = q0 + col;
     f16x8 qfh[KS], qfl[KS];
@@ -843,7 +847,7 @@ hipError_t linear(const fh_llama *m, hipStream_t s, const fh_qweight *w, const f
 }
 
 hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t) {
-    const dim3 grid((unsigned)((t + 31) / 32), (unsigned)m->heads);
+    const dim3 grid((unsigned)m->heads, (unsigned)((t + 31) / 32));
     const uint32_t w = (uint32_t)m->qkv_width(), group = (uint32_t)(m->heads / m->kv_heads);
     const float scale = 1.0f / sqrtf((float)m->head_dim);
     const uint32_t T = (uint32_t)t, H = (uint32_t)m->heads;
