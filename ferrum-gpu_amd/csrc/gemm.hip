@@ -34,6 +34,7 @@
 
 #include "device_common.hpp"
 #include "internal.hpp"
+#include "xsplit.hpp"
 
 namespace fh {
 namespace {
@@ -111,84 +112,14 @@ __device__ __forceinline__ int elem_of_pos(int p) {
     }
 }
 
-// ---- x -> hi (f16, per block in operand order) and the fp8 correction ----
-// One workgroup per row m. hi = f16(x) (|x| beyond the f16 range saturates); lo = x - hi, kept as
-// e4m3 of lo * 2^s (natural k order, rows of K rounded up to 64 with a zero tail), where 2^s puts the row's largest lo (below 2^-11 of the
-// row's largest |x|) just under 2^8; xsc[m] holds the E8M0 byte of 2^-s (four copies) for the
-// scaled MFMA. Eight lanes per block, lane j taking elements 4j .. 4j + 3.
-__device__ __forceinline__ _Float16 f16_sat(float e) { return (_Float16)fminf(fmaxf(e, -65504.0f), 65504.0f); }
-
-__device__ __forceinline__ uint32_t fp8x4(float a, float b, float c, float d) {
-    // e4m3 has no infinity: values beyond +-448 would become NaN, so they are clamped first
-    const auto cl = [](float v) { return fminf(fmaxf(v, -448.0f), 448.0f); };
-    int w = __builtin_amdgcn_cvt_pk_fp8_f32(cl(a), cl(b), 0, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(cl(c), cl(d), w, true);
-    return (uint32_t)w;
-}
-
+// ---- x -> hi (f16, per block in operand order) and the fp8 correction (split_row_fast) ----
+// One workgroup per row m.
 template <int KIND>
 __global__ __launch_bounds__(256) void split_x_kernel(const float *__restrict__ x, _Float16 *__restrict__ xh,
                                                       uint8_t *__restrict__ xl, int32_t *__restrict__ xsc, uint32_t K) {
     __shared__ float red[4];
-    const uint32_t m = blockIdx.x, tid = threadIdx.x, nb = K / 32, K64 = (K + 63) / 64 * 64;
-    if (K64 != K && tid < 8) *(uint32_t *)(xl + (size_t)m * K64 + K + 4 * tid) = 0u;  // the row's zero tail
-    // The row is read once: thread t keeps float4 t + 256 i for i < kKeep in registers (rows up
-    // to 8192 wide; wider rows read the rest twice). Float4 q is elements 4 (q % 8) .. + 3 of
-    // block q / 8, so eight consecutive lanes hold one block.
-    constexpr int kKeep = 8;
-    const uint32_t nq = K / 4;
-    const f32x4 *xr = (const f32x4 *)(x + (size_t)m * K);
-    f32x4 v[kKeep];
-    float mx = 0.0f;
-    auto amax = [](f32x4 a) { return fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))); };
-#pragma unroll
-    for (int i = 0; i < kKeep; i++) {
-        const uint32_t q = tid + 256 * i;
-        v[i] = q < nq ? xr[q] : f32x4{0.f, 0.f, 0.f, 0.f};
-        mx = fmaxf(mx, amax(v[i]));
-    }
-    for (uint32_t q = tid + 256 * kKeep; q < nq; q += 256) mx = fmaxf(mx, amax(xr[q]));
-#pragma unroll
-    for (int o = 32; o >= 1; o /= 2) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    if (tid % 64 == 0) red[tid / 64] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    // 2^E <= mx < 2^(E+1); |lo| < 2^(E-10); s = 18 - E puts |lo| 2^s below 2^8
-    int sc = 0;
-    if (mx > 0.0f && mx <= 3.4028235e38f) sc = 18 - ((int)(__float_as_uint(mx) >> 23) - 127);
-    sc = sc < -126 ? -126 : (sc > 126 ? 126 : sc);
-    const float f = __uint_as_float((uint32_t)(127 + sc) << 23);
-    if (tid == 0) xsc[m] = (127 - sc) * 0x01010101;
-    const int j = tid % 8;
-    // (q < nq is the same for the eight lanes of a block: nq is a multiple of 8)
-    auto put = [&](uint32_t qi, f32x4 v) {
-        const uint32_t t = qi / 8;
-        _Float16 h[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) h[q] = f16_sat(v[q]);
-        *(uint32_t *)(xl + (size_t)m * K64 + t * 32 + 4 * j) =
-            fp8x4((v.x - (float)h[0]) * f, (v.y - (float)h[1]) * f, (v.z - (float)h[2]) * f, (v.w - (float)h[3]) * f);
-        _Float16 *out = xh + ((size_t)m * nb + t) * 32;
-        typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-        if constexpr (KIND == FH_Q8_0) {
-            // positions 4j..4j+3 hold elements 4j + {0, 2, 1, 3}
-            *(f16x4 *)(out + 4 * j) = f16x4{h[0], h[2], h[1], h[3]};
-        } else {
-            // positions 8i..8i+7 hold elements 4i + {0, 2, 1, 3} and 16 + 4i + {0, 2, 1, 3}: lane i < 4
-            // takes lane i + 4's four values and writes the eight
-            _Float16 o[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                o[q] = __builtin_bit_cast(_Float16, (uint16_t)__shfl_xor((int)__builtin_bit_cast(uint16_t, h[q]), 4, 8));
-            if (j < 4) *(f16x8 *)(out + 8 * j) = f16x8{h[0], h[2], h[1], h[3], o[0], o[2], o[1], o[3]};
-        }
-    };
-#pragma unroll
-    for (int i = 0; i < kKeep; i++) {
-        const uint32_t q = tid + 256 * i;
-        if (q < nq) put(q, v[i]);
-    }
-    for (uint32_t q = tid + 256 * kKeep; q < nq; q += 256) put(q, xr[q]);
+    const f32x4 *xr = (const f32x4 *)(x + (size_t)blockIdx.x * K);
+    split_row_fast<KIND>([&](uint32_t q) { return xr[q]; }, blockIdx.x, K, xh, xl, xsc, red);
 }
 
 // ---- the weights' fp8 correction operand: e4m3 of d * q * 2^t per element, natural k order, ----
@@ -1417,6 +1348,12 @@ hipError_t gemm_f16_dispatch(hipStream_t s, const GemmF16Args &g) {
 
 }  // namespace
 
+GemmXSplit gemm_x_split(void *workspace, size_t rows, size_t k) {
+    const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    uint8_t *ws = (uint8_t *)workspace;
+    return GemmXSplit{(_Float16 *)ws, ws + up(rows * k * 2), (int32_t *)(ws + up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)))};
+}
+
 // x hi (2 bytes per element), x lo (1 byte), one scale word per row, each piece 256-aligned
 size_t gemm_workspace_bytes(size_t rows, size_t k, size_t n) {
     const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
@@ -1506,10 +1443,13 @@ hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uin
     g.N = (uint32_t)n;
     g.defer = defer;
     if (kind == FH_Q8_0) {
-        split_x_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
+        if (x)
+            split_x_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc,
+                                                                   g.K);
         return gemm_dispatch<FH_Q8_0>(s, g);
     }
-    split_x_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
+    if (x)
+        split_x_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
     return gemm_dispatch<FH_Q4_0>(s, g);
 }
 

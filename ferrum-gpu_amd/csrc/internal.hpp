@@ -193,9 +193,19 @@ size_t gemm_b8_bytes(size_t k, size_t n);
 bool gemm_supported(size_t rows, size_t k, size_t n);
 hipError_t launch_make_b8(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, uint8_t *b8, size_t k,
                           size_t n);
+// x == nullptr: the workspace already holds x in the split form (gemm_x_split, written by
+// split_row_fast in xsplit.hpp).
 hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
                        const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace,
                        SplitOut *defer = nullptr);
+// Where the fast GEMM's split x lives in its workspace: hi (rows x k f16), lo (rows x k rounded
+// up to 64, e4m3), one scale word per row.
+struct GemmXSplit {
+    _Float16 *xh;
+    uint8_t *xl;
+    int32_t *xsc;
+};
+GemmXSplit gemm_x_split(void *workspace, size_t rows, size_t k);
 // The dequant-f16 MFMA GEMM (x as f16 with a power-of-two row scale, weights dequantised to f16
 // in LDS; split into workspace, then the product).
 size_t gemm_f16_workspace_bytes(size_t rows, size_t k, size_t n);

@@ -33,6 +33,7 @@
 
 #include "device_common.hpp"
 #include "internal.hpp"
+#include "xsplit.hpp"
 
 using namespace fh;
 
@@ -139,6 +140,51 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *__restrict__ x, con
     const float ms = block_sum_256(ss, red) / (float)d;
     const float inv = 1.0f / sqrtf(ms + eps);
     for (uint32_t i = threadIdx.x; i < d; i += 256) h[base + i] = __fmul_rn(__fmul_rn(x[base + i], inv), g[i]);
+}
+
+// The fast path's fused producers: rmsnorm_kernel and swiglu_kernel with the same arithmetic, the
+// row kept in LDS and written straight into the fast GEMM's split x (split_row_fast), so the
+// f32 activation is never written to memory and read back by a split pass. One workgroup per row.
+template <bool ADD, int KIND>
+__global__ __launch_bounds__(256) void rmsnorm_split_kernel(float *__restrict__ x, const float *__restrict__ o,
+                                                            const float *__restrict__ g, uint32_t d, float eps,
+                                                            uint32_t o_splits, size_t o_stride, GemmXSplit dst) {
+    extern __shared__ __attribute__((aligned(16))) float hrow[];
+    __shared__ float red[4], red2[4];
+    const size_t base = (size_t)blockIdx.x * d;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < d; i += 256) {
+        float v = x[base + i];
+        if constexpr (ADD) {
+            v = v + split_sum(o, base + i, o_splits, o_stride);
+            x[base + i] = v;
+        }
+        ss += v * v;
+    }
+    const float ms = block_sum_256(ss, red) / (float)d;
+    const float inv = 1.0f / sqrtf(ms + eps);
+    for (uint32_t i = threadIdx.x; i < d; i += 256) hrow[i] = __fmul_rn(__fmul_rn(x[base + i], inv), g[i]);
+    __syncthreads();
+    split_row_fast<KIND>([&](uint32_t q) { return *(const f32x4 *)&hrow[4 * q]; }, blockIdx.x, d, dst.xh, dst.xl,
+                         dst.xsc, red2);
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void swiglu_split_kernel(const float *__restrict__ gu, uint32_t hid, GemmXSplit dst) {
+    extern __shared__ __attribute__((aligned(16))) float hrow[];
+    __shared__ float red[4];
+    const size_t r = blockIdx.x;
+    for (uint32_t j = threadIdx.x; j < hid / 4; j += 256) {
+        const f32x4 gg = *(const f32x4 *)(gu + r * 2 * hid + 4 * j);
+        const f32x4 u = *(const f32x4 *)(gu + r * 2 * hid + hid + 4 * j);
+        f32x4 y;
+#pragma unroll
+        for (int c = 0; c < 4; c++) y[c] = __fmul_rn(gg[c] / (1.0f + expf(-gg[c])), u[c]);
+        *(f32x4 *)&hrow[4 * j] = y;
+    }
+    __syncthreads();
+    split_row_fast<KIND>([&](uint32_t q) { return *(const f32x4 *)&hrow[4 * q]; }, (uint32_t)r, hid, dst.xh, dst.xl,
+                         dst.xsc, red);
 }
 
 // q/k/v bias and RoPE in place on one row of qkv (ferrum_ref/src/models/llama/ops.rs:105-127):
@@ -886,26 +932,55 @@ hipError_t enqueue_body(fh_llama *m, hipStream_t s, size_t t) {
     hipError_t e = hipGetLastError();
     const uint32_t width = (uint32_t)m->qkv_width();
     const size_t td = t * m->dim;
+    // The fast path's RMSNorms and SwiGLU write the next product's split x themselves (the
+    // product then skips its split pass); rows up to 16384 wide, held in LDS.
+    const bool fused = m->path == FH_PATH_TILED_FAST && m->dim <= 16384 && m->hidden <= 16384;
+    const GemmXSplit xd = gemm_x_split(m->ws, t, m->dim), xh = gemm_x_split(m->ws, t, m->hidden);
+    auto norm = [&](bool add, const fh_buffer *g, const SplitOut &o) {
+        if (fused && m->kind == FH_Q8_0) {
+            if (add)
+                rmsnorm_split_kernel<true, FH_Q8_0><<<T, 256, d * 4, s>>>(m->x, o.part, fp(g), d, m->eps, o.splits, td, xd);
+            else
+                rmsnorm_split_kernel<false, FH_Q8_0><<<T, 256, d * 4, s>>>(m->x, nullptr, fp(g), d, m->eps, 1, 0, xd);
+        } else if (fused) {
+            if (add)
+                rmsnorm_split_kernel<true, FH_Q4_0><<<T, 256, d * 4, s>>>(m->x, o.part, fp(g), d, m->eps, o.splits, td, xd);
+            else
+                rmsnorm_split_kernel<false, FH_Q4_0><<<T, 256, d * 4, s>>>(m->x, nullptr, fp(g), d, m->eps, 1, 0, xd);
+        } else if (add) {
+            rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, o.part, fp(g), m->h, d, m->eps, o.splits, td);
+        } else {
+            rmsnorm_kernel<false><<<T, 256, 0, s>>>(m->x, nullptr, fp(g), m->h, d, m->eps, 1, 0);
+        }
+    };
+    const float *hx = fused ? nullptr : m->h;  // the input the next products read
     SplitOut down{m->o, 1};  // the previous block's FFN output, added to x by the next RMSNorm
     for (size_t l = 0; l < m->layers && !e; l++) {
         const auto &L = m->blocks[l];
-        if (l == 0)
-            rmsnorm_kernel<false><<<T, 256, 0, s>>>(m->x, nullptr, fp(L.attn_norm), m->h, d, m->eps, 1, 0);
-        else
-            rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, down.part, fp(L.attn_norm), m->h, d, m->eps, down.splits, td);
+        norm(l > 0, L.attn_norm, down);
         SplitOut qkv{m->qkv, 1}, att{m->o, 1}, gu{m->gu, 1};
-        if ((e = linear(m, s, L.wqkv, m->h, m->qkv, t, &qkv))) break;
+        if ((e = linear(m, s, L.wqkv, hx, m->qkv, t, &qkv))) break;
         qkv_rope_kernel<<<T, 256, width * 4, s>>>(qkv.part, qkv.splits, t * width, m->qkv, fp(L.bqkv), fp(m->rope_cos),
                                                   fp(m->rope_sin), width, (uint32_t)(m->heads + m->kv_heads),
                                                   (uint32_t)m->head_dim, (uint32_t)m->rope_dim, m->neox ? 1 : 0);
         if ((e = launch_attention(m, s, t))) break;
         if ((e = linear(m, s, L.wo, m->att, m->o, t, &att))) break;
-        rmsnorm_kernel<true><<<T, 256, 0, s>>>(m->x, att.part, fp(L.ffn_norm), m->h, d, m->eps, att.splits, td);
-        if ((e = linear(m, s, L.wgu, m->h, m->gu, t, &gu))) break;
-        const size_t quads = t * m->hidden / 4;
-        swiglu_kernel<<<(unsigned)std::min<size_t>((quads + 255) / 256, 65536), 256, 0, s>>>(
-            gu.part, gu.splits, t * 2 * m->hidden, m->act, T, (uint32_t)m->hidden);
-        if ((e = linear(m, s, L.down, m->act, m->o, t, &down))) break;
+        norm(true, L.ffn_norm, att);
+        if (fused) {
+            // (gate/up reduced in place: SwiGLU's split x would overwrite its partial sums)
+            if ((e = linear(m, s, L.wgu, nullptr, m->gu, t))) break;
+            if (m->kind == FH_Q8_0)
+                swiglu_split_kernel<FH_Q8_0><<<T, 256, m->hidden * 4, s>>>(m->gu, (uint32_t)m->hidden, xh);
+            else
+                swiglu_split_kernel<FH_Q4_0><<<T, 256, m->hidden * 4, s>>>(m->gu, (uint32_t)m->hidden, xh);
+            if ((e = linear(m, s, L.down, nullptr, m->o, t, &down))) break;
+        } else {
+            if ((e = linear(m, s, L.wgu, m->h, m->gu, t, &gu))) break;
+            const size_t quads = t * m->hidden / 4;
+            swiglu_kernel<<<(unsigned)std::min<size_t>((quads + 255) / 256, 65536), 256, 0, s>>>(
+                gu.part, gu.splits, t * 2 * m->hidden, m->act, T, (uint32_t)m->hidden);
+            if ((e = linear(m, s, L.down, m->act, m->o, t, &down))) break;
+        }
         e = hipGetLastError();
     }
     if (e) return e;
