@@ -177,17 +177,21 @@ def bench_gemv_pool(fh, g, ev, kind, groups, pool_bytes, steps, warmup, seed=0):
             "gbs": step_bytes / (step_ms * 1e-3) / 1e9, "launches": launches}
 
 
-def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0, path=None):
+def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0, path=None, copies=1):
+    """One step = every product of `shapes` (times `copies` distinct weight copies, to exceed the
+    last-level cache for the HBM-bound small-M rates). Returns flops and algorithmic bytes per step."""
     path = fh.QPath.Tiled if path is None else path
     rng = np.random.default_rng(seed)
     items = []
     for k, n in shapes:
         w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
-        qw = fh.upload_quantised(g, kind, w, k, n)
-        gx = g.upload(rng.standard_normal(m * k).astype(np.float32))
-        gy = g.zeros(m * n)
-        items.append((qw, gx, gy))
-    flops = sum(2 * m * k * n for k, n in shapes)
+        for _ in range(copies):
+            qw = fh.upload_quantised(g, kind, w, k, n)
+            gx = g.upload(rng.standard_normal(m * k).astype(np.float32))
+            gy = g.zeros(m * n)
+            items.append((qw, gx, gy))
+    flops = copies * sum(2 * m * k * n for k, n in shapes)
+    nbytes = copies * sum((k // 32) * n * kind.file_bytes() + 4 * m * k + 4 * m * n for k, n in shapes)
     for qw, gx, gy in items:
         fh.linear_q_with(g, gx, qw, gy, m, path)
     g.sync()
@@ -200,7 +204,8 @@ def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0, path=None):
     g.sync()
     ms = ev.ms(e0, e1) / steps
     ev.destroy([e0, e1])
-    return {"m": m, "flops_per_step": flops, "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12}
+    return {"m": m, "flops_per_step": flops, "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+            "bytes_per_step": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9}
 
 
 def bench_copy(g, ev, nbytes=512 * 2**20, reps=10):
@@ -442,6 +447,15 @@ def main():
                                                   "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                                                   "ms_per_step": r["ms_per_step"],
                                                   "flops_per_step": r["flops_per_step"]}
+        # config 5's small M (HBM-bound): the library's own path choice, 12 distinct copies of the
+        # four products (about 300 MB of Q4_0 weights, more than the 256 MB last-level cache)
+        for kind, tag in ((fh.QKind.Q4_0, "q4_0"), (fh.QKind.Q8_0, "q8_0")):
+            for m in (8, 64):
+                r = bench_gemm(fh, g, ev, kind, m, LLAMA1B_SHAPES, 10, path=fh.QPath.Auto, copies=12)
+                log(f"{tag} small-M products M={m}:", r)
+                extra[f"{tag}_gemm_llama1b_m{m}"] = {"gbs": round(r["gbs"], 2), "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                                                     "tflops": round(r["tflops"], 2), "ms_per_step": r["ms_per_step"],
+                                                     "bytes_per_step": r["bytes_per_step"], "path": "auto"}
         sc = bench_scoring(fh, g, ev, cpu=not a.no_cpu)
         log("Qwen2-0.5B Q4_0 scoring:", sc)
         extra["qwen2_0_5b_q4_0_scoring"] = sc
