@@ -423,7 +423,9 @@ def f16_bound(x, wd, m, k, n):
     ("Q8_0", 2048, 896, 4864), ("Q4_0", 300, 2080, 200), ("Q4_0", 2048, 2080, 4096), ("Q8_0", 1030, 992, 8010),
     # 256 x 256 tiles: CTAs that stream two tiles each, with a K split and an odd block count
     # (2304 x 8192: 288 tiles, 4 splits) and without a split (4096 x 8192: 512 tiles)
-    ("Q4_0", 2304, 2080, 8192), ("Q8_0", 4096, 512, 8192)])
+    ("Q4_0", 2304, 2080, 8192), ("Q8_0", 4096, 512, 8192),
+    # ragged rows and columns, an odd block count, two tiles for some CTAs, no K split
+    ("Q4_0", 2100, 544, 8200)])
 def test_f16_gemm_meets_its_bounds_at_the_scoring_shapes(fh, g, orc, kind_name, m, k, n):
     kind = fh.QKind[kind_name]
     rng = np.random.default_rng(m + k + n)
