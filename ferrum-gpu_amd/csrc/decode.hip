@@ -40,7 +40,7 @@ enum { PRO_NONE = 0, PRO_LN = 1, PRO_GLOBAL = 2 };
 enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_GELU = 2, EPI_QKV = 3, EPI_ARGMAX = 4 };
 
 constexpr int kMaxWaves = 8;           // wavefronts per decode-GEMV workgroup (two per SIMD)
-constexpr uint32_t kMaxBlocks = 512;   // blocks per row (k <= 16384): 64 KiB of prepared x in LDS
+constexpr uint32_t kMaxBlocks = 512;   // blocks per row (k <= 16384): 80 KiB of prepared x in LDS
 constexpr uint32_t kLnSlots = 2;       // LayerNorm prologue: (block, lane) slots a thread keeps in registers
 constexpr uint32_t kNone = 0xffffffffu;
 constexpr int kAttnThreads = 512;
@@ -148,9 +148,9 @@ __device__ __forceinline__ void ln_prep(const float *x, const float *lg, const f
                 prep_values<KIND>(h, j, (__attribute__((address_space(3))) uint32_t *)rec);
         } else {
             if constexpr (GLOBAL)
-                *(__attribute__((address_space(1))) u32x4 *)(rec + 16 * j) = u32x4{0u, 0u, 0u, 0u};
+                zero_record(j, (__attribute__((address_space(1))) uint32_t *)rec);
             else
-                *(__attribute__((address_space(3))) u32x4 *)(rec + 16 * j) = u32x4{0u, 0u, 0u, 0u};
+                zero_record(j, (__attribute__((address_space(3))) uint32_t *)rec);
         }
     }
 }
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
     const auto rd = make_rsrc(a.ds + (size_t)g * nb8 * 256, nb8 * 512);
     const auto ra = make_rsrc(a.prep, PRO == PRO_GLOBAL ? span * kPrepBytes : 0);
     const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16);
-    const uint32_t os = (uint32_t)(r * 16), oa = (uint32_t)(r * 32 + 16 * upper);
+    const uint32_t os = (uint32_t)(r * 16), oa = prep_a_offset(lane), ot = prep_tail_offset(lane);
     uint8_t *prep = dlds;  // records of blocks b0 .. b1 (PRO_LN: of every block)
     float *part = (float *)(dlds + (PRO == PRO_GLOBAL ? 0 : (PRO == PRO_LN ? span : a.chunk) * kPrepBytes));
     float *red = part + W * 32;
@@ -212,8 +212,10 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
     uint32_t bb = b0 + wave * kBatch;
     if (bb < b1) {
         load_weights<KIND>(cur, rq, rd, oq, os, bb);
-        if constexpr (PRO == PRO_GLOBAL)
+        if constexpr (PRO == PRO_GLOBAL) {
             cur.a = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(bb * kPrepBytes + oa), 0, 0));
+            cur.t = __builtin_amdgcn_raw_buffer_load_b32(ra, (int)(bb * kPrepBytes + ot), 0, 0);
+        }
     }
     if constexpr (PRO == PRO_LN) {
         ln_prep<KIND, false>(a.x, a.ln_g, a.ln_b, a.eps, nb, span, prep, red);
@@ -227,7 +229,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
             if (blk < nb)
                 prep_values<KIND>(gload4(a.x + blk * 32 + 4 * j), j, rec);
             else
-                *(__attribute__((address_space(3))) u32x4 *)(rec + 4 * j) = u32x4{0u, 0u, 0u, 0u};
+                zero_record(j, rec);
         }
         __syncthreads();
     }
@@ -237,11 +239,15 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
         const uint32_t nxt = bb + W * kBatch;
         if (nxt < b1) {
             load_weights<KIND>(nx, rq, rd, oq, os, nxt);
-            if constexpr (PRO == PRO_GLOBAL)
+            if constexpr (PRO == PRO_GLOBAL) {
                 nx.a = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(nxt * kPrepBytes + oa), 0, 0));
+                nx.t = __builtin_amdgcn_raw_buffer_load_b32(ra, (int)(nxt * kPrepBytes + ot), 0, 0);
+            }
         }
-        if constexpr (PRO != PRO_GLOBAL)
+        if constexpr (PRO != PRO_GLOBAL) {
             cur.a = *(const __attribute__((address_space(3))) i32x4 *)(prep + (bb - pbase) * kPrepBytes + oa);
+            cur.t = *(const __attribute__((address_space(3))) uint32_t *)(prep + (bb - pbase) * kPrepBytes + ot);
+        }
         compute_batch<KIND>(cur, upper, acc);
         cur = nx;
         bb = nxt;
@@ -757,7 +763,7 @@ fh_status fh_gpt2_from_gguf(fh_device *dev, const fh_gguf *g, fh_gpt2 **out) {
     const size_t max_groups = groups_d;
     m->n_tickets = max_groups + 1;
     const size_t total = 2 * m->layers * cache + 3 * up(d * 4) + up(h * 4) + up(m->vocab * 4) + up(16) +
-                         up((m->ctx + 1) * 4) + up(d / 32 * 8 * 128 + 1024) + up(part_floats * 4) +
+                         up((m->ctx + 1) * 4) + up((d / 32 + 7) / 8 * 8 * kPrepBytes) + up(part_floats * 4) +
                          up(groups_v * 4) + up(m->n_tickets * 4);
     if ((st = alloc_bytes(dev, total, &m->arena))) return gpt2_fail_free(m, st);
     uint8_t *p = (uint8_t *)m->arena;
@@ -782,7 +788,7 @@ fh_status fh_gpt2_from_gguf(fh_device *dev, const fh_gguf *g, fh_gpt2 **out) {
     m->inputs = (int32_t *)p;
     p += up((m->ctx + 1) * 4);
     m->prep = p;
-    p += up(d / 32 * 8 * 128 + 1024);
+    p += up((d / 32 + 7) / 8 * 8 * kPrepBytes);
     m->partial = (float *)p;
     p += up(part_floats * 4);
     m->pick = (uint32_t *)p;

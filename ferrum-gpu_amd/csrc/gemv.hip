@@ -6,12 +6,13 @@
 // The dot products run on the matrix cores as exact integer arithmetic.
 //
 // x side (gemv_prep_kernel, once per product): each 32-element block of x is put on the
-// fixed-point grid of its largest magnitude: with 2^(E-1) <= amax < 2^E, xi = rint(x * 2^(22-E))
-// (|xi| <= 2^22, error <= 2^-22 amax per element: the grid an f32 sum of the block rounds to) and
-// xi = a * 2^16 + b * 2^8 + c with a, b, c signed bytes. A 128-byte record per block holds the
-// three limb rows in the MFMA's k order (32 bytes each), then the scale 2^(E-22) and, for Q4_0,
-// the integer bias -8 * sum(xi) that turns the stored nibbles (0..15) into q = nibble - 8. A
-// block holding a non-finite x contributes NaN.
+// fixed-point grid of its largest magnitude: with 2^(E-1) <= amax < 2^E, xi = rint(x * 2^(30-E))
+// (|xi| <= 2^30, error <= 2^-30 amax per element, so an element far below its block's largest
+// still keeps more bits than its own f32 rounding when it is above 2^-7 amax) and
+// xi = a 2^24 + b 2^16 + c 2^8 + e with a, b, c, e signed bytes. A 160-byte record per block holds
+// the four limb rows in the MFMA's k order (32 bytes each), then the scale 2^(E-30) and, for
+// Q4_0, the biases that turn the stored nibbles (0..15) into q = nibble - 8. A block holding a
+// non-finite x contributes NaN.
 //
 // Weight side: the tiled planes (tile_slot, scale_slot). For 32 rows and one block the 32 quant
 // slots are contiguous, so a wavefront reads one Q8_0 block or two Q4_0 blocks of 32 rows with one
@@ -21,11 +22,11 @@
 // The dot products are exact integer arithmetic on the matrix cores: per block, one
 // v_mfma_i32_32x32x32_i8 with B = the block's quants (Q8_0 bytes as they are; Q4_0 nibbles
 // masked into bytes, after a lane-half swap that gives each lane half h of two blocks) and A =
-// the prepared x of eight blocks at once, block j's limb rows in A rows 4j .. 4j + 2. C rows
-// 4j .. 4j + 2 are then block j's three limb sums for each of the 32 rows, exact in int32, and
+// the prepared x of eight blocks at once, block j's limb rows in A rows 4j .. 4j + 3. C rows
+// 4j .. 4j + 3 are then block j's four limb sums for each of the 32 rows, exact in int32, and
 // they lie in lanes 0..31 for even j and lanes 32..63 for odd j, so each lane half finishes its
-// own blocks: Q4_0 combines the sums exactly in int32, Q8_0 in f32, and the lane adds
-// d * 2^(E-22) * S to its f32 accumulator. One cross-half add per row ends the task.
+// own blocks: the sums combine in int32 into two halves (exact) and those into one f32, and the
+// lane adds d * 2^(E-30) * S to its f32 accumulator. One cross-half add per row ends the task.
 //
 // Work: a task is one group of 32 rows of one product; each wavefront takes a contiguous range
 // of tasks (one launch can hold many products: descriptors in device memory, and a map from
@@ -109,7 +110,7 @@ struct Pos {
 // Per-lane byte offsets inside a batch (the batch offset is added in the offset register, which
 // the range check covers: batches past the task's last block read 0).
 struct LaneOffsets {
-    uint32_t q, s, a;
+    uint32_t q, s, a, t;
 };
 
 // Prepared x in LDS: one region per wavefront (kernel argument lds_blocks records, a multiple
@@ -131,10 +132,13 @@ __device__ __forceinline__ void load_batch(Batch<KIND> &bt, const Task<KIND> &tk
                 u32x4, __builtin_amdgcn_raw_buffer_load_b128(tk.rq, (int)(o.q + (b + 2 * i) * 512), 0, kNonTemporal));
     }
     bt.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(tk.rd, (int)(o.s + b * 64), 0, 0));
-    if constexpr (LDSX)
+    if constexpr (LDSX) {
         bt.a = *(const i32x4 *)&gemv_lds[lds_base + b * kPrepBytes + o.a];
-    else
+        bt.t = *(const uint32_t *)&gemv_lds[lds_base + b * kPrepBytes + o.t];
+    } else {
         bt.a = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(tk.ra, (int)(o.a + b * kPrepBytes), 0, 0));
+        bt.t = __builtin_amdgcn_raw_buffer_load_b32(tk.ra, (int)(o.t + b * kPrepBytes), 0, 0);
+    }
 }
 
 template <int KIND, bool LDSX>
@@ -150,9 +154,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ 
     const int r = lane % 32;
     const bool upper = lane >= 32;
     // Q4_0: block pair chunk of 1 KiB, lane l at 16 l; Q8_0: block tile of 1 KiB, row r at 32 r;
-    // scales: row r's eight at 16 r; prepared x: A row r (block r / 4) at 32 r, k half at + 16
+    // scales: row r's eight at 16 r; prepared x: prep_a_offset, prep_tail_offset
     const LaneOffsets o{KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16), (uint32_t)(r * 16),
-                        (uint32_t)(r * 32 + 16 * upper)};
+                        prep_a_offset(lane), prep_tail_offset(lane)};
     // The wavefront's tasks are one stream of batches: the loads of the next batch (of this task
     // or the next) are in flight while a batch is computed, so the pipeline never drains at a
     // task boundary. lp is the batch being loaded, cp the batch being computed.
@@ -172,8 +176,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ 
                 if (b < d.nb) {
                     prep_block<KIND>(d.x, aligned, b, lane % 8, rec);
                 } else {
-                    // padding records: four zero dwords per lane
-                    *(__attribute__((address_space(3))) u32x4 *)(rec + 4 * (lane % 8)) = u32x4{0u, 0u, 0u, 0u};
+                    zero_record(lane % 8, rec);  // padding records
                 }
             }
         }
@@ -257,7 +260,7 @@ uint32_t waves_per_cu() {
     return w;
 }
 
-constexpr uint32_t kMaxLdsBlocks = 160;  // per wavefront: 20 KiB of prepared x, 80 KiB per workgroup
+constexpr uint32_t kMaxLdsBlocks = 128;  // per wavefront: 20 KiB of prepared x, 80 KiB per workgroup
 constexpr uint32_t kMinLdsTasks = 8;     // tasks per wavefront below which x is prepared once, globally
 
 // Resident workgroups per CU for a kernel and its dynamic LDS (cached per LDS size).

@@ -1,7 +1,7 @@
 // Device pieces shared by the batch-1 GEMV kernels (gemv.hip, decode.hip): the prepared-x
-// record of a block (three signed-byte limb rows in the MFMA's k order, the block's x scale and
-// the Q4_0 bias) and the exact integer block products on the matrix cores. Included by .hip files
-// only; everything is internal to the including file.
+// record of a block (four signed-byte limb rows in the MFMA's k order, then the block's x scale
+// and the Q4_0 biases) and the exact integer block products on the matrix cores. Included by .hip
+// files only; everything is internal to the including file.
 #pragma once
 
 #include "device_common.hpp"
@@ -24,7 +24,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
 }
 constexpr int kNonTemporal = 2;             // cache-policy bit of a streaming load
-constexpr int kPrepBytes = 128;             // prepared-x record per block
+// Prepared-x record of a block (160 bytes): dwords 0..31 are the four limb rows (32 bytes each,
+// most significant first), dword 32 the x scale, 33 and 34 the Q4_0 biases, 35..39 zero.
+constexpr int kPrepBytes = 160;
 constexpr int kBatch = 8;                   // blocks per pipeline batch
 
 // k slot of the MFMA operands -> element of the block. Lane half h (lanes 32h..32h+31) holds
@@ -57,9 +59,16 @@ static_assert(prep_dwords_match_slots<FH_Q8_0>() && prep_dwords_match_slots<FH_Q
               "prepared-x dwords must hold the MFMA k slots");
 
 // ---- x preparation: eight lanes per block, lane j taking elements 4j .. 4j + 3 ----
-// Writes the 128-byte record of the block whose elements 4j .. 4j + 3 are v at rec (a global or
-// an LDS pointer). The eight lanes of a block must run this together (they reduce over one
-// another with shuffles).
+// Each block of x is put on the fixed-point grid of its largest magnitude: with
+// 2^(E-1) <= amax < 2^E, xi = rint(x * 2^(30-E)) (|xi| <= 2^30, error <= 2^-30 amax per element,
+// finer than the f32 rounding of any element above 2^-7 amax) and xi = a 2^24 + b 2^16 + c 2^8 + e
+// with a, b, c, e signed bytes (|a| <= 64). The record's scale is 2^(E-30) (the grid is capped at
+// 2^-149, where it holds every float exactly). For Q4_0 the stored nibbles (0..15) stand for
+// q = nibble - 8, so the record carries the biases -8 sum(a 2^8 + b) and -8 sum(c 2^8 + e) that
+// the two halves of the limb sums take (both exact in int32).
+// Writes the record of the block whose elements 4j .. 4j + 3 are v at rec (a global or an LDS
+// pointer). The eight lanes of a block must run this together (they reduce over one another
+// with shuffles).
 template <int KIND, class U32Ptr>
 __device__ __forceinline__ void prep_values(f32x4 v, int j, U32Ptr rec) {
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
@@ -70,44 +79,73 @@ __device__ __forceinline__ void prep_values(f32x4 v, int j, U32Ptr rec) {
         amax = fmaxf(amax, __shfl_xor(amax, m, 8));
         finite &= __shfl_xor(finite, m, 8);
     }
-    // grid 2^-sh with 2^21 <= amax * 2^sh < 2^22 (subnormal amax: exponent field 1); the
-    // scaling is split in two exact power-of-two products so that no factor overflows
-    const int sh = 148 - (int)max(__float_as_uint(amax) >> 23, 1u);  // -106 .. 147
+    // grid 2^-sh with 2^29 <= amax * 2^sh < 2^30, at most 2^149 (subnormal amax: exponent field
+    // 1); the scaling is split in two exact power-of-two products so that no factor overflows
+    const int sh = min(156 - (int)max(__float_as_uint(amax) >> 23, 1u), 149);  // -98 .. 149
     const int sh1 = min(sh, 100);
     const float m1 = __uint_as_float((uint32_t)(127 + sh1) << 23);
     const float m2 = __uint_as_float((uint32_t)(127 + sh - sh1) << 23);
     const float xs = !finite ? __builtin_nanf("")
                      : sh <= 126 ? __uint_as_float((uint32_t)(127 - sh) << 23)  // 2^-sh, normal
                                  : __uint_as_float(1u << (149 - sh));            // 2^-sh, subnormal
-    uint32_t la = 0, lb = 0, lc = 0;
-    int32_t sum = 0;
+    uint32_t la = 0, lb = 0, lc = 0, le = 0;
+    int32_t shi = 0, slo = 0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        // |xi| <= 2^22; non-finite blocks take 0 here and NaN through xs
+        // |xi| <= 2^30; non-finite blocks take 0 here and NaN through xs
         const float sx = finite ? (v[k] * m1) * m2 : 0.0f;
         const int32_t xi = (int32_t)rintf(sx);
-        const int32_t c = (xi << 24) >> 24;
-        const int32_t r = (xi - c) >> 8;
-        const int32_t bb = (r << 24) >> 24;
-        const int32_t a = (r - bb) >> 8;
+        const int32_t e = (xi << 24) >> 24;
+        int32_t r = (xi - e) >> 8;
+        const int32_t c = (r << 24) >> 24;
+        r = (r - c) >> 8;
+        const int32_t b = (r << 24) >> 24;
+        const int32_t a = (r - b) >> 8;
         la |= (uint32_t)(a & 0xff) << (8 * k);
-        lb |= (uint32_t)(bb & 0xff) << (8 * k);
+        lb |= (uint32_t)(b & 0xff) << (8 * k);
         lc |= (uint32_t)(c & 0xff) << (8 * k);
-        sum += xi;
+        le |= (uint32_t)(e & 0xff) << (8 * k);
+        shi += a * 256 + b;
+        slo += c * 256 + e;
     }
+    if constexpr (KIND == FH_Q4_0) {
 #pragma unroll
-    for (int m = 1; m < 8; m *= 2) sum += __shfl_xor(sum, m, 8);
+        for (int m = 1; m < 8; m *= 2) {
+            shi += __shfl_xor(shi, m, 8);
+            slo += __shfl_xor(slo, m, 8);
+        }
+    }
     const int dw = prep_dword<KIND>(j);
     rec[dw] = la;
     rec[8 + dw] = lb;
     rec[16 + dw] = lc;
+    rec[24 + dw] = le;
     if (j == 0) {
-        const int32_t bias = KIND == FH_Q4_0 ? -8 * sum : 0;
-        rec[24] = __float_as_uint(xs);
-        rec[25] = (uint32_t)bias;
-    } else if (j < 7) {
-        rec[24 + j + 1] = 0u;  // bytes 104 .. 127 are zero
+        rec[32] = __float_as_uint(xs);
+        rec[33] = KIND == FH_Q4_0 ? (uint32_t)(-8 * shi) : 0u;
+        rec[34] = KIND == FH_Q4_0 ? (uint32_t)(-8 * slo) : 0u;
+    } else if (j < 6) {
+        rec[34 + j] = 0u;  // dwords 35 .. 39 are zero
     }
+}
+
+// A zero record (a padding block: contributes 0), written by its eight lanes.
+template <class U32Ptr>
+__device__ __forceinline__ void zero_record(int j, U32Ptr rec) {
+#pragma unroll
+    for (int i = 0; i < kPrepBytes / 32; i++) rec[j * (kPrepBytes / 32) + i] = 0u;
+}
+
+// Per-lane byte offsets into the records of an 8-block batch: the MFMA's A operand (lane l
+// holds A row l % 32, i.e. limb (l % 4) of block (l % 32) / 4, k half l / 32) and the record
+// tail (lanes 4j .. 4j + 3 and 32 + 4j .. 32 + 4j + 3 take dwords 32 .. 35 of block j).
+__device__ __forceinline__ uint32_t prep_a_offset(int lane) {
+    const int r = lane % 32;
+    return (uint32_t)((r / 4) * kPrepBytes + (r % 4) * 32 + 16 * (lane / 32));
+}
+__device__ __forceinline__ uint32_t prep_tail_offset(int lane) {
+    const int r = lane % 32;
+    return (uint32_t)((r / 4) * kPrepBytes + 128 + 4 * (r % 4));
 }
 
 // The same for block b of x in global memory.
@@ -133,6 +171,7 @@ struct Batch {  // what one lane loads for a batch of kBatch blocks of its task
                   // Q8_0: bytes 16h .. 16h + 15 of block i of the row (h = lane / 32)
     u32x4 s;      // the row's eight scales
     i32x4 a;      // the prepared x of the eight blocks, as the MFMA's A operand
+    uint32_t t;   // a record-tail dword of the eight blocks (prep_tail_offset)
 };
 
 __device__ __forceinline__ i32x4 nibbles(uint32_t q0, uint32_t q1) {
@@ -159,27 +198,25 @@ __device__ __forceinline__ void compute_batch(const Batch<KIND> &bt, bool upper,
             be = nibbles(s0[0], s1[0]);
             bo = nibbles(s0[1], s1[1]);
         }
-        // A rows 4j .. 4j + 2 hold block j's limb rows (row 4j + 3 its x scale and bias), so
-        // C rows 4j .. 4j + 2 are block j's limb sums: for j = 2p in registers 4p .. 4p + 2 of
-        // lanes 0..31, for j = 2p + 1 in the same registers of lanes 32..63. The other rows
-        // mix blocks and are not used.
+        // A rows 4j .. 4j + 3 hold block j's limb rows, so C rows 4j .. 4j + 3 are block j's
+        // limb sums: for j = 2p in registers 4p .. 4p + 3 of lanes 0..31, for j = 2p + 1 in the
+        // same registers of lanes 32..63. The other rows mix blocks and are not used.
         const i32x16 ce = __builtin_amdgcn_mfma_i32_32x32x32_i8(bt.a, be, i32x16{}, 0, 0, 0);
         const i32x16 co = __builtin_amdgcn_mfma_i32_32x32x32_i8(bt.a, bo, i32x16{}, 0, 0, 0);
         const int32_t c0 = upper ? co[4 * p] : ce[4 * p];
         const int32_t c1 = upper ? co[4 * p + 1] : ce[4 * p + 1];
         const int32_t c2 = upper ? co[4 * p + 2] : ce[4 * p + 2];
-        // the block's x scale and bias: A row 4j + 3 is lane 4j + 3
-        const float xe = __int_as_float(__builtin_amdgcn_readlane(bt.a[0], 8 * p + 3));
-        const float xo = __int_as_float(__builtin_amdgcn_readlane(bt.a[0], 8 * p + 7));
-        float f;
-        if constexpr (KIND == FH_Q8_0) {
-            f = fmaf((float)c0, 65536.0f, (float)((c1 << 8) + c2));  // |sum| < 2^34: two roundings
-        } else {
-            // exact: |sum nibble * xi| < 2^31 and |sum (nibble - 8) * xi| <= 2^30
-            const int32_t ie = __builtin_amdgcn_readlane(bt.a[1], 8 * p + 3);
-            const int32_t io = __builtin_amdgcn_readlane(bt.a[1], 8 * p + 7);
-            f = (float)((c0 << 16) + (c1 << 8) + c2 + (upper ? io : ie));
+        const int32_t c3 = upper ? co[4 * p + 3] : ce[4 * p + 3];
+        // the block's record tail: block 2p in lanes 8p .., block 2p + 1 in lanes 8p + 4 ..
+        const float xe = __int_as_float(__builtin_amdgcn_readlane(bt.t, 8 * p));
+        const float xo = __int_as_float(__builtin_amdgcn_readlane(bt.t, 8 * p + 4));
+        // the sum is hi 2^16 + lo; |hi|, |lo| < 2^27 (Q8_0), < 2^23 (Q4_0, biases included)
+        int32_t hi = c0 * 256 + c1, lo = c2 * 256 + c3;
+        if constexpr (KIND == FH_Q4_0) {
+            hi += upper ? __builtin_amdgcn_readlane(bt.t, 8 * p + 5) : __builtin_amdgcn_readlane(bt.t, 8 * p + 1);
+            lo += upper ? __builtin_amdgcn_readlane(bt.t, 8 * p + 6) : __builtin_amdgcn_readlane(bt.t, 8 * p + 2);
         }
+        const float f = fmaf((float)hi, 65536.0f, (float)lo);  // Q4_0: one rounding
         const float d = half_to_float(bt.s[p] >> (upper ? 16 : 0));
         acc = fmaf(d * f, upper ? xo : xe, acc);
     }
