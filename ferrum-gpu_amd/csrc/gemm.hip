@@ -1356,9 +1356,13 @@ GemmXSplit gemm_x_split(void *workspace, size_t rows, size_t k) {
 }
 
 // x hi (2 bytes per element), x lo (1 byte), one scale word per row, each piece 256-aligned
-size_t gemm_workspace_bytes(size_t rows, size_t k, size_t n) {
+size_t gemm_xsplit_bytes(size_t rows, size_t k) {
     const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
-    return up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)) + up(rows * 4) + gemm_partial_bytes(rows, k, n);
+    return up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)) + up(rows * 4);
+}
+
+size_t gemm_workspace_bytes(size_t rows, size_t k, size_t n) {
+    return gemm_xsplit_bytes(rows, k) + gemm_partial_bytes(rows, k, n);
 }
 
 // Room for the K-split partial products when the product's tile grid is too small to fill the
@@ -1425,7 +1429,8 @@ hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const ui
 }
 
 hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
-                       const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace, SplitOut *defer) {
+                       const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace, SplitOut *defer,
+                       float *partial) {
     const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     uint8_t *ws = (uint8_t *)workspace;
     GemmArgs g;
@@ -1438,7 +1443,7 @@ hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uin
     g.bsc = (const int32_t *)(b8 + up(n * ((k + 63) / 64 * 64)));
     g.y = y;
     const size_t pb = gemm_partial_bytes(rows, k, n);
-    g.partial = pb ? (float *)(ws + up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)) + up(rows * 4)) : nullptr;
+    g.partial = !pb ? nullptr : partial ? partial : (float *)(ws + gemm_xsplit_bytes(rows, k));
     g.M = (uint32_t)rows;
     g.K = (uint32_t)k;
     g.N = (uint32_t)n;

@@ -186,7 +186,10 @@ hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const ui
                         float *y, size_t rows, size_t k, size_t n);
 // The fast MFMA GEMM (two launches: split x into workspace, then the product); workspace holds
 // gemm_workspace_bytes(rows, k) bytes, b8 the weight's correction operand (launch_make_b8).
+// The workspace is the split x (gemm_xsplit_bytes) followed by the K-split partial products
+// (gemm_partial_bytes).
 size_t gemm_workspace_bytes(size_t rows, size_t k, size_t n);
+size_t gemm_xsplit_bytes(size_t rows, size_t k);
 size_t gemm_partial_bytes(size_t rows, size_t k, size_t n);
 size_t gemm_b8_bytes(size_t k, size_t n);
 // Whether the GEMM's 32-bit buffer offsets cover rows x (k, n) (every operand under 2^31 bytes).
@@ -194,10 +197,12 @@ bool gemm_supported(size_t rows, size_t k, size_t n);
 hipError_t launch_make_b8(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, uint8_t *b8, size_t k,
                           size_t n);
 // x == nullptr: the workspace already holds x in the split form (gemm_x_split, written by
-// split_row_fast in xsplit.hpp).
+// split_row_fast in xsplit.hpp). partial != nullptr: the K-split partial products go there
+// (gemm_partial_bytes) instead of after the split x, so that a consumer of deferred partial sums
+// can write the next product's split x (of another width) while it reads them.
 hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
                        const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace,
-                       SplitOut *defer = nullptr);
+                       SplitOut *defer = nullptr, float *partial = nullptr);
 // Where the fast GEMM's split x lives in its workspace: hi (rows x k f16), lo (rows x k rounded
 // up to 64, e4m3), one scale word per row.
 struct GemmXSplit {

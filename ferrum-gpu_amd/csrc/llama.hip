@@ -59,6 +59,10 @@ struct fh_llama {
           *logits = nullptr, *scores = nullptr;
     int32_t *ids = nullptr;
     void *ws = nullptr;
+    // fast path: the GEMMs' K-split partial products, after the widest split x in ws (the fused
+    // RMSNorm reads one product's deferred partial sums while it writes the next product's split
+    // x, which is sized for another width)
+    float *part = nullptr;
     // split attention operands (head dims 32, 64, 128): f16 parts and exponents, rows padded to 32
     _Float16 *sqh = nullptr, *sql = nullptr, *skh = nullptr, *skl = nullptr, *svh = nullptr, *svl = nullptr;
     int8_t *seq = nullptr, *sek = nullptr, *sev = nullptr;
@@ -794,12 +798,10 @@ size_t logit_chunk(const fh_llama *m, size_t t) {
     return std::max<size_t>(1, std::min(t, lim));
 }
 
+// Workspace of the precise and dequant-f16 paths (split x, then their partial products).
 size_t linear_ws(const fh_llama *m, size_t rows, size_t k, size_t n) {
-    switch (m->path) {
-    case FH_PATH_TILED_FAST: return gemm_workspace_bytes(rows, k, n);
-    case FH_PATH_TILED_F16: return gemm_f16_workspace_bytes(rows, k, n);
-    default: return gemm_precise_workspace_bytes(rows, k, n);
-    }
+    return m->path == FH_PATH_TILED_F16 ? gemm_f16_workspace_bytes(rows, k, n)
+                                        : gemm_precise_workspace_bytes(rows, k, n);
 }
 
 // The activations for t rows (kept when already large enough).
@@ -809,17 +811,25 @@ bool split_attention(const fh_llama *m) { return m->head_dim == 32 || m->head_di
 fh_status ensure_rows(fh_llama *m, size_t t) {
     if (t <= m->rows) return FH_OK;
     const size_t d = m->dim, qd = m->q_dim(), w = m->qkv_width(), hid = m->hidden, chunk = logit_chunk(m, t);
-    size_t ws = 0;
-    for (auto kn : {std::pair<size_t, size_t>{d, w}, {qd, d}, {d, 2 * hid}, {hid, d}})
-        ws = std::max(ws, linear_ws(m, t, kn.first, kn.second));
-    ws = std::max(ws, linear_ws(m, chunk, d, m->vocab));
+    size_t ws = 0, part = 0;
+    const bool fast = m->path == FH_PATH_TILED_FAST;
+    const std::pair<size_t, size_t> prods[] = {{t, d}, {t, qd}, {t, hid}, {chunk, d}};
+    const std::pair<size_t, size_t> kns[] = {{d, w}, {qd, d}, {d, 2 * hid}, {hid, d}};
+    if (fast) {
+        for (auto rk : prods) ws = std::max(ws, gemm_xsplit_bytes(rk.first, rk.second));
+        for (auto kn : kns) part = std::max(part, gemm_partial_bytes(t, kn.first, kn.second));
+        part = std::max(part, gemm_partial_bytes(chunk, d, m->vocab));
+    } else {
+        for (auto kn : kns) ws = std::max(ws, linear_ws(m, t, kn.first, kn.second));
+        ws = std::max(ws, linear_ws(m, chunk, d, m->vocab));
+    }
     const size_t tp = (t + 31) / 32 * 32, kvd = m->kv_dim();
     const size_t split = split_attention(m) ? 2 * up256(tp * qd * 2) + 4 * up256(tp * kvd * 2) + up256(tp * m->heads) +
                                                   2 * up256(tp * m->kv_heads)
                                             : 0;
     const size_t total = 3 * up256(t * d * 4) + up256(t * w * 4) + up256(t * qd * 4) + up256(t * 2 * hid * 4) +
                          up256(t * hid * 4) + up256(chunk * m->vocab * 4) + up256(2 * t * 4) + up256((t + 1) * 4) +
-                         up256(ws) + split;
+                         up256(ws) + up256(part) + split;
     void *p = nullptr;
     fh_status st = alloc_bytes(m->dev, total, &p);
     if (st) return st;
@@ -847,6 +857,7 @@ fh_status ensure_rows(fh_llama *m, size_t t) {
     m->scores = (float *)take(2 * t * 4);
     m->ids = (int32_t *)take((t + 1) * 4);
     m->ws = take(ws);
+    m->part = part ? (float *)take(part) : nullptr;
     if (split) {
         m->sqh = (_Float16 *)take(tp * qd * 2);
         m->sql = (_Float16 *)take(tp * qd * 2);
@@ -886,7 +897,8 @@ fh_status check_shapes(const fh_llama *m, size_t t) {
 hipError_t linear(const fh_llama *m, hipStream_t s, const fh_qweight *w, const float *x, float *y, size_t rows,
                   SplitOut *defer = nullptr) {
     switch (m->path) {
-    case FH_PATH_TILED_FAST: return launch_gemm(s, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, m->ws, defer);
+    case FH_PATH_TILED_FAST:
+        return launch_gemm(s, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, m->ws, defer, m->part);
     case FH_PATH_TILED_F16: return launch_gemm_f16(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws, defer);
     default: return launch_gemm_precise(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws, defer);
     }

@@ -216,3 +216,26 @@ def test_qwen2_0_5b_scoring_matches_the_oracle(fh, g, orc, qwen, path):
     assert lp512.shape == (512,) and lp2048.shape == (2048,)
     assert np.all(np.isfinite(lp2048)) and np.all(lp2048 <= 0)
     assert lp_err(lp512[:128], wlp) < bound and lp_err(lp2048[:512], lp512) < bound
+
+
+@pytest.mark.parametrize("kind", [lm.Q8_0, lm.Q4_0])
+def test_fast_path_with_narrow_attention_and_ffn(fh, g, orc, kind):
+    """heads * key_length and the FFN width both below dim (ferrum_model/src/gguf/llama/mod.rs:133
+    reads key_length from the file): the attention-output and down products are narrower than
+    dim, and at t = 160 both split along K. Their partial sums are added by the next RMSNorm while
+    it writes the next product's split x, which is dim wide; the two must not share memory."""
+    c = lm.config(vocab=300, ctx=160, dim=1024, heads=8, kv_heads=2, head_dim=64, layers=2, hidden=512,
+                  rope_base=10000.0, neox=True, eps=1e-5)
+    data = lm.to_gguf(lm.llama_random(c, 13, True, False), kind)
+    ref = lm.from_gguf(data)
+    ids = [int(t) for t in np.random.default_rng(3).integers(0, 300, 160)]
+    wlp, whit = orc.llama_score(ref, ids, threads=min(16, os.cpu_count() or 1))
+    precise = load(fh, g, data, fh.QPath.Tiled)
+    plp, phit = precise.score_arrays(ids)
+    assert lp_err(plp, wlp) < SCORE and np.array_equal(phit, whit)
+    fast = load(fh, g, data, fh.QPath.TiledFast)
+    for rep in range(3):
+        lp, hit = fast.score_arrays(ids)
+        e = lp_err(lp, wlp)
+        say(f"kind {kind} fast path rep {rep}: log-prob rel err {e:.2e}")
+        assert e < FAST_LOGPROB, (rep, e)
