@@ -1112,7 +1112,7 @@ __global__ __launch_bounds__(512, 1) void gemm_f16_big_kernel(const _Float16 *__
         const uint32_t st = st0 + p % split_stages;
         const bool live = p < stream && st < st1, two = live && 2 * st + 1 < nb;
         uint32_t m0, n0;
-        origin(p / split_stages, m0, n0);
+        origin(min(p / split_stages, my_tiles - 1), m0, n0);  // (positions past the stream load nothing)
         uint32_t o_a[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {

@@ -51,6 +51,7 @@ struct fh_qweight {
     uint8_t *qs = nullptr;    // quant plane (256-byte aligned)
     uint16_t *ds = nullptr;   // scale plane
     size_t nbytes = 0;        // exact GGUF byte count of the weight
+    size_t alloc = 0;         // bytes of the allocation (the padded planes)
     // The MFMA GEMM's fp8 correction operand (e4m3 of d * q per element, per-row power-of-two
     // scales; gemm_b8_bytes), built on the weight's first multi-row product and freed with it.
     mutable uint8_t *b8 = nullptr;

@@ -54,6 +54,7 @@ struct fh_llama {
     uint64_t weight_bytes = 0;
     // Activations for up to `rows` rows, grown on demand and kept.
     void *arena = nullptr;
+    size_t arena_bytes = 0;
     size_t rows = 0, chunk = 0;  // chunk: rows of logits the arena holds
     float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *o = nullptr, *gu = nullptr, *act = nullptr,
           *logits = nullptr, *scores = nullptr;
@@ -838,6 +839,7 @@ fh_status ensure_rows(fh_llama *m, size_t t) {
         (void)hipFree(m->arena);
     }
     m->arena = p;
+    m->arena_bytes = total;
     m->rows = t;
     m->chunk = chunk;
     uint8_t *q = (uint8_t *)p;
@@ -1220,6 +1222,21 @@ fh_status fh_llama_config(const fh_llama *m, fh_llama_cfg *out) {
 }
 
 uint64_t fh_llama_weight_bytes(const fh_llama *m) { return m ? m->weight_bytes : 0; }
+
+uint64_t fh_llama_device_bytes(const fh_llama *m) {
+    if (!m) return 0;
+    uint64_t b = fh_qweight_device_bytes(m->tok) + m->arena_bytes;
+    if (m->head != m->tok) b += fh_qweight_device_bytes(m->head);
+    for (const fh_buffer *v : {m->out_norm, m->rope_cos, m->rope_sin})
+        if (v) b += v->nbytes;
+    for (const auto &L : m->blocks) {
+        for (const fh_qweight *w : {L.wqkv, L.wo, L.wgu, L.down})
+            if (w) b += fh_qweight_device_bytes(w);
+        for (const fh_buffer *v : {L.attn_norm, L.ffn_norm, L.bqkv})
+            if (v) b += v->nbytes;
+    }
+    return b;
+}
 
 fh_status fh_llama_forward_all(fh_device *dev, fh_llama *m, const int32_t *ids, size_t n, float *logits) {
     fh_status st = check_dev(dev);

@@ -208,6 +208,7 @@ fh_status new_ext_qweight(fh_device *dev, fh_kind kind, size_t k, size_t n, fh_q
     w->qs = (uint8_t *)p;
     w->ds = nullptr;
     w->nbytes = nbytes;
+    w->alloc = nbytes;
     *out = w;
     return FH_OK;
 }
@@ -221,8 +222,9 @@ fh_status new_qweight(fh_device *dev, fh_kind kind, size_t k, size_t n, fh_qweig
         return fail(FH_ERR_INVALID, "a %zu x %zu weight is out of range", k, n);
     const size_t slots = tile_slots(n, k / QK);
     size_t nbytes = (k / QK) * n * block_bytes(kind);
+    const size_t alloc = scale_plane_offset(kind, slots) + scale_slots(n, k / QK) * 2;
     void *p = nullptr;
-    fh_status st = alloc_bytes(dev, scale_plane_offset(kind, slots) + scale_slots(n, k / QK) * 2, &p);
+    fh_status st = alloc_bytes(dev, alloc, &p);
     if (st) return st;
     fh_qweight *w = new (std::nothrow) fh_qweight;
     if (!w) {
@@ -238,6 +240,7 @@ fh_status new_qweight(fh_device *dev, fh_kind kind, size_t k, size_t n, fh_qweig
     w->qs = (uint8_t *)p;
     w->ds = (uint16_t *)((uint8_t *)p + scale_plane_offset(kind, slots));
     w->nbytes = nbytes;
+    w->alloc = alloc;
     *out = w;
     return FH_OK;
 }
@@ -594,7 +597,9 @@ void fh_qweight_free(fh_qweight *w) {
 fh_kind fh_qweight_kind(const fh_qweight *w) { return w->kind; }
 size_t fh_qweight_k(const fh_qweight *w) { return w->k; }
 size_t fh_qweight_n(const fh_qweight *w) { return w->n; }
-uint64_t fh_qweight_device_bytes(const fh_qweight *w) { return w->nbytes; }
+uint64_t fh_qweight_device_bytes(const fh_qweight *w) {
+    return w->alloc + (w->b8 ? gemm_b8_bytes(w->k, w->n) : 0);
+}
 
 fh_status fh_qweight_read_gguf(fh_device *dev, const fh_qweight *w, uint8_t *host, size_t len) {
     fh_status st = check_dev(dev);

@@ -166,6 +166,7 @@ def lib() -> ctypes.CDLL:
         "fh_llama_free": (None, [P]),
         "fh_llama_config": (I, [P, P]),
         "fh_llama_weight_bytes": (U64, [P]),
+        "fh_llama_device_bytes": (U64, [P]),
         "fh_llama_forward_all": (I, [P, P, P, S, P]),
         "fh_llama_score": (I, [P, P, P, S, P, P]),
         "fh_llama_score_device": (I, [P, P, P, S, P]),
@@ -361,8 +362,12 @@ class QWeight:
     def device_bytes(self) -> int:
         return lib().fh_qweight_device_bytes(self._h)
 
+    def gguf_bytes(self) -> int:
+        """Bytes of the weight's GGUF rows."""
+        return nbytes(self.kind(), self.k() * self.n())
+
     def read_gguf(self) -> np.ndarray:
-        out = np.empty(self.device_bytes(), np.uint8)
+        out = np.empty(self.gguf_bytes(), np.uint8)
         _check(lib().fh_qweight_read_gguf(self.gpu.handle, self._h, _ptr(out), out.size))
         return out
 

@@ -76,6 +76,11 @@ class GpuLlama:
         """Packed bytes of every block matrix and the head (what one forward reads)."""
         return lib().fh_llama_weight_bytes(self._h)
 
+    def device_bytes(self) -> int:
+        """Device memory the model holds (padded weight planes, the fast path's correction
+        operands, vectors, tables and the activation arena)."""
+        return lib().fh_llama_device_bytes(self._h)
+
     @staticmethod
     def _ids(ids) -> np.ndarray:
         a = np.asarray(ids)

@@ -8,7 +8,10 @@
  * Formats: GGUF Q8_0 (34-byte blocks: f16 scale + 32 x i8) and Q4_0 (18-byte blocks: f16 scale
  * + 16 bytes, byte j holds element j in its low nibble and element j+16 in its high nibble),
  * blocks of 32 along the input dimension. A quantized weight W of k inputs and n outputs is
- * resident as GGUF rows: n rows of k/32 blocks, byte-for-byte the tensor data of a GGUF file.
+ * uploaded as GGUF rows (n rows of k/32 blocks, the tensor data of a GGUF file) and kept as the
+ * same bytes repacked into tiles for the matrix cores: a plane of quants and a plane of f16 scales,
+ * rows padded to a multiple of 32 and scales to a multiple of eight blocks. fh_qweight_read_gguf
+ * gives the GGUF rows back bit for bit.
  *
  * Errors: every call returns an fh_status; on failure fh_last_error() (thread-local) holds a
  * message carrying the same substrings the reference's GpuError texts carry, so tests can match
@@ -158,7 +161,10 @@ FH_API fh_status fh_qweight_upload_f32(fh_device *dev, fh_kind kind, const float
 FH_API fh_status fh_qweight_quantise(fh_device *dev, fh_kind kind, const fh_buffer *w, size_t k,
                               size_t n, fh_qweight **out);
 FH_API void fh_qweight_free(fh_qweight *w);
-/* QWeight::{kind, k, n, device_bytes} (quant.rs:163-182). */
+/* QWeight::{kind, k, n, device_bytes} (quant.rs:163-182). device_bytes is the device memory the
+ * weight holds: its padded tile planes (the GGUF rows for F16, MXFP4, FP8 and Q2_K) and, once a
+ * multi-row FH_PATH_TILED_FAST product or a fast-path model has built it, the fast GEMM's e4m3
+ * correction operand (about one byte per weight). */
 FH_API fh_kind fh_qweight_kind(const fh_qweight *w);
 FH_API size_t fh_qweight_k(const fh_qweight *w);
 FH_API size_t fh_qweight_n(const fh_qweight *w);
@@ -355,8 +361,12 @@ FH_API fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path pa
 FH_API void fh_llama_free(fh_llama *m);
 /* Config (ferrum_ref/src/models/llama/mod.rs:24-51) and how the model is stored. */
 FH_API fh_status fh_llama_config(const fh_llama *m, fh_llama_cfg *out);
-/* Packed weight bytes one forward reads (every block matrix and the head). */
+/* Packed weight bytes one forward reads (every block matrix and the head, GGUF sizes). */
 FH_API uint64_t fh_llama_weight_bytes(const fh_llama *m);
+/* Device memory the model holds: every weight's device_bytes (the tied head once), the vectors,
+ * the RoPE tables and the activation arena at its current size (no counterpart in the reference,
+ * whose GpuLlama keeps f32 weights). */
+FH_API uint64_t fh_llama_device_bytes(const fh_llama *m);
 /* GpuLlama::forward_all (forward.rs:13-73): every position's logits of ids[0..n), [n, vocab]
  * row-major into host memory. Errors: "sequence length N must be in 1..=ctx", "token T is out of
  * range for vocab V". */

@@ -198,6 +198,12 @@ def test_qwen2_0_5b_scoring_matches_the_oracle(fh, g, orc, qwen, path):
     data, ref = qwen
     dev = load(fh, g, data, fh.QPath[path])
     assert dev.weight_bytes() == 277_853_184  # the packed Q4_0 bytes of every matrix and the head
+    # the device footprint: padded planes, vectors, tables; the fast path adds a byte per weight
+    db = dev.device_bytes()
+    say(f"{path}: device bytes {db / 1e6:.1f} MB")
+    assert db > 277_853_184
+    if path == "TiledFast":
+        assert db > 277_853_184 + 493_961_216
     ids = [int(t) for t in np.random.default_rng(2024).integers(0, 151936, 129)]
     t0 = time.time()
     wlp, whit = orc.llama_score(ref, ids, threads=min(16, os.cpu_count() or 1))

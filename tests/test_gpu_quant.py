@@ -79,17 +79,31 @@ def test_pack_and_quantise_refuse_bad_shapes(fh, g):
             fh.upload_quantised(g, kind, np.zeros(63, np.float32), 32, 2)
 
 
-def test_resident_bytes_are_the_gguf_bytes_and_the_size_is_the_file_size(fh, g, orc):
-    """ops/quant/tests.rs:182-198 (our resident layout is the GGUF bytes themselves: 34 / 18
-    bytes per 32 weights, against the reference's widened 36 / 20)."""
-    k, n = 64, 32
-    w = orc.rand_vec(k * n, 1)
-    for kind, ratio in [(fh.QKind.Q8_0, 128 / 34), (fh.QKind.Q4_0, 128 / 18)]:
-        b = orc.quantise_matrix(int(kind), w, k, n)
-        qw = fh.upload_qweight(g, kind, b, k, n)
-        assert np.array_equal(qw.read_gguf(), b)
-        assert abs(k * n * 4 / qw.device_bytes() - ratio) < 1e-9
-        assert (qw.k(), qw.n(), qw.kind()) == (k, n, kind)
+def test_resident_bytes_read_back_and_device_bytes_is_the_real_footprint(fh, g, orc):
+    """ops/quant/tests.rs:182-198: device_bytes is the device memory the weight holds. Here the
+    GGUF bytes are kept as tiles: the quants of 32-row groups (16 / 32 bytes per block) and the
+    f16 scales padded to eight blocks per row; at 8 blocks per row and whole 32-row groups that
+    is exactly the GGUF size (34 / 18 bytes per 32 weights, against the reference's widened
+    36 / 20). A fast multi-row product adds the e4m3 correction operand (one byte per weight,
+    k rounded up to 64, plus a scale word per row)."""
+    for k, n in [(256, 64), (64, 32), (96, 40)]:
+        w = orc.rand_vec(k * n, 1)
+        for kind in kinds(fh):
+            b = orc.quantise_matrix(int(kind), w, k, n)
+            qw = fh.upload_qweight(g, kind, b, k, n)
+            assert np.array_equal(qw.read_gguf(), b)
+            assert (qw.k(), qw.n(), qw.kind(), qw.gguf_bytes()) == (k, n, kind, b.size)
+            nb, groups = k // 32, (n + 31) // 32
+            planes = -(-groups * 32 * nb * (32 if kind == fh.QKind.Q8_0 else 16) // 256) * 256
+            planes += groups * 32 * (-(-nb // 8) * 8) * 2
+            assert qw.device_bytes() == planes, (k, n, kind)
+            if (k, n) == (256, 64):
+                assert planes == b.size  # whole 32-row groups and 8-block runs: the file's size
+                assert abs(k * n * 4 / qw.device_bytes() - (128 / 34 if kind == fh.QKind.Q8_0 else 128 / 18)) < 1e-9
+            gx, gy = g.upload(orc.rand_vec(8 * k, 2)), g.zeros(8 * n)
+            fh.linear_q_with(g, gx, qw, gy, 8, fh.QPath.TiledFast)
+            b8 = -(-n * (-(-k // 64) * 64) // 256) * 256 + 4 * n
+            assert qw.device_bytes() == planes + b8, (k, n, kind)
 
 
 def test_device_quantise_matrix_is_bit_exact(fh, g, orc):
