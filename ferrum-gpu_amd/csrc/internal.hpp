@@ -30,6 +30,9 @@ struct fh_device {
     std::mutex ws_mu;
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    // This GPU's copy of the no-allocation entry point's static scratch array (its device
+    // address, taken when the device is opened).
+    void *scratch = nullptr;
 };
 
 struct fh_buffer {

@@ -9,6 +9,12 @@
 
 #include "internal.hpp"
 
+// Scratch of the no-allocation entry point (fh_linear_q_noalloc): one array per GPU, made when
+// the library's code object loads on that GPU and held until the process ends. Host code never
+// uses this name as an address: fh_device_open takes this GPU's device address of it with
+// hipGetSymbolAddress, and every launch gets that pointer.
+static __device__ __align__(256) uint8_t scratch[FH_NOALLOC_SCRATCH_BYTES];
+
 namespace fh {
 
 static thread_local std::string g_err;
@@ -290,6 +296,11 @@ fh_status fh_device_open(int ordinal, fh_device **out) {
     d->ordinal = ordinal;
     d->cus = prop.multiProcessorCount;
     d->name = prop.name[0] ? prop.name : prop.gcnArchName;
+    // this GPU's copy of the no-allocation scratch (the device is current)
+    if ((e = hipGetSymbolAddress(&d->scratch, HIP_SYMBOL(scratch))) != hipSuccess) {
+        delete d;
+        return hip_fail(nullptr, e, "scratch address");
+    }
     if ((e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking)) != hipSuccess) {
         delete d;
         return hip_fail(nullptr, e, "create stream");
@@ -648,8 +659,20 @@ fh_path fh_choose(size_t rows, fh_kind kind, size_t k, size_t n) {
     return FH_PATH_TILED;
 }
 
+// Scratch for one linear command: the device's workspace (grown on demand) or, for the
+// no-allocation entry point (fixed = the device's static scratch), that array within its size.
+static fh_status command_scratch(fh_device *dev, void *fixed, size_t bytes, void **out) {
+    if (!fixed) return workspace(dev, bytes, out);
+    if (bytes > FH_NOALLOC_SCRATCH_BYTES)
+        return fail(FH_ERR_INVALID,
+                    "linear_q_noalloc: the product needs %zu bytes of scratch, more than the %u the library holds",
+                    bytes, (unsigned)FH_NOALLOC_SCRATCH_BYTES);
+    *out = fixed;
+    return FH_OK;
+}
+
 static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, float *y, size_t rows,
-                        fh_path path) {
+                        fh_path path, void *fixed = nullptr) {
     if (path == FH_PATH_AUTO) path = fh_choose(rows, w->kind, w->k, w->n);
     fh_status st;
     if (ext_kind(w->kind)) {  // decoded on the fly, f32 products (formats.hip)
@@ -668,7 +691,7 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
             return fail(FH_ERR_INVALID, "the GEMV kernel's 32-bit offsets do not cover a %zu x %zu weight",
                         w->n, w->k);
         void *prep = nullptr;
-        if ((st = workspace(dev, gemv_prep_bytes(w->k), &prep))) return st;
+        if ((st = command_scratch(dev, fixed, gemv_prep_bytes(w->k), &prep))) return st;
         if ((st = begin_command(dev, "linear_q"))) return st;
         (void)launch_gemv(dev->stream, w->kind, w->qs, w->ds, x, y, w->k, w->n, prep, dev->cus);
         return end_command(dev, "linear_q");
@@ -679,7 +702,8 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
         return end_command(dev, "linear_q");
     case FH_PATH_TILED: {
         void *ws = nullptr;
-        if (rows && (st = workspace(dev, gemm_precise_workspace_bytes(rows, w->k, w->n), &ws))) return st;
+        if (rows && (st = command_scratch(dev, fixed, gemm_precise_workspace_bytes(rows, w->k, w->n), &ws)))
+            return st;
         if ((st = begin_command(dev, "linear_q"))) return st;
         if (rows) (void)launch_gemm_precise(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, ws);
         return end_command(dev, "linear_q");
@@ -688,8 +712,11 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
         if (!gemm_supported(rows, w->k, w->n))
             return fail(FH_ERR_INVALID, "the MFMA GEMM's 32-bit offsets do not cover %zu rows of a %zu x %zu weight",
                         rows, w->n, w->k);
+        if (fixed && rows && !w->b8)
+            return fail(FH_ERR_INVALID, "linear_q_noalloc: the fast GEMM needs the weight's correction operand, "
+                                        "which its first multi-row FH_PATH_TILED_FAST linear_q builds");
         void *ws = nullptr;
-        if (rows && (st = workspace(dev, gemm_workspace_bytes(rows, w->k, w->n), &ws))) return st;
+        if (rows && (st = command_scratch(dev, fixed, gemm_workspace_bytes(rows, w->k, w->n), &ws))) return st;
         void *fresh = nullptr;  // the correction operand, built within the weight's first multi-row command
         if (rows && !w->b8 && (st = alloc_bytes(dev, gemm_b8_bytes(w->k, w->n), &fresh))) return st;
         if ((st = begin_command(dev, "linear_q"))) {
@@ -708,7 +735,7 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
             return fail(FH_ERR_INVALID, "the MFMA GEMM's 32-bit offsets do not cover %zu rows of a %zu x %zu weight",
                         rows, w->n, w->k);
         void *ws = nullptr;
-        if (rows && (st = workspace(dev, gemm_f16_workspace_bytes(rows, w->k, w->n), &ws))) return st;
+        if (rows && (st = command_scratch(dev, fixed, gemm_f16_workspace_bytes(rows, w->k, w->n), &ws))) return st;
         if ((st = begin_command(dev, "linear_q"))) return st;
         if (rows) (void)launch_gemm_f16(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, ws);
         return end_command(dev, "linear_q");
@@ -738,6 +765,18 @@ fh_status fh_linear_q_ptr(fh_device *dev, const float *x, const fh_qweight *w, f
     if (!x) return fail(FH_ERR_INVALID, "linear_q x: null pointer");
     if (!y) return fail(FH_ERR_INVALID, "linear_q y: null pointer");
     return linear(dev, x, w, y, rows, path);
+}
+
+fh_status fh_linear_q_noalloc(fh_device *dev, const float *x, const fh_qweight *w, float *y, size_t rows,
+                              fh_path path) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!w) return fail(FH_ERR_INVALID, "linear_q: no weight");
+    if (rows > (1u << 24)) return fail(FH_ERR_INVALID, "linear_q: %zu rows is too many", rows);
+    if (!x) return fail(FH_ERR_INVALID, "linear_q x: null pointer");
+    if (!y) return fail(FH_ERR_INVALID, "linear_q y: null pointer");
+    if (!dev->scratch) return fail(FH_ERR_DEVICE, "linear_q_noalloc: the device has no scratch address");
+    return linear(dev, x, w, y, rows, path, dev->scratch);
 }
 
 // ---- grouped batch-1 GEMV ----

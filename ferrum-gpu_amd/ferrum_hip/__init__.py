@@ -124,6 +124,7 @@ def lib() -> ctypes.CDLL:
         "fh_choose": (I, [S, I, S, S]),
         "fh_linear_q": (I, [P, P, P, P, S, I]),
         "fh_linear_q_ptr": (I, [P, P, P, P, S, I]),
+        "fh_linear_q_noalloc": (I, [P, P, P, P, S, I]),
         "fh_gemv_plan_create": (I, [P, P, S, PP]),
         "fh_gemv_plan_run": (I, [P, P]),
         "fh_gemv_plan_launches": (S, [P]),
@@ -472,6 +473,15 @@ def linear_q_with(gpu: Gpu, x: GpuBuf, w: QWeight, y: GpuBuf, rows: int, path: Q
 def linear_q_ptr(gpu: Gpu, x_ptr: int, w: QWeight, y_ptr: int, rows: int, path: QPath = QPath.Auto) -> None:
     """linear_q on raw device pointers (e.g. torch tensors' data_ptr())."""
     _check(lib().fh_linear_q_ptr(gpu.handle, x_ptr, w.handle, y_ptr, rows, int(path)))
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20  # FH_NOALLOC_SCRATCH_BYTES
+
+
+def linear_q_noalloc(gpu: Gpu, x_ptr: int, w: QWeight, y_ptr: int, rows: int, path: QPath = QPath.Auto) -> None:
+    """linear_q_ptr without any device allocation (no counterpart in the reference): scratch from
+    the library's static per-GPU array; calls that overlap on one GPU race."""
+    _check(lib().fh_linear_q_noalloc(gpu.handle, x_ptr, w.handle, y_ptr, rows, int(path)))
 
 
 class _Problem(ctypes.Structure):

@@ -187,6 +187,19 @@ FH_API fh_status fh_linear_q(fh_device *dev, const fh_buffer *x, const fh_qweigh
  * own their memory (a torch tensor, a KV-cache arena). Same checks on rows and shapes. */
 FH_API fh_status fh_linear_q_ptr(fh_device *dev, const float *x, const fh_qweight *w, float *y,
                           size_t rows, fh_path path);
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): fh_linear_q_ptr with
+ * the same kernels and results, but no device allocation or free of any kind. Its scratch (the
+ * GEMV's prepared x, the GEMMs' split x and K-split partial sums) is one static device array of
+ * FH_NOALLOC_SCRATCH_BYTES per GPU, made when the library loads on that GPU and held until the
+ * process ends; a product that needs more fails with "scratch". Every call on one GPU shares that
+ * array and it keeps the last call's contents: calls that overlap on one GPU (from two threads, or
+ * through two fh_device handles of one ordinal, each with its own stream) race. FH_PATH_TILED_FAST
+ * also needs the weight's correction operand, built by an ordinary multi-row FH_PATH_TILED_FAST
+ * linear_q on that weight; without it the call fails. */
+#define FH_NOALLOC_SCRATCH_BYTES (32u << 20)
+FH_API fh_status fh_linear_q_noalloc(fh_device *dev, const float *x, const fh_qweight *w, float *y,
+                                     size_t rows, fh_path path);
 
 /* No counterpart in the reference: one launch for many independent batch-1 products
  * y_i = x_i * W_i (a decode step's projections, or several models' layers). The plan is built
