@@ -202,7 +202,9 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
     const auto rd = make_rsrc(a.ds + (size_t)g * nb8 * 256, nb8 * 512);
     const auto ra = make_rsrc(a.prep, PRO == PRO_GLOBAL ? span * kPrepBytes : 0);
     const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16);
-    const uint32_t os = (uint32_t)(r * 16), oa = prep_a_offset(lane), ot = prep_tail_offset(lane);
+    const uint32_t os = (uint32_t)(r * 16), oa = prep_a_offset(lane), ot = prep_tail_offset<KIND>(lane);
+    const auto g16 = [&](uint32_t off) { return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)off, 0, 0)); };
+    const auto g4 = [&](uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(ra, (int)off, 0, 0); };
     uint8_t *prep = dlds;  // records of blocks b0 .. b1 (PRO_LN: of every block)
     float *part = (float *)(dlds + (PRO == PRO_GLOBAL ? 0 : (PRO == PRO_LN ? span : a.chunk) * kPrepBytes));
     float *red = part + W * 32;
@@ -214,7 +216,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
         load_weights<KIND>(cur, rq, rd, oq, os, bb);
         if constexpr (PRO == PRO_GLOBAL) {
             cur.a = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(bb * kPrepBytes + oa), 0, 0));
-            cur.t = __builtin_amdgcn_raw_buffer_load_b32(ra, (int)(bb * kPrepBytes + ot), 0, 0);
+            load_tails<KIND>(cur, bb * kPrepBytes, ot, g16, g4);
         }
     }
     if constexpr (PRO == PRO_LN) {
@@ -241,12 +243,16 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
             load_weights<KIND>(nx, rq, rd, oq, os, nxt);
             if constexpr (PRO == PRO_GLOBAL) {
                 nx.a = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)(nxt * kPrepBytes + oa), 0, 0));
-                nx.t = __builtin_amdgcn_raw_buffer_load_b32(ra, (int)(nxt * kPrepBytes + ot), 0, 0);
+                load_tails<KIND>(nx, nxt * kPrepBytes, ot, g16, g4);
             }
         }
         if constexpr (PRO != PRO_GLOBAL) {
-            cur.a = *(const __attribute__((address_space(3))) i32x4 *)(prep + (bb - pbase) * kPrepBytes + oa);
-            cur.t = *(const __attribute__((address_space(3))) uint32_t *)(prep + (bb - pbase) * kPrepBytes + ot);
+            typedef __attribute__((address_space(3))) const uint8_t lbyte;
+            lbyte *lp = (lbyte *)prep;
+            cur.a = *(const __attribute__((address_space(3))) i32x4 *)(lp + (bb - pbase) * kPrepBytes + oa);
+            load_tails<KIND>(cur, (bb - pbase) * kPrepBytes, ot,
+                             [&](uint32_t off) { return *(const __attribute__((address_space(3))) u32x4 *)(lp + off); },
+                             [&](uint32_t off) { return *(const __attribute__((address_space(3))) uint32_t *)(lp + off); });
         }
         compute_batch<KIND>(cur, upper, acc);
         cur = nx;

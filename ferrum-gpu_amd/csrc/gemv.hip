@@ -133,11 +133,16 @@ __device__ __forceinline__ void load_batch(Batch<KIND> &bt, const Task<KIND> &tk
     }
     bt.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(tk.rd, (int)(o.s + b * 64), 0, 0));
     if constexpr (LDSX) {
-        bt.a = *(const i32x4 *)&gemv_lds[lds_base + b * kPrepBytes + o.a];
-        bt.t = *(const uint32_t *)&gemv_lds[lds_base + b * kPrepBytes + o.t];
+        const uint8_t *base = &gemv_lds[lds_base];
+        bt.a = *(const i32x4 *)&base[b * kPrepBytes + o.a];
+        load_tails<KIND>(bt, b * kPrepBytes, o.t, [&](uint32_t off) { return *(const u32x4 *)&base[off]; },
+                         [&](uint32_t off) { return *(const uint32_t *)&base[off]; });
     } else {
         bt.a = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(tk.ra, (int)(o.a + b * kPrepBytes), 0, 0));
-        bt.t = __builtin_amdgcn_raw_buffer_load_b32(tk.ra, (int)(o.t + b * kPrepBytes), 0, 0);
+        load_tails<KIND>(
+            bt, b * kPrepBytes, o.t,
+            [&](uint32_t off) { return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(tk.ra, (int)off, 0, 0)); },
+            [&](uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(tk.ra, (int)off, 0, 0); });
     }
 }
 
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ 
     // Q4_0: block pair chunk of 1 KiB, lane l at 16 l; Q8_0: block tile of 1 KiB, row r at 32 r;
     // scales: row r's eight at 16 r; prepared x: prep_a_offset, prep_tail_offset
     const LaneOffsets o{KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16), (uint32_t)(r * 16),
-                        prep_a_offset(lane), prep_tail_offset(lane)};
+                        prep_a_offset(lane), prep_tail_offset<KIND>(lane)};
     // The wavefront's tasks are one stream of batches: the loads of the next batch (of this task
     // or the next) are in flight while a batch is computed, so the pipeline never drains at a
     // task boundary. lp is the batch being loaded, cp the batch being computed.

@@ -138,15 +138,22 @@ __device__ __forceinline__ void zero_record(int j, U32Ptr rec) {
 
 // Per-lane byte offsets into the records of an 8-block batch: the MFMA's A operand (lane l
 // holds A row l % 32, i.e. limb (l % 4) of block (l % 32) / 4, k half l / 32) and the record
-// tail (lanes 4j .. 4j + 3 and 32 + 4j .. 32 + 4j + 3 take dwords 32 .. 35 of block j).
+// tails. Q8_0 needs only each block's scale: lanes 4j .. 4j + 3 and 32 + 4j .. 32 + 4j + 3 take
+// dwords 32 .. 35 of block j (one dword load; the scales are read across lanes). Q4_0 needs the
+// scale and both biases of the block a lane finishes: lane half h takes the 16-byte tail of block
+// 2p + h for each block pair p (one 16-byte load per pair, at + 2 p kPrepBytes; every lane of a
+// half reads the same bytes).
 __device__ __forceinline__ uint32_t prep_a_offset(int lane) {
     const int r = lane % 32;
     return (uint32_t)((r / 4) * kPrepBytes + (r % 4) * 32 + 16 * (lane / 32));
 }
+template <int KIND>
 __device__ __forceinline__ uint32_t prep_tail_offset(int lane) {
     const int r = lane % 32;
-    return (uint32_t)((r / 4) * kPrepBytes + 128 + 4 * (r % 4));
+    return KIND == FH_Q8_0 ? (uint32_t)((r / 4) * kPrepBytes + 128 + 4 * (r % 4))
+                           : (uint32_t)((lane / 32) * kPrepBytes + 128);
 }
+constexpr int kTailLoads = 4;  // Q4_0: 16-byte tail loads per batch (one per block pair)
 
 // The same for block b of x in global memory.
 template <int KIND, class U32Ptr>
@@ -171,8 +178,21 @@ struct Batch {  // what one lane loads for a batch of kBatch blocks of its task
                   // Q8_0: bytes 16h .. 16h + 15 of block i of the row (h = lane / 32)
     u32x4 s;      // the row's eight scales
     i32x4 a;      // the prepared x of the eight blocks, as the MFMA's A operand
-    uint32_t t;   // a record-tail dword of the eight blocks (prep_tail_offset)
+    static constexpr int TL = KIND == FH_Q8_0 ? 1 : kTailLoads;
+    u32x4 t[TL];  // record tails (prep_tail_offset): Q8_0 t[0].x, Q4_0 t[p] = block 2p + h's tail
 };
+
+// The record tails of a batch whose records start at byte b_off: `load16(off)` reads 16 bytes,
+// `load4(off)` 4 bytes, at byte offset off of the records' memory.
+template <int KIND, class L16, class L4>
+__device__ __forceinline__ void load_tails(Batch<KIND> &bt, uint32_t b_off, uint32_t lane_off, L16 load16, L4 load4) {
+    if constexpr (KIND == FH_Q8_0) {
+        bt.t[0].x = load4(b_off + lane_off);
+    } else {
+#pragma unroll
+        for (int p = 0; p < kTailLoads; p++) bt.t[p] = load16(b_off + lane_off + 2 * p * kPrepBytes);
+    }
+}
 
 __device__ __forceinline__ i32x4 nibbles(uint32_t q0, uint32_t q1) {
     return i32x4{(int32_t)(q0 & 0x0f0f0f0fu), (int32_t)(q1 & 0x0f0f0f0fu), (int32_t)((q0 >> 4) & 0x0f0f0f0fu),
@@ -180,11 +200,13 @@ __device__ __forceinline__ i32x4 nibbles(uint32_t q0, uint32_t q1) {
 }
 
 // The batch's contribution to the lane's accumulator: lanes 0..31 take the even blocks of the
-// batch, lanes 32..63 the odd ones (row lane % 32 in both halves).
+// batch, lanes 32..63 the odd ones (row lane % 32 in both halves). Pipelined by block pair: the
+// MFMAs of pair p + 1 are issued before pair p's sums are finished, and no more than two pairs'
+// accumulators are live (scheduling barriers keep the compiler from issuing every MFMA first).
 template <int KIND, int PAIRS = kBatch / 2>
 __device__ __forceinline__ void compute_batch(const Batch<KIND> &bt, bool upper, float &acc) {
-#pragma unroll
-    for (int p = 0; p < PAIRS; p++) {  // blocks 2p and 2p + 1 of the batch
+    i32x16 ce[2], co[2];
+    auto issue = [&](int p) {  // blocks 2p and 2p + 1 of the batch
         i32x4 be, bo;
         if constexpr (KIND == FH_Q8_0) {
             be = __builtin_bit_cast(i32x4, bt.q[2 * p]);
@@ -201,24 +223,40 @@ __device__ __forceinline__ void compute_batch(const Batch<KIND> &bt, bool upper,
         // A rows 4j .. 4j + 3 hold block j's limb rows, so C rows 4j .. 4j + 3 are block j's
         // limb sums: for j = 2p in registers 4p .. 4p + 3 of lanes 0..31, for j = 2p + 1 in the
         // same registers of lanes 32..63. The other rows mix blocks and are not used.
-        const i32x16 ce = __builtin_amdgcn_mfma_i32_32x32x32_i8(bt.a, be, i32x16{}, 0, 0, 0);
-        const i32x16 co = __builtin_amdgcn_mfma_i32_32x32x32_i8(bt.a, bo, i32x16{}, 0, 0, 0);
-        const int32_t c0 = upper ? co[4 * p] : ce[4 * p];
-        const int32_t c1 = upper ? co[4 * p + 1] : ce[4 * p + 1];
-        const int32_t c2 = upper ? co[4 * p + 2] : ce[4 * p + 2];
-        const int32_t c3 = upper ? co[4 * p + 3] : ce[4 * p + 3];
-        // the block's record tail: block 2p in lanes 8p .., block 2p + 1 in lanes 8p + 4 ..
-        const float xe = __int_as_float(__builtin_amdgcn_readlane(bt.t, 8 * p));
-        const float xo = __int_as_float(__builtin_amdgcn_readlane(bt.t, 8 * p + 4));
+        ce[p & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bt.a, be, i32x16{}, 0, 0, 0);
+        co[p & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bt.a, bo, i32x16{}, 0, 0, 0);
+    };
+    auto finish = [&](int p) {
+        const i32x16 &e = ce[p & 1], &o = co[p & 1];
+        const int32_t c0 = upper ? o[4 * p] : e[4 * p];
+        const int32_t c1 = upper ? o[4 * p + 1] : e[4 * p + 1];
+        const int32_t c2 = upper ? o[4 * p + 2] : e[4 * p + 2];
+        const int32_t c3 = upper ? o[4 * p + 3] : e[4 * p + 3];
         // the sum is hi 2^16 + lo; |hi|, |lo| < 2^27 (Q8_0), < 2^23 (Q4_0, biases included)
         int32_t hi = c0 * 256 + c1, lo = c2 * 256 + c3;
-        if constexpr (KIND == FH_Q4_0) {
-            hi += upper ? __builtin_amdgcn_readlane(bt.t, 8 * p + 5) : __builtin_amdgcn_readlane(bt.t, 8 * p + 1);
-            lo += upper ? __builtin_amdgcn_readlane(bt.t, 8 * p + 6) : __builtin_amdgcn_readlane(bt.t, 8 * p + 2);
+        float xs;
+        if constexpr (KIND == FH_Q8_0) {
+            // the block's x scale: block 2p in lanes 8p .., block 2p + 1 in lanes 8p + 4 ..
+            const float xe = __int_as_float(__builtin_amdgcn_readlane(bt.t[0].x, 8 * p));
+            const float xo = __int_as_float(__builtin_amdgcn_readlane(bt.t[0].x, 8 * p + 4));
+            xs = upper ? xo : xe;
+        } else {
+            // this lane's block: its scale and biases
+            xs = __uint_as_float(bt.t[p].x);
+            hi += (int32_t)bt.t[p].y;
+            lo += (int32_t)bt.t[p].z;
         }
         const float f = fmaf((float)hi, 65536.0f, (float)lo);  // Q4_0: one rounding
         const float d = half_to_float(bt.s[p] >> (upper ? 16 : 0));
-        acc = fmaf(d * f, upper ? xo : xe, acc);
+        acc = fmaf(d * f, xs, acc);
+    };
+    issue(0);
+#pragma unroll
+    for (int p = 0; p < PAIRS; p++) {
+        if (p + 1 < PAIRS) issue(p + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        finish(p);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
