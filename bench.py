@@ -107,6 +107,21 @@ def measured_traffic(bytes_per_launch):
     return L and {"traffic_bytes": L["traffic_bytes"], "source": d.get("source", path)}
 
 
+PREWARM_S = 0.1
+
+
+def prewarm(g, run, seconds=PREWARM_S):
+    """Untimed load before a measurement: the GPU takes several milliseconds of sustained work
+    to reach its steady clocks (a 20-step loop straight after 5 warm-up steps measured 4-6% below
+    the same loop after 40 more steps). Runs `run` until `seconds` of wall time have passed."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            run()
+        g.sync()
+    return time.perf_counter() - t0
+
+
 def bench_gemv_pool(fh, g, ev, kind, groups, pool_bytes, steps, warmup, seed=0):
     """Batch-1 GEMV over a pool of distinct resident weights. `groups` is a list of shape lists;
     each group becomes one grouped launch (one plan) per step. The K timed steps run back to back
@@ -134,6 +149,7 @@ def bench_gemv_pool(fh, g, ev, kind, groups, pool_bytes, steps, warmup, seed=0):
         plans.append(fh.GemvPlan(g, probs))
     for p in plans:
         assert p.launches() == 1, "each group must be one launch"
+    warm_s = prewarm(g, lambda: [p.run() for p in plans])
     for _ in range(warmup):
         for p in plans:
             p.run()
@@ -174,7 +190,7 @@ def bench_gemv_pool(fh, g, ev, kind, groups, pool_bytes, steps, warmup, seed=0):
     return {"copies": copies, "products": copies * len(shapes), "launches_per_step": npl,
             "bytes_per_step": step_bytes, "ms_per_step": step_ms,
             "wall_ms_per_step": wall * 1e3 / steps,
-            "gbs": step_bytes / (step_ms * 1e-3) / 1e9, "launches": launches}
+            "gbs": step_bytes / (step_ms * 1e-3) / 1e9, "launches": launches, "prewarm_s": round(warm_s, 3)}
 
 
 def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0, path=None, copies=1):
@@ -490,7 +506,8 @@ def main():
         "data": "synthetic: seeded N(0,0.02) weights packed Q4_0, x ~ N(0,1)",
         "config": {"workload": "Q4_0 GEMV sweep, K x N in {896x1152, 896x4864, 4864x896}, "
                                f"{head['copies']} distinct copies each ({head['bytes_per_step'] / 2**30:.2f} GiB per step)",
-                   "products_per_step": head["products"], "launches_per_step": head["launches_per_step"]},
+                   "products_per_step": head["products"], "launches_per_step": head["launches_per_step"],
+                   "prewarm_s": head["prewarm_s"]},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic and traffic["traffic_bytes"],
                      "kernel": f"grouped Q4_0 GEMV (x preparation + product kernels) over {dom['shapes']} x "

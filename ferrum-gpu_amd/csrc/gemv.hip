@@ -117,6 +117,15 @@ struct LaneOffsets {
 // of eight), holding the records of the product the wavefront works on.
 extern __shared__ __attribute__((aligned(16))) uint8_t gemv_lds[];
 
+// Finished rows wait in LDS and are stored kStage tasks at a time (two tasks per store
+// instruction): loads and stores share one in-order completion counter, so a store after every
+// task would make the next batch's wait for its loads also wait for that store.
+constexpr uint32_t kStage = 16;
+struct StageMeta {
+    float *y;
+    uint32_t row0, n;
+};
+
 template <int KIND, bool LDSX>
 __device__ __forceinline__ void load_batch(Batch<KIND> &bt, const Task<KIND> &tk, uint32_t b,
                                            const LaneOffsets &o, uint32_t lds_base) {
@@ -210,17 +219,34 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ 
         }
     };
     float acc = 0.0f;
+    __shared__ float stage_rows[4][kStage][32];
+    __shared__ StageMeta stage_meta[4][kStage];
+    const uint32_t wv = threadIdx.x / 64;
+    uint32_t staged = 0;  // wave-uniform
+    // Store the staged rows: lanes 0..31 take staged task 2i, lanes 32..63 task 2i + 1.
+    auto flush = [&]() {
+        for (uint32_t i = 0; i < staged; i += 2) {
+            const uint32_t s = i + (upper ? 1 : 0);
+            if (s < staged) {
+                const StageMeta m = stage_meta[wv][s];
+                const uint32_t row = m.row0 + r;
+                // (a global-address-space store: a flat store would also count against the
+                // scalar-load counter and make the next wait for loads a full drain)
+                if (row < m.n) ((__attribute__((address_space(1))) float *)m.y)[row] = stage_rows[wv][s][r];
+            }
+        }
+        staged = 0;
+    };
     // After computing batch cp: on a task's last batch, add the row's odd blocks (lane 32 + r) to
-    // its even ones (lane r) and store the row.
+    // its even ones (lane r) and stage the row.
     auto finish = [&](const Pos &cp) {
         if (cp.b + kBatch >= cp.nb) {
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc), false, false);
             const float sum = acc + __uint_as_float(upper ? sw[0] : sw[1]);
-            // (a global-address-space store: a flat store would also count against the
-            // scalar-load counter and make the next wait for loads a full drain)
-            const uint32_t row = cp.g * 32 + r;
-            if (!upper && row < cp.n) ((__attribute__((address_space(1))) float *)cp.y)[row] = sum;
+            if (!upper) stage_rows[wv][staged][r] = sum;
+            if (lane == 0) stage_meta[wv][staged] = StageMeta{cp.y, cp.g * 32, cp.n};
             acc = 0.0f;
+            if (++staged == kStage) flush();
         }
     };
     Batch<KIND> b0, b1;
@@ -252,6 +278,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ 
         cp = lp;
         advance();
     }
+    flush();
 }
 
 // Wavefronts per CU a launch aims for (FERRUM_HIP_GEMV_WAVES_PER_CU overrides, 1..32), at most
@@ -265,7 +292,7 @@ uint32_t waves_per_cu() {
     return w;
 }
 
-constexpr uint32_t kMaxLdsBlocks = 128;  // per wavefront: 20 KiB of prepared x, 80 KiB per workgroup
+constexpr uint32_t kMaxLdsBlocks = 112;  // per wavefront: 17.5 KiB of prepared x, 70 KiB per workgroup (two fit a CU)
 constexpr uint32_t kMinLdsTasks = 8;     // tasks per wavefront below which x is prepared once, globally
 
 // Resident workgroups per CU for a kernel and its dynamic LDS (cached per LDS size).
