@@ -177,6 +177,31 @@ hipError_t launch_gemv(hipStream_t s, fh_kind kind, const uint8_t *qs, const uin
 hipError_t launch_gemv_group(hipStream_t s, fh_kind kind, const GemvDesc *descs, const uint32_t *map,
                              uint32_t count, uint32_t tasks, uint32_t max_nb, int cus);
 
+// rows.hip: few-row products (2 <= rows <= kRowsMax)
+constexpr size_t kRowsMax = 64;
+struct RowsDesc {          // one few-row product, as the kernels read it
+    const uint8_t *qs;     // quant plane
+    const uint16_t *ds;    // scale plane
+    const float *x;        // rows x k
+    _Float16 *xs;          // rows_xsplit_bytes(rows, k) bytes: x split into f16 parts
+    float *y;              // rows x n
+    uint32_t nb;           // blocks per row (k / 32)
+    uint32_t n;            // outputs per row
+    uint32_t m;            // rows
+    uint32_t task0;        // first task of this product in its launch (rows_tasks)
+};
+bool rows_supported(size_t rows, size_t k, size_t n);
+size_t rows_xsplit_bytes(size_t rows, size_t k);
+// Tasks of a product of n outputs in a launch whose products have at most max_m rows.
+uint32_t rows_tasks(size_t n, size_t max_m);
+// Two launches: split x into `xsplit`, then the product.
+hipError_t launch_rows(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x, float *y,
+                       size_t rows, size_t k, size_t n, void *xsplit, int cus);
+// Many products of one format: descs and map (device memory) as for launch_gemv_group; max_m the
+// most rows of any product, max_items the largest rows * k / 32.
+hipError_t launch_rows_group(hipStream_t s, fh_kind kind, const RowsDesc *descs, const uint32_t *map, uint32_t count,
+                             uint32_t tasks, uint32_t max_m, uint32_t max_items, int cus);
+
 // A K-split product left unreduced for its consumer: y(r, c) = the sum over s < splits of
 // part[s * rows * n + r * n + c], added in split order (the reduction kernel's order, so a
 // consumer that sums them reproduces the reduced product bit for bit). splits == 1: part is y.

@@ -656,6 +656,7 @@ fh_path fh_choose(size_t rows, fh_kind kind, size_t k, size_t n) {
     (void)n;
     if (ext_kind(kind)) return rows == 1 ? FH_PATH_GEMV : FH_PATH_TILED;
     if (rows == 1 && kind_ok(kind) && gemv_supported(kind, k, n)) return FH_PATH_GEMV;
+    if (rows >= 2 && rows <= kRowsMax && kind_ok(kind) && rows_supported(rows, k, n)) return FH_PATH_ROWS;
     return FH_PATH_TILED;
 }
 
@@ -694,6 +695,18 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
         if ((st = command_scratch(dev, fixed, gemv_prep_bytes(w->k), &prep))) return st;
         if ((st = begin_command(dev, "linear_q"))) return st;
         (void)launch_gemv(dev->stream, w->kind, w->qs, w->ds, x, y, w->k, w->n, prep, dev->cus);
+        return end_command(dev, "linear_q");
+    }
+    case FH_PATH_ROWS: {
+        if (rows > kRowsMax)
+            return fail(FH_ERR_INVALID, "the few-row kernel takes 1 to %zu rows, not %zu", kRowsMax, rows);
+        if (rows && !rows_supported(rows, w->k, w->n))
+            return fail(FH_ERR_INVALID, "the few-row kernel's 32-bit offsets do not cover %zu rows of a %zu x %zu weight",
+                        rows, w->n, w->k);
+        void *xs = nullptr;
+        if (rows && (st = command_scratch(dev, fixed, rows_xsplit_bytes(rows, w->k), &xs))) return st;
+        if ((st = begin_command(dev, "linear_q"))) return st;
+        if (rows) (void)launch_rows(dev->stream, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, xs, dev->cus);
         return end_command(dev, "linear_q");
     }
     case FH_PATH_NAIVE:
@@ -893,6 +906,126 @@ void fh_gemv_plan_free(fh_gemv_plan *plan) {
     fh_device *dev = plan->dev;
     if (plan->descs) free_bytes(dev, plan->descs);
     if (plan->prep) free_bytes(dev, plan->prep);
+    if (plan->map) free_bytes(dev, plan->map);
+    delete plan;
+    dev_release(dev);
+}
+
+// ---- grouped few-row products ----
+
+struct fh_rows_plan {
+    fh_device *dev = nullptr;
+    struct Launch {
+        fh_kind kind;
+        size_t first, count;  // descriptors
+        size_t map0;          // first entry of the launch's task -> product map
+        uint32_t tasks, max_m, max_items;
+    };
+    std::vector<Launch> launches;
+    RowsDesc *descs = nullptr;  // device array
+    uint32_t *map = nullptr;    // device array: per launch, the product of each task
+    _Float16 *xs = nullptr;     // split x of every product
+    uint64_t bytes = 0;
+};
+
+fh_status fh_rows_plan_create(fh_device *dev, const fh_rows_problem *problems, size_t count, fh_rows_plan **out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!out || (count && !problems)) return fail(FH_ERR_INVALID, "rows plan: null argument");
+    fh_rows_plan *plan = new (std::nothrow) fh_rows_plan;
+    if (!plan) return fail(FH_ERR_OOM, "host out of memory");
+    dev_retain(dev);
+    plan->dev = dev;
+    for (size_t i = 0; i < count; i++) {
+        const fh_rows_problem &p = problems[i];
+        const char *why = !p.w || !p.x || !p.y ? "has a null pointer"
+                          : !kind_ok(p.w->kind) ? "is not a Q8_0 or Q4_0 weight"
+                          : p.rows < 1 || p.rows > kRowsMax ? "needs 1 to 64 rows"
+                          : !rows_supported(p.rows, p.w->k, p.w->n) ? "is too large for one product"
+                                                                    : nullptr;
+        if (why) {
+            fh_rows_plan_free(plan);
+            return fail(FH_ERR_INVALID, "rows plan: problem %zu %s", i, why);
+        }
+    }
+    if (count > 65535) {
+        fh_rows_plan_free(plan);
+        return fail(FH_ERR_INVALID, "rows plan: %zu products, at most 65535 per plan", count);
+    }
+    std::vector<RowsDesc> host;
+    std::vector<uint32_t> map;
+    std::vector<size_t> xs_off;
+    size_t xs_bytes = 0;
+    for (int kind : {FH_Q8_0, FH_Q4_0}) {
+        fh_rows_plan::Launch L{(fh_kind)kind, host.size(), 0, map.size(), 0, 0, 0};
+        for (size_t i = 0; i < count; i++)  // the launch's tile shape follows its largest row count
+            if ((int)problems[i].w->kind == kind) L.max_m = std::max<uint32_t>(L.max_m, (uint32_t)problems[i].rows);
+        for (size_t i = 0; i < count; i++) {
+            const fh_rows_problem &p = problems[i];
+            if ((int)p.w->kind != kind) continue;
+            const uint32_t nb = (uint32_t)(p.w->k / QK), tasks = rows_tasks(p.w->n, L.max_m);
+            const uint64_t t = (uint64_t)L.tasks + tasks;
+            if (t >= (1ull << 31)) {
+                fh_rows_plan_free(plan);
+                return fail(FH_ERR_INVALID, "rows plan: too many rows in one launch");
+            }
+            host.push_back(RowsDesc{p.w->qs, p.w->ds, p.x, nullptr, p.y, nb, (uint32_t)p.w->n, (uint32_t)p.rows, L.tasks});
+            map.insert(map.end(), tasks, (uint32_t)L.count);
+            L.tasks = (uint32_t)t;
+            L.max_items = std::max<uint32_t>(L.max_items, (uint32_t)(p.rows * nb));
+            xs_off.push_back(xs_bytes);
+            xs_bytes += (rows_xsplit_bytes(p.rows, p.w->k) + 255) / 256 * 256;
+            plan->bytes += p.w->nbytes + 4ull * p.rows * (p.w->k + p.w->n);
+            L.count++;
+        }
+        if (L.count) plan->launches.push_back(L);
+    }
+    if (!host.empty()) {
+        void *p = nullptr;
+        if ((st = alloc_bytes(dev, xs_bytes, &p))) {
+            fh_rows_plan_free(plan);
+            return st;
+        }
+        plan->xs = (_Float16 *)p;
+        for (size_t i = 0; i < host.size(); i++) host[i].xs = (_Float16 *)((uint8_t *)plan->xs + xs_off[i]);
+        if ((st = alloc_bytes(dev, host.size() * sizeof(RowsDesc), &p)) == FH_OK) {
+            plan->descs = (RowsDesc *)p;
+            st = upload_bytes(dev, p, host.data(), host.size() * sizeof(RowsDesc), "rows plan");
+        }
+        if (st == FH_OK && (st = alloc_bytes(dev, map.size() * sizeof(uint32_t), &p)) == FH_OK) {
+            plan->map = (uint32_t *)p;
+            st = upload_bytes(dev, p, map.data(), map.size() * sizeof(uint32_t), "rows plan");
+        }
+        if (st) {
+            fh_rows_plan_free(plan);
+            return st;
+        }
+    }
+    *out = plan;
+    return FH_OK;
+}
+
+fh_status fh_rows_plan_run(fh_device *dev, const fh_rows_plan *plan) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!plan || plan->dev != dev) return fail(FH_ERR_INVALID, "rows plan: wrong device");
+    for (const auto &L : plan->launches) {
+        if ((st = begin_command(dev, "rows plan"))) return st;
+        (void)launch_rows_group(dev->stream, L.kind, plan->descs + L.first, plan->map + L.map0, (uint32_t)L.count,
+                                L.tasks, L.max_m, L.max_items, dev->cus);
+        if ((st = end_command(dev, "rows plan"))) return st;
+    }
+    return FH_OK;
+}
+
+size_t fh_rows_plan_launches(const fh_rows_plan *plan) { return plan ? plan->launches.size() : 0; }
+uint64_t fh_rows_plan_bytes(const fh_rows_plan *plan) { return plan ? plan->bytes : 0; }
+
+void fh_rows_plan_free(fh_rows_plan *plan) {
+    if (!plan) return;
+    fh_device *dev = plan->dev;
+    if (plan->descs) free_bytes(dev, plan->descs);
+    if (plan->xs) free_bytes(dev, plan->xs);
     if (plan->map) free_bytes(dev, plan->map);
     delete plan;
     dev_release(dev);

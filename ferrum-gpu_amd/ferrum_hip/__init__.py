@@ -62,13 +62,15 @@ class QPath(enum.IntEnum):
     reference's 1e-5); TiledFast (no counterpart in the reference) is the scoring GEMM with an fp8
     correction, within the MFMA-GEMM tolerance |g - w| <= 1e-3 + 2e-3 |w|; TiledF16 (no
     counterpart either) dequantises the weights to f16 and runs plain f16 MFMA, within the same
-    tolerance."""
+    tolerance; Rows (no counterpart either) is the few-row kernel for 1 to 64 rows, within the
+    reference's 1e-5."""
     Auto = 0
     Naive = 1
     Gemv = 2
     Tiled = 3
     TiledFast = 4
     TiledF16 = 5
+    Rows = 6
 
 
 _lib = None
@@ -130,6 +132,11 @@ def lib() -> ctypes.CDLL:
         "fh_gemv_plan_launches": (S, [P]),
         "fh_gemv_plan_bytes": (U64, [P]),
         "fh_gemv_plan_free": (None, [P]),
+        "fh_rows_plan_create": (I, [P, P, S, PP]),
+        "fh_rows_plan_run": (I, [P, P]),
+        "fh_rows_plan_launches": (S, [P]),
+        "fh_rows_plan_bytes": (U64, [P]),
+        "fh_rows_plan_free": (None, [P]),
         "fh_q8_snap_rows": (I, [P, P, P, S]),
         "fh_q8_snap_cols": (I, [P, P, P, S, S]),
         "fh_ggml_nbytes": (I, [U32, U64, ctypes.POINTER(U64)]),
@@ -515,6 +522,47 @@ class GemvPlan:
     def free(self) -> None:
         if self._h:
             lib().fh_gemv_plan_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class _RowsProblem(ctypes.Structure):
+    _fields_ = [("w", ctypes.c_void_p), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p), ("rows", ctypes.c_size_t)]
+
+
+class RowsPlan:
+    """Many independent few-row products (1 to 64 rows each) in one launch pair per block format,
+    on the QPath.Rows kernel; no counterpart in the reference (which issues one linear_q per
+    matrix). problems: (weight, x device pointer, y device pointer, rows)."""
+
+    def __init__(self, gpu: Gpu, problems: Sequence[tuple[QWeight, int, int, int]]):
+        arr = (_RowsProblem * max(len(problems), 1))()
+        for i, (w, xp, yp, rows) in enumerate(problems):
+            arr[i] = _RowsProblem(w.handle.value if hasattr(w.handle, "value") else w.handle, xp, yp, rows)
+        self._keep = [p[0] for p in problems]
+        self.gpu = gpu
+        h = ctypes.c_void_p()
+        _check(lib().fh_rows_plan_create(gpu.handle, ctypes.cast(arr, ctypes.c_void_p), len(problems),
+                                         ctypes.byref(h)))
+        self._h = h
+
+    def run(self) -> None:
+        _check(lib().fh_rows_plan_run(self.gpu.handle, self._h))
+
+    def launches(self) -> int:
+        return lib().fh_rows_plan_launches(self._h)
+
+    def bytes(self) -> int:
+        return lib().fh_rows_plan_bytes(self._h)
+
+    def free(self) -> None:
+        if self._h:
+            lib().fh_rows_plan_free(self._h)
             self._h = None
 
     def __del__(self):

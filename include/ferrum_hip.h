@@ -83,14 +83,17 @@ typedef enum fh_kind {
  * the MFMA-GEMM tolerance |g - w| <= 1e-3 + 2e-3 |w|, about 5e-5 absolute at the scoring shapes);
  * TILED_F16 = the dequant-f16 GEMM (weights dequantised to f16 d*q in LDS, x as f16 with a
  * power-of-two row scale, plain f16 MFMA with f32 accumulation; each product rounds both operands
- * to f16, so |g - w| <= 2^-10 sum_k |x_k w_k| roughly, within the MFMA-GEMM tolerance). */
+ * to f16, so |g - w| <= 2^-10 sum_k |x_k w_k| roughly, within the MFMA-GEMM tolerance);
+ * ROWS = the few-row kernel for 2..64 rows (the weights streamed once from HBM into registers for
+ * every row, x carried to about 22 bits as TILED does; within the reference's 1e-5). */
 typedef enum fh_path {
     FH_PATH_AUTO = 0,
     FH_PATH_NAIVE = 1,
     FH_PATH_GEMV = 2,
     FH_PATH_TILED = 3,
     FH_PATH_TILED_FAST = 4,
-    FH_PATH_TILED_F16 = 5
+    FH_PATH_TILED_F16 = 5,
+    FH_PATH_ROWS = 6
 } fh_path;
 
 typedef struct fh_device fh_device;   /* replaces ferrum_wgpu::device::Gpu */
@@ -218,6 +221,26 @@ FH_API fh_status fh_gemv_plan_run(fh_device *dev, const fh_gemv_plan *plan);
 FH_API size_t fh_gemv_plan_launches(const fh_gemv_plan *plan);
 FH_API uint64_t fh_gemv_plan_bytes(const fh_gemv_plan *plan);
 FH_API void fh_gemv_plan_free(fh_gemv_plan *plan);
+
+/* No counterpart in the reference: one launch pair for many independent few-row products
+ * y_i = x_i * W_i, x_i of rows_i x k_i and y_i of rows_i x n_i floats (device pointers), rows_i in
+ * 1..64, on the FH_PATH_ROWS kernel (the reference issues one linear_q per matrix,
+ * ferrum_wgpu/src/ops/quant.rs:326-381). Built once, run any number of times; products with the
+ * same block format share a launch (two kernels: x split, then the products). Q8_0 and Q4_0 only. */
+typedef struct fh_rows_plan fh_rows_plan;
+typedef struct fh_rows_problem {
+    const fh_qweight *w;
+    const float *x;
+    float *y;
+    size_t rows;
+} fh_rows_problem;
+FH_API fh_status fh_rows_plan_create(fh_device *dev, const fh_rows_problem *problems, size_t count,
+                                     fh_rows_plan **out);
+FH_API fh_status fh_rows_plan_run(fh_device *dev, const fh_rows_plan *plan);
+FH_API size_t fh_rows_plan_launches(const fh_rows_plan *plan);
+/* Algorithmic bytes one run moves: the packed weights, x and y of every product. */
+FH_API uint64_t fh_rows_plan_bytes(const fh_rows_plan *plan);
+FH_API void fh_rows_plan_free(fh_rows_plan *plan);
 
 /* ---- quantisation-aware training snap (ferrum_wgpu/src/ops/qat.rs:21-57) ---- */
 /* q8_snap_rows: snap src into dst along rows (blocks of 32 consecutive values). ne0 not a

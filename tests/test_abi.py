@@ -54,8 +54,8 @@ def test_abi_version_and_host_side_helpers(fh):
 
 def test_choose_rules(fh):
     """The MI355X dispatch (replaces quant.rs:306-323, which was measured on MX330/Xe):
-    one row -> the int8-MFMA GEMV while its 32-bit offsets cover a row (k <= 2^25); otherwise
-    the MFMA GEMM."""
+    one row -> the int8-MFMA GEMV while its 32-bit offsets cover a row (k <= 2^25); 2 to 64 rows
+    -> the few-row kernel (weights streamed once for every row); more rows -> the MFMA GEMM."""
     Q8, Q4 = fh.QKind.Q8_0, fh.QKind.Q4_0
     for kind in (Q8, Q4):
         assert fh.choose(1, kind, 768, 2304) == fh.QPath.Gemv
@@ -64,7 +64,10 @@ def test_choose_rules(fh):
         assert fh.choose(1, kind, 8192 + 32, 64) == fh.QPath.Gemv
         assert fh.choose(1, kind, 2**25, 151936) == fh.QPath.Gemv
         assert fh.choose(1, kind, 2**25 + 32, 8) == fh.QPath.Tiled
-        assert fh.choose(2, kind, 768, 2304) == fh.QPath.Tiled
+        assert fh.choose(2, kind, 768, 2304) == fh.QPath.Rows
+        assert fh.choose(8, kind, 5632, 2048) == fh.QPath.Rows
+        assert fh.choose(64, kind, 2048, 11264) == fh.QPath.Rows
+        assert fh.choose(65, kind, 2048, 2048) == fh.QPath.Tiled
         assert fh.choose(512, kind, 896, 4864) == fh.QPath.Tiled
 
 

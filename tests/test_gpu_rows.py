@@ -1,0 +1,201 @@
+"""The few-row kernel (QPath.Rows, 1 to 64 rows; no counterpart in the reference, which sends
+these products to its naive or tiled kernels by ferrum_wgpu/src/ops/quant.rs:306-323) and its
+grouped launches (RowsPlan), through the C ABI, against the CPU oracle (ferrum_ref's matmul on the
+dequantised weights).
+
+Bars (written here): max_rel_err < 1e-5 against the CPU product (REDUCING,
+ferrum_wgpu/src/tolerance.rs:7) on uniform weights (as the reference's product tests draw them) and
+activation outliers; on the reference's awkward codec weights (ferrum_wgpu/src/ops/quant/
+tests.rs:11-23) the summation error bound of the test below; the identity read-back equals
+the dequantised weights (f32 ==, as the reference compares); a grouped launch gives each product the bits of its single
+launch; where the CPU's own f32 error grows (k = 5632), the device is held to the CPU's distance
+from the float64 product."""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+REDUCING = 1e-5
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def fh():
+    import ferrum_hip
+
+    return ferrum_hip
+
+
+@pytest.fixture(scope="module")
+def g(fh):
+    gpu = fh.Gpu.open_for_test()
+    if gpu is None:
+        pytest.skip("no gfx950 device")
+    yield gpu
+    gpu.close()
+
+
+def nasty(orc, n, seed=9):
+    """ferrum_wgpu/src/ops/quant/tests.rs:11-23"""
+    v = orc.rand_vec(n, seed) * np.float32(3.0)
+    i = np.arange(n)
+    sel = (i // 32) % 7
+    v = np.where(sel == 0, v * np.float32(1e-6), v)
+    v = np.where(sel == 1, np.float32(0), v)
+    v = np.where(sel == 2, v * np.float32(1e4), v)
+    v = np.where(sel == 3, (i % 9).astype(np.float32) - np.float32(4), v)
+    return v.astype(np.float32)
+
+
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def cpu(orc, kind, b, x, m, k, n):
+    w = orc.dequantised_in_out(int(kind), b, k, n)
+    return orc.matmul_tuned(x, w, m, k, n, THREADS) if m * k * n > 2e7 else orc.matmul(x, w, m, k, n)
+
+
+@pytest.mark.parametrize("kind_name", ["Q8_0", "Q4_0"])
+def test_rows_kernel_matches_the_cpu_on_awkward_shapes(fh, g, orc, kind_name):
+    """ops/quant/tests.rs:134-157, 272-304 (uniform weights and x, as the reference's product tests
+    draw them) at row counts across the tile shapes (1 .. 32 one x tile, 33 .. 64 two), widths
+    whose block count is not a multiple of the four-block batch, outputs that are not whole tiles
+    or tasks. Beyond k = 512 (the reference's widest shape under its 1e-5) and on the reference's
+    awkward codec weights (blocks scaled by 1e-6, 0, 1e4, small integers) the CPU's own f32 sums
+    leave the float64 product by 1e-5 to 5e-3, and which of two
+    summation orders lands closer varies from case to case; there every output is held to the
+    summation error bound of any order, |g - exact| <= (k + 8) 2^-24 sum_k |x_k w_k| (k + 2
+    roundings of f32 sums and scalings, and x's two f16 parts, 2^-22 relative), which the CPU's
+    product meets too; a dropped or misplaced term moves an output by |x_k w_k|, far beyond it."""
+    kind = fh.QKind[kind_name]
+    for k, n in [(32, 1), (64, 7), (96, 40), (160, 300), (288, 257), (1024, 513)]:
+        for weights in ("uniform", "awkward"):
+            w = orc.rand_vec(k * n, 6) if weights == "uniform" else nasty(orc, k * n)
+            b = orc.quantise_matrix(int(kind), w, k, n)
+            wd = orc.dequantised_in_out(int(kind), b, k, n)
+            qw = fh.upload_qweight(g, kind, b, k, n)
+            for m in (1, 2, 3, 8, 17, 32, 33, 64):
+                x = orc.rand_vec(m * k, 100 + m)
+                want = cpu(orc, kind, b, x, m, k, n)
+                gx, gy = g.upload(x), g.zeros(m * n)
+                fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.Rows)
+                got = g.read(gy)
+                if weights == "uniform" and k <= 512:  # the reference's 1e-5 holds its shapes
+                    e = orc.max_rel_err(got, want)
+                    assert e < REDUCING, (kind_name, m, k, n, e)
+                else:
+                    x64, w64 = x.reshape(m, k).astype(np.float64), wd.reshape(k, n).astype(np.float64)
+                    ex = (x64 @ w64).reshape(-1)
+                    bound = (k + 8) * 2.0**-24 * (np.abs(x64) @ np.abs(w64)).reshape(-1)
+                    assert np.all(np.abs(want - ex) <= bound), (kind_name, m, k, n, "cpu")
+                    r = float(np.max(np.abs(got - ex) / np.maximum(bound, 1e-38)))
+                    assert r <= 1.0, (kind_name, m, k, n, r)
+        say(f"{kind_name} {k}x{n}: rows 1..64 within their bars")
+
+
+@pytest.mark.parametrize("kind_name", ["Q8_0", "Q4_0"])
+def test_rows_identity_reads_back_the_dequantised_weights(fh, g, orc, kind_name):
+    """ops/quant/tests.rs:107-131 on the few-row kernel: x = identity gives the dequantised weights,
+    compared with f32 == as the reference does (an all-zero Q4_0 block stores the scale -0.0, whose
+    decoded zeros are -0.0 on the CPU and +0.0 as sums)."""
+    kind = fh.QKind[kind_name]
+    for k, n in [(32, 5), (64, 65), (64, 300)]:
+        b = orc.quantise_matrix(int(kind), nasty(orc, k * n), k, n)
+        want = orc.dequantised_in_out(int(kind), b, k, n)
+        qw = fh.upload_qweight(g, kind, b, k, n)
+        gx, gy = g.upload(np.eye(k, dtype=np.float32)), g.zeros(k * n)
+        fh.linear_q_with(g, gx, qw, gy, k, fh.QPath.Rows)
+        assert np.array_equal(g.read(gy), want), (kind_name, k, n)
+
+
+LLAMA1B = [(2048, 2560), (2048, 2048), (2048, 11264), (5632, 2048)]
+
+
+@pytest.mark.parametrize("kind_name", ["Q8_0", "Q4_0"])
+@pytest.mark.parametrize("m", [8, 64])
+def test_rows_kernel_at_the_tinyllama_shapes(fh, g, orc, kind_name, m):
+    """Config 5's few-row products (M = 8, 64) at the TinyLlama-1.1B layer shapes, x ~ N(0, 1),
+    W ~ N(0, 0.02), through AUTO (which picks the few-row kernel)."""
+    kind = fh.QKind[kind_name]
+    rng = np.random.default_rng(5 + m)
+    for k, n in LLAMA1B:
+        assert fh.choose(m, kind, k, n) == fh.QPath.Rows
+        w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+        x = rng.standard_normal(m * k).astype(np.float32)
+        b = orc.quantise_matrix(int(kind), w, k, n)
+        wd = orc.dequantised_in_out(int(kind), b, k, n)
+        want = orc.matmul_tuned(x, wd, m, k, n, THREADS)
+        qw = fh.upload_qweight(g, kind, b, k, n)
+        gx, gy = g.upload(x), g.zeros(m * n)
+        fh.linear_q(g, gx, qw, gy, m)
+        got = g.read(gy)
+        e = orc.max_rel_err(got, want)
+        exact = (x.reshape(m, k).astype(np.float64) @ wd.reshape(k, n).astype(np.float64)).reshape(-1)
+        e_cpu, e_dev = orc.max_rel_err(want, exact.astype(np.float32)), orc.max_rel_err(got, exact.astype(np.float32))
+        say(f"{kind_name} M={m} {k}x{n}: vs CPU {e:.2e}; vs float64: device {e_dev:.2e}, CPU {e_cpu:.2e}")
+        assert e < REDUCING or e_dev <= e_cpu, (k, n, e, e_dev, e_cpu)
+
+
+def test_rows_kernel_keeps_the_neighbours_of_outliers(fh, g, orc):
+    """x carried per element as two f16 parts: an outlier of 1e4 beside small values over zero
+    weights leaves the product within 1e-5."""
+    k, n, m = 896, 1152, 8
+    rng = np.random.default_rng(3)
+    for kind in (fh.QKind.Q8_0, fh.QKind.Q4_0):
+        w = (rng.standard_normal(k * n) * 0.02).astype(np.float32).reshape(k, n)
+        x = rng.standard_normal(m * k).astype(np.float32).reshape(m, k)
+        x[:, [3, 17, 450]] *= np.float32(1e4)
+        w[[3, 17, 450], :] = 0.0
+        b = orc.quantise_matrix(int(kind), w.reshape(-1), k, n)
+        want = cpu(orc, kind, b, x.reshape(-1), m, k, n)
+        qw = fh.upload_qweight(g, kind, b, k, n)
+        gx, gy = g.upload(x), g.zeros(m * n)
+        fh.linear_q(g, gx, qw, gy, m)
+        assert orc.max_rel_err(g.read(gy), want) < REDUCING
+
+
+def test_rows_plan_gives_each_product_its_single_launch_bits(fh, g, orc):
+    """One plan over products of both formats, mixed row counts (one and two x tiles in one launch)
+    and ragged shapes; every product equals its single QPath.Rows launch bit for bit."""
+    rng = np.random.default_rng(11)
+    probs, keep, checks = [], [], []
+    for i, (kind, m, k, n) in enumerate([(fh.QKind.Q4_0, 8, 2048, 2560), (fh.QKind.Q4_0, 40, 896, 300),
+                                         (fh.QKind.Q8_0, 2, 768, 2304), (fh.QKind.Q4_0, 64, 160, 33),
+                                         (fh.QKind.Q8_0, 33, 5632, 257), (fh.QKind.Q8_0, 5, 64, 7)]):
+        w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+        x = rng.standard_normal(m * k).astype(np.float32)
+        b = orc.quantise_matrix(int(kind), w, k, n)
+        qw = fh.upload_qweight(g, kind, b, k, n)
+        gx, gy, gs = g.upload(x), g.zeros(m * n), g.zeros(m * n)
+        fh.linear_q_with(g, gx, qw, gs, m, fh.QPath.Rows)
+        keep += [qw, gx, gy, gs]
+        probs.append((qw, gx.device_ptr(), gy.device_ptr(), m))
+        checks.append((gy, gs, cpu(orc, kind, b, x, m, k, n)))
+    plan = fh.RowsPlan(g, probs)
+    assert plan.launches() == 2
+    for rep in range(2):
+        plan.run()
+        for gy, gs, want in checks:
+            got = g.read(gy)
+            assert np.array_equal(got.view(np.uint32), g.read(gs).view(np.uint32)), rep
+            assert orc.max_rel_err(got, want) < REDUCING
+    plan.free()
+
+
+def test_rows_refusals(fh, g, orc):
+    qw = fh.upload_quantised(g, fh.QKind.Q4_0, orc.rand_vec(64 * 32, 1), 64, 32)
+    gx, gy = g.upload(orc.rand_vec(65 * 64, 2)), g.zeros(65 * 32)
+    with pytest.raises(fh.GpuError, match="1 to 64 rows"):
+        fh.linear_q_with(g, gx, qw, gy, 65, fh.QPath.Rows)
+    with pytest.raises(fh.GpuError, match="needs 1 to 64 rows"):
+        fh.RowsPlan(g, [(qw, gx.device_ptr(), gy.device_ptr(), 65)])
+    fw = fh.upload_quantised(g, fh.QKind.F16, orc.rand_vec(64 * 32, 1), 64, 32)
+    with pytest.raises(fh.GpuError, match="Q8_0 or Q4_0"):
+        fh.RowsPlan(g, [(fw, gx.device_ptr(), gy.device_ptr(), 4)])
+    # the device still works
+    fh.linear_q_ptr(g, gx.device_ptr(), qw, gy.device_ptr(), 64, fh.QPath.Rows)
