@@ -224,6 +224,42 @@ def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0, path=None, copies=1):
             "bytes_per_step": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9}
 
 
+def bench_rows_pool(fh, g, ev, kind, m, shapes, steps, copies=12, seed=0):
+    """Config 5's few-row products as one grouped launch pair (RowsPlan: x split, then the
+    few-row kernel over every product): `copies` distinct copies of `shapes` (12 copies of the
+    TinyLlama-1.1B products hold about 300 MB of Q4_0 weights, more than the 256 MB last-level
+    cache). One step = one run of the plan; algorithmic bytes = packed weights + x + y."""
+    rng = np.random.default_rng(seed)
+    keep, probs = [], []
+    for k, n in shapes:
+        w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+        packed = fh.upload_quantised(g, kind, w, k, n).read_gguf()
+        for _ in range(copies):
+            qw = fh.upload_qweight(g, kind, packed, k, n)
+            gx = g.upload(rng.standard_normal(m * k).astype(np.float32))
+            gy = g.zeros(m * n)
+            keep += [qw, gx, gy]
+            probs.append((qw, gx.device_ptr(), gy.device_ptr(), m))
+    plan = fh.RowsPlan(g, probs)
+    prewarm(g, plan.run)
+    e0, e1 = ev.create(2)
+    ev.record(e0)
+    for _ in range(steps):
+        plan.run()
+    ev.record(e1)
+    g.sync()
+    ms = ev.ms(e0, e1) / steps
+    ev.destroy([e0, e1])
+    nbytes = plan.bytes()
+    wbytes = copies * sum((k // 32) * n * kind.file_bytes() for k, n in shapes)
+    flops = copies * sum(2 * m * k * n for k, n in shapes)
+    launches = plan.launches()
+    plan.free()
+    return {"m": m, "ms_per_step": ms, "bytes_per_step": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9,
+            "weight_gbs": wbytes / (ms * 1e-3) / 1e9, "tflops": flops / (ms * 1e-3) / 1e12,
+            "products": len(probs), "launches": launches}
+
+
 def bench_copy(g, ev, nbytes=512 * 2**20, reps=10):
     """A plain device copy (Gpu::copy_f32, one 16-byte-vector kernel) of a known size: the
     measured HBM ceiling for a read+write stream, and the known-size dispatch that calibrates the
@@ -463,15 +499,21 @@ def main():
                                                   "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                                                   "ms_per_step": r["ms_per_step"],
                                                   "flops_per_step": r["flops_per_step"]}
-        # config 5's small M (HBM-bound): the library's own path choice, 12 distinct copies of the
-        # four products (about 300 MB of Q4_0 weights, more than the 256 MB last-level cache)
+        # config 5's small M (HBM-bound): 12 distinct copies of the four products (about 300 MB of
+        # Q4_0 weights, more than the 256 MB last-level cache), as one grouped launch of the few-row
+        # kernel, and as one linear_q per product with the library's own path choice
         for kind, tag in ((fh.QKind.Q4_0, "q4_0"), (fh.QKind.Q8_0, "q8_0")):
             for m in (8, 64):
-                r = bench_gemm(fh, g, ev, kind, m, LLAMA1B_SHAPES, 10, path=fh.QPath.Auto, copies=12)
-                log(f"{tag} small-M products M={m}:", r)
-                extra[f"{tag}_gemm_llama1b_m{m}"] = {"gbs": round(r["gbs"], 2), "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
-                                                     "tflops": round(r["tflops"], 2), "ms_per_step": r["ms_per_step"],
-                                                     "bytes_per_step": r["bytes_per_step"], "path": "auto"}
+                r = bench_rows_pool(fh, g, ev, kind, m, LLAMA1B_SHAPES, 20)
+                log(f"{tag} few-row products M={m}, grouped:", r)
+                r1 = bench_gemm(fh, g, ev, kind, m, LLAMA1B_SHAPES, 10, path=fh.QPath.Auto, copies=12)
+                log(f"{tag} few-row products M={m}, one linear_q each:", r1)
+                extra[f"{tag}_gemm_llama1b_m{m}"] = {
+                    "gbs": round(r["gbs"], 2), "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                    "weight_gbs": round(r["weight_gbs"], 2), "tflops": round(r["tflops"], 2),
+                    "ms_per_step": r["ms_per_step"], "bytes_per_step": r["bytes_per_step"],
+                    "path": "rows plan (QPath.Rows), one launch pair for 48 products",
+                    "single_calls_gbs": round(r1["gbs"], 2), "single_calls_ms_per_step": r1["ms_per_step"]}
         sc = bench_scoring(fh, g, ev, cpu=not a.no_cpu)
         log("Qwen2-0.5B Q4_0 scoring:", sc)
         extra["qwen2_0_5b_q4_0_scoring"] = sc

@@ -192,8 +192,8 @@ struct RowsDesc {          // one few-row product, as the kernels read it
 };
 bool rows_supported(size_t rows, size_t k, size_t n);
 size_t rows_xsplit_bytes(size_t rows, size_t k);
-// Tasks of a product of n outputs in a launch whose products have at most max_m rows.
-uint32_t rows_tasks(size_t n, size_t max_m);
+// Tasks of a product of k inputs and n outputs in a launch whose products have at most max_m rows.
+uint32_t rows_tasks(size_t n, size_t k, size_t max_m);
 // Two launches: split x into `xsplit`, then the product.
 hipError_t launch_rows(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x, float *y,
                        size_t rows, size_t k, size_t n, void *xsplit, int cus);

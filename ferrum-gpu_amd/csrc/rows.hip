@@ -21,8 +21,13 @@
 // 16 h + 8 s + perm[j] (lane half h holds bytes 16h .. 16h + 15, step s the 8 bytes at 16h + 8s).
 // perm is the order in which a dword unpacks into f16 pairs (bytes 0 and 2, then 1 and 3).
 //
-// Work: a task is 256 output rows (four wavefronts x two 32-row tiles; 128 rows, one tile per
-// wavefront, when M > 32) of one product over all of K, in batches of four blocks. Per batch the workgroup stages x's split rows for the batch in LDS
+// Work: a task is 128 output rows (four wavefronts x one 32-row tile) of one product over all of K,
+// or over one half of K for products of 64 blocks or more, in batches of four blocks. Small tasks
+// keep a launch's workgroups evenly loaded (with tasks of 256 rows over all of K, the four
+// TinyLlama products at M = 8 made 840 tasks for 768 resident workgroups, and the 72 that ran a
+// second task set the launch's length). The two halves of K add their partial sums atomically
+// into y, zeroed by the split pass: f32 addition is commutative and the first add onto +0 is
+// exact, so the result does not depend on which half arrives first. Per batch the workgroup stages x's split rows for the batch in LDS
 // (double buffered, one barrier per batch) and every wavefront reads its A fragments from there,
 // while its own weights for the next batch are already in flight. Workgroups loop over the tasks.
 #include "device_common.hpp"
@@ -36,13 +41,22 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kKB = 4;     // blocks per batch (one LDS stage of x)
+// blocks per batch (one LDS stage of x): eight for up to 8 rows, else four (measured: eight
+// blocks take more registers, and from 16 rows on the lost occupancy costs more than the fewer
+// barriers save)
+__host__ __device__ constexpr int rows_kb(int R) { return R > 8 ? 4 : 8; }
 constexpr int kWaves = 4;  // wavefronts per workgroup
 constexpr int kXRec = 72;  // LDS halves per (x row, block): 32 hi + 32 lo + 8 pad
 
-// 32-row x tiles (MT) and 32-row weight tiles per wavefront (TW) for a launch whose products have
-// at most max_m rows
-__host__ __device__ constexpr int rows_tw(int mt) { return mt == 1 ? 2 : 1; }
+// A launch's row capacity R (8, 16, 32 or 64: its largest product's rows, rounded up) sets the
+// 32-row x tiles (MT), the weight tiles per wavefront (TW) and the accumulator groups of four
+// rows a lane keeps per tile (RG: x rows 8 g + 4 h + 0..3 for g < RG).
+__host__ __device__ constexpr int rows_cap(uint32_t max_m) { return max_m <= 8 ? 8 : max_m <= 16 ? 16 : max_m <= 32 ? 32 : 64; }
+__host__ __device__ constexpr int rows_mt(int R) { return R > 32 ? 2 : 1; }
+__host__ __device__ constexpr int rows_tw(int) { return 1; }
+// K halves of a product of nb blocks (see above)
+__host__ __device__ constexpr uint32_t rows_splits(uint32_t nb) { return nb >= 64 ? 2 : 1; }
+__host__ __device__ constexpr int rows_rg(int R) { return R >= 32 ? 4 : R / 8; }
 constexpr int kNonTemporal = 2;
 
 __host__ __device__ constexpr int rows_perm(int j) { return j < 4 ? (j == 1 ? 2 : j == 2 ? 1 : j) : 4 + rows_perm(j - 4); }
@@ -91,6 +105,9 @@ template <int KIND>
 __global__ __launch_bounds__(256) void rows_split_kernel(const RowsDesc *__restrict__ descs, RowsDesc one) {
     const RowsDesc d = uniform_desc(descs, blockIdx.y, one);
     const size_t items = (size_t)d.m * d.nb;
+    if (rows_splits(d.nb) > 1)  // the K halves add into y
+        for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < (size_t)d.m * d.n; i += (size_t)gridDim.x * 256)
+            d.y[i] = 0.0f;
     const int j = threadIdx.x % 8;
     for (size_t t = ((size_t)blockIdx.x * 256 + threadIdx.x) / 8; t < items; t += (size_t)gridDim.x * 32) {
         const float *src = d.x + t * 32;
@@ -123,22 +140,25 @@ __device__ __forceinline__ uint32_t q8_pair(uint32_t t, uint32_t sel) {
     return f16x2_add(__builtin_amdgcn_perm(0x64646464u, t, sel), (_Float16)-1152.0f);
 }
 
-template <int KIND, int TW>
+template <int KIND, int TW, int KB>
 struct RowsLoad {  // one lane's weights and scales for a batch
-    static constexpr int QL = KIND == FH_Q8_0 ? kKB : kKB / 2;  // 16-byte quant loads per tile
+    static constexpr int QL = KIND == FH_Q8_0 ? KB : KB / 2;  // 16-byte quant loads per tile
     u32x4 q[TW][QL];
-    u32x2 d[TW];  // the lane's row's four scales per tile
+    u32x4 d[TW];  // the lane's row's scales of the batch's blocks (KB halves) per tile
 };
 
-template <int KIND, int MT>
+template <int KIND, int R>
 __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict__ descs,
                                                       const uint32_t *__restrict__ map, RowsDesc one,
                                                       uint32_t tasks) {
-    constexpr int kTW = rows_tw(MT), kTaskRows = 32 * kTW * kWaves;
-    using L = RowsLoad<KIND, kTW>;
+    constexpr int MT = rows_mt(R), kTW = rows_tw(R), RG = rows_rg(R), kTaskRows = 32 * kTW * kWaves;
+    constexpr int kKB = rows_kb(R);
+    using L = RowsLoad<KIND, kTW, kKB>;
     constexpr int QB = KIND == FH_Q8_0 ? 32 : 16;  // quant bytes per block and row
-    constexpr int XCH = MT * 32 * kKB * 8 / 256;    // 16-byte x chunks each thread stages per batch
-    __shared__ __attribute__((aligned(16))) _Float16 sx[2][MT * 32 * kKB * kXRec];
+    constexpr int XCH = R * kKB * 8 / 256;          // 16-byte x chunks each thread stages per batch
+    // x rows of a batch in LDS, block by block (row stride 144 bytes: the eight lanes that read
+    // together hit distinct banks)
+    __shared__ __attribute__((aligned(16))) _Float16 sx[2][kKB * R * kXRec];
 
     const int tid = threadIdx.x, lane = tid % 64, r = lane % 32, h = lane / 32;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
@@ -150,8 +170,9 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
     for (uint32_t task = blockIdx.x; task < tasks; task += gridDim.x) {
         const uint32_t p = map ? map[task] : 0;
         const RowsDesc d = uniform_desc(descs, p, one);
-        const uint32_t nb = d.nb, nb8 = (nb + 7) / 8, groups = (d.n + 31) / 32;
-        const uint32_t g0 = (task - d.task0) * (kTaskRows / 32) + wave * kTW;  // this wavefront's first tile
+        const uint32_t nb = d.nb, nb8 = (nb + 7) / 8, groups = (d.n + 31) / 32, S = rows_splits(nb);
+        const uint32_t tl = task - d.task0, split = tl % S;
+        const uint32_t g0 = (tl / S) * (kTaskRows / 32) + wave * kTW;  // this wavefront's first tile
         __amdgpu_buffer_rsrc_t rq[kTW], rd[kTW];
 #pragma unroll
         for (int j = 0; j < kTW; j++) {
@@ -161,10 +182,12 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
             rd[j] = make_rsrc(d.ds + (size_t)(live ? g : 0) * nb8 * 256, live ? nb8 * 512 : 0);
         }
         const auto rx = make_rsrc(d.xs, d.m * nb * 128);
-        const uint32_t nbt = (nb + kKB - 1) / kKB;
+        // this task's batches: all of them, or one half of them
+        const uint32_t all_bt = (nb + kKB - 1) / kKB, half = (all_bt + S - 1) / S;
+        const uint32_t bt0 = split * half, nbt = min(all_bt, bt0 + half) - bt0;
 
         auto load_w = [&](L &ld, uint32_t bt) {
-            const uint32_t b = bt * kKB;
+            const uint32_t b = (bt0 + bt) * kKB;
 #pragma unroll
             for (int j = 0; j < kTW; j++) {
 #pragma unroll
@@ -173,15 +196,20 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
                     ld.q[j][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[j], (int)off, 0, kNonTemporal));
                 }
                 const uint32_t so = os + (b / 8) * 512 + (b % 8) * 2;
-                ld.d[j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rd[j], (int)so, 0, 0));
+                if constexpr (kKB == 8) {
+                    ld.d[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rd[j], (int)so, 0, 0));
+                } else {
+                    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rd[j], (int)so, 0, 0));
+                    ld.d[j] = u32x4{v[0], v[1], 0u, 0u};
+                }
             }
         };
-        // x chunks of a batch: chunk c = tid + 256 i is row c / 32, block (c / 8) % kKB, part c % 8
+        // x chunks of a batch: chunk c = tid + 256 i is block c / (8 R), row (c / 8) % R, part c % 8
         u32x4 xr[XCH];
         auto load_x = [&](uint32_t bt) {
 #pragma unroll
             for (int i = 0; i < XCH; i++) {
-                const uint32_t c = tid + 256 * i, m = c / 32, kb = bt * kKB + (c / 8) % kKB;
+                const uint32_t c = tid + 256 * i, m = (c / 8) % R, kb = (bt0 + bt) * kKB + c / (8 * R);
                 const bool ok = m < d.m && kb < nb;
                 xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                       rx, (int)(ok ? (m * nb + kb) * 128 + (c % 8) * 16 : 0x80000000u), 0, 0));
@@ -190,18 +218,20 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
         auto store_x = [&](int buf) {
 #pragma unroll
             for (int i = 0; i < XCH; i++) {
-                const uint32_t c = tid + 256 * i, m = c / 32, kb = (c / 8) % kKB;
-                *(u32x4 *)&sx[buf][(m * kKB + kb) * kXRec + (c % 8) * 8] = xr[i];
+                const uint32_t c = tid + 256 * i;
+                *(u32x4 *)&sx[buf][(c / 8) * kXRec + (c % 8) * 8] = xr[i];
             }
         };
 
-        f32x16 acc[MT][kTW];
+        // accumulators: tile (i, j), group g of four x rows (8 g + 4 h + 0..3 of x tile i)
+        f32x4 acc[MT][kTW][4];
 #pragma unroll
         for (int i = 0; i < MT; i++)
 #pragma unroll
             for (int j = 0; j < kTW; j++)
 #pragma unroll
-                for (int q = 0; q < 16; q++) acc[i][j][q] = 0.0f;
+                for (int q = 0; q < 4; q++) acc[i][j][q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        constexpr int G0 = RG;  // groups kept in x tile 0 (tile 1, when there is one, keeps all four)
 
         auto compute = [&](const L &ld, int buf) {
 #pragma unroll
@@ -237,9 +267,16 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
                 }
 #pragma unroll
                 for (int i = 0; i < MT; i++) {
-                    const _Float16 *row = &sx[buf][((i * 32 + r) * kKB + kb) * kXRec];
-                    const f16x8 a0 = *(const f16x8 *)(row + 8 * h), a1 = *(const f16x8 *)(row + 16 + 8 * h);
-                    const f16x8 l0 = *(const f16x8 *)(row + 32 + 8 * h), l1 = *(const f16x8 *)(row + 48 + 8 * h);
+                    // A fragments: x row i 32 + r (rows past the row capacity are zero)
+                    const int xr_row = i * 32 + r;
+                    f16x8 a0 = {}, a1 = {}, l0 = {}, l1 = {};
+                    if (R >= 32 || xr_row < R) {
+                        const _Float16 *row = &sx[buf][(kb * R + xr_row) * kXRec];
+                        a0 = *(const f16x8 *)(row + 8 * h);
+                        a1 = *(const f16x8 *)(row + 16 + 8 * h);
+                        l0 = *(const f16x8 *)(row + 32 + 8 * h);
+                        l1 = *(const f16x8 *)(row + 48 + 8 * h);
+                    }
 #pragma unroll
                     for (int j = 0; j < kTW; j++) {
                         f32x16 pp = {};
@@ -248,7 +285,9 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
                         pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(l0, bf[j][0], pp, 0, 0, 0);
                         pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(l1, bf[j][1], pp, 0, 0, 0);
 #pragma unroll
-                        for (int q = 0; q < 16; q++) acc[i][j][q] = fmaf(dv[j], pp[q], acc[i][j][q]);
+                        for (int g = 0; g < (i == 0 ? G0 : 4); g++)
+#pragma unroll
+                            for (int q = 0; q < 4; q++) acc[i][j][g][q] = fmaf(dv[j], pp[4 * g + q], acc[i][j][g][q]);
                     }
                 }
                 // one block at a time: the scale FMAs are not sunk past the next block's MFMAs
@@ -256,21 +295,26 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
 #pragma unroll
                 for (int i = 0; i < MT; i++)
 #pragma unroll
-                    for (int j = 0; j < kTW; j++) asm volatile("" : "+v"(acc[i][j]));
+                    for (int j = 0; j < kTW; j++)
+#pragma unroll
+                        for (int g = 0; g < (i == 0 ? G0 : 4); g++) asm volatile("" : "+v"(acc[i][j][g]));
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
 
+        // x of the next batch is requested before its weights: loads complete in order, so the LDS
+        // store of x waits only for x, and the weights stay in flight across the barrier until the
+        // batch is computed
         L w0, w1;
-        load_w(w0, 0);
         load_x(0);
+        load_w(w0, 0);
         store_x(0);
         __syncthreads();
         for (uint32_t bt = 0; bt < nbt; bt += 2) {
             const bool m1 = bt + 1 < nbt;
             if (m1) {
-                load_w(w1, bt + 1);
                 load_x(bt + 1);
+                load_w(w1, bt + 1);
             }
             compute(w0, 0);
             if (m1) store_x(1);
@@ -278,8 +322,8 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
             if (!m1) break;
             const bool m2 = bt + 2 < nbt;
             if (m2) {
-                load_w(w0, bt + 2);
                 load_x(bt + 2);
+                load_w(w0, bt + 2);
             }
             compute(w1, 1);
             if (m2) store_x(0);
@@ -296,37 +340,47 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
 #pragma unroll
             for (int i = 0; i < MT; i++)
 #pragma unroll
-                for (int q = 0; q < 16; q++) {
-                    const uint32_t m = i * 32 + 8 * (q / 4) + 4 * h + q % 4;
-                    if (m < d.m) ((gfloat *)d.y)[(size_t)m * d.n + n] = acc[i][j][q];
-                }
+                for (int g = 0; g < (i == 0 ? G0 : 4); g++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const uint32_t m = i * 32 + 8 * g + 4 * h + q;
+                        if (m >= d.m) continue;
+                        if (S > 1)
+                            unsafeAtomicAdd(d.y + (size_t)m * d.n + n, acc[i][j][g][q]);
+                        else
+                            ((gfloat *)d.y)[(size_t)m * d.n + n] = acc[i][j][g][q];
+                    }
         }
     }
 }
 
-template <int KIND, int MT>
+template <int KIND, int R>
 int rows_resident_groups() {
     static int b = 0;
-    if (b == 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, rows_kernel<KIND, MT>, 256, 0) != hipSuccess || b < 1))
+    if (b == 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, rows_kernel<KIND, R>, 256, 0) != hipSuccess || b < 1))
         b = 1;
     return b;
 }
 
-template <int KIND, int MT>
+template <int KIND, int R>
 hipError_t launch_rows_kind(hipStream_t s, const RowsDesc *descs, const uint32_t *map, const RowsDesc &one,
                             uint32_t count, uint32_t tasks, uint32_t max_items, int cus) {
     const uint32_t gx = (max_items + 31) / 32;
     rows_split_kernel<KIND><<<dim3(gx < 8192 ? gx : 8192, count), 256, 0, s>>>(descs, one);
-    const uint32_t slots = (uint32_t)(cus > 0 ? cus : 256) * (uint32_t)rows_resident_groups<KIND, MT>();
-    rows_kernel<KIND, MT><<<tasks < slots ? tasks : slots, 256, 0, s>>>(descs, map, one, tasks);
+    const uint32_t slots = (uint32_t)(cus > 0 ? cus : 256) * (uint32_t)rows_resident_groups<KIND, R>();
+    rows_kernel<KIND, R><<<tasks < slots ? tasks : slots, 256, 0, s>>>(descs, map, one, tasks);
     return hipGetLastError();
 }
 
 template <int KIND>
 hipError_t launch_rows_mt(hipStream_t s, const RowsDesc *descs, const uint32_t *map, const RowsDesc &one,
                           uint32_t count, uint32_t tasks, uint32_t max_m, uint32_t max_items, int cus) {
-    if (max_m <= 32) return launch_rows_kind<KIND, 1>(s, descs, map, one, count, tasks, max_items, cus);
-    return launch_rows_kind<KIND, 2>(s, descs, map, one, count, tasks, max_items, cus);
+    switch (rows_cap(max_m)) {
+    case 8: return launch_rows_kind<KIND, 8>(s, descs, map, one, count, tasks, max_items, cus);
+    case 16: return launch_rows_kind<KIND, 16>(s, descs, map, one, count, tasks, max_items, cus);
+    case 32: return launch_rows_kind<KIND, 32>(s, descs, map, one, count, tasks, max_items, cus);
+    default: return launch_rows_kind<KIND, 64>(s, descs, map, one, count, tasks, max_items, cus);
+    }
 }
 
 }  // namespace
@@ -340,16 +394,16 @@ bool rows_supported(size_t rows, size_t k, size_t n) {
 
 size_t rows_xsplit_bytes(size_t rows, size_t k) { return rows * (k / 32) * 128; }
 
-uint32_t rows_tasks(size_t n, size_t max_m) {
-    const size_t task_rows = 32 * rows_tw(max_m <= 32 ? 1 : 2) * kWaves;
-    return (uint32_t)((n + task_rows - 1) / task_rows);
+uint32_t rows_tasks(size_t n, size_t k, size_t max_m) {
+    const size_t task_rows = 32 * rows_tw(rows_cap((uint32_t)max_m)) * kWaves;
+    return (uint32_t)((n + task_rows - 1) / task_rows * rows_splits((uint32_t)(k / 32)));
 }
 
 hipError_t launch_rows(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x, float *y,
                        size_t rows, size_t k, size_t n, void *xsplit, int cus) {
     const RowsDesc one{qs, ds, x, (_Float16 *)xsplit, y, (uint32_t)(k / 32), (uint32_t)n, (uint32_t)rows, 0};
     const uint32_t items = (uint32_t)(rows * (k / 32));
-    const uint32_t tasks = rows_tasks(n, rows);
+    const uint32_t tasks = rows_tasks(n, k, rows);
     if (kind == FH_Q8_0) return launch_rows_mt<FH_Q8_0>(s, nullptr, nullptr, one, 1, tasks, (uint32_t)rows, items, cus);
     return launch_rows_mt<FH_Q4_0>(s, nullptr, nullptr, one, 1, tasks, (uint32_t)rows, items, cus);
 }

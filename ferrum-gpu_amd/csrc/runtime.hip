@@ -963,7 +963,7 @@ fh_status fh_rows_plan_create(fh_device *dev, const fh_rows_problem *problems, s
         for (size_t i = 0; i < count; i++) {
             const fh_rows_problem &p = problems[i];
             if ((int)p.w->kind != kind) continue;
-            const uint32_t nb = (uint32_t)(p.w->k / QK), tasks = rows_tasks(p.w->n, L.max_m);
+            const uint32_t nb = (uint32_t)(p.w->k / QK), tasks = rows_tasks(p.w->n, p.w->k, L.max_m);
             const uint64_t t = (uint64_t)L.tasks + tasks;
             if (t >= (1ull << 31)) {
                 fh_rows_plan_free(plan);
