@@ -400,6 +400,123 @@ def bench_scoring(fh, g, ev, ms=(512, 2048), paths=None, reps=5, cpu=True, cpu_r
     return out
 
 
+# TinyLlama-1.1B block matrices, [in, out]: q, k, v, o, gate, up, down; 22 blocks
+LLAMA1B_MATRICES = [(2048, 2048), (2048, 256), (2048, 256), (2048, 2048), (2048, 5632), (2048, 5632), (5632, 2048)]
+LLAMA1B_LAYERS = 22
+
+
+def bench_codec(fh, g, ev, reps=5, copies=8):
+    """The block codec on the device at the TinyLlama-1.1B gate matrix (2048 x 5632 = 11.5M values),
+    inputs resident: encode (f32 -> GGUF blocks), decode (blocks -> f32), snap rows and columns
+    (f32 -> f32), and the weight's dequantise (tiles -> the [k, n] f32 weight); GB/s of the bytes
+    each reads and writes. Each line rotates over `copies` distinct source and destination
+    buffers (8 x 92 MB, more than the 256 MB last-level cache), so every call streams from HBM.
+    Then config 5's QAT fake-quant pass: the column snap of every block matrix of the 1.1B model
+    (the seven matrices of each of its 22 blocks, each its own buffer: 3.9 GB in, 3.9 GB out)."""
+    rng = np.random.default_rng(3)
+    k, n = 2048, 5632
+    vals = k * n
+    host = (rng.standard_normal(vals) * 0.02).astype(np.float32)
+    srcs = [g.upload(host) for _ in range(copies)]
+    dsts = [g.zeros(vals) for _ in range(copies)]
+    out = {}
+
+    def timed(fn, nbytes, calls):
+        for c in range(calls):
+            fn(c)
+        g.sync()
+        e0, e1 = ev.create(2)
+        ev.record(e0)
+        for _ in range(reps):
+            for c in range(calls):
+                fn(c)
+        ev.record(e1)
+        g.sync()
+        ms = ev.ms(e0, e1) / (reps * calls)
+        ev.destroy([e0, e1])
+        return {"us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    for kind, tag in ((fh.QKind.Q8_0, "q8_0"), (fh.QKind.Q4_0, "q4_0")):
+        pb = fh.nbytes(kind, vals)
+        blocks = [g.bytes_zeros(pb) for _ in range(copies)]
+        out[f"encode_{tag}"] = timed(lambda c: fh.encode(g, kind, srcs[c], vals, blocks[c]), 4 * vals + pb, copies)
+        out[f"decode_{tag}"] = timed(lambda c: fh.decode(g, kind, blocks[c], vals, dsts[c]), 4 * vals + pb, copies)
+        gguf = g.read_bytes(blocks[0])
+        qws = [fh.upload_qweight(g, kind, gguf, k, n) for _ in range(copies)]
+        out[f"dequantise_{tag}"] = timed(
+            lambda c: fh._check(fh.lib().fh_qweight_dequantise(g.handle, qws[c].handle, dsts[c].handle)),
+            4 * vals + pb, copies)
+        for q in qws:
+            q.free()
+        # GGUF bytes from the host into the tiled planes (allocation, PCIe copy, repack kernel): wall
+        # time, PCIe-inclusive; the repack kernel's own time is in the kernel trace
+        t0 = time.perf_counter()
+        for _ in range(3):
+            fh.upload_qweight(g, kind, gguf, k, n).free()
+        g.sync()
+        out[f"upload_gguf_{tag}_pcie_inclusive_ms"] = round((time.perf_counter() - t0) / 3 * 1e3, 3)
+        for b in blocks:
+            b.free()
+    out["snap_rows"] = timed(lambda c: fh.q8_snap_rows(g, srcs[c], dsts[c], k), 8 * vals, copies)
+    out["snap_cols"] = timed(lambda c: fh.q8_snap_cols(g, srcs[c], dsts[c], (k, n)), 8 * vals, copies)
+    for b in srcs + dsts:
+        b.free()
+    # the QAT pass: every matrix of every block its own source and destination
+    mats = []
+    for a, b in LLAMA1B_MATRICES:
+        h = (rng.standard_normal(a * b) * 0.02).astype(np.float32)
+        mats += [(g.upload(h), g.zeros(a * b), a, b) for _ in range(LLAMA1B_LAYERS)]
+    pass_vals = sum(a * b for _, _, a, b in mats)
+
+    def qat_pass(_):
+        for s_, d_, a, b in mats:
+            fh.q8_snap_cols(g, s_, d_, (a, b))
+
+    r = timed(qat_pass, 8 * pass_vals, 1)
+    r["values"] = pass_vals
+    r["launches"] = len(mats)
+    out["qat_fake_quant_pass_llama1b"] = r
+    for s_, d_, _, _ in mats:
+        s_.free()
+        d_.free()
+    out["shape"] = (f"{k} x {n} ({vals} values), {copies} rotating copies; QAT pass: {LLAMA1B_LAYERS} x "
+                    f"{LLAMA1B_MATRICES} [in, out], distinct buffers")
+    return out
+
+
+def host_info():
+    """The host's core count and CPU model (for the CPU baseline's report)."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model}
+
+
+def cpu_matmul_tuned(threads, m=64, k=2048, n=2048, budget_s=3.0):
+    """ferrum_ref's matmul_tuned (kernels/tuned.rs:99-134, the oracle's restatement) on `threads`
+    threads at a config-5 shape: GFLOP/s, median of repeats (bench_util::time_ms)."""
+    import oracle as orc
+
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+    orc.matmul_tuned(x, w, m, k, n, threads)
+    times, t0 = [], time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or len(times) < 7:
+        t1 = time.perf_counter()
+        orc.matmul_tuned(x, w, m, k, n, threads)
+        times.append(time.perf_counter() - t1)
+    med = float(np.median(times))
+    return {"gflops": round(2 * m * k * n / med / 1e9, 2), "threads": threads, "shape": f"{m} x {k} x {n}",
+            "ms": round(med * 1e3, 3)}
+
+
 def cpu_baseline(shapes, kind_bytes, budget_s=12.0):
     """The reference's CPU decode path restated in C (oracle/gemv: f32 weights [k, n], ascending
     k, one thread), on the same shapes; the rate is the same algorithmic bytes (the packed
@@ -420,11 +537,14 @@ def cpu_baseline(shapes, kind_bytes, budget_s=12.0):
     med = float(np.median(times))
     alg = sum(gemv_bytes(kind_bytes, k, n) for k, n in shapes)
     f32b = sum(4 * k * n for k, n in shapes)
+    hi = host_info()
     return {"value": alg / med / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{len(times)} reps (median) of one pass over {shapes} Q4_0-sized work on f32 "
                       f"dequantised weights, {sum(x[2]*x[3] for x in mats)} weights; f32 stream "
-                      f"{f32b / med / 1e9:.2f} GB/s; {med * 1e3:.3f} ms per pass",
-            "f32_gbs": f32b / med / 1e9, "ms_per_pass": med * 1e3}
+                      f"{f32b / med / 1e9:.2f} GB/s; {med * 1e3:.3f} ms per pass; host {hi['nproc']} "
+                      f"cores, {hi['cpu_model']}",
+            "f32_gbs": f32b / med / 1e9, "ms_per_pass": med * 1e3, "host_nproc": hi["nproc"],
+            "host_cpu_model": hi["cpu_model"]}
 
 
 def main():
@@ -441,6 +561,10 @@ def main():
                     help="the GEMM --gemm-only measures")
     ap.add_argument("--score-only", action="store_true",
                     help="only the Qwen2-0.5B Q4_0 scoring forward (config 4), one JSON line (for profiling)")
+    ap.add_argument("--codec-only", action="store_true",
+                    help="only the codec and QAT-pass lines at the TinyLlama-1.1B sizes, one JSON line (for profiling)")
+    ap.add_argument("--rows-only", action="store_true",
+                    help="only config 5's grouped few-row products (M = 8, 64), one JSON line (for profiling)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the scoring GEMM at the TinyLlama-1.1B shapes, M = 4096, one JSON line (for profiling)")
     a = ap.parse_args()
@@ -464,6 +588,22 @@ def main():
         best = r["fast_m2048"]
         print(json.dumps({"metric": "Qwen2-0.5B Q4_0 scoring tokens/s, M = 2048", "value": best["tok_s"],
                           "unit": "tok/s", "n_gpus": 1, "higher_is_better": True, "detail": r}))
+        g.close()
+        return
+    if a.codec_only:
+        r = bench_codec(fh, g, ev)
+        print(json.dumps({"metric": "Q8_0 QAT fake-quant pass over TinyLlama-1.1B's block matrices, GB/s",
+                          "value": r["qat_fake_quant_pass_llama1b"]["gbs"], "unit": "GB/s", "n_gpus": 1,
+                          "higher_is_better": True, "detail": r}))
+        g.close()
+        return
+    if a.rows_only:
+        det = {}
+        for kind, tag in ((fh.QKind.Q4_0, "q4_0"), (fh.QKind.Q8_0, "q8_0")):
+            for m in (8, 64):
+                det[f"{tag}_m{m}"] = bench_rows_pool(fh, g, ev, kind, m, LLAMA1B_SHAPES, a.steps)
+        print(json.dumps({"metric": "config 5 few-row products, weight GB/s", "value": det["q4_0_m8"]["weight_gbs"],
+                          "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "detail": det}))
         g.close()
         return
     if a.gemm_only:
@@ -514,6 +654,9 @@ def main():
                     "ms_per_step": r["ms_per_step"], "bytes_per_step": r["bytes_per_step"],
                     "path": "rows plan (QPath.Rows), one launch pair for 48 products",
                     "single_calls_gbs": round(r1["gbs"], 2), "single_calls_ms_per_step": r1["ms_per_step"]}
+        codec = bench_codec(fh, g, ev)
+        log("codec:", codec)
+        extra["codec_llama1b"] = codec
         sc = bench_scoring(fh, g, ev, cpu=not a.no_cpu)
         log("Qwen2-0.5B Q4_0 scoring:", sc)
         extra["qwen2_0_5b_q4_0_scoring"] = sc
@@ -529,6 +672,10 @@ def main():
     if not a.no_cpu:
         cpu = cpu_baseline(QWEN_SHAPES, 18)
         log("cpu baseline:", cpu)
+        if not a.no_extra:  # the CPU matmul on all host cores, beside the GEMM lines
+            cores = min(16, os.cpu_count() or 1)
+            extra["cpu_matmul_tuned"] = cpu_matmul_tuned(cores)
+            log("cpu matmul_tuned:", extra["cpu_matmul_tuned"])
 
     gbs = head["gbs"]
     dom = max(head["launches"], key=lambda L: L["avg_ms"])  # the launch that takes the most time
@@ -544,7 +691,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 weights, f32 activations and accumulation",
+        "dtype": "q4_0 weights (exact int8 quants); x on a per-32-block fixed-point grid of 30 bits "
+                 "(2^-30 of the block's largest |x|, four int8 limbs) on int8 MFMA with exact int32 block "
+                 "sums; f32 block scales and accumulation",
         "data": "synthetic: seeded N(0,0.02) weights packed Q4_0, x ~ N(0,1)",
         "config": {"workload": "Q4_0 GEMV sweep, K x N in {896x1152, 896x4864, 4864x896}, "
                                f"{head['copies']} distinct copies each ({head['bytes_per_step'] / 2**30:.2f} GiB per step)",
@@ -558,7 +707,8 @@ def main():
                      "traffic_source": traffic and traffic["source"]},
         "launches": [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in L.items()}
                      for L in head["launches"]],
-        "cpu_baseline": cpu and {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "cpu_baseline": cpu and {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample", "host_nproc",
+                                                     "host_cpu_model")},
         "extra": extra,
         "hbm_copy_gbs": round(copy["gbs"], 1),
     }

@@ -154,19 +154,30 @@ __global__ __launch_bounds__(kThreads) void decode_rows_kernel(const uint8_t *__
     constexpr int IN = kTaskBlocks * BB;
     __shared__ __attribute__((aligned(16))) uint8_t stage[IN];
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    constexpr int CH = (IN / 16 + kThreads - 1) / kThreads;  // 16-byte chunks per thread
     const size_t ntasks = (nblocks + kTaskBlocks - 1) / kTaskBlocks;
+    // this thread's chunks of a task's packed bytes; the next task's are in flight while this
+    // one is decoded
+    auto fetch = [&](size_t task, u32x4 (&p)[CH]) {
+        const size_t blk0 = task * kTaskBlocks;
+        const size_t valid = (nblocks - blk0 < (size_t)kTaskBlocks ? nblocks - blk0 : kTaskBlocks) * BB;
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const size_t off = (size_t)(tid + c * kThreads) * 16;
+            if (off < IN && off < valid)  // a partial last chunk reads into the allocation's padding
+                p[c] = __builtin_nontemporal_load((const u32x4 *)(src + blk0 * BB + off));
+        }
+    };
+    u32x4 ahead[CH];
+    if (blockIdx.x < ntasks) fetch(blockIdx.x, ahead);
     for (size_t task = blockIdx.x; task < ntasks; task += gridDim.x) {
         const size_t blk0 = task * kTaskBlocks;
-        const size_t nvalid = nblocks - blk0 < (size_t)kTaskBlocks ? nblocks - blk0 : kTaskBlocks;
-        const size_t valid = nvalid * BB;
-        const uint8_t *in = src + blk0 * BB;
+        __syncthreads();  // the previous task's stage has been read
+#pragma unroll
+        for (int c = 0; c < CH; c++)
+            if ((tid + c * kThreads) * 16 < IN) *(u32x4 *)(stage + (tid + c * kThreads) * 16) = ahead[c];
         __syncthreads();
-        for (int c = tid; c < IN / 16; c += kThreads) {
-            size_t off = (size_t)c * 16;
-            if (off < valid)  // a partial last chunk reads into the allocation's padding
-                *(u32x4 *)(stage + off) = __builtin_nontemporal_load((const u32x4 *)(in + off));
-        }
-        __syncthreads();
+        if (task + gridDim.x < ntasks) fetch(task + gridDim.x, ahead);
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
             const int lb = (wave * kUnroll + u) * 8 + lane / 8;
@@ -372,26 +383,59 @@ __global__ __launch_bounds__(kThreads) void planes_to_gguf_kernel(const uint8_t 
 }
 
 // Snap an [rows_in, cols_out] matrix down its columns (q8_snap_cols, ops/qat.rs:33-57).
+// One wavefront per (block row kb, 64 columns): lane (cq = lane % 16, rg = lane / 16) holds four
+// adjacent columns of rows 8rg..8rg+7 of the block row, so each load instruction moves four
+// 256-byte row segments (16 bytes a lane) and a column's block spans lanes cq, cq+16, cq+32,
+// cq+48, whose maxima meet by two lane exchanges. VEC: columns a multiple of 4 and 16-byte
+// aligned buffers (f32x4 loads and stores); otherwise one guarded f32 per column.
+template <bool VEC>
 __global__ __launch_bounds__(kThreads) void snap_cols_kernel(const float *__restrict__ src,
                                                              float *__restrict__ dst, size_t k,
                                                              size_t n) {
-    const size_t nb = k / 32;
-    const size_t total = nb * n;
-    for (size_t t = (size_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (size_t)gridDim.x * kThreads) {
-        const size_t kb = t / n, c = t % n;
-        const float *in = src + kb * 32 * n + c;
-        float v[32];
+    const int lane = threadIdx.x % 64, cq = lane % 16, rg = lane / 16;
+    const size_t cg = (n + 63) / 64, tasks = k / 32 * cg;
+    const size_t waves = (size_t)gridDim.x * (kThreads / 64);
+    for (size_t t = (size_t)blockIdx.x * (kThreads / 64) + threadIdx.x / 64; t < tasks; t += waves) {
+        const size_t c0 = (t % cg) * 64 + 4 * cq;
+        const size_t at = (t / cg * 32 + (size_t)rg * 8) * n + c0;  // row 0 of this lane's rows
+        f32x4 v[8];
 #pragma unroll
-        for (int e = 0; e < 32; e++) v[e] = in[e * n];
-        float amax = 0.0f;
+        for (int r = 0; r < 8; r++) {
+            if constexpr (VEC) {
+                v[r] = c0 < n ? __builtin_nontemporal_load((const f32x4 *)(src + at + r * n))
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
+            } else {
 #pragma unroll
-        for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(v[e]));
-        float d = amax / 127.0f;
-        float id = d != 0.0f ? 1.0f / d : 0.0f;
-        float dh = half_bits_to_float(float_to_half_bits(d));
-        float *out = dst + kb * 32 * n + c;
+                for (int i = 0; i < 4; i++) v[r][i] = c0 + i < n ? src[at + r * n + i] : 0.0f;
+            }
+        }
+        f32x4 amax = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int e = 0; e < 32; e++) out[e * n] = dh * (float)round_sat_i8(v[e] * id);
+        for (int r = 0; r < 8; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) amax[i] = fmaxf(amax[i], fabsf(v[r][i]));
+        f32x4 id, dh;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float a = fmaxf(amax[i], __shfl_xor(amax[i], 16));
+            a = fmaxf(a, __shfl_xor(a, 32));
+            const float d = a / 127.0f;
+            id[i] = d != 0.0f ? 1.0f / d : 0.0f;
+            dh[i] = half_bits_to_float(float_to_half_bits(d));
+        }
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            f32x4 o;
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = dh[i] * (float)round_sat_i8(v[r][i] * id[i]);
+            if constexpr (VEC) {
+                if (c0 < n) __builtin_nontemporal_store(o, (f32x4 *)(dst + at + r * n));
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (c0 + i < n) dst[at + r * n + i] = o[i];
+            }
+        }
     }
 }
 
@@ -421,6 +465,16 @@ unsigned grid_for(size_t work_items, size_t per_group, unsigned cap) {
     return g > cap ? cap : (unsigned)g;
 }
 
+// Workgroups for `tasks` equal tasks when at most `resident` fit the device at once: every
+// workgroup takes the same number of tasks (the last fewer), so none waits on a second round
+// of a few stragglers.
+constexpr unsigned kResident = 2048;  // 8 workgroups of 256 on each of 256 CUs
+unsigned balanced_grid(size_t tasks, unsigned resident) {
+    if (tasks < 1) return 1;
+    const size_t per = (tasks + resident - 1) / resident;
+    return (unsigned)((tasks + per - 1) / per);
+}
+
 }  // namespace
 
 hipError_t launch_encode_rows(hipStream_t s, fh_kind kind, const float *src, uint8_t *dst, size_t nblocks) {
@@ -433,7 +487,7 @@ hipError_t launch_encode_rows(hipStream_t s, fh_kind kind, const float *src, uin
 }
 
 hipError_t launch_decode_rows(hipStream_t s, fh_kind kind, const uint8_t *src, float *dst, size_t nblocks) {
-    unsigned g = grid_for(nblocks, kTaskBlocks, 65535);
+    unsigned g = balanced_grid((nblocks + kTaskBlocks - 1) / kTaskBlocks, kResident);
     if (kind == FH_Q8_0)
         decode_rows_kernel<FH_Q8_0><<<g, kThreads, 0, s>>>(src, dst, nblocks);
     else
@@ -503,8 +557,11 @@ hipError_t launch_decode_f16(hipStream_t s, const uint16_t *src, float *dst, siz
 }
 
 hipError_t launch_snap_cols(hipStream_t s, const float *src, float *dst, size_t rows_in, size_t cols_out) {
-    unsigned g = grid_for(rows_in / 32 * cols_out, kThreads, 65535);
-    snap_cols_kernel<<<g, kThreads, 0, s>>>(src, dst, rows_in, cols_out);
+    unsigned g = grid_for(rows_in / 32 * ((cols_out + 63) / 64), kThreads / 64, 65535);
+    if (cols_out % 4 == 0 && ((uintptr_t)src | (uintptr_t)dst) % 16 == 0)
+        snap_cols_kernel<true><<<g, kThreads, 0, s>>>(src, dst, rows_in, cols_out);
+    else
+        snap_cols_kernel<false><<<g, kThreads, 0, s>>>(src, dst, rows_in, cols_out);
     return hipGetLastError();
 }
 
