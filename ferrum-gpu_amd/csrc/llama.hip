@@ -44,12 +44,30 @@ struct fh_llama {
     bool neox = false, tied = false;
     fh_kind kind = (fh_kind)0;
     fh_path path = FH_PATH_TILED;
+    // A weight matrix of k inputs and n outputs: packed (q), or the f32 rows (f: n rows of k
+    // values, the GGUF row order) of a matrix the file does not store as Q8_0/Q4_0, e.g. one whose
+    // width is not whole 32-blocks (Lin::upload keeps those f32, ferrum_wgpu/src/models/llama/
+    // lin.rs:30-62).
+    struct Mat {
+        fh_qweight *q = nullptr;
+        fh_buffer *f = nullptr;
+        size_t k = 0, n = 0;
+        uint64_t bytes() const { return q ? q->nbytes : (uint64_t)k * n * 4; }
+        uint64_t device_bytes() const { return q ? fh_qweight_device_bytes(q) : f ? f->nbytes : 0; }
+        void release() {
+            fh_qweight_free(q);
+            fh_buffer_free(f);
+            q = nullptr;
+            f = nullptr;
+        }
+    };
     struct Layer {
         fh_buffer *attn_norm = nullptr, *ffn_norm = nullptr, *bqkv = nullptr;
-        fh_qweight *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *down = nullptr;
+        Mat wqkv, wo, wgu, down;
     };
     std::vector<Layer> blocks;
-    fh_qweight *tok = nullptr, *head = nullptr;  // head == tok when tied
+    Mat tok, head;  // head is tok's copy when tied
+    bool packed = true;  // every block matrix packed (the fast path's fused producers need it)
     fh_buffer *out_norm = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
     uint64_t weight_bytes = 0;
     // Activations for up to `rows` rows, grown on demand and kept.
@@ -104,6 +122,58 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const uint8_t *__restri
         }
         x[(size_t)r * d + i] = ok ? half_bits_to_float(ds[scale_slot(t, b, nb)]) * q : NAN;
     }
+}
+
+// Row r of x = row ids[r] of an f32 token embedding (vocab rows of d); an id outside the
+// vocabulary poisons the row with NaN, as above.
+__global__ __launch_bounds__(256) void embed_rows_f32_kernel(const float *__restrict__ tok, const int32_t *__restrict__ ids,
+                                                             float *__restrict__ x, uint32_t d, uint32_t vocab) {
+    const uint32_t r = blockIdx.x;
+    const int32_t id = ids[r];
+    const bool ok = id >= 0 && (uint32_t)id < vocab;
+    const size_t row = (size_t)(ok ? (uint32_t)id : 0u) * d;
+    for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) x[(size_t)r * d + i] = ok ? tok[row + i] : NAN;
+}
+
+// y[M][N] = x[M][K] . W^T for an f32 matrix held as N rows of K (the product of an unpacked
+// Mat; any K). 64 x 64 outputs a workgroup, K in steps of 16 staged in LDS (k-major, so a
+// wavefront reads 16 consecutive columns and 4 broadcast rows), 4 x 4 outputs a thread (rows
+// ty + 16 i, columns tx + 16 j), each an fma chain in ascending k.
+__global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                         float *__restrict__ y, uint32_t M, uint32_t K, uint32_t N) {
+    __shared__ float xs[16][65], ws[16][65];
+    const uint32_t m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const uint32_t tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    const uint32_t lr = threadIdx.x / 4, lk = threadIdx.x % 4 * 4;  // this thread's loads: row lr, k lk..lk+3
+    float acc[4][4] = {};
+    for (uint32_t k0 = 0; k0 < K; k0 += 16) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t k = k0 + lk + e;
+            xs[lk + e][lr] = m0 + lr < M && k < K ? x[(size_t)(m0 + lr) * K + k] : 0.0f;
+            ws[lk + e][lr] = n0 + lr < N && k < K ? w[(size_t)(n0 + lr) * K + k] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; kk++) {
+            float a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) a[i] = xs[kk][ty + 16 * i];
+#pragma unroll
+            for (int j = 0; j < 4; j++) b[j] = ws[kk][tx + 16 * j];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (m0 + ty + 16 * i < M && n0 + tx + 16 * j < N)
+                y[(size_t)(m0 + ty + 16 * i) * N + n0 + tx + 16 * j] = acc[i][j];
 }
 
 // Sum over a block of 256 threads (four wavefronts); every thread gets the total.
@@ -626,6 +696,19 @@ __global__ __launch_bounds__(64 * W) void attention_split_kernel(
 }
 
 // SwiGLU (ferrum_ref/src/models/llama/ops.rs:69-76): act[r][j] = silu(gu[r][j]) * gu[r][hid + j].
+// Widths that are not a multiple of 4 take swiglu_scalar_kernel.
+__global__ __launch_bounds__(256) void swiglu_scalar_kernel(const float *__restrict__ gu, uint32_t gu_splits,
+                                                            size_t gu_stride, float *__restrict__ act, uint32_t rows,
+                                                            uint32_t hid) {
+    const size_t n = (size_t)rows * hid;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const size_t r = i / hid, j = i % hid;
+        const float g = split_sum(gu, r * 2 * hid + j, gu_splits, gu_stride);
+        const float u = split_sum(gu, r * 2 * hid + hid + j, gu_splits, gu_stride);
+        act[i] = __fmul_rn(g / (1.0f + expf(-g)), u);
+    }
+}
+
 __global__ __launch_bounds__(256) void swiglu_kernel(const float *__restrict__ gu, uint32_t gu_splits, size_t gu_stride,
                                                      float *__restrict__ act, uint32_t rows, uint32_t hid) {
     const uint32_t q = hid / 4;
@@ -874,7 +957,9 @@ fh_status ensure_rows(fh_llama *m, size_t t) {
     return FH_OK;
 }
 
-bool linear_supported(const fh_llama *m, size_t rows, size_t k, size_t n) {
+bool linear_supported(const fh_llama *m, size_t rows, const fh_llama::Mat &w) {
+    const size_t k = w.k, n = w.n;
+    if (!w.q) return rows <= 65535 * 64;  // the f32 product's grid rows
     switch (m->path) {
     case FH_PATH_TILED_FAST: return gemm_supported(rows, k, n);
     case FH_PATH_TILED_F16: return gemm_f16_supported(rows, k, n);
@@ -883,21 +968,27 @@ bool linear_supported(const fh_llama *m, size_t rows, size_t k, size_t n) {
 }
 
 fh_status check_shapes(const fh_llama *m, size_t t) {
-    const size_t d = m->dim;
-    const std::pair<size_t, size_t> kn[] = {{d, m->qkv_width()}, {m->q_dim(), d}, {d, 2 * m->hidden}, {m->hidden, d}};
-    for (auto p : kn)
-        if (!linear_supported(m, t, p.first, p.second))
-            return fail(FH_ERR_UNSUPPORTED, "llama: %zu rows exceed the MFMA GEMM's 32-bit offsets for a %zu x %zu weight",
-                        t, p.second, p.first);
-    if (!linear_supported(m, logit_chunk(m, t), d, m->vocab))
-        return fail(FH_ERR_UNSUPPORTED, "llama: the head exceeds the MFMA GEMM's 32-bit offsets");
+    for (const auto &L : m->blocks)
+        for (const fh_llama::Mat *w : {&L.wqkv, &L.wo, &L.wgu, &L.down})
+            if (!linear_supported(m, t, *w))
+                return fail(FH_ERR_UNSUPPORTED, "llama: %zu rows exceed the GEMM's 32-bit offsets for a %zu x %zu weight",
+                            t, w->n, w->k);
+    if (!linear_supported(m, logit_chunk(m, t), m->head))
+        return fail(FH_ERR_UNSUPPORTED, "llama: the head exceeds the GEMM's 32-bit offsets");
     return FH_OK;
 }
 
 // With defer, a K-split product is left as partial sums in the workspace for the next kernel to
 // add up (every consumer runs before the next product overwrites the workspace).
-hipError_t linear(const fh_llama *m, hipStream_t s, const fh_qweight *w, const float *x, float *y, size_t rows,
+hipError_t linear(const fh_llama *m, hipStream_t s, const fh_llama::Mat &mat, const float *x, float *y, size_t rows,
                   SplitOut *defer = nullptr) {
+    if (!mat.q) {  // f32 rows: x is always given (the fused producers run only when every matrix is packed)
+        const dim3 grid((unsigned)((mat.n + 63) / 64), (unsigned)((rows + 63) / 64));
+        linear_f32_kernel<<<grid, 256, 0, s>>>(x, (const float *)mat.f->ptr, y, (uint32_t)rows, (uint32_t)mat.k,
+                                               (uint32_t)mat.n);
+        return hipGetLastError();
+    }
+    const fh_qweight *w = mat.q;
     switch (m->path) {
     case FH_PATH_TILED_FAST:
         return launch_gemm(s, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, m->ws, defer, m->part);
@@ -939,16 +1030,19 @@ hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t) {
 // The forward over the t ids already in m->ids, up to the final norm's output in m->h.
 hipError_t enqueue_body(fh_llama *m, hipStream_t s, size_t t) {
     const uint32_t d = (uint32_t)m->dim, T = (uint32_t)t;
-    if (m->kind == FH_Q8_0)
-        embed_rows_kernel<FH_Q8_0><<<T, 256, 0, s>>>(m->tok->qs, m->tok->ds, m->ids, m->x, d, (uint32_t)m->vocab);
+    const fh_qweight *tq = m->tok.q;
+    if (!tq)
+        embed_rows_f32_kernel<<<T, 256, 0, s>>>((const float *)m->tok.f->ptr, m->ids, m->x, d, (uint32_t)m->vocab);
+    else if (tq->kind == FH_Q8_0)
+        embed_rows_kernel<FH_Q8_0><<<T, 256, 0, s>>>(tq->qs, tq->ds, m->ids, m->x, d, (uint32_t)m->vocab);
     else
-        embed_rows_kernel<FH_Q4_0><<<T, 256, 0, s>>>(m->tok->qs, m->tok->ds, m->ids, m->x, d, (uint32_t)m->vocab);
+        embed_rows_kernel<FH_Q4_0><<<T, 256, 0, s>>>(tq->qs, tq->ds, m->ids, m->x, d, (uint32_t)m->vocab);
     hipError_t e = hipGetLastError();
     const uint32_t width = (uint32_t)m->qkv_width();
     const size_t td = t * m->dim;
     // The fast path's RMSNorms and SwiGLU write the next product's split x themselves (the
     // product then skips its split pass); rows up to 16384 wide, held in LDS.
-    const bool fused = m->path == FH_PATH_TILED_FAST && m->dim <= 16384 && m->hidden <= 16384;
+    const bool fused = m->path == FH_PATH_TILED_FAST && m->packed && m->dim <= 16384 && m->hidden <= 16384;
     const GemmXSplit xd = gemm_x_split(m->ws, t, m->dim), xh = gemm_x_split(m->ws, t, m->hidden);
     auto norm = [&](bool add, const fh_buffer *g, const SplitOut &o) {
         if (fused && m->kind == FH_Q8_0) {
@@ -990,9 +1084,14 @@ hipError_t enqueue_body(fh_llama *m, hipStream_t s, size_t t) {
             if ((e = linear(m, s, L.down, nullptr, m->o, t, &down))) break;
         } else {
             if ((e = linear(m, s, L.wgu, m->h, m->gu, t, &gu))) break;
-            const size_t quads = t * m->hidden / 4;
-            swiglu_kernel<<<(unsigned)std::min<size_t>((quads + 255) / 256, 65536), 256, 0, s>>>(
-                gu.part, gu.splits, t * 2 * m->hidden, m->act, T, (uint32_t)m->hidden);
+            if (m->hidden % 4) {
+                swiglu_scalar_kernel<<<(unsigned)std::min<size_t>((t * m->hidden + 255) / 256, 65536), 256, 0, s>>>(
+                    gu.part, gu.splits, t * 2 * m->hidden, m->act, T, (uint32_t)m->hidden);
+            } else {
+                const size_t quads = t * m->hidden / 4;
+                swiglu_kernel<<<(unsigned)std::min<size_t>((quads + 255) / 256, 65536), 256, 0, s>>>(
+                    gu.part, gu.splits, t * 2 * m->hidden, m->act, T, (uint32_t)m->hidden);
+            }
             if ((e = linear(m, s, L.down, m->act, m->o, t, &down))) break;
         }
         e = hipGetLastError();
@@ -1025,6 +1124,48 @@ hipError_t enqueue_score(fh_llama *m, hipStream_t s, size_t t, float *out) {
         e = hipGetLastError();
     }
     return e;
+}
+
+// A block matrix of k inputs, or the stacked rows of several (q/k/v, gate/up): packed when every
+// part is stored Q8_0 or Q4_0 (in the model's one format), else f32 rows, each part decoded on the
+// device from what the file stores and stacked in order (Lin::upload, ferrum_wgpu/src/models/
+// llama/lin.rs:30-62: a width that is not whole 32-blocks stays f32; the GGUF writer stores such
+// matrices as F32, ferrum_model/src/gguf/quant.rs:57-69).
+fh_status load_lin(fh_device *dev, const fh_gguf *g, const std::string *names, const size_t *ns, size_t count,
+                   size_t k, fh_kind *kind, fh_llama::Mat *out) {
+    bool packed = true;
+    size_t n = 0;
+    for (size_t i = 0; i < count; i++) {
+        size_t idx;
+        fh_gguf_tensor t;
+        fh_status st;
+        if ((st = fh_gguf_find_tensor(g, names[i].c_str(), &idx)) || (st = fh_gguf_tensor_info(g, idx, &t))) return st;
+        if (t.n_dims != 2 || t.dims[0] != k || t.dims[1] != ns[i])
+            return fail(FH_ERR_INVALID, "llama: tensor '%s' must have dims [%zu, %zu]", names[i].c_str(), k, ns[i]);
+        if (t.ggml_type != FH_Q8_0 && t.ggml_type != FH_Q4_0) packed = false;
+        n += ns[i];
+    }
+    out->k = k;
+    out->n = n;
+    if (packed)
+        return count == 1 ? load_mat(dev, g, "llama", names[0], k, n, kind, &out->q)
+                          : load_mat_rows(dev, g, "llama", names, ns, count, k, kind, &out->q);
+    fh_status st = fh_buffer_zeros(dev, k * n, &out->f);
+    size_t at = 0;
+    for (size_t i = 0; i < count && !st; i++) {
+        fh_buffer *part = nullptr;
+        if ((st = fh_gguf_upload_f32(dev, g, names[i].c_str(), &part))) break;
+        st = fh_copy_f32(dev, part, 0, out->f, at, k * ns[i]);
+        if (!st) st = fh_device_sync(dev);
+        fh_buffer_free(part);
+        at += k * ns[i];
+    }
+    return st;
+}
+
+fh_status load_lin(fh_device *dev, const fh_gguf *g, const std::string &name, size_t k, size_t n, fh_kind *kind,
+                   fh_llama::Mat *out) {
+    return load_lin(dev, g, &name, &n, 1, k, kind, out);
 }
 
 }  // namespace
@@ -1105,22 +1246,21 @@ fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_
     if (!std::isfinite(m->eps) || m->eps <= 0.0f || !std::isfinite(m->rope_base) || m->rope_base <= 0.0f)
         return llama_fail_free(m, fail(FH_ERR_INVALID, "eps and rope_base must be finite and positive"));
     const size_t d = m->dim, hid = m->hidden, qd = m->q_dim(), kvd = m->kv_dim(), hd = m->head_dim;
-    // what the kernels take
-    if (d % 32 || hid % 32 || qd % 32 || (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128) ||
-        m->qkv_width() > kMaxQkvWidth || m->ctx > (1u << 20) || m->vocab > (1u << 30))
+    // what the kernels take (matrices of any width: those not stored packed are multiplied as f32)
+    if ((hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128) || m->qkv_width() > kMaxQkvWidth ||
+        m->ctx > (1u << 20) || m->vocab > (1u << 30))
         return llama_fail_free(m, fail(FH_ERR_UNSUPPORTED,
-                                       "llama: dim %zu / hidden %zu / q width %zu / head %zu outside what the kernels take "
-                                       "(packed matrices need widths in whole 32-blocks; heads 8, 16, 32, 64 or 128 wide; "
-                                       "q + k + v at most %u wide)",
-                                       d, hid, qd, hd, kMaxQkvWidth));
+                                       "llama: head %zu / q + k + v width %zu outside what the kernels take "
+                                       "(heads 8, 16, 32, 64 or 128 wide; q + k + v at most %u wide)",
+                                       hd, m->qkv_width(), kMaxQkvWidth));
     std::vector<float> ff, cos_t, sin_t;
     if ((st = rope_scaling(g, arch, m->rope_dim, &m->linear_factor, &ff))) return llama_fail_free(m, st);
     fh_kind kind = (fh_kind)0;
-    if ((st = load_mat(dev, g, "llama", "token_embd.weight", d, m->vocab, &kind, &m->tok))) return llama_fail_free(m, st);
+    if ((st = load_lin(dev, g, "token_embd.weight", d, m->vocab, &kind, &m->tok))) return llama_fail_free(m, st);
     m->tied = fh_gguf_find_tensor(g, "output.weight", &tidx) != FH_OK;
     if (m->tied) {
         m->head = m->tok;  // the file omits a head tied to the embedding (llama/mod.rs:191-197)
-    } else if ((st = load_mat(dev, g, "llama", "output.weight", d, m->vocab, &kind, &m->head))) {
+    } else if ((st = load_lin(dev, g, "output.weight", d, m->vocab, &kind, &m->head))) {
         return llama_fail_free(m, st);
     }
     if (fh_gguf_find_tensor(g, "output.bias", &tidx) == FH_OK)
@@ -1140,12 +1280,13 @@ fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_
         const std::string gu[2] = {n("ffn_gate.weight"), n("ffn_up.weight")};
         const size_t gu_n[2] = {hid, hid};
         if ((st = load_vec(dev, g, "llama", n("attn_norm.weight"), d, &L.attn_norm)) ||
-            (st = load_mat_rows(dev, g, "llama", qkv, qkv_n, 3, d, &kind, &L.wqkv)) ||
-            (st = load_mat(dev, g, "llama", n("attn_output.weight"), qd, d, &kind, &L.wo)) ||
+            (st = load_lin(dev, g, qkv, qkv_n, 3, d, &kind, &L.wqkv)) ||
+            (st = load_lin(dev, g, n("attn_output.weight"), qd, d, &kind, &L.wo)) ||
             (st = load_vec(dev, g, "llama", n("ffn_norm.weight"), d, &L.ffn_norm)) ||
-            (st = load_mat_rows(dev, g, "llama", gu, gu_n, 2, d, &kind, &L.wgu)) ||
-            (st = load_mat(dev, g, "llama", n("ffn_down.weight"), hid, d, &kind, &L.down)))
+            (st = load_lin(dev, g, gu, gu_n, 2, d, &kind, &L.wgu)) ||
+            (st = load_lin(dev, g, n("ffn_down.weight"), hid, d, &kind, &L.down)))
             return llama_fail_free(m, st);
+        m->packed = m->packed && L.wqkv.q && L.wo.q && L.wgu.q && L.down.q;
         // q/k/v biases, absent ones zero (one vector over the stacked rows)
         std::vector<float> bias(m->qkv_width(), 0.0f), part;
         bool any = false;
@@ -1160,18 +1301,19 @@ fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_
             at += qkv_n[i];
         }
         if (any && (st = fh_buffer_upload(dev, bias.data(), bias.size(), &L.bqkv))) return llama_fail_free(m, st);
-        m->weight_bytes += L.wqkv->nbytes + L.wo->nbytes + L.wgu->nbytes + L.down->nbytes;
+        m->weight_bytes += L.wqkv.bytes() + L.wo.bytes() + L.wgu.bytes() + L.down.bytes();
     }
-    m->weight_bytes += m->head->nbytes;
+    m->weight_bytes += m->head.bytes();
     m->kind = kind;
     rope_tables(m->ctx, m->rope_dim, m->rope_base, ff, m->linear_factor, &cos_t, &sin_t);
     if ((st = fh_buffer_upload(dev, cos_t.data(), cos_t.size(), &m->rope_cos)) ||
         (st = fh_buffer_upload(dev, sin_t.data(), sin_t.size(), &m->rope_sin)))
         return llama_fail_free(m, st);
     if (path == FH_PATH_TILED_FAST) {  // the fast GEMM's fp8 correction operand of every weight
-        std::vector<fh_qweight *> ws = {m->head};
-        for (auto &L : m->blocks) ws.insert(ws.end(), {L.wqkv, L.wo, L.wgu, L.down});
+        std::vector<fh_qweight *> ws = {m->head.q};
+        for (auto &L : m->blocks) ws.insert(ws.end(), {L.wqkv.q, L.wo.q, L.wgu.q, L.down.q});
         for (fh_qweight *w : ws) {
+            if (!w) continue;  // f32 rows
             void *b8 = nullptr;
             if ((st = alloc_bytes(dev, gemm_b8_bytes(w->k, w->n), &b8))) return llama_fail_free(m, st);
             w->b8 = (uint8_t *)b8;
@@ -1188,10 +1330,10 @@ fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_
 void fh_llama_free(fh_llama *m) {
     if (!m) return;
     if (m->dev) (void)hipStreamSynchronize(m->dev->stream);
-    if (m->head && m->head != m->tok) fh_qweight_free(m->head);
-    fh_qweight_free(m->tok);
+    if (!m->tied) m->head.release();
+    m->tok.release();
     for (auto &L : m->blocks) {
-        for (fh_qweight *w : {L.wqkv, L.wo, L.wgu, L.down}) fh_qweight_free(w);
+        for (fh_llama::Mat *w : {&L.wqkv, &L.wo, &L.wgu, &L.down}) w->release();
         for (fh_buffer *b : {L.attn_norm, L.ffn_norm, L.bqkv}) fh_buffer_free(b);
     }
     for (fh_buffer *b : {m->out_norm, m->rope_cos, m->rope_sin}) fh_buffer_free(b);
@@ -1225,13 +1367,12 @@ uint64_t fh_llama_weight_bytes(const fh_llama *m) { return m ? m->weight_bytes :
 
 uint64_t fh_llama_device_bytes(const fh_llama *m) {
     if (!m) return 0;
-    uint64_t b = fh_qweight_device_bytes(m->tok) + m->arena_bytes;
-    if (m->head != m->tok) b += fh_qweight_device_bytes(m->head);
+    uint64_t b = m->tok.device_bytes() + m->arena_bytes;
+    if (!m->tied) b += m->head.device_bytes();
     for (const fh_buffer *v : {m->out_norm, m->rope_cos, m->rope_sin})
         if (v) b += v->nbytes;
     for (const auto &L : m->blocks) {
-        for (const fh_qweight *w : {L.wqkv, L.wo, L.wgu, L.down})
-            if (w) b += fh_qweight_device_bytes(w);
+        for (const fh_llama::Mat *w : {&L.wqkv, &L.wo, &L.wgu, &L.down}) b += w->device_bytes();
         for (const fh_buffer *v : {L.attn_norm, L.ffn_norm, L.bqkv})
             if (v) b += v->nbytes;
     }

@@ -375,11 +375,13 @@ FH_API fh_status fh_gpt2_generate(fh_device *dev, fh_gpt2 *m, const int32_t *pro
 
 /* ---- Llama / Qwen2 full-sequence forward and scoring on resident Q8_0 / Q4_0 weights ----
  * Replaces the batched passes of ferrum_wgpu::models::llama::GpuLlama (ferrum_wgpu/src/models/
- * llama/forward.rs:13-88: forward_all, score), whose weights may be f32; here every matrix stays
- * packed. The model comes from a `llama` (NORM RoPE) or `qwen2` (NEOX RoPE) GGUF as
- * ferrum_model reads and writes it (ferrum_model/src/gguf/llama/mod.rs:56-323): Q8_0 or Q4_0
- * matrices (one format per model, widths in whole 32-blocks), F32 vectors, optional q/k/v biases,
- * `output.weight` absent for a head tied to `token_embd.weight`, linear / rope_freqs RoPE scaling.
+ * llama/forward.rs:13-88: forward_all, score). The model comes from a `llama` (NORM RoPE) or
+ * `qwen2` (NEOX RoPE) GGUF as ferrum_model reads and writes it (ferrum_model/src/gguf/llama/
+ * mod.rs:56-323): Q8_0 or Q4_0 matrices (one format per model) stay packed; a matrix stored in
+ * another type, as the writer stores one whose width is not whole 32-blocks (F32), is decoded to
+ * f32 rows and multiplied as f32 (Lin::upload, ferrum_wgpu/src/models/llama/lin.rs:30-62); F32
+ * vectors, optional q/k/v biases, `output.weight` absent for a head tied to `token_embd.weight`,
+ * linear / rope_freqs RoPE scaling.
  * Its CPU counterpart is ferrum_ref's Llama::forward_logits on the decoded weights
  * (ferrum_ref/src/models/llama/mod.rs:166-259) and nn::score (ferrum_ref/src/kernels/nn.rs:117-129).
  * `path` picks the products: FH_PATH_TILED (or AUTO) the precise MFMA GEMM, FH_PATH_TILED_FAST
@@ -397,7 +399,8 @@ FH_API fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path pa
 FH_API void fh_llama_free(fh_llama *m);
 /* Config (ferrum_ref/src/models/llama/mod.rs:24-51) and how the model is stored. */
 FH_API fh_status fh_llama_config(const fh_llama *m, fh_llama_cfg *out);
-/* Packed weight bytes one forward reads (every block matrix and the head, GGUF sizes). */
+/* Weight bytes one forward reads (every block matrix and the head: GGUF sizes when packed, 4 per
+ * weight when f32). */
 FH_API uint64_t fh_llama_weight_bytes(const fh_llama *m);
 /* Device memory the model holds: every weight's device_bytes (the tied head once), the vectors,
  * the RoPE tables and the activation arena at its current size (no counterpart in the reference,

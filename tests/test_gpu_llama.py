@@ -44,10 +44,13 @@ def cfg(**kw):
 
 
 def variants():
-    """tests.rs:29-45 without dim24, whose 24-wide matrices have no Q8_0/Q4_0 form (the device
-    multiplies packed matrices only; test_unpackable_widths_are_refused)."""
+    """tests.rs:29-45: llama-like, qwen-like with biases and a tied head, partial rotary with MQA,
+    and dim24, whose 24-wide matrices (q/k/v, output, gate/up, the embedding and head) have no
+    Q8_0/Q4_0 form: the GGUF stores them F32 and the device multiplies them as f32 (Lin::upload,
+    ferrum_wgpu/src/models/llama/lin.rs:30-62), while ffn_down (64 wide) stays packed."""
     return [("llama", cfg(), False, False), ("qwen", cfg(neox=True), True, True),
-            ("mqa+partial", cfg(kv_heads=1, rope_dim=4), False, False)]
+            ("mqa+partial", cfg(kv_heads=1, rope_dim=4), False, False),
+            ("dim24", cfg(dim=24, heads=3, kv_heads=3, head_dim=8, rope_dim=8), True, False)]
 
 
 @pytest.fixture(scope="module")
@@ -158,11 +161,27 @@ def test_rope_scaling_is_honoured_on_the_device(fh, g, orc):
     assert rel(load(fh, g, data).forward_all(IDS[:6]), want) < FORWARD
 
 
-def test_unpackable_widths_are_refused(fh, g, orc):
+@pytest.mark.parametrize("kind", [lm.Q8_0, lm.Q4_0])
+def test_unpackable_widths_run_as_f32(fh, g, orc, kind):
+    """dim24 (tests.rs:36-41): the 24-wide matrices load as f32 rows (4 bytes a weight), the
+    64-wide ffn_down packed; the fast scoring path, whose fused producers need packed
+    consumers, runs its unfused form; every path scores like the oracle."""
     c = cfg(dim=24, heads=3, kv_heads=3, head_dim=8, rope_dim=8)
-    with pytest.raises(fh.GpuError) as err:
-        load(fh, g, lm.to_gguf(lm.llama_random(c, 1, True, False), lm.Q8_0))
-    assert "Q8_0 or Q4_0" in str(err.value) or "32-blocks" in str(err.value)
+    data = lm.to_gguf(lm.llama_random(c, 1, True, False), kind)
+    ref = lm.from_gguf(data)
+    d, h, L = 24, 64, 2
+    f32_bytes = 4 * (V * d + L * (d * (3 * d) + d * d + d * 2 * h))  # head, q/k/v, o, gate/up (untied: the
+    # embedding is a lookup table, not a product's weight)
+    packed = L * (h // 32) * d * (34 if kind == lm.Q8_0 else 18)  # ffn_down
+    wlp, whit = orc.llama_score(ref, IDS)
+    for path, bar in (("Tiled", SCORE), ("TiledFast", FAST_LOGPROB), ("TiledF16", F16_LOGPROB)):
+        dev = load(fh, g, data, fh.QPath[path])
+        assert dev.weight_bytes() == f32_bytes + packed
+        assert dev.device_bytes() >= f32_bytes + packed
+        lp, hit = dev.score_arrays(IDS)
+        e = lp_err(lp, wlp)
+        say(f"dim24 kind {kind} {path}: log-prob rel err {e:.2e}")
+        assert e < bar, (path, e)
 
 
 @pytest.mark.parametrize("path", ["TiledFast", "TiledF16"])
