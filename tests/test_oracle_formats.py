@@ -5,9 +5,13 @@ read-only GGUF block types (blocks.rs). The known answers restate the reference'
 independent numpy statement of the format (exhaustive over all codes, or a second decoder
 written from the ggml layout) checks the C code.
 
-Q2_K's encoder (ggml's make_qkx2_quants search) has no golden bytes in the reference: its output
-is pinned by the reference's properties only (error bounds, zero / constant / negative blocks,
-determinism and block independence), so the exact bytes are "parity unpinned"."""
+Q2_K's encoder (ggml's make_qkx2_quants search) has no golden bytes in the reference; besides
+the reference's properties (error bounds, zero / constant / negative blocks, determinism and
+block independence), its bytes are pinned by a second statement of the search written here in
+numpy (vectorised over sub-blocks, f32 throughout, sequential sums by cumsum, the nearest_int
+magic by its bit definition, f16 by numpy's IEEE cast), which must give the C oracle's bytes on
+data that reaches every branch; the same statement with one search constant perturbed (rmin,
+rdelta, the step count, the negative-min clamp, the grid's moving min) must not, which shows the data exercises them."""
 import math
 
 import numpy as np
@@ -181,6 +185,132 @@ def test_q2k_known_answers_and_properties(orc):
     a = orc.encode(orc.Q2_K, w)
     assert np.array_equal(a, orc.encode(orc.Q2_K, w))
     assert np.array_equal(a[:84], orc.encode(orc.Q2_K, w[:256])) and np.array_equal(a[84:], orc.encode(orc.Q2_K, w[256:]))
+
+
+def q2k_nearest_int_np(x):
+    """ggml's nearest_int: (x + 1.5 * 2^23) in f32, then the low 23 bits minus 2^22."""
+    return ((np.asarray(x, np.float32) + np.float32(12582912.0)).view(np.int32) & 0x7FFFFF) - 0x400000
+
+
+def seqsum(a):
+    """Left-to-right f32 sum along the last axis (0 + a0 + a1 + ...)."""
+    return np.cumsum(a, axis=-1, dtype=np.float32)[..., -1]
+
+
+def q2k_fit_np(x, rmin=-0.5, rdelta=0.1, nstep=15, clamp_min=True, moving_min=True):
+    """make_qkx2_quants for nmax = 3 over sub-blocks x [S, 16]: the scale and (negated) min of the
+    candidate grid point whose weighted (|x|) absolute deviation is smallest, first wins (each
+    candidate's grid spans max - min with the min of the best candidate so far); the quants of
+    that candidate."""
+    f = np.float32
+    x = np.asarray(x, f)
+    w = np.abs(x)
+    mn, mx = x.min(axis=1), x.max(axis=1)
+    sum_w, sum_x = seqsum(w), seqsum(w * x)
+    mn = np.where(mn > 0, f(0), mn)
+    mn0 = mn
+    flat = mx == mn
+    with np.errstate(all="ignore"):
+        rng = mx - mn
+        iscale = f(3) / rng
+        scale = f(1) / iscale
+        lv = np.clip(q2k_nearest_int_np(iscale[:, None] * (x - mn[:, None])), 0, 3)
+        best = seqsum(w * np.abs(scale[:, None] * lv.astype(f) + mn[:, None] - x))
+        for step in range(nstep + 1):  # a taken candidate's min moves the grid of the later ones
+            lo = mn if moving_min else mn0
+            isc = (f(rmin) + f(rdelta) * f(step) + f(3)) / (mx - lo)
+            la = np.clip(q2k_nearest_int_np(isc[:, None] * (x - lo[:, None])), 0, 3)
+            qf = la.astype(f)
+            sl, sl2, sxl = seqsum(w * qf), seqsum(w * qf * qf), seqsum(w * qf * x)
+            d = sum_w * sl2 - sl * sl
+            ts = (sum_w * sxl - sum_x * sl) / d
+            tm = (sl2 * sum_x - sl * sxl) / d
+            if clamp_min:
+                pos = tm > 0
+                tm = np.where(pos, f(0), tm)
+                ts = np.where(pos, sxl / sl2, ts)
+            mad = seqsum(w * np.abs(ts[:, None] * qf + tm[:, None] - x))
+            take = (d > 0) & (mad < best) & ~flat
+            lv = np.where(take[:, None], la, lv)
+            best = np.where(take, mad, best)
+            scale = np.where(take, ts, scale)
+            mn = np.where(take, tm, mn)
+    lv = np.where(flat[:, None], 0, lv)
+    scale = np.where(flat, f(0), scale)
+    return scale.astype(f), (-mn).astype(f), lv
+
+
+def q2k_encode_np(data, **search):
+    """Q2_K super-blocks from q2k_fit_np: 4-bit scales and mins against the f16 super scale and
+    min, the quants re-fitted to the rounded scales, then the ggml layout."""
+    f = np.float32
+    blocks = np.asarray(data, f).reshape(-1, 256)
+    sc, mins, lv = q2k_fit_np(blocks.reshape(-1, 16), **search)
+    sc, mins, lv = sc.reshape(-1, 16), mins.reshape(-1, 16), lv.reshape(-1, 256)
+    out = []
+    for b in range(blocks.shape[0]):
+        ms, mm = max(f(0), sc[b].max()), max(f(0), mins[b].max())
+        packed = np.zeros(16, np.int64)
+        dbits = mbits = 0
+        if ms > 0:
+            packed = q2k_nearest_int_np((f(15) / ms) * sc[b]).astype(np.int64) & 0xFF
+            dbits = int(np.float32(ms / f(15)).astype(np.float16).view(np.uint16))
+        if mm > 0:
+            packed |= ((q2k_nearest_int_np((f(15) / mm) * mins[b]).astype(np.int64) & 0xFF) << 4) & 0xFF
+            mbits = int(np.float32(mm / f(15)).astype(np.float16).view(np.uint16))
+        d32 = np.array(dbits, np.uint16).view(np.float16).astype(f)
+        m32 = np.array(mbits, np.uint16).view(np.float16).astype(f)
+        levels = lv[b].copy()
+        for j in range(16):
+            s_ = d32 * f(packed[j] & 15)
+            if s_ == 0:
+                continue
+            dm = m32 * f(packed[j] >> 4)
+            levels[16 * j:16 * j + 16] = np.clip(q2k_nearest_int_np((blocks[b, 16 * j:16 * j + 16] + dm) / s_), 0, 3)
+        qs = []
+        for half in (0, 128):
+            for l in range(32):
+                qs.append(levels[half + l] | levels[half + l + 32] << 2 | levels[half + l + 64] << 4 |
+                          levels[half + l + 96] << 6)
+        out.append(np.concatenate([packed.astype(np.uint8), np.array(qs, np.uint8),
+                                   np.array([dbits & 0xFF, dbits >> 8, mbits & 0xFF, mbits >> 8], np.uint8)]))
+    return np.concatenate(out)
+
+
+def q2k_cases():
+    """Data that reaches every branch of the search: smooth and noisy signals, all-positive
+    sub-blocks (min clamped to zero), all-negative ones, flat sub-blocks, lone spikes, magnitudes
+    from 1e-6 to 1e3 side by side, and scales small enough to round to f16 subnormals."""
+    rng = np.random.default_rng(21)
+    cases = {"wave": wave(4096), "normal": (rng.standard_normal(16384) * 0.02).astype(np.float32),
+             "heavy": rng.standard_t(2, 8192).astype(np.float32),
+             "positive": np.abs(rng.standard_normal(4096)).astype(np.float32) + np.float32(0.1),
+             "negative": -np.abs(rng.standard_normal(4096)).astype(np.float32)}
+    mixed = rng.standard_normal(8192).astype(np.float32)
+    mixed *= np.float32(10.0) ** rng.integers(-6, 4, 8192 // 16).repeat(16).astype(np.float32)
+    cases["mixed"] = mixed
+    spiky = np.zeros(4096, np.float32)
+    spiky[rng.integers(0, 4096, 64)] = rng.standard_normal(64).astype(np.float32)
+    cases["spiky"] = spiky
+    flat = rng.standard_normal(4096).astype(np.float32)
+    flat[: 2048] = np.repeat(rng.standard_normal(128).astype(np.float32), 16)
+    cases["flat"] = flat
+    cases["tiny"] = (rng.standard_normal(2048) * 1e-7).astype(np.float32)
+    return cases
+
+
+@pytest.mark.parametrize("name", list(q2k_cases()))
+def test_q2k_encoder_equals_an_independent_numpy_search(orc, name):
+    data = q2k_cases()[name]
+    assert np.array_equal(orc.encode(orc.Q2_K, data), q2k_encode_np(data)), name
+
+
+def test_q2k_search_constants_are_pinned_by_the_cases(orc):
+    """Each perturbation of the search changes some case's bytes, so the match above pins them."""
+    cases = q2k_cases()
+    want = {n: orc.encode(orc.Q2_K, d) for n, d in cases.items()}
+    for bad in ({"rmin": -0.4}, {"rdelta": 0.11}, {"nstep": 14}, {"clamp_min": False}, {"moving_min": False}):
+        assert any(not np.array_equal(want[n], q2k_encode_np(d, **bad)) for n, d in cases.items()), bad
 
 
 # ---- read-only block types (blocks/tests.rs) ----
