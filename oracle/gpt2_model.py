@@ -2,6 +2,8 @@
 
 * ``gpt2_random``   restates Gpt2::random (ferrum_ref/src/models/gpt2/mod.rs:139-190): the
                     reference's seeded weights, drawn from its rand_vec in the same order.
+* ``gpt2_init``     restates Gpt2::init (ferrum_ref/src/models/gpt2/params.rs:160-180): the
+                    random draws rescaled to GPT-style magnitudes, gains 1, biases 0.
 * ``fake_quantize`` restates Gpt2::fake_quantize (ferrum_ref/src/training/qat.rs:56-74): the f32
                     model a Q8_0 export stores, which the CPU decode runs on.
 * ``to_gguf``       restates to_gguf (ferrum_model/src/gguf/gpt2.rs:179-233): GGUF rows of every
@@ -67,6 +69,30 @@ def gpt2_random(cfg: dict, seed: int) -> dict:
     m["lnf_g"] = gain(d)
     m["lnf_b"] = mat(d, 0.1)
     m["head"] = mat(d * v, 0.5)
+    return m
+
+
+def gpt2_init(cfg: dict, seed: int) -> dict:
+    """Gpt2::init (ferrum_ref/src/models/gpt2/params.rs:160-180): Gpt2::random's draws, then every
+    canonical parameter by kind: the token and position embeddings, the block matrices (canonical
+    block indices 2, 4, 6, 8, 12, 14) and the head times 0.02 * sqrt(3) in f32 (rand_vec is uniform
+    on [-1, 1), std 1 / sqrt(3)); LayerNorm gains (block indices 0, 10 and the final one) 1; block
+    biases and LayerNorm shifts 0. The head stays untied (tie_head ties it)."""
+    m = gpt2_random(cfg, seed)
+    scale = np.float32(0.02) * np.sqrt(np.float32(3.0))
+    weights = ("wq", "wk", "wv", "wo", "w1", "w2")
+    gains = ("ln1_g", "ln2_g")
+    for b in m["blocks"]:
+        for k in GPT2_BLOCK_NAMES:
+            if k in weights:
+                b[k] = (b[k] * scale).astype(np.float32)
+            elif k in gains:
+                b[k] = np.ones_like(b[k])
+            else:
+                b[k] = np.zeros_like(b[k])
+    for k in ("tok", "pos", "head"):
+        m[k] = (m[k] * scale).astype(np.float32)
+    m["lnf_g"], m["lnf_b"] = np.ones_like(m["lnf_g"]), np.zeros_like(m["lnf_b"])
     return m
 
 

@@ -137,24 +137,32 @@ def test_generate_continues_from_the_current_position(g, orc):
     assert "full" in str(err.value)
 
 
-def test_gpt2_small_shape_decodes_the_oracles_tokens(fh, g, orc):
+@pytest.mark.parametrize("init", ["reference", "gpt2"])
+def test_gpt2_small_shape_decodes_the_oracles_tokens(fh, g, orc, init):
     """The decode benchmark's model: GPT-2-small shapes (12 layers, d 768, 12 heads, vocab 50257,
-    ctx 1024, tied head) with GPT-2's initialisation, stored Q8_0 by the device encoder; 32
-    uniform-random prompt tokens, 256 greedy tokens, identical IDs. The file the device writes is
-    byte for byte the oracle's export of the same weights. (With the reference's Gpt2::random
-    weights this shape is numerically chaotic: the CPU's own f32 logits leave the float64 ones by
-    1e-1 within 40 tokens, so no differently rounded implementation can follow it token for token.)"""
+    ctx 1024, tied head), stored Q8_0 by the device encoder; 32 uniform-random prompt tokens, 256
+    greedy tokens, identical IDs, and the logits of the first 8 steps within FORWARD. The file the
+    device writes is byte for byte the oracle's export of the same weights. Weights: "reference"
+    is ferrum_ref's Gpt2::init (params.rs:160-180) with the head tied (Gpt2::tie_head, mod.rs:
+    119-123); "gpt2" is GPT-2's published initialisation (ferrum_hip.gpt2.gpt2_init, the bench's
+    model). (Gpt2::random's raw weights, uniform +-0.5, make this shape numerically chaotic: the
+    CPU's own f32 logits leave the float64 ones by 1e-1 within 40 tokens, so no differently
+    rounded implementation can follow them token for token; Gpt2::init rescales those draws.)"""
     from ferrum_hip.gpt2 import gpt2_init, to_gguf
 
     cfg = {"vocab": 50257, "ctx": 1024, "dim": 768, "heads": 12, "layers": 12, "hidden": 3072}
     t0 = time.time()
-    m = gpt2_init(cfg, 1)
+    if init == "reference":
+        m = gm.gpt2_init(cfg, 1)
+        m["head"] = None  # tied: the transposed token embedding
+    else:
+        m = gpt2_init(cfg, 1)
     data = to_gguf(g, m, fh.QKind.Q8_0)
     om = dict(m)
     om["head"] = orc.transpose(m["tok"], cfg["vocab"], cfg["dim"])
     assert data == gm.to_gguf(om, gm.Q8_0)
     ref = gm.from_gguf(data)
-    say(f"gpt2-small model built and checked in {time.time() - t0:.1f} s ({len(data) / 1e6:.1f} MB GGUF)")
+    say(f"gpt2-small ({init} init) built and checked in {time.time() - t0:.1f} s ({len(data) / 1e6:.1f} MB GGUF)")
     prompt = [int(t) for t in np.random.default_rng(2024).integers(0, cfg["vocab"], 32)]
     dev = load(g, data)
     assert dev.step_bytes() == 131_252_784
@@ -169,5 +177,5 @@ def test_gpt2_small_shape_decodes_the_oracles_tokens(fh, g, orc):
     worst = 0.0
     for t in prompt[:8]:
         worst = max(worst, rel(dev.feed(t), cpu.feed(t)))
-    say(f"gpt2-small logits max rel err over 8 steps: {worst:.2e}")
-    assert worst < 1e-4
+    say(f"gpt2-small ({init} init) logits max rel err over 8 steps: {worst:.2e}")
+    assert worst < FORWARD

@@ -96,6 +96,30 @@ def test_random_model_draw_order(orc):
     assert np.array_equal(m["head"], orc.rand_vec(d * SMALL["vocab"], 2037) * np.float32(0.5))
 
 
+def test_init_model_scales_gains_and_biases(orc):
+    """Gpt2::init (params.rs:160-180) on Gpt2::random's draws: gains exactly 1, block biases and
+    LayerNorm shifts exactly 0; the weights keep random's draws (each tensor a positive multiple
+    of it, so the draw order above carries over) at GPT-style spreads: the token embedding's std
+    is 0.02 (uniform draws times 0.02 sqrt 3) and the tensors random scales by 0.5 (position
+    embedding, block matrices, head) 0.01, each within 3% on these sizes. A dropped rescale (std
+    0.29 / 0.58), a lost 0.5 (0.02 for a matrix) or a gain left random fails one of them."""
+    cfg = {"vocab": 512, "ctx": 64, "dim": 64, "heads": 4, "layers": 2, "hidden": 256}
+    r, m = gm.gpt2_random(cfg, 3), gm.gpt2_init(cfg, 3)
+    for b in m["blocks"]:
+        for k in ("ln1_g", "ln2_g"):
+            assert np.all(b[k] == 1.0)
+        for k in ("ln1_b", "bq", "bk", "bv", "bo", "ln2_b", "b1", "b2"):
+            assert np.all(b[k] == 0.0) and not np.signbit(b[k]).any()
+    assert np.all(m["lnf_g"] == 1.0) and np.all(m["lnf_b"] == 0.0)
+    pairs = [(m["tok"], r["tok"], 0.02), (m["pos"], r["pos"], 0.01), (m["head"], r["head"], 0.01)]
+    for bm, br in zip(m["blocks"], r["blocks"]):
+        pairs += [(bm[k], br[k], 0.01) for k in ("wq", "wk", "wv", "wo", "w1", "w2")]
+    for got, drawn, std in pairs:
+        ratio = got.astype(np.float64)[drawn != 0] / drawn[drawn != 0]
+        assert np.all(np.abs(ratio / ratio[0] - 1) < 1e-6) and ratio[0] > 0
+        assert abs(float(np.std(got)) / std - 1) < 0.03, (std, float(np.std(got)))
+
+
 @pytest.mark.parametrize("kind", [gm.Q8_0, gm.Q4_0])
 def test_export_decodes_to_the_snapped_model(orc, kind):
     m = gm.gpt2_random(SMALL, 5)
