@@ -193,9 +193,11 @@ def bench_gemv_pool(fh, g, ev, kind, groups, pool_bytes, steps, warmup, seed=0):
             "gbs": step_bytes / (step_ms * 1e-3) / 1e9, "launches": launches, "prewarm_s": round(warm_s, 3)}
 
 
-def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0, path=None, copies=1):
+def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0, path=None, copies=1, bound=False):
     """One step = every product of `shapes` (times `copies` distinct weight copies, to exceed the
-    last-level cache for the HBM-bound small-M rates). Returns flops and algorithmic bytes per step."""
+    last-level cache for the HBM-bound small-M rates). Returns flops and algorithmic bytes per step.
+    With `bound`, also the fraction of outputs outside the MFMA-GEMM bound |g - w| <= 1e-3 +
+    2e-3 |w|, w taken from the precise path (QPath.Tiled, itself within 1e-5 of the CPU oracle)."""
     path = fh.QPath.Tiled if path is None else path
     rng = np.random.default_rng(seed)
     items = []
@@ -205,23 +207,39 @@ def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0, path=None, copies=1):
             qw = fh.upload_quantised(g, kind, w, k, n)
             gx = g.upload(rng.standard_normal(m * k).astype(np.float32))
             gy = g.zeros(m * n)
-            items.append((qw, gx, gy))
+            items.append((qw, gx, gy, n))
     flops = copies * sum(2 * m * k * n for k, n in shapes)
     nbytes = copies * sum((k // 32) * n * kind.file_bytes() + 4 * m * k + 4 * m * n for k, n in shapes)
-    for qw, gx, gy in items:
+    for qw, gx, gy, _ in items:
         fh.linear_q_with(g, gx, qw, gy, m, path)
     g.sync()
     e0, e1 = ev.create(2)
     ev.record(e0)
     for _ in range(steps):
-        for qw, gx, gy in items:
+        for qw, gx, gy, _ in items:
             fh.linear_q_with(g, gx, qw, gy, m, path)
     ev.record(e1)
     g.sync()
     ms = ev.ms(e0, e1) / steps
     ev.destroy([e0, e1])
-    return {"m": m, "flops_per_step": flops, "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
-            "bytes_per_step": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9}
+    out = {"m": m, "flops_per_step": flops, "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+           "bytes_per_step": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9}
+    if bound and path != fh.QPath.Tiled:
+        outside = total = 0
+        worst = 0.0
+        for qw, gx, gy, n in items[::copies]:
+            ref = g.zeros(m * n)
+            fh.linear_q_with(g, gx, qw, ref, m, fh.QPath.Tiled)
+            got, want = g.read(gy), g.read(ref)
+            ref.free()
+            lim = 1e-3 + 2e-3 * np.abs(want)
+            r = np.abs(got - want) / lim
+            outside += int(np.count_nonzero(r > 1.0))
+            total += got.size
+            worst = max(worst, float(r.max()))
+        out["outside_bound_frac"] = outside / total
+        out["worst_of_bound"] = round(worst, 4)
+    return out
 
 
 def bench_rows_pool(fh, g, ev, kind, m, shapes, steps, copies=12, seed=0):
@@ -633,12 +651,15 @@ def main():
                                        ("q8_0_gemm_llama1b", fh.QKind.Q8_0, LLAMA1B_SHAPES, (512, 4096))):
             for m in ms:
                 for tag, path in (("", fh.QPath.TiledFast), ("_f16", fh.QPath.TiledF16), ("_precise", fh.QPath.Tiled)):
-                    r = bench_gemm(fh, g, ev, kind, m, shapes, 10, path=path)
+                    r = bench_gemm(fh, g, ev, kind, m, shapes, 10, path=path, bound=True)
                     log(f"{name}{tag} M={m}:", r)
                     extra[f"{name}{tag}_m{m}"] = {"tflops": round(r["tflops"], 2),
                                                   "frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
                                                   "ms_per_step": r["ms_per_step"],
                                                   "flops_per_step": r["flops_per_step"]}
+                    if "outside_bound_frac" in r:
+                        extra[f"{name}{tag}_m{m}"].update(outside_bound_frac=r["outside_bound_frac"],
+                                                          worst_of_bound=r["worst_of_bound"])
         # config 5's small M (HBM-bound): 12 distinct copies of the four products (about 300 MB of
         # Q4_0 weights, more than the 256 MB last-level cache), as one grouped launch of the few-row
         # kernel, and as one linear_q per product with the library's own path choice
