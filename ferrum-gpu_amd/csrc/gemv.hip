@@ -155,13 +155,22 @@ __device__ __forceinline__ void load_batch(Batch<KIND> &bt, const Task<KIND> &tk
     }
 }
 
+// Workgroups are dealt to the eight XCDs round robin (workgroup b runs on XCD b % 8). This numbers
+// them so that each XCD's workgroups hold one contiguous run of the task order: the tasks of a
+// product, which all read its prepared x, then share one XCD's L2 instead of fetching the
+// records into several.
+__device__ __forceinline__ uint32_t xcd_order(uint32_t b, uint32_t groups) {
+    const uint32_t per = groups / 8, rem = groups % 8, x = b % 8, i = b / 8;
+    return x * per + min(x, rem) + i;
+}
+
 template <int KIND, bool LDSX>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ descs,
                                                    const uint32_t *__restrict__ map, GemvDesc one, uint32_t count,
                                                    uint32_t tasks, uint32_t tasks_per_wave, uint32_t lds_blocks) {
     const int lane = threadIdx.x % 64;
     // wave-uniform (readfirstlane): descriptor reads are scalar loads
-    const uint32_t wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const uint32_t wave = xcd_order(blockIdx.x, gridDim.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t t0 = wave * tasks_per_wave;
     if (t0 >= tasks) return;
     const uint32_t t1 = min(tasks, t0 + tasks_per_wave);
