@@ -131,9 +131,17 @@ __device__ __forceinline__ uint32_t f16x2_add(uint32_t w, _Float16 bias) {
     const f16x2 v = __builtin_bit_cast(f16x2, w) + f16x2{bias, bias};
     return __builtin_bit_cast(uint32_t, v);
 }
-// Q4_0: nibbles under the f16 exponent of 1024, minus 1032 = nibble - 8 (exact)
-__device__ __forceinline__ uint32_t q4_pair(uint32_t v) {
-    return f16x2_add((v & 0x000f000fu) | 0x64006400u, (_Float16)-1032.0f);
+// (v & m) | c in one instruction (the compiler splits it in two: this target's three-operand
+// encoding takes no literal constants, so m comes in a scalar register and c in a vector one)
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(m), "v"(c));
+    return r;
+}
+// Q4_0: nibbles under the f16 exponent of 1024, minus 1032 = nibble - 8 (exact); magic holds
+// 0x64006400
+__device__ __forceinline__ uint32_t q4_pair(uint32_t v, uint32_t magic) {
+    return f16x2_add(and_or(v, 0x000f000fu, magic), (_Float16)-1032.0f);
 }
 // Q8_0: bytes (0, 2) or (1, 3) of w ^ 0x80808080 under the exponent of 1024, minus 1152 = q
 __device__ __forceinline__ uint32_t q8_pair(uint32_t t, uint32_t sel) {
@@ -159,6 +167,8 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
     // x rows of a batch in LDS, block by block (row stride 144 bytes: the eight lanes that read
     // together hit distinct banks)
     __shared__ __attribute__((aligned(16))) _Float16 sx[2][kKB * R * kXRec];
+    // the A rows past the row capacity (lanes r >= R of a single x tile) read this zero row
+    __shared__ __attribute__((aligned(16))) _Float16 zrow[kXRec];
 
     const int tid = threadIdx.x, lane = tid % 64, r = lane % 32, h = lane / 32;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
@@ -166,6 +176,12 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
     // 32 r, half h at + 16 h), scales (row r's run of eight blocks at 16 r)
     const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * h) : (uint32_t)(lane * 16);
     const uint32_t os = (uint32_t)(r * 16);
+    if (R < 32) {
+        for (int i = tid; i < kXRec / 8; i += 256) *(u32x4 *)&zrow[8 * i] = u32x4{0u, 0u, 0u, 0u};
+        // (the first batch's barrier orders these stores before any read)
+    }
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));  // kept in a vector register for and_or
 
     for (uint32_t task = blockIdx.x; task < tasks; task += gridDim.x) {
         const uint32_t p = map ? map[task] : 0;
@@ -234,6 +250,7 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
         constexpr int G0 = RG;  // groups kept in x tile 0 (tile 1, when there is one, keeps all four)
 
         auto compute = [&](const L &ld, int buf) {
+            decltype(__builtin_amdgcn_permlane32_swap(0u, 0u, false, false)) sw0[kTW], sw1[kTW];  // Q4_0 pair swaps
 #pragma unroll
             for (int kb = 0; kb < kKB; kb++) {
                 // B fragments: step 0 and step 1 of block kb for each tile
@@ -253,13 +270,16 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
                     } else {
                         // lane r holds block 2i of row r, lane 32 + r block 2i + 1; swapping the
                         // upper lanes' dwords 0, 1 with the lower lanes' 2, 3 gives each lane half h
-                        // bytes 8h .. 8h + 7 of both blocks
-                        const u32x4 q = ld.q[j][kb / 2];
-                        const auto s0 = __builtin_amdgcn_permlane32_swap(q[0], q[2], false, false);
-                        const auto s1 = __builtin_amdgcn_permlane32_swap(q[1], q[3], false, false);
-                        const uint32_t w0 = kb % 2 ? s0[1] : s0[0], w1 = kb % 2 ? s1[1] : s1[0];
-                        b0 = u32x4{q4_pair(w0), q4_pair(w0 >> 8), q4_pair(w1), q4_pair(w1 >> 8)};
-                        b1 = u32x4{q4_pair(w0 >> 4), q4_pair(w0 >> 12), q4_pair(w1 >> 4), q4_pair(w1 >> 12)};
+                        // bytes 8h .. 8h + 7 of both blocks (one swap serves the pair)
+                        if (kb % 2 == 0) {
+                            const u32x4 q = ld.q[j][kb / 2];
+                            sw0[j] = __builtin_amdgcn_permlane32_swap(q[0], q[2], false, false);
+                            sw1[j] = __builtin_amdgcn_permlane32_swap(q[1], q[3], false, false);
+                        }
+                        const uint32_t w0 = kb % 2 ? sw0[j][1] : sw0[j][0], w1 = kb % 2 ? sw1[j][1] : sw1[j][0];
+                        b0 = u32x4{q4_pair(w0, magic), q4_pair(w0 >> 8, magic), q4_pair(w1, magic), q4_pair(w1 >> 8, magic)};
+                        b1 = u32x4{q4_pair(w0 >> 4, magic), q4_pair(w0 >> 12, magic), q4_pair(w1 >> 4, magic),
+                                   q4_pair(w1 >> 12, magic)};
                     }
                     bf[j][0] = __builtin_bit_cast(f16x8, b0);
                     bf[j][1] = __builtin_bit_cast(f16x8, b1);
@@ -269,14 +289,11 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
                 for (int i = 0; i < MT; i++) {
                     // A fragments: x row i 32 + r (rows past the row capacity are zero)
                     const int xr_row = i * 32 + r;
-                    f16x8 a0 = {}, a1 = {}, l0 = {}, l1 = {};
-                    if (R >= 32 || xr_row < R) {
-                        const _Float16 *row = &sx[buf][(kb * R + xr_row) * kXRec];
-                        a0 = *(const f16x8 *)(row + 8 * h);
-                        a1 = *(const f16x8 *)(row + 16 + 8 * h);
-                        l0 = *(const f16x8 *)(row + 32 + 8 * h);
-                        l1 = *(const f16x8 *)(row + 48 + 8 * h);
-                    }
+                    const _Float16 *row = (R >= 32 || xr_row < R) ? &sx[buf][(kb * R + xr_row) * kXRec] : zrow;
+                    const f16x8 a0 = *(const f16x8 *)(row + 8 * h);
+                    const f16x8 a1 = *(const f16x8 *)(row + 16 + 8 * h);
+                    const f16x8 l0 = *(const f16x8 *)(row + 32 + 8 * h);
+                    const f16x8 l1 = *(const f16x8 *)(row + 48 + 8 * h);
 #pragma unroll
                     for (int j = 0; j < kTW; j++) {
                         f32x16 pp = {};
