@@ -387,53 +387,131 @@ __global__ __launch_bounds__(kThreads) void planes_to_gguf_kernel(const uint8_t 
 // adjacent columns of rows 8rg..8rg+7 of the block row, so each load instruction moves four
 // 256-byte row segments (16 bytes a lane) and a column's block spans lanes cq, cq+16, cq+32,
 // cq+48, whose maxima meet by two lane exchanges. VEC: columns a multiple of 4 and 16-byte
-// aligned buffers (f32x4 loads and stores); otherwise one guarded f32 per column.
+// aligned buffers (f32x4 loads and stores); otherwise one guarded f32 per column. Task t of a
+// matrix of cg = ceil(n / 64) column groups is block row t / cg, column group t % cg; the whole
+// wavefront runs it (the lane exchanges need every lane).
+template <bool VEC>
+__device__ __forceinline__ void snap_cols_task(const float *__restrict__ src, float *__restrict__ dst, size_t n,
+                                               size_t cg, size_t t, int lane) {
+    const int cq = lane % 16, rg = lane / 16;
+    const size_t c0 = (t % cg) * 64 + 4 * cq;
+    const size_t at = (t / cg * 32 + (size_t)rg * 8) * n + c0;  // row 0 of this lane's rows
+    f32x4 v[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        if constexpr (VEC) {
+            v[r] = c0 < n ? __builtin_nontemporal_load((const f32x4 *)(src + at + r * n)) : f32x4{0.f, 0.f, 0.f, 0.f};
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[r][i] = c0 + i < n ? src[at + r * n + i] : 0.0f;
+        }
+    }
+    f32x4 amax = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 8; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) amax[i] = fmaxf(amax[i], fabsf(v[r][i]));
+    f32x4 id, dh;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float a = fmaxf(amax[i], __shfl_xor(amax[i], 16));
+        a = fmaxf(a, __shfl_xor(a, 32));
+        const float d = a / 127.0f;
+        id[i] = d != 0.0f ? 1.0f / d : 0.0f;
+        dh[i] = half_bits_to_float(float_to_half_bits(d));
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        f32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = dh[i] * (float)round_sat_i8(v[r][i] * id[i]);
+        if constexpr (VEC) {
+            if (c0 < n) __builtin_nontemporal_store(o, (f32x4 *)(dst + at + r * n));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (c0 + i < n) dst[at + r * n + i] = o[i];
+        }
+    }
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void snap_cols_kernel(const float *__restrict__ src,
                                                              float *__restrict__ dst, size_t k,
                                                              size_t n) {
-    const int lane = threadIdx.x % 64, cq = lane % 16, rg = lane / 16;
     const size_t cg = (n + 63) / 64, tasks = k / 32 * cg;
     const size_t waves = (size_t)gridDim.x * (kThreads / 64);
-    for (size_t t = (size_t)blockIdx.x * (kThreads / 64) + threadIdx.x / 64; t < tasks; t += waves) {
-        const size_t c0 = (t % cg) * 64 + 4 * cq;
-        const size_t at = (t / cg * 32 + (size_t)rg * 8) * n + c0;  // row 0 of this lane's rows
-        f32x4 v[8];
+    for (size_t t = (size_t)blockIdx.x * (kThreads / 64) + threadIdx.x / 64; t < tasks; t += waves)
+        snap_cols_task<VEC>(src, dst, n, cg, t, (int)(threadIdx.x % 64));
+}
+
+// ---- a grouped snap pass (fh_snap_plan_*): every problem's wavefront tasks in one launch ----
+constexpr uint32_t kSnapVec = 0x100;  // mode flag: a column snap that takes the f32x4 form
+constexpr uint32_t kRowsTaskBlocks = 8 * kUnroll;  // rows snap: blocks per wavefront task
+constexpr uint32_t kCopyTask = 1024;               // copy: floats per wavefront task
+
+// The descriptor as wave-uniform values (every dword through readfirstlane).
+__device__ __forceinline__ SnapDesc uniform_snap_desc(const SnapDesc *descs, uint32_t p) {
+    constexpr int W = sizeof(SnapDesc) / 4;
+    static_assert(sizeof(SnapDesc) % 4 == 0, "descriptor of whole dwords");
+    struct Words {
+        uint32_t w[W];
+    };
+    Words v = __builtin_bit_cast(Words, descs[p]);
 #pragma unroll
-        for (int r = 0; r < 8; r++) {
-            if constexpr (VEC) {
-                v[r] = c0 < n ? __builtin_nontemporal_load((const f32x4 *)(src + at + r * n))
-                              : f32x4{0.f, 0.f, 0.f, 0.f};
-            } else {
+    for (int i = 0; i < W; i++) v.w[i] = __builtin_amdgcn_readfirstlane(v.w[i]);
+    return __builtin_bit_cast(SnapDesc, v);
+}
+
+__global__ __launch_bounds__(kThreads) void snap_group_kernel(const SnapDesc *__restrict__ descs, uint32_t count,
+                                                              uint32_t tasks) {
+    const int lane = threadIdx.x % 64;
+    const uint32_t waves = gridDim.x * (kThreads / 64);
+    for (uint32_t t = __builtin_amdgcn_readfirstlane(blockIdx.x * (kThreads / 64) + threadIdx.x / 64); t < tasks;
+         t += waves) {
+        // the problem holding task t: the last one whose first task is at most t
+        uint32_t lo = 0, hi = count;
+        while (hi - lo > 1) {
+            const uint32_t mid = (lo + hi) / 2;
+            if (__builtin_amdgcn_readfirstlane(descs[mid].task0) <= t)
+                lo = mid;
+            else
+                hi = mid;
+        }
+        const SnapDesc d = uniform_snap_desc(descs, lo);
+        const uint32_t lt = t - d.task0;
+        if ((d.mode & 0xff) == FH_SNAP_COLS) {
+            const size_t cg = (d.n + 63) / 64;
+            if (d.mode & kSnapVec)
+                snap_cols_task<true>(d.src, d.dst, d.n, cg, lt, lane);
+            else
+                snap_cols_task<false>(d.src, d.dst, d.n, cg, lt, lane);
+        } else if ((d.mode & 0xff) == FH_SNAP_ROWS) {
+            // kUnroll groups of eight blocks, eight lanes a block (the rows snap's wavefront step)
+            const size_t nblocks = d.len / 32, g0 = (size_t)lt * kUnroll;
+            f32x4 v[kUnroll];
 #pragma unroll
-                for (int i = 0; i < 4; i++) v[r][i] = c0 + i < n ? src[at + r * n + i] : 0.0f;
+            for (int u = 0; u < kUnroll; u++) {
+                const size_t blk = (g0 + u) * 8 + lane / 8;
+                v[u] = blk < nblocks ? __builtin_nontemporal_load((const f32x4 *)d.src + blk * 8 + lane % 8)
+                                     : f32x4{0.f, 0.f, 0.f, 0.f};
             }
-        }
-        f32x4 amax = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 8; r++)
+            for (int u = 0; u < kUnroll; u++) {
+                int32_t q[4];
+                uint32_t h;
+                quantise4<FH_Q8_0>(v[u], lane, q, h);
+                const float dd = half_bits_to_float(h);
+                const f32x4 o = {dd * (float)q[0], dd * (float)q[1], dd * (float)q[2], dd * (float)q[3]};
+                const size_t blk = (g0 + u) * 8 + lane / 8;
+                if (blk < nblocks) __builtin_nontemporal_store(o, (f32x4 *)d.dst + blk * 8 + lane % 8);
+            }
+        } else {
+            const size_t base = (size_t)lt * kCopyTask;
 #pragma unroll
-            for (int i = 0; i < 4; i++) amax[i] = fmaxf(amax[i], fabsf(v[r][i]));
-        f32x4 id, dh;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float a = fmaxf(amax[i], __shfl_xor(amax[i], 16));
-            a = fmaxf(a, __shfl_xor(a, 32));
-            const float d = a / 127.0f;
-            id[i] = d != 0.0f ? 1.0f / d : 0.0f;
-            dh[i] = half_bits_to_float(float_to_half_bits(d));
-        }
-#pragma unroll
-        for (int r = 0; r < 8; r++) {
-            f32x4 o;
-#pragma unroll
-            for (int i = 0; i < 4; i++) o[i] = dh[i] * (float)round_sat_i8(v[r][i] * id[i]);
-            if constexpr (VEC) {
-                if (c0 < n) __builtin_nontemporal_store(o, (f32x4 *)(dst + at + r * n));
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (c0 + i < n) dst[at + r * n + i] = o[i];
+            for (int i = 0; i < (int)(kCopyTask / 64); i++) {
+                const size_t e = base + (size_t)i * 64 + lane;
+                if (e < d.len) d.dst[e] = d.src[e];
             }
         }
     }
@@ -553,6 +631,22 @@ hipError_t launch_copy_f32(hipStream_t s, const float *src, float *dst, size_t n
 
 hipError_t launch_decode_f16(hipStream_t s, const uint16_t *src, float *dst, size_t n) {
     decode_f16_kernel<<<grid_for(n, kThreads * 4, 16384), kThreads, 0, s>>>(src, dst, n);
+    return hipGetLastError();
+}
+
+uint32_t snap_tasks(const SnapDesc &d) {
+    switch (d.mode & 0xff) {
+    case FH_SNAP_COLS: return (uint32_t)(d.k / 32 * ((d.n + 63) / 64));
+    case FH_SNAP_ROWS: return (uint32_t)((d.len / 32 + kRowsTaskBlocks - 1) / kRowsTaskBlocks);
+    default: return (uint32_t)((d.len + kCopyTask - 1) / kCopyTask);
+    }
+}
+
+hipError_t launch_snap_group(hipStream_t s, const SnapDesc *descs, uint32_t count, uint32_t tasks, int cus) {
+    if (!count || !tasks) return hipSuccess;
+    // every wavefront the chip holds at once (eight workgroups of four per CU), each a strided share
+    const unsigned g = grid_for(tasks, kThreads / 64, (unsigned)(cus > 0 ? cus : 256) * 8);
+    snap_group_kernel<<<g, kThreads, 0, s>>>(descs, count, tasks);
     return hipGetLastError();
 }
 

@@ -130,6 +130,17 @@ hipError_t launch_encode_cols(hipStream_t s, fh_kind kind, const float *w, uint8
 hipError_t launch_decode_cols(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, float *w,
                               size_t k, size_t n);
 hipError_t launch_snap_rows(hipStream_t s, const float *src, float *dst, size_t nblocks);
+// A grouped snap pass: one descriptor per problem (mode FH_SNAP_ROWS / COLS / COPY after the
+// host's fallbacks), task0 = its first wavefront task; tasks = the launch's total.
+struct SnapDesc {
+    const float *src;
+    float *dst;
+    uint64_t len;  // floats
+    uint32_t k, n;  // COLS: rows_in, cols_out
+    uint32_t mode, task0;
+};
+uint32_t snap_tasks(const SnapDesc &d);
+hipError_t launch_snap_group(hipStream_t s, const SnapDesc *descs, uint32_t count, uint32_t tasks, int cus);
 hipError_t launch_snap_cols(hipStream_t s, const float *src, float *dst, size_t rows_in,
                             size_t cols_out);
 hipError_t launch_copy_f32(hipStream_t s, const float *src, float *dst, size_t n);

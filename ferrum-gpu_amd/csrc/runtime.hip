@@ -1065,4 +1065,98 @@ fh_status fh_q8_snap_cols(fh_device *dev, const fh_buffer *src, fh_buffer *dst, 
     return end_command(dev, "q8_snap");
 }
 
+// ---- grouped snap pass ----
+
+}  // extern "C"
+
+struct fh_snap_plan {
+    fh_device *dev = nullptr;
+    SnapDesc *descs = nullptr;  // device array
+    uint32_t count = 0, tasks = 0;
+    uint64_t bytes = 0;
+};
+
+extern "C" {
+
+fh_status fh_snap_plan_create(fh_device *dev, const fh_snap_problem *problems, size_t count, fh_snap_plan **out) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!out || (count && !problems)) return fail(FH_ERR_INVALID, "snap plan: null argument");
+    *out = nullptr;
+    std::vector<SnapDesc> host;
+    host.reserve(count);
+    uint64_t tasks = 0, bytes = 0;
+    for (size_t i = 0; i < count; i++) {
+        const fh_snap_problem &p = problems[i];
+        if (p.len && (!p.src || !p.dst))
+            return fail(FH_ERR_INVALID, "snap plan: problem %zu has a null pointer", i);
+        if (p.len > ((size_t)1 << 36))
+            return fail(FH_ERR_INVALID, "snap plan: problem %zu holds too many values (%zu)", i, p.len);
+        SnapDesc d{p.src, p.dst, (uint64_t)p.len, 0, 0, FH_SNAP_COPY, 0};
+        switch (p.mode) {
+        case FH_SNAP_ROWS:  // q8_snap_rows' fallback: ne0 or the length not whole blocks copies
+            if (p.a && p.a % QK == 0 && p.len % QK == 0) d.mode = FH_SNAP_ROWS;
+            break;
+        case FH_SNAP_COLS:
+            if (p.len != p.a * p.b)
+                return fail(FH_ERR_INVALID, "snap plan: problem %zu: %zu elements is not %zu x %zu", i, p.len, p.a, p.b);
+            if (p.a && p.a % QK == 0) {  // q8_snap_cols' fallback: rows_in not whole blocks copies
+                if (p.a >= (1ull << 32) || p.b >= (1ull << 32))
+                    return fail(FH_ERR_INVALID, "snap plan: problem %zu is too large", i);
+                d.mode = FH_SNAP_COLS;
+                d.k = (uint32_t)p.a;
+                d.n = (uint32_t)p.b;
+                if (p.b % 4 == 0 && ((uintptr_t)p.src | (uintptr_t)p.dst) % 16 == 0) d.mode |= 0x100;  // f32x4 form
+            }
+            break;
+        case FH_SNAP_COPY: break;
+        default: return fail(FH_ERR_INVALID, "snap plan: problem %zu has mode %d", i, p.mode);
+        }
+        if (!p.len) continue;
+        d.task0 = (uint32_t)tasks;
+        tasks += snap_tasks(d);
+        if (tasks >= (1ull << 31)) return fail(FH_ERR_INVALID, "snap plan: too many values for one launch");
+        bytes += 8ull * p.len;
+        host.push_back(d);
+    }
+    fh_snap_plan *plan = new (std::nothrow) fh_snap_plan;
+    if (!plan) return fail(FH_ERR_OOM, "host out of memory");
+    dev_retain(dev);
+    plan->dev = dev;
+    plan->count = (uint32_t)host.size();
+    plan->tasks = (uint32_t)tasks;
+    plan->bytes = bytes;
+    if (!host.empty()) {
+        void *p = nullptr;
+        if ((st = alloc_bytes(dev, host.size() * sizeof(SnapDesc), &p)) ||
+            (plan->descs = (SnapDesc *)p,
+             (st = upload_bytes(dev, p, host.data(), host.size() * sizeof(SnapDesc), "snap plan")))) {
+            fh_snap_plan_free(plan);
+            return st;
+        }
+    }
+    *out = plan;
+    return FH_OK;
+}
+
+fh_status fh_snap_plan_run(fh_device *dev, const fh_snap_plan *plan) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!plan || plan->dev != dev) return fail(FH_ERR_INVALID, "snap plan: wrong device");
+    if (!plan->count) return FH_OK;
+    if ((st = begin_command(dev, "snap plan"))) return st;
+    (void)launch_snap_group(dev->stream, plan->descs, plan->count, plan->tasks, dev->cus);
+    return end_command(dev, "snap plan");
+}
+
+uint64_t fh_snap_plan_bytes(const fh_snap_plan *plan) { return plan ? plan->bytes : 0; }
+
+void fh_snap_plan_free(fh_snap_plan *plan) {
+    if (!plan) return;
+    fh_device *dev = plan->dev;
+    if (plan->descs) free_bytes(dev, plan->descs);
+    delete plan;
+    dev_release(dev);
+}
+
 }  // extern "C"

@@ -137,6 +137,10 @@ def lib() -> ctypes.CDLL:
         "fh_rows_plan_launches": (S, [P]),
         "fh_rows_plan_bytes": (U64, [P]),
         "fh_rows_plan_free": (None, [P]),
+        "fh_snap_plan_create": (I, [P, P, S, PP]),
+        "fh_snap_plan_run": (I, [P, P]),
+        "fh_snap_plan_bytes": (U64, [P]),
+        "fh_snap_plan_free": (None, [P]),
         "fh_q8_snap_rows": (I, [P, P, P, S]),
         "fh_q8_snap_cols": (I, [P, P, P, S, S]),
         "fh_ggml_nbytes": (I, [U32, U64, ctypes.POINTER(U64)]),
@@ -563,6 +567,59 @@ class RowsPlan:
     def free(self) -> None:
         if self._h:
             lib().fh_rows_plan_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+SNAP_ROWS, SNAP_COLS, SNAP_COPY = 0, 1, 2
+
+
+class _SnapProblem(ctypes.Structure):
+    _fields_ = [("src", ctypes.c_void_p), ("dst", ctypes.c_void_p), ("len", ctypes.c_size_t), ("a", ctypes.c_size_t),
+                ("b", ctypes.c_size_t), ("mode", ctypes.c_int)]
+
+
+class SnapPlan:
+    """A whole QAT snap pass in one launch (GpuTrainer::record_snap's loop of q8_snap_rows /
+    q8_snap_cols / copy calls, ferrum_wgpu/src/training/gpt2/qat.rs:58-72). problems: (mode,
+    src, dst, shape), src and dst GpuBufs of one length; shape is ne0 for SNAP_ROWS,
+    (rows_in, cols_out) for SNAP_COLS and ignored for SNAP_COPY; the single calls' fallbacks
+    apply. No counterpart in the reference as one launch."""
+
+    def __init__(self, gpu: Gpu, problems):
+        arr = (_SnapProblem * max(len(problems), 1))()
+        self._keep = []
+        for i, (mode, src, dst, shape) in enumerate(problems):
+            n = src.len()
+            if dst.len() != n:
+                raise GpuError(f"snap plan: problem {i}: source holds {n} elements but destination {dst.len()}")
+            self._keep += [src, dst]
+            if mode == SNAP_COLS:
+                a, b = shape
+            elif mode == SNAP_ROWS:
+                a, b = shape, 0
+            else:
+                a, b = 0, 0
+            arr[i] = _SnapProblem(src.device_ptr(), dst.device_ptr(), n, a, b, mode)
+        self.gpu = gpu
+        h = ctypes.c_void_p()
+        _check(lib().fh_snap_plan_create(gpu.handle, ctypes.cast(arr, ctypes.c_void_p), len(problems), ctypes.byref(h)))
+        self._h = h
+
+    def run(self) -> None:
+        _check(lib().fh_snap_plan_run(self.gpu.handle, self._h))
+
+    def bytes(self) -> int:
+        return lib().fh_snap_plan_bytes(self._h)
+
+    def free(self) -> None:
+        if self._h:
+            lib().fh_snap_plan_free(self._h)
             self._h = None
 
     def __del__(self):

@@ -252,6 +252,29 @@ FH_API fh_status fh_q8_snap_rows(fh_device *dev, const fh_buffer *src, fh_buffer
 FH_API fh_status fh_q8_snap_cols(fh_device *dev, const fh_buffer *src, fh_buffer *dst, size_t rows_in,
                           size_t cols_out);
 
+/* A whole QAT snap pass in one launch: replaces the loop of GpuTrainer::record_snap
+ * (ferrum_wgpu/src/training/gpt2/qat.rs:58-72), which records one q8_snap_rows / q8_snap_cols /
+ * copy per parameter. Each problem is one of those calls on device pointers of len floats:
+ * FH_SNAP_ROWS (a = ne0), FH_SNAP_COLS (a = rows_in, b = cols_out, len = a * b) or FH_SNAP_COPY;
+ * the same fallbacks apply (a rows snap whose ne0 or len is not whole 32-blocks, or a column snap
+ * whose rows_in is not, copies). Built once, run any number of times; every problem shares one
+ * launch, bit-identical to its single call. */
+typedef enum fh_snap_mode { FH_SNAP_ROWS = 0, FH_SNAP_COLS = 1, FH_SNAP_COPY = 2 } fh_snap_mode;
+typedef struct fh_snap_problem {
+    const float *src;
+    float *dst;
+    size_t len;
+    size_t a, b;
+    int mode; /* fh_snap_mode */
+} fh_snap_problem;
+typedef struct fh_snap_plan fh_snap_plan;
+FH_API fh_status fh_snap_plan_create(fh_device *dev, const fh_snap_problem *problems, size_t count,
+                                     fh_snap_plan **out);
+FH_API fh_status fh_snap_plan_run(fh_device *dev, const fh_snap_plan *plan);
+/* Bytes one run reads and writes (8 per value). */
+FH_API uint64_t fh_snap_plan_bytes(const fh_snap_plan *plan);
+FH_API void fh_snap_plan_free(fh_snap_plan *plan);
+
 /* ---- GGUF v3 container (ferrum_gguf/src/io/reader.rs:167-322) ----
  * Replaces ferrum_gguf::Gguf. The parser is hostile-input safe: every read is bounds-checked,
  * sizes use checked arithmetic, and nothing is allocated from a header count before the count is

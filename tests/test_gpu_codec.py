@@ -192,3 +192,72 @@ def test_shape_errors_and_faults_are_reported(fh, g):
     assert g.sweep_faults(lambda: fh.q8_snap_cols(g, a, c, (32, 2))) == 1
     assert g.sweep_faults(lambda: fh.q8_snap_rows(g, a, c, 32)) == 1
     assert g.sweep_faults(lambda: fh.q8_snap_rows(g, a, c, 8)) == 1
+
+
+# ---- grouped snap pass (fh_snap_plan_*, GpuTrainer::record_snap's loop in one launch) ----
+
+def test_snap_plan_equals_the_single_calls_bit_for_bit(fh, g, orc):
+    """Every mode and fallback in one plan: column snaps in the f32x4 form (cols a multiple of
+    4) and the per-column form (7, 33 and 301 columns), row snaps, row snaps and column snaps whose
+    shapes are not whole blocks (copied, as the single calls do), plain copies of odd lengths."""
+    cases = [(fh.SNAP_COLS, (64, 32)), (fh.SNAP_COLS, (32, 7)), (fh.SNAP_COLS, (96, 33)), (fh.SNAP_COLS, (256, 300)),
+             (fh.SNAP_COLS, (64, 301)), (fh.SNAP_ROWS, 32), (fh.SNAP_ROWS, 8), (fh.SNAP_COLS, (8, 5)),
+             (fh.SNAP_COPY, None), (fh.SNAP_ROWS, 64), (fh.SNAP_COLS, (2048, 256))]
+    sizes = [64 * 32, 32 * 7, 96 * 33, 256 * 300, 64 * 301, 32 * 1000, 8 * 13, 8 * 5, 1237, 64 * 77, 2048 * 256]
+    probs, want = [], []
+    for i, ((mode, shape), n) in enumerate(zip(cases, sizes)):
+        data = nasty(orc, n) if n % 32 == 0 else (orc.rand_vec(n, 40 + i) * np.float32(3)).astype(np.float32)
+        src, dst, one = g.upload(data), g.zeros(n), g.zeros(n)
+        if mode == fh.SNAP_COLS:
+            fh.q8_snap_cols(g, src, one, shape)
+        elif mode == fh.SNAP_ROWS:
+            fh.q8_snap_rows(g, src, one, shape)
+        else:
+            g.copy_f32(src, 0, one, 0, n)
+        probs.append((mode, src, dst, shape))
+        want.append((dst, g.read(one), data, mode, shape))
+    plan = fh.SnapPlan(g, probs)
+    assert plan.bytes() == 8 * sum(sizes)
+    for rep in range(2):
+        plan.run()
+        for dst, single, data, mode, shape in want:
+            got = g.read(dst)
+            assert np.array_equal(bits(got), bits(single)), (mode, shape, rep)
+            if mode == fh.SNAP_COLS and shape[0] % 32 == 0:
+                assert np.array_equal(bits(got), bits(orc.snap_cols(data, *shape))), shape
+            elif mode == fh.SNAP_ROWS and shape % 32 == 0 and data.size % 32 == 0:
+                assert np.array_equal(bits(got), bits(orc.snap_rows(data, shape))), shape
+            else:
+                assert np.array_equal(bits(got), bits(data)), (mode, shape)
+    plan.free()
+
+
+def test_snap_plan_runs_the_tinyllama_qat_pass(fh, g, orc):
+    """Config 5's QAT fake-quant pass as one launch: the column snap of two blocks' worth of
+    TinyLlama-1.1B matrices (seven shapes each), bit-exact with the oracle's snap_cols."""
+    rng = np.random.default_rng(12)
+    shapes = [(2048, 2048), (2048, 256), (2048, 256), (2048, 2048), (2048, 5632), (2048, 5632), (5632, 2048)]
+    probs, checks = [], []
+    for a, b in shapes:
+        w = (rng.standard_normal(a * b) * 0.02).astype(np.float32)
+        want = orc.snap_cols(w, a, b)
+        for _ in range(2):
+            src, dst = g.upload(w), g.zeros(a * b)
+            probs.append((fh.SNAP_COLS, src, dst, (a, b)))
+            checks.append((dst, want))
+    plan = fh.SnapPlan(g, probs)
+    plan.run()
+    for dst, want in checks:
+        assert np.array_equal(g.read(dst).view(np.uint32), want.view(np.uint32))
+    plan.free()
+
+
+def test_snap_plan_refusals(fh, g):
+    a, b = g.zeros(64), g.zeros(64)
+    with pytest.raises(fh.GpuError, match="is not 32 x 3"):
+        fh.SnapPlan(g, [(fh.SNAP_COLS, a, b, (32, 3))])
+    with pytest.raises(fh.GpuError, match="has mode 7"):
+        fh.SnapPlan(g, [(7, a, b, 0)])
+    with pytest.raises(fh.GpuError, match="destination"):
+        fh.SnapPlan(g, [(fh.SNAP_ROWS, a, g.zeros(32), 32)])
+    fh.SnapPlan(g, [(fh.SNAP_ROWS, a, b, 32)]).run()  # the device still works
