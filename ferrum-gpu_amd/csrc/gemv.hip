@@ -164,130 +164,150 @@ __device__ __forceinline__ uint32_t xcd_order(uint32_t b, uint32_t groups) {
     return x * per + min(x, rem) + i;
 }
 
+// Prepared-x jobs another launch of the same plan needs (run by this launch's workgroups before
+// their own tasks: that launch starts only after this one ends, and this one reads none of them):
+// job j prepares blocks 32 (j % py) .. + 31 of product j / py of descs.
+struct PrepJobs {
+    const GemvDesc *descs;
+    uint32_t count, py;
+};
+
 template <int KIND, bool LDSX>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvDesc *__restrict__ descs,
                                                    const uint32_t *__restrict__ map, GemvDesc one, uint32_t count,
-                                                   uint32_t tasks, uint32_t tasks_per_wave, uint32_t lds_blocks) {
+                                                   uint32_t tasks, uint32_t tasks_per_wave, uint32_t lds_blocks,
+                                                   PrepJobs jobs) {
     const int lane = threadIdx.x % 64;
     // wave-uniform (readfirstlane): descriptor reads are scalar loads
     const uint32_t wave = xcd_order(blockIdx.x, gridDim.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const uint32_t t0 = wave * tasks_per_wave;
-    if (t0 >= tasks) return;
-    const uint32_t t1 = min(tasks, t0 + tasks_per_wave);
-    const int r = lane % 32;
-    const bool upper = lane >= 32;
-    // Q4_0: block pair chunk of 1 KiB, lane l at 16 l; Q8_0: block tile of 1 KiB, row r at 32 r;
-    // scales: row r's eight at 16 r; prepared x: prep_a_offset, prep_tail_offset
-    const LaneOffsets o{KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16), (uint32_t)(r * 16),
-                        prep_a_offset(lane), prep_tail_offset<KIND>(lane)};
-    // The wavefront's tasks are one stream of batches: the loads of the next batch (of this task
-    // or the next) are in flight while a batch is computed, so the pipeline never drains at a
-    // task boundary. lp is the batch being loaded, cp the batch being computed.
-    Cursor cur{descs, count, tasks, 0, 0, {}};
-    cur.seek(t0, map, one);
-    // With LDSX the wavefront prepares its product's x into its LDS region (all of it, padded
-    // with zero records to a multiple of eight blocks), whenever it starts a product; the
-    // batch in flight already holds its own x in registers, so the region can be rewritten.
-    const uint32_t lds_base = (threadIdx.x / 64) * lds_blocks * kPrepBytes;
-    auto prepare = [&](const GemvDesc &d) {
-        if constexpr (LDSX) {
-            const bool aligned = ((uintptr_t)d.x & 15) == 0;
-            const uint32_t nb8 = (d.nb + 7) / 8 * 8;
-            for (uint32_t b = lane / 8; b < nb8; b += 8) {
-                __attribute__((address_space(3))) uint32_t *rec =
-                    (__attribute__((address_space(3))) uint32_t *)&gemv_lds[lds_base + b * kPrepBytes];
-                if (b < d.nb) {
-                    prep_block<KIND>(d.x, aligned, b, lane % 8, rec);
-                } else {
-                    zero_record(lane % 8, rec);  // padding records
+    // the wavefront's tasks (waves past the last task have none), then its workgroup's share of
+    // the preparation jobs: at the end, where they fill the launch's tail instead of delaying
+    // every workgroup's first loads
+    if (t0 < tasks) {
+        const uint32_t t1 = min(tasks, t0 + tasks_per_wave);
+        const int r = lane % 32;
+        const bool upper = lane >= 32;
+        // Q4_0: block pair chunk of 1 KiB, lane l at 16 l; Q8_0: block tile of 1 KiB, row r at 32 r;
+        // scales: row r's eight at 16 r; prepared x: prep_a_offset, prep_tail_offset
+        const LaneOffsets o{KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16), (uint32_t)(r * 16),
+                            prep_a_offset(lane), prep_tail_offset<KIND>(lane)};
+        // The wavefront's tasks are one stream of batches: the loads of the next batch (of this task
+        // or the next) are in flight while a batch is computed, so the pipeline never drains at a
+        // task boundary. lp is the batch being loaded, cp the batch being computed.
+        Cursor cur{descs, count, tasks, 0, 0, {}};
+        cur.seek(t0, map, one);
+        // With LDSX the wavefront prepares its product's x into its LDS region (all of it, padded
+        // with zero records to a multiple of eight blocks), whenever it starts a product; the
+        // batch in flight already holds its own x in registers, so the region can be rewritten.
+        const uint32_t lds_base = (threadIdx.x / 64) * lds_blocks * kPrepBytes;
+        auto prepare = [&](const GemvDesc &d) {
+            if constexpr (LDSX) {
+                const bool aligned = ((uintptr_t)d.x & 15) == 0;
+                const uint32_t nb8 = (d.nb + 7) / 8 * 8;
+                for (uint32_t b = lane / 8; b < nb8; b += 8) {
+                    __attribute__((address_space(3))) uint32_t *rec =
+                        (__attribute__((address_space(3))) uint32_t *)&gemv_lds[lds_base + b * kPrepBytes];
+                    if (b < d.nb) {
+                        prep_block<KIND>(d.x, aligned, b, lane % 8, rec);
+                    } else {
+                        zero_record(lane % 8, rec);  // padding records
+                    }
                 }
             }
-        }
-    };
-    prepare(cur.d);
-    Task<KIND> ltk;
-    Pos lp{t0, 0, t0 - cur.d.task0, cur.d.n, cur.d.nb, cur.d.y};
-    ltk.set(cur.d, lp.g);
-    auto advance = [&]() {
-        lp.b += kBatch;
-        if (lp.b >= lp.nb) {
-            lp.t++;
-            lp.b = 0;
-            if (lp.t < t1) {
-                const uint32_t p0 = cur.p;
-                cur.advance(lp.t);
-                if (cur.p != p0) prepare(cur.d);
-                lp.g = lp.t - cur.d.task0;
-                lp.n = cur.d.n;
-                lp.nb = cur.d.nb;
-                lp.y = cur.d.y;
-                ltk.set(cur.d, lp.g);
-            } else {
-                ltk.clear(cur.d);  // the stream's end: the last loads fetch nothing
+        };
+        prepare(cur.d);
+        Task<KIND> ltk;
+        Pos lp{t0, 0, t0 - cur.d.task0, cur.d.n, cur.d.nb, cur.d.y};
+        ltk.set(cur.d, lp.g);
+        auto advance = [&]() {
+            lp.b += kBatch;
+            if (lp.b >= lp.nb) {
+                lp.t++;
+                lp.b = 0;
+                if (lp.t < t1) {
+                    const uint32_t p0 = cur.p;
+                    cur.advance(lp.t);
+                    if (cur.p != p0) prepare(cur.d);
+                    lp.g = lp.t - cur.d.task0;
+                    lp.n = cur.d.n;
+                    lp.nb = cur.d.nb;
+                    lp.y = cur.d.y;
+                    ltk.set(cur.d, lp.g);
+                } else {
+                    ltk.clear(cur.d);  // the stream's end: the last loads fetch nothing
+                }
             }
-        }
-    };
-    float acc = 0.0f;
-    __shared__ float stage_rows[4][kStage][32];
-    __shared__ StageMeta stage_meta[4][kStage];
-    const uint32_t wv = threadIdx.x / 64;
-    uint32_t staged = 0;  // wave-uniform
-    // Store the staged rows: lanes 0..31 take staged task 2i, lanes 32..63 task 2i + 1.
-    auto flush = [&]() {
-        for (uint32_t i = 0; i < staged; i += 2) {
-            const uint32_t s = i + (upper ? 1 : 0);
-            if (s < staged) {
-                const StageMeta m = stage_meta[wv][s];
-                const uint32_t row = m.row0 + r;
-                // (a global-address-space store: a flat store would also count against the
-                // scalar-load counter and make the next wait for loads a full drain)
-                if (row < m.n) ((__attribute__((address_space(1))) float *)m.y)[row] = stage_rows[wv][s][r];
+        };
+        float acc = 0.0f;
+        __shared__ float stage_rows[4][kStage][32];
+        __shared__ StageMeta stage_meta[4][kStage];
+        const uint32_t wv = threadIdx.x / 64;
+        uint32_t staged = 0;  // wave-uniform
+        // Store the staged rows: lanes 0..31 take staged task 2i, lanes 32..63 task 2i + 1.
+        auto flush = [&]() {
+            for (uint32_t i = 0; i < staged; i += 2) {
+                const uint32_t s = i + (upper ? 1 : 0);
+                if (s < staged) {
+                    const StageMeta m = stage_meta[wv][s];
+                    const uint32_t row = m.row0 + r;
+                    // (a global-address-space store: a flat store would also count against the
+                    // scalar-load counter and make the next wait for loads a full drain)
+                    if (row < m.n) ((__attribute__((address_space(1))) float *)m.y)[row] = stage_rows[wv][s][r];
+                }
             }
-        }
-        staged = 0;
-    };
-    // After computing batch cp: on a task's last batch, add the row's odd blocks (lane 32 + r) to
-    // its even ones (lane r) and stage the row.
-    auto finish = [&](const Pos &cp) {
-        if (cp.b + kBatch >= cp.nb) {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc), false, false);
-            const float sum = acc + __uint_as_float(upper ? sw[0] : sw[1]);
-            if (!upper) stage_rows[wv][staged][r] = sum;
-            if (lane == 0) stage_meta[wv][staged] = StageMeta{cp.y, cp.g * 32, cp.n};
-            acc = 0.0f;
-            if (++staged == kStage) flush();
-        }
-    };
-    Batch<KIND> b0, b1;
-    load_batch<KIND, LDSX>(b0, ltk, lp.b, o, lds_base);
-    Pos cp = lp;
-    advance();
-    // (scheduling barriers keep each batch's loads together, so a batch waits only for its own)
-    for (;;) {
-        load_batch<KIND, LDSX>(b1, ltk, lp.b, o, lds_base);
-        __builtin_amdgcn_sched_barrier(0);
-        if (cp.b + kBatch / 2 >= cp.nb)
-            compute_batch<KIND, kBatch / 4>(b0, upper, acc);  // a task's last half batch
-        else
-            compute_batch<KIND>(b0, upper, acc);
-        __builtin_amdgcn_sched_barrier(0);
-        finish(cp);
-        if (lp.t >= t1) break;
-        cp = lp;
-        advance();
+            staged = 0;
+        };
+        // After computing batch cp: on a task's last batch, add the row's odd blocks (lane 32 + r) to
+        // its even ones (lane r) and stage the row.
+        auto finish = [&](const Pos &cp) {
+            if (cp.b + kBatch >= cp.nb) {
+                const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc), false, false);
+                const float sum = acc + __uint_as_float(upper ? sw[0] : sw[1]);
+                if (!upper) stage_rows[wv][staged][r] = sum;
+                if (lane == 0) stage_meta[wv][staged] = StageMeta{cp.y, cp.g * 32, cp.n};
+                acc = 0.0f;
+                if (++staged == kStage) flush();
+            }
+        };
+        Batch<KIND> b0, b1;
         load_batch<KIND, LDSX>(b0, ltk, lp.b, o, lds_base);
-        __builtin_amdgcn_sched_barrier(0);
-        if (cp.b + kBatch / 2 >= cp.nb)
-            compute_batch<KIND, kBatch / 4>(b1, upper, acc);
-        else
-            compute_batch<KIND>(b1, upper, acc);
-        __builtin_amdgcn_sched_barrier(0);
-        finish(cp);
-        if (lp.t >= t1) break;
-        cp = lp;
+        Pos cp = lp;
         advance();
+        // (scheduling barriers keep each batch's loads together, so a batch waits only for its own)
+        for (;;) {
+            load_batch<KIND, LDSX>(b1, ltk, lp.b, o, lds_base);
+            __builtin_amdgcn_sched_barrier(0);
+            if (cp.b + kBatch / 2 >= cp.nb)
+                compute_batch<KIND, kBatch / 4>(b0, upper, acc);  // a task's last half batch
+            else
+                compute_batch<KIND>(b0, upper, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            finish(cp);
+            if (lp.t >= t1) break;
+            cp = lp;
+            advance();
+            load_batch<KIND, LDSX>(b0, ltk, lp.b, o, lds_base);
+            __builtin_amdgcn_sched_barrier(0);
+            if (cp.b + kBatch / 2 >= cp.nb)
+                compute_batch<KIND, kBatch / 4>(b1, upper, acc);
+            else
+                compute_batch<KIND>(b1, upper, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            finish(cp);
+            if (lp.t >= t1) break;
+            cp = lp;
+            advance();
+        }
+        flush();
     }
-    flush();
+    for (uint32_t j = blockIdx.x; j < jobs.count * jobs.py; j += gridDim.x) {
+        const GemvDesc d = jobs.descs[j / jobs.py];
+        const uint32_t b = (j % jobs.py) * 32 + threadIdx.x / 8;  // (the eight lanes of a block agree)
+        if (b < d.nb)
+            prep_block<KIND>(d.x, ((uintptr_t)d.x & 15) == 0, b, threadIdx.x % 8,
+                             (__attribute__((address_space(1))) uint32_t *)(d.prep + (size_t)b * kPrepBytes));
+    }
 }
 
 // Wavefronts per CU a launch aims for (FERRUM_HIP_GEMV_WAVES_PER_CU overrides, 1..32), at most
@@ -301,7 +321,7 @@ uint32_t waves_per_cu() {
     return w;
 }
 
-constexpr uint32_t kMaxLdsBlocks = 112;  // per wavefront: 17.5 KiB of prepared x, 70 KiB per workgroup (two fit a CU)
+constexpr uint32_t kMaxLdsBlocks = kGemvLdsBlocks;  // per wavefront: 17.5 KiB of prepared x, 70 KiB per workgroup (two fit a CU)
 constexpr uint32_t kMinLdsTasks = 8;     // tasks per wavefront below which x is prepared once, globally
 
 // Resident workgroups per CU for a kernel and its dynamic LDS (cached per LDS size).
@@ -318,9 +338,12 @@ int resident_groups(uint32_t lds_bytes) {
     return b;
 }
 
+// other: the products of another launch whose prepared x this launch may write (other->count 0:
+// none). Returns through *other_done whether it did (then that launch skips its own preparation).
 template <int KIND>
 hipError_t launch_kind(hipStream_t s, const GemvDesc *descs, const uint32_t *map, const GemvDesc &one,
-                       uint32_t count, uint32_t tasks, uint32_t max_nb, int cus) {
+                       uint32_t count, uint32_t tasks, uint32_t max_nb, int cus, const GemvPrep &other,
+                       bool skip_prep, bool *other_done) {
     // Prepared x in LDS when every product's fits in a wavefront's region and a wavefront's
     // share of tasks is long enough to pay for preparing it (each wavefront prepares every
     // product it touches); otherwise a separate preparation kernel (a row of workgroups per
@@ -329,10 +352,22 @@ hipError_t launch_kind(hipStream_t s, const GemvDesc *descs, const uint32_t *map
     const uint32_t waves_est = (uint32_t)(cus > 0 ? cus : 256) * min(4u * resident_groups<KIND, false>(0), waves_per_cu());
     const bool ldsx = nb8 <= kMaxLdsBlocks && (tasks + waves_est - 1) / waves_est >= kMinLdsTasks;
     const uint32_t lds_bytes = ldsx ? 4 * nb8 * kPrepBytes : 0;
+    PrepJobs jobs{other.descs, 0, (other.max_nb + 31) / 32};
+    if (other_done) *other_done = false;
     if (!ldsx) {
-        const uint32_t py = (max_nb + 31) / 32;
-        gemv_prep_kernel<KIND><<<dim3(count, py < 4096 ? py : 4096), 256, 0, s>>>(descs, one);
+        // one preparation launch for this launch's products and, when they follow them in the
+        // descriptor array, the other launch's
+        const bool both = other.count && other.descs == descs + count;
+        const uint32_t py = (max(max_nb, both ? other.max_nb : 0u) + 31) / 32;
+        if (!skip_prep || both)
+            gemv_prep_kernel<KIND><<<dim3(count + (both ? other.count : 0), py < 4096 ? py : 4096), 256, 0, s>>>(
+                descs, one);
+        if (both && other_done) *other_done = true;
     } else {
+        if (other.count && other_done) {
+            jobs.count = other.count;
+            *other_done = true;
+        }
         static const hipError_t attr = hipFuncSetAttribute((const void *)gemv_kernel<KIND, true>,
                                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                                            (int)(4 * kMaxLdsBlocks * kPrepBytes));
@@ -346,9 +381,10 @@ hipError_t launch_kind(hipStream_t s, const GemvDesc *descs, const uint32_t *map
     const uint32_t per = (tasks + max_waves - 1) / max_waves;
     const uint32_t waves = (tasks + per - 1) / per;
     if (ldsx)
-        gemv_kernel<KIND, true><<<(waves + 3) / 4, 256, lds_bytes, s>>>(descs, map, one, count, tasks, per, nb8);
+        gemv_kernel<KIND, true><<<(waves + 3) / 4, 256, lds_bytes, s>>>(descs, map, one, count, tasks, per, nb8, jobs);
     else
-        gemv_kernel<KIND, false><<<(waves + 3) / 4, 256, 0, s>>>(descs, map, one, count, tasks, per, 0);
+        gemv_kernel<KIND, false><<<(waves + 3) / 4, 256, 0, s>>>(descs, map, one, count, tasks, per, 0,
+                                                                 PrepJobs{nullptr, 0, 1});
     return hipGetLastError();
 }
 
@@ -370,17 +406,23 @@ uint32_t gemv_tasks(size_t n) { return (uint32_t)((n + 31) / 32); }
 hipError_t launch_gemv(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
                        float *y, size_t k, size_t n, void *prep, int cus) {
     const GemvDesc one{qs, ds, x, y, (uint8_t *)prep, (uint32_t)(k / 32), (uint32_t)n, 0, 0};
+    const GemvPrep none{nullptr, 0, 0};
     if (kind == FH_Q8_0)
-        return launch_kind<FH_Q8_0>(s, nullptr, nullptr, one, 1, gemv_tasks(n), (uint32_t)(k / 32), cus);
-    return launch_kind<FH_Q4_0>(s, nullptr, nullptr, one, 1, gemv_tasks(n), (uint32_t)(k / 32), cus);
+        return launch_kind<FH_Q8_0>(s, nullptr, nullptr, one, 1, gemv_tasks(n), (uint32_t)(k / 32), cus, none, false,
+                                    nullptr);
+    return launch_kind<FH_Q4_0>(s, nullptr, nullptr, one, 1, gemv_tasks(n), (uint32_t)(k / 32), cus, none, false,
+                                nullptr);
 }
 
 hipError_t launch_gemv_group(hipStream_t s, fh_kind kind, const GemvDesc *descs, const uint32_t *map,
-                             uint32_t count, uint32_t tasks, uint32_t max_nb, int cus) {
+                             uint32_t count, uint32_t tasks, uint32_t max_nb, int cus, const GemvPrep &other,
+                             bool skip_prep, bool *other_done) {
+    if (other_done) *other_done = false;
     if (count == 0 || tasks == 0) return hipSuccess;
     const GemvDesc none{};
-    if (kind == FH_Q8_0) return launch_kind<FH_Q8_0>(s, descs, map, none, count, tasks, max_nb, cus);
-    return launch_kind<FH_Q4_0>(s, descs, map, none, count, tasks, max_nb, cus);
+    if (kind == FH_Q8_0)
+        return launch_kind<FH_Q8_0>(s, descs, map, none, count, tasks, max_nb, cus, other, skip_prep, other_done);
+    return launch_kind<FH_Q4_0>(s, descs, map, none, count, tasks, max_nb, cus, other, skip_prep, other_done);
 }
 
 }  // namespace fh

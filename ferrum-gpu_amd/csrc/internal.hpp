@@ -175,6 +175,8 @@ struct GemvDesc {          // one batch-1 product, as the kernels read it
     uint32_t task0;        // first task (group of 32 rows) of this product in its launch
     uint32_t pad;
 };
+// Widest product (in 32-blocks) whose prepared x the GEMV keeps in a wavefront's LDS region.
+constexpr uint32_t kGemvLdsBlocks = 112;
 // Whether the kernel's 32-bit offsets cover rows of k inputs (k a multiple of 32, up to 2^25).
 bool gemv_supported(fh_kind kind, size_t k, size_t n);
 size_t gemv_prep_bytes(size_t k);
@@ -185,8 +187,16 @@ hipError_t launch_gemv(hipStream_t s, fh_kind kind, const uint8_t *qs, const uin
 // Many products of one format: `descs` (device memory) in task order with task0 prefix sums,
 // `map` (device memory) the product of each of the `tasks` tasks, max_nb the widest product's
 // block count.
+// Products of another launch of the same plan (descs, count, their widest nb) whose prepared x a
+// launch may write for it: fused into its product kernel when that one prepares its own x in
+// LDS, else into its preparation kernel when their descriptors follow its own.
+struct GemvPrep {
+    const GemvDesc *descs;
+    uint32_t count, max_nb;
+};
 hipError_t launch_gemv_group(hipStream_t s, fh_kind kind, const GemvDesc *descs, const uint32_t *map,
-                             uint32_t count, uint32_t tasks, uint32_t max_nb, int cus);
+                             uint32_t count, uint32_t tasks, uint32_t max_nb, int cus, const GemvPrep &other,
+                             bool skip_prep, bool *other_done);
 
 // rows.hip: few-row products (2 <= rows <= kRowsMax)
 constexpr size_t kRowsMax = 64;

@@ -260,6 +260,8 @@ struct fh_gemv_plan {
         size_t first, count;  // descriptors
         size_t map0;          // first entry of the launch's task -> product map
         uint32_t tasks, max_nb;
+        bool narrow;          // every product's x fits the kernel's LDS region
+        bool prepared;        // the previous (narrow) launch of its format writes its prepared x
     };
     std::vector<Launch> launches;
     GemvDesc *descs = nullptr;  // device array
@@ -803,8 +805,10 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
     if (!plan) return fail(FH_ERR_OOM, "host out of memory");
     dev_retain(dev);
     plan->dev = dev;
-    // Check every problem, then group by format, keeping the caller's order inside a group:
-    // each group is one launch (x preparation, then the products).
+    // Check every problem, then group by format and, within a format, by width (the products whose
+    // x fits the kernel's LDS region, then the wider ones), keeping the caller's order inside a
+    // group: each group is one launch. The narrow launch prepares x in LDS and also writes the wide
+    // launch's prepared x, which then needs no preparation kernel of its own.
     for (size_t i = 0; i < count; i++) {
         const fh_gemv_problem &p = problems[i];
         if (!p.w || !p.x || !p.y) {
@@ -831,11 +835,12 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
     std::vector<size_t> prep_off;  // byte offset of each product's prepared x in plan->prep
     host.reserve(count);
     size_t prep_bytes = 0;
-    for (int kind : {FH_Q8_0, FH_Q4_0}) {
-        fh_gemv_plan::Launch L{(fh_kind)kind, host.size(), 0, map.size(), 0, 0};
+    for (int kind : {FH_Q8_0, FH_Q4_0})
+    for (bool narrow : {true, false}) {
+        fh_gemv_plan::Launch L{(fh_kind)kind, host.size(), 0, map.size(), 0, 0, narrow, false};
         for (size_t i = 0; i < count; i++) {
             const fh_gemv_problem &p = problems[i];
-            if ((int)p.w->kind != kind) continue;
+            if ((int)p.w->kind != kind || (p.w->k / QK <= kGemvLdsBlocks) != narrow) continue;
             const uint32_t nb = (uint32_t)(p.w->k / QK);
             GemvDesc d{p.w->qs, p.w->ds, p.x, p.y, nullptr, nb, (uint32_t)p.w->n, L.tasks, 0};
             const uint64_t t = (uint64_t)L.tasks + gemv_tasks(p.w->n);
@@ -852,7 +857,11 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
             plan->bytes += p.w->nbytes + 4ull * (p.w->k + p.w->n);
             L.count++;
         }
-        if (L.count) plan->launches.push_back(L);
+        if (L.count) {
+            L.prepared = !narrow && !plan->launches.empty() && plan->launches.back().kind == L.kind &&
+                         plan->launches.back().narrow;
+            plan->launches.push_back(L);
+        }
     }
     if (!host.empty()) {
         void *p = nullptr;
@@ -885,16 +894,34 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
     return FH_OK;
 }
 
+fh_status fh_gemv_plan_run_launch(fh_device *dev, const fh_gemv_plan *plan, size_t i) {
+    fh_status st = check_dev(dev);
+    if (st) return st;
+    if (!plan || plan->dev != dev) return fail(FH_ERR_INVALID, "gemv plan: wrong device");
+    if (i >= plan->launches.size())
+        return fail(FH_ERR_INVALID, "gemv plan: launch %zu of %zu", i, plan->launches.size());
+    const auto &L = plan->launches[i];
+    GemvPrep other{nullptr, 0, 0};
+    if (i + 1 < plan->launches.size() && plan->launches[i + 1].prepared) {
+        const auto &W = plan->launches[i + 1];
+        other = GemvPrep{plan->descs + W.first, (uint32_t)W.count, W.max_nb};
+    }
+    bool done = false;
+    if ((st = begin_command(dev, "gemv plan"))) return st;
+    (void)launch_gemv_group(dev->stream, L.kind, plan->descs + L.first, plan->map + L.map0, (uint32_t)L.count,
+                            L.tasks, L.max_nb, dev->cus, other, L.prepared, &done);
+    if ((st = end_command(dev, "gemv plan"))) return st;
+    if (other.count && !done)  // (not reached: the wide launch's descriptors follow the narrow one's)
+        return fail(FH_ERR_DEVICE, "gemv plan: launch %zu did not prepare the next launch's x", i);
+    return FH_OK;
+}
+
 fh_status fh_gemv_plan_run(fh_device *dev, const fh_gemv_plan *plan) {
     fh_status st = check_dev(dev);
     if (st) return st;
     if (!plan || plan->dev != dev) return fail(FH_ERR_INVALID, "gemv plan: wrong device");
-    for (const auto &L : plan->launches) {
-        if ((st = begin_command(dev, "gemv plan"))) return st;
-        (void)launch_gemv_group(dev->stream, L.kind, plan->descs + L.first, plan->map + L.map0, (uint32_t)L.count,
-                                L.tasks, L.max_nb, dev->cus);
-        if ((st = end_command(dev, "gemv plan"))) return st;
-    }
+    for (size_t i = 0; i < plan->launches.size(); i++)
+        if ((st = fh_gemv_plan_run_launch(dev, plan, i))) return st;
     return FH_OK;
 }
 

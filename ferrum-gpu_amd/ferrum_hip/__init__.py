@@ -129,6 +129,7 @@ def lib() -> ctypes.CDLL:
         "fh_linear_q_noalloc": (I, [P, P, P, P, S, I]),
         "fh_gemv_plan_create": (I, [P, P, S, PP]),
         "fh_gemv_plan_run": (I, [P, P]),
+        "fh_gemv_plan_run_launch": (I, [P, P, S]),
         "fh_gemv_plan_launches": (S, [P]),
         "fh_gemv_plan_bytes": (U64, [P]),
         "fh_gemv_plan_free": (None, [P]),
@@ -516,6 +517,10 @@ class GemvPlan:
 
     def run(self) -> None:
         _check(lib().fh_gemv_plan_run(self.gpu.handle, self._h))
+
+    def run_launch(self, i: int) -> None:
+        """Launch i alone (launches must run in order: one may write the next one's prepared x)."""
+        _check(lib().fh_gemv_plan_run_launch(self.gpu.handle, self._h, i))
 
     def launches(self) -> int:
         return lib().fh_gemv_plan_launches(self._h)

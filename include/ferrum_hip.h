@@ -207,8 +207,9 @@ FH_API fh_status fh_linear_q_noalloc(fh_device *dev, const float *x, const fh_qw
 /* No counterpart in the reference: one launch for many independent batch-1 products
  * y_i = x_i * W_i (a decode step's projections, or several models' layers). The plan is built
  * once (the descriptors are uploaded then) and run any number of times; x_i and y_i are device
- * pointers of k_i and n_i floats. Products with the same block format share a launch (two
- * kernels: x preparation, then the products). */
+ * pointers of k_i and n_i floats. Per block format, the products up to 3,584 inputs wide share
+ * one launch (x prepared in the product kernel, or by a preparation kernel first) and the wider
+ * ones another, whose prepared x the first launch writes. */
 typedef struct fh_gemv_problem {
     const fh_qweight *w;
     const float *x;
@@ -217,6 +218,9 @@ typedef struct fh_gemv_problem {
 FH_API fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, size_t count,
                               fh_gemv_plan **out);
 FH_API fh_status fh_gemv_plan_run(fh_device *dev, const fh_gemv_plan *plan);
+/* Launch i of a plan alone (fh_gemv_plan_run is launches 0 .. n-1 in order; a launch may write
+ * the prepared x of the next one, so run them in order): for timing a launch on its own. */
+FH_API fh_status fh_gemv_plan_run_launch(fh_device *dev, const fh_gemv_plan *plan, size_t i);
 /* Grouped launches one run issues (one per block format), and the algorithmic bytes it moves (weights + x + y). */
 FH_API size_t fh_gemv_plan_launches(const fh_gemv_plan *plan);
 FH_API uint64_t fh_gemv_plan_bytes(const fh_gemv_plan *plan);

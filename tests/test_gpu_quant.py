@@ -501,10 +501,38 @@ def test_grouped_gemv_plan_equals_single_launches(fh, g, orc):
         singles.append((gy, gs))
         keep += [qw, gx, gy, gs]
     plan = fh.GemvPlan(g, probs)
-    assert plan.launches() == 2  # one per block format
+    assert plan.launches() == 4  # per block format: the products up to 112 blocks wide, then the wider ones
     plan.run()
     for gy, gs in singles:
         assert np.array_equal(g.read(gy), g.read(gs))
+    plan.free()
+
+
+def test_grouped_gemv_plan_fuses_the_wide_launchs_preparation(fh, g, orc):
+    """A plan of many 896-wide products (enough tasks per wavefront for x in LDS) and a few
+    4864-wide ones: the narrow launch writes the wide launch's prepared x inside its own kernel;
+    every product still equals its single launch bit for bit, on two runs (the second over the
+    records the first left)."""
+    rng = np.random.default_rng(8)
+    shapes = [(896, 4864)] * 120 + [(4864, 896)] * 6 + [(896, 1152)] * 4 + [(4864, 896)] * 2
+    packed = {}
+    probs, singles, keep = [], [], []
+    for i, (k, n) in enumerate(shapes):
+        if (k, n) not in packed:
+            w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+            packed[(k, n)] = fh.upload_quantised(g, fh.QKind.Q4_0, w, k, n).read_gguf()
+        qw = fh.upload_qweight(g, fh.QKind.Q4_0, packed[(k, n)], k, n)
+        gx, gy, gs = g.upload(rng.standard_normal(k).astype(np.float32)), g.zeros(n), g.zeros(n)
+        fh.linear_q_with(g, gx, qw, gs, 1, fh.QPath.Gemv)
+        probs.append((qw, gx.device_ptr(), gy.device_ptr()))
+        singles.append((gy, gs))
+        keep += [qw, gx, gy, gs]
+    plan = fh.GemvPlan(g, probs)
+    assert plan.launches() == 2
+    for rep in range(2):
+        plan.run()
+        for gy, gs in singles:
+            assert np.array_equal(g.read(gy), g.read(gs)), rep
     plan.free()
 
 
