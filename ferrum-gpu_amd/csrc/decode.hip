@@ -209,6 +209,13 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
     float *part = (float *)(dlds + (PRO == PRO_GLOBAL ? 0 : (PRO == PRO_LN ? span : a.chunk) * kPrepBytes));
     float *red = part + W * 32;
 
+    // the epilogue's bias and residual inputs are requested first (the epilogue runs in lanes 0..31
+    // of wavefront 0; nothing in this launch writes them before it)
+    float pre_bias = 0.0f, pre_y = 0.0f;
+    if (wave == 0 && !upper && g * 32 + r < a.n) {
+        if (a.bias) pre_bias = a.bias[g * 32 + r];
+        if constexpr (EPI == EPI_RESIDUAL) pre_y = a.y[g * 32 + r];
+    }
     // the wavefront's first batch is requested before x is prepared
     Batch<KIND> cur, nx;
     uint32_t bb = b0 + wave * kBatch;
@@ -300,11 +307,11 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
         return;
     }
     if (row >= a.n) return;
-    if (a.bias) t = t + a.bias[row];  // decode.rs:42-53: the bias joins after the products
+    if (a.bias) t = t + pre_bias;  // decode.rs:42-53: the bias joins after the products
     if constexpr (EPI == EPI_STORE) {
         a.y[row] = t;
     } else if constexpr (EPI == EPI_RESIDUAL) {
-        a.y[row] = a.y[row] + t;  // nn::add(x, gemv(..)), decode.rs:100,111
+        a.y[row] = pre_y + t;  // nn::add(x, gemv(..)), decode.rs:100,111
     } else if constexpr (EPI == EPI_GELU) {
         a.y[row] = gelu(t);
     } else {
