@@ -241,6 +241,37 @@ def bench_gemm(fh, g, ev, kind, m, shapes, steps, seed=0, path=None, copies=1, b
     return out
 
 
+def bench_single_calls(fh, g, ev, kind, shapes, reps=3, seed=4):
+    """One linear_q per product (batch 1, the library's own path choice): microseconds per call
+    at each shape, over enough distinct weight copies (about 512 MB) that every call reads HBM;
+    a decode step that calls the library once per matrix pays this per matrix."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for k, n in shapes:
+        w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+        data = fh.upload_quantised(g, kind, w, k, n).read_gguf()
+        copies = max(2, int(512e6 // data.size))
+        qs = [fh.upload_qweight(g, kind, data, k, n) for _ in range(copies)]
+        xs = [g.upload(rng.standard_normal(k).astype(np.float32)) for _ in range(copies)]
+        ys = [g.zeros(n) for _ in range(copies)]
+        for i in range(copies):
+            fh.linear_q(g, xs[i], qs[i], ys[i], 1)
+        g.sync()
+        e0, e1 = ev.create(2)
+        ev.record(e0)
+        for _ in range(reps):
+            for i in range(copies):
+                fh.linear_q(g, xs[i], qs[i], ys[i], 1)
+        ev.record(e1)
+        g.sync()
+        ms = ev.ms(e0, e1) / (reps * copies)
+        ev.destroy([e0, e1])
+        out[f"{k}x{n}"] = {"us": round(ms * 1e3, 2), "gbs": round((data.size + 4 * k + 4 * n) / (ms * 1e-3) / 1e9, 1)}
+        for q in qs:
+            q.free()
+    return out
+
+
 def bench_rows_pool(fh, g, ev, kind, m, shapes, steps, copies=12, seed=0):
     """Config 5's few-row products as one grouped launch pair (RowsPlan: x split, then the
     few-row kernel over every product): `copies` distinct copies of `shapes` (12 copies of the
@@ -682,6 +713,10 @@ def main():
                     "ms_per_step": r["ms_per_step"], "bytes_per_step": r["bytes_per_step"],
                     "path": "rows plan (QPath.Rows), one launch pair for 48 products",
                     "single_calls_gbs": round(r1["gbs"], 2), "single_calls_ms_per_step": r1["ms_per_step"]}
+        for kind, tag in ((fh.QKind.Q4_0, "q4_0"), (fh.QKind.Q8_0, "q8_0")):
+            sc1 = bench_single_calls(fh, g, ev, kind, QWEN_SHAPES + LLAMA1B_SHAPES)
+            log(f"{tag} single-call GEMV:", sc1)
+            extra[f"{tag}_gemv_single_call_us"] = sc1
         codec = bench_codec(fh, g, ev)
         log("codec:", codec)
         extra["codec_llama1b"] = codec

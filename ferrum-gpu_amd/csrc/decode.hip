@@ -25,6 +25,7 @@
 // the QKV scatter into the caches. The block products are the exact integer MFMA products of the
 // batch-1 GEMV (gemv_parts.hpp).
 #include <algorithm>
+#include <cstdlib>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -549,7 +550,8 @@ hipError_t launch_dgemv(hipStream_t s, DecodeGemv a, bool allow_split) {
 
 #define FH_DGEMV_KERNELS(K)                                                                             \
     (const void *)decode_gemv_kernel<K, PRO_LN, EPI_QKV>, (const void *)decode_gemv_kernel<K, PRO_NONE, EPI_RESIDUAL>, \
-        (const void *)decode_gemv_kernel<K, PRO_LN, EPI_GELU>, (const void *)decode_gemv_kernel<K, PRO_GLOBAL, EPI_ARGMAX>
+        (const void *)decode_gemv_kernel<K, PRO_LN, EPI_GELU>, (const void *)decode_gemv_kernel<K, PRO_GLOBAL, EPI_ARGMAX>, \
+        (const void *)decode_gemv_kernel<K, PRO_NONE, EPI_STORE>
 
 // Dynamic LDS beyond the default 64 KiB: prepared x of up to kMaxBlocks blocks plus the row
 // sums, and the attention scores of up to 16384 positions. Set once, before any capture.
@@ -685,6 +687,36 @@ fh_status run_step(fh_gpt2 *m) {
 }
 
 }  // namespace
+
+namespace fh {
+
+hipError_t decode_lds_limits() { return set_lds_limits(); }
+
+bool gemv_latency_fits(size_t k, size_t n, int cus) {
+    // one workgroup per 32 rows holding all of x's prepared records in LDS; worth it while the
+    // row groups are few enough that their workgroups run in about one round
+    const size_t env = [] {
+        const char *e = getenv("FERRUM_HIP_GEMV_LATENCY_GROUPS_PER_CU");
+        const long v = e ? strtol(e, nullptr, 10) : 0;
+        return (size_t)(v >= 0 && v <= 64 && e ? v : 2);  // (measured: 2 to 8 alike; 1 leaves 352 groups slow)
+    }();
+    return k / 32 <= kMaxBlocks && (n + 31) / 32 <= env * (size_t)(cus > 0 ? cus : 256);
+}
+
+hipError_t launch_gemv_latency(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
+                               float *y, size_t k, size_t n) {
+    DecodeGemv a{};
+    a.qs = qs;
+    a.ds = ds;
+    a.x = x;
+    a.y = y;
+    a.nb = (uint32_t)(k / 32);
+    a.n = (uint32_t)n;
+    return dgemv<PRO_NONE, EPI_STORE>(s, kind, a);
+}
+
+}  // namespace fh
+
 
 extern "C" {
 

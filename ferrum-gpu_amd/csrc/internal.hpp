@@ -175,6 +175,15 @@ struct GemvDesc {          // one batch-1 product, as the kernels read it
     uint32_t task0;        // first task (group of 32 rows) of this product in its launch
     uint32_t pad;
 };
+// A single batch-1 product on the decode GEMV's kernel (decode.hip: one workgroup per 32 rows,
+// its wavefronts splitting the row's blocks, x prepared in LDS by every workgroup): a lower
+// latency than launch_gemv when the product's row groups alone leave the chip underfilled
+// (gemv_latency_fits). decode_lds_limits raises the decode kernels' LDS limit (once per process,
+// before any graph capture).
+hipError_t decode_lds_limits();
+bool gemv_latency_fits(size_t k, size_t n, int cus);
+hipError_t launch_gemv_latency(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
+                               float *y, size_t k, size_t n);
 // Widest product (in 32-blocks) whose prepared x the GEMV keeps in a wavefront's LDS region.
 constexpr uint32_t kGemvLdsBlocks = 112;
 // Whether the kernel's 32-bit offsets cover rows of k inputs (k a multiple of 32, up to 2^25).

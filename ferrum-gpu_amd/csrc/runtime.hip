@@ -307,6 +307,11 @@ fh_status fh_device_open(int ordinal, fh_device **out) {
         delete d;
         return hip_fail(nullptr, e, "create stream");
     }
+    if ((e = decode_lds_limits()) != hipSuccess) {  // (before any capture a caller may start)
+        (void)hipStreamDestroy(d->stream);
+        delete d;
+        return hip_fail(nullptr, e, "kernel LDS limits");
+    }
     *out = d;
     return FH_OK;
 }
@@ -693,6 +698,11 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
         if (!gemv_supported(w->kind, w->k, w->n))
             return fail(FH_ERR_INVALID, "the GEMV kernel's 32-bit offsets do not cover a %zu x %zu weight",
                         w->n, w->k);
+        if (gemv_latency_fits(w->k, w->n, dev->cus) && ((uintptr_t)x & 15) == 0) {  // few row groups
+            if ((st = begin_command(dev, "linear_q"))) return st;
+            (void)launch_gemv_latency(dev->stream, w->kind, w->qs, w->ds, x, y, w->k, w->n);
+            return end_command(dev, "linear_q");
+        }
         void *prep = nullptr;
         if ((st = command_scratch(dev, fixed, gemv_prep_bytes(w->k), &prep))) return st;
         if ((st = begin_command(dev, "linear_q"))) return st;

@@ -486,7 +486,9 @@ def test_f16_gemm_on_awkward_shapes_and_values(fh, g, orc):
 
 
 def test_grouped_gemv_plan_equals_single_launches(fh, g, orc):
-    """The grouped launch runs the same per-row code: results are bit-identical to linear_q."""
+    """The grouped launch runs the same per-row code as a plan of one product: results are
+    bit-identical to it. A single linear_q of a product with few row groups runs the K-split
+    GEMV instead (the decode's kernel): within 1e-5 of the plan and of the CPU."""
     rng = np.random.default_rng(5)
     probs, singles, keep = [], [], []
     for i, (kind, k, n) in enumerate([(fh.QKind.Q4_0, 896, 1152), (fh.QKind.Q4_0, 896, 300),
@@ -495,23 +497,29 @@ def test_grouped_gemv_plan_equals_single_launches(fh, g, orc):
         w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
         x = rng.standard_normal(k).astype(np.float32)
         qw = fh.upload_quantised(g, kind, w, k, n)
-        gx, gy, gs = g.upload(x), g.zeros(n), g.zeros(n)
-        fh.linear_q_with(g, gx, qw, gs, 1, fh.QPath.Gemv)
+        gx, gy, gs, gl = g.upload(x), g.zeros(n), g.zeros(n), g.zeros(n)
+        one = fh.GemvPlan(g, [(qw, gx.device_ptr(), gs.device_ptr())])
+        one.run()
+        one.free()
+        fh.linear_q_with(g, gx, qw, gl, 1, fh.QPath.Gemv)
+        want = orc.matmul(x, qw.dequantised().reshape(-1), 1, k, n)
         probs.append((qw, gx.device_ptr(), gy.device_ptr()))
-        singles.append((gy, gs))
-        keep += [qw, gx, gy, gs]
+        singles.append((gy, gs, gl, want))
+        keep += [qw, gx, gy, gs, gl]
     plan = fh.GemvPlan(g, probs)
     assert plan.launches() == 4  # per block format: the products up to 112 blocks wide, then the wider ones
     plan.run()
-    for gy, gs in singles:
-        assert np.array_equal(g.read(gy), g.read(gs))
+    for gy, gs, gl, want in singles:
+        got = g.read(gy)
+        assert np.array_equal(got, g.read(gs))
+        assert orc.max_rel_err(g.read(gl), got) < 1e-5 and orc.max_rel_err(g.read(gl), want) < 1e-5
     plan.free()
 
 
 def test_grouped_gemv_plan_fuses_the_wide_launchs_preparation(fh, g, orc):
     """A plan of many 896-wide products (enough tasks per wavefront for x in LDS) and a few
     4864-wide ones: the narrow launch writes the wide launch's prepared x inside its own kernel;
-    every product still equals its single launch bit for bit, on two runs (the second over the
+    every product still equals its plan of one bit for bit, on two runs (the second over the
     records the first left)."""
     rng = np.random.default_rng(8)
     shapes = [(896, 4864)] * 120 + [(4864, 896)] * 6 + [(896, 1152)] * 4 + [(4864, 896)] * 2
@@ -523,7 +531,9 @@ def test_grouped_gemv_plan_fuses_the_wide_launchs_preparation(fh, g, orc):
             packed[(k, n)] = fh.upload_quantised(g, fh.QKind.Q4_0, w, k, n).read_gguf()
         qw = fh.upload_qweight(g, fh.QKind.Q4_0, packed[(k, n)], k, n)
         gx, gy, gs = g.upload(rng.standard_normal(k).astype(np.float32)), g.zeros(n), g.zeros(n)
-        fh.linear_q_with(g, gx, qw, gs, 1, fh.QPath.Gemv)
+        one = fh.GemvPlan(g, [(qw, gx.device_ptr(), gs.device_ptr())])
+        one.run()
+        one.free()
         probs.append((qw, gx.device_ptr(), gy.device_ptr()))
         singles.append((gy, gs))
         keep += [qw, gx, gy, gs]
