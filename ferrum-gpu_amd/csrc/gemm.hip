@@ -315,7 +315,6 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
     // K split blockIdx.y: stages [st0, st1) (one split: all of them); each split writes its own
     // partial product, y + split * M * N, added up by gemm_reduce_kernel in split order
     const uint32_t st0 = blockIdx.y * split_stages, st1 = min(all_stages, st0 + split_stages);
-    const uint32_t stages = st1 > st0 ? st1 - st0 : 0;
     y += (size_t)blockIdx.y * M * N;
     const int fr = lane % 32;        // fragment row (x) / column (weights)
     const int fk = 8 * (lane / 32);  // first of this lane's 8 positions in a K = 16 step
@@ -333,17 +332,18 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
         const uint32_t n = n0 + (wn * C::TN + j) * 32 + fr;
         bscv[j] = n < N ? bsc[n] : 0x7f7f7f7f;
     }
+    // Drain these loads here (vmcnt 0, the other counters left alone): otherwise their possible
+    // pendency at the loop head makes the compiler wait for every load in flight, the stage
+    // prefetch included, at their first use inside the loop.
+    __builtin_amdgcn_s_waitcnt(0x0f70);
 
     // Per-thread operand offsets at stage 0 (bytes), advanced by a fixed stride per stage. Buffer
     // loads return zeros past each array's end (rows past M and columns past the weight's padded
     // row count); the second block of an odd last stage reads whatever follows, which the f16 pass
     // skips, and the fp8 operands' zero row tails cover it for the correction.
     const uint32_t K64 = (K + 63) / 64 * 64;
-    const auto r_xh = make_rsrc(xh, M * nb * 64);
-    const auto r_xl = make_rsrc(xl, M * K64);
-    const auto r_q = make_rsrc(qs, (N + 31) / 32 * 32 * nb * C::QB);
-    const auto r_b8 = make_rsrc(b8, N * K64);
-    const auto r_d = make_rsrc(ds, (N + 31) / 32 * 32 * ((nb + 7) / 8 * 8) * 2);
+    const uint32_t n_xh = M * nb * 64, n_xl = M * K64, n_q = (N + 31) / 32 * 32 * nb * C::QB, n_b8 = N * K64,
+                   n_d = (N + 31) / 32 * 32 * ((nb + 7) / 8 * 8) * 2;
     constexpr uint32_t kOut = 0x80000000u;  // an offset past every array: loads return zeros
     uint32_t o_xh[C::XH], o_xl[C::XL], o_q[C::QL], o_b8[C::BL], o_d;
     uint32_t s_xh[C::XH], s_xl[C::XL], s_q[C::QL], s_b8[C::BL];  // LDS byte offsets
@@ -384,7 +384,16 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
     // two register sets of staged operands: stage st + 2 is requested while stage st is computed
     u32x4 rxh[2][C::XH], rxl[2][C::XL], rq[2][C::QL], rb8[2][C::BL];
     uint32_t rd[2] = {0u, 0u};
+    // Every stage issues its loads, also the two past the split's end (through empty resources,
+    // which return zeros): the number of loads in flight is then the same on every path, so the
+    // compiler's waits count exactly the older register set and never drain the prefetch.
     auto load_stage = [&](uint32_t st, int rs) {
+        const bool live = st < st1;
+        const auto r_xh = make_rsrc(xh, live ? n_xh : 0u);
+        const auto r_xl = make_rsrc(xl, live ? n_xl : 0u);
+        const auto r_q = make_rsrc(qs, live ? n_q : 0u);
+        const auto r_b8 = make_rsrc(b8, live ? n_b8 : 0u);
+        const auto r_d = make_rsrc(ds, live ? n_d : 0u);
 #pragma unroll
         for (int i = 0; i < C::XH; i++)
             rxh[rs][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_xh, (int)(o_xh[i] + st * 128), 0, 0));
@@ -446,7 +455,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
         __syncthreads();  // every wave is done reading the previous stage
         store_stage(rs);
         __syncthreads();
-        if (st + 2 < st1) load_stage(st + 2, rs);  // in flight during the next two stages' MFMAs
+        load_stage(st + 2, rs);  // in flight during the next two stages' MFMAs
         const int nbb = nb - 2 * st < 2u ? 1 : 2;  // wave-uniform
 #pragma unroll
         for (int bb = 0; bb < 2; bb++) {
@@ -497,12 +506,16 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
                 acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8[i], b8f[j], acc[i][j], 0, 0, 0, asc[i], 0,
                                                                             bscv[j]);
     };
-    if (stages > 0) load_stage(st0, 0);
-    if (stages > 1) load_stage(st0 + 1, 1);
-    for (uint32_t st = st0; st < st1; st += 2) {  // unrolled by two: register sets are named statically
+    load_stage(st0, 0);
+    load_stage(st0 + 1, 1);
+    // unrolled by two (the register sets are named statically); an odd last stage runs after the
+    // loop, so every trip round the loop issues the same loads
+    uint32_t st = st0;
+    for (; st + 1 < st1; st += 2) {
         stage(st, std::integral_constant<int, 0>{});
-        if (st + 1 < st1) stage(st + 1, std::integral_constant<int, 1>{});
+        stage(st + 1, std::integral_constant<int, 1>{});
     }
+    if (st < st1) stage(st, std::integral_constant<int, 0>{});
 
     // D layout of a 32x32 tile: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32
 #pragma unroll
