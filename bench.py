@@ -621,6 +621,8 @@ def main():
                     help="only the codec and QAT-pass lines at the TinyLlama-1.1B sizes, one JSON line (for profiling)")
     ap.add_argument("--rows-only", action="store_true",
                     help="only config 5's grouped few-row products (M = 8, 64), one JSON line (for profiling)")
+    ap.add_argument("--ext-only", action="store_true",
+                    help="only the one-row GEMV on the other weight formats (F16, FP8, MXFP4, Q2_K), one JSON line")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the scoring GEMM at the TinyLlama-1.1B shapes, M = 4096, one JSON line (for profiling)")
     a = ap.parse_args()
@@ -660,6 +662,16 @@ def main():
                 det[f"{tag}_m{m}"] = bench_rows_pool(fh, g, ev, kind, m, LLAMA1B_SHAPES, a.steps)
         print(json.dumps({"metric": "config 5 few-row products, weight GB/s", "value": det["q4_0_m8"]["weight_gbs"],
                           "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "detail": det}))
+        g.close()
+        return
+    if a.ext_only:
+        ext = {}
+        for kind in (fh.QKind.F16, fh.QKind.Fp8E4M3, fh.QKind.Fp8E5M2, fh.QKind.Fp4, fh.QKind.Q2K):
+            shapes = [(8192, 8192), (1024 if kind == fh.QKind.Q2K else 896, 151936)]
+            ext[kind.label()] = bench_single_calls(fh, g, ev, kind, shapes, reps=2, seed=5)
+        print(json.dumps({"metric": "one-row GEMV GB/s on the other weight formats, 8192 x 8192",
+                          "value": ext["MXFP4"]["8192x8192"]["gbs"], "unit": "GB/s", "n_gpus": 1,
+                          "higher_is_better": True, "detail": ext}))
         g.close()
         return
     if a.gemm_only:
@@ -717,6 +729,15 @@ def main():
             sc1 = bench_single_calls(fh, g, ev, kind, QWEN_SHAPES + LLAMA1B_SHAPES)
             log(f"{tag} single-call GEMV:", sc1)
             extra[f"{tag}_gemv_single_call_us"] = sc1
+        ext = {}
+        for kind in (fh.QKind.F16, fh.QKind.Fp8E4M3, fh.QKind.Fp8E5M2, fh.QKind.Fp4, fh.QKind.Q2K):
+            shapes = [(8192, 8192), (1024 if kind == fh.QKind.Q2K else 896, 151936)]
+            ext[kind.label()] = bench_single_calls(fh, g, ev, kind, shapes, reps=2, seed=5)
+        log("other formats, single-call GEMV:", ext)
+        extra["ext_formats_gemv_single_call"] = {
+            "kernel": "ext_gemv_rows_kernel: GGUF rows decoded in registers, x shared by up to 8 rows per lane, "
+                      "f32 accumulation; one launch per call, launch gaps included",
+            "by_format": ext}
         codec = bench_codec(fh, g, ev)
         log("codec:", codec)
         extra["codec_llama1b"] = codec

@@ -421,7 +421,8 @@ __global__ __launch_bounds__(256) void ext_naive_kernel(const uint8_t *__restric
     y[idx] = acc;
 }
 
-// Batch-1: one workgroup per output; thread t takes elements t, t + 256, ...; a tree sum ends it.
+// Batch-1 with an x that is not 16-byte aligned: one workgroup per output; thread t takes elements
+// t, t + 256, ...; a tree sum ends it.
 template <uint32_t T>
 __global__ __launch_bounds__(256) void ext_gemv_kernel(const uint8_t *__restrict__ w, const float *__restrict__ x,
                                                        float *__restrict__ y, uint32_t k) {
@@ -435,6 +436,295 @@ __global__ __launch_bounds__(256) void ext_gemv_kernel(const uint8_t *__restrict
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
     __syncthreads();
     if (threadIdx.x == 0) y[c] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// ---- batch-1 GEMV on resident rows, the one-row path ----
+// A lane takes whole segments of a row (F16: 8 elements, FP8: 16, MXFP4: a block of 32, Q2_K: 32
+// elements of one half super-block), loads the segment's x once and uses it for R rows (1, 2, 4 or
+// 8), decodes the weights in registers and accumulates in f32: per segment the block's integer-valued
+// codes are summed against x and the block scale is applied once (FP8 and Q2_K: the scale times
+// the segment's sum, MXFP4: the power-of-two scale likewise). L lanes share a group of rows
+// (segments l, l + L, ...), summed by shuffles and, for L > 64, through LDS. Rows are GGUF rows
+// of B-byte blocks at any byte offset: a segment that is not 4-byte aligned is loaded as the
+// dwords around it and realigned with v_alignbyte (allocations carry 256 zero bytes past their
+// end, so the last block's over-read stays inside its buffer).
+
+__device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *(const uint32_t *)p; }
+// bytes [p, p + 16) for any p: five dwords from p rounded down, realigned
+__device__ __forceinline__ u32x4 ld16_any(const uint8_t *p) {
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+    const uint8_t *q = p - sh;  // derived from p, so the loads stay global ones
+    const uint32_t d0 = ld32(q), d1 = ld32(q + 4), d2 = ld32(q + 8), d3 = ld32(q + 12), d4 = ld32(q + 16);
+    return u32x4{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
+                 __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh)};
+}
+__device__ __forceinline__ float lo_half(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)v); }
+__device__ __forceinline__ float hi_half(uint32_t v) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+}
+__device__ __forceinline__ float sbyte(uint32_t v, int i) { return (float)(int32_t)(int8_t)(v >> (8 * i)); }
+__device__ __forceinline__ float ubyte(uint32_t v, int i) { return (float)((v >> (8 * i)) & 0xffu); }
+
+template <uint32_t T>
+struct ExtSeg;
+
+template <>
+struct ExtSeg<FH_F16> {  // segment s: halves 8 s .. 8 s + 7 of the row (16-byte aligned)
+    static constexpr uint32_t SPB = 4, XN = 8;
+    struct W {
+        u32x4 q;
+    };
+    __device__ static void load(const uint8_t *row, uint32_t s, W &w) { w.q = *(const u32x4 *)(row + 16 * s); }
+    __device__ static uint32_t xat(uint32_t s) { return 8 * s; }
+    __device__ static float dot(const W &w, const float (&x)[XN]) {
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            a = fmaf(x[2 * i], lo_half(w.q[i]), a);
+            a = fmaf(x[2 * i + 1], hi_half(w.q[i]), a);
+        }
+        return a;
+    }
+};
+
+// FP8 (fp8.rs:34-63): segment s = codes 16 p .. 16 p + 15 of block s / 2, p = s % 2, times the
+// block's f16 scale. E5M2 codes are the high byte of an f16; E4M3 code c is the f16 with bits
+// (c & 0x7f) << 7 | (c & 0x80) << 8 times 2^8 (normal and subnormal alike), its NaN codes
+// (0x7f, 0xff) flagged separately.
+template <bool E5M2>
+struct Fp8Seg {
+    static constexpr uint32_t SPB = 2, XN = 16;
+    struct W {
+        uint32_t d;
+        u32x4 c;
+    };
+    __device__ static void load(const uint8_t *row, uint32_t s, W &w) {
+        const uint8_t *blk = row + 34 * (s / 2);
+        w.d = *(const uint16_t *)blk;
+        w.c = ld16_any(blk + 2 + 16 * (s % 2));
+    }
+    __device__ static uint32_t xat(uint32_t s) { return 16 * s; }
+    __device__ static float dot(const W &w, const float (&x)[XN]) {
+        float a = 0.0f;
+        uint32_t nan = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v = w.c[i];
+            uint32_t p0, p1;  // f16 pairs of codes (0, 1) and (2, 3)
+            if constexpr (E5M2) {
+                p0 = __builtin_amdgcn_perm(v, 0u, 0x050c040cu);
+                p1 = __builtin_amdgcn_perm(v, 0u, 0x070c060cu);
+            } else {
+                const uint32_t t0 = __builtin_amdgcn_perm(v, 0u, 0x0c050c04u), t1 = __builtin_amdgcn_perm(v, 0u, 0x0c070c06u);
+                p0 = ((t0 & 0x007f007fu) << 7) | ((t0 & 0x00800080u) << 8);
+                p1 = ((t1 & 0x007f007fu) << 7) | ((t1 & 0x00800080u) << 8);
+                nan |= ((v & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
+            }
+            a = fmaf(x[4 * i], lo_half(p0), a);
+            a = fmaf(x[4 * i + 1], hi_half(p0), a);
+            a = fmaf(x[4 * i + 2], lo_half(p1), a);
+            a = fmaf(x[4 * i + 3], hi_half(p1), a);
+        }
+        const float d = lo_half(w.d) * (E5M2 ? 1.0f : 256.0f);
+        return nan ? __uint_as_float(0x7fc00000u) : d * a;
+    }
+};
+template <>
+struct ExtSeg<FH_FP8_E4M3> : Fp8Seg<false> {};
+template <>
+struct ExtSeg<FH_FP8_E5M2> : Fp8Seg<true> {};
+
+// MXFP4 (mxfp4.rs:13-33): segment = block s (E8M0 byte, then element i < 16 in the low nibble of
+// byte 1 + i, element 16 + i in its high nibble). Four nibbles at a time become signed bytes
+// through two byte-permute tables (values 0, 1, 2, 3, 4, 6, 8, 12 and their negatives).
+template <>
+struct ExtSeg<FH_MXFP4> {
+    static constexpr uint32_t SPB = 1, XN = 32;
+    struct W {
+        uint32_t e;
+        u32x4 q;
+    };
+    __device__ static void load(const uint8_t *row, uint32_t s, W &w) {
+        const uint8_t *blk = row + 17 * s;
+        w.e = blk[0];
+        w.q = ld16_any(blk + 1);
+    }
+    __device__ static uint32_t xat(uint32_t s) { return 32 * s; }
+    __device__ static uint32_t vals(uint32_t n) {  // four nibbles (one per byte) -> four signed bytes
+        const uint32_t m = n & 0x07070707u;
+        const uint32_t pos = __builtin_amdgcn_perm(0x0c080604u, 0x03020100u, m);
+        const uint32_t neg = __builtin_amdgcn_perm(0xf4f8fafcu, 0xfdfeff00u, m);
+        const uint32_t sgn = ((n >> 3) & 0x01010101u) * 0xffu;
+        return (neg & sgn) | (pos & ~sgn);
+    }
+    __device__ static float dot(const W &w, const float (&x)[XN]) {
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lo = vals(w.q[i] & 0x0f0f0f0fu), hi = vals((w.q[i] >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+            for (int j = 0; j < 4; j++) a = fmaf(x[4 * i + j], sbyte(lo, j), a);
+#pragma unroll
+            for (int j = 0; j < 4; j++) a = fmaf(x[16 + 4 * i + j], sbyte(hi, j), a);
+        }
+        return a * mx_half_scale(w.e);
+    }
+};
+
+// Q2_K (blocks.rs:201-250): segment s of super-block s / 8: half h = (s % 8) / 4, quant bytes
+// 16 + 32 h + 8 g .. + 7 (g = s % 4), i.e. elements 128 h + 32 j + 8 g + l for the four 2-bit
+// planes j; plane j's sub-block scale byte is 8 h + 2 j + g / 2. Per plane: d (sc & 15) sum(x q)
+// - dmin (sc >> 4) sum(x).
+template <>
+struct ExtSeg<FH_Q2_K> {
+    static constexpr uint32_t SPB = 8, XN = 32;
+    struct W {
+        uint32_t q0, q1, s0, s1, dd;
+    };
+    __device__ static void load(const uint8_t *row, uint32_t s, W &w) {
+        const uint8_t *blk = row + 84 * (s / 8);
+        const uint32_t h = (s % 8) / 4, g = s % 4;
+        w.q0 = ld32(blk + 16 + 32 * h + 8 * g);
+        w.q1 = ld32(blk + 20 + 32 * h + 8 * g);
+        w.s0 = ld32(blk + 8 * h);
+        w.s1 = ld32(blk + 8 * h + 4);
+        w.dd = ld32(blk + 80);
+    }
+    // x of the segment: plane j's 8 elements at x[xat(s) + 32 j ..]
+    __device__ static uint32_t xat(uint32_t s) { return 256 * (s / 8) + 128 * ((s % 8) / 4) + 8 * (s % 4); }
+    __device__ static float dot(const W &w, const float (&x)[XN], uint32_t s, const float (&xs)[4]) {
+        const float d = lo_half(w.dd), dmin = hi_half(w.dd);
+        const uint32_t g2 = (s % 4) / 2;
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t v0 = (w.q0 >> (2 * j)) & 0x03030303u, v1 = (w.q1 >> (2 * j)) & 0x03030303u;
+            float t = 0.0f;
+#pragma unroll
+            for (int l = 0; l < 4; l++) t = fmaf(x[8 * j + l], ubyte(v0, l), t);
+#pragma unroll
+            for (int l = 0; l < 4; l++) t = fmaf(x[8 * j + 4 + l], ubyte(v1, l), t);
+            const uint32_t sc = ((j < 2 ? w.s0 : w.s1) >> (8 * (2 * (j % 2) + g2))) & 0xffu;
+            a = fmaf(d * (float)(sc & 15u), t, a);
+            a = fmaf(-(dmin * (float)(sc >> 4)), xs[j], a);
+        }
+        return a;
+    }
+};
+
+template <uint32_t T>
+__device__ __forceinline__ void ext_load_x(const float *__restrict__ x, uint32_t s, float (&xv)[ExtSeg<T>::XN]) {
+    using S = ExtSeg<T>;
+    if constexpr (T == FH_Q2_K) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const f32x4 a = *(const f32x4 *)(x + S::xat(s) + 32 * j), b = *(const f32x4 *)(x + S::xat(s) + 32 * j + 4);
+#pragma unroll
+            for (int l = 0; l < 4; l++) {
+                xv[8 * j + l] = a[l];
+                xv[8 * j + 4 + l] = b[l];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < (int)S::XN / 4; i++) {
+            const f32x4 a = *(const f32x4 *)(x + S::xat(s) + 4 * i);
+#pragma unroll
+            for (int l = 0; l < 4; l++) xv[4 * i + l] = a[l];
+        }
+    }
+}
+
+template <uint32_t T, uint32_t R>
+__global__ __launch_bounds__(256) void ext_gemv_rows_kernel(const uint8_t *__restrict__ w, const float *__restrict__ x,
+                                                            float *__restrict__ y, uint32_t k, uint32_t n,
+                                                            uint32_t lg) {
+    using F = Fmt<T>;
+    using S = ExtSeg<T>;
+    constexpr uint32_t kExtRows = R;
+    __shared__ float red[4][kExtRows];
+    const uint32_t L = 1u << lg, tid = threadIdx.x, l = tid & (L - 1);
+    const uint32_t grp = blockIdx.x * (256u >> lg) + (tid >> lg), r0 = grp * kExtRows;
+    const size_t row_bytes = (size_t)(k / F::E) * F::B;
+    const uint32_t segs = (k / F::E) * S::SPB;
+    float acc[kExtRows] = {};
+    if (r0 < n) {
+        const uint8_t *rows[kExtRows];
+#pragma unroll
+        for (uint32_t r = 0; r < kExtRows; r++) rows[r] = w + (size_t)min(r0 + r, n - 1) * row_bytes;
+#pragma unroll 2
+        for (uint32_t s = l; s < segs; s += L) {
+            float xv[S::XN];
+            ext_load_x<T>(x, s, xv);
+            typename S::W wv[kExtRows];
+#pragma unroll
+            for (uint32_t r = 0; r < kExtRows; r++) S::load(rows[r], s, wv[r]);
+            if constexpr (T == FH_Q2_K) {
+                float xs[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float t = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) t += xv[8 * j + e];
+                    xs[j] = t;
+                }
+#pragma unroll
+                for (uint32_t r = 0; r < kExtRows; r++) acc[r] += S::dot(wv[r], xv, s, xs);
+            } else {
+#pragma unroll
+                for (uint32_t r = 0; r < kExtRows; r++) acc[r] += S::dot(wv[r], xv);
+            }
+        }
+    }
+    // sum over the L lanes of the group: within the wavefront by shuffles, across wavefronts in LDS
+#pragma unroll
+    for (uint32_t o = 32; o; o >>= 1)
+        if (o < L)
+#pragma unroll
+            for (uint32_t r = 0; r < kExtRows; r++) acc[r] += __shfl_xor(acc[r], (int)o);
+    if (L > 64) {  // uniform over the launch
+        if ((tid & 63) == 0)
+#pragma unroll
+            for (uint32_t r = 0; r < kExtRows; r++) red[tid / 64][r] = acc[r];
+        __syncthreads();
+        if (l == 0) {
+            const uint32_t w0 = tid / 64, nw = L / 64;
+#pragma unroll
+            for (uint32_t r = 0; r < kExtRows; r++) {
+                float t = red[w0][r];
+                for (uint32_t i = 1; i < nw; i++) t += red[w0 + i][r];
+                acc[r] = t;
+            }
+        }
+    }
+    if (l == 0)
+#pragma unroll
+        for (uint32_t r = 0; r < kExtRows; r++)
+            if (r0 + r < n) y[r0 + r] = acc[r];
+}
+
+// Rows per lane group R (at most max_rows: 8, 4, 2 or 1) and lanes per group 2^lg (at most 256 and
+// at most the row's segments): the largest R whose grid still holds about four wavefronts per
+// SIMD, with about four segments per lane where the grid is that large already.
+void ext_gemv_shape(uint32_t segs, uint64_t n, uint32_t max_rows, uint32_t *rows, uint32_t *lg) {
+    constexpr uint64_t kTargetLanes = 256ull * 4 * 4 * 64;
+    auto floor_log2 = [](uint64_t v) {
+        uint32_t l = 0;
+        while ((2ull << l) <= v) l++;
+        return l;
+    };
+    const uint32_t cap = min(8u, floor_log2(max(segs, 1u)));
+    const uint32_t work = min(cap, floor_log2(max(segs / 4, 1u)));
+    for (uint32_t r = max_rows;; r /= 2) {
+        const uint64_t groups = (n + r - 1) / r;
+        uint32_t l = work;
+        while (l < cap && (groups << l) < kTargetLanes) l++;
+        if ((groups << l) >= kTargetLanes || r == 1) {
+            *rows = r;
+            *lg = l;
+            return;
+        }
+    }
 }
 
 // Several rows: 32 x 64 output tiles; per 32-k step the x tile and the decoded weight tile
@@ -492,8 +782,23 @@ hipError_t linear_as(hipStream_t s, fh_path path, const uint8_t *w, const float 
     if (path == FH_PATH_NAIVE) {
         ext_naive_kernel<T><<<(unsigned)((rows * n + 255) / 256), 256, 0, s>>>(w, x, y, (uint32_t)rows, (uint32_t)k,
                                                                                (uint32_t)n);
-    } else if (path == FH_PATH_GEMV) {
+    } else if (path == FH_PATH_GEMV && ((uintptr_t)x & 15)) {  // x not 16-byte aligned: scalar loads
         ext_gemv_kernel<T><<<(unsigned)n, 256, 0, s>>>(w, x, y, (uint32_t)k);
+    } else if (path == FH_PATH_GEMV) {
+        uint32_t r, lg;
+        // MXFP4 reads more x than weight bytes per segment: up to eight rows share it
+        constexpr uint32_t kMaxRows = T == FH_MXFP4 ? 8 : 4;
+        ext_gemv_shape((uint32_t)(k / Fmt<T>::E * ExtSeg<T>::SPB), n, kMaxRows, &r, &lg);
+        const uint64_t per_cta = (256u >> lg) * r;
+        const unsigned grid = (unsigned)((n + per_cta - 1) / per_cta);
+        if (r == 8)
+            ext_gemv_rows_kernel<T, kMaxRows><<<grid, 256, 0, s>>>(w, x, y, (uint32_t)k, (uint32_t)n, lg);
+        else if (r == 4)
+            ext_gemv_rows_kernel<T, 4><<<grid, 256, 0, s>>>(w, x, y, (uint32_t)k, (uint32_t)n, lg);
+        else if (r == 2)
+            ext_gemv_rows_kernel<T, 2><<<grid, 256, 0, s>>>(w, x, y, (uint32_t)k, (uint32_t)n, lg);
+        else
+            ext_gemv_rows_kernel<T, 1><<<grid, 256, 0, s>>>(w, x, y, (uint32_t)k, (uint32_t)n, lg);
     } else {
         const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((rows + 31) / 32));
         ext_tiled_kernel<T><<<grid, 256, 0, s>>>(w, x, y, (uint32_t)rows, (uint32_t)k, (uint32_t)n);

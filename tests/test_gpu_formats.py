@@ -237,6 +237,122 @@ def test_larger_products_stay_within_reducing(fh, g, orc):
             assert e <= REDUCING
 
 
+def _close_or_same_special(got, want):
+    """NaN where the CPU has NaN, the same infinity where it has one, REDUCING elsewhere."""
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    inf = np.isinf(want)
+    assert np.array_equal(got[inf], want[inf])
+    fin = np.isfinite(want)
+    assert np.all(np.isfinite(got[fin]))
+    e = orc_max_rel(got[fin], want[fin])
+    assert e <= REDUCING, e
+
+
+def orc_max_rel(got, want):
+    return float(np.max(np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want), 1.0))) if got.size else 0.0
+
+
+def _block_bytes(fh, kind, rows, k, fill):
+    """GGUF rows of `kind` built byte by byte: fill(r, b) -> the bytes of block b of row r."""
+    bb = kind.file_bytes()
+    out = np.zeros((rows, k // kind.elems(), bb), np.uint8)
+    for r in range(rows):
+        for b in range(k // kind.elems()):
+            out[r, b] = fill(r, b)
+    return out.reshape(-1)
+
+
+def test_gemv_decodes_every_code_like_the_cpu(fh, g, orc):
+    """The one-row GEMV on hand-built blocks holding every code of each format (FP8 E4M3 / E5M2
+    including NaN and infinity codes, every MXFP4 nibble pair under E8M0 scales down to the
+    denormal ones, every finite F16 pattern), against the CPU matmul on the oracle's decode: NaN and
+    infinities where the CPU has them, REDUCING elsewhere."""
+    rng = np.random.default_rng(31)
+    scales = np.float16([1.0, 0.5, 2.0, 1e-3, 3.0, -0.75, 2.0 ** -20, 0.25]).view(np.uint16)
+    cases = []
+    for kind in (fh.QKind.Fp8E4M3, fh.QKind.Fp8E5M2):
+        bad = [0x7f, 0xff] if kind == fh.QKind.Fp8E4M3 else [0x7c, 0x7d, 0x7e, 0x7f, 0xfc, 0xfd, 0xfe, 0xff]
+        k, rows = 512, 6
+
+        top = 0x7e if kind == fh.QKind.Fp8E4M3 else 0x7c  # the largest finite E4M3 / E5M2's +infinity
+
+        def fill(r, b, bad=bad, top=top):
+            codes = (np.arange(32) + 32 * b + 7 * r) % 256
+            if r != 1:  # row 1 keeps its NaN / infinity codes
+                codes = np.where(np.isin(codes, bad), 0, codes)
+            if r == 2 and b == 3:  # row 2 holds one +infinity (E5M2)
+                codes[0] = top
+            return np.concatenate([np.frombuffer(scales[(b + r) % 8].tobytes(), np.uint8), codes.astype(np.uint8)])
+
+        cases.append((kind, k, rows, _block_bytes(fh, kind, rows, k, fill)))
+    e8 = [0, 1, 2, 3, 125, 126, 127, 128, 129, 130, 120, 127, 131, 124, 127, 128]
+    cases.append((fh.QKind.Fp4, 512, 4, _block_bytes(
+        fh, fh.QKind.Fp4, 4, 512,
+        lambda r, b: np.concatenate([[e8[(b + r) % 16]], (np.arange(16) + 16 * b + 37 * r) % 256]).astype(np.uint8))))
+    pats = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = np.isfinite(pats.view(np.float16))
+    pats = np.where(finite, pats, 0).astype(np.uint16)
+    cases.append((fh.QKind.F16, 65536, 1, pats.view(np.uint8).copy()))
+    for kind, k, rows, raw in cases:
+        wd = orc.transpose(orc.decode(oid(orc, kind), raw, k * rows), rows, k)
+        x = (rng.standard_normal(k) * (1e-3 if kind == fh.QKind.F16 else 1.0)).astype(np.float32)
+        want = orc.matmul(x, wd, 1, k, rows)
+        qw = fh.upload_qweight(g, kind, raw, k, rows)
+        gy = g.zeros(rows)
+        fh.linear_q_with(g, g.upload(x), qw, gy, 1, fh.QPath.Gemv)
+        got = g.read(gy)
+        say(f"{kind.label()}: {got} vs {want}")
+        _close_or_same_special(got, want)
+        qw.free()
+
+
+def test_gemv_takes_x_at_any_float_offset(fh, g, orc):
+    """x handed over as a raw pointer 4, 8, 12 and 16 bytes into a buffer: the misaligned ones run
+    the scalar-load GEMV, the aligned one the segment GEMV; all within REDUCING."""
+    rng = np.random.default_rng(32)
+    for kind in ext(fh):
+        k, n = (512, 37) if kind == fh.QKind.Q2K else (96, 37)
+        b = orc.quantise_matrix(oid(orc, kind), (rng.standard_normal(k * n) * 0.02).astype(np.float32), k, n)
+        wd = orc.transpose(orc.decode(oid(orc, kind), b, k * n), n, k)
+        qw = fh.upload_qweight(g, kind, b, k, n)
+        x = rng.standard_normal(k + 4).astype(np.float32)
+        gx = g.upload(x)
+        for off in (1, 2, 3, 4):
+            want = orc.matmul(x[off:off + k].copy(), wd, 1, k, n)
+            gy = g.zeros(n)
+            fh.linear_q_ptr(g, gx.device_ptr() + 4 * off, qw, gy.device_ptr(), 1, fh.QPath.Gemv)
+            e = orc.max_rel_err(g.read(gy), want)
+            assert e <= REDUCING, (kind, off, e)
+        qw.free()
+
+
+def test_gemv_launch_shapes_cover_every_row_grouping(fh, g, orc):
+    """k = 2048 with 3001, 4101 and 16401 output rows (and 33001 for MXFP4), so the GEMV
+    runs with groups of 8, 4, 2 and 1 rows and partial groups at the end, within REDUCING. Q2_K rows are random bytes under fixed
+    super-block scales (any such bytes decode to finite values)."""
+    rng = np.random.default_rng(33)
+    k = 2048
+    for kind in ext(fh):
+        for n in (3001, 4101, 16401) + ((33001,) if kind == fh.QKind.Fp4 else ()):
+            if kind == fh.QKind.Q2K:
+                raw = rng.integers(0, 256, (n * k // 256, 84), dtype=np.uint8)
+                raw[:, 80:84] = np.frombuffer(np.float16([0.001, 0.0004]).tobytes(), np.uint8)  # |w| ~ 0.02
+                raw = raw.reshape(-1)
+            else:
+                raw = orc.quantise_matrix(oid(orc, kind), (rng.standard_normal(k * n) * 0.02).astype(np.float32), k, n)
+            wd = orc.transpose(orc.decode(oid(orc, kind), raw, k * n), n, k)
+            x = rng.standard_normal(k).astype(np.float32)
+            want = orc.matmul(x, wd, 1, k, n)
+            qw = fh.upload_qweight(g, kind, raw, k, n)
+            gy = g.zeros(n)
+            fh.linear_q_with(g, g.upload(x), qw, gy, 1, fh.QPath.Gemv)
+            e = orc.max_rel_err(g.read(gy), want)
+            say(f"{kind.label()} 1x{k}x{n}: {e:.2e}")
+            assert e <= REDUCING, (kind, n, e)
+            qw.free()
+
+
 def test_gguf_uploads_of_the_new_formats(fh, g, orc):
     """A GGUF holding MXFP4, Q2_K and F16 matrices and read-only block tensors: the matrices
     upload as resident weights (bytes kept), every tensor decodes on the device as the oracle
