@@ -184,7 +184,19 @@ __global__ __launch_bounds__(256) void split_x_precise_kernel(const float *__res
         const f32x4 v = __builtin_nontemporal_load((const f32x4 *)(x + t * 32) + j);
         _Float16 *out = xs + t * 64;
         typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-        if constexpr (KIND == FH_Q8_0) {
+        if constexpr (KIND == 0) {  // natural k order (the other formats' MFMA GEMM)
+            const float e[4] = {v.x, v.y, v.z, v.w};
+            f16x4 hi, lo;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                _Float16 h, l;
+                split1(e[q], h, l);
+                hi[q] = h;
+                lo[q] = l;
+            }
+            *(f16x4 *)(out + 4 * j) = hi;
+            *(f16x4 *)(out + 32 + 4 * j) = lo;
+        } else if constexpr (KIND == FH_Q8_0) {
             // positions 4j..4j+3 hold elements 4j + {0, 2, 1, 3}
             const float e[4] = {v.x, v.z, v.y, v.w};
             f16x4 hi, lo;
@@ -813,6 +825,275 @@ hipError_t gemm_precise_dispatch(hipStream_t s, const _Float16 *xs, const uint8_
     return run_gemm_precise<KIND, 128, 128, 2>(s, xs, qs, ds, y, partial, M, K, N, defer);
 }
 
+// ---- the MFMA GEMM on the other weight formats' GGUF rows (F16, FP8 E4M3 / E5M2, MXFP4) ----
+// Every element of these formats is an f16-exact value times a per-32-block f32 scale: F16 its
+// own value (scale 1), E5M2 code c the f16 with bits c << 8 (fp8.rs:34-63), E4M3 code c the f16
+// with bits (c & 0x7f) << 7 | (c & 0x80) << 8 times 2^8 (normal and subnormal alike), MXFP4
+// nibble v the integer 0, 1, 2, 3, 4, 6, 8, 12 or its
+// negative (mxfp4.rs:13-14) times the E8M0 half scale. A block holding a non-finite value (an
+// F16 or E5M2 infinity or NaN, an E4M3 NaN) gets a NaN scale, so its outputs are NaN: the split
+// x would otherwise meet an infinity with lo = 0 or of the other sign. The precise GEMM's
+// arithmetic applies unchanged: x = hi + lo in f16 (natural k order here), per 32 x 32 tile and block
+// P = hi * v + lo * v on four v_mfma_f32_32x32x16_f16, acc += scale * P. Per stage (one block)
+// thread t < BN decodes column n0 + t's block from its row (unaligned for FP8 and MXFP4: the
+// dwords around it, realigned with v_alignbyte; allocations carry 256 zero bytes past their end)
+// into 32 f16 in LDS and the block's scale; the next stage's bytes are requested before the
+// current stage's MFMAs.
+__device__ __forceinline__ float e8m0_half_scale(uint32_t e) {  // mxfp4.rs:26-33
+    return e < 2 ? __uint_as_float(0x00200000u << e) : __uint_as_float((e - 1) << 23);
+}
+__device__ __forceinline__ uint32_t mx_biased(uint32_t n) {  // 4 nibbles (one per byte) -> value + 16 per byte
+    const uint32_t m = n & 0x07070707u;
+    const uint32_t pos = __builtin_amdgcn_perm(0x1c181614u, 0x13121110u, m);
+    const uint32_t neg = __builtin_amdgcn_perm(0x04080a0cu, 0x0d0e0f10u, m);
+    const uint32_t sgn = ((n >> 3) & 0x01010101u) * 0xffu;
+    return (neg & sgn) | (pos & ~sgn);
+}
+
+template <uint32_t T>
+struct ExtBlock;  // raw bytes of one block of a column, held in registers between stages
+template <>
+struct ExtBlock<FH_F16> {
+    static constexpr uint32_t B = 64;
+    u32x4 q[4];
+    __device__ void load(const uint8_t *blk) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[i] = *(const u32x4 *)(blk + 16 * i);
+    }
+    __device__ float unpack(u32x4 (&o)[4]) const {
+        uint32_t bad = 0;  // an infinity or NaN half (exponent bits all ones)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o[i] = q[i];
+#pragma unroll
+            for (int c = 0; c < 4; c++) bad |= ((q[i][c] & 0x7c007c00u) + 0x04000400u) & 0x80008000u;
+        }
+        return bad ? __uint_as_float(0x7fc00000u) : 1.0f;
+    }
+};
+template <bool E5M2>
+struct Fp8Block {
+    static constexpr uint32_t B = 34;
+    uint32_t d[9], sh;  // the dwords around the block, its byte offset in the first
+    __device__ void load(const uint8_t *blk) {
+        sh = (uint32_t)((uintptr_t)blk & 3);
+        const uint8_t *q = blk - sh;
+#pragma unroll
+        for (int i = 0; i < 9; i++) d[i] = *(const uint32_t *)(q + 4 * i);
+    }
+    __device__ float unpack(u32x4 (&o)[4]) const {
+        uint32_t a[9];  // block bytes 0 .. 35
+#pragma unroll
+        for (int i = 0; i < 8; i++) a[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
+        a[8] = d[8] >> (8 * sh);
+        uint32_t nan = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {  // codes 4i .. 4i + 3 = bytes 2 + 4i .. 5 + 4i
+            const uint32_t v = __builtin_amdgcn_alignbyte(a[i + 1], a[i], 2);
+            uint32_t p0, p1;
+            if constexpr (E5M2) {
+                p0 = __builtin_amdgcn_perm(v, 0u, 0x050c040cu);
+                p1 = __builtin_amdgcn_perm(v, 0u, 0x070c060cu);
+                nan |= ((v & 0x7c7c7c7cu) + 0x04040404u) & 0x80808080u;  // infinity and NaN codes
+            } else {
+                const uint32_t t0 = __builtin_amdgcn_perm(v, 0u, 0x0c050c04u), t1 = __builtin_amdgcn_perm(v, 0u, 0x0c070c06u);
+                p0 = ((t0 & 0x007f007fu) << 7) | ((t0 & 0x00800080u) << 8);
+                p1 = ((t1 & 0x007f007fu) << 7) | ((t1 & 0x00800080u) << 8);
+                nan |= ((v & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
+            }
+            o[i / 2][2 * (i % 2)] = p0;
+            o[i / 2][2 * (i % 2) + 1] = p1;
+        }
+        const float sc = half_to_float(a[0] & 0xffffu) * (E5M2 ? 1.0f : 256.0f);
+        return nan ? __uint_as_float(0x7fc00000u) : sc;
+    }
+};
+template <>
+struct ExtBlock<FH_FP8_E4M3> : Fp8Block<false> {};
+template <>
+struct ExtBlock<FH_FP8_E5M2> : Fp8Block<true> {};
+template <>
+struct ExtBlock<FH_MXFP4> {
+    static constexpr uint32_t B = 17;
+    uint32_t d[6], sh;
+    __device__ void load(const uint8_t *blk) {
+        sh = (uint32_t)((uintptr_t)blk & 3);
+        const uint8_t *q = blk - sh;
+#pragma unroll
+        for (int i = 0; i < 6; i++) d[i] = *(const uint32_t *)(q + 4 * i);
+    }
+    __device__ float unpack(u32x4 (&o)[4]) const {
+        uint32_t a[5];  // block bytes 0 .. 19
+#pragma unroll
+        for (int i = 0; i < 5; i++) a[i] = __builtin_amdgcn_alignbyte(d[i + 1], d[i], sh);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {  // nibble bytes 4i .. 4i + 3 (block bytes 1 + 4i ..)
+            const uint32_t v = __builtin_amdgcn_alignbyte(a[i + 1], a[i], 1);
+            const uint32_t lo = mx_biased(v & 0x0f0f0f0fu), hi = mx_biased((v >> 4) & 0x0f0f0f0fu);
+            // elements 4i .. 4i + 3 (low nibbles) and 16 + 4i .. (high): 1024 + value + 16, - 1040
+            const uint32_t l0 = f16x2_add(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u), (_Float16)-1040.0f);
+            const uint32_t l1 = f16x2_add(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u), (_Float16)-1040.0f);
+            const uint32_t h0 = f16x2_add(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u), (_Float16)-1040.0f);
+            const uint32_t h1 = f16x2_add(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u), (_Float16)-1040.0f);
+            o[i / 2][2 * (i % 2)] = l0;
+            o[i / 2][2 * (i % 2) + 1] = l1;
+            o[2 + i / 2][2 * (i % 2)] = h0;
+            o[2 + i / 2][2 * (i % 2) + 1] = h1;
+        }
+        return e8m0_half_scale(a[0] & 0xffu);
+    }
+};
+
+template <uint32_t T, int BM, int BN, int WAVES_M>
+__global__ __launch_bounds__(256, 2) void gemm_ext_kernel(const _Float16 *__restrict__ xs, const uint8_t *__restrict__ w,
+                                                          float *__restrict__ y, uint32_t M, uint32_t K, uint32_t N,
+                                                          uint32_t mt, uint32_t nt, uint32_t split_stages) {
+    constexpr int WAVES_N = 4 / WAVES_M, TM = BM / WAVES_M / 32, TN = BN / WAVES_N / 32;
+    constexpr int A_LD = BM * 8 / 256;  // 16-byte x chunks per thread per block
+    static_assert(TM >= 1 && TN >= 1 && BM * 8 % 256 == 0 && BN <= 256, "tile shape");
+    using EB = ExtBlock<T>;
+    __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * kARow2];
+    __shared__ __attribute__((aligned(16))) _Float16 sB[2][BN * kBRow2];
+    __shared__ float sD[2][BN];
+
+    const uint32_t tiles = mt * nt, c = blockIdx.x, per_xcd = (tiles + 7) / 8;
+    const uint32_t t = (c % 8) * per_xcd + c / 8;
+    if (t >= tiles) return;  // whole CTA: no barrier is left waiting
+    const uint32_t m0 = (t / nt) * BM, n0 = (t % nt) * BN;
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const int wm = wave % WAVES_M, wn = wave / WAVES_M;
+    const uint32_t nb = K / 32;
+    const uint32_t st0 = blockIdx.y * split_stages, st1 = min(nb, st0 + split_stages);
+    y += (size_t)blockIdx.y * M * N;
+    const size_t row_bytes = (size_t)nb * EB::B;
+    const uint32_t wcol = n0 + tid;  // the column this thread decodes (tid < BN)
+    const uint8_t *wrow = w + (size_t)min(wcol, N - 1) * row_bytes;
+
+    u32x4 ra[A_LD];
+    EB rb;
+    auto load_stage = [&](uint32_t kb) {
+#pragma unroll
+        for (int i = 0; i < A_LD; i++) {
+            const int cc = tid + 256 * i, r = cc / 8, ch = cc % 8;
+            const uint32_t m = m0 + r;
+            ra[i] = m < M ? *(const u32x4 *)(xs + ((size_t)m * nb + kb) * 64 + ch * 8) : u32x4{0u, 0u, 0u, 0u};
+        }
+        if (tid < BN) rb.load(wrow + (size_t)kb * EB::B);
+    };
+    auto store_stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_LD; i++) {
+            const int cc = tid + 256 * i, r = cc / 8, ch = cc % 8;
+            *(u32x4 *)(&sA[buf][r * kARow2 + ch * 8]) = ra[i];
+        }
+        if (tid < BN) {
+            u32x4 o[4];
+            float sc = rb.unpack(o);
+            if (wcol >= N) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) o[i] = u32x4{0u, 0u, 0u, 0u};
+                sc = 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) *(u32x4 *)(&sB[buf][tid * kBRow2 + 8 * i]) = o[i];
+            sD[buf][tid] = sc;
+        }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    const int fr = lane % 32, fk = 8 * (lane / 32);
+
+    if (st0 < st1) {
+        load_stage(st0);
+        store_stage(0);
+    }
+    __syncthreads();
+    for (uint32_t kb = st0; kb < st1; kb++) {
+        const int buf = (kb - st0) & 1;
+        const bool more = kb + 1 < st1;
+        if (more) load_stage(kb + 1);  // in flight during the MFMAs below
+        f16x8 bf[TN][2];
+        float dcol[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int col = (wn * TN + j) * 32 + fr;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) bf[j][s2] = *(const f16x8 *)(&sB[buf][col * kBRow2 + 16 * s2 + fk]);
+            dcol[j] = sD[buf][col];
+        }
+        f16x8 ah[TM][2], al[TM][2];
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int r = (wm * TM + i) * 32 + fr;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) {
+                ah[i][s2] = *(const f16x8 *)(&sA[buf][r * kARow2 + 16 * s2 + fk]);
+                al[i][s2] = *(const f16x8 *)(&sA[buf][r * kARow2 + 32 + 16 * s2 + fk]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                f32x16 p = {};
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], bf[j][0], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], bf[j][1], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][0], bf[j][0], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][1], bf[j][1], p, 0, 0, 0);
+#pragma unroll
+                for (int q = 0; q < 16; q++) acc[i][j][q] = fmaf(dcol[j], p[q], acc[i][j][q]);
+            }
+        if (more) store_stage(buf ^ 1);  // nobody reads buf ^ 1 during this stage
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const uint32_t col = n0 + (wn * TN + j) * 32 + fr;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = m0 + (wm * TM + i) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+                if (row < M && col < N) y[(size_t)row * N + col] = acc[i][j][r];
+            }
+        }
+}
+
+template <uint32_t T, int BM, int BN, int WAVES_M>
+hipError_t run_gemm_ext(hipStream_t s, const _Float16 *xs, const uint8_t *w, float *y, float *partial, uint32_t M,
+                        uint32_t K, uint32_t N) {
+    const uint32_t mt = (M + BM - 1) / BM, nt = (N + BN - 1) / BN;
+    const uint64_t tiles = (uint64_t)mt * nt;
+    if (tiles > 0x7fffffffull) return hipErrorInvalidValue;
+    const uint32_t grid = (uint32_t)((tiles + 7) / 8 * 8);
+    const uint32_t stages = K / 32;
+    const uint32_t sp = partial ? precise_splits(M, K, N) : 1;
+    const uint32_t per = (stages + sp - 1) / sp;
+    float *out = sp > 1 ? partial : y;
+    gemm_ext_kernel<T, BM, BN, WAVES_M><<<dim3(grid, sp), 256, 0, s>>>(xs, w, out, M, K, N, mt, nt, per);
+    if (sp > 1) {
+        const size_t n = (size_t)M * N;
+        const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
+        gemm_reduce_kernel<<<rg, 256, 0, s>>>(partial, y, n, sp);
+    }
+    return hipGetLastError();
+}
+
+template <uint32_t T>
+hipError_t gemm_ext_dispatch(hipStream_t s, const _Float16 *xs, const uint8_t *w, float *y, float *partial,
+                             uint32_t M, uint32_t K, uint32_t N) {
+    if (M <= 32) return run_gemm_ext<T, 32, 256, 1>(s, xs, w, y, partial, M, K, N);
+    if (M <= 64) return run_gemm_ext<T, 64, 128, 2>(s, xs, w, y, partial, M, K, N);
+    return run_gemm_ext<T, 128, 128, 2>(s, xs, w, y, partial, M, K, N);
+}
+
 // ---- the dequant-f16 GEMM (FH_PATH_TILED_F16): weights dequantised into LDS, plain f16 MFMA ----
 // x -> f16 of x 2^-s per row (2^s puts the row's largest |x| in [2^14, 2^15), so no element
 // overflows and every one keeps f16's 11 bits), in operand order, and xs[m] = 2^s.
@@ -1428,6 +1709,29 @@ hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, c
     split_x_precise_kernel<FH_Q4_0><<<g, 256, 0, s>>>(x, xs, items);
     return gemm_precise_dispatch<FH_Q4_0>(s, xs, qs, ds, y, partial, (uint32_t)rows, (uint32_t)k, (uint32_t)n,
                                           defer);
+}
+
+bool gemm_ext_kind(int kind) {
+    return kind == FH_F16 || kind == FH_FP8_E4M3 || kind == FH_FP8_E5M2 || kind == FH_MXFP4;
+}
+
+hipError_t launch_gemm_ext(hipStream_t s, int kind, const uint8_t *w, const float *x, float *y, size_t rows, size_t k,
+                           size_t n, void *workspace) {
+    _Float16 *xs = (_Float16 *)workspace;
+    float *partial = precise_splits(rows, k, n) > 1
+                         ? (float *)((uint8_t *)workspace + (rows * k * 4 + 255) / 256 * 256)
+                         : nullptr;
+    const size_t items = rows * (k / 32);
+    const unsigned g = (unsigned)(items / 32 + 1 < 65535 ? items / 32 + 1 : 65535);
+    split_x_precise_kernel<0><<<g, 256, 0, s>>>(x, xs, items);
+    const uint32_t M = (uint32_t)rows, K = (uint32_t)k, N = (uint32_t)n;
+    switch (kind) {
+    case FH_F16: return gemm_ext_dispatch<FH_F16>(s, xs, w, y, partial, M, K, N);
+    case FH_FP8_E4M3: return gemm_ext_dispatch<FH_FP8_E4M3>(s, xs, w, y, partial, M, K, N);
+    case FH_FP8_E5M2: return gemm_ext_dispatch<FH_FP8_E5M2>(s, xs, w, y, partial, M, K, N);
+    case FH_MXFP4: return gemm_ext_dispatch<FH_MXFP4>(s, xs, w, y, partial, M, K, N);
+    default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,

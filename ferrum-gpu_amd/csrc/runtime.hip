@@ -683,11 +683,18 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
                         fh_path path, void *fixed = nullptr) {
     if (path == FH_PATH_AUTO) path = fh_choose(rows, w->kind, w->k, w->n);
     fh_status st;
-    if (ext_kind(w->kind)) {  // decoded on the fly, f32 products (formats.hip)
+    if (ext_kind(w->kind)) {  // decoded on the fly (formats.hip; the multi-row MFMA GEMM in gemm.hip)
         if (path != FH_PATH_NAIVE && path != FH_PATH_GEMV && path != FH_PATH_TILED)
             return fail(FH_ERR_UNSUPPORTED, "kernel path %d does not take %s weights", (int)path, ext_label(w->kind));
         if (path == FH_PATH_GEMV && rows != 1)
             return fail(FH_ERR_INVALID, "the GEMV kernel takes one row, not %zu", rows);
+        if (path == FH_PATH_TILED && rows >= 2 && gemm_ext_kind(w->kind)) {  // the MFMA GEMM (gemm.hip)
+            void *ws = nullptr;
+            if ((st = command_scratch(dev, fixed, gemm_precise_workspace_bytes(rows, w->k, w->n), &ws))) return st;
+            if ((st = begin_command(dev, "linear_q"))) return st;
+            (void)launch_gemm_ext(dev->stream, w->kind, w->qs, x, y, rows, w->k, w->n, ws);
+            return end_command(dev, "linear_q");
+        }
         if ((st = begin_command(dev, "linear_q"))) return st;
         (void)launch_linear_ext(dev->stream, w->kind, path, w->qs, x, y, rows, w->k, w->n);
         return end_command(dev, "linear_q");

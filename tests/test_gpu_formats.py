@@ -250,7 +250,8 @@ def _close_or_same_special(got, want):
 
 
 def orc_max_rel(got, want):
-    return float(np.max(np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want), 1.0))) if got.size else 0.0
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want) / np.maximum(np.abs(want), 1.0))) if got.size else 0.0
 
 
 def _block_bytes(fh, kind, rows, k, fill):
@@ -304,6 +305,52 @@ def test_gemv_decodes_every_code_like_the_cpu(fh, g, orc):
         got = g.read(gy)
         say(f"{kind.label()}: {got} vs {want}")
         _close_or_same_special(got, want)
+        qw.free()
+
+
+def test_mfma_gemm_on_every_code(fh, g, orc):
+    """The multi-row MFMA GEMM (F16, FP8 E4M3 / E5M2, MXFP4) decodes every code as the CPU does:
+    with x the 512 x 512 identity the product is the decoded weight itself, compared bit for bit
+    with the CPU matmul on the oracle's decode (every FP8 code under f16 scales down to a
+    subnormal one, every MXFP4 nibble pair under E8M0 scales down to the denormal ones, random
+    F16 patterns). A block holding an infinity or NaN makes its output column NaN, as the CPU's
+    0 x inf terms do."""
+    rng = np.random.default_rng(34)
+    scales = np.float16([1.0, 0.5, 2.0, 1e-3, 3.0, -0.75, 2.0 ** -20, 0.25]).view(np.uint16)
+    k, n = 512, 70
+    x = np.eye(k, dtype=np.float32).reshape(-1)
+    for kind in (fh.QKind.Fp8E4M3, fh.QKind.Fp8E5M2, fh.QKind.Fp4, fh.QKind.F16):
+        if kind == fh.QKind.F16:
+            pats = (rng.integers(0, 65536, k * n)).astype(np.uint16)
+            finite = np.isfinite(pats.view(np.float16))
+            keep = np.zeros(k * n, bool)
+            keep[3 * k + 5] = keep[7 * k + 100] = True  # rows 3 and 7 hold one non-finite half each
+            raw = np.where(finite | keep, pats, 0).astype(np.uint16).view(np.uint8).copy()
+        elif kind == fh.QKind.Fp4:
+            e8 = [0, 1, 2, 3, 125, 126, 127, 128, 129, 130, 120, 127, 131, 124, 127, 128]
+            raw = _block_bytes(fh, kind, n, k, lambda r, b: np.concatenate(
+                [[e8[(b + r) % 16]], (np.arange(16) + 16 * b + 37 * r) % 256]).astype(np.uint8))
+        else:
+            bad = [0x7f, 0xff] if kind == fh.QKind.Fp8E4M3 else [0x7c, 0x7d, 0x7e, 0x7f, 0xfc, 0xfd, 0xfe, 0xff]
+
+            def fill(r, b, bad=bad):
+                codes = (np.arange(32) + 32 * b + 7 * r) % 256
+                if r not in (1, 9):  # rows 1 and 9 keep their non-finite codes
+                    codes = np.where(np.isin(codes, bad), 0, codes)
+                return np.concatenate([np.frombuffer(scales[(b + r) % 8].tobytes(), np.uint8),
+                                       codes.astype(np.uint8)])
+
+            raw = _block_bytes(fh, kind, n, k, fill)
+        wd = orc.transpose(orc.decode(oid(orc, kind), raw, k * n), n, k)
+        want = orc.matmul(x, wd, k, k, n)
+        qw = fh.upload_qweight(g, kind, raw, k, n)
+        gy = g.zeros(k * n)
+        fh.linear_q_with(g, g.upload(x), qw, gy, k, fh.QPath.Tiled)
+        got = g.read(gy)
+        nan = np.isnan(want)
+        say(f"{kind.label()}: {int(nan.sum())} NaN outputs, {int(np.isinf(want).sum())} infinite")
+        assert np.array_equal(np.isnan(got), nan), kind
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)), kind
         qw.free()
 
 
