@@ -944,6 +944,41 @@ struct ExtBlock<FH_MXFP4> {
     }
 };
 
+// Q2_K (blocks.rs:201-250): stage kb = elements 32 kb .. 32 kb + 31 of the row, i.e. super-block
+// kb / 8, half h = (kb % 8) / 4, 2-bit plane j = kb % 4: element 128 h + 32 j + l is bits 2j of
+// quant byte 32 h + l, in sub-block 8 h + 2 j + l / 16 (value d (sc & 15) q - dmin (sc >> 4)). Two
+// sub-blocks per stage, each one MFMA k-step: the stage carries both sub-blocks' d (sc & 15) and
+// dmin (sc >> 4), and the kernel subtracts dmin (sc >> 4) times the row's sum of x over the
+// sub-block.
+template <>
+struct ExtBlock<FH_Q2_K> {
+    static constexpr uint32_t B = 84;
+    uint32_t q[8], sc, dd;
+    __device__ void load(const uint8_t *row, uint32_t kb) {
+        const uint8_t *blk = row + 84 * (kb / 8);
+        const uint32_t h = (kb % 8) / 4, j = kb % 4;
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = *(const uint32_t *)(blk + 16 + 32 * h + 4 * i);
+        sc = *(const uint16_t *)(blk + 8 * h + 2 * j);
+        dd = *(const uint32_t *)(blk + 80);
+    }
+    // 32 exact f16 quants and (dl0, dl1, ml0, ml1)
+    __device__ void unpack(uint32_t kb, u32x4 (&o)[4], float (&s4)[4]) const {
+        const uint32_t j = kb % 4;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t v = (q[i] >> (2 * j)) & 0x03030303u;  // elements 4i .. 4i + 3
+            o[i / 2][2 * (i % 2)] = f16x2_add(__builtin_amdgcn_perm(0x64646464u, v, 0x04010400u), (_Float16)-1024.0f);
+            o[i / 2][2 * (i % 2) + 1] = f16x2_add(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u), (_Float16)-1024.0f);
+        }
+        const float d = half_to_float(dd & 0xffffu), dmin = half_to_float(dd >> 16);
+        s4[0] = d * (float)(sc & 15u);
+        s4[1] = d * (float)((sc >> 8) & 15u);
+        s4[2] = dmin * (float)((sc >> 4) & 15u);
+        s4[3] = dmin * (float)((sc >> 12) & 15u);
+    }
+};
+
 template <uint32_t T, int BM, int BN, int WAVES_M>
 __global__ __launch_bounds__(256, 2) void gemm_ext_kernel(const _Float16 *__restrict__ xs, const uint8_t *__restrict__ w,
                                                           float *__restrict__ y, uint32_t M, uint32_t K, uint32_t N,
@@ -952,9 +987,12 @@ __global__ __launch_bounds__(256, 2) void gemm_ext_kernel(const _Float16 *__rest
     constexpr int A_LD = BM * 8 / 256;  // 16-byte x chunks per thread per block
     static_assert(TM >= 1 && TN >= 1 && BM * 8 % 256 == 0 && BN <= 256, "tile shape");
     using EB = ExtBlock<T>;
+    constexpr bool Q2K = T == FH_Q2_K;
+    constexpr int NS = Q2K ? 4 : 1;  // scales per column and stage
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][BM * kARow2];
     __shared__ __attribute__((aligned(16))) _Float16 sB[2][BN * kBRow2];
-    __shared__ float sD[2][BN];
+    __shared__ float sD[2][NS * BN];
+    __shared__ __attribute__((aligned(16))) float sS[2][Q2K ? 2 * BM : 1];  // Q2_K: x sums per row and sub-block
 
     const uint32_t tiles = mt * nt, c = blockIdx.x, per_xcd = (tiles + 7) / 8;
     const uint32_t t = (c % 8) * per_xcd + c / 8;
@@ -965,7 +1003,7 @@ __global__ __launch_bounds__(256, 2) void gemm_ext_kernel(const _Float16 *__rest
     const uint32_t nb = K / 32;
     const uint32_t st0 = blockIdx.y * split_stages, st1 = min(nb, st0 + split_stages);
     y += (size_t)blockIdx.y * M * N;
-    const size_t row_bytes = (size_t)nb * EB::B;
+    const size_t row_bytes = (size_t)(Q2K ? nb / 8 : nb) * EB::B;
     const uint32_t wcol = n0 + tid;  // the column this thread decodes (tid < BN)
     const uint8_t *wrow = w + (size_t)min(wcol, N - 1) * row_bytes;
 
@@ -978,25 +1016,48 @@ __global__ __launch_bounds__(256, 2) void gemm_ext_kernel(const _Float16 *__rest
             const uint32_t m = m0 + r;
             ra[i] = m < M ? *(const u32x4 *)(xs + ((size_t)m * nb + kb) * 64 + ch * 8) : u32x4{0u, 0u, 0u, 0u};
         }
-        if (tid < BN) rb.load(wrow + (size_t)kb * EB::B);
+        if (tid < BN) {
+            if constexpr (Q2K)
+                rb.load(wrow, kb);
+            else
+                rb.load(wrow + (size_t)kb * EB::B);
+        }
     };
-    auto store_stage = [&](int buf) {
+    auto store_stage = [&](int buf, uint32_t kb) {
 #pragma unroll
         for (int i = 0; i < A_LD; i++) {
             const int cc = tid + 256 * i, r = cc / 8, ch = cc % 8;
             *(u32x4 *)(&sA[buf][r * kARow2 + ch * 8]) = ra[i];
+            if constexpr (Q2K) {
+                // chunk ch holds hi (ch < 4) or lo halves 8 (ch % 4) .. + 7: sub-block (ch >> 1) & 1;
+                // the eight lanes of a row meet by shuffles
+                typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+                const h8 v = __builtin_bit_cast(h8, ra[i]);
+                float t = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) t += (float)v[e];
+                t += __shfl_xor(t, 1);
+                t += __shfl_xor(t, 4);
+                if ((ch & 5) == 0) sS[buf][((ch >> 1) & 1) * BM + r] = t;
+            }
         }
         if (tid < BN) {
             u32x4 o[4];
-            float sc = rb.unpack(o);
+            float sc[NS];
+            if constexpr (Q2K)
+                rb.unpack(kb, o, sc);
+            else
+                sc[0] = rb.unpack(o);
             if (wcol >= N) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) o[i] = u32x4{0u, 0u, 0u, 0u};
-                sc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NS; i++) sc[i] = 0.0f;
             }
 #pragma unroll
             for (int i = 0; i < 4; i++) *(u32x4 *)(&sB[buf][tid * kBRow2 + 8 * i]) = o[i];
-            sD[buf][tid] = sc;
+#pragma unroll
+            for (int i = 0; i < NS; i++) sD[buf][i * BN + tid] = sc[i];
         }
     };
 
@@ -1011,7 +1072,7 @@ __global__ __launch_bounds__(256, 2) void gemm_ext_kernel(const _Float16 *__rest
 
     if (st0 < st1) {
         load_stage(st0);
-        store_stage(0);
+        store_stage(0, st0);
     }
     __syncthreads();
     for (uint32_t kb = st0; kb < st1; kb++) {
@@ -1019,13 +1080,14 @@ __global__ __launch_bounds__(256, 2) void gemm_ext_kernel(const _Float16 *__rest
         const bool more = kb + 1 < st1;
         if (more) load_stage(kb + 1);  // in flight during the MFMAs below
         f16x8 bf[TN][2];
-        float dcol[TN];
+        float dcol[TN][NS];
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             const int col = (wn * TN + j) * 32 + fr;
 #pragma unroll
             for (int s2 = 0; s2 < 2; s2++) bf[j][s2] = *(const f16x8 *)(&sB[buf][col * kBRow2 + 16 * s2 + fk]);
-            dcol[j] = sD[buf][col];
+#pragma unroll
+            for (int i = 0; i < NS; i++) dcol[j][i] = sD[buf][i * BN + col];
         }
         f16x8 ah[TM][2], al[TM][2];
 #pragma unroll
@@ -1037,19 +1099,43 @@ __global__ __launch_bounds__(256, 2) void gemm_ext_kernel(const _Float16 *__rest
                 al[i][s2] = *(const f16x8 *)(&sA[buf][r * kARow2 + 32 + 16 * s2 + fk]);
             }
         }
+        if constexpr (Q2K) {
+            // per sub-block s2: P = hi * q + lo * q over its 16 k, acc += dl P - ml sum(x)
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+            for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                f32x16 p = {};
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], bf[j][0], p, 0, 0, 0);
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], bf[j][1], p, 0, 0, 0);
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][0], bf[j][0], p, 0, 0, 0);
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][1], bf[j][1], p, 0, 0, 0);
+                for (int s2 = 0; s2 < 2; s2++) {
+                    f32x4 sx[4];  // this lane's 16 rows: 8 g + 4 (lane / 32) + 0..3
 #pragma unroll
-                for (int q = 0; q < 16; q++) acc[i][j][q] = fmaf(dcol[j], p[q], acc[i][j][q]);
-            }
-        if (more) store_stage(buf ^ 1);  // nobody reads buf ^ 1 during this stage
+                    for (int g = 0; g < 4; g++)
+                        sx[g] = *(const f32x4 *)(&sS[buf][s2 * BM + (wm * TM + i) * 32 + 8 * g + 4 * (lane / 32)]);
+#pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        f32x16 p = {};
+                        p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][s2], bf[j][s2], p, 0, 0, 0);
+                        p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][s2], bf[j][s2], p, 0, 0, 0);
+#pragma unroll
+                        for (int q = 0; q < 16; q++) {
+                            acc[i][j][q] = fmaf(dcol[j][s2], p[q], acc[i][j][q]);
+                            acc[i][j][q] = fmaf(-dcol[j][2 + s2], sx[q / 4][q % 4], acc[i][j][q]);
+                        }
+                    }
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    f32x16 p = {};
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], bf[j][0], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], bf[j][1], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][0], bf[j][0], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][1], bf[j][1], p, 0, 0, 0);
+#pragma unroll
+                    for (int q = 0; q < 16; q++) acc[i][j][q] = fmaf(dcol[j][0], p[q], acc[i][j][q]);
+                }
+        }
+        if (more) store_stage(buf ^ 1, kb + 1);  // nobody reads buf ^ 1 during this stage
         __syncthreads();
     }
 
@@ -1090,7 +1176,8 @@ template <uint32_t T>
 hipError_t gemm_ext_dispatch(hipStream_t s, const _Float16 *xs, const uint8_t *w, float *y, float *partial,
                              uint32_t M, uint32_t K, uint32_t N) {
     if (M <= 32) return run_gemm_ext<T, 32, 256, 1>(s, xs, w, y, partial, M, K, N);
-    if (M <= 64) return run_gemm_ext<T, 64, 128, 2>(s, xs, w, y, partial, M, K, N);
+    // Q2_K's per-sub-block terms need more registers: its 128-row tile would spill
+    if (M <= 64 || T == FH_Q2_K) return run_gemm_ext<T, 64, 128, 2>(s, xs, w, y, partial, M, K, N);
     return run_gemm_ext<T, 128, 128, 2>(s, xs, w, y, partial, M, K, N);
 }
 
@@ -1712,7 +1799,7 @@ hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, c
 }
 
 bool gemm_ext_kind(int kind) {
-    return kind == FH_F16 || kind == FH_FP8_E4M3 || kind == FH_FP8_E5M2 || kind == FH_MXFP4;
+    return kind == FH_F16 || kind == FH_FP8_E4M3 || kind == FH_FP8_E5M2 || kind == FH_MXFP4 || kind == FH_Q2_K;
 }
 
 hipError_t launch_gemm_ext(hipStream_t s, int kind, const uint8_t *w, const float *x, float *y, size_t rows, size_t k,
@@ -1730,6 +1817,7 @@ hipError_t launch_gemm_ext(hipStream_t s, int kind, const uint8_t *w, const floa
     case FH_FP8_E4M3: return gemm_ext_dispatch<FH_FP8_E4M3>(s, xs, w, y, partial, M, K, N);
     case FH_FP8_E5M2: return gemm_ext_dispatch<FH_FP8_E5M2>(s, xs, w, y, partial, M, K, N);
     case FH_MXFP4: return gemm_ext_dispatch<FH_MXFP4>(s, xs, w, y, partial, M, K, N);
+    case FH_Q2_K: return gemm_ext_dispatch<FH_Q2_K>(s, xs, w, y, partial, M, K, N);
     default: return hipErrorInvalidValue;
     }
 }

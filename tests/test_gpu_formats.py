@@ -313,14 +313,19 @@ def test_mfma_gemm_on_every_code(fh, g, orc):
     with x the 512 x 512 identity the product is the decoded weight itself, compared bit for bit
     with the CPU matmul on the oracle's decode (every FP8 code under f16 scales down to a
     subnormal one, every MXFP4 nibble pair under E8M0 scales down to the denormal ones, random
-    F16 patterns). A block holding an infinity or NaN makes its output column NaN, as the CPU's
-    0 x inf terms do."""
+    F16 patterns, random Q2_K super-blocks under varied d and dmin). A block holding an infinity or
+    NaN makes its output column NaN, as the CPU's 0 x inf terms do."""
     rng = np.random.default_rng(34)
     scales = np.float16([1.0, 0.5, 2.0, 1e-3, 3.0, -0.75, 2.0 ** -20, 0.25]).view(np.uint16)
     k, n = 512, 70
     x = np.eye(k, dtype=np.float32).reshape(-1)
-    for kind in (fh.QKind.Fp8E4M3, fh.QKind.Fp8E5M2, fh.QKind.Fp4, fh.QKind.F16):
-        if kind == fh.QKind.F16:
+    for kind in (fh.QKind.Fp8E4M3, fh.QKind.Fp8E5M2, fh.QKind.Fp4, fh.QKind.F16, fh.QKind.Q2K):
+        if kind == fh.QKind.Q2K:
+            raw = rng.integers(0, 256, (n * k // 256, 84), dtype=np.uint8)
+            dd = np.float16(rng.choice([0.01, 0.5, 3.0, 2.0 ** -18, 1e-3], (n * k // 256, 2)))
+            raw[:, 80:84] = dd.view(np.uint8).reshape(-1, 4)
+            raw = raw.reshape(-1)
+        elif kind == fh.QKind.F16:
             pats = (rng.integers(0, 65536, k * n)).astype(np.uint16)
             finite = np.isfinite(pats.view(np.float16))
             keep = np.zeros(k * n, bool)
