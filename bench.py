@@ -272,6 +272,36 @@ def bench_single_calls(fh, g, ev, kind, shapes, reps=3, seed=4):
     return out
 
 
+def bench_ext_gemm(fh, g, ev, kinds, cases, reps=5, seed=6):
+    """Multi-row products on the other weight formats through linear_q (QPath.Tiled: the MFMA GEMM
+    on the GGUF rows, x split included): TFLOP/s per (format, M, K, N)."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for kind in kinds:
+        r = {}
+        for m, k, n in cases:
+            w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+            q = fh.upload_quantised(g, kind, w, k, n)
+            x, y = g.upload(rng.standard_normal(m * k).astype(np.float32)), g.zeros(m * n)
+            for _ in range(2):
+                fh.linear_q_with(g, x, q, y, m, fh.QPath.Tiled)
+            g.sync()
+            e0, e1 = ev.create(2)
+            ev.record(e0)
+            for _ in range(reps):
+                fh.linear_q_with(g, x, q, y, m, fh.QPath.Tiled)
+            ev.record(e1)
+            g.sync()
+            ms = ev.ms(e0, e1) / reps
+            ev.destroy([e0, e1])
+            tf = 2 * m * k * n / (ms * 1e-3) / 1e12
+            r[f"m{m}_{k}x{n}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
+                                  "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+            q.free()
+        out[kind.label()] = r
+    return out
+
+
 def bench_rows_pool(fh, g, ev, kind, m, shapes, steps, copies=12, seed=0):
     """Config 5's few-row products as one grouped launch pair (RowsPlan: x split, then the
     few-row kernel over every product): `copies` distinct copies of `shapes` (12 copies of the
@@ -451,6 +481,11 @@ def bench_scoring(fh, g, ev, ms=(512, 2048), paths=None, reps=5, cpu=True, cpu_r
 # TinyLlama-1.1B block matrices, [in, out]: q, k, v, o, gate, up, down; 22 blocks
 LLAMA1B_MATRICES = [(2048, 2048), (2048, 256), (2048, 256), (2048, 2048), (2048, 5632), (2048, 5632), (5632, 2048)]
 LLAMA1B_LAYERS = 22
+EXT_GEMM_CASES = [(512, 2048, 2048), (4096, 2048, 5632)]
+
+
+def ext_kinds(fh):
+    return (fh.QKind.F16, fh.QKind.Fp8E4M3, fh.QKind.Fp8E5M2, fh.QKind.Fp4, fh.QKind.Q2K)
 
 
 def bench_codec(fh, g, ev, reps=5, copies=8):
@@ -666,12 +701,13 @@ def main():
         return
     if a.ext_only:
         ext = {}
-        for kind in (fh.QKind.F16, fh.QKind.Fp8E4M3, fh.QKind.Fp8E5M2, fh.QKind.Fp4, fh.QKind.Q2K):
+        for kind in ext_kinds(fh):
             shapes = [(8192, 8192), (1024 if kind == fh.QKind.Q2K else 896, 151936)]
             ext[kind.label()] = bench_single_calls(fh, g, ev, kind, shapes, reps=2, seed=5)
+        gemm = bench_ext_gemm(fh, g, ev, ext_kinds(fh), EXT_GEMM_CASES)
         print(json.dumps({"metric": "one-row GEMV GB/s on the other weight formats, 8192 x 8192",
                           "value": ext["MXFP4"]["8192x8192"]["gbs"], "unit": "GB/s", "n_gpus": 1,
-                          "higher_is_better": True, "detail": ext}))
+                          "higher_is_better": True, "detail": ext, "gemm": gemm}))
         g.close()
         return
     if a.gemm_only:
@@ -730,7 +766,7 @@ def main():
             log(f"{tag} single-call GEMV:", sc1)
             extra[f"{tag}_gemv_single_call_us"] = sc1
         ext = {}
-        for kind in (fh.QKind.F16, fh.QKind.Fp8E4M3, fh.QKind.Fp8E5M2, fh.QKind.Fp4, fh.QKind.Q2K):
+        for kind in ext_kinds(fh):
             shapes = [(8192, 8192), (1024 if kind == fh.QKind.Q2K else 896, 151936)]
             ext[kind.label()] = bench_single_calls(fh, g, ev, kind, shapes, reps=2, seed=5)
         log("other formats, single-call GEMV:", ext)
@@ -738,6 +774,12 @@ def main():
             "kernel": "ext_gemv_rows_kernel: GGUF rows decoded in registers, x shared by up to 8 rows per lane, "
                       "f32 accumulation; one launch per call, launch gaps included",
             "by_format": ext}
+        eg = bench_ext_gemm(fh, g, ev, ext_kinds(fh), EXT_GEMM_CASES)
+        log("other formats, MFMA GEMM:", eg)
+        extra["ext_formats_gemm"] = {
+            "kernel": "gemm_ext_kernel: x as two f16 parts, f16-exact decoded values times per-block f32 scales "
+                      "(Q2_K: per 16-element sub-block, minus dmin times the x sums) on f16 MFMA; x split included",
+            "by_format": eg}
         codec = bench_codec(fh, g, ev)
         log("codec:", codec)
         extra["codec_llama1b"] = codec
