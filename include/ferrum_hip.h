@@ -54,7 +54,9 @@ typedef enum fh_status {
 /* Block formats, by ggml tensor type id (ferrum_gguf/src/lib.rs:25-55). Replaces
  * ferrum_wgpu::ops_quant::QKind (ferrum_wgpu/src/ops/quant.rs:27-121): Q8_0, Q4_0 (the tiled
  * planes and the MFMA kernels), F16, MXFP4 (Fp4), FP8 E4M3 / E5M2 (no ggml type: the ids 1024 and
- * 1025 are this library's) and Q2_K (resident as GGUF rows, decoded on the fly, f32 products).
+ * 1025 are this library's) and Q2_K (resident as GGUF rows, decoded on the fly: an f32-accumulating
+ * GEMV for one row, an MFMA GEMM with x carried to about 22 bits for more; a block holding an
+ * infinity or NaN makes that GEMM's outputs NaN).
  * The read-only GGUF block types (ferrum_gguf/src/codec/blocks.rs:34-48) are accepted by
  * fh_nbytes and fh_decode only. */
 typedef enum fh_kind {
