@@ -345,50 +345,72 @@ __device__ void q2k_fit(const float *x, uint8_t *l, float *scale_out, float *min
     *min_out = -mn;
 }
 
-__global__ __launch_bounds__(64) void encode_q2k_kernel(const float *__restrict__ src, uint8_t *__restrict__ dst,
-                                                        size_t nblocks) {
-    for (size_t b = (size_t)blockIdx.x * 64 + threadIdx.x; b < nblocks; b += (size_t)gridDim.x * 64) {
-        const float *blk = src + b * 256;
-        uint8_t *o = dst + b * 84;
-        float scales[16], mins[16];
-        uint8_t levels[256];
-        for (int j = 0; j < 16; j++) q2k_fit(blk + 16 * j, levels + 16 * j, &scales[j], &mins[j]);
-        float max_scale = 0.0f, max_min = 0.0f;
-        for (int j = 0; j < 16; j++) {
-            max_scale = fmaxf(max_scale, scales[j]);
-            max_min = fmaxf(max_min, mins[j]);
+// Sixteen lanes per super-block, lane j fitting sub-block j (the same arithmetic as one thread
+// doing all sixteen in turn): the super-block's largest scale and min meet by shuffles within
+// the sixteen lanes, each lane requantises its own sub-block, and the 2-bit levels are packed
+// through LDS (byte 16 + 32 half + l holds the levels of elements 128 half + l + 32 s, s = 0..3).
+__global__ __launch_bounds__(256) void encode_q2k_kernel(const float *__restrict__ src, uint8_t *__restrict__ dst,
+                                                         size_t nblocks) {
+    __shared__ uint8_t lv[16][256];  // the levels of the workgroup's sixteen super-blocks
+    const uint32_t j = threadIdx.x % 16, slot = threadIdx.x / 16;
+    for (size_t base = (size_t)blockIdx.x * 16; base < nblocks; base += (size_t)gridDim.x * 16) {
+        const size_t b = base + slot;
+        const bool live = b < nblocks;
+        const float *blk = src + (live ? b : 0) * 256;
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const f32x4 v = *(const f32x4 *)(blk + 16 * j + i);
+            x[i] = v.x;
+            x[i + 1] = v.y;
+            x[i + 2] = v.z;
+            x[i + 3] = v.w;
         }
-        uint8_t packed[16];
-        for (int j = 0; j < 16; j++) packed[j] = 0;
-        uint32_t d = 0, dmin = 0;
+        uint8_t lev[16];
+        float scale, mn;
+        q2k_fit(x, lev, &scale, &mn);
+        float max_scale = scale, max_min = mn;
+#pragma unroll
+        for (int o = 8; o >= 1; o /= 2) {
+            max_scale = fmaxf(max_scale, __shfl_xor(max_scale, o, 16));
+            max_min = fmaxf(max_min, __shfl_xor(max_min, o, 16));
+        }
+        uint32_t packed = 0, d = 0, dmin = 0;
         if (max_scale > 0.0f) {
-            const float iscale = 15.0f / max_scale;
-            for (int j = 0; j < 16; j++) packed[j] = (uint8_t)nearest_int(iscale * scales[j]);
+            packed = (uint8_t)nearest_int((15.0f / max_scale) * scale);
             d = float_to_half_bits(max_scale / 15.0f);
         }
         if (max_min > 0.0f) {
-            const float iscale = 15.0f / max_min;
-            for (int j = 0; j < 16; j++) packed[j] |= (uint8_t)((uint8_t)nearest_int(iscale * mins[j]) << 4);
+            packed |= (uint32_t)(uint8_t)((uint8_t)nearest_int((15.0f / max_min) * mn) << 4);
             dmin = float_to_half_bits(max_min / 15.0f);
         }
-        const float d32 = half_bits_to_float(d), dmin32 = half_bits_to_float(dmin);
-        for (int j = 0; j < 16; j++) {
-            const float sc = d32 * (float)(packed[j] & 15);
-            if (sc == 0.0f) continue;
-            const float dm = dmin32 * (float)(packed[j] >> 4);
-            for (int ii = 0; ii < 16; ii++)
-                levels[16 * j + ii] = (uint8_t)clamp3(nearest_int((blk[16 * j + ii] + dm) / sc));
+        packed &= 0xffu;
+        const float sc = half_bits_to_float(d) * (float)(packed & 15u);
+        if (sc != 0.0f) {
+            const float dm = half_bits_to_float(dmin) * (float)(packed >> 4);
+#pragma unroll
+            for (int i = 0; i < 16; i++) lev[i] = (uint8_t)clamp3(nearest_int((x[i] + dm) / sc));
         }
-        for (int j = 0; j < 16; j++) o[j] = packed[j];
-        int at = 16;
-        for (int half = 0; half < 256; half += 128)
-            for (int l = 0; l < 32; l++)
-                o[at++] = (uint8_t)(levels[half + l] | (levels[half + l + 32] << 2) | (levels[half + l + 64] << 4) |
-                                    (levels[half + l + 96] << 6));
-        o[80] = (uint8_t)(d & 0xff);
-        o[81] = (uint8_t)(d >> 8);
-        o[82] = (uint8_t)(dmin & 0xff);
-        o[83] = (uint8_t)(dmin >> 8);
+#pragma unroll
+        for (int i = 0; i < 16; i++) lv[slot][16 * j + i] = lev[i];
+        __syncthreads();
+        if (live) {
+            uint8_t *o = dst + b * 84;
+            o[j] = (uint8_t)packed;
+            // lane j packs quant bytes 4 j .. 4 j + 3: half = j / 8, l = 4 (j % 8) .. + 3
+            const uint32_t half = j / 8;
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t l = 4 * (j % 8) + e, at = 128 * half + l;
+                const uint32_t byte = lv[slot][at] | (lv[slot][at + 32] << 2) | (lv[slot][at + 64] << 4) |
+                                      (lv[slot][at + 96] << 6);
+                word |= byte << (8 * e);
+            }
+            *(uint32_t *)(o + 16 + 4 * j) = word;
+            if (j == 0) *(uint32_t *)(o + 80) = d | (dmin << 16);
+        }
+        __syncthreads();
     }
 }
 
@@ -873,7 +895,7 @@ hipError_t launch_encode_ext(hipStream_t s, int kind, const float *src, uint8_t 
     case FH_FP8_E4M3: encode_fp8_kernel<false><<<grid_of(n / 32, 256), 256, 0, s>>>(src, dst, n / 32); break;
     case FH_FP8_E5M2: encode_fp8_kernel<true><<<grid_of(n / 32, 256), 256, 0, s>>>(src, dst, n / 32); break;
     case FH_MXFP4: encode_mxfp4_kernel<<<grid_of(n / 32, 256), 256, 0, s>>>(src, dst, n / 32); break;
-    case FH_Q2_K: encode_q2k_kernel<<<grid_of(n / 256, 64), 64, 0, s>>>(src, dst, n / 256); break;
+    case FH_Q2_K: encode_q2k_kernel<<<grid_of(n / 256, 16), 256, 0, s>>>(src, dst, n / 256); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -101,11 +101,12 @@ def test_pack_and_quantise_refuse_bad_shapes(fh, g, orc):
 
 def test_device_encode_is_bit_exact(fh, g, orc):
     """The device encoders against the oracle's restatement of the reference's, on the reference's
-    awkward weights (blocks scaled by 1e-5, zero and 300) and wide random data."""
+    awkward weights (blocks scaled by 1e-5, zero and 300) and wide random data (1287 Q2_K
+    super-blocks: a partly filled last workgroup of sixteen)."""
     rng = np.random.default_rng(5)
     for kind in ext(fh):
         for data in (weights(orc, 4096), rng.standard_normal(8192).astype(np.float32) * np.float32(3.0),
-                     orc.rand_vec(2048, 9)):
+                     orc.rand_vec(2048, 9), (rng.standard_normal(256 * 1287) * 0.02).astype(np.float32)):
             n = data.size
             want = orc.encode(oid(orc, kind), data)
             got = g.read_bytes(fh.encode(g, kind, g.upload(data), n))[: want.size]
