@@ -584,10 +584,18 @@ hipError_t run_gemm(hipStream_t s, const GemmArgs &g) {
     return hipGetLastError();
 }
 
+// The fast GEMM's CTA tile by rows: 64-row tiles up to 1024 rows (more row tiles, fewer K splits
+// on the scoring shapes), 128 beyond.
+constexpr uint32_t kFastMidRows = 1024;
+void fast_tile(size_t rows, size_t *bm, size_t *bn) {
+    *bm = rows <= 32 ? 32 : rows <= kFastMidRows ? 64 : 128;
+    *bn = rows <= 32 ? 256 : 128;
+}
+
 template <int KIND>
 hipError_t gemm_dispatch(hipStream_t s, const GemmArgs &g) {
     if (g.M <= 32) return run_gemm<KIND, 32, 256, 1>(s, g);
-    if (g.M <= 64) return run_gemm<KIND, 64, 128, 2>(s, g);
+    if (g.M <= kFastMidRows) return run_gemm<KIND, 64, 128, 2>(s, g);
     return run_gemm<KIND, 128, 128, 2>(s, g);
 }
 
@@ -1747,9 +1755,10 @@ size_t gemm_workspace_bytes(size_t rows, size_t k, size_t n) {
 }
 
 // Room for the K-split partial products when the product's tile grid is too small to fill the
-// chip (the tile shapes and split rule of gemm_dispatch / run_gemm); none otherwise.
+// chip (the tile shapes of fast_tile and the split rule of run_gemm); none otherwise.
 size_t gemm_partial_bytes(size_t rows, size_t k, size_t n) {
-    const size_t bm = rows <= 32 ? 32 : rows <= 64 ? 64 : 128, bn = rows <= 32 ? 256 : 128;
+    size_t bm, bn;
+    fast_tile(rows, &bm, &bn);
     const uint64_t tiles = (uint64_t)((rows + bm - 1) / bm) * ((n + bn - 1) / bn);
     const uint32_t sp = gemm_splits(tiles, (uint32_t)((k / 32 + 1) / 2));
     return sp > 1 ? (size_t)sp * rows * n * 4 : 0;
