@@ -584,18 +584,18 @@ hipError_t run_gemm(hipStream_t s, const GemmArgs &g) {
     return hipGetLastError();
 }
 
-// The fast GEMM's CTA tile by rows: 64-row tiles up to 1024 rows (more row tiles, fewer K splits
-// on the scoring shapes), 128 beyond.
-constexpr uint32_t kFastMidRows = 1024;
+// The fast and the other formats' MFMA GEMMs take 64-row tiles up to 1024 rows (more row tiles,
+// fewer K splits on the scoring shapes), 128 beyond (measured: the precise GEMM gains nothing).
+constexpr uint32_t kMidRows = 1024;
 void fast_tile(size_t rows, size_t *bm, size_t *bn) {
-    *bm = rows <= 32 ? 32 : rows <= kFastMidRows ? 64 : 128;
+    *bm = rows <= 32 ? 32 : rows <= kMidRows ? 64 : 128;
     *bn = rows <= 32 ? 256 : 128;
 }
 
 template <int KIND>
 hipError_t gemm_dispatch(hipStream_t s, const GemmArgs &g) {
     if (g.M <= 32) return run_gemm<KIND, 32, 256, 1>(s, g);
-    if (g.M <= kFastMidRows) return run_gemm<KIND, 64, 128, 2>(s, g);
+    if (g.M <= kMidRows) return run_gemm<KIND, 64, 128, 2>(s, g);
     return run_gemm<KIND, 128, 128, 2>(s, g);
 }
 
@@ -1160,6 +1160,19 @@ __global__ __launch_bounds__(256, 2) void gemm_ext_kernel(const _Float16 *__rest
         }
 }
 
+// The other formats' GEMM tile (64-row tiles up to kMidRows rows, and always for Q2_K) and its K
+// split (the rule of gemm_splits over those tiles).
+void ext_tile(int kind, size_t rows, size_t *bm, size_t *bn) {
+    *bm = rows <= 32 ? 32 : (rows <= kMidRows || kind == FH_Q2_K) ? 64 : 128;
+    *bn = rows <= 32 ? 256 : 128;
+}
+uint32_t ext_splits(int kind, size_t rows, size_t k, size_t n) {
+    size_t bm, bn;
+    ext_tile(kind, rows, &bm, &bn);
+    const uint64_t tiles = (uint64_t)((rows + bm - 1) / bm) * ((n + bn - 1) / bn);
+    return gemm_splits(tiles, (uint32_t)(k / 32));
+}
+
 template <uint32_t T, int BM, int BN, int WAVES_M>
 hipError_t run_gemm_ext(hipStream_t s, const _Float16 *xs, const uint8_t *w, float *y, float *partial, uint32_t M,
                         uint32_t K, uint32_t N) {
@@ -1168,7 +1181,7 @@ hipError_t run_gemm_ext(hipStream_t s, const _Float16 *xs, const uint8_t *w, flo
     if (tiles > 0x7fffffffull) return hipErrorInvalidValue;
     const uint32_t grid = (uint32_t)((tiles + 7) / 8 * 8);
     const uint32_t stages = K / 32;
-    const uint32_t sp = partial ? precise_splits(M, K, N) : 1;
+    const uint32_t sp = partial ? ext_splits((int)T, M, K, N) : 1;
     const uint32_t per = (stages + sp - 1) / sp;
     float *out = sp > 1 ? partial : y;
     gemm_ext_kernel<T, BM, BN, WAVES_M><<<dim3(grid, sp), 256, 0, s>>>(xs, w, out, M, K, N, mt, nt, per);
@@ -1183,9 +1196,10 @@ hipError_t run_gemm_ext(hipStream_t s, const _Float16 *xs, const uint8_t *w, flo
 template <uint32_t T>
 hipError_t gemm_ext_dispatch(hipStream_t s, const _Float16 *xs, const uint8_t *w, float *y, float *partial,
                              uint32_t M, uint32_t K, uint32_t N) {
-    if (M <= 32) return run_gemm_ext<T, 32, 256, 1>(s, xs, w, y, partial, M, K, N);
-    // Q2_K's per-sub-block terms need more registers: its 128-row tile would spill
-    if (M <= 64 || T == FH_Q2_K) return run_gemm_ext<T, 64, 128, 2>(s, xs, w, y, partial, M, K, N);
+    size_t bm, bn;
+    ext_tile((int)T, M, &bm, &bn);  // (Q2_K's per-sub-block terms would spill in a 128-row tile)
+    if (bm == 32) return run_gemm_ext<T, 32, 256, 1>(s, xs, w, y, partial, M, K, N);
+    if (bm == 64) return run_gemm_ext<T, 64, 128, 2>(s, xs, w, y, partial, M, K, N);
     return run_gemm_ext<T, 128, 128, 2>(s, xs, w, y, partial, M, K, N);
 }
 
@@ -1811,10 +1825,15 @@ bool gemm_ext_kind(int kind) {
     return kind == FH_F16 || kind == FH_FP8_E4M3 || kind == FH_FP8_E5M2 || kind == FH_MXFP4 || kind == FH_Q2_K;
 }
 
+size_t gemm_ext_workspace_bytes(int kind, size_t rows, size_t k, size_t n) {
+    const uint32_t sp = ext_splits(kind, rows, k, n);
+    return (rows * k * 4 + 255) / 256 * 256 + (sp > 1 ? (size_t)sp * rows * n * 4 : 0);
+}
+
 hipError_t launch_gemm_ext(hipStream_t s, int kind, const uint8_t *w, const float *x, float *y, size_t rows, size_t k,
                            size_t n, void *workspace) {
     _Float16 *xs = (_Float16 *)workspace;
-    float *partial = precise_splits(rows, k, n) > 1
+    float *partial = ext_splits(kind, rows, k, n) > 1
                          ? (float *)((uint8_t *)workspace + (rows * k * 4 + 255) / 256 * 256)
                          : nullptr;
     const size_t items = rows * (k / 32);

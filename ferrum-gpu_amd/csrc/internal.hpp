@@ -278,9 +278,10 @@ hipError_t launch_gemm_f16(hipStream_t s, fh_kind kind, const uint8_t *qs, const
                            size_t rows, size_t k, size_t n, void *workspace, SplitOut *defer = nullptr);
 // The precise MFMA GEMM (x as two f16 parts; split into workspace, then the product).
 size_t gemm_precise_workspace_bytes(size_t rows, size_t k, size_t n);
-// The MFMA GEMM on the GGUF rows of F16, FP8 E4M3 / E5M2, MXFP4 and Q2_K weights (rows >= 2); its
-// workspace is gemm_precise_workspace_bytes(rows, k, n).
+// The MFMA GEMM on the GGUF rows of F16, FP8 E4M3 / E5M2, MXFP4 and Q2_K weights (rows >= 2) and
+// its workspace (x split, then the K-split partial products).
 bool gemm_ext_kind(int kind);
+size_t gemm_ext_workspace_bytes(int kind, size_t rows, size_t k, size_t n);
 hipError_t launch_gemm_ext(hipStream_t s, int kind, const uint8_t *w, const float *x, float *y, size_t rows, size_t k,
                            size_t n, void *workspace);
 hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,

@@ -690,7 +690,8 @@ static fh_status linear(fh_device *dev, const float *x, const fh_qweight *w, flo
             return fail(FH_ERR_INVALID, "the GEMV kernel takes one row, not %zu", rows);
         if (path == FH_PATH_TILED && rows >= 2 && gemm_ext_kind(w->kind)) {  // the MFMA GEMM (gemm.hip)
             void *ws = nullptr;
-            if ((st = command_scratch(dev, fixed, gemm_precise_workspace_bytes(rows, w->k, w->n), &ws))) return st;
+            const size_t wsb = gemm_ext_workspace_bytes(w->kind, rows, w->k, w->n);
+            if ((st = command_scratch(dev, fixed, wsb, &ws))) return st;
             if ((st = begin_command(dev, "linear_q"))) return st;
             (void)launch_gemm_ext(dev->stream, w->kind, w->qs, x, y, rows, w->k, w->n, ws);
             return end_command(dev, "linear_q");
