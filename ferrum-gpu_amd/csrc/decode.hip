@@ -91,9 +91,6 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 __device__ __forceinline__ float coherent_load(const float *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint32_t coherent_load(const uint32_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // The first maximum wins; NaN never does (ferrum_model/src/sampling.rs:32-40). kNone: no candidate.
 __device__ __forceinline__ bool better(float v2, uint32_t i2, float v1, uint32_t i1) {
