@@ -510,9 +510,8 @@ struct ExtSeg<FH_F16> {  // segment s: halves 8 s .. 8 s + 7 of the row (16-byte
 };
 
 // FP8 (fp8.rs:34-63): segment s = codes 16 p .. 16 p + 15 of block s / 2, p = s % 2, times the
-// block's f16 scale. E5M2 codes are the high byte of an f16; E4M3 code c is the f16 with bits
-// (c & 0x7f) << 7 | (c & 0x80) << 8 times 2^8 (normal and subnormal alike), its NaN codes
-// (0x7f, 0xff) flagged separately.
+// block's f16 scale. gfx950's conversions read OCP E4M3 / E5M2 (the reference's formats: E4M3
+// NaN at 0x7f and 0xff only, E5M2 with infinities), two codes per instruction.
 template <bool E5M2>
 struct Fp8Seg {
     static constexpr uint32_t SPB = 2, XN = 16;
@@ -528,27 +527,17 @@ struct Fp8Seg {
     __device__ static uint32_t xat(uint32_t s) { return 16 * s; }
     __device__ static float dot(const W &w, const float (&x)[XN]) {
         float a = 0.0f;
-        uint32_t nan = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t v = w.c[i];
-            uint32_t p0, p1;  // f16 pairs of codes (0, 1) and (2, 3)
-            if constexpr (E5M2) {
-                p0 = __builtin_amdgcn_perm(v, 0u, 0x050c040cu);
-                p1 = __builtin_amdgcn_perm(v, 0u, 0x070c060cu);
-            } else {
-                const uint32_t t0 = __builtin_amdgcn_perm(v, 0u, 0x0c050c04u), t1 = __builtin_amdgcn_perm(v, 0u, 0x0c070c06u);
-                p0 = ((t0 & 0x007f007fu) << 7) | ((t0 & 0x00800080u) << 8);
-                p1 = ((t1 & 0x007f007fu) << 7) | ((t1 & 0x00800080u) << 8);
-                nan |= ((v & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
-            }
-            a = fmaf(x[4 * i], lo_half(p0), a);
-            a = fmaf(x[4 * i + 1], hi_half(p0), a);
-            a = fmaf(x[4 * i + 2], lo_half(p1), a);
-            a = fmaf(x[4 * i + 3], hi_half(p1), a);
+            const int v = (int)w.c[i];
+            const auto p0 = E5M2 ? __builtin_amdgcn_cvt_pk_f32_bf8(v, false) : __builtin_amdgcn_cvt_pk_f32_fp8(v, false);
+            const auto p1 = E5M2 ? __builtin_amdgcn_cvt_pk_f32_bf8(v, true) : __builtin_amdgcn_cvt_pk_f32_fp8(v, true);
+            a = fmaf(x[4 * i], p0[0], a);
+            a = fmaf(x[4 * i + 1], p0[1], a);
+            a = fmaf(x[4 * i + 2], p1[0], a);
+            a = fmaf(x[4 * i + 3], p1[1], a);
         }
-        const float d = lo_half(w.d) * (E5M2 ? 1.0f : 256.0f);
-        return nan ? __uint_as_float(0x7fc00000u) : d * a;
+        return lo_half(w.d) * a;
     }
 };
 template <>
