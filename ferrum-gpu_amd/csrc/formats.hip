@@ -546,8 +546,9 @@ template <>
 struct ExtSeg<FH_FP8_E5M2> : Fp8Seg<true> {};
 
 // MXFP4 (mxfp4.rs:13-33): segment = block s (E8M0 byte, then element i < 16 in the low nibble of
-// byte 1 + i, element 16 + i in its high nibble). Four nibbles at a time become signed bytes
-// through two byte-permute tables (values 0, 1, 2, 3, 4, 6, 8, 12 and their negatives).
+// byte 1 + i, element 16 + i in its high nibble). gfx950's scaled FP4 conversion turns one byte
+// into its two E2M1 values (0, 0.5, 1, 1.5, 2, 3, 4, 6 and negatives: the reference's table halved),
+// so sum(x v) = 2 sum(x e2m1) exactly, then times the half scale.
 template <>
 struct ExtSeg<FH_MXFP4> {
     static constexpr uint32_t SPB = 1, XN = 32;
@@ -561,24 +562,25 @@ struct ExtSeg<FH_MXFP4> {
         w.q = ld16_any(blk + 1);
     }
     __device__ static uint32_t xat(uint32_t s) { return 32 * s; }
-    __device__ static uint32_t vals(uint32_t n) {  // four nibbles (one per byte) -> four signed bytes
-        const uint32_t m = n & 0x07070707u;
-        const uint32_t pos = __builtin_amdgcn_perm(0x0c080604u, 0x03020100u, m);
-        const uint32_t neg = __builtin_amdgcn_perm(0xf4f8fafcu, 0xfdfeff00u, m);
-        const uint32_t sgn = ((n >> 3) & 0x01010101u) * 0xffu;
-        return (neg & sgn) | (pos & ~sgn);
-    }
     __device__ static float dot(const W &w, const float (&x)[XN]) {
         float a = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t lo = vals(w.q[i] & 0x0f0f0f0fu), hi = vals((w.q[i] >> 4) & 0x0f0f0f0fu);
-#pragma unroll
-            for (int j = 0; j < 4; j++) a = fmaf(x[4 * i + j], sbyte(lo, j), a);
-#pragma unroll
-            for (int j = 0; j < 4; j++) a = fmaf(x[16 + 4 * i + j], sbyte(hi, j), a);
+            // byte 4 i + b: elements 4 i + b (low nibble) and 16 + 4 i + b (high nibble)
+            const auto v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.q[i], 1.0f, 0);
+            const auto v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.q[i], 1.0f, 1);
+            const auto v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.q[i], 1.0f, 2);
+            const auto v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w.q[i], 1.0f, 3);
+            a = fmaf(x[4 * i], v0[0], a);
+            a = fmaf(x[16 + 4 * i], v0[1], a);
+            a = fmaf(x[4 * i + 1], v1[0], a);
+            a = fmaf(x[16 + 4 * i + 1], v1[1], a);
+            a = fmaf(x[4 * i + 2], v2[0], a);
+            a = fmaf(x[16 + 4 * i + 2], v2[1], a);
+            a = fmaf(x[4 * i + 3], v3[0], a);
+            a = fmaf(x[16 + 4 * i + 3], v3[1], a);
         }
-        return a * mx_half_scale(w.e);
+        return (a * 2.0f) * mx_half_scale(w.e);
     }
 };
 
