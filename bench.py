@@ -385,7 +385,7 @@ def bench_decode(fh, g, n_prompt=32, n_new=256, reps=3, cpu=True):
     steps = n_prompt + n_new - 1
     out = {"tok_s": n_new / t, "steps_per_s": steps / t, "ms_per_step": t / steps * 1e3,
            "weight_gbs": model.step_bytes() * steps / t / 1e9, "step_bytes": model.step_bytes(),
-           "first_tokens": toks[:8], "reps": reps}
+           "first_tokens": toks[:8], "reps": reps, "launches_per_step": model.step_launches()}
     if cpu:  # ferrum_ref's Gpt2::feed (restated in C) on the fake-quantised f32 weights, one thread
         import oracle as orc
         from oracle import gpt2_model as gm

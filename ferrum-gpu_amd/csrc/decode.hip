@@ -3,17 +3,20 @@
 // Gpt2::feed, ferrum_ref/src/models/gpt2/decode.rs:57-117, on the fake-quantised model).
 //
 // A decode step is latency-bound (GPT-2-small reads 131 MB of packed weights per token, 26 us
-// at HBM speed), so it is built from few, fused launches and replayed as one HIP graph:
-//   embed                 x = tok[token] + pos[p]                     (token and p from device state)
-//   per layer:
-//     gemv LN|QKV         q | kcache[p] | vcache[p] = LN1(x) W_qkv + b  (one product, n = 3d)
-//     attention           a = softmax(q k^T / sqrt(hd)) v, a workgroup per head
-//     gemv RESIDUAL       x += a W_o + b_o
-//     gemv LN|GELU        f = gelu(LN2(x) W_1 + b_1)
-//     gemv RESIDUAL       x += f W_2 + b_2
-//   gemv LN|STORE         logits = LNf(x) W_head
-//   argmax                next token (sampling.rs:32-40), written to the device's input array;
-//                         the position advances
+// at HBM speed), so it is built from few, fused launches and replayed as one HIP graph. Where
+// the head width is 64, 128 or 256 (GPT-2-small's 64) a layer is four launches:
+//   gemv LN|QKV         x = x_m + (sum_s down[s] + b_2) (layer 0: tok[token] + pos[p]);
+//                       q | kcache[p] | vcache[p] = LN1(x) W_qkv + b   (one product, n = 3d)
+//   attention + W_o     per head h: a_h = softmax(q k^T / sqrt(hd)) v, out[h] = a_h W_o[:, h]
+//   gemv LN|GELU        x_m = x + (sum_h out[h] + b_o); f = gelu(LN2(x_m) W_1 + b_1)
+//   gemv (K split)      down[s] = the split s share of f W_2
+// (the partial rows are added by their consumer in a fixed order), then
+//   final LN            LNf(x_m + (sum_s down[s] + b_2)) into prepared records
+//   gemv STORE          logits = LNf(x) W_head
+//   argmax              next token (sampling.rs:32-40), written to the device's input array;
+//                       the position advances.
+// Other head widths run five launches per layer (embed first; LN1|QKV, attention, W_o +
+// residual, LN2|GELU, W_2 + residual; the final LN from x).
 // The position lives in device memory, so the same graph serves every step, and greedy
 // generation runs without a host round trip per token.
 //
@@ -37,14 +40,21 @@
 namespace fh {
 namespace {
 
-enum { PRO_NONE = 0, PRO_LN = 1, PRO_GLOBAL = 2 };
-enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_GELU = 2, EPI_QKV = 3, EPI_ARGMAX = 4 };
+enum { PRO_NONE = 0, PRO_LN = 1, PRO_GLOBAL = 2, PRO_LNR = 3 };  // PRO_LNR: LayerNorm of the residual row (fused_residual)
+enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_GELU = 2, EPI_QKV = 3, EPI_ARGMAX = 4, EPI_PARTIAL = 5 };
 
 constexpr int kMaxWaves = 8;           // wavefronts per decode-GEMV workgroup (two per SIMD)
 constexpr uint32_t kMaxBlocks = 512;   // blocks per row (k <= 16384): 80 KiB of prepared x in LDS
 constexpr uint32_t kLnSlots = 2;       // LayerNorm prologue: (block, lane) slots a thread keeps in registers
 constexpr uint32_t kNone = 0xffffffffu;
 constexpr int kAttnThreads = 512;
+// Cache policy of the decode's weight loads: ordinary (cached) loads, so that a model whose
+// weights fit in the last-level cache (GPT-2-small's 131 MB in 256 MB) finds them there on the
+// next token (measured 3-11% faster per step than streaming loads).
+#ifndef FH_DECODE_LOAD_POLICY
+#define FH_DECODE_LOAD_POLICY 0
+#endif
+constexpr int kWeightPolicy = FH_DECODE_LOAD_POLICY;
 
 struct DecodeGemv {
     const uint8_t *qs;
@@ -63,6 +73,14 @@ struct DecodeGemv {
     uint32_t nb, n, split;     // split: EPI_QKV width of each of q, k, v
     uint32_t chunk;            // blocks per K split (a multiple of 8)
     float eps;
+    // PRO_LNR: the residual row x_in + (sum of nparts rows of rpart + rbias), or the embedding
+    // of inputs[state[0]] (x_in == null; emb_*, pos_tab); workgroup (0, 0) stores it at x_out
+    const float *x_in, *rpart, *rbias;
+    uint32_t nparts;
+    const uint8_t *emb_qs;
+    const uint16_t *emb_ds;
+    const float *pos_tab;
+    float *x_out;
 };
 
 // ferrum_ref/src/kernels/nn.rs:12-15
@@ -97,21 +115,21 @@ __device__ __forceinline__ bool better(float v2, uint32_t i2, float v1, uint32_t
     return i2 != kNone && (i1 == kNone || v2 > v1 || (v2 == v1 && i2 < i1));
 }
 
-// LayerNorm (ferrum_ref/src/kernels/nn.rs:31-44) of the k = 32 nb values of x, written as the
-// prepared records of `span` blocks (zero records past nb) at out (LDS, or global when GLOBAL).
-// x is read once: each thread keeps its kLnSlots (block, lane) slots in registers, so
-// span * 8 <= kLnSlots * blockDim.x.
+// LayerNorm (ferrum_ref/src/kernels/nn.rs:31-44) of the k = 32 nb values that the workgroup
+// holds in registers (thread slot u: block sl / 8, elements 4 sl .. 4 sl + 3 with
+// sl = threadIdx.x + u blockDim.x; slots past nb hold nothing), written as the prepared records
+// of `span` blocks (zero records past nb) at out (LDS, or global when GLOBAL). span * 8 <=
+// kLnSlots * blockDim.x.
 template <int KIND, bool GLOBAL>
-__device__ __forceinline__ void ln_prep(const float *x, const float *lg, const float *lb, float eps, uint32_t nb,
-                                        uint32_t span, uint8_t *out, float *red) {
+__device__ __forceinline__ void ln_records(const f32x4 (&v)[kLnSlots], const float *lg, const float *lb, float eps,
+                                           uint32_t nb, uint32_t span, uint8_t *out, float *red) {
     const uint32_t k = nb * 32;
-    f32x4 v[kLnSlots], gg[kLnSlots], bb[kLnSlots];
+    f32x4 gg[kLnSlots], bb[kLnSlots];
     float s = 0.0f;
 #pragma unroll
     for (uint32_t u = 0; u < kLnSlots; u++) {
-        const uint32_t sl = threadIdx.x + u * blockDim.x;  // slot: block sl / 8, elements 4 sl .. 4 sl + 3
+        const uint32_t sl = threadIdx.x + u * blockDim.x;
         if (sl / 8 < nb) {
-            v[u] = gload4(x + sl * 4);
             gg[u] = gload4(lg + sl * 4);
             bb[u] = gload4(lb + sl * 4);
             s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
@@ -153,6 +171,20 @@ __device__ __forceinline__ void ln_prep(const float *x, const float *lg, const f
     }
 }
 
+// The LayerNorm of x (k = 32 nb values in global memory) into prepared records (ln_records); x is
+// read once.
+template <int KIND, bool GLOBAL>
+__device__ __forceinline__ void ln_prep(const float *x, const float *lg, const float *lb, float eps, uint32_t nb,
+                                        uint32_t span, uint8_t *out, float *red) {
+    f32x4 v[kLnSlots];
+#pragma unroll
+    for (uint32_t u = 0; u < kLnSlots; u++) {
+        const uint32_t sl = threadIdx.x + u * blockDim.x;
+        if (sl / 8 < nb) v[u] = gload4(x + sl * 4);
+    }
+    ln_records<KIND, GLOBAL>(v, lg, lb, eps, nb, span, out, red);
+}
+
 // One workgroup: LayerNorm of x into global prepared records (for a product whose many row groups
 // would each repeat it).
 template <int KIND>
@@ -163,6 +195,79 @@ __global__ __launch_bounds__(64 * kMaxWaves) void ln_prep_kernel(const float *__
     ln_prep<KIND, true>(x, lg, lb, eps, nb, (nb + 7) / 8 * 8, out, red);
 }
 
+struct FusedArgs {
+    // the residual row: x_in + (sum over nparts rows of part + pbias), or (x_in == null) the
+    // embedding tok[inputs[p]] + pos_tab[p]
+    const float *x_in, *part, *pbias;
+    uint32_t nparts;
+    const uint8_t *emb_qs;
+    const uint16_t *emb_ds;
+    const float *pos_tab;
+    const int32_t *inputs;
+    const int32_t *state;
+    float *x_out;  // workgroup (0, 0) stores the residual row here
+    const float *ln_g, *ln_b;
+    float eps;
+    // attn_out_kernel: the query row, the caches [ctx][d], and the output projection (d rows of
+    // nb2 blocks; the workgroup takes blocks blockIdx.x * hd / 32 .. of each row)
+    const float *q;
+    float *kc, *vc;
+    const uint8_t *qs2;
+    const uint16_t *ds2;
+    uint32_t nb2;
+    float *out_part;  // [gridDim.x][d]
+    uint32_t d, nb;
+    float scale;
+};
+
+// The residual row into the thread's slots (see ln_records); workgroup (0, 0) stores it.
+template <int KIND>
+__device__ __forceinline__ void fused_residual(const FusedArgs &a, f32x4 (&v)[kLnSlots]) {
+    const uint32_t nb = a.nb, d = a.d;
+#pragma unroll
+    for (uint32_t u = 0; u < kLnSlots; u++) {
+        const uint32_t sl = threadIdx.x + u * blockDim.x;
+        if (sl / 8 >= nb) continue;
+        if (a.x_in == nullptr) {
+            // x = tok[t] + pos[p] (decode.rs:72-74), as embed_kernel
+            const uint32_t p = (uint32_t)a.state[0];
+            const uint32_t t = (uint32_t)a.inputs[p];
+            const f32x4 pv = gload4(a.pos_tab + (size_t)p * d + sl * 4);
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const uint32_t i = sl * 4 + c, b = i / 32, j = i % 32;
+                const size_t slot = tile_slot(t, b, nb);
+                float q;
+                if constexpr (KIND == FH_Q8_0) {
+                    q = (float)(int8_t)a.emb_qs[slot * 32 + j];
+                } else {
+                    const uint32_t byte = a.emb_qs[slot * 16 + (j % 16)];
+                    q = (float)((int32_t)(j < 16 ? byte & 15u : byte >> 4) - 8);
+                }
+                v[u][c] = half_bits_to_float(a.emb_ds[scale_slot(t, b, nb)]) * q + pv[c];
+            }
+        } else {
+            // nn::add(x, gemv(..) + b) (decode.rs:100,111): the partial sums in order, then the
+            // bias; sixteen rows' loads are issued before any of them is added (rows past
+            // nparts read as zero and add nothing)
+            const f32x4 x = gload4(a.x_in + sl * 4);
+            f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+            const float *pp = a.part + sl * 4;
+            for (uint32_t j = 0; j < a.nparts; j += 16) {
+                f32x4 r[16];
+#pragma unroll
+                for (int k = 0; k < 16; k++)
+                    r[k] = j + k < a.nparts ? gload4(pp + (size_t)(j + k) * d) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int k = 0; k < 16; k++) t += r[k];
+            }
+            t += gload4(a.pbias + sl * 4);
+            v[u] = x + t;
+        }
+        if (blockIdx.x == 0 && blockIdx.y == 0 && a.x_out) *(f32x4 *)(a.x_out + sl * 4) = v[u];
+    }
+}
+
 template <int KIND>
 __device__ __forceinline__ void load_weights(Batch<KIND> &bt, __amdgpu_buffer_rsrc_t rq, __amdgpu_buffer_rsrc_t rd,
                                              uint32_t oq, uint32_t os, uint32_t b) {
@@ -170,12 +275,12 @@ __device__ __forceinline__ void load_weights(Batch<KIND> &bt, __amdgpu_buffer_rs
 #pragma unroll
         for (int i = 0; i < kBatch; i++)
             bt.q[i] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(oq + (b + i) * 1024), 0, kNonTemporal));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(oq + (b + i) * 1024), 0, kWeightPolicy));
     } else {
 #pragma unroll
         for (int i = 0; i < kBatch / 2; i++)
             bt.q[i] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(oq + (b + 2 * i) * 512), 0, kNonTemporal));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(oq + (b + 2 * i) * 512), 0, kWeightPolicy));
     }
     bt.s = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rd, (int)(os + b * 64), 0, 0));
 }
@@ -204,7 +309,8 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
     const auto g16 = [&](uint32_t off) { return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (int)off, 0, 0)); };
     const auto g4 = [&](uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(ra, (int)off, 0, 0); };
     uint8_t *prep = dlds;  // records of blocks b0 .. b1 (PRO_LN: of every block)
-    float *part = (float *)(dlds + (PRO == PRO_GLOBAL ? 0 : (PRO == PRO_LN ? span : a.chunk) * kPrepBytes));
+    constexpr bool kLn = PRO == PRO_LN || PRO == PRO_LNR;  // every block's records in LDS
+    float *part = (float *)(dlds + (PRO == PRO_GLOBAL ? 0 : (kLn ? span : a.chunk) * kPrepBytes));
     float *red = part + W * 32;
 
     // the epilogue's bias and residual inputs are requested first (the epilogue runs in lanes 0..31
@@ -227,6 +333,24 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
     if constexpr (PRO == PRO_LN) {
         ln_prep<KIND, false>(a.x, a.ln_g, a.ln_b, a.eps, nb, span, prep, red);
         __syncthreads();
+    } else if constexpr (PRO == PRO_LNR) {
+        FusedArgs f{};
+        f.x_in = a.x_in;
+        f.part = a.rpart;
+        f.pbias = a.rbias;
+        f.nparts = a.nparts;
+        f.emb_qs = a.emb_qs;
+        f.emb_ds = a.emb_ds;
+        f.pos_tab = a.pos_tab;
+        f.inputs = a.inputs;
+        f.state = a.state;
+        f.x_out = a.x_out;
+        f.d = nb * 32;
+        f.nb = nb;
+        f32x4 v[kLnSlots];
+        fused_residual<KIND>(f, v);
+        ln_records<KIND, false>(v, a.ln_g, a.ln_b, a.eps, nb, span, prep, red);
+        __syncthreads();
     } else if constexpr (PRO == PRO_NONE) {
         // the split's blocks of x, eight lanes per block (the eight lanes share the loop bound)
         for (uint32_t blk = b0 + threadIdx.x / 8; blk < b1; blk += blockDim.x / 8) {
@@ -240,7 +364,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
         }
         __syncthreads();
     }
-    const uint32_t pbase = PRO == PRO_LN ? 0 : b0;
+    const uint32_t pbase = kLn ? 0 : b0;
     float acc = 0.0f;
     while (bb < b1) {
         const uint32_t nxt = bb + W * kBatch;
@@ -273,6 +397,11 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
     float t = 0.0f;
     for (uint32_t w = 0; w < W; w++) t += part[w * 32 + r];
     const uint32_t row = g * 32 + r;
+    if constexpr (EPI == EPI_PARTIAL) {
+        // the split's row sums, added in split order by their consumer (fused_residual)
+        if (row < a.n) a.y[(size_t)sp * a.n + row] = t;
+        return;
+    }
     if (S > 1) {
         a.partial[(size_t)sp * gridDim.x * 32 + row] = t;
         __threadfence();
@@ -467,6 +596,217 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float *__
     }
 }
 
+// ---- the four-launch step's own kernels ----
+// attn_out_kernel (one workgroup per head h): a_h = softmax(q k^T / sqrt(hd)) v over the cached
+// positions, then out_part[h] = a_h W_o[:, h] (the head's columns of the output projection). Its
+// partial rows, and those of the FFN-down product split along K, are added in a fixed order by
+// the next launch's prologue (fused_residual), so a step's results do not depend on timing; no
+// workgroup waits for another inside a launch.
+constexpr int kFuseThreads = 512;
+constexpr int kFuseWaves = kFuseThreads / 64;
+constexpr uint32_t kAttnSlots = 2 * kFuseThreads / 16;  // fused_attend: two floats per lane group (L >= 16)
+
+// The second product's task for row group rg: blocks b0 = blockIdx.x * G .. b0 + 2 PAIRS - 1 of
+// its rows (b0 even, all in one run of eight scales).
+template <int KIND, int PAIRS>
+__device__ __forceinline__ void load_task2(Batch<KIND> &bt, const FusedArgs &a, uint32_t rg, uint32_t oq,
+                                           uint32_t os) {
+    constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
+    const uint32_t nb2 = a.nb2, nb28 = (nb2 + 7) / 8, b0 = blockIdx.x * (2 * PAIRS);
+    const auto rq = make_rsrc(a.qs2 + (size_t)rg * nb2 * 32 * QB, nb2 * 32 * QB);
+    const auto rd = make_rsrc(a.ds2 + (size_t)rg * nb28 * 256, nb28 * 512);
+    if constexpr (KIND == FH_Q8_0) {
+#pragma unroll
+        for (int i = 0; i < 2 * PAIRS; i++)
+            bt.q[i] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(oq + (b0 + i) * 1024), 0, kWeightPolicy));
+    } else {
+#pragma unroll
+        for (int i = 0; i < PAIRS; i++)
+            bt.q[i] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(oq + (b0 + 2 * i) * 512), 0, kWeightPolicy));
+    }
+#pragma unroll
+    for (int p = 0; p < PAIRS; p++)
+        bt.s[p] = __builtin_amdgcn_raw_buffer_load_b32(rd, (int)(os + (b0 / 8) * 512 + ((b0 % 8) / 2 + p) * 4), 0, 0);
+}
+
+typedef __attribute__((address_space(3))) const uint8_t lds_byte;
+
+// x operand and record tails of a batch whose records start at rec (LDS).
+template <int KIND>
+__device__ __forceinline__ void lds_operands(Batch<KIND> &bt, const uint8_t *rec, uint32_t oa, uint32_t ot) {
+    lds_byte *lp = (lds_byte *)rec;
+    bt.a = *(const __attribute__((address_space(3))) i32x4 *)(lp + oa);
+    load_tails<KIND>(bt, 0, ot, [&](uint32_t off) { return *(const __attribute__((address_space(3))) u32x4 *)(lp + off); },
+                     [&](uint32_t off) { return *(const __attribute__((address_space(3))) uint32_t *)(lp + off); });
+}
+
+// Row r's sum over both lane halves (lanes 0..31 hold it).
+__device__ __forceinline__ float half_sum(float acc, bool upper) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc), false, false);
+    return acc + __uint_as_float(upper ? sw[0] : sw[1]);
+}
+
+// Prepared records of the `width` values at x (LDS), eight records (zero past width / 32); the
+// first 64 threads write them.
+template <int KIND>
+__device__ __forceinline__ void prep_lds(const float *x, uint32_t width, uint8_t *recs) {
+    if (threadIdx.x >= 64) return;
+    const uint32_t blk = threadIdx.x / 8;
+    const int j = (int)(threadIdx.x % 8);
+    auto *rec = (__attribute__((address_space(3))) uint32_t *)(recs + blk * kPrepBytes);
+    if (blk < width / 32)
+        prep_values<KIND>(*(const f32x4 *)(x + blk * 32 + 4 * j), j, rec);
+    else
+        zero_record(j, rec);
+}
+
+// The second product: row groups w, w + W, ... of the d rows, K in flight as above;
+// out_part[blockIdx.x] gets the workgroup's share of each row.
+template <int KIND, int PAIRS, int K>
+__device__ __forceinline__ void run_tasks2(const FusedArgs &a, Batch<KIND> (&set)[K], const uint8_t *recs, uint32_t oq,
+                                           uint32_t os, uint32_t oa, uint32_t ot) {
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int lane = threadIdx.x % 64;
+    const bool upper = lane >= 32;
+    const uint32_t groups = a.d / 32;
+    for (uint32_t base = wave; base < groups; base += K * kFuseWaves) {
+#pragma unroll
+        for (int i = 0; i < K; i++) {
+            const uint32_t rg = base + i * kFuseWaves;
+            if (rg < groups) {
+                lds_operands<KIND>(set[i], recs, oa, ot);
+                float acc = 0.0f;
+                compute_batch<KIND, PAIRS>(set[i], upper, acc);
+                const float sum = half_sum(acc, upper);
+                if (!upper) a.out_part[(size_t)blockIdx.x * a.d + rg * 32 + lane] = sum;
+                if (rg + K * kFuseWaves < groups) load_task2<KIND, PAIRS>(set[i], a, rg + K * kFuseWaves, oq, os);
+            }
+        }
+    }
+}
+
+// Attention of one head over positions 0..T-1 (decode.rs:81-105) with q and the newest
+// position's k and v rows (T - 1) given apart (they may not be in the caches yet); the result a
+// (hd floats) goes to out (LDS). One pass over the caches: L = hd / 4 lanes share a cache row (a
+// 16-byte load each of its k and v), a lane group takes U rows at a time with all their loads
+// issued together and keeps a running maximum, sum and output (the softmax's max-subtracted
+// exponentials, rescaled when the maximum grows); the NR groups then meet through LDS, rescaled
+// to the common maximum. Rows past T are read as row T - 1 and dropped.
+template <int L>
+__device__ __forceinline__ void fused_attend(const float *qh, const float *knew, const float *vnew, const float *kc,
+                                             const float *vc, uint32_t T, uint32_t d, float scale, float *s,
+                                             float *accs, float *red, float *out) {
+    constexpr uint32_t hd = 4 * L, NR = kFuseThreads / L;
+    constexpr int U = 8;
+    const uint32_t h = blockIdx.x, tid = threadIdx.x;
+    const uint32_t li = tid % L, rg = tid / L, last = T - 1;
+    (void)red;
+    const f32x4 qv = *(const f32x4 *)(qh + 4 * li);
+    const float *kb = kc + h * hd + 4 * li;
+    const float *vb = vc + h * hd + 4 * li;
+    const f32x4 kl = *(const f32x4 *)(knew + 4 * li), vl = *(const f32x4 *)(vnew + 4 * li);
+    float m = -INFINITY, z = 0.0f;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t j0 = rg; j0 < T; j0 += U * NR) {  // the L lanes of a row share the loop bound
+        f32x4 kr[U], vr[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t j = min(j0 + u * NR, last);
+            kr[u] = j == last ? kl : gload4(kb + (size_t)j * d);
+            vr[u] = j == last ? vl : gload4(vb + (size_t)j * d);
+        }
+        float sc[U];
+        float mc = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            float dt = (qv.x * kr[u].x + qv.y * kr[u].y) + (qv.z * kr[u].z + qv.w * kr[u].w);
+#pragma unroll
+            for (int o = L / 2; o >= 1; o /= 2) dt += __shfl_xor(dt, o, L);
+            sc[u] = j0 + u * NR < T ? dt * scale : -INFINITY;
+            mc = fmaxf(mc, sc[u]);
+        }
+        const float mn = fmaxf(m, mc);  // finite: row j0 < T is in the chunk
+        const float corr = expf(m - mn);
+        z *= corr;
+        acc *= corr;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const float e = expf(sc[u] - mn);
+            z += e;
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[c] += e * vr[u][c];
+        }
+        m = mn;
+    }
+    // the groups' maxima, then each group's sum and output at the common maximum
+    if (li == 0) s[rg] = m;
+    __syncthreads();
+    float M = -INFINITY;
+    for (uint32_t g = 0; g < NR; g++) M = fmaxf(M, s[g]);
+    const float f = m == -INFINITY ? 0.0f : expf(m - M);  // groups with no rows add nothing
+    *(f32x4 *)&accs[rg * hd + 4 * li] = acc * f;
+    __syncthreads();
+    if (li == 0) s[NR + rg] = z * f;
+    __syncthreads();
+    if (tid < hd) {
+        float zs = 0.0f, t = 0.0f;
+        for (uint32_t g = 0; g < NR; g++) {
+            zs += s[NR + g];
+            t += accs[g * hd + tid];
+        }
+        out[tid] = t / zs;
+    }
+}
+
+// LDS of attn_out_kernel: the lane groups' maxima and sums, output partials, reduction slots, the
+// head's output, its prepared records.
+__host__ __device__ inline uint32_t attn_out_lds(uint32_t hd) {
+    return kAttnSlots * 4 + kFuseThreads * 16 + 2 * kFuseWaves * 4 + hd * 4 + 8 * kPrepBytes;
+}
+
+// Attention of head blockIdx.x over the cached positions 0..p (the query row and the caches
+// written by the QKV launch), then the head's columns of the output projection:
+// out_part[h] = a_h W_o[:, h] (hd = 4 L, PAIRS = hd / 64); the weights are requested first.
+template <int KIND, int L, int K2>
+__global__ __launch_bounds__(kFuseThreads) void attn_out_kernel(FusedArgs a) {
+    constexpr int PAIRS = L / 16;
+    constexpr uint32_t hd = 4 * L;
+    extern __shared__ __attribute__((aligned(16))) uint8_t flds[];
+    float *s = (float *)flds;
+    float *accs = s + kAttnSlots;
+    float *red = accs + kFuseThreads * 4;
+    float *att = red + 2 * kFuseWaves;
+    uint8_t *recs2 = (uint8_t *)(att + hd);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int lane = threadIdx.x % 64, r = lane % 32;
+    const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * (lane >= 32)) : (uint32_t)(lane * 16);
+    const uint32_t os = (uint32_t)(r * 16), oa = prep_a_offset(lane), ot = prep_tail_offset<KIND>(lane);
+    Batch<KIND> s2[K2];
+#pragma unroll
+    for (int i = 0; i < K2; i++)
+        if (wave + i * kFuseWaves < a.d / 32) load_task2<KIND, PAIRS>(s2[i], a, wave + i * kFuseWaves, oq, os);
+    const uint32_t p = (uint32_t)a.state[0];
+    const size_t off = (size_t)blockIdx.x * hd;
+    fused_attend<L>(a.q + off, a.kc + (size_t)p * a.d + off, a.vc + (size_t)p * a.d + off, a.kc, a.vc, p + 1, a.d,
+                    a.scale, s, accs, red, att);
+    __syncthreads();
+    prep_lds<KIND>(att, hd, recs2);
+    __syncthreads();
+    run_tasks2<KIND, PAIRS, K2>(a, s2, recs2, oq, os, oa, ot);
+}
+
+// After the last layer: x = x_in + (sum_j part[j] + b) and its final LayerNorm into global
+// prepared records (the head's x); one workgroup.
+template <int KIND>
+__global__ __launch_bounds__(kFuseThreads) void fused_final_kernel(FusedArgs a, uint8_t *__restrict__ out) {
+    __shared__ float red[kFuseWaves];
+    f32x4 v[kLnSlots];
+    fused_residual<KIND>(a, v);
+    ln_records<KIND, true>(v, a.ln_g, a.ln_b, a.eps, a.nb, (a.nb + 7) / 8 * 8, out, red);
+}
+
 // Sets the position and the first position whose input the argmax writes.
 __global__ void set_state_kernel(int32_t *state, int32_t pos, int32_t fill_from) {
     state[0] = pos;
@@ -509,6 +849,13 @@ struct fh_gpt2 {
     hipGraphExec_t exec = nullptr;
     bool use_graph = true;
     bool split_k = false;  // FERRUM_HIP_DECODE_SPLIT_K=1: K splits for the narrow products
+    // the step's form: 4 launches per layer (the attention with the output projection's head
+    // columns; FFN-down split along K) where the model allows, else 5; FERRUM_HIP_DECODE_STEP=5
+    // at load keeps 5
+    int form = 5;
+    uint32_t down_splits = 0;
+    float *xc = nullptr, *xm = nullptr;  // the residual row before / after the attention block
+    float *po = nullptr, *pf = nullptr;  // partial rows: [heads][dim], [down_splits][dim]
     uint64_t step_bytes = 0;
 };
 
@@ -536,10 +883,11 @@ template <int KIND, int PRO, int EPI>
 hipError_t launch_dgemv(hipStream_t s, DecodeGemv a, bool allow_split) {
     const uint32_t nb8 = (a.nb + 7) / 8, groups = (a.n + 31) / 32;
     uint32_t splits = 1, chunk8 = nb8;
-    if (allow_split && PRO == PRO_NONE && EPI != EPI_ARGMAX) plan_splits(groups, nb8, &splits, &chunk8);
+    if ((allow_split || EPI == EPI_PARTIAL) && PRO == PRO_NONE && EPI != EPI_ARGMAX)
+        plan_splits(groups, nb8, &splits, &chunk8);
     a.chunk = chunk8 * 8;
     const uint32_t W = chunk8 < (uint32_t)kMaxWaves ? chunk8 : (uint32_t)kMaxWaves;
-    const size_t recs = PRO == PRO_GLOBAL ? 0 : (PRO == PRO_LN ? nb8 * 8 : a.chunk);
+    const size_t recs = PRO == PRO_GLOBAL ? 0 : (PRO == PRO_LN || PRO == PRO_LNR ? nb8 * 8 : a.chunk);
     const size_t lds = recs * kPrepBytes + (size_t)W * 32 * 4 + (size_t)kMaxWaves * 4;
     decode_gemv_kernel<KIND, PRO, EPI><<<dim3(groups, splits), 64 * W, lds, s>>>(a);
     return hipGetLastError();
@@ -548,7 +896,15 @@ hipError_t launch_dgemv(hipStream_t s, DecodeGemv a, bool allow_split) {
 #define FH_DGEMV_KERNELS(K)                                                                             \
     (const void *)decode_gemv_kernel<K, PRO_LN, EPI_QKV>, (const void *)decode_gemv_kernel<K, PRO_NONE, EPI_RESIDUAL>, \
         (const void *)decode_gemv_kernel<K, PRO_LN, EPI_GELU>, (const void *)decode_gemv_kernel<K, PRO_GLOBAL, EPI_ARGMAX>, \
-        (const void *)decode_gemv_kernel<K, PRO_NONE, EPI_STORE>
+        (const void *)decode_gemv_kernel<K, PRO_NONE, EPI_STORE>, (const void *)decode_gemv_kernel<K, PRO_LNR, EPI_QKV>, \
+        (const void *)decode_gemv_kernel<K, PRO_LNR, EPI_GELU>, (const void *)decode_gemv_kernel<K, PRO_NONE, EPI_PARTIAL>
+
+// Register sets in flight per wavefront of attn_out_kernel's product.
+template <int L> constexpr int attn_k2() { return L == 64 ? 2 : 3; }
+#define FH_ATTN_OUT_KERNELS(K)                                                                                    \
+    (const void *)attn_out_kernel<K, 16, attn_k2<16>()>, (const void *)attn_out_kernel<K, 32, attn_k2<32>()>,     \
+        (const void *)attn_out_kernel<K, 64, attn_k2<64>()>
+constexpr uint32_t kAttnOutLdsMax = 96 * 1024;
 
 // Dynamic LDS beyond the default 64 KiB: prepared x of up to kMaxBlocks blocks plus the row
 // sums, and the attention scores of up to 16384 positions. Set once, before any capture.
@@ -558,6 +914,11 @@ hipError_t set_lds_limits() {
         const void *fns[] = {FH_DGEMV_KERNELS(FH_Q8_0), FH_DGEMV_KERNELS(FH_Q4_0)};
         for (const void *f : fns) {
             hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, gemv_lds);
+            if (r) return r;
+        }
+        const void *ao[] = {FH_ATTN_OUT_KERNELS(FH_Q8_0), FH_ATTN_OUT_KERNELS(FH_Q4_0)};
+        for (const void *f : ao) {
+            hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnOutLdsMax);
             if (r) return r;
         }
         const void *att[] = {(const void *)attention_kernel<2>, (const void *)attention_kernel<4>,
@@ -572,6 +933,7 @@ hipError_t set_lds_limits() {
     return e;
 }
 #undef FH_DGEMV_KERNELS
+#undef FH_ATTN_OUT_KERNELS
 
 template <int PRO, int EPI>
 hipError_t dgemv(hipStream_t s, fh_kind kind, const DecodeGemv &a, bool allow_split = false) {
@@ -660,6 +1022,127 @@ hipError_t enqueue_step(fh_gpt2 *m, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Splits along K of the four-launch step's FFN-down product (launch_dgemv's EPI_PARTIAL rule).
+uint32_t down_splits(size_t d, size_t hidden) {
+    uint32_t sp, c8;
+    plan_splits((uint32_t)(d / 32), (uint32_t)((hidden / 32 + 7) / 8), &sp, &c8);
+    return sp;
+}
+
+// Whether the four-launch step takes this model (head width 64, 128 or 256, LDS within bounds).
+bool four_fits(size_t d, size_t heads) {
+    const size_t hd = d / heads;
+    if (hd != 64 && hd != 128 && hd != 256) return false;
+    return heads <= 64 && attn_out_lds((uint32_t)hd) <= kAttnOutLdsMax;
+}
+
+template <int KIND>
+hipError_t launch_attn_out(hipStream_t s, uint32_t hd, uint32_t heads, const FusedArgs &a) {
+    const size_t lds = attn_out_lds(hd);
+    switch (hd) {
+    case 64: attn_out_kernel<KIND, 16, attn_k2<16>()><<<heads, kFuseThreads, lds, s>>>(a); break;
+    case 128: attn_out_kernel<KIND, 32, attn_k2<32>()><<<heads, kFuseThreads, lds, s>>>(a); break;
+    default: attn_out_kernel<KIND, 64, attn_k2<64>()><<<heads, kFuseThreads, lds, s>>>(a); break;
+    }
+    return hipGetLastError();
+}
+
+// The head: the final LayerNorm of x_in + (sum of the partial rows + b), the head product and the
+// greedy pick.
+hipError_t enqueue_head(fh_gpt2 *m, hipStream_t s, const float *x_in, const float *part, uint32_t nparts,
+                        const float *b) {
+    FusedArgs z{};
+    z.x_in = x_in;
+    z.part = part;
+    z.pbias = b;
+    z.nparts = nparts;
+    z.state = m->state;
+    z.x_out = m->x;
+    z.ln_g = fp(m->lnf_g);
+    z.ln_b = fp(m->lnf_b);
+    z.eps = m->eps;
+    z.d = (uint32_t)m->dim;
+    z.nb = (uint32_t)(m->dim / 32);
+    if (m->kind == FH_Q8_0)
+        fused_final_kernel<FH_Q8_0><<<1, kFuseThreads, 0, s>>>(z, m->prep);
+    else
+        fused_final_kernel<FH_Q4_0><<<1, kFuseThreads, 0, s>>>(z, m->prep);
+    hipError_t e = hipGetLastError();
+    if (e) return e;
+    DecodeGemv a = dg(m, m->head, m->x, m->logits);
+    a.prep = m->prep;
+    a.pick = m->pick;
+    if ((e = dgemv<PRO_GLOBAL, EPI_ARGMAX>(s, m->kind, a))) return e;
+    pick_kernel<<<1, 1024, 0, s>>>(m->partial, m->pick, (uint32_t)((m->vocab + 31) / 32), m->state, m->inputs);
+    return hipGetLastError();
+}
+
+// Enqueue one four-launch step: per layer LN1 + QKV (the residual row formed from the previous
+// layer's partial rows), attention + the output projection's head columns (partial rows per
+// head), LN2 + FFN-up + GELU (the residual row from those), FFN-down split along K (partial rows
+// per split); then the head.
+hipError_t enqueue_four(fh_gpt2 *m, hipStream_t s) {
+    const uint32_t d = (uint32_t)m->dim, hd = (uint32_t)(m->dim / m->heads), nb = d / 32;
+    const uint32_t heads = (uint32_t)m->heads, S = m->down_splits;
+    hipError_t e = hipSuccess;
+    for (size_t l = 0; l < m->blocks.size(); l++) {
+        const auto &L = m->blocks[l];
+        DecodeGemv a = dg(m, L.wqkv, nullptr, m->q);
+        if (l == 0) {
+            a.emb_qs = m->tok->qs;
+            a.emb_ds = m->tok->ds;
+            a.pos_tab = fp(m->pos_tab);
+        } else {
+            a.x_in = m->xm;
+            a.rpart = m->pf;
+            a.rbias = fp(m->blocks[l - 1].b2);
+            a.nparts = S;
+        }
+        a.inputs = m->inputs;
+        a.x_out = m->xc;
+        a.ln_g = fp(L.ln1_g);
+        a.ln_b = fp(L.ln1_b);
+        a.eps = m->eps;
+        a.bias = fp(L.bqkv);
+        a.kc = L.kc;
+        a.vc = L.vc;
+        a.split = d;
+        if ((e = dgemv<PRO_LNR, EPI_QKV>(s, m->kind, a))) return e;
+        FusedArgs t{};
+        t.q = m->q;
+        t.kc = L.kc;
+        t.vc = L.vc;
+        t.state = m->state;
+        t.d = d;
+        t.nb = nb;
+        t.scale = 1.0f / sqrtf((float)hd);
+        t.qs2 = L.wo->qs;
+        t.ds2 = L.wo->ds;
+        t.nb2 = nb;
+        t.out_part = m->po;
+        if ((e = m->kind == FH_Q8_0 ? launch_attn_out<FH_Q8_0>(s, hd, heads, t) : launch_attn_out<FH_Q4_0>(s, hd, heads, t)))
+            return e;
+        a = dg(m, L.w1, nullptr, m->f);
+        a.x_in = m->xc;
+        a.rpart = m->po;
+        a.rbias = fp(L.bo);
+        a.nparts = heads;
+        a.x_out = m->xm;
+        a.ln_g = fp(L.ln2_g);
+        a.ln_b = fp(L.ln2_b);
+        a.eps = m->eps;
+        a.bias = fp(L.b1);
+        if ((e = dgemv<PRO_LNR, EPI_GELU>(s, m->kind, a))) return e;
+        a = dg(m, L.w2, m->f, m->pf);
+        if ((e = dgemv<PRO_NONE, EPI_PARTIAL>(s, m->kind, a))) return e;
+    }
+    return enqueue_head(m, s, m->xm, m->pf, S, fp(m->blocks.back().b2));
+}
+
+hipError_t enqueue_any(fh_gpt2 *m, hipStream_t s) {
+    return m->form == 4 ? enqueue_four(m, s) : enqueue_step(m, s);
+}
+
 // Run one step on the device stream: the captured graph (made on first use), or the launches.
 fh_status run_step(fh_gpt2 *m) {
     fh_device *dev = m->dev;
@@ -668,7 +1151,7 @@ fh_status run_step(fh_gpt2 *m) {
     if (m->use_graph && !m->exec) {
         hipError_t e = hipStreamBeginCapture(dev->stream, hipStreamCaptureModeThreadLocal);
         if (e) return hip_fail(dev, e, "gpt2 step capture");
-        const hipError_t le = enqueue_step(m, dev->stream);
+        const hipError_t le = enqueue_any(m, dev->stream);
         e = hipStreamEndCapture(dev->stream, &m->graph);
         if (le) return hip_fail(dev, le, "gpt2 step capture");
         if (e) return hip_fail(dev, e, "gpt2 step capture");
@@ -678,7 +1161,7 @@ fh_status run_step(fh_gpt2 *m) {
             return hip_fail(dev, e, "gpt2 step graph");
         }
     }
-    hipError_t e = m->use_graph ? hipGraphLaunch(m->exec, dev->stream) : enqueue_step(m, dev->stream);
+    hipError_t e = m->use_graph ? hipGraphLaunch(m->exec, dev->stream) : enqueue_any(m, dev->stream);
     if (e) return hip_fail(dev, e, "gpt2 step");
     return end_command(dev, "gpt2 step");
 }
@@ -804,9 +1287,14 @@ fh_status fh_gpt2_from_gguf(fh_device *dev, const fh_gguf *g, fh_gpt2 **out) {
     }
     const size_t max_groups = groups_d;
     m->n_tickets = max_groups + 1;
+    const char *sf = getenv("FERRUM_HIP_DECODE_STEP");
+    m->form = !(sf && atoi(sf) == 5) && four_fits(d, m->heads) ? 4 : 5;
+    m->down_splits = down_splits(d, h);
+    const size_t four_bytes =
+        m->form == 4 ? 2 * up(d * 4) + up(m->heads * d * 4) + up((size_t)m->down_splits * d * 4) : 0;
     const size_t total = 2 * m->layers * cache + 3 * up(d * 4) + up(h * 4) + up(m->vocab * 4) + up(16) +
                          up((m->ctx + 1) * 4) + up((d / 32 + 7) / 8 * 8 * kPrepBytes) + up(part_floats * 4) +
-                         up(groups_v * 4) + up(m->n_tickets * 4);
+                         up(groups_v * 4) + up(m->n_tickets * 4) + four_bytes;
     if ((st = alloc_bytes(dev, total, &m->arena))) return gpt2_fail_free(m, st);
     uint8_t *p = (uint8_t *)m->arena;
     for (auto &L : m->blocks) {
@@ -836,6 +1324,16 @@ fh_status fh_gpt2_from_gguf(fh_device *dev, const fh_gguf *g, fh_gpt2 **out) {
     m->pick = (uint32_t *)p;
     p += up(groups_v * 4);
     m->tickets = (uint32_t *)p;  // zero from the allocation; every launch leaves them zero
+    p += up(m->n_tickets * 4);
+    if (m->form == 4) {
+        m->xc = (float *)p;
+        p += up(d * 4);
+        m->xm = (float *)p;
+        p += up(d * 4);
+        m->po = (float *)p;
+        p += up(m->heads * d * 4);
+        m->pf = (float *)p;
+    }
     if (hipError_t e = set_lds_limits()) return gpt2_fail_free(m, hip_fail(dev, e, "gpt2 kernels"));
     const char *ng = getenv("FERRUM_HIP_NO_GRAPH");
     m->use_graph = !(ng && ng[0] == '1');
@@ -864,6 +1362,10 @@ fh_status fh_gpt2_config(const fh_gpt2 *m, size_t *vocab, size_t *ctx, size_t *d
 fh_kind fh_gpt2_kind(const fh_gpt2 *m) { return m ? m->kind : (fh_kind)0; }
 size_t fh_gpt2_pos(const fh_gpt2 *m) { return m ? m->pos : 0; }
 uint64_t fh_gpt2_step_bytes(const fh_gpt2 *m) { return m ? m->step_bytes : 0; }
+size_t fh_gpt2_step_launches(const fh_gpt2 *m) {
+    if (!m) return 0;
+    return m->form == 4 ? 4 * m->layers + 3 : 5 * m->layers + 4;
+}
 void fh_gpt2_reset(fh_gpt2 *m) {
     if (m) m->pos = 0;  // later positions overwrite the cache rows they read
 }

@@ -484,7 +484,6 @@ __device__ __forceinline__ float lo_half(uint32_t v) { return (float)__builtin_b
 __device__ __forceinline__ float hi_half(uint32_t v) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
 }
-__device__ __forceinline__ float sbyte(uint32_t v, int i) { return (float)(int32_t)(int8_t)(v >> (8 * i)); }
 __device__ __forceinline__ float ubyte(uint32_t v, int i) { return (float)((v >> (8 * i)) & 0xffu); }
 
 template <uint32_t T>

@@ -173,6 +173,7 @@ def lib() -> ctypes.CDLL:
         "fh_gpt2_pos": (S, [P]),
         "fh_gpt2_reset": (None, [P]),
         "fh_gpt2_step_bytes": (U64, [P]),
+        "fh_gpt2_step_launches": (S, [P]),
         "fh_gpt2_feed": (I, [P, P, S, P]),
         "fh_gpt2_generate": (I, [P, P, P, S, S, P]),
         "fh_llama_from_gguf": (I, [P, P, I, PP]),

@@ -63,6 +63,10 @@ class GpuGpt2:
     def step_bytes(self) -> int:
         return lib().fh_gpt2_step_bytes(self._h)
 
+    def step_launches(self) -> int:
+        """Kernel launches in one decode step (2 per layer + 3 on the fused step)."""
+        return lib().fh_gpt2_step_launches(self._h)
+
     def feed(self, token: int, logits: bool = True):
         """GpuGpt2::feed (gpt2.rs:216-265): the next-token logits row (or None)."""
         out = np.empty(self._cfg.vocab, np.float32) if logits else None

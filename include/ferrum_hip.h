@@ -391,6 +391,10 @@ FH_API size_t fh_gpt2_pos(const fh_gpt2 *m);
 FH_API void fh_gpt2_reset(fh_gpt2 *m);
 /* Packed weight bytes one step reads (every matrix and the head). */
 FH_API uint64_t fh_gpt2_step_bytes(const fh_gpt2 *m);
+/* Kernel launches in one step (no counterpart in the reference): 4 per layer + 3 where the head
+ * width is 64, 128 or 256 (FERRUM_HIP_DECODE_STEP=5 at load keeps the five-launch form), else 5 per
+ * layer + 4. */
+FH_API size_t fh_gpt2_step_launches(const fh_gpt2 *m);
 /* GpuGpt2::feed (gpt2.rs:216-265): consume `token` at the next position; when logits is not NULL
  * it receives the vocab next-token logits (and the call waits for them). Errors: "context of N
  * tokens is full", "token T is out of range for vocab V". */
