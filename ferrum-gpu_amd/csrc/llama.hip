@@ -195,14 +195,92 @@ __device__ __forceinline__ float split_sum(const float *__restrict__ p, size_t i
     return t;
 }
 
+// One row of an RMSNorm's input (ferrum_ref/src/models/llama/ops.rs:55-66): v = x, or with ADD
+// v = x + o (the residual add, nn::add; o possibly K-split partial sums, added in split order)
+// stored back into x. A thread takes float4 chunks q = tid + 256 i: chunk i < kKeepRow stays in
+// registers (rows up to 8192 floats; wider rows are read again), and a chunk's x and partial-sum
+// loads are issued together before any is added (a loop of dependent loads cost one round trip
+// per split). Returns the thread's sum of squares, chunk by chunk in order. Rows of whole float4s.
+constexpr int kKeepRow = 8;
+constexpr uint32_t kMaxSplits = 8;  // the MFMA GEMMs' K splits (gemm_splits)
+// Four consecutive elements (at offset off) of a product left as `splits` partial sums `stride`
+// floats apart, added in split order; the first kMaxSplits loads are issued together.
+__device__ __forceinline__ f32x4 split_chunk(const float *__restrict__ o, size_t off, uint32_t splits, size_t stride) {
+    f32x4 p[kMaxSplits];
+#pragma unroll
+    for (uint32_t sl = 0; sl < kMaxSplits; sl++) p[sl] = *(const f32x4 *)(o + (sl < splits ? sl : 0u) * stride + off);
+    f32x4 t = p[0];
+#pragma unroll
+    for (uint32_t sl = 1; sl < kMaxSplits; sl++) t = sl < splits ? t + p[sl] : t;
+    for (uint32_t sl = kMaxSplits; sl < splits; sl++) t += *(const f32x4 *)(o + sl * stride + off);
+    return t;
+}
+template <bool ADD>
+__device__ __forceinline__ f32x4 row_chunk(float *__restrict__ x, const float *__restrict__ o, size_t base, uint32_t q,
+                                           uint32_t splits, size_t stride) {
+    f32x4 v = *(const f32x4 *)(x + base + 4 * q);
+    if constexpr (ADD) v = v + split_chunk(o, base + 4 * q, splits, stride);
+    return v;
+}
+template <bool ADD>
+__device__ __forceinline__ float row_load4(float *__restrict__ x, const float *__restrict__ o, size_t base, uint32_t nq,
+                                           uint32_t splits, size_t stride, f32x4 (&v)[kKeepRow]) {
+    float ss = 0.0f;
+    const uint32_t tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < kKeepRow; i++) {
+        v[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (256u * i >= nq) continue;  // the workgroup agrees
+        const uint32_t q = tid + 256 * i;
+        const f32x4 w = row_chunk<ADD>(x, o, base, q < nq ? q : nq - 1, splits, stride);
+        if (q < nq) {
+            if constexpr (ADD) *(f32x4 *)(x + base + 4 * q) = w;
+            v[i] = w;
+#pragma unroll
+            for (int c = 0; c < 4; c++) ss += w[c] * w[c];
+        }
+    }
+    for (uint32_t q = tid + 256 * kKeepRow; q < nq; q += 256) {
+        const f32x4 w = row_chunk<ADD>(x, o, base, q, splits, stride);
+        if constexpr (ADD) *(f32x4 *)(x + base + 4 * q) = w;
+#pragma unroll
+        for (int c = 0; c < 4; c++) ss += w[c] * w[c];
+    }
+    return ss;
+}
+// Chunk q of the normalised row h = v / sqrt(mean(v^2) + eps) * g (two roundings, as ops.rs).
+__device__ __forceinline__ f32x4 row_norm4(f32x4 v, const float *__restrict__ g, uint32_t q, float inv) {
+    const f32x4 gg = *(const f32x4 *)(g + 4 * q);
+    f32x4 h;
+#pragma unroll
+    for (int c = 0; c < 4; c++) h[c] = __fmul_rn(__fmul_rn(v[c], inv), gg[c]);
+    return h;
+}
+
 // RMSNorm per row (ferrum_ref/src/models/llama/ops.rs:55-66): h = v / sqrt(mean(v^2) + eps) * g,
-// v = x, or with ADD v = x + o stored back into x first (the residual add, nn::add).
+// v = x, or with ADD v = x + o stored back into x first (the residual add, nn::add). Rows of whole
+// float4s take row_load4 (as rmsnorm_split_kernel, so the fast path's fused producers give the same
+// bits); others one element per thread.
 template <bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(float *__restrict__ x, const float *__restrict__ o,
                                                       const float *__restrict__ g, float *__restrict__ h, uint32_t d,
                                                       float eps, uint32_t o_splits, size_t o_stride) {
     __shared__ float red[4];
     const size_t base = (size_t)blockIdx.x * d;
+    if (d % 4 == 0) {
+        const uint32_t nq = d / 4;
+        f32x4 v[kKeepRow];
+        const float ms = block_sum_256(row_load4<ADD>(x, o, base, nq, o_splits, o_stride, v), red) / (float)d;
+        const float inv = 1.0f / sqrtf(ms + eps);
+#pragma unroll
+        for (int i = 0; i < kKeepRow; i++) {
+            const uint32_t q = threadIdx.x + 256 * i;
+            if (q < nq) *(f32x4 *)(h + base + 4 * q) = row_norm4(v[i], g, q, inv);
+        }
+        for (uint32_t q = threadIdx.x + 256 * kKeepRow; q < nq; q += 256)
+            *(f32x4 *)(h + base + 4 * q) = row_norm4(*(const f32x4 *)(x + base + 4 * q), g, q, inv);
+        return;
+    }
     float ss = 0.0f;
     for (uint32_t i = threadIdx.x; i < d; i += 256) {
         float v = x[base + i];
@@ -227,18 +305,32 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float *__restrict__ 
     extern __shared__ __attribute__((aligned(16))) float hrow[];
     __shared__ float red[4], red2[4];
     const size_t base = (size_t)blockIdx.x * d;
-    float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < d; i += 256) {
-        float v = x[base + i];
-        if constexpr (ADD) {
-            v = v + split_sum(o, base + i, o_splits, o_stride);
-            x[base + i] = v;
+    if (d % 4 == 0) {
+        const uint32_t nq = d / 4;
+        f32x4 v[kKeepRow];
+        const float ms = block_sum_256(row_load4<ADD>(x, o, base, nq, o_splits, o_stride, v), red) / (float)d;
+        const float inv = 1.0f / sqrtf(ms + eps);
+#pragma unroll
+        for (int i = 0; i < kKeepRow; i++) {
+            const uint32_t q = threadIdx.x + 256 * i;
+            if (q < nq) *(f32x4 *)&hrow[4 * q] = row_norm4(v[i], g, q, inv);
         }
-        ss += v * v;
+        for (uint32_t q = threadIdx.x + 256 * kKeepRow; q < nq; q += 256)
+            *(f32x4 *)&hrow[4 * q] = row_norm4(*(const f32x4 *)(x + base + 4 * q), g, q, inv);
+    } else {
+        float ss = 0.0f;
+        for (uint32_t i = threadIdx.x; i < d; i += 256) {
+            float v = x[base + i];
+            if constexpr (ADD) {
+                v = v + split_sum(o, base + i, o_splits, o_stride);
+                x[base + i] = v;
+            }
+            ss += v * v;
+        }
+        const float ms = block_sum_256(ss, red) / (float)d;
+        const float inv = 1.0f / sqrtf(ms + eps);
+        for (uint32_t i = threadIdx.x; i < d; i += 256) hrow[i] = __fmul_rn(__fmul_rn(x[base + i], inv), g[i]);
     }
-    const float ms = block_sum_256(ss, red) / (float)d;
-    const float inv = 1.0f / sqrtf(ms + eps);
-    for (uint32_t i = threadIdx.x; i < d; i += 256) hrow[i] = __fmul_rn(__fmul_rn(x[base + i], inv), g[i]);
     __syncthreads();
     split_row_fast<KIND>([&](uint32_t q) { return *(const f32x4 *)&hrow[4 * q]; }, blockIdx.x, d, dst.xh, dst.xl,
                          dst.xsc, red2);
@@ -249,14 +341,29 @@ __global__ __launch_bounds__(256) void swiglu_split_kernel(const float *__restri
     extern __shared__ __attribute__((aligned(16))) float hrow[];
     __shared__ float red[4];
     const size_t r = blockIdx.x;
-    for (uint32_t j = threadIdx.x; j < hid / 4; j += 256) {
-        const f32x4 gg = *(const f32x4 *)(gu + r * 2 * hid + 4 * j);
-        const f32x4 u = *(const f32x4 *)(gu + r * 2 * hid + hid + 4 * j);
+    const uint32_t nq = hid / 4;
+    auto act = [&](uint32_t j, f32x4 gg, f32x4 u) {
         f32x4 y;
 #pragma unroll
         for (int c = 0; c < 4; c++) y[c] = __fmul_rn(gg[c] / (1.0f + expf(-gg[c])), u[c]);
         *(f32x4 *)&hrow[4 * j] = y;
+    };
+    // the row's first kKeepRow chunks are all requested before any is used (one round trip)
+    f32x4 gk[kKeepRow], uk[kKeepRow];
+#pragma unroll
+    for (int i = 0; i < kKeepRow; i++) {
+        if (256u * i >= nq) continue;  // the workgroup agrees
+        const uint32_t j = min(threadIdx.x + 256 * i, nq - 1);
+        gk[i] = *(const f32x4 *)(gu + r * 2 * hid + 4 * j);
+        uk[i] = *(const f32x4 *)(gu + r * 2 * hid + hid + 4 * j);
     }
+#pragma unroll
+    for (int i = 0; i < kKeepRow; i++) {
+        const uint32_t j = threadIdx.x + 256 * i;
+        if (256u * i < nq && j < nq) act(j, gk[i], uk[i]);
+    }
+    for (uint32_t j = threadIdx.x + 256 * kKeepRow; j < nq; j += 256)
+        act(j, *(const f32x4 *)(gu + r * 2 * hid + 4 * j), *(const f32x4 *)(gu + r * 2 * hid + hid + 4 * j));
     __syncthreads();
     split_row_fast<KIND>([&](uint32_t q) { return *(const f32x4 *)&hrow[4 * q]; }, (uint32_t)r, hid, dst.xh, dst.xl,
                          dst.xsc, red);
@@ -271,11 +378,18 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(const float *__restrict__
                                                        const float *__restrict__ bias, const float *__restrict__ cos_t,
                                                        const float *__restrict__ sin_t, uint32_t width,
                                                        uint32_t rot_heads, uint32_t hd, uint32_t rope_dim, int neox) {
-    extern __shared__ float row[];
+    extern __shared__ __attribute__((aligned(16))) float row[];
     const size_t base = (size_t)blockIdx.x * width;
-    for (uint32_t c = threadIdx.x; c < width; c += 256) {
-        const float v = split_sum(src, base + c, src_splits, src_stride);
-        row[c] = bias ? v + bias[c] : v;
+    if (width % 4 == 0) {  // four elements a thread, the splits' loads issued together
+        for (uint32_t q = threadIdx.x; q < width / 4; q += 256) {
+            const f32x4 v = split_chunk(src, base + 4 * q, src_splits, src_stride);
+            *(f32x4 *)&row[4 * q] = bias ? v + *(const f32x4 *)(bias + 4 * q) : v;
+        }
+    } else {
+        for (uint32_t c = threadIdx.x; c < width; c += 256) {
+            const float v = split_sum(src, base + c, src_splits, src_stride);
+            row[c] = bias ? v + bias[c] : v;
+        }
     }
     __syncthreads();
     const uint32_t half = rope_dim / 2, rotated = rot_heads * hd;

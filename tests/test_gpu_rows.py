@@ -113,6 +113,55 @@ def test_rows_identity_reads_back_the_dequantised_weights(fh, g, orc, kind_name)
         assert np.array_equal(g.read(gy), want), (kind_name, k, n)
 
 
+@pytest.mark.parametrize("kind_name", ["Q8_0", "Q4_0"])
+def test_rows8_identity_rows_read_back_every_k_position(fh, g, orc, kind_name):
+    """Products of at most 8 rows (one launch of row capacity 8): x = 8 (and 3) rows of the
+    identity pick weight rows, compared with f32 == (every k position of a block is hit once over
+    the four sweeps, so a misplaced element, a swapped x part or a wrong scale shows); widths past
+    64 blocks run the two K halves."""
+    kind = fh.QKind[kind_name]
+    for k, n in [(256, 40), (2304, 96)]:
+        b = orc.quantise_matrix(int(kind), nasty(orc, k * n), k, n)
+        want = orc.dequantised_in_out(int(kind), b, k, n).reshape(k, n)
+        qw = fh.upload_qweight(g, kind, b, k, n)
+        for sweep in range(4):
+            ks = [(8 * sweep + i) % 32 + 32 * ((5 * i + sweep) % (k // 32)) for i in range(8)]
+            for m in (8, 3):
+                x = np.zeros((m, k), dtype=np.float32)
+                for r in range(m):
+                    x[r, ks[r]] = 1.0
+                gx, gy = g.upload(x.reshape(-1)), g.zeros(m * n)
+                fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.Rows)
+                got = g.read(gy).reshape(m, n)
+                assert np.array_equal(got, want[ks[:m]] + 0.0), (kind_name, k, n, sweep, m)
+
+
+def test_rows8_plan_gives_each_product_its_single_launch_bits(fh, g, orc):
+    """A plan of products of at most 8 rows (row capacity 8) over both formats, with one and two
+    K halves and ragged outputs: every product equals its single launch bit for bit."""
+    rng = np.random.default_rng(12)
+    probs, keep, checks = [], [], []
+    for kind, m, k, n in [(fh.QKind.Q4_0, 8, 2048, 2560), (fh.QKind.Q4_0, 3, 896, 300),
+                          (fh.QKind.Q8_0, 2, 768, 2304), (fh.QKind.Q8_0, 8, 5632, 257)]:
+        w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+        x = rng.standard_normal(m * k).astype(np.float32)
+        b = orc.quantise_matrix(int(kind), w, k, n)
+        qw = fh.upload_qweight(g, kind, b, k, n)
+        gx, gy, gs = g.upload(x), g.zeros(m * n), g.zeros(m * n)
+        fh.linear_q_with(g, gx, qw, gs, m, fh.QPath.Rows)
+        keep += [qw, gx, gy, gs]
+        probs.append((qw, gx.device_ptr(), gy.device_ptr(), m))
+        checks.append((gy, gs, cpu(orc, kind, b, x, m, k, n)))
+    plan = fh.RowsPlan(g, probs)
+    for rep in range(2):
+        plan.run()
+        for gy, gs, want in checks:
+            got = g.read(gy)
+            assert np.array_equal(got.view(np.uint32), g.read(gs).view(np.uint32)), rep
+            assert orc.max_rel_err(got, want) < REDUCING
+    plan.free()
+
+
 LLAMA1B = [(2048, 2560), (2048, 2048), (2048, 11264), (5632, 2048)]
 
 
