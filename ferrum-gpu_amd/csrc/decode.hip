@@ -40,7 +40,7 @@
 namespace fh {
 namespace {
 
-enum { PRO_NONE = 0, PRO_LN = 1, PRO_GLOBAL = 2, PRO_LNR = 3 };  // PRO_LNR: LayerNorm of the residual row (fused_residual)
+enum { PRO_NONE = 0, PRO_LN = 1, PRO_GLOBAL = 2, PRO_LNR = 3 };  // PRO_LNR: LayerNorm of the residual row (residual_row)
 enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_GELU = 2, EPI_QKV = 3, EPI_ARGMAX = 4, EPI_PARTIAL = 5 };
 
 constexpr int kMaxWaves = 8;           // wavefronts per decode-GEMV workgroup (two per SIMD)
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void ln_prep_kernel(const float *__
     ln_prep<KIND, true>(x, lg, lb, eps, nb, (nb + 7) / 8 * 8, out, red);
 }
 
-struct FusedArgs {
+struct StepArgs {
     // the residual row: x_in + (sum over nparts rows of part + pbias), or (x_in == null) the
     // embedding tok[inputs[p]] + pos_tab[p]
     const float *x_in, *part, *pbias;
@@ -222,7 +222,7 @@ struct FusedArgs {
 
 // The residual row into the thread's slots (see ln_records); workgroup (0, 0) stores it.
 template <int KIND>
-__device__ __forceinline__ void fused_residual(const FusedArgs &a, f32x4 (&v)[kLnSlots]) {
+__device__ __forceinline__ void residual_row(const StepArgs &a, f32x4 (&v)[kLnSlots]) {
     const uint32_t nb = a.nb, d = a.d;
 #pragma unroll
     for (uint32_t u = 0; u < kLnSlots; u++) {
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
         ln_prep<KIND, false>(a.x, a.ln_g, a.ln_b, a.eps, nb, span, prep, red);
         __syncthreads();
     } else if constexpr (PRO == PRO_LNR) {
-        FusedArgs f{};
+        StepArgs f{};
         f.x_in = a.x_in;
         f.part = a.rpart;
         f.pbias = a.rbias;
@@ -348,7 +348,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
         f.d = nb * 32;
         f.nb = nb;
         f32x4 v[kLnSlots];
-        fused_residual<KIND>(f, v);
+        residual_row<KIND>(f, v);
         ln_records<KIND, false>(v, a.ln_g, a.ln_b, a.eps, nb, span, prep, red);
         __syncthreads();
     } else if constexpr (PRO == PRO_NONE) {
@@ -398,7 +398,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
     for (uint32_t w = 0; w < W; w++) t += part[w * 32 + r];
     const uint32_t row = g * 32 + r;
     if constexpr (EPI == EPI_PARTIAL) {
-        // the split's row sums, added in split order by their consumer (fused_residual)
+        // the split's row sums, added in split order by their consumer (residual_row)
         if (row < a.n) a.y[(size_t)sp * a.n + row] = t;
         return;
     }
@@ -600,16 +600,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float *__
 // attn_out_kernel (one workgroup per head h): a_h = softmax(q k^T / sqrt(hd)) v over the cached
 // positions, then out_part[h] = a_h W_o[:, h] (the head's columns of the output projection). Its
 // partial rows, and those of the FFN-down product split along K, are added in a fixed order by
-// the next launch's prologue (fused_residual), so a step's results do not depend on timing; no
+// the next launch's prologue (residual_row), so a step's results do not depend on timing; no
 // workgroup waits for another inside a launch.
-constexpr int kFuseThreads = 512;
-constexpr int kFuseWaves = kFuseThreads / 64;
-constexpr uint32_t kAttnSlots = 2 * kFuseThreads / 16;  // fused_attend: two floats per lane group (L >= 16)
+constexpr int kStepThreads = 512;
+constexpr int kStepWaves = kStepThreads / 64;
+constexpr uint32_t kAttnSlots = 2 * kStepThreads / 16;  // attend_head: two floats per lane group (L >= 16)
 
 // The second product's task for row group rg: blocks b0 = blockIdx.x * G .. b0 + 2 PAIRS - 1 of
 // its rows (b0 even, all in one run of eight scales).
 template <int KIND, int PAIRS>
-__device__ __forceinline__ void load_task2(Batch<KIND> &bt, const FusedArgs &a, uint32_t rg, uint32_t oq,
+__device__ __forceinline__ void load_task2(Batch<KIND> &bt, const StepArgs &a, uint32_t rg, uint32_t oq,
                                            uint32_t os) {
     constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
     const uint32_t nb2 = a.nb2, nb28 = (nb2 + 7) / 8, b0 = blockIdx.x * (2 * PAIRS);
@@ -665,23 +665,23 @@ __device__ __forceinline__ void prep_lds(const float *x, uint32_t width, uint8_t
 // The second product: row groups w, w + W, ... of the d rows, K in flight as above;
 // out_part[blockIdx.x] gets the workgroup's share of each row.
 template <int KIND, int PAIRS, int K>
-__device__ __forceinline__ void run_tasks2(const FusedArgs &a, Batch<KIND> (&set)[K], const uint8_t *recs, uint32_t oq,
+__device__ __forceinline__ void run_tasks2(const StepArgs &a, Batch<KIND> (&set)[K], const uint8_t *recs, uint32_t oq,
                                            uint32_t os, uint32_t oa, uint32_t ot) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int lane = threadIdx.x % 64;
     const bool upper = lane >= 32;
     const uint32_t groups = a.d / 32;
-    for (uint32_t base = wave; base < groups; base += K * kFuseWaves) {
+    for (uint32_t base = wave; base < groups; base += K * kStepWaves) {
 #pragma unroll
         for (int i = 0; i < K; i++) {
-            const uint32_t rg = base + i * kFuseWaves;
+            const uint32_t rg = base + i * kStepWaves;
             if (rg < groups) {
                 lds_operands<KIND>(set[i], recs, oa, ot);
                 float acc = 0.0f;
                 compute_batch<KIND, PAIRS>(set[i], upper, acc);
                 const float sum = half_sum(acc, upper);
                 if (!upper) a.out_part[(size_t)blockIdx.x * a.d + rg * 32 + lane] = sum;
-                if (rg + K * kFuseWaves < groups) load_task2<KIND, PAIRS>(set[i], a, rg + K * kFuseWaves, oq, os);
+                if (rg + K * kStepWaves < groups) load_task2<KIND, PAIRS>(set[i], a, rg + K * kStepWaves, oq, os);
             }
         }
     }
@@ -695,10 +695,10 @@ __device__ __forceinline__ void run_tasks2(const FusedArgs &a, Batch<KIND> (&set
 // exponentials, rescaled when the maximum grows); the NR groups then meet through LDS, rescaled
 // to the common maximum. Rows past T are read as row T - 1 and dropped.
 template <int L>
-__device__ __forceinline__ void fused_attend(const float *qh, const float *knew, const float *vnew, const float *kc,
+__device__ __forceinline__ void attend_head(const float *qh, const float *knew, const float *vnew, const float *kc,
                                              const float *vc, uint32_t T, uint32_t d, float scale, float *s,
                                              float *accs, float *red, float *out) {
-    constexpr uint32_t hd = 4 * L, NR = kFuseThreads / L;
+    constexpr uint32_t hd = 4 * L, NR = kStepThreads / L;
     constexpr int U = 8;
     const uint32_t h = blockIdx.x, tid = threadIdx.x;
     const uint32_t li = tid % L, rg = tid / L, last = T - 1;
@@ -763,21 +763,21 @@ __device__ __forceinline__ void fused_attend(const float *qh, const float *knew,
 // LDS of attn_out_kernel: the lane groups' maxima and sums, output partials, reduction slots, the
 // head's output, its prepared records.
 __host__ __device__ inline uint32_t attn_out_lds(uint32_t hd) {
-    return kAttnSlots * 4 + kFuseThreads * 16 + 2 * kFuseWaves * 4 + hd * 4 + 8 * kPrepBytes;
+    return kAttnSlots * 4 + kStepThreads * 16 + 2 * kStepWaves * 4 + hd * 4 + 8 * kPrepBytes;
 }
 
 // Attention of head blockIdx.x over the cached positions 0..p (the query row and the caches
 // written by the QKV launch), then the head's columns of the output projection:
 // out_part[h] = a_h W_o[:, h] (hd = 4 L, PAIRS = hd / 64); the weights are requested first.
 template <int KIND, int L, int K2>
-__global__ __launch_bounds__(kFuseThreads) void attn_out_kernel(FusedArgs a) {
+__global__ __launch_bounds__(kStepThreads) void attn_out_kernel(StepArgs a) {
     constexpr int PAIRS = L / 16;
     constexpr uint32_t hd = 4 * L;
     extern __shared__ __attribute__((aligned(16))) uint8_t flds[];
     float *s = (float *)flds;
     float *accs = s + kAttnSlots;
-    float *red = accs + kFuseThreads * 4;
-    float *att = red + 2 * kFuseWaves;
+    float *red = accs + kStepThreads * 4;
+    float *att = red + 2 * kStepWaves;
     uint8_t *recs2 = (uint8_t *)(att + hd);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int lane = threadIdx.x % 64, r = lane % 32;
@@ -786,10 +786,10 @@ __global__ __launch_bounds__(kFuseThreads) void attn_out_kernel(FusedArgs a) {
     Batch<KIND> s2[K2];
 #pragma unroll
     for (int i = 0; i < K2; i++)
-        if (wave + i * kFuseWaves < a.d / 32) load_task2<KIND, PAIRS>(s2[i], a, wave + i * kFuseWaves, oq, os);
+        if (wave + i * kStepWaves < a.d / 32) load_task2<KIND, PAIRS>(s2[i], a, wave + i * kStepWaves, oq, os);
     const uint32_t p = (uint32_t)a.state[0];
     const size_t off = (size_t)blockIdx.x * hd;
-    fused_attend<L>(a.q + off, a.kc + (size_t)p * a.d + off, a.vc + (size_t)p * a.d + off, a.kc, a.vc, p + 1, a.d,
+    attend_head<L>(a.q + off, a.kc + (size_t)p * a.d + off, a.vc + (size_t)p * a.d + off, a.kc, a.vc, p + 1, a.d,
                     a.scale, s, accs, red, att);
     __syncthreads();
     prep_lds<KIND>(att, hd, recs2);
@@ -800,10 +800,10 @@ __global__ __launch_bounds__(kFuseThreads) void attn_out_kernel(FusedArgs a) {
 // After the last layer: x = x_in + (sum_j part[j] + b) and its final LayerNorm into global
 // prepared records (the head's x); one workgroup.
 template <int KIND>
-__global__ __launch_bounds__(kFuseThreads) void fused_final_kernel(FusedArgs a, uint8_t *__restrict__ out) {
-    __shared__ float red[kFuseWaves];
+__global__ __launch_bounds__(kStepThreads) void final_ln_kernel(StepArgs a, uint8_t *__restrict__ out) {
+    __shared__ float red[kStepWaves];
     f32x4 v[kLnSlots];
-    fused_residual<KIND>(a, v);
+    residual_row<KIND>(a, v);
     ln_records<KIND, true>(v, a.ln_g, a.ln_b, a.eps, a.nb, (a.nb + 7) / 8 * 8, out, red);
 }
 
@@ -1037,12 +1037,12 @@ bool four_fits(size_t d, size_t heads) {
 }
 
 template <int KIND>
-hipError_t launch_attn_out(hipStream_t s, uint32_t hd, uint32_t heads, const FusedArgs &a) {
+hipError_t launch_attn_out(hipStream_t s, uint32_t hd, uint32_t heads, const StepArgs &a) {
     const size_t lds = attn_out_lds(hd);
     switch (hd) {
-    case 64: attn_out_kernel<KIND, 16, attn_k2<16>()><<<heads, kFuseThreads, lds, s>>>(a); break;
-    case 128: attn_out_kernel<KIND, 32, attn_k2<32>()><<<heads, kFuseThreads, lds, s>>>(a); break;
-    default: attn_out_kernel<KIND, 64, attn_k2<64>()><<<heads, kFuseThreads, lds, s>>>(a); break;
+    case 64: attn_out_kernel<KIND, 16, attn_k2<16>()><<<heads, kStepThreads, lds, s>>>(a); break;
+    case 128: attn_out_kernel<KIND, 32, attn_k2<32>()><<<heads, kStepThreads, lds, s>>>(a); break;
+    default: attn_out_kernel<KIND, 64, attn_k2<64>()><<<heads, kStepThreads, lds, s>>>(a); break;
     }
     return hipGetLastError();
 }
@@ -1051,7 +1051,7 @@ hipError_t launch_attn_out(hipStream_t s, uint32_t hd, uint32_t heads, const Fus
 // greedy pick.
 hipError_t enqueue_head(fh_gpt2 *m, hipStream_t s, const float *x_in, const float *part, uint32_t nparts,
                         const float *b) {
-    FusedArgs z{};
+    StepArgs z{};
     z.x_in = x_in;
     z.part = part;
     z.pbias = b;
@@ -1064,9 +1064,9 @@ hipError_t enqueue_head(fh_gpt2 *m, hipStream_t s, const float *x_in, const floa
     z.d = (uint32_t)m->dim;
     z.nb = (uint32_t)(m->dim / 32);
     if (m->kind == FH_Q8_0)
-        fused_final_kernel<FH_Q8_0><<<1, kFuseThreads, 0, s>>>(z, m->prep);
+        final_ln_kernel<FH_Q8_0><<<1, kStepThreads, 0, s>>>(z, m->prep);
     else
-        fused_final_kernel<FH_Q4_0><<<1, kFuseThreads, 0, s>>>(z, m->prep);
+        final_ln_kernel<FH_Q4_0><<<1, kStepThreads, 0, s>>>(z, m->prep);
     hipError_t e = hipGetLastError();
     if (e) return e;
     DecodeGemv a = dg(m, m->head, m->x, m->logits);
@@ -1108,7 +1108,7 @@ hipError_t enqueue_four(fh_gpt2 *m, hipStream_t s) {
         a.vc = L.vc;
         a.split = d;
         if ((e = dgemv<PRO_LNR, EPI_QKV>(s, m->kind, a))) return e;
-        FusedArgs t{};
+        StepArgs t{};
         t.q = m->q;
         t.kc = L.kc;
         t.vc = L.vc;

@@ -63,7 +63,7 @@ def rel(got, want) -> float:
 @pytest.mark.parametrize("form", [4])
 @pytest.mark.parametrize("kind", [gm.Q8_0, gm.Q4_0])
 @pytest.mark.parametrize("name", list(CFGS))
-def test_fused_step_feeds_the_whole_context_like_the_oracle(g, orc, name, kind, form):
+def test_four_launch_step_feeds_the_whole_context_like_the_oracle(g, orc, name, kind, form):
     cfg = CFGS[name]
     m = gm.gpt2_init(cfg, 3)
     if name == "hd64":
@@ -83,7 +83,7 @@ def test_fused_step_feeds_the_whole_context_like_the_oracle(g, orc, name, kind, 
         other = five.feed(t)
         first.append(got)
         e, e5, eo = rel(got, want), rel(got, other), rel(other, want)
-        say(f"pos {i}: fused vs cpu {e:.2e}, fused vs five-launch {e5:.2e}, five-launch vs cpu {eo:.2e}")
+        say(f"pos {i}: four-launch vs cpu {e:.2e}, four-launch vs five-launch {e5:.2e}, five-launch vs cpu {eo:.2e}")
         worst, worst5 = max(worst, e), max(worst5, e5)
     say(f"{name} kind {kind}: {cfg['ctx']} positions, max rel err {worst:.2e} (vs five-launch step {worst5:.2e})")
     assert worst < FORWARD and worst5 < FORWARD
@@ -99,7 +99,7 @@ def test_fused_step_feeds_the_whole_context_like_the_oracle(g, orc, name, kind, 
 
 
 @pytest.mark.parametrize("form", [4])
-def test_fused_greedy_generation_matches_the_oracle(g, orc, form):
+def test_four_launch_greedy_generation_matches_the_oracle(g, orc, form):
     cfg = dict(CFGS["hd64"], ctx=128)
     m = gm.gpt2_init(cfg, 6)
     data = gm.to_gguf(m, gm.Q8_0)
@@ -114,10 +114,10 @@ def test_fused_greedy_generation_matches_the_oracle(g, orc, form):
 
 @pytest.mark.parametrize("form", [4])
 @pytest.mark.parametrize("kind", [gm.Q8_0, gm.Q4_0])
-def test_fused_step_on_raw_random_weights_is_no_further_from_the_oracle(g, orc, kind, form):
+def test_four_launch_step_on_raw_random_weights_is_no_further_from_the_oracle(g, orc, kind, form):
     """Gpt2::random's raw weights (uniform +-0.5) amplify every rounding along the context, so the
-    five-launch step itself leaves the CPU by about 1e-5 there: the fused step, which adds the
-    same products in another order, must stay as close (within twice the five-launch step's
+    five-launch step itself leaves the CPU by about 1e-5 there: the four-launch step, which adds
+    the same products in another order, must stay as close (within twice the five-launch step's
     distance, and 2e-5)."""
     cfg = CFGS["hd64"]
     m = gm.gpt2_random(cfg, 3)
@@ -129,9 +129,9 @@ def test_fused_step_on_raw_random_weights_is_no_further_from_the_oracle(g, orc, 
     for i, t in enumerate(ids):
         want = cpu.feed(t)
         e, eo = rel(dev.feed(t), want), rel(five.feed(t), want)
-        say(f"pos {i}: fused vs cpu {e:.2e}, five-launch vs cpu {eo:.2e}")
+        say(f"pos {i}: four-launch vs cpu {e:.2e}, five-launch vs cpu {eo:.2e}")
         worst, worst_five = max(worst, e), max(worst_five, eo)
-    say(f"kind {kind}: fused {worst:.2e}, five-launch {worst_five:.2e}")
+    say(f"kind {kind}: four-launch {worst:.2e}, five-launch {worst_five:.2e}")
     assert worst <= max(2 * worst_five, FORWARD) and worst < 2 * FORWARD
     dev.free()
     five.free()
