@@ -285,26 +285,45 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
                     bf[j][1] = __builtin_bit_cast(f16x8, b1);
                     dv[j] = half_to_float(ld.d[j][kb / 2] >> (16 * (kb % 2)));
                 }
-#pragma unroll
-                for (int i = 0; i < MT; i++) {
-                    // A fragments: x row i 32 + r (rows past the row capacity are zero)
-                    const int xr_row = i * 32 + r;
-                    const _Float16 *row = (R >= 32 || xr_row < R) ? &sx[buf][(kb * R + xr_row) * kXRec] : zrow;
+                if constexpr (R == 8) {
+                    // Up to 8 rows: A rows 0..7 are x's hi parts and rows 8..15 its lo parts (rows
+                    // 16..31 zero), so one MFMA per k step covers both parts: C rows 4h + q (hi) and
+                    // 8 + 4h + q (lo) of lane (column, h) are the two parts of x row 4h + q, added
+                    // before the block's scale. Two MFMAs per block instead of four.
+                    const _Float16 *row = r < 16 ? &sx[buf][(kb * R + r % 8) * kXRec] + (r < 8 ? 0 : 32) : zrow;
                     const f16x8 a0 = *(const f16x8 *)(row + 8 * h);
                     const f16x8 a1 = *(const f16x8 *)(row + 16 + 8 * h);
-                    const f16x8 l0 = *(const f16x8 *)(row + 32 + 8 * h);
-                    const f16x8 l1 = *(const f16x8 *)(row + 48 + 8 * h);
 #pragma unroll
                     for (int j = 0; j < kTW; j++) {
                         f32x16 pp = {};
                         pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf[j][0], pp, 0, 0, 0);
                         pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf[j][1], pp, 0, 0, 0);
-                        pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(l0, bf[j][0], pp, 0, 0, 0);
-                        pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(l1, bf[j][1], pp, 0, 0, 0);
 #pragma unroll
-                        for (int g = 0; g < (i == 0 ? G0 : 4); g++)
+                        for (int q = 0; q < 4; q++) acc[0][j][0][q] = fmaf(dv[j], pp[q] + pp[4 + q], acc[0][j][0][q]);
+                    }
+                } else {
 #pragma unroll
-                            for (int q = 0; q < 4; q++) acc[i][j][g][q] = fmaf(dv[j], pp[4 * g + q], acc[i][j][g][q]);
+                    for (int i = 0; i < MT; i++) {
+                        // A fragments: x row i 32 + r (rows past the row capacity are zero)
+                        const int xr_row = i * 32 + r;
+                        const _Float16 *row = (R >= 32 || xr_row < R) ? &sx[buf][(kb * R + xr_row) * kXRec] : zrow;
+                        const f16x8 a0 = *(const f16x8 *)(row + 8 * h);
+                        const f16x8 a1 = *(const f16x8 *)(row + 16 + 8 * h);
+                        const f16x8 l0 = *(const f16x8 *)(row + 32 + 8 * h);
+                        const f16x8 l1 = *(const f16x8 *)(row + 48 + 8 * h);
+#pragma unroll
+                        for (int j = 0; j < kTW; j++) {
+                            f32x16 pp = {};
+                            pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf[j][0], pp, 0, 0, 0);
+                            pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf[j][1], pp, 0, 0, 0);
+                            pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(l0, bf[j][0], pp, 0, 0, 0);
+                            pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(l1, bf[j][1], pp, 0, 0, 0);
+#pragma unroll
+                            for (int g = 0; g < (i == 0 ? G0 : 4); g++)
+#pragma unroll
+                                for (int q = 0; q < 4; q++)
+                                    acc[i][j][g][q] = fmaf(dv[j], pp[4 * g + q], acc[i][j][g][q]);
+                        }
                     }
                 }
                 // one block at a time: the scale FMAs are not sunk past the next block's MFMAs
