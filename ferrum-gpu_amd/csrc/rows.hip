@@ -285,12 +285,13 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
                     bf[j][1] = __builtin_bit_cast(f16x8, b1);
                     dv[j] = half_to_float(ld.d[j][kb / 2] >> (16 * (kb % 2)));
                 }
-                if constexpr (R == 8) {
-                    // Up to 8 rows: A rows 0..7 are x's hi parts and rows 8..15 its lo parts (rows
-                    // 16..31 zero), so one MFMA per k step covers both parts: C rows 4h + q (hi) and
-                    // 8 + 4h + q (lo) of lane (column, h) are the two parts of x row 4h + q, added
-                    // before the block's scale. Two MFMAs per block instead of four.
-                    const _Float16 *row = r < 16 ? &sx[buf][(kb * R + r % 8) * kXRec] + (r < 8 ? 0 : 32) : zrow;
+                if constexpr (R <= 16) {
+                    // Up to 16 rows: A rows 0..R-1 are x's hi parts and rows R..2R-1 its lo parts
+                    // (rows past 2R zero), so one MFMA per k step covers both parts: C register
+                    // 4g + q of lane (column, h) is hi of x row 8g + 4h + q and register
+                    // 4g + q + R / 2 its lo, added before the block's scale. Two MFMAs per block
+                    // instead of four.
+                    const _Float16 *row = r < 2 * R ? &sx[buf][(kb * R + r % R) * kXRec] + (r < R ? 0 : 32) : zrow;
                     const f16x8 a0 = *(const f16x8 *)(row + 8 * h);
                     const f16x8 a1 = *(const f16x8 *)(row + 16 + 8 * h);
 #pragma unroll
@@ -299,7 +300,10 @@ __global__ __launch_bounds__(256, 2) void rows_kernel(const RowsDesc *__restrict
                         pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf[j][0], pp, 0, 0, 0);
                         pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf[j][1], pp, 0, 0, 0);
 #pragma unroll
-                        for (int q = 0; q < 4; q++) acc[0][j][0][q] = fmaf(dv[j], pp[q] + pp[4 + q], acc[0][j][0][q]);
+                        for (int g = 0; g < G0; g++)
+#pragma unroll
+                            for (int q = 0; q < 4; q++)
+                                acc[0][j][g][q] = fmaf(dv[j], pp[4 * g + q] + pp[4 * g + q + R / 2], acc[0][j][g][q]);
                     }
                 } else {
 #pragma unroll

@@ -63,7 +63,8 @@ def cpu(orc, kind, b, x, m, k, n):
 @pytest.mark.parametrize("kind_name", ["Q8_0", "Q4_0"])
 def test_rows_kernel_matches_the_cpu_on_awkward_shapes(fh, g, orc, kind_name):
     """ops/quant/tests.rs:134-157, 272-304 (uniform weights and x, as the reference's product tests
-    draw them) at row counts across the tile shapes (1 .. 32 one x tile, 33 .. 64 two), widths
+    draw them) at row counts across the tile shapes (1 .. 8 and 9 .. 16 stacking x's two parts in
+    one MFMA, 17 .. 32 one x tile, 33 .. 64 two), widths
     whose block count is not a multiple of the four-block batch, outputs that are not whole tiles
     or tasks. Beyond k = 512 (the reference's widest shape under its 1e-5) and on the reference's
     awkward codec weights (blocks scaled by 1e-6, 0, 1e4, small integers) the CPU's own f32 sums
@@ -79,7 +80,7 @@ def test_rows_kernel_matches_the_cpu_on_awkward_shapes(fh, g, orc, kind_name):
             b = orc.quantise_matrix(int(kind), w, k, n)
             wd = orc.dequantised_in_out(int(kind), b, k, n)
             qw = fh.upload_qweight(g, kind, b, k, n)
-            for m in (1, 2, 3, 8, 17, 32, 33, 64):
+            for m in (1, 2, 3, 8, 12, 16, 17, 32, 33, 64):
                 x = orc.rand_vec(m * k, 100 + m)
                 want = cpu(orc, kind, b, x, m, k, n)
                 gx, gy = g.upload(x), g.zeros(m * n)
@@ -114,19 +115,19 @@ def test_rows_identity_reads_back_the_dequantised_weights(fh, g, orc, kind_name)
 
 
 @pytest.mark.parametrize("kind_name", ["Q8_0", "Q4_0"])
-def test_rows8_identity_rows_read_back_every_k_position(fh, g, orc, kind_name):
-    """Products of at most 8 rows (one launch of row capacity 8): x = 8 (and 3) rows of the
-    identity pick weight rows, compared with f32 == (every k position of a block is hit once over
-    the four sweeps, so a misplaced element, a swapped x part or a wrong scale shows); widths past
-    64 blocks run the two K halves."""
+def test_rows16_identity_rows_read_back_every_k_position(fh, g, orc, kind_name):
+    """Products of at most 16 rows (row capacities 8 and 16, which stack x's two parts in one
+    MFMA): x = 16, 11, 8 or 3 rows of the identity pick weight rows, compared with f32 == (every k
+    position of a block is hit over the four sweeps, so a misplaced element, a swapped x part or a
+    wrong scale shows); widths past 64 blocks run the two K halves."""
     kind = fh.QKind[kind_name]
     for k, n in [(256, 40), (2304, 96)]:
         b = orc.quantise_matrix(int(kind), nasty(orc, k * n), k, n)
         want = orc.dequantised_in_out(int(kind), b, k, n).reshape(k, n)
         qw = fh.upload_qweight(g, kind, b, k, n)
         for sweep in range(4):
-            ks = [(8 * sweep + i) % 32 + 32 * ((5 * i + sweep) % (k // 32)) for i in range(8)]
-            for m in (8, 3):
+            ks = [(8 * sweep + i) % 32 + 32 * ((5 * i + sweep) % (k // 32)) for i in range(16)]
+            for m in (8, 3, 16, 11):
                 x = np.zeros((m, k), dtype=np.float32)
                 for r in range(m):
                     x[r, ks[r]] = 1.0
@@ -211,9 +212,9 @@ def test_rows_kernel_keeps_the_neighbours_of_outliers(fh, g, orc):
 def test_rows_plan_gives_each_product_its_single_launch_bits(fh, g, orc):
     """One plan over products of both formats, mixed row counts (one and two x tiles in one launch)
     and ragged shapes; every product equals its single QPath.Rows launch bit for bit where that
-    launch has the plan's row capacity class (more than 8 rows), and within 1e-5 of it where the
-    single launch has at most 8 rows (that capacity stacks x's hi and lo parts in one MFMA and adds
-    them before the scale, another rounding order)."""
+    launch has the plan's row capacity class (more than 16 rows), and within 1e-5 of it where the
+    single launch has at most 16 rows (those capacities stack x's hi and lo parts in one MFMA and
+    add them before the scale, another rounding order)."""
     rng = np.random.default_rng(11)
     probs, keep, checks = [], [], []
     for i, (kind, m, k, n) in enumerate([(fh.QKind.Q4_0, 8, 2048, 2560), (fh.QKind.Q4_0, 40, 896, 300),
@@ -227,7 +228,7 @@ def test_rows_plan_gives_each_product_its_single_launch_bits(fh, g, orc):
         fh.linear_q_with(g, gx, qw, gs, m, fh.QPath.Rows)
         keep += [qw, gx, gy, gs]
         probs.append((qw, gx.device_ptr(), gy.device_ptr(), m))
-        checks.append((gy, gs, cpu(orc, kind, b, x, m, k, n), m > 8))
+        checks.append((gy, gs, cpu(orc, kind, b, x, m, k, n), m > 16))
     plan = fh.RowsPlan(g, probs)
     assert plan.launches() == 2
     for rep in range(2):
