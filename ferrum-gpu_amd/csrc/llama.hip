@@ -561,9 +561,31 @@ __global__ __launch_bounds__(64 * W) void attention_kernel(const float *__restri
 // two such values is hi hi + hi lo + lo hi up to 2^-22 of its size (the lo lo term dropped), so
 // each f32-accurate 32 x 32 x 16 product costs three v_mfma_f32_32x32x16_f16 instead of eight
 // v_mfma_f32_32x32x2_f32 of twice the length. Layouts (tp = t rounded up to 32, rows t .. tp - 1
-// zero with exponent -127): q' [tp, heads HD] and k' [tp, kv_heads HD] row-major, v' transposed
-// per kv head [kv_heads HD, tp] (keys contiguous), exponents [slot, tp] as bytes.
+// zero with exponent -127): q' [tp, heads HD] row-major; k' and v' in the attention kernel's
+// fragment order, per kv head and 32-key tile one 32 HD block, in which every 64-lane load
+// instruction of the kernel reads 1 KB contiguous (a row-major k' spread each such load over 32
+// key rows): k' [s = dim / 16][lane][8], the lane being the A-matrix row that holds the key
+// (key_row) plus 32 for dims 8..15 of the 16; v' [b = dim / 32][u = key / 16 % 2][lane][8], lane
+// = dim % 32 + 32 (key / 8 % 2), the 8 being keys; exponents [slot, tp] as bytes.
 constexpr int kSplitPad = -127;
+
+// The A-matrix row of S^T that holds key r of a 32-key tile: row rho = 16 u + w holds key 16 u +
+// 8 ((w % 8) / 4) + 4 (w / 8) + w % 4, so that accumulator register i of lane half h holds key
+// 16 (i / 8) + 8 h + i % 8; the map swaps bits 2 and 3 of the key's index within its 16.
+__device__ __forceinline__ uint32_t key_row(uint32_t r) { return (r & 19u) | ((r & 4u) << 1) | ((r & 8u) >> 1); }
+
+// Offsets (in halves) of the fragment-order k' and v' element (key, dim) of kv head g.
+template <int HD>
+__device__ __forceinline__ size_t frag_k(uint32_t g, uint32_t key, uint32_t dim, uint32_t tp) {
+    const uint32_t lane = key_row(key % 32) + 32 * ((dim % 16) / 8);
+    return ((size_t)g * (tp / 32) + key / 32) * (32 * HD) + (dim / 16) * 512 + lane * 8 + dim % 8;
+}
+template <int HD>
+__device__ __forceinline__ size_t frag_v(uint32_t g, uint32_t key, uint32_t dim, uint32_t tp) {
+    const uint32_t lane = dim % 32 + 32 * ((key % 16) / 8);
+    return ((size_t)g * (tp / 32) + key / 32) * (32 * HD) + ((dim / 32) * 2 + (key % 32) / 16) * 512 + lane * 8 +
+           key % 8;
+}
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict__ qkv, _Float16 *__restrict__ qh,
@@ -574,7 +596,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
                                                          uint32_t tp, uint32_t width, uint32_t heads,
                                                          uint32_t kv_heads) {
     const uint32_t row = blockIdx.x, lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-    const uint32_t qd = heads * HD, kvd = kv_heads * HD;
+    const uint32_t qd = heads * HD;
     for (uint32_t slot = wave; slot < heads + 2 * kv_heads; slot += 4) {
         float v[2];
 #pragma unroll
@@ -603,11 +625,11 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
                 qh[o] = hi;
                 ql[o] = lo;
             } else if (slot < heads + kv_heads) {
-                const size_t o = (size_t)row * kvd + (slot - heads) * HD + d;
+                const size_t o = frag_k<HD>(slot - heads, row, d, tp);
                 kh[o] = hi;
                 kl[o] = lo;
             } else {
-                const size_t o = ((size_t)(slot - heads - kv_heads) * HD + d) * tp + row;
+                const size_t o = frag_v<HD>(slot - heads - kv_heads, row, d, tp);
                 vh[o] = hi;
                 vl[o] = lo;
             }
@@ -644,29 +666,28 @@ template <int HD>
 __device__ __forceinline__ void split_load_v(SplitV<HD> &T, const _Float16 *__restrict__ vh,
                                              const _Float16 *__restrict__ vl, uint32_t k0, uint32_t tp, uint32_t g,
                                              uint32_t col, uint32_t hf) {
+    const size_t vo = frag_v<HD>(g, k0 + 8 * hf, col, tp);  // (b, u) = (0, 0); each further one 512 on
 #pragma unroll
     for (int b = 0; b < HD / 32; b++)
 #pragma unroll
         for (int u = 0; u < 2; u++) {
-            const size_t vo = (size_t)(g * HD + 32 * b + col) * tp + k0 + 16 * u + 8 * hf;
-            T.vh[b][u] = *(const f16x8 *)(vh + vo);
-            T.vl[b][u] = *(const f16x8 *)(vl + vo);
+            T.vh[b][u] = *(const f16x8 *)(vh + vo + (2 * b + u) * 512);
+            T.vl[b][u] = *(const f16x8 *)(vl + vo + (2 * b + u) * 512);
         }
 }
 
 template <int HD>
 __device__ __forceinline__ void split_load(SplitTile<HD> &T, const _Float16 *__restrict__ kh,
                                            const _Float16 *__restrict__ kl, const int8_t *__restrict__ ek,
-                                           const int8_t *__restrict__ ev, uint32_t k0, uint32_t tp, uint32_t kvd,
-                                           uint32_t g, uint32_t col, uint32_t hf) {
-    // A row rho of S^T holds key pi(rho) = 16 u + 8 ((w % 8) / 4) + 4 (w / 8) + w % 4 (rho = 16 u + w),
-    // so that register r of lane half h holds key 16 (r / 8) + 8 h + r % 8
-    const uint32_t w = col % 16, key = k0 + 16 * (col / 16) + 8 * ((w % 8) / 4) + 4 * (w / 8) + w % 4;
-    const size_t ko = (size_t)key * kvd + g * HD + 8 * hf;
+                                           const int8_t *__restrict__ ev, uint32_t k0, uint32_t tp, uint32_t g,
+                                           uint32_t col, uint32_t hf) {
+    // lane (col, hf) holds A row col of S^T, the tile's key key_row(col) (key_row is its own
+    // inverse), dims 16 s + 8 hf + 0..7
+    const size_t ko = frag_k<HD>(g, k0 + key_row(col), 8 * hf, tp);  // s = 0; each further one 512 on
 #pragma unroll
     for (int s = 0; s < SplitTile<HD>::KS; s++) {
-        T.kh[s] = *(const f16x8 *)(kh + ko + 16 * s);
-        T.kl[s] = *(const f16x8 *)(kl + ko + 16 * s);
+        T.kh[s] = *(const f16x8 *)(kh + ko + 512 * s);
+        T.kl[s] = *(const f16x8 *)(kl + ko + 512 * s);
     }
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -695,8 +716,8 @@ __global__ __launch_bounds__(64 * W) void attention_split_kernel(
     // grid (heads, query blocks): workgroups are dispatched x fastest, so every head's longest
     // query blocks start first and the short ones fill in at the end
     const uint32_t q0 = (gridDim.y - 1 - blockIdx.y) * 32;
-    const uint32_t h = blockIdx.x, g = h / group, kv_heads = heads / group;
-    const uint32_t qd = heads * HD, kvd = kv_heads * HD;
+    const uint32_t h = blockIdx.x, g = h / group;
+    const uint32_t qd = heads * HD;
     const uint32_t query = q0 + col;
     f16x8 qfh[KS], qfl[KS];
     {
@@ -716,12 +737,12 @@ __global__ __launch_bounds__(64 * W) void attention_split_kernel(
     float mrun = -INFINITY, lrun = 0.0f;
     const uint32_t tiles = (min(q0 + 31u, t - 1u)) / 32 + 1;  // key tiles any valid query of the block sees
     T cur, nxt;
-    if (w < tiles) split_load<HD>(cur, kh, kl, ek, ev, 32 * w, tp, kvd, g, col, hf);
+    if (w < tiles) split_load<HD>(cur, kh, kl, ek, ev, 32 * w, tp, g, col, hf);
     for (uint32_t kt = w; kt < tiles; kt += W) {
         const uint32_t k0 = 32 * kt;
         SplitV<HD> vt;  // the tile's values, needed after the softmax
         split_load_v<HD>(vt, vh, vl, k0, tp, g, col, hf);
-        if (kt + W < tiles) split_load<HD>(nxt, kh, kl, ek, ev, k0 + 32 * W, tp, kvd, g, col, hf);
+        if (kt + W < tiles) split_load<HD>(nxt, kh, kl, ek, ev, k0 + 32 * W, tp, g, col, hf);
         f32x16 s;
 #pragma unroll
         for (int i = 0; i < 16; i++) s[i] = 0.0f;

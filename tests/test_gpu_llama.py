@@ -243,6 +243,28 @@ def test_qwen2_0_5b_scoring_matches_the_oracle(fh, g, orc, qwen, path):
     assert lp_err(lp512[:128], wlp) < bound and lp_err(lp2048[:512], lp512) < bound
 
 
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+def test_split_attention_head_dims_match_the_oracle(fh, g, orc, head_dim):
+    """Head dims 32, 64 and 128 take the f16-split attention (q, k, v on a power-of-two scale in
+    two f16 parts, k and v stored in the kernel's fragment order); grouped kv heads, sequence
+    lengths that leave some wavefronts without a key tile (1, 33) and span several query blocks
+    and key tiles with a ragged last one (97). Logits against the oracle within SCORE (1e-4
+    relative to max(|w|, 1)), not FORWARD: at these widths (dim 128 to 512, logits up to 26) the
+    f32 oracle is itself 1.2e-5 to 4.3e-5 from an f64 evaluation of the same model (measured), so
+    1e-5 would test the oracle's rounding. A misplaced fragment element gives O(1) errors and an
+    f16-only operand (the lo part lost) errors of the order of f16 rounding, 2^-11 = 4.9e-4."""
+    c = lm.config(vocab=300, ctx=128, dim=4 * head_dim, heads=4, kv_heads=2, head_dim=head_dim, layers=2,
+                  hidden=256, rope_base=10000.0, neox=True, eps=1e-5)
+    data = lm.to_gguf(lm.llama_random(c, 17, True, False), lm.Q8_0)
+    ref = lm.from_gguf(data)
+    dev = load(fh, g, data)
+    ids = [int(t) for t in np.random.default_rng(head_dim).integers(0, 300, 97)]
+    for t in (1, 33, 97):
+        e = rel(dev.forward_all(ids[:t]), orc.llama_forward(ref, ids[:t]))
+        say(f"head_dim {head_dim} t={t}: {e:.2e}")
+        assert e < SCORE, (head_dim, t, e)
+
+
 @pytest.mark.parametrize("kind", [lm.Q8_0, lm.Q4_0])
 def test_fast_path_with_narrow_attention_and_ffn(fh, g, orc, kind):
     """heads * key_length and the FFN width both below dim (ferrum_model/src/gguf/llama/mod.rs:133
