@@ -42,6 +42,7 @@ struct fh_llama {
     size_t vocab = 0, ctx = 0, dim = 0, heads = 0, kv_heads = 0, head_dim = 0, layers = 0, hidden = 0, rope_dim = 0;
     float rope_base = 10000.0f, eps = 1e-5f, linear_factor = 1.0f;
     bool neox = false, tied = false;
+    bool fuse_rope = true;  // qkv_rope_split_kernel where it fits (FERRUM_HIP_ROPE_UNFUSED=1 at load: never)
     fh_kind kind = (fh_kind)0;
     fh_path path = FH_PATH_TILED;
     // A weight matrix of k inputs and n outputs: packed (q), or the f32 rows (f: n rows of k
@@ -369,17 +370,15 @@ __global__ __launch_bounds__(256) void swiglu_split_kernel(const float *__restri
                          dst.xsc, red);
 }
 
-// q/k/v bias and RoPE in place on one row of qkv (ferrum_ref/src/models/llama/ops.rs:105-127):
-// the row's q and k heads rotate their first rope_dim channels by table row `row` (the position),
-// NORM pairing (2i, 2i + 1) or NEOX (i, i + rope_dim / 2). The row is staged in LDS so every
-// output reads the biased inputs.
-__global__ __launch_bounds__(256) void qkv_rope_kernel(const float *__restrict__ src, uint32_t src_splits,
-                                                       size_t src_stride, float *__restrict__ qkv,
-                                                       const float *__restrict__ bias, const float *__restrict__ cos_t,
-                                                       const float *__restrict__ sin_t, uint32_t width,
-                                                       uint32_t rot_heads, uint32_t hd, uint32_t rope_dim, int neox) {
-    extern __shared__ __attribute__((aligned(16))) float row[];
-    const size_t base = (size_t)blockIdx.x * width;
+// q/k/v bias and RoPE on one row of qkv (ferrum_ref/src/models/llama/ops.rs:105-127): the row's
+// q and k heads rotate their first rope_dim channels by table row `row` (the position), NORM
+// pairing (2i, 2i + 1) or NEOX (i, i + rope_dim / 2). The row is staged in LDS so every output
+// reads the biased inputs. qkv_rope_row loads row `r` (its K-split partial sums and the bias)
+// into LDS; rope_value is channel c of the rotated row.
+__device__ __forceinline__ void qkv_rope_row(const float *__restrict__ src, uint32_t src_splits, size_t src_stride,
+                                             const float *__restrict__ bias, uint32_t width, uint32_t r,
+                                             float *row) {
+    const size_t base = (size_t)r * width;
     if (width % 4 == 0) {  // four elements a thread, the splits' loads issued together
         for (uint32_t q = threadIdx.x; q < width / 4; q += 256) {
             const f32x4 v = split_chunk(src, base + 4 * q, src_splits, src_stride);
@@ -391,23 +390,36 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(const float *__restrict__
             row[c] = bias ? v + bias[c] : v;
         }
     }
-    __syncthreads();
-    const uint32_t half = rope_dim / 2, rotated = rot_heads * hd;
-    const float *cr = cos_t + (size_t)blockIdx.x * half, *sr = sin_t + (size_t)blockIdx.x * half;
-    for (uint32_t c = threadIdx.x; c < width; c += 256) {
-        float v = row[c];
-        if (c < rotated) {
-            const uint32_t j = c % hd, off = c - j;
-            if (j < rope_dim) {
-                const bool first = neox ? j < half : (j & 1u) == 0;
-                const uint32_t i = neox ? (first ? j : j - half) : j / 2;
-                const uint32_t ia = neox ? off + i : off + 2 * i, ib = neox ? ia + half : ia + 1;
-                const float a = row[ia], b = row[ib], cs = cr[i], sn = sr[i];
-                v = first ? __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn)) : __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs));
-            }
+}
+
+__device__ __forceinline__ float rope_value(const float *row, uint32_t c, const float *cr, const float *sr,
+                                            uint32_t rotated, uint32_t hd, uint32_t rope_dim, int neox) {
+    float v = row[c];
+    if (c < rotated) {
+        const uint32_t j = c % hd, off = c - j, half = rope_dim / 2;
+        if (j < rope_dim) {
+            const bool first = neox ? j < half : (j & 1u) == 0;
+            const uint32_t i = neox ? (first ? j : j - half) : j / 2;
+            const uint32_t ia = neox ? off + i : off + 2 * i, ib = neox ? ia + half : ia + 1;
+            const float a = row[ia], b = row[ib], cs = cr[i], sn = sr[i];
+            v = first ? __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn)) : __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs));
         }
-        qkv[base + c] = v;
     }
+    return v;
+}
+
+__global__ __launch_bounds__(256) void qkv_rope_kernel(const float *__restrict__ src, uint32_t src_splits,
+                                                       size_t src_stride, float *__restrict__ qkv,
+                                                       const float *__restrict__ bias, const float *__restrict__ cos_t,
+                                                       const float *__restrict__ sin_t, uint32_t width,
+                                                       uint32_t rot_heads, uint32_t hd, uint32_t rope_dim, int neox) {
+    extern __shared__ __attribute__((aligned(16))) float row[];
+    qkv_rope_row(src, src_splits, src_stride, bias, width, blockIdx.x, row);
+    __syncthreads();
+    const uint32_t half = rope_dim / 2;
+    const float *cr = cos_t + (size_t)blockIdx.x * half, *sr = sin_t + (size_t)blockIdx.x * half;
+    for (uint32_t c = threadIdx.x; c < width; c += 256)
+        qkv[(size_t)blockIdx.x * width + c] = rope_value(row, c, cr, sr, rot_heads * hd, hd, rope_dim, neox);
 }
 
 // Causal grouped-query attention (ferrum_ref/src/models/llama/ops.rs:131-162 for every row) from
@@ -587,26 +599,29 @@ __device__ __forceinline__ size_t frag_v(uint32_t g, uint32_t key, uint32_t dim,
            key % 8;
 }
 
-template <int HD>
-__global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict__ qkv, _Float16 *__restrict__ qh,
-                                                         _Float16 *__restrict__ ql, _Float16 *__restrict__ kh,
-                                                         _Float16 *__restrict__ kl, _Float16 *__restrict__ vh,
-                                                         _Float16 *__restrict__ vl, int8_t *__restrict__ eq,
-                                                         int8_t *__restrict__ ek, int8_t *__restrict__ ev, uint32_t t,
-                                                         uint32_t tp, uint32_t width, uint32_t heads,
-                                                         uint32_t kv_heads) {
-    const uint32_t row = blockIdx.x, lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+// Where the split operands go (layouts above).
+struct SplitDst {
+    _Float16 *qh, *ql, *kh, *kl, *vh, *vl;
+    int8_t *eq, *ek, *ev;
+};
+
+// Row `row` of every q, k and v head into its split form, one head per wavefront at a time;
+// get(slot, d) is element d of head slot (q heads, then k heads, then v heads) of the row.
+template <int HD, class Get>
+__device__ __forceinline__ void split_heads(Get get, const SplitDst &o, uint32_t row, uint32_t t, uint32_t tp,
+                                            uint32_t heads, uint32_t kv_heads) {
+    const uint32_t lane = threadIdx.x % 64, wave = threadIdx.x / 64;
     const uint32_t qd = heads * HD;
     for (uint32_t slot = wave; slot < heads + 2 * kv_heads; slot += 4) {
         float v[2];
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const uint32_t d = lane + 64 * i;
-            v[i] = row < t && d < (uint32_t)HD ? qkv[(size_t)row * width + slot * HD + d] : 0.0f;
+            v[i] = row < t && d < (uint32_t)HD ? get(slot, d) : 0.0f;
         }
         float mx = fmaxf(fabsf(v[0]), fabsf(v[1]));
 #pragma unroll
-        for (int o = 32; o >= 1; o /= 2) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        for (int s = 32; s >= 1; s /= 2) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
         // 2^E <= mx < 2^(E+1), e = E - 14; zero rows, padding rows and non-finite rows keep e = 0
         // (non-finite values then stay non-finite) and padding rows report -127
         int e = 0;
@@ -621,28 +636,65 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
             const float x = v[i] * f;
             const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
             if (slot < heads) {
-                const size_t o = (size_t)row * qd + slot * HD + d;
-                qh[o] = hi;
-                ql[o] = lo;
+                const size_t at = (size_t)row * qd + slot * HD + d;
+                o.qh[at] = hi;
+                o.ql[at] = lo;
             } else if (slot < heads + kv_heads) {
-                const size_t o = frag_k<HD>(slot - heads, row, d, tp);
-                kh[o] = hi;
-                kl[o] = lo;
+                const size_t at = frag_k<HD>(slot - heads, row, d, tp);
+                o.kh[at] = hi;
+                o.kl[at] = lo;
             } else {
-                const size_t o = frag_v<HD>(slot - heads - kv_heads, row, d, tp);
-                vh[o] = hi;
-                vl[o] = lo;
+                const size_t at = frag_v<HD>(slot - heads - kv_heads, row, d, tp);
+                o.vh[at] = hi;
+                o.vl[at] = lo;
             }
         }
         if (lane == 0) {
             if (slot < heads)
-                eq[(size_t)slot * tp + row] = code;
+                o.eq[(size_t)slot * tp + row] = code;
             else if (slot < heads + kv_heads)
-                ek[(size_t)(slot - heads) * tp + row] = code;
+                o.ek[(size_t)(slot - heads) * tp + row] = code;
             else
-                ev[(size_t)(slot - heads - kv_heads) * tp + row] = code;
+                o.ev[(size_t)(slot - heads - kv_heads) * tp + row] = code;
         }
     }
+}
+
+// The split operands from qkv [t, width] (already biased and rotated); one workgroup per row of
+// tp, rows t .. tp - 1 written as zeros.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict__ qkv, SplitDst o, uint32_t t,
+                                                         uint32_t tp, uint32_t width, uint32_t heads,
+                                                         uint32_t kv_heads) {
+    const uint32_t row = blockIdx.x;
+    split_heads<HD>([&](uint32_t slot, uint32_t d) { return qkv[(size_t)row * width + slot * HD + d]; }, o, row, t,
+                    tp, heads, kv_heads);
+}
+
+// qkv_rope_kernel and attn_split_kernel in one pass: row `row` of the QKV product (its K-split
+// partial sums and the bias) into LDS, RoPE into a second LDS row (rope_value, the same
+// roundings), then the row's split operands; the f32 q, k and v are not written. One workgroup
+// per row of tp; dynamic LDS 2 width floats.
+template <int HD>
+__global__ __launch_bounds__(256) void qkv_rope_split_kernel(const float *__restrict__ src, uint32_t src_splits,
+                                                             size_t src_stride, const float *__restrict__ bias,
+                                                             const float *__restrict__ cos_t,
+                                                             const float *__restrict__ sin_t, SplitDst o, uint32_t t,
+                                                             uint32_t tp, uint32_t width, uint32_t heads,
+                                                             uint32_t kv_heads, uint32_t rope_dim, int neox) {
+    extern __shared__ __attribute__((aligned(16))) float row[];
+    float *rot = row + (width + 3) / 4 * 4;
+    const uint32_t r = blockIdx.x;
+    if (r < t) {  // (uniform over the workgroup)
+        qkv_rope_row(src, src_splits, src_stride, bias, width, r, row);
+        __syncthreads();
+        const uint32_t half = rope_dim / 2;
+        const float *cr = cos_t + (size_t)r * half, *sr = sin_t + (size_t)r * half;
+        for (uint32_t c = threadIdx.x; c < width; c += 256)
+            rot[c] = rope_value(row, c, cr, sr, (heads + kv_heads) * HD, HD, rope_dim, neox);
+        __syncthreads();
+    }
+    split_heads<HD>([&](uint32_t slot, uint32_t d) { return rot[slot * HD + d]; }, o, r, t, tp, heads, kv_heads);
 }
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -1132,17 +1184,34 @@ hipError_t linear(const fh_llama *m, hipStream_t s, const fh_llama::Mat &mat, co
     }
 }
 
-hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t) {
+// RoPE (with the q/k/v bias and the QKV product's K-split partial sums) and the attention of t
+// rows. The split attention's head dims take qkv_rope_split_kernel when two rows of qkv fit in
+// 64 KB of LDS (the f32 q, k, v are then never written), else (or when the model was loaded
+// with FERRUM_HIP_ROPE_UNFUSED=1) qkv_rope_kernel and attn_split_kernel, with the same results;
+// the other head dims qkv_rope_kernel and the f32 attention_kernel.
+hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t, const SplitOut &qkv, const float *bias) {
     const dim3 grid((unsigned)m->heads, (unsigned)((t + 31) / 32));
     const uint32_t w = (uint32_t)m->qkv_width(), group = (uint32_t)(m->heads / m->kv_heads);
     const float scale = 1.0f / sqrtf((float)m->head_dim);
-    const uint32_t T = (uint32_t)t, H = (uint32_t)m->heads;
+    const uint32_t T = (uint32_t)t, H = (uint32_t)m->heads, KV = (uint32_t)m->kv_heads;
+    const uint32_t hd = (uint32_t)m->head_dim, rd = (uint32_t)m->rope_dim;
+    const int neox = m->neox ? 1 : 0;
+    const size_t fused_lds = 2 * ((size_t)(w + 3) / 4 * 4) * 4;
+    const float *cos_t = fp(m->rope_cos), *sin_t = fp(m->rope_sin);
+    const bool fused = m->fuse_rope && split_attention(m) && fused_lds <= 65536;
+    if (!fused)
+        qkv_rope_kernel<<<T, 256, w * 4, s>>>(qkv.part, qkv.splits, t * w, m->qkv, bias, cos_t, sin_t, w,
+                                              H + KV, hd, rd, neox);
     if (split_attention(m)) {
-        const uint32_t tp = (T + 31) / 32 * 32, KV = (uint32_t)m->kv_heads;
-#define FH_SPLIT_ATTN(HD, W)                                                                                        \
-    attn_split_kernel<HD><<<tp, 256, 0, s>>>(m->qkv, m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl, m->seq, m->sek, \
-                                             m->sev, T, tp, w, H, KV);                                             \
-    attention_split_kernel<HD, W><<<grid, 64 * W, 0, s>>>(m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl, m->seq,  \
+        const uint32_t tp = (T + 31) / 32 * 32;
+        const SplitDst o{m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl, m->seq, m->sek, m->sev};
+#define FH_SPLIT_ATTN(HD, W)                                                                                      \
+    if (fused)                                                                                                    \
+        qkv_rope_split_kernel<HD><<<tp, 256, fused_lds, s>>>(qkv.part, qkv.splits, t * w, bias, cos_t, sin_t, o, \
+                                                             T, tp, w, H, KV, rd, neox);                          \
+    else                                                                                                          \
+        attn_split_kernel<HD><<<tp, 256, 0, s>>>(m->qkv, o, T, tp, w, H, KV);                                     \
+    attention_split_kernel<HD, W><<<grid, 64 * W, 0, s>>>(m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl, m->seq, \
                                                           m->sek, m->sev, m->att, T, tp, H, group, scale)
         switch (m->head_dim) {
         case 32: FH_SPLIT_ATTN(32, 4); break;
@@ -1173,7 +1242,6 @@ hipError_t enqueue_body(fh_llama *m, hipStream_t s, size_t t) {
     else
         embed_rows_kernel<FH_Q4_0><<<T, 256, 0, s>>>(tq->qs, tq->ds, m->ids, m->x, d, (uint32_t)m->vocab);
     hipError_t e = hipGetLastError();
-    const uint32_t width = (uint32_t)m->qkv_width();
     const size_t td = t * m->dim;
     // The fast path's RMSNorms and SwiGLU write the next product's split x themselves (the
     // product then skips its split pass); rows up to 16384 wide, held in LDS.
@@ -1203,10 +1271,7 @@ hipError_t enqueue_body(fh_llama *m, hipStream_t s, size_t t) {
         norm(l > 0, L.attn_norm, down);
         SplitOut qkv{m->qkv, 1}, att{m->o, 1}, gu{m->gu, 1};
         if ((e = linear(m, s, L.wqkv, hx, m->qkv, t, &qkv))) break;
-        qkv_rope_kernel<<<T, 256, width * 4, s>>>(qkv.part, qkv.splits, t * width, m->qkv, fp(L.bqkv), fp(m->rope_cos),
-                                                  fp(m->rope_sin), width, (uint32_t)(m->heads + m->kv_heads),
-                                                  (uint32_t)m->head_dim, (uint32_t)m->rope_dim, m->neox ? 1 : 0);
-        if ((e = launch_attention(m, s, t))) break;
+        if ((e = launch_attention(m, s, t, qkv, fp(L.bqkv)))) break;
         if ((e = linear(m, s, L.wo, m->att, m->o, t, &att))) break;
         norm(true, L.ffn_norm, att);
         if (fused) {
@@ -1328,6 +1393,8 @@ fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_
     m->dev = dev;
     m->path = path;
     m->neox = arch == "qwen2";  // ferrum_model/src/gguf/llama/mod.rs:108-117
+    const char *unfused = getenv("FERRUM_HIP_ROPE_UNFUSED");
+    m->fuse_rope = !(unfused && unfused[0] == '1');
     auto key = [&](const char *k) { return arch + "." + k; };
     auto has = [&](const std::string &k) {
         size_t i;

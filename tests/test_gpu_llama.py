@@ -258,11 +258,19 @@ def test_split_attention_head_dims_match_the_oracle(fh, g, orc, head_dim):
     data = lm.to_gguf(lm.llama_random(c, 17, True, False), lm.Q8_0)
     ref = lm.from_gguf(data)
     dev = load(fh, g, data)
+    # the RoPE and the split as two kernels (what q/k/v rows too wide for one workgroup's LDS take)
+    os.environ["FERRUM_HIP_ROPE_UNFUSED"] = "1"
+    try:
+        two = load(fh, g, data)
+    finally:
+        del os.environ["FERRUM_HIP_ROPE_UNFUSED"]
     ids = [int(t) for t in np.random.default_rng(head_dim).integers(0, 300, 97)]
     for t in (1, 33, 97):
-        e = rel(dev.forward_all(ids[:t]), orc.llama_forward(ref, ids[:t]))
+        got = dev.forward_all(ids[:t])
+        e = rel(got, orc.llama_forward(ref, ids[:t]))
         say(f"head_dim {head_dim} t={t}: {e:.2e}")
         assert e < SCORE, (head_dim, t, e)
+        assert np.array_equal(got, two.forward_all(ids[:t])), (head_dim, t)
 
 
 @pytest.mark.parametrize("kind", [lm.Q8_0, lm.Q4_0])
