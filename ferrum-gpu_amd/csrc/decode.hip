@@ -92,10 +92,44 @@ typedef __attribute__((address_space(1))) const f32x4 gf32x4;
 
 __device__ __forceinline__ f32x4 gload4(const float *p) { return *(gf32x4 *)p; }
 
+// Reductions over lanes by DPP row operations (one VALU instruction a step) where the lanes share
+// a 16-lane row, instead of LDS permutes: group_reduce<L> combines the lane's aligned group of L
+// lanes (L = 2 .. 64: quad_perm lanes ^ 1, quad_perm lanes ^ 2, the half-row mirror, the row
+// mirror, then permutes across rows) and leaves the result in every lane of the group;
+// wave_reduce combines the four row results of a wavefront by readlane (a uniform value).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+struct AddOp {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct MaxOp {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+template <int L, class Op>
+__device__ __forceinline__ float group_reduce(float v, Op op) {
+    static_assert(L == 2 || L == 4 || L == 8 || L == 16 || L == 32 || L == 64, "lane groups of 2 to 64");
+    v = op(v, dpp_f<0xB1>(v));                               // quad_perm [1, 0, 3, 2]
+    if constexpr (L >= 4) v = op(v, dpp_f<0x4E>(v));         // quad_perm [2, 3, 0, 1]
+    if constexpr (L >= 8) v = op(v, dpp_f<0x141>(v));        // row_half_mirror
+    if constexpr (L >= 16) v = op(v, dpp_f<0x140>(v));       // row_mirror
+    if constexpr (L >= 32) v = op(v, __shfl_xor(v, 16, 64));
+    if constexpr (L >= 64) v = op(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+    v = group_reduce<16>(v, op);
+    return op(op(lane_f(v, 0), lane_f(v, 16)), op(lane_f(v, 32), lane_f(v, 48)));
+}
+
 // Sum over the workgroup (every thread gets the total); red holds one float per wavefront.
 __device__ __forceinline__ float block_sum(float v, float *red) {
-#pragma unroll
-    for (int m = 32; m >= 1; m /= 2) v += __shfl_xor(v, m, 64);
+    v = wave_reduce(v, AddOp());
     const uint32_t w = threadIdx.x / 64, nw = blockDim.x / 64;
     __syncthreads();  // red may still be read by a previous call
     if (threadIdx.x % 64 == 0) red[w] = v;
@@ -544,11 +578,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float *__
         const f32x4 k1 = two ? gload4(kb + (size_t)(j + NR) * d) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         float d0 = (qv.x * k0.x + qv.y * k0.y) + (qv.z * k0.z + qv.w * k0.w);
         float d1 = (qv.x * k1.x + qv.y * k1.y) + (qv.z * k1.z + qv.w * k1.w);
-#pragma unroll
-        for (int o = L / 2; o >= 1; o /= 2) {
-            d0 += __shfl_xor(d0, o, L);
-            d1 += __shfl_xor(d1, o, L);
-        }
+        d0 = group_reduce<L>(d0, AddOp());
+        d1 = group_reduce<L>(d1, AddOp());
         if (li == 0) {
             s[j] = d0 * scale;
             if (two) s[j + NR] = d1 * scale;
@@ -558,8 +589,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float *__
     constexpr uint32_t NW = kAttnThreads / 64;
     float m = -INFINITY;
     for (uint32_t j = tid; j < T; j += kAttnThreads) m = fmaxf(m, s[j]);
-#pragma unroll
-    for (int o = 32; o >= 1; o /= 2) m = fmaxf(m, __shfl_xor(m, o, 64));
+    m = wave_reduce(m, MaxOp());
     if (tid % 64 == 0) red[tid / 64] = m;
     __syncthreads();
     m = red[0];
@@ -570,8 +600,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float *__
         s[j] = e;
         z += e;
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o /= 2) z += __shfl_xor(z, o, 64);
+    z = wave_reduce(z, AddOp());
     if (tid % 64 == 0) red[NW + tid / 64] = z;
     __syncthreads();
     float sum = 0.0f;
@@ -722,8 +751,7 @@ __device__ __forceinline__ void attend_head(const float *qh, const float *knew, 
 #pragma unroll
         for (int u = 0; u < U; u++) {
             float dt = (qv.x * kr[u].x + qv.y * kr[u].y) + (qv.z * kr[u].z + qv.w * kr[u].w);
-#pragma unroll
-            for (int o = L / 2; o >= 1; o /= 2) dt += __shfl_xor(dt, o, L);
+            dt = group_reduce<L>(dt, AddOp());
             sc[u] = j0 + u * NR < T ? dt * scale : -INFINITY;
             mc = fmaxf(mc, sc[u]);
         }
