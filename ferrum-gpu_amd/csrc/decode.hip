@@ -92,40 +92,6 @@ typedef __attribute__((address_space(1))) const f32x4 gf32x4;
 
 __device__ __forceinline__ f32x4 gload4(const float *p) { return *(gf32x4 *)p; }
 
-// Reductions over lanes by DPP row operations (one VALU instruction a step) where the lanes share
-// a 16-lane row, instead of LDS permutes: group_reduce<L> combines the lane's aligned group of L
-// lanes (L = 2 .. 64: quad_perm lanes ^ 1, quad_perm lanes ^ 2, the half-row mirror, the row
-// mirror, then permutes across rows) and leaves the result in every lane of the group;
-// wave_reduce combines the four row results of a wavefront by readlane (a uniform value).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float lane_f(float v, int l) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
-}
-struct AddOp {
-    __device__ float operator()(float a, float b) const { return a + b; }
-};
-struct MaxOp {
-    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
-};
-template <int L, class Op>
-__device__ __forceinline__ float group_reduce(float v, Op op) {
-    static_assert(L == 2 || L == 4 || L == 8 || L == 16 || L == 32 || L == 64, "lane groups of 2 to 64");
-    v = op(v, dpp_f<0xB1>(v));                               // quad_perm [1, 0, 3, 2]
-    if constexpr (L >= 4) v = op(v, dpp_f<0x4E>(v));         // quad_perm [2, 3, 0, 1]
-    if constexpr (L >= 8) v = op(v, dpp_f<0x141>(v));        // row_half_mirror
-    if constexpr (L >= 16) v = op(v, dpp_f<0x140>(v));       // row_mirror
-    if constexpr (L >= 32) v = op(v, __shfl_xor(v, 16, 64));
-    if constexpr (L >= 64) v = op(v, __shfl_xor(v, 32, 64));
-    return v;
-}
-template <class Op>
-__device__ __forceinline__ float wave_reduce(float v, Op op) {
-    v = group_reduce<16>(v, op);
-    return op(op(lane_f(v, 0), lane_f(v, 16)), op(lane_f(v, 32), lane_f(v, 48)));
-}
 
 // Sum over the workgroup (every thread gets the total); red holds one float per wavefront.
 __device__ __forceinline__ float block_sum(float v, float *red) {

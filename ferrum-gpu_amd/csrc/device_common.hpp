@@ -114,4 +114,46 @@ __device__ __forceinline__ uint32_t scale_bits(uint32_t w0, size_t off) {
     return (off & 2) ? (w0 >> 16) : (w0 & 0xffffu);
 }
 
+// Reductions over lanes by DPP row operations (one VALU instruction a step, usually fused into
+// the combining instruction) where the lanes share a 16-lane row, instead of LDS permutes:
+// group_reduce<L> combines the lane's aligned group of L lanes (L = 2 .. 64: quad_perm lanes ^ 1,
+// quad_perm lanes ^ 2, the half-row mirror, the row mirror, then permutes across rows) and leaves
+// the result in every lane of the group; wave_reduce combines the four row results of a wavefront
+// by readlane (a uniform value). A group's lanes must be active together.
+template <int CTRL, class T>
+__device__ __forceinline__ T dpp_mov(T v) {
+    static_assert(sizeof(T) == 4, "32-bit values");
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <class T>
+__device__ __forceinline__ T lane_value(T v, int l) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+struct AddOp {
+    template <class T>
+    __device__ T operator()(T a, T b) const { return a + b; }
+};
+struct MaxOp {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct AndOp {
+    __device__ int operator()(int a, int b) const { return a & b; }
+};
+template <int L, class T, class Op>
+__device__ __forceinline__ T group_reduce(T v, Op op) {
+    static_assert(L == 2 || L == 4 || L == 8 || L == 16 || L == 32 || L == 64, "lane groups of 2 to 64");
+    v = op(v, dpp_mov<0xB1>(v));                          // quad_perm [1, 0, 3, 2]
+    if constexpr (L >= 4) v = op(v, dpp_mov<0x4E>(v));    // quad_perm [2, 3, 0, 1]
+    if constexpr (L >= 8) v = op(v, dpp_mov<0x141>(v));   // row_half_mirror
+    if constexpr (L >= 16) v = op(v, dpp_mov<0x140>(v));  // row_mirror
+    if constexpr (L >= 32) v = op(v, __shfl_xor(v, 16, 64));
+    if constexpr (L >= 64) v = op(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+template <class T, class Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+    v = group_reduce<16>(v, op);
+    return op(op(lane_value(v, 0), lane_value(v, 16)), op(lane_value(v, 32), lane_value(v, 48)));
+}
+
 }  // namespace fh

@@ -68,17 +68,14 @@ static_assert(prep_dwords_match_slots<FH_Q8_0>() && prep_dwords_match_slots<FH_Q
 // the two halves of the limb sums take (both exact in int32).
 // Writes the record of the block whose elements 4j .. 4j + 3 are v at rec (a global or an LDS
 // pointer). The eight lanes of a block must run this together (they reduce over one another
-// with shuffles).
+// by DPP).
 template <int KIND, class U32Ptr>
 __device__ __forceinline__ void prep_values(f32x4 v, int j, U32Ptr rec) {
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     int finite = (int)(fabsf(v.x) <= 3.4028235e38f) & (int)(fabsf(v.y) <= 3.4028235e38f) &
                  (int)(fabsf(v.z) <= 3.4028235e38f) & (int)(fabsf(v.w) <= 3.4028235e38f);  // 0: inf, NaN
-#pragma unroll
-    for (int m = 1; m < 8; m *= 2) {
-        amax = fmaxf(amax, __shfl_xor(amax, m, 8));
-        finite &= __shfl_xor(finite, m, 8);
-    }
+    amax = group_reduce<8>(amax, MaxOp());
+    finite = group_reduce<8>(finite, AndOp());
     // grid 2^-sh with 2^29 <= amax * 2^sh < 2^30, at most 2^149 (subnormal amax: exponent field
     // 1); the scaling is split in two exact power-of-two products so that no factor overflows
     const int sh = min(156 - (int)max(__float_as_uint(amax) >> 23, 1u), 149);  // -98 .. 149
@@ -109,11 +106,8 @@ __device__ __forceinline__ void prep_values(f32x4 v, int j, U32Ptr rec) {
         slo += c * 256 + e;
     }
     if constexpr (KIND == FH_Q4_0) {
-#pragma unroll
-        for (int m = 1; m < 8; m *= 2) {
-            shi += __shfl_xor(shi, m, 8);
-            slo += __shfl_xor(slo, m, 8);
-        }
+        shi = group_reduce<8>(shi, AddOp());
+        slo = group_reduce<8>(slo, AddOp());
     }
     const int dw = prep_dword<KIND>(j);
     rec[dw] = la;

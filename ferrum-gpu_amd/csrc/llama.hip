@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const float *__restrict
 
 // Sum over a block of 256 threads (four wavefronts); every thread gets the total.
 __device__ __forceinline__ float block_sum_256(float v, float *red) {
-    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+    v = wave_reduce(v, AddOp());
     const uint32_t w = threadIdx.x >> 6;
     __syncthreads();  // red may still be read by a previous call
     if ((threadIdx.x & 63) == 0) red[w] = v;
@@ -620,8 +620,7 @@ __device__ __forceinline__ void split_heads(Get get, const SplitDst &o, uint32_t
             v[i] = row < t && d < (uint32_t)HD ? get(slot, d) : 0.0f;
         }
         float mx = fmaxf(fabsf(v[0]), fabsf(v[1]));
-#pragma unroll
-        for (int s = 32; s >= 1; s /= 2) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
+        mx = wave_reduce(mx, MaxOp());
         // 2^E <= mx < 2^(E+1), e = E - 14; zero rows, padding rows and non-finite rows keep e = 0
         // (non-finite values then stay non-finite) and padding rows report -127
         int e = 0;

@@ -48,8 +48,7 @@ __device__ __forceinline__ void split_row_fast(Get get, uint32_t m, uint32_t K, 
         mx = fmaxf(mx, amax(v[i]));
     }
     for (uint32_t q = tid + 256 * kKeep; q < nq; q += 256) mx = fmaxf(mx, amax(get(q)));
-#pragma unroll
-    for (int o = 32; o >= 1; o /= 2) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = wave_reduce(mx, MaxOp());
     if (tid % 64 == 0) red[tid / 64] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
