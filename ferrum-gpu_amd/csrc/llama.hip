@@ -938,8 +938,8 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ lo
     uint32_t first = 0xffffffffu;
     if ((vocab & 3u) == 0) {
         const f32x4 *x4 = (const f32x4 *)x;
-        for (uint32_t j = threadIdx.x; j < vocab / 4; j += 256) {
-            const f32x4 v = x4[j];
+        const uint32_t n4 = vocab / 4;
+        auto take4 = [&](f32x4 v, uint32_t j) {
             const float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
             if (mx > m) {
                 s = m == -INFINITY ? 0.0f : s * __expf(m - mx);
@@ -947,7 +947,17 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ lo
                 first = 4 * j + (v[0] == mx ? 0u : v[1] == mx ? 1u : v[2] == mx ? 2u : 3u);
             }
             s += (__expf(v[0] - m) + __expf(v[1] - m)) + (__expf(v[2] - m) + __expf(v[3] - m));
+        };
+        // four float4 loads in flight per thread, taken in the same order as one at a time
+        uint32_t j = threadIdx.x;
+        for (; j + 3 * 256 < n4; j += 4 * 256) {
+            f32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = x4[j + 256 * u];
+#pragma unroll
+            for (int u = 0; u < 4; u++) take4(v[u], j + 256 * u);
         }
+        for (; j < n4; j += 256) take4(x4[j], j);
     } else {
         for (uint32_t j = threadIdx.x; j < vocab; j += 256) score_take(x[j], j, m, s, first);
     }
