@@ -64,6 +64,7 @@ def lib() -> ctypes.CDLL:
             "fo_fp8_encode": (ctypes.c_uint8, [ctypes.c_int, ctypes.c_float]),
             "fo_mxfp4_half_scale": (ctypes.c_float, [ctypes.c_uint8]),
             "fo_q2k_nearest_int": (ctypes.c_int32, [ctypes.c_float]),
+            "fo_q2k_fit": (None, [P, P, P, P]),
             "fo_rope_tables": (None, [S, S, S, ctypes.c_float, P, ctypes.c_float, P, P]),
             "fo_rmsnorm": (None, [P, P, S, S, ctypes.c_float, P]),
             "fo_apply_rope": (None, [P, S, S, S, S, P, P, ctypes.c_int]),
@@ -472,6 +473,17 @@ def fp8_encode(e5m2: bool, x: float) -> int:
 def mxfp4_half_scale(e: int) -> float:
     """ferrum_gguf/src/codec/mxfp4.rs:26-33"""
     return lib().fo_mxfp4_half_scale(e)
+
+
+def q2k_fit(x16) -> tuple:
+    """ferrum_gguf/src/codec/q2k.rs:24-93: (scale, negated min, levels) of one 16-value sub-block."""
+    x = _f32(x16)
+    if x.size != 16:
+        raise ValueError("a Q2_K sub-block has 16 values")
+    lv = np.empty(16, np.uint8)
+    sc, mn = ctypes.c_float(), ctypes.c_float()
+    lib().fo_q2k_fit(_p(x), _p(lv), ctypes.byref(sc), ctypes.byref(mn))
+    return sc.value, mn.value, lv
 
 
 def q2k_nearest_int(x: float) -> int:

@@ -131,8 +131,9 @@ int32_t fo_q2k_nearest_int(float x) {
 
 static int32_t clamp3(int32_t q) { return q < 0 ? 0 : (q > 3 ? 3 : q); }
 
-/* q2k.rs:24-93 (make_qkx2_quants with nmax 3, rmin -0.5, rdelta 0.1, nstep 15) */
-static void q2k_fit(const float *x, uint8_t *l, float *scale_out, float *min_out) {
+/* q2k.rs:24-93 (make_qkx2_quants with nmax 3, rmin -0.5, rdelta 0.1, nstep 15). Exported so the
+ * tests can check the search's result against the weighted least-squares fit it claims to be. */
+void fo_q2k_fit(const float *x, uint8_t *l, float *scale_out, float *min_out) {
     float weights[16];
     for (int i = 0; i < 16; i++) weights[i] = fabsf(x[i]);
     float min = x[0], max = x[0];
@@ -203,7 +204,7 @@ void fo_q2k_encode_blocks(const float *data, size_t nblocks, uint8_t *out) {
         uint8_t *o = out + b * 84;
         float scales[16], mins[16];
         uint8_t levels[256];
-        for (int j = 0; j < 16; j++) q2k_fit(blk + 16 * j, levels + 16 * j, &scales[j], &mins[j]);
+        for (int j = 0; j < 16; j++) fo_q2k_fit(blk + 16 * j, levels + 16 * j, &scales[j], &mins[j]);
         float max_scale = 0.0f, max_min = 0.0f;
         for (int j = 0; j < 16; j++) {
             max_scale = fmaxf(max_scale, scales[j]);

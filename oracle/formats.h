@@ -45,6 +45,8 @@ void fo_mxfp4_encode_blocks(const float *data, size_t nblocks, uint8_t *out);
 
 /* ferrum_gguf/src/codec/q2k.rs:16-19 */
 int32_t fo_q2k_nearest_int(float x);
+/* ferrum_gguf/src/codec/q2k.rs:24-93: one 16-value sub-block's (scale, negated min) and levels */
+void fo_q2k_fit(const float *x16, uint8_t *levels16, float *scale, float *neg_min);
 /* ferrum_gguf/src/codec/q2k.rs:96-150 */
 void fo_q2k_encode_blocks(const float *data, size_t nblocks, uint8_t *out);
 

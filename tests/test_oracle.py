@@ -3,7 +3,11 @@
 Each check is one the reference's own tests make (cited file:line), a golden fixture, an
 independent restatement (numpy's IEEE casts, oracle/np_oracle.py) or a closed form. A planted
 mistake (swapped nibbles, round-half-even, a dropped scale rounding, a transposed operand) fails
-at least one of them; ``test_planted_mistakes_are_caught`` shows that for the codec.
+at least one of them; ``test_planted_mistakes_are_caught`` shows that for the codec. The Q4_0
+encoder's rounding, which the reference's own tests leave open (they bound the error by a whole
+step), is pinned by the nearest-level and upward-tie rules of ``q4_0_rounding_violations``, and
+``test_q4_0_rounding_rules_catch_planted_mistakes`` shows truncation, round-half-away and
+round-half-even each break them while passing every reference check.
 """
 import json
 import os
@@ -114,6 +118,102 @@ def test_q4_0_nibble_order_low_half_first(orc):
     blk[0], blk[16] = -8.0, 7.0
     back = orc.decode(orc.Q4_0, orc.encode(orc.Q4_0, blk), 32)
     assert back[0] == -8.0 and back[16] == 7.0 and back[1] == 0.0
+
+
+def q4_0_rounding_violations(x, blob):
+    """Blocks whose Q4_0 quants are not what the mathematics of quant.rs:120-133 fixes, judged in
+    float64 from the bytes and the input alone (no restatement of the encoder's arithmetic):
+    - with r = v * id (id = 1 / d in f32, d the unrounded f32 scale max / -8, max the signed value
+      of the first largest |v|), every quant is a nearest level: |r - (nibble - 8)| <= 1/2 wherever
+      r < 7.5, and nibble 15 from 7.5 up (the clamp);
+    - ties resolve upward (floor(r + 1/2), what trunc(r + 8.5) is for a positive argument): where
+      r + 1/2 is an integer, nibble - 8 equals it;
+    - the stored scale is d rounded to f16.
+    The f32 rounding of r and of r + 8.5 is allowed for (2^-18 slack away from ties)."""
+    b = np.asarray(x, np.float32).reshape(-1, 32)
+    raw = np.asarray(blob, np.uint8).reshape(-1, 18)
+    bad = []
+    for i, (v, blk) in enumerate(zip(b, raw)):
+        a = np.abs(v)
+        mx = v[int(np.argmax(a))] if a.max() > 0 else np.float32(0)
+        d = np.float32(mx / np.float32(-8))
+        idv = np.float32(1) / d if d != 0 else np.float32(0)
+        nib = np.concatenate([blk[2:] & 15, blk[2:] >> 4]).astype(np.float64)
+        r = v.astype(np.float64) * float(idv)
+        ok = np.float16(d).view(np.uint16) == (int(blk[0]) | int(blk[1]) << 8)
+        over = r >= 7.5
+        near = np.abs(r - (nib - 8)) <= 0.5 + 2.0 ** -18
+        ok &= bool(np.all(np.where(over, nib == 15, near)))
+        tie = (r + 0.5 == np.floor(r + 0.5)) & ~over
+        ok &= bool(np.all(nib[tie] - 8 == r[tie] + 0.5))
+        if not ok:
+            bad.append(i)
+    return bad
+
+
+def q4_0_tie_block():
+    """max -8 (so d = 1, id = 1), then the ties -2.5, -1.5, -0.5, 0.5, 1.5, 2.5 and 7.5, and +8
+    (past the top level: clamps to nibble 15)."""
+    blk = np.zeros(32, np.float32)
+    blk[:9] = [-8.0, -2.5, -1.5, -0.5, 0.5, 1.5, 2.5, 7.5, 8.0]
+    return blk
+
+
+def test_q4_0_quants_are_nearest_levels_with_ties_upward(orc):
+    """What pins the Q4_0 encoder's rounding: the reference's tests (quant.rs:250-286) bound the
+    error by a whole step and so leave the rule open. The tie block fixes it by hand: upward ties
+    give nibbles 6, 7, 8, 9, 10, 11 for -2.5 .. 2.5 (round-half-away would give 5, 6, 7, 9, 10,
+    11; round-half-even 6, 6, 8, 8, 10, 10; truncation 6, 7, 8, 8, 9, 10)."""
+    blk = q4_0_tie_block()
+    b = orc.encode(orc.Q4_0, blk)
+    nib = np.concatenate([b[2:] & 15, b[2:] >> 4])
+    assert list(nib[:9]) == [0, 6, 7, 8, 9, 10, 11, 15, 15]
+    assert list(orc.decode(orc.Q4_0, b, 32)[:9]) == [-8, -2, -1, 0, 1, 2, 3, 7, 7]
+    g = np.load(os.path.join(GOLDEN, "codec_nasty.npz"))
+    rng = np.random.default_rng(11)
+    for x in (g["x"], (rng.standard_normal(32 * 4096) * 0.02).astype(np.float32), blk,
+              # values on the half-integer grid of their block's step: every one a tie
+              np.where(rng.random(32 * 512) < 0.1, np.float32(-8),
+                       rng.integers(-16, 16, 32 * 512).astype(np.float32) / 2).astype(np.float32)):
+        finite = np.all(np.isfinite(np.asarray(x).reshape(-1, 32)), axis=1)
+        xs = np.asarray(x, np.float32).reshape(-1, 32)[finite].reshape(-1)
+        assert q4_0_rounding_violations(xs, orc.encode(orc.Q4_0, xs)) == []
+
+
+def test_q4_0_rounding_rules_catch_planted_mistakes(orc):
+    """Three plausible misreadings of `(v * id + 8.5) as i32`, planted in copies of the numpy
+    restatement: truncating v * id and adding 8, rounding half away from zero, rounding half to
+    even. The reference's own checks (error within a step, idempotence, nibble order, zero block)
+    pass all three; the rules above fail each one."""
+    def planted(rnd):
+        def enc(v):
+            b = np.asarray(v, np.float32).reshape(-1, 32)
+            out = np_oracle.encode_q4_0(v).reshape(-1, 18).copy()
+            a = np.abs(b)
+            mx = b[np.arange(b.shape[0]), np.argmax(a, axis=1)]
+            d = (mx / np.float32(-8)).astype(np.float32)
+            with np.errstate(all="ignore"):
+                idv = np.where(d != 0, np.float32(1) / np.where(d != 0, d, 1), 0).astype(np.float32)
+            q = np.clip(rnd((b * idv[:, None]).astype(np.float32)) + 8, 0, 15).astype(np.uint8)
+            out[:, 2:] = q[:, :16] | (q[:, 16:] << 4)
+            return out.reshape(-1)
+        return enc
+
+    mutants = {"truncate": planted(np.trunc), "half_away": planted(np_oracle._round_half_away),
+               "half_even": planted(np.round)}
+    rng = np.random.default_rng(12)
+    wide = (rng.standard_normal(32 * 4096) * 0.02).astype(np.float32)
+    blk = q4_0_tie_block()
+    assert q4_0_rounding_violations(blk, np_oracle.encode_q4_0(blk)) == []
+    for name, enc in mutants.items():
+        caught = q4_0_rounding_violations(blk, enc(blk)) or q4_0_rounding_violations(wide, enc(wide))
+        assert caught, name
+        # the reference's own properties do not see it (quant.rs:250-286)
+        d = data(64)
+        once = orc.decode(orc.Q4_0, enc(d), 64)
+        for b_, got in zip(d.reshape(-1, 32), once.reshape(-1, 32)):
+            assert np.all(np.abs(b_ - got) <= np.abs(b_).max() / 8 * 1.01 + 1e-4), name
+        assert np.array_equal(orc.decode(orc.Q4_0, enc(once), 64), once), name
 
 
 def test_zero_blocks_and_length_errors(orc):

@@ -11,7 +11,13 @@ block independence), its bytes are pinned by a second statement of the search wr
 numpy (vectorised over sub-blocks, f32 throughout, sequential sums by cumsum, the nearest_int
 magic by its bit definition, f16 by numpy's IEEE cast), which must give the C oracle's bytes on
 data that reaches every branch; the same statement with one search constant perturbed (rmin,
-rdelta, the step count, the negative-min clamp, the grid's moving min) must not, which shows the data exercises them."""
+rdelta, the step count, the negative-min clamp, the grid's moving min) must not, which shows the data exercises them.
+Because a misreading both statements shared would pass that, the C oracle's search result is also
+checked against what the mathematics fixes, with no search restated: each sub-block's (scale,
+min) is the first grid or the |x|-weighted least-squares fit of its levels (min clamped at 0), its
+weighted deviation is no worse than the first grid's, and the bytes pack the nearest 4-bit codes
+and the nearest levels to the decoder's own rounded scales. Planted mistakes (unweighted fit,
+worse candidate kept, clamp dropped, min sign flipped, levels not re-fitted) each break them."""
 import math
 
 import numpy as np
@@ -197,14 +203,15 @@ def seqsum(a):
     return np.cumsum(a, axis=-1, dtype=np.float32)[..., -1]
 
 
-def q2k_fit_np(x, rmin=-0.5, rdelta=0.1, nstep=15, clamp_min=True, moving_min=True):
+def q2k_fit_np(x, rmin=-0.5, rdelta=0.1, nstep=15, clamp_min=True, moving_min=True, unit_weights=False,
+               keep_worse=False):
     """make_qkx2_quants for nmax = 3 over sub-blocks x [S, 16]: the scale and (negated) min of the
     candidate grid point whose weighted (|x|) absolute deviation is smallest, first wins (each
     candidate's grid spans max - min with the min of the best candidate so far); the quants of
     that candidate."""
     f = np.float32
     x = np.asarray(x, f)
-    w = np.abs(x)
+    w = np.ones_like(x) if unit_weights else np.abs(x)
     mn, mx = x.min(axis=1), x.max(axis=1)
     sum_w, sum_x = seqsum(w), seqsum(w * x)
     mn = np.where(mn > 0, f(0), mn)
@@ -230,7 +237,7 @@ def q2k_fit_np(x, rmin=-0.5, rdelta=0.1, nstep=15, clamp_min=True, moving_min=Tr
                 tm = np.where(pos, f(0), tm)
                 ts = np.where(pos, sxl / sl2, ts)
             mad = seqsum(w * np.abs(ts[:, None] * qf + tm[:, None] - x))
-            take = (d > 0) & (mad < best) & ~flat
+            take = (d > 0) & ((mad > best) if keep_worse else (mad < best)) & ~flat
             lv = np.where(take[:, None], la, lv)
             best = np.where(take, mad, best)
             scale = np.where(take, ts, scale)
@@ -240,7 +247,7 @@ def q2k_fit_np(x, rmin=-0.5, rdelta=0.1, nstep=15, clamp_min=True, moving_min=Tr
     return scale.astype(f), (-mn).astype(f), lv
 
 
-def q2k_encode_np(data, **search):
+def q2k_encode_np(data, requant=True, **search):
     """Q2_K super-blocks from q2k_fit_np: 4-bit scales and mins against the f16 super scale and
     min, the quants re-fitted to the rounded scales, then the ggml layout."""
     f = np.float32
@@ -261,7 +268,7 @@ def q2k_encode_np(data, **search):
         d32 = np.array(dbits, np.uint16).view(np.float16).astype(f)
         m32 = np.array(mbits, np.uint16).view(np.float16).astype(f)
         levels = lv[b].copy()
-        for j in range(16):
+        for j in range(16 if requant else 0):
             s_ = d32 * f(packed[j] & 15)
             if s_ == 0:
                 continue
@@ -311,6 +318,129 @@ def test_q2k_search_constants_are_pinned_by_the_cases(orc):
     want = {n: orc.encode(orc.Q2_K, d) for n, d in cases.items()}
     for bad in ({"rmin": -0.4}, {"rdelta": 0.11}, {"nstep": 14}, {"clamp_min": False}, {"moving_min": False}):
         assert any(not np.array_equal(want[n], q2k_encode_np(d, **bad)) for n, d in cases.items()), bad
+
+
+# ---- Q2_K pinned by what the mathematics fixes, not by a second statement of the search ----
+
+def q2k_fit_violations(x, scale, neg_min, levels):
+    """Sub-blocks [S, 16] whose (scale, min, levels) break what make_qkx2_quants promises
+    (q2k.rs:24-93), judged in float64 from the definitions alone:
+    - a flat sub-block (max == min) gets scale 0 and levels 0;
+    - otherwise (scale, min) is either the first candidate, the grid spanning [min(x, 0), max]
+      (scale (max - min) / 3), or the |x|-weighted least-squares fit of x by scale * l + min over
+      the returned levels, with the min clamped to 0 (and the scale refitted) when the fit's min
+      is positive, to 1e-4 of the grid step (f32 sums of 16 terms);
+    - its |x|-weighted absolute deviation is no larger than the first candidate's (up to the f32
+      rounding of the scale and min).
+    Returns the indices of the failing sub-blocks."""
+    x = np.asarray(x, np.float64)
+    s = np.asarray(scale, np.float64)
+    m = -np.asarray(neg_min, np.float64)
+    lq = np.asarray(levels, np.float64)
+    bad = []
+    for i in range(x.shape[0]):
+        xi, li = x[i], lq[i]
+        mn, mx = min(xi.min(), 0.0), xi.max()
+        if mx == mn:
+            if s[i] != 0 or li.any():
+                bad.append(i)
+            continue
+        step = (mx - mn) / 3
+        w = np.abs(xi)
+        first_l = np.clip(np.rint((xi - mn) / step), 0, 3)
+        first_mad = np.sum(w * np.abs(step * first_l + mn - xi))
+        is_first = abs(s[i] - step) <= 1e-6 * step and abs(m[i] - mn) <= 1e-6 * step
+        if not is_first:
+            sw, sx, sl = w.sum(), (w * xi).sum(), (w * li).sum()
+            sl2, sxl = (w * li * li).sum(), (w * li * xi).sum()
+            det = sw * sl2 - sl * sl
+            if det <= 0:
+                bad.append(i)
+                continue
+            fs, fm = (sw * sxl - sx * sl) / det, (sl2 * sx - sl * sxl) / det
+            if fm > 0:
+                fs, fm = sxl / sl2, 0.0
+            if abs(s[i] - fs) > 1e-4 * step or abs(m[i] - fm) > 1e-4 * step:
+                bad.append(i)
+                continue
+        mad = np.sum(w * np.abs(s[i] * li + m[i] - xi))
+        if mad > first_mad * (1 + 1e-5) + 1e-6 * w.sum() * step:  # f32 scale and min roundings
+            bad.append(i)
+    return bad
+
+
+def q2k_block_violations(data, blob, scale, neg_min):
+    """Super-blocks whose bytes break the packing rules (q2k.rs:96-150), in float64: the 4-bit
+    scale (min) codes are the nearest integers to 15 * scale_j / max_scale (min_j / max_min), the
+    f16 super scale is max_scale / 15 rounded to f16, and every level is the nearest of 0..3 to
+    (x + dmin * m_j) / (d * s_j), the decoder's own sub-block scale and min (clamped at the ends),
+    wherever that scale is not 0."""
+    x = np.asarray(data, np.float64).reshape(-1, 256)
+    raw = np.asarray(blob, np.uint8).reshape(-1, 84)
+    sc, mi = np.asarray(scale, np.float64).reshape(-1, 16), np.asarray(neg_min, np.float64).reshape(-1, 16)
+    bad = []
+    for b in range(x.shape[0]):
+        codes = raw[b, :16]
+        d = float(raw[b, 80:82].copy().view(np.float16)[0])
+        dmin = float(raw[b, 82:84].copy().view(np.float16)[0])
+        ok = True
+        for vals, nib, sup in ((sc[b], codes & 15, d), (mi[b], codes >> 4, dmin)):
+            top = max(0.0, vals.max())
+            if top > 0:
+                ok &= bool(np.all(np.abs(15 * vals / top - nib) <= 0.5 + 1e-6))
+                ok &= float(np.float16(np.float32(top / 15))) == sup
+            else:
+                ok &= bool(np.all(nib == 0)) and sup == 0
+        q = raw[b, 16:80]
+        lv = np.empty(256, np.int64)
+        for h in range(2):
+            for j in range(4):
+                lv[128 * h + 32 * j:128 * h + 32 * j + 32] = (q[32 * h:32 * h + 32] >> (2 * j)) & 3
+        for j in range(16):
+            s_ = d * float(codes[j] & 15)
+            if s_ == 0:
+                continue
+            t = (x[b, 16 * j:16 * j + 16] + dmin * float(codes[j] >> 4)) / s_
+            L = lv[16 * j:16 * j + 16]
+            near = np.abs(t - L) <= 0.5 + 1e-6 * np.maximum(1, np.abs(t))
+            ok &= bool(np.all(near | ((L == 0) & (t < 0)) | ((L == 3) & (t > 3))))
+        if not ok:
+            bad.append(b)
+    return bad
+
+
+def oracle_q2k_fits(orc, data):
+    subs = np.asarray(data, np.float32).reshape(-1, 16)
+    out = [orc.q2k_fit(s) for s in subs]
+    return (subs, np.array([o[0] for o in out], np.float32), np.array([o[1] for o in out], np.float32),
+            np.stack([o[2] for o in out]))
+
+
+@pytest.mark.parametrize("name", list(q2k_cases()))
+def test_q2k_oracle_meets_the_least_squares_and_packing_rules(orc, name):
+    data = q2k_cases()[name]
+    subs, sc, mn, lv = oracle_q2k_fits(orc, data)
+    assert q2k_fit_violations(subs, sc, mn, lv) == [], name
+    assert q2k_block_violations(data, orc.encode(orc.Q2_K, data), sc, mn) == [], name
+
+
+def test_q2k_rules_catch_planted_mistakes(orc):
+    """Misreadings that a second statement of the search could share, each planted in the numpy
+    restatement: the fit unweighted (w = 1), the worse candidate kept, the min clamp dropped, the
+    min's sign flipped, and the levels left on the search grid instead of re-fitted to the rounded
+    scales. Each breaks the rules above on the cases."""
+    cases = q2k_cases()
+    both = np.concatenate([cases["normal"], cases["heavy"], cases["positive"], cases["mixed"]])
+    subs = both.reshape(-1, 16)
+    for bad in ({"unit_weights": True}, {"keep_worse": True}, {"clamp_min": False}):
+        sc, mn, lv = q2k_fit_np(subs, **bad)
+        assert len(q2k_fit_violations(subs, sc, mn, lv)) > 0, bad
+    sc, mn, lv = q2k_fit_np(subs)
+    assert q2k_fit_violations(subs, sc, mn, lv) == []
+    assert len(q2k_fit_violations(subs, sc, -mn, lv)) > 0
+    blob = q2k_encode_np(both, requant=False)
+    assert len(q2k_block_violations(both, blob, sc, mn)) > 0
+    assert q2k_block_violations(both, q2k_encode_np(both), sc, mn) == []
 
 
 # ---- read-only block types (blocks/tests.rs) ----
