@@ -41,6 +41,7 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float half_to_float(uint32_t h) {
@@ -825,9 +826,367 @@ hipError_t run_gemm_precise(hipStream_t s, const _Float16 *xs, const uint8_t *qs
     return hipGetLastError();
 }
 
+// ---- the precise GEMM on a streaming 256 x 256 skeleton (products with at least 128 such tiles) ----
+// Same numerics as gemm_precise_kernel (per 32 x 32 tile and block P = hi q + lo q on four
+// v_mfma_f32_32x32x16_f16, then acc += d P), on gemm_f16_big_kernel's structure: eight wavefronts
+// per CTA (two per SIMD), one CTA per CU working through its tiles as one stream of stages, so the
+// next tile's first stages are loaded while the current one finishes and a tile's output stores
+// drain during the next one. A stage is one block (32 k).
+//
+// Every operand goes from memory straight into LDS (buffer loads with the LDS destination, no
+// registers), two stages ahead: x's hi and lo rows (128 bytes per row, 32 KB per stage) into a
+// ring of three buffers; the block's packed quants (16 or 32 bytes per column) and the dwords
+// holding its scales into a ring of two. At the top of stage p the quants of stage p + 1 are
+// unpacked once, LDS to LDS, into exact f16 integers (and the scales to f32), double-buffered.
+// One barrier per stage. A wavefront owns a 64 x 128 part (2 x 4 tiles): per stage eight 16-byte
+// x reads and two weight reads per column tile feed 32 MFMAs.
+//
+// The loads are inline assembly with explicit s_waitcnt: the compiler's own wait insertion could
+// not tell the LDS-destination loads apart and drained every load in flight at each barrier
+// (one stage of lookahead instead of two), and a register destination written behind the
+// compiler's back was copied before its data arrived. Per wave the loads go out as weights(p + 2)
+// then x(p + 2) (four instructions) in stage p, so at the top of stage p + 1 waiting until at most
+// four loads are outstanding (loads complete in order) leaves weights(p + 2) and x(p + 1) in LDS;
+// the barrier then covers every wave's share.
+//
+// x rows in LDS are 128 bytes without padding; the 16-byte chunk c of row r sits at position
+// c ^ (r % 8), so the 32 rows a fragment read touches spread over the banks (each wave's load
+// instruction fills 1 KB of LDS, eight whole rows, choosing per lane which chunk it fetches).
+constexpr int kSB = 40;  // LDS halves per weight column and stage: 32 + 8 pad (80 B)
+
+// 2 quant dwords of a Q4_0 block (dwords 2h, 2h + 1) -> positions 16 h .. 16 h + 15 as exact f16
+__device__ __forceinline__ void unpack_q4_half(uint32_t w0, uint32_t w1, u32x4 &o0, u32x4 &o1) {
+    const uint32_t w[2] = {w0, w1};
+    u32x4 o[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        o[i][0] = f16x2_add((w[i] & 0x000f000fu) | 0x64006400u, (_Float16)-1032.0f);
+        o[i][1] = f16x2_add(((w[i] >> 8) & 0x000f000fu) | 0x64006400u, (_Float16)-1032.0f);
+        o[i][2] = f16x2_add(((w[i] >> 4) & 0x000f000fu) | 0x64006400u, (_Float16)-1032.0f);
+        o[i][3] = f16x2_add(((w[i] >> 12) & 0x000f000fu) | 0x64006400u, (_Float16)-1032.0f);
+    }
+    o0 = o[0];
+    o1 = o[1];
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// A raw buffer descriptor in scalar registers over [base, base + bytes) (the make_rsrc layout).
+__device__ __forceinline__ i32x4 sgpr_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    return i32x4{__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a),
+                 __builtin_amdgcn_readfirstlane((int32_t)((uint32_t)(a >> 32) & 0xffffu)),
+                 __builtin_amdgcn_readfirstlane((int32_t)bytes), 0x00020000};
+}
+// 16 (4) bytes per lane from r at voff into LDS at lds + 16 (4) * lane; lds wave-uniform. An M0
+// write needs one wait state before a load that reads it.
+__device__ __forceinline__ void asm_load_lds16(i32x4 r, uint32_t lds, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff),
+                 "s"(r)
+                 : "m0");
+}
+__device__ __forceinline__ void asm_load_lds4(i32x4 r, uint32_t lds, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
+                 : "m0");
+}
+
+template <int KIND>
+struct StreamLds {  // byte offsets of the rings inside the kernel's LDS arena
+    static constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
+    static constexpr uint32_t A = 0, A_SZ = 256 * 128;                      // x: three stages
+    static constexpr uint32_t W = 3 * A_SZ, W_Q = 256 * QB, W_SZ = W_Q + 1024;  // raw weights: two
+    static constexpr uint32_t B = W + 2 * W_SZ, B_SZ = 256 * kSB * 2;      // unpacked weights: two
+    static constexpr uint32_t D = B + 2 * B_SZ, D_SZ = 1024;                // f32 scales: two
+    static constexpr uint32_t TOTAL = D + 2 * D_SZ;
+};
+
+template <int KIND>
+__global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Float16 *__restrict__ xs,
+                                                                     const uint8_t *__restrict__ qs,
+                                                                     const uint16_t *__restrict__ ds,
+                                                                     float *__restrict__ y, uint32_t M, uint32_t K,
+                                                                     uint32_t N, uint32_t mt, uint32_t nt,
+                                                                     uint32_t split_stages) {
+    using S = StreamLds<KIND>;
+    constexpr uint32_t QB = S::QB;
+    __shared__ __attribute__((aligned(1024))) uint8_t arena[S::TOTAL];
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t *)arena;
+
+    // This CTA's tiles, as gemm_f16_big_kernel deals them: XCD x (blockIdx.x % 8) owns the x-th
+    // equal run of a grouped tile order (groups of eight row tiles) and its CTAs take the run's
+    // tiles round robin.
+    constexpr uint32_t GM = 8;
+    const uint32_t tiles = mt * nt, per_xcd = (tiles + 7) / 8, ctas = gridDim.x / 8;
+    const uint32_t run0 = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8, run1 = min(tiles, (blockIdx.x % 8 + 1) * per_xcd);
+    if (run0 >= run1) return;  // whole CTA: no barrier is left waiting
+    const uint32_t my_tiles = (run1 - run0 + ctas - 1) / ctas;
+    auto origin = [&](uint32_t k, uint32_t &m0, uint32_t &n0) {  // row and column of my k-th tile
+        const uint32_t t = run0 + k * ctas;
+        const uint32_t grp = t / (GM * nt), in = t % (GM * nt), gm = min(GM, mt - grp * GM);
+        m0 = (grp * GM + in % gm) * 256;
+        n0 = (in / gm) * 256;
+    };
+
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, wm = wave % 4, wn = wave / 4;
+    const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t nb = K / 32;
+    const uint32_t st0 = blockIdx.y * split_stages, st1 = min(nb, st0 + split_stages);
+    const uint32_t stream = my_tiles * split_stages;  // positions p: tile p / split_stages, block st0 + p % split_stages
+    y += (size_t)blockIdx.y * M * N;
+    const int fr = lane % 32, hf = lane / 32;
+
+    // The stage whose loads go out next (block lb of tile lt at (lm0, ln0)), advanced once per
+    // stage; the tile origin is recomputed only when the tile changes. A stage past the split or
+    // the stream loads through empty buffer resources (zeros); rows past M and columns past the
+    // padded weight rows fall past their resource's end by their offsets alone.
+    uint32_t lb = st0, lt = 0, lm0, ln0;
+    origin(0, lm0, ln0);
+    auto advance = [&]() {
+        if (++lb == st0 + split_stages) {
+            lb = st0;
+            ++lt;
+            origin(min(lt, my_tiles - 1), lm0, ln0);
+        }
+    };
+    // x: load instruction i of wave w fills rows 32 w + 8 i .. + 7 (1 KB); lane l fetches row
+    // 32 w + 8 i + l / 8's chunk (l % 8) ^ (l / 8), landing at position l % 8 of the row
+    const uint32_t xrow = 32 * wave + lane / 8, xchunk = ((lane % 8) ^ (lane / 8)) * 16;
+    auto dma_x = [&](uint32_t ring) {
+        const bool live = lt < my_tiles && lb < st1;
+        const i32x4 r = sgpr_rsrc(xs, live ? M * nb * 128 : 0u);
+        const uint32_t base = ((lm0 + xrow) * nb + lb) * 128 + xchunk;
+        const uint32_t lds = lds0 + S::A + ring * S::A_SZ + wave_u * 32 * 128;
+#pragma unroll
+        for (int i = 0; i < 4; i++) asm_load_lds16(r, lds + 8 * i * 128, base + 8 * i * nb * 128);
+    };
+    // weights: the block's quants of 256 columns as they lie in the tile plane (QB bytes per
+    // column, a group of 32 columns contiguous), one 1 KB load per wave (Q4_0: waves 0-3); the
+    // scale dwords (the pair of blocks b & ~1, b | 1 of each column, scale_slot's runs of eight),
+    // one 256-byte load per wave 4-7
+    auto dma_w = [&](uint32_t ring) {
+        const bool live = lt < my_tiles && lb < st1;
+        const uint32_t lds = lds0 + S::W + ring * S::W_SZ;
+        if (KIND == FH_Q8_0 || wave_u < 4) {
+            const i32x4 rq = sgpr_rsrc(qs, live ? (N + 31) / 32 * 32 * nb * QB : 0u);
+            // Q8_0: wave w, columns 32 w + lane / 2 (half lane % 2); Q4_0: columns 64 w + lane
+            const uint32_t g = KIND == FH_Q8_0 ? ln0 / 32 + wave_u : ln0 / 32 + 2 * wave_u + lane / 32;
+            const uint32_t r = KIND == FH_Q8_0 ? lane / 2 : lane % 32;
+            const uint32_t off = ((g * nb + lb) * 32 + r) * QB + (KIND == FH_Q8_0 ? (lane % 2) * 16 : 0);
+            asm_load_lds16(rq, lds + wave_u * 1024, off);
+        }
+        if (wave_u >= 4) {
+            const i32x4 rd = sgpr_rsrc(ds, live ? (N + 31) / 32 * 32 * ((nb + 7) / 8 * 8) * 2 : 0u);
+            const uint32_t n = ln0 + 64 * (wave_u - 4) + lane;
+            const uint32_t so = ((n >> 5) * ((nb + 7) / 8) * 32 + (n & 31)) * 16 + (lb / 8) * 512 + (lb % 8) / 2 * 4;
+            asm_load_lds4(rd, lds + S::W_Q + (wave_u - 4) * 256, so);
+        }
+    };
+    // the raw weights of ring slot `ring` (block parity odd) -> exact f16 integers and f32 scales
+    const int cq = tid % 256, hq = tid / 256;
+    auto unpack_w = [&](uint32_t ring, uint32_t odd, uint32_t slot) {
+        const uint8_t *raw = arena + S::W + ring * S::W_SZ;
+        _Float16 *col = (_Float16 *)(arena + S::B + slot * S::B_SZ) + cq * kSB + 16 * hq;
+        u32x4 o[2];
+        if constexpr (KIND == FH_Q8_0) {
+            unpack_q8(*(const u32x4 *)(raw + cq * 32 + hq * 16), o);
+        } else {
+            const u32x2 v = *(const u32x2 *)(raw + cq * 16 + hq * 8);
+            unpack_q4_half(v[0], v[1], o[0], o[1]);
+        }
+        *(u32x4 *)col = o[0];
+        *(u32x4 *)(col + 8) = o[1];
+        if (hq == 0) {
+            const uint32_t dd = *(const uint32_t *)(raw + S::W_Q + cq * 4);
+            ((float *)(arena + S::D + slot * S::D_SZ))[cq] = half_to_float(odd ? dd >> 16 : dd & 0xffffu);
+        }
+    };
+
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    // x fragments of a stage: row tile i, k16 step s, hi and lo (logical chunks hf + 2 s and
+    // 4 + hf + 2 s of the lane's row)
+    f16x8 ah[2][2], al[2][2];
+    auto read_a = [&](uint32_t ring) {
+        const uint8_t *sa = arena + S::A + ring * S::A_SZ;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t r = wm * 64 + i * 32 + fr;
+            const uint8_t *row = sa + r * 128;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) {
+                ah[i][s2] = *(const f16x8 *)(row + (((hf + 2 * s2) ^ (r % 8)) * 16));
+                al[i][s2] = *(const f16x8 *)(row + (((4 + hf + 2 * s2) ^ (r % 8)) * 16));
+            }
+        }
+    };
+    // Per stage the eight tiles (column tile j = t / 2, row tile i = t % 2) run as a software
+    // pipeline over two block-product registers: tile t's four MFMAs (a dependent chain) are each
+    // followed by four of tile t - 1's sixteen scale FMAs, which fill the chain's latency; the
+    // next column tile's weight fragments and scale are read one tile ahead. Scheduling barriers
+    // keep that order (left alone, the compiler started all eight products at once and spilled,
+    // or put the FMAs of tile t - 1 right behind the last MFMA they wait for).
+    auto compute = [&](uint32_t slot) {
+        const _Float16 *bp = (const _Float16 *)(arena + S::B + slot * S::B_SZ) + (wn * 128 + fr) * kSB + 8 * hf;
+        const float *dp = (const float *)(arena + S::D + slot * S::D_SZ) + wn * 128 + fr;
+        f32x16 p[2];
+        f16x8 bq[2][2];
+        float dq[2];
+        bq[0][0] = *(const f16x8 *)bp;
+        bq[0][1] = *(const f16x8 *)(bp + 16);
+        dq[0] = dp[0];
+#pragma unroll
+        for (int t = 0; t <= 8; t++) {
+            const int j = t / 2, i = t % 2, tp = t - 1, jp = tp / 2, ip = tp % 2;
+            f32x16 q = {};
+#pragma unroll
+            for (int s4 = 0; s4 < 4; s4++) {
+                if (t < 8) {
+                    const f16x8 a = s4 < 2 ? ah[i][s4] : al[i][s4 - 2];
+                    q = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bq[j % 2][s4 % 2], q, 0, 0, 0);
+                }
+                if (t > 0) {
+#pragma unroll
+                    for (int r = 4 * s4; r < 4 * s4 + 4; r++)
+                        acc[ip][jp][r] = fmaf(dq[jp % 2], p[tp % 2][r], acc[ip][jp][r]);
+                }
+            }
+            if (t < 8) p[t % 2] = q;
+            if (t < 6 && i == 0) {  // column tile j + 1's fragments (bq[(j + 1) % 2] was last used by tile t - 1)
+                bq[(j + 1) % 2][0] = *(const f16x8 *)(bp + (j + 1) * 32 * kSB);
+                bq[(j + 1) % 2][1] = *(const f16x8 *)(bp + (j + 1) * 32 * kSB + 16);
+            }
+            if (t < 6 && i == 1) dq[(j + 1) % 2] = dp[(j + 1) * 32];  // (dq[(j + 1) % 2]'s last FMA was at t - 1)
+            if (t > 0) asm volatile("" : "+v"(acc[ip][jp]));  // the FMAs stay here (not sunk below later products)
+#pragma unroll
+            for (int s4 = 0; s4 < 4; s4++) {
+                if (t < 8) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of tile t
+                if (t > 0) __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four FMAs of tile t - 1
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    uint32_t ct = 0;  // the tile being computed
+    auto epilogue = [&]() {
+        uint32_t m0, n0;
+        origin(ct++, m0, n0);
+        // D layout of a 32x32 tile: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * hf + r % 4;
+                if (row >= M) continue;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t col = n0 + wn * 128 + j * 32 + fr;
+                    if (col < N) y[(size_t)row * N + col] = acc[i][j][r];
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    };
+
+    // prologue: stages 0 and 1 requested, stage 0's weights unpacked
+    uint32_t par = lb & 1;  // block parity of the stage whose weights are unpacked next
+    dma_w(0);
+    dma_x(0);
+    advance();
+    dma_w(1);
+    dma_x(1);
+    advance();
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // weights(0): x(0), weights(1), x(1) came after
+    __syncthreads();
+    unpack_w(0, par, 0);
+    par = st0 + 1 < st0 + split_stages ? (st0 + 1) & 1 : st0 & 1;
+    uint32_t ra = 0, rw = 1;  // the x ring slot of stage p; the weights ring slot of stage p + 1
+    for (uint32_t p = 0; p < stream; p++) {
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // x(p) and weights(p + 1) are in
+        __syncthreads();
+        // weights(p + 1) unpacked into slot (p + 1) % 2 (last read in stage p - 1)
+        unpack_w(rw, par, (p + 1) & 1);
+        const uint32_t bp1 = st0 + (p + 2) % split_stages;  // the block of stage p + 2
+        par = bp1 & 1;
+        dma_w(rw ^ 1);  // weights(p + 2) into the raw slot unpacked in stage p - 1
+        dma_x(ra == 0 ? 2 : ra - 1);  // x(p + 2) into the slot last read in stage p - 1
+        advance();
+        read_a(ra);
+        compute(p & 1);
+        if ((p + 1) % split_stages == 0) epilogue();  // the tile's last stage
+        ra = ra == 2 ? 0 : ra + 1;
+        rw ^= 1;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (the last loads, past the stream, read zeros)
+}
+
+// The streaming kernel's plan: taken when the product has at least 128 tiles of 256 x 256; the K
+// split (at most 4, at least 16 blocks per split) that best fills whole rounds of one CTA per CU.
+bool stream_plan(size_t rows, size_t k, size_t n, uint32_t *splits) {
+    const uint64_t tiles = (uint64_t)((rows + 255) / 256) * ((n + 255) / 256);
+    if (tiles < 128) return false;
+    const uint32_t stages = (uint32_t)(k / 32), cus = 256;
+    uint32_t best = 1;
+    double best_eff = 0.0;
+    for (uint32_t sp = 1; sp <= 4 && (sp == 1 || stages / sp >= 16); sp++) {
+        const uint64_t ctas = tiles * sp, rounds = (ctas + cus - 1) / cus;
+        const double eff = (double)ctas / (double)(rounds * cus) - 0.04 * (sp - 1);  // the reduce pass
+        if (eff > best_eff + 1e-9) {
+            best_eff = eff;
+            best = sp;
+        }
+    }
+    *splits = best;
+    return true;
+}
+
+bool stream_supported(size_t rows, size_t k, size_t n) {
+    // every byte offset a CTA forms (columns up to the last tile's end) fits the 32-bit offsets
+    const size_t lim = (size_t)1 << 31;
+    return (rows + 255) * k * 4 < lim && (n + 255) * (k / 32) * 32 < lim;
+}
+
+template <int KIND>
+hipError_t run_gemm_stream_precise(hipStream_t s, const _Float16 *xs, const uint8_t *qs, const uint16_t *ds,
+                                   float *y, float *partial, uint32_t M, uint32_t K, uint32_t N, uint32_t sp,
+                                   SplitOut *defer) {
+    const uint32_t mt = (M + 255) / 256, nt = (N + 255) / 256;
+    const uint64_t tiles = (uint64_t)mt * nt;
+    if (tiles > 0x7ffffff0ull) return hipErrorInvalidValue;
+    const uint32_t per_xcd = (uint32_t)((tiles + 7) / 8);
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8)
+        cus = 256;
+    const uint32_t ctas = min(per_xcd, (uint32_t)cus / 8);
+    const uint32_t stages = K / 32;
+    const uint32_t per = (stages + sp - 1) / sp;
+    float *out = sp > 1 ? partial : y;
+    gemm_stream_precise_kernel<KIND><<<dim3(8 * ctas, sp), 512, 0, s>>>(xs, qs, ds, out, M, K, N, mt, nt, per);
+    if (defer) *defer = sp > 1 ? SplitOut{partial, sp} : SplitOut{y, 1u};
+    if (sp > 1 && !defer) {
+        const size_t n = (size_t)M * N;
+        const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
+        gemm_reduce_kernel<<<rg, 256, 0, s>>>(partial, y, n, sp);
+    }
+    return hipGetLastError();
+}
+
 template <int KIND>
 hipError_t gemm_precise_dispatch(hipStream_t s, const _Float16 *xs, const uint8_t *qs, const uint16_t *ds, float *y,
                                  float *partial, uint32_t M, uint32_t K, uint32_t N, SplitOut *defer) {
+    uint32_t sp = 1;
+    if (stream_plan(M, K, N, &sp) && stream_supported(M, K, N) && (sp == 1 || partial))
+        return run_gemm_stream_precise<KIND>(s, xs, qs, ds, y, partial, M, K, N, sp, defer);
     if (M <= 32) return run_gemm_precise<KIND, 32, 256, 1>(s, xs, qs, ds, y, partial, M, K, N, defer);
     if (M <= 64) return run_gemm_precise<KIND, 64, 128, 2>(s, xs, qs, ds, y, partial, M, K, N, defer);
     return run_gemm_precise<KIND, 128, 128, 2>(s, xs, qs, ds, y, partial, M, K, N, defer);
@@ -1799,16 +2158,17 @@ hipError_t launch_make_b8(hipStream_t s, fh_kind kind, const uint8_t *qs, const 
 
 // x split into f16 pairs (4 bytes per element), then the K-split partial products (256-aligned)
 size_t gemm_precise_workspace_bytes(size_t rows, size_t k, size_t n) {
-    const uint32_t sp = precise_splits(rows, k, n);
+    uint32_t sp = precise_splits(rows, k, n), ssp = 1;
+    if (stream_plan(rows, k, n, &ssp) && stream_supported(rows, k, n)) sp = max(sp, ssp);
     return (rows * k * 4 + 255) / 256 * 256 + (sp > 1 ? (size_t)sp * rows * n * 4 : 0);
 }
 
 hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const float *x,
                                float *y, size_t rows, size_t k, size_t n, void *workspace, SplitOut *defer) {
     _Float16 *xs = (_Float16 *)workspace;
-    float *partial = precise_splits(rows, k, n) > 1
-                         ? (float *)((uint8_t *)workspace + (rows * k * 4 + 255) / 256 * 256)
-                         : nullptr;
+    const size_t xbytes = (rows * k * 4 + 255) / 256 * 256;
+    float *partial = gemm_precise_workspace_bytes(rows, k, n) > xbytes ? (float *)((uint8_t *)workspace + xbytes)
+                                                                       : nullptr;
     const size_t items = rows * (k / 32);
     const unsigned g = (unsigned)(items / 32 + 1 < 65535 ? items / 32 + 1 : 65535);
     if (kind == FH_Q8_0) {
