@@ -576,6 +576,49 @@ def bench_codec(fh, g, ev, reps=5, copies=8):
     return out
 
 
+def compact(extra):
+    """One number per configuration for the final JSON line (the driver keeps only the tail of
+    stdout, so the line stays under 4 kB); the full detail goes to stderr as `bench detail:`."""
+    def pick(key, *fields):
+        d = extra.get(key)
+        if not isinstance(d, dict):
+            return None
+        return {f: d[f] for f in fields if f in d} or None
+
+    out = {"q8_0_gemv_768x2304_pool": pick("q8_0_gemv_768x2304", "gbs", "frac")}
+    gemm = {}  # TFLOP/s per path (fast = QPath.TiledFast, precise = QPath.Tiled, f16 = QPath.TiledF16)
+    for name in ("q4_0_gemm_llama1b", "q8_0_gemm_llama1b", "q4_0_gemm_qwen"):
+        for m in (512, 2048, 4096):
+            row = {}
+            for tag, label in (("", "fast"), ("_precise", "precise"), ("_f16", "f16")):
+                d = extra.get(f"{name}{tag}_m{m}")
+                if isinstance(d, dict):
+                    row[label] = round(d["tflops"], 1)
+                    if d.get("outside_bound_frac"):
+                        row[label + "_outside_bound"] = d["outside_bound_frac"]
+            if row:
+                gemm[f"{name[:4]}_{name.split('_')[-1]}_m{m}"] = row
+    out["gemm_tflops"] = gemm or None
+    for tag in ("q4_0", "q8_0"):
+        for m in (8, 64):
+            v = pick(f"{tag}_gemm_llama1b_m{m}", "gbs", "frac_hbm", "single_calls_gbs")
+            if v:
+                out[f"{tag}_rows_llama1b_m{m}"] = v
+    sc = extra.get("qwen2_0_5b_q4_0_scoring")
+    if isinstance(sc, dict):
+        out["qwen2_0_5b_scoring_ms"] = {k: v["ms"] for k, v in sc.items() if isinstance(v, dict) and "ms" in v}
+        out["qwen2_0_5b_scoring_logprob_rel_err_vs_cpu"] = {
+            k.split("_")[0]: v for k, v in sc.items() if k.endswith("logprob_rel_err_vs_cpu")}
+    dec = extra.get("gpt2_small_q8_0_decode")
+    if isinstance(dec, dict):
+        out["gpt2_small_q8_0_decode"] = {k: dec[k] for k in ("tok_s", "ms_per_step", "weight_gbs", "cpu_tok_s")
+                                         if k in dec}
+    codec = extra.get("codec_llama1b")
+    if isinstance(codec, dict) and isinstance(codec.get("qat_fake_quant_pass_llama1b"), dict):
+        out["qat_fake_quant_pass_llama1b_gbs"] = codec["qat_fake_quant_pass_llama1b"].get("gbs")
+    return {k: v for k, v in out.items() if v is not None}
+
+
 def host_info():
     """The host's core count and CPU model (for the CPU baseline's report)."""
     model = "unknown"
@@ -836,9 +879,10 @@ def main():
                      for L in head["launches"]],
         "cpu_baseline": cpu and {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample", "host_nproc",
                                                      "host_cpu_model")},
-        "extra": extra,
+        "extra": compact(extra),
         "hbm_copy_gbs": round(copy["gbs"], 1),
     }
+    log("bench detail: " + json.dumps(extra))
     print(json.dumps(out))
     g.close()
 
