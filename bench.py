@@ -272,6 +272,56 @@ def bench_single_calls(fh, g, ev, kind, shapes, reps=3, seed=4):
     return out
 
 
+CHOOSE_MS = (2, 4, 8, 16, 24, 32, 48, 64, 96, 128)
+
+
+def bench_choose_sweep(fh, g, ev, shapes, kinds, ms=CHOOSE_MS, pool_bytes=256e6, reps=3, seed=9):
+    """The measurement behind fh_choose's few-row / GEMM boundary (ferrum_wgpu/src/ops/quant.rs:
+    303-323 says its thresholds must be re-measured per adapter): one linear_q per product, the
+    few-row kernel (QPath.Rows, up to 64 rows) against the precise MFMA GEMM (QPath.Tiled) and the
+    library's own choice (QPath.Auto), at each row count, over enough distinct weight copies
+    (about `pool_bytes`) that every call reads its weight from HBM. Microseconds per call, the
+    median of `reps` passes over the copies."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for kind in kinds:
+        for k, n in shapes:
+            w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+            data = fh.upload_quantised(g, kind, w, k, n).read_gguf()
+            copies = max(2, int(pool_bytes // data.size))
+            qs = [fh.upload_qweight(g, kind, data, k, n) for _ in range(copies)]
+            for m in ms:
+                xs = [g.upload(rng.standard_normal(m * k).astype(np.float32)) for _ in range(copies)]
+                ys = [g.zeros(m * n) for _ in range(copies)]
+                row = {"auto": fh.choose(m, kind, k, n).name}
+                for path in (fh.QPath.Rows, fh.QPath.Tiled, fh.QPath.Auto):
+                    if path == fh.QPath.Rows and m > 64:
+                        continue
+                    for i in range(copies):
+                        fh.linear_q_with(g, xs[i], qs[i], ys[i], m, path)
+                    g.sync()
+                    times = []
+                    for _ in range(reps):
+                        e0, e1 = ev.create(2)
+                        ev.record(e0)
+                        for i in range(copies):
+                            fh.linear_q_with(g, xs[i], qs[i], ys[i], m, path)
+                        ev.record(e1)
+                        g.sync()
+                        times.append(ev.ms(e0, e1) * 1e3 / copies)
+                        ev.destroy([e0, e1])
+                    row[path.name.lower() + "_us"] = round(float(np.median(times)), 2)
+                best = min(v for key, v in row.items() if key in ("rows_us", "tiled_us"))
+                row["auto_over_best"] = round(row["auto_us"] / best, 3)
+                out[f"{kind.label()} {k}x{n} M={m}"] = row
+                log(f"choose sweep {kind.label()} {k}x{n} M={m}: {row}")
+                for b in xs + ys:
+                    b.free()
+            for q in qs:
+                q.free()
+    return out
+
+
 def bench_ext_gemm(fh, g, ev, kinds, cases, reps=5, seed=6):
     """Multi-row products on the other weight formats through linear_q (QPath.Tiled: the MFMA GEMM
     on the GGUF rows, x split included): TFLOP/s per (format, M, K, N)."""
@@ -701,6 +751,9 @@ def main():
                     help="only config 5's grouped few-row products (M = 8, 64), one JSON line (for profiling)")
     ap.add_argument("--ext-only", action="store_true",
                     help="only the one-row GEMV on the other weight formats (F16, FP8, MXFP4, Q2_K), one JSON line")
+    ap.add_argument("--choose-sweep", action="store_true",
+                    help="only the few-row kernel against the precise GEMM, one linear_q per product, M = 2..128 "
+                         "at the config 2 and config 5 shapes (the measurement behind fh_choose)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the scoring GEMM at the TinyLlama-1.1B shapes, M = 4096, one JSON line (for profiling)")
     a = ap.parse_args()
@@ -751,6 +804,13 @@ def main():
         print(json.dumps({"metric": "one-row GEMV GB/s on the other weight formats, 8192 x 8192",
                           "value": ext["MXFP4"]["8192x8192"]["gbs"], "unit": "GB/s", "n_gpus": 1,
                           "higher_is_better": True, "detail": ext, "gemm": gemm}))
+        g.close()
+        return
+    if a.choose_sweep:
+        r = bench_choose_sweep(fh, g, ev, QWEN_SHAPES + LLAMA1B_SHAPES, (fh.QKind.Q4_0, fh.QKind.Q8_0))
+        worst = max(v["auto_over_best"] for v in r.values())
+        print(json.dumps({"metric": "fh_choose: worst ratio of AUTO's time to the faster path's", "value": worst,
+                          "unit": "ratio", "n_gpus": 1, "higher_is_better": False, "detail": r}))
         g.close()
         return
     if a.gemm_only:

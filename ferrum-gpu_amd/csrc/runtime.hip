@@ -659,11 +659,21 @@ fh_status fh_qweight_dequantise(fh_device *dev, const fh_qweight *w, fh_buffer *
 
 // ---- linear layers ----
 
+// The few-row / GEMM boundary, measured on one MI355X with one linear_q per product (each call
+// reading its weight from HBM) at the Qwen2-0.5B and TinyLlama-1.1B shapes, Q4_0 and Q8_0, rows
+// 2 to 128. Single calls at these sizes are latency-bound: the MFMA GEMM costs a nearly flat
+// 17-33 us, while the few-row kernel's time steps up with its row capacity class (16, 32, 64)
+// and grows with k. Up to 16 rows the few-row kernel wins everywhere (by 20-45%); from 17 to 32
+// rows while k <= 4864 (at k = 5632 the GEMM is 4-5% faster); from 33 to 64 rows only on the wide,
+// short products (n >= 2560, k <= 2048: 896 x 4864, 2048 x 2560, 2048 x 11264).
 fh_path fh_choose(size_t rows, fh_kind kind, size_t k, size_t n) {
-    (void)n;
     if (ext_kind(kind)) return rows == 1 ? FH_PATH_GEMV : FH_PATH_TILED;
     if (rows == 1 && kind_ok(kind) && gemv_supported(kind, k, n)) return FH_PATH_GEMV;
-    if (rows >= 2 && rows <= kRowsMax && kind_ok(kind) && rows_supported(rows, k, n)) return FH_PATH_ROWS;
+    if (rows >= 2 && rows <= kRowsMax && kind_ok(kind) && rows_supported(rows, k, n)) {
+        if (rows <= 16) return FH_PATH_ROWS;
+        if (rows <= 32) return k <= 4864 ? FH_PATH_ROWS : FH_PATH_TILED;
+        return n >= 2560 && k <= 2048 ? FH_PATH_ROWS : FH_PATH_TILED;
+    }
     return FH_PATH_TILED;
 }
 

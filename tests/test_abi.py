@@ -54,8 +54,11 @@ def test_abi_version_and_host_side_helpers(fh):
 
 def test_choose_rules(fh):
     """The MI355X dispatch (replaces quant.rs:306-323, which was measured on MX330/Xe):
-    one row -> the int8-MFMA GEMV while its 32-bit offsets cover a row (k <= 2^25); 2 to 64 rows
-    -> the few-row kernel (weights streamed once for every row); more rows -> the MFMA GEMM."""
+    one row -> the int8-MFMA GEMV while its 32-bit offsets cover a row (k <= 2^25); 2 to 16 rows
+    -> the few-row kernel; 17 to 32 rows -> the few-row kernel while k <= 4864; 33 to 64 rows ->
+    the few-row kernel only for n >= 2560 and k <= 2048; otherwise the precise MFMA GEMM. The
+    boundary is measured (bench.py --choose-sweep, one linear_q per product at the config 2 and
+    config 5 shapes)."""
     Q8, Q4 = fh.QKind.Q8_0, fh.QKind.Q4_0
     for kind in (Q8, Q4):
         assert fh.choose(1, kind, 768, 2304) == fh.QPath.Gemv
@@ -67,6 +70,14 @@ def test_choose_rules(fh):
         assert fh.choose(2, kind, 768, 2304) == fh.QPath.Rows
         assert fh.choose(8, kind, 5632, 2048) == fh.QPath.Rows
         assert fh.choose(64, kind, 2048, 11264) == fh.QPath.Rows
+        assert fh.choose(16, kind, 5632, 2048) == fh.QPath.Rows
+        assert fh.choose(24, kind, 5632, 2048) == fh.QPath.Tiled
+        assert fh.choose(32, kind, 4864, 896) == fh.QPath.Rows
+        assert fh.choose(48, kind, 4864, 896) == fh.QPath.Tiled
+        assert fh.choose(48, kind, 2048, 2048) == fh.QPath.Tiled
+        assert fh.choose(48, kind, 896, 1152) == fh.QPath.Tiled
+        assert fh.choose(64, kind, 896, 4864) == fh.QPath.Rows
+        assert fh.choose(64, kind, 2048, 2560) == fh.QPath.Rows
         assert fh.choose(65, kind, 2048, 2048) == fh.QPath.Tiled
         assert fh.choose(512, kind, 896, 4864) == fh.QPath.Tiled
 

@@ -170,11 +170,11 @@ LLAMA1B = [(2048, 2560), (2048, 2048), (2048, 11264), (5632, 2048)]
 @pytest.mark.parametrize("m", [8, 64])
 def test_rows_kernel_at_the_tinyllama_shapes(fh, g, orc, kind_name, m):
     """Config 5's few-row products (M = 8, 64) at the TinyLlama-1.1B layer shapes, x ~ N(0, 1),
-    W ~ N(0, 0.02), through AUTO (which picks the few-row kernel)."""
+    W ~ N(0, 0.02), on the few-row kernel (QPath.Rows; at 64 rows AUTO takes it only for the wide
+    products, test_abi.py pins that rule)."""
     kind = fh.QKind[kind_name]
     rng = np.random.default_rng(5 + m)
     for k, n in LLAMA1B:
-        assert fh.choose(m, kind, k, n) == fh.QPath.Rows
         w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
         x = rng.standard_normal(m * k).astype(np.float32)
         b = orc.quantise_matrix(int(kind), w, k, n)
@@ -182,7 +182,7 @@ def test_rows_kernel_at_the_tinyllama_shapes(fh, g, orc, kind_name, m):
         want = orc.matmul_tuned(x, wd, m, k, n, THREADS)
         qw = fh.upload_qweight(g, kind, b, k, n)
         gx, gy = g.upload(x), g.zeros(m * n)
-        fh.linear_q(g, gx, qw, gy, m)
+        fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.Rows)
         got = g.read(gy)
         e = orc.max_rel_err(got, want)
         exact = (x.reshape(m, k).astype(np.float64) @ wd.reshape(k, n).astype(np.float64)).reshape(-1)
