@@ -3,8 +3,10 @@
 // gemv.hip and gemm.hip; this file only validates, accounts and launches.
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <new>
+#include <utility>
 #include <vector>
 
 #include "internal.hpp"
@@ -28,6 +30,54 @@ fh_status fail(fh_status st, const char *fmt, ...) {
     g_err = buf;
     return st;
 }
+
+// Byte ranges [a, a + an) and [b, b + bn) share a byte.
+static bool overlaps(const void *a, size_t an, const void *b, size_t bn) {
+    const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+    return an && bn && a0 < b0 + bn && b0 < a0 + an;
+}
+
+// Grouped launches read every product's x while they write (and, for the few-row kernel, first
+// zero) every product's y, so no x may overlap any y and no two y may overlap. `xs` and `ys` are
+// (address, bytes) per product; returns the product whose range collides, or -1.
+static long plan_overlap(const std::vector<std::pair<uintptr_t, size_t>> &xs,
+                         std::vector<std::pair<uintptr_t, size_t>> ys) {
+    std::vector<size_t> order(ys.size());
+    for (size_t i = 0; i < order.size(); i++) order[i] = i;
+    std::sort(order.begin(), order.end(), [&](size_t a, size_t b) { return ys[a].first < ys[b].first; });
+    for (size_t i = 1; i < order.size(); i++) {
+        const auto &p = ys[order[i - 1]], &q = ys[order[i]];
+        if (p.second && q.second && q.first < p.first + p.second) return (long)order[i];
+    }
+    for (size_t j = 0; j < xs.size(); j++) {
+        const uintptr_t x0 = xs[j].first, x1 = xs[j].first + xs[j].second;
+        // the y range starting last before x's end is the only one that can reach into x
+        size_t lo = 0, hi = order.size();
+        while (lo < hi) {
+            const size_t mid = (lo + hi) / 2;
+            if (ys[order[mid]].first < x1) lo = mid + 1;
+            else hi = mid;
+        }
+        if (lo > 0) {
+            const auto &y = ys[order[lo - 1]];
+            if (xs[j].second && y.second && y.first + y.second > x0) return (long)j;
+        }
+    }
+    return -1;
+}
+
+// Calls of fh_linear_q_noalloc on one GPU share its one scratch array whichever handle (stream)
+// they come through: each call waits for the previous call's work on that GPU (an event per GPU,
+// made when a handle is opened, recorded after each call), so calls through different handles of
+// one GPU do not race on it. Under stream capture no cross-stream wait is recorded (the caller
+// orders the captured work); the event is left alone.
+struct NoallocOrder {
+    std::mutex mu;
+    hipEvent_t ev = nullptr;
+    bool recorded = false;
+};
+static constexpr int kMaxOrdinals = 64;
+static NoallocOrder g_noalloc[kMaxOrdinals];
 
 static bool is_fatal(hipError_t e) {
     switch (e) {
@@ -298,10 +348,20 @@ fh_status fh_device_open(int ordinal, fh_device **out) {
     d->ordinal = ordinal;
     d->cus = prop.multiProcessorCount;
     d->name = prop.name[0] ? prop.name : prop.gcnArchName;
-    // this GPU's copy of the no-allocation scratch (the device is current)
+    // this GPU's copy of the no-allocation scratch (the device is current), and the event that
+    // orders the calls using it
     if ((e = hipGetSymbolAddress(&d->scratch, HIP_SYMBOL(scratch))) != hipSuccess) {
         delete d;
         return hip_fail(nullptr, e, "scratch address");
+    }
+    if (ordinal < kMaxOrdinals) {
+        std::lock_guard<std::mutex> lock(g_noalloc[ordinal].mu);
+        if (!g_noalloc[ordinal].ev &&
+            (e = hipEventCreateWithFlags(&g_noalloc[ordinal].ev, hipEventDisableTiming)) != hipSuccess) {
+            g_noalloc[ordinal].ev = nullptr;
+            delete d;
+            return hip_fail(nullptr, e, "scratch event");
+        }
     }
     if ((e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking)) != hipSuccess) {
         delete d;
@@ -796,6 +856,8 @@ fh_status fh_linear_q(fh_device *dev, const fh_buffer *x, const fh_qweight *w, f
     if (rows > (1u << 24)) return fail(FH_ERR_INVALID, "linear_q: %zu rows is too many", rows);
     if ((st = need("linear_q x", x, rows * w->k))) return st;
     if ((st = need("linear_q y", y, rows * w->n))) return st;
+    if (overlaps(x->ptr, rows * w->k * 4, y->ptr, rows * w->n * 4))
+        return fail(FH_ERR_INVALID, "linear_q: x and y overlap");
     return linear(dev, (const float *)x->ptr, w, (float *)y->ptr, rows, path);
 }
 
@@ -807,6 +869,7 @@ fh_status fh_linear_q_ptr(fh_device *dev, const float *x, const fh_qweight *w, f
     if (rows > (1u << 24)) return fail(FH_ERR_INVALID, "linear_q: %zu rows is too many", rows);
     if (!x) return fail(FH_ERR_INVALID, "linear_q x: null pointer");
     if (!y) return fail(FH_ERR_INVALID, "linear_q y: null pointer");
+    if (overlaps(x, rows * w->k * 4, y, rows * w->n * 4)) return fail(FH_ERR_INVALID, "linear_q: x and y overlap");
     return linear(dev, x, w, y, rows, path);
 }
 
@@ -818,8 +881,24 @@ fh_status fh_linear_q_noalloc(fh_device *dev, const float *x, const fh_qweight *
     if (rows > (1u << 24)) return fail(FH_ERR_INVALID, "linear_q: %zu rows is too many", rows);
     if (!x) return fail(FH_ERR_INVALID, "linear_q x: null pointer");
     if (!y) return fail(FH_ERR_INVALID, "linear_q y: null pointer");
+    if (overlaps(x, rows * w->k * 4, y, rows * w->n * 4)) return fail(FH_ERR_INVALID, "linear_q: x and y overlap");
     if (!dev->scratch) return fail(FH_ERR_DEVICE, "linear_q_noalloc: the device has no scratch address");
-    return linear(dev, x, w, y, rows, path, dev->scratch);
+    if (dev->ordinal >= kMaxOrdinals || !g_noalloc[dev->ordinal].ev)
+        return fail(FH_ERR_DEVICE, "linear_q_noalloc: no scratch order for device %d", dev->ordinal);
+    NoallocOrder &o = g_noalloc[dev->ordinal];
+    std::lock_guard<std::mutex> lock(o.mu);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(dev->stream, &cs) != hipSuccess) cs = hipStreamCaptureStatusNone;
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    hipError_t e;
+    if (!capturing && o.recorded && (e = hipStreamWaitEvent(dev->stream, o.ev, 0)) != hipSuccess)
+        return hip_fail(dev, e, "linear_q_noalloc: wait for the previous call");
+    if ((st = linear(dev, x, w, y, rows, path, dev->scratch))) return st;
+    if (!capturing) {
+        if ((e = hipEventRecord(o.ev, dev->stream)) != hipSuccess) return hip_fail(dev, e, "linear_q_noalloc: order");
+        o.recorded = true;
+    }
+    return FH_OK;
 }
 
 // ---- grouped batch-1 GEMV ----
@@ -856,6 +935,18 @@ fh_status fh_gemv_plan_create(fh_device *dev, const fh_gemv_problem *problems, s
             fh_gemv_plan_free(plan);
             return fail(FH_ERR_INVALID, "gemv plan: problem %zu (%zu x %zu) is too large for one product", i,
                         p.w->n, p.w->k);
+        }
+    }
+    {
+        std::vector<std::pair<uintptr_t, size_t>> xr, yr;
+        for (size_t i = 0; i < count; i++) {
+            xr.emplace_back((uintptr_t)problems[i].x, problems[i].w->k * 4);
+            yr.emplace_back((uintptr_t)problems[i].y, problems[i].w->n * 4);
+        }
+        const long bad = plan_overlap(xr, yr);
+        if (bad >= 0) {
+            fh_gemv_plan_free(plan);
+            return fail(FH_ERR_INVALID, "gemv plan: problem %ld's x or y overlaps another product's y", bad);
         }
     }
     std::vector<GemvDesc> host;
@@ -1006,6 +1097,19 @@ fh_status fh_rows_plan_create(fh_device *dev, const fh_rows_problem *problems, s
     if (count > 65535) {
         fh_rows_plan_free(plan);
         return fail(FH_ERR_INVALID, "rows plan: %zu products, at most 65535 per plan", count);
+    }
+    {
+        std::vector<std::pair<uintptr_t, size_t>> xr, yr;
+        for (size_t i = 0; i < count; i++) {
+            const fh_rows_problem &p = problems[i];
+            xr.emplace_back((uintptr_t)p.x, p.rows * p.w->k * 4);
+            yr.emplace_back((uintptr_t)p.y, p.rows * p.w->n * 4);
+        }
+        const long bad = plan_overlap(xr, yr);
+        if (bad >= 0) {
+            fh_rows_plan_free(plan);
+            return fail(FH_ERR_INVALID, "rows plan: problem %ld's x or y overlaps another product's y", bad);
+        }
     }
     std::vector<RowsDesc> host;
     std::vector<uint32_t> map;

@@ -561,3 +561,32 @@ def test_large_gemv_is_linear_in_x(fh, g, orc):
         outs.append(g.read(gy))
     assert np.max(np.abs(outs[0] + outs[1] - outs[2])) < 1e-4 * max(1, np.abs(outs[2]).max())
     assert np.array_equal(outs[3], 2 * outs[0])
+
+
+def test_overlapping_x_and_y_are_refused(fh, g, orc):
+    """A product reads x while it writes y (the few-row kernel first zeroes y in the launch that
+    splits x, and adds two K halves into it), so x and y may not share a byte: linear_q on one
+    buffer or overlapping pointers, and a grouped plan where one product's x or y overlaps a y,
+    fail with an "overlap" error instead of computing garbage. The wgpu reference cannot bind one
+    buffer as both (a validation error), so this keeps its behaviour."""
+    rng = np.random.default_rng(77)
+    k, n = 256, 256
+    w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+    qw = fh.upload_quantised(g, fh.QKind.Q4_0, w, k, n)
+    buf = g.upload(rng.standard_normal(8 * k).astype(np.float32))
+    with pytest.raises(fh.GpuError, match="overlap"):
+        fh.linear_q(g, buf, qw, buf, 8)
+    p = buf.device_ptr()
+    with pytest.raises(fh.GpuError, match="overlap"):
+        fh.linear_q_ptr(g, p, qw, p + 4 * k * 4, 8, fh.QPath.Rows)
+    xs = [g.upload(rng.standard_normal(k).astype(np.float32)) for _ in range(2)]
+    ys = [g.zeros(n) for _ in range(2)]
+    with pytest.raises(fh.GpuError, match="overlap"):  # product 1 reads what product 0 writes
+        fh.GemvPlan(g, [(qw, xs[0].device_ptr(), ys[0].device_ptr()), (qw, ys[0].device_ptr(), ys[1].device_ptr())])
+    with pytest.raises(fh.GpuError, match="overlap"):  # two products write one y
+        fh.RowsPlan(g, [(qw, xs[0].device_ptr(), ys[0].device_ptr(), 1), (qw, xs[1].device_ptr(), ys[0].device_ptr(), 1)])
+    # shared x is fine (products only read it), and the device still works
+    plan = fh.GemvPlan(g, [(qw, xs[0].device_ptr(), ys[0].device_ptr()), (qw, xs[0].device_ptr(), ys[1].device_ptr())])
+    plan.run()
+    assert np.array_equal(g.read(ys[0]), g.read(ys[1]))
+    plan.free()

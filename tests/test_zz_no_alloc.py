@@ -96,3 +96,41 @@ def test_noalloc_refuses_what_it_cannot_do_without_allocating(fh, g, orc):
     fh.linear_q_noalloc(g, gx.device_ptr(), qw, yb.device_ptr(), 16, fh.QPath.Tiled)
     fh.linear_q_ptr(g, gx.device_ptr(), qw, ya.device_ptr(), 16, fh.QPath.Tiled)
     assert np.array_equal(g.read(ya)[:16 * 256], g.read(yb)[:16 * 256])
+
+
+def test_noalloc_calls_through_two_handles_of_one_gpu_do_not_race(fh, g, orc):
+    """Two handles of one GPU (two streams) share its one scratch array: each noalloc call waits
+    for the previous one's work on that GPU, so interleaved calls through both handles, issued
+    without any synchronisation between them, still equal linear_q_ptr's results bit for bit."""
+    ordinal = int(__import__("os").environ.get("FERRUM_HIP_DEVICE", "0"))
+    g2 = fh.Gpu(ordinal)
+    work = []
+    try:
+        kind = fh.QKind.Q4_0
+        for i, h in enumerate((g, g2, g, g2)):
+            rows, k, n = (256, 2048, 2048) if i % 2 == 0 else (192, 2048, 1024)
+            qw, gx, ya, yb, _ = case(fh, h, orc, kind, rows, k, n, 60 + i, cpu=False)
+            fh.linear_q_ptr(h, gx.device_ptr(), qw, ya.device_ptr(), rows, fh.QPath.Tiled)
+            work.append((h, qw, gx, ya, yb, rows))
+        g.sync()
+        g2.sync()
+        for rep in range(3):
+            for h, qw, gx, _, yb, rows in work:
+                fh.linear_q_noalloc(h, gx.device_ptr(), qw, yb.device_ptr(), rows, fh.QPath.Tiled)
+        g.sync()
+        g2.sync()
+        for i, (h, qw, gx, ya, yb, rows) in enumerate(work):
+            assert np.array_equal(h.read(ya).view(np.uint32), h.read(yb).view(np.uint32)), i
+        say("noalloc through two handles of one GPU: 12 interleaved calls equal linear_q_ptr")
+    finally:
+        for h, qw, gx, ya, yb, rows in work:
+            for b in (gx, ya, yb):
+                b.free()
+            qw.free()
+        g2.close()
+
+
+def test_noalloc_refuses_overlapping_x_and_y(fh, g, orc):
+    qw, gx, ya, yb, _ = case(fh, g, orc, fh.QKind.Q8_0, 8, 256, 256, 9, cpu=False)
+    with pytest.raises(fh.GpuError, match="overlap"):
+        fh.linear_q_noalloc(g, gx.device_ptr(), qw, gx.device_ptr() + 4 * 256, 8, fh.QPath.Rows)
