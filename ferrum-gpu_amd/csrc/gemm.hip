@@ -1032,7 +1032,7 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Floa
     // next column tile's weight fragments and scale are read one tile ahead. Scheduling barriers
     // keep that order (left alone, the compiler started all eight products at once and spilled,
     // or put the FMAs of tile t - 1 right behind the last MFMA they wait for).
-    auto compute = [&](uint32_t slot) {
+    auto compute = [&](uint32_t slot, auto &&hook) {
         const _Float16 *bp = (const _Float16 *)(arena + S::B + slot * S::B_SZ) + (wn * 128 + fr) * kSB + 8 * hf;
         const float *dp = (const float *)(arena + S::D + slot * S::D_SZ) + wn * 128 + fr;
         f32x16 p[2];
@@ -1064,6 +1064,7 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Floa
             }
             if (t < 6 && i == 1) dq[(j + 1) % 2] = dp[(j + 1) * 32];  // (dq[(j + 1) % 2]'s last FMA was at t - 1)
             if (t > 0) asm volatile("" : "+v"(acc[ip][jp]));  // the FMAs stay here (not sunk below later products)
+            hook(t);  // the stage's other work, issued among the MFMAs
 #pragma unroll
             for (int s4 = 0; s4 < 4; s4++) {
                 if (t < 8) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of tile t
@@ -1113,15 +1114,23 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Floa
     for (uint32_t p = 0; p < stream; p++) {
         asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // x(p) and weights(p + 1) are in
         __syncthreads();
-        // weights(p + 1) unpacked into slot (p + 1) % 2 (last read in stage p - 1)
-        unpack_w(rw, par, (p + 1) & 1);
-        const uint32_t bp1 = st0 + (p + 2) % split_stages;  // the block of stage p + 2
-        par = bp1 & 1;
-        dma_w(rw ^ 1);  // weights(p + 2) into the raw slot unpacked in stage p - 1
-        dma_x(ra == 0 ? 2 : ra - 1);  // x(p + 2) into the slot last read in stage p - 1
-        advance();
         read_a(ra);
-        compute(p & 1);
+        // The stage's MFMAs start as soon as its x fragments arrive; the rest of the stage's work
+        // runs among them (issued after tiles 1 and 3): weights(p + 1) unpacked into slot
+        // (p + 1) % 2 (last read in stage p - 1), then weights(p + 2) and x(p + 2) requested into
+        // the raw slot unpacked in stage p - 1 and the x slot last read in stage p - 1. (Before, all
+        // of it ran between the barrier and the first MFMA, while the MFMAs of both wavefronts of
+        // a SIMD waited.)
+        compute(p & 1, [&](int t) {
+            if (t == 1) {
+                unpack_w(rw, par, (p + 1) & 1);
+                par = (st0 + (p + 2) % split_stages) & 1;  // the block parity of stage p + 2
+            } else if (t == 3) {
+                dma_w(rw ^ 1);
+                dma_x(ra == 0 ? 2 : ra - 1);
+                advance();
+            }
+        });
         if ((p + 1) % split_stages == 0) epilogue();  // the tile's last stage
         ra = ra == 2 ? 0 : ra + 1;
         rw ^= 1;
