@@ -1138,6 +1138,310 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Floa
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (the last loads, past the stream, read zeros)
 }
 
+// ---- the scoring GEMM (FH_PATH_TILED_FAST) on the streaming 256 x 256 skeleton ----
+// gemm_kernel's numerics (x = hi + lo: hi in f16 times the exact f16 integer quants on
+// v_mfma_f32_32x32x16_f16 with acc += d P per block; lo as e4m3 of lo 2^s times the weights' e4m3
+// correction operand d q 2^t on v_mfma_scale_f32_32x32x64_f8f6f4, which applies 2^-s 2^-t and
+// accumulates straight into acc, once per two blocks) on gemm_stream_precise_kernel's structure:
+// 256 x 256 tiles streamed by one CTA per CU, every operand loaded straight into LDS by inline
+// assembly with explicit waits, one barrier per stage of one block. Per stage: x hi (64 bytes per
+// row) into a ring of three, two stages ahead; the weights' raw quants and scale dwords into a
+// ring of two and unpacked one stage ahead, as in the precise kernel. Per pair of stages (the
+// correction's 64 k): x lo and the correction operand (64 bytes per row and per column) and the
+// tile's power-of-two row and column scales, requested at the pair's first stage and used at its
+// second. A wavefront owns 64 x 128 (2 x 4 tiles): per stage 16 f16 MFMAs and 128 scale FMAs, per
+// pair 8 scaled fp8 MFMAs (1.5 f16-equivalent passes where the precise kernel makes 2).
+//
+// 64-byte rows (x hi, x lo, the correction operand) sit in LDS with the 16-byte chunk c of row r at
+// position c ^ ((r >> 1) & 3); each 1 KB load instruction fills 16 whole rows.
+template <int KIND>
+struct FastLds {  // byte offsets inside the kernel's LDS arena
+    static constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
+    static constexpr uint32_t A = 0, A_SZ = 256 * 64;                          // x hi: three stages
+    static constexpr uint32_t W = 3 * A_SZ, W_Q = 256 * QB, W_SZ = W_Q + 1024;  // raw weights: two
+    static constexpr uint32_t B = W + 2 * W_SZ, B_SZ = 256 * kSB * 2;          // unpacked weights: two
+    static constexpr uint32_t D = B + 2 * B_SZ, D_SZ = 1024;                    // f32 scales: two
+    static constexpr uint32_t L8 = D + 2 * D_SZ, C8 = L8 + 256 * 64;            // x lo, correction (a pair)
+    static constexpr uint32_t SC = C8 + 256 * 64;                               // row, column scales
+    static constexpr uint32_t TOTAL = SC + 2048;
+};
+
+__device__ __forceinline__ uint32_t swz64(uint32_t r, uint32_t c) { return (r * 4 + (c ^ ((r >> 1) & 3))) * 16; }
+
+template <int KIND>
+__global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16 *__restrict__ xh,
+                                                                  const uint8_t *__restrict__ xl,
+                                                                  const int32_t *__restrict__ xsc,
+                                                                  const uint8_t *__restrict__ qs,
+                                                                  const uint16_t *__restrict__ ds,
+                                                                  const uint8_t *__restrict__ b8,
+                                                                  const int32_t *__restrict__ bsc,
+                                                                  float *__restrict__ y, uint32_t M, uint32_t K,
+                                                                  uint32_t N, uint32_t mt, uint32_t nt,
+                                                                  uint32_t split_stages) {
+    // split_stages is even, so every split and every tile starts on an even block (pairs never
+    // straddle them)
+    using S = FastLds<KIND>;
+    constexpr uint32_t QB = S::QB;
+    __shared__ __attribute__((aligned(1024))) uint8_t arena[S::TOTAL];
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t *)arena;
+
+    constexpr uint32_t GM = 8;
+    const uint32_t tiles = mt * nt, per_xcd = (tiles + 7) / 8, ctas = gridDim.x / 8;
+    const uint32_t run0 = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8, run1 = min(tiles, (blockIdx.x % 8 + 1) * per_xcd);
+    if (run0 >= run1) return;  // whole CTA: no barrier is left waiting
+    const uint32_t my_tiles = (run1 - run0 + ctas - 1) / ctas;
+    auto origin = [&](uint32_t k, uint32_t &m0, uint32_t &n0) {  // row and column of my k-th tile
+        const uint32_t t = run0 + k * ctas;
+        const uint32_t grp = t / (GM * nt), in = t % (GM * nt), gm = min(GM, mt - grp * GM);
+        m0 = (grp * GM + in % gm) * 256;
+        n0 = (in / gm) * 256;
+    };
+
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, wm = wave % 4, wn = wave / 4;
+    const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t nb = K / 32, K64 = (K + 63) / 64 * 64;
+    const uint32_t st0 = blockIdx.y * split_stages, st1 = min(nb, st0 + split_stages);
+    const uint32_t stream = my_tiles * split_stages;
+    y += (size_t)blockIdx.y * M * N;
+    const int fr = lane % 32, hf = lane / 32;
+
+    // the stage whose loads go out next (block lb of tile lt at (lm0, ln0))
+    uint32_t lb = st0, lt = 0, lm0, ln0;
+    origin(0, lm0, ln0);
+    auto advance = [&]() {
+        if (++lb == st0 + split_stages) {
+            lb = st0;
+            ++lt;
+            origin(min(lt, my_tiles - 1), lm0, ln0);
+        }
+    };
+    // 64-byte rows: load instruction i of wave w fills rows 16 (2 w + i) .. + 15; lane l fetches
+    // row + l / 4's chunk (l % 4) ^ ((row >> 1) & 3), landing at position l % 4
+    const uint32_t r64 = 32 * wave + lane / 4;  // (+ 16 i)
+    auto chunk64 = [&](uint32_t row) { return ((lane % 4) ^ ((row >> 1) & 3)) * 16; };
+    auto dma_x = [&](uint32_t ring) {
+        const bool live = lt < my_tiles && lb < st1;
+        const i32x4 r = sgpr_rsrc(xh, live ? M * nb * 64 : 0u);
+        const uint32_t lds = lds0 + S::A + ring * S::A_SZ + wave_u * 2048;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t row = r64 + 16 * i;
+            asm_load_lds16(r, lds + 1024 * i, ((lm0 + row) * nb + lb) * 64 + chunk64(row));
+        }
+    };
+    auto dma_w = [&](uint32_t ring) {  // as gemm_stream_precise_kernel's
+        const bool live = lt < my_tiles && lb < st1;
+        const uint32_t lds = lds0 + S::W + ring * S::W_SZ;
+        if (KIND == FH_Q8_0 || wave_u < 4) {
+            const i32x4 rq = sgpr_rsrc(qs, live ? (N + 31) / 32 * 32 * nb * QB : 0u);
+            const uint32_t g = KIND == FH_Q8_0 ? ln0 / 32 + wave_u : ln0 / 32 + 2 * wave_u + lane / 32;
+            const uint32_t r = KIND == FH_Q8_0 ? lane / 2 : lane % 32;
+            const uint32_t off = ((g * nb + lb) * 32 + r) * QB + (KIND == FH_Q8_0 ? (lane % 2) * 16 : 0);
+            asm_load_lds16(rq, lds + wave_u * 1024, off);
+        }
+        if (wave_u >= 4) {
+            const i32x4 rd = sgpr_rsrc(ds, live ? (N + 31) / 32 * 32 * ((nb + 7) / 8 * 8) * 2 : 0u);
+            const uint32_t n = ln0 + 64 * (wave_u - 4) + lane;
+            const uint32_t so = ((n >> 5) * ((nb + 7) / 8) * 32 + (n & 31)) * 16 + (lb / 8) * 512 + (lb % 8) / 2 * 4;
+            asm_load_lds4(rd, lds + S::W_Q + (wave_u - 4) * 256, so);
+        }
+    };
+    // the tile being computed (its origin), for the pair's correction operands and the epilogue
+    uint32_t ct = 0, cm0, cn0;
+    origin(0, cm0, cn0);
+    // the pair starting at (even) block b of the computed tile: x lo and the correction operand
+    // (natural k order, rows of K64, 32 bytes per block) and the tile's row and column scales (E8M0
+    // bytes, four copies); rows past M and columns past N read zeros, whose products are zero
+    auto dma_corr = [&](uint32_t b) {
+        const bool live = b < st1;
+        const i32x4 rl = sgpr_rsrc(xl, live ? M * K64 : 0u);
+        const i32x4 rc = sgpr_rsrc(b8, live ? N * K64 : 0u);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t row = r64 + 16 * i;
+            asm_load_lds16(rl, lds0 + S::L8 + wave_u * 2048 + 1024 * i, (cm0 + row) * K64 + b * 32 + chunk64(row));
+            asm_load_lds16(rc, lds0 + S::C8 + wave_u * 2048 + 1024 * i, (cn0 + row) * K64 + b * 32 + chunk64(row));
+        }
+        if (wave_u < 4) {
+            const i32x4 rs = sgpr_rsrc(xsc, M * 4);
+            asm_load_lds4(rs, lds0 + S::SC + wave_u * 256, (cm0 + 64 * wave_u + lane) * 4);
+        } else {
+            const i32x4 rs = sgpr_rsrc(bsc, N * 4);
+            asm_load_lds4(rs, lds0 + S::SC + 1024 + (wave_u - 4) * 256, (cn0 + 64 * (wave_u - 4) + lane) * 4);
+        }
+    };
+    const int cq = tid % 256, hq = tid / 256;
+    auto unpack_w = [&](uint32_t ring, uint32_t odd, uint32_t slot) {
+        const uint8_t *raw = arena + S::W + ring * S::W_SZ;
+        _Float16 *col = (_Float16 *)(arena + S::B + slot * S::B_SZ) + cq * kSB + 16 * hq;
+        u32x4 o[2];
+        if constexpr (KIND == FH_Q8_0) {
+            unpack_q8(*(const u32x4 *)(raw + cq * 32 + hq * 16), o);
+        } else {
+            const u32x2 v = *(const u32x2 *)(raw + cq * 16 + hq * 8);
+            unpack_q4_half(v[0], v[1], o[0], o[1]);
+        }
+        *(u32x4 *)col = o[0];
+        *(u32x4 *)(col + 8) = o[1];
+        if (hq == 0) {
+            const uint32_t dd = *(const uint32_t *)(raw + S::W_Q + cq * 4);
+            ((float *)(arena + S::D + slot * S::D_SZ))[cq] = half_to_float(odd ? dd >> 16 : dd & 0xffffu);
+        }
+    };
+
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    f16x8 ah[2][2];
+    auto read_a = [&](uint32_t ring) {
+        const uint8_t *sa = arena + S::A + ring * S::A_SZ;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t r = wm * 64 + i * 32 + fr;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) ah[i][s2] = *(const f16x8 *)(sa + swz64(r, hf + 2 * s2));
+        }
+    };
+    // the hi part, pipelined as in gemm_stream_precise_kernel: tile t's two MFMAs, each followed by
+    // eight of tile t - 1's scale FMAs
+    auto compute = [&](uint32_t slot, auto &&hook) {
+        const _Float16 *bp = (const _Float16 *)(arena + S::B + slot * S::B_SZ) + (wn * 128 + fr) * kSB + 8 * hf;
+        const float *dp = (const float *)(arena + S::D + slot * S::D_SZ) + wn * 128 + fr;
+        f32x16 p[2];
+        f16x8 bq[2][2];
+        float dq[2];
+        bq[0][0] = *(const f16x8 *)bp;
+        bq[0][1] = *(const f16x8 *)(bp + 16);
+        dq[0] = dp[0];
+#pragma unroll
+        for (int t = 0; t <= 8; t++) {
+            const int j = t / 2, i = t % 2, tp = t - 1, jp = tp / 2, ip = tp % 2;
+            f32x16 q = {};
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) {
+                if (t < 8) q = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][s2], bq[j % 2][s2], q, 0, 0, 0);
+                if (t > 0) {
+#pragma unroll
+                    for (int r = 8 * s2; r < 8 * s2 + 8; r++)
+                        acc[ip][jp][r] = fmaf(dq[jp % 2], p[tp % 2][r], acc[ip][jp][r]);
+                }
+            }
+            if (t < 8) p[t % 2] = q;
+            if (t < 6 && i == 0) {
+                bq[(j + 1) % 2][0] = *(const f16x8 *)(bp + (j + 1) * 32 * kSB);
+                bq[(j + 1) % 2][1] = *(const f16x8 *)(bp + (j + 1) * 32 * kSB + 16);
+            }
+            if (t < 6 && i == 1) dq[(j + 1) % 2] = dp[(j + 1) * 32];
+            if (t > 0) asm volatile("" : "+v"(acc[ip][jp]));
+            hook(t);
+#pragma unroll
+            for (int s2 = 0; s2 < 2; s2++) {
+                if (t < 8) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA of tile t
+                if (t > 0) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // eight FMAs of tile t - 1
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // the pair's correction: 32 bytes of x lo per row tile and of the operand per column tile
+    // (the lane's half of the 64 k), the scaled fp8 MFMA applying 2^-s 2^-t
+    typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+    auto correct = [&]() {
+        const int32_t *scl = (const int32_t *)(arena + S::SC);
+        int32_t asc[2], bscv[4];
+        i32x8 a8[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t r = wm * 64 + i * 32 + fr;
+            const u32x4 lo0 = *(const u32x4 *)(arena + S::L8 + swz64(r, 2 * hf));
+            const u32x4 lo1 = *(const u32x4 *)(arena + S::L8 + swz64(r, 2 * hf + 1));
+            a8[i] = i32x8{(int)lo0[0], (int)lo0[1], (int)lo0[2], (int)lo0[3], (int)lo1[0], (int)lo1[1], (int)lo1[2],
+                          (int)lo1[3]};
+            asc[i] = scl[r];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) bscv[j] = scl[256 + wn * 128 + j * 32 + fr];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t c = wn * 128 + j * 32 + fr;
+            const u32x4 w0 = *(const u32x4 *)(arena + S::C8 + swz64(c, 2 * hf));
+            const u32x4 w1 = *(const u32x4 *)(arena + S::C8 + swz64(c, 2 * hf + 1));
+            const i32x8 b8f{(int)w0[0], (int)w0[1], (int)w0[2], (int)w0[3], (int)w1[0], (int)w1[1], (int)w1[2], (int)w1[3]};
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8[i], b8f, acc[i][j], 0, 0, 0, asc[i], 0,
+                                                                            bscv[j]);
+        }
+    };
+    auto epilogue = [&]() {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = cm0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * hf + r % 4;
+                if (row >= M) continue;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t col = cn0 + wn * 128 + j * 32 + fr;
+                    if (col < N) y[(size_t)row * N + col] = acc[i][j][r];
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+        ++ct;
+        origin(min(ct, my_tiles - 1), cm0, cn0);
+    };
+
+    // prologue: stages 0 and 1 requested, stage 0's weights unpacked
+    uint32_t par = lb & 1;
+    dma_w(0);
+    dma_x(0);
+    advance();
+    dma_w(1);
+    dma_x(1);
+    advance();
+    asm volatile("s_waitcnt vmcnt(5)" ::: "memory");  // weights(0): x(0), weights(1), x(1) came after
+    __syncthreads();
+    unpack_w(0, par, 0);
+    par = (st0 + 1 % split_stages) & 1;
+    uint32_t ra = 0, rw = 1;
+    // Per wave the loads of stage p go out as [the pair's correction, at an even p] weights(p + 2),
+    // x(p + 2) (two instructions): at the top of stage p, waiting until at most 2 are outstanding
+    // leaves weights(p + 1), x(p) and the correction issued in stage p - 1 in LDS.
+    for (uint32_t p = 0; p < stream; p++) {
+        asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        __syncthreads();
+        read_a(ra);
+        const uint32_t cb = st0 + p % split_stages;  // this stage's block
+        compute(p & 1, [&](int t) {
+            if (t == 0 && !(p & 1)) {
+                dma_corr(cb);  // (the buffer's previous pair was used in stage p - 1)
+            } else if (t == 1) {
+                unpack_w(rw, par, (p + 1) & 1);
+                par = (st0 + (p + 2) % split_stages) & 1;
+            } else if (t == 5) {
+                dma_w(rw ^ 1);
+                dma_x(ra == 0 ? 2 : ra - 1);
+                advance();
+            }
+        });
+        if (p & 1) correct();  // the pair (p - 1, p)
+        if ((p + 1) % split_stages == 0) epilogue();
+        ra = ra == 2 ? 0 : ra + 1;
+        rw ^= 1;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 // The streaming kernel's plan: taken when the product has at least 128 tiles of 256 x 256; the K
 // split (at most 4, at least 16 blocks per split) that best fills whole rounds of one CTA per CU.
 bool stream_plan(size_t rows, size_t k, size_t n, uint32_t *splits) {
@@ -1199,6 +1503,58 @@ hipError_t gemm_precise_dispatch(hipStream_t s, const _Float16 *xs, const uint8_
     if (M <= 32) return run_gemm_precise<KIND, 32, 256, 1>(s, xs, qs, ds, y, partial, M, K, N, defer);
     if (M <= 64) return run_gemm_precise<KIND, 64, 128, 2>(s, xs, qs, ds, y, partial, M, K, N, defer);
     return run_gemm_precise<KIND, 128, 128, 2>(s, xs, qs, ds, y, partial, M, K, N, defer);
+}
+
+bool stream_fast_supported(size_t rows, size_t k, size_t n) {
+    // every byte offset a CTA forms (rows and columns up to the last tile's end) fits in 32 bits
+    const size_t k64 = (k + 63) / 64 * 64, lim = (size_t)1 << 31;
+    return (rows + 255) * k * 2 < lim && (rows + 255) * k64 < lim && (n + 255) * k64 < lim &&
+           (n + 255) * (k / 32) * 32 < lim;
+}
+
+template <int KIND>
+hipError_t run_gemm_stream_fast(hipStream_t s, const GemmArgs &g, uint32_t sp) {
+    const uint32_t mt = (g.M + 255) / 256, nt = (g.N + 255) / 256;
+    const uint64_t tiles = (uint64_t)mt * nt;
+    if (tiles > 0x7ffffff0ull) return hipErrorInvalidValue;
+    const uint32_t per_xcd = (uint32_t)((tiles + 7) / 8);
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8)
+        cus = 256;
+    const uint32_t ctas = min(per_xcd, (uint32_t)cus / 8);
+    const uint32_t stages = g.K / 32;
+    const uint32_t per = ((stages + sp - 1) / sp + 1) & ~1u;  // even: pairs never straddle a split
+    float *out = sp > 1 ? g.partial : g.y;
+    gemm_stream_fast_kernel<KIND><<<dim3(8 * ctas, sp), 512, 0, s>>>(g.xh, g.xl, g.xsc, g.qs, g.ds, g.b8, g.bsc, out,
+                                                                      g.M, g.K, g.N, mt, nt, per);
+    if (g.defer) *g.defer = sp > 1 ? SplitOut{g.partial, sp} : SplitOut{g.y, 1u};
+    if (sp > 1 && !g.defer) {
+        const size_t n = (size_t)g.M * g.N;
+        const unsigned rg = (unsigned)min((n + 1023) / 1024, (size_t)16384);
+        gemm_reduce_kernel<<<rg, 256, 0, s>>>(g.partial, g.y, n, sp);
+    }
+    return hipGetLastError();
+}
+
+// The scoring GEMM takes the streaming kernel for products of at least 640 tiles of 256 x 256
+// (two and a half rounds of one CTA per CU), gemm_kernel's 128-row tiles below that. Measured per
+// product (Q4_0, x split included): the streaming kernel is faster on the Qwen2-0.5B head
+// (151,936 columns; M = 2048: 1283 against 1426 us, M = 512: 349 against 440) and on the
+// TinyLlama gate/up at M = 4096 (704 tiles: 429 against 473 us), slower where a product is one or
+// two partly filled rounds (Qwen2 gate/up at M = 2048, 304 tiles: 121 against 98 us; TinyLlama
+// products at M = 1024-4096 with 128-352 tiles: 1-23% slower).
+bool stream_fast_plan(size_t rows, size_t k, size_t n, uint32_t *splits) {
+    const uint64_t tiles = (uint64_t)((rows + 255) / 256) * ((n + 255) / 256);
+    return tiles >= 640 && stream_plan(rows, k, n, splits);
+}
+
+template <int KIND>
+hipError_t gemm_fast_dispatch(hipStream_t s, const GemmArgs &g) {
+    uint32_t sp = 1;
+    if (stream_fast_plan(g.M, g.K, g.N, &sp) && stream_fast_supported(g.M, g.K, g.N) && (sp == 1 || g.partial))
+        return run_gemm_stream_fast<KIND>(s, g, sp);
+    return gemm_dispatch<KIND>(s, g);
 }
 
 // ---- the MFMA GEMM on the other weight formats' GGUF rows (F16, FP8 E4M3 / E5M2, MXFP4) ----
@@ -2142,7 +2498,8 @@ size_t gemm_partial_bytes(size_t rows, size_t k, size_t n) {
     size_t bm, bn;
     fast_tile(rows, &bm, &bn);
     const uint64_t tiles = (uint64_t)((rows + bm - 1) / bm) * ((n + bn - 1) / bn);
-    const uint32_t sp = gemm_splits(tiles, (uint32_t)((k / 32 + 1) / 2));
+    uint32_t sp = gemm_splits(tiles, (uint32_t)((k / 32 + 1) / 2)), ssp = 1;
+    if (stream_fast_plan(rows, k, n, &ssp) && stream_fast_supported(rows, k, n)) sp = max(sp, ssp);
     return sp > 1 ? (size_t)sp * rows * n * 4 : 0;
 }
 
@@ -2254,11 +2611,11 @@ hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uin
         if (x)
             split_x_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc,
                                                                    g.K);
-        return gemm_dispatch<FH_Q8_0>(s, g);
+        return gemm_fast_dispatch<FH_Q8_0>(s, g);
     }
     if (x)
         split_x_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
-    return gemm_dispatch<FH_Q4_0>(s, g);
+    return gemm_fast_dispatch<FH_Q4_0>(s, g);
 }
 
 // x as f16 (2 bytes per element), the row scales, then the K-split partials, each 256-aligned

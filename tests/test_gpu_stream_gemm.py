@@ -1,5 +1,6 @@
-"""The precise MFMA GEMM's streaming 256 x 256 kernel (QPath.Tiled on products with at least 128
-such tiles): one CTA per CU working through its tiles stage by stage, K split up to 4 ways.
+"""The MFMA GEMMs' streaming 256 x 256 kernels (QPath.Tiled and QPath.TiledFast on products with
+at least 128 such tiles): one CTA per CU working through its tiles stage by stage, K split up to 4
+ways.
 
 The reference path it replaces for these shapes is `linear_q` on many rows
 (ferrum_wgpu/src/ops/quant.rs:326-381, qlinear_tiled.wgsl:93-128), whose tests hold every product
@@ -9,6 +10,12 @@ CPU oracle's f32 product (16-thread matmul_tuned, bit-identical to matmul), or, 
 f32 product is that far from the float64 product, no farther from float64 than the CPU. Every
 output is compared: the kernel deals tiles to CTAs in an XCD-grouped order, so a mistake in that
 order shows up in some column tile, not necessarily the first.
+
+The scoring GEMM (TiledFast, no counterpart in the reference) is held to the MFMA-GEMM bound on
+every output, |g - w| <= 1e-3 + 2e-3 |w| against the same CPU product (0 outputs outside it). It
+takes the streaming kernel from 640 tiles on: the TinyLlama gate/up at M = 4096 (704 tiles), a
+ragged product with an odd block count (2085 x 1120 x 20000, 711 tiles) and one with a 2-way K
+split (2560 x 2048 x 16384, 640 tiles).
 
 Cases: whole tiles with a 2-way K split (2048 x 2048 x 4096), ragged rows, columns and an odd block
 count with a padding stage (2085 x 1120 x 4196), and the TinyLlama down product at M = 4096
@@ -69,3 +76,30 @@ def test_stream_precise_gemm_matches_the_cpu(fh, g, orc, kind_name, m, k, n):
     say(f"stream GEMM {kind_name} {m}x{k}x{n}: vs CPU {e:.2e}; vs float64 device {e_dev:.2e}, CPU {e_cpu:.2e}")
     assert np.all(np.isfinite(got))
     assert e < REDUCING or e_dev <= e_cpu, (e, e_dev, e_cpu)
+
+
+@pytest.mark.parametrize("kind_name", ["Q4_0", "Q8_0"])
+@pytest.mark.parametrize("m,k,n", [(4096, 2048, 11264), (2085, 1120, 20000), (2560, 2048, 16384)])
+def test_stream_fast_gemm_meets_the_per_output_bound(fh, g, orc, kind_name, m, k, n):
+    kind = fh.QKind[kind_name]
+    rng = np.random.default_rng(m + k + n + 1)
+    w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+    x = rng.standard_normal(m * k).astype(np.float32)
+    say(f"stream fast GEMM {kind_name} {m}x{k}x{n}: uploading")
+    qw = fh.upload_quantised(g, kind, w, k, n)
+    b = qw.read_gguf()
+    wd = orc.dequantised_in_out(int(kind), b, k, n)
+    gx, gy = g.upload(x), g.zeros(m * n)
+    fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.TiledFast)
+    got = g.read(gy).reshape(m, n)
+    again = g.zeros(m * n)
+    fh.linear_q_with(g, gx, qw, again, m, fh.QPath.TiledFast)
+    assert np.array_equal(g.read(again).reshape(m, n).view(np.uint32), got.view(np.uint32)), "not deterministic"
+    qw.free()
+    want = orc.matmul_tuned(x, wd, m, k, n, THREADS).reshape(m, n)
+    r = np.abs(got - want) / (1e-3 + 2e-3 * np.abs(want))
+    frac = float(np.mean(r > 1.0))
+    say(f"stream fast GEMM {kind_name} {m}x{k}x{n}: worst {float(r.max()):.3f} of the bound, outside {frac:.2e}, "
+        f"max_rel_err {orc.max_rel_err(got.reshape(-1), want.reshape(-1)):.2e}")
+    assert np.all(np.isfinite(got))
+    assert frac == 0.0
