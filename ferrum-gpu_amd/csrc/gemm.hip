@@ -850,8 +850,11 @@ hipError_t run_gemm_precise(hipStream_t s, const _Float16 *xs, const uint8_t *qs
 // the barrier then covers every wave's share.
 //
 // x rows in LDS are 128 bytes without padding; the 16-byte chunk c of row r sits at position
-// c ^ (r % 8), so the 32 rows a fragment read touches spread over the banks (each wave's load
+// c ^ ((r >> 1) & 7), so the sixteen rows that one cycle of a 16-byte fragment read serves (256
+// bytes of the 64 banks) fall on sixteen different 16-byte bank groups (each wave's load
 // instruction fills 1 KB of LDS, eight whole rows, choosing per lane which chunk it fetches).
+// (With c ^ (r % 8), conflict-free for eight lanes per cycle, SQ_LDS_BANK_CONFLICT counted as
+// many conflict cycles as LDS instruction cycles.)
 constexpr int kSB = 40;  // LDS halves per weight column and stage: 32 + 8 pad (80 B)
 
 // 2 quant dwords of a Q4_0 block (dwords 2h, 2h + 1) -> positions 16 h .. 16 h + 15 as exact f16
@@ -950,15 +953,17 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Floa
         }
     };
     // x: load instruction i of wave w fills rows 32 w + 8 i .. + 7 (1 KB); lane l fetches row
-    // 32 w + 8 i + l / 8's chunk (l % 8) ^ (l / 8), landing at position l % 8 of the row
-    const uint32_t xrow = 32 * wave + lane / 8, xchunk = ((lane % 8) ^ (lane / 8)) * 16;
+    // r = 32 w + 8 i + l / 8's chunk (l % 8) ^ ((r >> 1) & 7), landing at position l % 8 of the row
+    const uint32_t xrow = 32 * wave + lane / 8;
+    auto xchunk = [&](uint32_t row) { return ((lane % 8) ^ ((row >> 1) & 7)) * 16; };
     auto dma_x = [&](uint32_t ring) {
         const bool live = lt < my_tiles && lb < st1;
         const i32x4 r = sgpr_rsrc(xs, live ? M * nb * 128 : 0u);
-        const uint32_t base = ((lm0 + xrow) * nb + lb) * 128 + xchunk;
+        const uint32_t base = ((lm0 + xrow) * nb + lb) * 128;
         const uint32_t lds = lds0 + S::A + ring * S::A_SZ + wave_u * 32 * 128;
 #pragma unroll
-        for (int i = 0; i < 4; i++) asm_load_lds16(r, lds + 8 * i * 128, base + 8 * i * nb * 128);
+        for (int i = 0; i < 4; i++)
+            asm_load_lds16(r, lds + 8 * i * 128, base + 8 * i * nb * 128 + xchunk(xrow + 8 * i));
     };
     // weights: the block's quants of 256 columns as they lie in the tile plane (QB bytes per
     // column, a group of 32 columns contiguous), one 1 KB load per wave (Q4_0: waves 0-3); the
@@ -1021,8 +1026,8 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Floa
             const uint8_t *row = sa + r * 128;
 #pragma unroll
             for (int s2 = 0; s2 < 2; s2++) {
-                ah[i][s2] = *(const f16x8 *)(row + (((hf + 2 * s2) ^ (r % 8)) * 16));
-                al[i][s2] = *(const f16x8 *)(row + (((4 + hf + 2 * s2) ^ (r % 8)) * 16));
+                ah[i][s2] = *(const f16x8 *)(row + (((hf + 2 * s2) ^ ((r >> 1) & 7)) * 16));
+                al[i][s2] = *(const f16x8 *)(row + (((4 + hf + 2 * s2) ^ ((r >> 1) & 7)) * 16));
             }
         }
     };
@@ -1153,7 +1158,8 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Floa
 // pair 8 scaled fp8 MFMAs (1.5 f16-equivalent passes where the precise kernel makes 2).
 //
 // 64-byte rows (x hi, x lo, the correction operand) sit in LDS with the 16-byte chunk c of row r at
-// position c ^ ((r >> 1) & 3); each 1 KB load instruction fills 16 whole rows.
+// position c ^ ((r >> 2) & 3), so the sixteen rows one cycle of a fragment read serves fall on
+// sixteen different 16-byte bank groups; each 1 KB load instruction fills 16 whole rows.
 template <int KIND>
 struct FastLds {  // byte offsets inside the kernel's LDS arena
     static constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
@@ -1166,7 +1172,7 @@ struct FastLds {  // byte offsets inside the kernel's LDS arena
     static constexpr uint32_t TOTAL = SC + 2048;
 };
 
-__device__ __forceinline__ uint32_t swz64(uint32_t r, uint32_t c) { return (r * 4 + (c ^ ((r >> 1) & 3))) * 16; }
+__device__ __forceinline__ uint32_t swz64(uint32_t r, uint32_t c) { return (r * 4 + (c ^ ((r >> 2) & 3))) * 16; }
 
 template <int KIND>
 __global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16 *__restrict__ xh,
@@ -1217,9 +1223,9 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16
         }
     };
     // 64-byte rows: load instruction i of wave w fills rows 16 (2 w + i) .. + 15; lane l fetches
-    // row + l / 4's chunk (l % 4) ^ ((row >> 1) & 3), landing at position l % 4
+    // row + l / 4's chunk (l % 4) ^ ((row >> 2) & 3), landing at position l % 4
     const uint32_t r64 = 32 * wave + lane / 4;  // (+ 16 i)
-    auto chunk64 = [&](uint32_t row) { return ((lane % 4) ^ ((row >> 1) & 3)) * 16; };
+    auto chunk64 = [&](uint32_t row) { return ((lane % 4) ^ ((row >> 2) & 3)) * 16; };
     auto dma_x = [&](uint32_t ring) {
         const bool live = lt < my_tiles && lb < st1;
         const i32x4 r = sgpr_rsrc(xh, live ? M * nb * 64 : 0u);
