@@ -92,6 +92,24 @@ typedef __attribute__((address_space(1))) const f32x4 gf32x4;
 
 __device__ __forceinline__ f32x4 gload4(const float *p) { return *(gf32x4 *)p; }
 
+// Agent-coherent stores (relaxed atomics at agent scope: written through to the point where every
+// XCD sees them) for data one workgroup of a launch writes and another reads in the same launch,
+// without cache-wide fences. The readers use ordinary loads: each such address is written once per
+// launch before anything in the launch reads it (the one-launch step keeps a copy of every buffer
+// per layer), so no XCD's L2 can hold an older copy of it.
+typedef __attribute__((address_space(1))) uint64_t g_u64;
+typedef __attribute__((address_space(1))) uint32_t g_u32;
+__device__ __forceinline__ void cstore(float *p, float v) {
+    __hip_atomic_store((g_u32 *)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void cstore4(float *p, f32x4 v) {
+    g_u64 *q = (g_u64 *)p;
+    __hip_atomic_store(q, (uint64_t)__float_as_uint(v[0]) | (uint64_t)__float_as_uint(v[1]) << 32, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, (uint64_t)__float_as_uint(v[2]) | (uint64_t)__float_as_uint(v[3]) << 32, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
 
 // Sum over the workgroup (every thread gets the total); red holds one float per wavefront.
 __device__ __forceinline__ float block_sum(float v, float *red) {
@@ -517,6 +535,7 @@ __global__ __launch_bounds__(1024) void pick_kernel(const float *__restrict__ of
         state[2] = pick;
         if (p + 1 >= state[1]) inputs[p + 1] = pick;
         state[0] = p + 1;
+        state[3] = state[3] + 1;  // the step's epoch (one_step_kernel's counters)
     }
 }
 
@@ -601,13 +620,13 @@ constexpr int kStepThreads = 512;
 constexpr int kStepWaves = kStepThreads / 64;
 constexpr uint32_t kAttnSlots = 2 * kStepThreads / 16;  // attend_head: two floats per lane group (L >= 16)
 
-// The second product's task for row group rg: blocks b0 = blockIdx.x * G .. b0 + 2 PAIRS - 1 of
-// its rows (b0 even, all in one run of eight scales).
+// The second product's task for row group rg and head h: blocks b0 = h * 2 PAIRS .. b0 + 2 PAIRS - 1
+// of its rows (b0 even, all in one run of eight scales).
 template <int KIND, int PAIRS>
-__device__ __forceinline__ void load_task2(Batch<KIND> &bt, const StepArgs &a, uint32_t rg, uint32_t oq,
+__device__ __forceinline__ void load_task2(Batch<KIND> &bt, const StepArgs &a, uint32_t h, uint32_t rg, uint32_t oq,
                                            uint32_t os) {
     constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
-    const uint32_t nb2 = a.nb2, nb28 = (nb2 + 7) / 8, b0 = blockIdx.x * (2 * PAIRS);
+    const uint32_t nb2 = a.nb2, nb28 = (nb2 + 7) / 8, b0 = h * (2 * PAIRS);
     const auto rq = make_rsrc(a.qs2 + (size_t)rg * nb2 * 32 * QB, nb2 * 32 * QB);
     const auto rd = make_rsrc(a.ds2 + (size_t)rg * nb28 * 256, nb28 * 512);
     if constexpr (KIND == FH_Q8_0) {
@@ -658,10 +677,10 @@ __device__ __forceinline__ void prep_lds(const float *x, uint32_t width, uint8_t
 }
 
 // The second product: row groups w, w + W, ... of the d rows, K in flight as above;
-// out_part[blockIdx.x] gets the workgroup's share of each row.
-template <int KIND, int PAIRS, int K>
-__device__ __forceinline__ void run_tasks2(const StepArgs &a, Batch<KIND> (&set)[K], const uint8_t *recs, uint32_t oq,
-                                           uint32_t os, uint32_t oa, uint32_t ot) {
+// out_part[h] gets head h's share of each row (COH: agent-coherent stores).
+template <int KIND, int PAIRS, int K, bool COH = false>
+__device__ __forceinline__ void run_tasks2(const StepArgs &a, uint32_t h, Batch<KIND> (&set)[K], const uint8_t *recs,
+                                           uint32_t oq, uint32_t os, uint32_t oa, uint32_t ot) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int lane = threadIdx.x % 64;
     const bool upper = lane >= 32;
@@ -675,8 +694,13 @@ __device__ __forceinline__ void run_tasks2(const StepArgs &a, Batch<KIND> (&set)
                 float acc = 0.0f;
                 compute_batch<KIND, PAIRS>(set[i], upper, acc);
                 const float sum = half_sum(acc, upper);
-                if (!upper) a.out_part[(size_t)blockIdx.x * a.d + rg * 32 + lane] = sum;
-                if (rg + K * kStepWaves < groups) load_task2<KIND, PAIRS>(set[i], a, rg + K * kStepWaves, oq, os);
+                if (!upper) {
+                    if constexpr (COH)
+                        cstore(a.out_part + (size_t)h * a.d + rg * 32 + lane, sum);
+                    else
+                        a.out_part[(size_t)h * a.d + rg * 32 + lane] = sum;
+                }
+                if (rg + K * kStepWaves < groups) load_task2<KIND, PAIRS>(set[i], a, h, rg + K * kStepWaves, oq, os);
             }
         }
     }
@@ -688,14 +712,14 @@ __device__ __forceinline__ void run_tasks2(const StepArgs &a, Batch<KIND> (&set)
 // 16-byte load each of its k and v), a lane group takes U rows at a time with all their loads
 // issued together and keeps a running maximum, sum and output (the softmax's max-subtracted
 // exponentials, rescaled when the maximum grows); the NR groups then meet through LDS, rescaled
-// to the common maximum. Rows past T are read as row T - 1 and dropped.
+// to the common maximum. Rows past T are read as row T - 1 and dropped. h: the head.
 template <int L>
-__device__ __forceinline__ void attend_head(const float *qh, const float *knew, const float *vnew, const float *kc,
-                                             const float *vc, uint32_t T, uint32_t d, float scale, float *s,
-                                             float *accs, float *red, float *out) {
+__device__ __forceinline__ void attend_head(uint32_t h, const float *qh, const float *knew, const float *vnew,
+                                             const float *kc, const float *vc, uint32_t T, uint32_t d, float scale,
+                                             float *s, float *accs, float *red, float *out) {
     constexpr uint32_t hd = 4 * L, NR = kStepThreads / L;
     constexpr int U = 8;
-    const uint32_t h = blockIdx.x, tid = threadIdx.x;
+    const uint32_t tid = threadIdx.x;
     const uint32_t li = tid % L, rg = tid / L, last = T - 1;
     (void)red;
     const f32x4 qv = *(const f32x4 *)(qh + 4 * li);
@@ -780,15 +804,15 @@ __global__ __launch_bounds__(kStepThreads) void attn_out_kernel(StepArgs a) {
     Batch<KIND> s2[K2];
 #pragma unroll
     for (int i = 0; i < K2; i++)
-        if (wave + i * kStepWaves < a.d / 32) load_task2<KIND, PAIRS>(s2[i], a, wave + i * kStepWaves, oq, os);
+        if (wave + i * kStepWaves < a.d / 32) load_task2<KIND, PAIRS>(s2[i], a, blockIdx.x, wave + i * kStepWaves, oq, os);
     const uint32_t p = (uint32_t)a.state[0];
     const size_t off = (size_t)blockIdx.x * hd;
-    attend_head<L>(a.q + off, a.kc + (size_t)p * a.d + off, a.vc + (size_t)p * a.d + off, a.kc, a.vc, p + 1, a.d,
+    attend_head<L>(blockIdx.x, a.q + off, a.kc + (size_t)p * a.d + off, a.vc + (size_t)p * a.d + off, a.kc, a.vc, p + 1, a.d,
                     a.scale, s, accs, red, att);
     __syncthreads();
     prep_lds<KIND>(att, hd, recs2);
     __syncthreads();
-    run_tasks2<KIND, PAIRS, K2>(a, s2, recs2, oq, os, oa, ot);
+    run_tasks2<KIND, PAIRS, K2>(a, blockIdx.x, s2, recs2, oq, os, oa, ot);
 }
 
 // After the last layer: x = x_in + (sum_j part[j] + b) and its final LayerNorm into global
@@ -799,6 +823,410 @@ __global__ __launch_bounds__(kStepThreads) void final_ln_kernel(StepArgs a, uint
     f32x4 v[kLnSlots];
     residual_row<KIND>(a, v);
     ln_records<KIND, true>(v, a.ln_g, a.ln_b, a.eps, a.nb, (a.nb + 7) / 8 * 8, out, red);
+}
+
+// ---- the one-launch step: every layer in one launch ----
+// In the four-launch step each launch costs about 2 us of dispatch gap (the last workgroup's end to
+// the next launch's first workgroup, measured with wall-clock stamps inside the kernels) before
+// its first dependent load even leaves; with 48 launches per token that is a third of the step.
+// Here one launch runs all the layers. Each workgroup keeps one role through the layers: a QKV row
+// group (nA of them), an attention head with its output-projection columns (nB), an FFN-up row
+// group (nC) or an FFN-down task (nD: row group x K split), exactly the four-launch step's
+// workgroups with the same lane-level arithmetic, so a step's results are the same bit for bit.
+// Between phases a workgroup requests its next task's weights, then waits for the phase it
+// depends on: a completion counter per layer and phase, which every task of the phase
+// increments once its stores have landed, polled by one lane with agent-scope loads. What one
+// phase writes and a later phase of the same launch reads is stored with agent-coherent stores,
+// each address once per launch (every buffer has a copy per layer), and read with ordinary loads:
+// no L2 can hold an older copy, so no cache-wide release or acquire is needed (with 240
+// workgroups each fencing four times per layer, L2 write-backs and invalidations made the step
+// 2.7x slower; reading the shared rows with coherent loads instead, 1.6x slower: every workgroup
+// then fetched them past its L2). The counters only grow: the step
+// with epoch e (state[3], advanced by the pick) waits for (e + 1) x the phase's tasks. Every wait
+// is bounded: after kSpinLimit polls (about a second), or once another workgroup has given up,
+// it sets the error flag and goes on, so every wavefront reaches its end; the host reports the
+// flag. The launch needs all of its workgroups resident at once: the host takes this form only
+// where the occupancy query says they fit.
+struct OneLayer {  // one layer's operands and buffers (a device table, read with scalar loads)
+    const uint8_t *qkv_qs, *o_qs, *w1_qs, *w2_qs;
+    const uint16_t *qkv_ds, *o_ds, *w1_ds, *w2_ds;
+    const float *ln1_g, *ln1_b, *bqkv, *bo, *ln2_g, *ln2_b, *b1, *b2;
+    float *kc, *vc;
+    // this layer's copies of the step's buffers: the query row, the residual rows before and after
+    // the attention block, the attention's and FFN-down's partial rows, the FFN activation
+    float *q, *xc, *xm, *po, *pf, *f;
+};
+
+struct OneArgs {
+    const OneLayer *layers;
+    uint32_t n_layers;
+    const uint8_t *emb_qs;
+    const uint16_t *emb_ds;
+    const float *pos_tab;
+    int32_t *inputs;
+    int32_t *state;
+    float *x_final;
+    const float *lnf_g, *lnf_b;
+    uint8_t *prep;   // the final LayerNorm's prepared records (the head's x)
+    uint32_t *sync;  // [n_layers][4] completion counters (one_counter), then the error flag
+    uint32_t d, hidden, heads, S, chunk_down;
+    float eps, scale;
+    uint32_t nA, nB, nC, nD;
+};
+constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr uint32_t kOneMaxLayers = 256;
+// Every counter has kCopies copies, a cache line apart, each incremented by every task of its phase
+// (one lane per copy); workgroup w polls copy w % kCopies. With one copy, about a hundred workgroups
+// polling one address while the tasks' atomics queued behind them made the step 1.5x slower than
+// with 8 copies; 32 were 2% faster again (measured, GPT-2-small).
+constexpr uint32_t kCopies = 32, kCopyStride = 32;  // (in uint32_t)
+constexpr uint32_t kCounter = kCopies * kCopyStride;  // uint32_t per counter
+__host__ __device__ constexpr uint32_t one_counter(uint32_t l, uint32_t phase) { return (4 * l + phase) * kCounter; }
+
+// Waits until the counter at cnt reaches target (wrapping compare), bounded as above.
+__device__ __forceinline__ void one_wait(uint32_t *cnt, uint32_t target, uint32_t *err) {
+    cnt += (blockIdx.x % kCopies) * kCopyStride;
+    if (threadIdx.x == 0) {
+        uint32_t n = 0;
+        while ((int32_t)(__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
+            if ((++n & 63u) == 0 &&
+                (n >= kSpinLimit || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)) {
+                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();  // (what the phase wrote is read with agent-coherent loads)
+}
+
+// After the task's agent-coherent stores (each wavefront that stored waited for them): one increment
+// of the counter.
+__device__ __forceinline__ void one_signal(uint32_t *cnt) {
+    __syncthreads();
+    if (threadIdx.x < kCopies)
+        __hip_atomic_fetch_add(cnt + threadIdx.x * kCopyStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int KIND>
+struct OneGemv {  // a decode-GEMV task's requested first batch and bias
+    Batch<KIND> cur;
+    float pre_bias;
+};
+
+// Requests task (g, sp)'s first batch (wavefront w: blocks b0 + 8 w ..) and the lane's bias, as
+// decode_gemv_kernel does at its start.
+template <int KIND>
+__device__ __forceinline__ void one_issue(const DecodeGemv &a, uint32_t g, uint32_t sp, OneGemv<KIND> &t) {
+    constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int lane = threadIdx.x % 64, r = lane % 32;
+    const bool upper = lane >= 32;
+    const uint32_t nb = a.nb, nb8 = (nb + 7) / 8, span = nb8 * 8;
+    const uint32_t b0 = sp * a.chunk, b1 = min(span, b0 + a.chunk);
+    const auto rq = make_rsrc(a.qs + (size_t)g * nb * 32 * QB, nb * 32 * QB);
+    const auto rd = make_rsrc(a.ds + (size_t)g * nb8 * 256, nb8 * 512);
+    const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16);
+    const uint32_t bb = b0 + wave * kBatch;
+    if (bb < b1) load_weights<KIND>(t.cur, rq, rd, oq, (uint32_t)(r * 16), bb);
+    t.pre_bias = 0.0f;
+    if (wave == 0 && !upper && g * 32 + r < a.n && a.bias) t.pre_bias = a.bias[g * 32 + r];
+}
+
+// The rest of decode_gemv_kernel's task (g, sp) for PRO_LNR / PRO_NONE and EPI_QKV / EPI_GELU /
+// EPI_PARTIAL, with the workgroup's eight wavefronts (those past the task's batches add zeros,
+// after the others, so the sums are those of the narrower launch). store_x: this task stores the
+// residual row at a.x_out. Outputs are written with agent-coherent stores; each wavefront that
+// stored waits until its stores have landed.
+template <int KIND, int PRO, int EPI>
+__device__ __forceinline__ void one_run(const DecodeGemv &a, uint32_t g, uint32_t sp, OneGemv<KIND> &t, uint8_t *lds,
+                                        bool store_x) {
+    constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
+    constexpr uint32_t W = kStepWaves;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int lane = threadIdx.x % 64, r = lane % 32;
+    const bool upper = lane >= 32;
+    const uint32_t nb = a.nb, nb8 = (nb + 7) / 8, span = nb8 * 8;
+    const uint32_t b0 = sp * a.chunk, b1 = min(span, b0 + a.chunk);
+    const auto rq = make_rsrc(a.qs + (size_t)g * nb * 32 * QB, nb * 32 * QB);
+    const auto rd = make_rsrc(a.ds + (size_t)g * nb8 * 256, nb8 * 512);
+    const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16);
+    const uint32_t os = (uint32_t)(r * 16), oa = prep_a_offset(lane), ot = prep_tail_offset<KIND>(lane);
+    constexpr bool kLn = PRO == PRO_LNR;
+    uint8_t *prep = lds;
+    float *part = (float *)(lds + (kLn ? span : a.chunk) * kPrepBytes);
+    float *red = part + W * 32;
+    f32x4 v[kLnSlots];
+    if constexpr (kLn) {
+        StepArgs f{};
+        f.x_in = a.x_in;
+        f.part = a.rpart;
+        f.pbias = a.rbias;
+        f.nparts = a.nparts;
+        f.emb_qs = a.emb_qs;
+        f.emb_ds = a.emb_ds;
+        f.pos_tab = a.pos_tab;
+        f.inputs = a.inputs;
+        f.state = a.state;
+        f.x_out = nullptr;  // stored at the end (store_x)
+        f.d = nb * 32;
+        f.nb = nb;
+        residual_row<KIND>(f, v);
+        ln_records<KIND, false>(v, a.ln_g, a.ln_b, a.eps, nb, span, prep, red);
+    } else {
+        for (uint32_t blk = b0 + threadIdx.x / 8; blk < b1; blk += blockDim.x / 8) {
+            const int j = threadIdx.x % 8;
+            __attribute__((address_space(3))) uint32_t *rec =
+                (__attribute__((address_space(3))) uint32_t *)(prep + (blk - b0) * kPrepBytes);
+            if (blk < nb)
+                prep_values<KIND>(gload4(a.x + blk * 32 + 4 * j), j, rec);
+            else
+                zero_record(j, rec);
+        }
+    }
+    __syncthreads();
+    const uint32_t pbase = kLn ? 0 : b0;
+    float acc = 0.0f;
+    uint32_t bb = b0 + wave * kBatch;
+    Batch<KIND> nx;
+    while (bb < b1) {
+        const uint32_t nxt = bb + W * kBatch;
+        if (nxt < b1) load_weights<KIND>(nx, rq, rd, oq, os, nxt);
+        lds_byte *lp = (lds_byte *)prep;
+        t.cur.a = *(const __attribute__((address_space(3))) i32x4 *)(lp + (bb - pbase) * kPrepBytes + oa);
+        load_tails<KIND>(t.cur, (bb - pbase) * kPrepBytes, ot,
+                         [&](uint32_t off) { return *(const __attribute__((address_space(3))) u32x4 *)(lp + off); },
+                         [&](uint32_t off) { return *(const __attribute__((address_space(3))) uint32_t *)(lp + off); });
+        compute_batch<KIND>(t.cur, upper, acc);
+        t.cur = nx;
+        bb = nxt;
+    }
+    const float sum = half_sum(acc, upper);
+    if (!upper) part[wave * 32 + r] = sum;
+    __syncthreads();
+    if (wave == 0 && !upper) {
+        float s = 0.0f;
+        for (uint32_t w = 0; w < W; w++) s += part[w * 32 + r];
+        const uint32_t row = g * 32 + r;
+        if (row < a.n) {
+            if constexpr (EPI == EPI_PARTIAL) {
+                cstore(a.y + (size_t)sp * a.n + row, s);
+            } else {
+                if (a.bias) s = s + t.pre_bias;
+                if constexpr (EPI == EPI_GELU) {
+                    cstore(a.y + row, gelu(s));
+                } else {
+                    const uint32_t p = (uint32_t)a.state[0];
+                    if (row < a.split)
+                        cstore(a.y + row, s);
+                    else if (row < 2 * a.split)
+                        cstore(a.kc + (size_t)p * a.split + row - a.split, s);
+                    else
+                        cstore(a.vc + (size_t)p * a.split + row - 2 * a.split, s);
+                }
+            }
+        }
+    }
+    if (store_x) {
+#pragma unroll
+        for (uint32_t u = 0; u < kLnSlots; u++) {
+            const uint32_t sl = threadIdx.x + u * blockDim.x;
+            if (sl / 8 < nb) cstore4(a.x_out + sl * 4, v[u]);
+        }
+    }
+    if (wave == 0 || store_x) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the stores have landed
+}
+
+// One layer of a role (the arguments live in device memory and are read with scalar loads, which
+// keeps the kernel's scalar registers free). e1: this step's counter multiple; lds: the
+// workgroup's dynamic LDS.
+template <int KIND>
+__device__ __forceinline__ void one_qkv(const OneArgs *A, uint32_t l, uint32_t task, uint32_t e1, uint8_t *lds) {
+    // LN1 + QKV (layer 0: the embedding), as dgemv<PRO_LNR, EPI_QKV>
+    const OneLayer &Y = A->layers[l];
+    const uint32_t d = A->d, nb = d / 32;
+    DecodeGemv g{};
+    g.qs = Y.qkv_qs;
+    g.ds = Y.qkv_ds;
+    g.nb = nb;
+    g.n = 3 * d;
+    g.chunk = (nb + 7) / 8 * 8;
+    g.bias = Y.bqkv;
+    g.y = Y.q;
+    g.kc = Y.kc;
+    g.vc = Y.vc;
+    g.split = d;
+    g.state = A->state;
+    g.inputs = A->inputs;
+    g.ln_g = Y.ln1_g;
+    g.ln_b = Y.ln1_b;
+    g.eps = A->eps;
+    g.x_out = Y.xc;
+    if (l == 0) {
+        g.emb_qs = A->emb_qs;
+        g.emb_ds = A->emb_ds;
+        g.pos_tab = A->pos_tab;
+    } else {
+        g.x_in = A->layers[l - 1].xm;
+        g.rpart = A->layers[l - 1].pf;
+        g.rbias = A->layers[l - 1].b2;
+        g.nparts = A->S;
+    }
+    OneGemv<KIND> t;
+    one_issue<KIND>(g, task, 0, t);
+    if (l > 0) one_wait(A->sync + one_counter(l - 1, 3), e1 * A->nD, A->sync + one_counter(A->n_layers, 0));
+    one_run<KIND, PRO_LNR, EPI_QKV>(g, task, 0, t, lds, task == 0);
+    one_signal(A->sync + one_counter(l, 0));
+}
+
+template <int KIND, int L, int K2>
+__device__ __forceinline__ void one_attn(const OneArgs *A, uint32_t l, uint32_t task, uint32_t e1, uint8_t *lds) {
+    // attention of head `task` + its output-projection columns, as attn_out_kernel
+    constexpr int PAIRS = L / 16;
+    constexpr uint32_t hd = 4 * L;
+    const OneLayer &Y = A->layers[l];
+    const uint32_t d = A->d, nb = d / 32;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int lane = threadIdx.x % 64, r = lane % 32;
+    StepArgs sa{};
+    sa.q = Y.q;
+    sa.kc = Y.kc;
+    sa.vc = Y.vc;
+    sa.state = A->state;
+    sa.d = d;
+    sa.nb = nb;
+    sa.scale = A->scale;
+    sa.qs2 = Y.o_qs;
+    sa.ds2 = Y.o_ds;
+    sa.nb2 = nb;
+    sa.out_part = Y.po;
+    const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * (lane >= 32)) : (uint32_t)(lane * 16);
+    const uint32_t os = (uint32_t)(r * 16), oa = prep_a_offset(lane), ot = prep_tail_offset<KIND>(lane);
+    Batch<KIND> s2[K2];
+#pragma unroll
+    for (int i = 0; i < K2; i++)
+        if (wave + i * kStepWaves < nb) load_task2<KIND, PAIRS>(s2[i], sa, task, wave + i * kStepWaves, oq, os);
+    one_wait(A->sync + one_counter(l, 0), e1 * A->nA, A->sync + one_counter(A->n_layers, 0));
+    float *s = (float *)lds;
+    float *accs = s + kAttnSlots;
+    float *red = accs + kStepThreads * 4;
+    float *att = red + 2 * kStepWaves;
+    uint8_t *recs2 = (uint8_t *)(att + hd);
+    const uint32_t p = (uint32_t)A->state[0];
+    const size_t off = (size_t)task * hd;
+    attend_head<L>(task, Y.q + off, Y.kc + (size_t)p * d + off, Y.vc + (size_t)p * d + off, Y.kc, Y.vc, p + 1, d,
+                   A->scale, s, accs, red, att);
+    __syncthreads();
+    prep_lds<KIND>(att, hd, recs2);
+    __syncthreads();
+    run_tasks2<KIND, PAIRS, K2, true>(sa, task, s2, recs2, oq, os, oa, ot);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial rows have landed
+    one_signal(A->sync + one_counter(l, 1));
+}
+
+template <int KIND>
+__device__ __forceinline__ void one_up(const OneArgs *A, uint32_t l, uint32_t task, uint32_t e1, uint8_t *lds) {
+    // LN2 + FFN-up + GELU, as dgemv<PRO_LNR, EPI_GELU>
+    const OneLayer &Y = A->layers[l];
+    const uint32_t nb = A->d / 32;
+    DecodeGemv g{};
+    g.qs = Y.w1_qs;
+    g.ds = Y.w1_ds;
+    g.nb = nb;
+    g.n = A->hidden;
+    g.chunk = (nb + 7) / 8 * 8;
+    g.bias = Y.b1;
+    g.y = Y.f;
+    g.state = A->state;
+    g.ln_g = Y.ln2_g;
+    g.ln_b = Y.ln2_b;
+    g.eps = A->eps;
+    g.x_in = Y.xc;
+    g.rpart = Y.po;
+    g.rbias = Y.bo;
+    g.nparts = A->heads;
+    g.x_out = Y.xm;
+    OneGemv<KIND> t;
+    one_issue<KIND>(g, task, 0, t);
+    one_wait(A->sync + one_counter(l, 1), e1 * A->nB, A->sync + one_counter(A->n_layers, 0));
+    one_run<KIND, PRO_LNR, EPI_GELU>(g, task, 0, t, lds, task == 0);
+    one_signal(A->sync + one_counter(l, 2));
+}
+
+template <int KIND>
+__device__ __forceinline__ void one_down(const OneArgs *A, uint32_t l, uint32_t task, uint32_t e1, uint8_t *lds) {
+    // FFN-down task (row group, K split), as dgemv<PRO_NONE, EPI_PARTIAL>
+    const OneLayer &Y = A->layers[l];
+    const uint32_t gd = A->d / 32;
+    DecodeGemv g{};
+    g.qs = Y.w2_qs;
+    g.ds = Y.w2_ds;
+    g.nb = A->hidden / 32;
+    g.n = A->d;
+    g.chunk = A->chunk_down;
+    g.x = Y.f;
+    g.y = Y.pf;
+    g.state = A->state;
+    const uint32_t rg = task % gd, sp = task / gd;
+    OneGemv<KIND> t;
+    one_issue<KIND>(g, rg, sp, t);
+    one_wait(A->sync + one_counter(l, 2), e1 * A->nC, A->sync + one_counter(A->n_layers, 0));
+    one_run<KIND, PRO_NONE, EPI_PARTIAL>(g, rg, sp, t, lds, false);
+    one_signal(A->sync + one_counter(l, 3));
+}
+
+template <int KIND>
+__device__ __forceinline__ void one_final(const OneArgs *A, uint32_t e1, uint8_t *lds) {
+    // x = x_m + (sum of the down partial rows + b_2), its final LayerNorm into global records
+    const uint32_t nb = A->d / 32, L = A->n_layers;
+    one_wait(A->sync + one_counter(L - 1, 3), e1 * A->nD, A->sync + one_counter(L, 0));
+    StepArgs z{};
+    z.x_in = A->layers[L - 1].xm;
+    z.part = A->layers[L - 1].pf;
+    z.pbias = A->layers[L - 1].b2;
+    z.nparts = A->S;
+    z.state = A->state;
+    z.x_out = A->x_final;
+    z.d = A->d;
+    z.nb = nb;
+    f32x4 v[kLnSlots];
+    residual_row<KIND>(z, v);
+    ln_records<KIND, true>(v, A->lnf_g, A->lnf_b, A->eps, nb, (nb + 7) / 8 * 8, A->prep, (float *)lds);
+}
+
+// The whole layer stack of one decode step, then the final LayerNorm into the head's records
+// (workgroup 0). The first max(nA, nC) workgroups take QKV task w and FFN-up task w, the next
+// max(nB, nD) attention head t and FFN-down task t: each pair of roles is one phase apart in both
+// directions (QKV, then attention, FFN-up, FFN-down, the next layer's QKV), so a workgroup's next
+// weights are requested a phase before they are needed. A workgroup runs its tasks in the phases'
+// order, and a phase waits only for earlier phases, so with every workgroup resident each wait
+// ends.
+template <int KIND, int L, int K2>
+__global__ __launch_bounds__(kStepThreads) void one_step_kernel(const OneArgs *__restrict__ A) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t olds[];
+    const uint32_t w = blockIdx.x;
+    const uint32_t e1 = (uint32_t)A->state[3] + 1u;  // this step's counters reach e1 x tasks
+    const uint32_t nA = A->nA, nB = A->nB, nC = A->nC, nD = A->nD, layers = A->n_layers;
+    const uint32_t nAC = nA > nC ? nA : nC;
+    for (uint32_t l = 0; l < layers; l++) {
+        if (w < nAC) {
+            if (w < nA) one_qkv<KIND>(A, l, w, e1, olds);
+            if (w < nC) one_up<KIND>(A, l, w, e1, olds);
+        } else {
+            const uint32_t t = w - nAC;
+            if (t < nB) one_attn<KIND, L, K2>(A, l, t, e1, olds);
+            if (t < nD) one_down<KIND>(A, l, t, e1, olds);
+        }
+    }
+    if (w == 0) one_final<KIND>(A, e1, olds);
+}
+
+// LDS of one_step_kernel: the largest of its roles'.
+__host__ inline size_t one_lds(size_t d, size_t hd, uint32_t chunk_down) {
+    const size_t nb = d / 32, span = (nb + 7) / 8 * 8;
+    const size_t tail = (size_t)kStepWaves * 32 * 4 + kStepWaves * 4;
+    const size_t b = std::max(span * kPrepBytes + tail, (size_t)chunk_down * kPrepBytes + tail);
+    return std::max(b, (size_t)attn_out_lds((uint32_t)hd));
 }
 
 // Sets the position and the first position whose input the argmax writes.
@@ -851,6 +1279,12 @@ struct fh_gpt2 {
     float *xc = nullptr, *xm = nullptr;  // the residual row before / after the attention block
     float *po = nullptr, *pf = nullptr;  // partial rows: [heads][dim], [down_splits][dim]
     uint64_t step_bytes = 0;
+    // the one-launch step (form 1): the layer table, the phase counters and error flag, the grid
+    void *one_mem = nullptr;
+    uint32_t *sync = nullptr;
+    const void *one_args = nullptr;  // the kernel's arguments (OneArgs), in device memory
+    uint32_t one_tasks[4] = {0, 0, 0, 0};
+    size_t one_lds_bytes = 0;
 };
 
 namespace {
@@ -899,6 +1333,9 @@ template <int L> constexpr int attn_k2() { return L == 64 ? 2 : 3; }
     (const void *)attn_out_kernel<K, 16, attn_k2<16>()>, (const void *)attn_out_kernel<K, 32, attn_k2<32>()>,     \
         (const void *)attn_out_kernel<K, 64, attn_k2<64>()>
 constexpr uint32_t kAttnOutLdsMax = 96 * 1024;
+#define FH_ONE_KERNELS(K)                                                                                         \
+    (const void *)one_step_kernel<K, 16, attn_k2<16>()>, (const void *)one_step_kernel<K, 32, attn_k2<32>()>,     \
+        (const void *)one_step_kernel<K, 64, attn_k2<64>()>
 
 // Dynamic LDS beyond the default 64 KiB: prepared x of up to kMaxBlocks blocks plus the row
 // sums, and the attention scores of up to 16384 positions. Set once, before any capture.
@@ -910,7 +1347,8 @@ hipError_t set_lds_limits() {
             hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, gemv_lds);
             if (r) return r;
         }
-        const void *ao[] = {FH_ATTN_OUT_KERNELS(FH_Q8_0), FH_ATTN_OUT_KERNELS(FH_Q4_0)};
+        const void *ao[] = {FH_ATTN_OUT_KERNELS(FH_Q8_0), FH_ATTN_OUT_KERNELS(FH_Q4_0), FH_ONE_KERNELS(FH_Q8_0),
+                            FH_ONE_KERNELS(FH_Q4_0)};
         for (const void *f : ao) {
             hipError_t r = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnOutLdsMax);
             if (r) return r;
@@ -928,6 +1366,7 @@ hipError_t set_lds_limits() {
 }
 #undef FH_DGEMV_KERNELS
 #undef FH_ATTN_OUT_KERNELS
+#undef FH_ONE_KERNELS
 
 template <int PRO, int EPI>
 hipError_t dgemv(hipStream_t s, fh_kind kind, const DecodeGemv &a, bool allow_split = false) {
@@ -1133,8 +1572,131 @@ hipError_t enqueue_four(fh_gpt2 *m, hipStream_t s) {
     return enqueue_head(m, s, m->xm, m->pf, S, fp(m->blocks.back().b2));
 }
 
+template <int KIND>
+const void *one_kernel(uint32_t hd) {
+    return hd == 64 ? (const void *)one_step_kernel<KIND, 16, attn_k2<16>()>
+                    : hd == 128 ? (const void *)one_step_kernel<KIND, 32, attn_k2<32>()>
+                                : (const void *)one_step_kernel<KIND, 64, attn_k2<64>()>;
+}
+
+// Enqueue one one-launch step: every layer and the final LayerNorm in one_step_kernel, then the head
+// product and the pick.
+hipError_t enqueue_one(fh_gpt2 *m, hipStream_t s) {
+    const uint32_t hd = (uint32_t)(m->dim / m->heads);
+    const uint32_t grid = std::max(m->one_tasks[0], m->one_tasks[2]) + std::max(m->one_tasks[1], m->one_tasks[3]);
+    const OneArgs *args = (const OneArgs *)m->one_args;
+    void *kargs[] = {&args};
+    hipError_t e = hipLaunchKernel(m->kind == FH_Q8_0 ? one_kernel<FH_Q8_0>(hd) : one_kernel<FH_Q4_0>(hd), dim3(grid),
+                                   dim3(kStepThreads), kargs, m->one_lds_bytes, s);
+    if (e) return e;
+    DecodeGemv h = dg(m, m->head, m->x, m->logits);
+    h.prep = m->prep;
+    h.pick = m->pick;
+    if ((e = dgemv<PRO_GLOBAL, EPI_ARGMAX>(s, m->kind, h))) return e;
+    pick_kernel<<<1, 1024, 0, s>>>(m->partial, m->pick, (uint32_t)((m->vocab + 31) / 32), m->state, m->inputs);
+    return hipGetLastError();
+}
+
+// Sets up the one-launch step where it fits: head widths 64, 128, 256, and all of its workgroups
+// resident at once (the occupancy query). Returns false (the four-launch step stays) otherwise.
+bool one_setup(fh_gpt2 *m) {
+    const size_t d = m->dim, hd = d / m->heads;
+    if (m->form != 4 || m->layers > kOneMaxLayers) return false;
+    uint32_t sp, c8;
+    plan_splits((uint32_t)(d / 32), (uint32_t)((m->hidden / 32 + 7) / 8), &sp, &c8);
+    const uint32_t tasks[4] = {(uint32_t)(3 * d / 32), (uint32_t)m->heads, (uint32_t)(m->hidden / 32),
+                               (uint32_t)(d / 32) * sp};
+    const uint32_t grid = std::max(tasks[0], tasks[2]) + std::max(tasks[1], tasks[3]);
+    const size_t lds = one_lds(d, hd, c8 * 8);
+    if (lds > kAttnOutLdsMax) return false;
+    int dev = 0, cus = 0, per = 0;
+    const void *k = m->kind == FH_Q8_0 ? one_kernel<FH_Q8_0>((uint32_t)hd) : one_kernel<FH_Q4_0>((uint32_t)hd);
+    if (hipGetDevice(&dev) || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, kStepThreads, lds))
+        return false;
+    if ((uint64_t)per * (uint64_t)cus < grid) return false;
+    auto up = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
+    const size_t table = m->layers * sizeof(OneLayer), sync = (size_t)one_counter((uint32_t)m->layers + 1, 0) * 4;
+    const size_t per_layer = 3 * up(d * 4) + up(m->heads * d * 4) + up((size_t)sp * d * 4) + up(m->hidden * 4);
+    const size_t bufs0 = up(table) + up(sync) + up(sizeof(OneArgs));
+    if (alloc_bytes(m->dev, bufs0 + m->layers * per_layer, &m->one_mem)) return false;
+    std::vector<OneLayer> t(m->layers);
+    for (size_t l = 0; l < m->layers; l++) {
+        const auto &L = m->blocks[l];
+        uint8_t *b = (uint8_t *)m->one_mem + bufs0 + l * per_layer;
+        float *q = (float *)b, *xc = (float *)(b + up(d * 4)), *xm = (float *)(b + 2 * up(d * 4));
+        float *po = (float *)(b + 3 * up(d * 4)), *pf = (float *)((uint8_t *)po + up(m->heads * d * 4));
+        float *f = (float *)((uint8_t *)pf + up((size_t)sp * d * 4));
+        t[l] = OneLayer{L.wqkv->qs, L.wo->qs, L.w1->qs, L.w2->qs, L.wqkv->ds, L.wo->ds, L.w1->ds, L.w2->ds,
+                        fp(L.ln1_g), fp(L.ln1_b), fp(L.bqkv), fp(L.bo), fp(L.ln2_g), fp(L.ln2_b), fp(L.b1), fp(L.b2),
+                        L.kc, L.vc, q, xc, xm, po, pf, f};
+    }
+    m->sync = (uint32_t *)((uint8_t *)m->one_mem + up(table));
+    OneArgs a{};
+    a.layers = (const OneLayer *)m->one_mem;
+    a.n_layers = (uint32_t)m->layers;
+    a.emb_qs = m->tok->qs;
+    a.emb_ds = m->tok->ds;
+    a.pos_tab = fp(m->pos_tab);
+    a.inputs = m->inputs;
+    a.state = m->state;
+    a.x_final = m->x;
+    a.lnf_g = fp(m->lnf_g);
+    a.lnf_b = fp(m->lnf_b);
+    a.prep = m->prep;
+    a.sync = m->sync;
+    a.d = (uint32_t)d;
+    a.hidden = (uint32_t)m->hidden;
+    a.heads = (uint32_t)m->heads;
+    a.S = sp;
+    a.chunk_down = c8 * 8;
+    a.eps = m->eps;
+    a.scale = 1.0f / sqrtf((float)hd);
+    a.nA = tasks[0];
+    a.nB = tasks[1];
+    a.nC = tasks[2];
+    a.nD = tasks[3];
+    m->one_args = (const void *)((uint8_t *)m->sync + up(sync));
+    // on the device stream, after the allocation's own clearing; the host copies are pageable
+    hipStream_t st = m->dev->stream;
+    if (hipMemcpyAsync(m->one_mem, t.data(), table, hipMemcpyHostToDevice, st) ||
+        hipMemsetAsync(m->sync, 0, sync, st) ||
+        hipMemcpyAsync((void *)m->one_args, &a, sizeof(a), hipMemcpyHostToDevice, st) || hipStreamSynchronize(st)) {
+        (void)hipFree(m->one_mem);
+        m->one_mem = nullptr;
+        m->sync = nullptr;
+        return false;
+    }
+    for (int i = 0; i < 4; i++) m->one_tasks[i] = tasks[i];
+    m->one_lds_bytes = lds;
+    m->form = 1;
+    return true;
+}
+
+// After a one-launch step's work has completed: a wait that gave up (a workgroup not resident)
+// leaves its flag; the counters are then reset and the model keeps the four-launch step.
+fh_status one_check(fh_gpt2 *m) {
+    if (m->form != 1) return FH_OK;
+    uint32_t flag = 0;
+    hipStream_t st = m->dev->stream;
+    hipError_t e = hipMemcpyAsync(&flag, m->sync + one_counter((uint32_t)m->layers, 0), 4, hipMemcpyDeviceToHost, st);
+    if (!e) e = hipStreamSynchronize(st);
+    if (e) return hip_fail(m->dev, e, "gpt2 step");
+    if (!flag) return FH_OK;
+    (void)hipMemsetAsync(m->sync, 0, (size_t)one_counter((uint32_t)m->layers + 1, 0) * 4, st);
+    (void)hipMemsetAsync(m->state + 3, 0, 4, st);
+    (void)hipStreamSynchronize(st);
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    m->exec = nullptr;
+    m->graph = nullptr;
+    m->form = 4;
+    return fail(FH_ERR_DEVICE, "gpt2 step: the one-launch step's workgroups did not all run at once (a wait gave "
+                               "up); the model now runs the four-launch step");
+}
+
 hipError_t enqueue_any(fh_gpt2 *m, hipStream_t s) {
-    return m->form == 4 ? enqueue_four(m, s) : enqueue_step(m, s);
+    return m->form == 1 ? enqueue_one(m, s) : m->form == 4 ? enqueue_four(m, s) : enqueue_step(m, s);
 }
 
 // Run one step on the device stream: the captured graph (made on first use), or the launches.
@@ -1329,6 +1891,7 @@ fh_status fh_gpt2_from_gguf(fh_device *dev, const fh_gguf *g, fh_gpt2 **out) {
         m->pf = (float *)p;
     }
     if (hipError_t e = set_lds_limits()) return gpt2_fail_free(m, hip_fail(dev, e, "gpt2 kernels"));
+    if (!(sf && atoi(sf) == 4)) (void)one_setup(m);
     const char *ng = getenv("FERRUM_HIP_NO_GRAPH");
     m->use_graph = !(ng && ng[0] == '1');
     const char *sk = getenv("FERRUM_HIP_DECODE_SPLIT_K");
@@ -1358,7 +1921,7 @@ size_t fh_gpt2_pos(const fh_gpt2 *m) { return m ? m->pos : 0; }
 uint64_t fh_gpt2_step_bytes(const fh_gpt2 *m) { return m ? m->step_bytes : 0; }
 size_t fh_gpt2_step_launches(const fh_gpt2 *m) {
     if (!m) return 0;
-    return m->form == 4 ? 4 * m->layers + 3 : 5 * m->layers + 4;
+    return m->form == 1 ? 3 : m->form == 4 ? 4 * m->layers + 3 : 5 * m->layers + 4;
 }
 void fh_gpt2_reset(fh_gpt2 *m) {
     if (m) m->pos = 0;  // later positions overwrite the cache rows they read
@@ -1375,6 +1938,11 @@ fh_status fh_gpt2_feed(fh_device *dev, fh_gpt2 *m, size_t token, float *logits) 
     set_input_kernel<<<1, 1, 0, dev->stream>>>(m->inputs, (int32_t)m->pos, (int32_t)token);
     if ((st = end_command(dev, "gpt2 feed"))) return st;
     if ((st = run_step(m))) return st;
+    if (m->form == 1) {
+        hipError_t e = hipStreamSynchronize(dev->stream);
+        if (e) return hip_fail(dev, e, "gpt2 feed");
+        if ((st = one_check(m))) return st;
+    }
     if (logits) {
         if ((st = begin_command(dev, "gpt2 logits"))) return st;
         hipError_t e = hipMemcpyAsync(logits, m->logits, m->vocab * 4, hipMemcpyDeviceToHost, dev->stream);
@@ -1415,6 +1983,7 @@ fh_status fh_gpt2_generate(fh_device *dev, fh_gpt2 *m, const int32_t *prompt, si
         if (e) return hip_fail(dev, e, "gpt2 tokens");
     }
     if ((e = hipStreamSynchronize(dev->stream))) return hip_fail(dev, e, "gpt2 generate");
+    if ((st = one_check(m))) return st;
     m->pos = p0 + steps;
     return FH_OK;
 }
@@ -1432,6 +2001,7 @@ void fh_gpt2_free(fh_gpt2 *m) {
     }
     for (fh_buffer *b : {m->pos_tab, m->lnf_g, m->lnf_b}) fh_buffer_free(b);
     if (m->arena) (void)hipFree(m->arena);
+    if (m->one_mem) (void)hipFree(m->one_mem);
     if (m->dev) dev_release(m->dev);
     delete m;
 }
