@@ -868,10 +868,12 @@ struct OneArgs {
     float *x_final;
     const float *lnf_g, *lnf_b;
     uint8_t *prep;   // the final LayerNorm's prepared records (the head's x)
-    uint32_t *sync;  // [n_layers][4] completion counters (one_counter), then the error flag
+    uint32_t *sync;  // completion counters, [n_layers][slots] (one_slot), then the error flag
     uint32_t d, hidden, heads, S, chunk_down;
     float eps, scale;
     uint32_t nA, nB, nC, nD;
+    uint32_t slots;  // counters per layer: heads (QKV, one per head) + 1 (attention) + S (FFN-up, one per
+                     // FFN-down K chunk) + 1 (FFN-down)
 };
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr uint32_t kOneMaxLayers = 256;
@@ -881,7 +883,9 @@ constexpr uint32_t kOneMaxLayers = 256;
 // with 8 copies; 32 were 2% faster again (measured, GPT-2-small).
 constexpr uint32_t kCopies = 32, kCopyStride = 32;  // (in uint32_t)
 constexpr uint32_t kCounter = kCopies * kCopyStride;  // uint32_t per counter
-__host__ __device__ constexpr uint32_t one_counter(uint32_t l, uint32_t phase) { return (4 * l + phase) * kCounter; }
+__host__ __device__ constexpr uint32_t one_counter(uint32_t l, uint32_t slot, uint32_t slots) {
+    return (l * slots + slot) * kCounter;
+}
 
 // Waits until the counter at cnt reaches target (wrapping compare), bounded as above.
 __device__ __forceinline__ void one_wait(uint32_t *cnt, uint32_t target, uint32_t *err) {
@@ -1074,9 +1078,10 @@ __device__ __forceinline__ void one_qkv(const OneArgs *A, uint32_t l, uint32_t t
     }
     OneGemv<KIND> t;
     one_issue<KIND>(g, task, 0, t);
-    if (l > 0) one_wait(A->sync + one_counter(l - 1, 3), e1 * A->nD, A->sync + one_counter(A->n_layers, 0));
+    const uint32_t H = A->heads, S = A->S, Z = A->slots;
+    if (l > 0) one_wait(A->sync + one_counter(l - 1, H + 1 + S, Z), e1 * A->nD, A->sync + one_counter(A->n_layers, 0, Z));
     one_run<KIND, PRO_LNR, EPI_QKV>(g, task, 0, t, lds, task == 0);
-    one_signal(A->sync + one_counter(l, 0));
+    one_signal(A->sync + one_counter(l, (task * 32 % d) / (d / H), Z));  // this row group's head
 }
 
 template <int KIND, int L, int K2>
@@ -1106,7 +1111,8 @@ __device__ __forceinline__ void one_attn(const OneArgs *A, uint32_t l, uint32_t 
 #pragma unroll
     for (int i = 0; i < K2; i++)
         if (wave + i * kStepWaves < nb) load_task2<KIND, PAIRS>(s2[i], sa, task, wave + i * kStepWaves, oq, os);
-    one_wait(A->sync + one_counter(l, 0), e1 * A->nA, A->sync + one_counter(A->n_layers, 0));
+    // the head's q, k and v row groups
+    one_wait(A->sync + one_counter(l, task, A->slots), e1 * 3 * (hd / 32), A->sync + one_counter(A->n_layers, 0, A->slots));
     float *s = (float *)lds;
     float *accs = s + kAttnSlots;
     float *red = accs + kStepThreads * 4;
@@ -1121,7 +1127,7 @@ __device__ __forceinline__ void one_attn(const OneArgs *A, uint32_t l, uint32_t 
     __syncthreads();
     run_tasks2<KIND, PAIRS, K2, true>(sa, task, s2, recs2, oq, os, oa, ot);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial rows have landed
-    one_signal(A->sync + one_counter(l, 1));
+    one_signal(A->sync + one_counter(l, A->heads, A->slots));
 }
 
 template <int KIND>
@@ -1148,9 +1154,10 @@ __device__ __forceinline__ void one_up(const OneArgs *A, uint32_t l, uint32_t ta
     g.x_out = Y.xm;
     OneGemv<KIND> t;
     one_issue<KIND>(g, task, 0, t);
-    one_wait(A->sync + one_counter(l, 1), e1 * A->nB, A->sync + one_counter(A->n_layers, 0));
+    one_wait(A->sync + one_counter(l, A->heads, A->slots), e1 * A->nB, A->sync + one_counter(A->n_layers, 0, A->slots));
     one_run<KIND, PRO_LNR, EPI_GELU>(g, task, 0, t, lds, task == 0);
-    one_signal(A->sync + one_counter(l, 2));
+    // the FFN-down K chunk this row group of f belongs to
+    one_signal(A->sync + one_counter(l, A->heads + 1 + task * 32 / A->chunk_down / 32, A->slots));
 }
 
 template <int KIND>
@@ -1170,16 +1177,20 @@ __device__ __forceinline__ void one_down(const OneArgs *A, uint32_t l, uint32_t 
     const uint32_t rg = task % gd, sp = task / gd;
     OneGemv<KIND> t;
     one_issue<KIND>(g, rg, sp, t);
-    one_wait(A->sync + one_counter(l, 2), e1 * A->nC, A->sync + one_counter(A->n_layers, 0));
+    // the FFN-up row groups of this task's K chunk
+    const uint32_t cb = A->chunk_down, in_chunk = min(cb, A->hidden / 32 - sp * cb);
+    one_wait(A->sync + one_counter(l, A->heads + 1 + sp, A->slots), e1 * in_chunk,
+             A->sync + one_counter(A->n_layers, 0, A->slots));
     one_run<KIND, PRO_NONE, EPI_PARTIAL>(g, rg, sp, t, lds, false);
-    one_signal(A->sync + one_counter(l, 3));
+    one_signal(A->sync + one_counter(l, A->heads + 1 + A->S, A->slots));
 }
 
 template <int KIND>
 __device__ __forceinline__ void one_final(const OneArgs *A, uint32_t e1, uint8_t *lds) {
     // x = x_m + (sum of the down partial rows + b_2), its final LayerNorm into global records
     const uint32_t nb = A->d / 32, L = A->n_layers;
-    one_wait(A->sync + one_counter(L - 1, 3), e1 * A->nD, A->sync + one_counter(L, 0));
+    one_wait(A->sync + one_counter(L - 1, A->heads + 1 + A->S, A->slots), e1 * A->nD,
+             A->sync + one_counter(L, 0, A->slots));
     StepArgs z{};
     z.x_in = A->layers[L - 1].xm;
     z.part = A->layers[L - 1].pf;
@@ -1616,7 +1627,8 @@ bool one_setup(fh_gpt2 *m) {
         return false;
     if ((uint64_t)per * (uint64_t)cus < grid) return false;
     auto up = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
-    const size_t table = m->layers * sizeof(OneLayer), sync = (size_t)one_counter((uint32_t)m->layers + 1, 0) * 4;
+    const uint32_t slots = (uint32_t)m->heads + sp + 2;
+    const size_t table = m->layers * sizeof(OneLayer), sync = (size_t)one_counter((uint32_t)m->layers, 1, slots) * 4;
     const size_t per_layer = 3 * up(d * 4) + up(m->heads * d * 4) + up((size_t)sp * d * 4) + up(m->hidden * 4);
     const size_t bufs0 = up(table) + up(sync) + up(sizeof(OneArgs));
     if (alloc_bytes(m->dev, bufs0 + m->layers * per_layer, &m->one_mem)) return false;
@@ -1656,6 +1668,7 @@ bool one_setup(fh_gpt2 *m) {
     a.nB = tasks[1];
     a.nC = tasks[2];
     a.nD = tasks[3];
+    a.slots = slots;
     m->one_args = (const void *)((uint8_t *)m->sync + up(sync));
     // on the device stream, after the allocation's own clearing; the host copies are pageable
     hipStream_t st = m->dev->stream;
@@ -1679,11 +1692,12 @@ fh_status one_check(fh_gpt2 *m) {
     if (m->form != 1) return FH_OK;
     uint32_t flag = 0;
     hipStream_t st = m->dev->stream;
-    hipError_t e = hipMemcpyAsync(&flag, m->sync + one_counter((uint32_t)m->layers, 0), 4, hipMemcpyDeviceToHost, st);
+    const uint32_t slots = (uint32_t)m->heads + m->down_splits + 2;
+    hipError_t e = hipMemcpyAsync(&flag, m->sync + one_counter((uint32_t)m->layers, 0, slots), 4, hipMemcpyDeviceToHost, st);
     if (!e) e = hipStreamSynchronize(st);
     if (e) return hip_fail(m->dev, e, "gpt2 step");
     if (!flag) return FH_OK;
-    (void)hipMemsetAsync(m->sync, 0, (size_t)one_counter((uint32_t)m->layers + 1, 0) * 4, st);
+    (void)hipMemsetAsync(m->sync, 0, (size_t)one_counter((uint32_t)m->layers, 1, slots) * 4, st);
     (void)hipMemsetAsync(m->state + 3, 0, 4, st);
     (void)hipStreamSynchronize(st);
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
