@@ -894,6 +894,122 @@ __device__ __forceinline__ void asm_load_lds4(i32x4 r, uint32_t lds, uint32_t vo
                  : "m0");
 }
 
+// ---- the scoring head's score epilogue (both streaming kernels) ----
+// nn::score (ferrum_ref/src/kernels/nn.rs:117-129) per row is a maximum, a sum of exp(v - max) and
+// the first column holding the maximum; they merge across stretches of the row as score_kernel's
+// lane groups do (the sums rescaled to the larger maximum; the smaller column wins a tie). The
+// head's epilogue reduces each row's 256 columns of a tile to these three (the logits themselves,
+// 1.24 GB at 2048 x 151,936, are never written), a small pass merges the tiles in order.
+constexpr uint32_t kNoCol = 0xffffffffu;
+__device__ __forceinline__ void score_merge(float &m, float &s, uint32_t &f, float m2, float s2, uint32_t f2) {
+    const float mx = fmaxf(m, m2);
+    s = (m == -INFINITY ? 0.0f : s * __expf(m - mx)) + (m2 == -INFINITY ? 0.0f : s2 * __expf(m2 - mx));
+    f = m2 > m || (m2 == m && f2 < f) ? f2 : f;
+    m = mx;
+}
+
+// One halving step of score_tile's row exchange: lanes whose bit W is clear keep rows 0..W-1 of
+// their set, the others rows W..2W-1 (renumbered from 0), each merged with its partner lane's copy.
+template <int W>
+__device__ __forceinline__ void score_halve(float (&vm)[32], float (&vs)[32], uint32_t (&vf)[32], int fr) {
+    const bool hi = (fr & W) != 0;
+#pragma unroll
+    for (int k = 0; k < W; k++) {
+        const float sm = hi ? vm[k] : vm[k + W], ss = hi ? vs[k] : vs[k + W];
+        const uint32_t sf = hi ? vf[k] : vf[k + W];
+        const float rm = __shfl_xor(sm, W), rs = __shfl_xor(ss, W);
+        const uint32_t rf = (uint32_t)__shfl_xor((int)sf, W);
+        float km = hi ? vm[k + W] : vm[k], ks = hi ? vs[k + W] : vs[k];
+        uint32_t kf = hi ? vf[k + W] : vf[k];
+        score_merge(km, ks, kf, rm, rs, rf);
+        vm[k] = km;
+        vs[k] = ks;
+        vf[k] = kf;
+    }
+}
+
+// The epilogue of the 256 x 256 tile at (m0, n0) (acc: the wavefront's 2 x 4 32x32 tiles, register
+// r of lane l holding row 8 (r / 4) + 4 (l / 32) + r % 4 and column l % 32 of its tile). Per lane
+// and row: the statistics of its four columns; then the 32 lanes of a half-wavefront, which share
+// 16 x 2 rows, halve their rows five times (each lane keeps one half and merges the partner's copy
+// of it), which leaves lane l with row l % 32 of its half over the wavefront's 128 columns; the
+// wavefronts of the two column halves meet through xch (3 KB of LDS), and so.part[row][n0 / 256]
+// gets the tile's statistics. The lane whose column is a row's target writes the logit. Every
+// wavefront of the CTA calls it (one barrier).
+__device__ __forceinline__ void score_tile(const f32x16 (&acc)[2][4], uint32_t m0, uint32_t n0, uint32_t M, uint32_t N,
+                                           const ScoreOut &so, uint8_t *xch) {
+    const int lane = threadIdx.x % 64, fr = lane % 32, hf = lane / 32;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), wm = wave % 4, wn = wave / 4;
+    const uint32_t cb = n0 + wn * 128 + fr;  // the lane's column in tile j = 0 (+ 32 j)
+    float vm[32], vs[32];
+    uint32_t vf[32];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            // the targets of band rows i 32 + 8 q .. + 7 (scalar loads; so.tgt is padded)
+            const int32_t *tb = so.tgt + m0 + wm * 64 + i * 32 + 8 * q;
+            int32_t T[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) T[e] = tb[e];
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) {
+                const int r = 4 * q + rr, k = 16 * i + r;
+                float v[4], mx = -INFINITY;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    v[j] = cb + 32 * j < N ? acc[i][j][r] : -INFINITY;
+                    mx = fmaxf(mx, v[j]);
+                }
+                uint32_t first = kNoCol;
+#pragma unroll
+                for (int j = 3; j >= 0; j--)
+                    if (v[j] == mx) first = cb + 32 * j;
+                float sum = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (cb + 32 * j < N) sum += __expf(v[j] - mx);
+                vm[k] = mx;
+                vs[k] = sum;
+                vf[k] = first;
+                int32_t t0 = T[rr], t1 = T[4 + rr];  // (named values, as below)
+                asm volatile("" : "+v"(t0), "+v"(t1));
+                const int32_t t = hf ? t1 : t0;
+                const int32_t dt = t - (int32_t)cb;
+                const uint32_t row = m0 + wm * 64 + i * 32 + 8 * q + 4 * hf + rr;
+                if (dt >= 0 && dt < 128 && (dt & 31) == 0 && row < M) {
+                    // (four named values: a select among the array's elements would become an indexed
+                    // access and put the accumulators in scratch memory)
+                    float a0 = v[0], a1 = v[1], a2 = v[2], a3 = v[3];
+                    asm volatile("" : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3));
+                    so.tlogit[row] = dt == 0 ? a0 : dt == 32 ? a1 : dt == 64 ? a2 : a3;
+                }
+            }
+        }
+    score_halve<16>(vm, vs, vf, fr);
+    score_halve<8>(vm, vs, vf, fr);
+    score_halve<4>(vm, vs, vf, fr);
+    score_halve<2>(vm, vs, vf, fr);
+    score_halve<1>(vm, vs, vf, fr);
+    // lane l now holds row k = l % 32 of its half: i = k / 16, r = k % 16
+    float *xm = (float *)xch, *xs = xm + 256;
+    uint32_t *xf = (uint32_t *)(xs + 256);
+    const uint32_t slot = wm * 64 + lane;
+    if (wn == 1) {
+        xm[slot] = vm[0];
+        xs[slot] = vs[0];
+        xf[slot] = vf[0];
+    }
+    __syncthreads();
+    if (wn == 0) {
+        score_merge(vm[0], vs[0], vf[0], xm[slot], xs[slot], xf[slot]);
+        const int k = fr, i = k / 16, r = k % 16;
+        const uint32_t row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * hf + r % 4;
+        if (row < M)
+            *(f32x4 *)(so.part + ((size_t)row * so.ntn + n0 / 256) * 4) = f32x4{vm[0], vs[0], __uint_as_float(vf[0]), 0.0f};
+    }
+}
+
 template <int KIND>
 struct StreamLds {  // byte offsets of the rings inside the kernel's LDS arena
     static constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
@@ -904,16 +1020,17 @@ struct StreamLds {  // byte offsets of the rings inside the kernel's LDS arena
     static constexpr uint32_t TOTAL = D + 2 * D_SZ;
 };
 
-template <int KIND>
+// SCORE: the scoring head's epilogue (score_tile into so) instead of the stores.
+template <int KIND, bool SCORE = false>
 __global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Float16 *__restrict__ xs,
                                                                      const uint8_t *__restrict__ qs,
                                                                      const uint16_t *__restrict__ ds,
                                                                      float *__restrict__ y, uint32_t M, uint32_t K,
                                                                      uint32_t N, uint32_t mt, uint32_t nt,
-                                                                     uint32_t split_stages) {
+                                                                     uint32_t split_stages, ScoreOut so) {
     using S = StreamLds<KIND>;
     constexpr uint32_t QB = S::QB;
-    __shared__ __attribute__((aligned(1024))) uint8_t arena[S::TOTAL];
+    __shared__ __attribute__((aligned(1024))) uint8_t arena[S::TOTAL + (SCORE ? 3072 : 0)];
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t *)arena;
 
     // This CTA's tiles, as gemm_f16_big_kernel deals them: XCD x (blockIdx.x % 8) owns the x-th
@@ -1082,6 +1199,9 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Floa
     auto epilogue = [&]() {
         uint32_t m0, n0;
         origin(ct++, m0, n0);
+        if constexpr (SCORE) {
+            score_tile(acc, m0, n0, M, N, so, arena + S::TOTAL);
+        } else {
         // D layout of a 32x32 tile: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32
 #pragma unroll
         for (int i = 0; i < 2; i++)
@@ -1095,6 +1215,7 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Floa
                     if (col < N) y[(size_t)row * N + col] = acc[i][j][r];
                 }
             }
+        }
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -1174,7 +1295,8 @@ struct FastLds {  // byte offsets inside the kernel's LDS arena
 
 __device__ __forceinline__ uint32_t swz64(uint32_t r, uint32_t c) { return (r * 4 + (c ^ ((r >> 2) & 3))) * 16; }
 
-template <int KIND>
+// SCORE: the scoring head's epilogue (score_tile into so) instead of the stores.
+template <int KIND, bool SCORE = false>
 __global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16 *__restrict__ xh,
                                                                   const uint8_t *__restrict__ xl,
                                                                   const int32_t *__restrict__ xsc,
@@ -1184,12 +1306,12 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16
                                                                   const int32_t *__restrict__ bsc,
                                                                   float *__restrict__ y, uint32_t M, uint32_t K,
                                                                   uint32_t N, uint32_t mt, uint32_t nt,
-                                                                  uint32_t split_stages) {
+                                                                  uint32_t split_stages, ScoreOut so) {
     // split_stages is even, so every split and every tile starts on an even block (pairs never
     // straddle them)
     using S = FastLds<KIND>;
     constexpr uint32_t QB = S::QB;
-    __shared__ __attribute__((aligned(1024))) uint8_t arena[S::TOTAL];
+    __shared__ __attribute__((aligned(1024))) uint8_t arena[S::TOTAL + (SCORE ? 3072 : 0)];
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t *)arena;
 
     constexpr uint32_t GM = 8;
@@ -1385,6 +1507,9 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16
         }
     };
     auto epilogue = [&]() {
+        if constexpr (SCORE) {
+            score_tile(acc, cm0, cn0, M, N, so, arena + S::TOTAL);
+        } else {
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -1397,6 +1522,7 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16
                     if (col < N) y[(size_t)row * N + col] = acc[i][j][r];
                 }
             }
+        }
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -1490,7 +1616,8 @@ hipError_t run_gemm_stream_precise(hipStream_t s, const _Float16 *xs, const uint
     const uint32_t stages = K / 32;
     const uint32_t per = (stages + sp - 1) / sp;
     float *out = sp > 1 ? partial : y;
-    gemm_stream_precise_kernel<KIND><<<dim3(8 * ctas, sp), 512, 0, s>>>(xs, qs, ds, out, M, K, N, mt, nt, per);
+    gemm_stream_precise_kernel<KIND><<<dim3(8 * ctas, sp), 512, 0, s>>>(xs, qs, ds, out, M, K, N, mt, nt, per,
+                                                                        ScoreOut{});
     if (defer) *defer = sp > 1 ? SplitOut{partial, sp} : SplitOut{y, 1u};
     if (sp > 1 && !defer) {
         const size_t n = (size_t)M * N;
@@ -1533,7 +1660,7 @@ hipError_t run_gemm_stream_fast(hipStream_t s, const GemmArgs &g, uint32_t sp) {
     const uint32_t per = ((stages + sp - 1) / sp + 1) & ~1u;  // even: pairs never straddle a split
     float *out = sp > 1 ? g.partial : g.y;
     gemm_stream_fast_kernel<KIND><<<dim3(8 * ctas, sp), 512, 0, s>>>(g.xh, g.xl, g.xsc, g.qs, g.ds, g.b8, g.bsc, out,
-                                                                      g.M, g.K, g.N, mt, nt, per);
+                                                                      g.M, g.K, g.N, mt, nt, per, ScoreOut{});
     if (g.defer) *g.defer = sp > 1 ? SplitOut{g.partial, sp} : SplitOut{g.y, 1u};
     if (sp > 1 && !g.defer) {
         const size_t n = (size_t)g.M * g.N;
@@ -1561,6 +1688,31 @@ hipError_t gemm_fast_dispatch(hipStream_t s, const GemmArgs &g) {
     if (stream_fast_plan(g.M, g.K, g.N, &sp) && stream_fast_supported(g.M, g.K, g.N) && (sp == 1 || g.partial))
         return run_gemm_stream_fast<KIND>(s, g, sp);
     return gemm_dispatch<KIND>(s, g);
+}
+
+// The scoring head with the score epilogue: the streaming kernels with one K split (the head's K
+// is the model width, a few dozen stages) over every tile.
+
+template <int KIND>
+hipError_t run_gemm_score(hipStream_t s, fh_path path, const void *xa, const uint8_t *xl, const int32_t *xsc,
+                          const uint8_t *qs, const uint16_t *ds, const uint8_t *b8, const int32_t *bsc, uint32_t M,
+                          uint32_t K, uint32_t N, const ScoreOut &so) {
+    const uint32_t mt = (M + 255) / 256, nt = (N + 255) / 256;
+    const uint64_t tiles = (uint64_t)mt * nt;
+    if (tiles > 0x7ffffff0ull || nt != so.ntn) return hipErrorInvalidValue;
+    const uint32_t per_xcd = (uint32_t)((tiles + 7) / 8);
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8)
+        cus = 256;
+    const uint32_t ctas = min(per_xcd, (uint32_t)cus / 8), stages = K / 32;
+    if (path == FH_PATH_TILED_FAST)
+        gemm_stream_fast_kernel<KIND, true><<<dim3(8 * ctas, 1), 512, 0, s>>>(
+            (const _Float16 *)xa, xl, xsc, qs, ds, b8, bsc, nullptr, M, K, N, mt, nt, (stages + 1) & ~1u, so);
+    else
+        gemm_stream_precise_kernel<KIND, true><<<dim3(8 * ctas, 1), 512, 0, s>>>((const _Float16 *)xa, qs, ds, nullptr,
+                                                                                 M, K, N, mt, nt, stages, so);
+    return hipGetLastError();
 }
 
 // ---- the MFMA GEMM on the other weight formats' GGUF rows (F16, FP8 E4M3 / E5M2, MXFP4) ----
@@ -2665,6 +2817,42 @@ hipError_t launch_gemm_f16(hipStream_t s, fh_kind kind, const uint8_t *qs, const
     }
     split_x_f16_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (float *)g.xs, g.K);
     return gemm_f16_dispatch<FH_Q4_0>(s, g);
+}
+
+bool gemm_score_supported(fh_path path, size_t rows, size_t k, size_t n) {
+    if (path == FH_PATH_TILED_FAST) return stream_fast_supported(rows, k, n) && gemm_supported(rows, k, n);
+    if (path == FH_PATH_TILED) return stream_supported(rows, k, n);
+    return false;
+}
+
+hipError_t launch_gemm_score(hipStream_t s, fh_path path, fh_kind kind, const uint8_t *qs, const uint16_t *ds,
+                             const uint8_t *b8, const float *x, size_t rows, size_t k, size_t n, void *workspace,
+                             const ScoreOut &so) {
+    if (!gemm_score_supported(path, rows, k, n)) return hipErrorInvalidValue;
+    const uint32_t M = (uint32_t)rows, K = (uint32_t)k, N = (uint32_t)n;
+    if (path == FH_PATH_TILED_FAST) {
+        const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+        uint8_t *ws = (uint8_t *)workspace;
+        _Float16 *xh = (_Float16 *)ws;
+        uint8_t *xl = ws + up(rows * k * 2);
+        int32_t *xsc = (int32_t *)(ws + up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)));
+        const int32_t *bsc = (const int32_t *)(b8 + up(n * ((k + 63) / 64 * 64)));
+        if (kind == FH_Q8_0) {
+            split_x_kernel<FH_Q8_0><<<M, 256, 0, s>>>(x, xh, xl, xsc, K);
+            return run_gemm_score<FH_Q8_0>(s, path, xh, xl, xsc, qs, ds, b8, bsc, M, K, N, so);
+        }
+        split_x_kernel<FH_Q4_0><<<M, 256, 0, s>>>(x, xh, xl, xsc, K);
+        return run_gemm_score<FH_Q4_0>(s, path, xh, xl, xsc, qs, ds, b8, bsc, M, K, N, so);
+    }
+    _Float16 *xs = (_Float16 *)workspace;
+    const size_t items = rows * (k / 32);
+    const unsigned g = (unsigned)(items / 32 + 1 < 65535 ? items / 32 + 1 : 65535);
+    if (kind == FH_Q8_0) {
+        split_x_precise_kernel<FH_Q8_0><<<g, 256, 0, s>>>(x, xs, items);
+        return run_gemm_score<FH_Q8_0>(s, path, xs, nullptr, nullptr, qs, ds, nullptr, nullptr, M, K, N, so);
+    }
+    split_x_precise_kernel<FH_Q4_0><<<g, 256, 0, s>>>(x, xs, items);
+    return run_gemm_score<FH_Q4_0>(s, path, xs, nullptr, nullptr, qs, ds, nullptr, nullptr, M, K, N, so);
 }
 
 }  // namespace fh

@@ -288,4 +288,20 @@ hipError_t launch_gemm_precise(hipStream_t s, fh_kind kind, const uint8_t *qs, c
                                float *y, size_t rows, size_t k, size_t n, void *workspace,
                                SplitOut *defer = nullptr);
 
+// The scoring head's product with the score folded into its epilogue: no logits are written;
+// per row and 256-column tile the tile's softmax statistics (maximum, sum of exp(v - maximum),
+// first column holding the maximum), and the target column's logit from the tile holding it.
+struct ScoreOut {
+    const int32_t *tgt;  // the target column of every row, rows padded to a multiple of 256
+    float *part;         // [rows][ntn][4]: maximum, sum, first column (as bits), 0
+    float *tlogit;       // [rows]
+    uint32_t ntn;        // column tiles: ceil(n / 256)
+};
+// Whether the score epilogue takes this product (the streaming 256 x 256 kernels' limits); path
+// FH_PATH_TILED_FAST or FH_PATH_TILED. b8: the fast path's correction operand.
+bool gemm_score_supported(fh_path path, size_t rows, size_t k, size_t n);
+hipError_t launch_gemm_score(hipStream_t s, fh_path path, fh_kind kind, const uint8_t *qs, const uint16_t *ds,
+                             const uint8_t *b8, const float *x, size_t rows, size_t k, size_t n, void *workspace,
+                             const ScoreOut &so);
+
 }  // namespace fh

@@ -43,6 +43,9 @@ struct fh_llama {
     float rope_base = 10000.0f, eps = 1e-5f, linear_factor = 1.0f;
     bool neox = false, tied = false;
     bool fuse_rope = true;  // qkv_rope_split_kernel where it fits (FERRUM_HIP_ROPE_UNFUSED=1 at load: never)
+    // the score in the head GEMM's epilogue (launch_gemm_score) on the TILED and TILED_FAST paths
+    // where it takes the shape (FERRUM_HIP_SCORE_UNFUSED=1 at load: the logits and score_kernel)
+    bool fuse_score = true;
     fh_kind kind = (fh_kind)0;
     fh_path path = FH_PATH_TILED;
     // A weight matrix of k inputs and n outputs: packed (q), or the f32 rows (f: n rows of k
@@ -78,6 +81,7 @@ struct fh_llama {
     float *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr, *o = nullptr, *gu = nullptr, *act = nullptr,
           *logits = nullptr, *scores = nullptr;
     int32_t *ids = nullptr;
+    float *sfold = nullptr;  // the score epilogue's per-tile statistics, target logits and padded targets
     void *ws = nullptr;
     // fast path: the GEMMs' K-split partial products, after the widest split x in ws (the fused
     // RMSNorm reads one product's deferred partial sums while it writes the next product's split
@@ -991,6 +995,49 @@ __global__ __launch_bounds__(256) void score_kernel(const float *__restrict__ lo
     out[2 * (size_t)blockIdx.x + 1] = ok && F == (uint32_t)t ? 1.0f : 0.0f;
 }
 
+// score_kernel's result from the head GEMM's per-tile statistics (ScoreOut: for every row and
+// 256-column tile the maximum, the sum of exp(v - maximum) and the first column holding the
+// maximum, and the target's logit): one wavefront per row merges the row's tiles (lane l tiles l,
+// l + 64, ... in order, then the lanes pairwise; the smaller column wins a tie, as a left-to-right
+// scan would have it), out[2r] = logit[t] - max - ln(sum), out[2r + 1] = (first == t); a target
+// outside the vocabulary gives NaN.
+__device__ __forceinline__ void score_combine(float &m, float &s, uint32_t &f, float m2, float s2, uint32_t f2) {
+    const float mx = fmaxf(m, m2);
+    s = (m == -INFINITY ? 0.0f : s * __expf(m - mx)) + (m2 == -INFINITY ? 0.0f : s2 * __expf(m2 - mx));
+    f = m2 > m || (m2 == m && f2 < f) ? f2 : f;
+    m = mx;
+}
+
+__global__ __launch_bounds__(256) void score_merge_kernel(const float *__restrict__ part, const float *__restrict__ tlogit,
+                                                          const int32_t *__restrict__ targets, float *__restrict__ out,
+                                                          uint32_t rows, uint32_t ntn, uint32_t vocab) {
+    const uint32_t row = blockIdx.x * 4 + threadIdx.x / 64, lane = threadIdx.x % 64;
+    if (row >= rows) return;  // (whole wavefronts)
+    float m = -INFINITY, s = 0.0f;
+    uint32_t f = 0xffffffffu;
+    for (uint32_t c = lane; c < ntn; c += 64) {
+        const f32x4 p = *(const f32x4 *)(part + ((size_t)row * ntn + c) * 4);
+        score_combine(m, s, f, p.x, p.y, __float_as_uint(p.z));
+    }
+    for (int o = 32; o; o >>= 1) {
+        const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+        const uint32_t f2 = (uint32_t)__shfl_xor((int)f, o);
+        score_combine(m, s, f, m2, s2, f2);
+    }
+    if (lane) return;
+    const int32_t t = targets[row];
+    const bool ok = t >= 0 && (uint32_t)t < vocab;
+    out[2 * (size_t)row] = ok ? tlogit[row] - m - logf(s) : NAN;
+    out[2 * (size_t)row + 1] = ok && f == (uint32_t)t ? 1.0f : 0.0f;
+}
+
+// The score epilogue's targets: rows 0..rows-1 from ids, then -1 up to `padded` (a multiple of 256).
+__global__ __launch_bounds__(256) void pad_targets_kernel(const int32_t *__restrict__ ids, int32_t *__restrict__ tgt,
+                                                          uint32_t rows, uint32_t padded) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < padded) tgt[i] = i < rows ? ids[i] : -1;
+}
+
 // ---- host side ----
 
 fh_status llama_fail_free(fh_llama *m, fh_status st) {
@@ -1084,6 +1131,12 @@ size_t linear_ws(const fh_llama *m, size_t rows, size_t k, size_t n) {
                                         : gemm_precise_workspace_bytes(rows, k, n);
 }
 
+// The score epilogue's buffers for `rows` rows (enqueue_score): the per-tile statistics (four floats
+// per row and 256-column tile), the target logits, the targets padded to a multiple of 256 rows.
+size_t score_fold_bytes(size_t rows, size_t vocab) {
+    return up256(rows * ((vocab + 255) / 256) * 16) + up256(rows * 4) + up256((rows + 255) / 256 * 256 * 4);
+}
+
 // The activations for t rows (kept when already large enough).
 // Head dims whose attention runs on the split f16 operands (the f32-MFMA kernel takes the rest).
 bool split_attention(const fh_llama *m) { return m->head_dim == 32 || m->head_dim == 64 || m->head_dim == 128; }
@@ -1107,9 +1160,10 @@ fh_status ensure_rows(fh_llama *m, size_t t) {
     const size_t split = split_attention(m) ? 2 * up256(tp * qd * 2) + 4 * up256(tp * kvd * 2) + up256(tp * m->heads) +
                                                   2 * up256(tp * m->kv_heads)
                                             : 0;
+    const size_t sfold = score_fold_bytes(chunk, m->vocab);
     const size_t total = 3 * up256(t * d * 4) + up256(t * w * 4) + up256(t * qd * 4) + up256(t * 2 * hid * 4) +
                          up256(t * hid * 4) + up256(chunk * m->vocab * 4) + up256(2 * t * 4) + up256((t + 1) * 4) +
-                         up256(ws) + up256(part) + split;
+                         up256(ws) + up256(part) + split + up256(sfold);
     void *p = nullptr;
     fh_status st = alloc_bytes(m->dev, total, &p);
     if (st) return st;
@@ -1139,6 +1193,7 @@ fh_status ensure_rows(fh_llama *m, size_t t) {
     m->ids = (int32_t *)take((t + 1) * 4);
     m->ws = take(ws);
     m->part = part ? (float *)take(part) : nullptr;
+    m->sfold = (float *)take(sfold);
     if (split) {
         m->sqh = (_Float16 *)take(tp * qd * 2);
         m->sql = (_Float16 *)take(tp * qd * 2);
@@ -1324,12 +1379,34 @@ fh_status check_len(const fh_llama *m, size_t t) {
 
 // The score pass over t rows whose ids (t + 1 of them, the targets being ids[1..]) are in m->ids;
 // out receives 2 t floats on the device.
+// With the score in the head GEMM's epilogue (fuse_score), no logits are written: sfold holds the
+// per-tile statistics, the target logits and the padded targets.
 hipError_t enqueue_score(fh_llama *m, hipStream_t s, size_t t, float *out) {
     hipError_t e = enqueue_body(m, s, t);
+    const fh_qweight *w = m->head.q;
+    const size_t most = std::min(m->chunk, t), ntn = (m->vocab + 255) / 256;
+    const bool fold = m->fuse_score && w && (m->path == FH_PATH_TILED_FAST || m->path == FH_PATH_TILED) &&
+                      gemm_score_supported(m->path, most, w->k, w->n);
     for (size_t r0 = 0; r0 < t && !e; r0 += m->chunk) {
         const size_t rows = std::min(m->chunk, t - r0);
-        if ((e = linear(m, s, m->head, m->h + r0 * m->dim, m->logits, rows))) break;
-        score_kernel<<<(unsigned)rows, 256, 0, s>>>(m->logits, m->ids + 1 + r0, out + 2 * r0, (uint32_t)m->vocab);
+        if (fold) {
+            const uint32_t padded = (uint32_t)((rows + 255) / 256 * 256);
+            ScoreOut so;
+            so.part = m->sfold;  // (laid out as score_fold_bytes)
+            so.tlogit = (float *)((uint8_t *)so.part + up256(rows * ntn * 16));
+            int32_t *tgt = (int32_t *)((uint8_t *)so.tlogit + up256(rows * 4));
+            so.tgt = tgt;
+            so.ntn = (uint32_t)ntn;
+            pad_targets_kernel<<<padded / 256, 256, 0, s>>>(m->ids + 1 + r0, tgt, (uint32_t)rows, padded);
+            if ((e = launch_gemm_score(s, m->path, w->kind, w->qs, w->ds, w->b8, m->h + r0 * m->dim, rows, w->k, w->n,
+                                       m->ws, so)))
+                break;
+            score_merge_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(so.part, so.tlogit, tgt, out + 2 * r0,
+                                                                         (uint32_t)rows, (uint32_t)ntn, (uint32_t)m->vocab);
+        } else {
+            if ((e = linear(m, s, m->head, m->h + r0 * m->dim, m->logits, rows))) break;
+            score_kernel<<<(unsigned)rows, 256, 0, s>>>(m->logits, m->ids + 1 + r0, out + 2 * r0, (uint32_t)m->vocab);
+        }
         e = hipGetLastError();
     }
     return e;
@@ -1404,6 +1481,8 @@ fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_
     m->neox = arch == "qwen2";  // ferrum_model/src/gguf/llama/mod.rs:108-117
     const char *unfused = getenv("FERRUM_HIP_ROPE_UNFUSED");
     m->fuse_rope = !(unfused && unfused[0] == '1');
+    const char *su = getenv("FERRUM_HIP_SCORE_UNFUSED");
+    m->fuse_score = !(su && su[0] == '1');
     auto key = [&](const char *k) { return arch + "." + k; };
     auto has = [&](const std::string &k) {
         size_t i;

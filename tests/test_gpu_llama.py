@@ -198,6 +198,43 @@ def test_fast_paths_stay_within_their_bounds(fh, g, orc, name, c, biases, tied, 
     assert e < (FAST_LOGPROB if path == "TiledFast" else F16_LOGPROB)
 
 
+@pytest.mark.parametrize("path", ["Tiled", "TiledFast"])
+def test_score_epilogue_matches_the_logits_and_score_kernel(fh, g, orc, path):
+    """The score folded into the head GEMM's epilogue (per row and 256-column tile the maximum, the
+    sum of exponentials, the first maximum's column and the target's logit, merged per row) against
+    the same model with FERRUM_HIP_SCORE_UNFUSED=1 (the logits written, then score_kernel): the same
+    logits, summed in another order, so log-probabilities within 1e-6 and identical first-argmax
+    flags; and both against the oracle. Vocab 1000 is four column tiles, the last 232 wide; 299
+    scored rows are two row tiles, the second partly filled; targets include every tile's first and
+    last column."""
+    c = cfg(vocab=1000, ctx=300, dim=64, heads=4, kv_heads=2, head_dim=16, hidden=128, rope_dim=16)
+    data = lm.to_gguf(lm.llama_random(c, 13, True, False), lm.Q8_0)
+    ref = lm.from_gguf(data)
+    fused = load(fh, g, data, fh.QPath[path])
+    old = os.environ.get("FERRUM_HIP_SCORE_UNFUSED")
+    os.environ["FERRUM_HIP_SCORE_UNFUSED"] = "1"
+    try:
+        plain = load(fh, g, data, fh.QPath[path])
+    finally:
+        if old is None:
+            os.environ.pop("FERRUM_HIP_SCORE_UNFUSED")
+        else:
+            os.environ["FERRUM_HIP_SCORE_UNFUSED"] = old
+    ids = [int(t) for t in np.random.default_rng(5).integers(0, 1000, 300)]
+    ids[1:9] = [0, 255, 256, 511, 512, 767, 768, 999]
+    lp, hit = fused.score_arrays(ids)
+    lp0, hit0 = plain.score_arrays(ids)
+    assert lp.shape == (299,) and np.all(np.isfinite(lp))
+    assert np.array_equal(hit, hit0)
+    e = lp_err(lp, lp0)
+    wlp, whit = orc.llama_score(ref, ids)
+    say(f"{path}: fused vs unfused log-prob rel err {e:.2e}; vs oracle {lp_err(lp, wlp):.2e}; hits {int(hit.sum())}")
+    assert e < 1e-6
+    assert lp_err(lp, wlp) < (SCORE if path == "Tiled" else FAST_LOGPROB)
+    if path == "Tiled":
+        assert np.array_equal(hit, whit)
+
+
 @pytest.fixture(scope="module")
 def qwen(fh, g):
     """The scoring benchmark's model: Qwen2-0.5B shapes (24 layers, d 896, FFN 4864, 14 q / 2 kv
