@@ -867,8 +867,12 @@ struct OneArgs {
     int32_t *state;
     float *x_final;
     const float *lnf_g, *lnf_b;
-    uint8_t *prep;   // the final LayerNorm's prepared records (the head's x)
-    uint32_t *sync;  // completion counters, [n_layers][slots] (one_slot), then the error flag
+    const uint8_t *head_qs;  // the head (tied: the token embedding), vocab rows of d
+    const uint16_t *head_ds;
+    uint32_t vocab;
+    float *logits;
+    uint64_t *offers;  // per head row group: its first maximum (value bits, row << 32)
+    uint32_t *sync;  // completion counters, [n_layers][slots] (one_counter), then the error flag, the head ticket
     uint32_t d, hidden, heads, S, chunk_down;
     float eps, scale;
     uint32_t nA, nB, nC, nD;
@@ -1185,28 +1189,149 @@ __device__ __forceinline__ void one_down(const OneArgs *A, uint32_t l, uint32_t 
     one_signal(A->sync + one_counter(l, A->heads + 1 + A->S, A->slots));
 }
 
+// The head, folded into the step (decode_gemv_kernel<PRO_GLOBAL, EPI_ARGMAX> and pick_kernel):
+// every workgroup with head row groups forms x = x_m + (the down partial rows + b_2) and its final
+// LayerNorm into its own LDS records (workgroup 0 also stores x), then takes row groups w, w + G,
+// ... (the next group's first batch requested while the current one is reduced): the logits go to
+// A->logits and each group's offer (its first maximum; NaN never wins) to A->offer_v / offer_i with
+// agent-coherent stores. A ticket counts the finished workgroups; the last one picks the next
+// token over the offers as pick_kernel does and advances the state (position, input, epoch).
 template <int KIND>
-__device__ __forceinline__ void one_final(const OneArgs *A, uint32_t e1, uint8_t *lds) {
-    // x = x_m + (sum of the down partial rows + b_2), its final LayerNorm into global records
-    const uint32_t nb = A->d / 32, L = A->n_layers;
-    one_wait(A->sync + one_counter(L - 1, A->heads + 1 + A->S, A->slots), e1 * A->nD,
-             A->sync + one_counter(L, 0, A->slots));
-    StepArgs z{};
-    z.x_in = A->layers[L - 1].xm;
-    z.part = A->layers[L - 1].pf;
-    z.pbias = A->layers[L - 1].b2;
-    z.nparts = A->S;
-    z.state = A->state;
-    z.x_out = A->x_final;
-    z.d = A->d;
-    z.nb = nb;
-    f32x4 v[kLnSlots];
-    residual_row<KIND>(z, v);
-    ln_records<KIND, true>(v, A->lnf_g, A->lnf_b, A->eps, nb, (nb + 7) / 8 * 8, A->prep, (float *)lds);
+__device__ __forceinline__ void one_head(const OneArgs *A, uint32_t e1, uint8_t *lds, uint32_t w, uint32_t G) {
+    const uint32_t d = A->d, nb = d / 32, nb8 = (nb + 7) / 8, span = nb8 * 8, L = A->n_layers;
+    const uint32_t groups = (A->vocab + 31) / 32;
+    uint32_t *err = A->sync + one_counter(L, 0, A->slots);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int lane = threadIdx.x % 64, r = lane % 32;
+    const bool upper = lane >= 32;
+    DecodeGemv g{};
+    g.qs = A->head_qs;
+    g.ds = A->head_ds;
+    g.nb = nb;
+    g.n = A->vocab;
+    g.chunk = span;
+    g.state = A->state;
+    OneGemv<KIND> t;
+    if (w < groups) one_issue<KIND>(g, w, 0, t);
+    one_wait(A->sync + one_counter(L - 1, A->heads + 1 + A->S, A->slots), e1 * A->nD, err);
+    uint8_t *prep = lds;
+    float *part = (float *)(lds + span * kPrepBytes);
+    float *red = part + kStepWaves * 32;
+    if (w < groups) {
+        StepArgs z{};
+        z.x_in = A->layers[L - 1].xm;
+        z.part = A->layers[L - 1].pf;
+        z.pbias = A->layers[L - 1].b2;
+        z.nparts = A->S;
+        z.state = A->state;
+        z.x_out = A->x_final;  // (workgroup 0 stores it)
+        z.d = d;
+        z.nb = nb;
+        f32x4 v[kLnSlots];
+        residual_row<KIND>(z, v);
+        ln_records<KIND, false>(v, A->lnf_g, A->lnf_b, A->eps, nb, span, prep, red);
+        __syncthreads();
+        constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
+        const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16);
+        const uint32_t os = (uint32_t)(r * 16), oa = prep_a_offset(lane), ot = prep_tail_offset<KIND>(lane);
+        lds_byte *lp = (lds_byte *)prep;
+        for (uint32_t rg = w; rg < groups; rg += G) {
+            const auto rq = make_rsrc(g.qs + (size_t)rg * nb * 32 * QB, nb * 32 * QB);
+            const auto rd = make_rsrc(g.ds + (size_t)rg * nb8 * 256, nb8 * 512);
+            float acc = 0.0f;
+            Batch<KIND> nx;
+            for (uint32_t bb = wave * kBatch; bb < span; bb += kStepWaves * kBatch) {
+                const uint32_t nxt = bb + kStepWaves * kBatch;
+                if (nxt < span) load_weights<KIND>(nx, rq, rd, oq, os, nxt);
+                t.cur.a = *(const __attribute__((address_space(3))) i32x4 *)(lp + bb * kPrepBytes + oa);
+                load_tails<KIND>(t.cur, bb * kPrepBytes, ot,
+                                 [&](uint32_t off) { return *(const __attribute__((address_space(3))) u32x4 *)(lp + off); },
+                                 [&](uint32_t off) { return *(const __attribute__((address_space(3))) uint32_t *)(lp + off); });
+                compute_batch<KIND>(t.cur, upper, acc);
+                t.cur = nx;
+            }
+            if (rg + G < groups) one_issue<KIND>(g, rg + G, 0, t);  // the next group's first batch
+            const float sum = half_sum(acc, upper);
+            if (!upper) part[wave * 32 + r] = sum;
+            __syncthreads();
+            if (wave == 0 && !upper) {
+                float s = 0.0f;
+                for (uint32_t k = 0; k < kStepWaves; k++) s += part[k * 32 + r];
+                const uint32_t row = rg * 32 + r;
+                if (row < A->vocab) A->logits[row] = s;
+                float bv = s;
+                uint32_t bi = (row < A->vocab && s == s) ? row : kNone;
+#pragma unroll
+                for (int o = 16; o >= 1; o /= 2) {
+                    const float ov = __shfl_xor(bv, o, 32);
+                    const uint32_t oi = __shfl_xor(bi, o, 32);
+                    if (better(ov, oi, bv, bi)) {
+                        bv = ov;
+                        bi = oi;
+                    }
+                }
+                if (r == 0) {
+                    __hip_atomic_store((g_u64 *)(A->offers + rg), (uint64_t)bi << 32 | __float_as_uint(bv),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+            __syncthreads();  // (part is rewritten by the next group)
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this workgroup's offers have landed
+    __syncthreads();
+    uint32_t *flag = (uint32_t *)red;
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(A->sync + one_counter(L, 1, A->slots), 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        flag[0] = old + 1 == e1 * G ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!flag[0]) return;
+    // the last workgroup: pick_kernel over the offers (written in this launch: agent-coherent loads)
+    float bv = 0.0f;
+    uint32_t bi = kNone;
+    for (uint32_t q = threadIdx.x; q < groups; q += blockDim.x) {
+        const uint64_t o = __hip_atomic_load((g_u64 *)(A->offers + q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float ov = __uint_as_float((uint32_t)o);
+        const uint32_t oi = (uint32_t)(o >> 32);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o /= 2) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const uint32_t oi = __shfl_xor(bi, o, 64);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    float *sv = part;
+    uint32_t *si = (uint32_t *)(part + kStepWaves);
+    if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (uint32_t k = 1; k < kStepWaves; k++)
+        if (better(sv[k], si[k], bv, bi)) {
+            bv = sv[k];
+            bi = si[k];
+        }
+    const int32_t pick = bi == kNone ? 0 : (int32_t)bi;
+    int32_t *state = A->state;
+    const int32_t p = state[0];
+    state[2] = pick;
+    if (p + 1 >= state[1]) A->inputs[p + 1] = pick;
+    state[0] = p + 1;
+    state[3] = state[3] + 1;  // the step's epoch
 }
 
-// The whole layer stack of one decode step, then the final LayerNorm into the head's records
-// (workgroup 0). The first max(nA, nC) workgroups take QKV task w and FFN-up task w, the next
+// One decode step: the whole layer stack, then the head and the greedy pick (one_head). The first max(nA, nC) workgroups take QKV task w and FFN-up task w, the next
 // max(nB, nD) attention head t and FFN-down task t: each pair of roles is one phase apart in both
 // directions (QKV, then attention, FFN-up, FFN-down, the next layer's QKV), so a workgroup's next
 // weights are requested a phase before they are needed. A workgroup runs its tasks in the phases'
@@ -1229,7 +1354,7 @@ __global__ __launch_bounds__(kStepThreads) void one_step_kernel(const OneArgs *_
             if (t < nD) one_down<KIND>(A, l, t, e1, olds);
         }
     }
-    if (w == 0) one_final<KIND>(A, e1, olds);
+    one_head<KIND>(A, e1, olds, w, gridDim.x);
 }
 
 // LDS of one_step_kernel: the largest of its roles'.
@@ -1590,8 +1715,7 @@ const void *one_kernel(uint32_t hd) {
                                 : (const void *)one_step_kernel<KIND, 64, attn_k2<64>()>;
 }
 
-// Enqueue one one-launch step: every layer and the final LayerNorm in one_step_kernel, then the head
-// product and the pick.
+// Enqueue one one-launch step: every layer, the head and the pick in one_step_kernel.
 hipError_t enqueue_one(fh_gpt2 *m, hipStream_t s) {
     const uint32_t hd = (uint32_t)(m->dim / m->heads);
     const uint32_t grid = std::max(m->one_tasks[0], m->one_tasks[2]) + std::max(m->one_tasks[1], m->one_tasks[3]);
@@ -1599,13 +1723,7 @@ hipError_t enqueue_one(fh_gpt2 *m, hipStream_t s) {
     void *kargs[] = {&args};
     hipError_t e = hipLaunchKernel(m->kind == FH_Q8_0 ? one_kernel<FH_Q8_0>(hd) : one_kernel<FH_Q4_0>(hd), dim3(grid),
                                    dim3(kStepThreads), kargs, m->one_lds_bytes, s);
-    if (e) return e;
-    DecodeGemv h = dg(m, m->head, m->x, m->logits);
-    h.prep = m->prep;
-    h.pick = m->pick;
-    if ((e = dgemv<PRO_GLOBAL, EPI_ARGMAX>(s, m->kind, h))) return e;
-    pick_kernel<<<1, 1024, 0, s>>>(m->partial, m->pick, (uint32_t)((m->vocab + 31) / 32), m->state, m->inputs);
-    return hipGetLastError();
+    return e;
 }
 
 // Sets up the one-launch step where it fits: head widths 64, 128, 256, and all of its workgroups
@@ -1628,7 +1746,7 @@ bool one_setup(fh_gpt2 *m) {
     if ((uint64_t)per * (uint64_t)cus < grid) return false;
     auto up = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
     const uint32_t slots = (uint32_t)m->heads + sp + 2;
-    const size_t table = m->layers * sizeof(OneLayer), sync = (size_t)one_counter((uint32_t)m->layers, 1, slots) * 4;
+    const size_t table = m->layers * sizeof(OneLayer), sync = (size_t)one_counter((uint32_t)m->layers, 2, slots) * 4;
     const size_t per_layer = 3 * up(d * 4) + up(m->heads * d * 4) + up((size_t)sp * d * 4) + up(m->hidden * 4);
     const size_t bufs0 = up(table) + up(sync) + up(sizeof(OneArgs));
     if (alloc_bytes(m->dev, bufs0 + m->layers * per_layer, &m->one_mem)) return false;
@@ -1655,7 +1773,11 @@ bool one_setup(fh_gpt2 *m) {
     a.x_final = m->x;
     a.lnf_g = fp(m->lnf_g);
     a.lnf_b = fp(m->lnf_b);
-    a.prep = m->prep;
+    a.head_qs = m->head->qs;
+    a.head_ds = m->head->ds;
+    a.vocab = (uint32_t)m->vocab;
+    a.logits = m->logits;
+    a.offers = (uint64_t *)m->partial;
     a.sync = m->sync;
     a.d = (uint32_t)d;
     a.hidden = (uint32_t)m->hidden;
@@ -1697,7 +1819,7 @@ fh_status one_check(fh_gpt2 *m) {
     if (!e) e = hipStreamSynchronize(st);
     if (e) return hip_fail(m->dev, e, "gpt2 step");
     if (!flag) return FH_OK;
-    (void)hipMemsetAsync(m->sync, 0, (size_t)one_counter((uint32_t)m->layers, 1, slots) * 4, st);
+    (void)hipMemsetAsync(m->sync, 0, (size_t)one_counter((uint32_t)m->layers, 2, slots) * 4, st);
     (void)hipMemsetAsync(m->state + 3, 0, 4, st);
     (void)hipStreamSynchronize(st);
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
@@ -1849,7 +1971,7 @@ fh_status fh_gpt2_from_gguf(fh_device *dev, const fh_gguf *g, fh_gpt2 **out) {
     // split-K scratch: the split products (attention output, FFN down) have d outputs and d or h
     // inputs; the head needs one value per row group
     const size_t groups_v = (m->vocab + 31) / 32, groups_d = d / 32;
-    size_t part_floats = groups_v;
+    size_t part_floats = 2 * groups_v;  // (the one-launch step keeps a 64-bit offer per row group here)
     for (size_t k : {d, h}) {
         uint32_t sp, c8;
         plan_splits((uint32_t)groups_d, (uint32_t)((k / 32 + 7) / 8), &sp, &c8);
@@ -1935,7 +2057,7 @@ size_t fh_gpt2_pos(const fh_gpt2 *m) { return m ? m->pos : 0; }
 uint64_t fh_gpt2_step_bytes(const fh_gpt2 *m) { return m ? m->step_bytes : 0; }
 size_t fh_gpt2_step_launches(const fh_gpt2 *m) {
     if (!m) return 0;
-    return m->form == 1 ? 3 : m->form == 4 ? 4 * m->layers + 3 : 5 * m->layers + 4;
+    return m->form == 1 ? 1 : m->form == 4 ? 4 * m->layers + 3 : 5 * m->layers + 4;
 }
 void fh_gpt2_reset(fh_gpt2 *m) {
     if (m) m->pos = 0;  // later positions overwrite the cache rows they read

@@ -1,5 +1,6 @@
-"""The one-launch GPT-2 decode step (every layer in one launch; phase counters between its
-workgroups) against the four-launch step (one launch per layer phase) on the same model.
+"""The one-launch GPT-2 decode step (every layer, the head and the greedy pick in one launch; phase
+counters between its workgroups) against the four-launch step (one launch per layer phase, then
+the head and the pick) on the same model.
 
 Both run the same lane-level arithmetic in the same order (the same workgroup tasks, wavefront
 batches, LayerNorm sums and partial-row sums), so every logit must be bit-identical and greedy
@@ -77,7 +78,7 @@ def test_one_launch_step_is_bit_identical_to_the_four_launch_step(fh, g, name):
     cfg = MID if name == "mid" else GPT2_SMALL
     data = model_bytes(fh, g, cfg, 3)
     one, four = load(g, data), load(g, data, form=4)
-    assert one.step_launches() == 3, one.step_launches()
+    assert one.step_launches() == 1, one.step_launches()
     assert four.step_launches() == 4 * cfg["layers"] + 3
     prompt = [int(t) for t in np.random.default_rng(11).integers(0, cfg["vocab"], 24)]
     say(f"{name}: feeding {len(prompt)} tokens to both steps")
@@ -104,7 +105,7 @@ def test_two_one_launch_models_alive_at_once(fh, g):
     d1, d2 = model_bytes(fh, g, MID, 5), model_bytes(fh, g, MID, 6)
     m1, m2 = load(g, d1), load(g, d2)
     r1, r2 = load(g, d1, form=4), load(g, d2, form=4)
-    assert m1.step_launches() == 3 and m2.step_launches() == 3
+    assert m1.step_launches() == 1 and m2.step_launches() == 1
     prompt = [int(t) for t in np.random.default_rng(12).integers(0, MID["vocab"], 10)]
     for t in prompt:
         a1, a2 = m1.feed(t), m2.feed(t)
