@@ -5,7 +5,10 @@ each launch adds the partial rows it consumes in a fixed order) against the CPU 
 (ferrum_ref's Gpt2::feed, ferrum_ref/src/models/gpt2/decode.rs:57-117): logits within FORWARD
 (1e-5, ferrum_wgpu/src/tolerance.rs) at every position of the context, greedy token IDs
 identical, and agreement with the five-launch step of the same model. The shapes cover every
-attention variant (head widths 64, 128 and 256), FFN widths split 1 to 6 ways, Q8_0 and Q4_0."""
+attention variant (head widths 64, 128 and 256), FFN widths split 1 to 6 ways, Q8_0 and Q4_0.
+Form 1 is the one-launch step (the four-launch step's phases in one launch, with the head and the
+pick): on every shape whose workgroups all fit on the chip at once (hd64: 64 workgroups, hd128:
+40), the same tests; hd256 needs 440 and keeps the four-launch step."""
 import os
 
 import numpy as np
@@ -41,7 +44,8 @@ def g():
 
 
 def load(g, data: bytes, form: int):
-    """The model with the decode step of `form` launches per layer (5 or 4)."""
+    """The model with the decode step of `form` launches per layer (5 or 4; 1: the one-launch step
+    where it fits)."""
     from ferrum_hip.gguf import Gguf
     from ferrum_hip.gpt2 import GpuGpt2
 
@@ -53,6 +57,8 @@ def load(g, data: bytes, form: int):
 
 
 def launches(cfg: dict, form: int) -> int:
+    if form == 1:  # the one-launch step where its workgroups fit: not hd256's 440 (FFN width 8448)
+        return 1 if cfg["hidden"] < 8448 else 4 * cfg["layers"] + 3
     return {5: 5 * cfg["layers"] + 4, 4: 4 * cfg["layers"] + 3}[form]
 
 
@@ -60,7 +66,7 @@ def rel(got, want) -> float:
     return float(np.abs(got - want).max() / max(np.abs(want).max(), 1.0))
 
 
-@pytest.mark.parametrize("form", [4])
+@pytest.mark.parametrize("form", [4, 1])
 @pytest.mark.parametrize("kind", [gm.Q8_0, gm.Q4_0])
 @pytest.mark.parametrize("name", list(CFGS))
 def test_four_launch_step_feeds_the_whole_context_like_the_oracle(g, orc, name, kind, form):
@@ -98,7 +104,7 @@ def test_four_launch_step_feeds_the_whole_context_like_the_oracle(g, orc, name, 
     five.free()
 
 
-@pytest.mark.parametrize("form", [4])
+@pytest.mark.parametrize("form", [4, 1])
 def test_four_launch_greedy_generation_matches_the_oracle(g, orc, form):
     cfg = dict(CFGS["hd64"], ctx=128)
     m = gm.gpt2_init(cfg, 6)
@@ -112,7 +118,7 @@ def test_four_launch_greedy_generation_matches_the_oracle(g, orc, form):
     dev.free()
 
 
-@pytest.mark.parametrize("form", [4])
+@pytest.mark.parametrize("form", [4, 1])
 @pytest.mark.parametrize("kind", [gm.Q8_0, gm.Q4_0])
 def test_four_launch_step_on_raw_random_weights_is_no_further_from_the_oracle(g, orc, kind, form):
     """Gpt2::random's raw weights (uniform +-0.5) amplify every rounding along the context, so the
