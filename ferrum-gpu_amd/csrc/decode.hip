@@ -1835,12 +1835,15 @@ hipError_t enqueue_any(fh_gpt2 *m, hipStream_t s) {
     return m->form == 1 ? enqueue_one(m, s) : m->form == 4 ? enqueue_four(m, s) : enqueue_step(m, s);
 }
 
-// Run one step on the device stream: the captured graph (made on first use), or the launches.
+// Run one step on the device stream: the captured graph (made on first use), or the launches. The
+// one-launch step is launched directly: replaying a one-node graph measured 6 us slower per step
+// (233 against 227 us at GPT-2-small).
 fh_status run_step(fh_gpt2 *m) {
     fh_device *dev = m->dev;
     fh_status st = begin_command(dev, "gpt2 step");
     if (st) return st;
-    if (m->use_graph && !m->exec) {
+    const bool graph = m->use_graph && m->form != 1;
+    if (graph && !m->exec) {
         hipError_t e = hipStreamBeginCapture(dev->stream, hipStreamCaptureModeThreadLocal);
         if (e) return hip_fail(dev, e, "gpt2 step capture");
         const hipError_t le = enqueue_any(m, dev->stream);
@@ -1853,7 +1856,7 @@ fh_status run_step(fh_gpt2 *m) {
             return hip_fail(dev, e, "gpt2 step graph");
         }
     }
-    hipError_t e = m->use_graph ? hipGraphLaunch(m->exec, dev->stream) : enqueue_any(m, dev->stream);
+    hipError_t e = graph ? hipGraphLaunch(m->exec, dev->stream) : enqueue_any(m, dev->stream);
     if (e) return hip_fail(dev, e, "gpt2 step");
     return end_command(dev, "gpt2 step");
 }
