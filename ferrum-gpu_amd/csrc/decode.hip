@@ -44,6 +44,7 @@ enum { PRO_NONE = 0, PRO_LN = 1, PRO_GLOBAL = 2, PRO_LNR = 3 };  // PRO_LNR: Lay
 enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_GELU = 2, EPI_QKV = 3, EPI_ARGMAX = 4, EPI_PARTIAL = 5 };
 
 constexpr int kMaxWaves = 8;           // wavefronts per decode-GEMV workgroup (two per SIMD)
+constexpr int kLnRed = 2 * kMaxWaves;  // reduction slots (floats) a LayerNorm prologue uses
 constexpr uint32_t kMaxBlocks = 512;   // blocks per row (k <= 16384): 80 KiB of prepared x in LDS
 constexpr uint32_t kLnSlots = 2;       // LayerNorm prologue: (block, lane) slots a thread keeps in registers
 constexpr uint32_t kNone = 0xffffffffu;
@@ -133,27 +134,49 @@ __device__ __forceinline__ bool better(float v2, uint32_t i2, float v1, uint32_t
     return i2 != kNone && (i1 == kNone || v2 > v1 || (v2 == v1 && i2 < i1));
 }
 
-// LayerNorm (ferrum_ref/src/kernels/nn.rs:31-44) of the k = 32 nb values that the workgroup
-// holds in registers (thread slot u: block sl / 8, elements 4 sl .. 4 sl + 3 with
-// sl = threadIdx.x + u blockDim.x; slots past nb hold nothing), written as the prepared records
-// of `span` blocks (zero records past nb) at out (LDS, or global when GLOBAL). span * 8 <=
-// kLnSlots * blockDim.x.
-template <int KIND, bool GLOBAL>
-__device__ __forceinline__ void ln_records(const f32x4 (&v)[kLnSlots], const float *lg, const float *lb, float eps,
-                                           uint32_t nb, uint32_t span, uint8_t *out, float *red) {
-    const uint32_t k = nb * 32;
-    f32x4 gg[kLnSlots], bb[kLnSlots];
-    float s = 0.0f;
+// As block_sum with one barrier: no wavefront may still be reading red from an earlier reduction.
+__device__ __forceinline__ float block_sum_once(float v, float *red) {
+    v = wave_reduce(v, AddOp());
+    const uint32_t nw = blockDim.x / 64;
+    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (uint32_t i = 0; i < nw; i++) t += red[i];
+    return t;
+}
+
+struct LnParams {  // a LayerNorm's gain and bias in the thread's slots (see ln_records_p)
+    f32x4 g[kLnSlots], b[kLnSlots];
+};
+
+__device__ __forceinline__ void load_ln(const float *lg, const float *lb, uint32_t nb, LnParams &p) {
 #pragma unroll
     for (uint32_t u = 0; u < kLnSlots; u++) {
         const uint32_t sl = threadIdx.x + u * blockDim.x;
         if (sl / 8 < nb) {
-            gg[u] = gload4(lg + sl * 4);
-            bb[u] = gload4(lb + sl * 4);
-            s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+            p.g[u] = gload4(lg + sl * 4);
+            p.b[u] = gload4(lb + sl * 4);
         }
     }
-    const float mean = block_sum(s, red) / (float)k;
+}
+
+// LayerNorm (ferrum_ref/src/kernels/nn.rs:31-44) of the k = 32 nb values that the workgroup
+// holds in registers (thread slot u: block sl / 8, elements 4 sl .. 4 sl + 3 with
+// sl = threadIdx.x + u blockDim.x; slots past nb hold nothing), with gain and bias pa (load_ln),
+// written as the prepared records of `span` blocks (zero records past nb) at out (LDS, or global
+// when GLOBAL). span * 8 <= kLnSlots * blockDim.x. red: kLnRed floats, not read by an earlier
+// reduction that a wavefront may still be in (the two reductions use halves of it).
+template <int KIND, bool GLOBAL>
+__device__ __forceinline__ void ln_records_p(const f32x4 (&v)[kLnSlots], const LnParams &pa, float eps, uint32_t nb,
+                                             uint32_t span, uint8_t *out, float *red) {
+    const uint32_t k = nb * 32;
+    float s = 0.0f;
+#pragma unroll
+    for (uint32_t u = 0; u < kLnSlots; u++) {
+        const uint32_t sl = threadIdx.x + u * blockDim.x;
+        if (sl / 8 < nb) s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+    }
+    const float mean = block_sum_once(s, red) / (float)k;
     float q = 0.0f;
 #pragma unroll
     for (uint32_t u = 0; u < kLnSlots; u++) {
@@ -165,7 +188,7 @@ __device__ __forceinline__ void ln_records(const f32x4 (&v)[kLnSlots], const flo
             }
         }
     }
-    const float rstd = 1.0f / sqrtf(block_sum(q, red) / (float)k + eps);
+    const float rstd = 1.0f / sqrtf(block_sum_once(q, red + kMaxWaves) / (float)k + eps);
 #pragma unroll
     for (uint32_t u = 0; u < kLnSlots; u++) {
         const uint32_t sl = threadIdx.x + u * blockDim.x, blk = sl / 8;
@@ -175,7 +198,7 @@ __device__ __forceinline__ void ln_records(const f32x4 (&v)[kLnSlots], const flo
         if (blk < nb) {
             f32x4 h;
 #pragma unroll
-            for (int c = 0; c < 4; c++) h[c] = (v[u][c] - mean) * rstd * gg[u][c] + bb[u][c];
+            for (int c = 0; c < 4; c++) h[c] = (v[u][c] - mean) * rstd * pa.g[u][c] + pa.b[u][c];
             if constexpr (GLOBAL)
                 prep_values<KIND>(h, j, (__attribute__((address_space(1))) uint32_t *)rec);
             else
@@ -187,6 +210,15 @@ __device__ __forceinline__ void ln_records(const f32x4 (&v)[kLnSlots], const flo
                 zero_record(j, (__attribute__((address_space(3))) uint32_t *)rec);
         }
     }
+}
+
+// As ln_records_p, reading the gain lg and bias lb here.
+template <int KIND, bool GLOBAL>
+__device__ __forceinline__ void ln_records(const f32x4 (&v)[kLnSlots], const float *lg, const float *lb, float eps,
+                                           uint32_t nb, uint32_t span, uint8_t *out, float *red) {
+    LnParams pa;
+    load_ln(lg, lb, nb, pa);
+    ln_records_p<KIND, GLOBAL>(v, pa, eps, nb, span, out, red);
 }
 
 // The LayerNorm of x (k = 32 nb values in global memory) into prepared records (ln_records); x is
@@ -209,7 +241,7 @@ template <int KIND>
 __global__ __launch_bounds__(64 * kMaxWaves) void ln_prep_kernel(const float *__restrict__ x, const float *__restrict__ lg,
                                                                  const float *__restrict__ lb, float eps, uint32_t nb,
                                                                  uint8_t *__restrict__ out) {
-    __shared__ float red[kMaxWaves];
+    __shared__ float red[kLnRed];
     ln_prep<KIND, true>(x, lg, lb, eps, nb, (nb + 7) / 8 * 8, out, red);
 }
 
@@ -239,8 +271,9 @@ struct StepArgs {
 };
 
 // The residual row into the thread's slots (see ln_records); workgroup (0, 0) stores it.
+// rb: the bias's slots already loaded (or null: read here).
 template <int KIND>
-__device__ __forceinline__ void residual_row(const StepArgs &a, f32x4 (&v)[kLnSlots]) {
+__device__ __forceinline__ void residual_row(const StepArgs &a, f32x4 (&v)[kLnSlots], const f32x4 *rb = nullptr) {
     const uint32_t nb = a.nb, d = a.d;
 #pragma unroll
     for (uint32_t u = 0; u < kLnSlots; u++) {
@@ -279,7 +312,7 @@ __device__ __forceinline__ void residual_row(const StepArgs &a, f32x4 (&v)[kLnSl
 #pragma unroll
                 for (int k = 0; k < 16; k++) t += r[k];
             }
-            t += gload4(a.pbias + sl * 4);
+            t += rb ? rb[u] : gload4(a.pbias + sl * 4);
             v[u] = x + t;
         }
         if (blockIdx.x == 0 && blockIdx.y == 0 && a.x_out) *(f32x4 *)(a.x_out + sl * 4) = v[u];
@@ -711,14 +744,39 @@ __device__ __forceinline__ void run_tasks2(const StepArgs &a, uint32_t h, Batch<
 // (hd floats) goes to out (LDS). One pass over the caches: L = hd / 4 lanes share a cache row (a
 // 16-byte load each of its k and v), a lane group takes U rows at a time with all their loads
 // issued together and keeps a running maximum, sum and output (the softmax's max-subtracted
-// exponentials, rescaled when the maximum grows); the NR groups then meet through LDS, rescaled
-// to the common maximum. Rows past T are read as row T - 1 and dropped. h: the head.
+// exponentials, rescaled when the maximum grows); the groups of a wavefront then meet through
+// lane exchanges and the wavefronts through LDS, each rescaled to the common maximum. Rows past T
+// are read as row T - 1 and dropped. h: the head. pre: the first rows of the thread's lane group,
+// requested ahead by attend_issue.
+constexpr int kAttnU = 8;  // rows a lane group takes at a time
+struct AttnRows {
+    f32x4 k[kAttnU], v[kAttnU];
+};
+
+// attend_head's first rows of the thread's lane group (rows rg, rg + NR, ... below T - 1): the
+// cached rows below the newest position do not change during a step, so they can be requested
+// before the newest row and q exist.
+template <int L>
+__device__ __forceinline__ void attend_issue(uint32_t h, const float *kc, const float *vc, uint32_t T, uint32_t d,
+                                             AttnRows &pre) {
+    constexpr uint32_t hd = 4 * L, NR = kStepThreads / L;
+    const uint32_t li = threadIdx.x % L, rg = threadIdx.x / L, last = T - 1;
+    const float *kb = kc + h * hd + 4 * li;
+    const float *vb = vc + h * hd + 4 * li;
+#pragma unroll
+    for (int u = 0; u < kAttnU; u++) {
+        const uint32_t j = min(rg + u * NR, last);
+        pre.k[u] = j < last ? gload4(kb + (size_t)j * d) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        pre.v[u] = j < last ? gload4(vb + (size_t)j * d) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
 template <int L>
 __device__ __forceinline__ void attend_head(uint32_t h, const float *qh, const float *knew, const float *vnew,
                                              const float *kc, const float *vc, uint32_t T, uint32_t d, float scale,
-                                             float *s, float *accs, float *red, float *out) {
+                                             float *s, float *accs, float *red, float *out, const AttnRows &pre) {
     constexpr uint32_t hd = 4 * L, NR = kStepThreads / L;
-    constexpr int U = 8;
+    constexpr int U = kAttnU;
     const uint32_t tid = threadIdx.x;
     const uint32_t li = tid % L, rg = tid / L, last = T - 1;
     (void)red;
@@ -728,14 +786,8 @@ __device__ __forceinline__ void attend_head(uint32_t h, const float *qh, const f
     const f32x4 kl = *(const f32x4 *)(knew + 4 * li), vl = *(const f32x4 *)(vnew + 4 * li);
     float m = -INFINITY, z = 0.0f;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t j0 = rg; j0 < T; j0 += U * NR) {  // the L lanes of a row share the loop bound
-        f32x4 kr[U], vr[U];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const uint32_t j = min(j0 + u * NR, last);
-            kr[u] = j == last ? kl : gload4(kb + (size_t)j * d);
-            vr[u] = j == last ? vl : gload4(vb + (size_t)j * d);
-        }
+    // rows j0, j0 + NR, ... (row T - 1 and those past it: the newest row, dropped past T)
+    auto chunk = [&](uint32_t j0, const f32x4 (&kr)[U], const f32x4 (&vr)[U]) {
         float sc[U];
         float mc = -INFINITY;
 #pragma unroll
@@ -757,21 +809,58 @@ __device__ __forceinline__ void attend_head(uint32_t h, const float *qh, const f
             for (int c = 0; c < 4; c++) acc[c] += e * vr[u][c];
         }
         m = mn;
+    };
+    if (rg < T) {  // the first rows: requested ahead (the L lanes of a row share the bounds)
+        f32x4 kr[U], vr[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const bool nw = min(rg + u * NR, last) == last;
+            kr[u] = nw ? kl : pre.k[u];
+            vr[u] = nw ? vl : pre.v[u];
+        }
+        chunk(rg, kr, vr);
     }
-    // the groups' maxima, then each group's sum and output at the common maximum
-    if (li == 0) s[rg] = m;
+    for (uint32_t j0 = rg + U * NR; j0 < T; j0 += U * NR) {
+        f32x4 kr[U], vr[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t j = min(j0 + u * NR, last);
+            kr[u] = j == last ? kl : gload4(kb + (size_t)j * d);
+            vr[u] = j == last ? vl : gload4(vb + (size_t)j * d);
+        }
+        chunk(j0, kr, vr);
+    }
+    // the wavefront's groups pairwise (lanes li + L, li + 2L, ...), at the larger maximum; groups
+    // with no rows (maximum -inf) add nothing
+#pragma unroll
+    for (uint32_t o = L; o < 64; o *= 2) {
+        const float mo = __shfl_xor(m, o, 64), zo = __shfl_xor(z, o, 64);
+        f32x4 ao;
+#pragma unroll
+        for (int c = 0; c < 4; c++) ao[c] = __shfl_xor(acc[c], o, 64);
+        const float mn = fmaxf(m, mo);
+        const float fa = m == -INFINITY ? 0.0f : expf(m - mn), fb = mo == -INFINITY ? 0.0f : expf(mo - mn);
+        z = z * fa + zo * fb;
+        acc = acc * fa + ao * fb;
+        m = mn;
+    }
+    // then the wavefronts: their maxima, then each one's sum and output at the common maximum
+    constexpr uint32_t NW = kStepThreads / 64;
+    const uint32_t wv = tid / 64, lw = tid % 64;
+    if (lw == 0) s[wv] = m;
     __syncthreads();
     float M = -INFINITY;
-    for (uint32_t g = 0; g < NR; g++) M = fmaxf(M, s[g]);
-    const float f = m == -INFINITY ? 0.0f : expf(m - M);  // groups with no rows add nothing
-    *(f32x4 *)&accs[rg * hd + 4 * li] = acc * f;
-    __syncthreads();
-    if (li == 0) s[NR + rg] = z * f;
+#pragma unroll
+    for (uint32_t g = 0; g < NW; g++) M = fmaxf(M, s[g]);
+    const float f = m == -INFINITY ? 0.0f : expf(m - M);
+    if (lw < L) *(f32x4 *)&accs[wv * hd + 4 * li] = acc * f;
+    if (lw == 0) s[NW + wv] = z * f;
     __syncthreads();
     if (tid < hd) {
         float zs = 0.0f, t = 0.0f;
-        for (uint32_t g = 0; g < NR; g++) {
-            zs += s[NR + g];
+#pragma unroll
+        for (uint32_t g = 0; g < NW; g++) {
+            zs += s[NW + g];
             t += accs[g * hd + tid];
         }
         out[tid] = t / zs;
@@ -807,8 +896,10 @@ __global__ __launch_bounds__(kStepThreads) void attn_out_kernel(StepArgs a) {
         if (wave + i * kStepWaves < a.d / 32) load_task2<KIND, PAIRS>(s2[i], a, blockIdx.x, wave + i * kStepWaves, oq, os);
     const uint32_t p = (uint32_t)a.state[0];
     const size_t off = (size_t)blockIdx.x * hd;
+    AttnRows pre;
+    attend_issue<L>(blockIdx.x, a.kc, a.vc, p + 1, a.d, pre);
     attend_head<L>(blockIdx.x, a.q + off, a.kc + (size_t)p * a.d + off, a.vc + (size_t)p * a.d + off, a.kc, a.vc, p + 1, a.d,
-                    a.scale, s, accs, red, att);
+                    a.scale, s, accs, red, att, pre);
     __syncthreads();
     prep_lds<KIND>(att, hd, recs2);
     __syncthreads();
@@ -819,7 +910,7 @@ __global__ __launch_bounds__(kStepThreads) void attn_out_kernel(StepArgs a) {
 // prepared records (the head's x); one workgroup.
 template <int KIND>
 __global__ __launch_bounds__(kStepThreads) void final_ln_kernel(StepArgs a, uint8_t *__restrict__ out) {
-    __shared__ float red[kStepWaves];
+    __shared__ float red[kLnRed];
     f32x4 v[kLnSlots];
     residual_row<KIND>(a, v);
     ln_records<KIND, true>(v, a.ln_g, a.ln_b, a.eps, a.nb, (a.nb + 7) / 8 * 8, out, red);
@@ -917,9 +1008,12 @@ __device__ __forceinline__ void one_signal(uint32_t *cnt) {
 }
 
 template <int KIND>
-struct OneGemv {  // a decode-GEMV task's requested first batch and bias
+struct OneGemv {  // a decode-GEMV task's requested first batch and bias; PRO_LNR: its LayerNorm's
+                  // gain and bias and the residual row's bias (one_issue_ln)
     Batch<KIND> cur;
     float pre_bias;
+    LnParams ln;
+    f32x4 rb[kLnSlots];
 };
 
 // Requests task (g, sp)'s first batch (wavefront w: blocks b0 + 8 w ..) and the lane's bias, as
@@ -939,6 +1033,20 @@ __device__ __forceinline__ void one_issue(const DecodeGemv &a, uint32_t g, uint3
     if (bb < b1) load_weights<KIND>(t.cur, rq, rd, oq, (uint32_t)(r * 16), bb);
     t.pre_bias = 0.0f;
     if (wave == 0 && !upper && g * 32 + r < a.n && a.bias) t.pre_bias = a.bias[g * 32 + r];
+}
+
+// PRO_LNR: requests the LayerNorm's gain and bias and the residual row's bias (constants of the
+// model, so they can be read before the wait for the row).
+template <int KIND>
+__device__ __forceinline__ void one_issue_ln(const DecodeGemv &a, OneGemv<KIND> &t) {
+    load_ln(a.ln_g, a.ln_b, a.nb, t.ln);
+    if (a.x_in) {
+#pragma unroll
+        for (uint32_t u = 0; u < kLnSlots; u++) {
+            const uint32_t sl = threadIdx.x + u * blockDim.x;
+            if (sl / 8 < a.nb) t.rb[u] = gload4(a.rbias + sl * 4);
+        }
+    }
 }
 
 // The rest of decode_gemv_kernel's task (g, sp) for PRO_LNR / PRO_NONE and EPI_QKV / EPI_GELU /
@@ -979,8 +1087,8 @@ __device__ __forceinline__ void one_run(const DecodeGemv &a, uint32_t g, uint32_
         f.x_out = nullptr;  // stored at the end (store_x)
         f.d = nb * 32;
         f.nb = nb;
-        residual_row<KIND>(f, v);
-        ln_records<KIND, false>(v, a.ln_g, a.ln_b, a.eps, nb, span, prep, red);
+        residual_row<KIND>(f, v, t.rb);
+        ln_records_p<KIND, false>(v, t.ln, a.eps, nb, span, prep, red);
     } else {
         for (uint32_t blk = b0 + threadIdx.x / 8; blk < b1; blk += blockDim.x / 8) {
             const int j = threadIdx.x % 8;
@@ -1082,6 +1190,7 @@ __device__ __forceinline__ void one_qkv(const OneArgs *A, uint32_t l, uint32_t t
     }
     OneGemv<KIND> t;
     one_issue<KIND>(g, task, 0, t);
+    one_issue_ln<KIND>(g, t);
     const uint32_t H = A->heads, S = A->S, Z = A->slots;
     if (l > 0) one_wait(A->sync + one_counter(l - 1, H + 1 + S, Z), e1 * A->nD, A->sync + one_counter(A->n_layers, 0, Z));
     one_run<KIND, PRO_LNR, EPI_QKV>(g, task, 0, t, lds, task == 0);
@@ -1115,17 +1224,22 @@ __device__ __forceinline__ void one_attn(const OneArgs *A, uint32_t l, uint32_t 
 #pragma unroll
     for (int i = 0; i < K2; i++)
         if (wave + i * kStepWaves < nb) load_task2<KIND, PAIRS>(s2[i], sa, task, wave + i * kStepWaves, oq, os);
+    const uint32_t p = (uint32_t)A->state[0];  // (the pick at the step's end advances it)
+    AttnRows pre;
+    // the first cache rows before the wait (with head width 256 after it: their registers on top of
+    // the W_o sets' would spill)
+    if constexpr (L < 64) attend_issue<L>(task, Y.kc, Y.vc, p + 1, d, pre);
     // the head's q, k and v row groups
     one_wait(A->sync + one_counter(l, task, A->slots), e1 * 3 * (hd / 32), A->sync + one_counter(A->n_layers, 0, A->slots));
+    if constexpr (L >= 64) attend_issue<L>(task, Y.kc, Y.vc, p + 1, d, pre);
     float *s = (float *)lds;
     float *accs = s + kAttnSlots;
     float *red = accs + kStepThreads * 4;
     float *att = red + 2 * kStepWaves;
     uint8_t *recs2 = (uint8_t *)(att + hd);
-    const uint32_t p = (uint32_t)A->state[0];
     const size_t off = (size_t)task * hd;
     attend_head<L>(task, Y.q + off, Y.kc + (size_t)p * d + off, Y.vc + (size_t)p * d + off, Y.kc, Y.vc, p + 1, d,
-                   A->scale, s, accs, red, att);
+                   A->scale, s, accs, red, att, pre);
     __syncthreads();
     prep_lds<KIND>(att, hd, recs2);
     __syncthreads();
@@ -1158,6 +1272,7 @@ __device__ __forceinline__ void one_up(const OneArgs *A, uint32_t l, uint32_t ta
     g.x_out = Y.xm;
     OneGemv<KIND> t;
     one_issue<KIND>(g, task, 0, t);
+    one_issue_ln<KIND>(g, t);
     one_wait(A->sync + one_counter(l, A->heads, A->slots), e1 * A->nB, A->sync + one_counter(A->n_layers, 0, A->slots));
     one_run<KIND, PRO_LNR, EPI_GELU>(g, task, 0, t, lds, task == 0);
     // the FFN-down K chunk this row group of f belongs to
@@ -1211,8 +1326,15 @@ __device__ __forceinline__ void one_head(const OneArgs *A, uint32_t e1, uint8_t 
     g.n = A->vocab;
     g.chunk = span;
     g.state = A->state;
+    g.ln_g = A->lnf_g;
+    g.ln_b = A->lnf_b;
+    g.x_in = A->layers[L - 1].xm;
+    g.rbias = A->layers[L - 1].b2;
     OneGemv<KIND> t;
-    if (w < groups) one_issue<KIND>(g, w, 0, t);
+    if (w < groups) {
+        one_issue<KIND>(g, w, 0, t);
+        one_issue_ln<KIND>(g, t);
+    }
     one_wait(A->sync + one_counter(L - 1, A->heads + 1 + A->S, A->slots), e1 * A->nD, err);
     uint8_t *prep = lds;
     float *part = (float *)(lds + span * kPrepBytes);
@@ -1228,8 +1350,8 @@ __device__ __forceinline__ void one_head(const OneArgs *A, uint32_t e1, uint8_t 
         z.d = d;
         z.nb = nb;
         f32x4 v[kLnSlots];
-        residual_row<KIND>(z, v);
-        ln_records<KIND, false>(v, A->lnf_g, A->lnf_b, A->eps, nb, span, prep, red);
+        residual_row<KIND>(z, v, t.rb);
+        ln_records_p<KIND, false>(v, t.ln, A->eps, nb, span, prep, red);
         __syncthreads();
         constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
         const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16);
@@ -1360,7 +1482,7 @@ __global__ __launch_bounds__(kStepThreads) void one_step_kernel(const OneArgs *_
 // LDS of one_step_kernel: the largest of its roles'.
 __host__ inline size_t one_lds(size_t d, size_t hd, uint32_t chunk_down) {
     const size_t nb = d / 32, span = (nb + 7) / 8 * 8;
-    const size_t tail = (size_t)kStepWaves * 32 * 4 + kStepWaves * 4;
+    const size_t tail = (size_t)kStepWaves * 32 * 4 + kLnRed * 4;
     const size_t b = std::max(span * kPrepBytes + tail, (size_t)chunk_down * kPrepBytes + tail);
     return std::max(b, (size_t)attn_out_lds((uint32_t)hd));
 }
@@ -1452,7 +1574,7 @@ hipError_t launch_dgemv(hipStream_t s, DecodeGemv a, bool allow_split) {
     a.chunk = chunk8 * 8;
     const uint32_t W = chunk8 < (uint32_t)kMaxWaves ? chunk8 : (uint32_t)kMaxWaves;
     const size_t recs = PRO == PRO_GLOBAL ? 0 : (PRO == PRO_LN || PRO == PRO_LNR ? nb8 * 8 : a.chunk);
-    const size_t lds = recs * kPrepBytes + (size_t)W * 32 * 4 + (size_t)kMaxWaves * 4;
+    const size_t lds = recs * kPrepBytes + (size_t)W * 32 * 4 + (size_t)kLnRed * 4;
     decode_gemv_kernel<KIND, PRO, EPI><<<dim3(groups, splits), 64 * W, lds, s>>>(a);
     return hipGetLastError();
 }
