@@ -44,7 +44,7 @@ enum { PRO_NONE = 0, PRO_LN = 1, PRO_GLOBAL = 2, PRO_LNR = 3 };  // PRO_LNR: Lay
 enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_GELU = 2, EPI_QKV = 3, EPI_ARGMAX = 4, EPI_PARTIAL = 5 };
 
 constexpr int kMaxWaves = 8;           // wavefronts per decode-GEMV workgroup (two per SIMD)
-constexpr int kLnRed = 2 * kMaxWaves;  // reduction slots (floats) a LayerNorm prologue uses
+constexpr int kLnRed = 4 * kMaxWaves;  // reduction slots (floats) a LayerNorm prologue uses
 constexpr uint32_t kMaxBlocks = 512;   // blocks per row (k <= 16384): 80 KiB of prepared x in LDS
 constexpr uint32_t kLnSlots = 2;       // LayerNorm prologue: (block, lane) slots a thread keeps in registers
 constexpr uint32_t kNone = 0xffffffffu;
@@ -112,18 +112,6 @@ __device__ __forceinline__ void cstore4(float *p, f32x4 v) {
 }
 
 
-// Sum over the workgroup (every thread gets the total); red holds one float per wavefront.
-__device__ __forceinline__ float block_sum(float v, float *red) {
-    v = wave_reduce(v, AddOp());
-    const uint32_t w = threadIdx.x / 64, nw = blockDim.x / 64;
-    __syncthreads();  // red may still be read by a previous call
-    if (threadIdx.x % 64 == 0) red[w] = v;
-    __syncthreads();
-    float t = 0.0f;
-    for (uint32_t i = 0; i < nw; i++) t += red[i];
-    return t;
-}
-
 // Loads from memory other workgroups wrote in this launch (past the per-CU caches).
 __device__ __forceinline__ float coherent_load(const float *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -132,17 +120,6 @@ __device__ __forceinline__ float coherent_load(const float *p) {
 // The first maximum wins; NaN never does (ferrum_model/src/sampling.rs:32-40). kNone: no candidate.
 __device__ __forceinline__ bool better(float v2, uint32_t i2, float v1, uint32_t i1) {
     return i2 != kNone && (i1 == kNone || v2 > v1 || (v2 == v1 && i2 < i1));
-}
-
-// As block_sum with one barrier: no wavefront may still be reading red from an earlier reduction.
-__device__ __forceinline__ float block_sum_once(float v, float *red) {
-    v = wave_reduce(v, AddOp());
-    const uint32_t nw = blockDim.x / 64;
-    if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = v;
-    __syncthreads();
-    float t = 0.0f;
-    for (uint32_t i = 0; i < nw; i++) t += red[i];
-    return t;
 }
 
 struct LnParams {  // a LayerNorm's gain and bias in the thread's slots (see ln_records_p)
@@ -164,31 +141,60 @@ __device__ __forceinline__ void load_ln(const float *lg, const float *lb, uint32
 // holds in registers (thread slot u: block sl / 8, elements 4 sl .. 4 sl + 3 with
 // sl = threadIdx.x + u blockDim.x; slots past nb hold nothing), with gain and bias pa (load_ln),
 // written as the prepared records of `span` blocks (zero records past nb) at out (LDS, or global
-// when GLOBAL). span * 8 <= kLnSlots * blockDim.x. red: kLnRed floats, not read by an earlier
-// reduction that a wavefront may still be in (the two reductions use halves of it).
+// when GLOBAL). span * 8 <= kLnSlots * blockDim.x. red: kLnRed floats (16-byte aligned) that no
+// wavefront may still be reading from an earlier use.
+//
+// The mean and variance take one barrier: each wavefront sums its values' offsets from a shift c_w
+// (its lane 0's first value) and their squares, and the wavefronts' sums meet through LDS, where
+// sum (x - mean)^2 = sum_w [S2_w - 2 (mean - c_w) S1_w + n_w (mean - c_w)^2] (S1_w, S2_w: the
+// wavefront's sums of x - c_w and of its squares; n_w its count). A shift taken from the data keeps
+// the squares' sums from cancelling; the result differs from the two-pass statistics of nn.rs only
+// in rounding.
 template <int KIND, bool GLOBAL>
 __device__ __forceinline__ void ln_records_p(const f32x4 (&v)[kLnSlots], const LnParams &pa, float eps, uint32_t nb,
                                              uint32_t span, uint8_t *out, float *red) {
-    const uint32_t k = nb * 32;
-    float s = 0.0f;
+    const uint32_t k = nb * 32, nw = blockDim.x / 64, w = threadIdx.x / 64;
+    // the wavefront's count: its slots below 8 nb, four values each
+    uint32_t cnt = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < kLnSlots; u++) {
+        const int32_t r = (int32_t)(8 * nb) - (int32_t)(64 * w + u * blockDim.x);
+        cnt += (uint32_t)min(max(r, 0), 64);
+    }
+    const float cw = 8 * w < nb ? lane_value(v[0].x, 0) : 0.0f;  // lane 0's slot 0 holds data iff any lane does
+    float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
     for (uint32_t u = 0; u < kLnSlots; u++) {
         const uint32_t sl = threadIdx.x + u * blockDim.x;
-        if (sl / 8 < nb) s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
-    }
-    const float mean = block_sum_once(s, red) / (float)k;
-    float q = 0.0f;
-#pragma unroll
-    for (uint32_t u = 0; u < kLnSlots; u++) {
-        if ((threadIdx.x + u * blockDim.x) / 8 < nb) {
+        if (sl / 8 < nb) {
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                const float t = v[u][c] - mean;
-                q += t * t;
+                const float t = v[u][c] - cw;
+                s1 += t;
+                s2 += t * t;
             }
         }
     }
-    const float rstd = 1.0f / sqrtf(block_sum_once(q, red + kMaxWaves) / (float)k + eps);
+    s1 = wave_reduce(s1, AddOp());
+    s2 = wave_reduce(s2, AddOp());
+    if (threadIdx.x % 64 == 0)
+        *(f32x4 *)&red[4 * w] = f32x4{s1, s2, cw, (float)(4 * cnt)};
+    __syncthreads();
+    // (the reads issued together: a loop that waits for each read costs an LDS latency a step)
+    f32x4 rw[kMaxWaves];
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxWaves; i++) rw[i] = i < nw ? *(const f32x4 *)&red[4 * i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float tot = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxWaves; i++) tot += rw[i].x + rw[i].w * rw[i].z;
+    const float mean = tot / (float)k;
+    float m2 = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxWaves; i++) {
+        const float dl = mean - rw[i].z;
+        m2 += rw[i].y - 2.0f * dl * rw[i].x + rw[i].w * dl * dl;
+    }
+    const float rstd = 1.0f / sqrtf(fmaxf(m2, 0.0f) / (float)k + eps);
 #pragma unroll
     for (uint32_t u = 0; u < kLnSlots; u++) {
         const uint32_t sl = threadIdx.x + u * blockDim.x, blk = sl / 8;
@@ -241,7 +247,7 @@ template <int KIND>
 __global__ __launch_bounds__(64 * kMaxWaves) void ln_prep_kernel(const float *__restrict__ x, const float *__restrict__ lg,
                                                                  const float *__restrict__ lb, float eps, uint32_t nb,
                                                                  uint8_t *__restrict__ out) {
-    __shared__ float red[kLnRed];
+    __shared__ __attribute__((aligned(16))) float red[kLnRed];
     ln_prep<KIND, true>(x, lg, lb, eps, nb, (nb + 7) / 8 * 8, out, red);
 }
 
@@ -445,8 +451,13 @@ __global__ __launch_bounds__(64 * kMaxWaves) void decode_gemv_kernel(DecodeGemv 
     if (!upper) part[wave * 32 + r] = sum;
     __syncthreads();
     if (wave != 0 || upper) return;
+    float pw[kMaxWaves];  // (the reads issued together)
+#pragma unroll
+    for (uint32_t w = 0; w < kMaxWaves; w++) pw[w] = w < W ? part[w * 32 + r] : 0.0f;
     float t = 0.0f;
-    for (uint32_t w = 0; w < W; w++) t += part[w * 32 + r];
+#pragma unroll
+    for (uint32_t w = 0; w < kMaxWaves; w++)
+        if (w < W) t += pw[w];
     const uint32_t row = g * 32 + r;
     if constexpr (EPI == EPI_PARTIAL) {
         // the split's row sums, added in split order by their consumer (residual_row)
@@ -786,15 +797,20 @@ __device__ __forceinline__ void attend_head(uint32_t h, const float *qh, const f
     const f32x4 kl = *(const f32x4 *)(knew + 4 * li), vl = *(const f32x4 *)(vnew + 4 * li);
     float m = -INFINITY, z = 0.0f;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    // rows j0, j0 + NR, ... (row T - 1 and those past it: the newest row, dropped past T)
+    // rows j0, j0 + NR, ... (row T - 1 and those past it: the newest row, dropped past T). Rows
+    // past T are skipped (branches uniform over a lane group): their weight would be exp(-inf) = 0,
+    // which adds nothing.
     auto chunk = [&](uint32_t j0, const f32x4 (&kr)[U], const f32x4 (&vr)[U]) {
         float sc[U];
         float mc = -INFINITY;
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            float dt = (qv.x * kr[u].x + qv.y * kr[u].y) + (qv.z * kr[u].z + qv.w * kr[u].w);
-            dt = group_reduce<L>(dt, AddOp());
-            sc[u] = j0 + u * NR < T ? dt * scale : -INFINITY;
+            sc[u] = -INFINITY;
+            if (j0 + u * NR < T) {
+                float dt = (qv.x * kr[u].x + qv.y * kr[u].y) + (qv.z * kr[u].z + qv.w * kr[u].w);
+                dt = group_reduce<L>(dt, AddOp());
+                sc[u] = dt * scale;
+            }
             mc = fmaxf(mc, sc[u]);
         }
         const float mn = fmaxf(m, mc);  // finite: row j0 < T is in the chunk
@@ -803,10 +819,12 @@ __device__ __forceinline__ void attend_head(uint32_t h, const float *qh, const f
         acc *= corr;
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const float e = expf(sc[u] - mn);
-            z += e;
+            if (j0 + u * NR < T) {
+                const float e = expf(sc[u] - mn);
+                z += e;
 #pragma unroll
-            for (int c = 0; c < 4; c++) acc[c] += e * vr[u][c];
+                for (int c = 0; c < 4; c++) acc[c] += e * vr[u][c];
+            }
         }
         m = mn;
     };
@@ -910,7 +928,7 @@ __global__ __launch_bounds__(kStepThreads) void attn_out_kernel(StepArgs a) {
 // prepared records (the head's x); one workgroup.
 template <int KIND>
 __global__ __launch_bounds__(kStepThreads) void final_ln_kernel(StepArgs a, uint8_t *__restrict__ out) {
-    __shared__ float red[kLnRed];
+    __shared__ __attribute__((aligned(16))) float red[kLnRed];
     f32x4 v[kLnSlots];
     residual_row<KIND>(a, v);
     ln_records<KIND, true>(v, a.ln_g, a.ln_b, a.eps, a.nb, (a.nb + 7) / 8 * 8, out, red);
@@ -975,8 +993,10 @@ constexpr uint32_t kOneMaxLayers = 256;
 // Every counter has kCopies copies, a cache line apart, each incremented by every task of its phase
 // (one lane per copy); workgroup w polls copy w % kCopies. With one copy, about a hundred workgroups
 // polling one address while the tasks' atomics queued behind them made the step 1.5x slower than
-// with 8 copies; 32 were 2% faster again (measured, GPT-2-small).
-constexpr uint32_t kCopies = 32, kCopyStride = 32;  // (in uint32_t)
+// with 8 copies. Measured on GPT-2-small (us per step): 16 copies 207.5, 32 copies 204.5, 64
+// copies 202.1, 128 copies 204.1, 256 copies 217.7 (each task's 256 atomics then cost more than the
+// pollers they spread). Four wavefronts polling each (staggered) cost 20 us: polls are not free.
+constexpr uint32_t kCopies = 64, kCopyStride = 32;  // (in uint32_t)
 constexpr uint32_t kCounter = kCopies * kCopyStride;  // uint32_t per counter
 __host__ __device__ constexpr uint32_t one_counter(uint32_t l, uint32_t slot, uint32_t slots) {
     return (l * slots + slot) * kCounter;
@@ -996,7 +1016,7 @@ __device__ __forceinline__ void one_wait(uint32_t *cnt, uint32_t target, uint32_
             __builtin_amdgcn_s_sleep(1);
         }
     }
-    __syncthreads();  // (what the phase wrote is read with agent-coherent loads)
+    __syncthreads();
 }
 
 // After the task's agent-coherent stores (each wavefront that stored waited for them): one increment
