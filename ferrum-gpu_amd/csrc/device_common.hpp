@@ -139,6 +139,9 @@ struct MaxOp {
 struct AndOp {
     __device__ int operator()(int a, int b) const { return a & b; }
 };
+struct MaxUOp {
+    __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; }
+};
 template <int L, class T, class Op>
 __device__ __forceinline__ T group_reduce(T v, Op op) {
     static_assert(L == 2 || L == 4 || L == 8 || L == 16 || L == 32 || L == 64, "lane groups of 2 to 64");

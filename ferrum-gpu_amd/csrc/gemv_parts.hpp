@@ -71,11 +71,13 @@ static_assert(prep_dwords_match_slots<FH_Q8_0>() && prep_dwords_match_slots<FH_Q
 // by DPP).
 template <int KIND, class U32Ptr>
 __device__ __forceinline__ void prep_values(f32x4 v, int j, U32Ptr rec) {
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    int finite = (int)(fabsf(v.x) <= 3.4028235e38f) & (int)(fabsf(v.y) <= 3.4028235e38f) &
-                 (int)(fabsf(v.z) <= 3.4028235e38f) & (int)(fabsf(v.w) <= 3.4028235e38f);  // 0: inf, NaN
-    amax = group_reduce<8>(amax, MaxOp());
-    finite = group_reduce<8>(finite, AndOp());
+    // the largest magnitude's bits, one integer reduction: the bit patterns of non-negative floats
+    // order as the values do, and inf (0x7f800000) and NaN (above it) order above every finite one
+    const uint32_t am = max(max(__float_as_uint(v.x) & 0x7fffffffu, __float_as_uint(v.y) & 0x7fffffffu),
+                            max(__float_as_uint(v.z) & 0x7fffffffu, __float_as_uint(v.w) & 0x7fffffffu));
+    const uint32_t abits = group_reduce<8>(am, MaxUOp());
+    const int finite = abits < 0x7f800000u;  // 0: inf, NaN
+    const float amax = __uint_as_float(abits);
     // grid 2^-sh with 2^29 <= amax * 2^sh < 2^30, at most 2^149 (subnormal amax: exponent field
     // 1); the scaling is split in two exact power-of-two products so that no factor overflows
     const int sh = min(156 - (int)max(__float_as_uint(amax) >> 23, 1u), 149);  // -98 .. 149
