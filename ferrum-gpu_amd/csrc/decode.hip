@@ -706,20 +706,6 @@ __device__ __forceinline__ float half_sum(float acc, bool upper) {
     return acc + __uint_as_float(upper ? sw[0] : sw[1]);
 }
 
-// Prepared records of the `width` values at x (LDS), eight records (zero past width / 32); the
-// first 64 threads write them.
-template <int KIND>
-__device__ __forceinline__ void prep_lds(const float *x, uint32_t width, uint8_t *recs) {
-    if (threadIdx.x >= 64) return;
-    const uint32_t blk = threadIdx.x / 8;
-    const int j = (int)(threadIdx.x % 8);
-    auto *rec = (__attribute__((address_space(3))) uint32_t *)(recs + blk * kPrepBytes);
-    if (blk < width / 32)
-        prep_values<KIND>(*(const f32x4 *)(x + blk * 32 + 4 * j), j, rec);
-    else
-        zero_record(j, rec);
-}
-
 // The second product: row groups w, w + W, ... of the d rows, K in flight as above;
 // out_part[h] gets head h's share of each row (COH: agent-coherent stores).
 template <int KIND, int PAIRS, int K, bool COH = false>
@@ -752,7 +738,7 @@ __device__ __forceinline__ void run_tasks2(const StepArgs &a, uint32_t h, Batch<
 
 // Attention of one head over positions 0..T-1 (decode.rs:81-105) with q and the newest
 // position's k and v rows (T - 1) given apart (they may not be in the caches yet); the result a
-// (hd floats) goes to out (LDS). One pass over the caches: L = hd / 4 lanes share a cache row (a
+// (hd floats) goes to recs (LDS) as its prepared records. One pass over the caches: L = hd / 4 lanes share a cache row (a
 // 16-byte load each of its k and v), a lane group takes U rows at a time with all their loads
 // issued together and keeps a running maximum, sum and output (the softmax's max-subtracted
 // exponentials, rescaled when the maximum grows); the groups of a wavefront then meet through
@@ -782,10 +768,10 @@ __device__ __forceinline__ void attend_issue(uint32_t h, const float *kc, const 
     }
 }
 
-template <int L>
+template <int KIND, int L>
 __device__ __forceinline__ void attend_head(uint32_t h, const float *qh, const float *knew, const float *vnew,
                                              const float *kc, const float *vc, uint32_t T, uint32_t d, float scale,
-                                             float *s, float *accs, float *red, float *out, const AttnRows &pre) {
+                                             float *s, float *accs, float *red, uint8_t *recs, const AttnRows &pre) {
     constexpr uint32_t hd = 4 * L, NR = kStepThreads / L;
     constexpr int U = kAttnU;
     const uint32_t tid = threadIdx.x;
@@ -874,14 +860,28 @@ __device__ __forceinline__ void attend_head(uint32_t h, const float *qh, const f
     if (lw < L) *(f32x4 *)&accs[wv * hd + 4 * li] = acc * f;
     if (lw == 0) s[NW + wv] = z * f;
     __syncthreads();
-    if (tid < hd) {
-        float zs = 0.0f, t = 0.0f;
+    // the output a = (sum of the wavefronts' outputs) / (sum of their sums), straight into the
+    // prepared records of its hd / 32 blocks (eight records, zero past them; wavefront 0's lanes,
+    // eight a block)
+    if (tid < 64) {
+        const uint32_t blk = tid / 8;
+        const int j = (int)(tid % 8);
+        auto *rec = (__attribute__((address_space(3))) uint32_t *)(recs + blk * kPrepBytes);
+        if (blk < hd / 32) {
+            float zs = 0.0f;
+            f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (uint32_t g = 0; g < NW; g++) {
-            zs += s[NW + g];
-            t += accs[g * hd + tid];
+            for (uint32_t g = 0; g < NW; g++) {
+                zs += s[NW + g];
+                t += *(const f32x4 *)&accs[g * hd + blk * 32 + 4 * j];
+            }
+            f32x4 o;
+#pragma unroll
+            for (int c = 0; c < 4; c++) o[c] = t[c] / zs;
+            prep_values<KIND>(o, j, rec);
+        } else {
+            zero_record(j, rec);
         }
-        out[tid] = t / zs;
     }
 }
 
@@ -916,10 +916,8 @@ __global__ __launch_bounds__(kStepThreads) void attn_out_kernel(StepArgs a) {
     const size_t off = (size_t)blockIdx.x * hd;
     AttnRows pre;
     attend_issue<L>(blockIdx.x, a.kc, a.vc, p + 1, a.d, pre);
-    attend_head<L>(blockIdx.x, a.q + off, a.kc + (size_t)p * a.d + off, a.vc + (size_t)p * a.d + off, a.kc, a.vc, p + 1, a.d,
-                    a.scale, s, accs, red, att, pre);
-    __syncthreads();
-    prep_lds<KIND>(att, hd, recs2);
+    attend_head<KIND, L>(blockIdx.x, a.q + off, a.kc + (size_t)p * a.d + off, a.vc + (size_t)p * a.d + off, a.kc, a.vc,
+                         p + 1, a.d, a.scale, s, accs, red, recs2, pre);
     __syncthreads();
     run_tasks2<KIND, PAIRS, K2>(a, blockIdx.x, s2, recs2, oq, os, oa, ot);
 }
@@ -1258,10 +1256,8 @@ __device__ __forceinline__ void one_attn(const OneArgs *A, uint32_t l, uint32_t 
     float *att = red + 2 * kStepWaves;
     uint8_t *recs2 = (uint8_t *)(att + hd);
     const size_t off = (size_t)task * hd;
-    attend_head<L>(task, Y.q + off, Y.kc + (size_t)p * d + off, Y.vc + (size_t)p * d + off, Y.kc, Y.vc, p + 1, d,
-                   A->scale, s, accs, red, att, pre);
-    __syncthreads();
-    prep_lds<KIND>(att, hd, recs2);
+    attend_head<KIND, L>(task, Y.q + off, Y.kc + (size_t)p * d + off, Y.vc + (size_t)p * d + off, Y.kc, Y.vc, p + 1, d,
+                         A->scale, s, accs, red, recs2, pre);
     __syncthreads();
     run_tasks2<KIND, PAIRS, K2, true>(sa, task, s2, recs2, oq, os, oa, ot);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial rows have landed
@@ -1324,13 +1320,22 @@ __device__ __forceinline__ void one_down(const OneArgs *A, uint32_t l, uint32_t 
     one_signal(A->sync + one_counter(l, A->heads + 1 + A->S, A->slots));
 }
 
+constexpr uint32_t kHeadPre = 3;  // head batches each wavefront has requested ahead
+// The most head items (row group, batch) a workgroup takes: groups row groups over G workgroups.
+__host__ __device__ inline uint32_t one_head_items(uint32_t groups, uint32_t G, uint32_t nb8) {
+    return (groups + G - 1) / G * nb8;
+}
+
 // The head, folded into the step (decode_gemv_kernel<PRO_GLOBAL, EPI_ARGMAX> and pick_kernel):
 // every workgroup with head row groups forms x = x_m + (the down partial rows + b_2) and its final
 // LayerNorm into its own LDS records (workgroup 0 also stores x), then takes row groups w, w + G,
-// ... (the next group's first batch requested while the current one is reduced): the logits go to
-// A->logits and each group's offer (its first maximum; NaN never wins) to A->offer_v / offer_i with
-// agent-coherent stores. A ticket counts the finished workgroups; the last one picks the next
-// token over the offers as pick_kernel does and advances the state (position, input, epoch).
+// ... as items (row group, batch of eight blocks) spread over its eight wavefronts, each with
+// kHeadPre items requested ahead (the first ones before the wait), so that every wavefront keeps
+// loads in flight; a group's batch sums are added in batch order as the four-launch head adds its
+// wavefronts' (d <= 2048: one batch per wavefront there). The logits go to A->logits and each
+// group's offer (its first maximum; NaN never wins) to A->offers with agent-coherent stores. A
+// ticket counts the finished workgroups; the last one picks the next token over the offers as
+// pick_kernel does and advances the state (position, input, epoch).
 template <int KIND>
 __device__ __forceinline__ void one_head(const OneArgs *A, uint32_t e1, uint8_t *lds, uint32_t w, uint32_t G) {
     const uint32_t d = A->d, nb = d / 32, nb8 = (nb + 7) / 8, span = nb8 * 8, L = A->n_layers;
@@ -1350,15 +1355,27 @@ __device__ __forceinline__ void one_head(const OneArgs *A, uint32_t e1, uint8_t 
     g.ln_b = A->lnf_b;
     g.x_in = A->layers[L - 1].xm;
     g.rbias = A->layers[L - 1].b2;
+    // the workgroup's row groups w, w + G, ... (K of them) as items (group k, batch b), i = k nb8 + b,
+    // wavefront v taking items v, v + 8, ... with kHeadPre of them requested ahead
+    constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
+    const uint32_t K = w < groups ? (groups - w + G - 1) / G : 0, items = K * nb8;
+    const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16);
+    const uint32_t os = (uint32_t)(r * 16), oa = prep_a_offset(lane), ot = prep_tail_offset<KIND>(lane);
+    auto issue = [&](Batch<KIND> &b, uint32_t i) {
+        const uint32_t rg = w + (i / nb8) * G;
+        load_weights<KIND>(b, make_rsrc(g.qs + (size_t)rg * nb * 32 * QB, nb * 32 * QB),
+                           make_rsrc(g.ds + (size_t)rg * nb8 * 256, nb8 * 512), oq, os, (i % nb8) * kBatch);
+    };
+    Batch<KIND> hb[kHeadPre];
+#pragma unroll
+    for (uint32_t p = 0; p < kHeadPre; p++)
+        if (wave + p * kStepWaves < items) issue(hb[p], wave + p * kStepWaves);
     OneGemv<KIND> t;
-    if (w < groups) {
-        one_issue<KIND>(g, w, 0, t);
-        one_issue_ln<KIND>(g, t);
-    }
+    if (w < groups) one_issue_ln<KIND>(g, t);
     one_wait(A->sync + one_counter(L - 1, A->heads + 1 + A->S, A->slots), e1 * A->nD, err);
     uint8_t *prep = lds;
-    float *part = (float *)(lds + span * kPrepBytes);
-    float *red = part + kStepWaves * 32;
+    float *part = (float *)(lds + span * kPrepBytes);  // [items][32]
+    float *red = part + one_head_items(groups, G, nb8) * 32;
     if (w < groups) {
         StepArgs z{};
         z.x_in = A->layers[L - 1].xm;
@@ -1373,51 +1390,49 @@ __device__ __forceinline__ void one_head(const OneArgs *A, uint32_t e1, uint8_t 
         residual_row<KIND>(z, v, t.rb);
         ln_records_p<KIND, false>(v, t.ln, A->eps, nb, span, prep, red);
         __syncthreads();
-        constexpr uint32_t QB = KIND == FH_Q8_0 ? 32 : 16;
-        const uint32_t oq = KIND == FH_Q8_0 ? (uint32_t)(r * 32 + 16 * upper) : (uint32_t)(lane * 16);
-        const uint32_t os = (uint32_t)(r * 16), oa = prep_a_offset(lane), ot = prep_tail_offset<KIND>(lane);
         lds_byte *lp = (lds_byte *)prep;
-        for (uint32_t rg = w; rg < groups; rg += G) {
-            const auto rq = make_rsrc(g.qs + (size_t)rg * nb * 32 * QB, nb * 32 * QB);
-            const auto rd = make_rsrc(g.ds + (size_t)rg * nb8 * 256, nb8 * 512);
-            float acc = 0.0f;
-            Batch<KIND> nx;
-            for (uint32_t bb = wave * kBatch; bb < span; bb += kStepWaves * kBatch) {
-                const uint32_t nxt = bb + kStepWaves * kBatch;
-                if (nxt < span) load_weights<KIND>(nx, rq, rd, oq, os, nxt);
-                t.cur.a = *(const __attribute__((address_space(3))) i32x4 *)(lp + bb * kPrepBytes + oa);
-                load_tails<KIND>(t.cur, bb * kPrepBytes, ot,
-                                 [&](uint32_t off) { return *(const __attribute__((address_space(3))) u32x4 *)(lp + off); },
-                                 [&](uint32_t off) { return *(const __attribute__((address_space(3))) uint32_t *)(lp + off); });
-                compute_batch<KIND>(t.cur, upper, acc);
-                t.cur = nx;
-            }
-            if (rg + G < groups) one_issue<KIND>(g, rg + G, 0, t);  // the next group's first batch
-            const float sum = half_sum(acc, upper);
-            if (!upper) part[wave * 32 + r] = sum;
-            __syncthreads();
-            if (wave == 0 && !upper) {
-                float s = 0.0f;
-                for (uint32_t k = 0; k < kStepWaves; k++) s += part[k * 32 + r];
-                const uint32_t row = rg * 32 + r;
-                if (row < A->vocab) A->logits[row] = s;
-                float bv = s;
-                uint32_t bi = (row < A->vocab && s == s) ? row : kNone;
+        for (uint32_t base = wave; base < items; base += kHeadPre * kStepWaves) {
 #pragma unroll
-                for (int o = 16; o >= 1; o /= 2) {
-                    const float ov = __shfl_xor(bv, o, 32);
-                    const uint32_t oi = __shfl_xor(bi, o, 32);
-                    if (better(ov, oi, bv, bi)) {
-                        bv = ov;
-                        bi = oi;
-                    }
-                }
-                if (r == 0) {
-                    __hip_atomic_store((g_u64 *)(A->offers + rg), (uint64_t)bi << 32 | __float_as_uint(bv),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (uint32_t p = 0; p < kHeadPre; p++) {
+                const uint32_t i = base + p * kStepWaves;
+                if (i < items) {
+                    const uint32_t bb = (i % nb8) * kBatch;
+                    hb[p].a = *(const __attribute__((address_space(3))) i32x4 *)(lp + bb * kPrepBytes + oa);
+                    load_tails<KIND>(hb[p], bb * kPrepBytes, ot,
+                                     [&](uint32_t off) { return *(const __attribute__((address_space(3))) u32x4 *)(lp + off); },
+                                     [&](uint32_t off) { return *(const __attribute__((address_space(3))) uint32_t *)(lp + off); });
+                    float acc = 0.0f;
+                    compute_batch<KIND>(hb[p], upper, acc);
+                    const float sum = half_sum(acc, upper);
+                    if (!upper) part[i * 32 + r] = sum;
+                    if (i + kHeadPre * kStepWaves < items) issue(hb[p], i + kHeadPre * kStepWaves);
                 }
             }
-            __syncthreads();  // (part is rewritten by the next group)
+        }
+        __syncthreads();
+        // row group k in wavefront k % 8: its batches' sums in batch order (the four-launch head's
+        // idle wavefronts add zeros), the logits, and the group's offer
+        for (uint32_t k = wave; k < K; k += kStepWaves) {
+            if (upper) continue;
+            float s = 0.0f;
+            for (uint32_t b = 0; b < kStepWaves; b++) s += b < nb8 ? part[(k * nb8 + b) * 32 + r] : 0.0f;
+            const uint32_t rg = w + k * G, row = rg * 32 + r;
+            if (row < A->vocab) A->logits[row] = s;
+            float bv = s;
+            uint32_t bi = (row < A->vocab && s == s) ? row : kNone;
+#pragma unroll
+            for (int o = 16; o >= 1; o /= 2) {
+                const float ov = __shfl_xor(bv, o, 32);
+                const uint32_t oi = __shfl_xor(bi, o, 32);
+                if (better(ov, oi, bv, bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            if (r == 0) {
+                __hip_atomic_store((g_u64 *)(A->offers + rg), (uint64_t)bi << 32 | __float_as_uint(bv), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this workgroup's offers have landed
@@ -1499,12 +1514,13 @@ __global__ __launch_bounds__(kStepThreads) void one_step_kernel(const OneArgs *_
     one_head<KIND>(A, e1, olds, w, gridDim.x);
 }
 
-// LDS of one_step_kernel: the largest of its roles'.
-__host__ inline size_t one_lds(size_t d, size_t hd, uint32_t chunk_down) {
-    const size_t nb = d / 32, span = (nb + 7) / 8 * 8;
+// LDS of one_step_kernel: the largest of its roles'. G: the grid.
+__host__ inline size_t one_lds(size_t d, size_t hd, uint32_t chunk_down, uint32_t vocab, uint32_t G) {
+    const size_t nb = d / 32, nb8 = (nb + 7) / 8, span = nb8 * 8;
     const size_t tail = (size_t)kStepWaves * 32 * 4 + kLnRed * 4;
     const size_t b = std::max(span * kPrepBytes + tail, (size_t)chunk_down * kPrepBytes + tail);
-    return std::max(b, (size_t)attn_out_lds((uint32_t)hd));
+    const size_t head = span * kPrepBytes + (size_t)one_head_items((vocab + 31) / 32, G, (uint32_t)nb8) * 32 * 4 + kLnRed * 4;
+    return std::max(std::max(b, head), (size_t)attn_out_lds((uint32_t)hd));
 }
 
 // Sets the position and the first position whose input the argmax writes.
@@ -1872,13 +1888,14 @@ hipError_t enqueue_one(fh_gpt2 *m, hipStream_t s) {
 // resident at once (the occupancy query). Returns false (the four-launch step stays) otherwise.
 bool one_setup(fh_gpt2 *m) {
     const size_t d = m->dim, hd = d / m->heads;
-    if (m->form != 4 || m->layers > kOneMaxLayers) return false;
+    // (d <= 2048: one_head takes one batch of eight blocks per item)
+    if (m->form != 4 || m->layers > kOneMaxLayers || (d / 32 + 7) / 8 > kStepWaves) return false;
     uint32_t sp, c8;
     plan_splits((uint32_t)(d / 32), (uint32_t)((m->hidden / 32 + 7) / 8), &sp, &c8);
     const uint32_t tasks[4] = {(uint32_t)(3 * d / 32), (uint32_t)m->heads, (uint32_t)(m->hidden / 32),
                                (uint32_t)(d / 32) * sp};
     const uint32_t grid = std::max(tasks[0], tasks[2]) + std::max(tasks[1], tasks[3]);
-    const size_t lds = one_lds(d, hd, c8 * 8);
+    const size_t lds = one_lds(d, hd, c8 * 8, (uint32_t)m->vocab, grid);
     if (lds > kAttnOutLdsMax) return false;
     int dev = 0, cus = 0, per = 0;
     const void *k = m->kind == FH_Q8_0 ? one_kernel<FH_Q8_0>((uint32_t)hd) : one_kernel<FH_Q4_0>((uint32_t)hd);
