@@ -153,6 +153,11 @@ __device__ __forceinline__ T group_reduce(T v, Op op) {
     if constexpr (L >= 64) v = op(v, __shfl_xor(v, 32, 64));
     return v;
 }
+// SwiGLU's activation of one unit (ferrum_ref/src/models/llama/ops.rs:69-76): silu(g) * u, with
+// the reference's two roundings. Every kernel that applies it (the SwiGLU passes and the fast
+// GEMM's fused epilogue) uses this one definition, so their results are bit-identical.
+__device__ __forceinline__ float swiglu_act(float g, float u) { return __fmul_rn(g / (1.0f + expf(-g)), u); }
+
 template <class T, class Op>
 __device__ __forceinline__ T wave_reduce(T v, Op op) {
     v = group_reduce<16>(v, op);

@@ -304,7 +304,11 @@ struct GemmCfg {
     static_assert(BM * 8 % 256 == 0, "x staging must divide over 256 threads");
 };
 
-template <int KIND, int BM, int BN, int WAVES_M>
+// SWIGLU: the weight's rows are gate and up interleaved in runs of 32 (rows 64c .. 64c + 31 gate
+// units 32c .., rows 64c + 32 .. up units 32c ..), so a wavefront's two 32-column fragments hold a
+// unit's gate and up; the epilogue writes act = swiglu_act(gate, up) into y as [M][N / 2] instead of
+// the N outputs (one K split; N a multiple of 64).
+template <int KIND, int BM, int BN, int WAVES_M, bool SWIGLU = false>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict__ xh, const uint8_t *__restrict__ xl,
                                                       const int32_t *__restrict__ xsc, const uint8_t *__restrict__ qs,
                                                       const uint16_t *__restrict__ ds, const uint8_t *__restrict__ b8,
@@ -531,17 +535,34 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
     if (st < st1) stage(st, std::integral_constant<int, 0>{});
 
     // D layout of a 32x32 tile: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32
+    if constexpr (SWIGLU) {
+        static_assert(C::TN % 2 == 0, "a wavefront's fragments pair gate and up");
+        const uint32_t units = N / 2;
 #pragma unroll
-    for (int i = 0; i < C::TM; i++)
+        for (int i = 0; i < C::TM; i++)
 #pragma unroll
-        for (int j = 0; j < C::TN; j++) {
-            const uint32_t col = n0 + (wn * C::TN + j) * 32 + fr;
+            for (int j = 0; j < C::TN; j += 2) {
+                const uint32_t col = n0 + (wn * C::TN + j) * 32;  // a gate run (a multiple of 64)
+                const uint32_t unit = col / 2 + fr;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const uint32_t row = m0 + (wm * C::TM + i) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-                if (row < M && col < N) y[(size_t)row * N + col] = acc[i][j][r];
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t row = m0 + (wm * C::TM + i) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+                    if (row < M && col < N) y[(size_t)row * units + unit] = swiglu_act(acc[i][j][r], acc[i][j + 1][r]);
+                }
             }
-        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < C::TM; i++)
+#pragma unroll
+            for (int j = 0; j < C::TN; j++) {
+                const uint32_t col = n0 + (wn * C::TN + j) * 32 + fr;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t row = m0 + (wm * C::TM + i) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+                    if (row < M && col < N) y[(size_t)row * N + col] = acc[i][j][r];
+                }
+            }
+    }
 }
 
 // K splits for a grid of `tiles` CTAs over `stages` stages: enough CTAs to cover the chip twice,
@@ -564,7 +585,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restric
     }
 }
 
-template <int KIND, int BM, int BN, int WAVES_M>
+template <int KIND, int BM, int BN, int WAVES_M, bool SWIGLU = false>
 hipError_t run_gemm(hipStream_t s, const GemmArgs &g) {
     const uint32_t mt = (g.M + BM - 1) / BM, nt = (g.N + BN - 1) / BN;
     const uint64_t tiles = (uint64_t)mt * nt;
@@ -572,10 +593,11 @@ hipError_t run_gemm(hipStream_t s, const GemmArgs &g) {
     const uint32_t grid = (uint32_t)((tiles + 7) / 8 * 8);  // an equal share for every XCD
     const uint32_t stages = (g.K / 32 + 1) / 2;
     const uint32_t sp = g.partial ? gemm_splits((uint64_t)mt * nt, stages) : 1;
+    if (SWIGLU && sp != 1) return hipErrorInvalidValue;  // (gemm_swiglu_supported rules it out)
     const uint32_t per = (stages + sp - 1) / sp;
     float *out = sp > 1 ? g.partial : g.y;
-    gemm_kernel<KIND, BM, BN, WAVES_M><<<dim3(grid, sp), 256, 0, s>>>(g.xh, g.xl, g.xsc, g.qs, g.ds, g.b8, g.bsc, out,
-                                                                       g.M, g.K, g.N, mt, nt, per);
+    gemm_kernel<KIND, BM, BN, WAVES_M, SWIGLU><<<dim3(grid, sp), 256, 0, s>>>(g.xh, g.xl, g.xsc, g.qs, g.ds, g.b8, g.bsc,
+                                                                               out, g.M, g.K, g.N, mt, nt, per);
     if (g.defer) *g.defer = sp > 1 ? SplitOut{g.partial, sp} : SplitOut{g.y, 1u};
     if (sp > 1 && !g.defer) {
         const size_t n = (size_t)g.M * g.N;
@@ -593,11 +615,11 @@ void fast_tile(size_t rows, size_t *bm, size_t *bn) {
     *bn = rows <= 32 ? 256 : 128;
 }
 
-template <int KIND>
+template <int KIND, bool SWIGLU = false>
 hipError_t gemm_dispatch(hipStream_t s, const GemmArgs &g) {
-    if (g.M <= 32) return run_gemm<KIND, 32, 256, 1>(s, g);
-    if (g.M <= kMidRows) return run_gemm<KIND, 64, 128, 2>(s, g);
-    return run_gemm<KIND, 128, 128, 2>(s, g);
+    if (g.M <= 32) return run_gemm<KIND, 32, 256, 1, SWIGLU>(s, g);
+    if (g.M <= kMidRows) return run_gemm<KIND, 64, 128, 2, SWIGLU>(s, g);
+    return run_gemm<KIND, 128, 128, 2, SWIGLU>(s, g);
 }
 
 // ---- the precise MFMA GEMM (FH_PATH_TILED): x as two f16 parts, about 22 bits ----
@@ -2774,6 +2796,48 @@ hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uin
     if (x)
         split_x_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
     return gemm_fast_dispatch<FH_Q4_0>(s, g);
+}
+
+// The fast GEMM with SwiGLU in its epilogue (gemm_kernel<..., true>) takes the product when the
+// plain fast product would run on gemm_kernel with one K split: not the streaming kernel, and a
+// tile grid that fills the chip or a K too short to split; n (gate and up) a multiple of 64.
+bool gemm_swiglu_supported(size_t rows, size_t k, size_t n) {
+    if (!rows || n % 64 || !gemm_supported(rows, k, n)) return false;
+    uint32_t ssp = 1;
+    if (stream_fast_plan(rows, k, n, &ssp) && stream_fast_supported(rows, k, n)) return false;
+    size_t bm, bn;
+    fast_tile(rows, &bm, &bn);
+    const uint64_t tiles = (uint64_t)((rows + bm - 1) / bm) * ((n + bn - 1) / bn);
+    return gemm_splits(tiles, (uint32_t)((k / 32 + 1) / 2)) == 1;
+}
+
+hipError_t launch_gemm_swiglu(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
+                              const float *x, float *act, size_t rows, size_t k, size_t n, void *workspace) {
+    if (!gemm_swiglu_supported(rows, k, n)) return hipErrorInvalidValue;
+    const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+    uint8_t *ws = (uint8_t *)workspace;
+    GemmArgs g;
+    g.xh = (const _Float16 *)ws;
+    g.xl = ws + up(rows * k * 2);
+    g.xsc = (const int32_t *)(ws + up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)));
+    g.qs = qs;
+    g.ds = ds;
+    g.b8 = b8;
+    g.bsc = (const int32_t *)(b8 + up(n * ((k + 63) / 64 * 64)));
+    g.y = act;
+    g.partial = nullptr;  // one K split
+    g.M = (uint32_t)rows;
+    g.K = (uint32_t)k;
+    g.N = (uint32_t)n;
+    if (kind == FH_Q8_0) {
+        if (x)
+            split_x_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc,
+                                                                   g.K);
+        return gemm_dispatch<FH_Q8_0, true>(s, g);
+    }
+    if (x)
+        split_x_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
+    return gemm_dispatch<FH_Q4_0, true>(s, g);
 }
 
 // x as f16 (2 bytes per element), the row scales, then the K-split partials, each 256-aligned

@@ -661,7 +661,9 @@ fh_status load_mat(fh_device *dev, const fh_gguf *g, const char *who, const std:
 }
 
 fh_status load_mat_rows(fh_device *dev, const fh_gguf *g, const char *who, const std::string *names,
-                        const size_t *ns, size_t count, size_t k, fh_kind *kind, fh_qweight **out) {
+                        const size_t *ns, size_t count, size_t k, fh_kind *kind, fh_qweight **out, bool interleave) {
+    if (interleave && (count != 2 || ns[0] != ns[1] || ns[0] % 32))
+        return fail(FH_ERR_INVALID, "%s: interleaving needs two parts of equal rows, a multiple of 32", who);
     std::vector<std::pair<const uint8_t *, size_t>> parts(count);
     size_t total = 0, rows = 0;
     for (size_t i = 0; i < count; i++) {
@@ -677,9 +679,18 @@ fh_status load_mat_rows(fh_device *dev, const fh_gguf *g, const char *who, const
         return fail(FH_ERR_OOM, "host out of memory");
     }
     size_t at = 0;
-    for (auto &p : parts) {
-        memcpy(joined.data() + at, p.first, p.second);
-        at += p.second;
+    if (interleave) {  // 32 rows of part 0, 32 of part 1, ... (rows are whole blocks of k)
+        const size_t run = parts[0].second / (ns[0] / 32);
+        for (size_t c = 0; c < ns[0] / 32; c++)
+            for (auto &p : parts) {
+                memcpy(joined.data() + at, p.first + c * run, run);
+                at += run;
+            }
+    } else {
+        for (auto &p : parts) {
+            memcpy(joined.data() + at, p.first, p.second);
+            at += p.second;
+        }
     }
     return fh_qweight_upload_gguf(dev, *kind, joined.data(), total, k, rows, out);
 }

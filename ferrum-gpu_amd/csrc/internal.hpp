@@ -114,9 +114,11 @@ fh_status load_vec(fh_device *dev, const fh_gguf *g, const char *who, const std:
 fh_status load_mat(fh_device *dev, const fh_gguf *g, const char *who, const std::string &name, size_t k, size_t n,
                    fh_kind *kind, fh_qweight **out);
 // Several matrices of k inputs stacked into one weight: the rows of names[0] (ns[0] of them),
-// then those of names[1], ... (a fused projection).
+// then those of names[1], ... (a fused projection). interleave (two parts of equal rows, a multiple
+// of 32): runs of 32 rows alternate between the parts instead (gemm_kernel's SwiGLU epilogue).
 fh_status load_mat_rows(fh_device *dev, const fh_gguf *g, const char *who, const std::string *names,
-                        const size_t *ns, size_t count, size_t k, fh_kind *kind, fh_qweight **out);
+                        const size_t *ns, size_t count, size_t k, fh_kind *kind, fh_qweight **out,
+                        bool interleave = false);
 
 // ---- kernel launchers (on dev->stream; a command may issue several) ----
 // codec.hip
@@ -262,6 +264,12 @@ hipError_t launch_make_b8(hipStream_t s, fh_kind kind, const uint8_t *qs, const 
 hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
                        const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace,
                        SplitOut *defer = nullptr, float *partial = nullptr);
+// The fast GEMM with SwiGLU fused into its epilogue: the weight's n rows are gate and up
+// interleaved in runs of 32 (load_mat_rows with interleave), act gets rows x n / 2 activations
+// (swiglu_act). Only where gemm_swiglu_supported; x null: the split x is already in the workspace.
+bool gemm_swiglu_supported(size_t rows, size_t k, size_t n);
+hipError_t launch_gemm_swiglu(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
+                              const float *x, float *act, size_t rows, size_t k, size_t n, void *workspace);
 // Where the fast GEMM's split x lives in its workspace: hi (rows x k f16), lo (rows x k rounded
 // up to 64, e4m3), one scale word per row.
 struct GemmXSplit {

@@ -72,6 +72,9 @@ struct fh_llama {
     std::vector<Layer> blocks;
     Mat tok, head;  // head is tok's copy when tied
     bool packed = true;  // every block matrix packed (the fast path's fused producers need it)
+    // the gate/up weights interleaved in runs of 32 rows for gemm_kernel's SwiGLU epilogue (the fast
+    // path with every block matrix packed, unless FERRUM_HIP_SWIGLU_UNFUSED=1 at load)
+    bool gu_inter = false;
     fh_buffer *out_norm = nullptr, *rope_cos = nullptr, *rope_sin = nullptr;
     uint64_t weight_bytes = 0;
     // Activations for up to `rows` rows, grown on demand and kept.
@@ -341,7 +344,10 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float *__restrict__ 
                          dst.xsc, red2);
 }
 
-template <int KIND>
+// INTER: gu's columns are gate and up interleaved in runs of 32 (the weight loaded for the
+// SwiGLU epilogue, when a product's shape does not take that epilogue): unit j's gate at column
+// 64 (j / 32) + j % 32, its up 32 columns later.
+template <int KIND, bool INTER = false>
 __global__ __launch_bounds__(256) void swiglu_split_kernel(const float *__restrict__ gu, uint32_t hid, GemmXSplit dst) {
     extern __shared__ __attribute__((aligned(16))) float hrow[];
     __shared__ float red[4];
@@ -350,17 +356,20 @@ __global__ __launch_bounds__(256) void swiglu_split_kernel(const float *__restri
     auto act = [&](uint32_t j, f32x4 gg, f32x4 u) {
         f32x4 y;
 #pragma unroll
-        for (int c = 0; c < 4; c++) y[c] = __fmul_rn(gg[c] / (1.0f + expf(-gg[c])), u[c]);
+        for (int c = 0; c < 4; c++) y[c] = swiglu_act(gg[c], u[c]);
         *(f32x4 *)&hrow[4 * j] = y;
     };
+    // units 4j .. 4j + 3: their gate columns (up: + hid, or + 32 when interleaved)
+    auto gcol = [&](uint32_t j) { return INTER ? 64 * (4 * j / 32) + (4 * j) % 32 : 4 * j; };
+    const uint32_t uoff = INTER ? 32 : hid;
     // the row's first kKeepRow chunks are all requested before any is used (one round trip)
     f32x4 gk[kKeepRow], uk[kKeepRow];
 #pragma unroll
     for (int i = 0; i < kKeepRow; i++) {
         if (256u * i >= nq) continue;  // the workgroup agrees
         const uint32_t j = min(threadIdx.x + 256 * i, nq - 1);
-        gk[i] = *(const f32x4 *)(gu + r * 2 * hid + 4 * j);
-        uk[i] = *(const f32x4 *)(gu + r * 2 * hid + hid + 4 * j);
+        gk[i] = *(const f32x4 *)(gu + r * 2 * hid + gcol(j));
+        uk[i] = *(const f32x4 *)(gu + r * 2 * hid + uoff + gcol(j));
     }
 #pragma unroll
     for (int i = 0; i < kKeepRow; i++) {
@@ -368,7 +377,7 @@ __global__ __launch_bounds__(256) void swiglu_split_kernel(const float *__restri
         if (256u * i < nq && j < nq) act(j, gk[i], uk[i]);
     }
     for (uint32_t j = threadIdx.x + 256 * kKeepRow; j < nq; j += 256)
-        act(j, *(const f32x4 *)(gu + r * 2 * hid + 4 * j), *(const f32x4 *)(gu + r * 2 * hid + hid + 4 * j));
+        act(j, *(const f32x4 *)(gu + r * 2 * hid + gcol(j)), *(const f32x4 *)(gu + r * 2 * hid + uoff + gcol(j)));
     __syncthreads();
     split_row_fast<KIND>([&](uint32_t q) { return *(const f32x4 *)&hrow[4 * q]; }, (uint32_t)r, hid, dst.xh, dst.xl,
                          dst.xsc, red);
@@ -895,7 +904,7 @@ __global__ __launch_bounds__(256) void swiglu_scalar_kernel(const float *__restr
         const size_t r = i / hid, j = i % hid;
         const float g = split_sum(gu, r * 2 * hid + j, gu_splits, gu_stride);
         const float u = split_sum(gu, r * 2 * hid + hid + j, gu_splits, gu_stride);
-        act[i] = __fmul_rn(g / (1.0f + expf(-g)), u);
+        act[i] = swiglu_act(g, u);
     }
 }
 
@@ -914,7 +923,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float *__restrict__ g
         const f32x4 u = load4(r * 2 * hid + hid + 4 * j);
         f32x4 y;
 #pragma unroll
-        for (int c = 0; c < 4; c++) y[c] = __fmul_rn(g[c] / (1.0f + expf(-g[c])), u[c]);
+        for (int c = 0; c < 4; c++) y[c] = swiglu_act(g[c], u[c]);
         *(f32x4 *)(act + r * hid + 4 * j) = y;
     }
 }
@@ -1338,13 +1347,25 @@ hipError_t enqueue_body(fh_llama *m, hipStream_t s, size_t t) {
         if ((e = launch_attention(m, s, t, qkv, fp(L.bqkv)))) break;
         if ((e = linear(m, s, L.wo, m->att, m->o, t, &att))) break;
         norm(true, L.ffn_norm, att);
-        if (fused) {
+        if (fused && m->gu_inter && gemm_swiglu_supported(t, d, 2 * m->hidden)) {
+            // SwiGLU in the gate/up product's epilogue (interleaved weight): the activation goes to
+            // act, whose split the down product makes itself
+            const fh_qweight *w = L.wgu.q;
+            if ((e = launch_gemm_swiglu(s, w->kind, w->qs, w->ds, w->b8, nullptr, m->act, t, w->k, w->n, m->ws))) break;
+            if ((e = linear(m, s, L.down, m->act, m->o, t, &down))) break;
+        } else if (fused) {
             // (gate/up reduced in place: SwiGLU's split x would overwrite its partial sums)
             if ((e = linear(m, s, L.wgu, nullptr, m->gu, t))) break;
-            if (m->kind == FH_Q8_0)
+            if (m->gu_inter) {
+                if (m->kind == FH_Q8_0)
+                    swiglu_split_kernel<FH_Q8_0, true><<<T, 256, m->hidden * 4, s>>>(m->gu, (uint32_t)m->hidden, xh);
+                else
+                    swiglu_split_kernel<FH_Q4_0, true><<<T, 256, m->hidden * 4, s>>>(m->gu, (uint32_t)m->hidden, xh);
+            } else if (m->kind == FH_Q8_0) {
                 swiglu_split_kernel<FH_Q8_0><<<T, 256, m->hidden * 4, s>>>(m->gu, (uint32_t)m->hidden, xh);
-            else
+            } else {
                 swiglu_split_kernel<FH_Q4_0><<<T, 256, m->hidden * 4, s>>>(m->gu, (uint32_t)m->hidden, xh);
+            }
             if ((e = linear(m, s, L.down, nullptr, m->o, t, &down))) break;
         } else {
             if ((e = linear(m, s, L.wgu, m->h, m->gu, t, &gu))) break;
@@ -1418,7 +1439,7 @@ hipError_t enqueue_score(fh_llama *m, hipStream_t s, size_t t, float *out) {
 // llama/lin.rs:30-62: a width that is not whole 32-blocks stays f32; the GGUF writer stores such
 // matrices as F32, ferrum_model/src/gguf/quant.rs:57-69).
 fh_status load_lin(fh_device *dev, const fh_gguf *g, const std::string *names, const size_t *ns, size_t count,
-                   size_t k, fh_kind *kind, fh_llama::Mat *out) {
+                   size_t k, fh_kind *kind, fh_llama::Mat *out, bool interleave = false) {
     bool packed = true;
     size_t n = 0;
     for (size_t i = 0; i < count; i++) {
@@ -1435,7 +1456,7 @@ fh_status load_lin(fh_device *dev, const fh_gguf *g, const std::string *names, c
     out->n = n;
     if (packed)
         return count == 1 ? load_mat(dev, g, "llama", names[0], k, n, kind, &out->q)
-                          : load_mat_rows(dev, g, "llama", names, ns, count, k, kind, &out->q);
+                          : load_mat_rows(dev, g, "llama", names, ns, count, k, kind, &out->q, interleave);
     fh_status st = fh_buffer_zeros(dev, k * n, &out->f);
     size_t at = 0;
     for (size_t i = 0; i < count && !st; i++) {
@@ -1557,6 +1578,23 @@ fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_
         return llama_fail_free(m, fail(FH_ERR_INVALID, "tensor 'output.bias' is not supported"));
     if ((st = load_vec(dev, g, "llama", "output_norm.weight", d, &m->out_norm))) return llama_fail_free(m, st);
     m->blocks.resize(m->layers);
+    {  // every block matrix stored Q8_0 / Q4_0 (what the fused producers need): then interleave gate / up
+        bool all = true;
+        for (size_t l = 0; l < m->layers && all; l++)
+            for (const char *stem : {"attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight",
+                                     "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"}) {
+                fh_gguf_tensor ti;
+                const std::string nm = tensor_name("blk.", l, stem);
+                if (fh_gguf_find_tensor(g, nm.c_str(), &tidx) != FH_OK || fh_gguf_tensor_info(g, tidx, &ti) != FH_OK ||
+                    (ti.ggml_type != FH_Q8_0 && ti.ggml_type != FH_Q4_0)) {
+                    all = false;
+                    break;
+                }
+            }
+        const char *sw = getenv("FERRUM_HIP_SWIGLU_UNFUSED");
+        m->gu_inter = all && path == FH_PATH_TILED_FAST && hid % 32 == 0 && d <= 16384 && hid <= 16384 &&
+                      !(sw && sw[0] == '1');
+    }
     for (size_t l = 0; l < m->layers; l++) {
         auto &L = m->blocks[l];
         auto n = [&](const char *s) { return tensor_name("blk.", l, s); };
@@ -1573,7 +1611,7 @@ fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_
             (st = load_lin(dev, g, qkv, qkv_n, 3, d, &kind, &L.wqkv)) ||
             (st = load_lin(dev, g, n("attn_output.weight"), qd, d, &kind, &L.wo)) ||
             (st = load_vec(dev, g, "llama", n("ffn_norm.weight"), d, &L.ffn_norm)) ||
-            (st = load_lin(dev, g, gu, gu_n, 2, d, &kind, &L.wgu)) ||
+            (st = load_lin(dev, g, gu, gu_n, 2, d, &kind, &L.wgu, m->gu_inter)) ||
             (st = load_lin(dev, g, n("ffn_down.weight"), hid, d, &kind, &L.down)))
             return llama_fail_free(m, st);
         m->packed = m->packed && L.wqkv.q && L.wo.q && L.wgu.q && L.down.q;

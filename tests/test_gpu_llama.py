@@ -235,6 +235,51 @@ def test_score_epilogue_matches_the_logits_and_score_kernel(fh, g, orc, path):
         assert np.array_equal(hit, whit)
 
 
+def load_env(fh, g, data, path, var):
+    """The model loaded with environment variable `var` set to 1 (a load-time switch)."""
+    old = os.environ.get(var)
+    os.environ[var] = "1"
+    try:
+        return load(fh, g, data, path)
+    finally:
+        if old is None:
+            os.environ.pop(var)
+        else:
+            os.environ[var] = old
+
+
+@pytest.mark.parametrize("shape", ["epilogue", "fallback"])
+def test_swiglu_epilogue_is_bit_identical_to_the_swiglu_pass(fh, g, orc, shape):
+    """The fast path's SwiGLU in the gate/up GEMM's epilogue (gate and up rows interleaved in runs
+    of 32 at load) against the same model loaded with FERRUM_HIP_SWIGLU_UNFUSED=1 (the stacked
+    product, then swiglu_split_kernel): the same accumulators and the same activation function,
+    so logits and log-probabilities bit-identical. "epilogue": d 64 (one pipeline stage, never
+    split along K), so the epilogue runs. "fallback": d 512 with 16 tiles, which the GEMM splits
+    along K, so the interleaved weight goes through the plain product and the interleave-aware
+    SwiGLU pass instead."""
+    if shape == "epilogue":
+        c = cfg(vocab=500, ctx=256, dim=64, heads=4, kv_heads=2, head_dim=16, hidden=256, rope_dim=16)
+        n_ids = 201
+    else:
+        c = cfg(vocab=500, ctx=256, dim=512, heads=8, kv_heads=4, head_dim=64, hidden=512, rope_dim=64)
+        n_ids = 101
+    data = lm.to_gguf(lm.llama_random(c, 17, True, False), lm.Q4_0)
+    fused = load(fh, g, data, fh.QPath.TiledFast)
+    plain = load_env(fh, g, data, fh.QPath.TiledFast, "FERRUM_HIP_SWIGLU_UNFUSED")
+    ids = [int(t) for t in np.random.default_rng(8).integers(0, 500, n_ids)]
+    lf, lp = fused.forward_all(ids), plain.forward_all(ids)
+    assert np.all(np.isfinite(lf))
+    same = np.array_equal(np.asarray(lf, np.float32).view(np.uint32), np.asarray(lp, np.float32).view(np.uint32))
+    sf, hf = fused.score_arrays(ids)
+    sp, hp = plain.score_arrays(ids)
+    wlp, _ = orc.llama_score(lm.from_gguf(data), ids)
+    say(f"{shape}: logits bit-identical {same}; log-probs vs oracle {lp_err(sf, wlp):.2e}")
+    assert same
+    assert np.array_equal(np.asarray(sf, np.float32).view(np.uint32), np.asarray(sp, np.float32).view(np.uint32))
+    assert np.array_equal(hf, hp)
+    assert lp_err(sf, wlp) < FAST_LOGPROB
+
+
 @pytest.fixture(scope="module")
 def qwen(fh, g):
     """The scoring benchmark's model: Qwen2-0.5B shapes (24 layers, d 896, FFN 4864, 14 q / 2 kv
