@@ -618,6 +618,17 @@ struct SplitDst {
     int8_t *eq, *ek, *ev;
 };
 
+// The exponent e of one (row, head) of the split operands, from the head's values v[i] (dim lane
+// + 64 i) over the wavefront: 2^E <= max |v| < 2^(E+1), e = E - 14; zero rows, padding rows and
+// non-finite rows keep e = 0 (non-finite values then stay non-finite).
+__device__ __forceinline__ int head_exponent(const float (&v)[2]) {
+    float mx = fmaxf(fabsf(v[0]), fabsf(v[1]));
+    mx = wave_reduce(mx, MaxOp());
+    int e = 0;
+    if (mx > 0.0f && mx <= 3.4028235e38f) e = ((int)(__float_as_uint(mx) >> 23) - 127) - 14;
+    return e < -100 ? -100 : (e > 100 ? 100 : e);
+}
+
 // Row `row` of every q, k and v head into its split form, one head per wavefront at a time;
 // get(slot, d) is element d of head slot (q heads, then k heads, then v heads) of the row.
 template <int HD, class Get>
@@ -632,13 +643,7 @@ __device__ __forceinline__ void split_heads(Get get, const SplitDst &o, uint32_t
             const uint32_t d = lane + 64 * i;
             v[i] = row < t && d < (uint32_t)HD ? get(slot, d) : 0.0f;
         }
-        float mx = fmaxf(fabsf(v[0]), fabsf(v[1]));
-        mx = wave_reduce(mx, MaxOp());
-        // 2^E <= mx < 2^(E+1), e = E - 14; zero rows, padding rows and non-finite rows keep e = 0
-        // (non-finite values then stay non-finite) and padding rows report -127
-        int e = 0;
-        if (mx > 0.0f && mx <= 3.4028235e38f) e = ((int)(__float_as_uint(mx) >> 23) - 127) - 14;
-        e = e < -100 ? -100 : (e > 100 ? 100 : e);
+        const int e = head_exponent(v);  // padding rows report kSplitPad
         const float f = ldexpf(1.0f, -e);
         const int8_t code = row < t ? (int8_t)e : (int8_t)kSplitPad;
 #pragma unroll
@@ -683,30 +688,93 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const float *__restrict
                     tp, heads, kv_heads);
 }
 
-// qkv_rope_kernel and attn_split_kernel in one pass: row `row` of the QKV product (its K-split
-// partial sums and the bias) into LDS, RoPE into a second LDS row (rope_value, the same
-// roundings), then the row's split operands; the f32 q, k and v are not written. One workgroup
-// per row of tp; dynamic LDS 2 width floats.
-template <int HD>
+// qkv_rope_kernel and attn_split_kernel in one pass, per R-row tile of tp (R = 16 or 32) and head
+// slot (q heads, then k heads, then v heads): the tile's rows of the slot (the QKV product's
+// K-split partial sums in split order, then the bias) into LDS; per row, RoPE (rope_value, the same
+// roundings) and the split as split_heads, assembled in LDS in the destination's order (q' rows,
+// or the tile's part of a 32-key fragment block of k' or v', whose keys 0-15 and 16-31 fill
+// separate 128-byte lines); then 16-byte stores, so each destination line is written whole by one
+// workgroup. The f32 q, k and v are not written. Grid (tp / R, heads + 2 kv_heads); rows t .. tp - 1
+// are written as zeros.
+template <int HD, int R>
 __global__ __launch_bounds__(256) void qkv_rope_split_kernel(const float *__restrict__ src, uint32_t src_splits,
                                                              size_t src_stride, const float *__restrict__ bias,
                                                              const float *__restrict__ cos_t,
                                                              const float *__restrict__ sin_t, SplitDst o, uint32_t t,
                                                              uint32_t tp, uint32_t width, uint32_t heads,
                                                              uint32_t kv_heads, uint32_t rope_dim, int neox) {
-    extern __shared__ __attribute__((aligned(16))) float row[];
-    float *rot = row + (width + 3) / 4 * 4;
-    const uint32_t r = blockIdx.x;
-    if (r < t) {  // (uniform over the workgroup)
-        qkv_rope_row(src, src_splits, src_stride, bias, width, r, row);
-        __syncthreads();
-        const uint32_t half = rope_dim / 2;
-        const float *cr = cos_t + (size_t)r * half, *sr = sin_t + (size_t)r * half;
-        for (uint32_t c = threadIdx.x; c < width; c += 256)
-            rot[c] = rope_value(row, c, cr, sr, (heads + kv_heads) * HD, HD, rope_dim, neox);
-        __syncthreads();
+    static_assert(R == 16 || R == 32, "tiles of half or whole 32-key fragment blocks");
+    constexpr uint32_t C4 = HD / 4, C8 = HD / 8;  // float4 chunks and 8-half chunks per row of a head
+    __shared__ __attribute__((aligned(16))) float tile[R][HD];
+    __shared__ __attribute__((aligned(16))) _Float16 part[2][32 * HD];  // hi and lo, destination order
+    const uint32_t r0 = blockIdx.x * R, slot = blockIdx.y, tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const uint32_t kind = slot < heads ? 0u : slot < heads + kv_heads ? 1u : 2u;  // q, k, v
+    const uint32_t k0 = r0 % 32;  // the tile's first key in its fragment block
+    for (uint32_t q = tid; q < R * C4; q += 256) {
+        const uint32_t rr = q / C4, c = q % C4, r = r0 + rr;
+        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (r < t) {
+            v = split_chunk(src, (size_t)r * width + slot * HD + 4 * c, src_splits, src_stride);
+            if (bias) v = v + *(const f32x4 *)(bias + slot * HD + 4 * c);
+        }
+        *(f32x4 *)&tile[rr][4 * c] = v;
     }
-    split_heads<HD>([&](uint32_t slot, uint32_t d) { return rot[slot * HD + d]; }, o, r, t, tp, heads, kv_heads);
+    __syncthreads();
+    const uint32_t half = rope_dim / 2;
+    for (uint32_t i = 0; i < R / 4; i++) {
+        const uint32_t rr = wave * (R / 4) + i, r = r0 + rr;
+        float v[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const uint32_t d = lane + 64 * u;
+            v[u] = r < t && d < HD ? rope_value(tile[rr], d, cos_t + (size_t)r * half, sin_t + (size_t)r * half,
+                                                kind < 2 ? HD : 0u, HD, rope_dim, neox)
+                                   : 0.0f;
+        }
+        const int e = head_exponent(v);
+        const float f = ldexpf(1.0f, -e);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const uint32_t d = lane + 64 * u;
+            if (d >= HD) continue;
+            const float x = v[u] * f;
+            const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
+            const size_t at =
+                kind == 0 ? rr * HD + d : kind == 1 ? frag_k<HD>(0, k0 + rr, d, 32) : frag_v<HD>(0, k0 + rr, d, 32);
+            part[0][at] = hi;
+            part[1][at] = lo;
+        }
+        if (lane == 0) {
+            const int8_t code = r < t ? (int8_t)e : (int8_t)kSplitPad;
+            if (kind == 0)
+                o.eq[(size_t)slot * tp + r] = code;
+            else if (kind == 1)
+                o.ek[(size_t)(slot - heads) * tp + r] = code;
+            else
+                o.ev[(size_t)(slot - heads - kv_heads) * tp + r] = code;
+        }
+    }
+    __syncthreads();
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    for (uint32_t c = tid; c < R * C8; c += 256) {
+        // chunk c's place among the 8-half chunks of the q' tile or of the 32-key block: a 16-key
+        // tile holds, of k', lanes k0 .. k0 + 15 and 32 + k0 .. of each 16-dim slab (key_row keeps
+        // bit 4), and of v', the u = k0 / 16 halves of each 32-dim part
+        uint32_t ch = c;
+        if (R == 16 && kind == 1) ch = c / 32 * 64 + (c % 32 < 16 ? k0 + c % 32 : 32 + k0 + c % 32 - 16);
+        if (R == 16 && kind == 2) ch = (c / 64 * 2 + k0 / 16) * 64 + c % 64;
+        const h8 a = *(const h8 *)&part[0][8 * ch], b = *(const h8 *)&part[1][8 * ch];
+        if (kind == 0) {
+            const size_t at = (size_t)(r0 + c / C8) * (heads * HD) + slot * HD + 8 * (c % C8);
+            *(h8 *)(o.qh + at) = a;
+            *(h8 *)(o.ql + at) = b;
+        } else {
+            const uint32_t g = kind == 1 ? slot - heads : slot - heads - kv_heads;
+            const size_t at = ((size_t)g * (tp / 32) + r0 / 32) * (32 * HD) + 8 * ch;
+            *(h8 *)((kind == 1 ? o.kh : o.vh) + at) = a;
+            *(h8 *)((kind == 1 ? o.kl : o.vl) + at) = b;
+        }
+    }
 }
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -1258,10 +1326,10 @@ hipError_t linear(const fh_llama *m, hipStream_t s, const fh_llama::Mat &mat, co
 }
 
 // RoPE (with the q/k/v bias and the QKV product's K-split partial sums) and the attention of t
-// rows. The split attention's head dims take qkv_rope_split_kernel when two rows of qkv fit in
-// 64 KB of LDS (the f32 q, k, v are then never written), else (or when the model was loaded
-// with FERRUM_HIP_ROPE_UNFUSED=1) qkv_rope_kernel and attn_split_kernel, with the same results;
-// the other head dims qkv_rope_kernel and the f32 attention_kernel.
+// rows. The split attention's head dims take qkv_rope_split_kernel (the f32 q, k, v are then
+// never written), or, when the model was loaded with FERRUM_HIP_ROPE_UNFUSED=1, qkv_rope_kernel
+// and attn_split_kernel, with the same results; the other head dims qkv_rope_kernel and the f32
+// attention_kernel.
 hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t, const SplitOut &qkv, const float *bias) {
     const dim3 grid((unsigned)m->heads, (unsigned)((t + 31) / 32));
     const uint32_t w = (uint32_t)m->qkv_width(), group = (uint32_t)(m->heads / m->kv_heads);
@@ -1269,19 +1337,25 @@ hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t, const Sp
     const uint32_t T = (uint32_t)t, H = (uint32_t)m->heads, KV = (uint32_t)m->kv_heads;
     const uint32_t hd = (uint32_t)m->head_dim, rd = (uint32_t)m->rope_dim;
     const int neox = m->neox ? 1 : 0;
-    const size_t fused_lds = 2 * ((size_t)(w + 3) / 4 * 4) * 4;
     const float *cos_t = fp(m->rope_cos), *sin_t = fp(m->rope_sin);
-    const bool fused = m->fuse_rope && split_attention(m) && fused_lds <= 65536;
+    const bool fused = m->fuse_rope && split_attention(m);
     if (!fused)
         qkv_rope_kernel<<<T, 256, w * 4, s>>>(qkv.part, qkv.splits, t * w, m->qkv, bias, cos_t, sin_t, w,
                                               H + KV, hd, rd, neox);
     if (split_attention(m)) {
         const uint32_t tp = (T + 31) / 32 * 32;
         const SplitDst o{m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl, m->seq, m->sek, m->sev};
+        // 16-row tiles while 32-row ones would give fewer than two workgroups per CU
+        const bool small = (size_t)(tp / 32) * (H + 2 * KV) < 512;
 #define FH_SPLIT_ATTN(HD, W)                                                                                      \
-    if (fused)                                                                                                    \
-        qkv_rope_split_kernel<HD><<<tp, 256, fused_lds, s>>>(qkv.part, qkv.splits, t * w, bias, cos_t, sin_t, o, \
-                                                             T, tp, w, H, KV, rd, neox);                          \
+    if (fused && small)                                                                                           \
+        qkv_rope_split_kernel<HD, 16><<<dim3(tp / 16, H + 2 * KV), 256, 0, s>>>(qkv.part, qkv.splits, t * w,     \
+                                                                                bias, cos_t, sin_t, o, T, tp, w,  \
+                                                                                H, KV, rd, neox);                 \
+    else if (fused)                                                                                               \
+        qkv_rope_split_kernel<HD, 32><<<dim3(tp / 32, H + 2 * KV), 256, 0, s>>>(qkv.part, qkv.splits, t * w,     \
+                                                                                bias, cos_t, sin_t, o, T, tp, w,  \
+                                                                                H, KV, rd, neox);                 \
     else                                                                                                          \
         attn_split_kernel<HD><<<tp, 256, 0, s>>>(m->qkv, o, T, tp, w, H, KV);                                     \
     attention_split_kernel<HD, W><<<grid, 64 * W, 0, s>>>(m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl, m->seq, \

@@ -325,18 +325,20 @@ def test_qwen2_0_5b_scoring_matches_the_oracle(fh, g, orc, qwen, path):
     assert lp_err(lp512[:128], wlp) < bound and lp_err(lp2048[:512], lp512) < bound
 
 
-@pytest.mark.parametrize("head_dim", [32, 64, 128])
-def test_split_attention_head_dims_match_the_oracle(fh, g, orc, head_dim):
+@pytest.mark.parametrize("head_dim,neox,rope_dim", [(32, True, None), (64, True, None), (128, True, None),
+                                                     (64, False, 32)])
+def test_split_attention_head_dims_match_the_oracle(fh, g, orc, head_dim, neox, rope_dim):
     """Head dims 32, 64 and 128 take the f16-split attention (q, k, v on a power-of-two scale in
     two f16 parts, k and v stored in the kernel's fragment order); grouped kv heads, sequence
     lengths that leave some wavefronts without a key tile (1, 33) and span several query blocks
-    and key tiles with a ragged last one (97). Logits against the oracle within SCORE (1e-4
+    and key tiles with a ragged last one (97); NEOX pairing over the whole head, and NORM pairing
+    over half of it (rope_dim 32 of 64). Logits against the oracle within SCORE (1e-4
     relative to max(|w|, 1)), not FORWARD: at these widths (dim 128 to 512, logits up to 26) the
     f32 oracle is itself 1.2e-5 to 4.3e-5 from an f64 evaluation of the same model (measured), so
     1e-5 would test the oracle's rounding. A misplaced fragment element gives O(1) errors and an
     f16-only operand (the lo part lost) errors of the order of f16 rounding, 2^-11 = 4.9e-4."""
     c = lm.config(vocab=300, ctx=128, dim=4 * head_dim, heads=4, kv_heads=2, head_dim=head_dim, layers=2,
-                  hidden=256, rope_base=10000.0, neox=True, eps=1e-5)
+                  hidden=256, rope_dim=rope_dim, rope_base=10000.0, neox=neox, eps=1e-5)
     data = lm.to_gguf(lm.llama_random(c, 17, True, False), lm.Q8_0)
     ref = lm.from_gguf(data)
     dev = load(fh, g, data)
@@ -353,6 +355,28 @@ def test_split_attention_head_dims_match_the_oracle(fh, g, orc, head_dim):
         say(f"head_dim {head_dim} t={t}: {e:.2e}")
         assert e < SCORE, (head_dim, t, e)
         assert np.array_equal(got, two.forward_all(ids[:t])), (head_dim, t)
+
+
+def test_rope_split_tiles_are_bit_identical_to_the_two_pass_split(fh, g):
+    """qkv_rope_split_kernel takes 32-row tiles when they give at least two workgroups per CU
+    (here 8 head slots x 64 tiles at t = 2048) and 16-row tiles below that (t = 1000, ragged):
+    each writes whole k' and v' fragment lines from one workgroup. Both against the two-pass
+    RoPE and split (FERRUM_HIP_ROPE_UNFUSED=1), logits bit for bit. dim 1024 against 4 heads of 64
+    splits the QKV product along K at both lengths, so the tiles add partial sums."""
+    c = lm.config(vocab=300, ctx=2048, dim=1024, heads=4, kv_heads=2, head_dim=64, layers=2, hidden=256,
+                  rope_base=10000.0, neox=False, eps=1e-5)
+    data = lm.to_gguf(lm.llama_random(c, 23, True, False), lm.Q8_0)
+    dev = load(fh, g, data, fh.QPath.TiledFast)
+    os.environ["FERRUM_HIP_ROPE_UNFUSED"] = "1"
+    try:
+        two = load(fh, g, data, fh.QPath.TiledFast)
+    finally:
+        del os.environ["FERRUM_HIP_ROPE_UNFUSED"]
+    ids = [int(t) for t in np.random.default_rng(5).integers(0, 300, 2048)]
+    for t in (2048, 1000):
+        got = dev.forward_all(ids[:t])
+        assert np.all(np.isfinite(got)), t
+        assert np.array_equal(got, two.forward_all(ids[:t])), t
 
 
 @pytest.mark.parametrize("kind", [lm.Q8_0, lm.Q4_0])
