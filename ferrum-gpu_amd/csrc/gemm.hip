@@ -17,16 +17,16 @@
 // + lo with hi in f16 and lo kept as e4m3 (about 15 bits in all). Per tile and block two f16
 // MFMAs on hi; per two blocks one v_mfma_scale_f32_32x32x64_f8f6f4 on lo times the weights'
 // e4m3 correction operand (d * q per element, made once per weight by make_b8_kernel), whose
-// two power-of-two row / column scales the instruction applies itself, so the correction
-// accumulates over all of K with no per-block work. That is 1.5 f16-equivalent passes instead
-// of 2. split_x_kernel prepares hi, lo and the row scales.
+// power-of-two scales (x lo: per row and 32-element block; the operand: per column) the
+// instruction applies itself, so the correction accumulates over all of K with no per-block work.
+// That is 1.5 f16-equivalent passes instead of 2. split_x_kernel prepares hi, lo and the scales
+// (the layouts are in xsplit.hpp).
 //
-// k order inside a block (f16 operands). The unpack produces f16 pairs from a quant dword w: for
-// Q8_0 the bytes (0, 2) and (1, 3), i.e. elements 4i + {0, 2, 1, 3}; for Q4_0 the low nibbles of
-// bytes (0, 2), (1, 3), then the high nibbles, i.e. elements 4i + {0, 2, 1, 3} and 16 + 4i +
-// {0, 2, 1, 3}. The MFMA sums over k, so x is laid out in that same order and no shuffle is
-// needed. The fp8 operands use the natural k order on both sides (the instruction pairs lane
-// (row, half h) byte j of A with lane (column, half h) byte j of B).
+// k order inside a block (f16 operands): fast_elem_of_pos (xsplit.hpp), the order the quant
+// unpack produces. The MFMA sums over k, so x is laid out in that same order and no shuffle is
+// needed. The fp8 operands use the pair order of lo_byte (xsplit.hpp) on both sides (the
+// instruction pairs lane (row, half h) byte j of A with lane (column, half h) byte j of B, and
+// takes bytes 0-15 of every lane as the first scale block, bytes 16-31 as the second).
 //
 // Tile order (fast kernel): CTAs are dealt round-robin to the 8 XCDs, and each XCD works through
 // whole 8 x 8 super-tiles, so the CTAs that run together share stripes of x and of the weights.
@@ -101,30 +101,17 @@ __global__ __launch_bounds__(256) void naive_kernel(const uint8_t *__restrict__ 
     y[idx] = acc;
 }
 
-// ---- the k order of a block (position p of the MFMA operands holds element elem(p)) ----
-template <int KIND>
-__device__ __forceinline__ int elem_of_pos(int p) {
-    const int sw = (p & 3) == 1 ? 2 : (p & 3) == 2 ? 1 : (p & 3);  // {0, 2, 1, 3}
-    if constexpr (KIND == FH_Q8_0) {
-        return (p & ~3) + sw;
-    } else {
-        const int i = p / 8, j = p % 8;
-        return (j < 4 ? 4 * i : 16 + 4 * i) + sw;
-    }
-}
-
 // ---- x -> hi (f16, per block in operand order) and the fp8 correction (split_row_fast) ----
-// One workgroup per row m.
+// One workgroup per row m (the grid: the M rows).
 template <int KIND>
 __global__ __launch_bounds__(256) void split_x_kernel(const float *__restrict__ x, _Float16 *__restrict__ xh,
-                                                      uint8_t *__restrict__ xl, int32_t *__restrict__ xsc, uint32_t K) {
-    __shared__ float red[4];
+                                                      uint8_t *__restrict__ xl, uint8_t *__restrict__ xsb, uint32_t K) {
     const f32x4 *xr = (const f32x4 *)(x + (size_t)blockIdx.x * K);
-    split_row_fast<KIND>([&](uint32_t q) { return xr[q]; }, blockIdx.x, K, xh, xl, xsc, red);
+    split_row_fast<KIND>([&](uint32_t q) { return xr[q]; }, blockIdx.x, gridDim.x, K, xh, xl, xsb);
 }
 
-// ---- the weights' fp8 correction operand: e4m3 of d * q * 2^t per element, natural k order, ----
-// ---- rows of K rounded up to 64 (zero tail) ----
+// ---- the weights' fp8 correction operand: e4m3 of d * q * 2^t per element in the pair order ----
+// ---- of x lo (lo_byte), rows of K rounded up to 64 (an odd block count's last pair ends in zeros) ----
 // One wavefront per weight row n (an output column of y): 2^t puts the row's largest |d q| just
 // under 2^8; bsc[n] holds the E8M0 byte of 2^-t (four copies). Built once per weight.
 template <int KIND>
@@ -134,7 +121,7 @@ __global__ __launch_bounds__(256) void make_b8_kernel(const uint8_t *__restrict_
     const uint32_t n = blockIdx.x * 4 + threadIdx.x / 64, lane = threadIdx.x % 64, nb = K / 32;
     const uint32_t K64 = (K + 63) / 64 * 64;
     if (n >= N) return;  // whole wavefront
-    if (K64 != K && lane < 2) *(u32x4 *)(b8 + (size_t)n * K64 + K + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+    if (nb % 2 && lane < 2) *(u32x4 *)(b8 + (size_t)n * K64 + lo_byte(nb, 16 * lane)) = u32x4{0u, 0u, 0u, 0u};
     float dm = 0.0f;
     for (uint32_t b = lane; b < nb; b += 64) dm = fmaxf(dm, fabsf(half_bits_to_float(ds[scale_slot(n, b, nb)])));
 #pragma unroll
@@ -165,7 +152,7 @@ __global__ __launch_bounds__(256) void make_b8_kernel(const uint8_t *__restrict_
             }
             o[w] = fp8x4(d * e[0], d * e[1], d * e[2], d * e[3]);
         }
-        *(u32x4 *)(b8 + (size_t)n * K64 + b * 32 + 16 * half) = o;
+        *(u32x4 *)(b8 + (size_t)n * K64 + lo_byte(b, 16 * half)) = o;
     }
 }
 
@@ -265,7 +252,7 @@ __device__ __forceinline__ void unpack_q8(const u32x4 q, u32x4 (&out)[2]) {
 struct GemmArgs {
     const _Float16 *xh;
     const uint8_t *xl;
-    const int32_t *xsc;
+    const uint8_t *xsb;
     const uint8_t *qs;
     const uint16_t *ds;
     const uint8_t *b8;
@@ -274,6 +261,7 @@ struct GemmArgs {
     float *partial;  // K-split partial products (up to 8 x M x N floats), or null: no split
     uint32_t M, K, N;
     SplitOut *defer = nullptr;  // set: the partial sums are left for the consumer
+    GemmXSplit act{};           // SWIGLU: where the activation's split x goes
 };
 
 // ---- the MFMA GEMM ----
@@ -306,21 +294,26 @@ struct GemmCfg {
 
 // SWIGLU: the weight's rows are gate and up interleaved in runs of 32 (rows 64c .. 64c + 31 gate
 // units 32c .., rows 64c + 32 .. up units 32c ..), so a wavefront's two 32-column fragments hold a
-// unit's gate and up; the epilogue writes act = swiglu_act(gate, up) into y as [M][N / 2] instead of
-// the N outputs (one K split; N a multiple of 64).
+// unit's gate and up, 32 units: one block of the activation act = swiglu_act(gate, up). The
+// epilogue passes the tile's activations through LDS and writes them into `act` as the next
+// product's split x (split_chunk4) instead of the N outputs (one K split; N a multiple of 64; the
+// activation's rows are M, its width N / 2).
 template <int KIND, int BM, int BN, int WAVES_M, bool SWIGLU = false>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict__ xh, const uint8_t *__restrict__ xl,
-                                                      const int32_t *__restrict__ xsc, const uint8_t *__restrict__ qs,
+                                                      const uint8_t *__restrict__ xsb, const uint8_t *__restrict__ qs,
                                                       const uint16_t *__restrict__ ds, const uint8_t *__restrict__ b8,
                                                       const int32_t *__restrict__ bsc, float *__restrict__ y,
                                                       uint32_t M, uint32_t K, uint32_t N, uint32_t mt, uint32_t nt,
-                                                      uint32_t split_stages) {
+                                                      uint32_t split_stages, GemmXSplit act) {
     using C = GemmCfg<KIND, BM, BN, WAVES_M>;
-    __shared__ __attribute__((aligned(16))) _Float16 sA[BM * kAStr];
-    __shared__ __attribute__((aligned(16))) uint8_t sL[BM * kLStr];
-    __shared__ __attribute__((aligned(16))) _Float16 sB[BN * kBStr];
-    __shared__ __attribute__((aligned(16))) uint8_t sB8[BN * kB8Str];
-    __shared__ float sD[2 * BN];
+    constexpr uint32_t kA = BM * kAStr * 2, kL = BM * kLStr, kB = BN * kBStr * 2, kB8 = BN * kB8Str, kD = 2 * BN * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t arena[kA + kL + kB + kB8 + kD + 2 * BM];
+    _Float16 *sA = (_Float16 *)arena;
+    uint8_t *sL = arena + kA;
+    _Float16 *sB = (_Float16 *)(arena + kA + kL);
+    uint8_t *sB8 = arena + kA + kL + kB;
+    float *sD = (float *)(arena + kA + kL + kB + kB8);
+    uint8_t *sS = arena + kA + kL + kB + kB8 + kD;  // the stage's x lo scale bytes, two per row
 
     uint32_t mi, ni;
     if (!xcd_tile(mt, nt, &mi, &ni)) return;  // whole CTA: no barrier is left waiting
@@ -337,13 +330,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
     const int fk = 8 * (lane / 32);  // first of this lane's 8 positions in a K = 16 step
     const int f8 = 32 * (lane / 32); // first of this lane's 32 bytes in the K = 64 correction step
 
-    // the correction's power-of-two scales per fragment row / column
-    int32_t asc[C::TM], bscv[C::TN];
-#pragma unroll
-    for (int i = 0; i < C::TM; i++) {
-        const uint32_t m = m0 + (wm * C::TM + i) * 32 + fr;
-        asc[i] = m < M ? xsc[m] : 0x7f7f7f7f;
-    }
+    // the correction's power-of-two scales per fragment column (the rows' come with each stage)
+    int32_t bscv[C::TN];
 #pragma unroll
     for (int j = 0; j < C::TN; j++) {
         const uint32_t n = n0 + (wn * C::TN + j) * 32 + fr;
@@ -359,10 +347,13 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
     // row count); the second block of an odd last stage reads whatever follows, which the f16 pass
     // skips, and the fp8 operands' zero row tails cover it for the correction.
     const uint32_t K64 = (K + 63) / 64 * 64;
+    const uint32_t MS = xsb_rows(M);
     const uint32_t n_xh = M * nb * 64, n_xl = M * K64, n_q = (N + 31) / 32 * 32 * nb * C::QB, n_b8 = N * K64,
-                   n_d = (N + 31) / 32 * 32 * ((nb + 7) / 8 * 8) * 2;
+                   n_d = (N + 31) / 32 * 32 * ((nb + 7) / 8 * 8) * 2, n_sc = K64 / 64 * MS * 2;
     constexpr uint32_t kOut = 0x80000000u;  // an offset past every array: loads return zeros
     uint32_t o_xh[C::XH], o_xl[C::XL], o_q[C::QL], o_b8[C::BL], o_d;
+    // threads t < BM / 2 stage 4 bytes of the tile's scale bytes (two per row) per stage
+    const uint32_t o_sc = (uint32_t)tid < BM / 2 ? m0 * 2 + 4 * tid : kOut;
     uint32_t s_xh[C::XH], s_xl[C::XL], s_q[C::QL], s_b8[C::BL];  // LDS byte offsets
 #pragma unroll
     for (int i = 0; i < C::XH; i++) {
@@ -400,7 +391,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
     }
     // two register sets of staged operands: stage st + 2 is requested while stage st is computed
     u32x4 rxh[2][C::XH], rxl[2][C::XL], rq[2][C::QL], rb8[2][C::BL];
-    uint32_t rd[2] = {0u, 0u};
+    uint32_t rd[2] = {0u, 0u}, rsc[2] = {0u, 0u};
     // Every stage issues its loads, also the two past the split's end (through empty resources,
     // which return zeros): the number of loads in flight is then the same on every path, so the
     // compiler's waits count exactly the older register set and never drain the prefetch.
@@ -411,6 +402,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
         const auto r_q = make_rsrc(qs, live ? n_q : 0u);
         const auto r_b8 = make_rsrc(b8, live ? n_b8 : 0u);
         const auto r_d = make_rsrc(ds, live ? n_d : 0u);
+        const auto r_sc = make_rsrc(xsb, live ? n_sc : 0u);
 #pragma unroll
         for (int i = 0; i < C::XH; i++)
             rxh[rs][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_xh, (int)(o_xh[i] + st * 128), 0, 0));
@@ -425,6 +417,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
             rb8[rs][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r_b8, (int)(o_b8[i] + st * 64), 0, 0));
         // blocks 2 st and 2 st + 1 are neighbours in one run of eight scales
         rd[rs] = __builtin_amdgcn_raw_buffer_load_b32(r_d, (int)(o_d + (st >> 2) * 512 + (st & 3) * 4), 0, 0);
+        rsc[rs] = __builtin_amdgcn_raw_buffer_load_b32(r_sc, (int)(o_sc + st * MS * 2), 0, 0);
     };
     auto store_stage = [&](int rs) {
         uint8_t *sAb = (uint8_t *)sA, *sBb = (uint8_t *)sB;
@@ -456,6 +449,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
             sD[tid] = half_to_float(rd[rs] & 0xffffu);
             sD[BN + tid] = half_to_float(rd[rs] >> 16);
         }
+        if (tid < BM / 2) *(uint32_t *)(sS + 4 * tid) = rsc[rs];
     };
 
     f32x16 acc[C::TM][C::TN];
@@ -504,7 +498,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
                     for (int q = 0; q < 16; q++) acc[i][j][q] = fmaf(dcol[j], p[q], acc[i][j][q]);
                 }
         }
-        // the correction over the stage's 64 k (blocks past nb hold zeros)
+        // the correction over the stage's 64 k (blocks past nb hold zeros), with the scale of the
+        // lane's half: block 2 st + lane / 32 of its fragment row (rows past M, lo zero, take 2^0)
+        int32_t asc[C::TM];
+#pragma unroll
+        for (int i = 0; i < C::TM; i++) {
+            const uint32_t r = (wm * C::TM + i) * 32 + fr;
+            asc[i] = m0 + r < M ? (int32_t)sS[2 * r + lane / 32] : 127;
+        }
         i32x8 b8f[C::TN], a8[C::TM];
 #pragma unroll
         for (int j = 0; j < C::TN; j++) {
@@ -537,19 +538,45 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(const _Float16 *__restrict
     // D layout of a 32x32 tile: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32
     if constexpr (SWIGLU) {
         static_assert(C::TN % 2 == 0, "a wavefront's fragments pair gate and up");
-        const uint32_t units = N / 2;
+        // the tile's BM x BN / 2 activations through LDS (rows kRow floats apart), then eight lanes
+        // per row and block write the split x with whole 64-unit rows per group of 16 lanes
+        constexpr uint32_t U = BN / 2, kRow = U + 4;
+        static_assert(BM * kRow * 4 <= kA + kL + kB + kB8, "the epilogue's LDS fits the stage buffers");
+        static_assert(BM * U / 4 % 256 == 0, "whole 8-lane groups");
+        float *sT = (float *)arena;
+        __syncthreads();  // every wave is done reading the last stage
 #pragma unroll
         for (int i = 0; i < C::TM; i++)
 #pragma unroll
             for (int j = 0; j < C::TN; j += 2) {
-                const uint32_t col = n0 + (wn * C::TN + j) * 32;  // a gate run (a multiple of 64)
-                const uint32_t unit = col / 2 + fr;
+                const uint32_t u = (wn * C::TN + j) * 16 + fr;  // the tile's unit (gate run / 2 + fr)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const uint32_t row = m0 + (wm * C::TM + i) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
-                    if (row < M && col < N) y[(size_t)row * units + unit] = swiglu_act(acc[i][j][r], acc[i][j + 1][r]);
+                    const uint32_t rl = (wm * C::TM + i) * 32 + 8 * (r / 4) + 4 * (lane / 32) + r % 4;
+                    sT[rl * kRow + u] = swiglu_act(acc[i][j][r], acc[i][j + 1][r]);
                 }
             }
+        __syncthreads();
+        const uint32_t units = N / 2, MS = xsb_rows(M), onb = units / 32, oK64 = (units + 63) / 64 * 64;
+        // thread t: float4 q = t % (U / 4) (the same block b and place j) of rows t / (U / 4) + i R
+        constexpr uint32_t R = 256 / (U / 4);
+        const uint32_t q = tid % (U / 4), unit = n0 / 2 + 4 * q, b = unit / 32, j = q % 8;
+        if (unit < units) {  // (the same for the eight lanes of a block)
+            const uint32_t r0 = tid / (U / 4);
+            _Float16 *hb = act.xh + ((size_t)(m0 + r0) * onb + b) * 32;
+            uint8_t *lw = act.xl + (size_t)(m0 + r0) * oK64 + lo_byte(b, 4 * j);
+            uint8_t *sb = act.xsb + xsb_at(m0 + r0, b, MS);
+            const bool tail = onb % 2 && b == onb - 1 && j < 2;
+#pragma unroll
+            for (uint32_t rl = r0; rl < BM; rl += R) {
+                if (m0 + rl >= M) break;
+                split_chunk4_at<KIND>(*(const f32x4 *)(sT + rl * kRow + 4 * q), j, hb, lw, sb);
+                if (tail) split_tail(m0 + rl, onb, oK64, MS, act.xl, act.xsb, j);
+                hb += (size_t)R * onb * 32;
+                lw += (size_t)R * oK64;
+                sb += 2 * R;
+            }
+        }
     } else {
 #pragma unroll
         for (int i = 0; i < C::TM; i++)
@@ -606,8 +633,8 @@ hipError_t run_gemm(hipStream_t s, const GemmArgs &g) {
     if (SWIGLU && sp != 1) return hipErrorInvalidValue;  // (gemm_swiglu_supported rules it out)
     const uint32_t per = (stages + sp - 1) / sp;
     float *out = sp > 1 ? g.partial : g.y;
-    gemm_kernel<KIND, BM, BN, WAVES_M, SWIGLU><<<dim3(grid, sp), 256, 0, s>>>(g.xh, g.xl, g.xsc, g.qs, g.ds, g.b8, g.bsc,
-                                                                               out, g.M, g.K, g.N, mt, nt, per);
+    gemm_kernel<KIND, BM, BN, WAVES_M, SWIGLU><<<dim3(grid, sp), 256, 0, s>>>(g.xh, g.xl, g.xsb, g.qs, g.ds, g.b8, g.bsc,
+                                                                               out, g.M, g.K, g.N, mt, nt, per, g.act);
     if (g.defer) *g.defer = sp > 1 ? SplitOut{g.partial, sp} : SplitOut{g.y, 1u};
     if (sp > 1 && !g.defer) {
         const size_t n = (size_t)g.M * g.N;
@@ -1331,7 +1358,7 @@ __device__ __forceinline__ uint32_t swz64(uint32_t r, uint32_t c) { return (r * 
 template <int KIND, bool SCORE = false>
 __global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16 *__restrict__ xh,
                                                                   const uint8_t *__restrict__ xl,
-                                                                  const int32_t *__restrict__ xsc,
+                                                                  const uint8_t *__restrict__ xsb,
                                                                   const uint8_t *__restrict__ qs,
                                                                   const uint16_t *__restrict__ ds,
                                                                   const uint8_t *__restrict__ b8,
@@ -1360,7 +1387,7 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16
 
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, wm = wave % 4, wn = wave / 4;
     const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
-    const uint32_t nb = K / 32, K64 = (K + 63) / 64 * 64;
+    const uint32_t nb = K / 32, K64 = (K + 63) / 64 * 64, MS = xsb_rows(M);
     const uint32_t st0 = blockIdx.y * split_stages, st1 = min(nb, st0 + split_stages);
     const uint32_t stream = my_tiles * split_stages;
     y += (size_t)blockIdx.y * M * N;
@@ -1411,8 +1438,9 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16
     uint32_t ct = 0, cm0, cn0;
     origin(0, cm0, cn0);
     // the pair starting at (even) block b of the computed tile: x lo and the correction operand
-    // (natural k order, rows of K64, 32 bytes per block) and the tile's row and column scales (E8M0
-    // bytes, four copies); rows past M and columns past N read zeros, whose products are zero
+    // (rows of K64, 64 bytes per pair in the order of lo_byte), the pair's scale bytes of the tile's
+    // rows (two per row) and the columns' scales (E8M0 bytes, four copies); rows past M and columns
+    // past N read zeros, whose products are zero
     auto dma_corr = [&](uint32_t b) {
         const bool live = b < st1;
         const i32x4 rl = sgpr_rsrc(xl, live ? M * K64 : 0u);
@@ -1423,10 +1451,10 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16
             asm_load_lds16(rl, lds0 + S::L8 + wave_u * 2048 + 1024 * i, (cm0 + row) * K64 + b * 32 + chunk64(row));
             asm_load_lds16(rc, lds0 + S::C8 + wave_u * 2048 + 1024 * i, (cn0 + row) * K64 + b * 32 + chunk64(row));
         }
-        if (wave_u < 4) {
-            const i32x4 rs = sgpr_rsrc(xsc, M * 4);
-            asm_load_lds4(rs, lds0 + S::SC + wave_u * 256, (cm0 + 64 * wave_u + lane) * 4);
-        } else {
+        if (wave_u < 2) {  // the pair's scale bytes of the tile's 256 rows, two rows a lane
+            const i32x4 rs = sgpr_rsrc(xsb, live ? K64 / 64 * MS * 2 : 0u);
+            asm_load_lds4(rs, lds0 + S::SC + wave_u * 256, ((b / 2) * MS + cm0 + 128 * wave_u + 2 * lane) * 2);
+        } else if (wave_u >= 4) {
             const i32x4 rs = sgpr_rsrc(bsc, N * 4);
             asm_load_lds4(rs, lds0 + S::SC + 1024 + (wave_u - 4) * 256, (cn0 + 64 * (wave_u - 4) + lane) * 4);
         }
@@ -1522,7 +1550,8 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_fast_kernel(const _Float16
             const u32x4 lo1 = *(const u32x4 *)(arena + S::L8 + swz64(r, 2 * hf + 1));
             a8[i] = i32x8{(int)lo0[0], (int)lo0[1], (int)lo0[2], (int)lo0[3], (int)lo1[0], (int)lo1[1], (int)lo1[2],
                           (int)lo1[3]};
-            asc[i] = scl[r];
+            // the scale of the lane's block (2 p + hf) of its row; rows past M (lo zero) take 2^0
+            asc[i] = cm0 + r < M ? (int32_t)(arena + S::SC)[2 * r + hf] : 127;
         }
 #pragma unroll
         for (int j = 0; j < 4; j++) bscv[j] = scl[256 + wn * 128 + j * 32 + fr];
@@ -1691,7 +1720,7 @@ hipError_t run_gemm_stream_fast(hipStream_t s, const GemmArgs &g, uint32_t sp) {
     const uint32_t stages = g.K / 32;
     const uint32_t per = ((stages + sp - 1) / sp + 1) & ~1u;  // even: pairs never straddle a split
     float *out = sp > 1 ? g.partial : g.y;
-    gemm_stream_fast_kernel<KIND><<<dim3(8 * ctas, sp), 512, 0, s>>>(g.xh, g.xl, g.xsc, g.qs, g.ds, g.b8, g.bsc, out,
+    gemm_stream_fast_kernel<KIND><<<dim3(8 * ctas, sp), 512, 0, s>>>(g.xh, g.xl, g.xsb, g.qs, g.ds, g.b8, g.bsc, out,
                                                                       g.M, g.K, g.N, mt, nt, per, ScoreOut{});
     if (g.defer) *g.defer = sp > 1 ? SplitOut{g.partial, sp} : SplitOut{g.y, 1u};
     if (sp > 1 && !g.defer) {
@@ -1726,7 +1755,7 @@ hipError_t gemm_fast_dispatch(hipStream_t s, const GemmArgs &g) {
 // is the model width, a few dozen stages) over every tile.
 
 template <int KIND>
-hipError_t run_gemm_score(hipStream_t s, fh_path path, const void *xa, const uint8_t *xl, const int32_t *xsc,
+hipError_t run_gemm_score(hipStream_t s, fh_path path, const void *xa, const uint8_t *xl, const uint8_t *xsb,
                           const uint8_t *qs, const uint16_t *ds, const uint8_t *b8, const int32_t *bsc, uint32_t M,
                           uint32_t K, uint32_t N, const ScoreOut &so) {
     const uint32_t mt = (M + 255) / 256, nt = (N + 255) / 256;
@@ -1740,7 +1769,7 @@ hipError_t run_gemm_score(hipStream_t s, fh_path path, const void *xa, const uin
     const uint32_t ctas = min(per_xcd, (uint32_t)cus / 8), stages = K / 32;
     if (path == FH_PATH_TILED_FAST)
         gemm_stream_fast_kernel<KIND, true><<<dim3(8 * ctas, 1), 512, 0, s>>>(
-            (const _Float16 *)xa, xl, xsc, qs, ds, b8, bsc, nullptr, M, K, N, mt, nt, (stages + 1) & ~1u, so);
+            (const _Float16 *)xa, xl, xsb, qs, ds, b8, bsc, nullptr, M, K, N, mt, nt, (stages + 1) & ~1u, so);
     else
         gemm_stream_precise_kernel<KIND, true><<<dim3(8 * ctas, 1), 512, 0, s>>>((const _Float16 *)xa, qs, ds, nullptr,
                                                                                  M, K, N, mt, nt, stages, so);
@@ -2669,13 +2698,14 @@ hipError_t gemm_f16_dispatch(hipStream_t s, const GemmF16Args &g) {
 GemmXSplit gemm_x_split(void *workspace, size_t rows, size_t k) {
     const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     uint8_t *ws = (uint8_t *)workspace;
-    return GemmXSplit{(_Float16 *)ws, ws + up(rows * k * 2), (int32_t *)(ws + up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)))};
+    return GemmXSplit{(_Float16 *)ws, ws + up(rows * k * 2), ws + up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64))};
 }
 
-// x hi (2 bytes per element), x lo (1 byte), one scale word per row, each piece 256-aligned
+// x hi (2 bytes per element), x lo (1 byte, rows of k rounded up to 64), two scale bytes per row
+// and 64 k (rows rounded up to 8), each piece 256-aligned (the planes of xsplit.hpp)
 size_t gemm_xsplit_bytes(size_t rows, size_t k) {
     const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
-    return up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)) + up(rows * 4);
+    return up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)) + up((k + 63) / 64 * xsb_rows((uint32_t)rows) * 2);
 }
 
 size_t gemm_workspace_bytes(size_t rows, size_t k, size_t n) {
@@ -2779,13 +2809,14 @@ hipError_t launch_naive(hipStream_t s, fh_kind kind, const uint8_t *qs, const ui
 
 hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
                        const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace, SplitOut *defer,
-                       float *partial) {
+                       float *partial, const GemmXSplit *xs) {
     const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
     uint8_t *ws = (uint8_t *)workspace;
+    const GemmXSplit sx = xs && !x ? *xs : gemm_x_split(ws, rows, k);
     GemmArgs g;
-    g.xh = (const _Float16 *)ws;
-    g.xl = ws + up(rows * k * 2);
-    g.xsc = (const int32_t *)(ws + up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)));
+    g.xh = sx.xh;
+    g.xl = sx.xl;
+    g.xsb = sx.xsb;
     g.qs = qs;
     g.ds = ds;
     g.b8 = b8;
@@ -2798,13 +2829,10 @@ hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uin
     g.N = (uint32_t)n;
     g.defer = defer;
     if (kind == FH_Q8_0) {
-        if (x)
-            split_x_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc,
-                                                                   g.K);
+        if (x) split_x_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, sx.xh, sx.xl, sx.xsb, g.K);
         return gemm_fast_dispatch<FH_Q8_0>(s, g);
     }
-    if (x)
-        split_x_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
+    if (x) split_x_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, sx.xh, sx.xl, sx.xsb, g.K);
     return gemm_fast_dispatch<FH_Q4_0>(s, g);
 }
 
@@ -2822,31 +2850,30 @@ bool gemm_swiglu_supported(size_t rows, size_t k, size_t n) {
 }
 
 hipError_t launch_gemm_swiglu(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
-                              const float *x, float *act, size_t rows, size_t k, size_t n, void *workspace) {
+                              const float *x, const GemmXSplit &act, size_t rows, size_t k, size_t n,
+                              void *workspace) {
     if (!gemm_swiglu_supported(rows, k, n)) return hipErrorInvalidValue;
     const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
-    uint8_t *ws = (uint8_t *)workspace;
+    const GemmXSplit sx = gemm_x_split(workspace, rows, k);
     GemmArgs g;
-    g.xh = (const _Float16 *)ws;
-    g.xl = ws + up(rows * k * 2);
-    g.xsc = (const int32_t *)(ws + up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)));
+    g.xh = sx.xh;
+    g.xl = sx.xl;
+    g.xsb = sx.xsb;
     g.qs = qs;
     g.ds = ds;
     g.b8 = b8;
     g.bsc = (const int32_t *)(b8 + up(n * ((k + 63) / 64 * 64)));
-    g.y = act;
+    g.y = nullptr;
     g.partial = nullptr;  // one K split
     g.M = (uint32_t)rows;
     g.K = (uint32_t)k;
     g.N = (uint32_t)n;
+    g.act = act;
     if (kind == FH_Q8_0) {
-        if (x)
-            split_x_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc,
-                                                                   g.K);
+        if (x) split_x_kernel<FH_Q8_0><<<(unsigned)rows, 256, 0, s>>>(x, sx.xh, sx.xl, sx.xsb, g.K);
         return gemm_dispatch<FH_Q8_0, true>(s, g);
     }
-    if (x)
-        split_x_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, (_Float16 *)g.xh, (uint8_t *)g.xl, (int32_t *)g.xsc, g.K);
+    if (x) split_x_kernel<FH_Q4_0><<<(unsigned)rows, 256, 0, s>>>(x, sx.xh, sx.xl, sx.xsb, g.K);
     return gemm_dispatch<FH_Q4_0, true>(s, g);
 }
 
@@ -2906,17 +2933,14 @@ hipError_t launch_gemm_score(hipStream_t s, fh_path path, fh_kind kind, const ui
     const uint32_t M = (uint32_t)rows, K = (uint32_t)k, N = (uint32_t)n;
     if (path == FH_PATH_TILED_FAST) {
         const auto up = [](size_t v) { return (v + 255) / 256 * 256; };
-        uint8_t *ws = (uint8_t *)workspace;
-        _Float16 *xh = (_Float16 *)ws;
-        uint8_t *xl = ws + up(rows * k * 2);
-        int32_t *xsc = (int32_t *)(ws + up(rows * k * 2) + up(rows * ((k + 63) / 64 * 64)));
+        const GemmXSplit sx = gemm_x_split(workspace, rows, k);
         const int32_t *bsc = (const int32_t *)(b8 + up(n * ((k + 63) / 64 * 64)));
         if (kind == FH_Q8_0) {
-            split_x_kernel<FH_Q8_0><<<M, 256, 0, s>>>(x, xh, xl, xsc, K);
-            return run_gemm_score<FH_Q8_0>(s, path, xh, xl, xsc, qs, ds, b8, bsc, M, K, N, so);
+            split_x_kernel<FH_Q8_0><<<M, 256, 0, s>>>(x, sx.xh, sx.xl, sx.xsb, K);
+            return run_gemm_score<FH_Q8_0>(s, path, sx.xh, sx.xl, sx.xsb, qs, ds, b8, bsc, M, K, N, so);
         }
-        split_x_kernel<FH_Q4_0><<<M, 256, 0, s>>>(x, xh, xl, xsc, K);
-        return run_gemm_score<FH_Q4_0>(s, path, xh, xl, xsc, qs, ds, b8, bsc, M, K, N, so);
+        split_x_kernel<FH_Q4_0><<<M, 256, 0, s>>>(x, sx.xh, sx.xl, sx.xsb, K);
+        return run_gemm_score<FH_Q4_0>(s, path, sx.xh, sx.xl, sx.xsb, qs, ds, b8, bsc, M, K, N, so);
     }
     _Float16 *xs = (_Float16 *)workspace;
     const size_t items = rows * (k / 32);

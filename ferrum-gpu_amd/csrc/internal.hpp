@@ -257,27 +257,32 @@ size_t gemm_b8_bytes(size_t k, size_t n);
 bool gemm_supported(size_t rows, size_t k, size_t n);
 hipError_t launch_make_b8(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, uint8_t *b8, size_t k,
                           size_t n);
-// x == nullptr: the workspace already holds x in the split form (gemm_x_split, written by
-// split_row_fast in xsplit.hpp). partial != nullptr: the K-split partial products go there
-// (gemm_partial_bytes) instead of after the split x, so that a consumer of deferred partial sums
-// can write the next product's split x (of another width) while it reads them.
-hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
-                       const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace,
-                       SplitOut *defer = nullptr, float *partial = nullptr);
-// The fast GEMM with SwiGLU fused into its epilogue: the weight's n rows are gate and up
-// interleaved in runs of 32 (load_mat_rows with interleave), act gets rows x n / 2 activations
-// (swiglu_act). Only where gemm_swiglu_supported; x null: the split x is already in the workspace.
-bool gemm_swiglu_supported(size_t rows, size_t k, size_t n);
-hipError_t launch_gemm_swiglu(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
-                              const float *x, float *act, size_t rows, size_t k, size_t n, void *workspace);
-// Where the fast GEMM's split x lives in its workspace: hi (rows x k f16), lo (rows x k rounded
-// up to 64, e4m3), one scale word per row.
+// Where the fast GEMM's split x lives (gemm_x_split: at the start of its workspace): hi (rows x k
+// f16), lo (rows x k rounded up to 64, e4m3), the scale bytes (two per row and 64 k); the layouts
+// are in xsplit.hpp.
 struct GemmXSplit {
     _Float16 *xh;
     uint8_t *xl;
-    int32_t *xsc;
+    uint8_t *xsb;
 };
 GemmXSplit gemm_x_split(void *workspace, size_t rows, size_t k);
+// x == nullptr: x is already in the split form (written by split_row_fast or split_chunk4 in
+// xsplit.hpp), in the workspace or, when xs is given, at xs. partial != nullptr: the K-split
+// partial products go there (gemm_partial_bytes) instead of after the split x, so that a consumer
+// of deferred partial sums can write the next product's split x (of another width) while it reads
+// them.
+hipError_t launch_gemm(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
+                       const float *x, float *y, size_t rows, size_t k, size_t n, void *workspace,
+                       SplitOut *defer = nullptr, float *partial = nullptr, const GemmXSplit *xs = nullptr);
+// The fast GEMM with SwiGLU fused into its epilogue: the weight's n rows are gate and up
+// interleaved in runs of 32 (load_mat_rows with interleave); the rows x n / 2 activations
+// (swiglu_act) are written as the down product's split x at act (gemm_xsplit_bytes(rows, n / 2)
+// bytes, apart from the workspace). Only where gemm_swiglu_supported; x null: the split x is
+// already in the workspace.
+bool gemm_swiglu_supported(size_t rows, size_t k, size_t n);
+hipError_t launch_gemm_swiglu(hipStream_t s, fh_kind kind, const uint8_t *qs, const uint16_t *ds, const uint8_t *b8,
+                              const float *x, const GemmXSplit &act, size_t rows, size_t k, size_t n,
+                              void *workspace);
 // The dequant-f16 MFMA GEMM (x as f16 with a power-of-two row scale, weights dequantised to f16
 // in LDS; split into workspace, then the product).
 size_t gemm_f16_workspace_bytes(size_t rows, size_t k, size_t n);

@@ -43,6 +43,9 @@ struct fh_llama {
     float rope_base = 10000.0f, eps = 1e-5f, linear_factor = 1.0f;
     bool neox = false, tied = false;
     bool fuse_rope = true;  // qkv_rope_split_kernel where it fits (FERRUM_HIP_ROPE_UNFUSED=1 at load: never)
+    // on the fast path with the split attention, the attention writes the output product's split x
+    // itself (FERRUM_HIP_ATTN_SPLIT_UNFUSED=1 at load: f32 rows, then the product's split pass)
+    bool att_split = true;
     // the score in the head GEMM's epilogue (launch_gemm_score) on the TILED and TILED_FAST paths
     // where it takes the shape (FERRUM_HIP_SCORE_UNFUSED=1 at load: the logits and score_kernel)
     bool fuse_score = true;
@@ -311,7 +314,7 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float *__restrict__ 
                                                             const float *__restrict__ g, uint32_t d, float eps,
                                                             uint32_t o_splits, size_t o_stride, GemmXSplit dst) {
     extern __shared__ __attribute__((aligned(16))) float hrow[];
-    __shared__ float red[4], red2[4];
+    __shared__ float red[4];
     const size_t base = (size_t)blockIdx.x * d;
     if (d % 4 == 0) {
         const uint32_t nq = d / 4;
@@ -340,8 +343,8 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float *__restrict__ 
         for (uint32_t i = threadIdx.x; i < d; i += 256) hrow[i] = __fmul_rn(__fmul_rn(x[base + i], inv), g[i]);
     }
     __syncthreads();
-    split_row_fast<KIND>([&](uint32_t q) { return *(const f32x4 *)&hrow[4 * q]; }, blockIdx.x, d, dst.xh, dst.xl,
-                         dst.xsc, red2);
+    split_row_fast<KIND>([&](uint32_t q) { return *(const f32x4 *)&hrow[4 * q]; }, blockIdx.x, gridDim.x, d, dst.xh,
+                         dst.xl, dst.xsb);
 }
 
 // INTER: gu's columns are gate and up interleaved in runs of 32 (the weight loaded for the
@@ -350,7 +353,6 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float *__restrict__ 
 template <int KIND, bool INTER = false>
 __global__ __launch_bounds__(256) void swiglu_split_kernel(const float *__restrict__ gu, uint32_t hid, GemmXSplit dst) {
     extern __shared__ __attribute__((aligned(16))) float hrow[];
-    __shared__ float red[4];
     const size_t r = blockIdx.x;
     const uint32_t nq = hid / 4;
     auto act = [&](uint32_t j, f32x4 gg, f32x4 u) {
@@ -379,8 +381,8 @@ __global__ __launch_bounds__(256) void swiglu_split_kernel(const float *__restri
     for (uint32_t j = threadIdx.x + 256 * kKeepRow; j < nq; j += 256)
         act(j, *(const f32x4 *)(gu + r * 2 * hid + gcol(j)), *(const f32x4 *)(gu + r * 2 * hid + uoff + gcol(j)));
     __syncthreads();
-    split_row_fast<KIND>([&](uint32_t q) { return *(const f32x4 *)&hrow[4 * q]; }, (uint32_t)r, hid, dst.xh, dst.xl,
-                         dst.xsc, red);
+    split_row_fast<KIND>([&](uint32_t q) { return *(const f32x4 *)&hrow[4 * q]; }, (uint32_t)r, gridDim.x, hid, dst.xh,
+                         dst.xl, dst.xsb);
 }
 
 // q/k/v bias and RoPE on one row of qkv (ferrum_ref/src/models/llama/ops.rs:105-127): the row's
@@ -835,12 +837,16 @@ __device__ __forceinline__ int exp_byte(uint64_t w, int i) { return (int)(int8_t
 // S = S' 2^(e_q + e_k) scale, masked, online softmax -> p; p' = p 2^(14 + e_v - sigma) (sigma the
 // tile's largest v exponent, so p' <= 2^14) split into two f16 parts; the tile's O'^T = v'^T p'^T
 // (three f16 MFMAs per 16 keys per 32 dims) enters the f32 accumulator scaled by 2^(sigma - 14).
-template <int HD, int W>
+// XKIND 0: the output goes to att as f32 [t][heads HD]; FH_Q8_0 / FH_Q4_0: it goes to xo as the
+// fast GEMM's split x for a weight of that kind (xsplit.hpp, t rows of heads HD), the same values
+// split_x_kernel would make of the f32 rows.
+template <int HD, int W, int XKIND = 0>
 __global__ __launch_bounds__(64 * W) void attention_split_kernel(
     const _Float16 *__restrict__ qh, const _Float16 *__restrict__ ql, const _Float16 *__restrict__ kh,
     const _Float16 *__restrict__ kl, const _Float16 *__restrict__ vh, const _Float16 *__restrict__ vl,
     const int8_t *__restrict__ eq, const int8_t *__restrict__ ek, const int8_t *__restrict__ ev,
-    float *__restrict__ att, uint32_t t, uint32_t tp, uint32_t heads, uint32_t group, float scale) {
+    float *__restrict__ att, uint32_t t, uint32_t tp, uint32_t heads, uint32_t group, float scale,
+    GemmXSplit xo = GemmXSplit{}) {
     using T = SplitTile<HD>;
     constexpr int DB = T::DB, KS = T::KS;
     __shared__ float red[W][2 + 16 * DB][64];
@@ -948,7 +954,56 @@ __global__ __launch_bounds__(64 * W) void attention_split_kernel(
     }
     l += __shfl_xor(l, 32);
     const float inv = 1.0f / l;
-    if (query >= t) return;
+    if (query >= t) return;  // (the same for lanes l and l ^ 32)
+    if constexpr (XKIND != 0) {
+        // per 32-dim block b: lane (query, hf) holds its dims 8 k + 4 hf + 0..3, i.e. element groups
+        // G = 2 k + hf of four; the block's largest |x| with the partner lane, then the split
+        typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+        typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
+        const uint32_t nb = qd / 32, K64 = (qd + 63) / 64 * 64, MS = xsb_rows(t);
+#pragma unroll
+        for (int b = 0; b < DB; b++) {
+            float v[16], mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < W; j++) acc += red[j][2 + 16 * b + i][lane] * f[j];
+                v[i] = acc * inv;
+                mx = fmaxf(mx, fabsf(v[i]));
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const int sc = lo_shift(mx);
+            const float sf = __uint_as_float((uint32_t)(127 + sc) << 23);
+            const uint32_t blk = h * HD / 32 + b;
+            if (hf == 0) xo.xsb[xsb_at(query, blk, MS)] = (uint8_t)(127 - sc);
+            _Float16 hv[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) hv[i] = f16_sat(v[i]);
+            uint8_t *lo = xo.xl + (size_t)query * K64;
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                *(uint32_t *)(lo + lo_byte(blk, 4 * (2 * k + hf))) =
+                    fp8x4((v[4 * k] - (float)hv[4 * k]) * sf, (v[4 * k + 1] - (float)hv[4 * k + 1]) * sf,
+                          (v[4 * k + 2] - (float)hv[4 * k + 2]) * sf, (v[4 * k + 3] - (float)hv[4 * k + 3]) * sf);
+            _Float16 *hb = xo.xh + ((size_t)query * nb + blk) * 32;
+            if constexpr (XKIND == FH_Q8_0) {
+                // positions 4 G .. 4 G + 3 hold group G's elements {0, 2, 1, 3}
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    *(h16x4 *)(hb + 4 * (2 * k + hf)) = h16x4{hv[4 * k], hv[4 * k + 2], hv[4 * k + 1], hv[4 * k + 3]};
+            } else {
+                // positions 8 I .. 8 I + 7 hold groups I and I + 4 (both this lane's for I = 2 k + hf)
+#pragma unroll
+                for (int k = 0; k < 2; k++)
+                    *(h16x8 *)(hb + 8 * (2 * k + hf)) =
+                        h16x8{hv[4 * k], hv[4 * k + 2], hv[4 * k + 1], hv[4 * k + 3], hv[4 * k + 8], hv[4 * k + 10],
+                              hv[4 * k + 9], hv[4 * k + 11]};
+            }
+            if (nb % 2 && blk == nb - 1) split_tail(query, nb, K64, MS, xo.xl, xo.xsb, hf);
+        }
+        return;
+    }
     float *out = att + (size_t)query * qd + h * HD;
 #pragma unroll
     for (int b = 0; b < DB; b++)
@@ -1238,8 +1293,12 @@ fh_status ensure_rows(fh_llama *m, size_t t) {
                                                   2 * up256(tp * m->kv_heads)
                                             : 0;
     const size_t sfold = score_fold_bytes(chunk, m->vocab);
-    const size_t total = 3 * up256(t * d * 4) + up256(t * w * 4) + up256(t * qd * 4) + up256(t * 2 * hid * 4) +
-                         up256(t * hid * 4) + up256(chunk * m->vocab * 4) + up256(2 * t * 4) + up256((t + 1) * 4) +
+    // act: the f32 activation, or on the fast path the down product's split x (the SwiGLU epilogue)
+    const size_t act = std::max(t * hid * 4, fast ? gemm_xsplit_bytes(t, hid) : (size_t)0);
+    // att: the f32 attention output, or on the fast path the output product's split x
+    const size_t att = std::max(t * qd * 4, fast ? gemm_xsplit_bytes(t, qd) : (size_t)0);
+    const size_t total = 3 * up256(t * d * 4) + up256(t * w * 4) + up256(att) + up256(t * 2 * hid * 4) +
+                         up256(act) + up256(chunk * m->vocab * 4) + up256(2 * t * 4) + up256((t + 1) * 4) +
                          up256(ws) + up256(part) + split + up256(sfold);
     void *p = nullptr;
     fh_status st = alloc_bytes(m->dev, total, &p);
@@ -1262,9 +1321,9 @@ fh_status ensure_rows(fh_llama *m, size_t t) {
     m->h = (float *)take(t * d * 4);
     m->o = (float *)take(t * d * 4);
     m->qkv = (float *)take(t * w * 4);
-    m->att = (float *)take(t * qd * 4);
+    m->att = (float *)take(att);
     m->gu = (float *)take(t * 2 * hid * 4);
-    m->act = (float *)take(t * hid * 4);
+    m->act = (float *)take(act);
     m->logits = (float *)take(chunk * m->vocab * 4);
     m->scores = (float *)take(2 * t * 4);
     m->ids = (int32_t *)take((t + 1) * 4);
@@ -1309,7 +1368,7 @@ fh_status check_shapes(const fh_llama *m, size_t t) {
 // With defer, a K-split product is left as partial sums in the workspace for the next kernel to
 // add up (every consumer runs before the next product overwrites the workspace).
 hipError_t linear(const fh_llama *m, hipStream_t s, const fh_llama::Mat &mat, const float *x, float *y, size_t rows,
-                  SplitOut *defer = nullptr) {
+                  SplitOut *defer = nullptr, const GemmXSplit *xs = nullptr) {
     if (!mat.q) {  // f32 rows: x is always given (the fused producers run only when every matrix is packed)
         const dim3 grid((unsigned)((mat.n + 63) / 64), (unsigned)((rows + 63) / 64));
         linear_f32_kernel<<<grid, 256, 0, s>>>(x, (const float *)mat.f->ptr, y, (uint32_t)rows, (uint32_t)mat.k,
@@ -1319,7 +1378,7 @@ hipError_t linear(const fh_llama *m, hipStream_t s, const fh_llama::Mat &mat, co
     const fh_qweight *w = mat.q;
     switch (m->path) {
     case FH_PATH_TILED_FAST:
-        return launch_gemm(s, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, m->ws, defer, m->part);
+        return launch_gemm(s, w->kind, w->qs, w->ds, w->b8, x, y, rows, w->k, w->n, m->ws, defer, m->part, xs);
     case FH_PATH_TILED_F16: return launch_gemm_f16(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws, defer);
     default: return launch_gemm_precise(s, w->kind, w->qs, w->ds, x, y, rows, w->k, w->n, m->ws, defer);
     }
@@ -1330,7 +1389,10 @@ hipError_t linear(const fh_llama *m, hipStream_t s, const fh_llama::Mat &mat, co
 // never written), or, when the model was loaded with FERRUM_HIP_ROPE_UNFUSED=1, qkv_rope_kernel
 // and attn_split_kernel, with the same results; the other head dims qkv_rope_kernel and the f32
 // attention_kernel.
-hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t, const SplitOut &qkv, const float *bias) {
+// xo: where the split attention writes its output as the output product's split x (m->kind's
+// operand order) instead of f32 rows in m->att; only when split_attention(m).
+hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t, const SplitOut &qkv, const float *bias,
+                            const GemmXSplit *xo = nullptr) {
     const dim3 grid((unsigned)m->heads, (unsigned)((t + 31) / 32));
     const uint32_t w = (uint32_t)m->qkv_width(), group = (uint32_t)(m->heads / m->kv_heads);
     const float scale = 1.0f / sqrtf((float)m->head_dim);
@@ -1358,8 +1420,18 @@ hipError_t launch_attention(const fh_llama *m, hipStream_t s, size_t t, const Sp
                                                                                 H, KV, rd, neox);                 \
     else                                                                                                          \
         attn_split_kernel<HD><<<tp, 256, 0, s>>>(m->qkv, o, T, tp, w, H, KV);                                     \
-    attention_split_kernel<HD, W><<<grid, 64 * W, 0, s>>>(m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl, m->seq, \
-                                                          m->sek, m->sev, m->att, T, tp, H, group, scale)
+    if (xo && m->kind == FH_Q8_0)                                                                                 \
+        attention_split_kernel<HD, W, FH_Q8_0><<<grid, 64 * W, 0, s>>>(                                           \
+            m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl, m->seq, m->sek, m->sev, m->att, T, tp, H, group, scale, \
+            *xo);                                                                                                 \
+    else if (xo)                                                                                                  \
+        attention_split_kernel<HD, W, FH_Q4_0><<<grid, 64 * W, 0, s>>>(                                           \
+            m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl, m->seq, m->sek, m->sev, m->att, T, tp, H, group, scale, \
+            *xo);                                                                                                 \
+    else                                                                                                          \
+        attention_split_kernel<HD, W><<<grid, 64 * W, 0, s>>>(m->sqh, m->sql, m->skh, m->skl, m->svh, m->svl,     \
+                                                              m->seq, m->sek, m->sev, m->att, T, tp, H, group,    \
+                                                              scale)
         switch (m->head_dim) {
         case 32: FH_SPLIT_ATTN(32, 4); break;
         case 64: FH_SPLIT_ATTN(64, 4); break;
@@ -1394,6 +1466,9 @@ hipError_t enqueue_body(fh_llama *m, hipStream_t s, size_t t) {
     // product then skips its split pass); rows up to 16384 wide, held in LDS.
     const bool fused = m->path == FH_PATH_TILED_FAST && m->packed && m->dim <= 16384 && m->hidden <= 16384;
     const GemmXSplit xd = gemm_x_split(m->ws, t, m->dim), xh = gemm_x_split(m->ws, t, m->hidden);
+    // the attention's output as the output product's split x, in att
+    const bool att_split = fused && m->att_split && split_attention(m);
+    const GemmXSplit xatt = gemm_x_split(m->att, t, m->q_dim());
     auto norm = [&](bool add, const fh_buffer *g, const SplitOut &o) {
         if (fused && m->kind == FH_Q8_0) {
             if (add)
@@ -1418,15 +1493,17 @@ hipError_t enqueue_body(fh_llama *m, hipStream_t s, size_t t) {
         norm(l > 0, L.attn_norm, down);
         SplitOut qkv{m->qkv, 1}, att{m->o, 1}, gu{m->gu, 1};
         if ((e = linear(m, s, L.wqkv, hx, m->qkv, t, &qkv))) break;
-        if ((e = launch_attention(m, s, t, qkv, fp(L.bqkv)))) break;
-        if ((e = linear(m, s, L.wo, m->att, m->o, t, &att))) break;
+        if ((e = launch_attention(m, s, t, qkv, fp(L.bqkv), att_split ? &xatt : nullptr))) break;
+        if ((e = linear(m, s, L.wo, att_split ? nullptr : m->att, m->o, t, &att, att_split ? &xatt : nullptr))) break;
         norm(true, L.ffn_norm, att);
         if (fused && m->gu_inter && gemm_swiglu_supported(t, d, 2 * m->hidden)) {
-            // SwiGLU in the gate/up product's epilogue (interleaved weight): the activation goes to
-            // act, whose split the down product makes itself
+            // SwiGLU in the gate/up product's epilogue (interleaved weight), which writes the
+            // activation as the down product's split x, in act (the gate/up product still reads its
+            // own split x from the workspace)
             const fh_qweight *w = L.wgu.q;
-            if ((e = launch_gemm_swiglu(s, w->kind, w->qs, w->ds, w->b8, nullptr, m->act, t, w->k, w->n, m->ws))) break;
-            if ((e = linear(m, s, L.down, m->act, m->o, t, &down))) break;
+            const GemmXSplit xa = gemm_x_split(m->act, t, m->hidden);
+            if ((e = launch_gemm_swiglu(s, w->kind, w->qs, w->ds, w->b8, nullptr, xa, t, w->k, w->n, m->ws))) break;
+            if ((e = linear(m, s, L.down, nullptr, m->o, t, &down, &xa))) break;
         } else if (fused) {
             // (gate/up reduced in place: SwiGLU's split x would overwrite its partial sums)
             if ((e = linear(m, s, L.wgu, nullptr, m->gu, t))) break;
@@ -1578,6 +1655,8 @@ fh_status fh_llama_from_gguf(fh_device *dev, const fh_gguf *g, fh_path path, fh_
     m->fuse_rope = !(unfused && unfused[0] == '1');
     const char *su = getenv("FERRUM_HIP_SCORE_UNFUSED");
     m->fuse_score = !(su && su[0] == '1');
+    const char *au = getenv("FERRUM_HIP_ATTN_SPLIT_UNFUSED");
+    m->att_split = !(au && au[0] == '1');
     auto key = [&](const char *k) { return arch + "." + k; };
     auto has = [&](const std::string &k) {
         size_t i;

@@ -280,6 +280,30 @@ def test_swiglu_epilogue_is_bit_identical_to_the_swiglu_pass(fh, g, orc, shape):
     assert lp_err(sf, wlp) < FAST_LOGPROB
 
 
+@pytest.mark.parametrize("kind,head_dim,heads,kv_heads,dim", [(lm.Q4_0, 32, 3, 1, 128), (lm.Q8_0, 64, 4, 2, 256),
+                                                              (lm.Q4_0, 128, 2, 1, 256)])
+def test_attention_split_output_is_bit_identical_to_the_split_pass(fh, g, kind, head_dim, heads, kv_heads, dim):
+    """On the fast path the split attention writes the output product's split x itself (per
+    32-dim block: hi in the weight kind's operand order, lo in the pair order, the block's scale)
+    instead of f32 rows that split_x_kernel then splits (FERRUM_HIP_ATTN_SPLIT_UNFUSED=1 at load):
+    the same values, so logits and log-probabilities bit-identical. Both operand orders, head dims
+    32, 64 and 128, and 3 heads of 32 (an odd block count: the last pair's empty block), at a
+    ragged length."""
+    c = lm.config(vocab=300, ctx=128, dim=dim, heads=heads, kv_heads=kv_heads, head_dim=head_dim, layers=2,
+                  hidden=256, rope_base=10000.0, neox=True, eps=1e-5)
+    data = lm.to_gguf(lm.llama_random(c, 29, True, False), kind)
+    fused = load(fh, g, data, fh.QPath.TiledFast)
+    plain = load_env(fh, g, data, fh.QPath.TiledFast, "FERRUM_HIP_ATTN_SPLIT_UNFUSED")
+    ids = [int(t) for t in np.random.default_rng(head_dim).integers(0, 300, 97)]
+    lf, lp = fused.forward_all(ids), plain.forward_all(ids)
+    assert np.all(np.isfinite(lf))
+    assert np.array_equal(np.asarray(lf, np.float32).view(np.uint32), np.asarray(lp, np.float32).view(np.uint32))
+    sf, hf = fused.score_arrays(ids)
+    sp, hp = plain.score_arrays(ids)
+    assert np.array_equal(np.asarray(sf, np.float32).view(np.uint32), np.asarray(sp, np.float32).view(np.uint32))
+    assert np.array_equal(hf, hp)
+
+
 @pytest.fixture(scope="module")
 def qwen(fh, g):
     """The scoring benchmark's model: Qwen2-0.5B shapes (24 layers, d 896, FFN 4864, 14 q / 2 kv
