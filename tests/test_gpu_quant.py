@@ -379,6 +379,36 @@ def test_fast_gemm_meets_the_gemm_bound_at_the_scoring_shapes(fh, g, orc, kind_n
     assert np.array_equal(g.read(gy2), got)
 
 
+def test_fast_gemm_k_split_sums(fh, g, orc):
+    """Products the fast GEMM splits along K (3 to 8 splits, both kinds) and whose partial
+    products gemm_reduce_kernel adds in split order: whole float4s, and a width that is not (the
+    scalar sum). Interleaved and repeated, every repeat gives the first result's bits, each within
+    the bound."""
+    rng = np.random.default_rng(21)
+    cases = [(fh.QKind.Q4_0, 512, 896, 896), (fh.QKind.Q8_0, 512, 4864, 896), (fh.QKind.Q4_0, 96, 2048, 200),
+             (fh.QKind.Q8_0, 2048, 896, 1152), (fh.QKind.Q4_0, 64, 1024, 70)]
+    runs = []
+    for kind, m, k, n in cases:
+        w = (rng.standard_normal(k * n) * 0.02).astype(np.float32)
+        b = orc.quantise_matrix(int(kind), w, k, n)
+        x = rng.standard_normal(m * k).astype(np.float32)
+        runs.append((kind, m, k, n, fh.upload_qweight(g, kind, b, k, n), g.upload(x), cpu_linear(orc, kind, b, x, m, k, n)))
+    first = []
+    for kind, m, k, n, qw, gx, want in runs:
+        gy = g.zeros(m * n)
+        say("k split sums", kind.label(), m, k, n)
+        fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.TiledFast)
+        got = g.read(gy)
+        assert np.mean(np.abs(got - want) > 1e-3 + 2e-3 * np.abs(want)) == 0, (kind, m, k, n)
+        assert orc.max_rel_err(got, want) < FAST_BOUND, (kind, m, k, n)
+        first.append(got)
+    for rep in range(2):
+        for (kind, m, k, n, qw, gx, _), f in zip(runs, first):
+            gy = g.zeros(m * n)
+            fh.linear_q_with(g, gx, qw, gy, m, fh.QPath.TiledFast)
+            assert np.array_equal(g.read(gy).view(np.uint32), f.view(np.uint32)), (rep, kind, m, k, n)
+
+
 def test_fast_gemm_on_awkward_shapes_and_values(fh, g, orc):
     """Odd block counts (the last stage holds one block), rows and columns that are not whole
     tiles, the reference's uniform test data and rows of very different magnitudes (each row's
