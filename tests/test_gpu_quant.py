@@ -436,6 +436,33 @@ def test_fast_gemm_on_awkward_shapes_and_values(fh, g, orc):
                 assert e < FAST_BOUND, (kind, rows, k, n, r, e)
 
 
+def test_fast_gemm_x_lo_scale_is_per_block(fh, g, orc):
+    """x's lo part carries one power-of-two scale per row and 32-element block: blocks of x 1e6
+    times larger than the rest of their row, facing zero weights, leave the small blocks' lo
+    intact. With one scale per row, set by the large blocks, the small blocks' lo drops below
+    e4m3's range: a numpy model of both forms on these inputs gives 2.8e-4 (Q8_0) and 3.1e-4
+    (Q4_0) per row, over FAST_BOUND, against 7.1e-6 and 7.6e-6 per block."""
+    rng = np.random.default_rng(5)
+    rows, k, n = 64, 512, 96
+    big = np.zeros(k // 32, bool)
+    big[::3] = True  # blocks 0, 3, 6, ... large in x, zero in the weights
+    for kind in kinds(fh):
+        w = (rng.standard_normal((k, n)) * 0.02).astype(np.float32)  # [k, n], as quantise_matrix takes it
+        w[np.repeat(big, 32), :] = 0.0
+        w = w.reshape(-1)
+        b = orc.quantise_matrix(int(kind), w, k, n)
+        x = rng.standard_normal((rows, k)).astype(np.float32)
+        x[:, np.repeat(big, 32)] *= 1e6
+        x = x.reshape(-1)
+        want = cpu_linear(orc, kind, b, x, rows, k, n)
+        qw = fh.upload_qweight(g, kind, b, k, n)
+        gx, gy = g.upload(x), g.zeros(rows * n)
+        fh.linear_q_with(g, gx, qw, gy, rows, fh.QPath.TiledFast)
+        e = orc.max_rel_err(g.read(gy), want)
+        say(f"per-block lo scales {kind.label()}: max rel err {e:.2e}")
+        assert e < FAST_BOUND, (kind, e)
+
+
 def test_fast_gemm_is_one_command_and_fails_cleanly(fh, g, orc):
     """The first multi-row product of a weight also builds its correction operand: still one
     command, and an injected fault at it leaves the weight usable."""
