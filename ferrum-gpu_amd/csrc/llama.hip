@@ -723,30 +723,38 @@ __global__ __launch_bounds__(256) void qkv_rope_split_kernel(const float *__rest
     }
     __syncthreads();
     const uint32_t half = rope_dim / 2;
-    for (uint32_t i = 0; i < R / 4; i++) {
-        const uint32_t rr = wave * (R / 4) + i, r = r0 + rr;
-        float v[2];
+    // LPR lanes per row, four dims each, RPI rows of the wavefront's R / 4 at a time; the row's
+    // largest |value| (head_exponent's) by shuffles within its LPR lanes
+    constexpr uint32_t LPR = HD / 4, RPI = 64 / LPR, ROWS = R / 4;
+    for (uint32_t it = 0; it < (ROWS + RPI - 1) / RPI; it++) {
+        const uint32_t rl = it * RPI + lane / LPR;
+        if (rl >= ROWS) break;  // (a whole group of LPR lanes)
+        const uint32_t rr = wave * ROWS + rl, r = r0 + rr, d0 = 4 * (lane % LPR);
+        float v[4], mx = 0.0f;
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const uint32_t d = lane + 64 * u;
-            v[u] = r < t && d < HD ? rope_value(tile[rr], d, cos_t + (size_t)r * half, sin_t + (size_t)r * half,
-                                                kind < 2 ? HD : 0u, HD, rope_dim, neox)
-                                   : 0.0f;
+        for (int c = 0; c < 4; c++) {
+            v[c] = r < t ? rope_value(tile[rr], d0 + c, cos_t + (size_t)r * half, sin_t + (size_t)r * half,
+                                      kind < 2 ? HD : 0u, HD, rope_dim, neox)
+                         : 0.0f;
+            mx = fmaxf(mx, fabsf(v[c]));
         }
-        const int e = head_exponent(v);
+#pragma unroll
+        for (uint32_t o = 1; o < LPR; o *= 2) mx = fmaxf(mx, __shfl_xor(mx, o, LPR));
+        int e = 0;  // as head_exponent
+        if (mx > 0.0f && mx <= 3.4028235e38f) e = ((int)(__float_as_uint(mx) >> 23) - 127) - 14;
+        e = e < -100 ? -100 : (e > 100 ? 100 : e);
         const float f = ldexpf(1.0f, -e);
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const uint32_t d = lane + 64 * u;
-            if (d >= HD) continue;
-            const float x = v[u] * f;
+        for (int c = 0; c < 4; c++) {
+            const uint32_t d = d0 + c;
+            const float x = v[c] * f;
             const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
             const size_t at =
                 kind == 0 ? rr * HD + d : kind == 1 ? frag_k<HD>(0, k0 + rr, d, 32) : frag_v<HD>(0, k0 + rr, d, 32);
             part[0][at] = hi;
             part[1][at] = lo;
         }
-        if (lane == 0) {
+        if (lane % LPR == 0) {
             const int8_t code = r < t ? (int8_t)e : (int8_t)kSplitPad;
             if (kind == 0)
                 o.eq[(size_t)slot * tp + r] = code;
