@@ -842,7 +842,8 @@ __device__ __forceinline__ int exp_byte(uint64_t w, int i) { return (int)(int8_t
 
 // Causal grouped-query attention on the split operands; the work split, the online softmax and
 // the merge are attention_kernel's. Per key tile: S'^T = k' q'^T (three f16 MFMAs per 16 dims),
-// S = S' 2^(e_q + e_k) scale, masked, online softmax -> p; p' = p 2^(14 + e_v - sigma) (sigma the
+// S = S' 2^(e_q + e_k) scale log2(e), masked, online softmax in base 2 -> p;
+// p' = p 2^(14 + e_v - sigma) (sigma the
 // tile's largest v exponent, so p' <= 2^14) split into two f16 parts; the tile's O'^T = v'^T p'^T
 // (three f16 MFMAs per 16 keys per 32 dims) enters the f32 accumulator scaled by 2^(sigma - 14).
 // XKIND 0: the output goes to att as f32 [t][heads HD]; FH_Q8_0 / FH_Q4_0: it goes to xo as the
@@ -880,6 +881,8 @@ __global__ __launch_bounds__(64 * W) void attention_split_kernel(
     for (int b = 0; b < DB; b++)
 #pragma unroll
         for (int i = 0; i < 16; i++) o[b][i] = 0.0f;
+    // scores in the base-2 domain (scale log2(e) folded in), so each exponential is one v_exp_f32
+    const float sl2 = scale * 1.44269504088896341f;
     float mrun = -INFINITY, lrun = 0.0f;
     const uint32_t tiles = (min(q0 + 31u, t - 1u)) / 32 + 1;  // key tiles any valid query of the block sees
     T cur, nxt;
@@ -903,7 +906,7 @@ __global__ __launch_bounds__(64 * W) void attention_split_kernel(
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const uint32_t key = k0 + 16 * (i / 8) + 8 * hf + i % 8;
-            const float v = key <= query ? ldexpf(s[i], e_q + exp_byte(cur.ek[i / 8], i % 8)) * scale : -INFINITY;
+            const float v = key <= query ? ldexpf(s[i], e_q + exp_byte(cur.ek[i / 8], i % 8)) * sl2 : -INFINITY;
             s[i] = v;
             mt = fmaxf(mt, v);
             sig = max(sig, exp_byte(cur.ev[i / 8], i % 8));
@@ -911,12 +914,12 @@ __global__ __launch_bounds__(64 * W) void attention_split_kernel(
         mt = fmaxf(mt, __shfl_xor(mt, 32));
         sig = max(sig, __shfl_xor(sig, 32));
         const float mnew = fmaxf(mrun, mt);  // finite: key k0 <= query in every tile
-        const float alpha = __expf(mrun - mnew);
+        const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
         float ls = 0.0f;
         f16x8 ph[2], pl[2];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const float p = __expf(s[i] - mnew);
+            const float p = __builtin_amdgcn_exp2f(s[i] - mnew);
             ls += p;
             const float x = ldexpf(p, 14 + exp_byte(cur.ev[i / 8], i % 8) - sig);
             const _Float16 hi = (_Float16)x;
@@ -957,7 +960,7 @@ __global__ __launch_bounds__(64 * W) void attention_split_kernel(
     float f[W], l = 0.0f;
 #pragma unroll
     for (int j = 0; j < W; j++) {
-        f[j] = __expf(red[j][0][lane] - M);  // a wavefront without tiles: e^(-inf) = 0
+        f[j] = __builtin_amdgcn_exp2f(red[j][0][lane] - M);  // a wavefront without tiles: 2^(-inf) = 0
         l += red[j][1][lane] * f[j];
     }
     l += __shfl_xor(l, 32);
