@@ -316,6 +316,24 @@ __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float *__restrict__ 
     extern __shared__ __attribute__((aligned(16))) float hrow[];
     __shared__ float red[4];
     const size_t base = (size_t)blockIdx.x * d;
+    if (d % 32 == 0) {
+        // a thread's chunks go from registers straight into the split (float4 q = tid + 256 i is
+        // the one split_row_fast gives it: eight consecutive lanes hold a block)
+        const uint32_t nq = d / 4, nb = d / 32, K64 = (d + 63) / 64 * 64, MS = xsb_rows(gridDim.x), m = blockIdx.x;
+        f32x4 v[kKeepRow];
+        const float ms = block_sum_256(row_load4<ADD>(x, o, base, nq, o_splits, o_stride, v), red) / (float)d;
+        const float inv = 1.0f / sqrtf(ms + eps);
+#pragma unroll
+        for (int i = 0; i < kKeepRow; i++) {
+            const uint32_t q = threadIdx.x + 256 * i;
+            if (q < nq)
+                split_chunk4<KIND>(row_norm4(v[i], g, q, inv), m, q / 8, q % 8, MS, nb, K64, dst.xh, dst.xl, dst.xsb);
+        }
+        for (uint32_t q = threadIdx.x + 256 * kKeepRow; q < nq; q += 256)
+            split_chunk4<KIND>(row_norm4(*(const f32x4 *)(x + base + 4 * q), g, q, inv), m, q / 8, q % 8, MS, nb, K64,
+                               dst.xh, dst.xl, dst.xsb);
+        return;
+    }
     if (d % 4 == 0) {
         const uint32_t nq = d / 4;
         f32x4 v[kKeepRow];
