@@ -1333,8 +1333,8 @@ __global__ __launch_bounds__(512, 1) void gemm_stream_precise_kernel(const _Floa
 // row) into a ring of three, two stages ahead; the weights' raw quants and scale dwords into a
 // ring of two and unpacked one stage ahead, as in the precise kernel. Per pair of stages (the
 // correction's 64 k): x lo and the correction operand (64 bytes per row and per column) and the
-// tile's power-of-two row and column scales, requested at the pair's first stage and used at its
-// second. A wavefront owns 64 x 128 (2 x 4 tiles): per stage 16 f16 MFMAs and 128 scale FMAs, per
+// power-of-two scales (x lo: the tile's rows' two block scales of the pair; the operand: per
+// column), requested at the pair's first stage and used at its second. A wavefront owns 64 x 128 (2 x 4 tiles): per stage 16 f16 MFMAs and 128 scale FMAs, per
 // pair 8 scaled fp8 MFMAs (1.5 f16-equivalent passes where the precise kernel makes 2).
 //
 // 64-byte rows (x hi, x lo, the correction operand) sit in LDS with the 16-byte chunk c of row r at

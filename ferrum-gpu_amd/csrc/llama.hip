@@ -306,9 +306,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float *__restrict__ x, con
     for (uint32_t i = threadIdx.x; i < d; i += 256) h[base + i] = __fmul_rn(__fmul_rn(x[base + i], inv), g[i]);
 }
 
-// The fast path's fused producers: rmsnorm_kernel and swiglu_kernel with the same arithmetic, the
-// row kept in LDS and written straight into the fast GEMM's split x (split_row_fast), so the
-// f32 activation is never written to memory and read back by a split pass. One workgroup per row.
+// The fast path's fused producers: rmsnorm_kernel and swiglu_kernel with the same arithmetic,
+// written straight into the fast GEMM's split x (split_chunk4: from the threads' registers where
+// the row is whole 32-element blocks, else through a row in LDS and split_row_fast), so the f32
+// activation is never written to memory and read back by a split pass. One workgroup per row.
 template <bool ADD, int KIND>
 __global__ __launch_bounds__(256) void rmsnorm_split_kernel(float *__restrict__ x, const float *__restrict__ o,
                                                             const float *__restrict__ g, uint32_t d, float eps,
