@@ -248,17 +248,20 @@ def load_env(fh, g, data, path, var):
             os.environ[var] = old
 
 
-@pytest.mark.parametrize("shape", ["epilogue", "fallback"])
+@pytest.mark.parametrize("shape", ["epilogue", "epilogue_odd_blocks", "fallback"])
 def test_swiglu_epilogue_is_bit_identical_to_the_swiglu_pass(fh, g, orc, shape):
     """The fast path's SwiGLU in the gate/up GEMM's epilogue (gate and up rows interleaved in runs
     of 32 at load) against the same model loaded with FERRUM_HIP_SWIGLU_UNFUSED=1 (the stacked
     product, then swiglu_split_kernel): the same accumulators and the same activation function,
     so logits and log-probabilities bit-identical. "epilogue": d 64 (one pipeline stage, never
-    split along K), so the epilogue runs. "fallback": d 512 with 16 tiles, which the GEMM splits
+    split along K), so the epilogue runs; "epilogue_odd_blocks" the same with an FFN of 96 (three
+    32-unit blocks, so the epilogue also writes the empty block that completes the down product's
+    last x lo pair). "fallback": d 512 with 16 tiles, which the GEMM splits
     along K, so the interleaved weight goes through the plain product and the interleave-aware
     SwiGLU pass instead."""
-    if shape == "epilogue":
-        c = cfg(vocab=500, ctx=256, dim=64, heads=4, kv_heads=2, head_dim=16, hidden=256, rope_dim=16)
+    if shape.startswith("epilogue"):
+        hid = 96 if shape == "epilogue_odd_blocks" else 256
+        c = cfg(vocab=500, ctx=256, dim=64, heads=4, kv_heads=2, head_dim=16, hidden=hid, rope_dim=16)
         n_ids = 201
     else:
         c = cfg(vocab=500, ctx=256, dim=512, heads=8, kv_heads=4, head_dim=64, hidden=512, rope_dim=64)
