@@ -384,13 +384,15 @@ def test_split_attention_head_dims_match_the_oracle(fh, g, orc, head_dim, neox, 
         assert np.array_equal(got, two.forward_all(ids[:t])), (head_dim, t)
 
 
-def test_rope_split_tiles_are_bit_identical_to_the_two_pass_split(fh, g):
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+def test_rope_split_tiles_are_bit_identical_to_the_two_pass_split(fh, g, head_dim):
     """qkv_rope_split_kernel takes 32-row tiles when they give at least two workgroups per CU
     (here 8 head slots x 64 tiles at t = 2048) and 16-row tiles below that (t = 1000, ragged):
     each writes whole k' and v' fragment lines from one workgroup. Both against the two-pass
-    RoPE and split (FERRUM_HIP_ROPE_UNFUSED=1), logits bit for bit. dim 1024 against 4 heads of 64
-    splits the QKV product along K at both lengths, so the tiles add partial sums."""
-    c = lm.config(vocab=300, ctx=2048, dim=1024, heads=4, kv_heads=2, head_dim=64, layers=2, hidden=256,
+    RoPE and split (FERRUM_HIP_ROPE_UNFUSED=1), logits bit for bit, for head dims 32, 64 and 128
+    (a row's lane group of 8, 16 or 32 lanes). dim 1024 against 4 heads splits the QKV product
+    along K at both lengths, so the tiles add partial sums."""
+    c = lm.config(vocab=300, ctx=2048, dim=1024, heads=4, kv_heads=2, head_dim=head_dim, layers=2, hidden=256,
                   rope_base=10000.0, neox=False, eps=1e-5)
     data = lm.to_gguf(lm.llama_random(c, 23, True, False), lm.Q8_0)
     dev = load(fh, g, data, fh.QPath.TiledFast)
